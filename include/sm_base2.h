@@ -1,0 +1,137 @@
+/*
+ * sm_base2.h - C ABI of the MI355X integer ("all base 2") GPT-2 decode step.
+ *
+ * One shared library (libsm_base2.so, gfx950 HIP) owns the device weights, the tables and the per-layer
+ * integer KV cache, and runs the decode step: every number a whole number, every emitted word the word
+ * base2.py's forward() gives on the same inputs.  All entry points return 0 (SM_OK) or a negative code;
+ * sm_last_error() gives the calling thread's last message.  No exception crosses this ABI.
+ *
+ * The reference has no C ABI: its machine is base2.py's stage functions (the operator API research code
+ * wraps, e.g. recording/C_plain.py:15-22) and the Swift/Metal streaming machine (base2_stream.swift).  Each
+ * declaration below names the reference interface it replaces.
+ *
+ * Threading: a machine is one HIP stream and is not thread-safe; callers serialise calls on a handle.
+ */
+#ifndef SM_BASE2_H
+#define SM_BASE2_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum {
+    SM_OK = 0,
+    SM_E_ARG = -1,       /* bad argument (sizes, ids, state) */
+    SM_E_IO = -2,        /* a layout file is missing, short or malformed */
+    SM_E_HIP = -3,       /* a HIP runtime call failed */
+    SM_E_OOM = -4,       /* device allocation failed */
+    SM_E_CTX = -5,       /* the context (positions) would pass max_ctx */
+    SM_E_OVERFLOW = -6,  /* an integer left the range the device layout holds (checked on the device) */
+    SM_E_STATE = -7      /* call out of order (e.g. generate before prefill) */
+};
+
+typedef struct sm_machine sm_machine;
+
+typedef struct {
+    int32_t max_streams;   /* B: independent streams decoded in lockstep (1 = the batch-1 path) */
+    int32_t max_ctx;       /* positions per stream, at most the position table's rows */
+    int32_t use_graph;     /* 1: replay each decode step as one captured HIP graph; 0: plain launches */
+    int32_t head_grid;     /* blocks of the head's plate read (0: default) */
+} sm_config;
+
+/* Replaces base2_stream.swift:151-208 (device, pipelines, loading base2_gpu/ and its buffers) and
+ * base2.py:12-16 (np.load of the converted model).  layout_dir is a base2_gpu.py directory
+ * (base2_gpu.py:9-17: manifest.json, {bank}.wc/.e/.b, wte/wpe/phi/arrival/log2/exp2 .bin). */
+int sm_create(const char* layout_dir, const sm_config* cfg, sm_machine** out);
+int sm_destroy(sm_machine* m);
+
+/* Empties every stream (positions, words, KV cache).  base2.py has no state; base2_stream.swift resets per
+ * prompt at :264-271. */
+int sm_reset(sm_machine* m);
+
+/* Queues a prompt for one stream (base2_stream.swift:265-271: seq = ids, R0 rows from wte + wpe).  All
+ * streams of one run must have prompts of the same length. */
+int sm_prefill(sm_machine* m, int32_t stream, const int32_t* ids, int32_t n);
+
+/* Runs the decode loop until every stream has n_words more greedy words; out is [n_streams][n_words].
+ * Replaces base2.py:123 (got.append(forward(ids + got)) per word) and base2_stream.swift:273-281 (prompt,
+ * then each word fed straight back on the device).  The first call also runs the prompt. */
+int sm_generate(sm_machine* m, int32_t n_words, int32_t* out);
+
+/* Records every intermediate of stream 0 at one position (-1: off).  Replaces fr2's rec=1 (recp kernel,
+ * base2_stream_fr2.swift:564-570) and recording/C_plain.py's wrapped product. */
+int sm_record_at(sm_machine* m, int32_t pos);
+
+/* What sm_read returns (int64 unless noted). */
+enum {
+    SM_READ_K16 = 1,      /* int32 [768]  per-head 16-bit keys at (layer, stream, pos) */
+    SM_READ_EK = 2,       /* int32 [12]   their water levels */
+    SM_READ_V = 3,        /* int32 [768]  values */
+    SM_READ_RESID = 4,    /* [768] the stream R of `stream` after its last position */
+    SM_READ_SEQ = 5,      /* int32 [max_ctx + 1] words per position of `stream` */
+    SM_READ_REC_X16 = 10, /* [12][4][3072] light entering each bank (qkv, proj, fc, mproj) */
+    SM_READ_REC_EXLS = 11,/* [12][4][2] its water level ex and gauge LS */
+    SM_READ_REC_PILE = 12,/* [12][4][3072] piles */
+    SM_READ_REC_QKV = 13, /* [12][2304] */
+    SM_READ_REC_ATT = 14, /* [12][768] */
+    SM_READ_REC_HID = 15, /* [12][3072] after the edge */
+    SM_READ_REC_RESID = 16,/* [12][2][768] stream after each half layer */
+    SM_READ_REC_HX16 = 17,/* [768] the head's light */
+    SM_READ_REC_HEXLS = 18,/* [2] */
+    SM_READ_REC_HPILE = 19,/* [vocab] */
+    SM_READ_REC_LOGITS = 20 /* [vocab] gauged logits + standing amount */
+};
+/* Copies one device array to host memory dst (bytes must match).  Replaces reading MTLBuffer contents
+ * (base2_stream.swift:282-286) for per-intermediate parity. */
+int sm_read(sm_machine* m, int32_t what, int32_t layer, int32_t stream, int32_t pos, void* dst, size_t bytes);
+
+/* Facts about a created machine: vocab, max_ctx, max_streams, n_ctx of the position table. */
+int sm_info(const sm_machine* m, int32_t* vocab, int32_t* max_ctx, int32_t* max_streams, int32_t* n_pos);
+
+const char* sm_last_error(void);
+
+/* ---------------------------------------------------------------------------------------------------
+ * Stage entry points: base2.py's stage functions on caller-owned DEVICE buffers (unit parity, microbench).
+ * stream is a hipStream_t (NULL: the null stream).  The tables come from sm_tables_create.
+ * ------------------------------------------------------------------------------------------------- */
+typedef struct sm_tables sm_tables;
+
+/* the tables of base2_convert.py:48-61 (int64 host arrays, as in the npz) */
+int sm_tables_create(const int64_t* phi, const int64_t* arrival, int32_t alen, const int64_t* log2t,
+                     const int64_t* exp2t, int64_t log2_768, int64_t eps40, sm_tables** out);
+int sm_tables_destroy(sm_tables* t);
+
+int sm_stage_rshift(const int64_t* x, const int64_t* s, int64_t* out, int64_t n, void* stream);          /* base2.py:18-22 */
+int sm_stage_log2fix(const sm_tables* t, const int64_t* v, int64_t* out, int64_t n, void* stream);       /* base2.py:42-48 */
+int sm_stage_power(const sm_tables* t, const int64_t* x, const int64_t* F, int64_t* out, int64_t n, void* stream); /* base2.py:50-53 */
+int sm_stage_edge(const sm_tables* t, const int64_t* h, int64_t* out, int64_t n, void* stream);          /* base2.py:78-83 */
+int sm_stage_to16(const int64_t* X, int32_t rows, int32_t n, int64_t* x16, int64_t* ex, void* stream);  /* base2.py:24-27 */
+int sm_stage_gauge_log(const sm_tables* t, const int64_t* R, int32_t rows, int64_t* x16, int64_t* ex,
+                       int64_t* LS, void* stream);                                                      /* base2.py:55-60 */
+int sm_stage_race(const int64_t* v, int64_t n, int64_t* out_index, void* stream);                       /* base2.py:34-40 */
+
+/* One new position's attention for one stream (base2.py:85-100 for the last row; base2_stream.swift:120-133
+ * without its 64-position cap).  qkv: device int64 [2304] (the gauged q, k, v of position pos); the caches
+ * hold positions < pos and receive position pos: k16 int32 [ctx][768], ek int32 [ctx][12], v int32
+ * [ctx][768]; out: device int64 [768]. */
+int sm_stage_attend(const sm_tables* t, const int64_t* qkv, int32_t* k16, int32_t* ek, int32_t* v,
+                    int32_t pos, int32_t ctx, int64_t* out, void* stream);
+
+/* A plate on the device (laid out for the GEMV), from an input-major int16 [nin][nout] host array. */
+typedef struct sm_plate sm_plate;
+int sm_plate_create(const int16_t* w, const int32_t* e, const int64_t* b, int32_t nin, int32_t nout,
+                    int32_t tile_cols, sm_plate** out);
+int sm_plate_destroy(sm_plate* p);
+/* pile[j] = sum_i x16[i] w[i][j], exact (base2.py:29-32; the split cells of base2_stream.swift:61-73).
+ * x16: device int64 [nin] with values in [-32768, 32768]; pile: device int64 [nout]. */
+int sm_plate_product(const sm_plate* p, const int64_t* x16, int64_t* pile, int32_t grid, void* stream);
+/* bytes of the device plate (for bandwidth accounting) */
+int64_t sm_plate_bytes(const sm_plate* p);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

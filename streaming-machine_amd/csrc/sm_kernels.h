@@ -1,0 +1,73 @@
+// Kernel argument blocks shared by the host code (sm_machine.hip) and the kernels (sm_kernels.hip).
+#pragma once
+#include "sm_device.h"
+
+// prologue: how a phase forms its 16-bit light from the row it reads
+enum { PRO_GAUGE = 0,   // gauge_log of the stream row R (768): x16, ex, LS (base2.py:55-60)
+       PRO_TO16 = 1,    // to16 of an activation row (768 or 3072): x16, ex (base2.py:24-27)
+       PRO_EMBED = 2,   // the word enters: R = wte[word] + wpe[pos] (base2.py:103), then PRO_GAUGE
+       PRO_X16 = 3 };   // the light is given (int64 x16 values, ex = -16): the raw product test
+// epilogue: what a phase does with each finished pile
+enum { EPI_GAUGED = 0,       // power(pile, (we + ex + 16) 65536 - LS) + b          (base2.py:70-71)
+       EPI_GAUGED_EDGE = 1,  // the same, then the edge                               (base2.py:106, 78-83)
+       EPI_PLAIN_ADD = 2,    // R += rshift(pile, -(we + ex + 16)) + b                  (base2.py:73-76, 105-106)
+       EPI_HEAD = 3,         // gauged logit + standing amount, then the race           (base2.py:107-114)
+       EPI_PILE = 4 };       // the raw pile (product only)                             (base2.py:29-32)
+
+struct Tables {
+    const int* LOG2; const int* EXP2; const int* PHI; const int* ARR;
+    int alen; i64 log768; i64 eps40;
+};
+
+// Record of one position's intermediates (stream 0), written when the position equals *pos.
+struct Rec {
+    const int* pos;
+    i64* x16;    // [L][4][3072]
+    i64* exls;   // [L][4][2]
+    i64* pile;   // [L][4][3072]
+    i64* qkv;    // [L][2304]
+    i64* att;    // [L][768]
+    i64* hid;    // [L][3072]
+    i64* resid;  // [L][2][768]
+    i64* hx16;   // [768]
+    i64* hexls;  // [2]
+    i64* hpile;  // [vocab]
+    i64* logits; // [vocab]
+};
+
+struct GemvArgs {
+    const int4* W;              // the plate in column tiles of TC (see sm_machine.hip: tile_plate)
+    const int* we;              // per-column power of two
+    const i64* bias;            // per-column bias (2^-16)
+    int nout, ntiles;
+    const i64* X;               // the row this phase reads (PRO_GAUGE / PRO_TO16 / PRO_X16)
+    const i64* wte; const i64* wpe;   // PRO_EMBED
+    const int* seq;             // [ctx] word per position (PRO_EMBED reads seq[pos])
+    const int* pos;             // device position counter
+    i64* Rw;                    // PRO_EMBED: block 0 writes the entering row here
+    i64* Y;                     // output row (or the stream R for EPI_PLAIN_ADD)
+    Tables tb;
+    // record slot for this phase (layer l, bank k) or null
+    i64* rx16; i64* rexls; i64* rpile; i64* rout;
+    const int* rec_pos;         // record when the position equals *rec_pos
+    // head only
+    i64* part_v; int* part_i; unsigned* counter;
+    int* seq_w; const int* plen; int* pos_w; int* words; int* nwords;
+    i64* rlogits;
+};
+
+struct AttArgs {
+    const i64* QKV;     // [B][2304]
+    int* K16;           // [B][ctx][768]  per-head 16-bit keys (values in [-32768, 32768])
+    int* EK;            // [B][ctx][12]   their water levels
+    int* V;             // [B][ctx][768]  raw gauged values (checked to fit 32 bits)
+    i64* out;           // [B][768]
+    const int* pos;     // position being written and read up to (inclusive)
+    int ctx;
+    Tables tb;
+    int* err;           // bit 0: a value left 32 bits
+    const int* rec_pos; i64* ratt;
+};
+
+// error bits in the device error word
+#define SM_ERR_V32 1

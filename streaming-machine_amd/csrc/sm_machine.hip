@@ -1,0 +1,660 @@
+// Host side of libsm_base2.so: the C ABI of include/sm_base2.h.
+//
+// One machine = one HIP stream, the device image of a base2_gpu.py directory, the per-layer integer KV
+// cache and a few control words on the device (position, prompt length, error bits).  A decode step is the
+// launch sequence
+//     for each of the 12 layers:  qkv (gauge + product + gauged)  ->  attention  ->  proj (to16 + product +
+//                                 plain, added to the stream)  ->  fc (gauge + product + gauged + edge)  ->
+//                                 mproj (to16 + product + plain, added)
+//     head (gauge + product + gauged + standing amount + race; the word goes straight back into seq)
+// i.e. 61 launches with the device-side position advancing in the head, so one captured HIP graph replays
+// every step; the host synchronises once per sm_generate call (base2_stream.swift:273-281 commits one
+// command buffer per prompt the same way).
+#include "sm_kernels.hip"
+#include "../../include/sm_base2.h"
+
+#include <cstdio>
+#include <cstring>
+#include <fstream>
+#include <string>
+#include <vector>
+
+static thread_local std::string g_err;
+
+static int fail(int code, const std::string& msg) {
+    g_err = msg;
+    return code;
+}
+
+#define HIP_TRY(x)                                                                                   \
+    do {                                                                                             \
+        hipError_t e_ = (x);                                                                         \
+        if (e_ != hipSuccess) return fail(SM_E_HIP, std::string(#x) + ": " + hipGetErrorString(e_)); \
+    } while (0)
+
+extern "C" const char* sm_last_error(void) { return g_err.c_str(); }
+
+// ---------------------------------------------------------------------------------------------------------
+// plates
+struct DevPlate {
+    int nin = 0, nout = 0, tc = 0, ntiles = 0;
+    int16_t* W = nullptr;
+    int* e = nullptr;
+    i64* b = nullptr;
+};
+
+// input-major [nin][nout] -> column tiles of tc: unit u of tile t holds inputs 8 (u / tc) .. + 8 of column
+// t tc + u % tc (padding columns are zero)
+static std::vector<int16_t> tile_plate(const int16_t* w, int nin, int nout, int tc) {
+    const int ntiles = (nout + tc - 1) / tc;
+    std::vector<int16_t> t((size_t)ntiles * tc * nin, 0);
+    for (int k = 0; k < nin; k++) {
+        const int16_t* row = w + (size_t)k * nout;
+        const size_t kb = (size_t)(k / 8) * tc * 8 + (k % 8);
+        for (int j = 0; j < nout; j++) {
+            const int tile = j / tc, jj = j % tc;
+            t[(size_t)tile * tc * nin + kb + (size_t)jj * 8] = row[j];
+        }
+    }
+    return t;
+}
+
+static void hfree(void* p) {
+    if (p) (void)hipFree(p);
+}
+
+template <typename T>
+static int dalloc(T** p, size_t count) {
+    if (count == 0) count = 1;
+    hipError_t e = hipMalloc((void**)p, count * sizeof(T));
+    if (e != hipSuccess) return fail(SM_E_OOM, std::string("hipMalloc: ") + hipGetErrorString(e));
+    return SM_OK;
+}
+
+static int upload_plate(DevPlate& P, const int16_t* w, const int32_t* e, const i64* b, int nin, int nout, int tc) {
+    if (nin % 8 || nin <= 0 || nout <= 0 || (tc != 1 && tc != 2 && tc != 4 && tc != 8))
+        return fail(SM_E_ARG, "plate: nin must be a multiple of 8 and tile_cols one of 1, 2, 4, 8");
+    P.nin = nin; P.nout = nout; P.tc = tc; P.ntiles = (nout + tc - 1) / tc;
+    std::vector<int16_t> t = tile_plate(w, nin, nout, tc);
+    int rc;
+    if ((rc = dalloc(&P.W, t.size())) || (rc = dalloc(&P.e, (size_t)nout)) || (rc = dalloc(&P.b, (size_t)nout))) return rc;
+    HIP_TRY(hipMemcpy(P.W, t.data(), t.size() * 2, hipMemcpyHostToDevice));
+    HIP_TRY(hipMemcpy(P.e, e, (size_t)nout * 4, hipMemcpyHostToDevice));
+    HIP_TRY(hipMemcpy(P.b, b, (size_t)nout * 8, hipMemcpyHostToDevice));
+    return SM_OK;
+}
+
+static void free_plate(DevPlate& P) {
+    hfree(P.W); hfree(P.e); hfree(P.b);
+    P = DevPlate();
+}
+
+// ---------------------------------------------------------------------------------------------------------
+// tables
+struct sm_tables {
+    int* LOG2 = nullptr; int* EXP2 = nullptr; int* PHI = nullptr; int* ARR = nullptr;
+    int alen = 0;
+    i64 log768 = 0, eps40 = 0;
+    int* scratch = nullptr;   // [0] pos for sm_stage_attend, [1] error bits
+    Tables tb() const { return Tables{LOG2, EXP2, PHI, ARR, alen, log768, eps40}; }
+};
+
+static int upload_table(int** dst, const i64* src, size_t n, i64 lo, i64 hi, const char* name) {
+    std::vector<int> v(n);
+    for (size_t i = 0; i < n; i++) {
+        if (src[i] < lo || src[i] > hi) return fail(SM_E_IO, std::string("table ") + name + " value out of range");
+        v[i] = (int)src[i];
+    }
+    int rc = dalloc(dst, n);
+    if (rc) return rc;
+    HIP_TRY(hipMemcpy(*dst, v.data(), n * 4, hipMemcpyHostToDevice));
+    return SM_OK;
+}
+
+static int tables_init(sm_tables& T, const i64* phi, const i64* arr, int alen, const i64* log2t, const i64* exp2t,
+                       i64 log768, i64 eps40) {
+    if (alen <= 0 || alen > (1 << 20)) return fail(SM_E_ARG, "arrival table length");
+    int rc;
+    if ((rc = upload_table(&T.PHI, phi, 65536, 0, 65536, "phi"))) return rc;
+    if ((rc = upload_table(&T.ARR, arr, alen, 0, 1 << 24, "arrival"))) return rc;
+    if ((rc = upload_table(&T.LOG2, log2t, 65536, 0, 65536, "log2"))) return rc;
+    if ((rc = upload_table(&T.EXP2, exp2t, 65536, 65536, 131072, "exp2"))) return rc;
+    if ((rc = dalloc(&T.scratch, 16))) return rc;
+    HIP_TRY(hipMemset(T.scratch, 0, 64));
+    T.alen = alen; T.log768 = log768; T.eps40 = eps40;
+    return SM_OK;
+}
+
+static void tables_free(sm_tables& T) {
+    hfree(T.LOG2); hfree(T.EXP2); hfree(T.PHI); hfree(T.ARR); hfree(T.scratch);
+    T = sm_tables();
+}
+
+// ---------------------------------------------------------------------------------------------------------
+// the machine
+enum { CTL_POS = 0, CTL_PLEN = 1, CTL_NWORDS = 2, CTL_ERR = 3, CTL_RECPOS = 4, CTL_COUNTER = 5, CTL_N = 8 };
+static const int NIN[4] = {768, 768, 768, 3072};
+static const int NOUT[4] = {2304, 768, 3072, 768};
+static const int TCOLS[4] = {8, 2, 8, 2};
+static const char* BANK[4] = {"qkv", "proj", "fc", "mproj"};
+
+struct sm_machine {
+    sm_config cfg{};
+    int B = 1, ctx = 0, vocab = 0, npos = 0, head_grid = 1024;
+    hipStream_t st = nullptr;
+    DevPlate bank[12][4];
+    DevPlate head;
+    i64* wte = nullptr;
+    i64* wpe = nullptr;
+    sm_tables T;
+    // state
+    i64 *R = nullptr, *QKV = nullptr, *att = nullptr, *hid = nullptr;
+    int *K16 = nullptr, *EK = nullptr, *V = nullptr;   // [L][B][ctx][...]
+    int* seq = nullptr;                                 // [B][ctx + 1]
+    int* words = nullptr;                               // [B][ctx + 1]
+    int* ctl = nullptr;
+    i64* part_v = nullptr;
+    int* part_i = nullptr;
+    // record
+    i64 *r_x16 = nullptr, *r_exls = nullptr, *r_pile = nullptr, *r_qkv = nullptr, *r_att = nullptr, *r_hid = nullptr,
+        *r_resid = nullptr, *r_hx16 = nullptr, *r_hexls = nullptr, *r_hpile = nullptr, *r_logits = nullptr;
+    hipGraphExec_t gexec = nullptr;
+    hipGraph_t graph = nullptr;
+    // host mirror
+    int h_plen = 0, h_pos = 0, h_words = 0;
+    std::vector<std::vector<int>> prompts;
+};
+
+static bool read_file(const std::string& path, std::vector<char>& out) {
+    std::ifstream f(path, std::ios::binary | std::ios::ate);
+    if (!f) return false;
+    std::streamsize n = f.tellg();
+    f.seekg(0);
+    out.resize((size_t)n);
+    return n == 0 || (bool)f.read(out.data(), n);
+}
+
+template <typename T>
+static int read_array(const std::string& path, std::vector<T>& v, size_t count) {
+    std::vector<char> raw;
+    if (!read_file(path, raw)) return fail(SM_E_IO, "cannot read " + path);
+    if (count != (size_t)-1 && raw.size() != count * sizeof(T))
+        return fail(SM_E_IO, path + ": expected " + std::to_string(count * sizeof(T)) + " bytes, found " + std::to_string(raw.size()));
+    if (raw.size() % sizeof(T)) return fail(SM_E_IO, path + ": size is not a whole number of elements");
+    v.resize(raw.size() / sizeof(T));
+    memcpy(v.data(), raw.data(), raw.size());
+    return SM_OK;
+}
+
+// the few manifest.json facts we need (base2_gpu.py:16): banks[{name, nin, nout}], log2_768, eps40, arrival_len
+static bool json_int(const std::string& s, size_t from, const std::string& key, long long& v) {
+    size_t k = s.find("\"" + key + "\"", from);
+    if (k == std::string::npos) return false;
+    size_t c = s.find(':', k);
+    if (c == std::string::npos) return false;
+    c++;
+    while (c < s.size() && (s[c] == ' ' || s[c] == '\t' || s[c] == '\n' || s[c] == '\r')) c++;
+    char* end = nullptr;
+    v = strtoll(s.c_str() + c, &end, 10);
+    return end != s.c_str() + c;
+}
+
+struct BankInfo { std::string name; long long nin, nout; };
+
+static int parse_manifest(const std::string& text, std::vector<BankInfo>& banks, long long& log768, long long& eps40, long long& alen) {
+    size_t b = text.find("\"banks\"");
+    if (b == std::string::npos) return fail(SM_E_IO, "manifest.json: no banks");
+    size_t lb = text.find('[', b), rb = text.find(']', b);
+    if (lb == std::string::npos || rb == std::string::npos) return fail(SM_E_IO, "manifest.json: malformed banks");
+    size_t cur = lb;
+    while (true) {
+        size_t ob = text.find('{', cur);
+        if (ob == std::string::npos || ob > rb) break;
+        size_t cb = text.find('}', ob);
+        std::string obj = text.substr(ob, cb - ob + 1);
+        BankInfo bi;
+        size_t nk = obj.find("\"name\"");
+        if (nk == std::string::npos) return fail(SM_E_IO, "manifest.json: bank without name");
+        size_t q1 = obj.find('"', obj.find(':', nk) + 1), q2 = obj.find('"', q1 + 1);
+        bi.name = obj.substr(q1 + 1, q2 - q1 - 1);
+        if (!json_int(obj, 0, "nin", bi.nin) || !json_int(obj, 0, "nout", bi.nout)) return fail(SM_E_IO, "manifest.json: bank sizes");
+        banks.push_back(bi);
+        cur = cb + 1;
+    }
+    std::string rest = text.substr(0, lb) + text.substr(rb);
+    if (!json_int(rest, 0, "log2_768", log768) || !json_int(rest, 0, "eps40", eps40) || !json_int(rest, 0, "arrival_len", alen))
+        return fail(SM_E_IO, "manifest.json: constants missing");
+    return SM_OK;
+}
+
+static void machine_free(sm_machine* m) {
+    if (!m) return;
+    if (m->gexec) (void)hipGraphExecDestroy(m->gexec);
+    if (m->graph) (void)hipGraphDestroy(m->graph);
+    for (int l = 0; l < 12; l++)
+        for (int k = 0; k < 4; k++) free_plate(m->bank[l][k]);
+    free_plate(m->head);
+    tables_free(m->T);
+    void* ps[] = {m->wte, m->wpe, m->R, m->QKV, m->att, m->hid, m->K16, m->EK, m->V, m->seq, m->words, m->ctl,
+                  m->part_v, m->part_i, m->r_x16, m->r_exls, m->r_pile, m->r_qkv, m->r_att, m->r_hid, m->r_resid,
+                  m->r_hx16, m->r_hexls, m->r_hpile, m->r_logits};
+    for (void* p : ps) hfree(p);
+    if (m->st) (void)hipStreamDestroy(m->st);
+    delete m;
+}
+
+// the launch sequence of one decode step (all streams, one position each)
+static int launch_step(sm_machine* m) {
+    const Tables tb = m->T.tb();
+    int* ctl = m->ctl;
+    for (int l = 0; l < 12; l++) {
+        GemvArgs base{};
+        base.tb = tb;
+        base.pos = ctl + CTL_POS;
+        base.rec_pos = ctl + CTL_RECPOS;
+        // qkv: the stream's gauge, the product, power + bias (base2.py:105 gauged_bank(R, "qkv.l"))
+        {
+            GemvArgs a = base;
+            const DevPlate& P = m->bank[l][0];
+            a.W = reinterpret_cast<const int4*>(P.W); a.we = P.e; a.bias = P.b; a.nout = P.nout; a.ntiles = P.ntiles;
+            a.X = m->R; a.Y = m->QKV;
+            a.wte = m->wte; a.wpe = m->wpe; a.seq = m->seq; a.Rw = m->R;
+            a.rx16 = m->r_x16 + (l * 4 + 0) * 3072; a.rexls = m->r_exls + (l * 4 + 0) * 2;
+            a.rpile = m->r_pile + (l * 4 + 0) * 3072; a.rout = m->r_qkv + l * 2304;
+            if (l == 0) k_gemv<768, 8, PRO_EMBED, EPI_GAUGED><<<P.ntiles, NTHR, 0, m->st>>>(a);
+            else k_gemv<768, 8, PRO_GAUGE, EPI_GAUGED><<<P.ntiles, NTHR, 0, m->st>>>(a);
+        }
+        // attention (base2.py:85-100) on the KV cache of layer l
+        {
+            AttArgs a{};
+            const size_t per = (size_t)m->B * m->ctx;
+            a.QKV = m->QKV; a.K16 = m->K16 + l * per * 768; a.EK = m->EK + l * per * 12; a.V = m->V + l * per * 768;
+            a.out = m->att; a.pos = ctl + CTL_POS; a.ctx = m->ctx; a.tb = tb; a.err = ctl + CTL_ERR;
+            a.rec_pos = ctl + CTL_RECPOS; a.ratt = m->r_att + l * 768;
+            k_attend<<<dim3(12, m->B), NTHR, (size_t)m->ctx * 12, m->st>>>(a);
+        }
+        // proj: to16 of the attention row, product, plain shift + bias, added to R (base2.py:105)
+        {
+            GemvArgs a = base;
+            const DevPlate& P = m->bank[l][1];
+            a.W = reinterpret_cast<const int4*>(P.W); a.we = P.e; a.bias = P.b; a.nout = P.nout; a.ntiles = P.ntiles;
+            a.X = m->att; a.Y = m->R;
+            a.rx16 = m->r_x16 + (l * 4 + 1) * 3072; a.rexls = m->r_exls + (l * 4 + 1) * 2;
+            a.rpile = m->r_pile + (l * 4 + 1) * 3072; a.rout = m->r_resid + (l * 2 + 0) * 768;
+            k_gemv<768, 2, PRO_TO16, EPI_PLAIN_ADD><<<P.ntiles, NTHR, 0, m->st>>>(a);
+        }
+        // fc: gauge, product, gauged, edge (base2.py:106)
+        {
+            GemvArgs a = base;
+            const DevPlate& P = m->bank[l][2];
+            a.W = reinterpret_cast<const int4*>(P.W); a.we = P.e; a.bias = P.b; a.nout = P.nout; a.ntiles = P.ntiles;
+            a.X = m->R; a.Y = m->hid;
+            a.rx16 = m->r_x16 + (l * 4 + 2) * 3072; a.rexls = m->r_exls + (l * 4 + 2) * 2;
+            a.rpile = m->r_pile + (l * 4 + 2) * 3072; a.rout = m->r_hid + l * 3072;
+            k_gemv<768, 8, PRO_GAUGE, EPI_GAUGED_EDGE><<<P.ntiles, NTHR, 0, m->st>>>(a);
+        }
+        // mproj: to16 of the hidden row (3072), product, plain, added to R (base2.py:106)
+        {
+            GemvArgs a = base;
+            const DevPlate& P = m->bank[l][3];
+            a.W = reinterpret_cast<const int4*>(P.W); a.we = P.e; a.bias = P.b; a.nout = P.nout; a.ntiles = P.ntiles;
+            a.X = m->hid; a.Y = m->R;
+            a.rx16 = m->r_x16 + (l * 4 + 3) * 3072; a.rexls = m->r_exls + (l * 4 + 3) * 2;
+            a.rpile = m->r_pile + (l * 4 + 3) * 3072; a.rout = m->r_resid + (l * 2 + 1) * 768;
+            k_gemv<3072, 2, PRO_TO16, EPI_PLAIN_ADD><<<P.ntiles, NTHR, 0, m->st>>>(a);
+        }
+    }
+    // head: gauge, product with the tied word table, power + standing amount, race (base2.py:107-114)
+    {
+        GemvArgs a{};
+        a.tb = tb;
+        a.pos = ctl + CTL_POS; a.rec_pos = ctl + CTL_RECPOS;
+        const DevPlate& P = m->head;
+        a.W = reinterpret_cast<const int4*>(P.W); a.we = P.e; a.bias = P.b; a.nout = P.nout; a.ntiles = P.ntiles;
+        a.X = m->R;
+        a.rx16 = m->r_hx16; a.rexls = m->r_hexls; a.rpile = m->r_hpile; a.rlogits = m->r_logits;
+        a.part_v = m->part_v; a.part_i = m->part_i; a.counter = reinterpret_cast<unsigned*>(ctl + CTL_COUNTER);
+        a.seq_w = m->seq; a.plen = ctl + CTL_PLEN; a.pos_w = ctl + CTL_POS; a.words = m->words; a.nwords = ctl + CTL_NWORDS;
+        k_gemv<768, 8, PRO_GAUGE, EPI_HEAD><<<m->head_grid, NTHR, 0, m->st>>>(a);
+    }
+    HIP_TRY(hipGetLastError());
+    return SM_OK;
+}
+
+extern "C" int sm_create(const char* layout_dir, const sm_config* cfg, sm_machine** out) {
+    if (!layout_dir || !out) return fail(SM_E_ARG, "sm_create: null argument");
+    *out = nullptr;
+    sm_config c{1, 1024, 1, 0};
+    if (cfg) c = *cfg;
+    if (c.max_streams != 1) return fail(SM_E_ARG, "sm_create: this build decodes one stream per machine (max_streams = 1)");
+    if (c.max_ctx <= 0) return fail(SM_E_ARG, "sm_create: max_ctx must be positive");
+    const std::string dir = std::string(layout_dir) + "/";
+    std::vector<char> mj;
+    if (!read_file(dir + "manifest.json", mj)) return fail(SM_E_IO, "cannot read " + dir + "manifest.json");
+    std::vector<BankInfo> banks;
+    long long log768, eps40, alen;
+    int rc = parse_manifest(std::string(mj.begin(), mj.end()), banks, log768, eps40, alen);
+    if (rc) return rc;
+    auto find = [&](const std::string& n) -> const BankInfo* {
+        for (auto& b : banks) if (b.name == n) return &b;
+        return nullptr;
+    };
+    sm_machine* m = new sm_machine();
+    m->cfg = c;
+    m->B = c.max_streams;
+    auto bail = [&](int code) { machine_free(m); return code; };
+    {
+        hipError_t e = hipStreamCreateWithFlags(&m->st, hipStreamNonBlocking);
+        if (e != hipSuccess) return bail(fail(SM_E_HIP, std::string("hipStreamCreate: ") + hipGetErrorString(e)));
+    }
+    // banks
+    for (int l = 0; l < 12; l++) {
+        for (int k = 0; k < 4; k++) {
+            const std::string name = std::string(BANK[k]) + "." + std::to_string(l);
+            const BankInfo* bi = find(name);
+            if (!bi || bi->nin != NIN[k] || bi->nout != NOUT[k]) return bail(fail(SM_E_IO, "manifest.json: bank " + name + " missing or of the wrong shape"));
+            std::vector<int16_t> w; std::vector<int32_t> e; std::vector<i64> b;
+            if ((rc = read_array(dir + name + ".wc", w, (size_t)NIN[k] * NOUT[k])) || (rc = read_array(dir + name + ".e", e, NOUT[k])) ||
+                (rc = read_array(dir + name + ".b", b, NOUT[k])))
+                return bail(rc);
+            if ((rc = upload_plate(m->bank[l][k], w.data(), e.data(), b.data(), NIN[k], NOUT[k], TCOLS[k]))) return bail(rc);
+        }
+    }
+    const BankInfo* hb = find("head");
+    if (!hb || hb->nin != 768 || hb->nout <= 0 || hb->nout > (1 << 24)) return bail(fail(SM_E_IO, "manifest.json: head bank missing or of the wrong shape"));
+    m->vocab = (int)hb->nout;
+    {
+        std::vector<int16_t> w; std::vector<int32_t> e; std::vector<i64> b;
+        if ((rc = read_array(dir + "head.wc", w, (size_t)768 * m->vocab)) || (rc = read_array(dir + "head.e", e, m->vocab)) ||
+            (rc = read_array(dir + "head.b", b, m->vocab)))
+            return bail(rc);
+        if ((rc = upload_plate(m->head, w.data(), e.data(), b.data(), 768, m->vocab, 8))) return bail(rc);
+    }
+    // word and position tables
+    {
+        std::vector<i64> wte, wpe;
+        if ((rc = read_array(dir + "wte.bin", wte, (size_t)m->vocab * 768)) || (rc = read_array(dir + "wpe.bin", wpe, (size_t)-1))) return bail(rc);
+        if (wpe.size() % 768 || wpe.empty()) return bail(fail(SM_E_IO, "wpe.bin: not a whole number of 768-wide rows"));
+        m->npos = (int)(wpe.size() / 768);
+        if ((rc = dalloc(&m->wte, wte.size())) || (rc = dalloc(&m->wpe, wpe.size()))) return bail(rc);
+        if (hipMemcpy(m->wte, wte.data(), wte.size() * 8, hipMemcpyHostToDevice) != hipSuccess ||
+            hipMemcpy(m->wpe, wpe.data(), wpe.size() * 8, hipMemcpyHostToDevice) != hipSuccess)
+            return bail(fail(SM_E_HIP, "upload wte/wpe"));
+    }
+    // tables
+    {
+        std::vector<i64> phi, arr, lg, ep;
+        if ((rc = read_array(dir + "phi.bin", phi, 65536)) || (rc = read_array(dir + "arrival.bin", arr, (size_t)alen)) ||
+            (rc = read_array(dir + "log2.bin", lg, 65536)) || (rc = read_array(dir + "exp2.bin", ep, 65536)))
+            return bail(rc);
+        if ((rc = tables_init(m->T, phi.data(), arr.data(), (int)alen, lg.data(), ep.data(), log768, eps40))) return bail(rc);
+    }
+    m->ctx = c.max_ctx < m->npos ? c.max_ctx : m->npos;
+    m->head_grid = c.head_grid > 0 ? c.head_grid : 1024;
+    // state
+    const size_t B = m->B, ctx = m->ctx;
+    if ((rc = dalloc(&m->R, B * 768)) || (rc = dalloc(&m->QKV, B * 2304)) || (rc = dalloc(&m->att, B * 768)) ||
+        (rc = dalloc(&m->hid, B * 3072)) || (rc = dalloc(&m->K16, 12 * B * ctx * 768)) || (rc = dalloc(&m->EK, 12 * B * ctx * 12)) ||
+        (rc = dalloc(&m->V, 12 * B * ctx * 768)) || (rc = dalloc(&m->seq, B * (ctx + 1))) || (rc = dalloc(&m->words, B * (ctx + 1))) ||
+        (rc = dalloc(&m->ctl, (size_t)CTL_N)) || (rc = dalloc(&m->part_v, (size_t)m->head_grid)) ||
+        (rc = dalloc(&m->part_i, (size_t)m->head_grid)) || (rc = dalloc(&m->r_x16, (size_t)12 * 4 * 3072)) ||
+        (rc = dalloc(&m->r_exls, (size_t)12 * 4 * 2)) || (rc = dalloc(&m->r_pile, (size_t)12 * 4 * 3072)) ||
+        (rc = dalloc(&m->r_qkv, (size_t)12 * 2304)) || (rc = dalloc(&m->r_att, (size_t)12 * 768)) ||
+        (rc = dalloc(&m->r_hid, (size_t)12 * 3072)) || (rc = dalloc(&m->r_resid, (size_t)12 * 2 * 768)) ||
+        (rc = dalloc(&m->r_hx16, 768)) || (rc = dalloc(&m->r_hexls, 2)) || (rc = dalloc(&m->r_hpile, (size_t)m->vocab)) ||
+        (rc = dalloc(&m->r_logits, (size_t)m->vocab)))
+        return bail(rc);
+    m->prompts.assign(B, {});
+    if ((rc = sm_reset(m))) return bail(rc);
+    *out = m;
+    return SM_OK;
+}
+
+extern "C" int sm_destroy(sm_machine* m) {
+    if (m) {
+        (void)hipStreamSynchronize(m->st);
+        machine_free(m);
+    }
+    return SM_OK;
+}
+
+extern "C" int sm_reset(sm_machine* m) {
+    if (!m) return fail(SM_E_ARG, "sm_reset: null machine");
+    const size_t B = m->B, ctx = m->ctx;
+    HIP_TRY(hipMemsetAsync(m->ctl, 0, CTL_N * 4, m->st));
+    int rp = -1;
+    HIP_TRY(hipMemcpyAsync(m->ctl + CTL_RECPOS, &rp, 4, hipMemcpyHostToDevice, m->st));
+    HIP_TRY(hipMemsetAsync(m->K16, 0, 12 * B * ctx * 768 * 4, m->st));
+    HIP_TRY(hipMemsetAsync(m->EK, 0, 12 * B * ctx * 12 * 4, m->st));
+    HIP_TRY(hipMemsetAsync(m->V, 0, 12 * B * ctx * 768 * 4, m->st));
+    HIP_TRY(hipMemsetAsync(m->seq, 0, B * (ctx + 1) * 4, m->st));
+    HIP_TRY(hipMemsetAsync(m->words, 0, B * (ctx + 1) * 4, m->st));
+    HIP_TRY(hipMemsetAsync(m->R, 0, B * 768 * 8, m->st));
+    HIP_TRY(hipStreamSynchronize(m->st));
+    m->h_plen = m->h_pos = m->h_words = 0;
+    for (auto& p : m->prompts) p.clear();
+    return SM_OK;
+}
+
+extern "C" int sm_prefill(sm_machine* m, int32_t stream, const int32_t* ids, int32_t n) {
+    if (!m || !ids) return fail(SM_E_ARG, "sm_prefill: null argument");
+    if (stream < 0 || stream >= m->B) return fail(SM_E_ARG, "sm_prefill: stream out of range");
+    if (m->h_pos != 0) return fail(SM_E_STATE, "sm_prefill: the machine has already run; call sm_reset first");
+    if (n <= 0 || n > m->ctx) return fail(SM_E_CTX, "sm_prefill: prompt length must be in [1, max_ctx]");
+    for (int i = 0; i < n; i++)
+        if (ids[i] < 0 || ids[i] >= m->vocab) return fail(SM_E_ARG, "sm_prefill: token id out of range");
+    m->prompts[stream].assign(ids, ids + n);
+    HIP_TRY(hipMemcpy(m->seq + (size_t)stream * (m->ctx + 1), ids, (size_t)n * 4, hipMemcpyHostToDevice));
+    return SM_OK;
+}
+
+extern "C" int sm_record_at(sm_machine* m, int32_t pos) {
+    if (!m) return fail(SM_E_ARG, "sm_record_at: null machine");
+    HIP_TRY(hipMemcpy(m->ctl + CTL_RECPOS, &pos, 4, hipMemcpyHostToDevice));
+    return SM_OK;
+}
+
+static int ensure_graph(sm_machine* m) {
+    if (m->gexec) return SM_OK;
+    HIP_TRY(hipStreamBeginCapture(m->st, hipStreamCaptureModeThreadLocal));
+    int rc = launch_step(m);
+    hipGraph_t g = nullptr;
+    hipError_t e = hipStreamEndCapture(m->st, &g);
+    if (rc) { if (g) (void)hipGraphDestroy(g); return rc; }
+    if (e != hipSuccess) return fail(SM_E_HIP, std::string("hipStreamEndCapture: ") + hipGetErrorString(e));
+    m->graph = g;
+    HIP_TRY(hipGraphInstantiate(&m->gexec, g, nullptr, nullptr, 0));
+    return SM_OK;
+}
+
+extern "C" int sm_generate(sm_machine* m, int32_t n_words, int32_t* out) {
+    if (!m) return fail(SM_E_ARG, "sm_generate: null machine");
+    if (n_words <= 0) return fail(SM_E_ARG, "sm_generate: n_words must be positive");
+    if (m->h_pos == 0) {
+        size_t n = m->prompts[0].size();
+        for (int b = 0; b < m->B; b++)
+            if (m->prompts[b].empty() || m->prompts[b].size() != n) return fail(SM_E_STATE, "sm_generate: every stream needs a prompt of the same length");
+        m->h_plen = (int)n;
+        HIP_TRY(hipMemcpyAsync(m->ctl + CTL_PLEN, &m->h_plen, 4, hipMemcpyHostToDevice, m->st));
+    }
+    const int target = m->h_words + n_words;
+    const int steps = (m->h_plen - 1 + target) - m->h_pos;
+    if (m->h_plen - 1 + target > m->ctx) return fail(SM_E_CTX, "sm_generate: prompt + words would pass max_ctx");
+    int rc;
+    if (m->cfg.use_graph) {
+        if ((rc = ensure_graph(m))) return rc;
+        for (int s = 0; s < steps; s++) HIP_TRY(hipGraphLaunch(m->gexec, m->st));
+    } else {
+        for (int s = 0; s < steps; s++)
+            if ((rc = launch_step(m))) return rc;
+    }
+    HIP_TRY(hipStreamSynchronize(m->st));
+    int ctl[CTL_N];
+    HIP_TRY(hipMemcpy(ctl, m->ctl, sizeof(ctl), hipMemcpyDeviceToHost));
+    m->h_pos += steps;
+    m->h_words = target;
+    if (ctl[CTL_POS] != m->h_pos) return fail(SM_E_STATE, "sm_generate: device position disagrees with the host");
+    if (ctl[CTL_ERR] & SM_ERR_V32) return fail(SM_E_OVERFLOW, "sm_generate: an attention value left 32 bits (the V cache holds int32)");
+    for (int b = 0; b < m->B; b++)
+        HIP_TRY(hipMemcpy(out + (size_t)b * n_words, m->words + (size_t)b * (m->ctx + 1) + (target - n_words), (size_t)n_words * 4,
+                          hipMemcpyDeviceToHost));
+    return SM_OK;
+}
+
+extern "C" int sm_read(sm_machine* m, int32_t what, int32_t layer, int32_t stream, int32_t pos, void* dst, size_t bytes) {
+    if (!m || !dst) return fail(SM_E_ARG, "sm_read: null argument");
+    if (stream < 0 || stream >= m->B) return fail(SM_E_ARG, "sm_read: stream out of range");
+    const size_t B = m->B, ctx = m->ctx;
+    const void* src = nullptr;
+    size_t need = 0;
+    auto kv_ok = [&]() { return layer >= 0 && layer < 12 && pos >= 0 && pos < m->ctx; };
+    switch (what) {
+        case SM_READ_K16: if (!kv_ok()) return fail(SM_E_ARG, "sm_read: layer/pos"); src = m->K16 + (((size_t)layer * B + stream) * ctx + pos) * 768; need = 768 * 4; break;
+        case SM_READ_EK: if (!kv_ok()) return fail(SM_E_ARG, "sm_read: layer/pos"); src = m->EK + (((size_t)layer * B + stream) * ctx + pos) * 12; need = 12 * 4; break;
+        case SM_READ_V: if (!kv_ok()) return fail(SM_E_ARG, "sm_read: layer/pos"); src = m->V + (((size_t)layer * B + stream) * ctx + pos) * 768; need = 768 * 4; break;
+        case SM_READ_RESID: src = m->R + (size_t)stream * 768; need = 768 * 8; break;
+        case SM_READ_SEQ: src = m->seq + (size_t)stream * (ctx + 1); need = (ctx + 1) * 4; break;
+        case SM_READ_REC_X16: src = m->r_x16; need = 12 * 4 * 3072 * 8; break;
+        case SM_READ_REC_EXLS: src = m->r_exls; need = 12 * 4 * 2 * 8; break;
+        case SM_READ_REC_PILE: src = m->r_pile; need = 12 * 4 * 3072 * 8; break;
+        case SM_READ_REC_QKV: src = m->r_qkv; need = 12 * 2304 * 8; break;
+        case SM_READ_REC_ATT: src = m->r_att; need = 12 * 768 * 8; break;
+        case SM_READ_REC_HID: src = m->r_hid; need = 12 * 3072 * 8; break;
+        case SM_READ_REC_RESID: src = m->r_resid; need = 12 * 2 * 768 * 8; break;
+        case SM_READ_REC_HX16: src = m->r_hx16; need = 768 * 8; break;
+        case SM_READ_REC_HEXLS: src = m->r_hexls; need = 2 * 8; break;
+        case SM_READ_REC_HPILE: src = m->r_hpile; need = (size_t)m->vocab * 8; break;
+        case SM_READ_REC_LOGITS: src = m->r_logits; need = (size_t)m->vocab * 8; break;
+        default: return fail(SM_E_ARG, "sm_read: unknown array");
+    }
+    if (bytes != need) return fail(SM_E_ARG, "sm_read: expected " + std::to_string(need) + " bytes");
+    HIP_TRY(hipStreamSynchronize(m->st));
+    HIP_TRY(hipMemcpy(dst, src, need, hipMemcpyDeviceToHost));
+    return SM_OK;
+}
+
+extern "C" int sm_info(const sm_machine* m, int32_t* vocab, int32_t* max_ctx, int32_t* max_streams, int32_t* n_pos) {
+    if (!m) return fail(SM_E_ARG, "sm_info: null machine");
+    if (vocab) *vocab = m->vocab;
+    if (max_ctx) *max_ctx = m->ctx;
+    if (max_streams) *max_streams = m->B;
+    if (n_pos) *n_pos = m->npos;
+    return SM_OK;
+}
+
+// ---------------------------------------------------------------------------------------------------------
+// stage entry points
+extern "C" int sm_tables_create(const int64_t* phi, const int64_t* arrival, int32_t alen, const int64_t* log2t,
+                                const int64_t* exp2t, int64_t log2_768, int64_t eps40, sm_tables** out) {
+    if (!phi || !arrival || !log2t || !exp2t || !out) return fail(SM_E_ARG, "sm_tables_create: null argument");
+    sm_tables* t = new sm_tables();
+    int rc = tables_init(*t, (const i64*)phi, (const i64*)arrival, alen, (const i64*)log2t, (const i64*)exp2t, log2_768, eps40);
+    if (rc) { tables_free(*t); delete t; return rc; }
+    *out = t;
+    return SM_OK;
+}
+
+extern "C" int sm_tables_destroy(sm_tables* t) {
+    if (t) { tables_free(*t); delete t; }
+    return SM_OK;
+}
+
+static inline int blocks_for(int64_t n, int per) { return (int)((n + per - 1) / per); }
+
+extern "C" int sm_stage_rshift(const int64_t* x, const int64_t* s, int64_t* out, int64_t n, void* stream) {
+    if (n < 0 || (n > 0 && (!x || !s || !out))) return fail(SM_E_ARG, "sm_stage_rshift: arguments");
+    if (n) k_stage_rshift<<<blocks_for(n, 256), 256, 0, (hipStream_t)stream>>>((const i64*)x, (const i64*)s, (i64*)out, n);
+    HIP_TRY(hipGetLastError());
+    return SM_OK;
+}
+extern "C" int sm_stage_log2fix(const sm_tables* t, const int64_t* v, int64_t* out, int64_t n, void* stream) {
+    if (!t || n < 0 || (n > 0 && (!v || !out))) return fail(SM_E_ARG, "sm_stage_log2fix: arguments");
+    if (n) k_stage_log2fix<<<blocks_for(n, 256), 256, 0, (hipStream_t)stream>>>((const i64*)v, (i64*)out, n, t->LOG2);
+    HIP_TRY(hipGetLastError());
+    return SM_OK;
+}
+extern "C" int sm_stage_power(const sm_tables* t, const int64_t* x, const int64_t* F, int64_t* out, int64_t n, void* stream) {
+    if (!t || n < 0 || (n > 0 && (!x || !F || !out))) return fail(SM_E_ARG, "sm_stage_power: arguments");
+    if (n) k_stage_power<<<blocks_for(n, 256), 256, 0, (hipStream_t)stream>>>((const i64*)x, (const i64*)F, (i64*)out, n, t->EXP2);
+    HIP_TRY(hipGetLastError());
+    return SM_OK;
+}
+extern "C" int sm_stage_edge(const sm_tables* t, const int64_t* h, int64_t* out, int64_t n, void* stream) {
+    if (!t || n < 0 || (n > 0 && (!h || !out))) return fail(SM_E_ARG, "sm_stage_edge: arguments");
+    if (n) k_stage_edge<<<blocks_for(n, 256), 256, 0, (hipStream_t)stream>>>((const i64*)h, (i64*)out, n, t->PHI);
+    HIP_TRY(hipGetLastError());
+    return SM_OK;
+}
+extern "C" int sm_stage_to16(const int64_t* X, int32_t rows, int32_t n, int64_t* x16, int64_t* ex, void* stream) {
+    if (rows < 0 || n <= 0 || (rows > 0 && (!X || !x16 || !ex))) return fail(SM_E_ARG, "sm_stage_to16: arguments");
+    if (rows) k_stage_rows<<<rows, NTHR, 0, (hipStream_t)stream>>>((const i64*)X, n, 0, (i64*)x16, (i64*)ex, nullptr, Tables{});
+    HIP_TRY(hipGetLastError());
+    return SM_OK;
+}
+extern "C" int sm_stage_gauge_log(const sm_tables* t, const int64_t* R, int32_t rows, int64_t* x16, int64_t* ex, int64_t* LS, void* stream) {
+    if (!t || rows < 0 || (rows > 0 && (!R || !x16 || !ex || !LS))) return fail(SM_E_ARG, "sm_stage_gauge_log: arguments");
+    if (rows) k_stage_rows<<<rows, NTHR, 0, (hipStream_t)stream>>>((const i64*)R, 768, 1, (i64*)x16, (i64*)ex, (i64*)LS, t->tb());
+    HIP_TRY(hipGetLastError());
+    return SM_OK;
+}
+extern "C" int sm_stage_race(const int64_t* v, int64_t n, int64_t* out_index, void* stream) {
+    if (n <= 0 || !v || !out_index) return fail(SM_E_ARG, "sm_stage_race: arguments");
+    k_stage_race<<<1, 1024, 0, (hipStream_t)stream>>>((const i64*)v, n, (i64*)out_index);
+    HIP_TRY(hipGetLastError());
+    return SM_OK;
+}
+extern "C" int sm_stage_attend(const sm_tables* t, const int64_t* qkv, int32_t* k16, int32_t* ek, int32_t* v, int32_t pos,
+                               int32_t ctx, int64_t* out, void* stream) {
+    if (!t || !qkv || !k16 || !ek || !v || !out || ctx <= 0 || pos < 0 || pos >= ctx || ctx > 8192)
+        return fail(SM_E_ARG, "sm_stage_attend: arguments");
+    hipStream_t s = (hipStream_t)stream;
+    HIP_TRY(hipMemcpyAsync(t->scratch, &pos, 4, hipMemcpyHostToDevice, s));
+    HIP_TRY(hipStreamSynchronize(s));
+    AttArgs a{};
+    a.QKV = (const i64*)qkv; a.K16 = k16; a.EK = ek; a.V = v; a.out = (i64*)out; a.pos = t->scratch; a.ctx = ctx;
+    a.tb = t->tb(); a.err = t->scratch + 1;
+    k_attend<<<dim3(12, 1), NTHR, (size_t)ctx * 12, s>>>(a);
+    HIP_TRY(hipGetLastError());
+    int err = 0;
+    HIP_TRY(hipMemcpyAsync(&err, t->scratch + 1, 4, hipMemcpyDeviceToHost, s));
+    HIP_TRY(hipStreamSynchronize(s));
+    if (err & SM_ERR_V32) {
+        HIP_TRY(hipMemset(t->scratch + 1, 0, 4));
+        return fail(SM_E_OVERFLOW, "sm_stage_attend: a value left 32 bits");
+    }
+    return SM_OK;
+}
+
+struct sm_plate { DevPlate P; };
+
+extern "C" int sm_plate_create(const int16_t* w, const int32_t* e, const int64_t* b, int32_t nin, int32_t nout, int32_t tile_cols, sm_plate** out) {
+    if (!w || !e || !b || !out) return fail(SM_E_ARG, "sm_plate_create: null argument");
+    if (!((nin == 768 || nin == 3072) && (tile_cols == 2 || tile_cols == 8)))
+        return fail(SM_E_ARG, "sm_plate_create: built for nin in {768, 3072} and tile_cols in {2, 8}");
+    sm_plate* p = new sm_plate();
+    int rc = upload_plate(p->P, w, e, (const i64*)b, nin, nout, tile_cols);
+    if (rc) { free_plate(p->P); delete p; return rc; }
+    *out = p;
+    return SM_OK;
+}
+extern "C" int sm_plate_destroy(sm_plate* p) {
+    if (p) { free_plate(p->P); delete p; }
+    return SM_OK;
+}
+extern "C" int64_t sm_plate_bytes(const sm_plate* p) { return p ? (int64_t)p->P.ntiles * p->P.tc * p->P.nin * 2 : 0; }
+
+extern "C" int sm_plate_product(const sm_plate* p, const int64_t* x16, int64_t* pile, int32_t grid, void* stream) {
+    if (!p || !x16 || !pile) return fail(SM_E_ARG, "sm_plate_product: null argument");
+    const DevPlate& P = p->P;
+    GemvArgs a{};
+    a.W = reinterpret_cast<const int4*>(P.W); a.we = P.e; a.bias = P.b; a.nout = P.nout; a.ntiles = P.ntiles;
+    a.X = (const i64*)x16; a.Y = (i64*)pile;
+    const int g = grid > 0 ? grid : P.ntiles;
+    hipStream_t s = (hipStream_t)stream;
+    if (P.nin == 768 && P.tc == 8) k_gemv<768, 8, PRO_X16, EPI_PILE><<<g, NTHR, 0, s>>>(a);
+    else if (P.nin == 768 && P.tc == 2) k_gemv<768, 2, PRO_X16, EPI_PILE><<<g, NTHR, 0, s>>>(a);
+    else if (P.nin == 3072 && P.tc == 2) k_gemv<3072, 2, PRO_X16, EPI_PILE><<<g, NTHR, 0, s>>>(a);
+    else k_gemv<3072, 8, PRO_X16, EPI_PILE><<<g, NTHR, 0, s>>>(a);
+    HIP_TRY(hipGetLastError());
+    return SM_OK;
+}

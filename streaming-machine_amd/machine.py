@@ -1,0 +1,236 @@
+"""ctypes binding of libsm_base2.so (include/sm_base2.h) and the host-side machine API.
+
+Machine mirrors the reference's machine (base2.py:forward and base2_stream.swift's run loop): it owns the
+device image of a base2_gpu.py directory and decodes greedy words on the GPU.  There is no CPU fallback:
+if the HIP library is missing or the device call fails, an SmError is raised.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libsm_base2.so")
+
+SM_OK, SM_E_ARG, SM_E_IO, SM_E_HIP, SM_E_OOM, SM_E_CTX, SM_E_OVERFLOW, SM_E_STATE = 0, -1, -2, -3, -4, -5, -6, -7
+CODES = {SM_E_ARG: "SM_E_ARG", SM_E_IO: "SM_E_IO", SM_E_HIP: "SM_E_HIP", SM_E_OOM: "SM_E_OOM", SM_E_CTX: "SM_E_CTX",
+         SM_E_OVERFLOW: "SM_E_OVERFLOW", SM_E_STATE: "SM_E_STATE"}
+
+READ = dict(k16=1, ek=2, v=3, resid=4, seq=5, x16=10, exls=11, pile=12, qkv=13, att=14, hid=15, rresid=16,
+            hx16=17, hexls=18, hpile=19, logits=20)
+
+
+class SmError(RuntimeError):
+    def __init__(self, code: int, msg: str):
+        super().__init__(f"{CODES.get(code, code)}: {msg}")
+        self.code = code
+
+
+class SmConfig(ctypes.Structure):
+    _fields_ = [("max_streams", ctypes.c_int32), ("max_ctx", ctypes.c_int32), ("use_graph", ctypes.c_int32),
+                ("head_grid", ctypes.c_int32)]
+
+
+_LIB = None
+vp = ctypes.c_void_p
+i32, i64 = ctypes.c_int32, ctypes.c_int64
+i32p, i64p = ctypes.POINTER(ctypes.c_int32), ctypes.POINTER(ctypes.c_int64)
+
+
+def lib():
+    """Load the HIP library (built by __graft_entry__.build()); raises if it is not there."""
+    global _LIB
+    if _LIB is None:
+        if not os.path.exists(LIB_PATH):
+            raise SmError(SM_E_IO, f"{LIB_PATH} is missing: build it (python -c 'import __graft_entry__ as g; g.build()')")
+        L = ctypes.CDLL(LIB_PATH)
+        L.sm_last_error.restype = ctypes.c_char_p
+        L.sm_create.argtypes = [ctypes.c_char_p, ctypes.POINTER(SmConfig), ctypes.POINTER(vp)]
+        L.sm_destroy.argtypes = [vp]
+        L.sm_reset.argtypes = [vp]
+        L.sm_prefill.argtypes = [vp, i32, i32p, i32]
+        L.sm_generate.argtypes = [vp, i32, i32p]
+        L.sm_record_at.argtypes = [vp, i32]
+        L.sm_read.argtypes = [vp, i32, i32, i32, i32, vp, ctypes.c_size_t]
+        L.sm_info.argtypes = [vp, i32p, i32p, i32p, i32p]
+        L.sm_tables_create.argtypes = [i64p, i64p, i32, i64p, i64p, i64, i64, ctypes.POINTER(vp)]
+        L.sm_tables_destroy.argtypes = [vp]
+        L.sm_stage_rshift.argtypes = [vp, vp, vp, i64, vp]
+        L.sm_stage_log2fix.argtypes = [vp, vp, vp, i64, vp]
+        L.sm_stage_power.argtypes = [vp, vp, vp, vp, i64, vp]
+        L.sm_stage_edge.argtypes = [vp, vp, vp, i64, vp]
+        L.sm_stage_to16.argtypes = [vp, i32, i32, vp, vp, vp]
+        L.sm_stage_gauge_log.argtypes = [vp, vp, i32, vp, vp, vp, vp]
+        L.sm_stage_race.argtypes = [vp, i64, vp, vp]
+        L.sm_stage_attend.argtypes = [vp, vp, vp, vp, vp, i32, i32, vp, vp]
+        L.sm_plate_create.argtypes = [ctypes.POINTER(ctypes.c_int16), i32p, i64p, i32, i32, i32, ctypes.POINTER(vp)]
+        L.sm_plate_destroy.argtypes = [vp]
+        L.sm_plate_product.argtypes = [vp, vp, vp, i32, vp]
+        L.sm_plate_bytes.restype = i64
+        L.sm_plate_bytes.argtypes = [vp]
+        _LIB = L
+    return _LIB
+
+
+def check(rc: int):
+    if rc != SM_OK:
+        raise SmError(rc, lib().sm_last_error().decode(errors="replace"))
+
+
+def _np(a, dtype):
+    return np.ascontiguousarray(a, dtype=dtype)
+
+
+class Machine:
+    """The integer GPT-2 machine on one MI355X.
+
+    Machine(layout_dir, max_ctx=1024, max_streams=1, use_graph=True, gauge="int", edge="int", arrival="int")
+      .stream(prompt_ids, n_words) -> list of words        (base2.py:123's loop, KV-cached on the device)
+      .forward(ids) -> word                                 (base2.py:forward's contract)
+      .reset(); .prefill(ids, stream=0); .generate(n_words) -> int32 [n_streams][n_words]
+      .record_at(pos); .read(name, layer=0, stream=0, pos=0)
+    The stage switches of base2.py:10-11 are accepted for API parity; the device machine is the integer
+    machine, so any value other than "int" raises (the float stages are diagnostics of the CPU script).
+    """
+
+    def __init__(self, layout_dir: str, max_ctx: int = 1024, max_streams: int = 1, use_graph: bool = True,
+                 head_grid: int = 0, gauge: str = "int", edge: str = "int", arrival: str = "int"):
+        for name, v in (("gauge", gauge), ("edge", edge), ("arrival", arrival)):
+            if v != "int":
+                raise NotImplementedError(f"{name}={v}: the GPU machine runs the integer stages only")
+        self.L = lib()
+        cfg = SmConfig(max_streams, max_ctx, 1 if use_graph else 0, head_grid)
+        h = vp()
+        check(self.L.sm_create(os.fsencode(layout_dir), ctypes.byref(cfg), ctypes.byref(h)))
+        self.h = h
+        v, c, s, n = i32(), i32(), i32(), i32()
+        check(self.L.sm_info(self.h, ctypes.byref(v), ctypes.byref(c), ctypes.byref(s), ctypes.byref(n)))
+        self.vocab, self.max_ctx, self.max_streams, self.n_pos = v.value, c.value, s.value, n.value
+
+    def close(self):
+        if getattr(self, "h", None):
+            self.L.sm_destroy(self.h)
+            self.h = None
+
+    __del__ = close
+
+    def reset(self):
+        check(self.L.sm_reset(self.h))
+
+    def prefill(self, ids, stream: int = 0):
+        a = _np(ids, np.int32)
+        check(self.L.sm_prefill(self.h, stream, a.ctypes.data_as(i32p), len(a)))
+
+    def generate(self, n_words: int) -> np.ndarray:
+        out = np.zeros((self.max_streams, n_words), dtype=np.int32)
+        check(self.L.sm_generate(self.h, n_words, out.ctypes.data_as(i32p)))
+        return out
+
+    def stream(self, prompt, n_words: int, stream: int = 0) -> list:
+        self.reset()
+        self.prefill(prompt, stream)
+        return [int(w) for w in self.generate(n_words)[stream]]
+
+    def forward(self, ids) -> int:
+        """base2.py:forward: the word that follows ids."""
+        return self.stream(ids, 1)[0]
+
+    def record_at(self, pos: int):
+        check(self.L.sm_record_at(self.h, pos))
+
+    def read(self, name: str, layer: int = 0, stream: int = 0, pos: int = 0) -> np.ndarray:
+        shapes = {"k16": ((768,), np.int32), "ek": ((12,), np.int32), "v": ((768,), np.int32),
+                  "resid": ((768,), np.int64), "seq": ((self.max_ctx + 1,), np.int32),
+                  "x16": ((12, 4, 3072), np.int64), "exls": ((12, 4, 2), np.int64), "pile": ((12, 4, 3072), np.int64),
+                  "qkv": ((12, 2304), np.int64), "att": ((12, 768), np.int64), "hid": ((12, 3072), np.int64),
+                  "rresid": ((12, 2, 768), np.int64), "hx16": ((768,), np.int64), "hexls": ((2,), np.int64),
+                  "hpile": ((self.vocab,), np.int64), "logits": ((self.vocab,), np.int64)}
+        shape, dt = shapes[name]
+        out = np.zeros(shape, dtype=dt)
+        check(self.L.sm_read(self.h, READ[name], layer, stream, pos, out.ctypes.data, out.nbytes))
+        return out
+
+
+class Tables:
+    """Device tables for the stage entry points (base2_convert.py:48-61)."""
+
+    def __init__(self, tabs: dict):
+        self.L = lib()
+        self._keep = [_np(tabs[k], np.int64) for k in ("phi", "arrival", "log2", "exp2")]
+        phi, arr, lg, ep = self._keep
+        h = vp()
+        check(self.L.sm_tables_create(phi.ctypes.data_as(i64p), arr.ctypes.data_as(i64p), len(arr),
+                                      lg.ctypes.data_as(i64p), ep.ctypes.data_as(i64p), int(tabs["log2_768"]),
+                                      int(tabs["eps40"]), ctypes.byref(h)))
+        self.h = h
+
+    def close(self):
+        if getattr(self, "h", None):
+            self.L.sm_tables_destroy(self.h)
+            self.h = None
+
+    __del__ = close
+
+
+class Plate:
+    """A plate on the device laid out for the GEMV (input-major int16 [nin][nout] on the host)."""
+
+    def __init__(self, w, e, b, tile_cols: int = 8):
+        self.L = lib()
+        w = _np(w, np.int16)
+        self.nin, self.nout = w.shape
+        e = _np(e, np.int32)
+        b = _np(b, np.int64)
+        h = vp()
+        check(self.L.sm_plate_create(w.ctypes.data_as(ctypes.POINTER(ctypes.c_int16)), e.ctypes.data_as(i32p),
+                                     b.ctypes.data_as(i64p), self.nin, self.nout, tile_cols, ctypes.byref(h)))
+        self.h = h
+        self.bytes = int(self.L.sm_plate_bytes(self.h))
+
+    def product(self, x16_ptr: int, pile_ptr: int, grid: int = 0, stream: int = 0):
+        check(self.L.sm_plate_product(self.h, x16_ptr, pile_ptr, grid, stream))
+
+    def close(self):
+        if getattr(self, "h", None):
+            self.L.sm_plate_destroy(self.h)
+            self.h = None
+
+    __del__ = close
+
+
+class stages:
+    """base2.py's stage functions on device buffers (pointers to device memory; stream = hipStream_t or 0)."""
+
+    @staticmethod
+    def rshift(x, s, out, n, stream=0):
+        check(lib().sm_stage_rshift(x, s, out, n, stream))
+
+    @staticmethod
+    def log2fix(t: Tables, v, out, n, stream=0):
+        check(lib().sm_stage_log2fix(t.h, v, out, n, stream))
+
+    @staticmethod
+    def power(t: Tables, x, F, out, n, stream=0):
+        check(lib().sm_stage_power(t.h, x, F, out, n, stream))
+
+    @staticmethod
+    def edge(t: Tables, h, out, n, stream=0):
+        check(lib().sm_stage_edge(t.h, h, out, n, stream))
+
+    @staticmethod
+    def to16(X, rows, n, x16, ex, stream=0):
+        check(lib().sm_stage_to16(X, rows, n, x16, ex, stream))
+
+    @staticmethod
+    def gauge_log(t: Tables, R, rows, x16, ex, LS, stream=0):
+        check(lib().sm_stage_gauge_log(t.h, R, rows, x16, ex, LS, stream))
+
+    @staticmethod
+    def race(v, n, out, stream=0):
+        check(lib().sm_stage_race(v, n, out, stream))
+
+    @staticmethod
+    def attend(t: Tables, qkv, k16, ek, v, pos, ctx, out, stream=0):
+        check(lib().sm_stage_attend(t.h, qkv, k16, ek, v, pos, ctx, out, stream))

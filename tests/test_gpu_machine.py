@@ -1,0 +1,149 @@
+"""GPU parity of the whole decode step through the C ABI: emitted words, every recorded intermediate and the KV
+cache, bit-exact against base2.py's golden vectors and the oracle."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from conftest import golden_case, h64
+
+pytestmark = pytest.mark.gpu
+
+BANKS = ("qkv", "proj", "fc", "mproj")
+NIN = (768, 768, 768, 3072)
+NOUT = (2304, 768, 3072, 768)
+
+
+def machine_record(m) -> dict:
+    """the device record of one position, keyed like the golden fixture"""
+    x16, exls, pile = m.read("x16"), m.read("exls"), m.read("pile")
+    qkv, att, hid, rr = m.read("qkv"), m.read("att"), m.read("hid"), m.read("rresid")
+    out = {}
+    for l in range(12):
+        for k, b in enumerate(BANKS):
+            out[f"x16.{b}.{l}"] = h64(x16[l, k, :NIN[k]])
+            out[f"pile.{b}.{l}"] = h64(pile[l, k, :NOUT[k]])
+            out[f"ex.{b}.{l}"] = int(exls[l, k, 0])
+            if b in ("qkv", "fc"):
+                out[f"ls.{b}.{l}"] = int(exls[l, k, 1])
+        out[f"out.qkv.{l}"] = h64(qkv[l])
+        out[f"att.{l}"] = h64(att[l])
+        out[f"hid.{l}"] = h64(hid[l])
+        out[f"resid_attn.{l}"] = h64(rr[l, 0])
+        out[f"resid_mlp.{l}"] = h64(rr[l, 1])
+        out[f"out.mproj.{l}"] = h64(rr[l, 1] - rr[l, 0])             # the MLP half's addition
+        if l:
+            out[f"out.proj.{l}"] = h64(rr[l, 0] - rr[l - 1, 1])      # the attention half's addition
+    hexls = m.read("hexls")
+    out["x16.head"] = h64(m.read("hx16"))
+    out["ex.head"], out["ls.head"] = int(hexls[0]), int(hexls[1])
+    out["pile.head"] = h64(m.read("hpile"))
+    out["logits"] = h64(m.read("logits"))
+    return out
+
+
+def compare_record(got: dict, want: dict):
+    keys = [k for k in want if k in got]
+    assert len(keys) > 200
+    bad = [k for k in keys if got[k] != want[k]]
+    assert not bad, f"{len(bad)} intermediates differ, first: {sorted(bad)[:8]}"
+
+
+@pytest.mark.parametrize("use_graph", [True, False])
+def test_small_model_words(sm, small_dir, golden, use_graph):
+    c = golden_case(golden, "small_p8_w8")
+    m = sm.Machine(small_dir, max_ctx=64, use_graph=use_graph)
+    assert m.stream(c["prompt"], len(c["words"])) == c["words"]
+    m.close()
+
+
+def test_small_model_record(sm, small_dir, golden):
+    c = golden_case(golden, "small_p8_w8")
+    m = sm.Machine(small_dir, max_ctx=64)
+    last = c["records"]["last"]
+    m.reset()
+    m.record_at(last["position"])
+    m.prefill(c["prompt"])
+    m.generate(len(c["words"]))
+    compare_record(machine_record(m), last)
+    m.close()
+
+
+@pytest.fixture(scope="module")
+def full_machine(sm, full_dir):
+    m = sm.Machine(full_dir, max_ctx=1024)
+    yield m
+    m.close()
+
+
+def test_config1_words_and_records(full_machine, golden):
+    """GPT-2 124M, batch 1, 8-token prompt, 16 greedy words: the words and every intermediate of the first and
+    the last position against base2.py"""
+    m = full_machine
+    c = golden_case(golden, "c1_p8_w16")
+    for which in ("first", "last"):
+        rec = c["records"][which]
+        m.reset()
+        m.record_at(rec["position"])
+        m.prefill(c["prompt"])
+        assert [int(w) for w in m.generate(len(c["words"]))[0]] == c["words"]
+        compare_record(machine_record(m), rec)
+
+
+@pytest.mark.parametrize("stream", [0, 1])
+def test_config4_prompts(full_machine, golden, stream):
+    """32-token prompts of the batched config, one stream at a time"""
+    c = golden_case(golden, f"c4_stream{stream}_p32_w4")
+    assert full_machine.stream(c["prompt"], len(c["words"])) == c["words"]
+
+
+def test_kv_cache_matches_oracle(full_machine, full_oracle, sm):
+    """the cache the device keeps equals the oracle's (k16, ek, v at every layer and position)"""
+    m = full_machine
+    prompt = sm.prompt_ids(7, 5)
+    words = m.stream(prompt, 6)
+    s = full_oracle.session(32)
+    seq = prompt + words
+    ow = []
+    for i, t in enumerate(seq[:-1]):
+        w = s.step(t, want_head=i >= len(prompt) - 1)
+        if i >= len(prompt) - 1:
+            ow.append(w)
+    assert ow == words
+    for l in (0, 5, 11):
+        for p in (0, 3, len(seq) - 2):
+            k16, ek, v = s.read_kv(l, p)
+            assert np.array_equal(m.read("k16", l, 0, p), k16)
+            assert np.array_equal(m.read("ek", l, 0, p), ek)
+            assert np.array_equal(m.read("v", l, 0, p), v)
+    assert np.array_equal(m.read("resid"), s.resid())
+
+
+def test_long_context_against_oracle(full_machine, full_oracle, sm):
+    """a 200-token prompt and 40 words (context 240): words equal the KV-cached oracle's"""
+    prompt = sm.prompt_ids(9, 200)
+    assert full_machine.stream(prompt, 40) == full_oracle.generate(prompt, 40, 256)
+
+
+def test_prompt_of_one_word_and_continuation(full_machine, full_oracle, sm):
+    m = full_machine
+    m.reset()
+    m.prefill([464])
+    a = [int(w) for w in m.generate(3)[0]]
+    b = [int(w) for w in m.generate(2)[0]]        # continues where it stopped
+    assert a + b == full_oracle.generate([464], 5)
+
+
+def test_errors(full_machine, sm):
+    m = full_machine
+    m.reset()
+    with pytest.raises(sm.SmError) as e:
+        m.prefill([50257])
+    assert e.value.code == -1
+    with pytest.raises(sm.SmError) as e:
+        m.generate(2)                             # no prompt
+    assert e.value.code == -7
+    m.prefill(list(range(1000)))
+    with pytest.raises(sm.SmError) as e:
+        m.generate(100)                           # 1000 + 100 - 1 > 1024
+    assert e.value.code == -5
