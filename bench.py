@@ -1,0 +1,195 @@
+"""Decode benchmark of the integer ("all base 2") GPT-2 124M machine on one MI355X.
+
+Workload (the batch-1 configuration the metric is quoted on): GPT-2 124M shape, random-init N(0, 0.02) weights
+from seed 0 converted to int16 plates with per-column powers of two; batch 1; an 8-token prompt drawn from
+default_rng(1); 16 greedy words per sequence, i.e. the prompt pass plus 15 decode steps at context 9..23.
+A "step" is one decode position (one new word).  The timed region covers exactly --steps decode steps, in
+sequences of 15 (each sequence's prompt pass runs untimed first), with the weights, tables and KV cache resident
+in HBM.  Before any number is printed the emitted words are checked against the CPU oracle.
+
+Printed: one JSON line with the driver's fields plus
+  roofline      the head kernel (the largest single launch: the 768 x 50257 plate read + race), its mean
+                duration from HIP event pairs recorded around every head launch inside the timed region
+  step_roofline the whole decode step's algorithmic bytes over its measured time
+  cpu_baseline  base2.py's CPU path restated in numpy (full recompute per word, float64 products, the
+                top-down race loop), timed on a bounded sample of the same sequence on the host cores
+"""
+from __future__ import annotations
+
+import argparse
+import importlib.util
+import json
+import os
+import sys
+import tempfile
+import time
+
+import numpy as np
+
+REPO = os.path.dirname(os.path.abspath(__file__))
+METRIC = "decode tokens/s, GPT-2-124M int base-2, B=1 & B=64; % HBM roofline"
+HBM_PEAK_GBS = 8000.0
+WORDS = 16          # words per sequence (the prompt pass gives the first)
+PROMPT = 8
+
+
+def load_sm():
+    if "streaming_machine_amd" in sys.modules:
+        return sys.modules["streaming_machine_amd"]
+    root = os.path.join(REPO, "streaming-machine_amd")
+    spec = importlib.util.spec_from_file_location("streaming_machine_amd", os.path.join(root, "__init__.py"),
+                                                  submodule_search_locations=[root])
+    mod = importlib.util.module_from_spec(spec)
+    sys.modules["streaming_machine_amd"] = mod
+    spec.loader.exec_module(mod)
+    return mod
+
+
+def log(msg):
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def head_bytes(vocab: int) -> int:
+    """algorithmic bytes of one head launch: the int16 plate plus an int32 exponent and an int64 bias per word"""
+    return 2 * 768 * vocab + 12 * vocab
+
+
+def step_bytes(vocab: int, ctx: float) -> float:
+    """algorithmic bytes of one decode step: every plate once (int16), the per-column exponents and biases,
+    and the KV cache read at context ctx (int32 k16 and v per layer)"""
+    layer_w = 2 * (768 * 2304 + 768 * 768 + 768 * 3072 + 3072 * 768)
+    layer_cols = 12 * (2304 + 768 + 3072 + 768)
+    return 12 * (layer_w + layer_cols) + head_bytes(vocab) + 12 * 768 * 8 * ctx
+
+
+def cpu_baseline(npz, prompt, want, budget_s: float = 20.0):
+    """base2.py's CPU path (numpy restatement): forward(ids + got) per word, as base2.py:123 does."""
+    sys.path.insert(0, REPO)
+    from oracle.base2_np import Base2Numpy
+    try:
+        from threadpoolctl import threadpool_info
+        blas = [i for i in threadpool_info() if i.get("user_api") == "blas"]
+        cores = int(blas[0]["num_threads"]) if blas else 1
+    except Exception:
+        cores = 1
+    nb = Base2Numpy(npz)
+    got, t_total, n = [], 0.0, 0
+    for i in range(len(want)):
+        t0 = time.perf_counter()
+        w = nb.forward(list(prompt) + got)
+        dt = time.perf_counter() - t0
+        got.append(w)
+        if i > 0:                       # decode words only (the first word is the prompt pass)
+            t_total += dt
+            n += 1
+        if t_total > budget_s and n >= 2:
+            break
+    if got != want[:len(got)]:
+        raise RuntimeError(f"cpu baseline words differ from the oracle: {got} vs {want[:len(got)]}")
+    return {"value": n / t_total, "unit": "tokens/s", "cores": cores, "kind": "port",
+            "sample": f"words 2..{n + 1} of the 8-token-prompt sequence, full recompute per word (context 9..{8 + n}), "
+                      f"numpy float64-BLAS products and the top-down race loop"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=150)
+    ap.add_argument("--warmup", type=int, default=15)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--head-grid", type=int, default=0)
+    ap.add_argument("--layout", default="", help="reuse a layout directory (else one is built in a temp dir)")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported (the batched streams would "
+              f"shard as independent replicas, see DESIGN.md)", file=sys.stderr)
+        sys.exit(2)
+    if args.steps <= 0 or args.warmup < 0:
+        sys.exit("bench.py: --steps must be positive and --warmup non-negative")
+
+    sm = load_sm()
+    sys.path.insert(0, REPO)
+    import oracle
+
+    t0 = time.time()
+    sd = sm.random_gpt2(seed=0)
+    npz = sm.convert(sd)
+    del sd
+    lay = args.layout or tempfile.mkdtemp(prefix="sm_bench_")
+    if not os.path.exists(os.path.join(lay, "manifest.json")):
+        sm.layout(npz, lay)
+    log(f"model converted and laid out in {time.time() - t0:.1f}s")
+    prompt = sm.prompt_ids(1, PROMPT)
+
+    # the oracle's words for the sequence (parity gate)
+    orc = oracle.Oracle(npz)
+    want = orc.generate(prompt, WORDS)
+    log(f"oracle words: {want}")
+
+    import torch
+    m = sm.Machine(lay, max_ctx=64, head_grid=args.head_grid, graph_steps=WORDS - 1, profile=True)
+    vocab = m.vocab
+
+    def sequence(timed: bool):
+        m.reset()
+        m.prefill(prompt)
+        first = int(m.generate(1)[0, 0])
+        torch.cuda.synchronize()
+        m.profile(clear=True)
+        t = time.perf_counter()
+        rest = [int(w) for w in m.generate(WORDS - 1)[0]]
+        torch.cuda.synchronize()
+        dt = time.perf_counter() - t
+        words = [first] + rest
+        if words != want:
+            raise RuntimeError(f"GPU words differ from the oracle: {words} vs {want}")
+        n, us = m.profile(clear=True)
+        return dt, n, us
+
+    for _ in range(max(1, -(-args.warmup // (WORDS - 1)))):
+        sequence(False)
+    total, steps, head_n, head_us_sum = 0.0, 0, 0, 0.0
+    while steps < args.steps:
+        dt, n, us = sequence(True)
+        k = min(WORDS - 1, args.steps - steps)
+        total += dt * k / (WORDS - 1)
+        steps += k
+        head_n += n
+        head_us_sum += us * n
+    head_us = head_us_sum / head_n
+    ms_per_step = 1000.0 * total / steps
+    tok_s = steps / total
+    hb = head_bytes(vocab)
+    ach = hb / (head_us * 1e-6) / 1e9
+    ctx_mean = PROMPT + WORDS / 2.0
+    sb = step_bytes(vocab, ctx_mean)
+    step_ach = sb / (ms_per_step * 1e-3) / 1e9
+
+    traffic = None
+    tfile = os.path.join(REPO, "profiles", "head_gemv_traffic.txt")
+    if os.path.exists(tfile):
+        for line in open(tfile):
+            if line.startswith("traffic_bytes_per_launch:"):
+                traffic = int(float(line.split(":")[1]))
+
+    cpu = None if args.no_cpu else cpu_baseline(npz, prompt, want)
+    out = {
+        "metric": METRIC, "value": round(tok_s, 2), "unit": "tokens/s", "n_gpus": 1, "steps": steps,
+        "warmup": args.warmup, "ms_per_step": round(ms_per_step, 4), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "int64", "data": "synthetic",
+        "config": {"workload": "GPT-2 124M integer base-2 decode, batch 1, 8-token random prompt, 16 greedy words "
+                               "per sequence (15 decode steps, context 9..23), random-init N(0,0.02) seed 0",
+                   "batch": 1, "prompt": PROMPT, "words": WORDS, "vocab": vocab},
+        "roofline": {"bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": traffic,
+                     "kernel": "k_gemv<768,8,PRO_GAUGE,EPI_HEAD> (head plate read + race)",
+                     "bytes_per_launch": hb, "mean_launch_us": round(head_us, 3), "launches_timed": head_n},
+        "step_roofline": {"bytes_per_step": int(sb), "achieved": round(step_ach, 1), "frac": round(step_ach / HBM_PEAK_GBS, 4)},
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(out), flush=True)
+    m.close()
+
+
+if __name__ == "__main__":
+    main()

@@ -38,8 +38,10 @@ typedef struct sm_machine sm_machine;
 typedef struct {
     int32_t max_streams;   /* B: independent streams decoded in lockstep (1 = the batch-1 path) */
     int32_t max_ctx;       /* positions per stream, at most the position table's rows */
-    int32_t use_graph;     /* 1: replay each decode step as one captured HIP graph; 0: plain launches */
+    int32_t use_graph;     /* 1: replay captured HIP graphs of decode steps; 0: plain launches */
     int32_t head_grid;     /* blocks of the head's plate read (0: default) */
+    int32_t graph_steps;   /* decode steps per captured graph (0: 16) */
+    int32_t profile;       /* 1: time every head launch with a HIP event pair on the machine's stream */
 } sm_config;
 
 /* Replaces base2_stream.swift:151-208 (device, pipelines, loading base2_gpu/ and its buffers) and
@@ -87,6 +89,10 @@ enum {
 /* Copies one device array to host memory dst (bytes must match).  Replaces reading MTLBuffer contents
  * (base2_stream.swift:282-286) for per-intermediate parity. */
 int sm_read(sm_machine* m, int32_t what, int32_t layer, int32_t stream, int32_t pos, void* dst, size_t bytes);
+
+/* Head-launch timing gathered with profile = 1: launches seen and their summed duration (microseconds,
+ * HIP events on the machine's stream).  Replaces fr2's bench= timing (base2_stream_fr2.swift:1060-1075). */
+int sm_profile(sm_machine* m, int64_t* n_heads, double* head_us, int32_t clear);
 
 /* Facts about a created machine: vocab, max_ctx, max_streams, n_ctx of the position table. */
 int sm_info(const sm_machine* m, int32_t* vocab, int32_t* max_ctx, int32_t* max_streams, int32_t* n_pos);

@@ -7,9 +7,9 @@
 //                                 plain, added to the stream)  ->  fc (gauge + product + gauged + edge)  ->
 //                                 mproj (to16 + product + plain, added)
 //     head (gauge + product + gauged + standing amount + race; the word goes straight back into seq)
-// i.e. 61 launches with the device-side position advancing in the head, so one captured HIP graph replays
-// every step; the host synchronises once per sm_generate call (base2_stream.swift:273-281 commits one
-// command buffer per prompt the same way).
+// i.e. 61 launches with the device-side position advancing in the head, so a captured HIP graph of
+// graph_steps consecutive steps replays the loop; the host synchronises once per sm_generate call
+// (base2_stream.swift:273-281 commits one command buffer per prompt the same way).
 #include "sm_kernels.hip"
 #include "../../include/sm_base2.h"
 
@@ -158,8 +158,14 @@ struct sm_machine {
     // record
     i64 *r_x16 = nullptr, *r_exls = nullptr, *r_pile = nullptr, *r_qkv = nullptr, *r_att = nullptr, *r_hid = nullptr,
         *r_resid = nullptr, *r_hx16 = nullptr, *r_hexls = nullptr, *r_hpile = nullptr, *r_logits = nullptr;
-    hipGraphExec_t gexec = nullptr;
-    hipGraph_t graph = nullptr;
+    // captured decode steps: [0] graph_steps whole steps, [1] one whole step, [2] one step's layers, [3] its head
+    hipGraphExec_t gexec[4] = {nullptr, nullptr, nullptr, nullptr};
+    hipGraph_t graph[4] = {nullptr, nullptr, nullptr, nullptr};
+    int gsteps = 16;
+    // profiling: an event pair around each step's head kernel (the largest single launch)
+    std::vector<hipEvent_t> ev_s, ev_e;
+    double prof_head_us = 0.0;
+    long long prof_n = 0;
     // host mirror
     int h_plen = 0, h_pos = 0, h_words = 0;
     std::vector<std::vector<int>> prompts;
@@ -229,8 +235,12 @@ static int parse_manifest(const std::string& text, std::vector<BankInfo>& banks,
 
 static void machine_free(sm_machine* m) {
     if (!m) return;
-    if (m->gexec) (void)hipGraphExecDestroy(m->gexec);
-    if (m->graph) (void)hipGraphDestroy(m->graph);
+    for (int i = 0; i < 4; i++) {
+        if (m->gexec[i]) (void)hipGraphExecDestroy(m->gexec[i]);
+        if (m->graph[i]) (void)hipGraphDestroy(m->graph[i]);
+    }
+    for (auto e : m->ev_s) (void)hipEventDestroy(e);
+    for (auto e : m->ev_e) (void)hipEventDestroy(e);
     for (int l = 0; l < 12; l++)
         for (int k = 0; k < 4; k++) free_plate(m->bank[l][k]);
     free_plate(m->head);
@@ -243,11 +253,12 @@ static void machine_free(sm_machine* m) {
     delete m;
 }
 
-// the launch sequence of one decode step (all streams, one position each)
-static int launch_step(sm_machine* m) {
+// the launch sequence of one decode step (all streams, one position each): the layers and/or the head
+enum { STEP_ALL = 3, STEP_LAYERS = 1, STEP_HEAD = 2 };
+static int launch_step(sm_machine* m, int parts = STEP_ALL) {
     const Tables tb = m->T.tb();
     int* ctl = m->ctl;
-    for (int l = 0; l < 12; l++) {
+    for (int l = 0; l < 12 && (parts & STEP_LAYERS); l++) {
         GemvArgs base{};
         base.tb = tb;
         base.pos = ctl + CTL_POS;
@@ -305,7 +316,7 @@ static int launch_step(sm_machine* m) {
         }
     }
     // head: gauge, product with the tied word table, power + standing amount, race (base2.py:107-114)
-    {
+    if (parts & STEP_HEAD) {
         GemvArgs a{};
         a.tb = tb;
         a.pos = ctl + CTL_POS; a.rec_pos = ctl + CTL_RECPOS;
@@ -324,7 +335,7 @@ static int launch_step(sm_machine* m) {
 extern "C" int sm_create(const char* layout_dir, const sm_config* cfg, sm_machine** out) {
     if (!layout_dir || !out) return fail(SM_E_ARG, "sm_create: null argument");
     *out = nullptr;
-    sm_config c{1, 1024, 1, 0};
+    sm_config c{1, 1024, 1, 0, 16, 0};
     if (cfg) c = *cfg;
     if (c.max_streams != 1) return fail(SM_E_ARG, "sm_create: this build decodes one stream per machine (max_streams = 1)");
     if (c.max_ctx <= 0) return fail(SM_E_ARG, "sm_create: max_ctx must be positive");
@@ -405,6 +416,15 @@ extern "C" int sm_create(const char* layout_dir, const sm_config* cfg, sm_machin
         (rc = dalloc(&m->r_logits, (size_t)m->vocab)))
         return bail(rc);
     m->prompts.assign(B, {});
+    m->gsteps = c.graph_steps > 0 ? c.graph_steps : 16;
+    if (m->gsteps > 256) return bail(fail(SM_E_ARG, "sm_create: graph_steps at most 256"));
+    if (c.profile) {
+        m->ev_s.resize(m->gsteps);
+        m->ev_e.resize(m->gsteps);
+        for (int i = 0; i < m->gsteps; i++)
+            if (hipEventCreate(&m->ev_s[i]) != hipSuccess || hipEventCreate(&m->ev_e[i]) != hipSuccess)
+                return bail(fail(SM_E_HIP, "hipEventCreate"));
+    }
     if ((rc = sm_reset(m))) return bail(rc);
     *out = m;
     return SM_OK;
@@ -454,16 +474,48 @@ extern "C" int sm_record_at(sm_machine* m, int32_t pos) {
     return SM_OK;
 }
 
-static int ensure_graph(sm_machine* m) {
-    if (m->gexec) return SM_OK;
+// capture n consecutive launch sequences (parts of a step) into graph slot `which`
+static int capture(sm_machine* m, int which, int n, int parts) {
+    if (m->gexec[which]) return SM_OK;
     HIP_TRY(hipStreamBeginCapture(m->st, hipStreamCaptureModeThreadLocal));
-    int rc = launch_step(m);
+    int rc = SM_OK;
+    for (int s = 0; s < n && !rc; s++) rc = launch_step(m, parts);
     hipGraph_t g = nullptr;
     hipError_t e = hipStreamEndCapture(m->st, &g);
     if (rc) { if (g) (void)hipGraphDestroy(g); return rc; }
     if (e != hipSuccess) return fail(SM_E_HIP, std::string("hipStreamEndCapture: ") + hipGetErrorString(e));
-    m->graph = g;
-    HIP_TRY(hipGraphInstantiate(&m->gexec, g, nullptr, nullptr, 0));
+    m->graph[which] = g;
+    HIP_TRY(hipGraphInstantiate(&m->gexec[which], g, nullptr, nullptr, 0));
+    return SM_OK;
+}
+
+// one profiled step: the layers, then the head bracketed by HIP events recorded on the machine's stream
+static int profiled_step(sm_machine* m, int slot) {
+    int rc;
+    if (m->cfg.use_graph) {
+        if ((rc = capture(m, 2, 1, STEP_LAYERS)) || (rc = capture(m, 3, 1, STEP_HEAD))) return rc;
+        HIP_TRY(hipGraphLaunch(m->gexec[2], m->st));
+        HIP_TRY(hipEventRecord(m->ev_s[slot], m->st));
+        HIP_TRY(hipGraphLaunch(m->gexec[3], m->st));
+        HIP_TRY(hipEventRecord(m->ev_e[slot], m->st));
+    } else {
+        if ((rc = launch_step(m, STEP_LAYERS))) return rc;
+        HIP_TRY(hipEventRecord(m->ev_s[slot], m->st));
+        if ((rc = launch_step(m, STEP_HEAD))) return rc;
+        HIP_TRY(hipEventRecord(m->ev_e[slot], m->st));
+    }
+    return SM_OK;
+}
+
+// wait for the n profiled steps just queued and add their head durations
+static int collect(sm_machine* m, int n) {
+    HIP_TRY(hipStreamSynchronize(m->st));
+    for (int s = 0; s < n; s++) {
+        float ms = 0.f;
+        HIP_TRY(hipEventElapsedTime(&ms, m->ev_s[s], m->ev_e[s]));
+        m->prof_head_us += 1000.0 * ms;
+        m->prof_n++;
+    }
     return SM_OK;
 }
 
@@ -478,26 +530,45 @@ extern "C" int sm_generate(sm_machine* m, int32_t n_words, int32_t* out) {
         HIP_TRY(hipMemcpyAsync(m->ctl + CTL_PLEN, &m->h_plen, 4, hipMemcpyHostToDevice, m->st));
     }
     const int target = m->h_words + n_words;
-    const int steps = (m->h_plen - 1 + target) - m->h_pos;
+    int steps = (m->h_plen - 1 + target) - m->h_pos;
     if (m->h_plen - 1 + target > m->ctx) return fail(SM_E_CTX, "sm_generate: prompt + words would pass max_ctx");
+    const int total = steps;
     int rc;
-    if (m->cfg.use_graph) {
-        if ((rc = ensure_graph(m))) return rc;
-        for (int s = 0; s < steps; s++) HIP_TRY(hipGraphLaunch(m->gexec, m->st));
+    if (m->cfg.profile) {
+        while (steps > 0) {
+            const int n = steps < m->gsteps ? steps : m->gsteps;
+            for (int s = 0; s < n; s++)
+                if ((rc = profiled_step(m, s))) return rc;
+            if ((rc = collect(m, n))) return rc;
+            steps -= n;
+        }
+    } else if (m->cfg.use_graph) {
+        if (steps >= m->gsteps && (rc = capture(m, 0, m->gsteps, STEP_ALL))) return rc;
+        for (; steps >= m->gsteps; steps -= m->gsteps) HIP_TRY(hipGraphLaunch(m->gexec[0], m->st));
+        if (steps > 0 && (rc = capture(m, 1, 1, STEP_ALL))) return rc;
+        for (; steps > 0; steps--) HIP_TRY(hipGraphLaunch(m->gexec[1], m->st));
     } else {
-        for (int s = 0; s < steps; s++)
+        for (; steps > 0; steps--)
             if ((rc = launch_step(m))) return rc;
     }
     HIP_TRY(hipStreamSynchronize(m->st));
     int ctl[CTL_N];
     HIP_TRY(hipMemcpy(ctl, m->ctl, sizeof(ctl), hipMemcpyDeviceToHost));
-    m->h_pos += steps;
+    m->h_pos += total;
     m->h_words = target;
     if (ctl[CTL_POS] != m->h_pos) return fail(SM_E_STATE, "sm_generate: device position disagrees with the host");
     if (ctl[CTL_ERR] & SM_ERR_V32) return fail(SM_E_OVERFLOW, "sm_generate: an attention value left 32 bits (the V cache holds int32)");
     for (int b = 0; b < m->B; b++)
         HIP_TRY(hipMemcpy(out + (size_t)b * n_words, m->words + (size_t)b * (m->ctx + 1) + (target - n_words), (size_t)n_words * 4,
                           hipMemcpyDeviceToHost));
+    return SM_OK;
+}
+
+extern "C" int sm_profile(sm_machine* m, int64_t* n_heads, double* head_us, int32_t clear) {
+    if (!m) return fail(SM_E_ARG, "sm_profile: null machine");
+    if (n_heads) *n_heads = m->prof_n;
+    if (head_us) *head_us = m->prof_head_us;
+    if (clear) { m->prof_n = 0; m->prof_head_us = 0.0; }
     return SM_OK;
 }
 

@@ -30,7 +30,7 @@ class SmError(RuntimeError):
 
 class SmConfig(ctypes.Structure):
     _fields_ = [("max_streams", ctypes.c_int32), ("max_ctx", ctypes.c_int32), ("use_graph", ctypes.c_int32),
-                ("head_grid", ctypes.c_int32)]
+                ("head_grid", ctypes.c_int32), ("graph_steps", ctypes.c_int32), ("profile", ctypes.c_int32)]
 
 
 _LIB = None
@@ -55,6 +55,7 @@ def lib():
         L.sm_record_at.argtypes = [vp, i32]
         L.sm_read.argtypes = [vp, i32, i32, i32, i32, vp, ctypes.c_size_t]
         L.sm_info.argtypes = [vp, i32p, i32p, i32p, i32p]
+        L.sm_profile.argtypes = [vp, i64p, ctypes.POINTER(ctypes.c_double), i32]
         L.sm_tables_create.argtypes = [i64p, i64p, i32, i64p, i64p, i64, i64, ctypes.POINTER(vp)]
         L.sm_tables_destroy.argtypes = [vp]
         L.sm_stage_rshift.argtypes = [vp, vp, vp, i64, vp]
@@ -96,12 +97,13 @@ class Machine:
     """
 
     def __init__(self, layout_dir: str, max_ctx: int = 1024, max_streams: int = 1, use_graph: bool = True,
-                 head_grid: int = 0, gauge: str = "int", edge: str = "int", arrival: str = "int"):
+                 head_grid: int = 0, graph_steps: int = 16, profile: bool = False,
+                 gauge: str = "int", edge: str = "int", arrival: str = "int"):
         for name, v in (("gauge", gauge), ("edge", edge), ("arrival", arrival)):
             if v != "int":
                 raise NotImplementedError(f"{name}={v}: the GPU machine runs the integer stages only")
         self.L = lib()
-        cfg = SmConfig(max_streams, max_ctx, 1 if use_graph else 0, head_grid)
+        cfg = SmConfig(max_streams, max_ctx, 1 if use_graph else 0, head_grid, graph_steps, 1 if profile else 0)
         h = vp()
         check(self.L.sm_create(os.fsencode(layout_dir), ctypes.byref(cfg), ctypes.byref(h)))
         self.h = h
@@ -136,6 +138,12 @@ class Machine:
     def forward(self, ids) -> int:
         """base2.py:forward: the word that follows ids."""
         return self.stream(ids, 1)[0]
+
+    def profile(self, clear: bool = True):
+        """(head launches timed, their mean duration in microseconds) since the last clear"""
+        n, us = ctypes.c_int64(), ctypes.c_double()
+        check(self.L.sm_profile(self.h, ctypes.byref(n), ctypes.byref(us), 1 if clear else 0))
+        return n.value, (us.value / n.value if n.value else float("nan"))
 
     def record_at(self, pos: int):
         check(self.L.sm_record_at(self.h, pos))

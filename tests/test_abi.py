@@ -1,0 +1,60 @@
+"""The C ABI without a GPU: the library loads, exports every function include/sm_base2.h declares, and the
+host-side error paths (which fail before any device call) report the documented codes."""
+from __future__ import annotations
+
+import ctypes
+import json
+import os
+import re
+
+import pytest
+
+from conftest import REPO
+
+HEADER = os.path.join(REPO, "include", "sm_base2.h")
+
+
+def declared():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(sm_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_header_declares_the_entry_points():
+    names = declared()
+    for n in ("sm_create", "sm_destroy", "sm_reset", "sm_prefill", "sm_generate", "sm_read", "sm_record_at",
+              "sm_last_error", "sm_stage_attend", "sm_plate_product", "sm_profile"):
+        assert n in names
+
+
+def test_library_exports_every_declared_symbol(sm):
+    L = sm.lib()
+    missing = [n for n in declared() if not hasattr(L, n)]
+    assert missing == []
+
+
+def test_create_reports_io_errors_before_any_device_call(sm, tmp_path):
+    with pytest.raises(sm.SmError) as e:
+        sm.Machine(str(tmp_path / "no_such_dir"))
+    assert e.value.code == -2 and "manifest.json" in str(e.value)
+    (tmp_path / "manifest.json").write_text(json.dumps({"banks": [], "log2_768": 1}))
+    with pytest.raises(sm.SmError) as e:
+        sm.Machine(str(tmp_path))
+    assert e.value.code == -2
+
+
+def test_float_switches_are_not_silently_routed(sm, tmp_path):
+    with pytest.raises(NotImplementedError):
+        sm.Machine(str(tmp_path), gauge="float")
+
+
+def test_last_error_is_a_string(sm):
+    L = sm.lib()
+    assert isinstance(L.sm_last_error(), bytes)
+
+
+def test_null_arguments(sm):
+    L = sm.lib()
+    assert L.sm_create(None, None, None) == -1
+    assert L.sm_reset(None) == -1
+    assert L.sm_generate(None, 1, None) == -1

@@ -147,3 +147,13 @@ def test_errors(full_machine, sm):
     with pytest.raises(sm.SmError) as e:
         m.generate(100)                           # 1000 + 100 - 1 > 1024
     assert e.value.code == -5
+
+
+@pytest.mark.parametrize("use_graph", [True, False])
+def test_profiled_machine_gives_the_same_words(sm, full_dir, golden, use_graph):
+    c = golden_case(golden, "c1_p8_w16")
+    m = sm.Machine(full_dir, max_ctx=64, profile=True, graph_steps=4, use_graph=use_graph)
+    assert m.stream(c["prompt"], len(c["words"])) == c["words"]
+    n, us = m.profile()
+    assert n == len(c["prompt"]) + len(c["words"]) - 1 and us > 0
+    m.close()
