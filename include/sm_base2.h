@@ -42,6 +42,8 @@ typedef struct {
     int32_t head_grid;     /* blocks of the head's plate read (0: default) */
     int32_t graph_steps;   /* decode steps per captured graph (0: 16) */
     int32_t profile;       /* 1: time every head launch with a HIP event pair on the machine's stream */
+    int32_t table_mode;    /* 0: read the tables from memory; 1: recompute each entry from its formula when every
+                              loaded entry matches it (checked on the device at create), else read the tables */
 } sm_config;
 
 /* Replaces base2_stream.swift:151-208 (device, pipelines, loading base2_gpu/ and its buffers) and
@@ -94,8 +96,10 @@ int sm_read(sm_machine* m, int32_t what, int32_t layer, int32_t stream, int32_t 
  * HIP events on the machine's stream).  Replaces fr2's bench= timing (base2_stream_fr2.swift:1060-1075). */
 int sm_profile(sm_machine* m, int64_t* n_heads, double* head_us, int32_t clear);
 
-/* Facts about a created machine: vocab, max_ctx, max_streams, n_ctx of the position table. */
-int sm_info(const sm_machine* m, int32_t* vocab, int32_t* max_ctx, int32_t* max_streams, int32_t* n_pos);
+/* Facts about a created machine: vocab, max_ctx, max_streams, rows of the position table, and whether the
+ * table entries are recomputed from their formulas (1) or read from memory (0). */
+int sm_info(const sm_machine* m, int32_t* vocab, int32_t* max_ctx, int32_t* max_streams, int32_t* n_pos,
+            int32_t* arith_tables);
 
 const char* sm_last_error(void);
 
@@ -109,6 +113,9 @@ typedef struct sm_tables sm_tables;
 int sm_tables_create(const int64_t* phi, const int64_t* arrival, int32_t alen, const int64_t* log2t,
                      const int64_t* exp2t, int64_t log2_768, int64_t eps40, sm_tables** out);
 int sm_tables_destroy(sm_tables* t);
+/* force_memory: 1 read the tables from memory (the default), 0 recompute verified entries, -1 leave as is;
+ * reports the mode in use */
+int sm_tables_mode(sm_tables* t, int32_t force_memory, int32_t* arith_tables);
 
 int sm_stage_rshift(const int64_t* x, const int64_t* s, int64_t* out, int64_t n, void* stream);          /* base2.py:18-22 */
 int sm_stage_log2fix(const sm_tables* t, const int64_t* v, int64_t* out, int64_t n, void* stream);       /* base2.py:42-48 */

@@ -10,6 +10,21 @@ typedef unsigned long long u64;
 
 #define SMD __device__ __forceinline__
 
+// The machine's four tables (base2_convert.py:48-61).  When `arith` is set, every entry is recomputed from its
+// defining formula in double precision instead of being read from memory; sm_create sets it only after an
+// exhaustive device check found every entry of the loaded tables equal to the recomputed one, so both paths give
+// the same integers.  The recomputation takes a dependent memory read off each phase's critical path.
+struct Tables {
+    const int* LOG2; const int* EXP2; const int* PHI; const int* ARR;
+    int alen; i64 log768; i64 eps40;
+    int arith;
+    // derived, exact integer compositions of the tables above (built on the host at create):
+    //   GPOW[r * 65536 + m] = EXP2[(log768 - ((r 65536 + LOG2[m]) >> 1)) & 0xFFFF]   the gauge's power factor
+    //   HPOW[m]             = EXP2[(-LOG2[m]) & 0xFFFF]                              the arrivals' divisor
+    // so that log2fix's mantissa m gives LOG2[m] and the EXP2 factor in two independent reads
+    const int* GPOW; const int* HPOW;
+};
+
 SMD i64 wadd(i64 a, i64 b) { return (i64)((u64)a + (u64)b); }
 SMD i64 wsub(i64 a, i64 b) { return (i64)((u64)a - (u64)b); }
 SMD i64 wmul(i64 a, i64 b) { return (i64)((u64)a * (u64)b); }
@@ -21,6 +36,18 @@ SMD int bitlen_py(i64 v) { return bitlen_u(v < 0 ? (u64)0 - (u64)v : (u64)v); }
 // np.abs on int64 (INT64_MIN stays INT64_MIN)
 SMD i64 iabs64(i64 v) { return v < 0 ? (i64)((u64)0 - (u64)v) : v; }
 
+// ---- the tables' defining formulas, term for term as base2_convert.py:49-59 evaluates them (round half even)
+SMD int log2_entry(int m) { return (int)rint(log2(1.0 + (double)m / 65536.0) * 65536.0); }
+SMD int exp2_entry(int f) { return (int)rint(pow(2.0, (double)f / 65536.0) * 65536.0); }
+SMD int phi_entry(int i) { return (int)rint(0.5 * (1.0 + erf(((double)(i - 32768) / 4096.0) / 1.4142135623730951)) * 65536.0); }
+SMD int arr_entry(i64 d) { return (int)rint(exp(-(double)d / 1024.0) * 16777216.0); }
+
+SMD i64 tab_log2(const Tables& tb, i64 m) { return tb.arith ? log2_entry((int)m) : tb.LOG2[m]; }
+SMD i64 tab_exp2(const Tables& tb, i64 f) { return tb.arith ? exp2_entry((int)f) : tb.EXP2[f]; }
+SMD i64 tab_phi(const Tables& tb, i64 i) { return tb.arith ? phi_entry((int)i) : tb.PHI[i]; }
+// the arrival: 0 past the table (base2.py:97)
+SMD int tab_arr(const Tables& tb, i64 d) { return d < tb.alen ? (tb.arith ? arr_entry(d) : tb.ARR[d]) : 0; }
+
 // base2.py:18-22  rshift(X, s): X * 2^-s rounded half up (s <= 0: a left shift)
 SMD i64 rsh(i64 x, i64 s) {
     if (s <= 0) return shl(x, -s);
@@ -28,22 +55,57 @@ SMD i64 rsh(i64 x, i64 s) {
 }
 
 // base2.py:42-48  log2fix(v): top-1 position t plus the table value of the next 16 bits (truncated)
-SMD i64 log2fix(i64 v, const int* __restrict__ LOG2) {
+SMD i64 log2fix(i64 v, const Tables& tb) {
     int t = bitlen_py(v) - 1;
     i64 m = t >= 16 ? (sar(v, t - 16) & 0xFFFF) : (shl(v, 16 - t) & 0xFFFF);
-    return wadd((i64)t * 65536, (i64)LOG2[m]);
+    return wadd((i64)t * 65536, tab_log2(tb, m));
+}
+
+// log2fix split into its top-1 position t and its mantissa index m (log2fix = t 65536 + LOG2[m])
+SMD void log2_parts(i64 v, int& t, i64& m) {
+    t = bitlen_py(v) - 1;
+    m = t >= 16 ? (sar(v, t - 16) & 0xFFFF) : (shl(v, 16 - t) & 0xFFFF);
+}
+// The same reads at a wave-uniform index, as scalar loads (constant address space): they are counted apart from
+// the vector loads, so they never wait behind plate tiles still in flight.
+typedef const __attribute__((address_space(4))) int* cint_p;
+SMD i64 utab_log2(const Tables& tb, int m) {
+    m = __builtin_amdgcn_readfirstlane(m);
+    return tb.arith ? log2_entry(m) : ((cint_p)tb.LOG2)[m];
+}
+SMD i64 utab_gpow(const Tables& tb, int r, int m) {
+    r = __builtin_amdgcn_readfirstlane(r);
+    m = __builtin_amdgcn_readfirstlane(m);
+    return tb.arith ? exp2_entry((int)((tb.log768 - (((i64)r * 65536 + log2_entry(m)) >> 1)) & 0xFFFF))
+                    : ((cint_p)tb.GPOW)[r * 65536 + m];
+}
+SMD i64 utab_hpow(const Tables& tb, int m) {
+    m = __builtin_amdgcn_readfirstlane(m);
+    return tb.arith ? exp2_entry((int)((-(i64)log2_entry(m)) & 0xFFFF)) : ((cint_p)tb.HPOW)[m];
+}
+SMD i64 tab_gpow(const Tables& tb, int r, i64 m) {
+    return tb.arith ? exp2_entry((int)((tb.log768 - (((i64)r * 65536 + log2_entry((int)m)) >> 1)) & 0xFFFF))
+                    : tb.GPOW[r * 65536 + m];
+}
+SMD i64 tab_hpow(const Tables& tb, i64 m) {
+    return tb.arith ? exp2_entry((int)((-(i64)log2_entry((int)m)) & 0xFFFF)) : tb.HPOW[m];
 }
 
 // base2.py:50-53  power(X, F) = rshift(X * EXP2[F & 0xFFFF], 16 - (F >> 16))
-SMD i64 power(i64 x, i64 F, const int* __restrict__ EXP2) {
+SMD i64 power(i64 x, i64 F, const Tables& tb) {
     i64 I = F >> 16, f = F & 0xFFFF;
-    return rsh(wmul(x, (i64)EXP2[f]), wsub(16, I));
+    return rsh(wmul(x, tab_exp2(tb, f)), wsub(16, I));
+}
+// the same with EXP2[F & 0xFFFF] already at hand (e = the table value for fine part fe)
+SMD i64 power_e(i64 x, i64 F, i64 fe, i64 e, const Tables& tb) {
+    i64 I = F >> 16, f = F & 0xFFFF;
+    return rsh(wmul(x, f == fe ? e : tab_exp2(tb, f)), wsub(16, I));
 }
 
 // base2.py:78-83  edge(H): the GELU share from PHI at rshift(H, 4) + 32768, then rshift(H * share, 16)
-SMD i64 edge1(i64 h, const int* __restrict__ PHI) {
+SMD i64 edge1(i64 h, const Tables& tb) {
     i64 idx = wadd(rsh(h, 4), 32768);
-    i64 share = idx < 0 ? 0 : (idx > 65535 ? 65536 : (i64)PHI[idx]);
+    i64 share = idx < 0 ? 0 : (idx > 65535 ? 65536 : tab_phi(tb, idx));
     return rsh(wmul(h, share), 16);
 }
 
@@ -61,25 +123,59 @@ SMD i64 eps_term(i64 eps40, i64 ex) {
 }
 
 // base2.py:58-60  LS from S1, S2 (d = 768 values) and ex
-SMD i64 gauge_ls(i64 s1, i64 s2, i64 ex, i64 log768, i64 eps40, const int* __restrict__ LOG2) {
-    i64 V = wadd(wsub(wmul(768, s2), wmul(s1, s1)), eps_term(eps40, ex));
-    return wadd(wsub(log2fix(V, LOG2) >> 1, log768), wmul(ex, 65536));
+SMD i64 gauge_ls(i64 s1, i64 s2, i64 ex, const Tables& tb) {
+    i64 V = wadd(wsub(wmul(768, s2), wmul(s1, s1)), eps_term(tb.eps40, ex));
+    return wadd(wsub(log2fix(V, tb) >> 1, tb.log768), wmul(ex, 65536));
+}
+// the same, also giving EXP2[(-LS) & 0xFFFF] (the power factor every gauged column uses) from one derived read
+SMD i64 gauge_ls_pow(i64 s1, i64 s2, i64 ex, const Tables& tb, i64& e2) {
+    i64 V = wadd(wsub(wmul(768, s2), wmul(s1, s1)), eps_term(tb.eps40, ex));
+    int t; i64 m;
+    log2_parts(V, t, m);
+    const i64 lg = utab_log2(tb, (int)m);           // V is the same in every lane: scalar reads
+    e2 = utab_gpow(tb, t & 1, (int)m);
+    const i64 l2 = wadd((i64)t * 65536, lg);
+    return wadd(wsub(l2 >> 1, tb.log768), wmul(ex, 65536));
+}
+
+// ---------------- wave64 reductions through DPP (a few VALU cycles per step) ----------------
+// update_dpp(old = 0, ...): lanes a step does not reach contribute 0, the identity of +, | and max of naturals
+#define DPP(v, ctrl, rm, bm) __builtin_amdgcn_update_dpp(0, (v), (ctrl), (rm), (bm), false)
+// full wave reduction of a 32-bit value (+ or |), the total read from lane 63 into a uniform register
+SMD int wave_add32(int v) {
+    v += DPP(v, 0x111, 0xf, 0xf); v += DPP(v, 0x112, 0xf, 0xf); v += DPP(v, 0x114, 0xf, 0xe);
+    v += DPP(v, 0x118, 0xf, 0xc); v += DPP(v, 0x142, 0xa, 0xf); v += DPP(v, 0x143, 0xc, 0xf);
+    return __builtin_amdgcn_readlane(v, 63);
+}
+SMD unsigned wave_or32(unsigned u) {
+    int v = (int)u;
+    v |= DPP(v, 0x111, 0xf, 0xf); v |= DPP(v, 0x112, 0xf, 0xf); v |= DPP(v, 0x114, 0xf, 0xe);
+    v |= DPP(v, 0x118, 0xf, 0xc); v |= DPP(v, 0x142, 0xa, 0xf); v |= DPP(v, 0x143, 0xc, 0xf);
+    return (unsigned)__builtin_amdgcn_readlane(v, 63);
+}
+// 64-bit value moved by one DPP row shift (lo and hi words separately)
+template <int CTRL, int BM>
+SMD i64 dpp_shr64(i64 v) {
+    const int lo = DPP((int)v, CTRL, 0xf, BM), hi = DPP((int)(v >> 32), CTRL, 0xf, BM);
+    return (i64)(((u64)(unsigned)hi << 32) | (unsigned)lo);
+}
+// Sum of the lanes that share lane % TC (TC in 1, 2, 4, 8): in-row prefix steps of stride TC .. 8, then the
+// four rows through two xor exchanges.  The totals end in lanes 16 - TC .. 15 of every row.
+template <int TC>
+SMD i64 wave_colsum64(i64 v) {
+    if (TC <= 1) v += dpp_shr64<0x111, 0xf>(v);
+    if (TC <= 2) v += dpp_shr64<0x112, 0xf>(v);
+    if (TC <= 4) v += dpp_shr64<0x114, 0xe>(v);
+    v += dpp_shr64<0x118, 0xc>(v);
+    v += __shfl_xor(v, 16, 64);
+    v += __shfl_xor(v, 32, 64);
+    return v;
 }
 
 // ---------------- 64-wide wavefront reductions ----------------
-SMD i64 wave_sum64(i64 v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
-    return v;
-}
 SMD i64 wave_or64(i64 v) {
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) v |= __shfl_xor(v, o, 64);
-    return v;
-}
-SMD i64 wave_max64(i64 v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) { i64 w = __shfl_xor(v, o, 64); v = w > v ? w : v; }
     return v;
 }
 

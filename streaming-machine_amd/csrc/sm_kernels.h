@@ -14,11 +14,6 @@ enum { EPI_GAUGED = 0,       // power(pile, (we + ex + 16) 65536 - LS) + b      
        EPI_HEAD = 3,         // gauged logit + standing amount, then the race           (base2.py:107-114)
        EPI_PILE = 4 };       // the raw pile (product only)                             (base2.py:29-32)
 
-struct Tables {
-    const int* LOG2; const int* EXP2; const int* PHI; const int* ARR;
-    int alen; i64 log768; i64 eps40;
-};
-
 // Record of one position's intermediates (stream 0), written when the position equals *pos.
 struct Rec {
     const int* pos;

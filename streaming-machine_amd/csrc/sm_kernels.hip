@@ -13,16 +13,18 @@
 //   * the phase's whole-row dependencies (the water level's OR, the gauge's S1 and S2) are recomputed by every
 //     block from the row in L2 (768 or 3072 values) so that prologue, product and epilogue fuse into one
 //     launch and the next phase needs no extra pass.
+//   * a phase's critical path holds one dependent memory read (the row it consumes): the weights, exponents
+//     and biases of the block's first tile are requested before it, the gauge's power factor EXP2[f] is one
+//     value per block (f = -LS mod 2^16 for every column), and with arithmetic tables no table read remains.
 #include "sm_kernels.h"
 
 #define NTHR 256
 typedef int v4i __attribute__((ext_vector_type(4)));
 
 // ---------------------------------------------------------------------------------------------------------
-// block reductions (4 waves)
+// block reductions (4 waves).  red: 8 slots, free on entry; every thread gets the result.
 template <typename F>
 SMD i64 block_reduce(i64 v, i64* red, F op, int tid) {
-    // red: 4 slots; caller guarantees red is free on entry; returns the reduced value to all threads
     const int lane = tid & 63, wave = tid >> 6;
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) v = op(v, (i64)__shfl_xor(v, o, 64));
@@ -32,105 +34,140 @@ SMD i64 block_reduce(i64 v, i64* red, F op, int tid) {
     __syncthreads();
     return r;
 }
+// two sums in one pass
+SMD void block_sum2(i64& a, i64& b, i64* red, int tid) {
+    const int lane = tid & 63, wave = tid >> 6;
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) { a += __shfl_xor(a, o, 64); b += __shfl_xor(b, o, 64); }
+    if (lane == 0) { red[wave] = a; red[4 + wave] = b; }
+    __syncthreads();
+    a = red[0] + red[1] + red[2] + red[3];
+    b = red[4] + red[5] + red[6] + red[7];
+    __syncthreads();
+}
 struct OpOr { SMD i64 operator()(i64 a, i64 b) const { return a | b; } };
 struct OpAdd { SMD i64 operator()(i64 a, i64 b) const { return (i64)((u64)a + (u64)b); } };
 struct OpMax { SMD i64 operator()(i64 a, i64 b) const { return a > b ? a : b; } };
 
 // ---------------------------------------------------------------------------------------------------------
-// Prologue: the light entering the plate.  Writes xh/xl (NIN shorts each) into LDS and returns ex, LS.
-template <int NIN, int PRO>
-SMD void prologue(const GemvArgs& a, int tid, short* xh_s, short* xl_s, i64* red, i64& ex_o, i64& ls_o, bool rec) {
-    constexpr int PER = NIN / NTHR;
-    i64 v[PER];
+// Prologue: the light entering the plate, computed by every block from the row it reads (NIN values over the
+// block's NT threads).  Writes xh/xl (NIN shorts each) into LDS and returns ex, LS and the gauge's power factor.
+// The water level's OR is reduced as two 32-bit words and the gauge's sums as exact 32-bit pieces (S1 < 2^25,
+// S2 split at bit 16), each wave through DPP and the waves through one LDS exchange.
+// the row's loads, issued first: vector loads complete in order, so anything requested before them (plate
+// tiles from HBM) would have to arrive before the row could be used
+template <int NIN, int NT, int PRO>
+SMD void prologue_load(const GemvArgs& a, int tid, i64 (&v)[NIN / NT]) {
+    constexpr int PER = NIN / NT;
     if (PRO == PRO_EMBED) {
         const int p = *a.pos;
         const i64 tok = a.seq[p];
 #pragma unroll
         for (int m = 0; m < PER; m++) {
-            int i = tid + NTHR * m;
+            int i = tid + NT * m;
             v[m] = wadd(a.wte[tok * 768 + i], a.wpe[(i64)p * 768 + i]);
             if (blockIdx.x == 0) a.Rw[i] = v[m];
         }
     } else {
 #pragma unroll
-        for (int m = 0; m < PER; m++) v[m] = a.X[tid + NTHR * m];
+        for (int m = 0; m < PER; m++) v[m] = a.X[tid + NT * m];
     }
+}
+template <int NIN, int NT, int PRO>
+SMD void prologue(const GemvArgs& a, int tid, const i64 (&v)[NIN / NT], short* xh_s, short* xl_s, int* red, i64& ex_o,
+                  i64& ls_o, i64& e2_o, bool rec) {
+    constexpr int PER = NIN / NT, NW = NT / 64;
+    const int lane = tid & 63, wave = tid >> 6;
     int sh = 0;
     if (PRO != PRO_X16) {
-        i64 o = 0;
+        u64 o = 0;
 #pragma unroll
-        for (int m = 0; m < PER; m++) o |= iabs64(v[m]);
-        o = block_reduce(o, red, OpOr(), tid);
-        sh = water_shift(o);
+        for (int m = 0; m < PER; m++) o |= (u64)iabs64(v[m]);
+        const unsigned olo = wave_or32((unsigned)o), ohi = wave_or32((unsigned)(o >> 32));
+        if (lane == 0) { red[2 * wave] = (int)olo; red[2 * wave + 1] = (int)ohi; }
+        __syncthreads();
+        u64 all = 0;
+#pragma unroll
+        for (int w = 0; w < NW; w++) all |= ((u64)(unsigned)red[2 * w + 1] << 32) | (unsigned)red[2 * w];
+        sh = water_shift((i64)all);
     }
     const i64 ex = -16 + sh;
-    i64 s1 = 0, s2 = 0;
+    int s1 = 0;
+    i64 s2 = 0;
 #pragma unroll
     for (int m = 0; m < PER; m++) {
-        int i = tid + NTHR * m;
-        i64 x = PRO == PRO_X16 ? v[m] : rsh(v[m], sh);
-        int xi = (int)x;
+        int i = tid + NT * m;
+        const int xi = PRO == PRO_X16 ? (int)v[m] : (int)rsh(v[m], sh);
         xh_s[i] = (short)(xi >> 8);
         xl_s[i] = (short)(xi & 255);
-        s1 += x;
-        s2 += x * x;
-        if (rec && a.rx16) a.rx16[i] = x;
+        s1 += xi;
+        s2 += (i64)xi * xi;
+        if (rec && a.rx16) a.rx16[i] = xi;
     }
-    i64 ls = 0;
+    i64 ls = 0, e2 = 0;
     if (PRO == PRO_GAUGE || PRO == PRO_EMBED) {
-        s1 = block_reduce(s1, red, OpAdd(), tid);
-        s2 = block_reduce(s2, red, OpAdd(), tid);
-        ls = gauge_ls(s1, s2, ex, a.tb.log768, a.tb.eps40, a.tb.LOG2);
+        const int w1 = wave_add32(s1), w2h = wave_add32((int)(s2 >> 16)), w2l = wave_add32((int)(s2 & 0xFFFF));
+        if (lane == 0) { red[16 + 3 * wave] = w1; red[17 + 3 * wave] = w2h; red[18 + 3 * wave] = w2l; }
+        __syncthreads();
+        i64 S1 = 0, S2h = 0, S2l = 0;
+#pragma unroll
+        for (int w = 0; w < NW; w++) { S1 += red[16 + 3 * w]; S2h += red[17 + 3 * w]; S2l += red[18 + 3 * w]; }
+        ls = gauge_ls_pow(S1, (S2h << 16) + S2l, ex, a.tb, e2);
+    } else {
+        __syncthreads();
     }
     if (rec && a.rexls && tid == 0) { a.rexls[0] = ex; a.rexls[1] = ls; }
     ex_o = ex;
     ls_o = ls;
-    __syncthreads();
+    e2_o = e2;
 }
 
 // ---------------------------------------------------------------------------------------------------------
-template <int NIN, int TC, int NL>
-SMD void load_tile(v4i (&w)[NL], const int4* __restrict__ W, int tile, int tid) {
-    constexpr int UNITS = TC * NIN / 8;
-    const v4i* base = reinterpret_cast<const v4i*>(W) + (size_t)tile * UNITS;
+// One wave's share of a tile: U = TC NIN / 512 units of 16 bytes per lane (unit u = lane + 64 m).
+template <int NIN, int TC>
+struct WaveTile {
+    static constexpr int U = TC * NIN / 8 / 64;
+    static_assert(TC * NIN / 8 % 64 == 0, "a tile must split evenly over the 64 lanes");
+};
+
+template <int NIN, int TC, int U>
+SMD void load_wtile(v4i (&w)[U], const int4* __restrict__ W, int tile, int lane) {
+    const v4i* base = reinterpret_cast<const v4i*>(W) + (size_t)tile * (TC * NIN / 8) + lane;
 #pragma unroll
-    for (int m = 0; m < NL; m++) {
-        int u = tid + NTHR * m;
-        if (UNITS % NTHR == 0 || u < UNITS) w[m] = __builtin_nontemporal_load(base + u);
-    }
+    for (int m = 0; m < U; m++) w[m] = __builtin_nontemporal_load(base + 64 * m);
 }
 
-template <int NIN, int TC, int NL>
-SMD i64 tile_partial(const v4i (&w)[NL], const short* xh_s, const short* xl_s, int tid) {
-    constexpr int UNITS = TC * NIN / 8;
+// the lane's part of its column's pile: unit u holds inputs 8 (u / TC) .. + 8 of column u % TC = lane % TC
+template <int NIN, int TC, int U>
+SMD i64 wtile_partial(const v4i (&w)[U], const short* xh_s, const short* xl_s, int lane) {
     int ah = 0, al = 0;
 #pragma unroll
-    for (int m = 0; m < NL; m++) {
-        int u = tid + NTHR * m;
-        if (UNITS % NTHR == 0 || u < UNITS) {
-            const int c = u / TC;
-            const int4 xh = reinterpret_cast<const int4*>(xh_s)[c];
-            const int4 xl = reinterpret_cast<const int4*>(xl_s)[c];
-            const v4i ww = w[m];
-            ah = dot2(ww.x, xh.x, ah); ah = dot2(ww.y, xh.y, ah); ah = dot2(ww.z, xh.z, ah); ah = dot2(ww.w, xh.w, ah);
-            al = dot2(ww.x, xl.x, al); al = dot2(ww.y, xl.y, al); al = dot2(ww.z, xl.z, al); al = dot2(ww.w, xl.w, al);
-        }
+    for (int m = 0; m < U; m++) {
+        const int c = (lane + 64 * m) / TC;
+        const int4 xh = reinterpret_cast<const int4*>(xh_s)[c];
+        const int4 xl = reinterpret_cast<const int4*>(xl_s)[c];
+        const v4i ww = w[m];
+        ah = dot2(ww.x, xh.x, ah); ah = dot2(ww.y, xh.y, ah); ah = dot2(ww.z, xh.z, ah); ah = dot2(ww.w, xh.w, ah);
+        al = dot2(ww.x, xl.x, al); al = dot2(ww.y, xl.y, al); al = dot2(ww.z, xl.z, al); al = dot2(ww.w, xl.w, al);
     }
     return (i64)ah * 256 + (i64)al;
 }
 
-// The phase kernel: prologue (light), product over this block's tiles, epilogue per column.
-template <int NIN, int TC, int PRO, int EPI>
-__global__ __launch_bounds__(NTHR) void k_gemv(GemvArgs a) {
-    constexpr int UNITS = TC * NIN / 8;
-    constexpr int NL = (UNITS + NTHR - 1) / NTHR;
-    static_assert(NTHR % TC == 0 && 64 % TC == 0, "tile width");
+// The phase kernel.  NT = 64 WPB threads; every wave owns whole tiles (wave-global index w, tiles w, w + G, ..),
+// so after the block's prologue no block barrier is needed: a wave loads its tile, forms its TC piles with DPP
+// steps, and lanes 16 - TC .. 15 apply the epilogue of one column each.  The next tile of the wave (if any)
+// is in flight while the current one is reduced.
+template <int NIN, int TC, int WPB, int PRO, int EPI>
+__global__ __launch_bounds__(64 * WPB) void k_gemv(GemvArgs a) {
+    constexpr int NT = 64 * WPB, U = WaveTile<NIN, TC>::U;
     __shared__ __align__(16) short xh_s[NIN];
     __shared__ __align__(16) short xl_s[NIN];
-    __shared__ i64 red[4];
-    __shared__ i64 redp[4 * TC];
-    __shared__ int redi[TC];
+    __shared__ int red[32];
+    __shared__ i64 bestv[WPB];
+    __shared__ int besti[WPB];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int col = lane - (16 - TC);                 // the column this lane finishes (valid when 0 <= col < TC)
+    const bool fin = col >= 0 && col < TC;
 
     bool skip = false;
     int p = 0;
@@ -143,91 +180,113 @@ __global__ __launch_bounds__(NTHR) void k_gemv(GemvArgs a) {
     i64 best_v = 0;
     int best_i = -1;
     if (!skip) {
-        int tile = blockIdx.x;
-        v4i wc[NL];
-        if (tile < a.ntiles) load_tile<NIN, TC, NL>(wc, a.W, tile, tid);   // weights in flight during the prologue
-        i64 ex, ls;
-        prologue<NIN, PRO>(a, tid, xh_s, xl_s, red, ex, ls, rec && blockIdx.x == 0);
-        for (; tile < a.ntiles; tile += gridDim.x) {
-            v4i wn[NL];
-            const int nt = tile + gridDim.x;
-            if (nt < a.ntiles) load_tile<NIN, TC, NL>(wn, a.W, nt, tid);
-            i64 part = tile_partial<NIN, TC, NL>(wc, xh_s, xl_s, tid);
-#pragma unroll
-            for (int o = TC; o < 64; o <<= 1) part += __shfl_xor(part, o, 64);
-            if (lane < TC) redp[wave * TC + lane] = part;
-            __syncthreads();
-            if (tid < TC) {
-                const int j = tile * TC + tid;
-                if (j < a.nout) {
-                    const i64 pile = redp[tid] + redp[TC + tid] + redp[2 * TC + tid] + redp[3 * TC + tid];
-                    if (rec && a.rpile) a.rpile[j] = pile;
-                    const i64 we = a.we[j];
-                    if (EPI == EPI_PILE) {
-                        a.Y[j] = pile;
-                    } else if (EPI == EPI_PLAIN_ADD) {
-                        const i64 r = wadd(a.Y[j], wadd(rsh(pile, -(we + ex + 16)), a.bias[j]));
-                        a.Y[j] = r;
-                        if (rec && a.rout) a.rout[j] = r;
+        const int gw = blockIdx.x * WPB + wave, nw = gridDim.x * WPB;
+        // two named buffers in turn (no register copies, so a prefetch in flight is never waited on early);
+        // a tile's exponents and biases are requested before its weights, so waiting for the small loads
+        // never waits for the large ones behind them
+        v4i wA[U], wB[U];
+        i64 bA = 0, eA = 0, bB = 0, eB = 0;
+        // every lane loads (indices clamped into range): a load that writes only some lanes would have to be
+        // merged with the register's old value, and that merge waits for the load
+        auto fetch = [&](v4i (&w)[U], i64& we_, i64& b_, int t) {
+            t = t < a.ntiles ? t : a.ntiles - 1;
+            if (EPI != EPI_PILE) {
+                int j = t * TC + col;
+                j = j < 0 ? 0 : (j < a.nout ? j : a.nout - 1);
+                we_ = a.we[j];
+                b_ = a.bias[j];
+            }
+            load_wtile<NIN, TC, U>(w, a.W, t, lane);
+        };
+        int tile = gw;
+        i64 row[NIN / NT];
+        prologue_load<NIN, NT, PRO>(a, tid, row);        // the row first, then this wave's first tile
+        fetch(wA, eA, bA, tile);                         // unconditional (clamped): no branch for the wait count to merge
+        i64 ex, ls, e2;
+        prologue<NIN, NT, PRO>(a, tid, row, xh_s, xl_s, red, ex, ls, e2, rec && blockIdx.x == 0);
+        const i64 fe = wsub(0, ls) & 0xFFFF;          // the fine part of (we + ex + 16) 65536 - LS for every column
+        auto finish = [&](const v4i (&w)[U], i64 wec, i64 bc, int t) {
+            const i64 pile = wave_colsum64<TC>(wtile_partial<NIN, TC, U>(w, xh_s, xl_s, lane));
+            const int j = t * TC + col;
+            if (fin && j < a.nout) {
+                if (rec && a.rpile) a.rpile[j] = pile;
+                if (EPI == EPI_PILE) {
+                    a.Y[j] = pile;
+                } else if (EPI == EPI_PLAIN_ADD) {
+                    const i64 r = wadd(a.Y[j], wadd(rsh(pile, -(wec + ex + 16)), bc));
+                    a.Y[j] = r;
+                    if (rec && a.rout) a.rout[j] = r;
+                } else {
+                    i64 y = wadd(power_e(pile, wsub(wmul(wec + ex + 16, 65536), ls), fe, e2, a.tb), bc);
+                    if (EPI == EPI_GAUGED_EDGE) y = edge1(y, a.tb);
+                    if (EPI == EPI_HEAD) {
+                        if (rec && a.rlogits) a.rlogits[j] = y;
+                        if (best_i < 0 || y > best_v) { best_v = y; best_i = j; }   // j grows: ties keep the first
                     } else {
-                        i64 y = wadd(power(pile, wsub((we + ex + 16) * 65536, ls), a.tb.EXP2), a.bias[j]);
-                        if (EPI == EPI_GAUGED_EDGE) y = edge1(y, a.tb.PHI);
-                        if (EPI == EPI_HEAD) {
-                            if (rec && a.rlogits) a.rlogits[j] = y;
-                            if (best_i < 0 || y > best_v) { best_v = y; best_i = j; }   // j grows: ties keep the first
-                        } else {
-                            a.Y[j] = y;
-                            if (rec && a.rout) a.rout[j] = y;
-                        }
+                        a.Y[j] = y;
+                        if (rec && a.rout) a.rout[j] = y;
                     }
                 }
             }
-            __syncthreads();
-#pragma unroll
-            for (int m = 0; m < NL; m++) wc[m] = wn[m];
+        };
+        while (tile < a.ntiles) {
+            const int t1 = tile + nw;
+            fetch(wB, eB, bB, t1);
+            finish(wA, eA, bA, tile);
+            if (t1 >= a.ntiles) break;
+            const int t2 = t1 + nw;
+            fetch(wA, eA, bA, t2);
+            finish(wB, eB, bB, t1);
+            tile = t2;
         }
     }
     if (EPI != EPI_HEAD) return;
 
     // ---- the race (base2.py:34-40, 114): largest logit, ties to the lowest word ----
-    if (tid < TC) { redp[tid] = best_v; redi[tid] = best_i; }
+    // wave: the TC finishing lanes; block: the waves; grid: the last block to arrive
+#pragma unroll
+    for (int o = 1; o < TC; o <<= 1) {
+        const i64 ov = __shfl_xor(best_v, o, 64);
+        const int oi = __shfl_xor(best_i, o, 64);
+        if (oi >= 0 && (best_i < 0 || ov > best_v || (ov == best_v && oi < best_i))) { best_v = ov; best_i = oi; }
+    }
+    if (lane == 16 - TC) { bestv[wave] = best_v; besti[wave] = best_i; }
     __syncthreads();
+    __shared__ int last;
     if (tid == 0) {
         i64 bv = 0; int bi = -1;
-        for (int t = 0; t < TC; t++) {
-            const int ci = redi[t];
-            if (ci >= 0 && (bi < 0 || redp[t] > bv || (redp[t] == bv && ci < bi))) { bv = redp[t]; bi = ci; }
-        }
+        for (int w = 0; w < WPB; w++)
+            if (besti[w] >= 0 && (bi < 0 || bestv[w] > bv || (bestv[w] == bv && besti[w] < bi))) { bv = bestv[w]; bi = besti[w]; }
         a.part_v[blockIdx.x] = bv;
         a.part_i[blockIdx.x] = bi;
         __threadfence();
         const unsigned prev = atomicAdd(a.counter, 1u);
-        redi[0] = (prev == gridDim.x - 1);
+        last = (prev == gridDim.x - 1);
     }
     __syncthreads();
-    if (!redi[0]) return;
+    if (!last) return;
     // the last block: every partial is visible (fence before each arrival, fence after ours)
     __threadfence();
     if (!skip) {
         i64 bv = 0; int bi = -1;
-        for (int g = tid; g < (int)gridDim.x; g += NTHR) {
+        for (int g = tid; g < (int)gridDim.x; g += NT) {
             const i64 v = __hip_atomic_load(&a.part_v[g], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             const int ci = __hip_atomic_load(&a.part_i[g], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             if (ci >= 0 && (bi < 0 || v > bv || (v == bv && ci < bi))) { bv = v; bi = ci; }
         }
-        // block argmax with ties to the lowest index
 #pragma unroll
         for (int o = 32; o > 0; o >>= 1) {
             const i64 ov = __shfl_xor(bv, o, 64);
             const int oi = __shfl_xor(bi, o, 64);
             if (oi >= 0 && (bi < 0 || ov > bv || (ov == bv && oi < bi))) { bv = ov; bi = oi; }
         }
-        if (lane == 0) { redp[wave] = bv; redi[wave] = bi; }
+        __syncthreads();
+        if (lane == 0) { bestv[wave] = bv; besti[wave] = bi; }
         __syncthreads();
         if (tid == 0) {
-            bv = redp[0]; bi = redi[0];
-            for (int w = 1; w < 4; w++)
-                if (redi[w] >= 0 && (bi < 0 || redp[w] > bv || (redp[w] == bv && redi[w] < bi))) { bv = redp[w]; bi = redi[w]; }
+            bv = bestv[0]; bi = besti[0];
+            for (int w = 1; w < WPB; w++)
+                if (besti[w] >= 0 && (bi < 0 || bestv[w] > bv || (bestv[w] == bv && besti[w] < bi))) { bv = bestv[w]; bi = besti[w]; }
             a.seq_w[p + 1] = bi;                  // the word goes straight back in (base2_stream.swift:143-146)
             const int n = p + 1 - *a.plen;
             if (n >= 0) a.words[n] = bi;
@@ -246,17 +305,22 @@ __global__ __launch_bounds__(NTHR) void k_gemv(GemvArgs a) {
 //   2. scores over every cached position s <= p: rshift(q16 . k16, -(eq + ek + 7))          (base2.py:94)
 //   3. the clock starts at the maximum; arrivals ARR[max - sc] (0 past the table)            (base2.py:96-97)
 //   4. num = sum a v, out = power(num, -log2fix(sum a))                                        (base2.py:98-99)
-// The maximum is global over the row before any arrival is read (two passes over LDS), so it is exact for any
-// context length; the scores live in LDS (8 B each) and the arrivals beside them (4 B each).
+// Four lanes share a position (16 of its 64 dimensions each), so a block covers 64 positions per pass.  The
+// cached keys and values of the first 64 positions are requested at launch, before the new q, k, v arrive.
+// The maximum is global over the row before any arrival is read (two passes, scores in LDS), so the result is
+// exact for any context length.
+#define ACH 64
 __global__ __launch_bounds__(NTHR) void k_attend(AttArgs a) {
     extern __shared__ __align__(16) unsigned char smem[];
     i64* sc = reinterpret_cast<i64*>(smem);                 // [ctx]
-    int* av = reinterpret_cast<int*>(sc + a.ctx);            // [ctx]
-    __shared__ int q16s[64], k16s[64], vs[64];
-    __shared__ i64 red[4];
+    __shared__ __align__(16) int q16s[64];
+    __shared__ __align__(16) int k16s[64];
+    __shared__ __align__(16) int vs[64];
+    __shared__ i64 red[8];
     __shared__ i64 numr[4][64];
     __shared__ int eqs, eks;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int sl = tid >> 2, qd = tid & 3;                   // position in the pass, quarter of the dimensions
     const int h = blockIdx.x, b = blockIdx.y;
     const int p = *a.pos;
     const i64* qkv = a.QKV + (size_t)b * 2304;
@@ -265,9 +329,20 @@ __global__ __launch_bounds__(NTHR) void k_attend(AttArgs a) {
     int* V = a.V + (size_t)b * a.ctx * 768;
     const bool rec = b == 0 && a.rec_pos && *a.rec_pos == p;
 
-    // the new position's own key and value are used from LDS below: this block never reads back what it wrote
+    // the new q, k, v first (vector loads complete in order), then the cached positions of the first pass
+    const i64 xnew = wave < 3 ? qkv[wave * 768 + h * 64 + lane] : 0;
+    v4i kp[4], vp[4];
+    int ekp = 0;
+    if (sl < p) {
+        const v4i* kr = reinterpret_cast<const v4i*>(K16 + (size_t)sl * 768 + h * 64 + qd * 16);
+        const v4i* vr = reinterpret_cast<const v4i*>(V + (size_t)sl * 768 + h * 64 + qd * 16);
+#pragma unroll
+        for (int c = 0; c < 4; c++) { kp[c] = kr[c]; vp[c] = vr[c]; }
+        ekp = EK[(size_t)sl * 12 + h];
+    }
+    // the new position's own key and value are used from LDS: this block never reads back what it wrote
     if (wave < 2) {
-        const i64 x = qkv[wave * 768 + h * 64 + lane];
+        const i64 x = xnew;
         const int sh = water_shift(wave_or64(iabs64(x)));
         const int x16 = (int)rsh(x, sh);
         if (wave == 0) {
@@ -279,56 +354,117 @@ __global__ __launch_bounds__(NTHR) void k_attend(AttArgs a) {
             if (lane == 0) { eks = -16 + sh; EK[(size_t)p * 12 + h] = -16 + sh; }
         }
     } else if (wave == 2) {
-        const i64 x = qkv[1536 + h * 64 + lane];
+        const i64 x = xnew;
         if (x < (i64)INT32_MIN || x > (i64)INT32_MAX) atomicOr(a.err, SM_ERR_V32);
         vs[lane] = (int)x;
         V[(size_t)p * 768 + h * 64 + lane] = (int)x;
     }
     __syncthreads();
 
+    // pass 1: scores and their maximum
     const i64 eq = eqs;
-    i64 mx = INT64_MIN;
-    for (int s = tid; s <= p; s += NTHR) {
-        i64 dot = 0, ek;
-        if (s < p) {
-            const int4* kr = reinterpret_cast<const int4*>(K16 + (size_t)s * 768 + h * 64);
+    int qv[16];
 #pragma unroll
-            for (int c = 0; c < 16; c++) {
-                const int4 k4 = kr[c];
-                dot += (i64)q16s[4 * c] * k4.x + (i64)q16s[4 * c + 1] * k4.y + (i64)q16s[4 * c + 2] * k4.z + (i64)q16s[4 * c + 3] * k4.w;
+    for (int i = 0; i < 16; i++) qv[i] = q16s[qd * 16 + i];
+    i64 mx = INT64_MIN;
+    for (int s0 = 0; s0 <= p; s0 += ACH) {
+        const int s = s0 + sl;
+        i64 dot = 0, ek = 0;
+        if (s < p) {
+            v4i kk[4];
+            if (s0 == 0) {
+#pragma unroll
+                for (int c = 0; c < 4; c++) kk[c] = kp[c];
+                ek = ekp;
+            } else {
+                const v4i* kr = reinterpret_cast<const v4i*>(K16 + (size_t)s * 768 + h * 64 + qd * 16);
+#pragma unroll
+                for (int c = 0; c < 4; c++) kk[c] = kr[c];
+                ek = EK[(size_t)s * 12 + h];
             }
-            ek = EK[(size_t)s * 12 + h];
-        } else {
-            for (int c = 0; c < 64; c++) dot += (i64)q16s[c] * k16s[c];
+#pragma unroll
+            for (int c = 0; c < 4; c++)
+                dot += (i64)qv[4 * c] * kk[c].x + (i64)qv[4 * c + 1] * kk[c].y + (i64)qv[4 * c + 2] * kk[c].z + (i64)qv[4 * c + 3] * kk[c].w;
+        } else if (s == p) {
+#pragma unroll
+            for (int i = 0; i < 16; i++) dot += (i64)qv[i] * k16s[qd * 16 + i];
             ek = eks;
         }
-        const i64 v = rsh(dot, -(eq + ek + 7));
-        sc[s] = v;
-        mx = v > mx ? v : mx;
+        dot += __shfl_xor(dot, 1, 64);
+        dot += __shfl_xor(dot, 2, 64);
+        if (s <= p) {
+            const i64 v = rsh(dot, -(eq + ek + 7));
+            if (qd == 0) sc[s] = v;
+            mx = v > mx ? v : mx;
+        }
     }
-    mx = block_reduce(mx, red, OpMax(), tid);
+    mx = block_reduce(mx, red, OpMax(), tid);   // its barriers also publish sc[]
+
+    // pass 2: arrivals and the value sum, 16 dimensions per lane
+    i64 num[16];
+#pragma unroll
+    for (int i = 0; i < 16; i++) num[i] = 0;
     i64 z = 0;
-    for (int s = tid; s <= p; s += NTHR) {
-        const i64 d = wsub(mx, sc[s]);
-        const int w = d < a.tb.alen ? a.tb.ARR[d] : 0;
-        av[s] = w;
-        z += w;
+    for (int s0 = 0; s0 <= p; s0 += ACH) {
+        const int s = s0 + sl;
+        if (s > p) continue;
+        const int w = tab_arr(a.tb, wsub(mx, sc[s]));
+        if (qd == 0) z += w;
+        if (!w) continue;
+        if (s < p) {
+            v4i vv[4];
+            if (s0 == 0) {
+#pragma unroll
+                for (int c = 0; c < 4; c++) vv[c] = vp[c];
+            } else {
+                const v4i* vr = reinterpret_cast<const v4i*>(V + (size_t)s * 768 + h * 64 + qd * 16);
+#pragma unroll
+                for (int c = 0; c < 4; c++) vv[c] = vr[c];
+            }
+#pragma unroll
+            for (int c = 0; c < 4; c++) {
+                num[4 * c] += (i64)w * vv[c].x; num[4 * c + 1] += (i64)w * vv[c].y;
+                num[4 * c + 2] += (i64)w * vv[c].z; num[4 * c + 3] += (i64)w * vv[c].w;
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < 16; i++) num[i] += (i64)w * vs[qd * 16 + i];
+        }
     }
-    z = block_reduce(z, red, OpAdd(), tid);   // includes a barrier: av[] complete
-    i64 num = 0;
-    for (int s = wave; s <= p; s += 4) {
-        const int w = av[s];
-        if (w) num += (i64)w * (s < p ? V[(size_t)s * 768 + h * 64 + lane] : vs[lane]);
+    // sum over the 16 positions of each wave (lanes that share a quarter), then over the 4 waves
+#pragma unroll
+    for (int i = 0; i < 16; i++) {
+        i64 v = num[i];
+        v += __shfl_xor(v, 4, 64); v += __shfl_xor(v, 8, 64); v += __shfl_xor(v, 16, 64); v += __shfl_xor(v, 32, 64);
+        num[i] = v;
     }
-    numr[wave][lane] = num;
-    __syncthreads();
+    if (lane < 4) {
+#pragma unroll
+        for (int i = 0; i < 16; i++) numr[wave][lane * 16 + i] = num[i];
+    }
+    z = block_reduce(z, red, OpAdd(), tid);   // its barriers also publish numr[]
     if (wave == 0) {
         const i64 tot = numr[0][lane] + numr[1][lane] + numr[2][lane] + numr[3][lane];
-        const i64 F = wsub(0, log2fix(z, a.tb.LOG2));
-        const i64 o = power(tot, F, a.tb.EXP2);
+        int t; i64 m;
+        log2_parts(z, t, m);
+        const i64 F = wsub(0, wadd((i64)t * 65536, utab_log2(a.tb, (int)m)));   // -log2fix(Z), Z the same in every lane
+        const i64 o = power_e(tot, F, F & 0xFFFF, utab_hpow(a.tb, (int)m), a.tb);
         a.out[(size_t)b * 768 + h * 64 + lane] = o;
         if (rec) a.ratt[h * 64 + lane] = o;
     }
+}
+
+// ---------------------------------------------------------------------------------------------------------
+// Exhaustive check of the loaded tables against their defining formulas (sets Tables.arith when all agree).
+__global__ void k_check_tables(Tables tb, unsigned* bad) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < 65536) {
+        if (log2_entry(i) != tb.LOG2[i]) atomicAdd(&bad[0], 1u);
+        if (exp2_entry(i) != tb.EXP2[i]) atomicAdd(&bad[1], 1u);
+        if (phi_entry(i) != tb.PHI[i]) atomicAdd(&bad[2], 1u);
+    }
+    if (i < tb.alen && arr_entry(i) != tb.ARR[i]) atomicAdd(&bad[3], 1u);
+    if (i == tb.alen && arr_entry(i) != 0) atomicAdd(&bad[3], 1u);       // the table ends where e^-d rounds to 0
 }
 
 // ---------------------------------------------------------------------------------------------------------
@@ -337,21 +473,21 @@ __global__ void k_stage_rshift(const i64* x, const i64* s, i64* out, i64 n) {
     const i64 i = (i64)blockIdx.x * blockDim.x + threadIdx.x;
     if (i < n) out[i] = rsh(x[i], s[i]);
 }
-__global__ void k_stage_power(const i64* x, const i64* F, i64* out, i64 n, const int* EXP2) {
+__global__ void k_stage_power(const i64* x, const i64* F, i64* out, i64 n, Tables tb) {
     const i64 i = (i64)blockIdx.x * blockDim.x + threadIdx.x;
-    if (i < n) out[i] = power(x[i], F[i], EXP2);
+    if (i < n) out[i] = power(x[i], F[i], tb);
 }
-__global__ void k_stage_log2fix(const i64* v, i64* out, i64 n, const int* LOG2) {
+__global__ void k_stage_log2fix(const i64* v, i64* out, i64 n, Tables tb) {
     const i64 i = (i64)blockIdx.x * blockDim.x + threadIdx.x;
-    if (i < n) out[i] = log2fix(v[i], LOG2);
+    if (i < n) out[i] = log2fix(v[i], tb);
 }
-__global__ void k_stage_edge(const i64* h, i64* out, i64 n, const int* PHI) {
+__global__ void k_stage_edge(const i64* h, i64* out, i64 n, Tables tb) {
     const i64 i = (i64)blockIdx.x * blockDim.x + threadIdx.x;
-    if (i < n) out[i] = edge1(h[i], PHI);
+    if (i < n) out[i] = edge1(h[i], tb);
 }
 // to16 per row (one block per row); gauge != 0 also gives LS for rows of 768 (base2.py:24-27, 55-60)
 __global__ __launch_bounds__(NTHR) void k_stage_rows(const i64* X, int n, int gauge, i64* x16, i64* ex, i64* LS, Tables tb) {
-    __shared__ i64 red[4];
+    __shared__ i64 red[8];
     const int tid = threadIdx.x;
     const i64* x = X + (size_t)blockIdx.x * n;
     i64 o = 0;
@@ -367,9 +503,8 @@ __global__ __launch_bounds__(NTHR) void k_stage_rows(const i64* X, int n, int ga
     }
     const i64 e = -16 + sh;
     if (gauge) {
-        s1 = block_reduce(s1, red, OpAdd(), tid);
-        s2 = block_reduce(s2, red, OpAdd(), tid);
-        if (tid == 0) LS[blockIdx.x] = gauge_ls(s1, s2, e, tb.log768, tb.eps40, tb.LOG2);
+        block_sum2(s1, s2, red, tid);
+        if (tid == 0) LS[blockIdx.x] = gauge_ls(s1, s2, e, tb);
     }
     if (tid == 0) ex[blockIdx.x] = e;
 }
@@ -399,16 +534,16 @@ __global__ __launch_bounds__(1024) void k_stage_race(const i64* v, i64 n, i64* o
 }
 
 // ---------------------------------------------------------------------------------------------------------
-// explicit instantiations used by the host
-#define INST(NIN, TC, PRO, EPI) template __global__ void k_gemv<NIN, TC, PRO, EPI>(GemvArgs);
-INST(768, 8, PRO_EMBED, EPI_GAUGED)
-INST(768, 8, PRO_GAUGE, EPI_GAUGED)
-INST(768, 2, PRO_TO16, EPI_PLAIN_ADD)
-INST(768, 8, PRO_GAUGE, EPI_GAUGED_EDGE)
-INST(3072, 2, PRO_TO16, EPI_PLAIN_ADD)
-INST(768, 8, PRO_GAUGE, EPI_HEAD)
-// stage/product test instantiations: raw piles of a given light
-INST(768, 8, PRO_X16, EPI_PILE)
-INST(768, 2, PRO_X16, EPI_PILE)
-INST(3072, 2, PRO_X16, EPI_PILE)
-INST(3072, 8, PRO_X16, EPI_PILE)
+// explicit instantiations used by the host: <NIN, TC, waves per block, prologue, epilogue>
+#define INST(NIN, TC, WPB, PRO, EPI) template __global__ void k_gemv<NIN, TC, WPB, PRO, EPI>(GemvArgs);
+INST(768, 2, 4, PRO_EMBED, EPI_GAUGED)        // qkv of layer 0 (the word enters)
+INST(768, 2, 4, PRO_GAUGE, EPI_GAUGED)        // qkv
+INST(768, 2, 2, PRO_TO16, EPI_PLAIN_ADD)      // proj
+INST(768, 2, 4, PRO_GAUGE, EPI_GAUGED_EDGE)   // fc
+INST(3072, 1, 4, PRO_TO16, EPI_PLAIN_ADD)     // mproj
+INST(768, 8, 4, PRO_GAUGE, EPI_HEAD)          // head + race
+// raw piles of a given light (stage entry point)
+INST(768, 2, 4, PRO_X16, EPI_PILE)
+INST(768, 8, 4, PRO_X16, EPI_PILE)
+INST(3072, 1, 4, PRO_X16, EPI_PILE)
+INST(3072, 2, 4, PRO_X16, EPI_PILE)

@@ -93,10 +93,13 @@ static void free_plate(DevPlate& P) {
 // tables
 struct sm_tables {
     int* LOG2 = nullptr; int* EXP2 = nullptr; int* PHI = nullptr; int* ARR = nullptr;
+    int* GPOW = nullptr; int* HPOW = nullptr;
     int alen = 0;
     i64 log768 = 0, eps40 = 0;
-    int* scratch = nullptr;   // [0] pos for sm_stage_attend, [1] error bits
-    Tables tb() const { return Tables{LOG2, EXP2, PHI, ARR, alen, log768, eps40}; }
+    int verified = 0;         // every entry equals its defining formula (checked on the device)
+    int force_memory = 1;     // read the tables from memory (the default; the recomputed form is slower)
+    int* scratch = nullptr;   // [0] pos for sm_stage_attend, [1] error bits, [4..7] mismatch counts
+    Tables tb() const { return Tables{LOG2, EXP2, PHI, ARR, alen, log768, eps40, verified && !force_memory, GPOW, HPOW}; }
 };
 
 static int upload_table(int** dst, const i64* src, size_t n, i64 lo, i64 hi, const char* name) {
@@ -119,14 +122,31 @@ static int tables_init(sm_tables& T, const i64* phi, const i64* arr, int alen, c
     if ((rc = upload_table(&T.ARR, arr, alen, 0, 1 << 24, "arrival"))) return rc;
     if ((rc = upload_table(&T.LOG2, log2t, 65536, 0, 65536, "log2"))) return rc;
     if ((rc = upload_table(&T.EXP2, exp2t, 65536, 65536, 131072, "exp2"))) return rc;
+    // derived tables: exact integer compositions of LOG2 and EXP2 (see Tables in sm_device.h)
+    {
+        std::vector<i64> g(2 * 65536), hp(65536);
+        for (int r = 0; r < 2; r++)
+            for (int m = 0; m < 65536; m++) g[r * 65536 + m] = exp2t[(log768 - (((i64)r * 65536 + log2t[m]) >> 1)) & 0xFFFF];
+        for (int m = 0; m < 65536; m++) hp[m] = exp2t[(-log2t[m]) & 0xFFFF];
+        if ((rc = upload_table(&T.GPOW, g.data(), g.size(), 65536, 131072, "gauge power")) ||
+            (rc = upload_table(&T.HPOW, hp.data(), hp.size(), 65536, 131072, "arrival divisor")))
+            return rc;
+    }
     if ((rc = dalloc(&T.scratch, 16))) return rc;
     HIP_TRY(hipMemset(T.scratch, 0, 64));
     T.alen = alen; T.log768 = log768; T.eps40 = eps40;
+    // every entry against its formula: the arithmetic form is used only if all of them agree
+    const int n = alen + 1 > 65536 ? alen + 1 : 65536;
+    k_check_tables<<<(n + 255) / 256, 256>>>(T.tb(), reinterpret_cast<unsigned*>(T.scratch + 4));
+    HIP_TRY(hipGetLastError());
+    unsigned bad[4];
+    HIP_TRY(hipMemcpy(bad, T.scratch + 4, sizeof(bad), hipMemcpyDeviceToHost));
+    T.verified = (bad[0] | bad[1] | bad[2] | bad[3]) == 0;
     return SM_OK;
 }
 
 static void tables_free(sm_tables& T) {
-    hfree(T.LOG2); hfree(T.EXP2); hfree(T.PHI); hfree(T.ARR); hfree(T.scratch);
+    hfree(T.LOG2); hfree(T.EXP2); hfree(T.PHI); hfree(T.ARR); hfree(T.GPOW); hfree(T.HPOW); hfree(T.scratch);
     T = sm_tables();
 }
 
@@ -135,7 +155,7 @@ static void tables_free(sm_tables& T) {
 enum { CTL_POS = 0, CTL_PLEN = 1, CTL_NWORDS = 2, CTL_ERR = 3, CTL_RECPOS = 4, CTL_COUNTER = 5, CTL_N = 8 };
 static const int NIN[4] = {768, 768, 768, 3072};
 static const int NOUT[4] = {2304, 768, 3072, 768};
-static const int TCOLS[4] = {8, 2, 8, 2};
+static const int TCOLS[4] = {2, 2, 2, 1};      // tile widths: qkv, proj, fc, mproj (one wave per tile)
 static const char* BANK[4] = {"qkv", "proj", "fc", "mproj"};
 
 struct sm_machine {
@@ -272,8 +292,9 @@ static int launch_step(sm_machine* m, int parts = STEP_ALL) {
             a.wte = m->wte; a.wpe = m->wpe; a.seq = m->seq; a.Rw = m->R;
             a.rx16 = m->r_x16 + (l * 4 + 0) * 3072; a.rexls = m->r_exls + (l * 4 + 0) * 2;
             a.rpile = m->r_pile + (l * 4 + 0) * 3072; a.rout = m->r_qkv + l * 2304;
-            if (l == 0) k_gemv<768, 8, PRO_EMBED, EPI_GAUGED><<<P.ntiles, NTHR, 0, m->st>>>(a);
-            else k_gemv<768, 8, PRO_GAUGE, EPI_GAUGED><<<P.ntiles, NTHR, 0, m->st>>>(a);
+            const int g = (P.ntiles + 3) / 4;
+            if (l == 0) k_gemv<768, 2, 4, PRO_EMBED, EPI_GAUGED><<<g, 256, 0, m->st>>>(a);
+            else k_gemv<768, 2, 4, PRO_GAUGE, EPI_GAUGED><<<g, 256, 0, m->st>>>(a);
         }
         // attention (base2.py:85-100) on the KV cache of layer l
         {
@@ -282,7 +303,7 @@ static int launch_step(sm_machine* m, int parts = STEP_ALL) {
             a.QKV = m->QKV; a.K16 = m->K16 + l * per * 768; a.EK = m->EK + l * per * 12; a.V = m->V + l * per * 768;
             a.out = m->att; a.pos = ctl + CTL_POS; a.ctx = m->ctx; a.tb = tb; a.err = ctl + CTL_ERR;
             a.rec_pos = ctl + CTL_RECPOS; a.ratt = m->r_att + l * 768;
-            k_attend<<<dim3(12, m->B), NTHR, (size_t)m->ctx * 12, m->st>>>(a);
+            k_attend<<<dim3(12, m->B), NTHR, (size_t)m->ctx * 8, m->st>>>(a);
         }
         // proj: to16 of the attention row, product, plain shift + bias, added to R (base2.py:105)
         {
@@ -292,7 +313,7 @@ static int launch_step(sm_machine* m, int parts = STEP_ALL) {
             a.X = m->att; a.Y = m->R;
             a.rx16 = m->r_x16 + (l * 4 + 1) * 3072; a.rexls = m->r_exls + (l * 4 + 1) * 2;
             a.rpile = m->r_pile + (l * 4 + 1) * 3072; a.rout = m->r_resid + (l * 2 + 0) * 768;
-            k_gemv<768, 2, PRO_TO16, EPI_PLAIN_ADD><<<P.ntiles, NTHR, 0, m->st>>>(a);
+            k_gemv<768, 2, 2, PRO_TO16, EPI_PLAIN_ADD><<<(P.ntiles + 1) / 2, 128, 0, m->st>>>(a);
         }
         // fc: gauge, product, gauged, edge (base2.py:106)
         {
@@ -302,7 +323,7 @@ static int launch_step(sm_machine* m, int parts = STEP_ALL) {
             a.X = m->R; a.Y = m->hid;
             a.rx16 = m->r_x16 + (l * 4 + 2) * 3072; a.rexls = m->r_exls + (l * 4 + 2) * 2;
             a.rpile = m->r_pile + (l * 4 + 2) * 3072; a.rout = m->r_hid + l * 3072;
-            k_gemv<768, 8, PRO_GAUGE, EPI_GAUGED_EDGE><<<P.ntiles, NTHR, 0, m->st>>>(a);
+            k_gemv<768, 2, 4, PRO_GAUGE, EPI_GAUGED_EDGE><<<(P.ntiles + 3) / 4, 256, 0, m->st>>>(a);
         }
         // mproj: to16 of the hidden row (3072), product, plain, added to R (base2.py:106)
         {
@@ -312,7 +333,7 @@ static int launch_step(sm_machine* m, int parts = STEP_ALL) {
             a.X = m->hid; a.Y = m->R;
             a.rx16 = m->r_x16 + (l * 4 + 3) * 3072; a.rexls = m->r_exls + (l * 4 + 3) * 2;
             a.rpile = m->r_pile + (l * 4 + 3) * 3072; a.rout = m->r_resid + (l * 2 + 1) * 768;
-            k_gemv<3072, 2, PRO_TO16, EPI_PLAIN_ADD><<<P.ntiles, NTHR, 0, m->st>>>(a);
+            k_gemv<3072, 1, 4, PRO_TO16, EPI_PLAIN_ADD><<<(P.ntiles + 3) / 4, 256, 0, m->st>>>(a);
         }
     }
     // head: gauge, product with the tied word table, power + standing amount, race (base2.py:107-114)
@@ -326,7 +347,7 @@ static int launch_step(sm_machine* m, int parts = STEP_ALL) {
         a.rx16 = m->r_hx16; a.rexls = m->r_hexls; a.rpile = m->r_hpile; a.rlogits = m->r_logits;
         a.part_v = m->part_v; a.part_i = m->part_i; a.counter = reinterpret_cast<unsigned*>(ctl + CTL_COUNTER);
         a.seq_w = m->seq; a.plen = ctl + CTL_PLEN; a.pos_w = ctl + CTL_POS; a.words = m->words; a.nwords = ctl + CTL_NWORDS;
-        k_gemv<768, 8, PRO_GAUGE, EPI_HEAD><<<m->head_grid, NTHR, 0, m->st>>>(a);
+        k_gemv<768, 8, 4, PRO_GAUGE, EPI_HEAD><<<m->head_grid, 256, 0, m->st>>>(a);
     }
     HIP_TRY(hipGetLastError());
     return SM_OK;
@@ -335,7 +356,7 @@ static int launch_step(sm_machine* m, int parts = STEP_ALL) {
 extern "C" int sm_create(const char* layout_dir, const sm_config* cfg, sm_machine** out) {
     if (!layout_dir || !out) return fail(SM_E_ARG, "sm_create: null argument");
     *out = nullptr;
-    sm_config c{1, 1024, 1, 0, 16, 0};
+    sm_config c{1, 1024, 1, 0, 16, 0, 0};
     if (cfg) c = *cfg;
     if (c.max_streams != 1) return fail(SM_E_ARG, "sm_create: this build decodes one stream per machine (max_streams = 1)");
     if (c.max_ctx <= 0) return fail(SM_E_ARG, "sm_create: max_ctx must be positive");
@@ -399,9 +420,10 @@ extern "C" int sm_create(const char* layout_dir, const sm_config* cfg, sm_machin
             (rc = read_array(dir + "log2.bin", lg, 65536)) || (rc = read_array(dir + "exp2.bin", ep, 65536)))
             return bail(rc);
         if ((rc = tables_init(m->T, phi.data(), arr.data(), (int)alen, lg.data(), ep.data(), log768, eps40))) return bail(rc);
+        m->T.force_memory = c.table_mode != 1;
     }
     m->ctx = c.max_ctx < m->npos ? c.max_ctx : m->npos;
-    m->head_grid = c.head_grid > 0 ? c.head_grid : 1024;
+    m->head_grid = c.head_grid > 0 ? c.head_grid : 512;
     // state
     const size_t B = m->B, ctx = m->ctx;
     if ((rc = dalloc(&m->R, B * 768)) || (rc = dalloc(&m->QKV, B * 2304)) || (rc = dalloc(&m->att, B * 768)) ||
@@ -604,8 +626,10 @@ extern "C" int sm_read(sm_machine* m, int32_t what, int32_t layer, int32_t strea
     return SM_OK;
 }
 
-extern "C" int sm_info(const sm_machine* m, int32_t* vocab, int32_t* max_ctx, int32_t* max_streams, int32_t* n_pos) {
+extern "C" int sm_info(const sm_machine* m, int32_t* vocab, int32_t* max_ctx, int32_t* max_streams, int32_t* n_pos,
+                       int32_t* arith_tables) {
     if (!m) return fail(SM_E_ARG, "sm_info: null machine");
+    if (arith_tables) *arith_tables = m->T.tb().arith;
     if (vocab) *vocab = m->vocab;
     if (max_ctx) *max_ctx = m->ctx;
     if (max_streams) *max_streams = m->B;
@@ -625,6 +649,13 @@ extern "C" int sm_tables_create(const int64_t* phi, const int64_t* arrival, int3
     return SM_OK;
 }
 
+extern "C" int sm_tables_mode(sm_tables* t, int32_t force_memory, int32_t* arith_tables) {
+    if (!t) return fail(SM_E_ARG, "sm_tables_mode: null tables");
+    if (force_memory >= 0) t->force_memory = force_memory != 0;
+    if (arith_tables) *arith_tables = t->tb().arith;
+    return SM_OK;
+}
+
 extern "C" int sm_tables_destroy(sm_tables* t) {
     if (t) { tables_free(*t); delete t; }
     return SM_OK;
@@ -640,19 +671,19 @@ extern "C" int sm_stage_rshift(const int64_t* x, const int64_t* s, int64_t* out,
 }
 extern "C" int sm_stage_log2fix(const sm_tables* t, const int64_t* v, int64_t* out, int64_t n, void* stream) {
     if (!t || n < 0 || (n > 0 && (!v || !out))) return fail(SM_E_ARG, "sm_stage_log2fix: arguments");
-    if (n) k_stage_log2fix<<<blocks_for(n, 256), 256, 0, (hipStream_t)stream>>>((const i64*)v, (i64*)out, n, t->LOG2);
+    if (n) k_stage_log2fix<<<blocks_for(n, 256), 256, 0, (hipStream_t)stream>>>((const i64*)v, (i64*)out, n, t->tb());
     HIP_TRY(hipGetLastError());
     return SM_OK;
 }
 extern "C" int sm_stage_power(const sm_tables* t, const int64_t* x, const int64_t* F, int64_t* out, int64_t n, void* stream) {
     if (!t || n < 0 || (n > 0 && (!x || !F || !out))) return fail(SM_E_ARG, "sm_stage_power: arguments");
-    if (n) k_stage_power<<<blocks_for(n, 256), 256, 0, (hipStream_t)stream>>>((const i64*)x, (const i64*)F, (i64*)out, n, t->EXP2);
+    if (n) k_stage_power<<<blocks_for(n, 256), 256, 0, (hipStream_t)stream>>>((const i64*)x, (const i64*)F, (i64*)out, n, t->tb());
     HIP_TRY(hipGetLastError());
     return SM_OK;
 }
 extern "C" int sm_stage_edge(const sm_tables* t, const int64_t* h, int64_t* out, int64_t n, void* stream) {
     if (!t || n < 0 || (n > 0 && (!h || !out))) return fail(SM_E_ARG, "sm_stage_edge: arguments");
-    if (n) k_stage_edge<<<blocks_for(n, 256), 256, 0, (hipStream_t)stream>>>((const i64*)h, (i64*)out, n, t->PHI);
+    if (n) k_stage_edge<<<blocks_for(n, 256), 256, 0, (hipStream_t)stream>>>((const i64*)h, (i64*)out, n, t->tb());
     HIP_TRY(hipGetLastError());
     return SM_OK;
 }
@@ -684,7 +715,7 @@ extern "C" int sm_stage_attend(const sm_tables* t, const int64_t* qkv, int32_t* 
     AttArgs a{};
     a.QKV = (const i64*)qkv; a.K16 = k16; a.EK = ek; a.V = v; a.out = (i64*)out; a.pos = t->scratch; a.ctx = ctx;
     a.tb = t->tb(); a.err = t->scratch + 1;
-    k_attend<<<dim3(12, 1), NTHR, (size_t)ctx * 12, s>>>(a);
+    k_attend<<<dim3(12, 1), NTHR, (size_t)ctx * 8, s>>>(a);
     HIP_TRY(hipGetLastError());
     int err = 0;
     HIP_TRY(hipMemcpyAsync(&err, t->scratch + 1, 4, hipMemcpyDeviceToHost, s));
@@ -700,8 +731,8 @@ struct sm_plate { DevPlate P; };
 
 extern "C" int sm_plate_create(const int16_t* w, const int32_t* e, const int64_t* b, int32_t nin, int32_t nout, int32_t tile_cols, sm_plate** out) {
     if (!w || !e || !b || !out) return fail(SM_E_ARG, "sm_plate_create: null argument");
-    if (!((nin == 768 || nin == 3072) && (tile_cols == 2 || tile_cols == 8)))
-        return fail(SM_E_ARG, "sm_plate_create: built for nin in {768, 3072} and tile_cols in {2, 8}");
+    if (!((nin == 768 && (tile_cols == 2 || tile_cols == 8)) || (nin == 3072 && (tile_cols == 1 || tile_cols == 2))))
+        return fail(SM_E_ARG, "sm_plate_create: built for (nin, tile_cols) in (768, 2), (768, 8), (3072, 1), (3072, 2)");
     sm_plate* p = new sm_plate();
     int rc = upload_plate(p->P, w, e, (const i64*)b, nin, nout, tile_cols);
     if (rc) { free_plate(p->P); delete p; return rc; }
@@ -720,12 +751,12 @@ extern "C" int sm_plate_product(const sm_plate* p, const int64_t* x16, int64_t* 
     GemvArgs a{};
     a.W = reinterpret_cast<const int4*>(P.W); a.we = P.e; a.bias = P.b; a.nout = P.nout; a.ntiles = P.ntiles;
     a.X = (const i64*)x16; a.Y = (i64*)pile;
-    const int g = grid > 0 ? grid : P.ntiles;
+    const int g = grid > 0 ? grid : (P.ntiles + 3) / 4;     // four waves per block, one tile per wave
     hipStream_t s = (hipStream_t)stream;
-    if (P.nin == 768 && P.tc == 8) k_gemv<768, 8, PRO_X16, EPI_PILE><<<g, NTHR, 0, s>>>(a);
-    else if (P.nin == 768 && P.tc == 2) k_gemv<768, 2, PRO_X16, EPI_PILE><<<g, NTHR, 0, s>>>(a);
-    else if (P.nin == 3072 && P.tc == 2) k_gemv<3072, 2, PRO_X16, EPI_PILE><<<g, NTHR, 0, s>>>(a);
-    else k_gemv<3072, 8, PRO_X16, EPI_PILE><<<g, NTHR, 0, s>>>(a);
+    if (P.nin == 768 && P.tc == 8) k_gemv<768, 8, 4, PRO_X16, EPI_PILE><<<g, 256, 0, s>>>(a);
+    else if (P.nin == 768 && P.tc == 2) k_gemv<768, 2, 4, PRO_X16, EPI_PILE><<<g, 256, 0, s>>>(a);
+    else if (P.nin == 3072 && P.tc == 1) k_gemv<3072, 1, 4, PRO_X16, EPI_PILE><<<g, 256, 0, s>>>(a);
+    else k_gemv<3072, 2, 4, PRO_X16, EPI_PILE><<<g, 256, 0, s>>>(a);
     HIP_TRY(hipGetLastError());
     return SM_OK;
 }

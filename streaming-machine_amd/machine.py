@@ -30,7 +30,8 @@ class SmError(RuntimeError):
 
 class SmConfig(ctypes.Structure):
     _fields_ = [("max_streams", ctypes.c_int32), ("max_ctx", ctypes.c_int32), ("use_graph", ctypes.c_int32),
-                ("head_grid", ctypes.c_int32), ("graph_steps", ctypes.c_int32), ("profile", ctypes.c_int32)]
+                ("head_grid", ctypes.c_int32), ("graph_steps", ctypes.c_int32), ("profile", ctypes.c_int32),
+                ("table_mode", ctypes.c_int32)]
 
 
 _LIB = None
@@ -54,7 +55,8 @@ def lib():
         L.sm_generate.argtypes = [vp, i32, i32p]
         L.sm_record_at.argtypes = [vp, i32]
         L.sm_read.argtypes = [vp, i32, i32, i32, i32, vp, ctypes.c_size_t]
-        L.sm_info.argtypes = [vp, i32p, i32p, i32p, i32p]
+        L.sm_info.argtypes = [vp, i32p, i32p, i32p, i32p, i32p]
+        L.sm_tables_mode.argtypes = [vp, i32, i32p]
         L.sm_profile.argtypes = [vp, i64p, ctypes.POINTER(ctypes.c_double), i32]
         L.sm_tables_create.argtypes = [i64p, i64p, i32, i64p, i64p, i64, i64, ctypes.POINTER(vp)]
         L.sm_tables_destroy.argtypes = [vp]
@@ -97,19 +99,21 @@ class Machine:
     """
 
     def __init__(self, layout_dir: str, max_ctx: int = 1024, max_streams: int = 1, use_graph: bool = True,
-                 head_grid: int = 0, graph_steps: int = 16, profile: bool = False,
+                 head_grid: int = 0, graph_steps: int = 16, profile: bool = False, memory_tables: bool = True,
                  gauge: str = "int", edge: str = "int", arrival: str = "int"):
         for name, v in (("gauge", gauge), ("edge", edge), ("arrival", arrival)):
             if v != "int":
                 raise NotImplementedError(f"{name}={v}: the GPU machine runs the integer stages only")
         self.L = lib()
-        cfg = SmConfig(max_streams, max_ctx, 1 if use_graph else 0, head_grid, graph_steps, 1 if profile else 0)
+        cfg = SmConfig(max_streams, max_ctx, 1 if use_graph else 0, head_grid, graph_steps, 1 if profile else 0,
+                       0 if memory_tables else 1)
         h = vp()
         check(self.L.sm_create(os.fsencode(layout_dir), ctypes.byref(cfg), ctypes.byref(h)))
         self.h = h
-        v, c, s, n = i32(), i32(), i32(), i32()
-        check(self.L.sm_info(self.h, ctypes.byref(v), ctypes.byref(c), ctypes.byref(s), ctypes.byref(n)))
+        v, c, s, n, ar = i32(), i32(), i32(), i32(), i32()
+        check(self.L.sm_info(self.h, ctypes.byref(v), ctypes.byref(c), ctypes.byref(s), ctypes.byref(n), ctypes.byref(ar)))
         self.vocab, self.max_ctx, self.max_streams, self.n_pos = v.value, c.value, s.value, n.value
+        self.arith_tables = bool(ar.value)
 
     def close(self):
         if getattr(self, "h", None):
@@ -173,6 +177,12 @@ class Tables:
                                       lg.ctypes.data_as(i64p), ep.ctypes.data_as(i64p), int(tabs["log2_768"]),
                                       int(tabs["eps40"]), ctypes.byref(h)))
         self.h = h
+
+    def mode(self, force_memory: int = -1) -> bool:
+        """force_memory 1/0 switches the table source (-1 leaves it); True when entries are recomputed"""
+        ar = i32()
+        check(self.L.sm_tables_mode(self.h, force_memory, ctypes.byref(ar)))
+        return bool(ar.value)
 
     def close(self):
         if getattr(self, "h", None):

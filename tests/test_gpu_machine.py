@@ -49,17 +49,19 @@ def compare_record(got: dict, want: dict):
     assert not bad, f"{len(bad)} intermediates differ, first: {sorted(bad)[:8]}"
 
 
-@pytest.mark.parametrize("use_graph", [True, False])
-def test_small_model_words(sm, small_dir, golden, use_graph):
+@pytest.mark.parametrize("use_graph,memory_tables", [(True, True), (False, True), (True, False)])
+def test_small_model_words(sm, small_dir, golden, use_graph, memory_tables):
     c = golden_case(golden, "small_p8_w8")
-    m = sm.Machine(small_dir, max_ctx=64, use_graph=use_graph)
+    m = sm.Machine(small_dir, max_ctx=64, use_graph=use_graph, memory_tables=memory_tables)
+    assert m.arith_tables == (not memory_tables)
     assert m.stream(c["prompt"], len(c["words"])) == c["words"]
     m.close()
 
 
-def test_small_model_record(sm, small_dir, golden):
+@pytest.mark.parametrize("memory_tables", [False, True])
+def test_small_model_record(sm, small_dir, golden, memory_tables):
     c = golden_case(golden, "small_p8_w8")
-    m = sm.Machine(small_dir, max_ctx=64)
+    m = sm.Machine(small_dir, max_ctx=64, memory_tables=memory_tables)
     last = c["records"]["last"]
     m.reset()
     m.record_at(last["position"])

@@ -27,8 +27,33 @@ def tabs(sm):
 
 
 @pytest.fixture(scope="module")
-def dtabs(sm, tabs):
+def dtabs_obj(sm, tabs):
     return sm.Tables(tabs)
+
+
+@pytest.fixture(scope="module", params=["arith", "memory"])
+def dtabs(request, dtabs_obj):
+    """the device tables, once with entries recomputed from their formulas and once read from memory"""
+    arith = dtabs_obj.mode(force_memory=0 if request.param == "arith" else 1)
+    assert arith == (request.param == "arith")
+    yield dtabs_obj
+    dtabs_obj.mode(force_memory=0)
+
+
+def test_tables_verified_against_their_formulas(dtabs_obj):
+    """every loaded entry equals its defining formula evaluated on the device"""
+    assert dtabs_obj.mode(force_memory=0) is True
+    assert dtabs_obj.mode(force_memory=1) is False
+
+
+def test_tampered_table_is_not_recomputed(sm, tabs):
+    """one changed entry: the device check must refuse the arithmetic form and read the tables"""
+    bad = dict(tabs)
+    bad["exp2"] = tabs["exp2"].copy()
+    bad["exp2"][12345] += 1
+    t = sm.Tables(bad)
+    assert t.mode(force_memory=0) is False
+    t.close()
 
 
 @pytest.fixture(scope="module")
@@ -120,7 +145,7 @@ def test_race(sm, orc, n):
     assert int(host(do)[0]) == orc.race(v) == int(np.argmax(v))
 
 
-SHAPES = [(768, 2304, 8), (768, 768, 2), (768, 3072, 8), (3072, 768, 2), (768, 50257, 8), (3072, 768, 8)]
+SHAPES = [(768, 2304, 2), (768, 768, 2), (768, 3072, 2), (3072, 768, 1), (768, 50257, 8), (3072, 768, 2), (768, 2304, 8)]
 
 
 @pytest.mark.parametrize("nin,nout,tc", SHAPES)
