@@ -13,6 +13,8 @@
 #include "sm_kernels.hip"
 #include "../../include/sm_base2.h"
 
+#include <hip/hip_ext.h>
+
 #include <cstdio>
 #include <cstring>
 #include <fstream>
@@ -275,7 +277,7 @@ static void machine_free(sm_machine* m) {
 
 // the launch sequence of one decode step (all streams, one position each): the layers and/or the head
 enum { STEP_ALL = 3, STEP_LAYERS = 1, STEP_HEAD = 2 };
-static int launch_step(sm_machine* m, int parts = STEP_ALL) {
+static int launch_step(sm_machine* m, int parts = STEP_ALL, hipEvent_t hs = nullptr, hipEvent_t he = nullptr) {
     const Tables tb = m->T.tb();
     int* ctl = m->ctl;
     for (int l = 0; l < 12 && (parts & STEP_LAYERS); l++) {
@@ -347,7 +349,10 @@ static int launch_step(sm_machine* m, int parts = STEP_ALL) {
         a.rx16 = m->r_hx16; a.rexls = m->r_hexls; a.rpile = m->r_hpile; a.rlogits = m->r_logits;
         a.part_v = m->part_v; a.part_i = m->part_i; a.counter = reinterpret_cast<unsigned*>(ctl + CTL_COUNTER);
         a.seq_w = m->seq; a.plen = ctl + CTL_PLEN; a.pos_w = ctl + CTL_POS; a.words = m->words; a.nwords = ctl + CTL_NWORDS;
-        k_gemv<768, 8, 4, PRO_GAUGE, EPI_HEAD><<<m->head_grid, 256, 0, m->st>>>(a);
+        if (hs)   // timed: the event pair is stamped by this dispatch itself (the interval a kernel trace reports)
+            hipExtLaunchKernelGGL(k_gemv<768, 8, 4, PRO_GAUGE, EPI_HEAD>, dim3(m->head_grid), dim3(256), 0, m->st, hs, he, 0, a);
+        else
+            k_gemv<768, 8, 4, PRO_GAUGE, EPI_HEAD><<<m->head_grid, 256, 0, m->st>>>(a);
     }
     HIP_TRY(hipGetLastError());
     return SM_OK;
@@ -511,22 +516,17 @@ static int capture(sm_machine* m, int which, int n, int parts) {
     return SM_OK;
 }
 
-// one profiled step: the layers, then the head bracketed by HIP events recorded on the machine's stream
+// one profiled step: the layers (a captured graph, or plain launches), then the head launched with the HIP
+// event pair its own dispatch stamps, on the machine's stream
 static int profiled_step(sm_machine* m, int slot) {
     int rc;
     if (m->cfg.use_graph) {
-        if ((rc = capture(m, 2, 1, STEP_LAYERS)) || (rc = capture(m, 3, 1, STEP_HEAD))) return rc;
+        if ((rc = capture(m, 2, 1, STEP_LAYERS))) return rc;
         HIP_TRY(hipGraphLaunch(m->gexec[2], m->st));
-        HIP_TRY(hipEventRecord(m->ev_s[slot], m->st));
-        HIP_TRY(hipGraphLaunch(m->gexec[3], m->st));
-        HIP_TRY(hipEventRecord(m->ev_e[slot], m->st));
-    } else {
-        if ((rc = launch_step(m, STEP_LAYERS))) return rc;
-        HIP_TRY(hipEventRecord(m->ev_s[slot], m->st));
-        if ((rc = launch_step(m, STEP_HEAD))) return rc;
-        HIP_TRY(hipEventRecord(m->ev_e[slot], m->st));
+    } else if ((rc = launch_step(m, STEP_LAYERS))) {
+        return rc;
     }
-    return SM_OK;
+    return launch_step(m, STEP_HEAD, m->ev_s[slot], m->ev_e[slot]);
 }
 
 // wait for the n profiled steps just queued and add their head durations
