@@ -133,7 +133,9 @@ int sm_stage_race(const int64_t* v, int64_t n, int64_t* out_index, void* stream)
 int sm_stage_attend(const sm_tables* t, const int64_t* qkv, int32_t* k16, int32_t* ek, int32_t* v,
                     int32_t pos, int32_t ctx, int64_t* out, void* stream);
 
-/* A plate on the device (laid out for the GEMV), from an input-major int16 [nin][nout] host array. */
+/* A plate on the device from an input-major int16 [nin][nout] host array: tile_cols > 0 lays it out for the
+ * one-row GEMV (sm_plate_product), tile_cols == 0 as int8 MFMA byte planes for rows of lights
+ * (sm_plate_product_rows, the batched streams' layout). */
 typedef struct sm_plate sm_plate;
 int sm_plate_create(const int16_t* w, const int32_t* e, const int64_t* b, int32_t nin, int32_t nout,
                     int32_t tile_cols, sm_plate** out);
@@ -141,6 +143,10 @@ int sm_plate_destroy(sm_plate* p);
 /* pile[j] = sum_i x16[i] w[i][j], exact (base2.py:29-32; the split cells of base2_stream.swift:61-73).
  * x16: device int64 [nin] with values in [-32768, 32768]; pile: device int64 [nout]. */
 int sm_plate_product(const sm_plate* p, const int64_t* x16, int64_t* pile, int32_t grid, void* stream);
+/* pile[r][j] = sum_i x16[r][i] w[i][j] for rows r < rows <= 64, exact, through the int8 MFMA byte-plane
+ * contraction (base2.py:29-32 for every row of a batch).  x16: device int64 [rows][nin] in [-32768, 32768];
+ * pile: device int64 [rows][nout].  Calls on one plate share its light planes: serialise them. */
+int sm_plate_product_rows(const sm_plate* p, const int64_t* x16, int32_t rows, int64_t* pile, void* stream);
 /* bytes of the device plate (for bandwidth accounting) */
 int64_t sm_plate_bytes(const sm_plate* p);
 

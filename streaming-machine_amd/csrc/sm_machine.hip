@@ -11,6 +11,7 @@
 // graph_steps consecutive steps replays the loop; the host synchronises once per sm_generate call
 // (base2_stream.swift:273-281 commits one command buffer per prompt the same way).
 #include "sm_kernels.hip"
+#include "sm_batch.hip"
 #include "../../include/sm_base2.h"
 
 #include <hip/hip_ext.h>
@@ -91,6 +92,50 @@ static void free_plate(DevPlate& P) {
     P = DevPlate();
 }
 
+// Byte planes for the MFMA path: column tiles of 16, 64-k steps, planes wh and wl' = (w & 255) - 128, in the
+// MFMA B-operand order (lane l: column l % 16, bytes k = 16 (l / 16) + b); plus each column's plane sums.
+struct MfmaPlate {
+    int K = 0, N = 0, ntiles = 0;
+    signed char* W = nullptr;
+    int* csum = nullptr;
+    int* e = nullptr;
+    i64* b = nullptr;
+};
+
+static int upload_mfma_plate(MfmaPlate& P, const int16_t* w, const int32_t* e, const i64* b, int K, int N) {
+    if (K % 64 || N <= 0) return fail(SM_E_ARG, "mfma plate: K must be a multiple of 64");
+    const int KS = K / 64, nt = (N + 15) / 16;
+    P.K = K; P.N = N; P.ntiles = nt;
+    std::vector<signed char> out((size_t)nt * KS * 2 * 1024, 0);
+    std::vector<int> cs((size_t)N * 2, 0);
+    for (int k = 0; k < K; k++) {
+        const int16_t* row = w + (size_t)k * N;
+        const int s = k >> 6, kk = k & 63, g = kk >> 4, bb = kk & 15;
+        for (int col = 0; col < N; col++) {
+            const int v = row[col], wh = v >> 8, wl = (v & 255) - 128;
+            const size_t base = ((size_t)((col >> 4) * KS + s) * 2) * 1024 + (size_t)((col & 15) + 16 * g) * 16 + bb;
+            out[base] = (signed char)wh;
+            out[base + 1024] = (signed char)wl;
+            cs[2 * col] += wh;
+            cs[2 * col + 1] += wl;
+        }
+    }
+    int rc;
+    if ((rc = dalloc(&P.W, out.size())) || (rc = dalloc(&P.csum, cs.size())) || (rc = dalloc(&P.e, (size_t)N)) ||
+        (rc = dalloc(&P.b, (size_t)N)))
+        return rc;
+    HIP_TRY(hipMemcpy(P.W, out.data(), out.size(), hipMemcpyHostToDevice));
+    HIP_TRY(hipMemcpy(P.csum, cs.data(), cs.size() * 4, hipMemcpyHostToDevice));
+    HIP_TRY(hipMemcpy(P.e, e, (size_t)N * 4, hipMemcpyHostToDevice));
+    HIP_TRY(hipMemcpy(P.b, b, (size_t)N * 8, hipMemcpyHostToDevice));
+    return SM_OK;
+}
+
+static void free_mfma_plate(MfmaPlate& P) {
+    hfree(P.W); hfree(P.csum); hfree(P.e); hfree(P.b);
+    P = MfmaPlate();
+}
+
 // ---------------------------------------------------------------------------------------------------------
 // tables
 struct sm_tables {
@@ -164,8 +209,12 @@ struct sm_machine {
     sm_config cfg{};
     int B = 1, ctx = 0, vocab = 0, npos = 0, head_grid = 1024;
     hipStream_t st = nullptr;
-    DevPlate bank[12][4];
+    DevPlate bank[12][4];          // batch 1: GEMV tiles
     DevPlate head;
+    MfmaPlate mbank[12][4];        // batched streams: MFMA byte planes
+    MfmaPlate mhead;
+    signed char* planes = nullptr; // [4][48][3][1024] light planes of the current phase
+    int* rowinfo = nullptr;        // [B][8]
     i64* wte = nullptr;
     i64* wpe = nullptr;
     sm_tables T;
@@ -264,10 +313,11 @@ static void machine_free(sm_machine* m) {
     for (auto e : m->ev_s) (void)hipEventDestroy(e);
     for (auto e : m->ev_e) (void)hipEventDestroy(e);
     for (int l = 0; l < 12; l++)
-        for (int k = 0; k < 4; k++) free_plate(m->bank[l][k]);
+        for (int k = 0; k < 4; k++) { free_plate(m->bank[l][k]); free_mfma_plate(m->mbank[l][k]); }
     free_plate(m->head);
+    free_mfma_plate(m->mhead);
     tables_free(m->T);
-    void* ps[] = {m->wte, m->wpe, m->R, m->QKV, m->att, m->hid, m->K16, m->EK, m->V, m->seq, m->words, m->ctl,
+    void* ps[] = {m->planes, m->rowinfo, m->wte, m->wpe, m->R, m->QKV, m->att, m->hid, m->K16, m->EK, m->V, m->seq, m->words, m->ctl,
                   m->part_v, m->part_i, m->r_x16, m->r_exls, m->r_pile, m->r_qkv, m->r_att, m->r_hid, m->r_resid,
                   m->r_hx16, m->r_hexls, m->r_hpile, m->r_logits};
     for (void* p : ps) hfree(p);
@@ -277,7 +327,88 @@ static void machine_free(sm_machine* m) {
 
 // the launch sequence of one decode step (all streams, one position each): the layers and/or the head
 enum { STEP_ALL = 3, STEP_LAYERS = 1, STEP_HEAD = 2 };
+
+// batched streams: every bank is [light kernel (one block per stream) -> MFMA kernel (one block per 16 columns)]
+template <int RT>
+static int launch_step_batched(sm_machine* m, int parts, hipEvent_t hs, hipEvent_t he) {
+    const Tables tb = m->T.tb();
+    int* ctl = m->ctl;
+    const int B = m->B;
+    auto light = [&](int K, int pro, const i64* X, int skip, i64* rx16, i64* rexls) {
+        LightArgs a{};
+        a.K = K; a.rows = B; a.X = X; a.wte = m->wte; a.wpe = m->wpe; a.seq = m->seq; a.seq_stride = m->ctx + 1;
+        a.Rw = m->R; a.pos = ctl + CTL_POS; a.plen = ctl + CTL_PLEN; a.skip_prompt = skip;
+        a.planes = m->planes; a.rowinfo = m->rowinfo; a.tb = tb;
+        a.rec_pos = ctl + CTL_RECPOS; a.rx16 = rx16; a.rexls = rexls;
+        if (K == 3072) k_light<3072, PRO_TO16><<<B, 256, 0, m->st>>>(a);
+        else if (pro == PRO_EMBED) k_light<768, PRO_EMBED><<<B, 256, 0, m->st>>>(a);
+        else if (pro == PRO_GAUGE) k_light<768, PRO_GAUGE><<<B, 256, 0, m->st>>>(a);
+        else k_light<768, PRO_TO16><<<B, 256, 0, m->st>>>(a);
+    };
+    auto gemm_args = [&](const MfmaPlate& P, i64* Y, int ystride, i64* rpile, i64* rout) {
+        GemmArgs a{};
+        a.K = P.K; a.N = P.N; a.rows = B; a.RT = RT; a.W = P.W; a.csum = P.csum; a.we = P.e; a.bias = P.b;
+        a.planes = m->planes; a.rowinfo = m->rowinfo; a.Y = Y; a.ystride = ystride; a.tb = tb;
+        a.pos = ctl + CTL_POS; a.plen = ctl + CTL_PLEN; a.rec_pos = ctl + CTL_RECPOS; a.rpile = rpile; a.rout = rout;
+        return a;
+    };
+    for (int l = 0; l < 12 && (parts & STEP_LAYERS); l++) {
+        i64* rx = m->r_x16 + (size_t)l * 4 * 3072;
+        i64* re = m->r_exls + (size_t)l * 4 * 2;
+        i64* rp = m->r_pile + (size_t)l * 4 * 3072;
+        light(768, l == 0 ? PRO_EMBED : PRO_GAUGE, m->R, 0, rx, re);
+        {
+            GemmArgs a = gemm_args(m->mbank[l][0], m->QKV, 2304, rp, m->r_qkv + l * 2304);
+            k_gemm<768, RT, EPI_GAUGED><<<m->mbank[l][0].ntiles, 256, 0, m->st>>>(a);
+        }
+        {
+            AttArgs a{};
+            const size_t per = (size_t)m->B * m->ctx;
+            a.QKV = m->QKV; a.K16 = m->K16 + l * per * 768; a.EK = m->EK + l * per * 12; a.V = m->V + l * per * 768;
+            a.out = m->att; a.pos = ctl + CTL_POS; a.ctx = m->ctx; a.tb = tb; a.err = ctl + CTL_ERR;
+            a.rec_pos = ctl + CTL_RECPOS; a.ratt = m->r_att + l * 768;
+            k_attend<<<dim3(12, m->B), NTHR, (size_t)m->ctx * 8, m->st>>>(a);
+        }
+        light(768, PRO_TO16, m->att, 0, rx + 3072, re + 2);
+        {
+            GemmArgs a = gemm_args(m->mbank[l][1], m->R, 768, rp + 3072, m->r_resid + (l * 2 + 0) * 768);
+            k_gemm<768, RT, EPI_PLAIN_ADD><<<m->mbank[l][1].ntiles, 256, 0, m->st>>>(a);
+        }
+        light(768, PRO_GAUGE, m->R, 0, rx + 2 * 3072, re + 4);
+        {
+            GemmArgs a = gemm_args(m->mbank[l][2], m->hid, 3072, rp + 2 * 3072, m->r_hid + l * 3072);
+            k_gemm<768, RT, EPI_GAUGED_EDGE><<<m->mbank[l][2].ntiles, 256, 0, m->st>>>(a);
+        }
+        light(3072, PRO_TO16, m->hid, 0, rx + 3 * 3072, re + 6);
+        {
+            GemmArgs a = gemm_args(m->mbank[l][3], m->R, 768, rp + 3 * 3072, m->r_resid + (l * 2 + 1) * 768);
+            k_gemm<3072, RT, EPI_PLAIN_ADD><<<m->mbank[l][3].ntiles, 256, 0, m->st>>>(a);
+        }
+    }
+    if (parts & STEP_HEAD) {
+        light(768, PRO_GAUGE, m->R, 1, m->r_hx16, m->r_hexls);
+        GemmArgs a = gemm_args(m->mhead, nullptr, 0, m->r_hpile, nullptr);
+        a.part_v = m->part_v; a.part_i = m->part_i; a.nblk = m->mhead.ntiles; a.rlogits = m->r_logits;
+        if (hs) hipExtLaunchKernelGGL(k_gemm<768, RT, EPI_HEAD>, dim3(m->mhead.ntiles), dim3(256), 0, m->st, hs, he, 0, a);
+        else k_gemm<768, RT, EPI_HEAD><<<m->mhead.ntiles, 256, 0, m->st>>>(a);
+        RaceArgs r{};
+        r.part_v = m->part_v; r.part_i = m->part_i; r.nblk = m->mhead.ntiles; r.seq = m->seq; r.seq_stride = m->ctx + 1;
+        r.words = m->words; r.words_stride = m->ctx + 1; r.pos = ctl + CTL_POS; r.plen = ctl + CTL_PLEN;
+        r.nwords = ctl + CTL_NWORDS; r.counter = reinterpret_cast<unsigned*>(ctl + CTL_COUNTER);
+        k_race_rows<<<B, 256, 0, m->st>>>(r);
+    }
+    HIP_TRY(hipGetLastError());
+    return SM_OK;
+}
+
 static int launch_step(sm_machine* m, int parts = STEP_ALL, hipEvent_t hs = nullptr, hipEvent_t he = nullptr) {
+    if (m->B > 1) {
+        const int RT = (m->B + 15) / 16;
+        if (RT == 1) return launch_step_batched<1>(m, parts, hs, he);
+        if (RT == 2) return launch_step_batched<2>(m, parts, hs, he);
+        if (RT == 3) return launch_step_batched<3>(m, parts, hs, he);
+        return launch_step_batched<4>(m, parts, hs, he);
+    }
     const Tables tb = m->T.tb();
     int* ctl = m->ctl;
     for (int l = 0; l < 12 && (parts & STEP_LAYERS); l++) {
@@ -363,7 +494,7 @@ extern "C" int sm_create(const char* layout_dir, const sm_config* cfg, sm_machin
     *out = nullptr;
     sm_config c{1, 1024, 1, 0, 16, 0, 0};
     if (cfg) c = *cfg;
-    if (c.max_streams != 1) return fail(SM_E_ARG, "sm_create: this build decodes one stream per machine (max_streams = 1)");
+    if (c.max_streams < 1 || c.max_streams > 64) return fail(SM_E_ARG, "sm_create: max_streams must be in [1, 64]");
     if (c.max_ctx <= 0) return fail(SM_E_ARG, "sm_create: max_ctx must be positive");
     const std::string dir = std::string(layout_dir) + "/";
     std::vector<char> mj;
@@ -394,7 +525,8 @@ extern "C" int sm_create(const char* layout_dir, const sm_config* cfg, sm_machin
             if ((rc = read_array(dir + name + ".wc", w, (size_t)NIN[k] * NOUT[k])) || (rc = read_array(dir + name + ".e", e, NOUT[k])) ||
                 (rc = read_array(dir + name + ".b", b, NOUT[k])))
                 return bail(rc);
-            if ((rc = upload_plate(m->bank[l][k], w.data(), e.data(), b.data(), NIN[k], NOUT[k], TCOLS[k]))) return bail(rc);
+            if (m->B == 1 && (rc = upload_plate(m->bank[l][k], w.data(), e.data(), b.data(), NIN[k], NOUT[k], TCOLS[k]))) return bail(rc);
+            if (m->B > 1 && (rc = upload_mfma_plate(m->mbank[l][k], w.data(), e.data(), b.data(), NIN[k], NOUT[k]))) return bail(rc);
         }
     }
     const BankInfo* hb = find("head");
@@ -405,7 +537,8 @@ extern "C" int sm_create(const char* layout_dir, const sm_config* cfg, sm_machin
         if ((rc = read_array(dir + "head.wc", w, (size_t)768 * m->vocab)) || (rc = read_array(dir + "head.e", e, m->vocab)) ||
             (rc = read_array(dir + "head.b", b, m->vocab)))
             return bail(rc);
-        if ((rc = upload_plate(m->head, w.data(), e.data(), b.data(), 768, m->vocab, 8))) return bail(rc);
+        if (m->B == 1 && (rc = upload_plate(m->head, w.data(), e.data(), b.data(), 768, m->vocab, 8))) return bail(rc);
+        if (m->B > 1 && (rc = upload_mfma_plate(m->mhead, w.data(), e.data(), b.data(), 768, m->vocab))) return bail(rc);
     }
     // word and position tables
     {
@@ -429,19 +562,23 @@ extern "C" int sm_create(const char* layout_dir, const sm_config* cfg, sm_machin
     }
     m->ctx = c.max_ctx < m->npos ? c.max_ctx : m->npos;
     m->head_grid = c.head_grid > 0 ? c.head_grid : 512;
+    const size_t nparts = m->B == 1 ? (size_t)m->head_grid : (size_t)m->B * ((m->vocab + 15) / 16);
     // state
     const size_t B = m->B, ctx = m->ctx;
     if ((rc = dalloc(&m->R, B * 768)) || (rc = dalloc(&m->QKV, B * 2304)) || (rc = dalloc(&m->att, B * 768)) ||
         (rc = dalloc(&m->hid, B * 3072)) || (rc = dalloc(&m->K16, 12 * B * ctx * 768)) || (rc = dalloc(&m->EK, 12 * B * ctx * 12)) ||
         (rc = dalloc(&m->V, 12 * B * ctx * 768)) || (rc = dalloc(&m->seq, B * (ctx + 1))) || (rc = dalloc(&m->words, B * (ctx + 1))) ||
-        (rc = dalloc(&m->ctl, (size_t)CTL_N)) || (rc = dalloc(&m->part_v, (size_t)m->head_grid)) ||
-        (rc = dalloc(&m->part_i, (size_t)m->head_grid)) || (rc = dalloc(&m->r_x16, (size_t)12 * 4 * 3072)) ||
+        (rc = dalloc(&m->ctl, (size_t)CTL_N)) || (rc = dalloc(&m->part_v, nparts)) ||
+        (rc = dalloc(&m->part_i, nparts)) || (rc = dalloc(&m->r_x16, (size_t)12 * 4 * 3072)) ||
+        (rc = dalloc(&m->planes, (size_t)4 * 48 * 3 * 1024)) || (rc = dalloc(&m->rowinfo, (size_t)m->B * 8)) ||
         (rc = dalloc(&m->r_exls, (size_t)12 * 4 * 2)) || (rc = dalloc(&m->r_pile, (size_t)12 * 4 * 3072)) ||
         (rc = dalloc(&m->r_qkv, (size_t)12 * 2304)) || (rc = dalloc(&m->r_att, (size_t)12 * 768)) ||
         (rc = dalloc(&m->r_hid, (size_t)12 * 3072)) || (rc = dalloc(&m->r_resid, (size_t)12 * 2 * 768)) ||
         (rc = dalloc(&m->r_hx16, 768)) || (rc = dalloc(&m->r_hexls, 2)) || (rc = dalloc(&m->r_hpile, (size_t)m->vocab)) ||
         (rc = dalloc(&m->r_logits, (size_t)m->vocab)))
         return bail(rc);
+    if (hipMemset(m->planes, 0, (size_t)4 * 48 * 3 * 1024) != hipSuccess || hipMemset(m->rowinfo, 0, (size_t)m->B * 32) != hipSuccess)
+        return bail(fail(SM_E_HIP, "hipMemset planes"));
     m->prompts.assign(B, {});
     m->gsteps = c.graph_steps > 0 ? c.graph_steps : 16;
     if (m->gsteps > 256) return bail(fail(SM_E_ARG, "sm_create: graph_steps at most 256"));
@@ -727,26 +864,94 @@ extern "C" int sm_stage_attend(const sm_tables* t, const int64_t* qkv, int32_t* 
     return SM_OK;
 }
 
-struct sm_plate { DevPlate P; };
+// tile_cols > 0: a GEMV plate (one light row per product); tile_cols == 0: an MFMA plate (rows of lights) with
+// its own light planes and row sums
+struct sm_plate {
+    DevPlate P;
+    MfmaPlate M;
+    bool mfma = false;
+    signed char* planes = nullptr;
+    int* rowinfo = nullptr;
+};
+
+static void plate_free(sm_plate* p) {
+    free_plate(p->P);
+    free_mfma_plate(p->M);
+    hfree(p->planes); hfree(p->rowinfo);
+    delete p;
+}
 
 extern "C" int sm_plate_create(const int16_t* w, const int32_t* e, const int64_t* b, int32_t nin, int32_t nout, int32_t tile_cols, sm_plate** out) {
     if (!w || !e || !b || !out) return fail(SM_E_ARG, "sm_plate_create: null argument");
-    if (!((nin == 768 && (tile_cols == 2 || tile_cols == 8)) || (nin == 3072 && (tile_cols == 1 || tile_cols == 2))))
-        return fail(SM_E_ARG, "sm_plate_create: built for (nin, tile_cols) in (768, 2), (768, 8), (3072, 1), (3072, 2)");
+    if (nout <= 0 || nout > (1 << 24)) return fail(SM_E_ARG, "sm_plate_create: nout out of range");
+    if (!((nin == 768 && (tile_cols == 0 || tile_cols == 2 || tile_cols == 8)) ||
+          (nin == 3072 && (tile_cols == 0 || tile_cols == 1 || tile_cols == 2))))
+        return fail(SM_E_ARG, "sm_plate_create: built for (nin, tile_cols) in (768, 0|2|8), (3072, 0|1|2)");
     sm_plate* p = new sm_plate();
-    int rc = upload_plate(p->P, w, e, (const i64*)b, nin, nout, tile_cols);
-    if (rc) { free_plate(p->P); delete p; return rc; }
+    int rc;
+    if (tile_cols == 0) {
+        p->mfma = true;
+        const size_t pb = (size_t)4 * (nin / 64) * 3 * 1024;
+        if ((rc = upload_mfma_plate(p->M, w, e, (const i64*)b, nin, nout)) || (rc = dalloc(&p->planes, pb)) ||
+            (rc = dalloc(&p->rowinfo, (size_t)64 * 8))) {
+            plate_free(p);
+            return rc;
+        }
+        if (hipMemset(p->planes, 0, pb) != hipSuccess) { plate_free(p); return fail(SM_E_HIP, "hipMemset planes"); }
+    } else if ((rc = upload_plate(p->P, w, e, (const i64*)b, nin, nout, tile_cols))) {
+        plate_free(p);
+        return rc;
+    }
     *out = p;
     return SM_OK;
 }
 extern "C" int sm_plate_destroy(sm_plate* p) {
-    if (p) { free_plate(p->P); delete p; }
+    if (p) {
+        (void)hipDeviceSynchronize();
+        plate_free(p);
+    }
     return SM_OK;
 }
-extern "C" int64_t sm_plate_bytes(const sm_plate* p) { return p ? (int64_t)p->P.ntiles * p->P.tc * p->P.nin * 2 : 0; }
+extern "C" int64_t sm_plate_bytes(const sm_plate* p) {
+    if (!p) return 0;
+    if (p->mfma) return (int64_t)p->M.ntiles * 16 * p->M.K * 2;
+    return (int64_t)p->P.ntiles * p->P.tc * p->P.nin * 2;
+}
+
+template <int RT>
+static void rows_product(const sm_plate* p, const int64_t* x16, int32_t rows, int64_t* pile, hipStream_t s) {
+    const MfmaPlate& P = p->M;
+    LightArgs la{};
+    la.K = P.K; la.rows = rows; la.X = (const i64*)x16; la.planes = p->planes; la.rowinfo = p->rowinfo;
+    GemmArgs ga{};
+    ga.K = P.K; ga.N = P.N; ga.rows = rows; ga.RT = RT; ga.W = P.W; ga.csum = P.csum; ga.we = P.e; ga.bias = P.b;
+    ga.planes = p->planes; ga.rowinfo = p->rowinfo; ga.Y = (i64*)pile; ga.ystride = P.N;
+    if (P.K == 768) {
+        k_light<768, PRO_X16><<<rows, 256, 0, s>>>(la);
+        k_gemm<768, RT, EPI_PILE><<<P.ntiles, 256, 0, s>>>(ga);
+    } else {
+        k_light<3072, PRO_X16><<<rows, 256, 0, s>>>(la);
+        k_gemm<3072, RT, EPI_PILE><<<P.ntiles, 256, 0, s>>>(ga);
+    }
+}
+
+extern "C" int sm_plate_product_rows(const sm_plate* p, const int64_t* x16, int32_t rows, int64_t* pile, void* stream) {
+    if (!p || !x16 || !pile) return fail(SM_E_ARG, "sm_plate_product_rows: null argument");
+    if (!p->mfma) return fail(SM_E_ARG, "sm_plate_product_rows: the plate was made for the GEMV (tile_cols > 0)");
+    if (rows < 1 || rows > 64) return fail(SM_E_ARG, "sm_plate_product_rows: rows must be in [1, 64]");
+    hipStream_t s = (hipStream_t)stream;
+    const int RT = (rows + 15) / 16;
+    if (RT == 1) rows_product<1>(p, x16, rows, pile, s);
+    else if (RT == 2) rows_product<2>(p, x16, rows, pile, s);
+    else if (RT == 3) rows_product<3>(p, x16, rows, pile, s);
+    else rows_product<4>(p, x16, rows, pile, s);
+    HIP_TRY(hipGetLastError());
+    return SM_OK;
+}
 
 extern "C" int sm_plate_product(const sm_plate* p, const int64_t* x16, int64_t* pile, int32_t grid, void* stream) {
     if (!p || !x16 || !pile) return fail(SM_E_ARG, "sm_plate_product: null argument");
+    if (p->mfma) return fail(SM_E_ARG, "sm_plate_product: the plate was made for rows (tile_cols == 0)");
     const DevPlate& P = p->P;
     GemvArgs a{};
     a.W = reinterpret_cast<const int4*>(P.W); a.we = P.e; a.bias = P.b; a.nout = P.nout; a.ntiles = P.ntiles;

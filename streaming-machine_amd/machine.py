@@ -71,6 +71,7 @@ def lib():
         L.sm_plate_create.argtypes = [ctypes.POINTER(ctypes.c_int16), i32p, i64p, i32, i32, i32, ctypes.POINTER(vp)]
         L.sm_plate_destroy.argtypes = [vp]
         L.sm_plate_product.argtypes = [vp, vp, vp, i32, vp]
+        L.sm_plate_product_rows.argtypes = [vp, vp, i32, vp, vp]
         L.sm_plate_bytes.restype = i64
         L.sm_plate_bytes.argtypes = [vp]
         _LIB = L
@@ -134,6 +135,13 @@ class Machine:
         check(self.L.sm_generate(self.h, n_words, out.ctypes.data_as(i32p)))
         return out
 
+    def streams(self, prompts, n_words: int) -> list:
+        """every stream at once: prompts[b] (all of one length) then n_words words each"""
+        self.reset()
+        for b, p in enumerate(prompts):
+            self.prefill(p, b)
+        return [[int(w) for w in row] for row in self.generate(n_words)]
+
     def stream(self, prompt, n_words: int, stream: int = 0) -> list:
         self.reset()
         self.prefill(prompt, stream)
@@ -193,7 +201,8 @@ class Tables:
 
 
 class Plate:
-    """A plate on the device laid out for the GEMV (input-major int16 [nin][nout] on the host)."""
+    """A plate on the device (input-major int16 [nin][nout] on the host): tile_cols > 0 lays it out for the
+    one-row GEMV (.product), tile_cols == 0 as int8 MFMA byte planes for rows of lights (.product_rows)."""
 
     def __init__(self, w, e, b, tile_cols: int = 8):
         self.L = lib()
@@ -209,6 +218,9 @@ class Plate:
 
     def product(self, x16_ptr: int, pile_ptr: int, grid: int = 0, stream: int = 0):
         check(self.L.sm_plate_product(self.h, x16_ptr, pile_ptr, grid, stream))
+
+    def product_rows(self, x16_ptr: int, rows: int, pile_ptr: int, stream: int = 0):
+        check(self.L.sm_plate_product_rows(self.h, x16_ptr, rows, pile_ptr, stream))
 
     def close(self):
         if getattr(self, "h", None):
