@@ -44,32 +44,42 @@ struct GemmArgs {
 
 // ---------------------------------------------------------------------------------------------------------
 // One block (256 threads) per stream row: the light of base2.py:24-27 (and the gauge of :55-60), written as
-// MFMA A planes plus the row's exponent, gauge, power factor and plane sums.
+// MFMA A planes plus the row's exponent, gauge, power factor and plane sums.  Each thread owns groups of four
+// consecutive k, so every plane byte group goes out as one 32-bit store.
 template <int K, int PRO>
 __global__ __launch_bounds__(256) void k_light(LightArgs a) {
-    constexpr int PER = K / 256, KS = K / 64;
+    constexpr int NG = K / 4, GPT = (NG + 255) / 256, KS = K / 64;
     __shared__ int red[32];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, r = blockIdx.x;
     const int p = a.pos ? *a.pos : 0;              // the stage product (PRO_X16) has no position
     if (a.skip_prompt && p < *a.plen - 1) return;
-    i64 v[PER];
-    if (PRO == PRO_EMBED) {
-        const i64 tok = a.seq[(size_t)r * a.seq_stride + p];
+    i64 v[GPT][4];
 #pragma unroll
-        for (int m = 0; m < PER; m++) {
-            const int i = tid + 256 * m;
-            v[m] = wadd(a.wte[tok * 768 + i], a.wpe[(i64)p * 768 + i]);
-            a.Rw[(size_t)r * 768 + i] = v[m];
+    for (int m = 0; m < GPT; m++) {
+        const int g = tid + 256 * m;
+#pragma unroll
+        for (int j = 0; j < 4; j++) v[m][j] = 0;
+        if (g >= NG) continue;
+        const int k = 4 * g;
+        if (PRO == PRO_EMBED) {
+            const i64 tok = a.seq[(size_t)r * a.seq_stride + p];
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                v[m][j] = wadd(a.wte[tok * 768 + k + j], a.wpe[(i64)p * 768 + k + j]);
+                a.Rw[(size_t)r * 768 + k + j] = v[m][j];
+            }
+        } else {
+#pragma unroll
+            for (int j = 0; j < 4; j++) v[m][j] = a.X[(size_t)r * K + k + j];
         }
-    } else {
-#pragma unroll
-        for (int m = 0; m < PER; m++) v[m] = a.X[(size_t)r * K + tid + 256 * m];
     }
     int sh = 0;                                     // PRO_X16: the lights are given
     if (PRO != PRO_X16) {
         u64 o = 0;
 #pragma unroll
-        for (int m = 0; m < PER; m++) o |= (u64)iabs64(v[m]);
+        for (int m = 0; m < GPT; m++)
+#pragma unroll
+            for (int j = 0; j < 4; j++) o |= (u64)iabs64(v[m][j]);
         const unsigned olo = wave_or32((unsigned)o), ohi = wave_or32((unsigned)(o >> 32));
         if (lane == 0) { red[2 * wave] = (int)olo; red[2 * wave + 1] = (int)ohi; }
         __syncthreads();
@@ -82,23 +92,32 @@ __global__ __launch_bounds__(256) void k_light(LightArgs a) {
     const bool rec = r == 0 && a.rec_pos && *a.rec_pos == p;
     int s1 = 0, sxh = 0, sxl = 0, n32 = 0;
     i64 s2 = 0;
-    signed char* pl = a.planes + (size_t)(r >> 4) * KS * 3 * 1024;
+    int* pl = reinterpret_cast<int*>(a.planes + (size_t)(r >> 4) * KS * 3 * 1024);
 #pragma unroll
-    for (int m = 0; m < PER; m++) {
-        const int k = tid + 256 * m;
-        const int x = (int)rsh(v[m], sh);
-        s1 += x;
-        s2 += (i64)x * x;
-        if (rec && a.rx16) a.rx16[k] = x;
-        const int c = x == 32768;
-        const int xc = x - c;                      // +32768 -> 32767, the rest unchanged
-        const int xh = xc >> 8, xl = (xc & 255) - 128;
-        sxh += xh; sxl += xl; n32 += c;
+    for (int m = 0; m < GPT; m++) {
+        const int g = tid + 256 * m;
+        if (g >= NG) continue;
+        const int k = 4 * g;
+        unsigned ph = 0, pl8 = 0, pc = 0;
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const int x = (int)rsh(v[m][j], sh);
+            s1 += x;
+            s2 += (i64)x * x;
+            if (rec && a.rx16) a.rx16[k + j] = x;
+            const int c = x == 32768;
+            const int xc = x - c;                  // +32768 -> 32767, the rest unchanged
+            const int xh = xc >> 8, xl = (xc & 255) - 128;
+            sxh += xh; sxl += xl; n32 += c;
+            ph |= (unsigned)(xh & 255) << (8 * j);
+            pl8 |= (unsigned)(xl & 255) << (8 * j);
+            pc |= (unsigned)c << (8 * j);
+        }
         const int s = k >> 6, kk = k & 63;
-        const size_t off = (size_t)s * 3 * 1024 + (size_t)((r & 15) + 16 * (kk >> 4)) * 16 + (kk & 15);
-        pl[off] = (signed char)xh;
-        pl[off + 1024] = (signed char)xl;
-        pl[off + 2048] = (signed char)c;
+        const size_t off = ((size_t)s * 3 * 1024 + (size_t)((r & 15) + 16 * (kk >> 4)) * 16 + (kk & 15)) / 4;
+        pl[off] = (int)ph;
+        pl[off + 256] = (int)pl8;
+        pl[off + 512] = (int)pc;
     }
     const int w1 = wave_add32(s1), w2h = wave_add32((int)(s2 >> 16)), w2l = wave_add32((int)(s2 & 0xFFFF));
     const int w3 = wave_add32(sxh), w4 = wave_add32(sxl), w5 = wave_add32(n32);
@@ -120,104 +139,297 @@ __global__ __launch_bounds__(256) void k_light(LightArgs a) {
 }
 
 // ---------------------------------------------------------------------------------------------------------
-// One block (4 waves) per 16-column tile; wave w takes the 64-k steps s = w, w + 4, .. (split K), every wave all
-// RT row tiles; the four partial results meet in LDS and each (row, column) pile gets its epilogue.
-template <int K, int RT, int EPI>
+// The byte-plane contraction.  A wave computes CT column tiles (16 columns each) for all RT row tiles with three
+// int32 accumulators per tile pair: HH, MID = HL + LH (+ CH), LL (+ CL).
+//   SK == 4: the block's four waves split the 64-k steps of one column group and meet in LDS; wave w then
+//            finishes rows 4 (l / 16) + w of every row tile (the layer banks: few columns, more blocks).
+//   SK == 1: each wave owns its own column group over all of K and finishes all its rows (the head).
+// The epilogue runs on the accumulator registers: lane l holds column l % 16 of each tile.
+template <int K, int RT, int CT, int SK, int EPI>
 __global__ __launch_bounds__(256) void k_gemm(GemmArgs a) {
-    constexpr int KS = K / 64;
-    __shared__ i64 acc_s[4][RT * 16][16 + 1];          // per wave partial piles [row][col] (padded)
+    constexpr int KS = K / 64, NS = KS / SK, NQ = SK == 1 ? 4 : 1;
+    static_assert(SK == 1 || SK == 4, "split over 1 or 4 waves");
+    static_assert(KS % SK == 0, "k steps split evenly");
+    __shared__ int rinfo[64 * 8];
+    __shared__ int red[SK > 1 ? SK * CT * RT * 12 * 64 : 1];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int nt = blockIdx.x;                          // column tile
     const int p = a.pos ? *a.pos : 0;                   // the stage product (EPI_PILE) has no position
     if (EPI == EPI_HEAD && p < *a.plen - 1) return;    // a prompt position: the race kernel only advances
-    // which row tiles need the +32768 correction (uniform)
-    unsigned corr = 0;
-    for (int rt = 0; rt < RT; rt++) {
-        int n = 0;
-        for (int i = 0; i < 16; i++) if (rt * 16 + i < a.rows) n += a.rowinfo[(size_t)(rt * 16 + i) * 8 + 6];
-        if (n) corr |= 1u << rt;
-    }
-    v4i_b hh[RT], hl[RT], lh[RT], ll[RT], ch[RT], cl[RT];
+    const int ntiles = (a.N + 15) >> 4;
+    const int g = SK == 1 ? blockIdx.x * 4 + wave : blockIdx.x;   // this wave's column group
+    const int tile0 = g * CT;
+    // row tiles with a +32768 light need the correction plane (one load per lane, one ballot)
+    const int n32 = lane < a.rows ? a.rowinfo[lane * 8 + 6] : 0;
+    const int rsv = tid < a.rows * 8 ? a.rowinfo[tid] : 0;
+    const int rsv2 = tid + 256 < a.rows * 8 ? a.rowinfo[tid + 256] : 0;
+    const u64 cmask = __ballot(n32 != 0);
+
+    typedef int v4 __attribute__((ext_vector_type(4)));
+    v4 acc[CT][RT][3];
 #pragma unroll
-    for (int t = 0; t < RT; t++) hh[t] = hl[t] = lh[t] = ll[t] = ch[t] = cl[t] = v4i_b{0, 0, 0, 0};
-    const v4i_b* Wp = reinterpret_cast<const v4i_b*>(a.W) + (size_t)nt * KS * 2 * 64 + lane;
-    const v4i_b* Ap = reinterpret_cast<const v4i_b*>(a.planes) + lane;
-    for (int s = wave; s < KS; s += 4) {
-        const v4i_b wh = __builtin_nontemporal_load(Wp + (size_t)s * 128);
-        const v4i_b wl = __builtin_nontemporal_load(Wp + (size_t)s * 128 + 64);
+    for (int c = 0; c < CT; c++)
 #pragma unroll
-        for (int t = 0; t < RT; t++) {
-            const v4i_b* ap = Ap + ((size_t)t * KS + s) * 3 * 64;
-            const v4i_b xh = ap[0], xl = ap[64];
-            hh[t] = __builtin_amdgcn_mfma_i32_16x16x64_i8(xh, wh, hh[t], 0, 0, 0);
-            hl[t] = __builtin_amdgcn_mfma_i32_16x16x64_i8(xh, wl, hl[t], 0, 0, 0);
-            lh[t] = __builtin_amdgcn_mfma_i32_16x16x64_i8(xl, wh, lh[t], 0, 0, 0);
-            ll[t] = __builtin_amdgcn_mfma_i32_16x16x64_i8(xl, wl, ll[t], 0, 0, 0);
-            if (corr & (1u << t)) {
-                const v4i_b c = ap[128];
-                ch[t] = __builtin_amdgcn_mfma_i32_16x16x64_i8(c, wh, ch[t], 0, 0, 0);
-                cl[t] = __builtin_amdgcn_mfma_i32_16x16x64_i8(c, wl, cl[t], 0, 0, 0);
+        for (int t = 0; t < RT; t++) acc[c][t][0] = acc[c][t][1] = acc[c][t][2] = v4{0, 0, 0, 0};
+    const v4* Wb = reinterpret_cast<const v4*>(a.W) + lane;
+    const v4* Ab = reinterpret_cast<const v4*>(a.planes) + lane;
+    int tl[CT];
+#pragma unroll
+    for (int c = 0; c < CT; c++) tl[c] = min(tile0 + c, ntiles - 1);   // loads stay inside the plate
+    if (tile0 < ntiles) {
+#pragma unroll
+        for (int i = 0; i < NS; i++) {
+            const int s = SK == 1 ? i : wave * NS + i;
+            v4 wh[CT], wl[CT], xh[RT], xl[RT];
+#pragma unroll
+            for (int c = 0; c < CT; c++) {
+                const v4* w = Wb + ((size_t)tl[c] * KS + s) * 128;
+                wh[c] = __builtin_nontemporal_load(w);
+                wl[c] = __builtin_nontemporal_load(w + 64);
             }
+#pragma unroll
+            for (int t = 0; t < RT; t++) {
+                const v4* x = Ab + ((size_t)t * KS + s) * 192;
+                xh[t] = x[0];
+                xl[t] = x[64];
+            }
+#pragma unroll
+            for (int t = 0; t < RT; t++)
+#pragma unroll
+                for (int c = 0; c < CT; c++) {
+                    acc[c][t][0] = __builtin_amdgcn_mfma_i32_16x16x64_i8(xh[t], wh[c], acc[c][t][0], 0, 0, 0);
+                    acc[c][t][1] = __builtin_amdgcn_mfma_i32_16x16x64_i8(xh[t], wl[c], acc[c][t][1], 0, 0, 0);
+                    acc[c][t][2] = __builtin_amdgcn_mfma_i32_16x16x64_i8(xl[t], wl[c], acc[c][t][2], 0, 0, 0);
+                    acc[c][t][1] = __builtin_amdgcn_mfma_i32_16x16x64_i8(xl[t], wh[c], acc[c][t][1], 0, 0, 0);
+                }
+#pragma unroll
+            for (int t = 0; t < RT; t++)
+                if ((cmask >> (16 * t)) & 0xFFFFull) {
+                    const v4 cc = Ab[((size_t)t * KS + s) * 192 + 128];
+#pragma unroll
+                    for (int c = 0; c < CT; c++) {
+                        acc[c][t][1] = __builtin_amdgcn_mfma_i32_16x16x64_i8(cc, wh[c], acc[c][t][1], 0, 0, 0);
+                        acc[c][t][2] = __builtin_amdgcn_mfma_i32_16x16x64_i8(cc, wl[c], acc[c][t][2], 0, 0, 0);
+                    }
+                }
         }
     }
-    // this wave's partial piles (the plane-sum terms are added once, below)
+    if (tid < a.rows * 8) rinfo[tid] = rsv;
+    if (tid + 256 < a.rows * 8) rinfo[tid + 256] = rsv2;
+    // fin[c][t][a][qi]: the full accumulators of row 16 t + 4 (l / 16) + q, q = qi (SK == 1) or wave (SK == 4)
+    int fin[CT][RT][3][NQ];
+    if (SK > 1) {
+#pragma unroll
+        for (int c = 0; c < CT; c++)
+#pragma unroll
+            for (int t = 0; t < RT; t++)
+#pragma unroll
+                for (int k3 = 0; k3 < 3; k3++)
+#pragma unroll
+                    for (int q = 0; q < 4; q++)
+                        red[((size_t)wave * CT * RT * 12 + ((c * RT + t) * 3 + k3) * 4 + q) * 64 + lane] = acc[c][t][k3][q];
+        __syncthreads();
+#pragma unroll
+        for (int c = 0; c < CT; c++)
+#pragma unroll
+            for (int t = 0; t < RT; t++)
+#pragma unroll
+                for (int k3 = 0; k3 < 3; k3++) {
+                    int sum = 0;
+#pragma unroll
+                    for (int w = 0; w < SK; w++) sum += red[((size_t)w * CT * RT * 12 + ((c * RT + t) * 3 + k3) * 4 + wave) * 64 + lane];
+                    fin[c][t][k3][0] = sum;
+                }
+    } else {
+        __syncthreads();
+#pragma unroll
+        for (int c = 0; c < CT; c++)
+#pragma unroll
+            for (int t = 0; t < RT; t++)
+#pragma unroll
+                for (int k3 = 0; k3 < 3; k3++)
+#pragma unroll
+                    for (int q = 0; q < NQ; q++) fin[c][t][k3][q] = acc[c][t][k3][q];
+    }
+    if (tile0 >= ntiles) return;
+    const bool rec0 = a.rec_pos && *a.rec_pos == p;
+    i64 bv[RT][NQ];
+    int bi[RT][NQ];
 #pragma unroll
     for (int t = 0; t < RT; t++)
 #pragma unroll
-        for (int q = 0; q < 4; q++) {
-            const int row = t * 16 + 4 * (lane >> 4) + q, col = lane & 15;
-            acc_s[wave][row][col] = 65536 * (i64)hh[t][q] + 256 * ((i64)hl[t][q] + lh[t][q]) + ll[t][q] +
-                                    256 * (i64)ch[t][q] + cl[t][q];
-        }
-    __syncthreads();
-    const bool rec0 = a.rec_pos && *a.rec_pos == p;
-    for (int e = tid; e < RT * 256; e += 256) {
-        const int row = e >> 4, col = e & 15, j = nt * 16 + col;
-        if (row >= a.rows || j >= a.N) continue;
-        const int* ri = a.rowinfo + (size_t)row * 8;
-        const i64 ex = ri[0];
-        const i64 ls = (i64)(((u64)(unsigned)ri[2] << 32) | (unsigned)ri[1]);
-        const i64 e2 = ri[3];
-        const i64 pile = acc_s[0][row][col] + acc_s[1][row][col] + acc_s[2][row][col] + acc_s[3][row][col] +
-                         32768 * ((i64)ri[4] + a.csum[2 * j]) + 128 * ((i64)ri[5] + a.csum[2 * j + 1]) +
-                         16384 * (i64)K + 128 * (i64)ri[6];
-        const bool rec = rec0 && row == 0;
-        if (rec && a.rpile) a.rpile[j] = pile;
+        for (int q = 0; q < NQ; q++) { bv[t][q] = 0; bi[t][q] = -1; }
+#pragma unroll
+    for (int c = 0; c < CT; c++) {
+        const int j = (tile0 + c) * 16 + (lane & 15);
+        if (tile0 + c >= ntiles || j >= a.N) continue;
+        const i64 swh = a.csum[2 * j], swl = a.csum[2 * j + 1];
         const i64 we = a.we[j], bc = a.bias[j];
-        if (EPI == EPI_PILE) {
-            a.Y[(size_t)row * a.ystride + j] = pile;
-        } else if (EPI == EPI_PLAIN_ADD) {
-            i64* y = a.Y + (size_t)row * a.ystride + j;
-            const i64 r = wadd(*y, wadd(rsh(pile, -(we + ex + 16)), bc));
-            *y = r;
-            if (rec && a.rout) a.rout[j] = r;
-        } else {
-            const i64 fe = wsub(0, ls) & 0xFFFF;
-            i64 y = wadd(power_e(pile, wsub(wmul(we + ex + 16, 65536), ls), fe, e2, a.tb), bc);
-            if (EPI == EPI_GAUGED_EDGE) y = edge1(y, a.tb);
-            if (EPI == EPI_HEAD) {
-                if (rec && a.rlogits) a.rlogits[j] = y;
-                acc_s[0][row][col] = y;               // only this thread reads or writes this cell
-            } else {
-                a.Y[(size_t)row * a.ystride + j] = y;
-                if (rec && a.rout) a.rout[j] = y;
+#pragma unroll
+        for (int t = 0; t < RT; t++)
+#pragma unroll
+            for (int qi = 0; qi < NQ; qi++) {
+                const int row = 16 * t + 4 * (lane >> 4) + (SK == 1 ? qi : wave);
+                if (row >= a.rows) continue;
+                const int* ri = rinfo + row * 8;
+                const i64 ex = ri[0];
+                const i64 pile = 65536 * (i64)fin[c][t][0][qi] + 256 * (i64)fin[c][t][1][qi] + fin[c][t][2][qi] +
+                                 32768 * ((i64)ri[4] + swh) + 128 * ((i64)ri[5] + swl) + 16384 * (i64)K + 128 * (i64)ri[6];
+                const bool rec = rec0 && row == 0;
+                if (rec && a.rpile) a.rpile[j] = pile;
+                if (EPI == EPI_PILE) {
+                    a.Y[(size_t)row * a.ystride + j] = pile;
+                } else if (EPI == EPI_PLAIN_ADD) {
+                    i64* y = a.Y + (size_t)row * a.ystride + j;
+                    const i64 r = wadd(*y, wadd(rsh(pile, -(we + ex + 16)), bc));
+                    *y = r;
+                    if (rec && a.rout) a.rout[j] = r;
+                } else {
+                    const i64 ls = (i64)(((u64)(unsigned)ri[2] << 32) | (unsigned)ri[1]);
+                    i64 y = wadd(power_known(pile, wsub(wmul(we + ex + 16, 65536), ls), (i64)ri[3]), bc);
+                    if (EPI == EPI_GAUGED_EDGE) y = edge1(y, a.tb);
+                    if (EPI == EPI_HEAD) {
+                        if (rec && a.rlogits) a.rlogits[j] = y;
+                        if (bi[t][qi] < 0 || y > bv[t][qi]) { bv[t][qi] = y; bi[t][qi] = j; }   // j grows with c
+                    } else {
+                        a.Y[(size_t)row * a.ystride + j] = y;
+                        if (rec && a.rout) a.rout[j] = y;
+                    }
+                }
             }
-        }
     }
     if (EPI != EPI_HEAD) return;
-    __syncthreads();
-    // per row: the largest logit of this tile, ties to the lowest column
-    for (int row = tid; row < RT * 16; row += 256) {
-        if (row >= a.rows) continue;
-        i64 b = 0; int ib = -1;
-        for (int col = 0; col < 16; col++) {
-            const int j = nt * 16 + col;
-            if (j >= a.N) break;
-            const i64 y = acc_s[0][row][col];
-            if (ib < 0 || y > b) { b = y; ib = j; }
+    // per row: the best of the 16 lanes that hold its columns (ties to the lowest column), then one store
+#pragma unroll
+    for (int t = 0; t < RT; t++)
+#pragma unroll
+        for (int qi = 0; qi < NQ; qi++) {
+            i64 v = bv[t][qi];
+            int i = bi[t][qi];
+#pragma unroll
+            for (int o = 1; o < 16; o <<= 1) {
+                const i64 ov = __shfl_xor(v, o, 64);
+                const int oi = __shfl_xor(i, o, 64);
+                if (oi >= 0 && (i < 0 || ov > v || (ov == v && oi < i))) { v = ov; i = oi; }
+            }
+            const int row = 16 * t + 4 * (lane >> 4) + (SK == 1 ? qi : wave);
+            if ((lane & 15) == 0 && row < a.rows) {
+                a.part_v[(size_t)row * a.nblk + g] = v;
+                a.part_i[(size_t)row * a.nblk + g] = i;
+            }
         }
-        a.part_v[(size_t)row * a.nblk + nt] = b;
-        a.part_i[(size_t)row * a.nblk + nt] = ib;
+}
+
+// ---------------------------------------------------------------------------------------------------------
+// The head (768 x vocab).  Wave w keeps row tile w's light planes in registers for the whole launch (12 steps x
+// xh, xl: 96 VGPRs); the block streams its 16-column weight tiles (24 KB each; tile = block + k * grid) through
+// two LDS buffers, two tiles ahead in registers, one barrier per tile.  A fetch past the end re-reads the last
+// tile, which every block shares, so it stays in cache.  Each lane keeps, per row, the best of the columns it
+// held (ties to the lowest); one 16-lane reduction per row at the end gives the block's part.
+template <int RT, int EPI>
+__global__ __launch_bounds__(256) void k_head_rows(GemmArgs a) {
+    constexpr int K = 768, KS = K / 64, TV = KS * 128, PER = TV / 256;   // v4 per tile, per thread
+    typedef int v4 __attribute__((ext_vector_type(4)));
+    __shared__ v4 ws[2][TV];
+    __shared__ int rinfo[64 * 8];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int p = a.pos ? *a.pos : 0;
+    if (EPI == EPI_HEAD && p < *a.plen - 1) return;
+    const int ntiles = (a.N + 15) >> 4, G = gridDim.x;
+    const v4* Wg = reinterpret_cast<const v4*>(a.W) + tid;
+    auto gfetch = [&](v4 (&r)[PER], int tile) {
+        const v4* src = Wg + (size_t)min(tile, ntiles - 1) * TV;
+#pragma unroll
+        for (int i = 0; i < PER; i++) r[i] = __builtin_nontemporal_load(src + i * 256);
+    };
+    v4 r0[PER], r1[PER];
+    gfetch(r0, blockIdx.x);
+    gfetch(r1, blockIdx.x + G);
+    // this wave's row tile (waves past the last row tile only help to stage)
+    const bool live = wave < RT;
+    const int t = live ? wave : 0;
+    const int n32 = lane < a.rows ? a.rowinfo[lane * 8 + 6] : 0;
+    const bool corr = live && ((__ballot(n32 != 0) >> (16 * t)) & 0xFFFFull);
+    const v4* Ab = reinterpret_cast<const v4*>(a.planes) + (size_t)t * KS * 192 + lane;
+    v4 xh[KS], xl[KS];
+#pragma unroll
+    for (int s = 0; s < KS; s++) { xh[s] = Ab[s * 192]; xl[s] = Ab[s * 192 + 64]; }
+    if (tid < a.rows * 8) rinfo[tid] = a.rowinfo[tid];
+    if (tid + 256 < a.rows * 8) rinfo[tid + 256] = a.rowinfo[tid + 256];
+    const bool rec0 = a.rec_pos && *a.rec_pos == p;
+    i64 bv[4];
+    int bi[4];
+#pragma unroll
+    for (int q = 0; q < 4; q++) { bv[q] = 0; bi[q] = -1; }
+    auto compute = [&](const v4* w, int tile) {
+        if (!live) return;
+        v4 hh = {0, 0, 0, 0}, mid = {0, 0, 0, 0}, ll = {0, 0, 0, 0};
+#pragma unroll
+        for (int s = 0; s < KS; s++) {
+            const v4 wh = w[s * 128 + lane], wl = w[s * 128 + 64 + lane];
+            hh = __builtin_amdgcn_mfma_i32_16x16x64_i8(xh[s], wh, hh, 0, 0, 0);
+            mid = __builtin_amdgcn_mfma_i32_16x16x64_i8(xh[s], wl, mid, 0, 0, 0);
+            ll = __builtin_amdgcn_mfma_i32_16x16x64_i8(xl[s], wl, ll, 0, 0, 0);
+            mid = __builtin_amdgcn_mfma_i32_16x16x64_i8(xl[s], wh, mid, 0, 0, 0);
+            if (corr) {
+                const v4 cc = Ab[s * 192 + 128];
+                mid = __builtin_amdgcn_mfma_i32_16x16x64_i8(cc, wh, mid, 0, 0, 0);
+                ll = __builtin_amdgcn_mfma_i32_16x16x64_i8(cc, wl, ll, 0, 0, 0);
+            }
+        }
+        const int j = tile * 16 + (lane & 15);
+        if (j >= a.N) return;
+        const i64 swh = a.csum[2 * j], swl = a.csum[2 * j + 1];
+        const i64 we = a.we[j], bc = a.bias[j];
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+            const int row = 16 * t + 4 * (lane >> 4) + q;
+            if (row >= a.rows) continue;
+            const int* ri = rinfo + row * 8;
+            const i64 pile = 65536 * (i64)hh[q] + 256 * (i64)mid[q] + ll[q] + 32768 * ((i64)ri[4] + swh) +
+                             128 * ((i64)ri[5] + swl) + 16384 * (i64)K + 128 * (i64)ri[6];
+            const bool rec = rec0 && row == 0;
+            if (rec && a.rpile) a.rpile[j] = pile;
+            if (EPI == EPI_PILE) {
+                a.Y[(size_t)row * a.ystride + j] = pile;
+            } else {
+                const i64 ls = (i64)(((u64)(unsigned)ri[2] << 32) | (unsigned)ri[1]);
+                const i64 y = wadd(power_known(pile, wsub(wmul(we + (i64)ri[0] + 16, 65536), ls), (i64)ri[3]), bc);
+                if (rec && a.rlogits) a.rlogits[j] = y;
+                if (bi[q] < 0 || y > bv[q]) { bv[q] = y; bi[q] = j; }      // j grows with the tile
+            }
+        }
+    };
+    for (int tile = blockIdx.x; tile < ntiles;) {
+#pragma unroll
+        for (int i = 0; i < PER; i++) ws[0][tid + i * 256] = r0[i];
+        gfetch(r0, tile + 2 * G);
+        __syncthreads();
+        compute(ws[0], tile);
+        tile += G;
+        if (tile >= ntiles) break;
+#pragma unroll
+        for (int i = 0; i < PER; i++) ws[1][tid + i * 256] = r1[i];
+        gfetch(r1, tile + 2 * G);
+        __syncthreads();
+        compute(ws[1], tile);
+        tile += G;
+    }
+    if (EPI != EPI_HEAD || !live) return;
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+        i64 v = bv[q];
+        int i = bi[q];
+#pragma unroll
+        for (int o = 1; o < 16; o <<= 1) {
+            const i64 ov = __shfl_xor(v, o, 64);
+            const int oi = __shfl_xor(i, o, 64);
+            if (oi >= 0 && (i < 0 || ov > v || (ov == v && oi < i))) { v = ov; i = oi; }
+        }
+        const int row = 16 * t + 4 * (lane >> 4) + q;
+        if ((lane & 15) == 0 && row < a.rows) {
+            a.part_v[(size_t)row * a.nblk + blockIdx.x] = v;
+            a.part_i[(size_t)row * a.nblk + blockIdx.x] = i;
+        }
     }
 }
 
@@ -278,10 +490,17 @@ BINST_L(768, PRO_TO16)
 BINST_L(3072, PRO_TO16)
 BINST_L(768, PRO_X16)
 BINST_L(3072, PRO_X16)
-#define BINST_G(K, RT, EPI) template __global__ void k_gemm<K, RT, EPI>(GemmArgs);
-#define BINST_GR(RT) BINST_G(768, RT, EPI_GAUGED) BINST_G(768, RT, EPI_PLAIN_ADD) BINST_G(768, RT, EPI_GAUGED_EDGE) \
-    BINST_G(3072, RT, EPI_PLAIN_ADD) BINST_G(768, RT, EPI_HEAD) BINST_G(768, RT, EPI_PILE) BINST_G(3072, RT, EPI_PILE)
+#define BINST_G(K, RT, CT, SK, EPI) template __global__ void k_gemm<K, RT, CT, SK, EPI>(GemmArgs);
+#define BINST_GR(RT) BINST_G(768, RT, 1, 4, EPI_GAUGED) BINST_G(768, RT, 1, 4, EPI_PLAIN_ADD) \
+    BINST_G(768, RT, 1, 4, EPI_GAUGED_EDGE) BINST_G(3072, RT, 1, 4, EPI_PLAIN_ADD) \
+    BINST_G(768, RT, 1, 4, EPI_PILE) BINST_G(3072, RT, 1, 4, EPI_PILE)
 BINST_GR(1)
 BINST_GR(2)
 BINST_GR(3)
 BINST_GR(4)
+#define BINST_H(RT) template __global__ void k_head_rows<RT, EPI_HEAD>(GemmArgs); \
+    template __global__ void k_head_rows<RT, EPI_PILE>(GemmArgs);
+BINST_H(1)
+BINST_H(2)
+BINST_H(3)
+BINST_H(4)

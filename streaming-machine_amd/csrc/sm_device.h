@@ -96,6 +96,9 @@ SMD i64 power(i64 x, i64 F, const Tables& tb) {
     i64 I = F >> 16, f = F & 0xFFFF;
     return rsh(wmul(x, tab_exp2(tb, f)), wsub(16, I));
 }
+// power(x, F) where EXP2[F & 0xFFFF] = e is known to the caller: for a gauged column F = (we + ex + 16) 65536 - LS,
+// so F & 0xFFFF = (-LS) & 0xFFFF is the row's fine part whatever the column (base2.py:70)
+SMD i64 power_known(i64 x, i64 F, i64 e) { return rsh(wmul(x, e), wsub(16, F >> 16)); }
 // the same with EXP2[F & 0xFFFF] already at hand (e = the table value for fine part fe)
 SMD i64 power_e(i64 x, i64 F, i64 fe, i64 e, const Tables& tb) {
     i64 I = F >> 16, f = F & 0xFFFF;

@@ -328,6 +328,9 @@ static void machine_free(sm_machine* m) {
 // the launch sequence of one decode step (all streams, one position each): the layers and/or the head
 enum { STEP_ALL = 3, STEP_LAYERS = 1, STEP_HEAD = 2 };
 
+// the head kernel's blocks: two per CU, each streaming about ntiles / 512 column tiles
+static int head_rows_grid(int ntiles) { return std::min(512, ntiles); }
+
 // batched streams: every bank is [light kernel (one block per stream) -> MFMA kernel (one block per 16 columns)]
 template <int RT>
 static int launch_step_batched(sm_machine* m, int parts, hipEvent_t hs, hipEvent_t he) {
@@ -359,7 +362,7 @@ static int launch_step_batched(sm_machine* m, int parts, hipEvent_t hs, hipEvent
         light(768, l == 0 ? PRO_EMBED : PRO_GAUGE, m->R, 0, rx, re);
         {
             GemmArgs a = gemm_args(m->mbank[l][0], m->QKV, 2304, rp, m->r_qkv + l * 2304);
-            k_gemm<768, RT, EPI_GAUGED><<<m->mbank[l][0].ntiles, 256, 0, m->st>>>(a);
+            k_gemm<768, RT, 1, 4, EPI_GAUGED><<<m->mbank[l][0].ntiles, 256, 0, m->st>>>(a);
         }
         {
             AttArgs a{};
@@ -372,27 +375,29 @@ static int launch_step_batched(sm_machine* m, int parts, hipEvent_t hs, hipEvent
         light(768, PRO_TO16, m->att, 0, rx + 3072, re + 2);
         {
             GemmArgs a = gemm_args(m->mbank[l][1], m->R, 768, rp + 3072, m->r_resid + (l * 2 + 0) * 768);
-            k_gemm<768, RT, EPI_PLAIN_ADD><<<m->mbank[l][1].ntiles, 256, 0, m->st>>>(a);
+            k_gemm<768, RT, 1, 4, EPI_PLAIN_ADD><<<m->mbank[l][1].ntiles, 256, 0, m->st>>>(a);
         }
         light(768, PRO_GAUGE, m->R, 0, rx + 2 * 3072, re + 4);
         {
             GemmArgs a = gemm_args(m->mbank[l][2], m->hid, 3072, rp + 2 * 3072, m->r_hid + l * 3072);
-            k_gemm<768, RT, EPI_GAUGED_EDGE><<<m->mbank[l][2].ntiles, 256, 0, m->st>>>(a);
+            k_gemm<768, RT, 1, 4, EPI_GAUGED_EDGE><<<m->mbank[l][2].ntiles, 256, 0, m->st>>>(a);
         }
         light(3072, PRO_TO16, m->hid, 0, rx + 3 * 3072, re + 6);
         {
             GemmArgs a = gemm_args(m->mbank[l][3], m->R, 768, rp + 3 * 3072, m->r_resid + (l * 2 + 1) * 768);
-            k_gemm<3072, RT, EPI_PLAIN_ADD><<<m->mbank[l][3].ntiles, 256, 0, m->st>>>(a);
+            k_gemm<3072, RT, 1, 4, EPI_PLAIN_ADD><<<m->mbank[l][3].ntiles, 256, 0, m->st>>>(a);
         }
     }
     if (parts & STEP_HEAD) {
         light(768, PRO_GAUGE, m->R, 1, m->r_hx16, m->r_hexls);
         GemmArgs a = gemm_args(m->mhead, nullptr, 0, m->r_hpile, nullptr);
-        a.part_v = m->part_v; a.part_i = m->part_i; a.nblk = m->mhead.ntiles; a.rlogits = m->r_logits;
-        if (hs) hipExtLaunchKernelGGL(k_gemm<768, RT, EPI_HEAD>, dim3(m->mhead.ntiles), dim3(256), 0, m->st, hs, he, 0, a);
-        else k_gemm<768, RT, EPI_HEAD><<<m->mhead.ntiles, 256, 0, m->st>>>(a);
+        // the head: light planes resident in LDS, eight waves per block streaming column tiles
+        const int grid = head_rows_grid(m->mhead.ntiles), parts = grid;
+        a.part_v = m->part_v; a.part_i = m->part_i; a.nblk = parts; a.rlogits = m->r_logits;
+        if (hs) hipExtLaunchKernelGGL(k_head_rows<RT, EPI_HEAD>, dim3(grid), dim3(256), 0, m->st, hs, he, 0, a);
+        else k_head_rows<RT, EPI_HEAD><<<grid, 256, 0, m->st>>>(a);
         RaceArgs r{};
-        r.part_v = m->part_v; r.part_i = m->part_i; r.nblk = m->mhead.ntiles; r.seq = m->seq; r.seq_stride = m->ctx + 1;
+        r.part_v = m->part_v; r.part_i = m->part_i; r.nblk = parts; r.seq = m->seq; r.seq_stride = m->ctx + 1;
         r.words = m->words; r.words_stride = m->ctx + 1; r.pos = ctl + CTL_POS; r.plen = ctl + CTL_PLEN;
         r.nwords = ctl + CTL_NWORDS; r.counter = reinterpret_cast<unsigned*>(ctl + CTL_COUNTER);
         k_race_rows<<<B, 256, 0, m->st>>>(r);
@@ -562,7 +567,7 @@ extern "C" int sm_create(const char* layout_dir, const sm_config* cfg, sm_machin
     }
     m->ctx = c.max_ctx < m->npos ? c.max_ctx : m->npos;
     m->head_grid = c.head_grid > 0 ? c.head_grid : 512;
-    const size_t nparts = m->B == 1 ? (size_t)m->head_grid : (size_t)m->B * ((m->vocab + 15) / 16);
+    const size_t nparts = m->B == 1 ? (size_t)m->head_grid : (size_t)m->B * head_rows_grid((m->vocab + 15) / 16);
     // state
     const size_t B = m->B, ctx = m->ctx;
     if ((rc = dalloc(&m->R, B * 768)) || (rc = dalloc(&m->QKV, B * 2304)) || (rc = dalloc(&m->att, B * 768)) ||
@@ -928,10 +933,13 @@ static void rows_product(const sm_plate* p, const int64_t* x16, int32_t rows, in
     ga.planes = p->planes; ga.rowinfo = p->rowinfo; ga.Y = (i64*)pile; ga.ystride = P.N;
     if (P.K == 768) {
         k_light<768, PRO_X16><<<rows, 256, 0, s>>>(la);
-        k_gemm<768, RT, EPI_PILE><<<P.ntiles, 256, 0, s>>>(ga);
+        if (P.N > 3072)       // head-shaped plates: the head's kernel (light planes in LDS)
+            k_head_rows<RT, EPI_PILE><<<head_rows_grid(P.ntiles), 256, 0, s>>>(ga);
+        else                  // layer-shaped plates: one column tile per block, K split over its four waves
+            k_gemm<768, RT, 1, 4, EPI_PILE><<<P.ntiles, 256, 0, s>>>(ga);
     } else {
         k_light<3072, PRO_X16><<<rows, 256, 0, s>>>(la);
-        k_gemm<3072, RT, EPI_PILE><<<P.ntiles, 256, 0, s>>>(ga);
+        k_gemm<3072, RT, 1, 4, EPI_PILE><<<P.ntiles, 256, 0, s>>>(ga);
     }
 }
 
