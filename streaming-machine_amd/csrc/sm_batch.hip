@@ -27,6 +27,11 @@ struct LightArgs {
     int* rowinfo;                 // [rows][8]: ex, LS lo, LS hi, e2, SXh, SXl, n32768
     Tables tb;
     const int* rec_pos; i64* rx16; i64* rexls;    // stream 0's record
+    // PRO_ADD_GAUGE / PRO_EDGE_TO16: the producing bank's epilogue first, from its partial accumulators
+    const int* part; int ksplit; int kin;         // [ksplit][3][rows][K] int32 (HH, MID, LL); the bank's K
+    const int* csum; const int* we; const i64* bias;   // the producing plate's column facts
+    i64* Y;                                       // [rows][K]: the epilogue's row (R: read and written)
+    i64* rpile_in; i64* rout_in;                  // stream 0's record of the producing bank
 };
 
 struct GemmArgs {
@@ -40,6 +45,7 @@ struct GemmArgs {
     const int* pos; const int* plen;
     i64* part_v; int* part_i; int nblk;   // EPI_HEAD: per (row, block) best
     const int* rec_pos; i64* rpile; i64* rout; i64* rlogits;
+    int* part;                    // EPI_PART: [ksplit][3][rows][N] int32
 };
 
 // ---------------------------------------------------------------------------------------------------------
@@ -54,6 +60,15 @@ __global__ __launch_bounds__(256) void k_light(LightArgs a) {
     const int p = a.pos ? *a.pos : 0;              // the stage product (PRO_X16) has no position
     if (a.skip_prompt && p < *a.plen - 1) return;
     i64 v[GPT][4];
+    typedef int v4l __attribute__((ext_vector_type(4)));
+    // the producing bank's light facts for this row (read before this block replaces them)
+    i64 i_ex = 0, i_ls = 0, i_e2 = 0, i_sxh = 0, i_sxl = 0, i_n32 = 0;
+    if (PRO == PRO_ADD_GAUGE || PRO == PRO_EDGE_TO16) {
+        const int* ri = a.rowinfo + (size_t)r * 8;
+        i_ex = ri[0]; i_ls = (i64)(((u64)(unsigned)ri[2] << 32) | (unsigned)ri[1]); i_e2 = ri[3];
+        i_sxh = ri[4]; i_sxl = ri[5]; i_n32 = ri[6];
+    }
+    const bool rec_in = r == 0 && a.rec_pos && *a.rec_pos == p;
 #pragma unroll
     for (int m = 0; m < GPT; m++) {
         const int g = tid + 256 * m;
@@ -61,7 +76,36 @@ __global__ __launch_bounds__(256) void k_light(LightArgs a) {
         for (int j = 0; j < 4; j++) v[m][j] = 0;
         if (g >= NG) continue;
         const int k = 4 * g;
-        if (PRO == PRO_EMBED) {
+        if (PRO == PRO_ADD_GAUGE || PRO == PRO_EDGE_TO16) {
+            v4l h = {0, 0, 0, 0}, mi = {0, 0, 0, 0}, lo = {0, 0, 0, 0};
+            for (int ks = 0; ks < a.ksplit; ks++) {
+                const int* q = a.part + ((size_t)ks * 3 * a.rows + r) * K + k;
+                h += *reinterpret_cast<const v4l*>(q);
+                mi += *reinterpret_cast<const v4l*>(q + (size_t)a.rows * K);
+                lo += *reinterpret_cast<const v4l*>(q + (size_t)2 * a.rows * K);
+            }
+            const v4l c0 = *reinterpret_cast<const v4l*>(a.csum + 2 * k), c1 = *reinterpret_cast<const v4l*>(a.csum + 2 * k + 4);
+            const v4l wv = *reinterpret_cast<const v4l*>(a.we + k);
+            const int sw[8] = {c0[0], c0[1], c0[2], c0[3], c1[0], c1[1], c1[2], c1[3]};
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const i64 pile = 65536 * (i64)h[j] + 256 * (i64)mi[j] + lo[j] + 32768 * (i_sxh + sw[2 * j]) +
+                                 128 * (i_sxl + sw[2 * j + 1]) + 16384 * (i64)a.kin + 128 * i_n32;
+                const i64 bc = a.bias[k + j];
+                i64 y;
+                if (PRO == PRO_ADD_GAUGE) {
+                    i64* yp = a.Y + (size_t)r * K + k + j;
+                    y = wadd(*yp, wadd(rsh(pile, -((i64)wv[j] + i_ex + 16)), bc));
+                    *yp = y;
+                } else {
+                    y = edge1(wadd(power_known(pile, wsub(wmul((i64)wv[j] + i_ex + 16, 65536), i_ls), i_e2), bc), a.tb);
+                    if (a.Y) a.Y[(size_t)r * K + k + j] = y;
+                }
+                v[m][j] = y;
+                if (rec_in && a.rpile_in) a.rpile_in[k + j] = pile;
+                if (rec_in && a.rout_in) a.rout_in[k + j] = y;
+            }
+        } else if (PRO == PRO_EMBED) {
             const i64 tok = a.seq[(size_t)r * a.seq_stride + p];
 #pragma unroll
             for (int j = 0; j < 4; j++) {
@@ -130,7 +174,7 @@ __global__ __launch_bounds__(256) void k_light(LightArgs a) {
             S1 += q[0]; S2h += q[1]; S2l += q[2]; SXh += q[3]; SXl += q[4]; N32 += q[5];
         }
         i64 ls = 0, e2 = 0;
-        if (PRO == PRO_GAUGE || PRO == PRO_EMBED) ls = gauge_ls_pow(S1, (S2h << 16) + S2l, ex, a.tb, e2);
+        if (PRO == PRO_GAUGE || PRO == PRO_EMBED || PRO == PRO_ADD_GAUGE) ls = gauge_ls_pow(S1, (S2h << 16) + S2l, ex, a.tb, e2);
         int* ri = a.rowinfo + (size_t)r * 8;
         ri[0] = (int)ex; ri[1] = (int)(u64)ls; ri[2] = (int)((u64)ls >> 32); ri[3] = (int)e2;
         ri[4] = (int)SXh; ri[5] = (int)SXl; ri[6] = (int)N32;
@@ -139,184 +183,116 @@ __global__ __launch_bounds__(256) void k_light(LightArgs a) {
 }
 
 // ---------------------------------------------------------------------------------------------------------
-// The byte-plane contraction.  A wave computes CT column tiles (16 columns each) for all RT row tiles with three
-// int32 accumulators per tile pair: HH, MID = HL + LH (+ CH), LL (+ CL).
-//   SK == 4: the block's four waves split the 64-k steps of one column group and meet in LDS; wave w then
-//            finishes rows 4 (l / 16) + w of every row tile (the layer banks: few columns, more blocks).
-//   SK == 1: each wave owns its own column group over all of K and finishes all its rows (the head).
-// The epilogue runs on the accumulator registers: lane l holds column l % 16 of each tile.
-template <int K, int RT, int CT, int SK, int EPI>
+// The byte-plane contraction of a layer bank.  One block per (16-column tile, K slice); its four waves split the
+// slice's 64-k steps (NS each) and meet in LDS, where each (row tile, column tile) pair holds three int32
+// accumulators: HH, MID = HL + LH (+ CH), LL (+ CL).  Wave w then finishes rows 4 (l / 16) + w of every row tile
+// for column l % 16.  Everything the block reads that depends on nothing else (weights, lights, row and column
+// facts) is issued before the first MFMA.
+//   EPI_PART: the accumulators go to part[kslice][3][rows][N]; the consumer's prologue finishes them.
+//   EPI_GAUGED / EPI_PILE: one K slice; the epilogue runs here.
+template <int K, int RT, int KSPLIT, int EPI>
 __global__ __launch_bounds__(256) void k_gemm(GemmArgs a) {
-    constexpr int KS = K / 64, NS = KS / SK, NQ = SK == 1 ? 4 : 1;
-    static_assert(SK == 1 || SK == 4, "split over 1 or 4 waves");
-    static_assert(KS % SK == 0, "k steps split evenly");
+    constexpr int KS = K / 64, NS = KS / (4 * KSPLIT);
+    static_assert(NS * 4 * KSPLIT == KS, "k steps split evenly over slices and waves");
+    static_assert(KSPLIT == 1 || EPI == EPI_PART, "a split K is finished by the consumer");
+    typedef int v4 __attribute__((ext_vector_type(4)));
     __shared__ int rinfo[64 * 8];
-    __shared__ int red[SK > 1 ? SK * CT * RT * 12 * 64 : 1];
+    __shared__ int red[4 * RT * 12 * 64];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int p = a.pos ? *a.pos : 0;                   // the stage product (EPI_PILE) has no position
-    if (EPI == EPI_HEAD && p < *a.plen - 1) return;    // a prompt position: the race kernel only advances
     const int ntiles = (a.N + 15) >> 4;
-    const int g = SK == 1 ? blockIdx.x * 4 + wave : blockIdx.x;   // this wave's column group
-    const int tile0 = g * CT;
-    // row tiles with a +32768 light need the correction plane (one load per lane, one ballot)
+    const int nt = blockIdx.x % ntiles, kb = blockIdx.x / ntiles;
+    const int s0 = kb * (KS / KSPLIT) + wave * NS;
+    const v4* Wb = reinterpret_cast<const v4*>(a.W) + (size_t)nt * KS * 128 + lane;
+    const v4* Ab = reinterpret_cast<const v4*>(a.planes) + lane;
+    v4 wh[NS], wl[NS], xh[NS][RT], xl[NS][RT];
+#pragma unroll
+    for (int i = 0; i < NS; i++) {
+        wh[i] = __builtin_nontemporal_load(Wb + (size_t)(s0 + i) * 128);
+        wl[i] = __builtin_nontemporal_load(Wb + (size_t)(s0 + i) * 128 + 64);
+    }
+#pragma unroll
+    for (int i = 0; i < NS; i++)
+#pragma unroll
+        for (int t = 0; t < RT; t++) {
+            xh[i][t] = Ab[((size_t)t * KS + s0 + i) * 192];
+            xl[i][t] = Ab[((size_t)t * KS + s0 + i) * 192 + 64];
+        }
     const int n32 = lane < a.rows ? a.rowinfo[lane * 8 + 6] : 0;
     const int rsv = tid < a.rows * 8 ? a.rowinfo[tid] : 0;
     const int rsv2 = tid + 256 < a.rows * 8 ? a.rowinfo[tid + 256] : 0;
-    const u64 cmask = __ballot(n32 != 0);
-
-    typedef int v4 __attribute__((ext_vector_type(4)));
-    v4 acc[CT][RT][3];
+    const int j = nt * 16 + (lane & 15);
+    const bool jok = j < a.N;
+    i64 swh = 0, swl = 0, we = 0, bc = 0;
+    if (EPI != EPI_PART && jok) { swh = a.csum[2 * j]; swl = a.csum[2 * j + 1]; we = a.we[j]; bc = a.bias[j]; }
+    const u64 cmask = __ballot(n32 != 0);       // row tiles with a +32768 light need the correction plane
+    v4 acc[RT][3];
 #pragma unroll
-    for (int c = 0; c < CT; c++)
+    for (int t = 0; t < RT; t++) acc[t][0] = acc[t][1] = acc[t][2] = v4{0, 0, 0, 0};
 #pragma unroll
-        for (int t = 0; t < RT; t++) acc[c][t][0] = acc[c][t][1] = acc[c][t][2] = v4{0, 0, 0, 0};
-    const v4* Wb = reinterpret_cast<const v4*>(a.W) + lane;
-    const v4* Ab = reinterpret_cast<const v4*>(a.planes) + lane;
-    int tl[CT];
+    for (int i = 0; i < NS; i++)
 #pragma unroll
-    for (int c = 0; c < CT; c++) tl[c] = min(tile0 + c, ntiles - 1);   // loads stay inside the plate
-    if (tile0 < ntiles) {
-#pragma unroll
-        for (int i = 0; i < NS; i++) {
-            const int s = SK == 1 ? i : wave * NS + i;
-            v4 wh[CT], wl[CT], xh[RT], xl[RT];
-#pragma unroll
-            for (int c = 0; c < CT; c++) {
-                const v4* w = Wb + ((size_t)tl[c] * KS + s) * 128;
-                wh[c] = __builtin_nontemporal_load(w);
-                wl[c] = __builtin_nontemporal_load(w + 64);
-            }
-#pragma unroll
-            for (int t = 0; t < RT; t++) {
-                const v4* x = Ab + ((size_t)t * KS + s) * 192;
-                xh[t] = x[0];
-                xl[t] = x[64];
-            }
-#pragma unroll
-            for (int t = 0; t < RT; t++)
-#pragma unroll
-                for (int c = 0; c < CT; c++) {
-                    acc[c][t][0] = __builtin_amdgcn_mfma_i32_16x16x64_i8(xh[t], wh[c], acc[c][t][0], 0, 0, 0);
-                    acc[c][t][1] = __builtin_amdgcn_mfma_i32_16x16x64_i8(xh[t], wl[c], acc[c][t][1], 0, 0, 0);
-                    acc[c][t][2] = __builtin_amdgcn_mfma_i32_16x16x64_i8(xl[t], wl[c], acc[c][t][2], 0, 0, 0);
-                    acc[c][t][1] = __builtin_amdgcn_mfma_i32_16x16x64_i8(xl[t], wh[c], acc[c][t][1], 0, 0, 0);
-                }
-#pragma unroll
-            for (int t = 0; t < RT; t++)
-                if ((cmask >> (16 * t)) & 0xFFFFull) {
-                    const v4 cc = Ab[((size_t)t * KS + s) * 192 + 128];
-#pragma unroll
-                    for (int c = 0; c < CT; c++) {
-                        acc[c][t][1] = __builtin_amdgcn_mfma_i32_16x16x64_i8(cc, wh[c], acc[c][t][1], 0, 0, 0);
-                        acc[c][t][2] = __builtin_amdgcn_mfma_i32_16x16x64_i8(cc, wl[c], acc[c][t][2], 0, 0, 0);
-                    }
-                }
+        for (int t = 0; t < RT; t++) {
+            acc[t][0] = __builtin_amdgcn_mfma_i32_16x16x64_i8(xh[i][t], wh[i], acc[t][0], 0, 0, 0);
+            acc[t][1] = __builtin_amdgcn_mfma_i32_16x16x64_i8(xh[i][t], wl[i], acc[t][1], 0, 0, 0);
+            acc[t][2] = __builtin_amdgcn_mfma_i32_16x16x64_i8(xl[i][t], wl[i], acc[t][2], 0, 0, 0);
+            acc[t][1] = __builtin_amdgcn_mfma_i32_16x16x64_i8(xl[i][t], wh[i], acc[t][1], 0, 0, 0);
         }
-    }
+#pragma unroll
+    for (int t = 0; t < RT; t++)
+        if ((cmask >> (16 * t)) & 0xFFFFull) {
+#pragma unroll
+            for (int i = 0; i < NS; i++) {
+                const v4 cc = Ab[((size_t)t * KS + s0 + i) * 192 + 128];
+                acc[t][1] = __builtin_amdgcn_mfma_i32_16x16x64_i8(cc, wh[i], acc[t][1], 0, 0, 0);
+                acc[t][2] = __builtin_amdgcn_mfma_i32_16x16x64_i8(cc, wl[i], acc[t][2], 0, 0, 0);
+            }
+        }
+#pragma unroll
+    for (int t = 0; t < RT; t++)
+#pragma unroll
+        for (int k3 = 0; k3 < 3; k3++)
+#pragma unroll
+            for (int q = 0; q < 4; q++) red[(((wave * RT + t) * 3 + k3) * 4 + q) * 64 + lane] = acc[t][k3][q];
     if (tid < a.rows * 8) rinfo[tid] = rsv;
     if (tid + 256 < a.rows * 8) rinfo[tid + 256] = rsv2;
-    // fin[c][t][a][qi]: the full accumulators of row 16 t + 4 (l / 16) + q, q = qi (SK == 1) or wave (SK == 4)
-    int fin[CT][RT][3][NQ];
-    if (SK > 1) {
-#pragma unroll
-        for (int c = 0; c < CT; c++)
-#pragma unroll
-            for (int t = 0; t < RT; t++)
-#pragma unroll
-                for (int k3 = 0; k3 < 3; k3++)
-#pragma unroll
-                    for (int q = 0; q < 4; q++)
-                        red[((size_t)wave * CT * RT * 12 + ((c * RT + t) * 3 + k3) * 4 + q) * 64 + lane] = acc[c][t][k3][q];
-        __syncthreads();
-#pragma unroll
-        for (int c = 0; c < CT; c++)
-#pragma unroll
-            for (int t = 0; t < RT; t++)
-#pragma unroll
-                for (int k3 = 0; k3 < 3; k3++) {
-                    int sum = 0;
-#pragma unroll
-                    for (int w = 0; w < SK; w++) sum += red[((size_t)w * CT * RT * 12 + ((c * RT + t) * 3 + k3) * 4 + wave) * 64 + lane];
-                    fin[c][t][k3][0] = sum;
-                }
-    } else {
-        __syncthreads();
-#pragma unroll
-        for (int c = 0; c < CT; c++)
-#pragma unroll
-            for (int t = 0; t < RT; t++)
-#pragma unroll
-                for (int k3 = 0; k3 < 3; k3++)
-#pragma unroll
-                    for (int q = 0; q < NQ; q++) fin[c][t][k3][q] = acc[c][t][k3][q];
-    }
-    if (tile0 >= ntiles) return;
-    const bool rec0 = a.rec_pos && *a.rec_pos == p;
-    i64 bv[RT][NQ];
-    int bi[RT][NQ];
+    __syncthreads();
+    int fin[RT][3];
 #pragma unroll
     for (int t = 0; t < RT; t++)
 #pragma unroll
-        for (int q = 0; q < NQ; q++) { bv[t][q] = 0; bi[t][q] = -1; }
+        for (int k3 = 0; k3 < 3; k3++) {
+            int sum = 0;
 #pragma unroll
-    for (int c = 0; c < CT; c++) {
-        const int j = (tile0 + c) * 16 + (lane & 15);
-        if (tile0 + c >= ntiles || j >= a.N) continue;
-        const i64 swh = a.csum[2 * j], swl = a.csum[2 * j + 1];
-        const i64 we = a.we[j], bc = a.bias[j];
-#pragma unroll
-        for (int t = 0; t < RT; t++)
-#pragma unroll
-            for (int qi = 0; qi < NQ; qi++) {
-                const int row = 16 * t + 4 * (lane >> 4) + (SK == 1 ? qi : wave);
-                if (row >= a.rows) continue;
-                const int* ri = rinfo + row * 8;
-                const i64 ex = ri[0];
-                const i64 pile = 65536 * (i64)fin[c][t][0][qi] + 256 * (i64)fin[c][t][1][qi] + fin[c][t][2][qi] +
-                                 32768 * ((i64)ri[4] + swh) + 128 * ((i64)ri[5] + swl) + 16384 * (i64)K + 128 * (i64)ri[6];
-                const bool rec = rec0 && row == 0;
-                if (rec && a.rpile) a.rpile[j] = pile;
-                if (EPI == EPI_PILE) {
-                    a.Y[(size_t)row * a.ystride + j] = pile;
-                } else if (EPI == EPI_PLAIN_ADD) {
-                    i64* y = a.Y + (size_t)row * a.ystride + j;
-                    const i64 r = wadd(*y, wadd(rsh(pile, -(we + ex + 16)), bc));
-                    *y = r;
-                    if (rec && a.rout) a.rout[j] = r;
-                } else {
-                    const i64 ls = (i64)(((u64)(unsigned)ri[2] << 32) | (unsigned)ri[1]);
-                    i64 y = wadd(power_known(pile, wsub(wmul(we + ex + 16, 65536), ls), (i64)ri[3]), bc);
-                    if (EPI == EPI_GAUGED_EDGE) y = edge1(y, a.tb);
-                    if (EPI == EPI_HEAD) {
-                        if (rec && a.rlogits) a.rlogits[j] = y;
-                        if (bi[t][qi] < 0 || y > bv[t][qi]) { bv[t][qi] = y; bi[t][qi] = j; }   // j grows with c
-                    } else {
-                        a.Y[(size_t)row * a.ystride + j] = y;
-                        if (rec && a.rout) a.rout[j] = y;
-                    }
-                }
-            }
-    }
-    if (EPI != EPI_HEAD) return;
-    // per row: the best of the 16 lanes that hold its columns (ties to the lowest column), then one store
-#pragma unroll
-    for (int t = 0; t < RT; t++)
-#pragma unroll
-        for (int qi = 0; qi < NQ; qi++) {
-            i64 v = bv[t][qi];
-            int i = bi[t][qi];
-#pragma unroll
-            for (int o = 1; o < 16; o <<= 1) {
-                const i64 ov = __shfl_xor(v, o, 64);
-                const int oi = __shfl_xor(i, o, 64);
-                if (oi >= 0 && (i < 0 || ov > v || (ov == v && oi < i))) { v = ov; i = oi; }
-            }
-            const int row = 16 * t + 4 * (lane >> 4) + (SK == 1 ? qi : wave);
-            if ((lane & 15) == 0 && row < a.rows) {
-                a.part_v[(size_t)row * a.nblk + g] = v;
-                a.part_i[(size_t)row * a.nblk + g] = i;
-            }
+            for (int w = 0; w < 4; w++) sum += red[(((w * RT + t) * 3 + k3) * 4 + wave) * 64 + lane];
+            fin[t][k3] = sum;
         }
+    if (!jok) return;
+    const int p = a.pos ? *a.pos : 0;
+    const bool rec0 = a.rec_pos && *a.rec_pos == p;
+#pragma unroll
+    for (int t = 0; t < RT; t++) {
+        const int row = 16 * t + 4 * (lane >> 4) + wave;
+        if (row >= a.rows) continue;
+        if (EPI == EPI_PART) {
+#pragma unroll
+            for (int k3 = 0; k3 < 3; k3++) a.part[(((size_t)kb * 3 + k3) * a.rows + row) * a.N + j] = fin[t][k3];
+            continue;
+        }
+        const int* ri = rinfo + row * 8;
+        const i64 ex = ri[0];
+        const i64 pile = 65536 * (i64)fin[t][0] + 256 * (i64)fin[t][1] + fin[t][2] + 32768 * ((i64)ri[4] + swh) +
+                         128 * ((i64)ri[5] + swl) + 16384 * (i64)K + 128 * (i64)ri[6];
+        const bool rec = rec0 && row == 0;
+        if (rec && a.rpile) a.rpile[j] = pile;
+        if (EPI == EPI_PILE) {
+            a.Y[(size_t)row * a.ystride + j] = pile;
+        } else {
+            const i64 ls = (i64)(((u64)(unsigned)ri[2] << 32) | (unsigned)ri[1]);
+            const i64 y = wadd(power_known(pile, wsub(wmul(we + ex + 16, 65536), ls), (i64)ri[3]), bc);
+            a.Y[(size_t)row * a.ystride + j] = y;
+            if (rec && a.rout) a.rout[j] = y;
+        }
+    }
 }
 
 // ---------------------------------------------------------------------------------------------------------
@@ -490,10 +466,11 @@ BINST_L(768, PRO_TO16)
 BINST_L(3072, PRO_TO16)
 BINST_L(768, PRO_X16)
 BINST_L(3072, PRO_X16)
-#define BINST_G(K, RT, CT, SK, EPI) template __global__ void k_gemm<K, RT, CT, SK, EPI>(GemmArgs);
-#define BINST_GR(RT) BINST_G(768, RT, 1, 4, EPI_GAUGED) BINST_G(768, RT, 1, 4, EPI_PLAIN_ADD) \
-    BINST_G(768, RT, 1, 4, EPI_GAUGED_EDGE) BINST_G(3072, RT, 1, 4, EPI_PLAIN_ADD) \
-    BINST_G(768, RT, 1, 4, EPI_PILE) BINST_G(3072, RT, 1, 4, EPI_PILE)
+BINST_L(768, PRO_ADD_GAUGE)
+BINST_L(3072, PRO_EDGE_TO16)
+#define BINST_G(K, RT, KSPLIT, EPI) template __global__ void k_gemm<K, RT, KSPLIT, EPI>(GemmArgs);
+#define BINST_GR(RT) BINST_G(768, RT, 1, EPI_GAUGED) BINST_G(768, RT, 1, EPI_PART) BINST_G(3072, RT, 4, EPI_PART) \
+    BINST_G(768, RT, 1, EPI_PILE) BINST_G(3072, RT, 1, EPI_PILE)
 BINST_GR(1)
 BINST_GR(2)
 BINST_GR(3)

@@ -6,13 +6,17 @@
 enum { PRO_GAUGE = 0,   // gauge_log of the stream row R (768): x16, ex, LS (base2.py:55-60)
        PRO_TO16 = 1,    // to16 of an activation row (768 or 3072): x16, ex (base2.py:24-27)
        PRO_EMBED = 2,   // the word enters: R = wte[word] + wpe[pos] (base2.py:103), then PRO_GAUGE
-       PRO_X16 = 3 };   // the light is given (int64 x16 values, ex = -16): the raw product test
+       PRO_X16 = 3,     // the light is given (int64 x16 values, ex = -16): the raw product test
+       // batched streams: the producing bank's epilogue from its partial accumulators, then the light
+       PRO_ADD_GAUGE = 4,   // R += rshift(pile, -(we + ex + 16)) + b, then PRO_GAUGE of R   (base2.py:105-106, 55-60)
+       PRO_EDGE_TO16 = 5 }; // edge(power(pile, ...) + b), then PRO_TO16 of that row       (base2.py:106, 78-83, 24-27)
 // epilogue: what a phase does with each finished pile
 enum { EPI_GAUGED = 0,       // power(pile, (we + ex + 16) 65536 - LS) + b          (base2.py:70-71)
        EPI_GAUGED_EDGE = 1,  // the same, then the edge                               (base2.py:106, 78-83)
        EPI_PLAIN_ADD = 2,    // R += rshift(pile, -(we + ex + 16)) + b                  (base2.py:73-76, 105-106)
        EPI_HEAD = 3,         // gauged logit + standing amount, then the race           (base2.py:107-114)
-       EPI_PILE = 4 };       // the raw pile (product only)                             (base2.py:29-32)
+       EPI_PILE = 4,         // the raw pile (product only)                             (base2.py:29-32)
+       EPI_PART = 5 };       // batched: the int32 accumulators, finished by the consumer's prologue
 
 // Record of one position's intermediates (stream 0), written when the position equals *pos.
 struct Rec {

@@ -213,7 +213,8 @@ struct sm_machine {
     DevPlate head;
     MfmaPlate mbank[12][4];        // batched streams: MFMA byte planes
     MfmaPlate mhead;
-    signed char* planes = nullptr; // [4][48][3][1024] light planes of the current phase
+    signed char* planes = nullptr;  // [4][48][3][1024] light planes of the current phase
+    int* part_acc = nullptr;        // batched: a bank's partial accumulators [K slices][3][streams][N] int32
     int* rowinfo = nullptr;        // [B][8]
     i64* wte = nullptr;
     i64* wpe = nullptr;
@@ -317,7 +318,7 @@ static void machine_free(sm_machine* m) {
     free_plate(m->head);
     free_mfma_plate(m->mhead);
     tables_free(m->T);
-    void* ps[] = {m->planes, m->rowinfo, m->wte, m->wpe, m->R, m->QKV, m->att, m->hid, m->K16, m->EK, m->V, m->seq, m->words, m->ctl,
+    void* ps[] = {m->planes, m->part_acc, m->rowinfo, m->wte, m->wpe, m->R, m->QKV, m->att, m->hid, m->K16, m->EK, m->V, m->seq, m->words, m->ctl,
                   m->part_v, m->part_i, m->r_x16, m->r_exls, m->r_pile, m->r_qkv, m->r_att, m->r_hid, m->r_resid,
                   m->r_hx16, m->r_hexls, m->r_hpile, m->r_logits};
     for (void* p : ps) hfree(p);
@@ -337,32 +338,41 @@ static int launch_step_batched(sm_machine* m, int parts, hipEvent_t hs, hipEvent
     const Tables tb = m->T.tb();
     int* ctl = m->ctl;
     const int B = m->B;
-    auto light = [&](int K, int pro, const i64* X, int skip, i64* rx16, i64* rexls) {
+    auto light_args = [&](int K, const i64* X, i64* rx16, i64* rexls) {
         LightArgs a{};
         a.K = K; a.rows = B; a.X = X; a.wte = m->wte; a.wpe = m->wpe; a.seq = m->seq; a.seq_stride = m->ctx + 1;
-        a.Rw = m->R; a.pos = ctl + CTL_POS; a.plen = ctl + CTL_PLEN; a.skip_prompt = skip;
+        a.Rw = m->R; a.pos = ctl + CTL_POS; a.plen = ctl + CTL_PLEN;
         a.planes = m->planes; a.rowinfo = m->rowinfo; a.tb = tb;
         a.rec_pos = ctl + CTL_RECPOS; a.rx16 = rx16; a.rexls = rexls;
-        if (K == 3072) k_light<3072, PRO_TO16><<<B, 256, 0, m->st>>>(a);
-        else if (pro == PRO_EMBED) k_light<768, PRO_EMBED><<<B, 256, 0, m->st>>>(a);
-        else if (pro == PRO_GAUGE) k_light<768, PRO_GAUGE><<<B, 256, 0, m->st>>>(a);
-        else k_light<768, PRO_TO16><<<B, 256, 0, m->st>>>(a);
+        return a;
+    };
+    // the producing bank's epilogue (from its partial accumulators) followed by the next light
+    auto finish_light = [&](const MfmaPlate& P, int ksplit, i64* Y, i64* rpile, i64* rout, i64* rx16, i64* rexls) {
+        LightArgs a = light_args(P.N, nullptr, rx16, rexls);
+        a.part = m->part_acc; a.ksplit = ksplit; a.kin = P.K; a.csum = P.csum; a.we = P.e; a.bias = P.b; a.Y = Y;
+        a.rpile_in = rpile; a.rout_in = rout;
+        if (P.N == 3072) k_light<3072, PRO_EDGE_TO16><<<B, 256, 0, m->st>>>(a);
+        else k_light<768, PRO_ADD_GAUGE><<<B, 256, 0, m->st>>>(a);
     };
     auto gemm_args = [&](const MfmaPlate& P, i64* Y, int ystride, i64* rpile, i64* rout) {
         GemmArgs a{};
         a.K = P.K; a.N = P.N; a.rows = B; a.RT = RT; a.W = P.W; a.csum = P.csum; a.we = P.e; a.bias = P.b;
         a.planes = m->planes; a.rowinfo = m->rowinfo; a.Y = Y; a.ystride = ystride; a.tb = tb;
         a.pos = ctl + CTL_POS; a.plen = ctl + CTL_PLEN; a.rec_pos = ctl + CTL_RECPOS; a.rpile = rpile; a.rout = rout;
+        a.part = m->part_acc;
         return a;
     };
     for (int l = 0; l < 12 && (parts & STEP_LAYERS); l++) {
         i64* rx = m->r_x16 + (size_t)l * 4 * 3072;
         i64* re = m->r_exls + (size_t)l * 4 * 2;
         i64* rp = m->r_pile + (size_t)l * 4 * 3072;
-        light(768, l == 0 ? PRO_EMBED : PRO_GAUGE, m->R, 0, rx, re);
+        if (l == 0) {      // the word enters; later layers get their light from the previous layer's last kernel
+            LightArgs a = light_args(768, m->R, rx, re);
+            k_light<768, PRO_EMBED><<<B, 256, 0, m->st>>>(a);
+        }
         {
             GemmArgs a = gemm_args(m->mbank[l][0], m->QKV, 2304, rp, m->r_qkv + l * 2304);
-            k_gemm<768, RT, 1, 4, EPI_GAUGED><<<m->mbank[l][0].ntiles, 256, 0, m->st>>>(a);
+            k_gemm<768, RT, 1, EPI_GAUGED><<<m->mbank[l][0].ntiles, 256, 0, m->st>>>(a);
         }
         {
             AttArgs a{};
@@ -372,26 +382,31 @@ static int launch_step_batched(sm_machine* m, int parts, hipEvent_t hs, hipEvent
             a.rec_pos = ctl + CTL_RECPOS; a.ratt = m->r_att + l * 768;
             k_attend<<<dim3(12, m->B), NTHR, (size_t)m->ctx * 8, m->st>>>(a);
         }
-        light(768, PRO_TO16, m->att, 0, rx + 3072, re + 2);
         {
-            GemmArgs a = gemm_args(m->mbank[l][1], m->R, 768, rp + 3072, m->r_resid + (l * 2 + 0) * 768);
-            k_gemm<768, RT, 1, 4, EPI_PLAIN_ADD><<<m->mbank[l][1].ntiles, 256, 0, m->st>>>(a);
+            LightArgs a = light_args(768, m->att, rx + 3072, re + 2);
+            k_light<768, PRO_TO16><<<B, 256, 0, m->st>>>(a);
         }
-        light(768, PRO_GAUGE, m->R, 0, rx + 2 * 3072, re + 4);
         {
-            GemmArgs a = gemm_args(m->mbank[l][2], m->hid, 3072, rp + 2 * 3072, m->r_hid + l * 3072);
-            k_gemm<768, RT, 1, 4, EPI_GAUGED_EDGE><<<m->mbank[l][2].ntiles, 256, 0, m->st>>>(a);
+            GemmArgs a = gemm_args(m->mbank[l][1], nullptr, 0, nullptr, nullptr);
+            k_gemm<768, RT, 1, EPI_PART><<<m->mbank[l][1].ntiles, 256, 0, m->st>>>(a);
         }
-        light(3072, PRO_TO16, m->hid, 0, rx + 3 * 3072, re + 6);
+        finish_light(m->mbank[l][1], 1, m->R, rp + 3072, m->r_resid + (l * 2 + 0) * 768, rx + 2 * 3072, re + 4);
         {
-            GemmArgs a = gemm_args(m->mbank[l][3], m->R, 768, rp + 3 * 3072, m->r_resid + (l * 2 + 1) * 768);
-            k_gemm<3072, RT, 1, 4, EPI_PLAIN_ADD><<<m->mbank[l][3].ntiles, 256, 0, m->st>>>(a);
+            GemmArgs a = gemm_args(m->mbank[l][2], nullptr, 0, nullptr, nullptr);
+            k_gemm<768, RT, 1, EPI_PART><<<m->mbank[l][2].ntiles, 256, 0, m->st>>>(a);
         }
+        finish_light(m->mbank[l][2], 1, nullptr, rp + 2 * 3072, m->r_hid + l * 3072, rx + 3 * 3072, re + 6);
+        {
+            GemmArgs a = gemm_args(m->mbank[l][3], nullptr, 0, nullptr, nullptr);
+            k_gemm<3072, RT, 4, EPI_PART><<<m->mbank[l][3].ntiles * 4, 256, 0, m->st>>>(a);
+        }
+        const bool last = l == 11;     // the last stream update lights the head
+        finish_light(m->mbank[l][3], 4, m->R, rp + 3 * 3072, m->r_resid + (l * 2 + 1) * 768,
+                     last ? m->r_hx16 : m->r_x16 + (size_t)(l + 1) * 4 * 3072, last ? m->r_hexls : m->r_exls + (size_t)(l + 1) * 4 * 2);
     }
     if (parts & STEP_HEAD) {
-        light(768, PRO_GAUGE, m->R, 1, m->r_hx16, m->r_hexls);
         GemmArgs a = gemm_args(m->mhead, nullptr, 0, m->r_hpile, nullptr);
-        // the head: light planes resident in LDS, eight waves per block streaming column tiles
+        // the head: each wave's row tile of lights in registers, weight tiles streamed through LDS
         const int grid = head_rows_grid(m->mhead.ntiles), parts = grid;
         a.part_v = m->part_v; a.part_i = m->part_i; a.nblk = parts; a.rlogits = m->r_logits;
         if (hs) hipExtLaunchKernelGGL(k_head_rows<RT, EPI_HEAD>, dim3(grid), dim3(256), 0, m->st, hs, he, 0, a);
@@ -576,6 +591,7 @@ extern "C" int sm_create(const char* layout_dir, const sm_config* cfg, sm_machin
         (rc = dalloc(&m->ctl, (size_t)CTL_N)) || (rc = dalloc(&m->part_v, nparts)) ||
         (rc = dalloc(&m->part_i, nparts)) || (rc = dalloc(&m->r_x16, (size_t)12 * 4 * 3072)) ||
         (rc = dalloc(&m->planes, (size_t)4 * 48 * 3 * 1024)) || (rc = dalloc(&m->rowinfo, (size_t)m->B * 8)) ||
+        (rc = dalloc(&m->part_acc, m->B > 1 ? (size_t)4 * 3 * m->B * 3072 : (size_t)1)) ||
         (rc = dalloc(&m->r_exls, (size_t)12 * 4 * 2)) || (rc = dalloc(&m->r_pile, (size_t)12 * 4 * 3072)) ||
         (rc = dalloc(&m->r_qkv, (size_t)12 * 2304)) || (rc = dalloc(&m->r_att, (size_t)12 * 768)) ||
         (rc = dalloc(&m->r_hid, (size_t)12 * 3072)) || (rc = dalloc(&m->r_resid, (size_t)12 * 2 * 768)) ||
@@ -936,10 +952,10 @@ static void rows_product(const sm_plate* p, const int64_t* x16, int32_t rows, in
         if (P.N > 3072)       // head-shaped plates: the head's kernel (light planes in LDS)
             k_head_rows<RT, EPI_PILE><<<head_rows_grid(P.ntiles), 256, 0, s>>>(ga);
         else                  // layer-shaped plates: one column tile per block, K split over its four waves
-            k_gemm<768, RT, 1, 4, EPI_PILE><<<P.ntiles, 256, 0, s>>>(ga);
+            k_gemm<768, RT, 1, EPI_PILE><<<P.ntiles, 256, 0, s>>>(ga);
     } else {
         k_light<3072, PRO_X16><<<rows, 256, 0, s>>>(la);
-        k_gemm<3072, RT, 1, 4, EPI_PILE><<<P.ntiles, 256, 0, s>>>(ga);
+        k_gemm<3072, RT, 1, EPI_PILE><<<P.ntiles, 256, 0, s>>>(ga);
     }
 }
 
