@@ -25,27 +25,7 @@
  * Parity pins: closed forms and brute force for each stage (tests/test_oracle_*),
  * golden vectors written by tests/golden/make_golden.py from base2.py itself.
  */
-#include <stdint.h>
-#include <stdlib.h>
-#include <string.h>
-
-#define ORC_OK 0
-#define ORC_E_BOUND 1      /* a product reached 2^52 (base2.py:31's assert) */
-#define ORC_E_ARG 2
-
-typedef int64_t i64;
-typedef uint64_t u64;
-
-/* ---------------- numpy int64 arithmetic ---------------- */
-static inline i64 wadd(i64 a, i64 b) { return (i64)((u64)a + (u64)b); }
-static inline i64 wsub(i64 a, i64 b) { return (i64)((u64)a - (u64)b); }
-static inline i64 wmul(i64 a, i64 b) { return (i64)((u64)a * (u64)b); }
-static inline i64 shl(i64 x, i64 n) { return ((u64)n >= 64) ? 0 : (i64)((u64)x << n); }
-static inline i64 sar(i64 x, i64 n) { return ((u64)n >= 64) ? (x < 0 ? -1 : 0) : (x >> n); }
-static inline int bitlen_u(u64 a) { return a ? 64 - __builtin_clzll(a) : 0; }
-/* Python int(v).bit_length() of a numpy int64 value: the length of |v| */
-static inline int bitlen_py(i64 v) { return bitlen_u(v < 0 ? (u64)0 - (u64)v : (u64)v); }
-static inline i64 iabs(i64 v) { return v < 0 ? (i64)((u64)0 - (u64)v) : v; }   /* np.abs wraps at INT64_MIN */
+#include "orc_common.h"
 
 /* base2.py:18-22  rshift(X, s): X x 2^-s rounded half up; s <= 0 is a left shift */
 i64 orc_rshift1(i64 x, i64 s) {

@@ -1,0 +1,136 @@
+"""The Pythia-160m-shaped integer machine's numbers: a seeded random checkpoint and its conversion.
+
+Restates foundation0/pythia_convert.py (the only place a float exists) for one checkpoint:
+  * every plate [in][out] as int16 with one power of two per output neuron, the smallest that holds the
+    neuron's largest weight in 16 places (pythia_convert.py:57-68, 75-77); the head per word column, the embed
+    table per word row (:104-106);
+  * biases and the norms' offsets as whole numbers at the stream's scale 2^-16 (:72, 79, 89-90);
+  * each norm's gain on 16 places with one power of two for the vector, NOT folded into the plate after it
+    (:85-90);
+  * tables: PHI and the arrival (as base2_convert.py builds them), LOG2/EXP2, cos/sin of the turns at 2^-30 for
+    every position (rotary on the first quarter of each head, pairs (i, i + quarter/2)), eps40 = eps d^2 2^40
+    and half_log2_hs = log2(head size)/2 at 2^-16 (:109-120).
+The reference converts a finished and a start checkpoint onto one grid (X.w / X.s); with one random checkpoint
+both are the same array, written under both names so the reference's machine loads the file unchanged.
+As in convert.py, ceil(log2(mx / 32767)) is evaluated exactly through frexp.
+"""
+from __future__ import annotations
+
+import math
+
+import numpy as np
+
+from .convert import ES, _ceil_log2, stream, tables
+
+PYTHIA_SHAPE = dict(n_layer=12, d=768, n_head=12, d_ff=3072, vocab=50304, n_ctx=2048, rotary_pct=0.25,
+                    rotary_emb_base=10000, layer_norm_eps=1e-5)
+P_BANKS = ("qkv", "proj", "fc", "mproj")
+P_NORMS = ("ln1", "ln2")
+
+
+def random_pythia(seed: int = 5, vocab: int = 50304, n_layer: int = 12, std: float = 0.02):
+    """HF GPTNeoX-named float32 state dict of a Pythia-160m-shaped model (d=768, 12 heads of 64, FFN 3072,
+    rotary on 25% of each head, parallel residual, untied embed_in / embed_out) and its config.
+
+    One default_rng(seed) walks the state dict in GPTNeoXForCausalLM order; weights, biases and norm offsets are
+    N(0, 0.02); norm gains are 1 + N(0, 0.02) (a literal N(0, 0.02) gain would shrink every normalised row about
+    fifty times)."""
+    rng = np.random.default_rng(seed)
+    d, f = 768, 3072
+
+    def nrm(*shape):
+        return (rng.standard_normal(shape) * std).astype(np.float32)
+
+    def gain(n):
+        return (1.0 + rng.standard_normal(n) * std).astype(np.float32)
+
+    sd = {"gpt_neox.embed_in.weight": nrm(vocab, d)}
+    for l in range(n_layer):
+        p = f"gpt_neox.layers.{l}."
+        sd[p + "input_layernorm.weight"] = gain(d)
+        sd[p + "input_layernorm.bias"] = nrm(d)
+        sd[p + "post_attention_layernorm.weight"] = gain(d)
+        sd[p + "post_attention_layernorm.bias"] = nrm(d)
+        sd[p + "attention.query_key_value.weight"] = nrm(3 * d, d)     # torch Linear [out][in]
+        sd[p + "attention.query_key_value.bias"] = nrm(3 * d)
+        sd[p + "attention.dense.weight"] = nrm(d, d)
+        sd[p + "attention.dense.bias"] = nrm(d)
+        sd[p + "mlp.dense_h_to_4h.weight"] = nrm(f, d)
+        sd[p + "mlp.dense_h_to_4h.bias"] = nrm(f)
+        sd[p + "mlp.dense_4h_to_h.weight"] = nrm(d, f)
+        sd[p + "mlp.dense_4h_to_h.bias"] = nrm(d)
+    sd["gpt_neox.final_layer_norm.weight"] = gain(d)
+    sd["gpt_neox.final_layer_norm.bias"] = nrm(d)
+    sd["embed_out.weight"] = nrm(vocab, d)
+    cfg = dict(PYTHIA_SHAPE, vocab=vocab, n_layer=n_layer)
+    return sd, cfg
+
+
+def q16(W: np.ndarray, axis: int):
+    """int16 values with one power of two per neuron along `axis` (0: per column, 1: per row)
+    (pythia_convert.py:57-68 with start == finished)."""
+    mx = np.maximum(np.abs(W).max(axis), 1e-30)
+    e = _ceil_log2(mx / 32767)
+    q = np.round(W / np.exp2(np.expand_dims(e, axis).astype(np.float64))).astype(np.int64)
+    if np.abs(q).max() > 32767:
+        raise ValueError("q16: a value does not fit 16 places")
+    return q.astype(np.int16), e
+
+
+def pythia_tables(d: int, hs: int, rot: int, n_pos: int, base: float, eps: float) -> dict:
+    """The Pythia machine's tables (pythia_convert.py:109-120)."""
+    t = tables()
+    inv = float(base) ** (-np.arange(0, rot, 2) / rot)
+    ang = np.arange(n_pos)[:, None] * inv[None, :]
+    half = round(math.log2(hs) / 2 * 65536)
+    if half * 2 != math.log2(hs) * 65536:
+        raise ValueError("head size must be a power of two")
+    return {"phi": t["phi"], "arrival": t["arrival"], "log2": t["log2"], "exp2": t["exp2"],
+            "cos": np.round(np.cos(ang) * 2 ** 30).astype(np.int64), "sin": np.round(np.sin(ang) * 2 ** 30).astype(np.int64),
+            "eps40": np.array(round(eps * d * d * 2 ** 40)), "half_log2_hs": np.array(half)}
+
+
+def convert_pythia(sd: dict, cfg: dict) -> dict:
+    """GPTNeoX-named state dict (numpy or torch) + config -> the npz dictionary pythia_base2.py loads."""
+    def get(k):
+        v = sd[k]
+        if hasattr(v, "detach"):
+            v = v.detach().cpu().numpy()
+        return np.asarray(v, dtype=np.float64)
+
+    d, L, nh = cfg["d"], cfg["n_layer"], cfg["n_head"]
+    hs = d // nh
+    rot = int(hs * cfg["rotary_pct"])
+    out = {}
+
+    def plate(name, key, bias=True):
+        w, e = q16(get(key + ".weight").T, 0)
+        out[name + ".w"], out[name + ".s"], out[name + ".e"] = w, w, e
+        if bias:
+            b = stream(get(key + ".bias"))
+            out[name + ".b"], out[name + ".bs"] = b, b
+
+    def norm(name, key):
+        g = get(key + ".weight")
+        ge = int(_ceil_log2(np.array([max(np.abs(g).max(), 1e-30) / 32767]))[0])
+        gq = np.round(g / 2.0 ** ge).astype(np.int64)
+        b = stream(get(key + ".bias"))
+        out[name + ".g"], out[name + ".gs"], out[name + ".ge"] = gq, gq, np.array(ge)
+        out[name + ".b"], out[name + ".bs"] = b, b
+
+    for l in range(L):
+        p = f"gpt_neox.layers.{l}."
+        norm(f"ln1.{l}", p + "input_layernorm")
+        norm(f"ln2.{l}", p + "post_attention_layernorm")
+        plate(f"qkv.{l}", p + "attention.query_key_value")
+        plate(f"proj.{l}", p + "attention.dense")
+        plate(f"fc.{l}", p + "mlp.dense_h_to_4h")
+        plate(f"mproj.{l}", p + "mlp.dense_4h_to_h")
+    norm("lnf", "gpt_neox.final_layer_norm")
+    plate("head", "embed_out", bias=False)
+    ew, ee = q16(get("gpt_neox.embed_in.weight"), 1)
+    out["embed.w"], out["embed.s"], out["embed.e"] = ew, ew, ee
+    out.update(pythia_tables(d, hs, rot, cfg["n_ctx"], cfg["rotary_emb_base"], cfg["layer_norm_eps"]))
+    for k, v in dict(d=d, L=L, heads=nh, hs=hs, rot=rot, vocab=cfg["vocab"]).items():
+        out[k] = np.array(v)
+    return out
