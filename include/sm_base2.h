@@ -86,7 +86,11 @@ enum {
     SM_READ_REC_HX16 = 17,/* [768] the head's light */
     SM_READ_REC_HEXLS = 18,/* [2] */
     SM_READ_REC_HPILE = 19,/* [vocab] */
-    SM_READ_REC_LOGITS = 20 /* [vocab] gauged logits + standing amount */
+    SM_READ_REC_LOGITS = 20,/* [vocab] gauged logits + standing amount (Pythia: plain logits, no bias) */
+    /* the Pythia machine (foundation0/pythia_base2.py) only */
+    SM_READ_REC_GAUGE = 21, /* [12][2][768] the gauge rows (ln1, ln2) of each layer (:100-110) */
+    SM_READ_REC_FCPRE = 22, /* [12][3072] fc's plain output before the edge */
+    SM_READ_REC_HGAUGE = 23 /* [768] the head's gauge row (lnf) */
 };
 /* Copies one device array to host memory dst (bytes must match).  Replaces reading MTLBuffer contents
  * (base2_stream.swift:282-286) for per-intermediate parity. */
@@ -98,6 +102,9 @@ int sm_profile(sm_machine* m, int64_t* n_heads, double* head_us, int32_t clear);
 
 /* Facts about a created machine: vocab, max_ctx, max_streams, rows of the position table, and whether the
  * table entries are recomputed from their formulas (1) or read from memory (0). */
+/* Which machine a layout holds: 0 the GPT-2 machine of base2.py, 1 the Pythia machine of
+ * foundation0/pythia_base2.py (a layout whose manifest says "kind": "pythia"); negative on error. */
+int sm_model_kind(const sm_machine* m);
 int sm_info(const sm_machine* m, int32_t* vocab, int32_t* max_ctx, int32_t* max_streams, int32_t* n_pos,
             int32_t* arith_tables);
 

@@ -21,8 +21,9 @@ struct Tables {
     // derived, exact integer compositions of the tables above (built on the host at create):
     //   GPOW[r * 65536 + m] = EXP2[(log768 - ((r 65536 + LOG2[m]) >> 1)) & 0xFFFF]   the gauge's power factor
     //   HPOW[m]             = EXP2[(-LOG2[m]) & 0xFFFF]                              the arrivals' divisor
+    //   PGPOW[r * 65536 + m] = EXP2[(-((r 65536 + LOG2[m]) >> 1)) & 0xFFFF]           Pythia's gauge factor
     // so that log2fix's mantissa m gives LOG2[m] and the EXP2 factor in two independent reads
-    const int* GPOW; const int* HPOW;
+    const int* GPOW; const int* HPOW; const int* PGPOW;
 };
 
 SMD i64 wadd(i64 a, i64 b) { return (i64)((u64)a + (u64)b); }
@@ -79,6 +80,12 @@ SMD i64 utab_gpow(const Tables& tb, int r, int m) {
     return tb.arith ? exp2_entry((int)((tb.log768 - (((i64)r * 65536 + log2_entry(m)) >> 1)) & 0xFFFF))
                     : ((cint_p)tb.GPOW)[r * 65536 + m];
 }
+SMD i64 utab_pgpow(const Tables& tb, int r, int m) {
+    r = __builtin_amdgcn_readfirstlane(r);
+    m = __builtin_amdgcn_readfirstlane(m);
+    return tb.arith ? exp2_entry((int)((-(((i64)r * 65536 + log2_entry(m)) >> 1)) & 0xFFFF))
+                    : ((cint_p)tb.PGPOW)[r * 65536 + m];
+}
 SMD i64 utab_hpow(const Tables& tb, int m) {
     m = __builtin_amdgcn_readfirstlane(m);
     return tb.arith ? exp2_entry((int)((-(i64)log2_entry(m)) & 0xFFFF)) : ((cint_p)tb.HPOW)[m];
@@ -129,6 +136,16 @@ SMD i64 eps_term(i64 eps40, i64 ex) {
 SMD i64 gauge_ls(i64 s1, i64 s2, i64 ex, const Tables& tb) {
     i64 V = wadd(wsub(wmul(768, s2), wmul(s1, s1)), eps_term(tb.eps40, ex));
     return wadd(wsub(log2fix(V, tb) >> 1, tb.log768), wmul(ex, 65536));
+}
+// foundation0/pythia_base2.py:106-108  Pythia's gauge level LS = log2fix(V) >> 1 (no log2(d), no ex term: the
+// centred lane is d x - S1, not x - S1 / d) and EXP2[(-LS) & 0xFFFF], its power factor for every lane
+SMD i64 pgauge_ls_pow(i64 s1, i64 s2, i64 ex, const Tables& tb, i64& e2) {
+    i64 V = wadd(wsub(wmul(768, s2), wmul(s1, s1)), eps_term(tb.eps40, ex));
+    int t; i64 m;
+    log2_parts(V, t, m);
+    const i64 lg = utab_log2(tb, (int)m);
+    e2 = utab_pgpow(tb, t & 1, (int)m);
+    return wadd((i64)t * 65536, lg) >> 1;
 }
 // the same, also giving EXP2[(-LS) & 0xFFFF] (the power factor every gauged column uses) from one derived read
 SMD i64 gauge_ls_pow(i64 s1, i64 s2, i64 ex, const Tables& tb, i64& e2) {

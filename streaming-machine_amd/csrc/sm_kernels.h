@@ -9,14 +9,21 @@ enum { PRO_GAUGE = 0,   // gauge_log of the stream row R (768): x16, ex, LS (bas
        PRO_X16 = 3,     // the light is given (int64 x16 values, ex = -16): the raw product test
        // batched streams: the producing bank's epilogue from its partial accumulators, then the light
        PRO_ADD_GAUGE = 4,   // R += rshift(pile, -(we + ex + 16)) + b, then PRO_GAUGE of R   (base2.py:105-106, 55-60)
-       PRO_EDGE_TO16 = 5 }; // edge(power(pile, ...) + b), then PRO_TO16 of that row       (base2.py:106, 78-83, 24-27)
+       PRO_EDGE_TO16 = 5,   // edge(power(pile, ...) + b), then PRO_TO16 of that row       (base2.py:106, 78-83, 24-27)
+       // the Pythia machine (foundation0/pythia_base2.py)
+       PRO_PGAUGE = 6,      // its gauge with the norm's gain and offset, then to16 of that row     (:100-110, 113)
+       PRO_PEMBED = 7 };    // R = rshift(embed.w[word], -(embed.e[word] + 16)) (:153), then PRO_PGAUGE
 // epilogue: what a phase does with each finished pile
 enum { EPI_GAUGED = 0,       // power(pile, (we + ex + 16) 65536 - LS) + b          (base2.py:70-71)
        EPI_GAUGED_EDGE = 1,  // the same, then the edge                               (base2.py:106, 78-83)
        EPI_PLAIN_ADD = 2,    // R += rshift(pile, -(we + ex + 16)) + b                  (base2.py:73-76, 105-106)
        EPI_HEAD = 3,         // gauged logit + standing amount, then the race           (base2.py:107-114)
        EPI_PILE = 4,         // the raw pile (product only)                             (base2.py:29-32)
-       EPI_PART = 5 };       // batched: the int32 accumulators, finished by the consumer's prologue
+       EPI_PART = 5,         // batched: the int32 accumulators, finished by the consumer's prologue
+       // the Pythia machine: every plate is plain (foundation0/pythia_base2.py:112-114)
+       EPI_PLAIN = 6,        // rshift(pile, -(we + ex + 16)) + b, written
+       EPI_PLAIN_EDGE = 7,   // the same, then the edge (:147)
+       EPI_PHEAD = 8 };      // rshift(pile, -(we + ex + 16)) with no bias, then the race (:158-160)
 
 // Record of one position's intermediates (stream 0), written when the position equals *pos.
 struct Rec {
@@ -53,6 +60,11 @@ struct GemvArgs {
     i64* part_v; int* part_i; unsigned* counter;
     int* seq_w; const int* plen; int* pos_w; int* words; int* nwords;
     i64* rlogits;
+    // the Pythia machine: the norm this phase's gauge uses, the embed table, extra record slots
+    const int* ng; const i64* nb; int nge;     // gain (16 places), offset (2^-16), the gain's power of two
+    const short* ew; const int* ee;            // embed.w [vocab][768], embed.e [vocab]
+    i64* rg;                                   // record: the gauge's output row
+    i64* rout2;                                // record: EPI_PLAIN_EDGE's row after the edge (rout: before)
 };
 
 struct AttArgs {
@@ -64,9 +76,13 @@ struct AttArgs {
     const int* pos;     // position being written and read up to (inclusive)
     int ctx;
     Tables tb;
-    int* err;           // bit 0: a value left 32 bits
+    int* err;           // bit 0: a value left 32 bits; bit 1: a value the reference asserts on
     const int* rec_pos; i64* ratt;
+    // the Pythia machine: turns on the first rot dims of q and k, the scores' half-log2(head size)
+    const int* cosT; const int* sinT;   // [npos][rot / 2] at 2^-30
+    int rot; i64 half; i64 ehalf;       // ehalf = EXP2[(-half) & 0xFFFF]
 };
 
 // error bits in the device error word
 #define SM_ERR_V32 1
+#define SM_ERR_RANGE 2

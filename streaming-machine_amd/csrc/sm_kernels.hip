@@ -57,9 +57,19 @@ struct OpMax { SMD i64 operator()(i64 a, i64 b) const { return a > b ? a : b; } 
 // the row's loads, issued first: vector loads complete in order, so anything requested before them (plate
 // tiles from HBM) would have to arrive before the row could be used
 template <int NIN, int NT, int PRO>
-SMD void prologue_load(const GemvArgs& a, int tid, i64 (&v)[NIN / NT]) {
+SMD void prologue_load(const GemvArgs& a, int tid, i64 (&v)[NIN / NT], int (&gq)[NIN / NT], i64 (&bq)[NIN / NT]) {
     constexpr int PER = NIN / NT;
-    if (PRO == PRO_EMBED) {
+    if (PRO == PRO_PEMBED) {
+        const int p = *a.pos;
+        const i64 tok = a.seq[p];
+        const i64 es = -((i64)a.ee[tok] + 16);
+#pragma unroll
+        for (int m = 0; m < PER; m++) {
+            int i = tid + NT * m;
+            v[m] = rsh((i64)a.ew[tok * 768 + i], es);
+            if (blockIdx.x == 0) a.Rw[i] = v[m];
+        }
+    } else if (PRO == PRO_EMBED) {
         const int p = *a.pos;
         const i64 tok = a.seq[p];
 #pragma unroll
@@ -72,6 +82,76 @@ SMD void prologue_load(const GemvArgs& a, int tid, i64 (&v)[NIN / NT]) {
 #pragma unroll
         for (int m = 0; m < PER; m++) v[m] = a.X[tid + NT * m];
     }
+    if (PRO == PRO_PGAUGE || PRO == PRO_PEMBED) {
+#pragma unroll
+        for (int m = 0; m < PER; m++) { gq[m] = a.ng[tid + NT * m]; bq[m] = a.nb[tid + NT * m]; }
+    }
+}
+
+// Pythia's prologue (foundation0/pythia_base2.py:100-110, 113): the gauge of the stream row R with the norm's own
+// gain and offset, then that row's water level.  Three block reductions: R's OR, the sums S1, S2, the gauged
+// row's OR.  c g < 2^41 and EXP2 < 2^17, so c g EXP2[f] is exact in 64 bits as the reference's int64 path is.
+template <int NT>
+SMD void prologue_py(const GemvArgs& a, int tid, const i64 (&v)[768 / NT], const int (&gq)[768 / NT],
+                     const i64 (&bq)[768 / NT], short* xh_s, short* xl_s, int* red, i64& ex_o, bool rec) {
+    constexpr int PER = 768 / NT, NW = NT / 64;
+    const int lane = tid & 63, wave = tid >> 6;
+    u64 o = 0;
+#pragma unroll
+    for (int m = 0; m < PER; m++) o |= (u64)iabs64(v[m]);
+    unsigned olo = wave_or32((unsigned)o), ohi = wave_or32((unsigned)(o >> 32));
+    if (lane == 0) { red[2 * wave] = (int)olo; red[2 * wave + 1] = (int)ohi; }
+    __syncthreads();
+    u64 all = 0;
+#pragma unroll
+    for (int w = 0; w < NW; w++) all |= ((u64)(unsigned)red[2 * w + 1] << 32) | (unsigned)red[2 * w];
+    const int sh = water_shift((i64)all);
+    int xi[PER];
+    int s1 = 0;
+    i64 s2 = 0;
+#pragma unroll
+    for (int m = 0; m < PER; m++) {
+        xi[m] = (int)rsh(v[m], sh);
+        s1 += xi[m];
+        s2 += (i64)xi[m] * xi[m];
+    }
+    const int w1 = wave_add32(s1), w2h = wave_add32((int)(s2 >> 16)), w2l = wave_add32((int)(s2 & 0xFFFF));
+    if (lane == 0) { red[16 + 3 * wave] = w1; red[17 + 3 * wave] = w2h; red[18 + 3 * wave] = w2l; }
+    __syncthreads();
+    i64 S1 = 0, S2h = 0, S2l = 0;
+#pragma unroll
+    for (int w = 0; w < NW; w++) { S1 += red[16 + 3 * w]; S2h += red[17 + 3 * w]; S2l += red[18 + 3 * w]; }
+    i64 e2;
+    const i64 ls = pgauge_ls_pow(S1, (S2h << 16) + S2l, -16 + sh, a.tb, e2);
+    const i64 sg = wsub(16, wsub(wmul((i64)a.nge + 16, 65536), ls) >> 16);     // 16 - I of the gauge's power
+    i64 g[PER];
+    o = 0;
+#pragma unroll
+    for (int m = 0; m < PER; m++) {
+        const i64 c = 768 * (i64)xi[m] - S1;
+        g[m] = wadd(rsh(wmul(c * gq[m], e2), sg), bq[m]);
+        o |= (u64)iabs64(g[m]);
+        if (rec && a.rg) a.rg[tid + NT * m] = g[m];
+    }
+    olo = wave_or32((unsigned)o);
+    ohi = wave_or32((unsigned)(o >> 32));
+    if (lane == 0) { red[8 + 2 * wave] = (int)olo; red[9 + 2 * wave] = (int)ohi; }
+    __syncthreads();
+    all = 0;
+#pragma unroll
+    for (int w = 0; w < NW; w++) all |= ((u64)(unsigned)red[9 + 2 * w] << 32) | (unsigned)red[8 + 2 * w];
+    const int sh2 = water_shift((i64)all);
+#pragma unroll
+    for (int m = 0; m < PER; m++) {
+        const int i = tid + NT * m;
+        const int x16 = (int)rsh(g[m], sh2);
+        xh_s[i] = (short)(x16 >> 8);
+        xl_s[i] = (short)(x16 & 255);
+        if (rec && a.rx16) a.rx16[i] = x16;
+    }
+    if (rec && a.rexls && tid == 0) { a.rexls[0] = -16 + sh2; a.rexls[1] = 0; }
+    ex_o = -16 + sh2;
+    __syncthreads();
 }
 template <int NIN, int NT, int PRO>
 SMD void prologue(const GemvArgs& a, int tid, const i64 (&v)[NIN / NT], short* xh_s, short* xl_s, int* red, i64& ex_o,
@@ -169,13 +249,14 @@ __global__ __launch_bounds__(64 * WPB) void k_gemv(GemvArgs a) {
     const int col = lane - (16 - TC);                 // the column this lane finishes (valid when 0 <= col < TC)
     const bool fin = col >= 0 && col < TC;
 
+    constexpr bool HEAD = EPI == EPI_HEAD || EPI == EPI_PHEAD;
     bool skip = false;
     int p = 0;
-    if (EPI == EPI_HEAD) {
+    if (HEAD) {
         p = *a.pos;
         skip = p < *a.plen - 1;     // a prompt position whose next word is already known
     }
-    const bool rec = a.rec_pos && *a.rec_pos == (EPI == EPI_HEAD ? p : (a.pos ? *a.pos : -2));
+    const bool rec = a.rec_pos && *a.rec_pos == (HEAD ? p : (a.pos ? *a.pos : -2));
 
     i64 best_v = 0;
     int best_i = -1;
@@ -194,16 +275,20 @@ __global__ __launch_bounds__(64 * WPB) void k_gemv(GemvArgs a) {
                 int j = t * TC + col;
                 j = j < 0 ? 0 : (j < a.nout ? j : a.nout - 1);
                 we_ = a.we[j];
-                b_ = a.bias[j];
+                if (EPI != EPI_PHEAD) b_ = a.bias[j];
             }
             load_wtile<NIN, TC, U>(w, a.W, t, lane);
         };
         int tile = gw;
-        i64 row[NIN / NT];
-        prologue_load<NIN, NT, PRO>(a, tid, row);        // the row first, then this wave's first tile
+        i64 row[NIN / NT], nbq[NIN / NT];
+        int ngq[NIN / NT];
+        prologue_load<NIN, NT, PRO>(a, tid, row, ngq, nbq);   // the row first, then this wave's first tile
         fetch(wA, eA, bA, tile);                         // unconditional (clamped): no branch for the wait count to merge
-        i64 ex, ls, e2;
-        prologue<NIN, NT, PRO>(a, tid, row, xh_s, xl_s, red, ex, ls, e2, rec && blockIdx.x == 0);
+        i64 ex, ls = 0, e2 = 0;
+        if constexpr (PRO == PRO_PGAUGE || PRO == PRO_PEMBED)
+            prologue_py<NT>(a, tid, row, ngq, nbq, xh_s, xl_s, red, ex, rec && blockIdx.x == 0);
+        else
+            prologue<NIN, NT, PRO>(a, tid, row, xh_s, xl_s, red, ex, ls, e2, rec && blockIdx.x == 0);
         const i64 fe = wsub(0, ls) & 0xFFFF;          // the fine part of (we + ex + 16) 65536 - LS for every column
         auto finish = [&](const v4i (&w)[U], i64 wec, i64 bc, int t) {
             const i64 pile = wave_colsum64<TC>(wtile_partial<NIN, TC, U>(w, xh_s, xl_s, lane));
@@ -216,6 +301,20 @@ __global__ __launch_bounds__(64 * WPB) void k_gemv(GemvArgs a) {
                     const i64 r = wadd(a.Y[j], wadd(rsh(pile, -(wec + ex + 16)), bc));
                     a.Y[j] = r;
                     if (rec && a.rout) a.rout[j] = r;
+                } else if (EPI == EPI_PLAIN || EPI == EPI_PLAIN_EDGE || EPI == EPI_PHEAD) {
+                    i64 y = rsh(pile, -(wec + ex + 16));
+                    if (EPI != EPI_PHEAD) y = wadd(y, bc);
+                    if (EPI == EPI_PHEAD) {
+                        if (rec && a.rlogits) a.rlogits[j] = y;
+                        if (best_i < 0 || y > best_v) { best_v = y; best_i = j; }   // j grows: ties keep the first
+                    } else {
+                        if (rec && a.rout) a.rout[j] = y;
+                        if (EPI == EPI_PLAIN_EDGE) {
+                            y = edge1(y, a.tb);
+                            if (rec && a.rout2) a.rout2[j] = y;
+                        }
+                        a.Y[j] = y;
+                    }
                 } else {
                     i64 y = wadd(power_e(pile, wsub(wmul(wec + ex + 16, 65536), ls), fe, e2, a.tb), bc);
                     if (EPI == EPI_GAUGED_EDGE) y = edge1(y, a.tb);
@@ -240,7 +339,7 @@ __global__ __launch_bounds__(64 * WPB) void k_gemv(GemvArgs a) {
             tile = t2;
         }
     }
-    if (EPI != EPI_HEAD) return;
+    if (!HEAD) return;
 
     // ---- the race (base2.py:34-40, 114): largest logit, ties to the lowest word ----
     // wave: the TC finishing lanes; block: the waves; grid: the last block to arrive
@@ -309,7 +408,12 @@ __global__ __launch_bounds__(64 * WPB) void k_gemv(GemvArgs a) {
 // cached keys and values of the first 64 positions are requested at launch, before the new q, k, v arrive.
 // The maximum is global over the row before any arrival is read (two passes, scores in LDS), so the result is
 // exact for any context length.
+// MODEL 1 is the Pythia machine (foundation0/pythia_base2.py:125-141): per-head interleaved q, k, v at h 192;
+// the first rot dims of q and k turned by position before their water level; scores
+// power(q16 . k16, (eq + ek + 10) 65536 - half); the final power exact in 128 bits (the reference's power never
+// wraps, :81-85); its asserts (turn input < 2^31, max|v| sum(a) < 2^62, a result that fits) set SM_ERR_RANGE.
 #define ACH 64
+template <int MODEL>
 __global__ __launch_bounds__(NTHR) void k_attend(AttArgs a) {
     extern __shared__ __align__(16) unsigned char smem[];
     i64* sc = reinterpret_cast<i64*>(smem);                 // [ctx]
@@ -330,7 +434,7 @@ __global__ __launch_bounds__(NTHR) void k_attend(AttArgs a) {
     const bool rec = b == 0 && a.rec_pos && *a.rec_pos == p;
 
     // the new q, k, v first (vector loads complete in order), then the cached positions of the first pass
-    const i64 xnew = wave < 3 ? qkv[wave * 768 + h * 64 + lane] : 0;
+    i64 xnew = wave < 3 ? qkv[MODEL == 1 ? h * 192 + wave * 64 + lane : wave * 768 + h * 64 + lane] : 0;
     v4i kp[4], vp[4];
     int ekp = 0;
     if (sl < p) {
@@ -339,6 +443,16 @@ __global__ __launch_bounds__(NTHR) void k_attend(AttArgs a) {
 #pragma unroll
         for (int c = 0; c < 4; c++) { kp[c] = kr[c]; vp[c] = vr[c]; }
         ekp = EK[(size_t)sl * 12 + h];
+    }
+    if (MODEL == 1 && wave < 2) {        // the turns (pythia_base2.py:116-123): pair (i, i + rot/2)
+        const int r = a.rot >> 1;
+        const i64 partner = __shfl(xnew, lane < r ? lane + r : lane - r, 64);
+        if (lane < a.rot) {
+            if (iabs64(xnew) >= ((i64)1 << 31)) atomicOr(a.err, SM_ERR_RANGE);
+            const int i = lane < r ? lane : lane - r;
+            const i64 c = a.cosT[(size_t)p * r + i], sn = a.sinT[(size_t)p * r + i];
+            xnew = lane < r ? rsh(wsub(wmul(xnew, c), wmul(partner, sn)), 30) : rsh(wadd(wmul(xnew, c), wmul(partner, sn)), 30);
+        }
     }
     // the new position's own key and value are used from LDS: this block never reads back what it wrote
     if (wave < 2) {
@@ -393,7 +507,8 @@ __global__ __launch_bounds__(NTHR) void k_attend(AttArgs a) {
         dot += __shfl_xor(dot, 1, 64);
         dot += __shfl_xor(dot, 2, 64);
         if (s <= p) {
-            const i64 v = rsh(dot, -(eq + ek + 7));
+            const i64 v = MODEL == 1 ? rsh(wmul(dot, a.ehalf), wsub(16, wsub(wmul(eq + ek + 10, 65536), a.half) >> 16))
+                                     : rsh(dot, -(eq + ek + 7));
             if (qd == 0) sc[s] = v;
             mx = v > mx ? v : mx;
         }
@@ -405,6 +520,7 @@ __global__ __launch_bounds__(NTHR) void k_attend(AttArgs a) {
 #pragma unroll
     for (int i = 0; i < 16; i++) num[i] = 0;
     i64 z = 0;
+    int vmax = 0;                                   // Pythia: the largest |v| this lane weighs (the 2^62 assert)
     for (int s0 = 0; s0 <= p; s0 += ACH) {
         const int s = s0 + sl;
         if (s > p) continue;
@@ -425,10 +541,14 @@ __global__ __launch_bounds__(NTHR) void k_attend(AttArgs a) {
             for (int c = 0; c < 4; c++) {
                 num[4 * c] += (i64)w * vv[c].x; num[4 * c + 1] += (i64)w * vv[c].y;
                 num[4 * c + 2] += (i64)w * vv[c].z; num[4 * c + 3] += (i64)w * vv[c].w;
+                if (MODEL == 1) vmax = max(vmax, max(max(abs(vv[c].x), abs(vv[c].y)), max(abs(vv[c].z), abs(vv[c].w))));
             }
         } else {
 #pragma unroll
-            for (int i = 0; i < 16; i++) num[i] += (i64)w * vs[qd * 16 + i];
+            for (int i = 0; i < 16; i++) {
+                num[i] += (i64)w * vs[qd * 16 + i];
+                if (MODEL == 1) vmax = max(vmax, abs(vs[qd * 16 + i]));
+            }
         }
     }
     // sum over the 16 positions of each wave (lanes that share a quarter), then over the 4 waves
@@ -443,12 +563,23 @@ __global__ __launch_bounds__(NTHR) void k_attend(AttArgs a) {
         for (int i = 0; i < 16; i++) numr[wave][lane * 16 + i] = num[i];
     }
     z = block_reduce(z, red, OpAdd(), tid);   // its barriers also publish numr[]
+    if (MODEL == 1 && (double)vmax * (double)z >= 4611686018427387904.0) atomicOr(a.err, SM_ERR_RANGE);
     if (wave == 0) {
         const i64 tot = numr[0][lane] + numr[1][lane] + numr[2][lane] + numr[3][lane];
         int t; i64 m;
         log2_parts(z, t, m);
         const i64 F = wsub(0, wadd((i64)t * 65536, utab_log2(a.tb, (int)m)));   // -log2fix(Z), Z the same in every lane
-        const i64 o = power_e(tot, F, F & 0xFFFF, utab_hpow(a.tb, (int)m), a.tb);
+        i64 o;
+        if (MODEL == 1) {
+            // exact: (tot EXP2[f] + 2^(s-1)) >> s with s = 16 - (F >> 16) > 16 (Z >= 2^24)
+            const __int128 X = (__int128)tot * utab_hpow(a.tb, (int)m);
+            const i64 sft = 16 - (F >> 16);
+            const __int128 r = sft >= 100 ? (__int128)0 : (X + ((__int128)1 << (sft - 1))) >> sft;
+            if (r > (__int128)INT64_MAX || r < (__int128)INT64_MIN) atomicOr(a.err, SM_ERR_RANGE);
+            o = (i64)r;
+        } else {
+            o = power_e(tot, F, F & 0xFFFF, utab_hpow(a.tb, (int)m), a.tb);
+        }
         a.out[(size_t)b * 768 + h * 64 + lane] = o;
         if (rec) a.ratt[h * 64 + lane] = o;
     }
@@ -542,6 +673,12 @@ INST(768, 2, 2, PRO_TO16, EPI_PLAIN_ADD)      // proj
 INST(768, 2, 4, PRO_GAUGE, EPI_GAUGED_EDGE)   // fc
 INST(3072, 1, 4, PRO_TO16, EPI_PLAIN_ADD)     // mproj
 INST(768, 8, 4, PRO_GAUGE, EPI_HEAD)          // head + race
+INST(768, 2, 4, PRO_PEMBED, EPI_PLAIN)        // Pythia: qkv of layer 0
+INST(768, 2, 4, PRO_PGAUGE, EPI_PLAIN)        // Pythia: qkv
+INST(768, 2, 4, PRO_PGAUGE, EPI_PLAIN_EDGE)   // Pythia: fc
+INST(768, 8, 4, PRO_PGAUGE, EPI_PHEAD)        // Pythia: head + race
+template __global__ void k_attend<0>(AttArgs);
+template __global__ void k_attend<1>(AttArgs);
 // raw piles of a given light (stage entry point)
 INST(768, 2, 4, PRO_X16, EPI_PILE)
 INST(768, 8, 4, PRO_X16, EPI_PILE)

@@ -140,13 +140,13 @@ static void free_mfma_plate(MfmaPlate& P) {
 // tables
 struct sm_tables {
     int* LOG2 = nullptr; int* EXP2 = nullptr; int* PHI = nullptr; int* ARR = nullptr;
-    int* GPOW = nullptr; int* HPOW = nullptr;
+    int* GPOW = nullptr; int* HPOW = nullptr; int* PGPOW = nullptr;
     int alen = 0;
     i64 log768 = 0, eps40 = 0;
     int verified = 0;         // every entry equals its defining formula (checked on the device)
     int force_memory = 1;     // read the tables from memory (the default; the recomputed form is slower)
     int* scratch = nullptr;   // [0] pos for sm_stage_attend, [1] error bits, [4..7] mismatch counts
-    Tables tb() const { return Tables{LOG2, EXP2, PHI, ARR, alen, log768, eps40, verified && !force_memory, GPOW, HPOW}; }
+    Tables tb() const { return Tables{LOG2, EXP2, PHI, ARR, alen, log768, eps40, verified && !force_memory, GPOW, HPOW, PGPOW}; }
 };
 
 static int upload_table(int** dst, const i64* src, size_t n, i64 lo, i64 hi, const char* name) {
@@ -171,11 +171,15 @@ static int tables_init(sm_tables& T, const i64* phi, const i64* arr, int alen, c
     if ((rc = upload_table(&T.EXP2, exp2t, 65536, 65536, 131072, "exp2"))) return rc;
     // derived tables: exact integer compositions of LOG2 and EXP2 (see Tables in sm_device.h)
     {
-        std::vector<i64> g(2 * 65536), hp(65536);
+        std::vector<i64> g(2 * 65536), pg(2 * 65536), hp(65536);
         for (int r = 0; r < 2; r++)
-            for (int m = 0; m < 65536; m++) g[r * 65536 + m] = exp2t[(log768 - (((i64)r * 65536 + log2t[m]) >> 1)) & 0xFFFF];
+            for (int m = 0; m < 65536; m++) {
+                g[r * 65536 + m] = exp2t[(log768 - (((i64)r * 65536 + log2t[m]) >> 1)) & 0xFFFF];
+                pg[r * 65536 + m] = exp2t[(-(((i64)r * 65536 + log2t[m]) >> 1)) & 0xFFFF];
+            }
         for (int m = 0; m < 65536; m++) hp[m] = exp2t[(-log2t[m]) & 0xFFFF];
         if ((rc = upload_table(&T.GPOW, g.data(), g.size(), 65536, 131072, "gauge power")) ||
+            (rc = upload_table(&T.PGPOW, pg.data(), pg.size(), 65536, 131072, "Pythia gauge power")) ||
             (rc = upload_table(&T.HPOW, hp.data(), hp.size(), 65536, 131072, "arrival divisor")))
             return rc;
     }
@@ -193,7 +197,7 @@ static int tables_init(sm_tables& T, const i64* phi, const i64* arr, int alen, c
 }
 
 static void tables_free(sm_tables& T) {
-    hfree(T.LOG2); hfree(T.EXP2); hfree(T.PHI); hfree(T.ARR); hfree(T.GPOW); hfree(T.HPOW); hfree(T.scratch);
+    hfree(T.LOG2); hfree(T.EXP2); hfree(T.PHI); hfree(T.ARR); hfree(T.GPOW); hfree(T.HPOW); hfree(T.PGPOW); hfree(T.scratch);
     T = sm_tables();
 }
 
@@ -218,6 +222,14 @@ struct sm_machine {
     int* rowinfo = nullptr;        // [B][8]
     i64* wte = nullptr;
     i64* wpe = nullptr;
+    // the Pythia machine (kind 1, foundation0/pythia_base2.py): norms with their own gain and offset, the embed
+    // table with a power of two per word, the turns' cos / sin, the scores' half-log2(head size)
+    int kind = 0;
+    int* ng[12][2] = {};  i64* nb[12][2] = {};  int nge[12][2] = {};
+    int* fg = nullptr;    i64* fb = nullptr;    int fge = 0;
+    short* ew = nullptr;  int* ee = nullptr;
+    int* cosT = nullptr;  int* sinT = nullptr;  int rot = 0;
+    i64 half = 0, ehalf = 0;
     sm_tables T;
     // state
     i64 *R = nullptr, *QKV = nullptr, *att = nullptr, *hid = nullptr;
@@ -230,6 +242,7 @@ struct sm_machine {
     // record
     i64 *r_x16 = nullptr, *r_exls = nullptr, *r_pile = nullptr, *r_qkv = nullptr, *r_att = nullptr, *r_hid = nullptr,
         *r_resid = nullptr, *r_hx16 = nullptr, *r_hexls = nullptr, *r_hpile = nullptr, *r_logits = nullptr;
+    i64 *r_gauge = nullptr, *r_fcpre = nullptr, *r_hgauge = nullptr;   // Pythia: gauges [L][2][768], fc before the edge
     // captured decode steps: [0] graph_steps whole steps, [1] one whole step, [2] one step's layers, [3] its head
     hipGraphExec_t gexec[4] = {nullptr, nullptr, nullptr, nullptr};
     hipGraph_t graph[4] = {nullptr, nullptr, nullptr, nullptr};
@@ -305,6 +318,27 @@ static int parse_manifest(const std::string& text, std::vector<BankInfo>& banks,
     return SM_OK;
 }
 
+// "norms": [{"name": "ln1.0", "ge": -14}, ...] (the Pythia layout)
+static int parse_norms(const std::string& text, std::vector<std::pair<std::string, long long>>& norms) {
+    size_t b = text.find("\"norms\"");
+    if (b == std::string::npos) return fail(SM_E_IO, "manifest.json: no norms");
+    size_t lb = text.find('[', b), rb = text.find(']', b);
+    if (lb == std::string::npos || rb == std::string::npos) return fail(SM_E_IO, "manifest.json: malformed norms");
+    for (size_t cur = lb;;) {
+        size_t ob = text.find('{', cur);
+        if (ob == std::string::npos || ob > rb) break;
+        size_t cb = text.find('}', ob);
+        std::string obj = text.substr(ob, cb - ob + 1);
+        size_t nk = obj.find("\"name\"");
+        long long ge;
+        if (nk == std::string::npos || !json_int(obj, 0, "ge", ge)) return fail(SM_E_IO, "manifest.json: malformed norm");
+        size_t q1 = obj.find('"', obj.find(':', nk) + 1), q2 = obj.find('"', q1 + 1);
+        norms.emplace_back(obj.substr(q1 + 1, q2 - q1 - 1), ge);
+        cur = cb + 1;
+    }
+    return SM_OK;
+}
+
 static void machine_free(sm_machine* m) {
     if (!m) return;
     for (int i = 0; i < 4; i++) {
@@ -320,8 +354,11 @@ static void machine_free(sm_machine* m) {
     tables_free(m->T);
     void* ps[] = {m->planes, m->part_acc, m->rowinfo, m->wte, m->wpe, m->R, m->QKV, m->att, m->hid, m->K16, m->EK, m->V, m->seq, m->words, m->ctl,
                   m->part_v, m->part_i, m->r_x16, m->r_exls, m->r_pile, m->r_qkv, m->r_att, m->r_hid, m->r_resid,
-                  m->r_hx16, m->r_hexls, m->r_hpile, m->r_logits};
+                  m->r_hx16, m->r_hexls, m->r_hpile, m->r_logits, m->r_gauge, m->r_fcpre, m->r_hgauge,
+                  m->fg, m->fb, m->ew, m->ee, m->cosT, m->sinT};
     for (void* p : ps) hfree(p);
+    for (int l = 0; l < 12; l++)
+        for (int j = 0; j < 2; j++) { hfree(m->ng[l][j]); hfree(m->nb[l][j]); }
     if (m->st) (void)hipStreamDestroy(m->st);
     delete m;
 }
@@ -380,7 +417,7 @@ static int launch_step_batched(sm_machine* m, int parts, hipEvent_t hs, hipEvent
             a.QKV = m->QKV; a.K16 = m->K16 + l * per * 768; a.EK = m->EK + l * per * 12; a.V = m->V + l * per * 768;
             a.out = m->att; a.pos = ctl + CTL_POS; a.ctx = m->ctx; a.tb = tb; a.err = ctl + CTL_ERR;
             a.rec_pos = ctl + CTL_RECPOS; a.ratt = m->r_att + l * 768;
-            k_attend<<<dim3(12, m->B), NTHR, (size_t)m->ctx * 8, m->st>>>(a);
+            k_attend<0><<<dim3(12, m->B), NTHR, (size_t)m->ctx * 8, m->st>>>(a);
         }
         {
             LightArgs a = light_args(768, m->att, rx + 3072, re + 2);
@@ -421,7 +458,93 @@ static int launch_step_batched(sm_machine* m, int parts, hipEvent_t hs, hipEvent
     return SM_OK;
 }
 
+// The Pythia machine at batch 1 (foundation0/pythia_base2.py:153-160), five phases a layer.  Both gauges read
+// the stream before either half adds to it (the parallel residual R + At + Mo, :155-157): qkv and fc first.
+static int launch_step_pythia(sm_machine* m, int parts, hipEvent_t hs, hipEvent_t he) {
+    const Tables tb = m->T.tb();
+    int* ctl = m->ctl;
+    for (int l = 0; l < 12 && (parts & STEP_LAYERS); l++) {
+        GemvArgs base{};
+        base.tb = tb;
+        base.pos = ctl + CTL_POS;
+        base.rec_pos = ctl + CTL_RECPOS;
+        auto plate = [&](GemvArgs& a, const DevPlate& P, int k) {
+            a.W = reinterpret_cast<const int4*>(P.W); a.we = P.e; a.bias = P.b; a.nout = P.nout; a.ntiles = P.ntiles;
+            a.rx16 = m->r_x16 + (l * 4 + k) * 3072; a.rexls = m->r_exls + (l * 4 + k) * 2;
+            a.rpile = m->r_pile + (l * 4 + k) * 3072;
+        };
+        // qkv: gauge ln1 of R (the word enters at layer 0), plain (:113, 130)
+        {
+            GemvArgs a = base;
+            const DevPlate& P = m->bank[l][0];
+            plate(a, P, 0);
+            a.X = m->R; a.Y = m->QKV; a.rout = m->r_qkv + l * 2304; a.rg = m->r_gauge + (l * 2 + 0) * 768;
+            a.ng = m->ng[l][0]; a.nb = m->nb[l][0]; a.nge = m->nge[l][0];
+            a.ew = m->ew; a.ee = m->ee; a.seq = m->seq; a.Rw = m->R;
+            const int g = (P.ntiles + 3) / 4;
+            if (l == 0) k_gemv<768, 2, 4, PRO_PEMBED, EPI_PLAIN><<<g, 256, 0, m->st>>>(a);
+            else k_gemv<768, 2, 4, PRO_PGAUGE, EPI_PLAIN><<<g, 256, 0, m->st>>>(a);
+        }
+        // fc: gauge ln2 of the same R, plain, edge (:156)
+        {
+            GemvArgs a = base;
+            const DevPlate& P = m->bank[l][2];
+            plate(a, P, 2);
+            a.X = m->R; a.Y = m->hid; a.rout = m->r_fcpre + l * 3072; a.rout2 = m->r_hid + l * 3072;
+            a.rg = m->r_gauge + (l * 2 + 1) * 768;
+            a.ng = m->ng[l][1]; a.nb = m->nb[l][1]; a.nge = m->nge[l][1];
+            k_gemv<768, 2, 4, PRO_PGAUGE, EPI_PLAIN_EDGE><<<(P.ntiles + 3) / 4, 256, 0, m->st>>>(a);
+        }
+        // attention with turns (:125-141)
+        {
+            AttArgs a{};
+            const size_t per = (size_t)m->B * m->ctx;
+            a.QKV = m->QKV; a.K16 = m->K16 + l * per * 768; a.EK = m->EK + l * per * 12; a.V = m->V + l * per * 768;
+            a.out = m->att; a.pos = ctl + CTL_POS; a.ctx = m->ctx; a.tb = tb; a.err = ctl + CTL_ERR;
+            a.rec_pos = ctl + CTL_RECPOS; a.ratt = m->r_att + l * 768;
+            a.cosT = m->cosT; a.sinT = m->sinT; a.rot = m->rot; a.half = m->half; a.ehalf = m->ehalf;
+            k_attend<1><<<dim3(12, m->B), NTHR, (size_t)m->ctx * 8, m->st>>>(a);
+        }
+        // proj: plain of the attention row, added to R (At)
+        {
+            GemvArgs a = base;
+            const DevPlate& P = m->bank[l][1];
+            plate(a, P, 1);
+            a.X = m->att; a.Y = m->R; a.rout = m->r_resid + (l * 2 + 0) * 768;
+            k_gemv<768, 2, 2, PRO_TO16, EPI_PLAIN_ADD><<<(P.ntiles + 1) / 2, 128, 0, m->st>>>(a);
+        }
+        // mproj: plain of the edge row, added to R (Mo)
+        {
+            GemvArgs a = base;
+            const DevPlate& P = m->bank[l][3];
+            plate(a, P, 3);
+            a.X = m->hid; a.Y = m->R; a.rout = m->r_resid + (l * 2 + 1) * 768;
+            k_gemv<3072, 1, 4, PRO_TO16, EPI_PLAIN_ADD><<<(P.ntiles + 3) / 4, 256, 0, m->st>>>(a);
+        }
+    }
+    // head: gauge lnf, plain with no bias, race (:158-160)
+    if (parts & STEP_HEAD) {
+        GemvArgs a{};
+        a.tb = tb;
+        a.pos = ctl + CTL_POS; a.rec_pos = ctl + CTL_RECPOS;
+        const DevPlate& P = m->head;
+        a.W = reinterpret_cast<const int4*>(P.W); a.we = P.e; a.bias = P.b; a.nout = P.nout; a.ntiles = P.ntiles;
+        a.X = m->R;
+        a.ng = m->fg; a.nb = m->fb; a.nge = m->fge; a.rg = m->r_hgauge;
+        a.rx16 = m->r_hx16; a.rexls = m->r_hexls; a.rpile = m->r_hpile; a.rlogits = m->r_logits;
+        a.part_v = m->part_v; a.part_i = m->part_i; a.counter = reinterpret_cast<unsigned*>(ctl + CTL_COUNTER);
+        a.seq_w = m->seq; a.plen = ctl + CTL_PLEN; a.pos_w = ctl + CTL_POS; a.words = m->words; a.nwords = ctl + CTL_NWORDS;
+        if (hs)
+            hipExtLaunchKernelGGL(k_gemv<768, 8, 4, PRO_PGAUGE, EPI_PHEAD>, dim3(m->head_grid), dim3(256), 0, m->st, hs, he, 0, a);
+        else
+            k_gemv<768, 8, 4, PRO_PGAUGE, EPI_PHEAD><<<m->head_grid, 256, 0, m->st>>>(a);
+    }
+    HIP_TRY(hipGetLastError());
+    return SM_OK;
+}
+
 static int launch_step(sm_machine* m, int parts = STEP_ALL, hipEvent_t hs = nullptr, hipEvent_t he = nullptr) {
+    if (m->kind == 1) return launch_step_pythia(m, parts, hs, he);
     if (m->B > 1) {
         const int RT = (m->B + 15) / 16;
         if (RT == 1) return launch_step_batched<1>(m, parts, hs, he);
@@ -456,7 +579,7 @@ static int launch_step(sm_machine* m, int parts = STEP_ALL, hipEvent_t hs = null
             a.QKV = m->QKV; a.K16 = m->K16 + l * per * 768; a.EK = m->EK + l * per * 12; a.V = m->V + l * per * 768;
             a.out = m->att; a.pos = ctl + CTL_POS; a.ctx = m->ctx; a.tb = tb; a.err = ctl + CTL_ERR;
             a.rec_pos = ctl + CTL_RECPOS; a.ratt = m->r_att + l * 768;
-            k_attend<<<dim3(12, m->B), NTHR, (size_t)m->ctx * 8, m->st>>>(a);
+            k_attend<0><<<dim3(12, m->B), NTHR, (size_t)m->ctx * 8, m->st>>>(a);
         }
         // proj: to16 of the attention row, product, plain shift + bias, added to R (base2.py:105)
         {
@@ -521,8 +644,18 @@ extern "C" int sm_create(const char* layout_dir, const sm_config* cfg, sm_machin
     if (!read_file(dir + "manifest.json", mj)) return fail(SM_E_IO, "cannot read " + dir + "manifest.json");
     std::vector<BankInfo> banks;
     long long log768, eps40, alen;
-    int rc = parse_manifest(std::string(mj.begin(), mj.end()), banks, log768, eps40, alen);
+    const std::string mtext(mj.begin(), mj.end());
+    int rc = parse_manifest(mtext, banks, log768, eps40, alen);
     if (rc) return rc;
+    const bool py = mtext.find("\"pythia\"") != std::string::npos;     // "kind": "pythia"
+    long long rot = 0, half = 0, hs = 64;
+    std::vector<std::pair<std::string, long long>> norms;
+    if (py) {
+        if (!json_int(mtext, 0, "rot", rot) || !json_int(mtext, 0, "half_log2_hs", half) || !json_int(mtext, 0, "hs", hs))
+            return fail(SM_E_IO, "manifest.json: Pythia constants missing");
+        if (hs != 64 || rot <= 0 || rot > 64 || rot % 2) return fail(SM_E_IO, "manifest.json: built for 12 heads of 64 and an even turned width");
+        if ((rc = parse_norms(mtext, norms))) return rc;
+    }
     auto find = [&](const std::string& n) -> const BankInfo* {
         for (auto& b : banks) if (b.name == n) return &b;
         return nullptr;
@@ -530,6 +663,8 @@ extern "C" int sm_create(const char* layout_dir, const sm_config* cfg, sm_machin
     sm_machine* m = new sm_machine();
     m->cfg = c;
     m->B = c.max_streams;
+    m->kind = py ? 1 : 0;
+    if (py && m->B > 1) { delete m; return fail(SM_E_ARG, "sm_create: the Pythia machine decodes one stream per machine"); }
     auto bail = [&](int code) { machine_free(m); return code; };
     {
         hipError_t e = hipStreamCreateWithFlags(&m->st, hipStreamNonBlocking);
@@ -554,14 +689,61 @@ extern "C" int sm_create(const char* layout_dir, const sm_config* cfg, sm_machin
     m->vocab = (int)hb->nout;
     {
         std::vector<int16_t> w; std::vector<int32_t> e; std::vector<i64> b;
-        if ((rc = read_array(dir + "head.wc", w, (size_t)768 * m->vocab)) || (rc = read_array(dir + "head.e", e, m->vocab)) ||
-            (rc = read_array(dir + "head.b", b, m->vocab)))
+        if ((rc = read_array(dir + "head.wc", w, (size_t)768 * m->vocab)) || (rc = read_array(dir + "head.e", e, m->vocab)))
             return bail(rc);
+        if (py) b.assign(m->vocab, 0);         // Pythia's head has no bias (foundation0/pythia_base2.py:159)
+        else if ((rc = read_array(dir + "head.b", b, m->vocab))) return bail(rc);
         if (m->B == 1 && (rc = upload_plate(m->head, w.data(), e.data(), b.data(), 768, m->vocab, 8))) return bail(rc);
         if (m->B > 1 && (rc = upload_mfma_plate(m->mhead, w.data(), e.data(), b.data(), 768, m->vocab))) return bail(rc);
     }
     // word and position tables
-    {
+    if (py) {
+        std::vector<int16_t> ew; std::vector<int32_t> ee; std::vector<i64> cs, sn;
+        if ((rc = read_array(dir + "embed.wc", ew, (size_t)m->vocab * 768)) || (rc = read_array(dir + "embed.e", ee, m->vocab)) ||
+            (rc = read_array(dir + "cos.bin", cs, (size_t)-1)) || (rc = read_array(dir + "sin.bin", sn, (size_t)-1)))
+            return bail(rc);
+        const size_t r2 = (size_t)rot / 2;
+        if (cs.empty() || cs.size() % r2 || sn.size() != cs.size()) return bail(fail(SM_E_IO, "cos.bin / sin.bin: not [positions][rot / 2]"));
+        m->npos = (int)(cs.size() / r2);
+        std::vector<int> c32(cs.size()), s32(sn.size());
+        for (size_t i = 0; i < cs.size(); i++) {
+            if (cs[i] < -(1 << 30) || cs[i] > (1 << 30) || sn[i] < -(1 << 30) || sn[i] > (1 << 30))
+                return bail(fail(SM_E_IO, "cos.bin / sin.bin: a value past 2^30"));
+            c32[i] = (int)cs[i]; s32[i] = (int)sn[i];
+        }
+        for (int v : ee) if (v < -80 || v > 40) return bail(fail(SM_E_IO, "embed.e: a power of two out of range"));
+        if ((rc = dalloc(&m->ew, ew.size())) || (rc = dalloc(&m->ee, ee.size())) || (rc = dalloc(&m->cosT, c32.size())) ||
+            (rc = dalloc(&m->sinT, s32.size())))
+            return bail(rc);
+        if (hipMemcpy(m->ew, ew.data(), ew.size() * 2, hipMemcpyHostToDevice) != hipSuccess ||
+            hipMemcpy(m->ee, ee.data(), ee.size() * 4, hipMemcpyHostToDevice) != hipSuccess ||
+            hipMemcpy(m->cosT, c32.data(), c32.size() * 4, hipMemcpyHostToDevice) != hipSuccess ||
+            hipMemcpy(m->sinT, s32.data(), s32.size() * 4, hipMemcpyHostToDevice) != hipSuccess)
+            return bail(fail(SM_E_HIP, "upload embed / turns"));
+        m->rot = (int)rot;
+        m->half = half;
+        // the norms: gain on 16 places, offset at 2^-16, one power of two each
+        auto norm = [&](const std::string& name, int*& g, i64*& b, int& ge) -> int {
+            long long gev = 0;
+            bool found = false;
+            for (auto& nv : norms) if (nv.first == name) { gev = nv.second; found = true; }
+            if (!found) return fail(SM_E_IO, "manifest.json: norm " + name + " missing");
+            std::vector<int32_t> gh; std::vector<i64> bh;
+            int r;
+            if ((r = read_array(dir + name + ".g", gh, 768)) || (r = read_array(dir + name + ".b", bh, 768))) return r;
+            for (int v : gh) if (v < -32767 || v > 32767) return fail(SM_E_IO, name + ".g: a gain past 16 places");
+            if (gev < -64 || gev > 16) return fail(SM_E_IO, name + ": gain power out of range");
+            if ((r = dalloc(&g, (size_t)768)) || (r = dalloc(&b, (size_t)768))) return r;
+            HIP_TRY(hipMemcpy(g, gh.data(), 768 * 4, hipMemcpyHostToDevice));
+            HIP_TRY(hipMemcpy(b, bh.data(), 768 * 8, hipMemcpyHostToDevice));
+            ge = (int)gev;
+            return SM_OK;
+        };
+        for (int l = 0; l < 12; l++)
+            for (int j = 0; j < 2; j++)
+                if ((rc = norm((j ? "ln2." : "ln1.") + std::to_string(l), m->ng[l][j], m->nb[l][j], m->nge[l][j]))) return bail(rc);
+        if ((rc = norm("lnf", m->fg, m->fb, m->fge))) return bail(rc);
+    } else {
         std::vector<i64> wte, wpe;
         if ((rc = read_array(dir + "wte.bin", wte, (size_t)m->vocab * 768)) || (rc = read_array(dir + "wpe.bin", wpe, (size_t)-1))) return bail(rc);
         if (wpe.size() % 768 || wpe.empty()) return bail(fail(SM_E_IO, "wpe.bin: not a whole number of 768-wide rows"));
@@ -578,6 +760,7 @@ extern "C" int sm_create(const char* layout_dir, const sm_config* cfg, sm_machin
             (rc = read_array(dir + "log2.bin", lg, 65536)) || (rc = read_array(dir + "exp2.bin", ep, 65536)))
             return bail(rc);
         if ((rc = tables_init(m->T, phi.data(), arr.data(), (int)alen, lg.data(), ep.data(), log768, eps40))) return bail(rc);
+        m->ehalf = ep[(-m->half) & 0xFFFF];
         m->T.force_memory = c.table_mode != 1;
     }
     m->ctx = c.max_ctx < m->npos ? c.max_ctx : m->npos;
@@ -596,7 +779,8 @@ extern "C" int sm_create(const char* layout_dir, const sm_config* cfg, sm_machin
         (rc = dalloc(&m->r_qkv, (size_t)12 * 2304)) || (rc = dalloc(&m->r_att, (size_t)12 * 768)) ||
         (rc = dalloc(&m->r_hid, (size_t)12 * 3072)) || (rc = dalloc(&m->r_resid, (size_t)12 * 2 * 768)) ||
         (rc = dalloc(&m->r_hx16, 768)) || (rc = dalloc(&m->r_hexls, 2)) || (rc = dalloc(&m->r_hpile, (size_t)m->vocab)) ||
-        (rc = dalloc(&m->r_logits, (size_t)m->vocab)))
+        (rc = dalloc(&m->r_logits, (size_t)m->vocab)) || (rc = dalloc(&m->r_gauge, (size_t)12 * 2 * 768)) ||
+        (rc = dalloc(&m->r_fcpre, (size_t)12 * 3072)) || (rc = dalloc(&m->r_hgauge, (size_t)768)))
         return bail(rc);
     if (hipMemset(m->planes, 0, (size_t)4 * 48 * 3 * 1024) != hipSuccess || hipMemset(m->rowinfo, 0, (size_t)m->B * 32) != hipSuccess)
         return bail(fail(SM_E_HIP, "hipMemset planes"));
@@ -738,6 +922,8 @@ extern "C" int sm_generate(sm_machine* m, int32_t n_words, int32_t* out) {
     m->h_words = target;
     if (ctl[CTL_POS] != m->h_pos) return fail(SM_E_STATE, "sm_generate: device position disagrees with the host");
     if (ctl[CTL_ERR] & SM_ERR_V32) return fail(SM_E_OVERFLOW, "sm_generate: an attention value left 32 bits (the V cache holds int32)");
+    if (ctl[CTL_ERR] & SM_ERR_RANGE)
+        return fail(SM_E_OVERFLOW, "sm_generate: a value passed a bound the reference asserts (turn input 2^31, attention sum 2^62)");
     for (int b = 0; b < m->B; b++)
         HIP_TRY(hipMemcpy(out + (size_t)b * n_words, m->words + (size_t)b * (m->ctx + 1) + (target - n_words), (size_t)n_words * 4,
                           hipMemcpyDeviceToHost));
@@ -776,12 +962,20 @@ extern "C" int sm_read(sm_machine* m, int32_t what, int32_t layer, int32_t strea
         case SM_READ_REC_HEXLS: src = m->r_hexls; need = 2 * 8; break;
         case SM_READ_REC_HPILE: src = m->r_hpile; need = (size_t)m->vocab * 8; break;
         case SM_READ_REC_LOGITS: src = m->r_logits; need = (size_t)m->vocab * 8; break;
+        case SM_READ_REC_GAUGE: src = m->r_gauge; need = 12 * 2 * 768 * 8; break;
+        case SM_READ_REC_FCPRE: src = m->r_fcpre; need = 12 * 3072 * 8; break;
+        case SM_READ_REC_HGAUGE: src = m->r_hgauge; need = 768 * 8; break;
         default: return fail(SM_E_ARG, "sm_read: unknown array");
     }
     if (bytes != need) return fail(SM_E_ARG, "sm_read: expected " + std::to_string(need) + " bytes");
     HIP_TRY(hipStreamSynchronize(m->st));
     HIP_TRY(hipMemcpy(dst, src, need, hipMemcpyDeviceToHost));
     return SM_OK;
+}
+
+extern "C" int sm_model_kind(const sm_machine* m) {
+    if (!m) return fail(SM_E_ARG, "sm_model_kind: null machine");
+    return m->kind;
 }
 
 extern "C" int sm_info(const sm_machine* m, int32_t* vocab, int32_t* max_ctx, int32_t* max_streams, int32_t* n_pos,
@@ -873,7 +1067,7 @@ extern "C" int sm_stage_attend(const sm_tables* t, const int64_t* qkv, int32_t* 
     AttArgs a{};
     a.QKV = (const i64*)qkv; a.K16 = k16; a.EK = ek; a.V = v; a.out = (i64*)out; a.pos = t->scratch; a.ctx = ctx;
     a.tb = t->tb(); a.err = t->scratch + 1;
-    k_attend<<<dim3(12, 1), NTHR, (size_t)ctx * 8, s>>>(a);
+    k_attend<0><<<dim3(12, 1), NTHR, (size_t)ctx * 8, s>>>(a);
     HIP_TRY(hipGetLastError());
     int err = 0;
     HIP_TRY(hipMemcpyAsync(&err, t->scratch + 1, 4, hipMemcpyDeviceToHost, s));

@@ -19,7 +19,7 @@ CODES = {SM_E_ARG: "SM_E_ARG", SM_E_IO: "SM_E_IO", SM_E_HIP: "SM_E_HIP", SM_E_OO
          SM_E_OVERFLOW: "SM_E_OVERFLOW", SM_E_STATE: "SM_E_STATE"}
 
 READ = dict(k16=1, ek=2, v=3, resid=4, seq=5, x16=10, exls=11, pile=12, qkv=13, att=14, hid=15, rresid=16,
-            hx16=17, hexls=18, hpile=19, logits=20)
+            hx16=17, hexls=18, hpile=19, logits=20, gauge=21, fcpre=22, hgauge=23)
 
 
 class SmError(RuntimeError):
@@ -56,6 +56,7 @@ def lib():
         L.sm_record_at.argtypes = [vp, i32]
         L.sm_read.argtypes = [vp, i32, i32, i32, i32, vp, ctypes.c_size_t]
         L.sm_info.argtypes = [vp, i32p, i32p, i32p, i32p, i32p]
+        L.sm_model_kind.argtypes = [vp]
         L.sm_tables_mode.argtypes = [vp, i32, i32p]
         L.sm_profile.argtypes = [vp, i64p, ctypes.POINTER(ctypes.c_double), i32]
         L.sm_tables_create.argtypes = [i64p, i64p, i32, i64p, i64p, i64, i64, ctypes.POINTER(vp)]
@@ -101,8 +102,8 @@ class Machine:
 
     def __init__(self, layout_dir: str, max_ctx: int = 1024, max_streams: int = 1, use_graph: bool = True,
                  head_grid: int = 0, graph_steps: int = 16, profile: bool = False, memory_tables: bool = True,
-                 gauge: str = "int", edge: str = "int", arrival: str = "int"):
-        for name, v in (("gauge", gauge), ("edge", edge), ("arrival", arrival)):
+                 gauge: str = "int", edge: str = "int", arrival: str = "int", turn: str = "int"):
+        for name, v in (("gauge", gauge), ("edge", edge), ("arrival", arrival), ("turn", turn)):
             if v != "int":
                 raise NotImplementedError(f"{name}={v}: the GPU machine runs the integer stages only")
         self.L = lib()
@@ -115,6 +116,9 @@ class Machine:
         check(self.L.sm_info(self.h, ctypes.byref(v), ctypes.byref(c), ctypes.byref(s), ctypes.byref(n), ctypes.byref(ar)))
         self.vocab, self.max_ctx, self.max_streams, self.n_pos = v.value, c.value, s.value, n.value
         self.arith_tables = bool(ar.value)
+        k = self.L.sm_model_kind(self.h)
+        check(min(k, 0))
+        self.kind = ("gpt2", "pythia")[k]
 
     def close(self):
         if getattr(self, "h", None):
@@ -166,7 +170,8 @@ class Machine:
                   "x16": ((12, 4, 3072), np.int64), "exls": ((12, 4, 2), np.int64), "pile": ((12, 4, 3072), np.int64),
                   "qkv": ((12, 2304), np.int64), "att": ((12, 768), np.int64), "hid": ((12, 3072), np.int64),
                   "rresid": ((12, 2, 768), np.int64), "hx16": ((768,), np.int64), "hexls": ((2,), np.int64),
-                  "hpile": ((self.vocab,), np.int64), "logits": ((self.vocab,), np.int64)}
+                  "hpile": ((self.vocab,), np.int64), "logits": ((self.vocab,), np.int64),
+                  "gauge": ((12, 2, 768), np.int64), "fcpre": ((12, 3072), np.int64), "hgauge": ((768,), np.int64)}
         shape, dt = shapes[name]
         out = np.zeros(shape, dtype=dt)
         check(self.L.sm_read(self.h, READ[name], layer, stream, pos, out.ctypes.data, out.nbytes))

@@ -16,11 +16,13 @@ As in convert.py, ceil(log2(mx / 32767)) is evaluated exactly through frexp.
 """
 from __future__ import annotations
 
+import json
 import math
+import os
 
 import numpy as np
 
-from .convert import ES, _ceil_log2, stream, tables
+from .convert import _ceil_log2, stream, tables
 
 PYTHIA_SHAPE = dict(n_layer=12, d=768, n_head=12, d_ff=3072, vocab=50304, n_ctx=2048, rotary_pct=0.25,
                     rotary_emb_base=10000, layer_norm_eps=1e-5)
@@ -134,3 +136,41 @@ def convert_pythia(sd: dict, cfg: dict) -> dict:
     for k, v in dict(d=d, L=L, heads=nh, hs=hs, rot=rot, vocab=cfg["vocab"]).items():
         out[k] = np.array(v)
     return out
+
+
+def pythia_layout(npz: dict, out_dir: str) -> str:
+    """Write a converted Pythia model as a device-image directory for the HIP library.  The reference runs this
+    machine on the CPU only and has no device format for it; this one extends base2_gpu.py's:
+
+      {qkv,proj,fc,mproj}.{l}.wc / .e / .b   int16 [nin][nout], int32 [nout], int64 [nout] (as base2_gpu.py)
+      head.wc / head.e                       int16 [768][vocab], int32 [vocab] (no bias)
+      embed.wc / embed.e                     int16 [vocab][768], int32 [vocab] (a power of two per word)
+      {ln1,ln2}.{l}.g / .b, lnf.g / .b       int32 [768] gain on 16 places, int64 [768] offset at 2^-16
+      phi.bin arrival.bin log2.bin exp2.bin cos.bin sin.bin   int64 (cos / sin [positions][rot / 2] at 2^-30)
+      manifest.json  {"kind": "pythia", "banks": [...], "norms": [{"name", "ge"}, ...], "hs", "rot",
+                      "half_log2_hs", "log2_768", "eps40", "arrival_len", "vocab"}
+    """
+    os.makedirs(out_dir, exist_ok=True)
+    L = int(npz["L"])
+    banks, norms = [], []
+    for name in [f"{b}.{l}" for l in range(L) for b in P_BANKS] + ["head"]:
+        w = np.ascontiguousarray(npz[name + ".w"]).astype(np.int16)
+        w.tofile(os.path.join(out_dir, f"{name}.wc"))
+        np.asarray(npz[name + ".e"]).astype(np.int32).tofile(os.path.join(out_dir, f"{name}.e"))
+        if name != "head":
+            np.asarray(npz[name + ".b"]).astype(np.int64).tofile(os.path.join(out_dir, f"{name}.b"))
+        banks.append(dict(name=name, nin=int(w.shape[0]), nout=int(w.shape[1])))
+    for name in [f"{n}.{l}" for l in range(L) for n in P_NORMS] + ["lnf"]:
+        np.asarray(npz[name + ".g"]).astype(np.int32).tofile(os.path.join(out_dir, f"{name}.g"))
+        np.asarray(npz[name + ".b"]).astype(np.int64).tofile(os.path.join(out_dir, f"{name}.b"))
+        norms.append(dict(name=name, ge=int(npz[name + ".ge"])))
+    np.ascontiguousarray(npz["embed.w"]).astype(np.int16).tofile(os.path.join(out_dir, "embed.wc"))
+    np.asarray(npz["embed.e"]).astype(np.int32).tofile(os.path.join(out_dir, "embed.e"))
+    for k in ("phi", "arrival", "log2", "exp2", "cos", "sin"):
+        np.ascontiguousarray(npz[k]).astype(np.int64).tofile(os.path.join(out_dir, f"{k}.bin"))
+    man = dict(kind="pythia", banks=banks, norms=norms, hs=int(npz["hs"]), rot=int(npz["rot"]),
+               half_log2_hs=int(npz["half_log2_hs"]), log2_768=round(math.log2(768) * 65536), eps40=int(npz["eps40"]),
+               arrival_len=int(len(npz["arrival"])), vocab=int(npz["vocab"]))
+    with open(os.path.join(out_dir, "manifest.json"), "w") as f:
+        json.dump(man, f)
+    return out_dir

@@ -74,6 +74,40 @@ def full_oracle(full_npz):
     return oracle.Oracle(full_npz)
 
 
+@pytest.fixture(scope="session")
+def pgolden():
+    with open(os.path.join(REPO, "tests", "golden", "pythia_golden.json")) as f:
+        return json.load(f)
+
+
+@pytest.fixture(scope="session")
+def py_small_npz(sm):
+    sd, cfg = sm.pythia.random_pythia(seed=5, vocab=1000)
+    return sm.pythia.convert_pythia(sd, cfg)
+
+
+@pytest.fixture(scope="session")
+def py_full_npz(sm):
+    sd, cfg = sm.pythia.random_pythia(seed=5, vocab=50304)
+    return sm.pythia.convert_pythia(sd, cfg)
+
+
+@pytest.fixture(scope="session")
+def py_small_dir(sm, py_small_npz, tmp_path_factory):
+    return sm.pythia.pythia_layout(py_small_npz, str(tmp_path_factory.mktemp("py_small_layout")))
+
+
+@pytest.fixture(scope="session")
+def py_full_dir(sm, py_full_npz, tmp_path_factory):
+    return sm.pythia.pythia_layout(py_full_npz, str(tmp_path_factory.mktemp("py_full_layout")))
+
+
+@pytest.fixture(scope="session")
+def py_small_oracle(py_small_npz):
+    from oracle.pythia import PythiaOracle
+    return PythiaOracle(py_small_npz)
+
+
 def golden_case(golden, name):
     for c in golden["cases"]:
         if c["name"] == name:

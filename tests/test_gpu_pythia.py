@@ -1,0 +1,122 @@
+"""GPU parity of the Pythia-shaped machine (foundation0/pythia_base2.py) through the C ABI: words, every recorded
+intermediate and the KV cache, bit-exact against the reference's golden vectors and the Pythia oracle."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from conftest import h64
+from test_oracle_pythia import run_case, small_cases
+
+pytestmark = pytest.mark.gpu
+
+BANKS = ("qkv", "proj", "fc", "mproj")
+NIN = (768, 768, 768, 3072)
+NOUT = (2304, 768, 3072, 768)
+
+
+def machine_record(m, stream0) -> dict:
+    """the device record of one position keyed like the golden fixture; stream0 is the row entering layer 0
+    (the device records the stream after each half layer, so out.proj.0 needs it)"""
+    x16, exls, pile = m.read("x16"), m.read("exls"), m.read("pile")
+    qkv, att, hid, rr = m.read("qkv"), m.read("att"), m.read("hid"), m.read("rresid")
+    gauge, fcpre = m.read("gauge"), m.read("fcpre")
+    out = {}
+    for l in range(12):
+        entering = stream0 if l == 0 else rr[l - 1, 1]
+        out[f"stream.{l}"] = h64(entering)
+        out[f"gauge.ln1.{l}"] = h64(gauge[l, 0])
+        out[f"gauge.ln2.{l}"] = h64(gauge[l, 1])
+        for k, b in enumerate(BANKS):
+            out[f"x16.{b}.{l}"] = h64(x16[l, k, :NIN[k]])
+            out[f"ex.{b}.{l}"] = int(exls[l, k, 0])
+            out[f"pile.{b}.{l}"] = h64(pile[l, k, :NOUT[k]])
+        out[f"out.qkv.{l}"] = h64(qkv[l])
+        out[f"out.proj.{l}"] = h64(rr[l, 0] - entering)           # the attention half's addition (int64 wraps)
+        out[f"out.fc.{l}"] = h64(fcpre[l])
+        out[f"out.mproj.{l}"] = h64(rr[l, 1] - rr[l, 0])
+        out[f"att.{l}"] = h64(att[l])
+        out[f"hid.{l}"] = h64(hid[l])
+    out["stream.final"] = h64(rr[11, 1])
+    out["gauge.lnf"] = h64(m.read("hgauge"))
+    out["x16.head"] = h64(m.read("hx16"))
+    out["ex.head"] = int(m.read("hexls")[0])
+    out["pile.head"] = h64(m.read("hpile"))
+    out["logits"] = h64(m.read("logits"))
+    return out
+
+
+def oracle_stream0(orc, case):
+    from oracle.pythia import new_record
+    s = orc.session(len(case["prompt"]) + len(case["words"]))
+    seq = case["prompt"] + case["words"]
+    rec = new_record(orc.vocab)
+    for i in range(len(seq) - 1):
+        s.step(seq[i], want_head=False, rec=rec if i == len(seq) - 2 else None)
+    return rec["stream"][0].copy()
+
+
+@pytest.mark.parametrize("use_graph", [True, False])
+def test_small_model_words_and_records(sm, py_small_dir, py_small_oracle, pgolden, use_graph):
+    m = sm.Machine(py_small_dir, max_ctx=64, use_graph=use_graph)
+    assert m.kind == "pythia"
+    for case in small_cases(pgolden):
+        last = case["records"]["last"]
+        m.reset()
+        m.record_at(last["position"])
+        m.prefill(case["prompt"])
+        assert [int(w) for w in m.generate(len(case["words"]))[0]] == case["words"], case["name"]
+        got = machine_record(m, oracle_stream0(py_small_oracle, case))
+        keys = [k for k in last if k in got]
+        assert len(keys) == 258
+        bad = [k for k in keys if got[k] != last[k]]
+        assert not bad, f"{case['name']}: {len(bad)} intermediates differ, first {sorted(bad)[:6]}"
+    m.close()
+
+
+def test_config5_golden_streams(sm, py_full_dir, pgolden):
+    """the two golden streams of the 160m-shaped workload: 64-word prompts, 4 words each"""
+    m = sm.Machine(py_full_dir, max_ctx=128)
+    for c in [c for c in pgolden["cases"] if c["model"] == "pythia_160m"]:
+        assert m.stream(c["prompt"], len(c["words"])) == c["words"], c["name"]
+    m.close()
+
+
+def test_kv_cache_matches_oracle(sm, py_small_dir, py_small_oracle):
+    m = sm.Machine(py_small_dir, max_ctx=64)
+    prompt = sm.prompt_ids(60, 6, 1000)
+    words = m.stream(prompt, 6)
+    s = py_small_oracle.session(32)
+    seq = prompt + words
+    ow = []
+    for i, t in enumerate(seq[:-1]):
+        w = s.step(t, want_head=i >= len(prompt) - 1)
+        if i >= len(prompt) - 1:
+            ow.append(w)
+    assert ow == words
+    for l in (0, 5, 11):
+        for p in (0, 3, len(seq) - 2):
+            k16, ek, v = s.read_kv(l, p)
+            assert np.array_equal(m.read("k16", l, 0, p), k16)
+            assert np.array_equal(m.read("ek", l, 0, p), ek)
+            assert np.array_equal(m.read("v", l, 0, p), v)
+    assert np.array_equal(m.read("resid"), s.resid())
+    m.close()
+
+
+def test_long_context_against_oracle(sm, py_small_dir, py_small_oracle):
+    """a 300-word prompt and 24 words: turns at positions past 256, context 324"""
+    m = sm.Machine(py_small_dir, max_ctx=400)
+    prompt = sm.prompt_ids(61, 300, 1000)
+    assert m.stream(prompt, 24) == py_small_oracle.generate(prompt, 24, 400)
+    m.close()
+
+
+@pytest.mark.parametrize("use_graph", [True, False])
+def test_profiled_machine(sm, py_small_dir, pgolden, use_graph):
+    c = small_cases(pgolden)[0]
+    m = sm.Machine(py_small_dir, max_ctx=64, profile=True, graph_steps=4, use_graph=use_graph)
+    assert m.stream(c["prompt"], len(c["words"])) == c["words"]
+    n, us = m.profile()
+    assert n == len(c["prompt"]) + len(c["words"]) - 1 and us > 0
+    m.close()

@@ -3,35 +3,13 @@ itself, plus negative controls that plant mistakes in the oracle's inputs and sh
 from __future__ import annotations
 
 import hashlib
-import json
-import os
 
 import numpy as np
 import pytest
 
-HERE = os.path.dirname(os.path.abspath(__file__))
-
 
 def h64(a) -> str:
     return hashlib.sha256(np.ascontiguousarray(np.asarray(a, dtype=np.int64)).tobytes()).hexdigest()
-
-
-@pytest.fixture(scope="session")
-def pgolden():
-    with open(os.path.join(HERE, "golden", "pythia_golden.json")) as f:
-        return json.load(f)
-
-
-@pytest.fixture(scope="session")
-def py_small_npz(sm):
-    sd, cfg = sm.pythia.random_pythia(seed=5, vocab=1000)
-    return sm.pythia.convert_pythia(sd, cfg)
-
-
-@pytest.fixture(scope="session")
-def py_small_oracle(py_small_npz):
-    from oracle.pythia import PythiaOracle
-    return PythiaOracle(py_small_npz)
 
 
 def record_hashes(rec) -> dict:
