@@ -286,6 +286,10 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs a) {
         if (rec && a.rpile) a.rpile[j] = pile;
         if (EPI == EPI_PILE) {
             a.Y[(size_t)row * a.ystride + j] = pile;
+        } else if (EPI == EPI_PLAIN) {                 // the Pythia machine's qkv (foundation0/pythia_base2.py:114)
+            const i64 y = wadd(rsh(pile, -(we + ex + 16)), bc);
+            a.Y[(size_t)row * a.ystride + j] = y;
+            if (rec && a.rout) a.rout[j] = y;
         } else {
             const i64 ls = (i64)(((u64)(unsigned)ri[2] << 32) | (unsigned)ri[1]);
             const i64 y = wadd(power_known(pile, wsub(wmul(we + ex + 16, 65536), ls), (i64)ri[3]), bc);
@@ -309,7 +313,7 @@ __global__ __launch_bounds__(256) void k_head_rows(GemmArgs a) {
     __shared__ int rinfo[64 * 8];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int p = a.pos ? *a.pos : 0;
-    if (EPI == EPI_HEAD && p < *a.plen - 1) return;
+    if ((EPI == EPI_HEAD || EPI == EPI_PHEAD) && p < *a.plen - 1) return;
     const int ntiles = (a.N + 15) >> 4, G = gridDim.x;
     const v4* Wg = reinterpret_cast<const v4*>(a.W) + tid;
     auto gfetch = [&](v4 (&r)[PER], int tile) {
@@ -355,7 +359,7 @@ __global__ __launch_bounds__(256) void k_head_rows(GemmArgs a) {
         const int j = tile * 16 + (lane & 15);
         if (j >= a.N) return;
         const i64 swh = a.csum[2 * j], swl = a.csum[2 * j + 1];
-        const i64 we = a.we[j], bc = a.bias[j];
+        const i64 we = a.we[j], bc = EPI == EPI_HEAD ? a.bias[j] : 0;
 #pragma unroll
         for (int q = 0; q < 4; q++) {
             const int row = 16 * t + 4 * (lane >> 4) + q;
@@ -369,7 +373,8 @@ __global__ __launch_bounds__(256) void k_head_rows(GemmArgs a) {
                 a.Y[(size_t)row * a.ystride + j] = pile;
             } else {
                 const i64 ls = (i64)(((u64)(unsigned)ri[2] << 32) | (unsigned)ri[1]);
-                const i64 y = wadd(power_known(pile, wsub(wmul(we + (i64)ri[0] + 16, 65536), ls), (i64)ri[3]), bc);
+                const i64 y = EPI == EPI_PHEAD ? rsh(pile, -(we + (i64)ri[0] + 16))       // Pythia: plain, no bias
+                                               : wadd(power_known(pile, wsub(wmul(we + (i64)ri[0] + 16, 65536), ls), (i64)ri[3]), bc);
                 if (rec && a.rlogits) a.rlogits[j] = y;
                 if (bi[q] < 0 || y > bv[q]) { bv[q] = y; bi[q] = j; }      // j grows with the tile
             }
@@ -390,7 +395,7 @@ __global__ __launch_bounds__(256) void k_head_rows(GemmArgs a) {
         compute(ws[1], tile);
         tile += G;
     }
-    if (EPI != EPI_HEAD || !live) return;
+    if ((EPI != EPI_HEAD && EPI != EPI_PHEAD) || !live) return;
 #pragma unroll
     for (int q = 0; q < 4; q++) {
         i64 v = bv[q];
@@ -406,6 +411,219 @@ __global__ __launch_bounds__(256) void k_head_rows(GemmArgs a) {
             a.part_v[(size_t)row * a.nblk + blockIdx.x] = v;
             a.part_i[(size_t)row * a.nblk + blockIdx.x] = i;
         }
+    }
+}
+
+// ---------------------------------------------------------------------------------------------------------
+// The Pythia machine, batched (foundation0/pythia_base2.py:100-160 for every stream).  One block per stream row.
+//
+// light_store<K>: a row of int64 values (thread t holds k = 4 g .. 4 g + 3 for g = t + 256 m) -> its water
+// level and the MFMA A planes (xh, xl', c) + the row facts {ex, 0, 0, 0, SXh, SXl, n32768}.
+template <int K>
+SMD void light_store(const i64 (&v)[(K / 4 + 255) / 256][4], int r, signed char* planes, int* rowinfo, int* red,
+                     bool rec, i64* rx16, i64* rexls) {
+    constexpr int NG = K / 4, GPT = (NG + 255) / 256, KS = K / 64;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    u64 o = 0;
+#pragma unroll
+    for (int m = 0; m < GPT; m++)
+#pragma unroll
+        for (int j = 0; j < 4; j++) o |= (u64)iabs64(v[m][j]);
+    const unsigned olo = wave_or32((unsigned)o), ohi = wave_or32((unsigned)(o >> 32));
+    if (lane == 0) { red[2 * wave] = (int)olo; red[2 * wave + 1] = (int)ohi; }
+    __syncthreads();
+    u64 all = 0;
+#pragma unroll
+    for (int w = 0; w < 4; w++) all |= ((u64)(unsigned)red[2 * w + 1] << 32) | (unsigned)red[2 * w];
+    const int sh = water_shift((i64)all);
+    int sxh = 0, sxl = 0, n32 = 0;
+    int* pl = reinterpret_cast<int*>(planes + (size_t)(r >> 4) * KS * 3 * 1024);
+#pragma unroll
+    for (int m = 0; m < GPT; m++) {
+        const int g = tid + 256 * m;
+        if (g >= NG) continue;
+        const int k = 4 * g;
+        unsigned ph = 0, pq = 0, pc = 0;
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const int x = (int)rsh(v[m][j], sh);
+            if (rec && rx16) rx16[k + j] = x;
+            const int c = x == 32768;
+            const int xc = x - c;
+            const int xh = xc >> 8, xl = (xc & 255) - 128;
+            sxh += xh; sxl += xl; n32 += c;
+            ph |= (unsigned)(xh & 255) << (8 * j);
+            pq |= (unsigned)(xl & 255) << (8 * j);
+            pc |= (unsigned)c << (8 * j);
+        }
+        const int s = k >> 6, kk = k & 63;
+        const size_t off = ((size_t)s * 3 * 1024 + (size_t)((r & 15) + 16 * (kk >> 4)) * 16 + (kk & 15)) / 4;
+        pl[off] = (int)ph;
+        pl[off + 256] = (int)pq;
+        pl[off + 512] = (int)pc;
+    }
+    const int w3 = wave_add32(sxh), w4 = wave_add32(sxl), w5 = wave_add32(n32);
+    if (lane == 0) { red[8 + 3 * wave] = w3; red[9 + 3 * wave] = w4; red[10 + 3 * wave] = w5; }
+    __syncthreads();
+    if (tid == 0) {
+        int SXh = 0, SXl = 0, N32 = 0;
+        for (int w = 0; w < 4; w++) { SXh += red[8 + 3 * w]; SXl += red[9 + 3 * w]; N32 += red[10 + 3 * w]; }
+        int* ri = rowinfo + (size_t)r * 8;
+        ri[0] = -16 + sh; ri[1] = 0; ri[2] = 0; ri[3] = 0; ri[4] = SXh; ri[5] = SXl; ri[6] = N32;
+        if (rec && rexls) { rexls[0] = -16 + sh; rexls[1] = 0; }
+    }
+    __syncthreads();                                // red is reused by the caller
+}
+
+struct PyRowArgs {
+    int rows;
+    i64* R;                                       // [rows][768] the stream
+    const short* ew; const int* ee; const int* seq; int seq_stride; const int* pos;   // the word enters
+    const int* ng1; const i64* nb1; int nge1;     // gauge 1 (ln1, or lnf at the top)
+    const int* ng2; const i64* nb2; int nge2;     // gauge 2 (ln2); null: one gauge only
+    signed char* planes1; int* rowinfo1;          // light of gauge 1 (PY_EDGE: of the edge row)
+    signed char* planes2; int* rowinfo2;          // light of gauge 2
+    // finished plain banks: A = proj (or fc for PY_EDGE), B = mproj
+    const int* partA; int ksA; int kinA; const int* rowinfoA; const int* csumA; const int* weA; const i64* biasA;
+    const int* partB; int ksB; int kinB; const int* rowinfoB; const int* csumB; const int* weB; const i64* biasB;
+    Tables tb;
+    const int* rec_pos;
+    i64* rg1; i64* rx1; i64* rex1; i64* rg2; i64* rx2; i64* rex2;   // the gauges and their lights
+    i64* rpileA; i64* routA; i64* rpileB; i64* routB;               // PY_ADD: stream after A, after A and B
+    i64* rpre;                                                       // PY_EDGE: fc's row before the edge
+};
+enum { PY_EMBED = 0, PY_ADD = 1, PY_EDGE = 2 };
+
+// plain(pile) of one bank for columns k .. k + 3 of row r, from its K-sliced partial accumulators (:112-114)
+SMD void plain4(const int* part, int ks, int rows, int N, int kin, const int* ri, const int* csum, const int* we,
+                const i64* bias, int r, int k, i64 (&pile)[4], i64 (&y)[4]) {
+    typedef int v4l __attribute__((ext_vector_type(4)));
+    v4l h = {0, 0, 0, 0}, mi = {0, 0, 0, 0}, lo = {0, 0, 0, 0};
+    for (int q = 0; q < ks; q++) {
+        const int* src = part + ((size_t)q * 3 * rows + r) * N + k;
+        h += *reinterpret_cast<const v4l*>(src);
+        mi += *reinterpret_cast<const v4l*>(src + (size_t)rows * N);
+        lo += *reinterpret_cast<const v4l*>(src + (size_t)2 * rows * N);
+    }
+    const v4l c0 = *reinterpret_cast<const v4l*>(csum + 2 * k), c1 = *reinterpret_cast<const v4l*>(csum + 2 * k + 4);
+    const v4l wv = *reinterpret_cast<const v4l*>(we + k);
+    const int sw[8] = {c0[0], c0[1], c0[2], c0[3], c1[0], c1[1], c1[2], c1[3]};
+    const i64 ex = ri[0], sxh = ri[4], sxl = ri[5], n32 = ri[6];
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        pile[j] = 65536 * (i64)h[j] + 256 * (i64)mi[j] + lo[j] + 32768 * (sxh + sw[2 * j]) + 128 * (sxl + sw[2 * j + 1]) +
+                  16384 * (i64)kin + 128 * n32;
+        y[j] = wadd(rsh(pile[j], -((i64)wv[j] + ex + 16)), bias[k + j]);
+    }
+}
+
+// One block per stream row.
+//   PY_EMBED: R = rshift(embed.w[word], -(embed.e[word] + 16)) (:153), then the two gauges' lights
+//   PY_ADD:   R += plain(proj) + plain(mproj) (:155-157), then the two gauges' lights (or lnf's alone)
+//   PY_EDGE:  edge(plain(fc)) (:156), then its light (K = 3072)
+// Both gauges share to16(R), S1, S2 and LS (:100-110); only the gain, its power and the offset differ.
+template <int MODE>
+__global__ __launch_bounds__(256) void k_py_rows(PyRowArgs a) {
+    __shared__ int red[32];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, r = blockIdx.x;
+    const int p = *a.pos;
+    const bool rec = r == 0 && a.rec_pos && *a.rec_pos == p;
+    if (MODE == PY_EDGE) {
+        i64 v[3][4];
+        const int* ri = a.rowinfoA + (size_t)r * 8;          // fc's light facts (this block's row only)
+#pragma unroll
+        for (int m = 0; m < 3; m++) {
+            const int k = 4 * (tid + 256 * m);
+            i64 pile[4], y[4];
+            plain4(a.partA, a.ksA, a.rows, 3072, a.kinA, ri, a.csumA, a.weA, a.biasA, r, k, pile, y);
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                if (rec && a.rpileA) a.rpileA[k + j] = pile[j];
+                if (rec && a.rpre) a.rpre[k + j] = y[j];
+                v[m][j] = edge1(y[j], a.tb);
+                if (rec && a.routA) a.routA[k + j] = v[m][j];
+            }
+        }
+        __syncthreads();                                    // every thread has read its rowinfo facts
+        light_store<3072>(v, r, a.planes1, a.rowinfo1, red, rec, a.rx1, a.rex1);
+        return;
+    }
+    // the stream row (192 threads hold four lanes each)
+    const bool act = tid < 192;
+    const int k = 4 * tid;
+    i64 R4[4] = {0, 0, 0, 0};
+    if (act) {
+        if (MODE == PY_EMBED) {
+            const i64 tok = a.seq[(size_t)r * a.seq_stride + p];
+            const i64 es = -((i64)a.ee[tok] + 16);
+#pragma unroll
+            for (int j = 0; j < 4; j++) R4[j] = rsh((i64)a.ew[tok * 768 + k + j], es);
+        } else {
+            i64 pA[4], yA[4], pB[4], yB[4];
+            plain4(a.partA, a.ksA, a.rows, 768, a.kinA, a.rowinfoA + (size_t)r * 8, a.csumA, a.weA, a.biasA, r, k, pA, yA);
+            plain4(a.partB, a.ksB, a.rows, 768, a.kinB, a.rowinfoB + (size_t)r * 8, a.csumB, a.weB, a.biasB, r, k, pB, yB);
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const i64 r0 = a.R[(size_t)r * 768 + k + j];
+                const i64 r1 = wadd(r0, yA[j]);
+                R4[j] = wadd(r1, yB[j]);
+                if (rec) {
+                    if (a.rpileA) a.rpileA[k + j] = pA[j];
+                    if (a.rpileB) a.rpileB[k + j] = pB[j];
+                    if (a.routA) a.routA[k + j] = r1;
+                    if (a.routB) a.routB[k + j] = R4[j];
+                }
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < 4; j++) a.R[(size_t)r * 768 + k + j] = R4[j];
+    }
+    // the gauge (:100-110): to16(R), S1, S2, LS, the power factor
+    u64 o = 0;
+#pragma unroll
+    for (int j = 0; j < 4; j++) o |= (u64)iabs64(R4[j]);
+    unsigned olo = wave_or32((unsigned)o), ohi = wave_or32((unsigned)(o >> 32));
+    if (lane == 0) { red[2 * wave] = (int)olo; red[2 * wave + 1] = (int)ohi; }
+    __syncthreads();
+    u64 all = 0;
+#pragma unroll
+    for (int w = 0; w < 4; w++) all |= ((u64)(unsigned)red[2 * w + 1] << 32) | (unsigned)red[2 * w];
+    const int sh = water_shift((i64)all);
+    int x[4];
+    int s1 = 0;
+    i64 s2 = 0;
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        x[j] = (int)rsh(R4[j], sh);
+        s1 += x[j];
+        s2 += (i64)x[j] * x[j];
+    }
+    const int w1 = wave_add32(s1), w2h = wave_add32((int)(s2 >> 16)), w2l = wave_add32((int)(s2 & 0xFFFF));
+    if (lane == 0) { red[16 + 3 * wave] = w1; red[17 + 3 * wave] = w2h; red[18 + 3 * wave] = w2l; }
+    __syncthreads();
+    i64 S1 = 0, S2h = 0, S2l = 0;
+#pragma unroll
+    for (int w = 0; w < 4; w++) { S1 += red[16 + 3 * w]; S2h += red[17 + 3 * w]; S2l += red[18 + 3 * w]; }
+    i64 e2;
+    const i64 ls = pgauge_ls_pow(S1, (S2h << 16) + S2l, -16 + sh, a.tb, e2);
+    __syncthreads();                                    // red is reused below
+    for (int gi = 0; gi < 2; gi++) {
+        const int* ng = gi ? a.ng2 : a.ng1;
+        if (!ng) break;
+        const i64* nb = gi ? a.nb2 : a.nb1;
+        const i64 sg = wsub(16, wsub(wmul((i64)(gi ? a.nge2 : a.nge1) + 16, 65536), ls) >> 16);
+        i64 v[1][4] = {{0, 0, 0, 0}};
+        if (act) {
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const i64 c = 768 * (i64)x[j] - S1;
+                v[0][j] = wadd(rsh(wmul(c * ng[k + j], e2), sg), nb[k + j]);
+                i64* rg = gi ? a.rg2 : a.rg1;
+                if (rec && rg) rg[k + j] = v[0][j];
+            }
+        }
+        light_store<768>(v, r, gi ? a.planes2 : a.planes1, gi ? a.rowinfo2 : a.rowinfo1, red, rec,
+                         gi ? a.rx2 : a.rx1, gi ? a.rex2 : a.rex1);
     }
 }
 
@@ -468,15 +686,18 @@ BINST_L(768, PRO_X16)
 BINST_L(3072, PRO_X16)
 BINST_L(768, PRO_ADD_GAUGE)
 BINST_L(3072, PRO_EDGE_TO16)
+template __global__ void k_py_rows<PY_EMBED>(PyRowArgs);
+template __global__ void k_py_rows<PY_ADD>(PyRowArgs);
+template __global__ void k_py_rows<PY_EDGE>(PyRowArgs);
 #define BINST_G(K, RT, KSPLIT, EPI) template __global__ void k_gemm<K, RT, KSPLIT, EPI>(GemmArgs);
 #define BINST_GR(RT) BINST_G(768, RT, 1, EPI_GAUGED) BINST_G(768, RT, 1, EPI_PART) BINST_G(3072, RT, 4, EPI_PART) \
-    BINST_G(768, RT, 1, EPI_PILE) BINST_G(3072, RT, 1, EPI_PILE)
+    BINST_G(768, RT, 1, EPI_PILE) BINST_G(3072, RT, 1, EPI_PILE) BINST_G(768, RT, 1, EPI_PLAIN)
 BINST_GR(1)
 BINST_GR(2)
 BINST_GR(3)
 BINST_GR(4)
 #define BINST_H(RT) template __global__ void k_head_rows<RT, EPI_HEAD>(GemmArgs); \
-    template __global__ void k_head_rows<RT, EPI_PILE>(GemmArgs);
+    template __global__ void k_head_rows<RT, EPI_PILE>(GemmArgs); template __global__ void k_head_rows<RT, EPI_PHEAD>(GemmArgs);
 BINST_H(1)
 BINST_H(2)
 BINST_H(3)

@@ -543,7 +543,132 @@ static int launch_step_pythia(sm_machine* m, int parts, hipEvent_t hs, hipEvent_
     return SM_OK;
 }
 
+// The Pythia machine, batched: eight launches a layer.  Light sets: A (ln1 -> qkv), B (ln2 -> fc), C (edge row
+// -> mproj, 3072 wide), D (attention row -> proj); partials: fc and mproj share region 0 (fc's are finished
+// before mproj writes), proj's follow mproj's.  The last row kernel of a layer adds both halves to the stream
+// (the parallel residual) and lights the next layer's two gauges, or the head's.
+template <int RT>
+static int launch_step_pythia_batched(sm_machine* m, int parts, hipEvent_t hs, hipEvent_t he) {
+    const Tables tb = m->T.tb();
+    int* ctl = m->ctl;
+    const int B = m->B;
+    const size_t PL = (size_t)4 * 48 * 3 * 1024;
+    signed char* pA = m->planes; signed char* pB = m->planes + PL; signed char* pC = m->planes + 2 * PL;
+    signed char* pD = m->planes + 3 * PL;
+    int* rA = m->rowinfo; int* rB = m->rowinfo + (size_t)B * 8; int* rC = m->rowinfo + (size_t)2 * B * 8;
+    int* rD = m->rowinfo + (size_t)3 * B * 8;
+    int* P0 = m->part_acc;
+    int* P3 = m->part_acc + (size_t)4 * 3 * B * 768;
+    auto gemm_args = [&](const MfmaPlate& P, signed char* planes, int* rowinfo) {
+        GemmArgs a{};
+        a.K = P.K; a.N = P.N; a.rows = B; a.RT = RT; a.W = P.W; a.csum = P.csum; a.we = P.e; a.bias = P.b;
+        a.planes = planes; a.rowinfo = rowinfo; a.tb = tb;
+        a.pos = ctl + CTL_POS; a.plen = ctl + CTL_PLEN; a.rec_pos = ctl + CTL_RECPOS;
+        return a;
+    };
+    auto rows_args = [&]() {
+        PyRowArgs a{};
+        a.rows = B; a.R = m->R; a.ew = m->ew; a.ee = m->ee; a.seq = m->seq; a.seq_stride = m->ctx + 1; a.pos = ctl + CTL_POS;
+        a.tb = tb; a.rec_pos = ctl + CTL_RECPOS;
+        return a;
+    };
+    auto gauges = [&](PyRowArgs& a, int l) {       // the two gauges of layer l (l == 12: lnf for the head)
+        a.planes1 = pA; a.rowinfo1 = rA; a.planes2 = pB; a.rowinfo2 = rB;
+        if (l < 12) {
+            a.ng1 = m->ng[l][0]; a.nb1 = m->nb[l][0]; a.nge1 = m->nge[l][0];
+            a.ng2 = m->ng[l][1]; a.nb2 = m->nb[l][1]; a.nge2 = m->nge[l][1];
+            a.rg1 = m->r_gauge + (l * 2 + 0) * 768; a.rx1 = m->r_x16 + (l * 4 + 0) * 3072; a.rex1 = m->r_exls + (l * 4 + 0) * 2;
+            a.rg2 = m->r_gauge + (l * 2 + 1) * 768; a.rx2 = m->r_x16 + (l * 4 + 2) * 3072; a.rex2 = m->r_exls + (l * 4 + 2) * 2;
+        } else {
+            a.ng1 = m->fg; a.nb1 = m->fb; a.nge1 = m->fge; a.ng2 = nullptr;
+            a.rg1 = m->r_hgauge; a.rx1 = m->r_hx16; a.rex1 = m->r_hexls;
+        }
+    };
+    for (int l = 0; l < 12 && (parts & STEP_LAYERS); l++) {
+        i64* rp = m->r_pile + (size_t)l * 4 * 3072;
+        if (l == 0) {
+            PyRowArgs a = rows_args();
+            gauges(a, 0);
+            k_py_rows<PY_EMBED><<<B, 256, 0, m->st>>>(a);
+        }
+        {   // qkv: plain, written
+            GemmArgs a = gemm_args(m->mbank[l][0], pA, rA);
+            a.Y = m->QKV; a.ystride = 2304; a.rpile = rp; a.rout = m->r_qkv + l * 2304;
+            k_gemm<768, RT, 1, EPI_PLAIN><<<m->mbank[l][0].ntiles, 256, 0, m->st>>>(a);
+        }
+        {   // fc: partials, then edge and the 3072-wide light
+            GemmArgs a = gemm_args(m->mbank[l][2], pB, rB);
+            a.part = P0;
+            k_gemm<768, RT, 1, EPI_PART><<<m->mbank[l][2].ntiles, 256, 0, m->st>>>(a);
+            PyRowArgs e = rows_args();
+            const MfmaPlate& F = m->mbank[l][2];
+            e.partA = P0; e.ksA = 1; e.kinA = 768; e.rowinfoA = rB; e.csumA = F.csum; e.weA = F.e; e.biasA = F.b;
+            e.planes1 = pC; e.rowinfo1 = rC;
+            e.rpileA = rp + 2 * 3072; e.rpre = m->r_fcpre + l * 3072; e.routA = m->r_hid + l * 3072;
+            e.rx1 = m->r_x16 + (l * 4 + 3) * 3072; e.rex1 = m->r_exls + (l * 4 + 3) * 2;
+            k_py_rows<PY_EDGE><<<B, 256, 0, m->st>>>(e);
+        }
+        {   // mproj: partials over four K slices
+            GemmArgs a = gemm_args(m->mbank[l][3], pC, rC);
+            a.part = P0;
+            k_gemm<3072, RT, 4, EPI_PART><<<m->mbank[l][3].ntiles * 4, 256, 0, m->st>>>(a);
+        }
+        {   // attention with turns
+            AttArgs a{};
+            const size_t per = (size_t)B * m->ctx;
+            a.QKV = m->QKV; a.K16 = m->K16 + l * per * 768; a.EK = m->EK + l * per * 12; a.V = m->V + l * per * 768;
+            a.out = m->att; a.pos = ctl + CTL_POS; a.ctx = m->ctx; a.tb = tb; a.err = ctl + CTL_ERR;
+            a.rec_pos = ctl + CTL_RECPOS; a.ratt = m->r_att + l * 768;
+            a.cosT = m->cosT; a.sinT = m->sinT; a.rot = m->rot; a.half = m->half; a.ehalf = m->ehalf;
+            k_attend<1><<<dim3(12, B), NTHR, (size_t)m->ctx * 8, m->st>>>(a);
+        }
+        {   // the attention row's light, then proj's partials
+            LightArgs a{};
+            a.K = 768; a.rows = B; a.X = m->att; a.pos = ctl + CTL_POS; a.plen = ctl + CTL_PLEN;
+            a.planes = pD; a.rowinfo = rD; a.tb = tb; a.rec_pos = ctl + CTL_RECPOS;
+            a.rx16 = m->r_x16 + (l * 4 + 1) * 3072; a.rexls = m->r_exls + (l * 4 + 1) * 2;
+            k_light<768, PRO_TO16><<<B, 256, 0, m->st>>>(a);
+            GemmArgs g = gemm_args(m->mbank[l][1], pD, rD);
+            g.part = P3;
+            k_gemm<768, RT, 1, EPI_PART><<<m->mbank[l][1].ntiles, 256, 0, m->st>>>(g);
+        }
+        {   // R += At + Mo, then the next gauges' lights
+            PyRowArgs a = rows_args();
+            const MfmaPlate& Pp = m->mbank[l][1];
+            const MfmaPlate& Pm = m->mbank[l][3];
+            a.partA = P3; a.ksA = 1; a.kinA = 768; a.rowinfoA = rD; a.csumA = Pp.csum; a.weA = Pp.e; a.biasA = Pp.b;
+            a.partB = P0; a.ksB = 4; a.kinB = 3072; a.rowinfoB = rC; a.csumB = Pm.csum; a.weB = Pm.e; a.biasB = Pm.b;
+            a.rpileA = rp + 3072; a.routA = m->r_resid + (l * 2 + 0) * 768;
+            a.rpileB = rp + 3 * 3072; a.routB = m->r_resid + (l * 2 + 1) * 768;
+            gauges(a, l + 1);
+            k_py_rows<PY_ADD><<<B, 256, 0, m->st>>>(a);
+        }
+    }
+    if (parts & STEP_HEAD) {
+        GemmArgs a = gemm_args(m->mhead, pA, rA);
+        a.rpile = m->r_hpile;
+        const int grid = head_rows_grid(m->mhead.ntiles);
+        a.part_v = m->part_v; a.part_i = m->part_i; a.nblk = grid; a.rlogits = m->r_logits;
+        if (hs) hipExtLaunchKernelGGL(k_head_rows<RT, EPI_PHEAD>, dim3(grid), dim3(256), 0, m->st, hs, he, 0, a);
+        else k_head_rows<RT, EPI_PHEAD><<<grid, 256, 0, m->st>>>(a);
+        RaceArgs r{};
+        r.part_v = m->part_v; r.part_i = m->part_i; r.nblk = grid; r.seq = m->seq; r.seq_stride = m->ctx + 1;
+        r.words = m->words; r.words_stride = m->ctx + 1; r.pos = ctl + CTL_POS; r.plen = ctl + CTL_PLEN;
+        r.nwords = ctl + CTL_NWORDS; r.counter = reinterpret_cast<unsigned*>(ctl + CTL_COUNTER);
+        k_race_rows<<<B, 256, 0, m->st>>>(r);
+    }
+    HIP_TRY(hipGetLastError());
+    return SM_OK;
+}
+
 static int launch_step(sm_machine* m, int parts = STEP_ALL, hipEvent_t hs = nullptr, hipEvent_t he = nullptr) {
+    if (m->kind == 1 && m->B > 1) {
+        const int RT = (m->B + 15) / 16;
+        if (RT == 1) return launch_step_pythia_batched<1>(m, parts, hs, he);
+        if (RT == 2) return launch_step_pythia_batched<2>(m, parts, hs, he);
+        if (RT == 3) return launch_step_pythia_batched<3>(m, parts, hs, he);
+        return launch_step_pythia_batched<4>(m, parts, hs, he);
+    }
     if (m->kind == 1) return launch_step_pythia(m, parts, hs, he);
     if (m->B > 1) {
         const int RT = (m->B + 15) / 16;
@@ -664,7 +789,7 @@ extern "C" int sm_create(const char* layout_dir, const sm_config* cfg, sm_machin
     m->cfg = c;
     m->B = c.max_streams;
     m->kind = py ? 1 : 0;
-    if (py && m->B > 1) { delete m; return fail(SM_E_ARG, "sm_create: the Pythia machine decodes one stream per machine"); }
+
     auto bail = [&](int code) { machine_free(m); return code; };
     {
         hipError_t e = hipStreamCreateWithFlags(&m->st, hipStreamNonBlocking);
@@ -768,12 +893,13 @@ extern "C" int sm_create(const char* layout_dir, const sm_config* cfg, sm_machin
     const size_t nparts = m->B == 1 ? (size_t)m->head_grid : (size_t)m->B * head_rows_grid((m->vocab + 15) / 16);
     // state
     const size_t B = m->B, ctx = m->ctx;
+    const size_t nsets = m->kind == 1 && m->B > 1 ? 4 : 1;      // light-plane sets (the batched Pythia machine keeps four)
     if ((rc = dalloc(&m->R, B * 768)) || (rc = dalloc(&m->QKV, B * 2304)) || (rc = dalloc(&m->att, B * 768)) ||
         (rc = dalloc(&m->hid, B * 3072)) || (rc = dalloc(&m->K16, 12 * B * ctx * 768)) || (rc = dalloc(&m->EK, 12 * B * ctx * 12)) ||
         (rc = dalloc(&m->V, 12 * B * ctx * 768)) || (rc = dalloc(&m->seq, B * (ctx + 1))) || (rc = dalloc(&m->words, B * (ctx + 1))) ||
         (rc = dalloc(&m->ctl, (size_t)CTL_N)) || (rc = dalloc(&m->part_v, nparts)) ||
         (rc = dalloc(&m->part_i, nparts)) || (rc = dalloc(&m->r_x16, (size_t)12 * 4 * 3072)) ||
-        (rc = dalloc(&m->planes, (size_t)4 * 48 * 3 * 1024)) || (rc = dalloc(&m->rowinfo, (size_t)m->B * 8)) ||
+        (rc = dalloc(&m->planes, (size_t)4 * 48 * 3 * 1024 * nsets)) || (rc = dalloc(&m->rowinfo, (size_t)m->B * 8 * nsets)) ||
         (rc = dalloc(&m->part_acc, m->B > 1 ? (size_t)4 * 3 * m->B * 3072 : (size_t)1)) ||
         (rc = dalloc(&m->r_exls, (size_t)12 * 4 * 2)) || (rc = dalloc(&m->r_pile, (size_t)12 * 4 * 3072)) ||
         (rc = dalloc(&m->r_qkv, (size_t)12 * 2304)) || (rc = dalloc(&m->r_att, (size_t)12 * 768)) ||
@@ -782,7 +908,7 @@ extern "C" int sm_create(const char* layout_dir, const sm_config* cfg, sm_machin
         (rc = dalloc(&m->r_logits, (size_t)m->vocab)) || (rc = dalloc(&m->r_gauge, (size_t)12 * 2 * 768)) ||
         (rc = dalloc(&m->r_fcpre, (size_t)12 * 3072)) || (rc = dalloc(&m->r_hgauge, (size_t)768)))
         return bail(rc);
-    if (hipMemset(m->planes, 0, (size_t)4 * 48 * 3 * 1024) != hipSuccess || hipMemset(m->rowinfo, 0, (size_t)m->B * 32) != hipSuccess)
+    if (hipMemset(m->planes, 0, (size_t)4 * 48 * 3 * 1024 * nsets) != hipSuccess || hipMemset(m->rowinfo, 0, (size_t)m->B * 32 * nsets) != hipSuccess)
         return bail(fail(SM_E_HIP, "hipMemset planes"));
     m->prompts.assign(B, {});
     m->gsteps = c.graph_steps > 0 ? c.graph_steps : 16;

@@ -120,3 +120,58 @@ def test_profiled_machine(sm, py_small_dir, pgolden, use_graph):
     n, us = m.profile()
     assert n == len(c["prompt"]) + len(c["words"]) - 1 and us > 0
     m.close()
+
+
+# ---- batched streams (int8 MFMA contraction, per-stream race) ----
+
+@pytest.mark.parametrize("B", [3, 20])
+def test_small_model_streams(sm, py_small_dir, py_small_oracle, B):
+    prompts = [sm.prompt_ids(80 + b, 8, 1000) for b in range(B)]
+    prompts[B - 1] = prompts[0]
+    m = sm.Machine(py_small_dir, max_ctx=64, max_streams=B)
+    got = m.streams(prompts, 10)
+    m.close()
+    assert got[B - 1] == got[0]
+    for b in range(B):
+        assert got[b] == py_small_oracle.generate(prompts[b], 10, 64), f"stream {b}"
+
+
+@pytest.mark.parametrize("use_graph", [True, False])
+def test_small_model_batched_record(sm, py_small_dir, py_small_oracle, pgolden, use_graph):
+    case = small_cases(pgolden)[0]
+    last = case["records"]["last"]
+    m = sm.Machine(py_small_dir, max_ctx=64, max_streams=5, use_graph=use_graph)
+    m.reset()
+    m.record_at(last["position"])
+    prompts = [case["prompt"]] + [sm.prompt_ids(90 + b, len(case["prompt"]), 1000) for b in range(4)]
+    for b, p in enumerate(prompts):
+        m.prefill(p, b)
+    assert [int(w) for w in m.generate(len(case["words"]))[0]] == case["words"]
+    got = machine_record(m, oracle_stream0(py_small_oracle, case))
+    bad = [k for k in last if k in got and got[k] != last[k]]
+    assert not bad, f"{len(bad)} intermediates differ, first {sorted(bad)[:6]}"
+    m.close()
+
+
+def test_config5_thirty_two_streams(sm, py_full_dir, py_full_npz, pgolden):
+    """32 streams of 64-word prompts: the two golden streams, a sample against the oracle, a late stream's cache"""
+    from oracle.pythia import PythiaOracle
+    cs = [c for c in pgolden["cases"] if c["model"] == "pythia_160m"]
+    prompts = [cs[0]["prompt"], cs[1]["prompt"]] + [sm.prompt_ids(500 + b, 64, 50304) for b in range(2, 32)]
+    m = sm.Machine(py_full_dir, max_ctx=96, max_streams=32)
+    got = m.streams(prompts, 4)
+    assert got[0] == cs[0]["words"] and got[1] == cs[1]["words"]
+    orc = PythiaOracle(py_full_npz)
+    for b in (13, 31):
+        assert got[b] == orc.generate(prompts[b], 4, 96), f"stream {b}"
+    s = orc.session(96)
+    seq = prompts[31] + got[31]
+    for t in seq[:-1]:
+        s.step(t, want_head=False)
+    for l in (0, 11):
+        for p in (0, 63, len(seq) - 2):
+            k16, ek, v = s.read_kv(l, p)
+            assert np.array_equal(m.read("k16", l, 31, p), k16)
+            assert np.array_equal(m.read("ek", l, 31, p), ek)
+            assert np.array_equal(m.read("v", l, 31, p), v)
+    m.close()
