@@ -5,12 +5,17 @@ from seed 0 converted to int16 plates with per-column powers of two; batch 1; an
 default_rng(1); 16 greedy words per sequence, i.e. the prompt pass plus 15 decode steps at context 9..23.
 A "step" is one decode position (one new word).  The timed region covers exactly --steps decode steps, in
 sequences of 15 (each sequence's prompt pass runs untimed first), with the weights, tables and KV cache resident
-in HBM.  Before any number is printed the emitted words are checked against the CPU oracle.
+in HBM.  Before any number is printed the emitted words are checked against the golden words that base2.py
+(and pythia_base2.py for the Pythia leg) gave for the same prompts (tests/golden, written by executing the
+reference itself); the CPU baseline's own words are checked against the GPU's.
 
 Printed: one JSON line with the driver's fields plus
   roofline      the head kernel (the largest single launch: the 768 x 50257 plate read + race), its mean
                 duration from HIP event pairs recorded around every head launch inside the timed region
   step_roofline the whole decode step's algorithmic bytes over its measured time
+  batched       the same machine with 64 streams in lockstep (int8 MFMA contraction), 32-token prompts,
+                128 words each (tokens/s over all streams)
+  pythia        the Pythia-160m-shaped machine with 32 streams, 64-token prompts, 256 words each
   cpu_baseline  base2.py's CPU path restated in numpy (full recompute per word, float64 products, the
                 top-down race loop), timed on a bounded sample of the same sequence on the host cores
 """
@@ -32,6 +37,7 @@ HBM_PEAK_GBS = 8000.0
 WORDS = 16          # words per sequence (the prompt pass gives the first)
 PROMPT = 8
 B_STREAMS, B_PROMPT, B_WORDS = 64, 32, 128     # the batched workload: 64 streams, 32-token prompts, 128 words
+P_STREAMS, P_PROMPT, P_WORDS = 32, 64, 256     # the Pythia-160m-shaped workload: 32 streams, 64-token prompts, 256 words
 
 
 def load_sm():
@@ -50,6 +56,12 @@ def log(msg):
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
+def golden_words(fname: str) -> dict:
+    """case name -> words, from the golden fixtures written by executing the reference itself"""
+    with open(os.path.join(REPO, "tests", "golden", fname)) as f:
+        return {c["name"]: c["words"] for c in json.load(f)["cases"]}
+
+
 def head_bytes(vocab: int) -> int:
     """algorithmic bytes of one head launch: the int16 plate plus an int32 exponent and an int64 bias per word"""
     return 2 * 768 * vocab + 12 * vocab
@@ -63,13 +75,15 @@ def step_bytes(vocab: int, ctx: float) -> float:
     return 12 * (layer_w + layer_cols) + head_bytes(vocab) + 12 * 768 * 8 * ctx
 
 
-def batched_leg(sm, orc, lay, check_streams=(0, 63)):
+def batched_leg(sm, lay):
     """64 independent streams decoded in lockstep (every bank an int8 MFMA contraction): one sequence of
     32-token prompts and 128 words per stream, KV cache up to 160.  Timed: the 127 decode steps after the
-    prompt pass; the head launches are timed with their own event pairs."""
+    prompt pass; the head launches are timed with their own event pairs.  Streams 0 and 1 begin with the golden
+    words base2.py gives for their prompts."""
     import torch
-    prompts = [sm.prompt_ids(1000 + b, B_PROMPT) for b in range(B_STREAMS)]
-    want = {b: orc.generate(prompts[b], B_WORDS, B_PROMPT + B_WORDS) for b in check_streams}
+    prompts = [sm.prompt_ids(4 + b, B_PROMPT) for b in range(B_STREAMS)]     # stream s: default_rng(4 + s)
+    gw = golden_words("base2_golden.json")
+    want = {b: gw[f"c4_stream{b}_p32_w4"] for b in (0, 1)}
     m = sm.Machine(lay, max_ctx=B_PROMPT + B_WORDS, max_streams=B_STREAMS, graph_steps=B_WORDS - 1, profile=True)
     res = None
     for it in range(2):                     # the first sequence warms up (graph instantiation)
@@ -85,9 +99,9 @@ def batched_leg(sm, orc, lay, check_streams=(0, 63)):
         dt = time.perf_counter() - t
         n, us = m.profile(clear=True)
         words = np.concatenate([first, rest], axis=1)
-        for b in check_streams:
-            if [int(w) for w in words[b]] != want[b]:
-                raise RuntimeError(f"batched stream {b}: GPU words differ from the oracle")
+        for b, w in want.items():
+            if [int(x) for x in words[b][:len(w)]] != w:
+                raise RuntimeError(f"batched stream {b}: GPU words differ from base2.py's golden words")
         res = (dt, n, us)
     m.close()
     dt, n, us = res
@@ -102,11 +116,68 @@ def batched_leg(sm, orc, lay, check_streams=(0, 63)):
     return {"streams": B_STREAMS, "value": round(B_STREAMS * steps / dt, 1), "unit": "tokens/s",
             "ms_per_step": round(ms, 4), "steps": steps,
             "workload": f"{B_STREAMS} streams, {B_PROMPT}-token random prompts, {B_WORDS} greedy words each "
-                        f"(context to {B_PROMPT + B_WORDS}); streams {list(check_streams)} checked against the oracle",
+                        f"(context to {B_PROMPT + B_WORDS}); streams 0 and 1 checked against base2.py's golden words",
             "roofline": {"bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                          "frac": round(ach / HBM_PEAK_GBS, 4), "kernel": "k_gemm<768,4,EPI_HEAD>",
                          "mean_launch_us": round(us, 3), "launches_timed": n,
                          "int8_tops": round(ops / (us * 1e-6) / 1e12, 1), "int8_frac": round(ops / (us * 1e-6) / 5.0e15, 4)},
+            "step_roofline": {"bytes_per_step": int(sb), "achieved": round(sb / (ms * 1e-3) / 1e9, 1),
+                              "frac": round(sb / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}}
+
+
+def pythia_leg(sm):
+    """The Pythia-160m-shaped machine (random N(0, 0.02) weights from default_rng(5), vocab 50304, rotary on a
+    quarter of each head, parallel residual): 32 streams decoded in lockstep, 64-token prompts (stream s:
+    default_rng(5 + s)), 256 greedy words each, context to 320.  Timed: the 255 decode steps after the prompt
+    pass.  Streams 0 and 1 begin with the golden words pythia_base2.py gives for their prompts."""
+    import torch
+    t0 = time.time()
+    sd, cfg = sm.pythia.random_pythia(seed=5)
+    npz = sm.pythia.convert_pythia(sd, cfg)
+    del sd
+    lay = tempfile.mkdtemp(prefix="sm_bench_py_")
+    sm.pythia.pythia_layout(npz, lay)
+    prompts = [sm.prompt_ids(5 + b, P_PROMPT, 50304) for b in range(P_STREAMS)]
+    gw = golden_words("pythia_golden.json")
+    want = {b: gw[f"py_c5_stream{b}_p64_w4"] for b in (0, 1)}
+    del npz
+    log(f"pythia: model converted and laid out in {time.time() - t0:.1f}s")
+    m = sm.Machine(lay, max_ctx=P_PROMPT + P_WORDS, max_streams=P_STREAMS, graph_steps=P_WORDS - 1, profile=True)
+    res = None
+    for it in range(2):                     # the first sequence warms up (graph instantiation)
+        m.reset()
+        for b, p in enumerate(prompts):
+            m.prefill(p, b)
+        first = m.generate(1)
+        torch.cuda.synchronize()
+        m.profile(clear=True)
+        t = time.perf_counter()
+        rest = m.generate(P_WORDS - 1)
+        torch.cuda.synchronize()
+        dt = time.perf_counter() - t
+        n, us = m.profile(clear=True)
+        words = np.concatenate([first, rest], axis=1)
+        for b, w in want.items():
+            if [int(x) for x in words[b][:len(w)]] != w:
+                raise RuntimeError(f"pythia stream {b}: GPU words differ from pythia_base2.py's golden words")
+        res = (dt, n, us)
+    vocab = m.vocab
+    m.close()
+    dt, n, us = res
+    steps = P_WORDS - 1
+    ms = 1000.0 * dt / steps
+    hb = head_bytes(vocab) - 8 * vocab                 # no bias on Pythia's head
+    ctx_mean = P_PROMPT + P_WORDS / 2.0
+    layer_w = 12 * (2 * (768 * 2304 + 768 * 768 + 768 * 3072 + 3072 * 768) + 12 * (2304 + 768 + 3072 + 768))
+    sb = layer_w + hb + P_STREAMS * 12 * 768 * 8 * ctx_mean
+    return {"streams": P_STREAMS, "value": round(P_STREAMS * steps / dt, 1), "unit": "tokens/s",
+            "ms_per_step": round(ms, 4), "steps": steps,
+            "workload": f"Pythia-160m-shaped integer machine, {P_STREAMS} streams, {P_PROMPT}-token random prompts, "
+                        f"{P_WORDS} greedy words each (context to {P_PROMPT + P_WORDS}); streams 0 and 1 checked "
+                        f"against pythia_base2.py's golden words",
+            "roofline": {"bound": "hbm", "achieved": round(hb / (us * 1e-6) / 1e9, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                         "frac": round(hb / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4), "kernel": "k_head_rows<2,EPI_PHEAD>",
+                         "mean_launch_us": round(us, 3), "launches_timed": n},
             "step_roofline": {"bytes_per_step": int(sb), "achieved": round(sb / (ms * 1e-3) / 1e9, 1),
                               "frac": round(sb / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}}
 
@@ -134,7 +205,7 @@ def cpu_baseline(npz, prompt, want, budget_s: float = 20.0):
         if t_total > budget_s and n >= 2:
             break
     if got != want[:len(got)]:
-        raise RuntimeError(f"cpu baseline words differ from the oracle: {got} vs {want[:len(got)]}")
+        raise RuntimeError(f"cpu baseline words differ from the GPU's: {got} vs {want[:len(got)]}")
     return {"value": n / t_total, "unit": "tokens/s", "cores": cores, "kind": "port",
             "sample": f"words 2..{n + 1} of the 8-token-prompt sequence, full recompute per word (context 9..{8 + n}), "
                       f"numpy float64-BLAS products and the top-down race loop"}
@@ -147,6 +218,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=15)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-batched", action="store_true", help="skip the 64-stream leg")
+    ap.add_argument("--no-pythia", action="store_true", help="skip the Pythia 32-stream leg")
     ap.add_argument("--head-grid", type=int, default=0)
     ap.add_argument("--layout", default="", help="reuse a layout directory (else one is built in a temp dir)")
     args = ap.parse_args()
@@ -158,9 +230,6 @@ def main():
         sys.exit("bench.py: --steps must be positive and --warmup non-negative")
 
     sm = load_sm()
-    sys.path.insert(0, REPO)
-    import oracle
-
     t0 = time.time()
     sd = sm.random_gpt2(seed=0)
     npz = sm.convert(sd)
@@ -171,10 +240,8 @@ def main():
     log(f"model converted and laid out in {time.time() - t0:.1f}s")
     prompt = sm.prompt_ids(1, PROMPT)
 
-    # the oracle's words for the sequence (parity gate)
-    orc = oracle.Oracle(npz)
-    want = orc.generate(prompt, WORDS)
-    log(f"oracle words: {want}")
+    # the parity gate: base2.py's own words for this sequence (golden fixture written from the reference)
+    want = golden_words("base2_golden.json")["c1_p8_w16"]
 
     import torch
     m = sm.Machine(lay, max_ctx=64, head_grid=args.head_grid, graph_steps=WORDS - 1, profile=True)
@@ -192,7 +259,7 @@ def main():
         dt = time.perf_counter() - t
         words = [first] + rest
         if words != want:
-            raise RuntimeError(f"GPU words differ from the oracle: {words} vs {want}")
+            raise RuntimeError(f"GPU words differ from base2.py's golden words: {words} vs {want}")
         n, us = m.profile(clear=True)
         return dt, n, us
 
@@ -223,9 +290,12 @@ def main():
                 traffic = int(float(line.split(":")[1]))
 
     m.close()
-    batched = None if args.no_batched else batched_leg(sm, orc, lay)
+    batched = None if args.no_batched else batched_leg(sm, lay)
     if batched:
         log(f"batched: {batched['value']} tokens/s, {batched['ms_per_step']} ms/step, head {batched['roofline']['mean_launch_us']} us")
+    pyleg = None if args.no_pythia else pythia_leg(sm)
+    if pyleg:
+        log(f"pythia: {pyleg['value']} tokens/s, {pyleg['ms_per_step']} ms/step, head {pyleg['roofline']['mean_launch_us']} us")
     cpu = None if args.no_cpu else cpu_baseline(npz, prompt, want)
     out = {
         "metric": METRIC, "value": round(tok_s, 2), "unit": "tokens/s", "n_gpus": 1, "steps": steps,
@@ -240,6 +310,7 @@ def main():
                      "bytes_per_launch": hb, "mean_launch_us": round(head_us, 3), "launches_timed": head_n},
         "step_roofline": {"bytes_per_step": int(sb), "achieved": round(step_ach, 1), "frac": round(step_ach / HBM_PEAK_GBS, 4)},
         "batched": batched,
+        "pythia": pyleg,
         "cpu_baseline": cpu,
     }
     print(json.dumps(out), flush=True)
