@@ -81,6 +81,9 @@ def batched_leg(sm, lay):
     prompt pass; the head launches are timed with their own event pairs.  Streams 0 and 1 begin with the golden
     words base2.py gives for their prompts."""
     import torch
+    if lay is None:
+        lay = tempfile.mkdtemp(prefix="sm_bench_")
+        sm.layout(sm.convert(sm.random_gpt2(seed=0)), lay)
     prompts = [sm.prompt_ids(4 + b, B_PROMPT) for b in range(B_STREAMS)]     # stream s: default_rng(4 + s)
     gw = golden_words("base2_golden.json")
     want = {b: gw[f"c4_stream{b}_p32_w4"] for b in (0, 1)}
@@ -220,6 +223,10 @@ def main():
     ap.add_argument("--no-batched", action="store_true", help="skip the 64-stream leg")
     ap.add_argument("--no-pythia", action="store_true", help="skip the Pythia 32-stream leg")
     ap.add_argument("--head-grid", type=int, default=0)
+    ap.add_argument("--only", choices=("b1", "b64", "pythia"), default="",
+                    help="profiling: run one leg and print only its result (not the bench line)")
+    ap.add_argument("--copy-probe", type=int, default=0, metavar="MB",
+                    help="profiling: first copy MB MiB device to device (calibrates HBM byte counters)")
     ap.add_argument("--layout", default="", help="reuse a layout directory (else one is built in a temp dir)")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -230,6 +237,20 @@ def main():
         sys.exit("bench.py: --steps must be positive and --warmup non-negative")
 
     sm = load_sm()
+    if args.copy_probe:
+        import torch
+        src = torch.ones(args.copy_probe << 18, dtype=torch.int32, device="cuda")
+        dst = torch.empty_like(src)
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        log(f"copy probe: {args.copy_probe} MiB device to device")
+        del src, dst
+    if args.only == "b64":
+        print(json.dumps(batched_leg(sm, None)), flush=True)
+        return
+    if args.only == "pythia":
+        print(json.dumps(pythia_leg(sm)), flush=True)
+        return
     t0 = time.time()
     sd = sm.random_gpt2(seed=0)
     npz = sm.convert(sd)
@@ -290,6 +311,9 @@ def main():
                 traffic = int(float(line.split(":")[1]))
 
     m.close()
+    if args.only == "b1":
+        print(json.dumps({"value": round(tok_s, 2), "ms_per_step": round(ms_per_step, 4), "head_us": round(head_us, 3)}), flush=True)
+        return
     batched = None if args.no_batched else batched_leg(sm, lay)
     if batched:
         log(f"batched: {batched['value']} tokens/s, {batched['ms_per_step']} ms/step, head {batched['roofline']['mean_launch_us']} us")
