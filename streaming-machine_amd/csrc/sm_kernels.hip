@@ -116,11 +116,11 @@ SMD void prologue_py(const GemvArgs& a, int tid, const i64 (&v)[768 / NT], const
         s2 += (i64)xi[m] * xi[m];
     }
     const int w1 = wave_add32(s1), w2h = wave_add32((int)(s2 >> 16)), w2l = wave_add32((int)(s2 & 0xFFFF));
-    if (lane == 0) { red[16 + 3 * wave] = w1; red[17 + 3 * wave] = w2h; red[18 + 3 * wave] = w2l; }
+    if (lane == 0) { red[32 + 3 * wave] = w1; red[33 + 3 * wave] = w2h; red[34 + 3 * wave] = w2l; }
     __syncthreads();
     i64 S1 = 0, S2h = 0, S2l = 0;
 #pragma unroll
-    for (int w = 0; w < NW; w++) { S1 += red[16 + 3 * w]; S2h += red[17 + 3 * w]; S2l += red[18 + 3 * w]; }
+    for (int w = 0; w < NW; w++) { S1 += red[32 + 3 * w]; S2h += red[33 + 3 * w]; S2l += red[34 + 3 * w]; }
     i64 e2;
     const i64 ls = pgauge_ls_pow(S1, (S2h << 16) + S2l, -16 + sh, a.tb, e2);
     const i64 sg = wsub(16, wsub(wmul((i64)a.nge + 16, 65536), ls) >> 16);     // 16 - I of the gauge's power
@@ -135,11 +135,11 @@ SMD void prologue_py(const GemvArgs& a, int tid, const i64 (&v)[768 / NT], const
     }
     olo = wave_or32((unsigned)o);
     ohi = wave_or32((unsigned)(o >> 32));
-    if (lane == 0) { red[8 + 2 * wave] = (int)olo; red[9 + 2 * wave] = (int)ohi; }
+    if (lane == 0) { red[72 + 2 * wave] = (int)olo; red[73 + 2 * wave] = (int)ohi; }
     __syncthreads();
     all = 0;
 #pragma unroll
-    for (int w = 0; w < NW; w++) all |= ((u64)(unsigned)red[9 + 2 * w] << 32) | (unsigned)red[8 + 2 * w];
+    for (int w = 0; w < NW; w++) all |= ((u64)(unsigned)red[73 + 2 * w] << 32) | (unsigned)red[72 + 2 * w];
     const int sh2 = water_shift((i64)all);
 #pragma unroll
     for (int m = 0; m < PER; m++) {
@@ -187,11 +187,11 @@ SMD void prologue(const GemvArgs& a, int tid, const i64 (&v)[NIN / NT], short* x
     i64 ls = 0, e2 = 0;
     if (PRO == PRO_GAUGE || PRO == PRO_EMBED) {
         const int w1 = wave_add32(s1), w2h = wave_add32((int)(s2 >> 16)), w2l = wave_add32((int)(s2 & 0xFFFF));
-        if (lane == 0) { red[16 + 3 * wave] = w1; red[17 + 3 * wave] = w2h; red[18 + 3 * wave] = w2l; }
+        if (lane == 0) { red[32 + 3 * wave] = w1; red[33 + 3 * wave] = w2h; red[34 + 3 * wave] = w2l; }
         __syncthreads();
         i64 S1 = 0, S2h = 0, S2l = 0;
 #pragma unroll
-        for (int w = 0; w < NW; w++) { S1 += red[16 + 3 * w]; S2h += red[17 + 3 * w]; S2l += red[18 + 3 * w]; }
+        for (int w = 0; w < NW; w++) { S1 += red[32 + 3 * w]; S2h += red[33 + 3 * w]; S2l += red[34 + 3 * w]; }
         ls = gauge_ls_pow(S1, (S2h << 16) + S2l, ex, a.tb, e2);
     } else {
         __syncthreads();
@@ -240,11 +240,13 @@ SMD i64 wtile_partial(const v4i (&w)[U], const short* xh_s, const short* xl_s, i
 template <int NIN, int TC, int WPB, int PRO, int EPI>
 __global__ __launch_bounds__(64 * WPB) void k_gemv(GemvArgs a) {
     constexpr int NT = 64 * WPB, U = WaveTile<NIN, TC>::U;
+    static_assert(NIN % NT == 0, "the block's threads must split the light row evenly");
     __shared__ __align__(16) short xh_s[NIN];
     __shared__ __align__(16) short xl_s[NIN];
-    __shared__ int red[32];
+    __shared__ int red[96];        // prologue: OR words [0, 24), sums [32, 68), second OR [72, 96)
     __shared__ i64 bestv[WPB];
     __shared__ int besti[WPB];
+    static_assert(WPB <= 12, "the prologue's LDS slots hold at most 12 waves");
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int col = lane - (16 - TC);                 // the column this lane finishes (valid when 0 <= col < TC)
     const bool fin = col >= 0 && col < TC;
@@ -351,6 +353,16 @@ __global__ __launch_bounds__(64 * WPB) void k_gemv(GemvArgs a) {
     }
     if (lane == 16 - TC) { bestv[wave] = best_v; besti[wave] = best_i; }
     __syncthreads();
+    if (!a.counter) {       // the race finishes in its own kernel (k_race_rows): this block's best only
+        if (tid == 0 && !skip) {
+            i64 bv = 0; int bi = -1;
+            for (int w = 0; w < WPB; w++)
+                if (besti[w] >= 0 && (bi < 0 || bestv[w] > bv || (bestv[w] == bv && besti[w] < bi))) { bv = bestv[w]; bi = besti[w]; }
+            a.part_v[blockIdx.x] = bv;
+            a.part_i[blockIdx.x] = bi;
+        }
+        return;
+    }
     __shared__ int last;
     if (tid == 0) {
         i64 bv = 0; int bi = -1;
@@ -672,11 +684,11 @@ INST(768, 2, 4, PRO_GAUGE, EPI_GAUGED)        // qkv
 INST(768, 2, 2, PRO_TO16, EPI_PLAIN_ADD)      // proj
 INST(768, 2, 4, PRO_GAUGE, EPI_GAUGED_EDGE)   // fc
 INST(3072, 1, 4, PRO_TO16, EPI_PLAIN_ADD)     // mproj
-INST(768, 8, 4, PRO_GAUGE, EPI_HEAD)          // head + race
+INST(768, 8, 4, PRO_GAUGE, EPI_HEAD)          // head (the race in its own kernel)
 INST(768, 2, 4, PRO_PEMBED, EPI_PLAIN)        // Pythia: qkv of layer 0
 INST(768, 2, 4, PRO_PGAUGE, EPI_PLAIN)        // Pythia: qkv
 INST(768, 2, 4, PRO_PGAUGE, EPI_PLAIN_EDGE)   // Pythia: fc
-INST(768, 8, 4, PRO_PGAUGE, EPI_PHEAD)        // Pythia: head + race
+INST(768, 8, 4, PRO_PGAUGE, EPI_PHEAD)        // Pythia: head
 template __global__ void k_attend<0>(AttArgs);
 template __global__ void k_attend<1>(AttArgs);
 // raw piles of a given light (stage entry point)

@@ -458,6 +458,20 @@ static int launch_step_batched(sm_machine* m, int parts, hipEvent_t hs, hipEvent
     return SM_OK;
 }
 
+// the batch-1 head: four waves per block, one block per CU by default (measured: 256 blocks of 4 waves
+// 17.0 us; 512 blocks 19.2 us; 256 blocks of 12 waves 59 us, register-bound)
+#define HEAD_WPB 4
+
+// the race over the head's per-block bests, one block per stream; it also advances the position
+static void launch_race(sm_machine* m, int nblk) {
+    int* ctl = m->ctl;
+    RaceArgs r{};
+    r.part_v = m->part_v; r.part_i = m->part_i; r.nblk = nblk; r.seq = m->seq; r.seq_stride = m->ctx + 1;
+    r.words = m->words; r.words_stride = m->ctx + 1; r.pos = ctl + CTL_POS; r.plen = ctl + CTL_PLEN;
+    r.nwords = ctl + CTL_NWORDS; r.counter = reinterpret_cast<unsigned*>(ctl + CTL_COUNTER);
+    k_race_rows<<<m->B, 256, 0, m->st>>>(r);
+}
+
 // The Pythia machine at batch 1 (foundation0/pythia_base2.py:153-160), five phases a layer.  Both gauges read
 // the stream before either half adds to it (the parallel residual R + At + Mo, :155-157): qkv and fc first.
 static int launch_step_pythia(sm_machine* m, int parts, hipEvent_t hs, hipEvent_t he) {
@@ -532,12 +546,13 @@ static int launch_step_pythia(sm_machine* m, int parts, hipEvent_t hs, hipEvent_
         a.X = m->R;
         a.ng = m->fg; a.nb = m->fb; a.nge = m->fge; a.rg = m->r_hgauge;
         a.rx16 = m->r_hx16; a.rexls = m->r_hexls; a.rpile = m->r_hpile; a.rlogits = m->r_logits;
-        a.part_v = m->part_v; a.part_i = m->part_i; a.counter = reinterpret_cast<unsigned*>(ctl + CTL_COUNTER);
-        a.seq_w = m->seq; a.plen = ctl + CTL_PLEN; a.pos_w = ctl + CTL_POS; a.words = m->words; a.nwords = ctl + CTL_NWORDS;
+        a.part_v = m->part_v; a.part_i = m->part_i; a.counter = nullptr;
+        a.plen = ctl + CTL_PLEN;
         if (hs)
-            hipExtLaunchKernelGGL(k_gemv<768, 8, 4, PRO_PGAUGE, EPI_PHEAD>, dim3(m->head_grid), dim3(256), 0, m->st, hs, he, 0, a);
+            hipExtLaunchKernelGGL(k_gemv<768, 8, HEAD_WPB, PRO_PGAUGE, EPI_PHEAD>, dim3(m->head_grid), dim3(64 * HEAD_WPB), 0, m->st, hs, he, 0, a);
         else
-            k_gemv<768, 8, 4, PRO_PGAUGE, EPI_PHEAD><<<m->head_grid, 256, 0, m->st>>>(a);
+            k_gemv<768, 8, HEAD_WPB, PRO_PGAUGE, EPI_PHEAD><<<m->head_grid, 64 * HEAD_WPB, 0, m->st>>>(a);
+        launch_race(m, m->head_grid);
     }
     HIP_TRY(hipGetLastError());
     return SM_OK;
@@ -746,12 +761,13 @@ static int launch_step(sm_machine* m, int parts = STEP_ALL, hipEvent_t hs = null
         a.W = reinterpret_cast<const int4*>(P.W); a.we = P.e; a.bias = P.b; a.nout = P.nout; a.ntiles = P.ntiles;
         a.X = m->R;
         a.rx16 = m->r_hx16; a.rexls = m->r_hexls; a.rpile = m->r_hpile; a.rlogits = m->r_logits;
-        a.part_v = m->part_v; a.part_i = m->part_i; a.counter = reinterpret_cast<unsigned*>(ctl + CTL_COUNTER);
-        a.seq_w = m->seq; a.plen = ctl + CTL_PLEN; a.pos_w = ctl + CTL_POS; a.words = m->words; a.nwords = ctl + CTL_NWORDS;
+        a.part_v = m->part_v; a.part_i = m->part_i; a.counter = nullptr;     // the race runs in its own kernel
+        a.plen = ctl + CTL_PLEN;
         if (hs)   // timed: the event pair is stamped by this dispatch itself (the interval a kernel trace reports)
-            hipExtLaunchKernelGGL(k_gemv<768, 8, 4, PRO_GAUGE, EPI_HEAD>, dim3(m->head_grid), dim3(256), 0, m->st, hs, he, 0, a);
+            hipExtLaunchKernelGGL(k_gemv<768, 8, HEAD_WPB, PRO_GAUGE, EPI_HEAD>, dim3(m->head_grid), dim3(64 * HEAD_WPB), 0, m->st, hs, he, 0, a);
         else
-            k_gemv<768, 8, 4, PRO_GAUGE, EPI_HEAD><<<m->head_grid, 256, 0, m->st>>>(a);
+            k_gemv<768, 8, HEAD_WPB, PRO_GAUGE, EPI_HEAD><<<m->head_grid, 64 * HEAD_WPB, 0, m->st>>>(a);
+        launch_race(m, m->head_grid);
     }
     HIP_TRY(hipGetLastError());
     return SM_OK;
@@ -889,7 +905,7 @@ extern "C" int sm_create(const char* layout_dir, const sm_config* cfg, sm_machin
         m->T.force_memory = c.table_mode != 1;
     }
     m->ctx = c.max_ctx < m->npos ? c.max_ctx : m->npos;
-    m->head_grid = c.head_grid > 0 ? c.head_grid : 512;
+    m->head_grid = c.head_grid > 0 ? c.head_grid : 256;     // one block per CU (measured best)
     const size_t nparts = m->B == 1 ? (size_t)m->head_grid : (size_t)m->B * head_rows_grid((m->vocab + 15) / 16);
     // state
     const size_t B = m->B, ctx = m->ctx;
