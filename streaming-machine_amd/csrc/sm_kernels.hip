@@ -420,6 +420,111 @@ __global__ __launch_bounds__(64 * WPB) void k_gemv(GemvArgs a) {
 // cached keys and values of the first 64 positions are requested at launch, before the new q, k, v arrive.
 // The maximum is global over the row before any arrival is read (two passes, scores in LDS), so the result is
 // exact for any context length.
+// The short-context path (position p < 64, one stream): one wave does a head alone, with no LDS and no block
+// barrier.  Lane s < p holds cached key row s (prefetched at launch) and scores it against q, which every lane
+// reads through readlane; lane p is the new position (its score is a wave sum); the maximum and the arrival sum
+// are wave reductions; lane d accumulates output dimension d from its prefetched V column.  Same numbers as the
+// general path below (base2.py:93-99 / pythia_base2.py:129-141).
+template <int MODEL>
+SMD void attend_short(const AttArgs& a, int p, int h, int b) {
+    const int lane = threadIdx.x;
+    const i64* qkv = a.QKV + (size_t)b * 2304;
+    int* K16 = a.K16 + (size_t)b * a.ctx * 768;
+    int* EK = a.EK + (size_t)b * a.ctx * 12;
+    int* V = a.V + (size_t)b * a.ctx * 768;
+    const bool rec = b == 0 && a.rec_pos && *a.rec_pos == p;
+    // the new q, k, v first (loads complete in order), then the cached rows and columns
+    i64 qv = qkv[MODEL == 1 ? h * 192 + lane : h * 64 + lane];
+    i64 kv = qkv[MODEL == 1 ? h * 192 + 64 + lane : 768 + h * 64 + lane];
+    const i64 vv = qkv[MODEL == 1 ? h * 192 + 128 + lane : 1536 + h * 64 + lane];
+    v4i krow[16];
+    int ekl = 0;
+    {
+        const int sr = lane < p ? lane : 0;                  // every lane loads (row 0 stands in past p)
+        const v4i* kr = reinterpret_cast<const v4i*>(K16 + (size_t)sr * 768 + h * 64);
+#pragma unroll
+        for (int c = 0; c < 16; c++) krow[c] = kr[c];
+        ekl = EK[(size_t)sr * 12 + h];
+    }
+    int vcol[64];
+#pragma unroll
+    for (int s = 0; s < 64; s++) vcol[s] = V[(size_t)(s < p ? s : 0) * 768 + h * 64 + lane];
+    if (MODEL == 1) {                                        // the turns (pythia_base2.py:116-123)
+        const int r = a.rot >> 1;
+        const i64 pq = __shfl(qv, lane < r ? lane + r : lane - r, 64);
+        const i64 pk = __shfl(kv, lane < r ? lane + r : lane - r, 64);
+        if (lane < a.rot) {
+            if (iabs64(qv) >= ((i64)1 << 31) || iabs64(kv) >= ((i64)1 << 31)) atomicOr(a.err, SM_ERR_RANGE);
+            const int i = lane < r ? lane : lane - r;
+            const i64 c = a.cosT[(size_t)p * r + i], sn = a.sinT[(size_t)p * r + i];
+            qv = lane < r ? rsh(wsub(wmul(qv, c), wmul(pq, sn)), 30) : rsh(wadd(wmul(qv, c), wmul(pq, sn)), 30);
+            kv = lane < r ? rsh(wsub(wmul(kv, c), wmul(pk, sn)), 30) : rsh(wadd(wmul(kv, c), wmul(pk, sn)), 30);
+        }
+    }
+    // the water levels of q and k (base2.py:93)
+    const int shq = water_shift(wave_or64(iabs64(qv))), shk = water_shift(wave_or64(iabs64(kv)));
+    const int q16 = (int)rsh(qv, shq), k16 = (int)rsh(kv, shk);
+    const i64 eq = -16 + shq, ekn = -16 + shk;
+    K16[(size_t)p * 768 + h * 64 + lane] = k16;
+    if (lane == 0) EK[(size_t)p * 12 + h] = (int)ekn;
+    if (vv < (i64)INT32_MIN || vv > (i64)INT32_MAX) atomicOr(a.err, SM_ERR_V32);
+    V[(size_t)p * 768 + h * 64 + lane] = (int)vv;
+    // scores (base2.py:94): lane s < p its cached row, lane p the new key
+    i64 dot = 0;
+#pragma unroll
+    for (int c = 0; c < 16; c++) {
+        dot += (i64)__builtin_amdgcn_readlane(q16, 4 * c) * krow[c].x + (i64)__builtin_amdgcn_readlane(q16, 4 * c + 1) * krow[c].y +
+               (i64)__builtin_amdgcn_readlane(q16, 4 * c + 2) * krow[c].z + (i64)__builtin_amdgcn_readlane(q16, 4 * c + 3) * krow[c].w;
+    }
+    i64 dn = (i64)q16 * k16;
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) dn += __shfl_xor(dn, o, 64);
+    const i64 ek = lane == p ? ekn : ekl;
+    const i64 d = lane == p ? dn : dot;
+    i64 sc = INT64_MIN;
+    if (lane <= p) sc = MODEL == 1 ? rsh(wmul(d, a.ehalf), wsub(16, wsub(wmul(eq + ek + 10, 65536), a.half) >> 16))
+                                   : rsh(d, -(eq + ek + 7));
+    i64 mx = sc;
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) { const i64 t = __shfl_xor(mx, o, 64); mx = t > mx ? t : mx; }
+    // arrivals (base2.py:96-97) and their sum
+    const int w = lane <= p ? tab_arr(a.tb, wsub(mx, sc)) : 0;
+    i64 z = w;
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) z += __shfl_xor(z, o, 64);
+    // the value sum of dimension `lane` (base2.py:98): cached positions, then the new one
+    i64 num = 0;
+    int vmax = 0;
+#pragma unroll
+    for (int s = 0; s < 64; s++) {
+        const int ws = __builtin_amdgcn_readlane(w, s);     // 0 for s > p
+        const int vs = s < p ? vcol[s] : 0;
+        num += (i64)ws * vs;
+        if (MODEL == 1 && ws) vmax = max(vmax, abs(vs));
+    }
+    const int wp = __builtin_amdgcn_readlane(w, p);
+    num += (i64)wp * (int)vv;
+    if (MODEL == 1 && wp) vmax = max(vmax, abs((int)vv));
+    if (MODEL == 1 && (double)vmax * (double)z >= 4611686018427387904.0) atomicOr(a.err, SM_ERR_RANGE);
+    // over the total through its log (base2.py:99)
+    int t; i64 m;
+    log2_parts(z, t, m);
+    const i64 F = wsub(0, wadd((i64)t * 65536, utab_log2(a.tb, (int)m)));
+    const i64 hp = utab_hpow(a.tb, (int)m);
+    i64 o;
+    if (MODEL == 1) {
+        const __int128 X = (__int128)num * hp;
+        const i64 sft = 16 - (F >> 16);
+        const __int128 r = sft >= 100 ? (__int128)0 : (X + ((__int128)1 << (sft - 1))) >> sft;
+        if (r > (__int128)INT64_MAX || r < (__int128)INT64_MIN) atomicOr(a.err, SM_ERR_RANGE);
+        o = (i64)r;
+    } else {
+        o = power_e(num, F, F & 0xFFFF, hp, a.tb);
+    }
+    a.out[(size_t)b * 768 + h * 64 + lane] = o;
+    if (rec) a.ratt[h * 64 + lane] = o;
+}
+
 // MODEL 1 is the Pythia machine (foundation0/pythia_base2.py:125-141): per-head interleaved q, k, v at h 192;
 // the first rot dims of q and k turned by position before their water level; scores
 // power(q16 . k16, (eq + ek + 10) 65536 - half); the final power exact in 128 bits (the reference's power never
@@ -439,6 +544,11 @@ __global__ __launch_bounds__(NTHR) void k_attend(AttArgs a) {
     const int sl = tid >> 2, qd = tid & 3;                   // position in the pass, quarter of the dimensions
     const int h = blockIdx.x, b = blockIdx.y;
     const int p = *a.pos;
+    if (p < 64 && gridDim.y == 1) {                          // one stream, short context: one wave, no barriers
+        // (with many streams the four-wave path below keeps more of the KV cache in flight per CU)
+        if (wave == 0) attend_short<MODEL>(a, p, h, b);
+        return;
+    }
     const i64* qkv = a.QKV + (size_t)b * 2304;
     int* K16 = a.K16 + (size_t)b * a.ctx * 768;
     int* EK = a.EK + (size_t)b * a.ctx * 12;
