@@ -52,10 +52,11 @@ struct GemmArgs {
 // One block (256 threads) per stream row: the light of base2.py:24-27 (and the gauge of :55-60), written as
 // MFMA A planes plus the row's exponent, gauge, power factor and plane sums.  Each thread owns groups of four
 // consecutive k, so every plane byte group goes out as one 32-bit store.
-template <int K, int PRO>
-__global__ __launch_bounds__(256) void k_light(LightArgs a) {
-    constexpr int NG = K / 4, GPT = (NG + 255) / 256, KS = K / 64;
-    __shared__ int red[32];
+template <int K, int PRO, int NT>
+__global__ __launch_bounds__(NT) void k_light(LightArgs a) {
+    constexpr int NG = K / 4, GPT = (NG + NT - 1) / NT, KS = K / 64, NW = NT / 64;
+    static_assert(NT % 64 == 0 && NW <= 12, "one to twelve waves");
+    __shared__ int red[24 + 6 * 12];   // OR words [0, 24), sums [24, 96)
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, r = blockIdx.x;
     const int p = a.pos ? *a.pos : 0;              // the stage product (PRO_X16) has no position
     if (a.skip_prompt && p < *a.plen - 1) return;
@@ -71,7 +72,7 @@ __global__ __launch_bounds__(256) void k_light(LightArgs a) {
     const bool rec_in = r == 0 && a.rec_pos && *a.rec_pos == p;
 #pragma unroll
     for (int m = 0; m < GPT; m++) {
-        const int g = tid + 256 * m;
+        const int g = tid + NT * m;
 #pragma unroll
         for (int j = 0; j < 4; j++) v[m][j] = 0;
         if (g >= NG) continue;
@@ -129,7 +130,7 @@ __global__ __launch_bounds__(256) void k_light(LightArgs a) {
         __syncthreads();
         u64 all = 0;
 #pragma unroll
-        for (int w = 0; w < 4; w++) all |= ((u64)(unsigned)red[2 * w + 1] << 32) | (unsigned)red[2 * w];
+        for (int w = 0; w < NW; w++) all |= ((u64)(unsigned)red[2 * w + 1] << 32) | (unsigned)red[2 * w];
         sh = water_shift((i64)all);
     }
     const i64 ex = -16 + sh;
@@ -139,7 +140,7 @@ __global__ __launch_bounds__(256) void k_light(LightArgs a) {
     int* pl = reinterpret_cast<int*>(a.planes + (size_t)(r >> 4) * KS * 3 * 1024);
 #pragma unroll
     for (int m = 0; m < GPT; m++) {
-        const int g = tid + 256 * m;
+        const int g = tid + NT * m;
         if (g >= NG) continue;
         const int k = 4 * g;
         unsigned ph = 0, pl8 = 0, pc = 0;
@@ -165,12 +166,12 @@ __global__ __launch_bounds__(256) void k_light(LightArgs a) {
     }
     const int w1 = wave_add32(s1), w2h = wave_add32((int)(s2 >> 16)), w2l = wave_add32((int)(s2 & 0xFFFF));
     const int w3 = wave_add32(sxh), w4 = wave_add32(sxl), w5 = wave_add32(n32);
-    if (lane == 0) { int* q = red + 8 + 6 * wave; q[0] = w1; q[1] = w2h; q[2] = w2l; q[3] = w3; q[4] = w4; q[5] = w5; }
+    if (lane == 0) { int* q = red + 24 + 6 * wave; q[0] = w1; q[1] = w2h; q[2] = w2l; q[3] = w3; q[4] = w4; q[5] = w5; }
     __syncthreads();
     if (tid == 0) {
         i64 S1 = 0, S2h = 0, S2l = 0, SXh = 0, SXl = 0, N32 = 0;
-        for (int w = 0; w < 4; w++) {
-            const int* q = red + 8 + 6 * w;
+        for (int w = 0; w < NW; w++) {
+            const int* q = red + 24 + 6 * w;
             S1 += q[0]; S2h += q[1]; S2l += q[2]; SXh += q[3]; SXl += q[4]; N32 += q[5];
         }
         i64 ls = 0, e2 = 0;
@@ -419,10 +420,10 @@ __global__ __launch_bounds__(256) void k_head_rows(GemmArgs a) {
 //
 // light_store<K>: a row of int64 values (thread t holds k = 4 g .. 4 g + 3 for g = t + 256 m) -> its water
 // level and the MFMA A planes (xh, xl', c) + the row facts {ex, 0, 0, 0, SXh, SXl, n32768}.
-template <int K>
-SMD void light_store(const i64 (&v)[(K / 4 + 255) / 256][4], int r, signed char* planes, int* rowinfo, int* red,
+template <int K, int NT>
+SMD void light_store(const i64 (&v)[(K / 4 + NT - 1) / NT][4], int r, signed char* planes, int* rowinfo, int* red,
                      bool rec, i64* rx16, i64* rexls) {
-    constexpr int NG = K / 4, GPT = (NG + 255) / 256, KS = K / 64;
+    constexpr int NG = K / 4, GPT = (NG + NT - 1) / NT, KS = K / 64, NW = NT / 64;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     u64 o = 0;
 #pragma unroll
@@ -434,13 +435,13 @@ SMD void light_store(const i64 (&v)[(K / 4 + 255) / 256][4], int r, signed char*
     __syncthreads();
     u64 all = 0;
 #pragma unroll
-    for (int w = 0; w < 4; w++) all |= ((u64)(unsigned)red[2 * w + 1] << 32) | (unsigned)red[2 * w];
+    for (int w = 0; w < NW; w++) all |= ((u64)(unsigned)red[2 * w + 1] << 32) | (unsigned)red[2 * w];
     const int sh = water_shift((i64)all);
     int sxh = 0, sxl = 0, n32 = 0;
     int* pl = reinterpret_cast<int*>(planes + (size_t)(r >> 4) * KS * 3 * 1024);
 #pragma unroll
     for (int m = 0; m < GPT; m++) {
-        const int g = tid + 256 * m;
+        const int g = tid + NT * m;
         if (g >= NG) continue;
         const int k = 4 * g;
         unsigned ph = 0, pq = 0, pc = 0;
@@ -463,11 +464,11 @@ SMD void light_store(const i64 (&v)[(K / 4 + 255) / 256][4], int r, signed char*
         pl[off + 512] = (int)pc;
     }
     const int w3 = wave_add32(sxh), w4 = wave_add32(sxl), w5 = wave_add32(n32);
-    if (lane == 0) { red[8 + 3 * wave] = w3; red[9 + 3 * wave] = w4; red[10 + 3 * wave] = w5; }
+    if (lane == 0) { red[24 + 3 * wave] = w3; red[25 + 3 * wave] = w4; red[26 + 3 * wave] = w5; }
     __syncthreads();
     if (tid == 0) {
         int SXh = 0, SXl = 0, N32 = 0;
-        for (int w = 0; w < 4; w++) { SXh += red[8 + 3 * w]; SXl += red[9 + 3 * w]; N32 += red[10 + 3 * w]; }
+        for (int w = 0; w < NW; w++) { SXh += red[24 + 3 * w]; SXl += red[25 + 3 * w]; N32 += red[26 + 3 * w]; }
         int* ri = rowinfo + (size_t)r * 8;
         ri[0] = -16 + sh; ri[1] = 0; ri[2] = 0; ri[3] = 0; ri[4] = SXh; ri[5] = SXl; ri[6] = N32;
         if (rec && rexls) { rexls[0] = -16 + sh; rexls[1] = 0; }
@@ -523,17 +524,18 @@ SMD void plain4(const int* part, int ks, int rows, int N, int kin, const int* ri
 //   PY_EDGE:  edge(plain(fc)) (:156), then its light (K = 3072)
 // Both gauges share to16(R), S1, S2 and LS (:100-110); only the gain, its power and the offset differ.
 template <int MODE>
-__global__ __launch_bounds__(256) void k_py_rows(PyRowArgs a) {
-    __shared__ int red[32];
+__global__ __launch_bounds__(MODE == PY_EDGE ? 768 : 192) void k_py_rows(PyRowArgs a) {
+    constexpr int NT = MODE == PY_EDGE ? 768 : 192, NW = NT / 64;
+    __shared__ int red[24 + 6 * 12];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, r = blockIdx.x;
     const int p = *a.pos;
     const bool rec = r == 0 && a.rec_pos && *a.rec_pos == p;
-    if (MODE == PY_EDGE) {
-        i64 v[3][4];
+    if constexpr (MODE == PY_EDGE) {
+        i64 v[1][4];
         const int* ri = a.rowinfoA + (size_t)r * 8;          // fc's light facts (this block's row only)
 #pragma unroll
-        for (int m = 0; m < 3; m++) {
-            const int k = 4 * (tid + 256 * m);
+        for (int m = 0; m < 1; m++) {
+            const int k = 4 * tid;
             i64 pile[4], y[4];
             plain4(a.partA, a.ksA, a.rows, 3072, a.kinA, ri, a.csumA, a.weA, a.biasA, r, k, pile, y);
 #pragma unroll
@@ -544,15 +546,13 @@ __global__ __launch_bounds__(256) void k_py_rows(PyRowArgs a) {
                 if (rec && a.routA) a.routA[k + j] = v[m][j];
             }
         }
-        __syncthreads();                                    // every thread has read its rowinfo facts
-        light_store<3072>(v, r, a.planes1, a.rowinfo1, red, rec, a.rx1, a.rex1);
+        light_store<3072, NT>(v, r, a.planes1, a.rowinfo1, red, rec, a.rx1, a.rex1);
         return;
     }
     // the stream row (192 threads hold four lanes each)
-    const bool act = tid < 192;
     const int k = 4 * tid;
     i64 R4[4] = {0, 0, 0, 0};
-    if (act) {
+    {
         if (MODE == PY_EMBED) {
             const i64 tok = a.seq[(size_t)r * a.seq_stride + p];
             const i64 es = -((i64)a.ee[tok] + 16);
@@ -587,7 +587,7 @@ __global__ __launch_bounds__(256) void k_py_rows(PyRowArgs a) {
     __syncthreads();
     u64 all = 0;
 #pragma unroll
-    for (int w = 0; w < 4; w++) all |= ((u64)(unsigned)red[2 * w + 1] << 32) | (unsigned)red[2 * w];
+    for (int w = 0; w < NW; w++) all |= ((u64)(unsigned)red[2 * w + 1] << 32) | (unsigned)red[2 * w];
     const int sh = water_shift((i64)all);
     int x[4];
     int s1 = 0;
@@ -599,11 +599,11 @@ __global__ __launch_bounds__(256) void k_py_rows(PyRowArgs a) {
         s2 += (i64)x[j] * x[j];
     }
     const int w1 = wave_add32(s1), w2h = wave_add32((int)(s2 >> 16)), w2l = wave_add32((int)(s2 & 0xFFFF));
-    if (lane == 0) { red[16 + 3 * wave] = w1; red[17 + 3 * wave] = w2h; red[18 + 3 * wave] = w2l; }
+    if (lane == 0) { red[24 + 3 * wave] = w1; red[25 + 3 * wave] = w2h; red[26 + 3 * wave] = w2l; }
     __syncthreads();
     i64 S1 = 0, S2h = 0, S2l = 0;
 #pragma unroll
-    for (int w = 0; w < 4; w++) { S1 += red[16 + 3 * w]; S2h += red[17 + 3 * w]; S2l += red[18 + 3 * w]; }
+    for (int w = 0; w < NW; w++) { S1 += red[24 + 3 * w]; S2h += red[25 + 3 * w]; S2l += red[26 + 3 * w]; }
     i64 e2;
     const i64 ls = pgauge_ls_pow(S1, (S2h << 16) + S2l, -16 + sh, a.tb, e2);
     __syncthreads();                                    // red is reused below
@@ -613,7 +613,7 @@ __global__ __launch_bounds__(256) void k_py_rows(PyRowArgs a) {
         const i64* nb = gi ? a.nb2 : a.nb1;
         const i64 sg = wsub(16, wsub(wmul((i64)(gi ? a.nge2 : a.nge1) + 16, 65536), ls) >> 16);
         i64 v[1][4] = {{0, 0, 0, 0}};
-        if (act) {
+        {
 #pragma unroll
             for (int j = 0; j < 4; j++) {
                 const i64 c = 768 * (i64)x[j] - S1;
@@ -622,7 +622,7 @@ __global__ __launch_bounds__(256) void k_py_rows(PyRowArgs a) {
                 if (rec && rg) rg[k + j] = v[0][j];
             }
         }
-        light_store<768>(v, r, gi ? a.planes2 : a.planes1, gi ? a.rowinfo2 : a.rowinfo1, red, rec,
+        light_store<768, NT>(v, r, gi ? a.planes2 : a.planes1, gi ? a.rowinfo2 : a.rowinfo1, red, rec,
                          gi ? a.rx2 : a.rx1, gi ? a.rex2 : a.rex1);
     }
 }
@@ -677,7 +677,7 @@ __global__ __launch_bounds__(256) void k_race_rows(RaceArgs a) {
     }
 }
 
-#define BINST_L(K, PRO) template __global__ void k_light<K, PRO>(LightArgs);
+#define BINST_L(K, PRO) template __global__ void k_light<K, PRO, (K) / 4>(LightArgs);
 BINST_L(768, PRO_EMBED)
 BINST_L(768, PRO_GAUGE)
 BINST_L(768, PRO_TO16)
