@@ -417,7 +417,7 @@ __global__ __launch_bounds__(64 * WPB) void k_gemv(GemvArgs a) {
 //   3. the clock starts at the maximum; arrivals ARR[max - sc] (0 past the table)            (base2.py:96-97)
 //   4. num = sum a v, out = power(num, -log2fix(sum a))                                        (base2.py:98-99)
 // Four lanes share a position (16 of its 64 dimensions each), so a block covers 64 positions per pass.  The
-// cached keys and values of the first 128 positions are requested at launch, before the new q, k, v arrive.
+// cached keys and values of the first 64 positions are requested at launch, before the new q, k, v arrive.
 // The maximum is global over the row before any arrival is read (two passes, scores in LDS), so the result is
 // exact for any context length.
 // The short-context path (position p < 64, one stream): one wave does a head alone, with no LDS and no block
@@ -566,17 +566,6 @@ __global__ __launch_bounds__(NTHR) void k_attend(AttArgs a) {
         for (int c = 0; c < 4; c++) { kp[c] = kr[c]; vp[c] = vr[c]; }
         ekp = EK[(size_t)sl * 12 + h];
     }
-    // the second pass's positions too (every lane loads; rows past p read row 0 and are not used)
-    v4i kp2[4], vp2[4];
-    int ekp2;
-    {
-        const int sr = sl + ACH < p ? sl + ACH : 0;
-        const v4i* kr = reinterpret_cast<const v4i*>(K16 + (size_t)sr * 768 + h * 64 + qd * 16);
-        const v4i* vr = reinterpret_cast<const v4i*>(V + (size_t)sr * 768 + h * 64 + qd * 16);
-#pragma unroll
-        for (int c = 0; c < 4; c++) { kp2[c] = kr[c]; vp2[c] = vr[c]; }
-        ekp2 = EK[(size_t)sr * 12 + h];
-    }
     if (MODEL == 1 && wave < 2) {        // the turns (pythia_base2.py:116-123): pair (i, i + rot/2)
         const int r = a.rot >> 1;
         const i64 partner = __shfl(xnew, lane < r ? lane + r : lane - r, 64);
@@ -623,10 +612,6 @@ __global__ __launch_bounds__(NTHR) void k_attend(AttArgs a) {
 #pragma unroll
                 for (int c = 0; c < 4; c++) kk[c] = kp[c];
                 ek = ekp;
-            } else if (s0 == ACH) {
-#pragma unroll
-                for (int c = 0; c < 4; c++) kk[c] = kp2[c];
-                ek = ekp2;
             } else {
                 const v4i* kr = reinterpret_cast<const v4i*>(K16 + (size_t)s * 768 + h * 64 + qd * 16);
 #pragma unroll
@@ -669,9 +654,6 @@ __global__ __launch_bounds__(NTHR) void k_attend(AttArgs a) {
             if (s0 == 0) {
 #pragma unroll
                 for (int c = 0; c < 4; c++) vv[c] = vp[c];
-            } else if (s0 == ACH) {
-#pragma unroll
-                for (int c = 0; c < 4; c++) vv[c] = vp2[c];
             } else {
                 const v4i* vr = reinterpret_cast<const v4i*>(V + (size_t)s * 768 + h * 64 + qd * 16);
 #pragma unroll
