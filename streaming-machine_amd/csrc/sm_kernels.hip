@@ -530,10 +530,14 @@ SMD void attend_short(const AttArgs& a, int p, int h, int b) {
 // power(q16 . k16, (eq + ek + 10) 65536 - half); the final power exact in 128 bits (the reference's power never
 // wraps, :81-85); its asserts (turn input < 2^31, max|v| sum(a) < 2^62, a result that fits) set SM_ERR_RANGE.
 #define ACH 64
-template <int MODEL>
-__global__ __launch_bounds__(NTHR) void k_attend(AttArgs a) {
+#define ATT_PRE 2            // passes of 64 positions whose keys and values are requested at launch
+// ONE = 1: one stream (the short-context path is available, full registers); ONE = 0: many streams, three waves
+// a SIMD so that 768 blocks are resident at once
+template <int MODEL, int ONE>
+__global__ __launch_bounds__(NTHR, ONE ? 1 : 3) void k_attend(AttArgs a) {
     extern __shared__ __align__(16) unsigned char smem[];
-    i64* sc = reinterpret_cast<i64*>(smem);                 // [ctx]
+    i64* sc = reinterpret_cast<i64*>(smem);                  // [ctx] scores
+    int* arr = reinterpret_cast<int*>(sc + a.ctx);           // [ctx] arrivals
     __shared__ __align__(16) int q16s[64];
     __shared__ __align__(16) int k16s[64];
     __shared__ __align__(16) int vs[64];
@@ -541,13 +545,15 @@ __global__ __launch_bounds__(NTHR) void k_attend(AttArgs a) {
     __shared__ i64 numr[4][64];
     __shared__ int eqs, eks;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int sl = tid >> 2, qd = tid & 3;                   // position in the pass, quarter of the dimensions
+    const int sl = tid >> 2, qd = tid & 3;                   // scores: position in the pass, lane of the position
+    const int d4 = tid & 15, g = tid >> 4;                   // value sum: four dimensions, position group
     const int h = blockIdx.x, b = blockIdx.y;
     const int p = *a.pos;
-    if (p < 64 && gridDim.y == 1) {                          // one stream, short context: one wave, no barriers
-        // (with many streams the four-wave path below keeps more of the KV cache in flight per CU)
-        if (wave == 0) attend_short<MODEL>(a, p, h, b);
-        return;
+    if constexpr (ONE) {
+        if (p < 64) {                                        // one stream, short context: one wave, no barriers
+            if (wave == 0) attend_short<MODEL>(a, p, h, b);
+            return;
+        }
     }
     const i64* qkv = a.QKV + (size_t)b * 2304;
     int* K16 = a.K16 + (size_t)b * a.ctx * 768;
@@ -555,16 +561,32 @@ __global__ __launch_bounds__(NTHR) void k_attend(AttArgs a) {
     int* V = a.V + (size_t)b * a.ctx * 768;
     const bool rec = b == 0 && a.rec_pos && *a.rec_pos == p;
 
-    // the new q, k, v first (vector loads complete in order), then the cached positions of the first pass
+    // requests first (vector loads complete in order): the new q, k, v; then the cached keys of the first
+    // ATT_PRE passes (a position's four lanes read its 256-byte row as 4 x 64 contiguous bytes: lane qd holds
+    // dimensions 16 u + 4 qd .. + 3 of step u) and the values of positions g, g + 16, .. in the same passes
+    // (16 lanes a 256-byte row, four rows a wave)
     i64 xnew = wave < 3 ? qkv[MODEL == 1 ? h * 192 + wave * 64 + lane : wave * 768 + h * 64 + lane] : 0;
-    v4i kp[4], vp[4];
-    int ekp = 0;
-    if (sl < p) {
-        const v4i* kr = reinterpret_cast<const v4i*>(K16 + (size_t)sl * 768 + h * 64 + qd * 16);
-        const v4i* vr = reinterpret_cast<const v4i*>(V + (size_t)sl * 768 + h * 64 + qd * 16);
+    v4i kp[ATT_PRE][4];
+    int ekp[ATT_PRE] = {};
 #pragma unroll
-        for (int c = 0; c < 4; c++) { kp[c] = kr[c]; vp[c] = vr[c]; }
-        ekp = EK[(size_t)sl * 12 + h];
+    for (int c = 0; c < ATT_PRE; c++) {
+        if (64 * c < p) {                                    // uniform: whole passes only
+            const int sr = sl + 64 * c < p ? sl + 64 * c : 0;
+            const v4i* kr = reinterpret_cast<const v4i*>(K16 + (size_t)sr * 768 + h * 64) + qd;
+#pragma unroll
+            for (int u = 0; u < 4; u++) kp[c][u] = kr[4 * u];
+            ekp[c] = EK[(size_t)sr * 12 + h];
+        }
+    }
+    constexpr int NV = 64 * ATT_PRE / 16;                    // value rows per thread requested at launch
+    v4i vp[NV];
+#pragma unroll
+    for (int i = 0; i < NV; i++) {
+        vp[i] = v4i{0, 0, 0, 0};
+        if (16 * i < p) {                                    // uniform
+            const int sv = g + 16 * i;
+            vp[i] = reinterpret_cast<const v4i*>(V + (size_t)(sv < p ? sv : 0) * 768 + h * 64)[d4];
+        }
     }
     if (MODEL == 1 && wave < 2) {        // the turns (pythia_base2.py:116-123): pair (i, i + rot/2)
         const int r = a.rot >> 1;
@@ -597,95 +619,89 @@ __global__ __launch_bounds__(NTHR) void k_attend(AttArgs a) {
     }
     __syncthreads();
 
-    // pass 1: scores and their maximum
+    // scores (base2.py:94 / pythia_base2.py:133) and their maximum
     const i64 eq = eqs;
-    int qv[16];
+    v4i qv[4];
 #pragma unroll
-    for (int i = 0; i < 16; i++) qv[i] = q16s[qd * 16 + i];
+    for (int u = 0; u < 4; u++) qv[u] = reinterpret_cast<const v4i*>(q16s)[4 * u + qd];
+    auto score = [&](i64 dot, i64 ek) -> i64 {
+        return MODEL == 1 ? rsh(wmul(dot, a.ehalf), wsub(16, wsub(wmul(eq + ek + 10, 65536), a.half) >> 16))
+                          : rsh(dot, -(eq + ek + 7));
+    };
     i64 mx = INT64_MIN;
     for (int s0 = 0; s0 <= p; s0 += ACH) {
         const int s = s0 + sl;
+        const int c = s0 / ACH;
         i64 dot = 0, ek = 0;
+        v4i kk[4];
         if (s < p) {
-            v4i kk[4];
-            if (s0 == 0) {
+            if (c < ATT_PRE) {
 #pragma unroll
-                for (int c = 0; c < 4; c++) kk[c] = kp[c];
-                ek = ekp;
+                for (int cc = 0; cc < ATT_PRE; cc++)
+                    if (cc == c) {
+#pragma unroll
+                        for (int u = 0; u < 4; u++) kk[u] = kp[cc][u];
+                        ek = ekp[cc];
+                    }
             } else {
-                const v4i* kr = reinterpret_cast<const v4i*>(K16 + (size_t)s * 768 + h * 64 + qd * 16);
+                const v4i* kr = reinterpret_cast<const v4i*>(K16 + (size_t)s * 768 + h * 64) + qd;
 #pragma unroll
-                for (int c = 0; c < 4; c++) kk[c] = kr[c];
+                for (int u = 0; u < 4; u++) kk[u] = kr[4 * u];
                 ek = EK[(size_t)s * 12 + h];
             }
+        } else {
 #pragma unroll
-            for (int c = 0; c < 4; c++)
-                dot += (i64)qv[4 * c] * kk[c].x + (i64)qv[4 * c + 1] * kk[c].y + (i64)qv[4 * c + 2] * kk[c].z + (i64)qv[4 * c + 3] * kk[c].w;
-        } else if (s == p) {
-#pragma unroll
-            for (int i = 0; i < 16; i++) dot += (i64)qv[i] * k16s[qd * 16 + i];
+            for (int u = 0; u < 4; u++) kk[u] = reinterpret_cast<const v4i*>(k16s)[4 * u + qd];   // s == p: the new key
             ek = eks;
+        }
+        if (s <= p) {
+#pragma unroll
+            for (int u = 0; u < 4; u++)
+                dot += (i64)qv[u].x * kk[u].x + (i64)qv[u].y * kk[u].y + (i64)qv[u].z * kk[u].z + (i64)qv[u].w * kk[u].w;
         }
         dot += __shfl_xor(dot, 1, 64);
         dot += __shfl_xor(dot, 2, 64);
         if (s <= p) {
-            const i64 v = MODEL == 1 ? rsh(wmul(dot, a.ehalf), wsub(16, wsub(wmul(eq + ek + 10, 65536), a.half) >> 16))
-                                     : rsh(dot, -(eq + ek + 7));
+            const i64 v = score(dot, ek);
             if (qd == 0) sc[s] = v;
             mx = v > mx ? v : mx;
         }
     }
     mx = block_reduce(mx, red, OpMax(), tid);   // its barriers also publish sc[]
 
-    // pass 2: arrivals and the value sum, 16 dimensions per lane
-    i64 num[16];
-#pragma unroll
-    for (int i = 0; i < 16; i++) num[i] = 0;
+    // arrivals (base2.py:96-97), one position per thread, into LDS; their sum
     i64 z = 0;
-    int vmax = 0;                                   // Pythia: the largest |v| this lane weighs (the 2^62 assert)
-    for (int s0 = 0; s0 <= p; s0 += ACH) {
-        const int s = s0 + sl;
-        if (s > p) continue;
+    for (int s = tid; s <= p; s += NTHR) {
         const int w = tab_arr(a.tb, wsub(mx, sc[s]));
-        if (qd == 0) z += w;
-        if (!w) continue;
-        if (s < p) {
-            v4i vv[4];
-            if (s0 == 0) {
-#pragma unroll
-                for (int c = 0; c < 4; c++) vv[c] = vp[c];
-            } else {
-                const v4i* vr = reinterpret_cast<const v4i*>(V + (size_t)s * 768 + h * 64 + qd * 16);
-#pragma unroll
-                for (int c = 0; c < 4; c++) vv[c] = vr[c];
-            }
-#pragma unroll
-            for (int c = 0; c < 4; c++) {
-                num[4 * c] += (i64)w * vv[c].x; num[4 * c + 1] += (i64)w * vv[c].y;
-                num[4 * c + 2] += (i64)w * vv[c].z; num[4 * c + 3] += (i64)w * vv[c].w;
-                if (MODEL == 1) vmax = max(vmax, max(max(abs(vv[c].x), abs(vv[c].y)), max(abs(vv[c].z), abs(vv[c].w))));
-            }
-        } else {
-#pragma unroll
-            for (int i = 0; i < 16; i++) {
-                num[i] += (i64)w * vs[qd * 16 + i];
-                if (MODEL == 1) vmax = max(vmax, abs(vs[qd * 16 + i]));
-            }
-        }
+        arr[s] = w;
+        z += w;
     }
-    // sum over the 16 positions of each wave (lanes that share a quarter), then over the 4 waves
+    z = block_reduce(z, red, OpAdd(), tid);     // its barriers also publish arr[]
+
+    // the value sums of dimensions 4 d4 .. + 3 over positions g, g + 16, .. (base2.py:98)
+    i64 n0 = 0, n1 = 0, n2 = 0, n3 = 0;
+    int vmax = 0;                               // Pythia: the largest |v| weighed (the 2^62 assert)
+    auto acc = [&](int w, v4i x) {
+        n0 += (i64)w * x.x; n1 += (i64)w * x.y; n2 += (i64)w * x.z; n3 += (i64)w * x.w;
+        if (MODEL == 1 && w) vmax = max(vmax, max(max(abs(x.x), abs(x.y)), max(abs(x.z), abs(x.w))));
+    };
 #pragma unroll
-    for (int i = 0; i < 16; i++) {
-        i64 v = num[i];
-        v += __shfl_xor(v, 4, 64); v += __shfl_xor(v, 8, 64); v += __shfl_xor(v, 16, 64); v += __shfl_xor(v, 32, 64);
-        num[i] = v;
+    for (int i = 0; i < NV; i++) {
+        const int sv = g + 16 * i;
+        if (16 * i > p) break;                  // uniform
+        if (sv < p) acc(arr[sv], vp[i]);
     }
-    if (lane < 4) {
-#pragma unroll
-        for (int i = 0; i < 16; i++) numr[wave][lane * 16 + i] = num[i];
-    }
-    z = block_reduce(z, red, OpAdd(), tid);   // its barriers also publish numr[]
+    for (int sv = g + 16 * NV; sv < p; sv += 16)                 // past the requested positions
+        acc(arr[sv], reinterpret_cast<const v4i*>(V + (size_t)sv * 768 + h * 64)[d4]);
+    if ((p & 15) == g) acc(arr[p], reinterpret_cast<const v4i*>(vs)[d4]);   // the new position (from LDS)
     if (MODEL == 1 && (double)vmax * (double)z >= 4611686018427387904.0) atomicOr(a.err, SM_ERR_RANGE);
+    // the 16 position groups: 4 in a wave (lanes 16 apart), then the 4 waves through LDS
+    n0 += __shfl_xor(n0, 16, 64); n1 += __shfl_xor(n1, 16, 64); n2 += __shfl_xor(n2, 16, 64); n3 += __shfl_xor(n3, 16, 64);
+    n0 += __shfl_xor(n0, 32, 64); n1 += __shfl_xor(n1, 32, 64); n2 += __shfl_xor(n2, 32, 64); n3 += __shfl_xor(n3, 32, 64);
+    if (lane < 16) {
+        numr[wave][4 * d4] = n0; numr[wave][4 * d4 + 1] = n1; numr[wave][4 * d4 + 2] = n2; numr[wave][4 * d4 + 3] = n3;
+    }
+    __syncthreads();
     if (wave == 0) {
         const i64 tot = numr[0][lane] + numr[1][lane] + numr[2][lane] + numr[3][lane];
         int t; i64 m;
@@ -799,8 +815,10 @@ INST(768, 2, 4, PRO_PEMBED, EPI_PLAIN)        // Pythia: qkv of layer 0
 INST(768, 2, 4, PRO_PGAUGE, EPI_PLAIN)        // Pythia: qkv
 INST(768, 2, 4, PRO_PGAUGE, EPI_PLAIN_EDGE)   // Pythia: fc
 INST(768, 8, 4, PRO_PGAUGE, EPI_PHEAD)        // Pythia: head
-template __global__ void k_attend<0>(AttArgs);
-template __global__ void k_attend<1>(AttArgs);
+template __global__ void k_attend<0, 0>(AttArgs);
+template __global__ void k_attend<0, 1>(AttArgs);
+template __global__ void k_attend<1, 0>(AttArgs);
+template __global__ void k_attend<1, 1>(AttArgs);
 // raw piles of a given light (stage entry point)
 INST(768, 2, 4, PRO_X16, EPI_PILE)
 INST(768, 8, 4, PRO_X16, EPI_PILE)

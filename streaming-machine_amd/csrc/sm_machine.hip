@@ -417,7 +417,8 @@ static int launch_step_batched(sm_machine* m, int parts, hipEvent_t hs, hipEvent
             a.QKV = m->QKV; a.K16 = m->K16 + l * per * 768; a.EK = m->EK + l * per * 12; a.V = m->V + l * per * 768;
             a.out = m->att; a.pos = ctl + CTL_POS; a.ctx = m->ctx; a.tb = tb; a.err = ctl + CTL_ERR;
             a.rec_pos = ctl + CTL_RECPOS; a.ratt = m->r_att + l * 768;
-            k_attend<0><<<dim3(12, m->B), NTHR, (size_t)m->ctx * 8, m->st>>>(a);
+            if (m->B == 1) k_attend<0, 1><<<dim3(12, 1), NTHR, (size_t)m->ctx * 12, m->st>>>(a);
+            else k_attend<0, 0><<<dim3(12, m->B), NTHR, (size_t)m->ctx * 12, m->st>>>(a);
         }
         {
             LightArgs a = light_args(768, m->att, rx + 3072, re + 2);
@@ -517,7 +518,8 @@ static int launch_step_pythia(sm_machine* m, int parts, hipEvent_t hs, hipEvent_
             a.out = m->att; a.pos = ctl + CTL_POS; a.ctx = m->ctx; a.tb = tb; a.err = ctl + CTL_ERR;
             a.rec_pos = ctl + CTL_RECPOS; a.ratt = m->r_att + l * 768;
             a.cosT = m->cosT; a.sinT = m->sinT; a.rot = m->rot; a.half = m->half; a.ehalf = m->ehalf;
-            k_attend<1><<<dim3(12, m->B), NTHR, (size_t)m->ctx * 8, m->st>>>(a);
+            if (m->B == 1) k_attend<1, 1><<<dim3(12, 1), NTHR, (size_t)m->ctx * 12, m->st>>>(a);
+            else k_attend<1, 0><<<dim3(12, m->B), NTHR, (size_t)m->ctx * 12, m->st>>>(a);
         }
         // proj: plain of the attention row, added to R (At)
         {
@@ -635,7 +637,7 @@ static int launch_step_pythia_batched(sm_machine* m, int parts, hipEvent_t hs, h
             a.out = m->att; a.pos = ctl + CTL_POS; a.ctx = m->ctx; a.tb = tb; a.err = ctl + CTL_ERR;
             a.rec_pos = ctl + CTL_RECPOS; a.ratt = m->r_att + l * 768;
             a.cosT = m->cosT; a.sinT = m->sinT; a.rot = m->rot; a.half = m->half; a.ehalf = m->ehalf;
-            k_attend<1><<<dim3(12, B), NTHR, (size_t)m->ctx * 8, m->st>>>(a);
+            k_attend<1, 0><<<dim3(12, B), NTHR, (size_t)m->ctx * 12, m->st>>>(a);
         }
         {   // the attention row's light, then proj's partials
             LightArgs a{};
@@ -719,7 +721,8 @@ static int launch_step(sm_machine* m, int parts = STEP_ALL, hipEvent_t hs = null
             a.QKV = m->QKV; a.K16 = m->K16 + l * per * 768; a.EK = m->EK + l * per * 12; a.V = m->V + l * per * 768;
             a.out = m->att; a.pos = ctl + CTL_POS; a.ctx = m->ctx; a.tb = tb; a.err = ctl + CTL_ERR;
             a.rec_pos = ctl + CTL_RECPOS; a.ratt = m->r_att + l * 768;
-            k_attend<0><<<dim3(12, m->B), NTHR, (size_t)m->ctx * 8, m->st>>>(a);
+            if (m->B == 1) k_attend<0, 1><<<dim3(12, 1), NTHR, (size_t)m->ctx * 12, m->st>>>(a);
+            else k_attend<0, 0><<<dim3(12, m->B), NTHR, (size_t)m->ctx * 12, m->st>>>(a);
         }
         // proj: to16 of the attention row, product, plain shift + bias, added to R (base2.py:105)
         {
@@ -1209,7 +1212,7 @@ extern "C" int sm_stage_attend(const sm_tables* t, const int64_t* qkv, int32_t* 
     AttArgs a{};
     a.QKV = (const i64*)qkv; a.K16 = k16; a.EK = ek; a.V = v; a.out = (i64*)out; a.pos = t->scratch; a.ctx = ctx;
     a.tb = t->tb(); a.err = t->scratch + 1;
-    k_attend<0><<<dim3(12, 1), NTHR, (size_t)ctx * 8, s>>>(a);
+    k_attend<0, 1><<<dim3(12, 1), NTHR, (size_t)ctx * 12, s>>>(a);
     HIP_TRY(hipGetLastError());
     int err = 0;
     HIP_TRY(hipMemcpyAsync(&err, t->scratch + 1, 4, hipMemcpyDeviceToHost, s));
