@@ -10,7 +10,7 @@ in HBM.  Before any number is printed the emitted words are checked against the 
 reference itself); the CPU baseline's own words are checked against the GPU's.
 
 Printed: one JSON line with the driver's fields plus
-  roofline      the head kernel (the largest single launch: the 768 x 50257 plate read + race), its mean
+  roofline      the head kernel (the largest single launch: the 768 x 50257 plate read), its mean
                 duration from HIP event pairs recorded around every head launch inside the timed region
   step_roofline the whole decode step's algorithmic bytes over its measured time
   batched       the same machine with 64 streams in lockstep (int8 MFMA contraction), 32-token prompts,
@@ -121,7 +121,7 @@ def batched_leg(sm, lay):
             "workload": f"{B_STREAMS} streams, {B_PROMPT}-token random prompts, {B_WORDS} greedy words each "
                         f"(context to {B_PROMPT + B_WORDS}); streams 0 and 1 checked against base2.py's golden words",
             "roofline": {"bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                         "frac": round(ach / HBM_PEAK_GBS, 4), "kernel": "k_gemm<768,4,EPI_HEAD>",
+                         "frac": round(ach / HBM_PEAK_GBS, 4), "kernel": "k_head_rows<4,EPI_HEAD>",
                          "mean_launch_us": round(us, 3), "launches_timed": n,
                          "int8_tops": round(ops / (us * 1e-6) / 1e12, 1), "int8_frac": round(ops / (us * 1e-6) / 5.0e15, 4)},
             "step_roofline": {"bytes_per_step": int(sb), "achieved": round(sb / (ms * 1e-3) / 1e9, 1),
@@ -330,7 +330,7 @@ def main():
                    "batch": 1, "prompt": PROMPT, "words": WORDS, "vocab": vocab},
         "roofline": {"bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": traffic,
-                     "kernel": "k_gemv<768,8,PRO_GAUGE,EPI_HEAD> (head plate read + race)",
+                     "kernel": "k_gemv<768,8,4,PRO_GAUGE,EPI_HEAD> (head plate read; the race is its own launch)",
                      "bytes_per_launch": hb, "mean_launch_us": round(head_us, 3), "launches_timed": head_n},
         "step_roofline": {"bytes_per_step": int(sb), "achieved": round(step_ach, 1), "frac": round(step_ach / HBM_PEAK_GBS, 4)},
         "batched": batched,
