@@ -13,6 +13,9 @@ Printed: one JSON line with the driver's fields plus
   roofline      the head kernel (the largest single launch: the 768 x 50257 plate read), its mean
                 duration from HIP event pairs recorded around every head launch inside the timed region
   step_roofline the whole decode step's algorithmic bytes over its measured time
+  prompt_included  words per second counting the prompt pass (every prompt position but the last through the
+                int8 MFMA banks in passes of up to 64 rows, then the first word's step), as the reference also
+                reports beside the after-the-prompt rate
   batched       the same machine with 64 streams in lockstep (int8 MFMA contraction), 32-token prompts,
                 128 words each (tokens/s over all streams)
   pythia        the Pythia-160m-shaped machine with 32 streams, 64-token prompts, 256 words each
@@ -38,6 +41,7 @@ WORDS = 16          # words per sequence (the prompt pass gives the first)
 PROMPT = 8
 B_STREAMS, B_PROMPT, B_WORDS = 64, 32, 128     # the batched workload: 64 streams, 32-token prompts, 128 words
 P_STREAMS, P_PROMPT, P_WORDS = 32, 64, 256     # the Pythia-160m-shaped workload: 32 streams, 64-token prompts, 256 words
+PREFILL_ROWS = 64   # prompt rows a pass through the int8 MFMA banks (0: position by position)
 
 
 def load_sm():
@@ -87,14 +91,18 @@ def batched_leg(sm, lay):
     prompts = [sm.prompt_ids(4 + b, B_PROMPT) for b in range(B_STREAMS)]     # stream s: default_rng(4 + s)
     gw = golden_words("base2_golden.json")
     want = {b: gw[f"c4_stream{b}_p32_w4"] for b in (0, 1)}
-    m = sm.Machine(lay, max_ctx=B_PROMPT + B_WORDS, max_streams=B_STREAMS, graph_steps=B_WORDS - 1, profile=True)
+    m = sm.Machine(lay, max_ctx=B_PROMPT + B_WORDS, max_streams=B_STREAMS, graph_steps=B_WORDS - 1, profile=True,
+                   prefill_rows=PREFILL_ROWS)
     res = None
     for it in range(2):                     # the first sequence warms up (graph instantiation)
         m.reset()
+        torch.cuda.synchronize()
+        t = time.perf_counter()
         for b, p in enumerate(prompts):
             m.prefill(p, b)
-        first = m.generate(1)
+        first = m.generate(1)               # the prompt pass and the first word
         torch.cuda.synchronize()
+        tp = time.perf_counter() - t
         m.profile(clear=True)
         t = time.perf_counter()
         rest = m.generate(B_WORDS - 1)
@@ -105,9 +113,9 @@ def batched_leg(sm, lay):
         for b, w in want.items():
             if [int(x) for x in words[b][:len(w)]] != w:
                 raise RuntimeError(f"batched stream {b}: GPU words differ from base2.py's golden words")
-        res = (dt, n, us)
+        res = (dt, n, us, tp)
     m.close()
-    dt, n, us = res
+    dt, n, us, tp = res
     steps = B_WORDS - 1
     ms = 1000.0 * dt / steps
     hb = head_bytes(m.vocab)
@@ -120,6 +128,8 @@ def batched_leg(sm, lay):
             "ms_per_step": round(ms, 4), "steps": steps,
             "workload": f"{B_STREAMS} streams, {B_PROMPT}-token random prompts, {B_WORDS} greedy words each "
                         f"(context to {B_PROMPT + B_WORDS}); streams 0 and 1 checked against base2.py's golden words",
+            "prompt_included": {"value": round(B_STREAMS * B_WORDS / (tp + dt), 1), "unit": "tokens/s",
+                                "prompt_ms": round(1000.0 * tp, 3)},
             "roofline": {"bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                          "frac": round(ach / HBM_PEAK_GBS, 4), "kernel": "k_head_rows<4,EPI_HEAD>",
                          "mean_launch_us": round(us, 3), "launches_timed": n,
@@ -145,14 +155,18 @@ def pythia_leg(sm):
     want = {b: gw[f"py_c5_stream{b}_p64_w4"] for b in (0, 1)}
     del npz
     log(f"pythia: model converted and laid out in {time.time() - t0:.1f}s")
-    m = sm.Machine(lay, max_ctx=P_PROMPT + P_WORDS, max_streams=P_STREAMS, graph_steps=P_WORDS - 1, profile=True)
+    m = sm.Machine(lay, max_ctx=P_PROMPT + P_WORDS, max_streams=P_STREAMS, graph_steps=P_WORDS - 1, profile=True,
+                   prefill_rows=PREFILL_ROWS)
     res = None
     for it in range(2):                     # the first sequence warms up (graph instantiation)
         m.reset()
+        torch.cuda.synchronize()
+        t = time.perf_counter()
         for b, p in enumerate(prompts):
             m.prefill(p, b)
-        first = m.generate(1)
+        first = m.generate(1)               # the prompt pass and the first word
         torch.cuda.synchronize()
+        tp = time.perf_counter() - t
         m.profile(clear=True)
         t = time.perf_counter()
         rest = m.generate(P_WORDS - 1)
@@ -163,10 +177,10 @@ def pythia_leg(sm):
         for b, w in want.items():
             if [int(x) for x in words[b][:len(w)]] != w:
                 raise RuntimeError(f"pythia stream {b}: GPU words differ from pythia_base2.py's golden words")
-        res = (dt, n, us)
+        res = (dt, n, us, tp)
     vocab = m.vocab
     m.close()
-    dt, n, us = res
+    dt, n, us, tp = res
     steps = P_WORDS - 1
     ms = 1000.0 * dt / steps
     hb = head_bytes(vocab) - 8 * vocab                 # no bias on Pythia's head
@@ -178,6 +192,8 @@ def pythia_leg(sm):
             "workload": f"Pythia-160m-shaped integer machine, {P_STREAMS} streams, {P_PROMPT}-token random prompts, "
                         f"{P_WORDS} greedy words each (context to {P_PROMPT + P_WORDS}); streams 0 and 1 checked "
                         f"against pythia_base2.py's golden words",
+            "prompt_included": {"value": round(P_STREAMS * P_WORDS / (tp + dt), 1), "unit": "tokens/s",
+                                "prompt_ms": round(1000.0 * tp, 3)},
             "roofline": {"bound": "hbm", "achieved": round(hb / (us * 1e-6) / 1e9, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                          "frac": round(hb / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4), "kernel": "k_head_rows<2,EPI_PHEAD>",
                          "mean_launch_us": round(us, 3), "launches_timed": n},
@@ -228,6 +244,8 @@ def main():
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MB",
                     help="profiling: first copy MB MiB device to device (calibrates HBM byte counters)")
     ap.add_argument("--layout", default="", help="reuse a layout directory (else one is built in a temp dir)")
+    ap.add_argument("--prefill-rows", type=int, default=64,
+                    help="prompt rows a pass through the MFMA banks (0: the prompt position by position)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported (the batched streams would "
@@ -236,6 +254,8 @@ def main():
     if args.steps <= 0 or args.warmup < 0:
         sys.exit("bench.py: --steps must be positive and --warmup non-negative")
 
+    global PREFILL_ROWS
+    PREFILL_ROWS = args.prefill_rows
     sm = load_sm()
     if args.copy_probe:
         import torch
@@ -265,14 +285,18 @@ def main():
     want = golden_words("base2_golden.json")["c1_p8_w16"]
 
     import torch
-    m = sm.Machine(lay, max_ctx=64, head_grid=args.head_grid, graph_steps=WORDS - 1, profile=True)
+    m = sm.Machine(lay, max_ctx=64, head_grid=args.head_grid, graph_steps=WORDS - 1, profile=True,
+                   prefill_rows=PREFILL_ROWS)
     vocab = m.vocab
 
     def sequence(timed: bool):
         m.reset()
-        m.prefill(prompt)
-        first = int(m.generate(1)[0, 0])
         torch.cuda.synchronize()
+        t = time.perf_counter()
+        m.prefill(prompt)
+        first = int(m.generate(1)[0, 0])        # the prompt pass and the first word
+        torch.cuda.synchronize()
+        tp = time.perf_counter() - t
         m.profile(clear=True)
         t = time.perf_counter()
         rest = [int(w) for w in m.generate(WORDS - 1)[0]]
@@ -282,13 +306,15 @@ def main():
         if words != want:
             raise RuntimeError(f"GPU words differ from base2.py's golden words: {words} vs {want}")
         n, us = m.profile(clear=True)
-        return dt, n, us
+        return dt, n, us, tp
 
     for _ in range(max(1, -(-args.warmup // (WORDS - 1)))):
         sequence(False)
-    total, steps, head_n, head_us_sum = 0.0, 0, 0, 0.0
+    total, steps, head_n, head_us_sum, prompt_s, nseq = 0.0, 0, 0, 0.0, 0.0, 0
     while steps < args.steps:
-        dt, n, us = sequence(True)
+        dt, n, us, tp = sequence(True)
+        prompt_s += tp
+        nseq += 1
         k = min(WORDS - 1, args.steps - steps)
         total += dt * k / (WORDS - 1)
         steps += k
@@ -312,7 +338,8 @@ def main():
 
     m.close()
     if args.only == "b1":
-        print(json.dumps({"value": round(tok_s, 2), "ms_per_step": round(ms_per_step, 4), "head_us": round(head_us, 3)}), flush=True)
+        print(json.dumps({"value": round(tok_s, 2), "ms_per_step": round(ms_per_step, 4), "head_us": round(head_us, 3),
+                          "prompt_ms": round(1000.0 * prompt_s / nseq, 3)}), flush=True)
         return
     batched = None if args.no_batched else batched_leg(sm, lay)
     if batched:
@@ -333,6 +360,10 @@ def main():
                      "kernel": "k_gemv<768,8,4,PRO_GAUGE,EPI_HEAD> (head plate read; the race is its own launch)",
                      "bytes_per_launch": hb, "mean_launch_us": round(head_us, 3), "launches_timed": head_n},
         "step_roofline": {"bytes_per_step": int(sb), "achieved": round(step_ach, 1), "frac": round(step_ach / HBM_PEAK_GBS, 4)},
+        "prompt_included": {"value": round(WORDS / (prompt_s / nseq + ms_per_step * 1e-3 * (WORDS - 1)), 2), "unit": "tokens/s",
+                            "prompt_ms": round(1000.0 * prompt_s / nseq, 3),
+                            "note": "16 words per sequence over the prompt pass (7 prompt rows through the int8 MFMA "
+                                    "banks, then the first word's step) plus 15 decode steps"},
         "batched": batched,
         "pythia": pyleg,
         "cpu_baseline": cpu,

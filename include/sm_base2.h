@@ -44,6 +44,10 @@ typedef struct {
     int32_t profile;       /* 1: time every head launch with a HIP event pair on the machine's stream */
     int32_t table_mode;    /* 0: read the tables from memory; 1: recompute each entry from its formula when every
                               loaded entry matches it (checked on the device at create), else read the tables */
+    int32_t prefill_rows;  /* 0: the prompt runs position by position through the decode step; 1..64: every prompt
+                              position but the last runs through the int8 MFMA banks that many rows a pass, each
+                              weight read shared by the pass's rows (base2_stream.swift:74-91, 274-275: the
+                              prompt through each layer at once); the last position is the first decode step */
 } sm_config;
 
 /* Replaces base2_stream.swift:151-208 (device, pipelines, loading base2_gpu/ and its buffers) and

@@ -32,6 +32,7 @@ struct LightArgs {
     const int* csum; const int* we; const i64* bias;   // the producing plate's column facts
     i64* Y;                                       // [rows][K]: the epilogue's row (R: read and written)
     i64* rpile_in; i64* rout_in;                  // stream 0's record of the producing bank
+    const int* rowmap;                            // prompt rows (PRO_EMBED): stream << 16 | position per row
 };
 
 struct GemmArgs {
@@ -107,10 +108,12 @@ __global__ __launch_bounds__(NT) void k_light(LightArgs a) {
                 if (rec_in && a.rout_in) a.rout_in[k + j] = y;
             }
         } else if (PRO == PRO_EMBED) {
-            const i64 tok = a.seq[(size_t)r * a.seq_stride + p];
+            const int pm = a.rowmap ? a.rowmap[r] : 0;
+            const int st = a.rowmap ? pm >> 16 : r, q = a.rowmap ? pm & 0xFFFF : p;
+            const i64 tok = a.seq[(size_t)st * a.seq_stride + q];
 #pragma unroll
             for (int j = 0; j < 4; j++) {
-                v[m][j] = wadd(a.wte[tok * 768 + k + j], a.wpe[(i64)p * 768 + k + j]);
+                v[m][j] = wadd(a.wte[tok * 768 + k + j], a.wpe[(i64)q * 768 + k + j]);
                 a.Rw[(size_t)r * 768 + k + j] = v[m][j];
             }
         } else {
@@ -492,6 +495,7 @@ struct PyRowArgs {
     i64* rg1; i64* rx1; i64* rex1; i64* rg2; i64* rx2; i64* rex2;   // the gauges and their lights
     i64* rpileA; i64* routA; i64* rpileB; i64* routB;               // PY_ADD: stream after A, after A and B
     i64* rpre;                                                       // PY_EDGE: fc's row before the edge
+    const int* rowmap;                            // prompt rows (PY_EMBED): stream << 16 | position per row
 };
 enum { PY_EMBED = 0, PY_ADD = 1, PY_EDGE = 2 };
 
@@ -528,7 +532,8 @@ __global__ __launch_bounds__(MODE == PY_EDGE ? 768 : 192) void k_py_rows(PyRowAr
     constexpr int NT = MODE == PY_EDGE ? 768 : 192, NW = NT / 64;
     __shared__ int red[24 + 6 * 12];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, r = blockIdx.x;
-    const int p = *a.pos;
+    const int pm = a.rowmap ? a.rowmap[r] : 0;
+    const int p = a.rowmap ? pm & 0xFFFF : *a.pos, st = a.rowmap ? pm >> 16 : r;
     const bool rec = r == 0 && a.rec_pos && *a.rec_pos == p;
     if constexpr (MODE == PY_EDGE) {
         i64 v[1][4];
@@ -554,7 +559,7 @@ __global__ __launch_bounds__(MODE == PY_EDGE ? 768 : 192) void k_py_rows(PyRowAr
     i64 R4[4] = {0, 0, 0, 0};
     {
         if (MODE == PY_EMBED) {
-            const i64 tok = a.seq[(size_t)r * a.seq_stride + p];
+            const i64 tok = a.seq[(size_t)st * a.seq_stride + p];
             const i64 es = -((i64)a.ee[tok] + 16);
 #pragma unroll
             for (int j = 0; j < 4; j++) R4[j] = rsh((i64)a.ew[tok * 768 + k + j], es);

@@ -81,6 +81,9 @@ struct AttArgs {
     // the Pythia machine: turns on the first rot dims of q and k, the scores' half-log2(head size)
     const int* cosT; const int* sinT;   // [npos][rot / 2] at 2^-30
     int rot; i64 half; i64 ehalf;       // ehalf = EXP2[(-half) & 0xFFFF]
+    // prompt rows: row r is position rowmap[r] & 0xFFFF of stream rowmap[r] >> 16 (null: row r is stream r at
+    // *pos).  Their keys and values are in the cache already (k_kv_rows), so the attention only reads it.
+    const int* rowmap;
 };
 
 // error bits in the device error word

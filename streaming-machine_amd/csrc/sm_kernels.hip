@@ -547,8 +547,10 @@ __global__ __launch_bounds__(NTHR, ONE ? 1 : 3) void k_attend(AttArgs a) {
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int sl = tid >> 2, qd = tid & 3;                   // scores: position in the pass, lane of the position
     const int d4 = tid & 15, g = tid >> 4;                   // value sum: four dimensions, position group
-    const int h = blockIdx.x, b = blockIdx.y;
-    const int p = *a.pos;
+    const int h = blockIdx.x, b = blockIdx.y;               // b: the row (a stream, or a prompt position)
+    const int pm = a.rowmap ? a.rowmap[b] : 0;
+    const int p = a.rowmap ? pm & 0xFFFF : *a.pos, st = a.rowmap ? pm >> 16 : b;
+    const bool store = !a.rowmap;                            // prompt rows: k_kv_rows stored every row's k and v
     if constexpr (ONE) {
         if (p < 64) {                                        // one stream, short context: one wave, no barriers
             if (wave == 0) attend_short<MODEL>(a, p, h, b);
@@ -556,10 +558,10 @@ __global__ __launch_bounds__(NTHR, ONE ? 1 : 3) void k_attend(AttArgs a) {
         }
     }
     const i64* qkv = a.QKV + (size_t)b * 2304;
-    int* K16 = a.K16 + (size_t)b * a.ctx * 768;
-    int* EK = a.EK + (size_t)b * a.ctx * 12;
-    int* V = a.V + (size_t)b * a.ctx * 768;
-    const bool rec = b == 0 && a.rec_pos && *a.rec_pos == p;
+    int* K16 = a.K16 + (size_t)st * a.ctx * 768;
+    int* EK = a.EK + (size_t)st * a.ctx * 12;
+    int* V = a.V + (size_t)st * a.ctx * 768;
+    const bool rec = store && b == 0 && a.rec_pos && *a.rec_pos == p;
 
     // requests first (vector loads complete in order): the new q, k, v; then the cached keys of the first
     // ATT_PRE passes (a position's four lanes read its 256-byte row as 4 x 64 contiguous bytes: lane qd holds
@@ -608,14 +610,17 @@ __global__ __launch_bounds__(NTHR, ONE ? 1 : 3) void k_attend(AttArgs a) {
             if (lane == 0) eqs = -16 + sh;
         } else {
             k16s[lane] = x16;
-            K16[(size_t)p * 768 + h * 64 + lane] = x16;
-            if (lane == 0) { eks = -16 + sh; EK[(size_t)p * 12 + h] = -16 + sh; }
+            if (store) K16[(size_t)p * 768 + h * 64 + lane] = x16;
+            if (lane == 0) {
+                eks = -16 + sh;
+                if (store) EK[(size_t)p * 12 + h] = -16 + sh;
+            }
         }
     } else if (wave == 2) {
         const i64 x = xnew;
         if (x < (i64)INT32_MIN || x > (i64)INT32_MAX) atomicOr(a.err, SM_ERR_V32);
         vs[lane] = (int)x;
-        V[(size_t)p * 768 + h * 64 + lane] = (int)x;
+        if (store) V[(size_t)p * 768 + h * 64 + lane] = (int)x;
     }
     __syncthreads();
 
@@ -723,6 +728,35 @@ __global__ __launch_bounds__(NTHR, ONE ? 1 : 3) void k_attend(AttArgs a) {
     }
 }
 
+// Prompt rows (several positions of a stream in one pass): every row's key water level and value go into the
+// cache before any row's attention reads it (base2.py:93 for k; pythia_base2.py:116-123 turns k first).
+// Grid (12 heads, rows), two waves: the key, the value.
+template <int MODEL>
+__global__ __launch_bounds__(128) void k_kv_rows(AttArgs a) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, h = blockIdx.x, r = blockIdx.y;
+    const int pm = a.rowmap[r], st = pm >> 16, p = pm & 0xFFFF;
+    const size_t at = (size_t)st * a.ctx + p;               // the row's cache slot
+    i64 x = a.QKV[(size_t)r * 2304 + (MODEL == 1 ? h * 192 + (wave + 1) * 64 + lane : (wave + 1) * 768 + h * 64 + lane)];
+    if (wave == 0) {
+        if (MODEL == 1) {                                    // the turn, pair (i, i + rot/2)
+            const int hr = a.rot >> 1;
+            const i64 partner = __shfl(x, lane < hr ? lane + hr : lane - hr, 64);
+            if (lane < a.rot) {
+                if (iabs64(x) >= ((i64)1 << 31)) atomicOr(a.err, SM_ERR_RANGE);
+                const int i = lane < hr ? lane : lane - hr;
+                const i64 c = a.cosT[(size_t)p * hr + i], sn = a.sinT[(size_t)p * hr + i];
+                x = lane < hr ? rsh(wsub(wmul(x, c), wmul(partner, sn)), 30) : rsh(wadd(wmul(x, c), wmul(partner, sn)), 30);
+            }
+        }
+        const int sh = water_shift(wave_or64(iabs64(x)));
+        a.K16[at * 768 + h * 64 + lane] = (int)rsh(x, sh);
+        if (lane == 0) a.EK[at * 12 + h] = -16 + sh;
+    } else {
+        if (x < (i64)INT32_MIN || x > (i64)INT32_MAX) atomicOr(a.err, SM_ERR_V32);
+        a.V[at * 768 + h * 64 + lane] = (int)x;
+    }
+}
+
 // ---------------------------------------------------------------------------------------------------------
 // Exhaustive check of the loaded tables against their defining formulas (sets Tables.arith when all agree).
 __global__ void k_check_tables(Tables tb, unsigned* bad) {
@@ -819,6 +853,8 @@ template __global__ void k_attend<0, 0>(AttArgs);
 template __global__ void k_attend<0, 1>(AttArgs);
 template __global__ void k_attend<1, 0>(AttArgs);
 template __global__ void k_attend<1, 1>(AttArgs);
+template __global__ void k_kv_rows<0>(AttArgs);
+template __global__ void k_kv_rows<1>(AttArgs);
 // raw piles of a given light (stage entry point)
 INST(768, 2, 4, PRO_X16, EPI_PILE)
 INST(768, 8, 4, PRO_X16, EPI_PILE)

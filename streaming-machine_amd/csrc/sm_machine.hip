@@ -212,6 +212,7 @@ static const char* BANK[4] = {"qkv", "proj", "fc", "mproj"};
 struct sm_machine {
     sm_config cfg{};
     int B = 1, ctx = 0, vocab = 0, npos = 0, head_grid = 1024;
+    int RC = 1;                    // rows the MFMA phases hold: the streams, or a pass of prompt rows
     hipStream_t st = nullptr;
     DevPlate bank[12][4];          // batch 1: GEMV tiles
     DevPlate head;
@@ -251,8 +252,12 @@ struct sm_machine {
     std::vector<hipEvent_t> ev_s, ev_e;
     double prof_head_us = 0.0;
     long long prof_n = 0;
+    // prompt passes: row r of a pass is position pfmap[r] & 0xFFFF of stream pfmap[r] >> 16
+    int* pfmap = nullptr;                               // [B][ctx]
+    std::vector<int> h_pfmap;
+    int h_pfpos = 0;
     // host mirror
-    int h_plen = 0, h_pos = 0, h_words = 0;
+    int h_plen = 0, h_pos = 0, h_words = 0, h_recpos = -1;
     std::vector<std::vector<int>> prompts;
 };
 
@@ -352,7 +357,7 @@ static void machine_free(sm_machine* m) {
     free_plate(m->head);
     free_mfma_plate(m->mhead);
     tables_free(m->T);
-    void* ps[] = {m->planes, m->part_acc, m->rowinfo, m->wte, m->wpe, m->R, m->QKV, m->att, m->hid, m->K16, m->EK, m->V, m->seq, m->words, m->ctl,
+    void* ps[] = {m->pfmap, m->planes, m->part_acc, m->rowinfo, m->wte, m->wpe, m->R, m->QKV, m->att, m->hid, m->K16, m->EK, m->V, m->seq, m->words, m->ctl,
                   m->part_v, m->part_i, m->r_x16, m->r_exls, m->r_pile, m->r_qkv, m->r_att, m->r_hid, m->r_resid,
                   m->r_hx16, m->r_hexls, m->r_hpile, m->r_logits, m->r_gauge, m->r_fcpre, m->r_hgauge,
                   m->fg, m->fb, m->ew, m->ee, m->cosT, m->sinT};
@@ -370,17 +375,23 @@ enum { STEP_ALL = 3, STEP_LAYERS = 1, STEP_HEAD = 2 };
 static int head_rows_grid(int ntiles) { return std::min(512, ntiles); }
 
 // batched streams: every bank is [light kernel (one block per stream) -> MFMA kernel (one block per 16 columns)]
+//
+// rowmap != null: a pass of nrows prompt rows (row r: position rowmap[r] & 0xFFFF of stream rowmap[r] >> 16)
+// instead of one position of every stream.  Their words are known, so no head runs, and the last layer only
+// stores keys and values (its attention and banks feed the head alone); nothing is recorded.
 template <int RT>
-static int launch_step_batched(sm_machine* m, int parts, hipEvent_t hs, hipEvent_t he) {
+static int launch_step_batched(sm_machine* m, int parts, hipEvent_t hs, hipEvent_t he, int nrows = 0,
+                               const int* rowmap = nullptr) {
     const Tables tb = m->T.tb();
     int* ctl = m->ctl;
-    const int B = m->B;
+    const int B = rowmap ? nrows : m->B;
+    const int* recp = rowmap ? nullptr : ctl + CTL_RECPOS;
     auto light_args = [&](int K, const i64* X, i64* rx16, i64* rexls) {
         LightArgs a{};
         a.K = K; a.rows = B; a.X = X; a.wte = m->wte; a.wpe = m->wpe; a.seq = m->seq; a.seq_stride = m->ctx + 1;
         a.Rw = m->R; a.pos = ctl + CTL_POS; a.plen = ctl + CTL_PLEN;
         a.planes = m->planes; a.rowinfo = m->rowinfo; a.tb = tb;
-        a.rec_pos = ctl + CTL_RECPOS; a.rx16 = rx16; a.rexls = rexls;
+        a.rec_pos = recp; a.rx16 = rx16; a.rexls = rexls; a.rowmap = rowmap;
         return a;
     };
     // the producing bank's epilogue (from its partial accumulators) followed by the next light
@@ -395,7 +406,7 @@ static int launch_step_batched(sm_machine* m, int parts, hipEvent_t hs, hipEvent
         GemmArgs a{};
         a.K = P.K; a.N = P.N; a.rows = B; a.RT = RT; a.W = P.W; a.csum = P.csum; a.we = P.e; a.bias = P.b;
         a.planes = m->planes; a.rowinfo = m->rowinfo; a.Y = Y; a.ystride = ystride; a.tb = tb;
-        a.pos = ctl + CTL_POS; a.plen = ctl + CTL_PLEN; a.rec_pos = ctl + CTL_RECPOS; a.rpile = rpile; a.rout = rout;
+        a.pos = ctl + CTL_POS; a.plen = ctl + CTL_PLEN; a.rec_pos = recp; a.rpile = rpile; a.rout = rout;
         a.part = m->part_acc;
         return a;
     };
@@ -416,9 +427,16 @@ static int launch_step_batched(sm_machine* m, int parts, hipEvent_t hs, hipEvent
             const size_t per = (size_t)m->B * m->ctx;
             a.QKV = m->QKV; a.K16 = m->K16 + l * per * 768; a.EK = m->EK + l * per * 12; a.V = m->V + l * per * 768;
             a.out = m->att; a.pos = ctl + CTL_POS; a.ctx = m->ctx; a.tb = tb; a.err = ctl + CTL_ERR;
-            a.rec_pos = ctl + CTL_RECPOS; a.ratt = m->r_att + l * 768;
-            if (m->B == 1) k_attend<0, 1><<<dim3(12, 1), NTHR, (size_t)m->ctx * 12, m->st>>>(a);
-            else k_attend<0, 0><<<dim3(12, m->B), NTHR, (size_t)m->ctx * 12, m->st>>>(a);
+            a.rec_pos = recp; a.ratt = m->r_att + l * 768; a.rowmap = rowmap;
+            if (rowmap) {
+                k_kv_rows<0><<<dim3(12, B), 128, 0, m->st>>>(a);
+                if (l == 11) break;
+                k_attend<0, 0><<<dim3(12, B), NTHR, (size_t)m->ctx * 12, m->st>>>(a);
+            } else if (m->B == 1) {
+                k_attend<0, 1><<<dim3(12, 1), NTHR, (size_t)m->ctx * 12, m->st>>>(a);
+            } else {
+                k_attend<0, 0><<<dim3(12, m->B), NTHR, (size_t)m->ctx * 12, m->st>>>(a);
+            }
         }
         {
             LightArgs a = light_args(768, m->att, rx + 3072, re + 2);
@@ -442,7 +460,7 @@ static int launch_step_batched(sm_machine* m, int parts, hipEvent_t hs, hipEvent
         finish_light(m->mbank[l][3], 4, m->R, rp + 3 * 3072, m->r_resid + (l * 2 + 1) * 768,
                      last ? m->r_hx16 : m->r_x16 + (size_t)(l + 1) * 4 * 3072, last ? m->r_hexls : m->r_exls + (size_t)(l + 1) * 4 * 2);
     }
-    if (parts & STEP_HEAD) {
+    if ((parts & STEP_HEAD) && !rowmap) {
         GemmArgs a = gemm_args(m->mhead, nullptr, 0, m->r_hpile, nullptr);
         // the head: each wave's row tile of lights in registers, weight tiles streamed through LDS
         const int grid = head_rows_grid(m->mhead.ntiles), parts = grid;
@@ -564,29 +582,32 @@ static int launch_step_pythia(sm_machine* m, int parts, hipEvent_t hs, hipEvent_
 // -> mproj, 3072 wide), D (attention row -> proj); partials: fc and mproj share region 0 (fc's are finished
 // before mproj writes), proj's follow mproj's.  The last row kernel of a layer adds both halves to the stream
 // (the parallel residual) and lights the next layer's two gauges, or the head's.
+// rowmap != null: a pass of nrows prompt rows, as in launch_step_batched.
 template <int RT>
-static int launch_step_pythia_batched(sm_machine* m, int parts, hipEvent_t hs, hipEvent_t he) {
+static int launch_step_pythia_batched(sm_machine* m, int parts, hipEvent_t hs, hipEvent_t he, int nrows = 0,
+                                      const int* rowmap = nullptr) {
     const Tables tb = m->T.tb();
     int* ctl = m->ctl;
-    const int B = m->B;
-    const size_t PL = (size_t)4 * 48 * 3 * 1024;
+    const int B = rowmap ? nrows : m->B;
+    const int* recp = rowmap ? nullptr : ctl + CTL_RECPOS;
+    const size_t PL = (size_t)4 * 48 * 3 * 1024, RC = m->RC;
     signed char* pA = m->planes; signed char* pB = m->planes + PL; signed char* pC = m->planes + 2 * PL;
     signed char* pD = m->planes + 3 * PL;
-    int* rA = m->rowinfo; int* rB = m->rowinfo + (size_t)B * 8; int* rC = m->rowinfo + (size_t)2 * B * 8;
-    int* rD = m->rowinfo + (size_t)3 * B * 8;
+    int* rA = m->rowinfo; int* rB = m->rowinfo + RC * 8; int* rC = m->rowinfo + 2 * RC * 8;
+    int* rD = m->rowinfo + 3 * RC * 8;
     int* P0 = m->part_acc;
-    int* P3 = m->part_acc + (size_t)4 * 3 * B * 768;
+    int* P3 = m->part_acc + 4 * 3 * RC * 768;
     auto gemm_args = [&](const MfmaPlate& P, signed char* planes, int* rowinfo) {
         GemmArgs a{};
         a.K = P.K; a.N = P.N; a.rows = B; a.RT = RT; a.W = P.W; a.csum = P.csum; a.we = P.e; a.bias = P.b;
         a.planes = planes; a.rowinfo = rowinfo; a.tb = tb;
-        a.pos = ctl + CTL_POS; a.plen = ctl + CTL_PLEN; a.rec_pos = ctl + CTL_RECPOS;
+        a.pos = ctl + CTL_POS; a.plen = ctl + CTL_PLEN; a.rec_pos = recp;
         return a;
     };
     auto rows_args = [&]() {
         PyRowArgs a{};
         a.rows = B; a.R = m->R; a.ew = m->ew; a.ee = m->ee; a.seq = m->seq; a.seq_stride = m->ctx + 1; a.pos = ctl + CTL_POS;
-        a.tb = tb; a.rec_pos = ctl + CTL_RECPOS;
+        a.tb = tb; a.rec_pos = recp; a.rowmap = rowmap;
         return a;
     };
     auto gauges = [&](PyRowArgs& a, int l) {       // the two gauges of layer l (l == 12: lnf for the head)
@@ -613,6 +634,15 @@ static int launch_step_pythia_batched(sm_machine* m, int parts, hipEvent_t hs, h
             a.Y = m->QKV; a.ystride = 2304; a.rpile = rp; a.rout = m->r_qkv + l * 2304;
             k_gemm<768, RT, 1, EPI_PLAIN><<<m->mbank[l][0].ntiles, 256, 0, m->st>>>(a);
         }
+        if (rowmap && l == 11) {   // prompt rows: the last layer only stores its keys and values
+            AttArgs a{};
+            const size_t per = (size_t)m->B * m->ctx;
+            a.QKV = m->QKV; a.K16 = m->K16 + l * per * 768; a.EK = m->EK + l * per * 12; a.V = m->V + l * per * 768;
+            a.ctx = m->ctx; a.tb = tb; a.err = ctl + CTL_ERR; a.rowmap = rowmap;
+            a.cosT = m->cosT; a.sinT = m->sinT; a.rot = m->rot; a.half = m->half; a.ehalf = m->ehalf;
+            k_kv_rows<1><<<dim3(12, B), 128, 0, m->st>>>(a);
+            break;
+        }
         {   // fc: partials, then edge and the 3072-wide light
             GemmArgs a = gemm_args(m->mbank[l][2], pB, rB);
             a.part = P0;
@@ -632,17 +662,18 @@ static int launch_step_pythia_batched(sm_machine* m, int parts, hipEvent_t hs, h
         }
         {   // attention with turns
             AttArgs a{};
-            const size_t per = (size_t)B * m->ctx;
+            const size_t per = (size_t)m->B * m->ctx;
             a.QKV = m->QKV; a.K16 = m->K16 + l * per * 768; a.EK = m->EK + l * per * 12; a.V = m->V + l * per * 768;
             a.out = m->att; a.pos = ctl + CTL_POS; a.ctx = m->ctx; a.tb = tb; a.err = ctl + CTL_ERR;
-            a.rec_pos = ctl + CTL_RECPOS; a.ratt = m->r_att + l * 768;
+            a.rec_pos = recp; a.ratt = m->r_att + l * 768; a.rowmap = rowmap;
             a.cosT = m->cosT; a.sinT = m->sinT; a.rot = m->rot; a.half = m->half; a.ehalf = m->ehalf;
+            if (rowmap) k_kv_rows<1><<<dim3(12, B), 128, 0, m->st>>>(a);
             k_attend<1, 0><<<dim3(12, B), NTHR, (size_t)m->ctx * 12, m->st>>>(a);
         }
         {   // the attention row's light, then proj's partials
             LightArgs a{};
             a.K = 768; a.rows = B; a.X = m->att; a.pos = ctl + CTL_POS; a.plen = ctl + CTL_PLEN;
-            a.planes = pD; a.rowinfo = rD; a.tb = tb; a.rec_pos = ctl + CTL_RECPOS;
+            a.planes = pD; a.rowinfo = rD; a.tb = tb; a.rec_pos = recp;
             a.rx16 = m->r_x16 + (l * 4 + 1) * 3072; a.rexls = m->r_exls + (l * 4 + 1) * 2;
             k_light<768, PRO_TO16, 192><<<B, 192, 0, m->st>>>(a);
             GemmArgs g = gemm_args(m->mbank[l][1], pD, rD);
@@ -661,7 +692,7 @@ static int launch_step_pythia_batched(sm_machine* m, int parts, hipEvent_t hs, h
             k_py_rows<PY_ADD><<<B, 192, 0, m->st>>>(a);
         }
     }
-    if (parts & STEP_HEAD) {
+    if ((parts & STEP_HEAD) && !rowmap) {
         GemmArgs a = gemm_args(m->mhead, pA, rA);
         a.rpile = m->r_hpile;
         const int grid = head_rows_grid(m->mhead.ntiles);
@@ -776,12 +807,44 @@ static int launch_step(sm_machine* m, int parts = STEP_ALL, hipEvent_t hs = null
     return SM_OK;
 }
 
+// positions [0, npos) of every stream as passes of up to prefill_rows prompt rows, stream by stream (rows of one
+// stream in position order, so a pass's keys and values at earlier positions are cached before it runs); then the
+// device position moves to npos.  Nothing is recorded: the caller stops short of a recorded position.
+static int run_prefill(sm_machine* m, int npos) {
+    const int total = m->B * npos, chunk = m->cfg.prefill_rows;
+    m->h_pfmap.resize(total);
+    for (int s = 0; s < m->B; s++)
+        for (int q = 0; q < npos; q++) m->h_pfmap[(size_t)s * npos + q] = s << 16 | q;
+    HIP_TRY(hipMemcpyAsync(m->pfmap, m->h_pfmap.data(), (size_t)total * 4, hipMemcpyHostToDevice, m->st));
+    for (int r0 = 0; r0 < total; r0 += chunk) {
+        const int n = std::min(chunk, total - r0), RT = (n + 15) / 16;
+        const int* map = m->pfmap + r0;
+        int rc;
+        if (m->kind == 1) {
+            rc = RT == 1 ? launch_step_pythia_batched<1>(m, STEP_LAYERS, nullptr, nullptr, n, map)
+               : RT == 2 ? launch_step_pythia_batched<2>(m, STEP_LAYERS, nullptr, nullptr, n, map)
+               : RT == 3 ? launch_step_pythia_batched<3>(m, STEP_LAYERS, nullptr, nullptr, n, map)
+                         : launch_step_pythia_batched<4>(m, STEP_LAYERS, nullptr, nullptr, n, map);
+        } else {
+            rc = RT == 1 ? launch_step_batched<1>(m, STEP_LAYERS, nullptr, nullptr, n, map)
+               : RT == 2 ? launch_step_batched<2>(m, STEP_LAYERS, nullptr, nullptr, n, map)
+               : RT == 3 ? launch_step_batched<3>(m, STEP_LAYERS, nullptr, nullptr, n, map)
+                         : launch_step_batched<4>(m, STEP_LAYERS, nullptr, nullptr, n, map);
+        }
+        if (rc) return rc;
+    }
+    m->h_pfpos = npos;
+    HIP_TRY(hipMemcpyAsync(m->ctl + CTL_POS, &m->h_pfpos, 4, hipMemcpyHostToDevice, m->st));
+    return SM_OK;
+}
+
 extern "C" int sm_create(const char* layout_dir, const sm_config* cfg, sm_machine** out) {
     if (!layout_dir || !out) return fail(SM_E_ARG, "sm_create: null argument");
     *out = nullptr;
-    sm_config c{1, 1024, 1, 0, 16, 0, 0};
+    sm_config c{1, 1024, 1, 0, 16, 0, 0, 64};
     if (cfg) c = *cfg;
     if (c.max_streams < 1 || c.max_streams > 64) return fail(SM_E_ARG, "sm_create: max_streams must be in [1, 64]");
+    if (c.prefill_rows < 0 || c.prefill_rows > 64) return fail(SM_E_ARG, "sm_create: prefill_rows must be in [0, 64]");
     if (c.max_ctx <= 0) return fail(SM_E_ARG, "sm_create: max_ctx must be positive");
     const std::string dir = std::string(layout_dir) + "/";
     std::vector<char> mj;
@@ -807,7 +870,9 @@ extern "C" int sm_create(const char* layout_dir, const sm_config* cfg, sm_machin
     sm_machine* m = new sm_machine();
     m->cfg = c;
     m->B = c.max_streams;
+    m->RC = std::max(m->B, c.prefill_rows);
     m->kind = py ? 1 : 0;
+    const bool mfma = m->B > 1 || c.prefill_rows > 0;     // the MFMA banks: batched streams or prompt passes
 
     auto bail = [&](int code) { machine_free(m); return code; };
     {
@@ -825,7 +890,7 @@ extern "C" int sm_create(const char* layout_dir, const sm_config* cfg, sm_machin
                 (rc = read_array(dir + name + ".b", b, NOUT[k])))
                 return bail(rc);
             if (m->B == 1 && (rc = upload_plate(m->bank[l][k], w.data(), e.data(), b.data(), NIN[k], NOUT[k], TCOLS[k]))) return bail(rc);
-            if (m->B > 1 && (rc = upload_mfma_plate(m->mbank[l][k], w.data(), e.data(), b.data(), NIN[k], NOUT[k]))) return bail(rc);
+            if (mfma && (rc = upload_mfma_plate(m->mbank[l][k], w.data(), e.data(), b.data(), NIN[k], NOUT[k]))) return bail(rc);
         }
     }
     const BankInfo* hb = find("head");
@@ -911,15 +976,16 @@ extern "C" int sm_create(const char* layout_dir, const sm_config* cfg, sm_machin
     m->head_grid = c.head_grid > 0 ? c.head_grid : 256;     // one block per CU (measured best)
     const size_t nparts = m->B == 1 ? (size_t)m->head_grid : (size_t)m->B * head_rows_grid((m->vocab + 15) / 16);
     // state
-    const size_t B = m->B, ctx = m->ctx;
-    const size_t nsets = m->kind == 1 && m->B > 1 ? 4 : 1;      // light-plane sets (the batched Pythia machine keeps four)
-    if ((rc = dalloc(&m->R, B * 768)) || (rc = dalloc(&m->QKV, B * 2304)) || (rc = dalloc(&m->att, B * 768)) ||
-        (rc = dalloc(&m->hid, B * 3072)) || (rc = dalloc(&m->K16, 12 * B * ctx * 768)) || (rc = dalloc(&m->EK, 12 * B * ctx * 12)) ||
+    const size_t B = m->B, ctx = m->ctx, RC = m->RC;
+    const size_t nsets = m->kind == 1 && mfma ? 4 : 1;      // light-plane sets (the Pythia MFMA phases keep four)
+    if ((rc = dalloc(&m->R, RC * 768)) || (rc = dalloc(&m->QKV, RC * 2304)) || (rc = dalloc(&m->att, RC * 768)) ||
+        (rc = dalloc(&m->hid, RC * 3072)) || (rc = dalloc(&m->K16, 12 * B * ctx * 768)) || (rc = dalloc(&m->EK, 12 * B * ctx * 12)) ||
+        (rc = dalloc(&m->pfmap, B * ctx)) ||
         (rc = dalloc(&m->V, 12 * B * ctx * 768)) || (rc = dalloc(&m->seq, B * (ctx + 1))) || (rc = dalloc(&m->words, B * (ctx + 1))) ||
         (rc = dalloc(&m->ctl, (size_t)CTL_N)) || (rc = dalloc(&m->part_v, nparts)) ||
         (rc = dalloc(&m->part_i, nparts)) || (rc = dalloc(&m->r_x16, (size_t)12 * 4 * 3072)) ||
-        (rc = dalloc(&m->planes, (size_t)4 * 48 * 3 * 1024 * nsets)) || (rc = dalloc(&m->rowinfo, (size_t)m->B * 8 * nsets)) ||
-        (rc = dalloc(&m->part_acc, m->B > 1 ? (size_t)4 * 3 * m->B * 3072 : (size_t)1)) ||
+        (rc = dalloc(&m->planes, (size_t)4 * 48 * 3 * 1024 * nsets)) || (rc = dalloc(&m->rowinfo, RC * 8 * nsets)) ||
+        (rc = dalloc(&m->part_acc, mfma ? (size_t)4 * 3 * RC * 3072 : (size_t)1)) ||
         (rc = dalloc(&m->r_exls, (size_t)12 * 4 * 2)) || (rc = dalloc(&m->r_pile, (size_t)12 * 4 * 3072)) ||
         (rc = dalloc(&m->r_qkv, (size_t)12 * 2304)) || (rc = dalloc(&m->r_att, (size_t)12 * 768)) ||
         (rc = dalloc(&m->r_hid, (size_t)12 * 3072)) || (rc = dalloc(&m->r_resid, (size_t)12 * 2 * 768)) ||
@@ -927,7 +993,7 @@ extern "C" int sm_create(const char* layout_dir, const sm_config* cfg, sm_machin
         (rc = dalloc(&m->r_logits, (size_t)m->vocab)) || (rc = dalloc(&m->r_gauge, (size_t)12 * 2 * 768)) ||
         (rc = dalloc(&m->r_fcpre, (size_t)12 * 3072)) || (rc = dalloc(&m->r_hgauge, (size_t)768)))
         return bail(rc);
-    if (hipMemset(m->planes, 0, (size_t)4 * 48 * 3 * 1024 * nsets) != hipSuccess || hipMemset(m->rowinfo, 0, (size_t)m->B * 32 * nsets) != hipSuccess)
+    if (hipMemset(m->planes, 0, (size_t)4 * 48 * 3 * 1024 * nsets) != hipSuccess || hipMemset(m->rowinfo, 0, RC * 32 * nsets) != hipSuccess)
         return bail(fail(SM_E_HIP, "hipMemset planes"));
     m->prompts.assign(B, {});
     m->gsteps = c.graph_steps > 0 ? c.graph_steps : 16;
@@ -963,9 +1029,10 @@ extern "C" int sm_reset(sm_machine* m) {
     HIP_TRY(hipMemsetAsync(m->V, 0, 12 * B * ctx * 768 * 4, m->st));
     HIP_TRY(hipMemsetAsync(m->seq, 0, B * (ctx + 1) * 4, m->st));
     HIP_TRY(hipMemsetAsync(m->words, 0, B * (ctx + 1) * 4, m->st));
-    HIP_TRY(hipMemsetAsync(m->R, 0, B * 768 * 8, m->st));
+    HIP_TRY(hipMemsetAsync(m->R, 0, (size_t)m->RC * 768 * 8, m->st));
     HIP_TRY(hipStreamSynchronize(m->st));
     m->h_plen = m->h_pos = m->h_words = 0;
+    m->h_recpos = -1;
     for (auto& p : m->prompts) p.clear();
     return SM_OK;
 }
@@ -985,6 +1052,7 @@ extern "C" int sm_prefill(sm_machine* m, int32_t stream, const int32_t* ids, int
 extern "C" int sm_record_at(sm_machine* m, int32_t pos) {
     if (!m) return fail(SM_E_ARG, "sm_record_at: null machine");
     HIP_TRY(hipMemcpy(m->ctl + CTL_RECPOS, &pos, 4, hipMemcpyHostToDevice));
+    m->h_recpos = pos;
     return SM_OK;
 }
 
@@ -1031,18 +1099,28 @@ static int collect(sm_machine* m, int n) {
 extern "C" int sm_generate(sm_machine* m, int32_t n_words, int32_t* out) {
     if (!m) return fail(SM_E_ARG, "sm_generate: null machine");
     if (n_words <= 0) return fail(SM_E_ARG, "sm_generate: n_words must be positive");
-    if (m->h_pos == 0) {
+    const bool first = m->h_pos == 0;
+    if (first) {
         size_t n = m->prompts[0].size();
         for (int b = 0; b < m->B; b++)
             if (m->prompts[b].empty() || m->prompts[b].size() != n) return fail(SM_E_STATE, "sm_generate: every stream needs a prompt of the same length");
         m->h_plen = (int)n;
-        HIP_TRY(hipMemcpyAsync(m->ctl + CTL_PLEN, &m->h_plen, 4, hipMemcpyHostToDevice, m->st));
     }
     const int target = m->h_words + n_words;
-    int steps = (m->h_plen - 1 + target) - m->h_pos;
     if (m->h_plen - 1 + target > m->ctx) return fail(SM_E_CTX, "sm_generate: prompt + words would pass max_ctx");
-    const int total = steps;
     int rc;
+    if (first) {
+        HIP_TRY(hipMemcpyAsync(m->ctl + CTL_PLEN, &m->h_plen, 4, hipMemcpyHostToDevice, m->st));
+        // the prompt's positions but its last in passes of rows (not past a recorded position)
+        int npos = m->h_plen - 1;
+        if (m->h_recpos >= 0 && m->h_recpos < npos) npos = m->h_recpos;
+        if (m->cfg.prefill_rows > 0 && npos > 0) {
+            if ((rc = run_prefill(m, npos))) return rc;
+            m->h_pos = npos;
+        }
+    }
+    int steps = (m->h_plen - 1 + target) - m->h_pos;
+    const int total = steps;
     if (m->cfg.profile) {
         while (steps > 0) {
             const int n = steps < m->gsteps ? steps : m->gsteps;

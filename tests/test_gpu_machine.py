@@ -151,11 +151,12 @@ def test_errors(full_machine, sm):
     assert e.value.code == -5
 
 
-@pytest.mark.parametrize("use_graph", [True, False])
-def test_profiled_machine_gives_the_same_words(sm, full_dir, golden, use_graph):
+@pytest.mark.parametrize("use_graph,rows", [(True, 64), (False, 64), (True, 0)])
+def test_profiled_machine_gives_the_same_words(sm, full_dir, golden, use_graph, rows):
+    """one timed head per decode step: the steps after the prompt pass (rows > 0), or every position (rows = 0)"""
     c = golden_case(golden, "c1_p8_w16")
-    m = sm.Machine(full_dir, max_ctx=64, profile=True, graph_steps=4, use_graph=use_graph)
+    m = sm.Machine(full_dir, max_ctx=64, profile=True, graph_steps=4, use_graph=use_graph, prefill_rows=rows)
     assert m.stream(c["prompt"], len(c["words"])) == c["words"]
     n, us = m.profile()
-    assert n == len(c["prompt"]) + len(c["words"]) - 1 and us > 0
+    assert n == len(c["words"]) + (len(c["prompt"]) - 1 if rows == 0 else 0) and us > 0
     m.close()

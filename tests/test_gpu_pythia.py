@@ -112,13 +112,13 @@ def test_long_context_against_oracle(sm, py_small_dir, py_small_oracle):
     m.close()
 
 
-@pytest.mark.parametrize("use_graph", [True, False])
-def test_profiled_machine(sm, py_small_dir, pgolden, use_graph):
+@pytest.mark.parametrize("use_graph,rows", [(True, 64), (False, 64), (True, 0)])
+def test_profiled_machine(sm, py_small_dir, pgolden, use_graph, rows):
     c = small_cases(pgolden)[0]
-    m = sm.Machine(py_small_dir, max_ctx=64, profile=True, graph_steps=4, use_graph=use_graph)
+    m = sm.Machine(py_small_dir, max_ctx=64, profile=True, graph_steps=4, use_graph=use_graph, prefill_rows=rows)
     assert m.stream(c["prompt"], len(c["words"])) == c["words"]
     n, us = m.profile()
-    assert n == len(c["prompt"]) + len(c["words"]) - 1 and us > 0
+    assert n == len(c["words"]) + (len(c["prompt"]) - 1 if rows == 0 else 0) and us > 0
     m.close()
 
 
