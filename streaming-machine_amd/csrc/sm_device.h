@@ -193,11 +193,28 @@ SMD i64 wave_colsum64(i64 v) {
 }
 
 // ---------------- 64-wide wavefront reductions ----------------
-SMD i64 wave_or64(i64 v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v |= __shfl_xor(v, o, 64);
-    return v;
+struct OpOr { static constexpr i64 id = 0; SMD i64 operator()(i64 a, i64 b) const { return a | b; } };
+struct OpAdd { static constexpr i64 id = 0; SMD i64 operator()(i64 a, i64 b) const { return (i64)((u64)a + (u64)b); } };
+struct OpMax { static constexpr i64 id = INT64_MIN; SMD i64 operator()(i64 a, i64 b) const { return a > b ? a : b; } };
+// a 64-bit value moved by one DPP step (both words by the same control); lanes the step does not write get id
+template <int CTRL, int RM, int BM>
+SMD i64 dpp64(i64 v, i64 id) {
+    const int lo = __builtin_amdgcn_update_dpp((int)id, (int)v, CTRL, RM, BM, false);
+    const int hi = __builtin_amdgcn_update_dpp((int)(id >> 32), (int)(v >> 32), CTRL, RM, BM, false);
+    return (i64)(((u64)(unsigned)hi << 32) | (unsigned)lo);
 }
+// the whole wave's op-total of a 64-bit value (the wave_add32 pattern: row shifts, then the two row broadcasts),
+// read from lane 63 into uniform registers
+template <class F>
+SMD i64 wave_reduce64(i64 v, F op) {
+    constexpr i64 id = F::id;
+    v = op(v, dpp64<0x111, 0xf, 0xf>(v, id)); v = op(v, dpp64<0x112, 0xf, 0xf>(v, id));
+    v = op(v, dpp64<0x114, 0xf, 0xe>(v, id)); v = op(v, dpp64<0x118, 0xf, 0xc>(v, id));
+    v = op(v, dpp64<0x142, 0xa, 0xf>(v, id)); v = op(v, dpp64<0x143, 0xc, 0xf>(v, id));
+    const int lo = __builtin_amdgcn_readlane((int)v, 63), hi = __builtin_amdgcn_readlane((int)(v >> 32), 63);
+    return (i64)(((u64)(unsigned)hi << 32) | (unsigned)lo);
+}
+SMD i64 wave_or64(i64 v) { return wave_reduce64(v, OpOr()); }
 
 // sdot2: acc + a.lo * b.lo + a.hi * b.hi for packed int16 pairs (no clamp: callers bound the sums)
 SMD int dot2(int a, int b, int acc) {

@@ -26,8 +26,7 @@ typedef int v4i __attribute__((ext_vector_type(4)));
 template <typename F>
 SMD i64 block_reduce(i64 v, i64* red, F op, int tid) {
     const int lane = tid & 63, wave = tid >> 6;
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v = op(v, (i64)__shfl_xor(v, o, 64));
+    v = wave_reduce64(v, op);
     if (lane == 0) red[wave] = v;
     __syncthreads();
     i64 r = op(op(red[0], red[1]), op(red[2], red[3]));
@@ -45,9 +44,6 @@ SMD void block_sum2(i64& a, i64& b, i64* red, int tid) {
     b = red[4] + red[5] + red[6] + red[7];
     __syncthreads();
 }
-struct OpOr { SMD i64 operator()(i64 a, i64 b) const { return a | b; } };
-struct OpAdd { SMD i64 operator()(i64 a, i64 b) const { return (i64)((u64)a + (u64)b); } };
-struct OpMax { SMD i64 operator()(i64 a, i64 b) const { return a > b ? a : b; } };
 
 // ---------------------------------------------------------------------------------------------------------
 // Prologue: the light entering the plate, computed by every block from the row it reads (NIN values over the
@@ -476,41 +472,41 @@ SMD void attend_short(const AttArgs& a, int p, int h, int b) {
         dot += (i64)__builtin_amdgcn_readlane(q16, 4 * c) * krow[c].x + (i64)__builtin_amdgcn_readlane(q16, 4 * c + 1) * krow[c].y +
                (i64)__builtin_amdgcn_readlane(q16, 4 * c + 2) * krow[c].z + (i64)__builtin_amdgcn_readlane(q16, 4 * c + 3) * krow[c].w;
     }
-    i64 dn = (i64)q16 * k16;
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) dn += __shfl_xor(dn, o, 64);
+    const i64 dn = wave_reduce64((i64)q16 * k16, OpAdd());
     const i64 ek = lane == p ? ekn : ekl;
     const i64 d = lane == p ? dn : dot;
     i64 sc = INT64_MIN;
     if (lane <= p) sc = MODEL == 1 ? rsh(wmul(d, a.ehalf), wsub(16, wsub(wmul(eq + ek + 10, 65536), a.half) >> 16))
                                    : rsh(d, -(eq + ek + 7));
-    i64 mx = sc;
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) { const i64 t = __shfl_xor(mx, o, 64); mx = t > mx ? t : mx; }
+    const i64 mx = wave_reduce64(sc, OpMax());
     // arrivals (base2.py:96-97) and their sum
     const int w = lane <= p ? tab_arr(a.tb, wsub(mx, sc)) : 0;
-    i64 z = w;
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) z += __shfl_xor(z, o, 64);
-    // the value sum of dimension `lane` (base2.py:98): cached positions, then the new one
+    const i64 z = wave_reduce64((i64)w, OpAdd());
+    // the divisor's table entries (base2.py:99) are requested now, so their latency passes during the value sum
+    int t; i64 m;
+    log2_parts(z, t, m);
+    const i64 F = wsub(0, wadd((i64)t * 65536, utab_log2(a.tb, (int)m)));
+    const i64 hp = utab_hpow(a.tb, (int)m);
+    // the value sum of dimension `lane` (base2.py:98): the cached positions s < p, then the new one
     i64 num = 0;
     int vmax = 0;
 #pragma unroll
-    for (int s = 0; s < 64; s++) {
-        const int ws = __builtin_amdgcn_readlane(w, s);     // 0 for s > p
-        const int vs = s < p ? vcol[s] : 0;
-        num += (i64)ws * vs;
-        if (MODEL == 1 && ws) vmax = max(vmax, abs(vs));
+    for (int s0 = 0; s0 < 64; s0 += 8) {
+        if (s0 < p) {                                        // uniform: whole groups of eight up to p
+#pragma unroll
+            for (int s = s0; s < s0 + 8; s++) {
+                const int ws = __builtin_amdgcn_readlane(w, s);     // 0 for s > p
+                const int vs = s < p ? vcol[s] : 0;
+                num += (i64)ws * vs;
+                if (MODEL == 1 && ws) vmax = max(vmax, abs(vs));
+            }
+        }
     }
     const int wp = __builtin_amdgcn_readlane(w, p);
     num += (i64)wp * (int)vv;
     if (MODEL == 1 && wp) vmax = max(vmax, abs((int)vv));
     if (MODEL == 1 && (double)vmax * (double)z >= 4611686018427387904.0) atomicOr(a.err, SM_ERR_RANGE);
     // over the total through its log (base2.py:99)
-    int t; i64 m;
-    log2_parts(z, t, m);
-    const i64 F = wsub(0, wadd((i64)t * 65536, utab_log2(a.tb, (int)m)));
-    const i64 hp = utab_hpow(a.tb, (int)m);
     i64 o;
     if (MODEL == 1) {
         const __int128 X = (__int128)num * hp;
@@ -542,7 +538,7 @@ __global__ __launch_bounds__(NTHR, ONE ? 1 : 3) void k_attend(AttArgs a) {
     __shared__ __align__(16) int k16s[64];
     __shared__ __align__(16) int vs[64];
     __shared__ i64 red[8];
-    __shared__ i64 numr[4][64];
+    __shared__ i64 numr[16][64];
     __shared__ int eqs, eks;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int sl = tid >> 2, qd = tid & 3;                   // scores: position in the pass, lane of the position
@@ -664,8 +660,8 @@ __global__ __launch_bounds__(NTHR, ONE ? 1 : 3) void k_attend(AttArgs a) {
             for (int u = 0; u < 4; u++)
                 dot += (i64)qv[u].x * kk[u].x + (i64)qv[u].y * kk[u].y + (i64)qv[u].z * kk[u].z + (i64)qv[u].w * kk[u].w;
         }
-        dot += __shfl_xor(dot, 1, 64);
-        dot += __shfl_xor(dot, 2, 64);
+        dot += dpp64<0xB1, 0xf, 0xf>(dot, 0);              // quad_perm [1, 0, 3, 2]: the position's four lanes
+        dot += dpp64<0x4E, 0xf, 0xf>(dot, 0);              // quad_perm [2, 3, 0, 1]
         if (s <= p) {
             const i64 v = score(dot, ek);
             if (qd == 0) sc[s] = v;
@@ -700,15 +696,13 @@ __global__ __launch_bounds__(NTHR, ONE ? 1 : 3) void k_attend(AttArgs a) {
         acc(arr[sv], reinterpret_cast<const v4i*>(V + (size_t)sv * 768 + h * 64)[d4]);
     if ((p & 15) == g) acc(arr[p], reinterpret_cast<const v4i*>(vs)[d4]);   // the new position (from LDS)
     if (MODEL == 1 && (double)vmax * (double)z >= 4611686018427387904.0) atomicOr(a.err, SM_ERR_RANGE);
-    // the 16 position groups: 4 in a wave (lanes 16 apart), then the 4 waves through LDS
-    n0 += __shfl_xor(n0, 16, 64); n1 += __shfl_xor(n1, 16, 64); n2 += __shfl_xor(n2, 16, 64); n3 += __shfl_xor(n3, 16, 64);
-    n0 += __shfl_xor(n0, 32, 64); n1 += __shfl_xor(n1, 32, 64); n2 += __shfl_xor(n2, 32, 64); n3 += __shfl_xor(n3, 32, 64);
-    if (lane < 16) {
-        numr[wave][4 * d4] = n0; numr[wave][4 * d4 + 1] = n1; numr[wave][4 * d4 + 2] = n2; numr[wave][4 * d4 + 3] = n3;
-    }
+    // the 16 position groups through LDS, summed by wave 0
+    numr[g][4 * d4] = n0; numr[g][4 * d4 + 1] = n1; numr[g][4 * d4 + 2] = n2; numr[g][4 * d4 + 3] = n3;
     __syncthreads();
     if (wave == 0) {
-        const i64 tot = numr[0][lane] + numr[1][lane] + numr[2][lane] + numr[3][lane];
+        i64 tot = 0;
+#pragma unroll
+        for (int i = 0; i < 16; i++) tot += numr[i][lane];
         int t; i64 m;
         log2_parts(z, t, m);
         const i64 F = wsub(0, wadd((i64)t * 65536, utab_log2(a.tb, (int)m)));   // -log2fix(Z), Z the same in every lane
@@ -844,11 +838,11 @@ INST(768, 2, 4, PRO_GAUGE, EPI_GAUGED)        // qkv
 INST(768, 2, 2, PRO_TO16, EPI_PLAIN_ADD)      // proj
 INST(768, 2, 4, PRO_GAUGE, EPI_GAUGED_EDGE)   // fc
 INST(3072, 1, 4, PRO_TO16, EPI_PLAIN_ADD)     // mproj
-INST(768, 8, 4, PRO_GAUGE, EPI_HEAD)          // head (the race in its own kernel)
+INST(768, 4, 4, PRO_GAUGE, EPI_HEAD)          // head (the race in its own kernel)
 INST(768, 2, 4, PRO_PEMBED, EPI_PLAIN)        // Pythia: qkv of layer 0
 INST(768, 2, 4, PRO_PGAUGE, EPI_PLAIN)        // Pythia: qkv
 INST(768, 2, 4, PRO_PGAUGE, EPI_PLAIN_EDGE)   // Pythia: fc
-INST(768, 8, 4, PRO_PGAUGE, EPI_PHEAD)        // Pythia: head
+INST(768, 4, 4, PRO_PGAUGE, EPI_PHEAD)        // Pythia: head
 template __global__ void k_attend<0, 0>(AttArgs);
 template __global__ void k_attend<0, 1>(AttArgs);
 template __global__ void k_attend<1, 0>(AttArgs);

@@ -477,9 +477,11 @@ static int launch_step_batched(sm_machine* m, int parts, hipEvent_t hs, hipEvent
     return SM_OK;
 }
 
-// the batch-1 head: four waves per block, one block per CU by default (measured: 256 blocks of 4 waves
-// 17.0 us; 512 blocks 19.2 us; 256 blocks of 12 waves 59 us, register-bound)
+// the batch-1 head: tiles of 4 columns, four waves per block, two blocks per CU by default (measured on the
+// 768 x 50257 plate: 4-column tiles at 512 blocks 15.7 us; 8-column tiles at 256 blocks 17.3 us (one wave a
+// SIMD, 256 VGPRs), at 512 blocks 19.2 us; 2-column tiles at 768 blocks 16.2 us)
 #define HEAD_WPB 4
+#define HEAD_TC 4
 
 // the race over the head's per-block bests, one block per stream; it also advances the position
 static void launch_race(sm_machine* m, int nblk) {
@@ -569,9 +571,9 @@ static int launch_step_pythia(sm_machine* m, int parts, hipEvent_t hs, hipEvent_
         a.part_v = m->part_v; a.part_i = m->part_i; a.counter = nullptr;
         a.plen = ctl + CTL_PLEN;
         if (hs)
-            hipExtLaunchKernelGGL(k_gemv<768, 8, HEAD_WPB, PRO_PGAUGE, EPI_PHEAD>, dim3(m->head_grid), dim3(64 * HEAD_WPB), 0, m->st, hs, he, 0, a);
+            hipExtLaunchKernelGGL(k_gemv<768, HEAD_TC, HEAD_WPB, PRO_PGAUGE, EPI_PHEAD>, dim3(m->head_grid), dim3(64 * HEAD_WPB), 0, m->st, hs, he, 0, a);
         else
-            k_gemv<768, 8, HEAD_WPB, PRO_PGAUGE, EPI_PHEAD><<<m->head_grid, 64 * HEAD_WPB, 0, m->st>>>(a);
+            k_gemv<768, HEAD_TC, HEAD_WPB, PRO_PGAUGE, EPI_PHEAD><<<m->head_grid, 64 * HEAD_WPB, 0, m->st>>>(a);
         launch_race(m, m->head_grid);
     }
     HIP_TRY(hipGetLastError());
@@ -798,9 +800,9 @@ static int launch_step(sm_machine* m, int parts = STEP_ALL, hipEvent_t hs = null
         a.part_v = m->part_v; a.part_i = m->part_i; a.counter = nullptr;     // the race runs in its own kernel
         a.plen = ctl + CTL_PLEN;
         if (hs)   // timed: the event pair is stamped by this dispatch itself (the interval a kernel trace reports)
-            hipExtLaunchKernelGGL(k_gemv<768, 8, HEAD_WPB, PRO_GAUGE, EPI_HEAD>, dim3(m->head_grid), dim3(64 * HEAD_WPB), 0, m->st, hs, he, 0, a);
+            hipExtLaunchKernelGGL(k_gemv<768, HEAD_TC, HEAD_WPB, PRO_GAUGE, EPI_HEAD>, dim3(m->head_grid), dim3(64 * HEAD_WPB), 0, m->st, hs, he, 0, a);
         else
-            k_gemv<768, 8, HEAD_WPB, PRO_GAUGE, EPI_HEAD><<<m->head_grid, 64 * HEAD_WPB, 0, m->st>>>(a);
+            k_gemv<768, HEAD_TC, HEAD_WPB, PRO_GAUGE, EPI_HEAD><<<m->head_grid, 64 * HEAD_WPB, 0, m->st>>>(a);
         launch_race(m, m->head_grid);
     }
     HIP_TRY(hipGetLastError());
@@ -902,7 +904,7 @@ extern "C" int sm_create(const char* layout_dir, const sm_config* cfg, sm_machin
             return bail(rc);
         if (py) b.assign(m->vocab, 0);         // Pythia's head has no bias (foundation0/pythia_base2.py:159)
         else if ((rc = read_array(dir + "head.b", b, m->vocab))) return bail(rc);
-        if (m->B == 1 && (rc = upload_plate(m->head, w.data(), e.data(), b.data(), 768, m->vocab, 8))) return bail(rc);
+        if (m->B == 1 && (rc = upload_plate(m->head, w.data(), e.data(), b.data(), 768, m->vocab, HEAD_TC))) return bail(rc);
         if (m->B > 1 && (rc = upload_mfma_plate(m->mhead, w.data(), e.data(), b.data(), 768, m->vocab))) return bail(rc);
     }
     // word and position tables
@@ -973,7 +975,7 @@ extern "C" int sm_create(const char* layout_dir, const sm_config* cfg, sm_machin
         m->T.force_memory = c.table_mode != 1;
     }
     m->ctx = c.max_ctx < m->npos ? c.max_ctx : m->npos;
-    m->head_grid = c.head_grid > 0 ? c.head_grid : 256;     // one block per CU (measured best)
+    m->head_grid = c.head_grid > 0 ? c.head_grid : 512;     // two blocks per CU (measured best)
     const size_t nparts = m->B == 1 ? (size_t)m->head_grid : (size_t)m->B * head_rows_grid((m->vocab + 15) / 16);
     // state
     const size_t B = m->B, ctx = m->ctx, RC = m->RC;
