@@ -205,6 +205,7 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs a) {
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int ntiles = (a.N + 15) >> 4;
     const int nt = blockIdx.x % ntiles, kb = blockIdx.x / ntiles;
+    const int t0 = blockIdx.y * RT;                  // this block's first row tile
     const int s0 = kb * (KS / KSPLIT) + wave * NS;
     const v4* Wb = reinterpret_cast<const v4*>(a.W) + (size_t)nt * KS * 128 + lane;
     const v4* Ab = reinterpret_cast<const v4*>(a.planes) + lane;
@@ -218,8 +219,8 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs a) {
     for (int i = 0; i < NS; i++)
 #pragma unroll
         for (int t = 0; t < RT; t++) {
-            xh[i][t] = Ab[((size_t)t * KS + s0 + i) * 192];
-            xl[i][t] = Ab[((size_t)t * KS + s0 + i) * 192 + 64];
+            xh[i][t] = Ab[((size_t)(t0 + t) * KS + s0 + i) * 192];
+            xl[i][t] = Ab[((size_t)(t0 + t) * KS + s0 + i) * 192 + 64];
         }
     const int n32 = lane < a.rows ? a.rowinfo[lane * 8 + 6] : 0;
     const int rsv = tid < a.rows * 8 ? a.rowinfo[tid] : 0;
@@ -243,10 +244,10 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs a) {
         }
 #pragma unroll
     for (int t = 0; t < RT; t++)
-        if ((cmask >> (16 * t)) & 0xFFFFull) {
+        if ((cmask >> (16 * (t0 + t))) & 0xFFFFull) {
 #pragma unroll
             for (int i = 0; i < NS; i++) {
-                const v4 cc = Ab[((size_t)t * KS + s0 + i) * 192 + 128];
+                const v4 cc = Ab[((size_t)(t0 + t) * KS + s0 + i) * 192 + 128];
                 acc[t][1] = __builtin_amdgcn_mfma_i32_16x16x64_i8(cc, wh[i], acc[t][1], 0, 0, 0);
                 acc[t][2] = __builtin_amdgcn_mfma_i32_16x16x64_i8(cc, wl[i], acc[t][2], 0, 0, 0);
             }
@@ -275,7 +276,7 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs a) {
     const bool rec0 = a.rec_pos && *a.rec_pos == p;
 #pragma unroll
     for (int t = 0; t < RT; t++) {
-        const int row = 16 * t + 4 * (lane >> 4) + wave;
+        const int row = 16 * (t0 + t) + 4 * (lane >> 4) + wave;
         if (row >= a.rows) continue;
         if (EPI == EPI_PART) {
 #pragma unroll
@@ -698,9 +699,6 @@ template __global__ void k_py_rows<PY_EDGE>(PyRowArgs);
 #define BINST_GR(RT) BINST_G(768, RT, 1, EPI_GAUGED) BINST_G(768, RT, 1, EPI_PART) BINST_G(3072, RT, 4, EPI_PART) \
     BINST_G(768, RT, 1, EPI_PILE) BINST_G(3072, RT, 1, EPI_PILE) BINST_G(768, RT, 1, EPI_PLAIN)
 BINST_GR(1)
-BINST_GR(2)
-BINST_GR(3)
-BINST_GR(4)
 #define BINST_H(RT) template __global__ void k_head_rows<RT, EPI_HEAD>(GemmArgs); \
     template __global__ void k_head_rows<RT, EPI_PILE>(GemmArgs); template __global__ void k_head_rows<RT, EPI_PHEAD>(GemmArgs);
 BINST_H(1)

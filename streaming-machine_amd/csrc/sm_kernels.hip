@@ -416,13 +416,14 @@ __global__ __launch_bounds__(64 * WPB) void k_gemv(GemvArgs a) {
 // cached keys and values of the first 64 positions are requested at launch, before the new q, k, v arrive.
 // The maximum is global over the row before any arrival is read (two passes, scores in LDS), so the result is
 // exact for any context length.
-// The short-context path (position p < 64, one stream): one wave does a head alone, with no LDS and no block
-// barrier.  Lane s < p holds cached key row s (prefetched at launch) and scores it against q, which every lane
-// reads through readlane; lane p is the new position (its score is a wave sum); the maximum and the arrival sum
-// are wave reductions; lane d accumulates output dimension d from its prefetched V column.  Same numbers as the
-// general path below (base2.py:93-99 / pythia_base2.py:129-141).
+// The short-context path (position p < 64, one stream): one wave does a head alone, with no block barrier.
+// Lane s < p holds cached key row s (prefetched at launch) and scores it against q, which every lane reads from
+// LDS (the wave's own writes, read back in order); lane p is the new position (its score is a wave sum); the
+// maximum and the arrival sum are wave reductions; lane d accumulates output dimension d from its prefetched V
+// column, the arrivals read back from LDS the same way.  Same numbers as the general path below
+// (base2.py:93-99 / pythia_base2.py:129-141).  q_s, w_s: 64 ints of LDS each.
 template <int MODEL>
-SMD void attend_short(const AttArgs& a, int p, int h, int b) {
+SMD void attend_short(const AttArgs& a, int p, int h, int b, int* q_s, int* w_s) {
     const int lane = threadIdx.x;
     const i64* qkv = a.QKV + (size_t)b * 2304;
     int* K16 = a.K16 + (size_t)b * a.ctx * 768;
@@ -466,11 +467,12 @@ SMD void attend_short(const AttArgs& a, int p, int h, int b) {
     if (vv < (i64)INT32_MIN || vv > (i64)INT32_MAX) atomicOr(a.err, SM_ERR_V32);
     V[(size_t)p * 768 + h * 64 + lane] = (int)vv;
     // scores (base2.py:94): lane s < p its cached row, lane p the new key
+    q_s[lane] = q16;
     i64 dot = 0;
 #pragma unroll
     for (int c = 0; c < 16; c++) {
-        dot += (i64)__builtin_amdgcn_readlane(q16, 4 * c) * krow[c].x + (i64)__builtin_amdgcn_readlane(q16, 4 * c + 1) * krow[c].y +
-               (i64)__builtin_amdgcn_readlane(q16, 4 * c + 2) * krow[c].z + (i64)__builtin_amdgcn_readlane(q16, 4 * c + 3) * krow[c].w;
+        const v4i q4 = reinterpret_cast<const v4i*>(q_s)[c];          // the same address in every lane
+        dot += (i64)q4.x * krow[c].x + (i64)q4.y * krow[c].y + (i64)q4.z * krow[c].z + (i64)q4.w * krow[c].w;
     }
     const i64 dn = wave_reduce64((i64)q16 * k16, OpAdd());
     const i64 ek = lane == p ? ekn : ekl;
@@ -488,14 +490,17 @@ SMD void attend_short(const AttArgs& a, int p, int h, int b) {
     const i64 F = wsub(0, wadd((i64)t * 65536, utab_log2(a.tb, (int)m)));
     const i64 hp = utab_hpow(a.tb, (int)m);
     // the value sum of dimension `lane` (base2.py:98): the cached positions s < p, then the new one
+    w_s[lane] = w;
     i64 num = 0;
     int vmax = 0;
 #pragma unroll
     for (int s0 = 0; s0 < 64; s0 += 8) {
         if (s0 < p) {                                        // uniform: whole groups of eight up to p
+            const v4i wa = reinterpret_cast<const v4i*>(w_s)[s0 / 4], wb = reinterpret_cast<const v4i*>(w_s)[s0 / 4 + 1];
+            const int wv[8] = {wa.x, wa.y, wa.z, wa.w, wb.x, wb.y, wb.z, wb.w};
 #pragma unroll
-            for (int s = s0; s < s0 + 8; s++) {
-                const int ws = __builtin_amdgcn_readlane(w, s);     // 0 for s > p
+            for (int j = 0; j < 8; j++) {
+                const int s = s0 + j, ws = wv[j];            // 0 for s > p
                 const int vs = s < p ? vcol[s] : 0;
                 num += (i64)ws * vs;
                 if (MODEL == 1 && ws) vmax = max(vmax, abs(vs));
@@ -549,7 +554,7 @@ __global__ __launch_bounds__(NTHR, ONE ? 1 : 3) void k_attend(AttArgs a) {
     const bool store = !a.rowmap;                            // prompt rows: k_kv_rows stored every row's k and v
     if constexpr (ONE) {
         if (p < 64) {                                        // one stream, short context: one wave, no barriers
-            if (wave == 0) attend_short<MODEL>(a, p, h, b);
+            if (wave == 0) attend_short<MODEL>(a, p, h, b, q16s, vs);
             return;
         }
     }

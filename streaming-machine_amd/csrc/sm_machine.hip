@@ -420,7 +420,7 @@ static int launch_step_batched(sm_machine* m, int parts, hipEvent_t hs, hipEvent
         }
         {
             GemmArgs a = gemm_args(m->mbank[l][0], m->QKV, 2304, rp, m->r_qkv + l * 2304);
-            k_gemm<768, RT, 1, EPI_GAUGED><<<m->mbank[l][0].ntiles, 256, 0, m->st>>>(a);
+            k_gemm<768, 1, 1, EPI_GAUGED><<<dim3(m->mbank[l][0].ntiles, RT), 256, 0, m->st>>>(a);
         }
         {
             AttArgs a{};
@@ -444,17 +444,17 @@ static int launch_step_batched(sm_machine* m, int parts, hipEvent_t hs, hipEvent
         }
         {
             GemmArgs a = gemm_args(m->mbank[l][1], nullptr, 0, nullptr, nullptr);
-            k_gemm<768, RT, 1, EPI_PART><<<m->mbank[l][1].ntiles, 256, 0, m->st>>>(a);
+            k_gemm<768, 1, 1, EPI_PART><<<dim3(m->mbank[l][1].ntiles, RT), 256, 0, m->st>>>(a);
         }
         finish_light(m->mbank[l][1], 1, m->R, rp + 3072, m->r_resid + (l * 2 + 0) * 768, rx + 2 * 3072, re + 4);
         {
             GemmArgs a = gemm_args(m->mbank[l][2], nullptr, 0, nullptr, nullptr);
-            k_gemm<768, RT, 1, EPI_PART><<<m->mbank[l][2].ntiles, 256, 0, m->st>>>(a);
+            k_gemm<768, 1, 1, EPI_PART><<<dim3(m->mbank[l][2].ntiles, RT), 256, 0, m->st>>>(a);
         }
         finish_light(m->mbank[l][2], 1, nullptr, rp + 2 * 3072, m->r_hid + l * 3072, rx + 3 * 3072, re + 6);
         {
             GemmArgs a = gemm_args(m->mbank[l][3], nullptr, 0, nullptr, nullptr);
-            k_gemm<3072, RT, 4, EPI_PART><<<m->mbank[l][3].ntiles * 4, 256, 0, m->st>>>(a);
+            k_gemm<3072, 1, 4, EPI_PART><<<dim3(m->mbank[l][3].ntiles * 4, RT), 256, 0, m->st>>>(a);
         }
         const bool last = l == 11;     // the last stream update lights the head
         finish_light(m->mbank[l][3], 4, m->R, rp + 3 * 3072, m->r_resid + (l * 2 + 1) * 768,
@@ -634,7 +634,7 @@ static int launch_step_pythia_batched(sm_machine* m, int parts, hipEvent_t hs, h
         {   // qkv: plain, written
             GemmArgs a = gemm_args(m->mbank[l][0], pA, rA);
             a.Y = m->QKV; a.ystride = 2304; a.rpile = rp; a.rout = m->r_qkv + l * 2304;
-            k_gemm<768, RT, 1, EPI_PLAIN><<<m->mbank[l][0].ntiles, 256, 0, m->st>>>(a);
+            k_gemm<768, 1, 1, EPI_PLAIN><<<dim3(m->mbank[l][0].ntiles, RT), 256, 0, m->st>>>(a);
         }
         if (rowmap && l == 11) {   // prompt rows: the last layer only stores its keys and values
             AttArgs a{};
@@ -648,7 +648,7 @@ static int launch_step_pythia_batched(sm_machine* m, int parts, hipEvent_t hs, h
         {   // fc: partials, then edge and the 3072-wide light
             GemmArgs a = gemm_args(m->mbank[l][2], pB, rB);
             a.part = P0;
-            k_gemm<768, RT, 1, EPI_PART><<<m->mbank[l][2].ntiles, 256, 0, m->st>>>(a);
+            k_gemm<768, 1, 1, EPI_PART><<<dim3(m->mbank[l][2].ntiles, RT), 256, 0, m->st>>>(a);
             PyRowArgs e = rows_args();
             const MfmaPlate& F = m->mbank[l][2];
             e.partA = P0; e.ksA = 1; e.kinA = 768; e.rowinfoA = rB; e.csumA = F.csum; e.weA = F.e; e.biasA = F.b;
@@ -660,7 +660,7 @@ static int launch_step_pythia_batched(sm_machine* m, int parts, hipEvent_t hs, h
         {   // mproj: partials over four K slices
             GemmArgs a = gemm_args(m->mbank[l][3], pC, rC);
             a.part = P0;
-            k_gemm<3072, RT, 4, EPI_PART><<<m->mbank[l][3].ntiles * 4, 256, 0, m->st>>>(a);
+            k_gemm<3072, 1, 4, EPI_PART><<<dim3(m->mbank[l][3].ntiles * 4, RT), 256, 0, m->st>>>(a);
         }
         {   // attention with turns
             AttArgs a{};
@@ -680,7 +680,7 @@ static int launch_step_pythia_batched(sm_machine* m, int parts, hipEvent_t hs, h
             k_light<768, PRO_TO16, 192><<<B, 192, 0, m->st>>>(a);
             GemmArgs g = gemm_args(m->mbank[l][1], pD, rD);
             g.part = P3;
-            k_gemm<768, RT, 1, EPI_PART><<<m->mbank[l][1].ntiles, 256, 0, m->st>>>(g);
+            k_gemm<768, 1, 1, EPI_PART><<<dim3(m->mbank[l][1].ntiles, RT), 256, 0, m->st>>>(g);
         }
         {   // R += At + Mo, then the next gauges' lights
             PyRowArgs a = rows_args();
@@ -1371,10 +1371,10 @@ static void rows_product(const sm_plate* p, const int64_t* x16, int32_t rows, in
         if (P.N > 3072)       // head-shaped plates: the head's kernel (light planes in LDS)
             k_head_rows<RT, EPI_PILE><<<head_rows_grid(P.ntiles), 256, 0, s>>>(ga);
         else                  // layer-shaped plates: one column tile per block, K split over its four waves
-            k_gemm<768, RT, 1, EPI_PILE><<<P.ntiles, 256, 0, s>>>(ga);
+            k_gemm<768, 1, 1, EPI_PILE><<<dim3(P.ntiles, RT), 256, 0, s>>>(ga);
     } else {
         k_light<3072, PRO_X16, 768><<<rows, 768, 0, s>>>(la);
-        k_gemm<3072, RT, 1, EPI_PILE><<<P.ntiles, 256, 0, s>>>(ga);
+        k_gemm<3072, 1, 1, EPI_PILE><<<dim3(P.ntiles, RT), 256, 0, s>>>(ga);
     }
 }
 
