@@ -28,7 +28,7 @@ struct LightArgs {
     Tables tb;
     const int* rec_pos; i64* rx16; i64* rexls;    // stream 0's record
     // PRO_ADD_GAUGE / PRO_EDGE_TO16: the producing bank's epilogue first, from its partial accumulators
-    const int* part; int ksplit; int kin;         // [ksplit][3][rows][K] int32 (HH, MID, LL); the bank's K
+    const int* part; int kin;                     // [K slices][3][rows][K] int32 (HH, MID, LL); the bank's K
     const int* csum; const int* we; const i64* bias;   // the producing plate's column facts
     i64* Y;                                       // [rows][K]: the epilogue's row (R: read and written)
     i64* rpile_in; i64* rout_in;                  // stream 0's record of the producing bank
@@ -52,8 +52,9 @@ struct GemmArgs {
 // ---------------------------------------------------------------------------------------------------------
 // One block (256 threads) per stream row: the light of base2.py:24-27 (and the gauge of :55-60), written as
 // MFMA A planes plus the row's exponent, gauge, power factor and plane sums.  Each thread owns groups of four
-// consecutive k, so every plane byte group goes out as one 32-bit store.
-template <int K, int PRO, int NT>
+// consecutive k, so every plane byte group goes out as one 32-bit store.  KSP: the producing bank's K slices
+// (PRO_ADD_GAUGE / PRO_EDGE_TO16), a compile-time count so that every load of the row is in flight at once.
+template <int K, int PRO, int NT, int KSP>
 __global__ __launch_bounds__(NT) void k_light(LightArgs a) {
     constexpr int NG = K / 4, GPT = (NG + NT - 1) / NT, KS = K / 64, NW = NT / 64;
     static_assert(NT % 64 == 0 && NW <= 12, "one to twelve waves");
@@ -79,26 +80,38 @@ __global__ __launch_bounds__(NT) void k_light(LightArgs a) {
         if (g >= NG) continue;
         const int k = 4 * g;
         if (PRO == PRO_ADD_GAUGE || PRO == PRO_EDGE_TO16) {
-            v4l h = {0, 0, 0, 0}, mi = {0, 0, 0, 0}, lo = {0, 0, 0, 0};
-            for (int ks = 0; ks < a.ksplit; ks++) {
-                const int* q = a.part + ((size_t)ks * 3 * a.rows + r) * K + k;
-                h += *reinterpret_cast<const v4l*>(q);
-                mi += *reinterpret_cast<const v4l*>(q + (size_t)a.rows * K);
-                lo += *reinterpret_cast<const v4l*>(q + (size_t)2 * a.rows * K);
-            }
+            typedef i64 v2q __attribute__((ext_vector_type(2)));
+            // every load first (column facts, the stream, the partial slices), then the arithmetic
             const v4l c0 = *reinterpret_cast<const v4l*>(a.csum + 2 * k), c1 = *reinterpret_cast<const v4l*>(a.csum + 2 * k + 4);
             const v4l wv = *reinterpret_cast<const v4l*>(a.we + k);
+            const v2q b01 = *reinterpret_cast<const v2q*>(a.bias + k), b23 = *reinterpret_cast<const v2q*>(a.bias + k + 2);
+            v2q y01 = {0, 0}, y23 = {0, 0};
+            if (PRO == PRO_ADD_GAUGE) {
+                y01 = *reinterpret_cast<const v2q*>(a.Y + (size_t)r * K + k);
+                y23 = *reinterpret_cast<const v2q*>(a.Y + (size_t)r * K + k + 2);
+            }
+            v4l hq[KSP], mq[KSP], lq[KSP];
+#pragma unroll
+            for (int ks = 0; ks < KSP; ks++) {
+                const int* q = a.part + ((size_t)ks * 3 * a.rows + r) * K + k;
+                hq[ks] = *reinterpret_cast<const v4l*>(q);
+                mq[ks] = *reinterpret_cast<const v4l*>(q + (size_t)a.rows * K);
+                lq[ks] = *reinterpret_cast<const v4l*>(q + (size_t)2 * a.rows * K);
+            }
+            v4l h = hq[0], mi = mq[0], lo = lq[0];
+#pragma unroll
+            for (int ks = 1; ks < KSP; ks++) { h += hq[ks]; mi += mq[ks]; lo += lq[ks]; }
             const int sw[8] = {c0[0], c0[1], c0[2], c0[3], c1[0], c1[1], c1[2], c1[3]};
+            const i64 bcs[4] = {b01[0], b01[1], b23[0], b23[1]}, ys[4] = {y01[0], y01[1], y23[0], y23[1]};
 #pragma unroll
             for (int j = 0; j < 4; j++) {
                 const i64 pile = 65536 * (i64)h[j] + 256 * (i64)mi[j] + lo[j] + 32768 * (i_sxh + sw[2 * j]) +
                                  128 * (i_sxl + sw[2 * j + 1]) + 16384 * (i64)a.kin + 128 * i_n32;
-                const i64 bc = a.bias[k + j];
+                const i64 bc = bcs[j];
                 i64 y;
                 if (PRO == PRO_ADD_GAUGE) {
-                    i64* yp = a.Y + (size_t)r * K + k + j;
-                    y = wadd(*yp, wadd(rsh(pile, -((i64)wv[j] + i_ex + 16)), bc));
-                    *yp = y;
+                    y = wadd(ys[j], wadd(rsh(pile, -((i64)wv[j] + i_ex + 16)), bc));
+                    a.Y[(size_t)r * K + k + j] = y;
                 } else {
                     y = edge1(wadd(power_known(pile, wsub(wmul((i64)wv[j] + i_ex + 16, 65536), i_ls), i_e2), bc), a.tb);
                     if (a.Y) a.Y[(size_t)r * K + k + j] = y;
@@ -489,8 +502,9 @@ struct PyRowArgs {
     signed char* planes1; int* rowinfo1;          // light of gauge 1 (PY_EDGE: of the edge row)
     signed char* planes2; int* rowinfo2;          // light of gauge 2
     // finished plain banks: A = proj (or fc for PY_EDGE), B = mproj
-    const int* partA; int ksA; int kinA; const int* rowinfoA; const int* csumA; const int* weA; const i64* biasA;
-    const int* partB; int ksB; int kinB; const int* rowinfoB; const int* csumB; const int* weB; const i64* biasB;
+    // (A has one K slice, B four: the banks' launch shapes)
+    const int* partA; int kinA; const int* rowinfoA; const int* csumA; const int* weA; const i64* biasA;
+    const int* partB; int kinB; const int* rowinfoB; const int* csumB; const int* weB; const i64* biasB;
     Tables tb;
     const int* rec_pos;
     i64* rg1; i64* rx1; i64* rex1; i64* rg2; i64* rx2; i64* rex2;   // the gauges and their lights
@@ -500,26 +514,41 @@ struct PyRowArgs {
 };
 enum { PY_EMBED = 0, PY_ADD = 1, PY_EDGE = 2 };
 
-// plain(pile) of one bank for columns k .. k + 3 of row r, from its K-sliced partial accumulators (:112-114)
-SMD void plain4(const int* part, int ks, int rows, int N, int kin, const int* ri, const int* csum, const int* we,
-                const i64* bias, int r, int k, i64 (&pile)[4], i64 (&y)[4]) {
-    typedef int v4l __attribute__((ext_vector_type(4)));
-    v4l h = {0, 0, 0, 0}, mi = {0, 0, 0, 0}, lo = {0, 0, 0, 0};
-    for (int q = 0; q < ks; q++) {
+// plain(pile) of one bank for columns k .. k + 3 of row r, from its KS K-sliced partial accumulators
+// (:112-114), in two halves so that a caller can have every load of its row in flight before the arithmetic
+typedef int v4l_p __attribute__((ext_vector_type(4)));
+typedef i64 v2q_p __attribute__((ext_vector_type(2)));
+template <int KS>
+struct Plain4 { v4l_p h[KS], mi[KS], lo[KS], c0, c1, wv; v2q_p b01, b23; };
+template <int KS>
+SMD void plain4_load(Plain4<KS>& P, const int* part, int rows, int N, const int* csum, const int* we, const i64* bias,
+                     int r, int k) {
+    P.c0 = *reinterpret_cast<const v4l_p*>(csum + 2 * k);
+    P.c1 = *reinterpret_cast<const v4l_p*>(csum + 2 * k + 4);
+    P.wv = *reinterpret_cast<const v4l_p*>(we + k);
+    P.b01 = *reinterpret_cast<const v2q_p*>(bias + k);
+    P.b23 = *reinterpret_cast<const v2q_p*>(bias + k + 2);
+#pragma unroll
+    for (int q = 0; q < KS; q++) {
         const int* src = part + ((size_t)q * 3 * rows + r) * N + k;
-        h += *reinterpret_cast<const v4l*>(src);
-        mi += *reinterpret_cast<const v4l*>(src + (size_t)rows * N);
-        lo += *reinterpret_cast<const v4l*>(src + (size_t)2 * rows * N);
+        P.h[q] = *reinterpret_cast<const v4l_p*>(src);
+        P.mi[q] = *reinterpret_cast<const v4l_p*>(src + (size_t)rows * N);
+        P.lo[q] = *reinterpret_cast<const v4l_p*>(src + (size_t)2 * rows * N);
     }
-    const v4l c0 = *reinterpret_cast<const v4l*>(csum + 2 * k), c1 = *reinterpret_cast<const v4l*>(csum + 2 * k + 4);
-    const v4l wv = *reinterpret_cast<const v4l*>(we + k);
-    const int sw[8] = {c0[0], c0[1], c0[2], c0[3], c1[0], c1[1], c1[2], c1[3]};
+}
+template <int KS>
+SMD void plain4_finish(const Plain4<KS>& P, int kin, const int* ri, i64 (&pile)[4], i64 (&y)[4]) {
+    v4l_p h = P.h[0], mi = P.mi[0], lo = P.lo[0];
+#pragma unroll
+    for (int q = 1; q < KS; q++) { h += P.h[q]; mi += P.mi[q]; lo += P.lo[q]; }
+    const int sw[8] = {P.c0[0], P.c0[1], P.c0[2], P.c0[3], P.c1[0], P.c1[1], P.c1[2], P.c1[3]};
+    const i64 bc[4] = {P.b01[0], P.b01[1], P.b23[0], P.b23[1]};
     const i64 ex = ri[0], sxh = ri[4], sxl = ri[5], n32 = ri[6];
 #pragma unroll
     for (int j = 0; j < 4; j++) {
         pile[j] = 65536 * (i64)h[j] + 256 * (i64)mi[j] + lo[j] + 32768 * (sxh + sw[2 * j]) + 128 * (sxl + sw[2 * j + 1]) +
                   16384 * (i64)kin + 128 * n32;
-        y[j] = wadd(rsh(pile[j], -((i64)wv[j] + ex + 16)), bias[k + j]);
+        y[j] = wadd(rsh(pile[j], -((i64)P.wv[j] + ex + 16)), bc[j]);
     }
 }
 
@@ -543,7 +572,9 @@ __global__ __launch_bounds__(MODE == PY_EDGE ? 768 : 192) void k_py_rows(PyRowAr
         for (int m = 0; m < 1; m++) {
             const int k = 4 * tid;
             i64 pile[4], y[4];
-            plain4(a.partA, a.ksA, a.rows, 3072, a.kinA, ri, a.csumA, a.weA, a.biasA, r, k, pile, y);
+            Plain4<1> PA;
+            plain4_load<1>(PA, a.partA, a.rows, 3072, a.csumA, a.weA, a.biasA, r, k);
+            plain4_finish<1>(PA, a.kinA, ri, pile, y);
 #pragma unroll
             for (int j = 0; j < 4; j++) {
                 if (rec && a.rpileA) a.rpileA[k + j] = pile[j];
@@ -566,11 +597,19 @@ __global__ __launch_bounds__(MODE == PY_EDGE ? 768 : 192) void k_py_rows(PyRowAr
             for (int j = 0; j < 4; j++) R4[j] = rsh((i64)a.ew[tok * 768 + k + j], es);
         } else {
             i64 pA[4], yA[4], pB[4], yB[4];
-            plain4(a.partA, a.ksA, a.rows, 768, a.kinA, a.rowinfoA + (size_t)r * 8, a.csumA, a.weA, a.biasA, r, k, pA, yA);
-            plain4(a.partB, a.ksB, a.rows, 768, a.kinB, a.rowinfoB + (size_t)r * 8, a.csumB, a.weB, a.biasB, r, k, pB, yB);
+            // proj's partials (one K slice), mproj's (four) and the stream row, all requested before any use
+            Plain4<1> PA;
+            Plain4<4> PB;
+            plain4_load<1>(PA, a.partA, a.rows, 768, a.csumA, a.weA, a.biasA, r, k);
+            plain4_load<4>(PB, a.partB, a.rows, 768, a.csumB, a.weB, a.biasB, r, k);
+            const v2q_p r01 = *reinterpret_cast<const v2q_p*>(a.R + (size_t)r * 768 + k);
+            const v2q_p r23 = *reinterpret_cast<const v2q_p*>(a.R + (size_t)r * 768 + k + 2);
+            const i64 rr[4] = {r01[0], r01[1], r23[0], r23[1]};
+            plain4_finish<1>(PA, a.kinA, a.rowinfoA + (size_t)r * 8, pA, yA);
+            plain4_finish<4>(PB, a.kinB, a.rowinfoB + (size_t)r * 8, pB, yB);
 #pragma unroll
             for (int j = 0; j < 4; j++) {
-                const i64 r0 = a.R[(size_t)r * 768 + k + j];
+                const i64 r0 = rr[j];
                 const i64 r1 = wadd(r0, yA[j]);
                 R4[j] = wadd(r1, yB[j]);
                 if (rec) {
@@ -683,15 +722,16 @@ __global__ __launch_bounds__(256) void k_race_rows(RaceArgs a) {
     }
 }
 
-#define BINST_L(K, PRO) template __global__ void k_light<K, PRO, (K) / 4>(LightArgs);
-BINST_L(768, PRO_EMBED)
-BINST_L(768, PRO_GAUGE)
-BINST_L(768, PRO_TO16)
-BINST_L(3072, PRO_TO16)
-BINST_L(768, PRO_X16)
-BINST_L(3072, PRO_X16)
-BINST_L(768, PRO_ADD_GAUGE)
-BINST_L(3072, PRO_EDGE_TO16)
+#define BINST_L(K, PRO, KSP) template __global__ void k_light<K, PRO, (K) / 4, KSP>(LightArgs);
+BINST_L(768, PRO_EMBED, 1)
+BINST_L(768, PRO_GAUGE, 1)
+BINST_L(768, PRO_TO16, 1)
+BINST_L(3072, PRO_TO16, 1)
+BINST_L(768, PRO_X16, 1)
+BINST_L(3072, PRO_X16, 1)
+BINST_L(768, PRO_ADD_GAUGE, 1)
+BINST_L(768, PRO_ADD_GAUGE, 4)
+BINST_L(3072, PRO_EDGE_TO16, 1)
 template __global__ void k_py_rows<PY_EMBED>(PyRowArgs);
 template __global__ void k_py_rows<PY_ADD>(PyRowArgs);
 template __global__ void k_py_rows<PY_EDGE>(PyRowArgs);

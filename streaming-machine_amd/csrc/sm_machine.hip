@@ -397,10 +397,11 @@ static int launch_step_batched(sm_machine* m, int parts, hipEvent_t hs, hipEvent
     // the producing bank's epilogue (from its partial accumulators) followed by the next light
     auto finish_light = [&](const MfmaPlate& P, int ksplit, i64* Y, i64* rpile, i64* rout, i64* rx16, i64* rexls) {
         LightArgs a = light_args(P.N, nullptr, rx16, rexls);
-        a.part = m->part_acc; a.ksplit = ksplit; a.kin = P.K; a.csum = P.csum; a.we = P.e; a.bias = P.b; a.Y = Y;
+        a.part = m->part_acc; a.kin = P.K; a.csum = P.csum; a.we = P.e; a.bias = P.b; a.Y = Y;
         a.rpile_in = rpile; a.rout_in = rout;
-        if (P.N == 3072) k_light<3072, PRO_EDGE_TO16, 768><<<B, 768, 0, m->st>>>(a);
-        else k_light<768, PRO_ADD_GAUGE, 192><<<B, 192, 0, m->st>>>(a);
+        if (P.N == 3072) k_light<3072, PRO_EDGE_TO16, 768, 1><<<B, 768, 0, m->st>>>(a);
+        else if (ksplit == 4) k_light<768, PRO_ADD_GAUGE, 192, 4><<<B, 192, 0, m->st>>>(a);
+        else k_light<768, PRO_ADD_GAUGE, 192, 1><<<B, 192, 0, m->st>>>(a);
     };
     auto gemm_args = [&](const MfmaPlate& P, i64* Y, int ystride, i64* rpile, i64* rout) {
         GemmArgs a{};
@@ -416,7 +417,7 @@ static int launch_step_batched(sm_machine* m, int parts, hipEvent_t hs, hipEvent
         i64* rp = m->r_pile + (size_t)l * 4 * 3072;
         if (l == 0) {      // the word enters; later layers get their light from the previous layer's last kernel
             LightArgs a = light_args(768, m->R, rx, re);
-            k_light<768, PRO_EMBED, 192><<<B, 192, 0, m->st>>>(a);
+            k_light<768, PRO_EMBED, 192, 1><<<B, 192, 0, m->st>>>(a);
         }
         {
             GemmArgs a = gemm_args(m->mbank[l][0], m->QKV, 2304, rp, m->r_qkv + l * 2304);
@@ -440,7 +441,7 @@ static int launch_step_batched(sm_machine* m, int parts, hipEvent_t hs, hipEvent
         }
         {
             LightArgs a = light_args(768, m->att, rx + 3072, re + 2);
-            k_light<768, PRO_TO16, 192><<<B, 192, 0, m->st>>>(a);
+            k_light<768, PRO_TO16, 192, 1><<<B, 192, 0, m->st>>>(a);
         }
         {
             GemmArgs a = gemm_args(m->mbank[l][1], nullptr, 0, nullptr, nullptr);
@@ -651,7 +652,7 @@ static int launch_step_pythia_batched(sm_machine* m, int parts, hipEvent_t hs, h
             k_gemm<768, 1, 1, EPI_PART><<<dim3(m->mbank[l][2].ntiles, RT), 256, 0, m->st>>>(a);
             PyRowArgs e = rows_args();
             const MfmaPlate& F = m->mbank[l][2];
-            e.partA = P0; e.ksA = 1; e.kinA = 768; e.rowinfoA = rB; e.csumA = F.csum; e.weA = F.e; e.biasA = F.b;
+            e.partA = P0; e.kinA = 768; e.rowinfoA = rB; e.csumA = F.csum; e.weA = F.e; e.biasA = F.b;
             e.planes1 = pC; e.rowinfo1 = rC;
             e.rpileA = rp + 2 * 3072; e.rpre = m->r_fcpre + l * 3072; e.routA = m->r_hid + l * 3072;
             e.rx1 = m->r_x16 + (l * 4 + 3) * 3072; e.rex1 = m->r_exls + (l * 4 + 3) * 2;
@@ -677,7 +678,7 @@ static int launch_step_pythia_batched(sm_machine* m, int parts, hipEvent_t hs, h
             a.K = 768; a.rows = B; a.X = m->att; a.pos = ctl + CTL_POS; a.plen = ctl + CTL_PLEN;
             a.planes = pD; a.rowinfo = rD; a.tb = tb; a.rec_pos = recp;
             a.rx16 = m->r_x16 + (l * 4 + 1) * 3072; a.rexls = m->r_exls + (l * 4 + 1) * 2;
-            k_light<768, PRO_TO16, 192><<<B, 192, 0, m->st>>>(a);
+            k_light<768, PRO_TO16, 192, 1><<<B, 192, 0, m->st>>>(a);
             GemmArgs g = gemm_args(m->mbank[l][1], pD, rD);
             g.part = P3;
             k_gemm<768, 1, 1, EPI_PART><<<dim3(m->mbank[l][1].ntiles, RT), 256, 0, m->st>>>(g);
@@ -686,8 +687,8 @@ static int launch_step_pythia_batched(sm_machine* m, int parts, hipEvent_t hs, h
             PyRowArgs a = rows_args();
             const MfmaPlate& Pp = m->mbank[l][1];
             const MfmaPlate& Pm = m->mbank[l][3];
-            a.partA = P3; a.ksA = 1; a.kinA = 768; a.rowinfoA = rD; a.csumA = Pp.csum; a.weA = Pp.e; a.biasA = Pp.b;
-            a.partB = P0; a.ksB = 4; a.kinB = 3072; a.rowinfoB = rC; a.csumB = Pm.csum; a.weB = Pm.e; a.biasB = Pm.b;
+            a.partA = P3; a.kinA = 768; a.rowinfoA = rD; a.csumA = Pp.csum; a.weA = Pp.e; a.biasA = Pp.b;
+            a.partB = P0; a.kinB = 3072; a.rowinfoB = rC; a.csumB = Pm.csum; a.weB = Pm.e; a.biasB = Pm.b;
             a.rpileA = rp + 3072; a.routA = m->r_resid + (l * 2 + 0) * 768;
             a.rpileB = rp + 3 * 3072; a.routB = m->r_resid + (l * 2 + 1) * 768;
             gauges(a, l + 1);
@@ -1367,13 +1368,13 @@ static void rows_product(const sm_plate* p, const int64_t* x16, int32_t rows, in
     ga.K = P.K; ga.N = P.N; ga.rows = rows; ga.RT = RT; ga.W = P.W; ga.csum = P.csum; ga.we = P.e; ga.bias = P.b;
     ga.planes = p->planes; ga.rowinfo = p->rowinfo; ga.Y = (i64*)pile; ga.ystride = P.N;
     if (P.K == 768) {
-        k_light<768, PRO_X16, 192><<<rows, 192, 0, s>>>(la);
+        k_light<768, PRO_X16, 192, 1><<<rows, 192, 0, s>>>(la);
         if (P.N > 3072)       // head-shaped plates: the head's kernel (light planes in LDS)
             k_head_rows<RT, EPI_PILE><<<head_rows_grid(P.ntiles), 256, 0, s>>>(ga);
         else                  // layer-shaped plates: one column tile per block, K split over its four waves
             k_gemm<768, 1, 1, EPI_PILE><<<dim3(P.ntiles, RT), 256, 0, s>>>(ga);
     } else {
-        k_light<3072, PRO_X16, 768><<<rows, 768, 0, s>>>(la);
+        k_light<3072, PRO_X16, 768, 1><<<rows, 768, 0, s>>>(la);
         k_gemm<3072, 1, 1, EPI_PILE><<<dim3(P.ntiles, RT), 256, 0, s>>>(ga);
     }
 }
