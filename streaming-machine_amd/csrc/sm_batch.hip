@@ -24,7 +24,8 @@ struct LightArgs {
     const int* pos; const int* plen;
     int skip_prompt;              // 1: nothing to do at a prompt position whose word is known (the head)
     signed char* planes;          // [RT][KS][3][64][16]: xh, xl', c
-    int* rowinfo;                 // [rows][8]: ex, LS lo, LS hi, e2, SXh, SXl, n32768
+    int* rowinfo;                 // [rows][8]: ex, S1, S2 lo, S2 hi, SXh, SXl, n32768 (a gauged light's consumer
+                                  // turns ex, S1, S2 into LS and the power factor, off the light's critical path)
     Tables tb;
     const int* rec_pos; i64* rx16; i64* rexls;    // stream 0's record
     // PRO_ADD_GAUGE / PRO_EDGE_TO16: the producing bank's epilogue first, from its partial accumulators
@@ -68,7 +69,9 @@ __global__ __launch_bounds__(NT) void k_light(LightArgs a) {
     i64 i_ex = 0, i_ls = 0, i_e2 = 0, i_sxh = 0, i_sxl = 0, i_n32 = 0;
     if (PRO == PRO_ADD_GAUGE || PRO == PRO_EDGE_TO16) {
         const int* ri = a.rowinfo + (size_t)r * 8;
-        i_ex = ri[0]; i_ls = (i64)(((u64)(unsigned)ri[2] << 32) | (unsigned)ri[1]); i_e2 = ri[3];
+        i_ex = ri[0];
+        if (PRO == PRO_EDGE_TO16)       // fc's gauge (base2.py:55-60) from the light's facts: scalar reads
+            i_ls = gauge_ls_pow(ri[1], (i64)(((u64)(unsigned)ri[3] << 32) | (unsigned)ri[2]), i_ex, a.tb, i_e2);
         i_sxh = ri[4]; i_sxl = ri[5]; i_n32 = ri[6];
     }
     const bool rec_in = r == 0 && a.rec_pos && *a.rec_pos == p;
@@ -190,12 +193,15 @@ __global__ __launch_bounds__(NT) void k_light(LightArgs a) {
             const int* q = red + 24 + 6 * w;
             S1 += q[0]; S2h += q[1]; S2l += q[2]; SXh += q[3]; SXl += q[4]; N32 += q[5];
         }
-        i64 ls = 0, e2 = 0;
-        if (PRO == PRO_GAUGE || PRO == PRO_EMBED || PRO == PRO_ADD_GAUGE) ls = gauge_ls_pow(S1, (S2h << 16) + S2l, ex, a.tb, e2);
+        const i64 S2 = (S2h << 16) + S2l;
         int* ri = a.rowinfo + (size_t)r * 8;
-        ri[0] = (int)ex; ri[1] = (int)(u64)ls; ri[2] = (int)((u64)ls >> 32); ri[3] = (int)e2;
+        ri[0] = (int)ex; ri[1] = (int)S1; ri[2] = (int)(u64)S2; ri[3] = (int)((u64)S2 >> 32);
         ri[4] = (int)SXh; ri[5] = (int)SXl; ri[6] = (int)N32;
-        if (rec && a.rexls) { a.rexls[0] = ex; a.rexls[1] = ls; }
+        if (rec && a.rexls) {
+            i64 e2;
+            a.rexls[0] = ex;
+            a.rexls[1] = PRO == PRO_GAUGE || PRO == PRO_EMBED || PRO == PRO_ADD_GAUGE ? gauge_ls_pow(S1, S2, ex, a.tb, e2) : 0;
+        }
     }
 }
 
@@ -222,6 +228,9 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs a) {
     const int s0 = kb * (KS / KSPLIT) + wave * NS;
     const v4* Wb = reinterpret_cast<const v4*>(a.W) + (size_t)nt * KS * 128 + lane;
     const v4* Ab = reinterpret_cast<const v4*>(a.planes) + lane;
+    // EPI_GAUGED: row tid's light facts first (loads complete in order: its gauge need not wait for the tiles)
+    v4 gf = {0, 0, 0, 0};
+    if (EPI == EPI_GAUGED) gf = *reinterpret_cast<const v4*>(a.rowinfo + (size_t)(tid < a.rows ? tid : 0) * 8);
     v4 wh[NS], wl[NS], xh[NS][RT], xl[NS][RT];
 #pragma unroll
     for (int i = 0; i < NS; i++) {
@@ -238,6 +247,11 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs a) {
     const int n32 = lane < a.rows ? a.rowinfo[lane * 8 + 6] : 0;
     const int rsv = tid < a.rows * 8 ? a.rowinfo[tid] : 0;
     const int rsv2 = tid + 256 < a.rows * 8 ? a.rowinfo[tid + 256] : 0;
+    // EPI_GAUGED: thread r < rows turns row r's light facts into LS and the power factor (table reads in
+    // flight during the contraction); they replace S1, S2 in the LDS copy of the row facts
+    i64 g_ls = 0, g_e2 = 0;
+    if (EPI == EPI_GAUGED)
+        g_ls = gauge_ls_pow_v(gf[1], (i64)(((u64)(unsigned)gf[3] << 32) | (unsigned)gf[2]), gf[0], a.tb, g_e2);
     const int j = nt * 16 + (lane & 15);
     const bool jok = j < a.N;
     i64 swh = 0, swl = 0, we = 0, bc = 0;
@@ -271,8 +285,12 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs a) {
         for (int k3 = 0; k3 < 3; k3++)
 #pragma unroll
             for (int q = 0; q < 4; q++) red[(((wave * RT + t) * 3 + k3) * 4 + q) * 64 + lane] = acc[t][k3][q];
-    if (tid < a.rows * 8) rinfo[tid] = rsv;
-    if (tid + 256 < a.rows * 8) rinfo[tid + 256] = rsv2;
+    const bool keep1 = EPI != EPI_GAUGED || (tid & 7) == 0 || (tid & 7) > 3;      // slots 1-3 carry LS, e2
+    if (tid < a.rows * 8 && keep1) rinfo[tid] = rsv;
+    if (tid + 256 < a.rows * 8 && keep1) rinfo[tid + 256] = rsv2;
+    if (EPI == EPI_GAUGED && tid < a.rows) {
+        rinfo[tid * 8 + 1] = (int)(u64)g_ls; rinfo[tid * 8 + 2] = (int)((u64)g_ls >> 32); rinfo[tid * 8 + 3] = (int)g_e2;
+    }
     __syncthreads();
     int fin[RT][3];
 #pragma unroll
@@ -333,6 +351,8 @@ __global__ __launch_bounds__(256) void k_head_rows(GemmArgs a) {
     const int p = a.pos ? *a.pos : 0;
     if ((EPI == EPI_HEAD || EPI == EPI_PHEAD) && p < *a.plen - 1) return;
     const int ntiles = (a.N + 15) >> 4, G = gridDim.x;
+    v4 gf = {0, 0, 0, 0};          // EPI_HEAD: row tid's light facts, before the weight stream
+    if (EPI == EPI_HEAD) gf = *reinterpret_cast<const v4*>(a.rowinfo + (size_t)(tid < a.rows ? tid : 0) * 8);
     const v4* Wg = reinterpret_cast<const v4*>(a.W) + tid;
     auto gfetch = [&](v4 (&r)[PER], int tile) {
         const v4* src = Wg + (size_t)min(tile, ntiles - 1) * TV;
@@ -351,8 +371,15 @@ __global__ __launch_bounds__(256) void k_head_rows(GemmArgs a) {
     v4 xh[KS], xl[KS];
 #pragma unroll
     for (int s = 0; s < KS; s++) { xh[s] = Ab[s * 192]; xl[s] = Ab[s * 192 + 64]; }
-    if (tid < a.rows * 8) rinfo[tid] = a.rowinfo[tid];
-    if (tid + 256 < a.rows * 8) rinfo[tid + 256] = a.rowinfo[tid + 256];
+    // EPI_HEAD: thread r < rows turns row r's light facts into LS and the power factor (slots 1-3)
+    const bool keep1 = EPI != EPI_HEAD || (tid & 7) == 0 || (tid & 7) > 3;
+    if (tid < a.rows * 8 && keep1) rinfo[tid] = a.rowinfo[tid];
+    if (tid + 256 < a.rows * 8 && keep1) rinfo[tid + 256] = a.rowinfo[tid + 256];
+    if (EPI == EPI_HEAD && tid < a.rows) {
+        i64 e2;
+        const i64 ls = gauge_ls_pow_v(gf[1], (i64)(((u64)(unsigned)gf[3] << 32) | (unsigned)gf[2]), gf[0], a.tb, e2);
+        rinfo[tid * 8 + 1] = (int)(u64)ls; rinfo[tid * 8 + 2] = (int)((u64)ls >> 32); rinfo[tid * 8 + 3] = (int)e2;
+    }
     const bool rec0 = a.rec_pos && *a.rec_pos == p;
     i64 bv[4];
     int bi[4];

@@ -157,6 +157,16 @@ SMD i64 gauge_ls_pow(i64 s1, i64 s2, i64 ex, const Tables& tb, i64& e2) {
     const i64 l2 = wadd((i64)t * 65536, lg);
     return wadd(wsub(l2 >> 1, tb.log768), wmul(ex, 65536));
 }
+// the same at a row that differs between lanes (vector table reads)
+SMD i64 gauge_ls_pow_v(i64 s1, i64 s2, i64 ex, const Tables& tb, i64& e2) {
+    i64 V = wadd(wsub(wmul(768, s2), wmul(s1, s1)), eps_term(tb.eps40, ex));
+    int t; i64 m;
+    log2_parts(V, t, m);
+    const i64 lg = tb.arith ? log2_entry((int)m) : tb.LOG2[m];
+    e2 = tab_gpow(tb, t & 1, m);
+    const i64 l2 = wadd((i64)t * 65536, lg);
+    return wadd(wsub(l2 >> 1, tb.log768), wmul(ex, 65536));
+}
 
 // ---------------- wave64 reductions through DPP (a few VALU cycles per step) ----------------
 // update_dpp(old = 0, ...): lanes a step does not reach contribute 0, the identity of +, | and max of naturals
