@@ -138,9 +138,9 @@ int sm_stage_gauge_log(const sm_tables* t, const int64_t* R, int32_t rows, int64
 int sm_stage_race(const int64_t* v, int64_t n, int64_t* out_index, void* stream);                       /* base2.py:34-40 */
 
 /* One new position's attention for one stream (base2.py:85-100 for the last row; base2_stream.swift:120-133
- * without its 64-position cap).  qkv: device int64 [2304] (the gauged q, k, v of position pos); the caches
- * hold positions < pos and receive position pos: k16 int32 [ctx][768], ek int32 [ctx][12], v int32
- * [ctx][768]; out: device int64 [768]. */
+ * without its 64-position cap).  qkv: device int64 [2304] (the gauged q, k, v of position pos); the caches,
+ * head-major, hold positions < pos and receive position pos: k16 int32 [12][ctx][64], ek int32 [12][ctx], v
+ * int32 [12][ctx][64]; out: device int64 [768]. */
 int sm_stage_attend(const sm_tables* t, const int64_t* qkv, int32_t* k16, int32_t* ek, int32_t* v,
                     int32_t pos, int32_t ctx, int64_t* out, void* stream);
 

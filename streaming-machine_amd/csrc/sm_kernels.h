@@ -69,9 +69,10 @@ struct GemvArgs {
 
 struct AttArgs {
     const i64* QKV;     // [B][2304]
-    int* K16;           // [B][ctx][768]  per-head 16-bit keys (values in [-32768, 32768])
-    int* EK;            // [B][ctx][12]   their water levels
-    int* V;             // [B][ctx][768]  raw gauged values (checked to fit 32 bits)
+    // the cache, head-major so that a (stream, head)'s positions are contiguous: [B][12 heads][ctx][64]
+    int* K16;           // [B][12][ctx][64] per-head 16-bit keys (values in [-32768, 32768])
+    int* EK;            // [B][12][ctx]     their water levels
+    int* V;             // [B][12][ctx][64] raw gauged values (checked to fit 32 bits)
     i64* out;           // [B][768]
     const int* pos;     // position being written and read up to (inclusive)
     int ctx;

@@ -426,9 +426,10 @@ template <int MODEL>
 SMD void attend_short(const AttArgs& a, int p, int h, int b, int* q_s, int* w_s) {
     const int lane = threadIdx.x;
     const i64* qkv = a.QKV + (size_t)b * 2304;
-    int* K16 = a.K16 + (size_t)b * a.ctx * 768;
-    int* EK = a.EK + (size_t)b * a.ctx * 12;
-    int* V = a.V + (size_t)b * a.ctx * 768;
+    const size_t hb = ((size_t)b * 12 + h) * a.ctx;         // this (stream, head)'s cache rows
+    int* K16 = a.K16 + hb * 64;
+    int* EK = a.EK + hb;
+    int* V = a.V + hb * 64;
     const bool rec = b == 0 && a.rec_pos && *a.rec_pos == p;
     // the new q, k, v first (loads complete in order), then the cached rows and columns
     i64 qv = qkv[MODEL == 1 ? h * 192 + lane : h * 64 + lane];
@@ -438,14 +439,14 @@ SMD void attend_short(const AttArgs& a, int p, int h, int b, int* q_s, int* w_s)
     int ekl = 0;
     {
         const int sr = lane < p ? lane : 0;                  // every lane loads (row 0 stands in past p)
-        const v4i* kr = reinterpret_cast<const v4i*>(K16 + (size_t)sr * 768 + h * 64);
+        const v4i* kr = reinterpret_cast<const v4i*>(K16 + (size_t)sr * 64);
 #pragma unroll
         for (int c = 0; c < 16; c++) krow[c] = kr[c];
-        ekl = EK[(size_t)sr * 12 + h];
+        ekl = EK[sr];
     }
     int vcol[64];
 #pragma unroll
-    for (int s = 0; s < 64; s++) vcol[s] = V[(size_t)(s < p ? s : 0) * 768 + h * 64 + lane];
+    for (int s = 0; s < 64; s++) vcol[s] = V[(size_t)(s < p ? s : 0) * 64 + lane];
     if (MODEL == 1) {                                        // the turns (pythia_base2.py:116-123)
         const int r = a.rot >> 1;
         const i64 pq = __shfl(qv, lane < r ? lane + r : lane - r, 64);
@@ -462,10 +463,10 @@ SMD void attend_short(const AttArgs& a, int p, int h, int b, int* q_s, int* w_s)
     const int shq = water_shift(wave_or64(iabs64(qv))), shk = water_shift(wave_or64(iabs64(kv)));
     const int q16 = (int)rsh(qv, shq), k16 = (int)rsh(kv, shk);
     const i64 eq = -16 + shq, ekn = -16 + shk;
-    K16[(size_t)p * 768 + h * 64 + lane] = k16;
-    if (lane == 0) EK[(size_t)p * 12 + h] = (int)ekn;
+    K16[(size_t)p * 64 + lane] = k16;
+    if (lane == 0) EK[p] = (int)ekn;
     if (vv < (i64)INT32_MIN || vv > (i64)INT32_MAX) atomicOr(a.err, SM_ERR_V32);
-    V[(size_t)p * 768 + h * 64 + lane] = (int)vv;
+    V[(size_t)p * 64 + lane] = (int)vv;
     // scores (base2.py:94): lane s < p its cached row, lane p the new key
     q_s[lane] = q16;
     i64 dot = 0;
@@ -559,37 +560,28 @@ __global__ __launch_bounds__(NTHR, ONE ? 1 : 3) void k_attend(AttArgs a) {
         }
     }
     const i64* qkv = a.QKV + (size_t)b * 2304;
-    int* K16 = a.K16 + (size_t)st * a.ctx * 768;
-    int* EK = a.EK + (size_t)st * a.ctx * 12;
-    int* V = a.V + (size_t)st * a.ctx * 768;
+    const size_t hb = ((size_t)st * 12 + h) * a.ctx;        // this (stream, head)'s cache rows
+    int* K16 = a.K16 + hb * 64;
+    int* EK = a.EK + hb;
+    int* V = a.V + hb * 64;
     const bool rec = store && b == 0 && a.rec_pos && *a.rec_pos == p;
 
     // requests first (vector loads complete in order): the new q, k, v; then the cached keys of the first
     // ATT_PRE passes (a position's four lanes read its 256-byte row as 4 x 64 contiguous bytes: lane qd holds
-    // dimensions 16 u + 4 qd .. + 3 of step u) and the values of positions g, g + 16, .. in the same passes
-    // (16 lanes a 256-byte row, four rows a wave)
+    // dimensions 16 u + 4 qd .. + 3 of step u); the values (16 lanes a 256-byte row, four rows a wave) follow
+    // once the new position is in
     i64 xnew = wave < 3 ? qkv[MODEL == 1 ? h * 192 + wave * 64 + lane : wave * 768 + h * 64 + lane] : 0;
+    // (unconditional, rows past p clamped to row 0: a load under a branch would make the first wait below
+    // a wait for every load in flight)
     v4i kp[ATT_PRE][4];
-    int ekp[ATT_PRE] = {};
+    int ekp[ATT_PRE];
 #pragma unroll
     for (int c = 0; c < ATT_PRE; c++) {
-        if (64 * c < p) {                                    // uniform: whole passes only
-            const int sr = sl + 64 * c < p ? sl + 64 * c : 0;
-            const v4i* kr = reinterpret_cast<const v4i*>(K16 + (size_t)sr * 768 + h * 64) + qd;
+        const int sr = sl + 64 * c < p ? sl + 64 * c : 0;
+        const v4i* kr = reinterpret_cast<const v4i*>(K16 + (size_t)sr * 64) + qd;
 #pragma unroll
-            for (int u = 0; u < 4; u++) kp[c][u] = kr[4 * u];
-            ekp[c] = EK[(size_t)sr * 12 + h];
-        }
-    }
-    constexpr int NV = 64 * ATT_PRE / 16;                    // value rows per thread requested at launch
-    v4i vp[NV];
-#pragma unroll
-    for (int i = 0; i < NV; i++) {
-        vp[i] = v4i{0, 0, 0, 0};
-        if (16 * i < p) {                                    // uniform
-            const int sv = g + 16 * i;
-            vp[i] = reinterpret_cast<const v4i*>(V + (size_t)(sv < p ? sv : 0) * 768 + h * 64)[d4];
-        }
+        for (int u = 0; u < 4; u++) kp[c][u] = kr[4 * u];
+        ekp[c] = EK[sr];
     }
     if (MODEL == 1 && wave < 2) {        // the turns (pythia_base2.py:116-123): pair (i, i + rot/2)
         const int r = a.rot >> 1;
@@ -611,19 +603,29 @@ __global__ __launch_bounds__(NTHR, ONE ? 1 : 3) void k_attend(AttArgs a) {
             if (lane == 0) eqs = -16 + sh;
         } else {
             k16s[lane] = x16;
-            if (store) K16[(size_t)p * 768 + h * 64 + lane] = x16;
+            if (store) K16[(size_t)p * 64 + lane] = x16;
             if (lane == 0) {
                 eks = -16 + sh;
-                if (store) EK[(size_t)p * 12 + h] = -16 + sh;
+                if (store) EK[p] = -16 + sh;
             }
         }
     } else if (wave == 2) {
         const i64 x = xnew;
         if (x < (i64)INT32_MIN || x > (i64)INT32_MAX) atomicOr(a.err, SM_ERR_V32);
         vs[lane] = (int)x;
-        if (store) V[(size_t)p * 768 + h * 64 + lane] = (int)x;
+        if (store) V[(size_t)p * 64 + lane] = (int)x;
     }
     __syncthreads();
+
+    // the values of positions g, g + 16, .. of the first ATT_PRE passes, requested now: the new q and the
+    // keys were ahead of them, and they arrive while the scores are formed
+    constexpr int NV = 64 * ATT_PRE / 16;
+    v4i vp[NV];
+#pragma unroll
+    for (int i = 0; i < NV; i++) {
+        const int sv = g + 16 * i;
+        vp[i] = reinterpret_cast<const v4i*>(V + (size_t)(sv < p ? sv : 0) * 64)[d4];
+    }
 
     // scores (base2.py:94 / pythia_base2.py:133) and their maximum
     const i64 eq = eqs;
@@ -650,10 +652,10 @@ __global__ __launch_bounds__(NTHR, ONE ? 1 : 3) void k_attend(AttArgs a) {
                         ek = ekp[cc];
                     }
             } else {
-                const v4i* kr = reinterpret_cast<const v4i*>(K16 + (size_t)s * 768 + h * 64) + qd;
+                const v4i* kr = reinterpret_cast<const v4i*>(K16 + (size_t)s * 64) + qd;
 #pragma unroll
                 for (int u = 0; u < 4; u++) kk[u] = kr[4 * u];
-                ek = EK[(size_t)s * 12 + h];
+                ek = EK[s];
             }
         } else {
 #pragma unroll
@@ -698,7 +700,7 @@ __global__ __launch_bounds__(NTHR, ONE ? 1 : 3) void k_attend(AttArgs a) {
         if (sv < p) acc(arr[sv], vp[i]);
     }
     for (int sv = g + 16 * NV; sv < p; sv += 16)                 // past the requested positions
-        acc(arr[sv], reinterpret_cast<const v4i*>(V + (size_t)sv * 768 + h * 64)[d4]);
+        acc(arr[sv], reinterpret_cast<const v4i*>(V + (size_t)sv * 64)[d4]);
     if ((p & 15) == g) acc(arr[p], reinterpret_cast<const v4i*>(vs)[d4]);   // the new position (from LDS)
     if (MODEL == 1 && (double)vmax * (double)z >= 4611686018427387904.0) atomicOr(a.err, SM_ERR_RANGE);
     // the 16 position groups through LDS, summed by wave 0
@@ -734,7 +736,7 @@ template <int MODEL>
 __global__ __launch_bounds__(128) void k_kv_rows(AttArgs a) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, h = blockIdx.x, r = blockIdx.y;
     const int pm = a.rowmap[r], st = pm >> 16, p = pm & 0xFFFF;
-    const size_t at = (size_t)st * a.ctx + p;               // the row's cache slot
+    const size_t at = ((size_t)st * 12 + h) * a.ctx + p;    // the row's cache slot (stream, head, position)
     i64 x = a.QKV[(size_t)r * 2304 + (MODEL == 1 ? h * 192 + (wave + 1) * 64 + lane : (wave + 1) * 768 + h * 64 + lane)];
     if (wave == 0) {
         if (MODEL == 1) {                                    // the turn, pair (i, i + rot/2)
@@ -748,11 +750,11 @@ __global__ __launch_bounds__(128) void k_kv_rows(AttArgs a) {
             }
         }
         const int sh = water_shift(wave_or64(iabs64(x)));
-        a.K16[at * 768 + h * 64 + lane] = (int)rsh(x, sh);
-        if (lane == 0) a.EK[at * 12 + h] = -16 + sh;
+        a.K16[at * 64 + lane] = (int)rsh(x, sh);
+        if (lane == 0) a.EK[at] = -16 + sh;
     } else {
         if (x < (i64)INT32_MIN || x > (i64)INT32_MAX) atomicOr(a.err, SM_ERR_V32);
-        a.V[at * 768 + h * 64 + lane] = (int)x;
+        a.V[at * 64 + lane] = (int)x;
     }
 }
 

@@ -234,7 +234,7 @@ struct sm_machine {
     sm_tables T;
     // state
     i64 *R = nullptr, *QKV = nullptr, *att = nullptr, *hid = nullptr;
-    int *K16 = nullptr, *EK = nullptr, *V = nullptr;   // [L][B][ctx][...]
+    int *K16 = nullptr, *EK = nullptr, *V = nullptr;   // [L][B][12 heads][ctx][64] (EK: [L][B][12][ctx])
     int* seq = nullptr;                                 // [B][ctx + 1]
     int* words = nullptr;                               // [B][ctx + 1]
     int* ctl = nullptr;
@@ -1172,9 +1172,18 @@ extern "C" int sm_read(sm_machine* m, int32_t what, int32_t layer, int32_t strea
     size_t need = 0;
     auto kv_ok = [&]() { return layer >= 0 && layer < 12 && pos >= 0 && pos < m->ctx; };
     switch (what) {
-        case SM_READ_K16: if (!kv_ok()) return fail(SM_E_ARG, "sm_read: layer/pos"); src = m->K16 + (((size_t)layer * B + stream) * ctx + pos) * 768; need = 768 * 4; break;
-        case SM_READ_EK: if (!kv_ok()) return fail(SM_E_ARG, "sm_read: layer/pos"); src = m->EK + (((size_t)layer * B + stream) * ctx + pos) * 12; need = 12 * 4; break;
-        case SM_READ_V: if (!kv_ok()) return fail(SM_E_ARG, "sm_read: layer/pos"); src = m->V + (((size_t)layer * B + stream) * ctx + pos) * 768; need = 768 * 4; break;
+        case SM_READ_K16: case SM_READ_EK: case SM_READ_V: {
+            // one position's row, gathered from the 12 heads of the head-major cache
+            if (!kv_ok()) return fail(SM_E_ARG, "sm_read: layer/pos");
+            const size_t h0 = ((size_t)layer * B + stream) * 12 * ctx + pos;     // head 0's slot
+            const bool ek = what == SM_READ_EK;
+            const size_t w = ek ? 4 : 256;
+            if (bytes != 12 * w) return fail(SM_E_ARG, "sm_read: expected " + std::to_string(12 * w) + " bytes");
+            const void* s0 = ek ? (const void*)(m->EK + h0) : (const void*)((what == SM_READ_K16 ? m->K16 : m->V) + h0 * 64);
+            HIP_TRY(hipStreamSynchronize(m->st));
+            HIP_TRY(hipMemcpy2D(dst, w, s0, ctx * w, w, 12, hipMemcpyDeviceToHost));
+            return SM_OK;
+        }
         case SM_READ_RESID: src = m->R + (size_t)stream * 768; need = 768 * 8; break;
         case SM_READ_SEQ: src = m->seq + (size_t)stream * (ctx + 1); need = (ctx + 1) * 4; break;
         case SM_READ_REC_X16: src = m->r_x16; need = 12 * 4 * 3072 * 8; break;
