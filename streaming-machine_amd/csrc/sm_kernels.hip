@@ -21,6 +21,17 @@
 #define NTHR 256
 typedef int v4i __attribute__((ext_vector_type(4)));
 
+// A buffer resource over [base, base + bytes) (raw, stride 0; the gfx9 word-3 format): a load past the end
+// returns zeros and sends no request to memory, so a fixed sequence of loads can cover a variable number of
+// cache rows with no branch around them (a branch would make the next wait count every load in flight).
+SMD __amdgpu_buffer_rsrc_t buf_rsrc(const void* base, unsigned bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, (int)bytes, 0x00020000);
+}
+SMD v4i buf_load4(__amdgpu_buffer_rsrc_t r, unsigned off) {
+    return __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 0));
+}
+SMD int buf_load1(__amdgpu_buffer_rsrc_t r, unsigned off) { return (int)__builtin_amdgcn_raw_buffer_load_b32(r, (int)off, 0, 0); }
+
 // ---------------------------------------------------------------------------------------------------------
 // block reductions (4 waves).  red: 8 slots, free on entry; every thread gets the result.
 template <typename F>
@@ -435,18 +446,16 @@ SMD void attend_short(const AttArgs& a, int p, int h, int b, int* q_s, int* w_s)
     i64 qv = qkv[MODEL == 1 ? h * 192 + lane : h * 64 + lane];
     i64 kv = qkv[MODEL == 1 ? h * 192 + 64 + lane : 768 + h * 64 + lane];
     const i64 vv = qkv[MODEL == 1 ? h * 192 + 128 + lane : 1536 + h * 64 + lane];
+    // the cached rows s < p (lanes and columns past p read zeros without a memory request)
+    const __amdgpu_buffer_rsrc_t rk = buf_rsrc(K16, (unsigned)p * 256), re = buf_rsrc(EK, (unsigned)p * 4),
+                                 rv = buf_rsrc(V, (unsigned)p * 256);
     v4i krow[16];
-    int ekl = 0;
-    {
-        const int sr = lane < p ? lane : 0;                  // every lane loads (row 0 stands in past p)
-        const v4i* kr = reinterpret_cast<const v4i*>(K16 + (size_t)sr * 64);
 #pragma unroll
-        for (int c = 0; c < 16; c++) krow[c] = kr[c];
-        ekl = EK[sr];
-    }
+    for (int c = 0; c < 16; c++) krow[c] = buf_load4(rk, (unsigned)lane * 256 + 16 * c);
+    const int ekl = buf_load1(re, (unsigned)lane * 4);
     int vcol[64];
 #pragma unroll
-    for (int s = 0; s < 64; s++) vcol[s] = V[(size_t)(s < p ? s : 0) * 64 + lane];
+    for (int s = 0; s < 64; s++) vcol[s] = buf_load1(rv, (unsigned)(s * 64 + lane) * 4);
     if (MODEL == 1) {                                        // the turns (pythia_base2.py:116-123)
         const int r = a.rot >> 1;
         const i64 pq = __shfl(qv, lane < r ? lane + r : lane - r, 64);
@@ -571,17 +580,17 @@ __global__ __launch_bounds__(NTHR, ONE ? 1 : 3) void k_attend(AttArgs a) {
     // dimensions 16 u + 4 qd .. + 3 of step u); the values (16 lanes a 256-byte row, four rows a wave) follow
     // once the new position is in
     i64 xnew = wave < 3 ? qkv[MODEL == 1 ? h * 192 + wave * 64 + lane : wave * 768 + h * 64 + lane] : 0;
-    // (unconditional, rows past p clamped to row 0: a load under a branch would make the first wait below
-    // a wait for every load in flight)
+    // (buffer loads bounded at position p: rows past it read zeros and cost no memory traffic)
+    const __amdgpu_buffer_rsrc_t rk = buf_rsrc(K16, (unsigned)p * 256), re = buf_rsrc(EK, (unsigned)p * 4),
+                                 rv = buf_rsrc(V, (unsigned)p * 256);
     v4i kp[ATT_PRE][4];
     int ekp[ATT_PRE];
 #pragma unroll
     for (int c = 0; c < ATT_PRE; c++) {
-        const int sr = sl + 64 * c < p ? sl + 64 * c : 0;
-        const v4i* kr = reinterpret_cast<const v4i*>(K16 + (size_t)sr * 64) + qd;
+        const unsigned sr = sl + 64 * c;
 #pragma unroll
-        for (int u = 0; u < 4; u++) kp[c][u] = kr[4 * u];
-        ekp[c] = EK[sr];
+        for (int u = 0; u < 4; u++) kp[c][u] = buf_load4(rk, sr * 256 + (4 * u + qd) * 16);
+        ekp[c] = buf_load1(re, sr * 4);
     }
     if (MODEL == 1 && wave < 2) {        // the turns (pythia_base2.py:116-123): pair (i, i + rot/2)
         const int r = a.rot >> 1;
@@ -622,10 +631,7 @@ __global__ __launch_bounds__(NTHR, ONE ? 1 : 3) void k_attend(AttArgs a) {
     constexpr int NV = 64 * ATT_PRE / 16;
     v4i vp[NV];
 #pragma unroll
-    for (int i = 0; i < NV; i++) {
-        const int sv = g + 16 * i;
-        vp[i] = reinterpret_cast<const v4i*>(V + (size_t)(sv < p ? sv : 0) * 64)[d4];
-    }
+    for (int i = 0; i < NV; i++) vp[i] = buf_load4(rv, (unsigned)(g + 16 * i) * 256 + d4 * 16);
 
     // scores (base2.py:94 / pythia_base2.py:133) and their maximum
     const i64 eq = eqs;
