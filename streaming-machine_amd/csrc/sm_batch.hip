@@ -28,7 +28,7 @@ struct LightArgs {
                                   // turns ex, S1, S2 into LS and the power factor, off the light's critical path)
     Tables tb;
     const int* rec_pos; i64* rx16; i64* rexls;    // stream 0's record
-    // PRO_ADD_GAUGE / PRO_EDGE_TO16: the producing bank's epilogue first, from its partial accumulators
+    // PRO_ADD_GAUGE: the producing bank's epilogue first, from its partial accumulators
     const int* part; int kin;                     // [K slices][3][rows][K] int32 (HH, MID, LL); the bank's K
     const int* csum; const int* we; const i64* bias;   // the producing plate's column facts
     i64* Y;                                       // [rows][K]: the epilogue's row (R: read and written)
@@ -54,7 +54,7 @@ struct GemmArgs {
 // One block (256 threads) per stream row: the light of base2.py:24-27 (and the gauge of :55-60), written as
 // MFMA A planes plus the row's exponent, gauge, power factor and plane sums.  Each thread owns groups of four
 // consecutive k, so every plane byte group goes out as one 32-bit store.  KSP: the producing bank's K slices
-// (PRO_ADD_GAUGE / PRO_EDGE_TO16), a compile-time count so that every load of the row is in flight at once.
+// (PRO_ADD_GAUGE), a compile-time count so that every load of the row is in flight at once.
 template <int K, int PRO, int NT, int KSP>
 __global__ __launch_bounds__(NT) void k_light(LightArgs a) {
     constexpr int NG = K / 4, GPT = (NG + NT - 1) / NT, KS = K / 64, NW = NT / 64;
@@ -66,12 +66,10 @@ __global__ __launch_bounds__(NT) void k_light(LightArgs a) {
     i64 v[GPT][4];
     typedef int v4l __attribute__((ext_vector_type(4)));
     // the producing bank's light facts for this row (read before this block replaces them)
-    i64 i_ex = 0, i_ls = 0, i_e2 = 0, i_sxh = 0, i_sxl = 0, i_n32 = 0;
-    if (PRO == PRO_ADD_GAUGE || PRO == PRO_EDGE_TO16) {
+    i64 i_ex = 0, i_sxh = 0, i_sxl = 0, i_n32 = 0;
+    if (PRO == PRO_ADD_GAUGE) {
         const int* ri = a.rowinfo + (size_t)r * 8;
         i_ex = ri[0];
-        if (PRO == PRO_EDGE_TO16)       // fc's gauge (base2.py:55-60) from the light's facts: scalar reads
-            i_ls = gauge_ls_pow(ri[1], (i64)(((u64)(unsigned)ri[3] << 32) | (unsigned)ri[2]), i_ex, a.tb, i_e2);
         i_sxh = ri[4]; i_sxl = ri[5]; i_n32 = ri[6];
     }
     const bool rec_in = r == 0 && a.rec_pos && *a.rec_pos == p;
@@ -82,17 +80,14 @@ __global__ __launch_bounds__(NT) void k_light(LightArgs a) {
         for (int j = 0; j < 4; j++) v[m][j] = 0;
         if (g >= NG) continue;
         const int k = 4 * g;
-        if (PRO == PRO_ADD_GAUGE || PRO == PRO_EDGE_TO16) {
+        if (PRO == PRO_ADD_GAUGE) {
             typedef i64 v2q __attribute__((ext_vector_type(2)));
             // every load first (column facts, the stream, the partial slices), then the arithmetic
             const v4l c0 = *reinterpret_cast<const v4l*>(a.csum + 2 * k), c1 = *reinterpret_cast<const v4l*>(a.csum + 2 * k + 4);
             const v4l wv = *reinterpret_cast<const v4l*>(a.we + k);
             const v2q b01 = *reinterpret_cast<const v2q*>(a.bias + k), b23 = *reinterpret_cast<const v2q*>(a.bias + k + 2);
-            v2q y01 = {0, 0}, y23 = {0, 0};
-            if (PRO == PRO_ADD_GAUGE) {
-                y01 = *reinterpret_cast<const v2q*>(a.Y + (size_t)r * K + k);
-                y23 = *reinterpret_cast<const v2q*>(a.Y + (size_t)r * K + k + 2);
-            }
+            const v2q y01 = *reinterpret_cast<const v2q*>(a.Y + (size_t)r * K + k);
+            const v2q y23 = *reinterpret_cast<const v2q*>(a.Y + (size_t)r * K + k + 2);
             v4l hq[KSP], mq[KSP], lq[KSP];
 #pragma unroll
             for (int ks = 0; ks < KSP; ks++) {
@@ -110,15 +105,8 @@ __global__ __launch_bounds__(NT) void k_light(LightArgs a) {
             for (int j = 0; j < 4; j++) {
                 const i64 pile = 65536 * (i64)h[j] + 256 * (i64)mi[j] + lo[j] + 32768 * (i_sxh + sw[2 * j]) +
                                  128 * (i_sxl + sw[2 * j + 1]) + 16384 * (i64)a.kin + 128 * i_n32;
-                const i64 bc = bcs[j];
-                i64 y;
-                if (PRO == PRO_ADD_GAUGE) {
-                    y = wadd(ys[j], wadd(rsh(pile, -((i64)wv[j] + i_ex + 16)), bc));
-                    a.Y[(size_t)r * K + k + j] = y;
-                } else {
-                    y = edge1(wadd(power_known(pile, wsub(wmul((i64)wv[j] + i_ex + 16, 65536), i_ls), i_e2), bc), a.tb);
-                    if (a.Y) a.Y[(size_t)r * K + k + j] = y;
-                }
+                const i64 y = wadd(ys[j], wadd(rsh(pile, -((i64)wv[j] + i_ex + 16)), bcs[j]));
+                a.Y[(size_t)r * K + k + j] = y;
                 v[m][j] = y;
                 if (rec_in && a.rpile_in) a.rpile_in[k + j] = pile;
                 if (rec_in && a.rout_in) a.rout_in[k + j] = y;
@@ -212,7 +200,7 @@ __global__ __launch_bounds__(NT) void k_light(LightArgs a) {
 // for column l % 16.  Everything the block reads that depends on nothing else (weights, lights, row and column
 // facts) is issued before the first MFMA.
 //   EPI_PART: the accumulators go to part[kslice][3][rows][N]; the consumer's prologue finishes them.
-//   EPI_GAUGED / EPI_PILE: one K slice; the epilogue runs here.
+//   EPI_GAUGED / EPI_GAUGED_EDGE / EPI_PLAIN_ADD / EPI_PILE: one K slice; the epilogue runs here.
 template <int K, int RT, int KSPLIT, int EPI>
 __global__ __launch_bounds__(256) void k_gemm(GemmArgs a) {
     constexpr int KS = K / 64, NS = KS / (4 * KSPLIT);
@@ -228,9 +216,11 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs a) {
     const int s0 = kb * (KS / KSPLIT) + wave * NS;
     const v4* Wb = reinterpret_cast<const v4*>(a.W) + (size_t)nt * KS * 128 + lane;
     const v4* Ab = reinterpret_cast<const v4*>(a.planes) + lane;
-    // EPI_GAUGED: row tid's light facts first (loads complete in order: its gauge need not wait for the tiles)
+    // gauged epilogues: row tid's light facts first (loads complete in order: its gauge need not wait for the
+    // tiles)
+    constexpr bool GAUGED = EPI == EPI_GAUGED || EPI == EPI_GAUGED_EDGE;
     v4 gf = {0, 0, 0, 0};
-    if (EPI == EPI_GAUGED) gf = *reinterpret_cast<const v4*>(a.rowinfo + (size_t)(tid < a.rows ? tid : 0) * 8);
+    if (GAUGED) gf = *reinterpret_cast<const v4*>(a.rowinfo + (size_t)(tid < a.rows ? tid : 0) * 8);
     v4 wh[NS], wl[NS], xh[NS][RT], xl[NS][RT];
 #pragma unroll
     for (int i = 0; i < NS; i++) {
@@ -247,10 +237,10 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs a) {
     const int n32 = lane < a.rows ? a.rowinfo[lane * 8 + 6] : 0;
     const int rsv = tid < a.rows * 8 ? a.rowinfo[tid] : 0;
     const int rsv2 = tid + 256 < a.rows * 8 ? a.rowinfo[tid + 256] : 0;
-    // EPI_GAUGED: thread r < rows turns row r's light facts into LS and the power factor (table reads in
+    // gauged: thread r < rows turns row r's light facts into LS and the power factor (table reads in
     // flight during the contraction); they replace S1, S2 in the LDS copy of the row facts
     i64 g_ls = 0, g_e2 = 0;
-    if (EPI == EPI_GAUGED)
+    if (GAUGED)
         g_ls = gauge_ls_pow_v(gf[1], (i64)(((u64)(unsigned)gf[3] << 32) | (unsigned)gf[2]), gf[0], a.tb, g_e2);
     const int j = nt * 16 + (lane & 15);
     const bool jok = j < a.N;
@@ -285,10 +275,10 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs a) {
         for (int k3 = 0; k3 < 3; k3++)
 #pragma unroll
             for (int q = 0; q < 4; q++) red[(((wave * RT + t) * 3 + k3) * 4 + q) * 64 + lane] = acc[t][k3][q];
-    const bool keep1 = EPI != EPI_GAUGED || (tid & 7) == 0 || (tid & 7) > 3;      // slots 1-3 carry LS, e2
+    const bool keep1 = !GAUGED || (tid & 7) == 0 || (tid & 7) > 3;      // slots 1-3 carry LS, e2
     if (tid < a.rows * 8 && keep1) rinfo[tid] = rsv;
     if (tid + 256 < a.rows * 8 && keep1) rinfo[tid + 256] = rsv2;
-    if (EPI == EPI_GAUGED && tid < a.rows) {
+    if (GAUGED && tid < a.rows) {
         rinfo[tid * 8 + 1] = (int)(u64)g_ls; rinfo[tid * 8 + 2] = (int)((u64)g_ls >> 32); rinfo[tid * 8 + 3] = (int)g_e2;
     }
     __syncthreads();
@@ -322,13 +312,19 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs a) {
         if (rec && a.rpile) a.rpile[j] = pile;
         if (EPI == EPI_PILE) {
             a.Y[(size_t)row * a.ystride + j] = pile;
+        } else if (EPI == EPI_PLAIN_ADD) {             // the stream takes the plain bank (base2.py:73-76, 105)
+            i64* yp = a.Y + (size_t)row * a.ystride + j;
+            const i64 y = wadd(*yp, wadd(rsh(pile, -(we + ex + 16)), bc));
+            *yp = y;
+            if (rec && a.rout) a.rout[j] = y;
         } else if (EPI == EPI_PLAIN) {                 // the Pythia machine's qkv (foundation0/pythia_base2.py:114)
             const i64 y = wadd(rsh(pile, -(we + ex + 16)), bc);
             a.Y[(size_t)row * a.ystride + j] = y;
             if (rec && a.rout) a.rout[j] = y;
         } else {
             const i64 ls = (i64)(((u64)(unsigned)ri[2] << 32) | (unsigned)ri[1]);
-            const i64 y = wadd(power_known(pile, wsub(wmul(we + ex + 16, 65536), ls), (i64)ri[3]), bc);
+            i64 y = wadd(power_known(pile, wsub(wmul(we + ex + 16, 65536), ls), (i64)ri[3]), bc);
+            if (EPI == EPI_GAUGED_EDGE) y = edge1(y, a.tb);
             a.Y[(size_t)row * a.ystride + j] = y;
             if (rec && a.rout) a.rout[j] = y;
         }
@@ -756,14 +752,13 @@ BINST_L(768, PRO_TO16, 1)
 BINST_L(3072, PRO_TO16, 1)
 BINST_L(768, PRO_X16, 1)
 BINST_L(3072, PRO_X16, 1)
-BINST_L(768, PRO_ADD_GAUGE, 1)
 BINST_L(768, PRO_ADD_GAUGE, 4)
-BINST_L(3072, PRO_EDGE_TO16, 1)
 template __global__ void k_py_rows<PY_EMBED>(PyRowArgs);
 template __global__ void k_py_rows<PY_ADD>(PyRowArgs);
 template __global__ void k_py_rows<PY_EDGE>(PyRowArgs);
 #define BINST_G(K, RT, KSPLIT, EPI) template __global__ void k_gemm<K, RT, KSPLIT, EPI>(GemmArgs);
-#define BINST_GR(RT) BINST_G(768, RT, 1, EPI_GAUGED) BINST_G(768, RT, 1, EPI_PART) BINST_G(3072, RT, 4, EPI_PART) \
+#define BINST_GR(RT) BINST_G(768, RT, 1, EPI_GAUGED) BINST_G(768, RT, 1, EPI_GAUGED_EDGE) BINST_G(768, RT, 1, EPI_PLAIN_ADD) \
+    BINST_G(768, RT, 1, EPI_PART) BINST_G(3072, RT, 4, EPI_PART) \
     BINST_G(768, RT, 1, EPI_PILE) BINST_G(3072, RT, 1, EPI_PILE) BINST_G(768, RT, 1, EPI_PLAIN)
 BINST_GR(1)
 #define BINST_H(RT) template __global__ void k_head_rows<RT, EPI_HEAD>(GemmArgs); \

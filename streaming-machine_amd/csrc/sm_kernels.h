@@ -9,7 +9,6 @@ enum { PRO_GAUGE = 0,   // gauge_log of the stream row R (768): x16, ex, LS (bas
        PRO_X16 = 3,     // the light is given (int64 x16 values, ex = -16): the raw product test
        // batched streams: the producing bank's epilogue from its partial accumulators, then the light
        PRO_ADD_GAUGE = 4,   // R += rshift(pile, -(we + ex + 16)) + b, then PRO_GAUGE of R   (base2.py:105-106, 55-60)
-       PRO_EDGE_TO16 = 5,   // edge(power(pile, ...) + b), then PRO_TO16 of that row       (base2.py:106, 78-83, 24-27)
        // the Pythia machine (foundation0/pythia_base2.py)
        PRO_PGAUGE = 6,      // its gauge with the norm's gain and offset, then to16 of that row     (:100-110, 113)
        PRO_PEMBED = 7 };    // R = rshift(embed.w[word], -(embed.e[word] + 16)) (:153), then PRO_PGAUGE

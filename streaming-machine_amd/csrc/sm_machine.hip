@@ -394,14 +394,12 @@ static int launch_step_batched(sm_machine* m, int parts, hipEvent_t hs, hipEvent
         a.rec_pos = recp; a.rx16 = rx16; a.rexls = rexls; a.rowmap = rowmap;
         return a;
     };
-    // the producing bank's epilogue (from its partial accumulators) followed by the next light
-    auto finish_light = [&](const MfmaPlate& P, int ksplit, i64* Y, i64* rpile, i64* rout, i64* rx16, i64* rexls) {
+    // mproj's epilogue (from its four K slices of partial accumulators) added into the stream, then the next light
+    auto finish_light = [&](const MfmaPlate& P, i64* rpile, i64* rout, i64* rx16, i64* rexls) {
         LightArgs a = light_args(P.N, nullptr, rx16, rexls);
-        a.part = m->part_acc; a.kin = P.K; a.csum = P.csum; a.we = P.e; a.bias = P.b; a.Y = Y;
+        a.part = m->part_acc; a.kin = P.K; a.csum = P.csum; a.we = P.e; a.bias = P.b; a.Y = m->R;
         a.rpile_in = rpile; a.rout_in = rout;
-        if (P.N == 3072) k_light<3072, PRO_EDGE_TO16, 768, 1><<<B, 768, 0, m->st>>>(a);
-        else if (ksplit == 4) k_light<768, PRO_ADD_GAUGE, 192, 4><<<B, 192, 0, m->st>>>(a);
-        else k_light<768, PRO_ADD_GAUGE, 192, 1><<<B, 192, 0, m->st>>>(a);
+        k_light<768, PRO_ADD_GAUGE, 192, 4><<<B, 192, 0, m->st>>>(a);
     };
     auto gemm_args = [&](const MfmaPlate& P, i64* Y, int ystride, i64* rpile, i64* rout) {
         GemmArgs a{};
@@ -443,22 +441,24 @@ static int launch_step_batched(sm_machine* m, int parts, hipEvent_t hs, hipEvent
             LightArgs a = light_args(768, m->att, rx + 3072, re + 2);
             k_light<768, PRO_TO16, 192, 1><<<B, 192, 0, m->st>>>(a);
         }
-        {
-            GemmArgs a = gemm_args(m->mbank[l][1], nullptr, 0, nullptr, nullptr);
-            k_gemm<768, 1, 1, EPI_PART><<<dim3(m->mbank[l][1].ntiles, RT), 256, 0, m->st>>>(a);
+        {   // proj: the plain bank added into the stream; then the stream's light for fc
+            GemmArgs a = gemm_args(m->mbank[l][1], m->R, 768, rp + 3072, m->r_resid + (l * 2 + 0) * 768);
+            k_gemm<768, 1, 1, EPI_PLAIN_ADD><<<dim3(m->mbank[l][1].ntiles, RT), 256, 0, m->st>>>(a);
+            LightArgs g = light_args(768, m->R, rx + 2 * 3072, re + 4);
+            k_light<768, PRO_GAUGE, 192, 1><<<B, 192, 0, m->st>>>(g);
         }
-        finish_light(m->mbank[l][1], 1, m->R, rp + 3072, m->r_resid + (l * 2 + 0) * 768, rx + 2 * 3072, re + 4);
-        {
-            GemmArgs a = gemm_args(m->mbank[l][2], nullptr, 0, nullptr, nullptr);
-            k_gemm<768, 1, 1, EPI_PART><<<dim3(m->mbank[l][2].ntiles, RT), 256, 0, m->st>>>(a);
+        {   // fc: gauged, the edge, written (the hidden rows); then their 3072-wide light
+            GemmArgs a = gemm_args(m->mbank[l][2], m->hid, 3072, rp + 2 * 3072, m->r_hid + l * 3072);
+            k_gemm<768, 1, 1, EPI_GAUGED_EDGE><<<dim3(m->mbank[l][2].ntiles, RT), 256, 0, m->st>>>(a);
+            LightArgs h = light_args(3072, m->hid, rx + 3 * 3072, re + 6);
+            k_light<3072, PRO_TO16, 768, 1><<<B, 768, 0, m->st>>>(h);
         }
-        finish_light(m->mbank[l][2], 1, nullptr, rp + 2 * 3072, m->r_hid + l * 3072, rx + 3 * 3072, re + 6);
         {
             GemmArgs a = gemm_args(m->mbank[l][3], nullptr, 0, nullptr, nullptr);
             k_gemm<3072, 1, 4, EPI_PART><<<dim3(m->mbank[l][3].ntiles * 4, RT), 256, 0, m->st>>>(a);
         }
         const bool last = l == 11;     // the last stream update lights the head
-        finish_light(m->mbank[l][3], 4, m->R, rp + 3 * 3072, m->r_resid + (l * 2 + 1) * 768,
+        finish_light(m->mbank[l][3], rp + 3 * 3072, m->r_resid + (l * 2 + 1) * 768,
                      last ? m->r_hx16 : m->r_x16 + (size_t)(l + 1) * 4 * 3072, last ? m->r_hexls : m->r_exls + (size_t)(l + 1) * 4 * 2);
     }
     if ((parts & STEP_HEAD) && !rowmap) {
