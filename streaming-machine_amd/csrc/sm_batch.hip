@@ -47,6 +47,7 @@ struct GemmArgs {
     const int* pos; const int* plen;
     i64* part_v; int* part_i; int nblk;   // EPI_HEAD: per (row, block) best
     const int* rec_pos; i64* rpile; i64* rout; i64* rlogits;
+    i64* rout2;                   // EPI_PLAIN_EDGE: the record after the edge (rout: before it)
     int* part;                    // EPI_PART: [ksplit][3][rows][N] int32
 };
 
@@ -317,10 +318,14 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs a) {
             const i64 y = wadd(*yp, wadd(rsh(pile, -(we + ex + 16)), bc));
             *yp = y;
             if (rec && a.rout) a.rout[j] = y;
-        } else if (EPI == EPI_PLAIN) {                 // the Pythia machine's qkv (foundation0/pythia_base2.py:114)
-            const i64 y = wadd(rsh(pile, -(we + ex + 16)), bc);
-            a.Y[(size_t)row * a.ystride + j] = y;
+        } else if (EPI == EPI_PLAIN || EPI == EPI_PLAIN_EDGE) {   // the Pythia machine's banks (:112-114, 156)
+            i64 y = wadd(rsh(pile, -(we + ex + 16)), bc);
             if (rec && a.rout) a.rout[j] = y;
+            if (EPI == EPI_PLAIN_EDGE) {
+                y = edge1(y, a.tb);
+                if (rec && a.rout2) a.rout2[j] = y;
+            }
+            a.Y[(size_t)row * a.ystride + j] = y;
         } else {
             const i64 ls = (i64)(((u64)(unsigned)ri[2] << 32) | (unsigned)ri[1]);
             i64 y = wadd(power_known(pile, wsub(wmul(we + ex + 16, 65536), ls), (i64)ri[3]), bc);
@@ -522,20 +527,17 @@ struct PyRowArgs {
     const short* ew; const int* ee; const int* seq; int seq_stride; const int* pos;   // the word enters
     const int* ng1; const i64* nb1; int nge1;     // gauge 1 (ln1, or lnf at the top)
     const int* ng2; const i64* nb2; int nge2;     // gauge 2 (ln2); null: one gauge only
-    signed char* planes1; int* rowinfo1;          // light of gauge 1 (PY_EDGE: of the edge row)
+    signed char* planes1; int* rowinfo1;          // light of gauge 1
     signed char* planes2; int* rowinfo2;          // light of gauge 2
-    // finished plain banks: A = proj (or fc for PY_EDGE), B = mproj
-    // (A has one K slice, B four: the banks' launch shapes)
-    const int* partA; int kinA; const int* rowinfoA; const int* csumA; const int* weA; const i64* biasA;
-    const int* partB; int kinB; const int* rowinfoB; const int* csumB; const int* weB; const i64* biasB;
+    // PY_ADD: mproj's four K slices of partial accumulators, finished here (proj's half is already in R)
+    const int* partM; int kinM; const int* rowinfoM; const int* csumM; const int* weM; const i64* biasM;
     Tables tb;
     const int* rec_pos;
     i64* rg1; i64* rx1; i64* rex1; i64* rg2; i64* rx2; i64* rex2;   // the gauges and their lights
-    i64* rpileA; i64* routA; i64* rpileB; i64* routB;               // PY_ADD: stream after A, after A and B
-    i64* rpre;                                                       // PY_EDGE: fc's row before the edge
+    i64* rpileM; i64* routM;                                         // PY_ADD: mproj's pile, the stream after it
     const int* rowmap;                            // prompt rows (PY_EMBED): stream << 16 | position per row
 };
-enum { PY_EMBED = 0, PY_ADD = 1, PY_EDGE = 2 };
+enum { PY_EMBED = 0, PY_ADD = 1 };
 
 // plain(pile) of one bank for columns k .. k + 3 of row r, from its KS K-sliced partial accumulators
 // (:112-114), in two halves so that a caller can have every load of its row in flight before the arithmetic
@@ -577,38 +579,17 @@ SMD void plain4_finish(const Plain4<KS>& P, int kin, const int* ri, i64 (&pile)[
 
 // One block per stream row.
 //   PY_EMBED: R = rshift(embed.w[word], -(embed.e[word] + 16)) (:153), then the two gauges' lights
-//   PY_ADD:   R += plain(proj) + plain(mproj) (:155-157), then the two gauges' lights (or lnf's alone)
-//   PY_EDGE:  edge(plain(fc)) (:156), then its light (K = 3072)
+//   PY_ADD:   R += plain(mproj) (:155-157; proj's half was added by its bank), then the two gauges' lights (or
+//             lnf's alone)
 // Both gauges share to16(R), S1, S2 and LS (:100-110); only the gain, its power and the offset differ.
 template <int MODE>
-__global__ __launch_bounds__(MODE == PY_EDGE ? 768 : 192) void k_py_rows(PyRowArgs a) {
-    constexpr int NT = MODE == PY_EDGE ? 768 : 192, NW = NT / 64;
+__global__ __launch_bounds__(192) void k_py_rows(PyRowArgs a) {
+    constexpr int NT = 192, NW = NT / 64;
     __shared__ int red[24 + 6 * 12];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, r = blockIdx.x;
     const int pm = a.rowmap ? a.rowmap[r] : 0;
     const int p = a.rowmap ? pm & 0xFFFF : *a.pos, st = a.rowmap ? pm >> 16 : r;
     const bool rec = r == 0 && a.rec_pos && *a.rec_pos == p;
-    if constexpr (MODE == PY_EDGE) {
-        i64 v[1][4];
-        const int* ri = a.rowinfoA + (size_t)r * 8;          // fc's light facts (this block's row only)
-#pragma unroll
-        for (int m = 0; m < 1; m++) {
-            const int k = 4 * tid;
-            i64 pile[4], y[4];
-            Plain4<1> PA;
-            plain4_load<1>(PA, a.partA, a.rows, 3072, a.csumA, a.weA, a.biasA, r, k);
-            plain4_finish<1>(PA, a.kinA, ri, pile, y);
-#pragma unroll
-            for (int j = 0; j < 4; j++) {
-                if (rec && a.rpileA) a.rpileA[k + j] = pile[j];
-                if (rec && a.rpre) a.rpre[k + j] = y[j];
-                v[m][j] = edge1(y[j], a.tb);
-                if (rec && a.routA) a.routA[k + j] = v[m][j];
-            }
-        }
-        light_store<3072, NT>(v, r, a.planes1, a.rowinfo1, red, rec, a.rx1, a.rex1);
-        return;
-    }
     // the stream row (192 threads hold four lanes each)
     const int k = 4 * tid;
     i64 R4[4] = {0, 0, 0, 0};
@@ -619,27 +600,20 @@ __global__ __launch_bounds__(MODE == PY_EDGE ? 768 : 192) void k_py_rows(PyRowAr
 #pragma unroll
             for (int j = 0; j < 4; j++) R4[j] = rsh((i64)a.ew[tok * 768 + k + j], es);
         } else {
-            i64 pA[4], yA[4], pB[4], yB[4];
-            // proj's partials (one K slice), mproj's (four) and the stream row, all requested before any use
-            Plain4<1> PA;
-            Plain4<4> PB;
-            plain4_load<1>(PA, a.partA, a.rows, 768, a.csumA, a.weA, a.biasA, r, k);
-            plain4_load<4>(PB, a.partB, a.rows, 768, a.csumB, a.weB, a.biasB, r, k);
+            i64 pM[4], yM[4];
+            // mproj's partials (four K slices) and the stream row, all requested before any use
+            Plain4<4> PM;
+            plain4_load<4>(PM, a.partM, a.rows, 768, a.csumM, a.weM, a.biasM, r, k);
             const v2q_p r01 = *reinterpret_cast<const v2q_p*>(a.R + (size_t)r * 768 + k);
             const v2q_p r23 = *reinterpret_cast<const v2q_p*>(a.R + (size_t)r * 768 + k + 2);
             const i64 rr[4] = {r01[0], r01[1], r23[0], r23[1]};
-            plain4_finish<1>(PA, a.kinA, a.rowinfoA + (size_t)r * 8, pA, yA);
-            plain4_finish<4>(PB, a.kinB, a.rowinfoB + (size_t)r * 8, pB, yB);
+            plain4_finish<4>(PM, a.kinM, a.rowinfoM + (size_t)r * 8, pM, yM);
 #pragma unroll
             for (int j = 0; j < 4; j++) {
-                const i64 r0 = rr[j];
-                const i64 r1 = wadd(r0, yA[j]);
-                R4[j] = wadd(r1, yB[j]);
+                R4[j] = wadd(rr[j], yM[j]);
                 if (rec) {
-                    if (a.rpileA) a.rpileA[k + j] = pA[j];
-                    if (a.rpileB) a.rpileB[k + j] = pB[j];
-                    if (a.routA) a.routA[k + j] = r1;
-                    if (a.routB) a.routB[k + j] = R4[j];
+                    if (a.rpileM) a.rpileM[k + j] = pM[j];
+                    if (a.routM) a.routM[k + j] = R4[j];
                 }
             }
         }
@@ -755,10 +729,9 @@ BINST_L(3072, PRO_X16, 1)
 BINST_L(768, PRO_ADD_GAUGE, 4)
 template __global__ void k_py_rows<PY_EMBED>(PyRowArgs);
 template __global__ void k_py_rows<PY_ADD>(PyRowArgs);
-template __global__ void k_py_rows<PY_EDGE>(PyRowArgs);
 #define BINST_G(K, RT, KSPLIT, EPI) template __global__ void k_gemm<K, RT, KSPLIT, EPI>(GemmArgs);
 #define BINST_GR(RT) BINST_G(768, RT, 1, EPI_GAUGED) BINST_G(768, RT, 1, EPI_GAUGED_EDGE) BINST_G(768, RT, 1, EPI_PLAIN_ADD) \
-    BINST_G(768, RT, 1, EPI_PART) BINST_G(3072, RT, 4, EPI_PART) \
+    BINST_G(768, RT, 1, EPI_PART) BINST_G(768, RT, 1, EPI_PLAIN_EDGE) BINST_G(3072, RT, 4, EPI_PART) \
     BINST_G(768, RT, 1, EPI_PILE) BINST_G(3072, RT, 1, EPI_PILE) BINST_G(768, RT, 1, EPI_PLAIN)
 BINST_GR(1)
 #define BINST_H(RT) template __global__ void k_head_rows<RT, EPI_HEAD>(GemmArgs); \

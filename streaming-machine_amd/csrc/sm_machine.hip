@@ -598,8 +598,7 @@ static int launch_step_pythia_batched(sm_machine* m, int parts, hipEvent_t hs, h
     signed char* pD = m->planes + 3 * PL;
     int* rA = m->rowinfo; int* rB = m->rowinfo + RC * 8; int* rC = m->rowinfo + 2 * RC * 8;
     int* rD = m->rowinfo + 3 * RC * 8;
-    int* P0 = m->part_acc;
-    int* P3 = m->part_acc + 4 * 3 * RC * 768;
+    int* P0 = m->part_acc;                          // mproj's partial accumulators
     auto gemm_args = [&](const MfmaPlate& P, signed char* planes, int* rowinfo) {
         GemmArgs a{};
         a.K = P.K; a.N = P.N; a.rows = B; a.RT = RT; a.W = P.W; a.csum = P.csum; a.we = P.e; a.bias = P.b;
@@ -646,17 +645,16 @@ static int launch_step_pythia_batched(sm_machine* m, int parts, hipEvent_t hs, h
             k_kv_rows<1><<<dim3(12, B), 128, 0, m->st>>>(a);
             break;
         }
-        {   // fc: partials, then edge and the 3072-wide light
+        {   // fc: plain and edged in its bank (the hidden rows), then their 3072-wide light
             GemmArgs a = gemm_args(m->mbank[l][2], pB, rB);
-            a.part = P0;
-            k_gemm<768, 1, 1, EPI_PART><<<dim3(m->mbank[l][2].ntiles, RT), 256, 0, m->st>>>(a);
-            PyRowArgs e = rows_args();
-            const MfmaPlate& F = m->mbank[l][2];
-            e.partA = P0; e.kinA = 768; e.rowinfoA = rB; e.csumA = F.csum; e.weA = F.e; e.biasA = F.b;
-            e.planes1 = pC; e.rowinfo1 = rC;
-            e.rpileA = rp + 2 * 3072; e.rpre = m->r_fcpre + l * 3072; e.routA = m->r_hid + l * 3072;
-            e.rx1 = m->r_x16 + (l * 4 + 3) * 3072; e.rex1 = m->r_exls + (l * 4 + 3) * 2;
-            k_py_rows<PY_EDGE><<<B, 768, 0, m->st>>>(e);
+            a.Y = m->hid; a.ystride = 3072;
+            a.rpile = rp + 2 * 3072; a.rout = m->r_fcpre + l * 3072; a.rout2 = m->r_hid + l * 3072;
+            k_gemm<768, 1, 1, EPI_PLAIN_EDGE><<<dim3(m->mbank[l][2].ntiles, RT), 256, 0, m->st>>>(a);
+            LightArgs h{};
+            h.K = 3072; h.rows = B; h.X = m->hid; h.pos = ctl + CTL_POS; h.plen = ctl + CTL_PLEN;
+            h.planes = pC; h.rowinfo = rC; h.tb = tb; h.rec_pos = recp;
+            h.rx16 = m->r_x16 + (l * 4 + 3) * 3072; h.rexls = m->r_exls + (l * 4 + 3) * 2;
+            k_light<3072, PRO_TO16, 768, 1><<<B, 768, 0, m->st>>>(h);
         }
         {   // mproj: partials over four K slices
             GemmArgs a = gemm_args(m->mbank[l][3], pC, rC);
@@ -673,24 +671,21 @@ static int launch_step_pythia_batched(sm_machine* m, int parts, hipEvent_t hs, h
             if (rowmap) k_kv_rows<1><<<dim3(12, B), 128, 0, m->st>>>(a);
             k_attend<1, 0><<<dim3(12, B), NTHR, (size_t)m->ctx * 12, m->st>>>(a);
         }
-        {   // the attention row's light, then proj's partials
+        {   // the attention row's light, then proj added into the stream by its bank (R + At)
             LightArgs a{};
             a.K = 768; a.rows = B; a.X = m->att; a.pos = ctl + CTL_POS; a.plen = ctl + CTL_PLEN;
             a.planes = pD; a.rowinfo = rD; a.tb = tb; a.rec_pos = recp;
             a.rx16 = m->r_x16 + (l * 4 + 1) * 3072; a.rexls = m->r_exls + (l * 4 + 1) * 2;
             k_light<768, PRO_TO16, 192, 1><<<B, 192, 0, m->st>>>(a);
             GemmArgs g = gemm_args(m->mbank[l][1], pD, rD);
-            g.part = P3;
-            k_gemm<768, 1, 1, EPI_PART><<<dim3(m->mbank[l][1].ntiles, RT), 256, 0, m->st>>>(g);
+            g.Y = m->R; g.ystride = 768; g.rpile = rp + 3072; g.rout = m->r_resid + (l * 2 + 0) * 768;
+            k_gemm<768, 1, 1, EPI_PLAIN_ADD><<<dim3(m->mbank[l][1].ntiles, RT), 256, 0, m->st>>>(g);
         }
-        {   // R += At + Mo, then the next gauges' lights
+        {   // R += Mo (the parallel residual's other half), then the next gauges' lights
             PyRowArgs a = rows_args();
-            const MfmaPlate& Pp = m->mbank[l][1];
             const MfmaPlate& Pm = m->mbank[l][3];
-            a.partA = P3; a.kinA = 768; a.rowinfoA = rD; a.csumA = Pp.csum; a.weA = Pp.e; a.biasA = Pp.b;
-            a.partB = P0; a.kinB = 3072; a.rowinfoB = rC; a.csumB = Pm.csum; a.weB = Pm.e; a.biasB = Pm.b;
-            a.rpileA = rp + 3072; a.routA = m->r_resid + (l * 2 + 0) * 768;
-            a.rpileB = rp + 3 * 3072; a.routB = m->r_resid + (l * 2 + 1) * 768;
+            a.partM = P0; a.kinM = 3072; a.rowinfoM = rC; a.csumM = Pm.csum; a.weM = Pm.e; a.biasM = Pm.b;
+            a.rpileM = rp + 3 * 3072; a.routM = m->r_resid + (l * 2 + 1) * 768;
             gauges(a, l + 1);
             k_py_rows<PY_ADD><<<B, 192, 0, m->st>>>(a);
         }
