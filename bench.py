@@ -357,7 +357,7 @@ def main():
                    "batch": 1, "prompt": PROMPT, "words": WORDS, "vocab": vocab},
         "roofline": {"bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": traffic,
-                     "kernel": "k_gemv<768,8,4,PRO_GAUGE,EPI_HEAD> (head plate read; the race is its own launch)",
+                     "kernel": "k_gemv<768,4,4,PRO_GAUGE,EPI_HEAD> (head plate read; the race is its own launch)",
                      "bytes_per_launch": hb, "mean_launch_us": round(head_us, 3), "launches_timed": head_n},
         "step_roofline": {"bytes_per_step": int(sb), "achieved": round(step_ach, 1), "frac": round(step_ach / HBM_PEAK_GBS, 4)},
         "prompt_included": {"value": round(WORDS / (prompt_s / nseq + ms_per_step * 1e-3 * (WORDS - 1)), 2), "unit": "tokens/s",
