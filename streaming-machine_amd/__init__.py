@@ -12,6 +12,7 @@ from .convert import convert, tables, cols16, stream, array_digest  # noqa: F401
 from .model import random_gpt2, prompt_ids, GPT2_SHAPE  # noqa: F401
 from .layout import layout, load_layout, bank_names  # noqa: F401
 from . import pythia  # noqa: F401
+from . import refs  # noqa: F401
 
 
 def __getattr__(name):

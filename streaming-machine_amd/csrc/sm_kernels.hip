@@ -221,7 +221,7 @@ template <int NIN, int TC, int U>
 SMD void load_wtile(v4i (&w)[U], const int4* __restrict__ W, int tile, int lane) {
     const v4i* base = reinterpret_cast<const v4i*>(W) + (size_t)tile * (TC * NIN / 8) + lane;
 #pragma unroll
-    for (int m = 0; m < U; m++) w[m] = __builtin_nontemporal_load(base + 64 * m);
+    for (int m = 0; m < U; m++) w[m] = base[64 * m];      // plain loads: measured 1 % faster a step than nontemporal
 }
 
 // the lane's part of its column's pile: unit u holds inputs 8 (u / TC) .. + 8 of column u % TC = lane % TC
