@@ -10,7 +10,7 @@ Host API, after the reference's "convert -> layout -> stream" (base2_convert.py,
 """
 from .convert import convert, tables, cols16, stream, array_digest  # noqa: F401
 from .model import random_gpt2, prompt_ids, GPT2_SHAPE  # noqa: F401
-from .layout import layout, load_layout, bank_names  # noqa: F401
+from .layout import layout, load_layout, bank_names, rewire  # noqa: F401
 from . import pythia  # noqa: F401
 from . import refs  # noqa: F401
 

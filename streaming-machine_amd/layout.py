@@ -59,3 +59,43 @@ def load_layout(dirname: str) -> dict:
     out["log2_768"] = np.array(man["log2_768"])
     out["eps40"] = np.array(man["eps40"])
     return out
+
+
+def rewire(npz: dict, seed: int, n_layer: int = 12):
+    """The random wiring of base2_stream.swift:161-190 (its seed= test): the stream's 768 channels (one order for
+    every layer), each layer's heads, the dimensions inside each head (one order shared by q and k, another for
+    v), each layer's 3072 neurons and the words at the top, all shuffled; every bank's rows and columns, its
+    powers and biases, and the word and position tables follow.  Every sum is of whole numbers, so every pile is
+    the same number in its new place and the machine's words are the same (ties between equal top logits aside,
+    which go to the lowest slot).  The permutations come from numpy's default_rng(seed) (the reference's own
+    generator is not needed: any shuffle must give the same words).
+
+    Returns (the rewired npz, the permutations): slot j of the word table holds word perms["words"][j], so a
+    prompt goes in as slots (perms["slot_of"][word]) and the machine's slots come back as perms["words"][slot].
+    """
+    rng = np.random.default_rng(seed)
+    d, vocab = 768, len(npz["wte"])
+    chan = rng.permutation(d)
+    out = dict(npz)
+    perms = {"chan": chan, "layers": []}
+    for l in range(n_layer):
+        hp, dqk, dv, neu = rng.permutation(12), rng.permutation(64), rng.permutation(64), rng.permutation(3072)
+        qkv_cols = np.array([part * 768 + hp[h] * 64 + (dqk[k] if part < 2 else dv[k])
+                             for part in range(3) for h in range(12) for k in range(64)])
+        proj_rows = np.array([hp[h] * 64 + dv[k] for h in range(12) for k in range(64)])
+        for name, rp, cp in ((f"qkv.{l}", chan, qkv_cols), (f"proj.{l}", proj_rows, chan),
+                             (f"fc.{l}", chan, neu), (f"mproj.{l}", neu, chan)):
+            out[name + ".w"] = np.ascontiguousarray(np.asarray(npz[name + ".w"])[np.ix_(rp, cp)])
+            out[name + ".e"] = np.asarray(npz[name + ".e"])[cp]
+            out[name + ".b"] = np.asarray(npz[name + ".b"])[cp]
+        perms["layers"].append({"qkv_cols": qkv_cols, "proj_rows": proj_rows, "neurons": neu})
+    words = rng.permutation(vocab)
+    out["head.w"] = np.ascontiguousarray(np.asarray(npz["head.w"])[np.ix_(chan, words)])
+    out["head.e"] = np.asarray(npz["head.e"])[words]
+    out["head.b"] = np.asarray(npz["head.b"])[words]
+    out["wte"] = np.ascontiguousarray(np.asarray(npz["wte"])[np.ix_(words, chan)])
+    out["wpe"] = np.ascontiguousarray(np.asarray(npz["wpe"])[:, chan])
+    slot_of = np.empty(vocab, dtype=np.int64)
+    slot_of[words] = np.arange(vocab)
+    perms["words"], perms["slot_of"] = words, slot_of
+    return out, perms
