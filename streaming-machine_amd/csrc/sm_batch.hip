@@ -49,7 +49,18 @@ struct GemmArgs {
     const int* rec_pos; i64* rpile; i64* rout; i64* rlogits;
     i64* rout2;                   // EPI_PLAIN_EDGE: the record after the edge (rout: before it)
     int* part;                    // EPI_PART: [ksplit][3][rows][N] int32
+    // the light formed in the bank (SRC > 0): the producing phase's rows, its OR words, stream 0's light record
+    const i64* X; int xstride;    // [rows][xstride] int64
+    const i64* orw;               // [rows][SRC]: OR of |x| over each part of a row the producer wrote
+    i64* rx16; i64* rexls;
 };
+
+// Where a bank's A operand comes from:
+//   SRC = 0: the light planes and row facts a light kernel wrote (planes, rowinfo);
+//   SRC = n > 0: the producing phase's int64 rows.  The producer left, per row, n OR words of the magnitudes it
+//   wrote (one per attention head, say); their OR is the row's water level (base2.py:24-27), so every block
+//   forms the 16-bit light of its own row tile and K steps in registers, with the plane sums its epilogue needs,
+//   and no light kernel runs between the two phases.
 
 // ---------------------------------------------------------------------------------------------------------
 // One block (256 threads) per stream row: the light of base2.py:24-27 (and the gauge of :55-60), written as
@@ -202,14 +213,25 @@ __global__ __launch_bounds__(NT) void k_light(LightArgs a) {
 // facts) is issued before the first MFMA.
 //   EPI_PART: the accumulators go to part[kslice][3][rows][N]; the consumer's prologue finishes them.
 //   EPI_GAUGED / EPI_GAUGED_EDGE / EPI_PLAIN_ADD / EPI_PILE: one K slice; the epilogue runs here.
-template <int K, int RT, int KSPLIT, int EPI>
+// SRC > 0 (one row tile, one K slice, a plain epilogue): each wave lights four rows of the tile from contiguous
+// loads into LDS as 16-bit pairs; after one barrier every wave reads its A operands from there and forms the
+// byte planes and plane sums in registers.
+template <int K, int RT, int KSPLIT, int EPI, int SRC = 0>
 __global__ __launch_bounds__(256) void k_gemm(GemmArgs a) {
     constexpr int KS = K / 64, NS = KS / (4 * KSPLIT);
+    constexpr bool ROWS = SRC > 0;
     static_assert(NS * 4 * KSPLIT == KS, "k steps split evenly over slices and waves");
     static_assert(KSPLIT == 1 || EPI == EPI_PART, "a split K is finished by the consumer");
     typedef int v4 __attribute__((ext_vector_type(4)));
     __shared__ int rinfo[64 * 8];
     __shared__ int red[4 * RT * 12 * 64];
+    // SRC > 0: the tile's 16-bit lights as pairs [tile row][K range / 2] (rows padded by 4 dwords, so that a
+    // wave's operand reads spread over the banks), each row's shift, a wave's "holds +32768" flag, and the plane
+    // sums [wave][tile row] (SXh, SXl, n32768)
+    constexpr int KR = K / KSPLIT, XSTR = KR / 2 + 4;
+    __shared__ int xs[ROWS ? 16 * XSTR : 1];
+    __shared__ int shs[16], cfw[4];
+    __shared__ int sfx[ROWS ? 4 * 16 * 4 : 1];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int ntiles = (a.N + 15) >> 4;
     const int nt = blockIdx.x % ntiles, kb = blockIdx.x / ntiles;
@@ -220,24 +242,132 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs a) {
     // gauged epilogues: row tid's light facts first (loads complete in order: its gauge need not wait for the
     // tiles)
     constexpr bool GAUGED = EPI == EPI_GAUGED || EPI == EPI_GAUGED_EDGE;
+    static_assert(!ROWS || (RT == 1 && KSPLIT == 1 && !GAUGED), "a light formed here: one row tile and K slice, plain");
     v4 gf = {0, 0, 0, 0};
     if (GAUGED) gf = *reinterpret_cast<const v4*>(a.rowinfo + (size_t)(tid < a.rows ? tid : 0) * 8);
     v4 wh[NS], wl[NS], xh[NS][RT], xl[NS][RT];
+    // SRC > 0: wave w lights tile rows 4 w .. 4 w + 3.  Their OR words (word n = lane + 64 m of the wave's
+    // 4 SRC), then their values as contiguous 1 KB wave loads (value pair 64 c + lane of row j), all ahead of the
+    // weights (their wait then leaves the weights in flight); rows past the last read zeros
+    constexpr int NWD = ROWS ? (4 * SRC + 63) / 64 : 1, NCH = ROWS ? KR / 128 : 1;
+    const int tr = lane & 15, q4 = lane >> 4;
+    i64 ow[NWD];
+    v4 xr[ROWS ? 4 : 1][NCH];
+    if constexpr (ROWS) {
+        const __amdgpu_buffer_rsrc_t ro = buf_rsrc(a.orw, (unsigned)(a.rows * SRC) * 8u);
+        const __amdgpu_buffer_rsrc_t rx = buf_rsrc(a.X, (unsigned)(a.rows * a.xstride) * 8u);
+        const int row0 = 16 * t0 + 4 * wave;
+#pragma unroll
+        for (int m = 0; m < NWD; m++) {
+            const int n = lane + 64 * m;
+            const unsigned off = n < 4 * SRC ? (unsigned)((row0 + n / SRC) * SRC + n % SRC) * 8u : 0x80000000u;
+            ow[m] = (i64)__builtin_bit_cast(u64, __builtin_amdgcn_raw_buffer_load_b64(ro, (int)off, 0, 0));
+        }
+#pragma unroll
+        for (int jr = 0; jr < 4; jr++)
+#pragma unroll
+            for (int c = 0; c < NCH; c++)
+                xr[jr][c] = buf_load4(rx, (unsigned)((row0 + jr) * a.xstride + kb * KR + 2 * (64 * c + lane)) * 8u);
+    }
 #pragma unroll
     for (int i = 0; i < NS; i++) {
         wh[i] = __builtin_nontemporal_load(Wb + (size_t)(s0 + i) * 128);
         wl[i] = __builtin_nontemporal_load(Wb + (size_t)(s0 + i) * 128 + 64);
     }
+    if constexpr (!ROWS) {
 #pragma unroll
-    for (int i = 0; i < NS; i++)
+        for (int i = 0; i < NS; i++)
 #pragma unroll
-        for (int t = 0; t < RT; t++) {
-            xh[i][t] = Ab[((size_t)(t0 + t) * KS + s0 + i) * 192];
-            xl[i][t] = Ab[((size_t)(t0 + t) * KS + s0 + i) * 192 + 64];
+            for (int t = 0; t < RT; t++) {
+                xh[i][t] = Ab[((size_t)(t0 + t) * KS + s0 + i) * 192];
+                xl[i][t] = Ab[((size_t)(t0 + t) * KS + s0 + i) * 192 + 64];
+            }
+    }
+    const int n32 = !ROWS && lane < a.rows ? a.rowinfo[lane * 8 + 6] : 0;
+    const int rsv = !ROWS && tid < a.rows * 8 ? a.rowinfo[tid] : 0;
+    const int rsv2 = !ROWS && tid + 256 < a.rows * 8 ? a.rowinfo[tid + 256] : 0;
+    // SRC > 0: the light (base2.py:24-27) of the wave's rows into LDS, then each wave's A operands and plane
+    // sums from there
+    v4 xc[ROWS ? NS : 1];
+    int l_n32 = 0;
+    if constexpr (ROWS) {
+        const int p = a.pos ? *a.pos : 0;
+        const bool rec = a.rx16 && t0 == 0 && nt == 0 && kb == 0 && a.rec_pos && *a.rec_pos == p;
+        int mx = 0;
+#pragma unroll
+        for (int jr = 0; jr < 4; jr++) {
+            i64 o = 0;                                   // the row's water level from its OR words
+#pragma unroll
+            for (int m = 0; m < NWD; m++)
+                if ((lane + 64 * m) / SRC == jr) o |= ow[m];
+            const int sh = water_shift(wave_or64(o));    // uniform
+            const i64 half = sh ? (i64)1 << (sh - 1) : 0;   // rshift(v, sh), sh in [0, 49]: (v + half) >> sh
+            if (lane == 0) shs[4 * wave + jr] = sh;
+#pragma unroll
+            for (int c = 0; c < NCH; c++) {
+                const v4 w = xr[jr][c];
+                const int x0 = (int)(wadd((i64)(((u64)(unsigned)w[1] << 32) | (unsigned)w[0]), half) >> sh);
+                const int x1 = (int)(wadd((i64)(((u64)(unsigned)w[3] << 32) | (unsigned)w[2]), half) >> sh);
+                mx = max(mx, max(x0, x1));
+                if (rec && wave == 0 && jr == 0) {       // stream 0's record
+                    a.rx16[2 * (64 * c + lane)] = x0;
+                    a.rx16[2 * (64 * c + lane) + 1] = x1;
+                }
+                // +32768 held as 32767 (the correction plane carries the rest)
+                xs[(4 * wave + jr) * XSTR + 64 * c + lane] =
+                    (int)__builtin_amdgcn_perm((unsigned)min(x1, 32767), (unsigned)min(x0, 32767), 0x05040100u);
+            }
+            if (rec && wave == 0 && jr == 0 && lane == 0) { a.rexls[0] = sh - 16; a.rexls[1] = 0; }
         }
-    const int n32 = lane < a.rows ? a.rowinfo[lane * 8 + 6] : 0;
-    const int rsv = tid < a.rows * 8 ? a.rowinfo[tid] : 0;
-    const int rsv2 = tid + 256 < a.rows * 8 ? a.rowinfo[tid + 256] : 0;
+        const bool c_here = __ballot(mx == 32768) != 0;
+        if (lane == 0) cfw[wave] = c_here;
+        __syncthreads();
+        // lane (tr, q4) of step i holds row tr, k = 64 (wave NS + i) + 16 q4 + b: 16-bit pairs d[n] = (b = 2n, 2n+1);
+        // xh is each light's high byte, xl' = xl - 128 its low byte ^ 0x80; the plane sums by dot products with ones
+        int sxh = 0, sxl = 0;
+#pragma unroll
+        for (int i = 0; i < NS; i++) {
+            const v4* src = reinterpret_cast<const v4*>(xs + tr * XSTR + 32 * (wave * NS + i) + 8 * q4);
+            const v4 d0 = src[0], d1 = src[1];
+            const unsigned d[8] = {(unsigned)d0[0], (unsigned)d0[1], (unsigned)d0[2], (unsigned)d0[3],
+                                   (unsigned)d1[0], (unsigned)d1[1], (unsigned)d1[2], (unsigned)d1[3]};
+            unsigned qh[4], ql[4];
+#pragma unroll
+            for (int g = 0; g < 4; g++) {
+                qh[g] = __builtin_amdgcn_perm(d[2 * g + 1], d[2 * g], 0x07050301u);
+                ql[g] = __builtin_amdgcn_perm(d[2 * g + 1], d[2 * g], 0x06040200u) ^ 0x80808080u;
+                sxh = __builtin_amdgcn_sdot4((int)qh[g], 0x01010101, sxh, false);
+                sxl = __builtin_amdgcn_sdot4((int)ql[g], 0x01010101, sxl, false);
+            }
+            xh[i][0] = v4{(int)qh[0], (int)qh[1], (int)qh[2], (int)qh[3]};
+            xl[i][0] = v4{(int)ql[0], (int)ql[1], (int)ql[2], (int)ql[3]};
+            xc[i] = v4{0, 0, 0, 0};
+        }
+        if (cfw[0] | cfw[1] | cfw[2] | cfw[3]) {       // a light of +32768 in the tile (rare): the correction
+            const int sh = shs[tr];                      // plane, from the rows read again
+            const i64 half = sh ? (i64)1 << (sh - 1) : 0;
+            const i64* xrow = a.X + (size_t)(16 * t0 + tr) * a.xstride + kb * KR;
+            const bool live = 16 * t0 + tr < a.rows;
+#pragma unroll
+            for (int i = 0; i < NS; i++) {
+                unsigned cw[4] = {0, 0, 0, 0};
+#pragma unroll
+                for (int b = 0; b < 16; b++) {
+                    const int c = live && (int)(wadd(xrow[64 * (wave * NS + i) + 16 * q4 + b], half) >> sh) == 32768;
+                    l_n32 += c;
+                    cw[b >> 2] |= (unsigned)c << (8 * (b & 3));
+                }
+                xc[i] = v4{(int)cw[0], (int)cw[1], (int)cw[2], (int)cw[3]};
+            }
+        }
+        int f0 = sxh, f1 = sxl, f2 = l_n32;
+        f0 += __shfl_xor(f0, 16, 64); f1 += __shfl_xor(f1, 16, 64); f2 += __shfl_xor(f2, 16, 64);
+        f0 += __shfl_xor(f0, 32, 64); f1 += __shfl_xor(f1, 32, 64); f2 += __shfl_xor(f2, 32, 64);
+        if (q4 == 0) {
+            int* f = sfx + (wave * 16 + tr) * 4;
+            f[0] = f0; f[1] = f1; f[2] = f2; f[3] = shs[tr] - 16;
+        }
+    }
     // gauged: thread r < rows turns row r's light facts into LS and the power factor (table reads in
     // flight during the contraction); they replace S1, S2 in the LDS copy of the row facts
     i64 g_ls = 0, g_e2 = 0;
@@ -260,16 +390,26 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs a) {
             acc[t][2] = __builtin_amdgcn_mfma_i32_16x16x64_i8(xl[i][t], wl[i], acc[t][2], 0, 0, 0);
             acc[t][1] = __builtin_amdgcn_mfma_i32_16x16x64_i8(xl[i][t], wh[i], acc[t][1], 0, 0, 0);
         }
-#pragma unroll
-    for (int t = 0; t < RT; t++)
-        if ((cmask >> (16 * (t0 + t))) & 0xFFFFull) {
+    if constexpr (ROWS) {
+        if (__ballot(l_n32 != 0)) {                      // this wave's steps hold a +32768 light
 #pragma unroll
             for (int i = 0; i < NS; i++) {
-                const v4 cc = Ab[((size_t)(t0 + t) * KS + s0 + i) * 192 + 128];
-                acc[t][1] = __builtin_amdgcn_mfma_i32_16x16x64_i8(cc, wh[i], acc[t][1], 0, 0, 0);
-                acc[t][2] = __builtin_amdgcn_mfma_i32_16x16x64_i8(cc, wl[i], acc[t][2], 0, 0, 0);
+                acc[0][1] = __builtin_amdgcn_mfma_i32_16x16x64_i8(xc[i], wh[i], acc[0][1], 0, 0, 0);
+                acc[0][2] = __builtin_amdgcn_mfma_i32_16x16x64_i8(xc[i], wl[i], acc[0][2], 0, 0, 0);
             }
         }
+    } else {
+#pragma unroll
+        for (int t = 0; t < RT; t++)
+            if ((cmask >> (16 * (t0 + t))) & 0xFFFFull) {
+#pragma unroll
+                for (int i = 0; i < NS; i++) {
+                    const v4 cc = Ab[((size_t)(t0 + t) * KS + s0 + i) * 192 + 128];
+                    acc[t][1] = __builtin_amdgcn_mfma_i32_16x16x64_i8(cc, wh[i], acc[t][1], 0, 0, 0);
+                    acc[t][2] = __builtin_amdgcn_mfma_i32_16x16x64_i8(cc, wl[i], acc[t][2], 0, 0, 0);
+                }
+            }
+    }
 #pragma unroll
     for (int t = 0; t < RT; t++)
 #pragma unroll
@@ -306,9 +446,16 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs a) {
             continue;
         }
         const int* ri = rinfo + row * 8;
-        const i64 ex = ri[0];
-        const i64 pile = 65536 * (i64)fin[t][0] + 256 * (i64)fin[t][1] + fin[t][2] + 32768 * ((i64)ri[4] + swh) +
-                         128 * ((i64)ri[5] + swl) + 16384 * (i64)K + 128 * (i64)ri[6];
+        i64 ex = ri[0], fsxh = ri[4], fsxl = ri[5], fn32 = ri[6];
+        if constexpr (ROWS) {                            // the row's facts from the four waves' steps
+            const int* f = sfx + (row - 16 * t0) * 4;
+            ex = f[3];
+            fsxh = f[0] + f[64] + f[128] + f[192];
+            fsxl = f[1] + f[65] + f[129] + f[193];
+            fn32 = f[2] + f[66] + f[130] + f[194];
+        }
+        const i64 pile = 65536 * (i64)fin[t][0] + 256 * (i64)fin[t][1] + fin[t][2] + 32768 * (fsxh + swh) +
+                         128 * (fsxl + swl) + 16384 * (i64)K + 128 * fn32;
         const bool rec = rec0 && row == 0;
         if (rec && a.rpile) a.rpile[j] = pile;
         if (EPI == EPI_PILE) {

@@ -168,6 +168,19 @@ SMD i64 gauge_ls_pow_v(i64 s1, i64 s2, i64 ex, const Tables& tb, i64& e2) {
     return wadd(wsub(l2 >> 1, tb.log768), wmul(ex, 65536));
 }
 
+// ---------------- bounded loads ----------------
+typedef int v4i __attribute__((ext_vector_type(4)));
+// A buffer resource over [base, base + bytes) (raw, stride 0; the gfx9 word-3 format): a load past the end
+// returns zeros and sends no request to memory, so a fixed sequence of loads can cover a variable number of
+// rows with no branch around them (a branch would make the next wait count every load in flight).
+SMD __amdgpu_buffer_rsrc_t buf_rsrc(const void* base, unsigned bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, (int)bytes, 0x00020000);
+}
+SMD v4i buf_load4(__amdgpu_buffer_rsrc_t r, unsigned off) {
+    return __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 0));
+}
+SMD int buf_load1(__amdgpu_buffer_rsrc_t r, unsigned off) { return (int)__builtin_amdgcn_raw_buffer_load_b32(r, (int)off, 0, 0); }
+
 // ---------------- wave64 reductions through DPP (a few VALU cycles per step) ----------------
 // update_dpp(old = 0, ...): lanes a step does not reach contribute 0, the identity of +, | and max of naturals
 #define DPP(v, ctrl, rm, bm) __builtin_amdgcn_update_dpp(0, (v), (ctrl), (rm), (bm), false)

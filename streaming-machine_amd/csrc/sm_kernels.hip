@@ -19,18 +19,6 @@
 #include "sm_kernels.h"
 
 #define NTHR 256
-typedef int v4i __attribute__((ext_vector_type(4)));
-
-// A buffer resource over [base, base + bytes) (raw, stride 0; the gfx9 word-3 format): a load past the end
-// returns zeros and sends no request to memory, so a fixed sequence of loads can cover a variable number of
-// cache rows with no branch around them (a branch would make the next wait count every load in flight).
-SMD __amdgpu_buffer_rsrc_t buf_rsrc(const void* base, unsigned bytes) {
-    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, (int)bytes, 0x00020000);
-}
-SMD v4i buf_load4(__amdgpu_buffer_rsrc_t r, unsigned off) {
-    return __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 0));
-}
-SMD int buf_load1(__amdgpu_buffer_rsrc_t r, unsigned off) { return (int)__builtin_amdgcn_raw_buffer_load_b32(r, (int)off, 0, 0); }
 
 // ---------------------------------------------------------------------------------------------------------
 // block reductions (4 waves).  red: 8 slots, free on entry; every thread gets the result.
@@ -533,6 +521,10 @@ SMD void attend_short(const AttArgs& a, int p, int h, int b, int* q_s, int* w_s)
         o = power_e(num, F, F & 0xFFFF, hp, a.tb);
     }
     a.out[(size_t)b * 768 + h * 64 + lane] = o;
+    if (a.out_or) {
+        const i64 w = wave_or64(iabs64(o));
+        if (lane == 0) a.out_or[(size_t)b * 12 + h] = w;
+    }
     if (rec) a.ratt[h * 64 + lane] = o;
 }
 
@@ -731,6 +723,10 @@ __global__ __launch_bounds__(NTHR, ONE ? 1 : 3) void k_attend(AttArgs a) {
             o = power_e(tot, F, F & 0xFFFF, utab_hpow(a.tb, (int)m), a.tb);
         }
         a.out[(size_t)b * 768 + h * 64 + lane] = o;
+        if (a.out_or) {
+            const i64 w = wave_or64(iabs64(o));
+            if (lane == 0) a.out_or[(size_t)b * 12 + h] = w;
+        }
         if (rec) a.ratt[h * 64 + lane] = o;
     }
 }

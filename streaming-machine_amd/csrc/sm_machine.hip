@@ -234,6 +234,7 @@ struct sm_machine {
     sm_tables T;
     // state
     i64 *R = nullptr, *QKV = nullptr, *att = nullptr, *hid = nullptr;
+    i64* attor = nullptr;                               // [rows][12] OR of |att| over each head's values
     int *K16 = nullptr, *EK = nullptr, *V = nullptr;   // [L][B][12 heads][ctx][64] (EK: [L][B][12][ctx])
     int* seq = nullptr;                                 // [B][ctx + 1]
     int* words = nullptr;                               // [B][ctx + 1]
@@ -357,7 +358,7 @@ static void machine_free(sm_machine* m) {
     free_plate(m->head);
     free_mfma_plate(m->mhead);
     tables_free(m->T);
-    void* ps[] = {m->pfmap, m->planes, m->part_acc, m->rowinfo, m->wte, m->wpe, m->R, m->QKV, m->att, m->hid, m->K16, m->EK, m->V, m->seq, m->words, m->ctl,
+    void* ps[] = {m->pfmap, m->planes, m->part_acc, m->rowinfo, m->wte, m->wpe, m->R, m->QKV, m->att, m->attor, m->hid, m->K16, m->EK, m->V, m->seq, m->words, m->ctl,
                   m->part_v, m->part_i, m->r_x16, m->r_exls, m->r_pile, m->r_qkv, m->r_att, m->r_hid, m->r_resid,
                   m->r_hx16, m->r_hexls, m->r_hpile, m->r_logits, m->r_gauge, m->r_fcpre, m->r_hgauge,
                   m->fg, m->fb, m->ew, m->ee, m->cosT, m->sinT};
@@ -426,7 +427,7 @@ static int launch_step_batched(sm_machine* m, int parts, hipEvent_t hs, hipEvent
             const size_t per = (size_t)m->B * m->ctx;
             a.QKV = m->QKV; a.K16 = m->K16 + l * per * 768; a.EK = m->EK + l * per * 12; a.V = m->V + l * per * 768;
             a.out = m->att; a.pos = ctl + CTL_POS; a.ctx = m->ctx; a.tb = tb; a.err = ctl + CTL_ERR;
-            a.rec_pos = recp; a.ratt = m->r_att + l * 768; a.rowmap = rowmap;
+            a.rec_pos = recp; a.ratt = m->r_att + l * 768; a.rowmap = rowmap; a.out_or = m->attor;
             if (rowmap) {
                 k_kv_rows<0><<<dim3(12, B), 128, 0, m->st>>>(a);
                 if (l == 11) break;
@@ -437,13 +438,11 @@ static int launch_step_batched(sm_machine* m, int parts, hipEvent_t hs, hipEvent
                 k_attend<0, 0><<<dim3(12, m->B), NTHR, (size_t)m->ctx * 12, m->st>>>(a);
             }
         }
-        {
-            LightArgs a = light_args(768, m->att, rx + 3072, re + 2);
-            k_light<768, PRO_TO16, 192, 1><<<B, 192, 0, m->st>>>(a);
-        }
-        {   // proj: the plain bank added into the stream; then the stream's light for fc
+        {   // proj: the attention rows' light formed in the bank, the plain bank added into the stream; then the
+            // stream's light for fc
             GemmArgs a = gemm_args(m->mbank[l][1], m->R, 768, rp + 3072, m->r_resid + (l * 2 + 0) * 768);
-            k_gemm<768, 1, 1, EPI_PLAIN_ADD><<<dim3(m->mbank[l][1].ntiles, RT), 256, 0, m->st>>>(a);
+            a.X = m->att; a.xstride = 768; a.orw = m->attor; a.rx16 = rx + 3072; a.rexls = re + 2;
+            k_gemm<768, 1, 1, EPI_PLAIN_ADD, 12><<<dim3(m->mbank[l][1].ntiles, RT), 256, 0, m->st>>>(a);
             LightArgs g = light_args(768, m->R, rx + 2 * 3072, re + 4);
             k_light<768, PRO_GAUGE, 192, 1><<<B, 192, 0, m->st>>>(g);
         }
@@ -668,18 +667,16 @@ static int launch_step_pythia_batched(sm_machine* m, int parts, hipEvent_t hs, h
             a.out = m->att; a.pos = ctl + CTL_POS; a.ctx = m->ctx; a.tb = tb; a.err = ctl + CTL_ERR;
             a.rec_pos = recp; a.ratt = m->r_att + l * 768; a.rowmap = rowmap;
             a.cosT = m->cosT; a.sinT = m->sinT; a.rot = m->rot; a.half = m->half; a.ehalf = m->ehalf;
+            a.out_or = m->attor;
             if (rowmap) k_kv_rows<1><<<dim3(12, B), 128, 0, m->st>>>(a);
             k_attend<1, 0><<<dim3(12, B), NTHR, (size_t)m->ctx * 12, m->st>>>(a);
         }
-        {   // the attention row's light, then proj added into the stream by its bank (R + At)
-            LightArgs a{};
-            a.K = 768; a.rows = B; a.X = m->att; a.pos = ctl + CTL_POS; a.plen = ctl + CTL_PLEN;
-            a.planes = pD; a.rowinfo = rD; a.tb = tb; a.rec_pos = recp;
-            a.rx16 = m->r_x16 + (l * 4 + 1) * 3072; a.rexls = m->r_exls + (l * 4 + 1) * 2;
-            k_light<768, PRO_TO16, 192, 1><<<B, 192, 0, m->st>>>(a);
+        {   // proj: the attention rows' light formed in its bank, added into the stream (R + At)
             GemmArgs g = gemm_args(m->mbank[l][1], pD, rD);
             g.Y = m->R; g.ystride = 768; g.rpile = rp + 3072; g.rout = m->r_resid + (l * 2 + 0) * 768;
-            k_gemm<768, 1, 1, EPI_PLAIN_ADD><<<dim3(m->mbank[l][1].ntiles, RT), 256, 0, m->st>>>(g);
+            g.X = m->att; g.xstride = 768; g.orw = m->attor;
+            g.rx16 = m->r_x16 + (l * 4 + 1) * 3072; g.rexls = m->r_exls + (l * 4 + 1) * 2;
+            k_gemm<768, 1, 1, EPI_PLAIN_ADD, 12><<<dim3(m->mbank[l][1].ntiles, RT), 256, 0, m->st>>>(g);
         }
         {   // R += Mo (the parallel residual's other half), then the next gauges' lights
             PyRowArgs a = rows_args();
@@ -976,7 +973,7 @@ extern "C" int sm_create(const char* layout_dir, const sm_config* cfg, sm_machin
     // state
     const size_t B = m->B, ctx = m->ctx, RC = m->RC;
     const size_t nsets = m->kind == 1 && mfma ? 4 : 1;      // light-plane sets (the Pythia MFMA phases keep four)
-    if ((rc = dalloc(&m->R, RC * 768)) || (rc = dalloc(&m->QKV, RC * 2304)) || (rc = dalloc(&m->att, RC * 768)) ||
+    if ((rc = dalloc(&m->R, RC * 768)) || (rc = dalloc(&m->QKV, RC * 2304)) || (rc = dalloc(&m->att, RC * 768)) || (rc = dalloc(&m->attor, RC * 12)) ||
         (rc = dalloc(&m->hid, RC * 3072)) || (rc = dalloc(&m->K16, 12 * B * ctx * 768)) || (rc = dalloc(&m->EK, 12 * B * ctx * 12)) ||
         (rc = dalloc(&m->pfmap, B * ctx)) ||
         (rc = dalloc(&m->V, 12 * B * ctx * 768)) || (rc = dalloc(&m->seq, B * (ctx + 1))) || (rc = dalloc(&m->words, B * (ctx + 1))) ||
