@@ -33,6 +33,7 @@ struct LightArgs {
     const int* csum; const int* we; const i64* bias;   // the producing plate's column facts
     i64* Y;                                       // [rows][K]: the epilogue's row (R: read and written)
     i64* rpile_in; i64* rout_in;                  // stream 0's record of the producing bank
+    const int* sfacts;                            // its K slices' light facts [KSP][rows][4]: SXh, SXl, n32768, ex
     const int* rowmap;                            // prompt rows (PRO_EMBED): stream << 16 | position per row
 };
 
@@ -53,6 +54,9 @@ struct GemmArgs {
     const i64* X; int xstride;    // [rows][xstride] int64
     const i64* orw;               // [rows][SRC]: OR of |x| over each part of a row the producer wrote
     i64* rx16; i64* rexls;
+    int* sfacts;                  // EPI_PART with SRC > 0: [KSPLIT][rows][4] each K slice's SXh, SXl, n32768, ex
+    i64* orw_out;                 // EPI_GAUGED_EDGE / EPI_PLAIN_EDGE (when non-null): [rows][N / 16] OR of |y| over
+                                  // each block's 16 columns, the consumer's water level
 };
 
 // Where a bank's A operand comes from:
@@ -61,6 +65,21 @@ struct GemmArgs {
 //   wrote (one per attention head, say); their OR is the row's water level (base2.py:24-27), so every block
 //   forms the 16-bit light of its own row tile and K steps in registers, with the plane sums its epilogue needs,
 //   and no light kernel runs between the two phases.
+
+// The light facts of a row that a K-split bank formed itself, from its slices' [KS][rows][4] (SXh, SXl, n32768
+// summed; ex, the same in every slice), in the row-fact slots of a light (0: ex, 4: SXh, 5: SXl, 6: n32768)
+template <int KS>
+SMD void slice_facts(const int* sf, int rows, int r, int (&ri)[8]) {
+    typedef int v4s __attribute__((ext_vector_type(4)));
+    v4s f[KS];
+#pragma unroll
+    for (int q = 0; q < KS; q++) f[q] = *reinterpret_cast<const v4s*>(sf + ((size_t)q * rows + r) * 4);
+    v4s t = f[0];
+#pragma unroll
+    for (int q = 1; q < KS; q++) t += f[q];
+    ri[0] = f[0][3]; ri[1] = ri[2] = ri[3] = ri[7] = 0;
+    ri[4] = t[0]; ri[5] = t[1]; ri[6] = t[2];
+}
 
 // ---------------------------------------------------------------------------------------------------------
 // One block (256 threads) per stream row: the light of base2.py:24-27 (and the gauge of :55-60), written as
@@ -77,10 +96,11 @@ __global__ __launch_bounds__(NT) void k_light(LightArgs a) {
     if (a.skip_prompt && p < *a.plen - 1) return;
     i64 v[GPT][4];
     typedef int v4l __attribute__((ext_vector_type(4)));
-    // the producing bank's light facts for this row (read before this block replaces them)
+    // the producing bank's light facts for this row (its K slices formed the light themselves)
     i64 i_ex = 0, i_sxh = 0, i_sxl = 0, i_n32 = 0;
     if (PRO == PRO_ADD_GAUGE) {
-        const int* ri = a.rowinfo + (size_t)r * 8;
+        int ri[8];
+        slice_facts<KSP>(a.sfacts, a.rows, r, ri);
         i_ex = ri[0];
         i_sxh = ri[4]; i_sxl = ri[5]; i_n32 = ri[6];
     }
@@ -206,17 +226,17 @@ __global__ __launch_bounds__(NT) void k_light(LightArgs a) {
 }
 
 // ---------------------------------------------------------------------------------------------------------
-// The byte-plane contraction of a layer bank.  One block per (16-column tile, K slice); its four waves split the
-// slice's 64-k steps (NS each) and meet in LDS, where each (row tile, column tile) pair holds three int32
-// accumulators: HH, MID = HL + LH (+ CH), LL (+ CL).  Wave w then finishes rows 4 (l / 16) + w of every row tile
-// for column l % 16.  Everything the block reads that depends on nothing else (weights, lights, row and column
-// facts) is issued before the first MFMA.
+// The byte-plane contraction of a layer bank.  One block per (group of NB 16-column tiles, K slice, 16-row
+// tile); its four waves split the slice's 64-k steps (NS each) and meet in LDS, where each column tile holds
+// three int32 accumulators: HH, MID = HL + LH (+ CH), LL (+ CL).  Wave w then finishes rows 4 (l / 16) + w of the
+// row tile for column l % 16 of every tile.  Everything the block reads that depends on nothing else (weights,
+// lights, row and column facts) is issued before the first MFMA.
 //   EPI_PART: the accumulators go to part[kslice][3][rows][N]; the consumer's prologue finishes them.
 //   EPI_GAUGED / EPI_GAUGED_EDGE / EPI_PLAIN_ADD / EPI_PILE: one K slice; the epilogue runs here.
-// SRC > 0 (one row tile, one K slice, a plain epilogue): each wave lights four rows of the tile from contiguous
-// loads into LDS as 16-bit pairs; after one barrier every wave reads its A operands from there and forms the
-// byte planes and plane sums in registers.
-template <int K, int RT, int KSPLIT, int EPI, int SRC = 0>
+// SRC > 0 (a plain epilogue or K-slice partials): each wave lights four rows of the tile from contiguous loads
+// into LDS as 16-bit pairs; after one barrier every wave reads its A operands from there and forms the byte
+// planes and plane sums in registers.  NB > 1 spreads that light over more columns.
+template <int K, int NB, int KSPLIT, int EPI, int SRC = 0>
 __global__ __launch_bounds__(256) void k_gemm(GemmArgs a) {
     constexpr int KS = K / 64, NS = KS / (4 * KSPLIT);
     constexpr bool ROWS = SRC > 0;
@@ -224,7 +244,7 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs a) {
     static_assert(KSPLIT == 1 || EPI == EPI_PART, "a split K is finished by the consumer");
     typedef int v4 __attribute__((ext_vector_type(4)));
     __shared__ int rinfo[64 * 8];
-    __shared__ int red[4 * RT * 12 * 64];
+    __shared__ int red[4 * NB * 12 * 64];
     // SRC > 0: the tile's 16-bit lights as pairs [tile row][K range / 2] (rows padded by 4 dwords, so that a
     // wave's operand reads spread over the banks), each row's shift, a wave's "holds +32768" flag, and the plane
     // sums [wave][tile row] (SXh, SXl, n32768)
@@ -233,19 +253,19 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs a) {
     __shared__ int shs[16], cfw[4];
     __shared__ int sfx[ROWS ? 4 * 16 * 4 : 1];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int ntiles = (a.N + 15) >> 4;
-    const int nt = blockIdx.x % ntiles, kb = blockIdx.x / ntiles;
-    const int t0 = blockIdx.y * RT;                  // this block's first row tile
+    const int ntiles = (a.N + 15) >> 4, ngr = ntiles / NB;   // ntiles a multiple of NB
+    const int nt = blockIdx.x % ngr, kb = blockIdx.x / ngr;   // column group, K slice
+    const int t0 = blockIdx.y;                               // row tile
     const int s0 = kb * (KS / KSPLIT) + wave * NS;
-    const v4* Wb = reinterpret_cast<const v4*>(a.W) + (size_t)nt * KS * 128 + lane;
+    const v4* Wb = reinterpret_cast<const v4*>(a.W) + (size_t)nt * NB * KS * 128 + lane;
     const v4* Ab = reinterpret_cast<const v4*>(a.planes) + lane;
     // gauged epilogues: row tid's light facts first (loads complete in order: its gauge need not wait for the
     // tiles)
     constexpr bool GAUGED = EPI == EPI_GAUGED || EPI == EPI_GAUGED_EDGE;
-    static_assert(!ROWS || (RT == 1 && KSPLIT == 1 && !GAUGED), "a light formed here: one row tile and K slice, plain");
+    static_assert(!ROWS || !GAUGED, "a light formed here feeds a plain epilogue or K-slice partials");
     v4 gf = {0, 0, 0, 0};
     if (GAUGED) gf = *reinterpret_cast<const v4*>(a.rowinfo + (size_t)(tid < a.rows ? tid : 0) * 8);
-    v4 wh[NS], wl[NS], xh[NS][RT], xl[NS][RT];
+    v4 wh[NB][NS], wl[NB][NS], xh[NS], xl[NS];
     // SRC > 0: wave w lights tile rows 4 w .. 4 w + 3.  Their OR words (word n = lane + 64 m of the wave's
     // 4 SRC), then their values as contiguous 1 KB wave loads (value pair 64 c + lane of row j), all ahead of the
     // weights (their wait then leaves the weights in flight); rows past the last read zeros
@@ -270,18 +290,18 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs a) {
                 xr[jr][c] = buf_load4(rx, (unsigned)((row0 + jr) * a.xstride + kb * KR + 2 * (64 * c + lane)) * 8u);
     }
 #pragma unroll
-    for (int i = 0; i < NS; i++) {
-        wh[i] = __builtin_nontemporal_load(Wb + (size_t)(s0 + i) * 128);
-        wl[i] = __builtin_nontemporal_load(Wb + (size_t)(s0 + i) * 128 + 64);
-    }
+    for (int nb = 0; nb < NB; nb++)
+#pragma unroll
+        for (int i = 0; i < NS; i++) {
+            wh[nb][i] = __builtin_nontemporal_load(Wb + (size_t)nb * KS * 128 + (size_t)(s0 + i) * 128);
+            wl[nb][i] = __builtin_nontemporal_load(Wb + (size_t)nb * KS * 128 + (size_t)(s0 + i) * 128 + 64);
+        }
     if constexpr (!ROWS) {
 #pragma unroll
-        for (int i = 0; i < NS; i++)
-#pragma unroll
-            for (int t = 0; t < RT; t++) {
-                xh[i][t] = Ab[((size_t)(t0 + t) * KS + s0 + i) * 192];
-                xl[i][t] = Ab[((size_t)(t0 + t) * KS + s0 + i) * 192 + 64];
-            }
+        for (int i = 0; i < NS; i++) {
+            xh[i] = Ab[((size_t)t0 * KS + s0 + i) * 192];
+            xl[i] = Ab[((size_t)t0 * KS + s0 + i) * 192 + 64];
+        }
     }
     const int n32 = !ROWS && lane < a.rows ? a.rowinfo[lane * 8 + 6] : 0;
     const int rsv = !ROWS && tid < a.rows * 8 ? a.rowinfo[tid] : 0;
@@ -292,7 +312,7 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs a) {
     int l_n32 = 0;
     if constexpr (ROWS) {
         const int p = a.pos ? *a.pos : 0;
-        const bool rec = a.rx16 && t0 == 0 && nt == 0 && kb == 0 && a.rec_pos && *a.rec_pos == p;
+        const bool rec = a.rx16 && t0 == 0 && nt == 0 && a.rec_pos && *a.rec_pos == p;
         int mx = 0;
 #pragma unroll
         for (int jr = 0; jr < 4; jr++) {
@@ -310,14 +330,14 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs a) {
                 const int x1 = (int)(wadd((i64)(((u64)(unsigned)w[3] << 32) | (unsigned)w[2]), half) >> sh);
                 mx = max(mx, max(x0, x1));
                 if (rec && wave == 0 && jr == 0) {       // stream 0's record
-                    a.rx16[2 * (64 * c + lane)] = x0;
-                    a.rx16[2 * (64 * c + lane) + 1] = x1;
+                    a.rx16[kb * KR + 2 * (64 * c + lane)] = x0;
+                    a.rx16[kb * KR + 2 * (64 * c + lane) + 1] = x1;
                 }
                 // +32768 held as 32767 (the correction plane carries the rest)
                 xs[(4 * wave + jr) * XSTR + 64 * c + lane] =
                     (int)__builtin_amdgcn_perm((unsigned)min(x1, 32767), (unsigned)min(x0, 32767), 0x05040100u);
             }
-            if (rec && wave == 0 && jr == 0 && lane == 0) { a.rexls[0] = sh - 16; a.rexls[1] = 0; }
+            if (rec && kb == 0 && wave == 0 && jr == 0 && lane == 0) { a.rexls[0] = sh - 16; a.rexls[1] = 0; }
         }
         const bool c_here = __ballot(mx == 32768) != 0;
         if (lane == 0) cfw[wave] = c_here;
@@ -339,8 +359,8 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs a) {
                 sxh = __builtin_amdgcn_sdot4((int)qh[g], 0x01010101, sxh, false);
                 sxl = __builtin_amdgcn_sdot4((int)ql[g], 0x01010101, sxl, false);
             }
-            xh[i][0] = v4{(int)qh[0], (int)qh[1], (int)qh[2], (int)qh[3]};
-            xl[i][0] = v4{(int)ql[0], (int)ql[1], (int)ql[2], (int)ql[3]};
+            xh[i] = v4{(int)qh[0], (int)qh[1], (int)qh[2], (int)qh[3]};
+            xl[i] = v4{(int)ql[0], (int)ql[1], (int)ql[2], (int)ql[3]};
             xc[i] = v4{0, 0, 0, 0};
         }
         if (cfw[0] | cfw[1] | cfw[2] | cfw[3]) {       // a light of +32768 in the tile (rare): the correction
@@ -373,49 +393,50 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs a) {
     i64 g_ls = 0, g_e2 = 0;
     if (GAUGED)
         g_ls = gauge_ls_pow_v(gf[1], (i64)(((u64)(unsigned)gf[3] << 32) | (unsigned)gf[2]), gf[0], a.tb, g_e2);
-    const int j = nt * 16 + (lane & 15);
-    const bool jok = j < a.N;
-    i64 swh = 0, swl = 0, we = 0, bc = 0;
-    if (EPI != EPI_PART && jok) { swh = a.csum[2 * j]; swl = a.csum[2 * j + 1]; we = a.we[j]; bc = a.bias[j]; }
-    const u64 cmask = __ballot(n32 != 0);       // row tiles with a +32768 light need the correction plane
-    v4 acc[RT][3];
+    // the column facts of each tile
+    i64 swh[NB], swl[NB], we[NB], bc[NB];
 #pragma unroll
-    for (int t = 0; t < RT; t++) acc[t][0] = acc[t][1] = acc[t][2] = v4{0, 0, 0, 0};
+    for (int nb = 0; nb < NB; nb++) {
+        const int j = (nt * NB + nb) * 16 + (lane & 15);
+        swh[nb] = swl[nb] = we[nb] = bc[nb] = 0;
+        if (EPI != EPI_PART && j < a.N) { swh[nb] = a.csum[2 * j]; swl[nb] = a.csum[2 * j + 1]; we[nb] = a.we[j]; bc[nb] = a.bias[j]; }
+    }
+    v4 acc[NB][3];
+#pragma unroll
+    for (int nb = 0; nb < NB; nb++) acc[nb][0] = acc[nb][1] = acc[nb][2] = v4{0, 0, 0, 0};
 #pragma unroll
     for (int i = 0; i < NS; i++)
 #pragma unroll
-        for (int t = 0; t < RT; t++) {
-            acc[t][0] = __builtin_amdgcn_mfma_i32_16x16x64_i8(xh[i][t], wh[i], acc[t][0], 0, 0, 0);
-            acc[t][1] = __builtin_amdgcn_mfma_i32_16x16x64_i8(xh[i][t], wl[i], acc[t][1], 0, 0, 0);
-            acc[t][2] = __builtin_amdgcn_mfma_i32_16x16x64_i8(xl[i][t], wl[i], acc[t][2], 0, 0, 0);
-            acc[t][1] = __builtin_amdgcn_mfma_i32_16x16x64_i8(xl[i][t], wh[i], acc[t][1], 0, 0, 0);
+        for (int nb = 0; nb < NB; nb++) {
+            acc[nb][0] = __builtin_amdgcn_mfma_i32_16x16x64_i8(xh[i], wh[nb][i], acc[nb][0], 0, 0, 0);
+            acc[nb][1] = __builtin_amdgcn_mfma_i32_16x16x64_i8(xh[i], wl[nb][i], acc[nb][1], 0, 0, 0);
+            acc[nb][2] = __builtin_amdgcn_mfma_i32_16x16x64_i8(xl[i], wl[nb][i], acc[nb][2], 0, 0, 0);
+            acc[nb][1] = __builtin_amdgcn_mfma_i32_16x16x64_i8(xl[i], wh[nb][i], acc[nb][1], 0, 0, 0);
         }
-    if constexpr (ROWS) {
-        if (__ballot(l_n32 != 0)) {                      // this wave's steps hold a +32768 light
+    // a +32768 light (held as 32767) adds its correction plane: SRC > 0, this wave's steps hold one; else
+    // the row tile has one (row facts)
+    bool corr;
+    if constexpr (ROWS) corr = __ballot(l_n32 != 0) != 0;
+    else corr = ((__ballot(n32 != 0) >> (16 * t0)) & 0xFFFFull) != 0;
+    if (corr) {
 #pragma unroll
-            for (int i = 0; i < NS; i++) {
-                acc[0][1] = __builtin_amdgcn_mfma_i32_16x16x64_i8(xc[i], wh[i], acc[0][1], 0, 0, 0);
-                acc[0][2] = __builtin_amdgcn_mfma_i32_16x16x64_i8(xc[i], wl[i], acc[0][2], 0, 0, 0);
+        for (int i = 0; i < NS; i++) {
+            v4 cc;
+            if constexpr (ROWS) cc = xc[i];
+            else cc = Ab[((size_t)t0 * KS + s0 + i) * 192 + 128];
+#pragma unroll
+            for (int nb = 0; nb < NB; nb++) {
+                acc[nb][1] = __builtin_amdgcn_mfma_i32_16x16x64_i8(cc, wh[nb][i], acc[nb][1], 0, 0, 0);
+                acc[nb][2] = __builtin_amdgcn_mfma_i32_16x16x64_i8(cc, wl[nb][i], acc[nb][2], 0, 0, 0);
             }
         }
-    } else {
-#pragma unroll
-        for (int t = 0; t < RT; t++)
-            if ((cmask >> (16 * (t0 + t))) & 0xFFFFull) {
-#pragma unroll
-                for (int i = 0; i < NS; i++) {
-                    const v4 cc = Ab[((size_t)(t0 + t) * KS + s0 + i) * 192 + 128];
-                    acc[t][1] = __builtin_amdgcn_mfma_i32_16x16x64_i8(cc, wh[i], acc[t][1], 0, 0, 0);
-                    acc[t][2] = __builtin_amdgcn_mfma_i32_16x16x64_i8(cc, wl[i], acc[t][2], 0, 0, 0);
-                }
-            }
     }
 #pragma unroll
-    for (int t = 0; t < RT; t++)
+    for (int nb = 0; nb < NB; nb++)
 #pragma unroll
         for (int k3 = 0; k3 < 3; k3++)
 #pragma unroll
-            for (int q = 0; q < 4; q++) red[(((wave * RT + t) * 3 + k3) * 4 + q) * 64 + lane] = acc[t][k3][q];
+            for (int q = 0; q < 4; q++) red[(((wave * NB + nb) * 3 + k3) * 4 + q) * 64 + lane] = acc[nb][k3][q];
     const bool keep1 = !GAUGED || (tid & 7) == 0 || (tid & 7) > 3;      // slots 1-3 carry LS, e2
     if (tid < a.rows * 8 && keep1) rinfo[tid] = rsv;
     if (tid + 256 < a.rows * 8 && keep1) rinfo[tid + 256] = rsv2;
@@ -423,62 +444,84 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs a) {
         rinfo[tid * 8 + 1] = (int)(u64)g_ls; rinfo[tid * 8 + 2] = (int)((u64)g_ls >> 32); rinfo[tid * 8 + 3] = (int)g_e2;
     }
     __syncthreads();
-    int fin[RT][3];
+    if constexpr (ROWS && EPI == EPI_PART) {   // the slice's light facts, for the consumer that finishes the bank
+        if (nt == 0 && tid < 16 && 16 * t0 + tid < a.rows) {
+            const int* f = sfx + tid * 4;
+            int* o = a.sfacts + ((size_t)kb * a.rows + 16 * t0 + tid) * 4;
+            o[0] = f[0] + f[64] + f[128] + f[192];
+            o[1] = f[1] + f[65] + f[129] + f[193];
+            o[2] = f[2] + f[66] + f[130] + f[194];
+            o[3] = f[3];
+        }
+    }
+    const int row = 16 * t0 + 4 * (lane >> 4) + wave;
+    if (row >= a.rows) return;
+    const int p = a.pos ? *a.pos : 0;
+    const bool rec = a.rec_pos && *a.rec_pos == p && row == 0;
+    // the row's light facts
+    const int* ri = rinfo + row * 8;
+    i64 ex = ri[0], fsxh = ri[4], fsxl = ri[5], fn32 = ri[6];
+    if constexpr (ROWS) {                            // from the four waves' steps
+        const int* f = sfx + (row - 16 * t0) * 4;
+        ex = f[3];
+        fsxh = f[0] + f[64] + f[128] + f[192];
+        fsxl = f[1] + f[65] + f[129] + f[193];
+        fn32 = f[2] + f[66] + f[130] + f[194];
+    }
 #pragma unroll
-    for (int t = 0; t < RT; t++)
+    for (int nb = 0; nb < NB; nb++) {
+        const int j = (nt * NB + nb) * 16 + (lane & 15);
+        if (j >= a.N) continue;
+        int fin[3];
 #pragma unroll
         for (int k3 = 0; k3 < 3; k3++) {
             int sum = 0;
 #pragma unroll
-            for (int w = 0; w < 4; w++) sum += red[(((w * RT + t) * 3 + k3) * 4 + wave) * 64 + lane];
-            fin[t][k3] = sum;
+            for (int w = 0; w < 4; w++) sum += red[(((w * NB + nb) * 3 + k3) * 4 + wave) * 64 + lane];
+            fin[k3] = sum;
         }
-    if (!jok) return;
-    const int p = a.pos ? *a.pos : 0;
-    const bool rec0 = a.rec_pos && *a.rec_pos == p;
-#pragma unroll
-    for (int t = 0; t < RT; t++) {
-        const int row = 16 * (t0 + t) + 4 * (lane >> 4) + wave;
-        if (row >= a.rows) continue;
         if (EPI == EPI_PART) {
 #pragma unroll
-            for (int k3 = 0; k3 < 3; k3++) a.part[(((size_t)kb * 3 + k3) * a.rows + row) * a.N + j] = fin[t][k3];
+            for (int k3 = 0; k3 < 3; k3++) a.part[(((size_t)kb * 3 + k3) * a.rows + row) * a.N + j] = fin[k3];
             continue;
         }
-        const int* ri = rinfo + row * 8;
-        i64 ex = ri[0], fsxh = ri[4], fsxl = ri[5], fn32 = ri[6];
-        if constexpr (ROWS) {                            // the row's facts from the four waves' steps
-            const int* f = sfx + (row - 16 * t0) * 4;
-            ex = f[3];
-            fsxh = f[0] + f[64] + f[128] + f[192];
-            fsxl = f[1] + f[65] + f[129] + f[193];
-            fn32 = f[2] + f[66] + f[130] + f[194];
-        }
-        const i64 pile = 65536 * (i64)fin[t][0] + 256 * (i64)fin[t][1] + fin[t][2] + 32768 * (fsxh + swh) +
-                         128 * (fsxl + swl) + 16384 * (i64)K + 128 * fn32;
-        const bool rec = rec0 && row == 0;
+        const i64 pile = 65536 * (i64)fin[0] + 256 * (i64)fin[1] + fin[2] + 32768 * (fsxh + swh[nb]) +
+                         128 * (fsxl + swl[nb]) + 16384 * (i64)K + 128 * fn32;
         if (rec && a.rpile) a.rpile[j] = pile;
+        i64 yo = 0;
         if (EPI == EPI_PILE) {
             a.Y[(size_t)row * a.ystride + j] = pile;
         } else if (EPI == EPI_PLAIN_ADD) {             // the stream takes the plain bank (base2.py:73-76, 105)
             i64* yp = a.Y + (size_t)row * a.ystride + j;
-            const i64 y = wadd(*yp, wadd(rsh(pile, -(we + ex + 16)), bc));
+            const i64 y = wadd(*yp, wadd(rsh(pile, -(we[nb] + ex + 16)), bc[nb]));
             *yp = y;
             if (rec && a.rout) a.rout[j] = y;
         } else if (EPI == EPI_PLAIN || EPI == EPI_PLAIN_EDGE) {   // the Pythia machine's banks (:112-114, 156)
-            i64 y = wadd(rsh(pile, -(we + ex + 16)), bc);
+            i64 y = wadd(rsh(pile, -(we[nb] + ex + 16)), bc[nb]);
             if (rec && a.rout) a.rout[j] = y;
             if (EPI == EPI_PLAIN_EDGE) {
                 y = edge1(y, a.tb);
                 if (rec && a.rout2) a.rout2[j] = y;
             }
             a.Y[(size_t)row * a.ystride + j] = y;
+            yo = y;
         } else {
             const i64 ls = (i64)(((u64)(unsigned)ri[2] << 32) | (unsigned)ri[1]);
-            i64 y = wadd(power_known(pile, wsub(wmul(we + ex + 16, 65536), ls), (i64)ri[3]), bc);
+            i64 y = wadd(power_known(pile, wsub(wmul(we[nb] + ex + 16, 65536), ls), (i64)ri[3]), bc[nb]);
             if (EPI == EPI_GAUGED_EDGE) y = edge1(y, a.tb);
             a.Y[(size_t)row * a.ystride + j] = y;
             if (rec && a.rout) a.rout[j] = y;
+            yo = y;
+        }
+        if ((EPI == EPI_GAUGED_EDGE || EPI == EPI_PLAIN_EDGE) && a.orw_out) {
+            // the row's OR over this tile's 16 columns (the 16 lanes of a DPP row hold one row; N is a multiple
+            // of 16, so all of them are here): prefix ORs, the total in lane 15
+            i64 o = iabs64(yo);
+            o |= dpp64<0x111, 0xf, 0xf>(o, 0);
+            o |= dpp64<0x112, 0xf, 0xf>(o, 0);
+            o |= dpp64<0x114, 0xf, 0xf>(o, 0);
+            o |= dpp64<0x118, 0xf, 0xf>(o, 0);
+            if ((lane & 15) == 15) a.orw_out[(size_t)row * ntiles + nt * NB + nb] = o;
         }
     }
 }
@@ -677,7 +720,8 @@ struct PyRowArgs {
     signed char* planes1; int* rowinfo1;          // light of gauge 1
     signed char* planes2; int* rowinfo2;          // light of gauge 2
     // PY_ADD: mproj's four K slices of partial accumulators, finished here (proj's half is already in R)
-    const int* partM; int kinM; const int* rowinfoM; const int* csumM; const int* weM; const i64* biasM;
+    const int* partM; int kinM; const int* csumM; const int* weM; const i64* biasM;
+    const int* sfactsM;                           // mproj's K slices' light facts [4][rows][4]
     Tables tb;
     const int* rec_pos;
     i64* rg1; i64* rx1; i64* rex1; i64* rg2; i64* rx2; i64* rex2;   // the gauges and their lights
@@ -754,7 +798,9 @@ __global__ __launch_bounds__(192) void k_py_rows(PyRowArgs a) {
             const v2q_p r01 = *reinterpret_cast<const v2q_p*>(a.R + (size_t)r * 768 + k);
             const v2q_p r23 = *reinterpret_cast<const v2q_p*>(a.R + (size_t)r * 768 + k + 2);
             const i64 rr[4] = {r01[0], r01[1], r23[0], r23[1]};
-            plain4_finish<4>(PM, a.kinM, a.rowinfoM + (size_t)r * 8, pM, yM);
+            int rim[8];
+            slice_facts<4>(a.sfactsM, a.rows, r, rim);
+            plain4_finish<4>(PM, a.kinM, rim, pM, yM);
 #pragma unroll
             for (int j = 0; j < 4; j++) {
                 R4[j] = wadd(rr[j], yM[j]);
@@ -876,7 +922,7 @@ BINST_L(3072, PRO_X16, 1)
 BINST_L(768, PRO_ADD_GAUGE, 4)
 template __global__ void k_py_rows<PY_EMBED>(PyRowArgs);
 template __global__ void k_py_rows<PY_ADD>(PyRowArgs);
-#define BINST_G(K, RT, KSPLIT, EPI) template __global__ void k_gemm<K, RT, KSPLIT, EPI>(GemmArgs);
+#define BINST_G(K, NB, KSPLIT, EPI) template __global__ void k_gemm<K, NB, KSPLIT, EPI>(GemmArgs);
 #define BINST_GR(RT) BINST_G(768, RT, 1, EPI_GAUGED) BINST_G(768, RT, 1, EPI_GAUGED_EDGE) BINST_G(768, RT, 1, EPI_PLAIN_ADD) \
     BINST_G(768, RT, 1, EPI_PART) BINST_G(768, RT, 1, EPI_PLAIN_EDGE) BINST_G(3072, RT, 4, EPI_PART) \
     BINST_G(768, RT, 1, EPI_PILE) BINST_G(3072, RT, 1, EPI_PILE) BINST_G(768, RT, 1, EPI_PLAIN)

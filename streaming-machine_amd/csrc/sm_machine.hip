@@ -235,6 +235,8 @@ struct sm_machine {
     // state
     i64 *R = nullptr, *QKV = nullptr, *att = nullptr, *hid = nullptr;
     i64* attor = nullptr;                               // [rows][12] OR of |att| over each head's values
+    i64* hidor = nullptr;                               // [rows][192] OR of |hid| over each fc block's columns
+    int* sfacts = nullptr;                              // [4][rows][4] mproj's K slices' light facts
     int *K16 = nullptr, *EK = nullptr, *V = nullptr;   // [L][B][12 heads][ctx][64] (EK: [L][B][12][ctx])
     int* seq = nullptr;                                 // [B][ctx + 1]
     int* words = nullptr;                               // [B][ctx + 1]
@@ -358,7 +360,7 @@ static void machine_free(sm_machine* m) {
     free_plate(m->head);
     free_mfma_plate(m->mhead);
     tables_free(m->T);
-    void* ps[] = {m->pfmap, m->planes, m->part_acc, m->rowinfo, m->wte, m->wpe, m->R, m->QKV, m->att, m->attor, m->hid, m->K16, m->EK, m->V, m->seq, m->words, m->ctl,
+    void* ps[] = {m->pfmap, m->planes, m->part_acc, m->rowinfo, m->wte, m->wpe, m->R, m->QKV, m->att, m->attor, m->hidor, m->sfacts, m->hid, m->K16, m->EK, m->V, m->seq, m->words, m->ctl,
                   m->part_v, m->part_i, m->r_x16, m->r_exls, m->r_pile, m->r_qkv, m->r_att, m->r_hid, m->r_resid,
                   m->r_hx16, m->r_hexls, m->r_hpile, m->r_logits, m->r_gauge, m->r_fcpre, m->r_hgauge,
                   m->fg, m->fb, m->ew, m->ee, m->cosT, m->sinT};
@@ -399,7 +401,7 @@ static int launch_step_batched(sm_machine* m, int parts, hipEvent_t hs, hipEvent
     auto finish_light = [&](const MfmaPlate& P, i64* rpile, i64* rout, i64* rx16, i64* rexls) {
         LightArgs a = light_args(P.N, nullptr, rx16, rexls);
         a.part = m->part_acc; a.kin = P.K; a.csum = P.csum; a.we = P.e; a.bias = P.b; a.Y = m->R;
-        a.rpile_in = rpile; a.rout_in = rout;
+        a.rpile_in = rpile; a.rout_in = rout; a.sfacts = m->sfacts;
         k_light<768, PRO_ADD_GAUGE, 192, 4><<<B, 192, 0, m->st>>>(a);
     };
     auto gemm_args = [&](const MfmaPlate& P, i64* Y, int ystride, i64* rpile, i64* rout) {
@@ -446,15 +448,16 @@ static int launch_step_batched(sm_machine* m, int parts, hipEvent_t hs, hipEvent
             LightArgs g = light_args(768, m->R, rx + 2 * 3072, re + 4);
             k_light<768, PRO_GAUGE, 192, 1><<<B, 192, 0, m->st>>>(g);
         }
-        {   // fc: gauged, the edge, written (the hidden rows); then their 3072-wide light
+        {   // fc: gauged, the edge, written (the hidden rows) with their OR words
             GemmArgs a = gemm_args(m->mbank[l][2], m->hid, 3072, rp + 2 * 3072, m->r_hid + l * 3072);
+            a.orw_out = m->hidor;
             k_gemm<768, 1, 1, EPI_GAUGED_EDGE><<<dim3(m->mbank[l][2].ntiles, RT), 256, 0, m->st>>>(a);
-            LightArgs h = light_args(3072, m->hid, rx + 3 * 3072, re + 6);
-            k_light<3072, PRO_TO16, 768, 1><<<B, 768, 0, m->st>>>(h);
         }
-        {
+        {   // mproj: the hidden rows' light formed in each K slice's blocks; partial accumulators and slice facts
             GemmArgs a = gemm_args(m->mbank[l][3], nullptr, 0, nullptr, nullptr);
-            k_gemm<3072, 1, 4, EPI_PART><<<dim3(m->mbank[l][3].ntiles * 4, RT), 256, 0, m->st>>>(a);
+            a.X = m->hid; a.xstride = 3072; a.orw = m->hidor; a.rx16 = rx + 3 * 3072; a.rexls = re + 6;
+            a.sfacts = m->sfacts;
+            k_gemm<3072, 3, 4, EPI_PART, 192><<<dim3(m->mbank[l][3].ntiles / 3 * 4, RT), 256, 0, m->st>>>(a);
         }
         const bool last = l == 11;     // the last stream update lights the head
         finish_light(m->mbank[l][3], rp + 3 * 3072, m->r_resid + (l * 2 + 1) * 768,
@@ -593,10 +596,8 @@ static int launch_step_pythia_batched(sm_machine* m, int parts, hipEvent_t hs, h
     const int B = rowmap ? nrows : m->B;
     const int* recp = rowmap ? nullptr : ctl + CTL_RECPOS;
     const size_t PL = (size_t)4 * 48 * 3 * 1024, RC = m->RC;
-    signed char* pA = m->planes; signed char* pB = m->planes + PL; signed char* pC = m->planes + 2 * PL;
-    signed char* pD = m->planes + 3 * PL;
-    int* rA = m->rowinfo; int* rB = m->rowinfo + RC * 8; int* rC = m->rowinfo + 2 * RC * 8;
-    int* rD = m->rowinfo + 3 * RC * 8;
+    signed char* pA = m->planes; signed char* pB = m->planes + PL;      // the two gauges' lights (qkv, fc)
+    int* rA = m->rowinfo; int* rB = m->rowinfo + RC * 8;
     int* P0 = m->part_acc;                          // mproj's partial accumulators
     auto gemm_args = [&](const MfmaPlate& P, signed char* planes, int* rowinfo) {
         GemmArgs a{};
@@ -644,21 +645,19 @@ static int launch_step_pythia_batched(sm_machine* m, int parts, hipEvent_t hs, h
             k_kv_rows<1><<<dim3(12, B), 128, 0, m->st>>>(a);
             break;
         }
-        {   // fc: plain and edged in its bank (the hidden rows), then their 3072-wide light
+        {   // fc: plain and edged in its bank (the hidden rows), with their OR words
             GemmArgs a = gemm_args(m->mbank[l][2], pB, rB);
             a.Y = m->hid; a.ystride = 3072;
             a.rpile = rp + 2 * 3072; a.rout = m->r_fcpre + l * 3072; a.rout2 = m->r_hid + l * 3072;
+            a.orw_out = m->hidor;
             k_gemm<768, 1, 1, EPI_PLAIN_EDGE><<<dim3(m->mbank[l][2].ntiles, RT), 256, 0, m->st>>>(a);
-            LightArgs h{};
-            h.K = 3072; h.rows = B; h.X = m->hid; h.pos = ctl + CTL_POS; h.plen = ctl + CTL_PLEN;
-            h.planes = pC; h.rowinfo = rC; h.tb = tb; h.rec_pos = recp;
-            h.rx16 = m->r_x16 + (l * 4 + 3) * 3072; h.rexls = m->r_exls + (l * 4 + 3) * 2;
-            k_light<3072, PRO_TO16, 768, 1><<<B, 768, 0, m->st>>>(h);
         }
-        {   // mproj: partials over four K slices
-            GemmArgs a = gemm_args(m->mbank[l][3], pC, rC);
+        {   // mproj: the hidden rows' light formed in each K slice's blocks; partials over four K slices
+            GemmArgs a = gemm_args(m->mbank[l][3], nullptr, nullptr);
             a.part = P0;
-            k_gemm<3072, 1, 4, EPI_PART><<<dim3(m->mbank[l][3].ntiles * 4, RT), 256, 0, m->st>>>(a);
+            a.X = m->hid; a.xstride = 3072; a.orw = m->hidor; a.sfacts = m->sfacts;
+            a.rx16 = m->r_x16 + (l * 4 + 3) * 3072; a.rexls = m->r_exls + (l * 4 + 3) * 2;
+            k_gemm<3072, 3, 4, EPI_PART, 192><<<dim3(m->mbank[l][3].ntiles / 3 * 4, RT), 256, 0, m->st>>>(a);
         }
         {   // attention with turns
             AttArgs a{};
@@ -672,7 +671,7 @@ static int launch_step_pythia_batched(sm_machine* m, int parts, hipEvent_t hs, h
             k_attend<1, 0><<<dim3(12, B), NTHR, (size_t)m->ctx * 12, m->st>>>(a);
         }
         {   // proj: the attention rows' light formed in its bank, added into the stream (R + At)
-            GemmArgs g = gemm_args(m->mbank[l][1], pD, rD);
+            GemmArgs g = gemm_args(m->mbank[l][1], nullptr, nullptr);
             g.Y = m->R; g.ystride = 768; g.rpile = rp + 3072; g.rout = m->r_resid + (l * 2 + 0) * 768;
             g.X = m->att; g.xstride = 768; g.orw = m->attor;
             g.rx16 = m->r_x16 + (l * 4 + 1) * 3072; g.rexls = m->r_exls + (l * 4 + 1) * 2;
@@ -681,7 +680,7 @@ static int launch_step_pythia_batched(sm_machine* m, int parts, hipEvent_t hs, h
         {   // R += Mo (the parallel residual's other half), then the next gauges' lights
             PyRowArgs a = rows_args();
             const MfmaPlate& Pm = m->mbank[l][3];
-            a.partM = P0; a.kinM = 3072; a.rowinfoM = rC; a.csumM = Pm.csum; a.weM = Pm.e; a.biasM = Pm.b;
+            a.partM = P0; a.kinM = 3072; a.sfactsM = m->sfacts; a.csumM = Pm.csum; a.weM = Pm.e; a.biasM = Pm.b;
             a.rpileM = rp + 3 * 3072; a.routM = m->r_resid + (l * 2 + 1) * 768;
             gauges(a, l + 1);
             k_py_rows<PY_ADD><<<B, 192, 0, m->st>>>(a);
@@ -972,8 +971,9 @@ extern "C" int sm_create(const char* layout_dir, const sm_config* cfg, sm_machin
     const size_t nparts = m->B == 1 ? (size_t)m->head_grid : (size_t)m->B * head_rows_grid((m->vocab + 15) / 16);
     // state
     const size_t B = m->B, ctx = m->ctx, RC = m->RC;
-    const size_t nsets = m->kind == 1 && mfma ? 4 : 1;      // light-plane sets (the Pythia MFMA phases keep four)
+    const size_t nsets = m->kind == 1 && mfma ? 2 : 1;      // light-plane sets (the Pythia MFMA phases keep two)
     if ((rc = dalloc(&m->R, RC * 768)) || (rc = dalloc(&m->QKV, RC * 2304)) || (rc = dalloc(&m->att, RC * 768)) || (rc = dalloc(&m->attor, RC * 12)) ||
+        (rc = dalloc(&m->hidor, RC * 192)) || (rc = dalloc(&m->sfacts, 4 * RC * 4)) ||
         (rc = dalloc(&m->hid, RC * 3072)) || (rc = dalloc(&m->K16, 12 * B * ctx * 768)) || (rc = dalloc(&m->EK, 12 * B * ctx * 12)) ||
         (rc = dalloc(&m->pfmap, B * ctx)) ||
         (rc = dalloc(&m->V, 12 * B * ctx * 768)) || (rc = dalloc(&m->seq, B * (ctx + 1))) || (rc = dalloc(&m->words, B * (ctx + 1))) ||
