@@ -468,10 +468,10 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs a) {
         fsxl = f[1] + f[65] + f[129] + f[193];
         fn32 = f[2] + f[66] + f[130] + f[194];
     }
+    // every tile's result first (the edge's table reads of all NB tiles in flight together), then the stores
+    i64 pile[NB], y1[NB], y2[NB];                   // y1: before the edge, y2: after it (the value written)
 #pragma unroll
     for (int nb = 0; nb < NB; nb++) {
-        const int j = (nt * NB + nb) * 16 + (lane & 15);
-        if (j >= a.N) continue;
         int fin[3];
 #pragma unroll
         for (int k3 = 0; k3 < 3; k3++) {
@@ -481,42 +481,46 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs a) {
             fin[k3] = sum;
         }
         if (EPI == EPI_PART) {
+            const int j = (nt * NB + nb) * 16 + (lane & 15);
+            if (j < a.N) {
 #pragma unroll
-            for (int k3 = 0; k3 < 3; k3++) a.part[(((size_t)kb * 3 + k3) * a.rows + row) * a.N + j] = fin[k3];
+                for (int k3 = 0; k3 < 3; k3++) a.part[(((size_t)kb * 3 + k3) * a.rows + row) * a.N + j] = fin[k3];
+            }
             continue;
         }
-        const i64 pile = 65536 * (i64)fin[0] + 256 * (i64)fin[1] + fin[2] + 32768 * (fsxh + swh[nb]) +
-                         128 * (fsxl + swl[nb]) + 16384 * (i64)K + 128 * fn32;
-        if (rec && a.rpile) a.rpile[j] = pile;
-        i64 yo = 0;
+        pile[nb] = 65536 * (i64)fin[0] + 256 * (i64)fin[1] + fin[2] + 32768 * (fsxh + swh[nb]) +
+                   128 * (fsxl + swl[nb]) + 16384 * (i64)K + 128 * fn32;
         if (EPI == EPI_PILE) {
-            a.Y[(size_t)row * a.ystride + j] = pile;
+            y1[nb] = y2[nb] = pile[nb];
         } else if (EPI == EPI_PLAIN_ADD) {             // the stream takes the plain bank (base2.py:73-76, 105)
-            i64* yp = a.Y + (size_t)row * a.ystride + j;
-            const i64 y = wadd(*yp, wadd(rsh(pile, -(we[nb] + ex + 16)), bc[nb]));
-            *yp = y;
-            if (rec && a.rout) a.rout[j] = y;
+            const int j = (nt * NB + nb) * 16 + (lane & 15);
+            const i64 old = j < a.N ? a.Y[(size_t)row * a.ystride + j] : 0;
+            y1[nb] = y2[nb] = wadd(old, wadd(rsh(pile[nb], -(we[nb] + ex + 16)), bc[nb]));
         } else if (EPI == EPI_PLAIN || EPI == EPI_PLAIN_EDGE) {   // the Pythia machine's banks (:112-114, 156)
-            i64 y = wadd(rsh(pile, -(we[nb] + ex + 16)), bc[nb]);
-            if (rec && a.rout) a.rout[j] = y;
-            if (EPI == EPI_PLAIN_EDGE) {
-                y = edge1(y, a.tb);
-                if (rec && a.rout2) a.rout2[j] = y;
-            }
-            a.Y[(size_t)row * a.ystride + j] = y;
-            yo = y;
+            y1[nb] = wadd(rsh(pile[nb], -(we[nb] + ex + 16)), bc[nb]);
+            y2[nb] = EPI == EPI_PLAIN_EDGE ? edge1(y1[nb], a.tb) : y1[nb];
         } else {
             const i64 ls = (i64)(((u64)(unsigned)ri[2] << 32) | (unsigned)ri[1]);
-            i64 y = wadd(power_known(pile, wsub(wmul(we[nb] + ex + 16, 65536), ls), (i64)ri[3]), bc[nb]);
-            if (EPI == EPI_GAUGED_EDGE) y = edge1(y, a.tb);
-            a.Y[(size_t)row * a.ystride + j] = y;
-            if (rec && a.rout) a.rout[j] = y;
-            yo = y;
+            y1[nb] = wadd(power_known(pile[nb], wsub(wmul(we[nb] + ex + 16, 65536), ls), (i64)ri[3]), bc[nb]);
+            y2[nb] = EPI == EPI_GAUGED_EDGE ? edge1(y1[nb], a.tb) : y1[nb];
+        }
+    }
+    if (EPI == EPI_PART) return;
+#pragma unroll
+    for (int nb = 0; nb < NB; nb++) {
+        const int j = (nt * NB + nb) * 16 + (lane & 15);
+        if (j < a.N) {
+            a.Y[(size_t)row * a.ystride + j] = y2[nb];
+            if (rec) {                                   // stream 0's record
+                if (a.rpile) a.rpile[j] = pile[nb];
+                if (a.rout) a.rout[j] = EPI == EPI_PLAIN_EDGE ? y1[nb] : y2[nb];
+                if (EPI == EPI_PLAIN_EDGE && a.rout2) a.rout2[j] = y2[nb];
+            }
         }
         if ((EPI == EPI_GAUGED_EDGE || EPI == EPI_PLAIN_EDGE) && a.orw_out) {
             // the row's OR over this tile's 16 columns (the 16 lanes of a DPP row hold one row; N is a multiple
             // of 16, so all of them are here): prefix ORs, the total in lane 15
-            i64 o = iabs64(yo);
+            i64 o = iabs64(y2[nb]);
             o |= dpp64<0x111, 0xf, 0xf>(o, 0);
             o |= dpp64<0x112, 0xf, 0xf>(o, 0);
             o |= dpp64<0x114, 0xf, 0xf>(o, 0);

@@ -235,7 +235,7 @@ struct sm_machine {
     // state
     i64 *R = nullptr, *QKV = nullptr, *att = nullptr, *hid = nullptr;
     i64* attor = nullptr;                               // [rows][12] OR of |att| over each head's values
-    i64* hidor = nullptr;                               // [rows][192] OR of |hid| over each fc block's columns
+    i64* hidor = nullptr;                               // [rows][192] OR of |hid| over each fc tile's columns
     int* sfacts = nullptr;                              // [4][rows][4] mproj's K slices' light facts
     int *K16 = nullptr, *EK = nullptr, *V = nullptr;   // [L][B][12 heads][ctx][64] (EK: [L][B][12][ctx])
     int* seq = nullptr;                                 // [B][ctx + 1]
@@ -441,7 +441,8 @@ static int launch_step_batched(sm_machine* m, int parts, hipEvent_t hs, hipEvent
             }
         }
         {   // proj: the attention rows' light formed in the bank, the plain bank added into the stream; then the
-            // stream's light for fc
+            // stream's light and gauge for fc (a light formed in fc's own blocks measured slower: the gauge's
+            // table reads would follow the row's conversion there)
             GemmArgs a = gemm_args(m->mbank[l][1], m->R, 768, rp + 3072, m->r_resid + (l * 2 + 0) * 768);
             a.X = m->att; a.xstride = 768; a.orw = m->attor; a.rx16 = rx + 3072; a.rexls = re + 2;
             k_gemm<768, 1, 1, EPI_PLAIN_ADD, 12><<<dim3(m->mbank[l][1].ntiles, RT), 256, 0, m->st>>>(a);
