@@ -657,62 +657,31 @@ __global__ __launch_bounds__(256) void k_head_rows(GemmArgs a) {
 // ---------------------------------------------------------------------------------------------------------
 // The Pythia machine, batched (foundation0/pythia_base2.py:100-160 for every stream).  One block per stream row.
 //
-// light_store<K>: a row of int64 values (thread t holds k = 4 g .. 4 g + 3 for g = t + 256 m) -> its water
-// level and the MFMA A planes (xh, xl', c) + the row facts {ex, 0, 0, 0, SXh, SXl, n32768}.
-template <int K, int NT>
-SMD void light_store(const i64 (&v)[(K / 4 + NT - 1) / NT][4], int r, signed char* planes, int* rowinfo, int* red,
-                     bool rec, i64* rx16, i64* rexls) {
-    constexpr int NG = K / 4, GPT = (NG + NT - 1) / NT, KS = K / 64, NW = NT / 64;
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    u64 o = 0;
-#pragma unroll
-    for (int m = 0; m < GPT; m++)
-#pragma unroll
-        for (int j = 0; j < 4; j++) o |= (u64)iabs64(v[m][j]);
-    const unsigned olo = wave_or32((unsigned)o), ohi = wave_or32((unsigned)(o >> 32));
-    if (lane == 0) { red[2 * wave] = (int)olo; red[2 * wave + 1] = (int)ohi; }
-    __syncthreads();
-    u64 all = 0;
-#pragma unroll
-    for (int w = 0; w < NW; w++) all |= ((u64)(unsigned)red[2 * w + 1] << 32) | (unsigned)red[2 * w];
-    const int sh = water_shift((i64)all);
-    int sxh = 0, sxl = 0, n32 = 0;
+// four lights k .. k + 3 of row r (x = rshift(v, sh)) into the MFMA A planes of a K-wide row (xh, xl', c, each
+// group of four as one 32-bit store), adding to the row's plane sums
+template <int K>
+SMD void planes4(const i64 (&v)[4], int sh, int r, int k, signed char* planes, bool rec, i64* rx16, int& sxh,
+                 int& sxl, int& n32) {
+    constexpr int KS = K / 64;
     int* pl = reinterpret_cast<int*>(planes + (size_t)(r >> 4) * KS * 3 * 1024);
+    unsigned ph = 0, pq = 0, pc = 0;
 #pragma unroll
-    for (int m = 0; m < GPT; m++) {
-        const int g = tid + NT * m;
-        if (g >= NG) continue;
-        const int k = 4 * g;
-        unsigned ph = 0, pq = 0, pc = 0;
-#pragma unroll
-        for (int j = 0; j < 4; j++) {
-            const int x = (int)rsh(v[m][j], sh);
-            if (rec && rx16) rx16[k + j] = x;
-            const int c = x == 32768;
-            const int xc = x - c;
-            const int xh = xc >> 8, xl = (xc & 255) - 128;
-            sxh += xh; sxl += xl; n32 += c;
-            ph |= (unsigned)(xh & 255) << (8 * j);
-            pq |= (unsigned)(xl & 255) << (8 * j);
-            pc |= (unsigned)c << (8 * j);
-        }
-        const int s = k >> 6, kk = k & 63;
-        const size_t off = ((size_t)s * 3 * 1024 + (size_t)((r & 15) + 16 * (kk >> 4)) * 16 + (kk & 15)) / 4;
-        pl[off] = (int)ph;
-        pl[off + 256] = (int)pq;
-        pl[off + 512] = (int)pc;
+    for (int j = 0; j < 4; j++) {
+        const int x = (int)rsh(v[j], sh);
+        if (rec && rx16) rx16[k + j] = x;
+        const int c = x == 32768;
+        const int xc = x - c;
+        const int xh = xc >> 8, xl = (xc & 255) - 128;
+        sxh += xh; sxl += xl; n32 += c;
+        ph |= (unsigned)(xh & 255) << (8 * j);
+        pq |= (unsigned)(xl & 255) << (8 * j);
+        pc |= (unsigned)c << (8 * j);
     }
-    const int w3 = wave_add32(sxh), w4 = wave_add32(sxl), w5 = wave_add32(n32);
-    if (lane == 0) { red[24 + 3 * wave] = w3; red[25 + 3 * wave] = w4; red[26 + 3 * wave] = w5; }
-    __syncthreads();
-    if (tid == 0) {
-        int SXh = 0, SXl = 0, N32 = 0;
-        for (int w = 0; w < NW; w++) { SXh += red[24 + 3 * w]; SXl += red[25 + 3 * w]; N32 += red[26 + 3 * w]; }
-        int* ri = rowinfo + (size_t)r * 8;
-        ri[0] = -16 + sh; ri[1] = 0; ri[2] = 0; ri[3] = 0; ri[4] = SXh; ri[5] = SXl; ri[6] = N32;
-        if (rec && rexls) { rexls[0] = -16 + sh; rexls[1] = 0; }
-    }
-    __syncthreads();                                // red is reused by the caller
+    const int s = k >> 6, kk = k & 63;
+    const size_t off = ((size_t)s * 3 * 1024 + (size_t)((r & 15) + 16 * (kk >> 4)) * 16 + (kk & 15)) / 4;
+    pl[off] = (int)ph;
+    pl[off + 256] = (int)pq;
+    pl[off + 512] = (int)pc;
 }
 
 struct PyRowArgs {
@@ -776,18 +745,28 @@ SMD void plain4_finish(const Plain4<KS>& P, int kin, const int* ri, i64 (&pile)[
 //   PY_EMBED: R = rshift(embed.w[word], -(embed.e[word] + 16)) (:153), then the two gauges' lights
 //   PY_ADD:   R += plain(mproj) (:155-157; proj's half was added by its bank), then the two gauges' lights (or
 //             lnf's alone)
-// Both gauges share to16(R), S1, S2 and LS (:100-110); only the gain, its power and the offset differ.
+// Both gauges share to16(R), S1, S2 and LS (:100-110); only the gain, its power and the offset differ.  The two
+// lights go through their water levels and plane sums together: four barriers in all (the OR of R, S1 and S2,
+// the lights' ORs, their plane sums), each with LDS slots of its own, and the gains and offsets are requested
+// with the row.
 template <int MODE>
 __global__ __launch_bounds__(192) void k_py_rows(PyRowArgs a) {
     constexpr int NT = 192, NW = NT / 64;
-    __shared__ int red[24 + 6 * 12];
+    __shared__ int red[NW * (2 + 3 + 4 + 6)];      // OR(R) | S1, S2 | OR of the two lights | their plane sums
+    int* const rOR = red;
+    int* const rS = red + 2 * NW;
+    int* const rLO = red + 5 * NW;
+    int* const rLS = red + 9 * NW;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, r = blockIdx.x;
     const int pm = a.rowmap ? a.rowmap[r] : 0;
     const int p = a.rowmap ? pm & 0xFFFF : *a.pos, st = a.rowmap ? pm >> 16 : r;
     const bool rec = r == 0 && a.rec_pos && *a.rec_pos == p;
+    const bool two = a.ng2 != nullptr;             // uniform
     // the stream row (192 threads hold four lanes each)
     const int k = 4 * tid;
     i64 R4[4] = {0, 0, 0, 0};
+    int gn[2][4];
+    i64 gb[2][4];
     {
         if (MODE == PY_EMBED) {
             const i64 tok = a.seq[(size_t)st * a.seq_stride + p];
@@ -804,6 +783,16 @@ __global__ __launch_bounds__(192) void k_py_rows(PyRowArgs a) {
             const i64 rr[4] = {r01[0], r01[1], r23[0], r23[1]};
             int rim[8];
             slice_facts<4>(a.sfactsM, a.rows, r, rim);
+            // the gains and offsets (they depend on nothing here)
+#pragma unroll
+            for (int gi = 0; gi < 2; gi++) {
+                const int* ng = gi ? (two ? a.ng2 : a.ng1) : a.ng1;
+                const i64* nb = gi ? (two ? a.nb2 : a.nb1) : a.nb1;
+                const v4l_p g4 = *reinterpret_cast<const v4l_p*>(ng + k);
+                const v2q_p b01 = *reinterpret_cast<const v2q_p*>(nb + k), b23 = *reinterpret_cast<const v2q_p*>(nb + k + 2);
+                gn[gi][0] = g4[0]; gn[gi][1] = g4[1]; gn[gi][2] = g4[2]; gn[gi][3] = g4[3];
+                gb[gi][0] = b01[0]; gb[gi][1] = b01[1]; gb[gi][2] = b23[0]; gb[gi][3] = b23[1];
+            }
             plain4_finish<4>(PM, a.kinM, rim, pM, yM);
 #pragma unroll
             for (int j = 0; j < 4; j++) {
@@ -814,6 +803,15 @@ __global__ __launch_bounds__(192) void k_py_rows(PyRowArgs a) {
                 }
             }
         }
+        if (MODE == PY_EMBED) {
+#pragma unroll
+            for (int gi = 0; gi < 2; gi++) {
+                const int* ng = gi ? (two ? a.ng2 : a.ng1) : a.ng1;
+                const i64* nb = gi ? (two ? a.nb2 : a.nb1) : a.nb1;
+#pragma unroll
+                for (int j = 0; j < 4; j++) { gn[gi][j] = ng[k + j]; gb[gi][j] = nb[k + j]; }
+            }
+        }
 #pragma unroll
         for (int j = 0; j < 4; j++) a.R[(size_t)r * 768 + k + j] = R4[j];
     }
@@ -822,11 +820,11 @@ __global__ __launch_bounds__(192) void k_py_rows(PyRowArgs a) {
 #pragma unroll
     for (int j = 0; j < 4; j++) o |= (u64)iabs64(R4[j]);
     unsigned olo = wave_or32((unsigned)o), ohi = wave_or32((unsigned)(o >> 32));
-    if (lane == 0) { red[2 * wave] = (int)olo; red[2 * wave + 1] = (int)ohi; }
+    if (lane == 0) { rOR[2 * wave] = (int)olo; rOR[2 * wave + 1] = (int)ohi; }
     __syncthreads();
     u64 all = 0;
 #pragma unroll
-    for (int w = 0; w < NW; w++) all |= ((u64)(unsigned)red[2 * w + 1] << 32) | (unsigned)red[2 * w];
+    for (int w = 0; w < NW; w++) all |= ((u64)(unsigned)rOR[2 * w + 1] << 32) | (unsigned)rOR[2 * w];
     const int sh = water_shift((i64)all);
     int x[4];
     int s1 = 0;
@@ -838,31 +836,62 @@ __global__ __launch_bounds__(192) void k_py_rows(PyRowArgs a) {
         s2 += (i64)x[j] * x[j];
     }
     const int w1 = wave_add32(s1), w2h = wave_add32((int)(s2 >> 16)), w2l = wave_add32((int)(s2 & 0xFFFF));
-    if (lane == 0) { red[24 + 3 * wave] = w1; red[25 + 3 * wave] = w2h; red[26 + 3 * wave] = w2l; }
+    if (lane == 0) { rS[3 * wave] = w1; rS[3 * wave + 1] = w2h; rS[3 * wave + 2] = w2l; }
     __syncthreads();
     i64 S1 = 0, S2h = 0, S2l = 0;
 #pragma unroll
-    for (int w = 0; w < NW; w++) { S1 += red[24 + 3 * w]; S2h += red[25 + 3 * w]; S2l += red[26 + 3 * w]; }
+    for (int w = 0; w < NW; w++) { S1 += rS[3 * w]; S2h += rS[3 * w + 1]; S2l += rS[3 * w + 2]; }
     i64 e2;
     const i64 ls = pgauge_ls_pow(S1, (S2h << 16) + S2l, -16 + sh, a.tb, e2);
-    __syncthreads();                                    // red is reused below
-    for (int gi = 0; gi < 2; gi++) {
-        const int* ng = gi ? a.ng2 : a.ng1;
-        if (!ng) break;
-        const i64* nb = gi ? a.nb2 : a.nb1;
-        const i64 sg = wsub(16, wsub(wmul((i64)(gi ? a.nge2 : a.nge1) + 16, 65536), ls) >> 16);
-        i64 v[1][4] = {{0, 0, 0, 0}};
-        {
+    // the two gauged rows (:109-110): rshift((768 x - S1) g e2, sg) + offset
+    i64 v[2][4];
+    u64 og[2] = {0, 0};
 #pragma unroll
-            for (int j = 0; j < 4; j++) {
-                const i64 c = 768 * (i64)x[j] - S1;
-                v[0][j] = wadd(rsh(wmul(c * ng[k + j], e2), sg), nb[k + j]);
-                i64* rg = gi ? a.rg2 : a.rg1;
-                if (rec && rg) rg[k + j] = v[0][j];
-            }
+    for (int gi = 0; gi < 2; gi++) {
+        const i64 sg = wsub(16, wsub(wmul((i64)(gi && two ? a.nge2 : a.nge1) + 16, 65536), ls) >> 16);
+        i64* rg = gi ? a.rg2 : a.rg1;
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const i64 c = 768 * (i64)x[j] - S1;
+            v[gi][j] = wadd(rsh(wmul(c * gn[gi][j], e2), sg), gb[gi][j]);
+            if (rec && rg && (gi == 0 || two)) rg[k + j] = v[gi][j];
+            og[gi] |= (u64)iabs64(v[gi][j]);
         }
-        light_store<768, NT>(v, r, gi ? a.planes2 : a.planes1, gi ? a.rowinfo2 : a.rowinfo1, red, rec,
-                         gi ? a.rx2 : a.rx1, gi ? a.rex2 : a.rex1);
+    }
+    // their water levels
+#pragma unroll
+    for (int gi = 0; gi < 2; gi++) {
+        const unsigned lo = wave_or32((unsigned)og[gi]), hi = wave_or32((unsigned)(og[gi] >> 32));
+        if (lane == 0) { rLO[4 * wave + 2 * gi] = (int)lo; rLO[4 * wave + 2 * gi + 1] = (int)hi; }
+    }
+    __syncthreads();
+    int shg[2], fs[2][3];
+#pragma unroll
+    for (int gi = 0; gi < 2; gi++) {
+        u64 ag = 0;
+#pragma unroll
+        for (int w = 0; w < NW; w++) ag |= ((u64)(unsigned)rLO[4 * w + 2 * gi + 1] << 32) | (unsigned)rLO[4 * w + 2 * gi];
+        shg[gi] = water_shift((i64)ag);
+        fs[gi][0] = fs[gi][1] = fs[gi][2] = 0;
+        if (gi == 0 || two)
+            planes4<768>(v[gi], shg[gi], r, k, gi ? a.planes2 : a.planes1, rec, gi ? a.rx2 : a.rx1, fs[gi][0],
+                         fs[gi][1], fs[gi][2]);
+    }
+    // their plane sums
+#pragma unroll
+    for (int gi = 0; gi < 2; gi++) {
+        const int w3 = wave_add32(fs[gi][0]), w4 = wave_add32(fs[gi][1]), w5 = wave_add32(fs[gi][2]);
+        if (lane == 0) { int* q = rLS + 6 * wave + 3 * gi; q[0] = w3; q[1] = w4; q[2] = w5; }
+    }
+    __syncthreads();
+    if (tid < 2 && (tid == 0 || two)) {
+        const int gi = tid;
+        int SXh = 0, SXl = 0, N32 = 0;
+        for (int w = 0; w < NW; w++) { const int* q = rLS + 6 * w + 3 * gi; SXh += q[0]; SXl += q[1]; N32 += q[2]; }
+        int* ri = (gi ? a.rowinfo2 : a.rowinfo1) + (size_t)r * 8;
+        ri[0] = -16 + shg[gi]; ri[1] = 0; ri[2] = 0; ri[3] = 0; ri[4] = SXh; ri[5] = SXl; ri[6] = N32;
+        i64* rex = gi ? a.rex2 : a.rex1;
+        if (rec && rex) { rex[0] = -16 + shg[gi]; rex[1] = 0; }
     }
 }
 
