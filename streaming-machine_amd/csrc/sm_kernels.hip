@@ -533,7 +533,9 @@ SMD void attend_short(const AttArgs& a, int p, int h, int b, int* q_s, int* w_s)
 // power(q16 . k16, (eq + ek + 10) 65536 - half); the final power exact in 128 bits (the reference's power never
 // wraps, :81-85); its asserts (turn input < 2^31, max|v| sum(a) < 2^62, a result that fits) set SM_ERR_RANGE.
 #define ACH 64
-#define ATT_PRE 2            // passes of 64 positions whose keys and values are requested at launch
+template <bool B> struct Flag { static constexpr bool value = B; };
+#define ATT_PRE 2            // passes of 64 positions whose keys and values are requested at launch (the ring
+                             // of key slots the scores loop refills two passes ahead)
 // ONE = 1: one stream (the short-context path is available, full registers); ONE = 0: many streams, three waves
 // a SIMD so that 768 blocks are resident at once
 template <int MODEL, int ONE>
@@ -575,6 +577,7 @@ __global__ __launch_bounds__(NTHR, ONE ? 1 : 3) void k_attend(AttArgs a) {
     // (buffer loads bounded at position p: rows past it read zeros and cost no memory traffic)
     const __amdgpu_buffer_rsrc_t rk = buf_rsrc(K16, (unsigned)p * 256), re = buf_rsrc(EK, (unsigned)p * 4),
                                  rv = buf_rsrc(V, (unsigned)p * 256);
+    static_assert(ATT_PRE == 2, "the scores loop refills a ring of two key slots");
     v4i kp[ATT_PRE][4];
     int ekp[ATT_PRE];
 #pragma unroll
@@ -634,30 +637,19 @@ __global__ __launch_bounds__(NTHR, ONE ? 1 : 3) void k_attend(AttArgs a) {
         return MODEL == 1 ? rsh(wmul(dot, a.ehalf), wsub(16, wsub(wmul(eq + ek + 10, 65536), a.half) >> 16))
                           : rsh(dot, -(eq + ek + 7));
     };
+    // passes of 64 positions.  Below 128 positions both passes' keys were requested at launch; beyond, two
+    // passes at a time, each pass's keys requested two passes earlier into the register slot it frees (rows past
+    // p read zeros and cost no memory traffic).  The two cases are separate code, so that each has exact waits.
     i64 mx = INT64_MIN;
-    for (int s0 = 0; s0 <= p; s0 += ACH) {
+    auto pass = [&](auto refill, int s0, v4i (&kk0)[4], int& ek0) {
         const int s = s0 + sl;
-        const int c = s0 / ACH;
-        i64 dot = 0, ek = 0;
+        i64 dot = 0, ek = ek0;
         v4i kk[4];
-        if (s < p) {
-            if (c < ATT_PRE) {
 #pragma unroll
-                for (int cc = 0; cc < ATT_PRE; cc++)
-                    if (cc == c) {
+        for (int u = 0; u < 4; u++) kk[u] = kk0[u];
+        if (s == p) {                                      // the new key
 #pragma unroll
-                        for (int u = 0; u < 4; u++) kk[u] = kp[cc][u];
-                        ek = ekp[cc];
-                    }
-            } else {
-                const v4i* kr = reinterpret_cast<const v4i*>(K16 + (size_t)s * 64) + qd;
-#pragma unroll
-                for (int u = 0; u < 4; u++) kk[u] = kr[4 * u];
-                ek = EK[s];
-            }
-        } else {
-#pragma unroll
-            for (int u = 0; u < 4; u++) kk[u] = reinterpret_cast<const v4i*>(k16s)[4 * u + qd];   // s == p: the new key
+            for (int u = 0; u < 4; u++) kk[u] = reinterpret_cast<const v4i*>(k16s)[4 * u + qd];
             ek = eks;
         }
         if (s <= p) {
@@ -671,6 +663,22 @@ __global__ __launch_bounds__(NTHR, ONE ? 1 : 3) void k_attend(AttArgs a) {
             const i64 v = score(dot, ek);
             if (qd == 0) sc[s] = v;
             mx = v > mx ? v : mx;
+        }
+        if constexpr (decltype(refill)::value) {          // the pass two ahead
+            const unsigned sr = s0 + 2 * ACH + sl;
+#pragma unroll
+            for (int u = 0; u < 4; u++) kk0[u] = buf_load4(rk, sr * 256 + (4 * u + qd) * 16);
+            ek0 = buf_load1(re, sr * 4);
+        }
+    };
+    const bool longc = p >= 2 * ACH;                       // uniform
+    if (!longc) {
+        pass(Flag<false>{}, 0, kp[0], ekp[0]);
+        if (ACH <= p) pass(Flag<false>{}, ACH, kp[1], ekp[1]);
+    } else {
+        for (int s0 = 0; s0 <= p; s0 += 2 * ACH) {
+            pass(Flag<true>{}, s0, kp[0], ekp[0]);
+            if (s0 + ACH <= p) pass(Flag<true>{}, s0 + ACH, kp[1], ekp[1]);
         }
     }
     mx = block_reduce(mx, red, OpMax(), tid);   // its barriers also publish sc[]
@@ -691,14 +699,26 @@ __global__ __launch_bounds__(NTHR, ONE ? 1 : 3) void k_attend(AttArgs a) {
         n0 += (i64)w * x.x; n1 += (i64)w * x.y; n2 += (i64)w * x.z; n3 += (i64)w * x.w;
         if (MODEL == 1 && w) vmax = max(vmax, max(max(abs(x.x), abs(x.y)), max(abs(x.z), abs(x.w))));
     };
+    // below 128 positions every value was requested after the new position came in; beyond, chunks of 16 NV
+    // positions, each value requested one chunk earlier into the register slot it frees
+    if (!longc) {
 #pragma unroll
-    for (int i = 0; i < NV; i++) {
-        const int sv = g + 16 * i;
-        if (16 * i > p) break;                  // uniform
-        if (sv < p) acc(arr[sv], vp[i]);
+        for (int i = 0; i < NV; i++) {
+            const int sv = g + 16 * i;
+            if (16 * i > p) break;                  // uniform
+            if (sv < p) acc(arr[sv], vp[i]);
+        }
+    } else {
+        for (int base = 0; base < p; base += 16 * NV) {
+#pragma unroll
+            for (int i = 0; i < NV; i++) {
+                const int sv = base + g + 16 * i;
+                const v4i x = vp[i];
+                vp[i] = buf_load4(rv, (unsigned)(sv + 16 * NV) * 256 + d4 * 16);
+                if (sv < p) acc(arr[sv], x);
+            }
+        }
     }
-    for (int sv = g + 16 * NV; sv < p; sv += 16)                 // past the requested positions
-        acc(arr[sv], reinterpret_cast<const v4i*>(V + (size_t)sv * 64)[d4]);
     if ((p & 15) == g) acc(arr[p], reinterpret_cast<const v4i*>(vs)[d4]);   // the new position (from LDS)
     if (MODEL == 1 && (double)vmax * (double)z >= 4611686018427387904.0) atomicOr(a.err, SM_ERR_RANGE);
     // the 16 position groups through LDS, summed by wave 0
