@@ -537,10 +537,11 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs a) {
 // tile, which every block shares, so it stays in cache.  Each lane keeps, per row, the best of the columns it
 // held (ties to the lowest); one 16-lane reduction per row at the end gives the block's part.
 template <int RT, int EPI>
-__global__ __launch_bounds__(256) void k_head_rows(GemmArgs a) {
+__global__ __launch_bounds__(256, 2) void k_head_rows(GemmArgs a) {     // two blocks a CU
     constexpr int K = 768, KS = K / 64, TV = KS * 128, PER = TV / 256;   // v4 per tile, per thread
     typedef int v4 __attribute__((ext_vector_type(4)));
     __shared__ v4 ws[2][TV];
+    __shared__ v4 wf[2][16][2];       // the tile's column facts: SWh, SWl, we, -; bias lo, hi, -, -
     __shared__ int rinfo[64 * 8];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int p = a.pos ? *a.pos : 0;
@@ -549,12 +550,25 @@ __global__ __launch_bounds__(256) void k_head_rows(GemmArgs a) {
     v4 gf = {0, 0, 0, 0};          // EPI_HEAD: row tid's light facts, before the weight stream
     if (EPI == EPI_HEAD) gf = *reinterpret_cast<const v4*>(a.rowinfo + (size_t)(tid < a.rows ? tid : 0) * 8);
     const v4* Wg = reinterpret_cast<const v4*>(a.W) + tid;
-    auto gfetch = [&](v4 (&r)[PER], int tile) {
-        const v4* src = Wg + (size_t)min(tile, ntiles - 1) * TV;
+    // a tile's weights, and (threads 0-15) the facts of its column tid: rows of the slot r, refilled in place
+    // (a copy of registers in flight would wait for every load: loads complete in order); threads past 15 read
+    // the facts' zeros past the buffers' ends, with no branch and no memory request
+    const __amdgpu_buffer_rsrc_t rcs = buf_rsrc(a.csum, (unsigned)a.N * 8u), rwe = buf_rsrc(a.we, (unsigned)a.N * 4u),
+                                 rbi = buf_rsrc(EPI == EPI_HEAD ? (const void*)a.bias : (const void*)a.we,
+                                                EPI == EPI_HEAD ? (unsigned)a.N * 8u : 0u);
+    auto gfetch = [&](v4 (&r)[PER + 2], int tile) {
+        const int tt = min(tile, ntiles - 1);
+        const v4* src = Wg + (size_t)tt * TV;
 #pragma unroll
         for (int i = 0; i < PER; i++) r[i] = __builtin_nontemporal_load(src + i * 256);
+        const unsigned j = tid < 16 ? (unsigned)(tt * 16 + tid) : 0x10000000u;
+        const u64 cs = __builtin_bit_cast(u64, __builtin_amdgcn_raw_buffer_load_b64(rcs, (int)(j * 8u), 0, 0));
+        const int we = (int)__builtin_amdgcn_raw_buffer_load_b32(rwe, (int)(j * 4u), 0, 0);
+        const u64 bi = __builtin_bit_cast(u64, __builtin_amdgcn_raw_buffer_load_b64(rbi, (int)(j * 8u), 0, 0));
+        r[PER] = v4{(int)(unsigned)cs, (int)(unsigned)(cs >> 32), we, 0};
+        r[PER + 1] = v4{(int)(unsigned)bi, (int)(unsigned)(bi >> 32), 0, 0};
     };
-    v4 r0[PER], r1[PER];
+    v4 r0[PER + 2], r1[PER + 2];
     gfetch(r0, blockIdx.x);
     gfetch(r1, blockIdx.x + G);
     // this wave's row tile (waves past the last row tile only help to stage)
@@ -580,7 +594,7 @@ __global__ __launch_bounds__(256) void k_head_rows(GemmArgs a) {
     int bi[4];
 #pragma unroll
     for (int q = 0; q < 4; q++) { bv[q] = 0; bi[q] = -1; }
-    auto compute = [&](const v4* w, int tile) {
+    auto compute = [&](const v4* w, const v4 (*wfs)[2], int tile) {
         if (!live) return;
         v4 hh = {0, 0, 0, 0}, mid = {0, 0, 0, 0}, ll = {0, 0, 0, 0};
 #pragma unroll
@@ -598,8 +612,9 @@ __global__ __launch_bounds__(256) void k_head_rows(GemmArgs a) {
         }
         const int j = tile * 16 + (lane & 15);
         if (j >= a.N) return;
-        const i64 swh = a.csum[2 * j], swl = a.csum[2 * j + 1];
-        const i64 we = a.we[j], bc = EPI == EPI_HEAD ? a.bias[j] : 0;
+        const v4 f0 = wfs[lane & 15][0], f1 = wfs[lane & 15][1];
+        const i64 swh = f0[0], swl = f0[1], we = f0[2];
+        const i64 bc = (i64)(((u64)(unsigned)f1[1] << 32) | (unsigned)f1[0]);
 #pragma unroll
         for (int q = 0; q < 4; q++) {
             const int row = 16 * t + 4 * (lane >> 4) + q;
@@ -623,16 +638,17 @@ __global__ __launch_bounds__(256) void k_head_rows(GemmArgs a) {
     for (int tile = blockIdx.x; tile < ntiles;) {
 #pragma unroll
         for (int i = 0; i < PER; i++) ws[0][tid + i * 256] = r0[i];
+        if (tid < 16) { wf[0][tid][0] = r0[PER]; wf[0][tid][1] = r0[PER + 1]; }
         gfetch(r0, tile + 2 * G);
         __syncthreads();
-        compute(ws[0], tile);
-        tile += G;
-        if (tile >= ntiles) break;
+        compute(ws[0], wf[0], tile);
+        tile += G;                                   // (a tile past the end computes nothing)
 #pragma unroll
         for (int i = 0; i < PER; i++) ws[1][tid + i * 256] = r1[i];
+        if (tid < 16) { wf[1][tid][0] = r1[PER]; wf[1][tid][1] = r1[PER + 1]; }
         gfetch(r1, tile + 2 * G);
         __syncthreads();
-        compute(ws[1], tile);
+        compute(ws[1], wf[1], tile);
         tile += G;
     }
     if ((EPI != EPI_HEAD && EPI != EPI_PHEAD) || !live) return;
