@@ -158,6 +158,14 @@ int sm_plate_product(const sm_plate* p, const int64_t* x16, int64_t* pile, int32
  * contraction (base2.py:29-32 for every row of a batch).  x16: device int64 [rows][nin] in [-32768, 32768];
  * pile: device int64 [rows][nout].  Calls on one plate share its light planes: serialise them. */
 int sm_plate_product_rows(const sm_plate* p, const int64_t* x16, int32_t rows, int64_t* pile, void* stream);
+/* The same product for a bank that forms its light from the producing phase's rows, as the batched machine's
+ * proj and mproj do: pile[r][j] = sum_i to16(X[r])[i] w[i][j] (base2.py:24-27, then :29-32).  X: device int64
+ * [rows][nin]; orw: device int64 [rows][12] (nin 768: one word per 64-value part, the attention's heads) or
+ * [rows][192] (nin 3072: one per 16-value part, fc's column tiles), each the OR of |x| over its part (their OR is
+ * the row's water level); pile: device int64 [rows][nout].  nout a multiple of 16 and at most 3072 (nin 768) or
+ * a multiple of 48 (nin 3072); rows 1..64.  Calls on one plate share its scratch: serialise them. */
+int sm_plate_product_rows_from(const sm_plate* p, const int64_t* X, const int64_t* orw, int32_t rows,
+                               int64_t* pile, void* stream);
 /* bytes of the device plate (for bandwidth accounting) */
 int64_t sm_plate_bytes(const sm_plate* p);
 

@@ -961,6 +961,27 @@ __global__ __launch_bounds__(256) void k_race_rows(RaceArgs a) {
     }
 }
 
+// The piles of a K-sliced bank whose blocks formed their light themselves (the stage product's finisher): the
+// slices' accumulators and plane sums with the column sums, by the pile identity at the top of this file.
+template <int KSP>
+__global__ __launch_bounds__(256) void k_part_piles(GemmArgs a) {
+    const int r = blockIdx.y;
+    int ri[8];
+    slice_facts<KSP>(a.sfacts, a.rows, r, ri);
+    for (int j = blockIdx.x * 256 + threadIdx.x; j < a.N; j += gridDim.x * 256) {
+        int hh = 0, mid = 0, ll = 0;                 // (as the machine's finisher sums them: each below 2^28)
+#pragma unroll
+        for (int q = 0; q < KSP; q++) {
+            const int* src = a.part + ((size_t)q * 3 * a.rows + r) * a.N + j;
+            hh += src[0];
+            mid += src[(size_t)a.rows * a.N];
+            ll += src[(size_t)2 * a.rows * a.N];
+        }
+        a.Y[(size_t)r * a.ystride + j] = 65536 * (i64)hh + 256 * (i64)mid + ll + 32768 * ((i64)ri[4] + a.csum[2 * j]) +
+                                         128 * ((i64)ri[5] + a.csum[2 * j + 1]) + 16384 * (i64)a.K + 128 * (i64)ri[6];
+    }
+}
+
 #define BINST_L(K, PRO, KSP) template __global__ void k_light<K, PRO, (K) / 4, KSP>(LightArgs);
 BINST_L(768, PRO_EMBED, 1)
 BINST_L(768, PRO_GAUGE, 1)
@@ -976,6 +997,8 @@ template __global__ void k_py_rows<PY_ADD>(PyRowArgs);
     BINST_G(768, RT, 1, EPI_PART) BINST_G(768, RT, 1, EPI_PLAIN_EDGE) BINST_G(3072, RT, 4, EPI_PART) \
     BINST_G(768, RT, 1, EPI_PILE) BINST_G(3072, RT, 1, EPI_PILE) BINST_G(768, RT, 1, EPI_PLAIN)
 BINST_GR(1)
+template __global__ void k_gemm<768, 1, 1, EPI_PILE, 12>(GemmArgs);
+template __global__ void k_part_piles<4>(GemmArgs);
 #define BINST_H(RT) template __global__ void k_head_rows<RT, EPI_HEAD>(GemmArgs); \
     template __global__ void k_head_rows<RT, EPI_PILE>(GemmArgs); template __global__ void k_head_rows<RT, EPI_PHEAD>(GemmArgs);
 BINST_H(1)

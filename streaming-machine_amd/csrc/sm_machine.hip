@@ -1315,12 +1315,14 @@ struct sm_plate {
     bool mfma = false;
     signed char* planes = nullptr;
     int* rowinfo = nullptr;
+    int* part = nullptr;       // nin 3072: the K slices' accumulators and light facts (sm_plate_product_rows_from)
+    int* sfacts = nullptr;
 };
 
 static void plate_free(sm_plate* p) {
     free_plate(p->P);
     free_mfma_plate(p->M);
-    hfree(p->planes); hfree(p->rowinfo);
+    hfree(p->planes); hfree(p->rowinfo); hfree(p->part); hfree(p->sfacts);
     delete p;
 }
 
@@ -1336,7 +1338,9 @@ extern "C" int sm_plate_create(const int16_t* w, const int32_t* e, const int64_t
         p->mfma = true;
         const size_t pb = (size_t)4 * (nin / 64) * 3 * 1024;
         if ((rc = upload_mfma_plate(p->M, w, e, (const i64*)b, nin, nout)) || (rc = dalloc(&p->planes, pb)) ||
-            (rc = dalloc(&p->rowinfo, (size_t)64 * 8))) {
+            (rc = dalloc(&p->rowinfo, (size_t)64 * 8)) ||
+            (nin == 3072 && ((rc = dalloc(&p->part, (size_t)4 * 3 * 64 * (size_t)p->M.ntiles * 16)) ||
+                             (rc = dalloc(&p->sfacts, (size_t)4 * 64 * 4))))) {
             plate_free(p);
             return rc;
         }
@@ -1391,6 +1395,33 @@ extern "C" int sm_plate_product_rows(const sm_plate* p, const int64_t* x16, int3
     else if (RT == 2) rows_product<2>(p, x16, rows, pile, s);
     else if (RT == 3) rows_product<3>(p, x16, rows, pile, s);
     else rows_product<4>(p, x16, rows, pile, s);
+    HIP_TRY(hipGetLastError());
+    return SM_OK;
+}
+
+// the machine's proj (nin 768: one block a column tile, the light from 12 OR words a row) and mproj (nin 3072:
+// three column tiles a block, four K slices, 192 OR words a row) on the caller's rows
+extern "C" int sm_plate_product_rows_from(const sm_plate* p, const int64_t* X, const int64_t* orw, int32_t rows,
+                                          int64_t* pile, void* stream) {
+    if (!p || !X || !orw || !pile) return fail(SM_E_ARG, "sm_plate_product_rows_from: null argument");
+    if (!p->mfma) return fail(SM_E_ARG, "sm_plate_product_rows_from: the plate was made for the GEMV (tile_cols > 0)");
+    if (rows < 1 || rows > 64) return fail(SM_E_ARG, "sm_plate_product_rows_from: rows must be in [1, 64]");
+    const MfmaPlate& P = p->M;
+    if (P.N % 16 != 0 || (P.K == 3072 && P.ntiles % 3 != 0) || (P.K == 768 && P.N > 3072))
+        return fail(SM_E_ARG, "sm_plate_product_rows_from: nout must be a multiple of 16 (nin 768, at most 3072) or 48 (nin 3072)");
+    hipStream_t s = (hipStream_t)stream;
+    const int RT = (rows + 15) / 16;
+    GemmArgs ga{};
+    ga.K = P.K; ga.N = P.N; ga.rows = rows; ga.RT = RT; ga.W = P.W; ga.csum = P.csum; ga.we = P.e; ga.bias = P.b;
+    ga.Y = (i64*)pile; ga.ystride = P.N;
+    ga.X = (const i64*)X; ga.xstride = P.K; ga.orw = (const i64*)orw;
+    if (P.K == 768) {
+        k_gemm<768, 1, 1, EPI_PILE, 12><<<dim3(P.ntiles, RT), 256, 0, s>>>(ga);
+    } else {
+        ga.part = p->part; ga.sfacts = p->sfacts;
+        k_gemm<3072, 3, 4, EPI_PART, 192><<<dim3(P.ntiles / 3 * 4, RT), 256, 0, s>>>(ga);
+        k_part_piles<4><<<dim3((P.N + 255) / 256, rows), 256, 0, s>>>(ga);
+    }
     HIP_TRY(hipGetLastError());
     return SM_OK;
 }

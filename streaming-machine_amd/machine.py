@@ -73,6 +73,7 @@ def lib():
         L.sm_plate_destroy.argtypes = [vp]
         L.sm_plate_product.argtypes = [vp, vp, vp, i32, vp]
         L.sm_plate_product_rows.argtypes = [vp, vp, i32, vp, vp]
+        L.sm_plate_product_rows_from.argtypes = [vp, vp, vp, i32, vp, vp]
         L.sm_plate_bytes.restype = i64
         L.sm_plate_bytes.argtypes = [vp]
         _LIB = L
@@ -229,6 +230,10 @@ class Plate:
 
     def product_rows(self, x16_ptr: int, rows: int, pile_ptr: int, stream: int = 0):
         check(self.L.sm_plate_product_rows(self.h, x16_ptr, rows, pile_ptr, stream))
+
+    def product_rows_from(self, x_ptr: int, orw_ptr: int, rows: int, pile_ptr: int, stream: int = 0):
+        """the light formed in the bank from int64 rows and their OR words (12 a row for nin 768, 192 for 3072)"""
+        check(self.L.sm_plate_product_rows_from(self.h, x_ptr, orw_ptr, rows, pile_ptr, stream))
 
     def close(self):
         if getattr(self, "h", None):

@@ -67,6 +67,58 @@ def test_rows_product(sm, nin, nout):
     plate.close()
 
 
+def producer_rows(rng, rows, nin, nparts):
+    """int64 rows as a producing phase leaves them, each with its own water level (shift 0 .. 40), lights at the
+    byte split's edges after the shift (values that round up to +32768, down to -32768, to 32767), planted at
+    different k so that different waves' steps hold them, and the OR words of the rows' nparts equal parts"""
+    shifts = [1, 0, 7, 20, 40, 3, 12]
+    X = np.zeros((rows, nin), np.int64)
+    for r in range(rows):
+        sh = shifts[r % len(shifts)]
+        top = 1 << (15 + sh)                          # |x| < top: the water level stays at sh
+        X[r] = rng.integers(-(top - 1), top, nin, dtype=np.int64)
+        if sh >= 1 and not 16 <= r < 32:
+            half = 1 << (sh - 1)
+            k = (r * 97) % nin
+            X[r, k] = top - half                      # +32768
+            X[r, (k + 1) % nin] = -top + half - 1     # -32768
+            X[r, (k + nin // 2) % nin] = top - half   # +32768 in another wave's steps
+            X[r, (k + 5) % nin] = top - 3 * half      # 32767
+    parts = np.abs(X).reshape(rows, nparts, nin // nparts)
+    orw = np.bitwise_or.reduce(parts, axis=2).astype(np.int64)
+    return X, orw
+
+
+@pytest.fixture(scope="module")
+def orc(sm):
+    import oracle
+    return oracle.Stages(sm.tables())
+
+
+@pytest.mark.parametrize("nin,nout", [(768, 768), (768, 2304), (3072, 768)])
+def test_rows_product_from_producer_rows(sm, orc, nin, nout):
+    """the light formed inside the bank (the machine's proj and mproj) from int64 rows and their OR words: the
+    piles equal the exact product of the oracle's lights, +32768 corrections included, for 1..64 rows"""
+    rng = np.random.default_rng(11)
+    w = rng.integers(-32768, 32768, (nin, nout)).astype(np.int16)
+    w[:, 1] = -32768
+    w[:, 2] = 32767
+    e = rng.integers(-16, -7, nout).astype(np.int32)
+    b = np.zeros(nout, np.int64)
+    nparts = 12 if nin == 768 else 192
+    X, orw = producer_rows(rng, 64, nin, nparts)
+    x16, _ = orc.to16(X)
+    assert (x16 == 32768).any(axis=1).sum() >= 30 and (x16 == -32768).any()
+    want = exact_rows(x16, w)
+    plate = sm.Plate(w, e, b, tile_cols=0)
+    dX, dorw = dev(X), dev(orw)
+    for rows in (64, 1, 17, 40):
+        dp = torch.full((rows, nout), -7, dtype=torch.int64, device="cuda")
+        plate.product_rows_from(dX.data_ptr(), dorw.data_ptr(), rows, dp.data_ptr())
+        assert np.array_equal(host(dp), want[:rows]), f"rows={rows}"
+    plate.close()
+
+
 def test_rows_product_rejects(sm):
     w = np.zeros((768, 32), np.int16)
     e = np.zeros(32, np.int32)
@@ -80,6 +132,10 @@ def test_rows_product_rejects(sm):
         assert err.value.code == -1
     with pytest.raises(sm.SmError):
         rows_plate.product(x.data_ptr(), p.data_ptr())
+    for plate, rows in ((rows_plate, 65), (rows_plate, 0), (gemv_plate, 1)):
+        with pytest.raises(sm.SmError) as err:
+            plate.product_rows_from(x.data_ptr(), x.data_ptr(), rows, p.data_ptr())
+        assert err.value.code == -1
     rows_plate.close()
     gemv_plate.close()
 
