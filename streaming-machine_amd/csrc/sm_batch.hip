@@ -35,6 +35,8 @@ struct LightArgs {
     i64* rpile_in; i64* rout_in;                  // stream 0's record of the producing bank
     const int* sfacts;                            // its K slices' light facts [KSP][rows][4]: SXh, SXl, n32768, ex
     const int* rowmap;                            // prompt rows (PRO_EMBED): stream << 16 | position per row
+    int ls_row;                                   // gauged: slots 1-3 carry LS lo, LS hi and EXP2[-LS & 0xFFFF]
+                                                  // in place of S1, S2 (the head's light)
 };
 
 struct GemmArgs {
@@ -216,6 +218,11 @@ __global__ __launch_bounds__(NT) void k_light(LightArgs a) {
         const i64 S2 = (S2h << 16) + S2l;
         int* ri = a.rowinfo + (size_t)r * 8;
         ri[0] = (int)ex; ri[1] = (int)S1; ri[2] = (int)(u64)S2; ri[3] = (int)((u64)S2 >> 32);
+        if (a.ls_row) {
+            i64 e2;
+            const i64 ls = gauge_ls_pow(S1, S2, ex, a.tb, e2);
+            ri[1] = (int)(u64)ls; ri[2] = (int)((u64)ls >> 32); ri[3] = (int)e2;
+        }
         ri[4] = (int)SXh; ri[5] = (int)SXl; ri[6] = (int)N32;
         if (rec && a.rexls) {
             i64 e2;
@@ -542,13 +549,20 @@ __global__ __launch_bounds__(256, 2) void k_head_rows(GemmArgs a) {     // two b
     typedef int v4 __attribute__((ext_vector_type(4)));
     __shared__ v4 ws[2][TV];
     __shared__ v4 wf[2][16][2];       // the tile's column facts: SWh, SWl, we, -; bias lo, hi, -, -
-    __shared__ int rinfo[64 * 8];
+    __shared__ i64 rc[64][3];         // per row: the pile's row terms, the power's row part, its factor
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int p = a.pos ? *a.pos : 0;
     if ((EPI == EPI_HEAD || EPI == EPI_PHEAD) && p < *a.plen - 1) return;
     const int ntiles = (a.N + 15) >> 4, G = gridDim.x;
-    v4 gf = {0, 0, 0, 0};          // EPI_HEAD: row tid's light facts, before the weight stream
-    if (EPI == EPI_HEAD) gf = *reinterpret_cast<const v4*>(a.rowinfo + (size_t)(tid < a.rows ? tid : 0) * 8);
+    // the row facts first (row tid): ex, LS, the power factor (EPI_HEAD: the producing light kernel turned S1, S2
+    // into LS and EXP2[-LS & 0xFFFF]), the plane sums; then the first tile, the light planes, the second tile, so
+    // that the first tile waits for nothing behind it (loads complete in order)
+    v4 rf0 = {0, 0, 0, 0}, rf1 = {0, 0, 0, 0};
+    if (tid < a.rows) {
+        rf0 = *reinterpret_cast<const v4*>(a.rowinfo + (size_t)tid * 8);
+        rf1 = *reinterpret_cast<const v4*>(a.rowinfo + (size_t)tid * 8 + 4);
+    }
+    const int n32 = lane < a.rows ? a.rowinfo[lane * 8 + 6] : 0;    // rows 0-63 in every wave
     const v4* Wg = reinterpret_cast<const v4*>(a.W) + tid;
     // a tile's weights, and (threads 0-15) the facts of its column tid: rows of the slot r, refilled in place
     // (a copy of registers in flight would wait for every load: loads complete in order); threads past 15 read
@@ -570,25 +584,28 @@ __global__ __launch_bounds__(256, 2) void k_head_rows(GemmArgs a) {     // two b
     };
     v4 r0[PER + 2], r1[PER + 2];
     gfetch(r0, blockIdx.x);
-    gfetch(r1, blockIdx.x + G);
     // this wave's row tile (waves past the last row tile only help to stage)
     const bool live = wave < RT;
     const int t = live ? wave : 0;
-    const int n32 = lane < a.rows ? a.rowinfo[lane * 8 + 6] : 0;
-    const bool corr = live && ((__ballot(n32 != 0) >> (16 * t)) & 0xFFFFull);
     const v4* Ab = reinterpret_cast<const v4*>(a.planes) + (size_t)t * KS * 192 + lane;
     v4 xh[KS], xl[KS];
 #pragma unroll
     for (int s = 0; s < KS; s++) { xh[s] = Ab[s * 192]; xl[s] = Ab[s * 192 + 64]; }
-    // EPI_HEAD: thread r < rows turns row r's light facts into LS and the power factor (slots 1-3)
-    const bool keep1 = EPI != EPI_HEAD || (tid & 7) == 0 || (tid & 7) > 3;
-    if (tid < a.rows * 8 && keep1) rinfo[tid] = a.rowinfo[tid];
-    if (tid + 256 < a.rows * 8 && keep1) rinfo[tid + 256] = a.rowinfo[tid + 256];
-    if (EPI == EPI_HEAD && tid < a.rows) {
-        i64 e2;
-        const i64 ls = gauge_ls_pow_v(gf[1], (i64)(((u64)(unsigned)gf[3] << 32) | (unsigned)gf[2]), gf[0], a.tb, e2);
-        rinfo[tid * 8 + 1] = (int)(u64)ls; rinfo[tid * 8 + 2] = (int)((u64)ls >> 32); rinfo[tid * 8 + 3] = (int)e2;
+    gfetch(r1, blockIdx.x + G);
+    // row tid's constants: pile = 65536 HH + 256 MID + LL + C_row + 32768 SWh + 128 SWl; the gauged logit
+    // power(pile, (we + ex + 16) 65536 - LS) + b = rshift(pile e2, 16 - we - (F_row >> 16)) + b with
+    // F_row = (ex + 16) 65536 - LS (base2.py:70, 108); Pythia's plain logit rshift(pile, -(we + ex + 16))
+    if (tid < a.rows) {
+        rc[tid][0] = 32768 * (i64)rf1[0] + 128 * (i64)rf1[1] + 16384 * (i64)K + 128 * (i64)rf1[2];
+        if (EPI == EPI_HEAD) {
+            const i64 ls = (i64)(((u64)(unsigned)rf0[2] << 32) | (unsigned)rf0[1]);
+            rc[tid][1] = wsub(wmul((i64)rf0[0] + 16, 65536), ls) >> 16;
+            rc[tid][2] = rf0[3];
+        } else {
+            rc[tid][1] = (i64)rf0[0] + 16;
+        }
     }
+    const bool corr = live && ((__ballot(n32 != 0) >> (16 * t)) & 0xFFFFull);   // a +32768 light in the row tile
     const bool rec0 = a.rec_pos && *a.rec_pos == p;
     i64 bv[4];
     int bi[4];
@@ -596,45 +613,44 @@ __global__ __launch_bounds__(256, 2) void k_head_rows(GemmArgs a) {     // two b
     for (int q = 0; q < 4; q++) { bv[q] = 0; bi[q] = -1; }
     auto compute = [&](const v4* w, const v4 (*wfs)[2], int tile) {
         if (!live) return;
-        v4 hh = {0, 0, 0, 0}, mid = {0, 0, 0, 0}, ll = {0, 0, 0, 0};
+        // HL and LH in accumulators of their own: two dependent chains of 12 instead of one of 24
+        v4 hh = {0, 0, 0, 0}, hl = {0, 0, 0, 0}, lh = {0, 0, 0, 0}, ll = {0, 0, 0, 0};
 #pragma unroll
         for (int s = 0; s < KS; s++) {
             const v4 wh = w[s * 128 + lane], wl = w[s * 128 + 64 + lane];
             hh = __builtin_amdgcn_mfma_i32_16x16x64_i8(xh[s], wh, hh, 0, 0, 0);
-            mid = __builtin_amdgcn_mfma_i32_16x16x64_i8(xh[s], wl, mid, 0, 0, 0);
+            hl = __builtin_amdgcn_mfma_i32_16x16x64_i8(xh[s], wl, hl, 0, 0, 0);
             ll = __builtin_amdgcn_mfma_i32_16x16x64_i8(xl[s], wl, ll, 0, 0, 0);
-            mid = __builtin_amdgcn_mfma_i32_16x16x64_i8(xl[s], wh, mid, 0, 0, 0);
+            lh = __builtin_amdgcn_mfma_i32_16x16x64_i8(xl[s], wh, lh, 0, 0, 0);
             if (corr) {
                 const v4 cc = Ab[s * 192 + 128];
-                mid = __builtin_amdgcn_mfma_i32_16x16x64_i8(cc, wh, mid, 0, 0, 0);
+                hl = __builtin_amdgcn_mfma_i32_16x16x64_i8(cc, wh, hl, 0, 0, 0);
                 ll = __builtin_amdgcn_mfma_i32_16x16x64_i8(cc, wl, ll, 0, 0, 0);
             }
         }
         const int j = tile * 16 + (lane & 15);
         if (j >= a.N) return;
         const v4 f0 = wfs[lane & 15][0], f1 = wfs[lane & 15][1];
-        const i64 swh = f0[0], swl = f0[1], we = f0[2];
+        const i64 ccol = 32768 * (i64)f0[0] + 128 * (i64)f0[1], we = f0[2];
         const i64 bc = (i64)(((u64)(unsigned)f1[1] << 32) | (unsigned)f1[0]);
 #pragma unroll
         for (int q = 0; q < 4; q++) {
             const int row = 16 * t + 4 * (lane >> 4) + q;
             if (row >= a.rows) continue;
-            const int* ri = rinfo + row * 8;
-            const i64 pile = 65536 * (i64)hh[q] + 256 * (i64)mid[q] + ll[q] + 32768 * ((i64)ri[4] + swh) +
-                             128 * ((i64)ri[5] + swl) + 16384 * (i64)K + 128 * (i64)ri[6];
+            const i64 pile = 65536 * (i64)hh[q] + 256 * ((i64)hl[q] + lh[q]) + ll[q] + rc[row][0] + ccol;
             const bool rec = rec0 && row == 0;
             if (rec && a.rpile) a.rpile[j] = pile;
             if (EPI == EPI_PILE) {
                 a.Y[(size_t)row * a.ystride + j] = pile;
             } else {
-                const i64 ls = (i64)(((u64)(unsigned)ri[2] << 32) | (unsigned)ri[1]);
-                const i64 y = EPI == EPI_PHEAD ? rsh(pile, -(we + (i64)ri[0] + 16))       // Pythia: plain, no bias
-                                               : wadd(power_known(pile, wsub(wmul(we + (i64)ri[0] + 16, 65536), ls), (i64)ri[3]), bc);
+                const i64 y = EPI == EPI_PHEAD ? rsh(pile, -(we + rc[row][1]))            // Pythia: plain, no bias
+                                               : wadd(rsh(wmul(pile, rc[row][2]), 16 - we - rc[row][1]), bc);
                 if (rec && a.rlogits) a.rlogits[j] = y;
                 if (bi[q] < 0 || y > bv[q]) { bv[q] = y; bi[q] = j; }      // j grows with the tile
             }
         }
     };
+    // (each slot is refilled in place once it is used; no exit inside the loop, so the waits stay exact)
     for (int tile = blockIdx.x; tile < ntiles;) {
 #pragma unroll
         for (int i = 0; i < PER; i++) ws[0][tid + i * 256] = r0[i];

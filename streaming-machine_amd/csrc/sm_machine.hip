@@ -398,8 +398,9 @@ static int launch_step_batched(sm_machine* m, int parts, hipEvent_t hs, hipEvent
         return a;
     };
     // mproj's epilogue (from its four K slices of partial accumulators) added into the stream, then the next light
-    auto finish_light = [&](const MfmaPlate& P, i64* rpile, i64* rout, i64* rx16, i64* rexls) {
+    auto finish_light = [&](const MfmaPlate& P, i64* rpile, i64* rout, i64* rx16, i64* rexls, int ls_row) {
         LightArgs a = light_args(P.N, nullptr, rx16, rexls);
+        a.ls_row = ls_row;
         a.part = m->part_acc; a.kin = P.K; a.csum = P.csum; a.we = P.e; a.bias = P.b; a.Y = m->R;
         a.rpile_in = rpile; a.rout_in = rout; a.sfacts = m->sfacts;
         k_light<768, PRO_ADD_GAUGE, 192, 4><<<B, 192, 0, m->st>>>(a);
@@ -462,7 +463,8 @@ static int launch_step_batched(sm_machine* m, int parts, hipEvent_t hs, hipEvent
         }
         const bool last = l == 11;     // the last stream update lights the head
         finish_light(m->mbank[l][3], rp + 3 * 3072, m->r_resid + (l * 2 + 1) * 768,
-                     last ? m->r_hx16 : m->r_x16 + (size_t)(l + 1) * 4 * 3072, last ? m->r_hexls : m->r_exls + (size_t)(l + 1) * 4 * 2);
+                     last ? m->r_hx16 : m->r_x16 + (size_t)(l + 1) * 4 * 3072, last ? m->r_hexls : m->r_exls + (size_t)(l + 1) * 4 * 2,
+                     last && !rowmap);     // the head takes LS and the power factor made here
     }
     if ((parts & STEP_HEAD) && !rowmap) {
         GemmArgs a = gemm_args(m->mhead, nullptr, 0, m->r_hpile, nullptr);
