@@ -272,6 +272,29 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs a) {
     static_assert(!ROWS || !GAUGED, "a light formed here feeds a plain epilogue or K-slice partials");
     v4 gf = {0, 0, 0, 0};
     if (GAUGED) gf = *reinterpret_cast<const v4*>(a.rowinfo + (size_t)(tid < a.rows ? tid : 0) * 8);
+    // SRC = 0: the row facts for LDS and each row's n32768, as bounded loads (rows past the last read zeros with
+    // no traffic), so that no guarded load makes the first use wait for everything issued after it
+    int n32 = 0, rsv = 0, rsv2 = 0;
+    if constexpr (!ROWS) {
+        const __amdgpu_buffer_rsrc_t rr = buf_rsrc(a.rowinfo, (unsigned)(a.rows * 8) * 4u);
+        n32 = buf_load1(rr, (unsigned)(lane * 8 + 6) * 4u);
+        rsv = buf_load1(rr, (unsigned)tid * 4u);
+        rsv2 = buf_load1(rr, (unsigned)(tid + 256) * 4u);
+    }
+    // the column facts of each tile (for the epilogue)
+    i64 swh[NB], swl[NB], we[NB], bc[NB];
+#pragma unroll
+    for (int nb = 0; nb < NB; nb++) swh[nb] = swl[nb] = we[nb] = bc[nb] = 0;
+    if constexpr (EPI != EPI_PART) {     // bounded loads: columns past N read zeros
+        const unsigned n = (unsigned)a.N;   // csum: int32 pairs, we: int32, bias: int64
+        const __amdgpu_buffer_rsrc_t rc = buf_rsrc(a.csum, 8u * n), rw = buf_rsrc(a.we, 4u * n), rb = buf_rsrc(a.bias, 8u * n);
+#pragma unroll
+        for (int nb = 0; nb < NB; nb++) {
+            const unsigned j = (unsigned)((nt * NB + nb) * 16 + (lane & 15));
+            swh[nb] = buf_load1(rc, 8u * j); swl[nb] = buf_load1(rc, 8u * j + 4u);
+            we[nb] = buf_load1(rw, 4u * j); bc[nb] = buf_load8(rb, 8u * j);
+        }
+    }
     v4 wh[NB][NS], wl[NB][NS], xh[NS], xl[NS];
     // SRC > 0: wave w lights tile rows 4 w .. 4 w + 3.  Their OR words (word n = lane + 64 m of the wave's
     // 4 SRC), then their values as contiguous 1 KB wave loads (value pair 64 c + lane of row j), all ahead of the
@@ -310,9 +333,9 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs a) {
             xl[i] = Ab[((size_t)t0 * KS + s0 + i) * 192 + 64];
         }
     }
-    const int n32 = !ROWS && lane < a.rows ? a.rowinfo[lane * 8 + 6] : 0;
-    const int rsv = !ROWS && tid < a.rows * 8 ? a.rowinfo[tid] : 0;
-    const int rsv2 = !ROWS && tid + 256 < a.rows * 8 ? a.rowinfo[tid + 256] : 0;
+    // keep every load above issued before any of the work below (the scheduler would sink the small ones past
+    // the first MFMAs, where their latency shows)
+    __builtin_amdgcn_sched_barrier(0);
     // SRC > 0: the light (base2.py:24-27) of the wave's rows into LDS, then each wave's A operands and plane
     // sums from there
     v4 xc[ROWS ? NS : 1];
@@ -400,14 +423,6 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs a) {
     i64 g_ls = 0, g_e2 = 0;
     if (GAUGED)
         g_ls = gauge_ls_pow_v(gf[1], (i64)(((u64)(unsigned)gf[3] << 32) | (unsigned)gf[2]), gf[0], a.tb, g_e2);
-    // the column facts of each tile
-    i64 swh[NB], swl[NB], we[NB], bc[NB];
-#pragma unroll
-    for (int nb = 0; nb < NB; nb++) {
-        const int j = (nt * NB + nb) * 16 + (lane & 15);
-        swh[nb] = swl[nb] = we[nb] = bc[nb] = 0;
-        if (EPI != EPI_PART && j < a.N) { swh[nb] = a.csum[2 * j]; swl[nb] = a.csum[2 * j + 1]; we[nb] = a.we[j]; bc[nb] = a.bias[j]; }
-    }
     v4 acc[NB][3];
 #pragma unroll
     for (int nb = 0; nb < NB; nb++) acc[nb][0] = acc[nb][1] = acc[nb][2] = v4{0, 0, 0, 0};

@@ -180,6 +180,9 @@ SMD v4i buf_load4(__amdgpu_buffer_rsrc_t r, unsigned off) {
     return __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 0));
 }
 SMD int buf_load1(__amdgpu_buffer_rsrc_t r, unsigned off) { return (int)__builtin_amdgcn_raw_buffer_load_b32(r, (int)off, 0, 0); }
+SMD i64 buf_load8(__amdgpu_buffer_rsrc_t r, unsigned off) {
+    return (i64)__builtin_bit_cast(u64, __builtin_amdgcn_raw_buffer_load_b64(r, (int)off, 0, 0));
+}
 
 // ---------------- wave64 reductions through DPP (a few VALU cycles per step) ----------------
 // update_dpp(old = 0, ...): lanes a step does not reach contribute 0, the identity of +, | and max of naturals
