@@ -94,11 +94,12 @@ __global__ __launch_bounds__(NT) void k_light(LightArgs a) {
     static_assert(NT % 64 == 0 && NW <= 12, "one to twelve waves");
     __shared__ int red[24 + 6 * 12];   // OR words [0, 24), sums [24, 96)
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, r = blockIdx.x;
-    const int p = a.pos ? *a.pos : 0;              // the stage product (PRO_X16) has no position
-    if (a.skip_prompt && p < *a.plen - 1) return;
     i64 v[GPT][4];
     typedef int v4l __attribute__((ext_vector_type(4)));
-    // the producing bank's light facts for this row (its K slices formed the light themselves)
+    typedef i64 v2q __attribute__((ext_vector_type(2)));
+    // every load of the row first: none depends on the position, so that reading it (and the prompt check)
+    // overlaps them.  PRO_ADD_GAUGE: the producing bank's light facts for this row (its K slices formed the
+    // light themselves), the column facts, the stream and the partial slices
     i64 i_ex = 0, i_sxh = 0, i_sxl = 0, i_n32 = 0;
     if (PRO == PRO_ADD_GAUGE) {
         int ri[8];
@@ -106,7 +107,9 @@ __global__ __launch_bounds__(NT) void k_light(LightArgs a) {
         i_ex = ri[0];
         i_sxh = ri[4]; i_sxl = ri[5]; i_n32 = ri[6];
     }
-    const bool rec_in = r == 0 && a.rec_pos && *a.rec_pos == p;
+    constexpr int GA = PRO == PRO_ADD_GAUGE ? GPT : 1, KA = PRO == PRO_ADD_GAUGE ? KSP : 1;
+    v4l c0[GA], c1[GA], wv[GA], hq[GA][KA], mq[GA][KA], lq[GA][KA];
+    v2q b01[GA], b23[GA], y01[GA], y23[GA];
 #pragma unroll
     for (int m = 0; m < GPT; m++) {
         const int g = tid + NT * m;
@@ -114,38 +117,49 @@ __global__ __launch_bounds__(NT) void k_light(LightArgs a) {
         for (int j = 0; j < 4; j++) v[m][j] = 0;
         if (g >= NG) continue;
         const int k = 4 * g;
-        if (PRO == PRO_ADD_GAUGE) {
-            typedef i64 v2q __attribute__((ext_vector_type(2)));
-            // every load first (column facts, the stream, the partial slices), then the arithmetic
-            const v4l c0 = *reinterpret_cast<const v4l*>(a.csum + 2 * k), c1 = *reinterpret_cast<const v4l*>(a.csum + 2 * k + 4);
-            const v4l wv = *reinterpret_cast<const v4l*>(a.we + k);
-            const v2q b01 = *reinterpret_cast<const v2q*>(a.bias + k), b23 = *reinterpret_cast<const v2q*>(a.bias + k + 2);
-            const v2q y01 = *reinterpret_cast<const v2q*>(a.Y + (size_t)r * K + k);
-            const v2q y23 = *reinterpret_cast<const v2q*>(a.Y + (size_t)r * K + k + 2);
-            v4l hq[KSP], mq[KSP], lq[KSP];
+        if constexpr (PRO == PRO_ADD_GAUGE) {
+            c0[m] = *reinterpret_cast<const v4l*>(a.csum + 2 * k); c1[m] = *reinterpret_cast<const v4l*>(a.csum + 2 * k + 4);
+            wv[m] = *reinterpret_cast<const v4l*>(a.we + k);
+            b01[m] = *reinterpret_cast<const v2q*>(a.bias + k); b23[m] = *reinterpret_cast<const v2q*>(a.bias + k + 2);
+            y01[m] = *reinterpret_cast<const v2q*>(a.Y + (size_t)r * K + k);
+            y23[m] = *reinterpret_cast<const v2q*>(a.Y + (size_t)r * K + k + 2);
 #pragma unroll
             for (int ks = 0; ks < KSP; ks++) {
                 const int* q = a.part + ((size_t)ks * 3 * a.rows + r) * K + k;
-                hq[ks] = *reinterpret_cast<const v4l*>(q);
-                mq[ks] = *reinterpret_cast<const v4l*>(q + (size_t)a.rows * K);
-                lq[ks] = *reinterpret_cast<const v4l*>(q + (size_t)2 * a.rows * K);
+                hq[m][ks] = *reinterpret_cast<const v4l*>(q);
+                mq[m][ks] = *reinterpret_cast<const v4l*>(q + (size_t)a.rows * K);
+                lq[m][ks] = *reinterpret_cast<const v4l*>(q + (size_t)2 * a.rows * K);
             }
-            v4l h = hq[0], mi = mq[0], lo = lq[0];
+        } else if constexpr (PRO != PRO_EMBED) {
 #pragma unroll
-            for (int ks = 1; ks < KSP; ks++) { h += hq[ks]; mi += mq[ks]; lo += lq[ks]; }
-            const int sw[8] = {c0[0], c0[1], c0[2], c0[3], c1[0], c1[1], c1[2], c1[3]};
-            const i64 bcs[4] = {b01[0], b01[1], b23[0], b23[1]}, ys[4] = {y01[0], y01[1], y23[0], y23[1]};
+            for (int j = 0; j < 4; j++) v[m][j] = a.X[(size_t)r * K + k + j];
+        }
+    }
+    const int p = a.pos ? *a.pos : 0;              // the stage product (PRO_X16) has no position
+    if (a.skip_prompt && p < *a.plen - 1) return;
+    const bool rec_in = r == 0 && a.rec_pos && *a.rec_pos == p;
+#pragma unroll
+    for (int m = 0; m < GPT; m++) {
+        const int g = tid + NT * m;
+        if (g >= NG) continue;
+        const int k = 4 * g;
+        if constexpr (PRO == PRO_ADD_GAUGE) {
+            v4l h = hq[m][0], mi = mq[m][0], lo = lq[m][0];
+#pragma unroll
+            for (int ks = 1; ks < KSP; ks++) { h += hq[m][ks]; mi += mq[m][ks]; lo += lq[m][ks]; }
+            const int sw[8] = {c0[m][0], c0[m][1], c0[m][2], c0[m][3], c1[m][0], c1[m][1], c1[m][2], c1[m][3]};
+            const i64 bcs[4] = {b01[m][0], b01[m][1], b23[m][0], b23[m][1]}, ys[4] = {y01[m][0], y01[m][1], y23[m][0], y23[m][1]};
 #pragma unroll
             for (int j = 0; j < 4; j++) {
                 const i64 pile = 65536 * (i64)h[j] + 256 * (i64)mi[j] + lo[j] + 32768 * (i_sxh + sw[2 * j]) +
                                  128 * (i_sxl + sw[2 * j + 1]) + 16384 * (i64)a.kin + 128 * i_n32;
-                const i64 y = wadd(ys[j], wadd(rsh(pile, -((i64)wv[j] + i_ex + 16)), bcs[j]));
+                const i64 y = wadd(ys[j], wadd(rsh(pile, -((i64)wv[m][j] + i_ex + 16)), bcs[j]));
                 a.Y[(size_t)r * K + k + j] = y;
                 v[m][j] = y;
                 if (rec_in && a.rpile_in) a.rpile_in[k + j] = pile;
                 if (rec_in && a.rout_in) a.rout_in[k + j] = y;
             }
-        } else if (PRO == PRO_EMBED) {
+        } else if constexpr (PRO == PRO_EMBED) {
             const int pm = a.rowmap ? a.rowmap[r] : 0;
             const int st = a.rowmap ? pm >> 16 : r, q = a.rowmap ? pm & 0xFFFF : p;
             const i64 tok = a.seq[(size_t)st * a.seq_stride + q];
@@ -154,9 +168,6 @@ __global__ __launch_bounds__(NT) void k_light(LightArgs a) {
                 v[m][j] = wadd(a.wte[tok * 768 + k + j], a.wpe[(i64)q * 768 + k + j]);
                 a.Rw[(size_t)r * 768 + k + j] = v[m][j];
             }
-        } else {
-#pragma unroll
-            for (int j = 0; j < 4; j++) v[m][j] = a.X[(size_t)r * K + k + j];
         }
     }
     int sh = 0;                                     // PRO_X16: the lights are given
@@ -572,12 +583,10 @@ __global__ __launch_bounds__(256, 2) void k_head_rows(GemmArgs a) {     // two b
     // the row facts first (row tid): ex, LS, the power factor (EPI_HEAD: the producing light kernel turned S1, S2
     // into LS and EXP2[-LS & 0xFFFF]), the plane sums; then the first tile, the light planes, the second tile, so
     // that the first tile waits for nothing behind it (loads complete in order)
-    v4 rf0 = {0, 0, 0, 0}, rf1 = {0, 0, 0, 0};
-    if (tid < a.rows) {
-        rf0 = *reinterpret_cast<const v4*>(a.rowinfo + (size_t)tid * 8);
-        rf1 = *reinterpret_cast<const v4*>(a.rowinfo + (size_t)tid * 8 + 4);
-    }
-    const int n32 = lane < a.rows ? a.rowinfo[lane * 8 + 6] : 0;    // rows 0-63 in every wave
+    // (bounded loads: rows past the last read zeros, with no branch whose join would wait for every load)
+    const __amdgpu_buffer_rsrc_t rr = buf_rsrc(a.rowinfo, (unsigned)(a.rows * 8) * 4u);
+    const v4 rf0 = buf_load4(rr, (unsigned)tid * 32u), rf1 = buf_load4(rr, (unsigned)tid * 32u + 16u);
+    const int n32 = buf_load1(rr, (unsigned)(lane * 8 + 6) * 4u);    // rows 0-63 in every wave
     const v4* Wg = reinterpret_cast<const v4*>(a.W) + tid;
     // a tile's weights, and (threads 0-15) the facts of its column tid: rows of the slot r, refilled in place
     // (a copy of registers in flight would wait for every load: loads complete in order); threads past 15 read
