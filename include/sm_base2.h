@@ -139,9 +139,10 @@ int sm_stage_race(const int64_t* v, int64_t n, int64_t* out_index, void* stream)
 
 /* One new position's attention for one stream (base2.py:85-100 for the last row; base2_stream.swift:120-133
  * without its 64-position cap).  qkv: device int64 [2304] (the gauged q, k, v of position pos); the caches,
- * head-major, hold positions < pos and receive position pos: k16 int32 [12][ctx][64], ek int32 [12][ctx], v
- * int32 [12][ctx][64]; out: device int64 [768]. */
-int sm_stage_attend(const sm_tables* t, const int64_t* qkv, int32_t* k16, int32_t* ek, int32_t* v,
+ * head-major, hold positions < pos and receive position pos: k16 int16 [12][ctx][64] (the 16-bit keys, a
+ * +32768 held as 32767), km int64 [12][ctx] (bit d set: dimension d of that key is +32768), ek int32 [12][ctx],
+ * v int32 [12][ctx][64]; out: device int64 [768].  Zeroed caches are empty caches. */
+int sm_stage_attend(const sm_tables* t, const int64_t* qkv, int16_t* k16, int64_t* km, int32_t* ek, int32_t* v,
                     int32_t pos, int32_t ctx, int64_t* out, void* stream);
 
 /* A plate on the device from an input-major int16 [nin][nout] host array: tile_cols > 0 lays it out for the

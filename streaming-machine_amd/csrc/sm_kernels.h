@@ -69,7 +69,8 @@ struct GemvArgs {
 struct AttArgs {
     const i64* QKV;     // [B][2304]
     // the cache, head-major so that a (stream, head)'s positions are contiguous: [B][12 heads][ctx][64]
-    int* K16;           // [B][12][ctx][64] per-head 16-bit keys (values in [-32768, 32768])
+    short* K16;         // [B][12][ctx][64] per-head 16-bit keys (values in [-32768, 32768]; +32768 held as 32767)
+    i64* KM;            // [B][12][ctx]     bit d: dimension d of the key is +32768 (one more than K16 holds)
     int* EK;            // [B][12][ctx]     their water levels
     int* V;             // [B][12][ctx][64] raw gauged values (checked to fit 32 bits)
     i64* out;           // [B][768]

@@ -406,6 +406,40 @@ __global__ __launch_bounds__(64 * WPB) void k_gemv(GemvArgs a) {
 }
 
 // ---------------------------------------------------------------------------------------------------------
+// The key cache holds a key's 64 dimensions as int16, 128 bytes a position: a +32768 (the top of to16's range,
+// base2.py:24-27) is held as 32767 and its bit set in the position's 64-bit mask, which the scores add back
+// (q . k = q . k' + the sum of q over the masked dimensions).  The whole wave stores one row, lane = dimension.
+SMD void key_store(short* krow, i64* km, int x16, int lane) {
+    krow[lane] = (short)min(x16, 32767);
+    const u64 m = __ballot(x16 == 32768);
+    if (lane == 0) *km = (i64)m;
+}
+SMD int lo16(int w) { return (w << 16) >> 16; }
+SMD int hi16(int w) { return w >> 16; }
+// q . k' over 16 dimensions: q as four int32 quads (dimensions 0-15), k' as 16 int16 in two quads of pairs
+// (dword w of quad h: dimensions 8 h + 2 w, + 1).  Each product fits 31 bits; the sum is taken in 64.
+SMD i64 dot16(const v4i (&q)[4], const v4i (&k)[2]) {
+    i64 d = 0;
+#pragma unroll
+    for (int h = 0; h < 2; h++)
+#pragma unroll
+        for (int w = 0; w < 4; w++) {
+            const int i = 8 * h + 2 * w;
+            d += (i64)(q[i >> 2][i & 3] * lo16(k[h][w])) + (i64)(q[(i + 1) >> 2][(i + 1) & 3] * hi16(k[h][w]));
+        }
+    return d;
+}
+// the masked dimensions' share: the sum of q over the set bits of mb (bit j: dimension j of the 16)
+SMD i64 dot16_mask(const v4i (&q)[4], unsigned mb) {
+    i64 d = 0;
+    if (mb) {
+#pragma unroll
+        for (int j = 0; j < 16; j++) d += (mb >> j) & 1 ? (i64)q[j >> 2][j & 3] : 0;
+    }
+    return d;
+}
+
+// ---------------------------------------------------------------------------------------------------------
 // Attention for the newest position of each stream, one block per (head, stream) (base2.py:85-100).
 //   1. the head's q, k through their own water level (base2.py:93); k16, ek and the raw v go to the cache
 //   2. scores over every cached position s <= p: rshift(q16 . k16, -(eq + ek + 7))          (base2.py:94)
@@ -426,7 +460,8 @@ SMD void attend_short(const AttArgs& a, int p, int h, int b, int* q_s, int* w_s)
     const int lane = threadIdx.x;
     const i64* qkv = a.QKV + (size_t)b * 2304;
     const size_t hb = ((size_t)b * 12 + h) * a.ctx;         // this (stream, head)'s cache rows
-    int* K16 = a.K16 + hb * 64;
+    short* K16 = a.K16 + hb * 64;
+    i64* KM = a.KM + hb;
     int* EK = a.EK + hb;
     int* V = a.V + hb * 64;
     const bool rec = b == 0 && a.rec_pos && *a.rec_pos == p;
@@ -435,12 +470,13 @@ SMD void attend_short(const AttArgs& a, int p, int h, int b, int* q_s, int* w_s)
     i64 kv = qkv[MODEL == 1 ? h * 192 + 64 + lane : 768 + h * 64 + lane];
     const i64 vv = qkv[MODEL == 1 ? h * 192 + 128 + lane : 1536 + h * 64 + lane];
     // the cached rows s < p (lanes and columns past p read zeros without a memory request)
-    const __amdgpu_buffer_rsrc_t rk = buf_rsrc(K16, (unsigned)p * 256), re = buf_rsrc(EK, (unsigned)p * 4),
-                                 rv = buf_rsrc(V, (unsigned)p * 256);
-    v4i krow[16];
+    const __amdgpu_buffer_rsrc_t rk = buf_rsrc(K16, (unsigned)p * 128), re = buf_rsrc(EK, (unsigned)p * 4),
+                                 rm = buf_rsrc(KM, (unsigned)p * 8), rv = buf_rsrc(V, (unsigned)p * 256);
+    v4i krow[8];                                             // dword w of krow[c]: dimensions 8 c + 2 w, + 1
 #pragma unroll
-    for (int c = 0; c < 16; c++) krow[c] = buf_load4(rk, (unsigned)lane * 256 + 16 * c);
+    for (int c = 0; c < 8; c++) krow[c] = buf_load4(rk, (unsigned)lane * 128 + 16 * c);
     const int ekl = buf_load1(re, (unsigned)lane * 4);
+    const u64 kml = (u64)buf_load8(rm, (unsigned)lane * 8);
     int vcol[64];
 #pragma unroll
     for (int s = 0; s < 64; s++) vcol[s] = buf_load1(rv, (unsigned)(s * 64 + lane) * 4);
@@ -460,7 +496,7 @@ SMD void attend_short(const AttArgs& a, int p, int h, int b, int* q_s, int* w_s)
     const int shq = water_shift(wave_or64(iabs64(qv))), shk = water_shift(wave_or64(iabs64(kv)));
     const int q16 = (int)rsh(qv, shq), k16 = (int)rsh(kv, shk);
     const i64 eq = -16 + shq, ekn = -16 + shk;
-    K16[(size_t)p * 64 + lane] = k16;
+    key_store(K16 + (size_t)p * 64, KM + p, k16, lane);
     if (lane == 0) EK[p] = (int)ekn;
     if (vv < (i64)INT32_MIN || vv > (i64)INT32_MAX) atomicOr(a.err, SM_ERR_V32);
     V[(size_t)p * 64 + lane] = (int)vv;
@@ -468,10 +504,13 @@ SMD void attend_short(const AttArgs& a, int p, int h, int b, int* q_s, int* w_s)
     q_s[lane] = q16;
     i64 dot = 0;
 #pragma unroll
-    for (int c = 0; c < 16; c++) {
-        const v4i q4 = reinterpret_cast<const v4i*>(q_s)[c];          // the same address in every lane
-        dot += (i64)q4.x * krow[c].x + (i64)q4.y * krow[c].y + (i64)q4.z * krow[c].z + (i64)q4.w * krow[c].w;
+    for (int c = 0; c < 8; c++) {
+        const v4i qa = reinterpret_cast<const v4i*>(q_s)[2 * c], qb = reinterpret_cast<const v4i*>(q_s)[2 * c + 1];
+        const v4i k = krow[c];                                         // (q: the same address in every lane)
+        dot += (i64)(qa.x * lo16(k.x)) + (i64)(qa.y * hi16(k.x)) + (i64)(qa.z * lo16(k.y)) + (i64)(qa.w * hi16(k.y)) +
+               (i64)(qb.x * lo16(k.z)) + (i64)(qb.y * hi16(k.z)) + (i64)(qb.z * lo16(k.w)) + (i64)(qb.w * hi16(k.w));
     }
+    for (u64 m = kml; m; m &= m - 1) dot += q_s[__builtin_ctzll(m)];   // the +32768 dimensions (rare)
     const i64 dn = wave_reduce64((i64)q16 * k16, OpAdd());
     const i64 ek = lane == p ? ekn : ekl;
     const i64 d = lane == p ? dn : dot;
@@ -564,28 +603,31 @@ __global__ __launch_bounds__(NTHR, ONE ? 1 : 3) void k_attend(AttArgs a) {
     }
     const i64* qkv = a.QKV + (size_t)b * 2304;
     const size_t hb = ((size_t)st * 12 + h) * a.ctx;        // this (stream, head)'s cache rows
-    int* K16 = a.K16 + hb * 64;
+    short* K16 = a.K16 + hb * 64;
+    i64* KM = a.KM + hb;
     int* EK = a.EK + hb;
     int* V = a.V + hb * 64;
     const bool rec = store && b == 0 && a.rec_pos && *a.rec_pos == p;
 
     // requests first (vector loads complete in order): the new q, k, v; then the cached keys of the first
-    // ATT_PRE passes (a position's four lanes read its 256-byte row as 4 x 64 contiguous bytes: lane qd holds
-    // dimensions 16 u + 4 qd .. + 3 of step u); the values (16 lanes a 256-byte row, four rows a wave) follow
-    // once the new position is in
+    // ATT_PRE passes (a position's four lanes read its 128-byte row, lane qd the 32 bytes of dimensions
+    // 16 qd .. + 15), their water levels and masks; the values (16 lanes a 256-byte row, four rows a wave)
+    // follow once the new position is in
     i64 xnew = wave < 3 ? qkv[MODEL == 1 ? h * 192 + wave * 64 + lane : wave * 768 + h * 64 + lane] : 0;
     // (buffer loads bounded at position p: rows past it read zeros and cost no memory traffic)
-    const __amdgpu_buffer_rsrc_t rk = buf_rsrc(K16, (unsigned)p * 256), re = buf_rsrc(EK, (unsigned)p * 4),
-                                 rv = buf_rsrc(V, (unsigned)p * 256);
+    const __amdgpu_buffer_rsrc_t rk = buf_rsrc(K16, (unsigned)p * 128), re = buf_rsrc(EK, (unsigned)p * 4),
+                                 rm = buf_rsrc(KM, (unsigned)p * 8), rv = buf_rsrc(V, (unsigned)p * 256);
     static_assert(ATT_PRE == 2, "the scores loop refills a ring of two key slots");
-    v4i kp[ATT_PRE][4];
+    v4i kp[ATT_PRE][2];
     int ekp[ATT_PRE];
+    i64 kmp[ATT_PRE];
 #pragma unroll
     for (int c = 0; c < ATT_PRE; c++) {
         const unsigned sr = sl + 64 * c;
-#pragma unroll
-        for (int u = 0; u < 4; u++) kp[c][u] = buf_load4(rk, sr * 256 + (4 * u + qd) * 16);
+        kp[c][0] = buf_load4(rk, sr * 128 + qd * 32);
+        kp[c][1] = buf_load4(rk, sr * 128 + qd * 32 + 16);
         ekp[c] = buf_load1(re, sr * 4);
+        kmp[c] = buf_load8(rm, sr * 8);
     }
     if (MODEL == 1 && wave < 2) {        // the turns (pythia_base2.py:116-123): pair (i, i + rot/2)
         const int r = a.rot >> 1;
@@ -607,7 +649,7 @@ __global__ __launch_bounds__(NTHR, ONE ? 1 : 3) void k_attend(AttArgs a) {
             if (lane == 0) eqs = -16 + sh;
         } else {
             k16s[lane] = x16;
-            if (store) K16[(size_t)p * 64 + lane] = x16;
+            if (store) key_store(K16 + (size_t)p * 64, KM + p, x16, lane);
             if (lane == 0) {
                 eks = -16 + sh;
                 if (store) EK[p] = -16 + sh;
@@ -630,9 +672,9 @@ __global__ __launch_bounds__(NTHR, ONE ? 1 : 3) void k_attend(AttArgs a) {
 
     // scores (base2.py:94 / pythia_base2.py:133) and their maximum
     const i64 eq = eqs;
-    v4i qv[4];
+    v4i qv[4];                                              // dimensions 16 qd .. + 15
 #pragma unroll
-    for (int u = 0; u < 4; u++) qv[u] = reinterpret_cast<const v4i*>(q16s)[4 * u + qd];
+    for (int u = 0; u < 4; u++) qv[u] = reinterpret_cast<const v4i*>(q16s)[4 * qd + u];
     auto score = [&](i64 dot, i64 ek) -> i64 {
         return MODEL == 1 ? rsh(wmul(dot, a.ehalf), wsub(16, wsub(wmul(eq + ek + 10, 65536), a.half) >> 16))
                           : rsh(dot, -(eq + ek + 7));
@@ -641,21 +683,19 @@ __global__ __launch_bounds__(NTHR, ONE ? 1 : 3) void k_attend(AttArgs a) {
     // passes at a time, each pass's keys requested two passes earlier into the register slot it frees (rows past
     // p read zeros and cost no memory traffic).  The two cases are separate code, so that each has exact waits.
     i64 mx = INT64_MIN;
-    auto pass = [&](auto refill, int s0, v4i (&kk0)[4], int& ek0) {
+    auto pass = [&](auto refill, int s0, v4i (&kk0)[2], int& ek0, i64& km0) {
         const int s = s0 + sl;
         i64 dot = 0, ek = ek0;
-        v4i kk[4];
+        if (s < p) {                                       // a cached key
+            const v4i kk[2] = {kk0[0], kk0[1]};
+            dot = dot16(qv, kk) + dot16_mask(qv, (unsigned)((u64)km0 >> (16 * qd)) & 0xFFFFu);
+        } else if (s == p) {                               // the new key (int32, from LDS)
 #pragma unroll
-        for (int u = 0; u < 4; u++) kk[u] = kk0[u];
-        if (s == p) {                                      // the new key
-#pragma unroll
-            for (int u = 0; u < 4; u++) kk[u] = reinterpret_cast<const v4i*>(k16s)[4 * u + qd];
+            for (int u = 0; u < 4; u++) {
+                const v4i kn = reinterpret_cast<const v4i*>(k16s)[4 * qd + u];
+                dot += (i64)qv[u].x * kn.x + (i64)qv[u].y * kn.y + (i64)qv[u].z * kn.z + (i64)qv[u].w * kn.w;
+            }
             ek = eks;
-        }
-        if (s <= p) {
-#pragma unroll
-            for (int u = 0; u < 4; u++)
-                dot += (i64)qv[u].x * kk[u].x + (i64)qv[u].y * kk[u].y + (i64)qv[u].z * kk[u].z + (i64)qv[u].w * kk[u].w;
         }
         dot += dpp64<0xB1, 0xf, 0xf>(dot, 0);              // quad_perm [1, 0, 3, 2]: the position's four lanes
         dot += dpp64<0x4E, 0xf, 0xf>(dot, 0);              // quad_perm [2, 3, 0, 1]
@@ -666,19 +706,20 @@ __global__ __launch_bounds__(NTHR, ONE ? 1 : 3) void k_attend(AttArgs a) {
         }
         if constexpr (decltype(refill)::value) {          // the pass two ahead
             const unsigned sr = s0 + 2 * ACH + sl;
-#pragma unroll
-            for (int u = 0; u < 4; u++) kk0[u] = buf_load4(rk, sr * 256 + (4 * u + qd) * 16);
+            kk0[0] = buf_load4(rk, sr * 128 + qd * 32);
+            kk0[1] = buf_load4(rk, sr * 128 + qd * 32 + 16);
             ek0 = buf_load1(re, sr * 4);
+            km0 = buf_load8(rm, sr * 8);
         }
     };
     const bool longc = p >= 2 * ACH;                       // uniform
     if (!longc) {
-        pass(Flag<false>{}, 0, kp[0], ekp[0]);
-        if (ACH <= p) pass(Flag<false>{}, ACH, kp[1], ekp[1]);
+        pass(Flag<false>{}, 0, kp[0], ekp[0], kmp[0]);
+        if (ACH <= p) pass(Flag<false>{}, ACH, kp[1], ekp[1], kmp[1]);
     } else {
         for (int s0 = 0; s0 <= p; s0 += 2 * ACH) {
-            pass(Flag<true>{}, s0, kp[0], ekp[0]);
-            if (s0 + ACH <= p) pass(Flag<true>{}, s0 + ACH, kp[1], ekp[1]);
+            pass(Flag<true>{}, s0, kp[0], ekp[0], kmp[0]);
+            if (s0 + ACH <= p) pass(Flag<true>{}, s0 + ACH, kp[1], ekp[1], kmp[1]);
         }
     }
     mx = block_reduce(mx, red, OpMax(), tid);   // its barriers also publish sc[]
@@ -772,7 +813,7 @@ __global__ __launch_bounds__(128) void k_kv_rows(AttArgs a) {
             }
         }
         const int sh = water_shift(wave_or64(iabs64(x)));
-        a.K16[at * 64 + lane] = (int)rsh(x, sh);
+        key_store(a.K16 + at * 64, a.KM + at, (int)rsh(x, sh), lane);
         if (lane == 0) a.EK[at] = -16 + sh;
     } else {
         if (x < (i64)INT32_MIN || x > (i64)INT32_MAX) atomicOr(a.err, SM_ERR_V32);

@@ -237,7 +237,9 @@ struct sm_machine {
     i64* attor = nullptr;                               // [rows][12] OR of |att| over each head's values
     i64* hidor = nullptr;                               // [rows][192] OR of |hid| over each fc tile's columns
     int* sfacts = nullptr;                              // [4][rows][4] mproj's K slices' light facts
-    int *K16 = nullptr, *EK = nullptr, *V = nullptr;   // [L][B][12 heads][ctx][64] (EK: [L][B][12][ctx])
+    short* K16 = nullptr;                              // [L][B][12 heads][ctx][64] int16 (+32768 as 32767)
+    i64* KM = nullptr;                                 // [L][B][12][ctx] the +32768 dimensions of each key
+    int *EK = nullptr, *V = nullptr;                   // [L][B][12][ctx], [L][B][12 heads][ctx][64]
     int* seq = nullptr;                                 // [B][ctx + 1]
     int* words = nullptr;                               // [B][ctx + 1]
     int* ctl = nullptr;
@@ -360,7 +362,7 @@ static void machine_free(sm_machine* m) {
     free_plate(m->head);
     free_mfma_plate(m->mhead);
     tables_free(m->T);
-    void* ps[] = {m->pfmap, m->planes, m->part_acc, m->rowinfo, m->wte, m->wpe, m->R, m->QKV, m->att, m->attor, m->hidor, m->sfacts, m->hid, m->K16, m->EK, m->V, m->seq, m->words, m->ctl,
+    void* ps[] = {m->pfmap, m->planes, m->part_acc, m->rowinfo, m->wte, m->wpe, m->R, m->QKV, m->att, m->attor, m->hidor, m->sfacts, m->hid, m->K16, m->KM, m->EK, m->V, m->seq, m->words, m->ctl,
                   m->part_v, m->part_i, m->r_x16, m->r_exls, m->r_pile, m->r_qkv, m->r_att, m->r_hid, m->r_resid,
                   m->r_hx16, m->r_hexls, m->r_hpile, m->r_logits, m->r_gauge, m->r_fcpre, m->r_hgauge,
                   m->fg, m->fb, m->ew, m->ee, m->cosT, m->sinT};
@@ -428,7 +430,7 @@ static int launch_step_batched(sm_machine* m, int parts, hipEvent_t hs, hipEvent
         {
             AttArgs a{};
             const size_t per = (size_t)m->B * m->ctx;
-            a.QKV = m->QKV; a.K16 = m->K16 + l * per * 768; a.EK = m->EK + l * per * 12; a.V = m->V + l * per * 768;
+            a.QKV = m->QKV; a.K16 = m->K16 + l * per * 768; a.KM = m->KM + l * per * 12; a.EK = m->EK + l * per * 12; a.V = m->V + l * per * 768;
             a.out = m->att; a.pos = ctl + CTL_POS; a.ctx = m->ctx; a.tb = tb; a.err = ctl + CTL_ERR;
             a.rec_pos = recp; a.ratt = m->r_att + l * 768; a.rowmap = rowmap; a.out_or = m->attor;
             if (rowmap) {
@@ -540,7 +542,7 @@ static int launch_step_pythia(sm_machine* m, int parts, hipEvent_t hs, hipEvent_
         {
             AttArgs a{};
             const size_t per = (size_t)m->B * m->ctx;
-            a.QKV = m->QKV; a.K16 = m->K16 + l * per * 768; a.EK = m->EK + l * per * 12; a.V = m->V + l * per * 768;
+            a.QKV = m->QKV; a.K16 = m->K16 + l * per * 768; a.KM = m->KM + l * per * 12; a.EK = m->EK + l * per * 12; a.V = m->V + l * per * 768;
             a.out = m->att; a.pos = ctl + CTL_POS; a.ctx = m->ctx; a.tb = tb; a.err = ctl + CTL_ERR;
             a.rec_pos = ctl + CTL_RECPOS; a.ratt = m->r_att + l * 768;
             a.cosT = m->cosT; a.sinT = m->sinT; a.rot = m->rot; a.half = m->half; a.ehalf = m->ehalf;
@@ -642,7 +644,7 @@ static int launch_step_pythia_batched(sm_machine* m, int parts, hipEvent_t hs, h
         if (rowmap && l == 11) {   // prompt rows: the last layer only stores its keys and values
             AttArgs a{};
             const size_t per = (size_t)m->B * m->ctx;
-            a.QKV = m->QKV; a.K16 = m->K16 + l * per * 768; a.EK = m->EK + l * per * 12; a.V = m->V + l * per * 768;
+            a.QKV = m->QKV; a.K16 = m->K16 + l * per * 768; a.KM = m->KM + l * per * 12; a.EK = m->EK + l * per * 12; a.V = m->V + l * per * 768;
             a.ctx = m->ctx; a.tb = tb; a.err = ctl + CTL_ERR; a.rowmap = rowmap;
             a.cosT = m->cosT; a.sinT = m->sinT; a.rot = m->rot; a.half = m->half; a.ehalf = m->ehalf;
             k_kv_rows<1><<<dim3(12, B), 128, 0, m->st>>>(a);
@@ -665,7 +667,7 @@ static int launch_step_pythia_batched(sm_machine* m, int parts, hipEvent_t hs, h
         {   // attention with turns
             AttArgs a{};
             const size_t per = (size_t)m->B * m->ctx;
-            a.QKV = m->QKV; a.K16 = m->K16 + l * per * 768; a.EK = m->EK + l * per * 12; a.V = m->V + l * per * 768;
+            a.QKV = m->QKV; a.K16 = m->K16 + l * per * 768; a.KM = m->KM + l * per * 12; a.EK = m->EK + l * per * 12; a.V = m->V + l * per * 768;
             a.out = m->att; a.pos = ctl + CTL_POS; a.ctx = m->ctx; a.tb = tb; a.err = ctl + CTL_ERR;
             a.rec_pos = recp; a.ratt = m->r_att + l * 768; a.rowmap = rowmap;
             a.cosT = m->cosT; a.sinT = m->sinT; a.rot = m->rot; a.half = m->half; a.ehalf = m->ehalf;
@@ -746,7 +748,7 @@ static int launch_step(sm_machine* m, int parts = STEP_ALL, hipEvent_t hs = null
         {
             AttArgs a{};
             const size_t per = (size_t)m->B * m->ctx;
-            a.QKV = m->QKV; a.K16 = m->K16 + l * per * 768; a.EK = m->EK + l * per * 12; a.V = m->V + l * per * 768;
+            a.QKV = m->QKV; a.K16 = m->K16 + l * per * 768; a.KM = m->KM + l * per * 12; a.EK = m->EK + l * per * 12; a.V = m->V + l * per * 768;
             a.out = m->att; a.pos = ctl + CTL_POS; a.ctx = m->ctx; a.tb = tb; a.err = ctl + CTL_ERR;
             a.rec_pos = ctl + CTL_RECPOS; a.ratt = m->r_att + l * 768;
             if (m->B == 1) k_attend<0, 1><<<dim3(12, 1), NTHR, (size_t)m->ctx * 12, m->st>>>(a);
@@ -977,7 +979,8 @@ extern "C" int sm_create(const char* layout_dir, const sm_config* cfg, sm_machin
     const size_t nsets = m->kind == 1 && mfma ? 2 : 1;      // light-plane sets (the Pythia MFMA phases keep two)
     if ((rc = dalloc(&m->R, RC * 768)) || (rc = dalloc(&m->QKV, RC * 2304)) || (rc = dalloc(&m->att, RC * 768)) || (rc = dalloc(&m->attor, RC * 12)) ||
         (rc = dalloc(&m->hidor, RC * 192)) || (rc = dalloc(&m->sfacts, 4 * RC * 4)) ||
-        (rc = dalloc(&m->hid, RC * 3072)) || (rc = dalloc(&m->K16, 12 * B * ctx * 768)) || (rc = dalloc(&m->EK, 12 * B * ctx * 12)) ||
+        (rc = dalloc(&m->hid, RC * 3072)) || (rc = dalloc(&m->K16, 12 * B * ctx * 768)) || (rc = dalloc(&m->KM, 12 * B * ctx * 12)) ||
+        (rc = dalloc(&m->EK, 12 * B * ctx * 12)) ||
         (rc = dalloc(&m->pfmap, B * ctx)) ||
         (rc = dalloc(&m->V, 12 * B * ctx * 768)) || (rc = dalloc(&m->seq, B * (ctx + 1))) || (rc = dalloc(&m->words, B * (ctx + 1))) ||
         (rc = dalloc(&m->ctl, (size_t)CTL_N)) || (rc = dalloc(&m->part_v, nparts)) ||
@@ -1022,7 +1025,8 @@ extern "C" int sm_reset(sm_machine* m) {
     HIP_TRY(hipMemsetAsync(m->ctl, 0, CTL_N * 4, m->st));
     int rp = -1;
     HIP_TRY(hipMemcpyAsync(m->ctl + CTL_RECPOS, &rp, 4, hipMemcpyHostToDevice, m->st));
-    HIP_TRY(hipMemsetAsync(m->K16, 0, 12 * B * ctx * 768 * 4, m->st));
+    HIP_TRY(hipMemsetAsync(m->K16, 0, 12 * B * ctx * 768 * 2, m->st));
+    HIP_TRY(hipMemsetAsync(m->KM, 0, 12 * B * ctx * 12 * 8, m->st));
     HIP_TRY(hipMemsetAsync(m->EK, 0, 12 * B * ctx * 12 * 4, m->st));
     HIP_TRY(hipMemsetAsync(m->V, 0, 12 * B * ctx * 768 * 4, m->st));
     HIP_TRY(hipMemsetAsync(m->seq, 0, B * (ctx + 1) * 4, m->st));
@@ -1174,8 +1178,18 @@ extern "C" int sm_read(sm_machine* m, int32_t what, int32_t layer, int32_t strea
             const bool ek = what == SM_READ_EK;
             const size_t w = ek ? 4 : 256;
             if (bytes != 12 * w) return fail(SM_E_ARG, "sm_read: expected " + std::to_string(12 * w) + " bytes");
-            const void* s0 = ek ? (const void*)(m->EK + h0) : (const void*)((what == SM_READ_K16 ? m->K16 : m->V) + h0 * 64);
             HIP_TRY(hipStreamSynchronize(m->st));
+            if (what == SM_READ_K16) {      // int16 rows and their +32768 masks back to the keys' int32 values
+                int16_t k[12][64];
+                uint64_t km[12];
+                HIP_TRY(hipMemcpy2D(k, 128, m->K16 + h0 * 64, ctx * 128, 128, 12, hipMemcpyDeviceToHost));
+                HIP_TRY(hipMemcpy2D(km, 8, m->KM + h0, ctx * 8, 8, 12, hipMemcpyDeviceToHost));
+                int32_t* out = static_cast<int32_t*>(dst);
+                for (int h = 0; h < 12; h++)
+                    for (int d = 0; d < 64; d++) out[h * 64 + d] = (int32_t)k[h][d] + (int32_t)((km[h] >> d) & 1);
+                return SM_OK;
+            }
+            const void* s0 = ek ? (const void*)(m->EK + h0) : (const void*)(m->V + h0 * 64);
             HIP_TRY(hipMemcpy2D(dst, w, s0, ctx * w, w, 12, hipMemcpyDeviceToHost));
             return SM_OK;
         }
@@ -1287,15 +1301,15 @@ extern "C" int sm_stage_race(const int64_t* v, int64_t n, int64_t* out_index, vo
     HIP_TRY(hipGetLastError());
     return SM_OK;
 }
-extern "C" int sm_stage_attend(const sm_tables* t, const int64_t* qkv, int32_t* k16, int32_t* ek, int32_t* v, int32_t pos,
-                               int32_t ctx, int64_t* out, void* stream) {
-    if (!t || !qkv || !k16 || !ek || !v || !out || ctx <= 0 || pos < 0 || pos >= ctx || ctx > 8192)
+extern "C" int sm_stage_attend(const sm_tables* t, const int64_t* qkv, int16_t* k16, int64_t* km, int32_t* ek, int32_t* v,
+                               int32_t pos, int32_t ctx, int64_t* out, void* stream) {
+    if (!t || !qkv || !k16 || !km || !ek || !v || !out || ctx <= 0 || pos < 0 || pos >= ctx || ctx > 8192)
         return fail(SM_E_ARG, "sm_stage_attend: arguments");
     hipStream_t s = (hipStream_t)stream;
     HIP_TRY(hipMemcpyAsync(t->scratch, &pos, 4, hipMemcpyHostToDevice, s));
     HIP_TRY(hipStreamSynchronize(s));
     AttArgs a{};
-    a.QKV = (const i64*)qkv; a.K16 = k16; a.EK = ek; a.V = v; a.out = (i64*)out; a.pos = t->scratch; a.ctx = ctx;
+    a.QKV = (const i64*)qkv; a.K16 = k16; a.KM = (i64*)km; a.EK = ek; a.V = v; a.out = (i64*)out; a.pos = t->scratch; a.ctx = ctx;
     a.tb = t->tb(); a.err = t->scratch + 1;
     k_attend<0, 1><<<dim3(12, 1), NTHR, (size_t)ctx * 12, s>>>(a);
     HIP_TRY(hipGetLastError());

@@ -68,7 +68,7 @@ def lib():
         L.sm_stage_to16.argtypes = [vp, i32, i32, vp, vp, vp]
         L.sm_stage_gauge_log.argtypes = [vp, vp, i32, vp, vp, vp, vp]
         L.sm_stage_race.argtypes = [vp, i64, vp, vp]
-        L.sm_stage_attend.argtypes = [vp, vp, vp, vp, vp, i32, i32, vp, vp]
+        L.sm_stage_attend.argtypes = [vp, vp, vp, vp, vp, vp, i32, i32, vp, vp]
         L.sm_plate_create.argtypes = [ctypes.POINTER(ctypes.c_int16), i32p, i64p, i32, i32, i32, ctypes.POINTER(vp)]
         L.sm_plate_destroy.argtypes = [vp]
         L.sm_plate_product.argtypes = [vp, vp, vp, i32, vp]
@@ -275,5 +275,7 @@ class stages:
         check(lib().sm_stage_race(v, n, out, stream))
 
     @staticmethod
-    def attend(t: Tables, qkv, k16, ek, v, pos, ctx, out, stream=0):
-        check(lib().sm_stage_attend(t.h, qkv, k16, ek, v, pos, ctx, out, stream))
+    def attend(t: Tables, qkv, k16, km, ek, v, pos, ctx, out, stream=0):
+        """k16: int16 [12][ctx][64] keys (+32768 held as 32767), km: int64 [12][ctx] masks of the +32768
+        dimensions, ek: int32 [12][ctx], v: int32 [12][ctx][64] (device pointers; zeroed = empty)"""
+        check(lib().sm_stage_attend(t.h, qkv, k16, km, ek, v, pos, ctx, out, stream))

@@ -173,13 +173,15 @@ def test_plate_product(sm, nin, nout, tc):
 def _attend_all(sm, dtabs, QKV, ctx):
     """run the device attention position by position over QKV rows (the cache fills as it goes)"""
     P = len(QKV)
-    k16 = torch.zeros((ctx, 768), dtype=torch.int32, device="cuda")
+    k16 = torch.zeros((ctx, 768), dtype=torch.int16, device="cuda")
+    km = torch.zeros((ctx, 12), dtype=torch.int64, device="cuda")
     ek = torch.zeros((ctx, 12), dtype=torch.int32, device="cuda")
     v = torch.zeros((ctx, 768), dtype=torch.int32, device="cuda")
     dq = dev(QKV)
     out = torch.zeros((P, 768), dtype=torch.int64, device="cuda")
     for p in range(P):
-        sm.stages.attend(dtabs, dq[p].data_ptr(), k16.data_ptr(), ek.data_ptr(), v.data_ptr(), p, ctx, out[p].data_ptr())
+        sm.stages.attend(dtabs, dq[p].data_ptr(), k16.data_ptr(), km.data_ptr(), ek.data_ptr(), v.data_ptr(), p, ctx,
+                         out[p].data_ptr())
     return host(out)
 
 
@@ -192,6 +194,31 @@ def test_attention_golden(sm, dtabs, golden):
         bad = [i for i, (a, b) in enumerate(zip(rows, case["row_sha16"])) if a != b]
         assert not bad, f"P={case['P']}: first differing row {bad[:5]}"
         assert h64(A) == case["out_sha256"]
+
+
+def test_attention_extreme_keys(sm, dtabs, small_oracle):
+    """keys at the ends of the 16-bit range, +32768 (held as 32767 with its mask bit) and -32768, in the
+    short path (p < 64), the general one and the long-context ring (p >= 128), against the oracle"""
+    rng = np.random.default_rng(21)
+    P = 200
+    Q = np.round(rng.standard_normal((P, 2304)) * 0.5 * 65536).astype(np.int64)
+    for p in range(0, P, 3):
+        for h in range(0, 12, 1 + p % 4):
+            k = Q[p, 768 + 64 * h: 768 + 64 * h + 64]
+            k[:] = rng.integers(-2 ** 19, 2 ** 19, 64)
+            k[(p + h) % 64] = 2 ** 21 - 1               # to16 (shift 6): +32768
+            k[(p + 3 * h + 1) % 64] = 1 - 2 ** 21       # -32768
+            if p % 2:
+                k[(p + 7) % 64] = 2 ** 21 - 1            # two +32768 in one row
+            if p % 5 == 0:
+                q = Q[p, 64 * h: 64 * h + 64]          # q at +32768 and -32768 too
+                q[:] = rng.integers(-2 ** 19, 2 ** 19, 64)
+                q[(p + h) % 64] = 2 ** 21 - 1
+                q[(p + 3 * h + 1) % 64] = 1 - 2 ** 21
+    want = small_oracle.attention(Q)
+    got = _attend_all(sm, dtabs, Q, 256)
+    bad = [i for i in range(P) if not np.array_equal(got[i], want[i])]
+    assert not bad, f"first differing positions {bad[:5]}"
 
 
 def test_attention_overflow_flag(sm, dtabs):
