@@ -578,6 +578,9 @@ __global__ __launch_bounds__(256, 2) void k_head_rows(GemmArgs a) {     // two b
     __shared__ i64 rc[64][3];         // per row: the pile's row terms, the power's row part, its factor
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int p = a.pos ? *a.pos : 0;
+    // stream 0's record position (-1: none; both pointers may be null), read here with the position (a read
+    // behind the tiles would wait for the tiles)
+    const int rpos = a.rec_pos ? *a.rec_pos : -1;
     if ((EPI == EPI_HEAD || EPI == EPI_PHEAD) && p < *a.plen - 1) return;
     const int ntiles = (a.N + 15) >> 4, G = gridDim.x;
     // the row facts first (row tid): ex, LS, the power factor (EPI_HEAD: the producing light kernel turned S1, S2
@@ -615,7 +618,11 @@ __global__ __launch_bounds__(256, 2) void k_head_rows(GemmArgs a) {     // two b
     v4 xh[KS], xl[KS];
 #pragma unroll
     for (int s = 0; s < KS; s++) { xh[s] = Ab[s * 192]; xl[s] = Ab[s * 192 + 64]; }
+    // the loads stay issued in this order: the row facts would otherwise sink into the branch below that uses
+    // them, behind the tiles, and a plane load moved behind the second tile would make the planes' wait cover it
+    __builtin_amdgcn_sched_barrier(0);
     gfetch(r1, blockIdx.x + G);
+    __builtin_amdgcn_sched_barrier(0);
     // row tid's constants: pile = 65536 HH + 256 MID + LL + C_row + 32768 SWh + 128 SWl; the gauged logit
     // power(pile, (we + ex + 16) 65536 - LS) + b = rshift(pile e2, 16 - we - (F_row >> 16)) + b with
     // F_row = (ex + 16) 65536 - LS (base2.py:70, 108); Pythia's plain logit rshift(pile, -(we + ex + 16))
@@ -629,8 +636,13 @@ __global__ __launch_bounds__(256, 2) void k_head_rows(GemmArgs a) {     // two b
             rc[tid][1] = (i64)rf0[0] + 16;
         }
     }
+    // the light planes are in before the tile loop starts (the second tile stays in flight): inside the loop the
+    // wait for them would otherwise be the loop's first use, and in every trip it would also wait for the tile
+    // requested one half-trip earlier
+#pragma unroll
+    for (int s = 0; s < KS; s++) asm volatile("" ::"v"(xh[s]), "v"(xl[s]));
     const bool corr = live && ((__ballot(n32 != 0) >> (16 * t)) & 0xFFFFull);   // a +32768 light in the row tile
-    const bool rec0 = a.rec_pos && *a.rec_pos == p;
+    const bool rec0 = rpos == p;
     i64 bv[4];
     int bi[4];
 #pragma unroll
