@@ -469,6 +469,14 @@ SMD void attend_short(const AttArgs& a, int p, int h, int b, int* q_s, int* w_s)
     i64 qv = qkv[MODEL == 1 ? h * 192 + lane : h * 64 + lane];
     i64 kv = qkv[MODEL == 1 ? h * 192 + 64 + lane : 768 + h * 64 + lane];
     const i64 vv = qkv[MODEL == 1 ? h * 192 + 128 + lane : 1536 + h * 64 + lane];
+    // Pythia: the turn's cos and sin for dimension lane, ahead of the cached rows (lanes past rot read zeros)
+    int tcos = 0, tsin = 0;
+    if constexpr (MODEL == 1) {
+        const int r = a.rot >> 1, ti = lane < r ? lane : lane - r;
+        const unsigned lim = (unsigned)((p + 1) * r) * 4u, off = (unsigned)(p * r + ti) * 4u;
+        tcos = buf_load1(buf_rsrc(a.cosT, lim), off);
+        tsin = buf_load1(buf_rsrc(a.sinT, lim), off);
+    }
     // the cached rows s < p (lanes and columns past p read zeros without a memory request)
     const __amdgpu_buffer_rsrc_t rk = buf_rsrc(K16, (unsigned)p * 128), re = buf_rsrc(EK, (unsigned)p * 4),
                                  rm = buf_rsrc(KM, (unsigned)p * 8), rv = buf_rsrc(V, (unsigned)p * 256);
@@ -480,14 +488,14 @@ SMD void attend_short(const AttArgs& a, int p, int h, int b, int* q_s, int* w_s)
     int vcol[64];
 #pragma unroll
     for (int s = 0; s < 64; s++) vcol[s] = buf_load1(rv, (unsigned)(s * 64 + lane) * 4);
+    if constexpr (MODEL == 1) __builtin_amdgcn_sched_barrier(0);   // (the loads above stay issued here)
     if (MODEL == 1) {                                        // the turns (pythia_base2.py:116-123)
         const int r = a.rot >> 1;
         const i64 pq = __shfl(qv, lane < r ? lane + r : lane - r, 64);
         const i64 pk = __shfl(kv, lane < r ? lane + r : lane - r, 64);
         if (lane < a.rot) {
             if (iabs64(qv) >= ((i64)1 << 31) || iabs64(kv) >= ((i64)1 << 31)) atomicOr(a.err, SM_ERR_RANGE);
-            const int i = lane < r ? lane : lane - r;
-            const i64 c = a.cosT[(size_t)p * r + i], sn = a.sinT[(size_t)p * r + i];
+            const i64 c = tcos, sn = tsin;
             qv = lane < r ? rsh(wsub(wmul(qv, c), wmul(pq, sn)), 30) : rsh(wadd(wmul(qv, c), wmul(pq, sn)), 30);
             kv = lane < r ? rsh(wsub(wmul(kv, c), wmul(pk, sn)), 30) : rsh(wadd(wmul(kv, c), wmul(pk, sn)), 30);
         }
@@ -614,6 +622,15 @@ __global__ __launch_bounds__(NTHR, ONE ? 1 : 3) void k_attend(AttArgs a) {
     // 16 qd .. + 15), their water levels and masks; the values (16 lanes a 256-byte row, four rows a wave)
     // follow once the new position is in
     i64 xnew = wave < 3 ? qkv[MODEL == 1 ? h * 192 + wave * 64 + lane : wave * 768 + h * 64 + lane] : 0;
+    // Pythia: the turn's cos and sin of dimension lane (lanes < rot) with the new position, ahead of the keys, so
+    // that the turn waits for them alone (row p of the [npos][rot / 2] tables; other lanes read past it: zeros)
+    int tcos = 0, tsin = 0;
+    if constexpr (MODEL == 1) {
+        const int r = a.rot >> 1, ti = lane < r ? lane : lane - r;
+        const unsigned lim = (unsigned)((p + 1) * r) * 4u, off = (unsigned)(p * r + ti) * 4u;
+        tcos = buf_load1(buf_rsrc(a.cosT, lim), off);
+        tsin = buf_load1(buf_rsrc(a.sinT, lim), off);
+    }
     // (buffer loads bounded at position p: rows past it read zeros and cost no memory traffic)
     const __amdgpu_buffer_rsrc_t rk = buf_rsrc(K16, (unsigned)p * 128), re = buf_rsrc(EK, (unsigned)p * 4),
                                  rm = buf_rsrc(KM, (unsigned)p * 8), rv = buf_rsrc(V, (unsigned)p * 256);
@@ -629,13 +646,14 @@ __global__ __launch_bounds__(NTHR, ONE ? 1 : 3) void k_attend(AttArgs a) {
         ekp[c] = buf_load1(re, sr * 4);
         kmp[c] = buf_load8(rm, sr * 8);
     }
+    // (the loads above stay issued here, ahead of the branches that use the turn's tables)
+    if constexpr (MODEL == 1) __builtin_amdgcn_sched_barrier(0);
     if (MODEL == 1 && wave < 2) {        // the turns (pythia_base2.py:116-123): pair (i, i + rot/2)
         const int r = a.rot >> 1;
         const i64 partner = __shfl(xnew, lane < r ? lane + r : lane - r, 64);
         if (lane < a.rot) {
             if (iabs64(xnew) >= ((i64)1 << 31)) atomicOr(a.err, SM_ERR_RANGE);
-            const int i = lane < r ? lane : lane - r;
-            const i64 c = a.cosT[(size_t)p * r + i], sn = a.sinT[(size_t)p * r + i];
+            const i64 c = tcos, sn = tsin;
             xnew = lane < r ? rsh(wsub(wmul(xnew, c), wmul(partner, sn)), 30) : rsh(wadd(wmul(xnew, c), wmul(partner, sn)), 30);
         }
     }
