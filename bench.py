@@ -71,12 +71,17 @@ def head_bytes(vocab: int) -> int:
     return 2 * 768 * vocab + 12 * vocab
 
 
+# the KV cache read per cached position of a stream: 12 layers x (int16 k16 and int32 v per dimension, and per
+# head an int32 key water level and an int64 mask of the key's +32768 dimensions)
+KV_BYTES = 12 * (768 * 6 + 12 * 12)
+
+
 def step_bytes(vocab: int, ctx: float) -> float:
     """algorithmic bytes of one decode step: every plate once (int16), the per-column exponents and biases,
-    and the KV cache read at context ctx (int32 k16 and v per layer)"""
+    and the KV cache read at context ctx"""
     layer_w = 2 * (768 * 2304 + 768 * 768 + 768 * 3072 + 3072 * 768)
     layer_cols = 12 * (2304 + 768 + 3072 + 768)
-    return 12 * (layer_w + layer_cols) + head_bytes(vocab) + 12 * 768 * 8 * ctx
+    return 12 * (layer_w + layer_cols) + head_bytes(vocab) + KV_BYTES * ctx
 
 
 def batched_leg(sm, lay):
@@ -123,7 +128,7 @@ def batched_leg(sm, lay):
     # int8 MFMA work of one head launch: 4 byte-plane products of 64 x 768 x vocab (2 ops per multiply-add)
     ops = 4 * 2 * B_STREAMS * 768 * m.vocab
     ctx_mean = B_PROMPT + B_WORDS / 2.0
-    sb = step_bytes(m.vocab, 0) + B_STREAMS * 12 * 768 * 8 * ctx_mean
+    sb = step_bytes(m.vocab, 0) + B_STREAMS * KV_BYTES * ctx_mean
     return {"streams": B_STREAMS, "value": round(B_STREAMS * steps / dt, 1), "unit": "tokens/s",
             "ms_per_step": round(ms, 4), "steps": steps,
             "workload": f"{B_STREAMS} streams, {B_PROMPT}-token random prompts, {B_WORDS} greedy words each "
@@ -186,7 +191,7 @@ def pythia_leg(sm):
     hb = head_bytes(vocab) - 8 * vocab                 # no bias on Pythia's head
     ctx_mean = P_PROMPT + P_WORDS / 2.0
     layer_w = 12 * (2 * (768 * 2304 + 768 * 768 + 768 * 3072 + 3072 * 768) + 12 * (2304 + 768 + 3072 + 768))
-    sb = layer_w + hb + P_STREAMS * 12 * 768 * 8 * ctx_mean
+    sb = layer_w + hb + P_STREAMS * KV_BYTES * ctx_mean
     return {"streams": P_STREAMS, "value": round(P_STREAMS * steps / dt, 1), "unit": "tokens/s",
             "ms_per_step": round(ms, 4), "steps": steps,
             "workload": f"Pythia-160m-shaped integer machine, {P_STREAMS} streams, {P_PROMPT}-token random prompts, "
