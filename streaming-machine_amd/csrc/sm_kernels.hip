@@ -414,10 +414,18 @@ SMD void key_store(short* krow, i64* km, int x16, int lane) {
     const u64 m = __ballot(x16 == 32768);
     if (lane == 0) *km = (i64)m;
 }
+// q . k' by 16-bit dot products (the one-wave short path): q = 256 qh + ql with qh = q >> 8 in [-128, 128] and
+// ql = q & 255, both int16, so that over 64 dimensions sum qh k' stays below 2^28 and sum ql k' below 2^30 in
+// magnitude (|k'| <= 32768): two exact int32 sums, then 256 A + B in 64 bits.
+typedef short s2v __attribute__((ext_vector_type(2)));
+SMD int sdot2(int a, int b, int c) {
+    return __builtin_amdgcn_sdot2(__builtin_bit_cast(s2v, a), __builtin_bit_cast(s2v, b), c, false);
+}
 SMD int lo16(int w) { return (w << 16) >> 16; }
 SMD int hi16(int w) { return w >> 16; }
-// q . k' over 16 dimensions: q as four int32 quads (dimensions 0-15), k' as 16 int16 in two quads of pairs
-// (dword w of quad h: dimensions 8 h + 2 w, + 1).  Each product fits 31 bits; the sum is taken in 64.
+// q . k' over 16 dimensions (the block path): q as four int32 quads (dimensions 0-15), k' as 16 int16 in two
+// quads of pairs (dword w of quad h: dimensions 8 h + 2 w, + 1).  Each product fits 31 bits; the sum is taken
+// in 64.  (The 16-bit dot products measured slower here: the pairs of q stay live through every pass.)
 SMD i64 dot16(const v4i (&q)[4], const v4i (&k)[2]) {
     i64 d = 0;
 #pragma unroll
@@ -510,14 +518,20 @@ SMD void attend_short(const AttArgs& a, int p, int h, int b, int* q_s, int* w_s)
     V[(size_t)p * 64 + lane] = (int)vv;
     // scores (base2.py:94): lane s < p its cached row, lane p the new key
     q_s[lane] = q16;
-    i64 dot = 0;
+    // q's halves as int16 (lane = dimension) in w_s, read back as pairs (the wave's own writes, in order; the
+    // arrivals overwrite w_s later): 64 16-bit dot products per lane, two exact int32 sums
+    short* qh_s = reinterpret_cast<short*>(w_s);
+    qh_s[lane] = (short)(q16 >> 8);
+    qh_s[64 + lane] = (short)(q16 & 255);
+    int A = 0, B = 0;
 #pragma unroll
     for (int c = 0; c < 8; c++) {
-        const v4i qa = reinterpret_cast<const v4i*>(q_s)[2 * c], qb = reinterpret_cast<const v4i*>(q_s)[2 * c + 1];
+        const v4i qh = reinterpret_cast<const v4i*>(qh_s)[c], ql = reinterpret_cast<const v4i*>(qh_s)[8 + c];
         const v4i k = krow[c];                                         // (q: the same address in every lane)
-        dot += (i64)(qa.x * lo16(k.x)) + (i64)(qa.y * hi16(k.x)) + (i64)(qa.z * lo16(k.y)) + (i64)(qa.w * hi16(k.y)) +
-               (i64)(qb.x * lo16(k.z)) + (i64)(qb.y * hi16(k.z)) + (i64)(qb.z * lo16(k.w)) + (i64)(qb.w * hi16(k.w));
+        A = sdot2(qh.x, k.x, A); A = sdot2(qh.y, k.y, A); A = sdot2(qh.z, k.z, A); A = sdot2(qh.w, k.w, A);
+        B = sdot2(ql.x, k.x, B); B = sdot2(ql.y, k.y, B); B = sdot2(ql.z, k.z, B); B = sdot2(ql.w, k.w, B);
     }
+    i64 dot = 256 * (i64)A + B;
     for (u64 m = kml; m; m &= m - 1) dot += q_s[__builtin_ctzll(m)];   // the +32768 dimensions (rare)
     const i64 dn = wave_reduce64((i64)q16 * k16, OpAdd());
     const i64 ek = lane == p ? ekn : ekl;
