@@ -50,5 +50,7 @@ def test_step_bytes_match_the_published_accounting():
     bench = importlib.util.module_from_spec(spec)
     spec.loader.exec_module(bench)
     assert bench.step_bytes(50257, 0) == 248_662_476             # weights + exponents/biases, per token
-    assert bench.step_bytes(50257, 16) - bench.step_bytes(50257, 0) == 73_728 * 16
+    # the KV cache per cached position: 12 layers x (768 int16 keys + 768 int32 values + per head an int32 key
+    # water level and an int64 mask of the +32768 dimensions)
+    assert bench.step_bytes(50257, 16) - bench.step_bytes(50257, 0) == 12 * (768 * 6 + 12 * 12) * 16 == 57_024 * 16
     assert bench.head_bytes(50257) == 2 * 768 * 50257 + 12 * 50257
