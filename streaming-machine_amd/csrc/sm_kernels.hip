@@ -764,6 +764,15 @@ __global__ __launch_bounds__(NTHR, ONE ? 1 : 3) void k_attend(AttArgs a) {
         z += w;
     }
     z = block_reduce(z, red, OpAdd(), tid);     // its barriers also publish arr[]
+    // the divisor's table entries (base2.py:99), requested now so that their latency passes during the value sum:
+    // vector loads behind the values (scalar reads would share the LDS reads' wait counter, and the value sum's
+    // first LDS read would wait for them); read unconditionally, the recomputed entries replace them where the
+    // tables verified
+    int zt; i64 zm;
+    log2_parts(z, zt, zm);
+    const int zmu = __builtin_amdgcn_readfirstlane((int)zm);
+    const int zlg_mem = buf_load1(buf_rsrc(a.tb.LOG2, 65536u * 4u), (unsigned)zmu * 4u);
+    const int zhp_mem = buf_load1(buf_rsrc(a.tb.HPOW, 65536u * 4u), (unsigned)zmu * 4u);
 
     // the value sums of dimensions 4 d4 .. + 3 over positions g, g + 16, .. (base2.py:98)
     i64 n0 = 0, n1 = 0, n2 = 0, n3 = 0;
@@ -801,19 +810,19 @@ __global__ __launch_bounds__(NTHR, ONE ? 1 : 3) void k_attend(AttArgs a) {
         i64 tot = 0;
 #pragma unroll
         for (int i = 0; i < 16; i++) tot += numr[i][lane];
-        int t; i64 m;
-        log2_parts(z, t, m);
-        const i64 F = wsub(0, wadd((i64)t * 65536, utab_log2(a.tb, (int)m)));   // -log2fix(Z), Z the same in every lane
+        const i64 zlg = a.tb.arith ? (i64)log2_entry(zmu) : (i64)zlg_mem;
+        const i64 zhp = a.tb.arith ? (i64)exp2_entry((int)((-(i64)log2_entry(zmu)) & 0xFFFF)) : (i64)zhp_mem;
+        const i64 F = wsub(0, wadd((i64)zt * 65536, zlg));   // -log2fix(Z), the same in every lane
         i64 o;
         if (MODEL == 1) {
             // exact: (tot EXP2[f] + 2^(s-1)) >> s with s = 16 - (F >> 16) > 16 (Z >= 2^24)
-            const __int128 X = (__int128)tot * utab_hpow(a.tb, (int)m);
+            const __int128 X = (__int128)tot * zhp;
             const i64 sft = 16 - (F >> 16);
             const __int128 r = sft >= 100 ? (__int128)0 : (X + ((__int128)1 << (sft - 1))) >> sft;
             if (r > (__int128)INT64_MAX || r < (__int128)INT64_MIN) atomicOr(a.err, SM_ERR_RANGE);
             o = (i64)r;
         } else {
-            o = power_e(tot, F, F & 0xFFFF, utab_hpow(a.tb, (int)m), a.tb);
+            o = power_e(tot, F, F & 0xFFFF, zhp, a.tb);
         }
         a.out[(size_t)b * 768 + h * 64 + lane] = o;
         if (a.out_or) {
