@@ -5,13 +5,12 @@
 // prologue: how a phase forms its 16-bit light from the row it reads
 enum { PRO_GAUGE = 0,   // gauge_log of the stream row R (768): x16, ex, LS (base2.py:55-60)
        PRO_TO16 = 1,    // to16 of an activation row (768 or 3072): x16, ex (base2.py:24-27)
-       PRO_EMBED = 2,   // the word enters: R = wte[word] + wpe[pos] (base2.py:103), then PRO_GAUGE
+       PRO_EMBED = 2,   // batched lights: the word enters, R = wte[word] + wpe[pos] (base2.py:103), then PRO_GAUGE
        PRO_X16 = 3,     // the light is given (int64 x16 values, ex = -16): the raw product test
        // batched streams: the producing bank's epilogue from its partial accumulators, then the light
        PRO_ADD_GAUGE = 4,   // R += rshift(pile, -(we + ex + 16)) + b, then PRO_GAUGE of R   (base2.py:105-106, 55-60)
        // the Pythia machine (foundation0/pythia_base2.py)
-       PRO_PGAUGE = 6,      // its gauge with the norm's gain and offset, then to16 of that row     (:100-110, 113)
-       PRO_PEMBED = 7 };    // R = rshift(embed.w[word], -(embed.e[word] + 16)) (:153), then PRO_PGAUGE
+       PRO_PGAUGE = 6 };    // its gauge with the norm's gain and offset, then to16 of that row     (:100-110, 113)
 // epilogue: what a phase does with each finished pile
 enum { EPI_GAUGED = 0,       // power(pile, (we + ex + 16) 65536 - LS) + b          (base2.py:70-71)
        EPI_GAUGED_EDGE = 1,  // the same, then the edge                               (base2.py:106, 78-83)
@@ -45,25 +44,32 @@ struct GemvArgs {
     const int* we;              // per-column power of two
     const i64* bias;            // per-column bias (2^-16)
     int nout, ntiles;
-    const i64* X;               // the row this phase reads (PRO_GAUGE / PRO_TO16 / PRO_X16)
-    const i64* wte; const i64* wpe;   // PRO_EMBED
-    const int* seq;             // [ctx] word per position (PRO_EMBED reads seq[pos])
-    const int* pos;             // device position counter
-    i64* Rw;                    // PRO_EMBED: block 0 writes the entering row here
+    const i64* X;               // the row this phase reads (PRO_GAUGE / PRO_TO16 / PRO_X16 / PRO_PGAUGE)
     i64* Y;                     // output row (or the stream R for EPI_PLAIN_ADD)
+    const i64* Yb;              // EPI_PLAIN_ADD: the row added to (null: Y itself; layer 0: the entering row)
     Tables tb;
-    // record slot for this phase (layer l, bank k) or null
+    // record slot for this phase (layer l, bank k) or null; read only by the REC = 1 instantiations
     i64* rx16; i64* rexls; i64* rpile; i64* rout;
+    const int* pos;             // device position counter
     const int* rec_pos;         // record when the position equals *rec_pos
-    // head only
-    i64* part_v; int* part_i; unsigned* counter;
-    int* seq_w; const int* plen; int* pos_w; int* words; int* nwords;
+    // head only: each block's best word
+    i64* part_v; int* part_i;
     i64* rlogits;
-    // the Pythia machine: the norm this phase's gauge uses, the embed table, extra record slots
+    // the Pythia machine: the norm this phase's gauge uses, extra record slots
     const int* ng; const i64* nb; int nge;     // gain (16 places), offset (2^-16), the gain's power of two
-    const short* ew; const int* ee;            // embed.w [vocab][768], embed.e [vocab]
     i64* rg;                                   // record: the gauge's output row
     i64* rout2;                                // record: EPI_PLAIN_EDGE's row after the edge (rout: before)
+};
+
+// Batch 1: the race over the head blocks' bests, the word fed back, and the next position's entering row
+// (base2.py:103: wte[word] + wpe[p]; foundation0/pythia_base2.py:153: rshift(embed.w[word], -(embed.e[word] + 16)))
+struct Race1Args {
+    const i64* part_v; const int* part_i; int nblk;
+    int* seq; int* words; int* pos; const int* plen; int* nwords;
+    i64* R0;                    // the entering row of the next position
+    int npos;                   // rows of the position table (GPT-2): no entering row past it
+    const i64* wte; const i64* wpe;             // GPT-2
+    const short* ew; const int* ee;             // Pythia
 };
 
 struct AttArgs {

@@ -54,30 +54,9 @@ SMD void block_sum2(i64& a, i64& b, i64* red, int tid) {
 template <int NIN, int NT, int PRO>
 SMD void prologue_load(const GemvArgs& a, int tid, i64 (&v)[NIN / NT], int (&gq)[NIN / NT], i64 (&bq)[NIN / NT]) {
     constexpr int PER = NIN / NT;
-    if (PRO == PRO_PEMBED) {
-        const int p = *a.pos;
-        const i64 tok = a.seq[p];
-        const i64 es = -((i64)a.ee[tok] + 16);
 #pragma unroll
-        for (int m = 0; m < PER; m++) {
-            int i = tid + NT * m;
-            v[m] = rsh((i64)a.ew[tok * 768 + i], es);
-            if (blockIdx.x == 0) a.Rw[i] = v[m];
-        }
-    } else if (PRO == PRO_EMBED) {
-        const int p = *a.pos;
-        const i64 tok = a.seq[p];
-#pragma unroll
-        for (int m = 0; m < PER; m++) {
-            int i = tid + NT * m;
-            v[m] = wadd(a.wte[tok * 768 + i], a.wpe[(i64)p * 768 + i]);
-            if (blockIdx.x == 0) a.Rw[i] = v[m];
-        }
-    } else {
-#pragma unroll
-        for (int m = 0; m < PER; m++) v[m] = a.X[tid + NT * m];
-    }
-    if (PRO == PRO_PGAUGE || PRO == PRO_PEMBED) {
+    for (int m = 0; m < PER; m++) v[m] = a.X[tid + NT * m];
+    if (PRO == PRO_PGAUGE) {
 #pragma unroll
         for (int m = 0; m < PER; m++) { gq[m] = a.ng[tid + NT * m]; bq[m] = a.nb[tid + NT * m]; }
     }
@@ -180,7 +159,7 @@ SMD void prologue(const GemvArgs& a, int tid, const i64 (&v)[NIN / NT], short* x
         if (rec && a.rx16) a.rx16[i] = xi;
     }
     i64 ls = 0, e2 = 0;
-    if (PRO == PRO_GAUGE || PRO == PRO_EMBED) {
+    if (PRO == PRO_GAUGE) {
         const int w1 = wave_add32(s1), w2h = wave_add32((int)(s2 >> 16)), w2l = wave_add32((int)(s2 & 0xFFFF));
         if (lane == 0) { red[32 + 3 * wave] = w1; red[33 + 3 * wave] = w2h; red[34 + 3 * wave] = w2l; }
         __syncthreads();
@@ -232,7 +211,9 @@ SMD i64 wtile_partial(const v4i (&w)[U], const short* xh_s, const short* xl_s, i
 // so after the block's prologue no block barrier is needed: a wave loads its tile, forms its TC piles with DPP
 // steps, and lanes 16 - TC .. 15 apply the epilogue of one column each.  The next tile of the wave (if any)
 // is in flight while the current one is reduced.
-template <int NIN, int TC, int WPB, int PRO, int EPI>
+// The first memory requests are the row and the first tile: nothing the kernel reads depends on another read
+// (the position is not needed; REC = 1 instantiations, launched only for a recorded step, compare it).
+template <int NIN, int TC, int WPB, int PRO, int EPI, int REC>
 __global__ __launch_bounds__(64 * WPB) void k_gemv(GemvArgs a) {
     constexpr int NT = 64 * WPB, U = WaveTile<NIN, TC>::U;
     static_assert(NIN % NT == 0, "the block's threads must split the light row evenly");
@@ -245,19 +226,11 @@ __global__ __launch_bounds__(64 * WPB) void k_gemv(GemvArgs a) {
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int col = lane - (16 - TC);                 // the column this lane finishes (valid when 0 <= col < TC)
     const bool fin = col >= 0 && col < TC;
-
     constexpr bool HEAD = EPI == EPI_HEAD || EPI == EPI_PHEAD;
-    bool skip = false;
-    int p = 0;
-    if (HEAD) {
-        p = *a.pos;
-        skip = p < *a.plen - 1;     // a prompt position whose next word is already known
-    }
-    const bool rec = a.rec_pos && *a.rec_pos == (HEAD ? p : (a.pos ? *a.pos : -2));
 
     i64 best_v = 0;
     int best_i = -1;
-    if (!skip) {
+    {
         const int gw = blockIdx.x * WPB + wave, nw = gridDim.x * WPB;
         // two named buffers in turn (no register copies, so a prefetch in flight is never waited on early);
         // a tile's exponents and biases are requested before its weights, so waiting for the small loads
@@ -281,8 +254,9 @@ __global__ __launch_bounds__(64 * WPB) void k_gemv(GemvArgs a) {
         int ngq[NIN / NT];
         prologue_load<NIN, NT, PRO>(a, tid, row, ngq, nbq);   // the row first, then this wave's first tile
         fetch(wA, eA, bA, tile);                         // unconditional (clamped): no branch for the wait count to merge
+        const bool rec = REC && a.rec_pos && *a.rec_pos == (a.pos ? *a.pos : -2);
         i64 ex, ls = 0, e2 = 0;
-        if constexpr (PRO == PRO_PGAUGE || PRO == PRO_PEMBED)
+        if constexpr (PRO == PRO_PGAUGE)
             prologue_py<NT>(a, tid, row, ngq, nbq, xh_s, xl_s, red, ex, rec && blockIdx.x == 0);
         else
             prologue<NIN, NT, PRO>(a, tid, row, xh_s, xl_s, red, ex, ls, e2, rec && blockIdx.x == 0);
@@ -295,7 +269,7 @@ __global__ __launch_bounds__(64 * WPB) void k_gemv(GemvArgs a) {
                 if (EPI == EPI_PILE) {
                     a.Y[j] = pile;
                 } else if (EPI == EPI_PLAIN_ADD) {
-                    const i64 r = wadd(a.Y[j], wadd(rsh(pile, -(wec + ex + 16)), bc));
+                    const i64 r = wadd(a.Yb[j], wadd(rsh(pile, -(wec + ex + 16)), bc));
                     a.Y[j] = r;
                     if (rec && a.rout) a.rout[j] = r;
                 } else if (EPI == EPI_PLAIN || EPI == EPI_PLAIN_EDGE || EPI == EPI_PHEAD) {
@@ -336,10 +310,10 @@ __global__ __launch_bounds__(64 * WPB) void k_gemv(GemvArgs a) {
             tile = t2;
         }
     }
-    if (!HEAD) return;
+    if constexpr (!HEAD) return;
 
-    // ---- the race (base2.py:34-40, 114): largest logit, ties to the lowest word ----
-    // wave: the TC finishing lanes; block: the waves; grid: the last block to arrive
+    // ---- this block's part of the race (base2.py:34-40, 114): largest logit, ties to the lowest word ----
+    // wave: the TC finishing lanes; block: the waves; the grid's race is its own kernel (k_race1)
 #pragma unroll
     for (int o = 1; o < TC; o <<= 1) {
         const i64 ov = __shfl_xor(best_v, o, 64);
@@ -348,60 +322,101 @@ __global__ __launch_bounds__(64 * WPB) void k_gemv(GemvArgs a) {
     }
     if (lane == 16 - TC) { bestv[wave] = best_v; besti[wave] = best_i; }
     __syncthreads();
-    if (!a.counter) {       // the race finishes in its own kernel (k_race_rows): this block's best only
-        if (tid == 0 && !skip) {
-            i64 bv = 0; int bi = -1;
-            for (int w = 0; w < WPB; w++)
-                if (besti[w] >= 0 && (bi < 0 || bestv[w] > bv || (bestv[w] == bv && besti[w] < bi))) { bv = bestv[w]; bi = besti[w]; }
-            a.part_v[blockIdx.x] = bv;
-            a.part_i[blockIdx.x] = bi;
-        }
-        return;
-    }
-    __shared__ int last;
     if (tid == 0) {
         i64 bv = 0; int bi = -1;
         for (int w = 0; w < WPB; w++)
             if (besti[w] >= 0 && (bi < 0 || bestv[w] > bv || (bestv[w] == bv && besti[w] < bi))) { bv = bestv[w]; bi = besti[w]; }
         a.part_v[blockIdx.x] = bv;
         a.part_i[blockIdx.x] = bi;
-        __threadfence();
-        const unsigned prev = atomicAdd(a.counter, 1u);
-        last = (prev == gridDim.x - 1);
+    }
+}
+
+// Batch 1, after the head: the race over its blocks' bests (base2.py:34-40, 114; ties to the lowest word), the
+// word fed straight back (base2_stream.swift:143-146), the position advanced, and the next position's entering
+// row R0 written (GPT-2 base2.py:103: wte[word] + wpe[p]; Pythia foundation0/pythia_base2.py:153:
+// rshift(embed.w[word], -(embed.e[word] + 16))), so that the next step's first phase reads a plain row.  At a
+// prompt position the next word is the prompt's.  The bests are requested before the position is read.
+template <int MODEL>
+__global__ __launch_bounds__(256) void k_race1(Race1Args a) {
+    __shared__ i64 bvs[4];
+    __shared__ int bis[4];
+    __shared__ int tok_s;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    constexpr int PER = 4;                              // bests a thread reads (nblk <= 1024)
+    i64 pv[PER];
+    int pi[PER];
+#pragma unroll
+    for (int k = 0; k < PER; k++) {
+        const int g = tid + 256 * k;
+        pv[k] = g < a.nblk ? a.part_v[g] : 0;
+        pi[k] = g < a.nblk ? a.part_i[g] : -1;
+    }
+    const int p = *a.pos, plen = *a.plen;
+    const bool known = p < plen - 1;                    // a prompt position: the next word is the prompt's
+    const int q = p + 1;                                // the next position
+    const bool embed = q < a.npos;
+    i64 wp[3] = {0, 0, 0};
+    if (MODEL == 0 && embed) {
+#pragma unroll
+        for (int m = 0; m < 3; m++) wp[m] = a.wpe[(size_t)q * 768 + tid + 256 * m];
+    }
+    i64 bv = 0; int bi = -1;
+#pragma unroll
+    for (int k = 0; k < PER; k++)
+        if (pi[k] >= 0 && (bi < 0 || pv[k] > bv || (pv[k] == bv && pi[k] < bi))) { bv = pv[k]; bi = pi[k]; }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        const i64 ov = __shfl_xor(bv, o, 64);
+        const int oi = __shfl_xor(bi, o, 64);
+        if (oi >= 0 && (bi < 0 || ov > bv || (ov == bv && oi < bi))) { bv = ov; bi = oi; }
+    }
+    if (lane == 0) { bvs[wave] = bv; bis[wave] = bi; }
+    __syncthreads();
+    if (tid == 0) {
+        bv = bvs[0]; bi = bis[0];
+        for (int w = 1; w < 4; w++)
+            if (bis[w] >= 0 && (bi < 0 || bvs[w] > bv || (bvs[w] == bv && bis[w] < bi))) { bv = bvs[w]; bi = bis[w]; }
+        int tok;
+        if (known) {
+            tok = a.seq[q];
+        } else {
+            tok = bi;
+            a.seq[q] = bi;
+            a.words[q - plen] = bi;
+        }
+        tok_s = tok;
+        *a.nwords = q - plen + 1;
+        *a.pos = q;
     }
     __syncthreads();
-    if (!last) return;
-    // the last block: every partial is visible (fence before each arrival, fence after ours)
-    __threadfence();
-    if (!skip) {
-        i64 bv = 0; int bi = -1;
-        for (int g = tid; g < (int)gridDim.x; g += NT) {
-            const i64 v = __hip_atomic_load(&a.part_v[g], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            const int ci = __hip_atomic_load(&a.part_i[g], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            if (ci >= 0 && (bi < 0 || v > bv || (v == bv && ci < bi))) { bv = v; bi = ci; }
-        }
+    if (!embed) return;
+    const size_t tok = (size_t)tok_s;
+    if (MODEL == 0) {
 #pragma unroll
-        for (int o = 32; o > 0; o >>= 1) {
-            const i64 ov = __shfl_xor(bv, o, 64);
-            const int oi = __shfl_xor(bi, o, 64);
-            if (oi >= 0 && (bi < 0 || ov > bv || (ov == bv && oi < bi))) { bv = ov; bi = oi; }
-        }
-        __syncthreads();
-        if (lane == 0) { bestv[wave] = bv; besti[wave] = bi; }
-        __syncthreads();
-        if (tid == 0) {
-            bv = bestv[0]; bi = besti[0];
-            for (int w = 1; w < WPB; w++)
-                if (besti[w] >= 0 && (bi < 0 || bestv[w] > bv || (bestv[w] == bv && besti[w] < bi))) { bv = bestv[w]; bi = besti[w]; }
-            a.seq_w[p + 1] = bi;                  // the word goes straight back in (base2_stream.swift:143-146)
-            const int n = p + 1 - *a.plen;
-            if (n >= 0) a.words[n] = bi;
-            *a.nwords = n + 1;
-        }
+        for (int m = 0; m < 3; m++) a.R0[tid + 256 * m] = wadd(a.wte[tok * 768 + tid + 256 * m], wp[m]);
+    } else {
+        const i64 es = -((i64)a.ee[tok] + 16);
+#pragma unroll
+        for (int m = 0; m < 3; m++) a.R0[tid + 256 * m] = rsh((i64)a.ew[tok * 768 + tid + 256 * m], es);
     }
-    if (tid == 0) {
-        *a.pos_w = p + 1;
-        *a.counter = 0u;
+}
+
+// Batch 1: the entering row of the current position (the first step of a run; later steps' rows come from the race)
+template <int MODEL>
+__global__ __launch_bounds__(256) void k_embed1(Race1Args a) {
+    const int tid = threadIdx.x;
+    const int p = *a.pos;
+    const size_t tok = (size_t)a.seq[p];
+    if (MODEL == 0) {
+#pragma unroll
+        for (int m = 0; m < 3; m++) {
+            const int i = tid + 256 * m;
+            a.R0[i] = wadd(a.wte[tok * 768 + i], a.wpe[(size_t)p * 768 + i]);
+        }
+    } else {
+        const i64 es = -((i64)a.ee[tok] + 16);
+#pragma unroll
+        for (int m = 0; m < 3; m++) a.R0[tid + 256 * m] = rsh((i64)a.ew[tok * 768 + tid + 256 * m], es);
     }
 }
 
@@ -463,20 +478,17 @@ SMD i64 dot16_mask(const v4i (&q)[4], unsigned mb) {
 // maximum and the arrival sum are wave reductions; lane d accumulates output dimension d from its prefetched V
 // column, the arrivals read back from LDS the same way.  Same numbers as the general path below
 // (base2.py:93-99 / pythia_base2.py:129-141).  q_s, w_s: 64 ints of LDS each.
+// Returns lane's output dimension; store: this wave writes the new key and value into the cache and reports
+// errors.
 template <int MODEL>
-SMD void attend_short(const AttArgs& a, int p, int h, int b, int* q_s, int* w_s) {
-    const int lane = threadIdx.x;
-    const i64* qkv = a.QKV + (size_t)b * 2304;
+SMD i64 attend_short(const AttArgs& a, int p, int h, int b, int* q_s, int* w_s, i64 qv, i64 kv, const i64 vv, bool store) {
+    const int lane = threadIdx.x & 63;
     const size_t hb = ((size_t)b * 12 + h) * a.ctx;         // this (stream, head)'s cache rows
     short* K16 = a.K16 + hb * 64;
     i64* KM = a.KM + hb;
     int* EK = a.EK + hb;
     int* V = a.V + hb * 64;
-    const bool rec = b == 0 && a.rec_pos && *a.rec_pos == p;
-    // the new q, k, v first (loads complete in order), then the cached rows and columns
-    i64 qv = qkv[MODEL == 1 ? h * 192 + lane : h * 64 + lane];
-    i64 kv = qkv[MODEL == 1 ? h * 192 + 64 + lane : 768 + h * 64 + lane];
-    const i64 vv = qkv[MODEL == 1 ? h * 192 + 128 + lane : 1536 + h * 64 + lane];
+    // (the new q, k, v were requested by the caller before the position was read; the cached rows follow)
     // Pythia: the turn's cos and sin for dimension lane, ahead of the cached rows (lanes past rot read zeros)
     int tcos = 0, tsin = 0;
     if constexpr (MODEL == 1) {
@@ -502,7 +514,7 @@ SMD void attend_short(const AttArgs& a, int p, int h, int b, int* q_s, int* w_s)
         const i64 pq = __shfl(qv, lane < r ? lane + r : lane - r, 64);
         const i64 pk = __shfl(kv, lane < r ? lane + r : lane - r, 64);
         if (lane < a.rot) {
-            if (iabs64(qv) >= ((i64)1 << 31) || iabs64(kv) >= ((i64)1 << 31)) atomicOr(a.err, SM_ERR_RANGE);
+            if (store && (iabs64(qv) >= ((i64)1 << 31) || iabs64(kv) >= ((i64)1 << 31))) atomicOr(a.err, SM_ERR_RANGE);
             const i64 c = tcos, sn = tsin;
             qv = lane < r ? rsh(wsub(wmul(qv, c), wmul(pq, sn)), 30) : rsh(wadd(wmul(qv, c), wmul(pq, sn)), 30);
             kv = lane < r ? rsh(wsub(wmul(kv, c), wmul(pk, sn)), 30) : rsh(wadd(wmul(kv, c), wmul(pk, sn)), 30);
@@ -512,10 +524,12 @@ SMD void attend_short(const AttArgs& a, int p, int h, int b, int* q_s, int* w_s)
     const int shq = water_shift(wave_or64(iabs64(qv))), shk = water_shift(wave_or64(iabs64(kv)));
     const int q16 = (int)rsh(qv, shq), k16 = (int)rsh(kv, shk);
     const i64 eq = -16 + shq, ekn = -16 + shk;
-    key_store(K16 + (size_t)p * 64, KM + p, k16, lane);
-    if (lane == 0) EK[p] = (int)ekn;
-    if (vv < (i64)INT32_MIN || vv > (i64)INT32_MAX) atomicOr(a.err, SM_ERR_V32);
-    V[(size_t)p * 64 + lane] = (int)vv;
+    if (store) {
+        key_store(K16 + (size_t)p * 64, KM + p, k16, lane);
+        if (lane == 0) EK[p] = (int)ekn;
+        if (vv < (i64)INT32_MIN || vv > (i64)INT32_MAX) atomicOr(a.err, SM_ERR_V32);
+        V[(size_t)p * 64 + lane] = (int)vv;
+    }
     // scores (base2.py:94): lane s < p its cached row, lane p the new key
     q_s[lane] = q16;
     // q's halves as int16 (lane = dimension) in w_s, read back as pairs (the wave's own writes, in order; the
@@ -569,24 +583,19 @@ SMD void attend_short(const AttArgs& a, int p, int h, int b, int* q_s, int* w_s)
     const int wp = __builtin_amdgcn_readlane(w, p);
     num += (i64)wp * (int)vv;
     if (MODEL == 1 && wp) vmax = max(vmax, abs((int)vv));
-    if (MODEL == 1 && (double)vmax * (double)z >= 4611686018427387904.0) atomicOr(a.err, SM_ERR_RANGE);
+    if (MODEL == 1 && store && (double)vmax * (double)z >= 4611686018427387904.0) atomicOr(a.err, SM_ERR_RANGE);
     // over the total through its log (base2.py:99)
     i64 o;
     if (MODEL == 1) {
         const __int128 X = (__int128)num * hp;
         const i64 sft = 16 - (F >> 16);
         const __int128 r = sft >= 100 ? (__int128)0 : (X + ((__int128)1 << (sft - 1))) >> sft;
-        if (r > (__int128)INT64_MAX || r < (__int128)INT64_MIN) atomicOr(a.err, SM_ERR_RANGE);
+        if (store && (r > (__int128)INT64_MAX || r < (__int128)INT64_MIN)) atomicOr(a.err, SM_ERR_RANGE);
         o = (i64)r;
     } else {
         o = power_e(num, F, F & 0xFFFF, hp, a.tb);
     }
-    a.out[(size_t)b * 768 + h * 64 + lane] = o;
-    if (a.out_or) {
-        const i64 w = wave_or64(iabs64(o));
-        if (lane == 0) a.out_or[(size_t)b * 12 + h] = w;
-    }
-    if (rec) a.ratt[h * 64 + lane] = o;
+    return o;
 }
 
 // MODEL 1 is the Pythia machine (foundation0/pythia_base2.py:125-141): per-head interleaved q, k, v at h 192;
@@ -599,7 +608,8 @@ template <bool B> struct Flag { static constexpr bool value = B; };
                              // of key slots the scores loop refills two passes ahead)
 // ONE = 1: one stream (the short-context path is available, full registers); ONE = 0: many streams, three waves
 // a SIMD so that 768 blocks are resident at once
-template <int MODEL, int ONE>
+// REC = 0: nothing is recorded (no record position is read)
+template <int MODEL, int ONE, int REC>
 __global__ __launch_bounds__(NTHR, ONE ? 1 : 3) void k_attend(AttArgs a) {
     extern __shared__ __align__(16) unsigned char smem[];
     i64* sc = reinterpret_cast<i64*>(smem);                  // [ctx] scores
@@ -614,28 +624,40 @@ __global__ __launch_bounds__(NTHR, ONE ? 1 : 3) void k_attend(AttArgs a) {
     const int sl = tid >> 2, qd = tid & 3;                   // scores: position in the pass, lane of the position
     const int d4 = tid & 15, g = tid >> 4;                   // value sum: four dimensions, position group
     const int h = blockIdx.x, b = blockIdx.y;               // b: the row (a stream, or a prompt position)
+    // requests first (vector loads complete in order): the new q, k, v (wave w < 3 its part; in the one-stream
+    // kernel wave 0 also k and v for the short path), before the position is read; then the cached keys of the
+    // first ATT_PRE passes (a position's four lanes read its 128-byte row, lane qd the 32 bytes of dimensions
+    // 16 qd .. + 15), their water levels and masks; the values (16 lanes a 256-byte row, four rows a wave)
+    // follow once the new position is in
+    const i64* qkv = a.QKV + (size_t)b * 2304;
+    auto qkv_at = [&](int part) { return MODEL == 1 ? h * 192 + part * 64 + lane : part * 768 + h * 64 + lane; };
+    i64 xnew = wave < 3 ? qkv[qkv_at(wave)] : 0;
+    i64 xk1 = 0, xv1 = 0;
+    if (ONE && wave == 0) { xk1 = qkv[qkv_at(1)]; xv1 = qkv[qkv_at(2)]; }
     const int pm = a.rowmap ? a.rowmap[b] : 0;
     const int p = a.rowmap ? pm & 0xFFFF : *a.pos, st = a.rowmap ? pm >> 16 : b;
     const bool store = !a.rowmap;                            // prompt rows: k_kv_rows stored every row's k and v
     if constexpr (ONE) {
         if (p < 64) {                                        // one stream, short context: one wave, no barriers
-            if (wave == 0) attend_short<MODEL>(a, p, h, b, q16s, vs);
+            if (wave == 0) {
+                const i64 o = attend_short<MODEL>(a, p, h, b, q16s, vs, xnew, xk1, xv1, true);
+                a.out[(size_t)b * 768 + h * 64 + lane] = o;
+                if (a.out_or) {
+                    const i64 w = wave_or64(iabs64(o));
+                    if (lane == 0) a.out_or[(size_t)b * 12 + h] = w;
+                }
+                if (REC && b == 0 && a.rec_pos && *a.rec_pos == p) a.ratt[h * 64 + lane] = o;
+            }
             return;
         }
     }
-    const i64* qkv = a.QKV + (size_t)b * 2304;
     const size_t hb = ((size_t)st * 12 + h) * a.ctx;        // this (stream, head)'s cache rows
     short* K16 = a.K16 + hb * 64;
     i64* KM = a.KM + hb;
     int* EK = a.EK + hb;
     int* V = a.V + hb * 64;
-    const bool rec = store && b == 0 && a.rec_pos && *a.rec_pos == p;
+    const bool rec = REC && store && b == 0 && a.rec_pos && *a.rec_pos == p;
 
-    // requests first (vector loads complete in order): the new q, k, v; then the cached keys of the first
-    // ATT_PRE passes (a position's four lanes read its 128-byte row, lane qd the 32 bytes of dimensions
-    // 16 qd .. + 15), their water levels and masks; the values (16 lanes a 256-byte row, four rows a wave)
-    // follow once the new position is in
-    i64 xnew = wave < 3 ? qkv[MODEL == 1 ? h * 192 + wave * 64 + lane : wave * 768 + h * 64 + lane] : 0;
     // Pythia: the turn's cos and sin of dimension lane (lanes < rot) with the new position, ahead of the keys, so
     // that the turn waits for them alone (row p of the [npos][rot / 2] tables; other lanes read past it: zeros)
     int tcos = 0, tsin = 0;
@@ -942,26 +964,31 @@ __global__ __launch_bounds__(1024) void k_stage_race(const i64* v, i64 n, i64* o
 }
 
 // ---------------------------------------------------------------------------------------------------------
-// explicit instantiations used by the host: <NIN, TC, waves per block, prologue, epilogue>
-#define INST(NIN, TC, WPB, PRO, EPI) template __global__ void k_gemv<NIN, TC, WPB, PRO, EPI>(GemvArgs);
-INST(768, 2, 4, PRO_EMBED, EPI_GAUGED)        // qkv of layer 0 (the word enters)
+// explicit instantiations used by the host: <NIN, TC, waves per block, prologue, epilogue, record>
+#define INST(NIN, TC, WPB, PRO, EPI) template __global__ void k_gemv<NIN, TC, WPB, PRO, EPI, 0>(GemvArgs); \
+    template __global__ void k_gemv<NIN, TC, WPB, PRO, EPI, 1>(GemvArgs);
 INST(768, 2, 4, PRO_GAUGE, EPI_GAUGED)        // qkv
 INST(768, 2, 2, PRO_TO16, EPI_PLAIN_ADD)      // proj
 INST(768, 2, 4, PRO_GAUGE, EPI_GAUGED_EDGE)   // fc
 INST(3072, 1, 4, PRO_TO16, EPI_PLAIN_ADD)     // mproj
 INST(768, 4, 4, PRO_GAUGE, EPI_HEAD)          // head (the race in its own kernel)
-INST(768, 2, 4, PRO_PEMBED, EPI_PLAIN)        // Pythia: qkv of layer 0
 INST(768, 2, 4, PRO_PGAUGE, EPI_PLAIN)        // Pythia: qkv
 INST(768, 2, 4, PRO_PGAUGE, EPI_PLAIN_EDGE)   // Pythia: fc
 INST(768, 4, 4, PRO_PGAUGE, EPI_PHEAD)        // Pythia: head
-template __global__ void k_attend<0, 0>(AttArgs);
-template __global__ void k_attend<0, 1>(AttArgs);
-template __global__ void k_attend<1, 0>(AttArgs);
-template __global__ void k_attend<1, 1>(AttArgs);
+template __global__ void k_attend<0, 0, 1>(AttArgs);
+template __global__ void k_attend<0, 1, 0>(AttArgs);
+template __global__ void k_attend<0, 1, 1>(AttArgs);
+template __global__ void k_attend<1, 0, 1>(AttArgs);
+template __global__ void k_attend<1, 1, 0>(AttArgs);
+template __global__ void k_attend<1, 1, 1>(AttArgs);
 template __global__ void k_kv_rows<0>(AttArgs);
 template __global__ void k_kv_rows<1>(AttArgs);
+template __global__ void k_race1<0>(Race1Args);
+template __global__ void k_race1<1>(Race1Args);
+template __global__ void k_embed1<0>(Race1Args);
+template __global__ void k_embed1<1>(Race1Args);
 // raw piles of a given light (stage entry point)
-INST(768, 2, 4, PRO_X16, EPI_PILE)
-INST(768, 8, 4, PRO_X16, EPI_PILE)
-INST(3072, 1, 4, PRO_X16, EPI_PILE)
-INST(3072, 2, 4, PRO_X16, EPI_PILE)
+template __global__ void k_gemv<768, 2, 4, PRO_X16, EPI_PILE, 0>(GemvArgs);
+template __global__ void k_gemv<768, 8, 4, PRO_X16, EPI_PILE, 0>(GemvArgs);
+template __global__ void k_gemv<3072, 1, 4, PRO_X16, EPI_PILE, 0>(GemvArgs);
+template __global__ void k_gemv<3072, 2, 4, PRO_X16, EPI_PILE, 0>(GemvArgs);

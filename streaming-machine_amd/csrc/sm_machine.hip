@@ -234,6 +234,7 @@ struct sm_machine {
     sm_tables T;
     // state
     i64 *R = nullptr, *QKV = nullptr, *att = nullptr, *hid = nullptr;
+    i64* R0 = nullptr;                                  // batch 1: the entering row of the next position
     i64* attor = nullptr;                               // [rows][12] OR of |att| over each head's values
     i64* hidor = nullptr;                               // [rows][192] OR of |hid| over each fc tile's columns
     int* sfacts = nullptr;                              // [4][rows][4] mproj's K slices' light facts
@@ -250,8 +251,8 @@ struct sm_machine {
         *r_resid = nullptr, *r_hx16 = nullptr, *r_hexls = nullptr, *r_hpile = nullptr, *r_logits = nullptr;
     i64 *r_gauge = nullptr, *r_fcpre = nullptr, *r_hgauge = nullptr;   // Pythia: gauges [L][2][768], fc before the edge
     // captured decode steps: [0] graph_steps whole steps, [1] one whole step, [2] one step's layers, [3] its head
-    hipGraphExec_t gexec[4] = {nullptr, nullptr, nullptr, nullptr};
-    hipGraph_t graph[4] = {nullptr, nullptr, nullptr, nullptr};
+    hipGraphExec_t gexec[4] = {};
+    hipGraph_t graph[4] = {};
     int gsteps = 16;
     // profiling: an event pair around each step's head kernel (the largest single launch)
     std::vector<hipEvent_t> ev_s, ev_e;
@@ -362,7 +363,7 @@ static void machine_free(sm_machine* m) {
     free_plate(m->head);
     free_mfma_plate(m->mhead);
     tables_free(m->T);
-    void* ps[] = {m->pfmap, m->planes, m->part_acc, m->rowinfo, m->wte, m->wpe, m->R, m->QKV, m->att, m->attor, m->hidor, m->sfacts, m->hid, m->K16, m->KM, m->EK, m->V, m->seq, m->words, m->ctl,
+    void* ps[] = {m->pfmap, m->planes, m->part_acc, m->rowinfo, m->wte, m->wpe, m->R, m->R0, m->QKV, m->att, m->attor, m->hidor, m->sfacts, m->hid, m->K16, m->KM, m->EK, m->V, m->seq, m->words, m->ctl,
                   m->part_v, m->part_i, m->r_x16, m->r_exls, m->r_pile, m->r_qkv, m->r_att, m->r_hid, m->r_resid,
                   m->r_hx16, m->r_hexls, m->r_hpile, m->r_logits, m->r_gauge, m->r_fcpre, m->r_hgauge,
                   m->fg, m->fb, m->ew, m->ee, m->cosT, m->sinT};
@@ -436,11 +437,9 @@ static int launch_step_batched(sm_machine* m, int parts, hipEvent_t hs, hipEvent
             if (rowmap) {
                 k_kv_rows<0><<<dim3(12, B), 128, 0, m->st>>>(a);
                 if (l == 11) break;
-                k_attend<0, 0><<<dim3(12, B), NTHR, (size_t)m->ctx * 12, m->st>>>(a);
-            } else if (m->B == 1) {
-                k_attend<0, 1><<<dim3(12, 1), NTHR, (size_t)m->ctx * 12, m->st>>>(a);
+                k_attend<0, 0, 1><<<dim3(12, B), NTHR, (size_t)m->ctx * 12, m->st>>>(a);
             } else {
-                k_attend<0, 0><<<dim3(12, m->B), NTHR, (size_t)m->ctx * 12, m->st>>>(a);
+                k_attend<0, 0, 1><<<dim3(12, m->B), NTHR, (size_t)m->ctx * 12, m->st>>>(a);
             }
         }
         {   // proj: the attention rows' light formed in the bank, the plain bank added into the stream; then the
@@ -492,18 +491,49 @@ static int launch_step_batched(sm_machine* m, int parts, hipEvent_t hs, hipEvent
 #define HEAD_TC 4
 
 // the race over the head's per-block bests, one block per stream; it also advances the position
-static void launch_race(sm_machine* m, int nblk) {
+// batch 1: the race over the head blocks' bests, the word fed back, the next position's entering row (k_race1);
+// k_embed1 writes the entering row of the current position (the first step of a run)
+static Race1Args race1_args(sm_machine* m) {
     int* ctl = m->ctl;
-    RaceArgs r{};
-    r.part_v = m->part_v; r.part_i = m->part_i; r.nblk = nblk; r.seq = m->seq; r.seq_stride = m->ctx + 1;
-    r.words = m->words; r.words_stride = m->ctx + 1; r.pos = ctl + CTL_POS; r.plen = ctl + CTL_PLEN;
-    r.nwords = ctl + CTL_NWORDS; r.counter = reinterpret_cast<unsigned*>(ctl + CTL_COUNTER);
-    k_race_rows<<<m->B, 256, 0, m->st>>>(r);
+    Race1Args r{};
+    r.part_v = m->part_v; r.part_i = m->part_i; r.nblk = m->head_grid;
+    r.seq = m->seq; r.words = m->words; r.pos = ctl + CTL_POS; r.plen = ctl + CTL_PLEN; r.nwords = ctl + CTL_NWORDS;
+    r.R0 = m->R0;
+    r.npos = m->kind == 1 ? m->ctx : m->npos;
+    r.wte = m->wte; r.wpe = m->wpe; r.ew = m->ew; r.ee = m->ee;
+    return r;
+}
+static void launch_race1(sm_machine* m) {
+    if (m->kind == 1) k_race1<1><<<1, 256, 0, m->st>>>(race1_args(m));
+    else k_race1<0><<<1, 256, 0, m->st>>>(race1_args(m));
+}
+static void launch_embed1(sm_machine* m) {
+    if (m->kind == 1) k_embed1<1><<<1, 256, 0, m->st>>>(race1_args(m));
+    else k_embed1<0><<<1, 256, 0, m->st>>>(race1_args(m));
+}
+
+// a batch-1 GEMV phase: rec selects the instantiation that records (launched only for the recorded step); an
+// event pair (hs, he) is stamped by the dispatch itself when given
+template <int NIN, int TC, int WPB, int PRO, int EPI>
+static void gemv(sm_machine* m, bool rec, int grid, const GemvArgs& a, hipEvent_t hs = nullptr, hipEvent_t he = nullptr) {
+    if (hs) {
+        if (rec) hipExtLaunchKernelGGL(k_gemv<NIN, TC, WPB, PRO, EPI, 1>, dim3(grid), dim3(64 * WPB), 0, m->st, hs, he, 0, a);
+        else hipExtLaunchKernelGGL(k_gemv<NIN, TC, WPB, PRO, EPI, 0>, dim3(grid), dim3(64 * WPB), 0, m->st, hs, he, 0, a);
+    } else if (rec) {
+        k_gemv<NIN, TC, WPB, PRO, EPI, 1><<<grid, 64 * WPB, 0, m->st>>>(a);
+    } else {
+        k_gemv<NIN, TC, WPB, PRO, EPI, 0><<<grid, 64 * WPB, 0, m->st>>>(a);
+    }
+}
+template <int MODEL>
+static void attend1(sm_machine* m, bool rec, const AttArgs& a) {
+    if (rec) k_attend<MODEL, 1, 1><<<dim3(12, 1), NTHR, (size_t)m->ctx * 12, m->st>>>(a);
+    else k_attend<MODEL, 1, 0><<<dim3(12, 1), NTHR, (size_t)m->ctx * 12, m->st>>>(a);
 }
 
 // The Pythia machine at batch 1 (foundation0/pythia_base2.py:153-160), five phases a layer.  Both gauges read
 // the stream before either half adds to it (the parallel residual R + At + Mo, :155-157): qkv and fc first.
-static int launch_step_pythia(sm_machine* m, int parts, hipEvent_t hs, hipEvent_t he) {
+static int launch_step_pythia(sm_machine* m, int parts, hipEvent_t hs, hipEvent_t he, bool rec) {
     const Tables tb = m->T.tb();
     int* ctl = m->ctl;
     for (int l = 0; l < 12 && (parts & STEP_LAYERS); l++) {
@@ -516,27 +546,25 @@ static int launch_step_pythia(sm_machine* m, int parts, hipEvent_t hs, hipEvent_
             a.rx16 = m->r_x16 + (l * 4 + k) * 3072; a.rexls = m->r_exls + (l * 4 + k) * 2;
             a.rpile = m->r_pile + (l * 4 + k) * 3072;
         };
-        // qkv: gauge ln1 of R (the word enters at layer 0), plain (:113, 130)
+        const i64* Rin = l == 0 ? m->R0 : m->R;        // layer 0 reads the entering row (k_race1 / k_embed1)
+        // qkv: gauge ln1 of R, plain (:113, 130)
         {
             GemvArgs a = base;
             const DevPlate& P = m->bank[l][0];
             plate(a, P, 0);
-            a.X = m->R; a.Y = m->QKV; a.rout = m->r_qkv + l * 2304; a.rg = m->r_gauge + (l * 2 + 0) * 768;
+            a.X = Rin; a.Y = m->QKV; a.rout = m->r_qkv + l * 2304; a.rg = m->r_gauge + (l * 2 + 0) * 768;
             a.ng = m->ng[l][0]; a.nb = m->nb[l][0]; a.nge = m->nge[l][0];
-            a.ew = m->ew; a.ee = m->ee; a.seq = m->seq; a.Rw = m->R;
-            const int g = (P.ntiles + 3) / 4;
-            if (l == 0) k_gemv<768, 2, 4, PRO_PEMBED, EPI_PLAIN><<<g, 256, 0, m->st>>>(a);
-            else k_gemv<768, 2, 4, PRO_PGAUGE, EPI_PLAIN><<<g, 256, 0, m->st>>>(a);
+            gemv<768, 2, 4, PRO_PGAUGE, EPI_PLAIN>(m, rec, (P.ntiles + 3) / 4, a);
         }
         // fc: gauge ln2 of the same R, plain, edge (:156)
         {
             GemvArgs a = base;
             const DevPlate& P = m->bank[l][2];
             plate(a, P, 2);
-            a.X = m->R; a.Y = m->hid; a.rout = m->r_fcpre + l * 3072; a.rout2 = m->r_hid + l * 3072;
+            a.X = Rin; a.Y = m->hid; a.rout = m->r_fcpre + l * 3072; a.rout2 = m->r_hid + l * 3072;
             a.rg = m->r_gauge + (l * 2 + 1) * 768;
             a.ng = m->ng[l][1]; a.nb = m->nb[l][1]; a.nge = m->nge[l][1];
-            k_gemv<768, 2, 4, PRO_PGAUGE, EPI_PLAIN_EDGE><<<(P.ntiles + 3) / 4, 256, 0, m->st>>>(a);
+            gemv<768, 2, 4, PRO_PGAUGE, EPI_PLAIN_EDGE>(m, rec, (P.ntiles + 3) / 4, a);
         }
         // attention with turns (:125-141)
         {
@@ -546,24 +574,21 @@ static int launch_step_pythia(sm_machine* m, int parts, hipEvent_t hs, hipEvent_
             a.out = m->att; a.pos = ctl + CTL_POS; a.ctx = m->ctx; a.tb = tb; a.err = ctl + CTL_ERR;
             a.rec_pos = ctl + CTL_RECPOS; a.ratt = m->r_att + l * 768;
             a.cosT = m->cosT; a.sinT = m->sinT; a.rot = m->rot; a.half = m->half; a.ehalf = m->ehalf;
-            if (m->B == 1) k_attend<1, 1><<<dim3(12, 1), NTHR, (size_t)m->ctx * 12, m->st>>>(a);
-            else k_attend<1, 0><<<dim3(12, m->B), NTHR, (size_t)m->ctx * 12, m->st>>>(a);
-        }
-        // proj: plain of the attention row, added to R (At)
-        {
-            GemvArgs a = base;
+            // proj: plain of the attention row, added to R (At; layer 0: to the entering row)
+            GemvArgs g = base;
             const DevPlate& P = m->bank[l][1];
-            plate(a, P, 1);
-            a.X = m->att; a.Y = m->R; a.rout = m->r_resid + (l * 2 + 0) * 768;
-            k_gemv<768, 2, 2, PRO_TO16, EPI_PLAIN_ADD><<<(P.ntiles + 1) / 2, 128, 0, m->st>>>(a);
+            plate(g, P, 1);
+            g.X = m->att; g.Y = m->R; g.Yb = Rin; g.rout = m->r_resid + (l * 2 + 0) * 768;
+            attend1<1>(m, rec, a);
+            gemv<768, 2, 2, PRO_TO16, EPI_PLAIN_ADD>(m, rec, (P.ntiles + 1) / 2, g);
         }
         // mproj: plain of the edge row, added to R (Mo)
         {
             GemvArgs a = base;
             const DevPlate& P = m->bank[l][3];
             plate(a, P, 3);
-            a.X = m->hid; a.Y = m->R; a.rout = m->r_resid + (l * 2 + 1) * 768;
-            k_gemv<3072, 1, 4, PRO_TO16, EPI_PLAIN_ADD><<<(P.ntiles + 3) / 4, 256, 0, m->st>>>(a);
+            a.X = m->hid; a.Y = m->R; a.Yb = m->R; a.rout = m->r_resid + (l * 2 + 1) * 768;
+            gemv<3072, 1, 4, PRO_TO16, EPI_PLAIN_ADD>(m, rec, (P.ntiles + 3) / 4, a);
         }
     }
     // head: gauge lnf, plain with no bias, race (:158-160)
@@ -576,13 +601,9 @@ static int launch_step_pythia(sm_machine* m, int parts, hipEvent_t hs, hipEvent_
         a.X = m->R;
         a.ng = m->fg; a.nb = m->fb; a.nge = m->fge; a.rg = m->r_hgauge;
         a.rx16 = m->r_hx16; a.rexls = m->r_hexls; a.rpile = m->r_hpile; a.rlogits = m->r_logits;
-        a.part_v = m->part_v; a.part_i = m->part_i; a.counter = nullptr;
-        a.plen = ctl + CTL_PLEN;
-        if (hs)
-            hipExtLaunchKernelGGL(k_gemv<768, HEAD_TC, HEAD_WPB, PRO_PGAUGE, EPI_PHEAD>, dim3(m->head_grid), dim3(64 * HEAD_WPB), 0, m->st, hs, he, 0, a);
-        else
-            k_gemv<768, HEAD_TC, HEAD_WPB, PRO_PGAUGE, EPI_PHEAD><<<m->head_grid, 64 * HEAD_WPB, 0, m->st>>>(a);
-        launch_race(m, m->head_grid);
+        a.part_v = m->part_v; a.part_i = m->part_i;
+        gemv<768, HEAD_TC, HEAD_WPB, PRO_PGAUGE, EPI_PHEAD>(m, rec, m->head_grid, a, hs, he);
+        launch_race1(m);
     }
     HIP_TRY(hipGetLastError());
     return SM_OK;
@@ -673,7 +694,7 @@ static int launch_step_pythia_batched(sm_machine* m, int parts, hipEvent_t hs, h
             a.cosT = m->cosT; a.sinT = m->sinT; a.rot = m->rot; a.half = m->half; a.ehalf = m->ehalf;
             a.out_or = m->attor;
             if (rowmap) k_kv_rows<1><<<dim3(12, B), 128, 0, m->st>>>(a);
-            k_attend<1, 0><<<dim3(12, B), NTHR, (size_t)m->ctx * 12, m->st>>>(a);
+            k_attend<1, 0, 1><<<dim3(12, B), NTHR, (size_t)m->ctx * 12, m->st>>>(a);
         }
         {   // proj: the attention rows' light formed in its bank, added into the stream (R + At)
             GemmArgs g = gemm_args(m->mbank[l][1], nullptr, nullptr);
@@ -708,7 +729,9 @@ static int launch_step_pythia_batched(sm_machine* m, int parts, hipEvent_t hs, h
     return SM_OK;
 }
 
-static int launch_step(sm_machine* m, int parts = STEP_ALL, hipEvent_t hs = nullptr, hipEvent_t he = nullptr) {
+// rec (batch 1): the step runs the kernels that record (sm_record_at's position)
+static int launch_step(sm_machine* m, int parts = STEP_ALL, hipEvent_t hs = nullptr, hipEvent_t he = nullptr,
+                       bool rec = false) {
     if (m->kind == 1 && m->B > 1) {
         const int RT = (m->B + 15) / 16;
         if (RT == 1) return launch_step_pythia_batched<1>(m, parts, hs, he);
@@ -716,7 +739,7 @@ static int launch_step(sm_machine* m, int parts = STEP_ALL, hipEvent_t hs = null
         if (RT == 3) return launch_step_pythia_batched<3>(m, parts, hs, he);
         return launch_step_pythia_batched<4>(m, parts, hs, he);
     }
-    if (m->kind == 1) return launch_step_pythia(m, parts, hs, he);
+    if (m->kind == 1) return launch_step_pythia(m, parts, hs, he, rec);
     if (m->B > 1) {
         const int RT = (m->B + 15) / 16;
         if (RT == 1) return launch_step_batched<1>(m, parts, hs, he);
@@ -731,18 +754,16 @@ static int launch_step(sm_machine* m, int parts = STEP_ALL, hipEvent_t hs = null
         base.tb = tb;
         base.pos = ctl + CTL_POS;
         base.rec_pos = ctl + CTL_RECPOS;
+        const i64* Rin = l == 0 ? m->R0 : m->R;        // layer 0 reads the entering row (k_race1 / k_embed1)
         // qkv: the stream's gauge, the product, power + bias (base2.py:105 gauged_bank(R, "qkv.l"))
         {
             GemvArgs a = base;
             const DevPlate& P = m->bank[l][0];
             a.W = reinterpret_cast<const int4*>(P.W); a.we = P.e; a.bias = P.b; a.nout = P.nout; a.ntiles = P.ntiles;
-            a.X = m->R; a.Y = m->QKV;
-            a.wte = m->wte; a.wpe = m->wpe; a.seq = m->seq; a.Rw = m->R;
+            a.X = Rin; a.Y = m->QKV;
             a.rx16 = m->r_x16 + (l * 4 + 0) * 3072; a.rexls = m->r_exls + (l * 4 + 0) * 2;
             a.rpile = m->r_pile + (l * 4 + 0) * 3072; a.rout = m->r_qkv + l * 2304;
-            const int g = (P.ntiles + 3) / 4;
-            if (l == 0) k_gemv<768, 2, 4, PRO_EMBED, EPI_GAUGED><<<g, 256, 0, m->st>>>(a);
-            else k_gemv<768, 2, 4, PRO_GAUGE, EPI_GAUGED><<<g, 256, 0, m->st>>>(a);
+            gemv<768, 2, 4, PRO_GAUGE, EPI_GAUGED>(m, rec, (P.ntiles + 3) / 4, a);
         }
         // attention (base2.py:85-100) on the KV cache of layer l
         {
@@ -751,18 +772,16 @@ static int launch_step(sm_machine* m, int parts = STEP_ALL, hipEvent_t hs = null
             a.QKV = m->QKV; a.K16 = m->K16 + l * per * 768; a.KM = m->KM + l * per * 12; a.EK = m->EK + l * per * 12; a.V = m->V + l * per * 768;
             a.out = m->att; a.pos = ctl + CTL_POS; a.ctx = m->ctx; a.tb = tb; a.err = ctl + CTL_ERR;
             a.rec_pos = ctl + CTL_RECPOS; a.ratt = m->r_att + l * 768;
-            if (m->B == 1) k_attend<0, 1><<<dim3(12, 1), NTHR, (size_t)m->ctx * 12, m->st>>>(a);
-            else k_attend<0, 0><<<dim3(12, m->B), NTHR, (size_t)m->ctx * 12, m->st>>>(a);
-        }
-        // proj: to16 of the attention row, product, plain shift + bias, added to R (base2.py:105)
-        {
-            GemvArgs a = base;
+            // proj: to16 of the attention row, product, plain shift + bias, added to R (base2.py:105; layer 0: to
+            // the entering row)
+            GemvArgs g = base;
             const DevPlate& P = m->bank[l][1];
-            a.W = reinterpret_cast<const int4*>(P.W); a.we = P.e; a.bias = P.b; a.nout = P.nout; a.ntiles = P.ntiles;
-            a.X = m->att; a.Y = m->R;
-            a.rx16 = m->r_x16 + (l * 4 + 1) * 3072; a.rexls = m->r_exls + (l * 4 + 1) * 2;
-            a.rpile = m->r_pile + (l * 4 + 1) * 3072; a.rout = m->r_resid + (l * 2 + 0) * 768;
-            k_gemv<768, 2, 2, PRO_TO16, EPI_PLAIN_ADD><<<(P.ntiles + 1) / 2, 128, 0, m->st>>>(a);
+            g.W = reinterpret_cast<const int4*>(P.W); g.we = P.e; g.bias = P.b; g.nout = P.nout; g.ntiles = P.ntiles;
+            g.X = m->att; g.Y = m->R; g.Yb = Rin;
+            g.rx16 = m->r_x16 + (l * 4 + 1) * 3072; g.rexls = m->r_exls + (l * 4 + 1) * 2;
+            g.rpile = m->r_pile + (l * 4 + 1) * 3072; g.rout = m->r_resid + (l * 2 + 0) * 768;
+            attend1<0>(m, rec, a);
+            gemv<768, 2, 2, PRO_TO16, EPI_PLAIN_ADD>(m, rec, (P.ntiles + 1) / 2, g);
         }
         // fc: gauge, product, gauged, edge (base2.py:106)
         {
@@ -772,17 +791,17 @@ static int launch_step(sm_machine* m, int parts = STEP_ALL, hipEvent_t hs = null
             a.X = m->R; a.Y = m->hid;
             a.rx16 = m->r_x16 + (l * 4 + 2) * 3072; a.rexls = m->r_exls + (l * 4 + 2) * 2;
             a.rpile = m->r_pile + (l * 4 + 2) * 3072; a.rout = m->r_hid + l * 3072;
-            k_gemv<768, 2, 4, PRO_GAUGE, EPI_GAUGED_EDGE><<<(P.ntiles + 3) / 4, 256, 0, m->st>>>(a);
+            gemv<768, 2, 4, PRO_GAUGE, EPI_GAUGED_EDGE>(m, rec, (P.ntiles + 3) / 4, a);
         }
         // mproj: to16 of the hidden row (3072), product, plain, added to R (base2.py:106)
         {
             GemvArgs a = base;
             const DevPlate& P = m->bank[l][3];
             a.W = reinterpret_cast<const int4*>(P.W); a.we = P.e; a.bias = P.b; a.nout = P.nout; a.ntiles = P.ntiles;
-            a.X = m->hid; a.Y = m->R;
+            a.X = m->hid; a.Y = m->R; a.Yb = m->R;
             a.rx16 = m->r_x16 + (l * 4 + 3) * 3072; a.rexls = m->r_exls + (l * 4 + 3) * 2;
             a.rpile = m->r_pile + (l * 4 + 3) * 3072; a.rout = m->r_resid + (l * 2 + 1) * 768;
-            k_gemv<3072, 1, 4, PRO_TO16, EPI_PLAIN_ADD><<<(P.ntiles + 3) / 4, 256, 0, m->st>>>(a);
+            gemv<3072, 1, 4, PRO_TO16, EPI_PLAIN_ADD>(m, rec, (P.ntiles + 3) / 4, a);
         }
     }
     // head: gauge, product with the tied word table, power + standing amount, race (base2.py:107-114)
@@ -794,13 +813,9 @@ static int launch_step(sm_machine* m, int parts = STEP_ALL, hipEvent_t hs = null
         a.W = reinterpret_cast<const int4*>(P.W); a.we = P.e; a.bias = P.b; a.nout = P.nout; a.ntiles = P.ntiles;
         a.X = m->R;
         a.rx16 = m->r_hx16; a.rexls = m->r_hexls; a.rpile = m->r_hpile; a.rlogits = m->r_logits;
-        a.part_v = m->part_v; a.part_i = m->part_i; a.counter = nullptr;     // the race runs in its own kernel
-        a.plen = ctl + CTL_PLEN;
-        if (hs)   // timed: the event pair is stamped by this dispatch itself (the interval a kernel trace reports)
-            hipExtLaunchKernelGGL(k_gemv<768, HEAD_TC, HEAD_WPB, PRO_GAUGE, EPI_HEAD>, dim3(m->head_grid), dim3(64 * HEAD_WPB), 0, m->st, hs, he, 0, a);
-        else
-            k_gemv<768, HEAD_TC, HEAD_WPB, PRO_GAUGE, EPI_HEAD><<<m->head_grid, 64 * HEAD_WPB, 0, m->st>>>(a);
-        launch_race(m, m->head_grid);
+        a.part_v = m->part_v; a.part_i = m->part_i;      // each block's best; the race runs in k_race1
+        gemv<768, HEAD_TC, HEAD_WPB, PRO_GAUGE, EPI_HEAD>(m, rec, m->head_grid, a, hs, he);
+        launch_race1(m);
     }
     HIP_TRY(hipGetLastError());
     return SM_OK;
@@ -973,11 +988,12 @@ extern "C" int sm_create(const char* layout_dir, const sm_config* cfg, sm_machin
     }
     m->ctx = c.max_ctx < m->npos ? c.max_ctx : m->npos;
     m->head_grid = c.head_grid > 0 ? c.head_grid : 512;     // two blocks per CU (measured best)
+    if (m->head_grid > 1024) return bail(fail(SM_E_ARG, "sm_create: head_grid at most 1024"));
     const size_t nparts = m->B == 1 ? (size_t)m->head_grid : (size_t)m->B * head_rows_grid((m->vocab + 15) / 16);
     // state
     const size_t B = m->B, ctx = m->ctx, RC = m->RC;
     const size_t nsets = m->kind == 1 && mfma ? 2 : 1;      // light-plane sets (the Pythia MFMA phases keep two)
-    if ((rc = dalloc(&m->R, RC * 768)) || (rc = dalloc(&m->QKV, RC * 2304)) || (rc = dalloc(&m->att, RC * 768)) || (rc = dalloc(&m->attor, RC * 12)) ||
+    if ((rc = dalloc(&m->R, RC * 768)) || (rc = dalloc(&m->R0, 768)) || (rc = dalloc(&m->QKV, RC * 2304)) || (rc = dalloc(&m->att, RC * 768)) || (rc = dalloc(&m->attor, RC * 12)) ||
         (rc = dalloc(&m->hidor, RC * 192)) || (rc = dalloc(&m->sfacts, 4 * RC * 4)) ||
         (rc = dalloc(&m->hid, RC * 3072)) || (rc = dalloc(&m->K16, 12 * B * ctx * 768)) || (rc = dalloc(&m->KM, 12 * B * ctx * 12)) ||
         (rc = dalloc(&m->EK, 12 * B * ctx * 12)) ||
@@ -1032,6 +1048,7 @@ extern "C" int sm_reset(sm_machine* m) {
     HIP_TRY(hipMemsetAsync(m->seq, 0, B * (ctx + 1) * 4, m->st));
     HIP_TRY(hipMemsetAsync(m->words, 0, B * (ctx + 1) * 4, m->st));
     HIP_TRY(hipMemsetAsync(m->R, 0, (size_t)m->RC * 768 * 8, m->st));
+    HIP_TRY(hipMemsetAsync(m->R0, 0, 768 * 8, m->st));
     HIP_TRY(hipStreamSynchronize(m->st));
     m->h_plen = m->h_pos = m->h_words = 0;
     m->h_recpos = -1;
@@ -1098,6 +1115,42 @@ static int collect(sm_machine* m, int n) {
     return SM_OK;
 }
 
+// n whole decode steps: profiled (event pairs around each head), replayed from captured graphs, or launched
+static int queue_steps(sm_machine* m, int steps) {
+    int rc;
+    if (m->cfg.profile) {
+        while (steps > 0) {
+            const int n = steps < m->gsteps ? steps : m->gsteps;
+            for (int s = 0; s < n; s++)
+                if ((rc = profiled_step(m, s))) return rc;
+            if ((rc = collect(m, n))) return rc;
+            steps -= n;
+        }
+    } else if (m->cfg.use_graph) {
+        if (steps >= m->gsteps && (rc = capture(m, 0, m->gsteps, STEP_ALL))) return rc;
+        for (; steps >= m->gsteps; steps -= m->gsteps) HIP_TRY(hipGraphLaunch(m->gexec[0], m->st));
+        if (steps > 0 && (rc = capture(m, 1, 1, STEP_ALL))) return rc;
+        for (; steps > 0; steps--) HIP_TRY(hipGraphLaunch(m->gexec[1], m->st));
+    } else {
+        for (; steps > 0; steps--)
+            if ((rc = launch_step(m))) return rc;
+    }
+    return SM_OK;
+}
+
+// n decode steps from position pos0.  At batch 1 the step at the recorded position runs on its own with the
+// kernels that record (the others read no record position); the batched kernels check it themselves.
+static int run_steps(sm_machine* m, int n, int pos0) {
+    const int rp = m->B == 1 ? m->h_recpos : -1;
+    int rc;
+    if (rp >= pos0 && rp < pos0 + n) {
+        if ((rc = queue_steps(m, rp - pos0))) return rc;
+        if ((rc = launch_step(m, STEP_ALL, nullptr, nullptr, true))) return rc;
+        return queue_steps(m, pos0 + n - rp - 1);
+    }
+    return queue_steps(m, n);
+}
+
 extern "C" int sm_generate(sm_machine* m, int32_t n_words, int32_t* out) {
     if (!m) return fail(SM_E_ARG, "sm_generate: null machine");
     if (n_words <= 0) return fail(SM_E_ARG, "sm_generate: n_words must be positive");
@@ -1121,25 +1174,10 @@ extern "C" int sm_generate(sm_machine* m, int32_t n_words, int32_t* out) {
             m->h_pos = npos;
         }
     }
-    int steps = (m->h_plen - 1 + target) - m->h_pos;
-    const int total = steps;
-    if (m->cfg.profile) {
-        while (steps > 0) {
-            const int n = steps < m->gsteps ? steps : m->gsteps;
-            for (int s = 0; s < n; s++)
-                if ((rc = profiled_step(m, s))) return rc;
-            if ((rc = collect(m, n))) return rc;
-            steps -= n;
-        }
-    } else if (m->cfg.use_graph) {
-        if (steps >= m->gsteps && (rc = capture(m, 0, m->gsteps, STEP_ALL))) return rc;
-        for (; steps >= m->gsteps; steps -= m->gsteps) HIP_TRY(hipGraphLaunch(m->gexec[0], m->st));
-        if (steps > 0 && (rc = capture(m, 1, 1, STEP_ALL))) return rc;
-        for (; steps > 0; steps--) HIP_TRY(hipGraphLaunch(m->gexec[1], m->st));
-    } else {
-        for (; steps > 0; steps--)
-            if ((rc = launch_step(m))) return rc;
-    }
+    // batch 1: the first step's entering row (later steps' rows are written by the race of the step before)
+    if (first && m->B == 1) launch_embed1(m);
+    const int total = (m->h_plen - 1 + target) - m->h_pos;
+    if ((rc = run_steps(m, total, m->h_pos))) return rc;
     HIP_TRY(hipStreamSynchronize(m->st));
     int ctl[CTL_N];
     HIP_TRY(hipMemcpy(ctl, m->ctl, sizeof(ctl), hipMemcpyDeviceToHost));
@@ -1311,7 +1349,7 @@ extern "C" int sm_stage_attend(const sm_tables* t, const int64_t* qkv, int16_t* 
     AttArgs a{};
     a.QKV = (const i64*)qkv; a.K16 = k16; a.KM = (i64*)km; a.EK = ek; a.V = v; a.out = (i64*)out; a.pos = t->scratch; a.ctx = ctx;
     a.tb = t->tb(); a.err = t->scratch + 1;
-    k_attend<0, 1><<<dim3(12, 1), NTHR, (size_t)ctx * 12, s>>>(a);
+    k_attend<0, 1, 0><<<dim3(12, 1), NTHR, (size_t)ctx * 12, s>>>(a);
     HIP_TRY(hipGetLastError());
     int err = 0;
     HIP_TRY(hipMemcpyAsync(&err, t->scratch + 1, 4, hipMemcpyDeviceToHost, s));
@@ -1451,10 +1489,10 @@ extern "C" int sm_plate_product(const sm_plate* p, const int64_t* x16, int64_t* 
     a.X = (const i64*)x16; a.Y = (i64*)pile;
     const int g = grid > 0 ? grid : (P.ntiles + 3) / 4;     // four waves per block, one tile per wave
     hipStream_t s = (hipStream_t)stream;
-    if (P.nin == 768 && P.tc == 8) k_gemv<768, 8, 4, PRO_X16, EPI_PILE><<<g, 256, 0, s>>>(a);
-    else if (P.nin == 768 && P.tc == 2) k_gemv<768, 2, 4, PRO_X16, EPI_PILE><<<g, 256, 0, s>>>(a);
-    else if (P.nin == 3072 && P.tc == 1) k_gemv<3072, 1, 4, PRO_X16, EPI_PILE><<<g, 256, 0, s>>>(a);
-    else k_gemv<3072, 2, 4, PRO_X16, EPI_PILE><<<g, 256, 0, s>>>(a);
+    if (P.nin == 768 && P.tc == 8) k_gemv<768, 8, 4, PRO_X16, EPI_PILE, 0><<<g, 256, 0, s>>>(a);
+    else if (P.nin == 768 && P.tc == 2) k_gemv<768, 2, 4, PRO_X16, EPI_PILE, 0><<<g, 256, 0, s>>>(a);
+    else if (P.nin == 3072 && P.tc == 1) k_gemv<3072, 1, 4, PRO_X16, EPI_PILE, 0><<<g, 256, 0, s>>>(a);
+    else k_gemv<3072, 2, 4, PRO_X16, EPI_PILE, 0><<<g, 256, 0, s>>>(a);
     HIP_TRY(hipGetLastError());
     return SM_OK;
 }
