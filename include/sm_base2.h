@@ -145,6 +145,13 @@ int sm_stage_race(const int64_t* v, int64_t n, int64_t* out_index, void* stream)
 int sm_stage_attend(const sm_tables* t, const int64_t* qkv, int16_t* k16, int64_t* km, int32_t* ek, int32_t* v,
                     int32_t pos, int32_t ctx, int64_t* out, void* stream);
 
+/* The same new position's attention for `rows` independent streams at once, through the batched machine's kernel
+ * (one block per head and stream; base2.py:85-100 for each stream's last row).  qkv: device int64 [rows][2304]; the
+ * caches are the same arrays per stream, stream-major: k16 int16 [rows][12][ctx][64], km int64 [rows][12][ctx],
+ * ek int32 [rows][12][ctx], v int32 [rows][12][ctx][64]; out: device int64 [rows][768]. */
+int sm_stage_attend_rows(const sm_tables* t, const int64_t* qkv, int32_t rows, int16_t* k16, int64_t* km, int32_t* ek,
+                         int32_t* v, int32_t pos, int32_t ctx, int64_t* out, void* stream);
+
 /* A plate on the device from an input-major int16 [nin][nout] host array: tile_cols > 0 lays it out for the
  * one-row GEMV (sm_plate_product), tile_cols == 0 as int8 MFMA byte planes for rows of lights
  * (sm_plate_product_rows, the batched streams' layout). */

@@ -1361,6 +1361,29 @@ extern "C" int sm_stage_attend(const sm_tables* t, const int64_t* qkv, int16_t* 
     return SM_OK;
 }
 
+extern "C" int sm_stage_attend_rows(const sm_tables* t, const int64_t* qkv, int32_t rows, int16_t* k16, int64_t* km,
+                                    int32_t* ek, int32_t* v, int32_t pos, int32_t ctx, int64_t* out, void* stream) {
+    if (!t || !qkv || !k16 || !km || !ek || !v || !out || rows <= 0 || rows > 1024 || ctx <= 0 || pos < 0 || pos >= ctx ||
+        ctx > 8192)
+        return fail(SM_E_ARG, "sm_stage_attend_rows: arguments");
+    hipStream_t s = (hipStream_t)stream;
+    HIP_TRY(hipMemcpyAsync(t->scratch, &pos, 4, hipMemcpyHostToDevice, s));
+    HIP_TRY(hipStreamSynchronize(s));
+    AttArgs a{};
+    a.QKV = (const i64*)qkv; a.K16 = k16; a.KM = (i64*)km; a.EK = ek; a.V = v; a.out = (i64*)out; a.pos = t->scratch; a.ctx = ctx;
+    a.tb = t->tb(); a.err = t->scratch + 1;
+    k_attend<0, 0, 1><<<dim3(12, rows), NTHR, (size_t)ctx * 12, s>>>(a);      // the batched machine's kernel
+    HIP_TRY(hipGetLastError());
+    int err = 0;
+    HIP_TRY(hipMemcpyAsync(&err, t->scratch + 1, 4, hipMemcpyDeviceToHost, s));
+    HIP_TRY(hipStreamSynchronize(s));
+    if (err & SM_ERR_V32) {
+        HIP_TRY(hipMemset(t->scratch + 1, 0, 4));
+        return fail(SM_E_OVERFLOW, "sm_stage_attend_rows: a value left 32 bits");
+    }
+    return SM_OK;
+}
+
 // tile_cols > 0: a GEMV plate (one light row per product); tile_cols == 0: an MFMA plate (rows of lights) with
 // its own light planes and row sums
 struct sm_plate {
@@ -1419,14 +1442,16 @@ extern "C" int64_t sm_plate_bytes(const sm_plate* p) {
     return (int64_t)p->P.ntiles * p->P.tc * p->P.nin * 2;
 }
 
+// the rows' light planes and row facts go to planes / rowinfo
 template <int RT>
-static void rows_product(const sm_plate* p, const int64_t* x16, int32_t rows, int64_t* pile, hipStream_t s) {
+static void rows_product(const sm_plate* p, const int64_t* x16, int32_t rows, int64_t* pile, hipStream_t s,
+                         signed char* planes, int* rowinfo) {
     const MfmaPlate& P = p->M;
     LightArgs la{};
-    la.K = P.K; la.rows = rows; la.X = (const i64*)x16; la.planes = p->planes; la.rowinfo = p->rowinfo;
+    la.K = P.K; la.rows = rows; la.X = (const i64*)x16; la.planes = planes; la.rowinfo = rowinfo;
     GemmArgs ga{};
     ga.K = P.K; ga.N = P.N; ga.rows = rows; ga.RT = RT; ga.W = P.W; ga.csum = P.csum; ga.we = P.e; ga.bias = P.b;
-    ga.planes = p->planes; ga.rowinfo = p->rowinfo; ga.Y = (i64*)pile; ga.ystride = P.N;
+    ga.planes = planes; ga.rowinfo = rowinfo; ga.Y = (i64*)pile; ga.ystride = P.N;
     if (P.K == 768) {
         k_light<768, PRO_X16, 192, 1><<<rows, 192, 0, s>>>(la);
         if (P.N > 3072)       // head-shaped plates: the head's kernel (light planes in LDS)
@@ -1445,10 +1470,10 @@ extern "C" int sm_plate_product_rows(const sm_plate* p, const int64_t* x16, int3
     if (rows < 1 || rows > 64) return fail(SM_E_ARG, "sm_plate_product_rows: rows must be in [1, 64]");
     hipStream_t s = (hipStream_t)stream;
     const int RT = (rows + 15) / 16;
-    if (RT == 1) rows_product<1>(p, x16, rows, pile, s);
-    else if (RT == 2) rows_product<2>(p, x16, rows, pile, s);
-    else if (RT == 3) rows_product<3>(p, x16, rows, pile, s);
-    else rows_product<4>(p, x16, rows, pile, s);
+    if (RT == 1) rows_product<1>(p, x16, rows, pile, s, p->planes, p->rowinfo);
+    else if (RT == 2) rows_product<2>(p, x16, rows, pile, s, p->planes, p->rowinfo);
+    else if (RT == 3) rows_product<3>(p, x16, rows, pile, s, p->planes, p->rowinfo);
+    else rows_product<4>(p, x16, rows, pile, s, p->planes, p->rowinfo);
     HIP_TRY(hipGetLastError());
     return SM_OK;
 }

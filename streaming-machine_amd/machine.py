@@ -44,6 +44,13 @@ def lib():
     """Load the HIP library (built by __graft_entry__.build()); raises if it is not there."""
     global _LIB
     if _LIB is None:
+        # torch bundles a HIP runtime under the same soname (libamdhip64.so.7) as the one this library links: when
+        # torch is present its copy must be the process's, so it is loaded first (whichever the caller imports
+        # later then binds to it); torch initialised on top of the other copy finds no GPU
+        try:
+            import torch  # noqa: F401
+        except ImportError:
+            pass
         if not os.path.exists(LIB_PATH):
             raise SmError(SM_E_IO, f"{LIB_PATH} is missing: build it (python -c 'import __graft_entry__ as g; g.build()')")
         L = ctypes.CDLL(LIB_PATH)
@@ -69,6 +76,7 @@ def lib():
         L.sm_stage_gauge_log.argtypes = [vp, vp, i32, vp, vp, vp, vp]
         L.sm_stage_race.argtypes = [vp, i64, vp, vp]
         L.sm_stage_attend.argtypes = [vp, vp, vp, vp, vp, vp, i32, i32, vp, vp]
+        L.sm_stage_attend_rows.argtypes = [vp, vp, i32, vp, vp, vp, vp, i32, i32, vp, vp]
         L.sm_plate_create.argtypes = [ctypes.POINTER(ctypes.c_int16), i32p, i64p, i32, i32, i32, ctypes.POINTER(vp)]
         L.sm_plate_destroy.argtypes = [vp]
         L.sm_plate_product.argtypes = [vp, vp, vp, i32, vp]
@@ -279,3 +287,9 @@ class stages:
         """k16: int16 [12][ctx][64] keys (+32768 held as 32767), km: int64 [12][ctx] masks of the +32768
         dimensions, ek: int32 [12][ctx], v: int32 [12][ctx][64] (device pointers; zeroed = empty)"""
         check(lib().sm_stage_attend(t.h, qkv, k16, km, ek, v, pos, ctx, out, stream))
+
+    @staticmethod
+    def attend_rows(t: Tables, qkv, rows, k16, km, ek, v, pos, ctx, out, stream=0):
+        """the same for `rows` streams through the batched machine's kernel: qkv [rows][2304], caches stream-major
+        ([rows][12][ctx][64] keys and values, [rows][12][ctx] masks and water levels), out [rows][768]"""
+        check(lib().sm_stage_attend_rows(t.h, qkv, rows, k16, km, ek, v, pos, ctx, out, stream))
