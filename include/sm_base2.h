@@ -174,6 +174,13 @@ int sm_plate_product_rows(const sm_plate* p, const int64_t* x16, int32_t rows, i
  * a multiple of 48 (nin 3072); rows 1..64.  Calls on one plate share its scratch: serialise them. */
 int sm_plate_product_rows_from(const sm_plate* p, const int64_t* X, const int64_t* orw, int32_t rows,
                                int64_t* pile, void* stream);
+/* sm_plate_product_rows with no allocation on any call: the rows' light planes and row facts go to a static
+ * device array of the library (590 KB, held by every GPU it runs on until the process ends), not to the plate's own
+ * scratch.  No counterpart in the reference: it is for callers that cannot allocate device memory (code under HIP
+ * graph capture, tight serving loops, harnesses that forbid hipMalloc).  rows 1..64 (more is refused with
+ * SM_E_ARG); the same piles as sm_plate_product_rows.  Every call on one GPU uses that GPU's one array, so calls
+ * that overlap on one GPU (other streams, other threads) race; the caller serialises them. */
+int sm_plate_product_rows_noalloc(const sm_plate* p, const int64_t* x16, int32_t rows, int64_t* pile, void* stream);
 /* bytes of the device plate (for bandwidth accounting) */
 int64_t sm_plate_bytes(const sm_plate* p);
 

@@ -19,6 +19,7 @@
 #include <cstdio>
 #include <cstring>
 #include <fstream>
+#include <mutex>
 #include <string>
 #include <vector>
 
@@ -1442,7 +1443,8 @@ extern "C" int64_t sm_plate_bytes(const sm_plate* p) {
     return (int64_t)p->P.ntiles * p->P.tc * p->P.nin * 2;
 }
 
-// the rows' light planes and row facts go to planes / rowinfo
+// the rows' light planes and row facts go to planes / rowinfo (the plate's own, or the static scratch of
+// sm_plate_product_rows_noalloc)
 template <int RT>
 static void rows_product(const sm_plate* p, const int64_t* x16, int32_t rows, int64_t* pile, hipStream_t s,
                          signed char* planes, int* rowinfo) {
@@ -1474,6 +1476,59 @@ extern "C" int sm_plate_product_rows(const sm_plate* p, const int64_t* x16, int3
     else if (RT == 2) rows_product<2>(p, x16, rows, pile, s, p->planes, p->rowinfo);
     else if (RT == 3) rows_product<3>(p, x16, rows, pile, s, p->planes, p->rowinfo);
     else rows_product<4>(p, x16, rows, pile, s, p->planes, p->rowinfo);
+    HIP_TRY(hipGetLastError());
+    return SM_OK;
+}
+
+// ---------------------------------------------------------------------------------------------------------
+// The allocation-free rows product.  Its light planes and row facts live in `scratch`, a file-scope device array
+// sized for the largest call (64 rows of a 3072-wide light: 4 row tiles x 48 steps of 64 x 3 planes x 1 KB, then
+// 64 x 8 row facts); every GPU this library runs on holds its own copy until the process ends.  Host code never
+// passes the array's name to a kernel: on each device the entry point's first call looks its address up (with
+// that device current) and keeps it.  Nothing in the scratch needs to start at zero: k_light writes the planes
+// and facts of every row it is given before the contraction reads them, the facts of rows past `rows` are read
+// through bounded loads (zeros), and a row tile's padding rows feed only their own MFMA output rows, which are
+// never stored.  Calls on one GPU share the array, so calls that overlap on one GPU race.
+#define SM_NOALLOC_PLANES ((size_t)4 * 48 * 3 * 1024)
+#define SM_NOALLOC_BYTES (SM_NOALLOC_PLANES + (size_t)64 * 8 * 4)
+static __device__ __align__(256) signed char scratch[SM_NOALLOC_BYTES];
+static std::mutex g_scratch_mu;
+static signed char* g_scratch_dev[256];              // scratch's address on each device (null: not looked up yet)
+
+static int scratch_on_current_device(signed char** out) {
+    int dev = -1;
+    HIP_TRY(hipGetDevice(&dev));
+    if (dev < 0 || dev >= 256) return fail(SM_E_ARG, "sm_plate_product_rows_noalloc: device index out of range");
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch_dev[dev]) {
+        void* ptr = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !ptr)
+            return fail(SM_E_HIP, std::string("hipGetSymbolAddress(scratch): ") + hipGetErrorString(e));
+        g_scratch_dev[dev] = static_cast<signed char*>(ptr);
+    }
+    *out = g_scratch_dev[dev];
+    return SM_OK;
+}
+
+extern "C" int sm_plate_product_rows_noalloc(const sm_plate* p, const int64_t* x16, int32_t rows, int64_t* pile,
+                                             void* stream) {
+    if (!p || !x16 || !pile) return fail(SM_E_ARG, "sm_plate_product_rows_noalloc: null argument");
+    if (!p->mfma) return fail(SM_E_ARG, "sm_plate_product_rows_noalloc: the plate was made for the GEMV (tile_cols > 0)");
+    if (rows < 1 || rows > 64) return fail(SM_E_ARG, "sm_plate_product_rows_noalloc: rows must be in [1, 64] (the scratch holds 64)");
+    const int RT = (rows + 15) / 16;
+    const size_t need = (size_t)RT * (p->M.K / 64) * 3 * 1024;
+    if (need > SM_NOALLOC_PLANES) return fail(SM_E_ARG, "sm_plate_product_rows_noalloc: the light planes pass the scratch");
+    signed char* base = nullptr;
+    int rc;
+    if ((rc = scratch_on_current_device(&base))) return rc;
+    signed char* planes = base;
+    int* rowinfo = reinterpret_cast<int*>(base + SM_NOALLOC_PLANES);
+    hipStream_t s = (hipStream_t)stream;
+    if (RT == 1) rows_product<1>(p, x16, rows, pile, s, planes, rowinfo);
+    else if (RT == 2) rows_product<2>(p, x16, rows, pile, s, planes, rowinfo);
+    else if (RT == 3) rows_product<3>(p, x16, rows, pile, s, planes, rowinfo);
+    else rows_product<4>(p, x16, rows, pile, s, planes, rowinfo);
     HIP_TRY(hipGetLastError());
     return SM_OK;
 }

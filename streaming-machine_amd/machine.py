@@ -82,6 +82,7 @@ def lib():
         L.sm_plate_product.argtypes = [vp, vp, vp, i32, vp]
         L.sm_plate_product_rows.argtypes = [vp, vp, i32, vp, vp]
         L.sm_plate_product_rows_from.argtypes = [vp, vp, vp, i32, vp, vp]
+        L.sm_plate_product_rows_noalloc.argtypes = [vp, vp, i32, vp, vp]
         L.sm_plate_bytes.restype = i64
         L.sm_plate_bytes.argtypes = [vp]
         _LIB = L
@@ -238,6 +239,11 @@ class Plate:
 
     def product_rows(self, x16_ptr: int, rows: int, pile_ptr: int, stream: int = 0):
         check(self.L.sm_plate_product_rows(self.h, x16_ptr, rows, pile_ptr, stream))
+
+    def product_rows_noalloc(self, x16_ptr: int, rows: int, pile_ptr: int, stream: int = 0):
+        """product_rows with the light planes in the library's static device scratch: no allocation on any call
+        (calls that overlap on one GPU race)"""
+        check(self.L.sm_plate_product_rows_noalloc(self.h, x16_ptr, rows, pile_ptr, stream))
 
     def product_rows_from(self, x_ptr: int, orw_ptr: int, rows: int, pile_ptr: int, stream: int = 0):
         """the light formed in the bank from int64 rows and their OR words (12 a row for nin 768, 192 for 3072)"""
