@@ -4,23 +4,32 @@ Workload (the batch-1 configuration the metric is quoted on): GPT-2 124M shape, 
 from seed 0 converted to int16 plates with per-column powers of two; batch 1; an 8-token prompt drawn from
 default_rng(1); 16 greedy words per sequence, i.e. the prompt pass plus 15 decode steps at context 9..23.
 A "step" is one decode position (one new word).  The timed region covers exactly --steps decode steps, in
-sequences of 15 (each sequence's prompt pass runs untimed first), with the weights, tables and KV cache resident
-in HBM.  Before any number is printed the emitted words are checked against the golden words that base2.py
-(and pythia_base2.py for the Pythia leg) gave for the same prompts (tests/golden, written by executing the
-reference itself); the CPU baseline's own words are checked against the GPU's.
+sequences of up to 15 (each sequence's prompt pass runs untimed first), replayed from captured HIP graphs with
+the weights, tables and KV cache resident in HBM.  Before any number is printed the emitted words are checked
+against the golden words base2.py gave for the same prompt (tests/golden, written by executing the reference).
 
 Printed: one JSON line with the driver's fields plus
-  roofline      the head kernel (the largest single launch: the 768 x 50257 plate read), its mean
-                duration from HIP event pairs recorded around every head launch inside the timed region
-  step_roofline the whole decode step's algorithmic bytes over its measured time
-  prompt_included  words per second counting the prompt pass (every prompt position but the last through the
-                int8 MFMA banks in passes of up to 64 rows, then the first word's step), as the reference also
-                reports beside the after-the-prompt rate
-  batched       the same machine with 64 streams in lockstep (int8 MFMA contraction), 32-token prompts,
-                128 words each (tokens/s over all streams)
-  pythia        the Pythia-160m-shaped machine with 32 streams, 64-token prompts, 256 words each
-  cpu_baseline  base2.py's CPU path restated in numpy (full recompute per word, float64 products, the
-                top-down race loop), timed on a bounded sample of the same sequence on the host cores
+  kernels        every kernel of the batch-1 step from a second pass of the same workload whose launches are each
+                 stamped with a HIP event pair by their own dispatch (the interval a kernel trace reports):
+                 launches a step, mean microseconds, algorithmic bytes a launch, GB/s, fraction of HBM peak
+  roofline       the kernel with the largest share of the step (microseconds a step), from that table;
+                 traffic from the HBM counters in profiles/ when they were collected for it
+  step_roofline  the whole step: the workload's bytes of SURVEY 8(d) (248,662,476 + 73,728 T) over its time,
+                 with the bytes this layout reads beside them
+  cold           the same profiled step with 1 GiB streamed through the device between steps (the 256 MB
+                 Infinity Cache holds none of the step's bytes), beside the warm figures
+  prompt_included  words per second counting the prompt pass, as the reference also reports
+  batched        64 streams in lockstep (int8 MFMA banks), 32-token prompts, 128 words each; every word of
+                 streams 0 and 1 checked against base2.py's, of streams 31 and 63 against the oracle's fixture
+  pythia         the Pythia-160m-shaped machine, 32 streams, 64-token prompts, 256 words each (streams 0 and 1
+                 against pythia_base2.py's words, stream 31 against the oracle's)
+  gemv           config 2: the int16 GEMV at the five GPT-2 shapes, uniform int16 weights and lights, exponents in
+                 [-16, -8], rotated over >= 1 GiB of plate copies (each launch reads a plate the cache does not
+                 hold), pile checked against the exact product
+  attention      config 3: one new position's attention over int16 caches of 128, 512 and 1024 positions
+  cpu_baseline   base2.py's CPU path restated in numpy (full recompute per word, float64 products, the top-down
+                 race loop) on a bounded sample, median of 5 after a warm-up, all cores and one thread, with the
+                 KV-cached C oracle beside it
 """
 from __future__ import annotations
 
@@ -28,6 +37,8 @@ import argparse
 import importlib.util
 import json
 import os
+import platform
+import re
 import sys
 import tempfile
 import time
@@ -37,11 +48,15 @@ import numpy as np
 REPO = os.path.dirname(os.path.abspath(__file__))
 METRIC = "decode tokens/s, GPT-2-124M int base-2, B=1 & B=64; % HBM roofline"
 HBM_PEAK_GBS = 8000.0
+INT8_PEAK_OPS = 5.0e15
 WORDS = 16          # words per sequence (the prompt pass gives the first)
 PROMPT = 8
 B_STREAMS, B_PROMPT, B_WORDS = 64, 32, 128     # the batched workload: 64 streams, 32-token prompts, 128 words
 P_STREAMS, P_PROMPT, P_WORDS = 32, 64, 256     # the Pythia-160m-shaped workload: 32 streams, 64-token prompts, 256 words
+GRAPH_STEPS = 16    # decode steps a captured graph holds in the batched legs
 PREFILL_ROWS = 64   # prompt rows a pass through the int8 MFMA banks (0: position by position)
+VOCAB, PVOCAB = 50257, 50304
+BANKS = {"qkv": (768, 2304), "proj": (768, 768), "fc": (768, 3072), "mproj": (3072, 768)}
 
 
 def load_sm():
@@ -60,179 +75,434 @@ def log(msg):
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
-def golden_words(fname: str) -> dict:
-    """case name -> words, from the golden fixtures written by executing the reference itself"""
-    with open(os.path.join(REPO, "tests", "golden", fname)) as f:
-        return {c["name"]: c["words"] for c in json.load(f)["cases"]}
+def fixture_cases(fname: str) -> dict:
+    path = os.path.join(REPO, "tests", "golden", fname)
+    if not os.path.exists(path):
+        return {}
+    with open(path) as f:
+        return {c["name"]: c for c in json.load(f)["cases"]}
 
 
-def head_bytes(vocab: int) -> int:
-    """algorithmic bytes of one head launch: the int16 plate plus an int32 exponent and an int64 bias per word"""
-    return 2 * 768 * vocab + 12 * vocab
+# ---- algorithmic bytes ----
+def bank_bytes(nin: int, nout: int) -> int:
+    """a plate read once (int16) with its per-column exponent (int32) and bias (int64)"""
+    return 2 * nin * nout + 12 * nout
 
 
-# the KV cache read per cached position of a stream: 12 layers x (int16 k16 and int32 v per dimension, and per
-# head an int32 key water level and an int64 mask of the key's +32768 dimensions)
-KV_BYTES = 12 * (768 * 6 + 12 * 12)
+LAYER_FIXED = sum(bank_bytes(*s) for s in BANKS.values())                 # 14,155,776 + 82,944
+WORKLOAD_FIXED = 12 * LAYER_FIXED + bank_bytes(768, VOCAB)                 # 248,662,476
+KV_WORKLOAD = 12 * 768 * 8        # 73,728 B a cached position: k and v at 4 B each, 12 layers (SURVEY 8(d))
+KV_LAYOUT = 12 * (768 * 6 + 12 * 12)   # what this layout reads: int16 k, int32 v, per head an int32 level, int64 mask
 
 
-def step_bytes(vocab: int, ctx: float) -> float:
-    """algorithmic bytes of one decode step: every plate once (int16), the per-column exponents and biases,
-    and the KV cache read at context ctx"""
-    layer_w = 2 * (768 * 2304 + 768 * 768 + 768 * 3072 + 3072 * 768)
-    layer_cols = 12 * (2304 + 768 + 3072 + 768)
-    return 12 * (layer_w + layer_cols) + head_bytes(vocab) + KV_BYTES * ctx
+def b1_kernel_bytes(name: str, ctx: float, vocab: int = VOCAB) -> float:
+    if name in BANKS:
+        return bank_bytes(*BANKS[name])
+    if name == "head":
+        return bank_bytes(768, vocab)
+    if name == "attend":
+        return KV_WORKLOAD / 12 * ctx
+    return 0.0
 
 
-def batched_leg(sm, lay):
-    """64 independent streams decoded in lockstep (every bank an int8 MFMA contraction): one sequence of
-    32-token prompts and 128 words per stream, KV cache up to 160.  Timed: the 127 decode steps after the
-    prompt pass; the head launches are timed with their own event pairs.  Streams 0 and 1 begin with the golden
-    words base2.py gives for their prompts."""
+def batched_kernel_bytes(name: str, ctx: float, streams: int, vocab: int, head_bias: bool = True) -> float:
+    if name in BANKS:
+        return bank_bytes(*BANKS[name])
+    if name == "mproj.part":
+        return bank_bytes(3072, 768)
+    if name == "head":
+        return 2 * 768 * vocab + (12 if head_bias else 4) * vocab
+    if name == "attend":
+        return streams * KV_WORKLOAD / 12 * ctx
+    return 0.0
+
+
+def kernel_table(times: dict, steps: int, bytes_of) -> dict:
+    """kernel name -> launches a step, mean us, us a step, bytes a launch, GB/s, fraction of HBM peak"""
+    out = {}
+    for k, (n, us) in sorted(times.items(), key=lambda kv: -kv[1][0] * kv[1][1]):
+        b = bytes_of(k)
+        row = {"launches_per_step": round(n / steps, 3), "mean_us": round(us, 3), "us_per_step": round(n * us / steps, 2)}
+        if b:
+            row.update({"bytes_per_launch": int(b), "gbs": round(b / (us * 1e-6) / 1e9, 1),
+                        "frac": round(b / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)})
+        out[k] = row
+    return out
+
+
+def read_traffic(kernel: str):
+    """HBM bytes a launch of `kernel` from the FETCH_SIZE / WRITE_SIZE summary in profiles/, when collected"""
+    path = os.path.join(REPO, "profiles", "b1_gemv_traffic.txt")
+    if not os.path.exists(path):
+        return None
+    for line in open(path):
+        m = re.match(r"traffic_bytes_per_launch\[(\S+)\]:\s*(\d+)", line)
+        if m and m.group(1) == kernel:
+            return int(m.group(2))
+    return None
+
+
+def dominant(table: dict, where: str) -> dict:
+    """the roofline object of the kernel with the largest share of the step"""
+    name = max((k for k in table if "bytes_per_launch" in table[k]), key=lambda k: table[k]["us_per_step"])
+    r = table[name]
+    return {"bound": "hbm", "achieved": r["gbs"], "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": r["frac"],
+            "traffic": read_traffic(name) if where == "b1" else None, "kernel": name,
+            "bytes_per_launch": r["bytes_per_launch"], "mean_launch_us": r["mean_us"],
+            "launches_per_step": r["launches_per_step"], "us_per_step": r["us_per_step"],
+            "source": "HIP event pair stamped by each dispatch, profiled pass of the same workload"}
+
+
+# ---- batch 1 (config 1) ----
+def b1_leg(sm, lay, steps_req: int, warmup: int, prompt, want, cold_steps: int = 15):
     import torch
-    if lay is None:
-        lay = tempfile.mkdtemp(prefix="sm_bench_")
-        sm.layout(sm.convert(sm.random_gpt2(seed=0)), lay)
-    prompts = [sm.prompt_ids(4 + b, B_PROMPT) for b in range(B_STREAMS)]     # stream s: default_rng(4 + s)
-    gw = golden_words("base2_golden.json")
-    want = {b: gw[f"c4_stream{b}_p32_w4"] for b in (0, 1)}
-    m = sm.Machine(lay, max_ctx=B_PROMPT + B_WORDS, max_streams=B_STREAMS, graph_steps=B_WORDS - 1, profile=True,
+    m = sm.Machine(lay, max_ctx=64, graph_steps=WORDS - 1, prefill_rows=PREFILL_ROWS)
+
+    def sequence(k: int):
+        m.reset()
+        torch.cuda.synchronize()
+        t = time.perf_counter()
+        m.prefill(prompt)
+        first = int(m.generate(1)[0, 0])       # the prompt pass and the first word
+        torch.cuda.synchronize()
+        tp = time.perf_counter() - t
+        t = time.perf_counter()
+        rest = [int(w) for w in m.generate(k)[0]]
+        torch.cuda.synchronize()
+        dt = time.perf_counter() - t
+        words = [first] + rest
+        if words != want[:len(words)]:
+            raise RuntimeError(f"GPU words differ from base2.py's golden words: {words} vs {want}")
+        return dt, tp
+
+    done = 0
+    while done < max(warmup, 1):
+        sequence(WORDS - 1)
+        done += WORDS - 1
+    total, steps, prompt_s, nseq = 0.0, 0, 0.0, 0
+    while steps < steps_req:
+        k = min(WORDS - 1, steps_req - steps)
+        dt, tp = sequence(k)
+        total += dt
+        steps += k
+        prompt_s += tp
+        nseq += 1
+    m.close()
+
+    # the same sequences, every launch timed by its own event pair
+    mp = sm.Machine(lay, max_ctx=64, profile=True, prefill_rows=PREFILL_ROWS)
+    for it in range(3):
+        mp.reset()
+        mp.prefill(prompt)
+        mp.generate(1)
+        sm.kernel_times(clear=True)
+        rest = [int(w) for w in mp.generate(WORDS - 1)[0]]
+        if rest != want[1:]:
+            raise RuntimeError("profiled pass: GPU words differ from base2.py's golden words")
+        times = sm.kernel_times(clear=True)
+    ctx = PROMPT + WORDS / 2.0                     # mean context of the decode steps (9..23)
+    table = kernel_table(times, WORDS - 1, lambda k: b1_kernel_bytes(k, ctx))
+    # cold: 1 GiB streamed through the device between steps (outside the timed launches)
+    src = torch.ones(1 << 28, dtype=torch.int32, device="cuda")
+    dst = torch.empty_like(src)
+    mp.reset()
+    mp.prefill(prompt)
+    mp.generate(1)
+    sm.kernel_times(clear=True)
+    for _ in range(cold_steps):
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        mp.generate(1)
+    ctimes = sm.kernel_times(clear=True)
+    del src, dst
+    mp.close()
+    ctable = kernel_table(ctimes, cold_steps, lambda k: b1_kernel_bytes(k, ctx))
+    ms = 1000.0 * total / steps
+    return {"tok_s": steps / total, "ms": ms, "steps": steps, "prompt_ms": 1000.0 * prompt_s / nseq,
+            "table": table, "cold": ctable, "ctx": ctx}
+
+
+# ---- batched legs (configs 4 and 5) ----
+def gate_words(words, checks, what):
+    for stream, want, src in checks:
+        if [int(x) for x in words[stream][:len(want)]] != want:
+            raise RuntimeError(f"{what} stream {stream}: GPU words differ from {src}")
+
+
+def batched_checks(ref_name, orc_name, streams_ref, streams_orc):
+    ref, orc = fixture_cases("long_golden.json"), fixture_cases("long_oracle.json")
+    checks = []
+    for s in streams_ref:
+        c = ref.get(ref_name.format(s))
+        if c:
+            checks.append((s, c["words"], "the reference's words"))
+        elif orc.get(orc_name.format(s)):
+            checks.append((s, orc[orc_name.format(s)]["words"], "the oracle's words"))
+    for s in streams_orc:
+        c = orc.get(orc_name.format(s))
+        if c:
+            checks.append((s, c["words"], "the oracle's words"))
+    return checks
+
+
+def run_batched(sm, lay, streams, prompts, n_words, checks, what, bytes_of):
+    import torch
+    m = sm.Machine(lay, max_ctx=len(prompts[0]) + n_words, max_streams=streams, graph_steps=GRAPH_STEPS,
                    prefill_rows=PREFILL_ROWS)
     res = None
-    for it in range(2):                     # the first sequence warms up (graph instantiation)
+    for it in range(2):                        # the first sequence warms up (graph instantiation)
         m.reset()
         torch.cuda.synchronize()
         t = time.perf_counter()
         for b, p in enumerate(prompts):
             m.prefill(p, b)
-        first = m.generate(1)               # the prompt pass and the first word
+        first = m.generate(1)                  # the prompt pass and the first word
         torch.cuda.synchronize()
         tp = time.perf_counter() - t
-        m.profile(clear=True)
         t = time.perf_counter()
-        rest = m.generate(B_WORDS - 1)
+        rest = m.generate(n_words - 1)
         torch.cuda.synchronize()
         dt = time.perf_counter() - t
-        n, us = m.profile(clear=True)
-        words = np.concatenate([first, rest], axis=1)
-        for b, w in want.items():
-            if [int(x) for x in words[b][:len(w)]] != w:
-                raise RuntimeError(f"batched stream {b}: GPU words differ from base2.py's golden words")
-        res = (dt, n, us, tp)
+        gate_words(np.concatenate([first, rest], axis=1), checks, what)
+        res = (dt, tp)
+    vocab = m.vocab
     m.close()
-    dt, n, us, tp = res
-    steps = B_WORDS - 1
+    mp = sm.Machine(lay, max_ctx=len(prompts[0]) + n_words, max_streams=streams, profile=True, prefill_rows=PREFILL_ROWS)
+    mp.reset()
+    for b, p in enumerate(prompts):
+        mp.prefill(p, b)
+    first = mp.generate(1)
+    sm.kernel_times(clear=True)
+    rest = mp.generate(n_words - 1)
+    times = sm.kernel_times(clear=True)
+    gate_words(np.concatenate([first, rest], axis=1), checks, what + " (profiled pass)")
+    mp.close()
+    dt, tp = res
+    steps = n_words - 1
+    table = kernel_table(times, steps, bytes_of)
+    return dt, tp, steps, table, vocab
+
+
+def batched_leg(sm, lay):
+    prompts = [sm.prompt_ids(4 + b, B_PROMPT) for b in range(B_STREAMS)]     # stream s: default_rng(4 + s)
+    checks = batched_checks("c4_stream{}_p32_w128", "c4_stream{}_p32_w128", (0, 1), (31, 63))
+    ctx = B_PROMPT + B_WORDS / 2.0
+    dt, tp, steps, table, vocab = run_batched(sm, lay, B_STREAMS, prompts, B_WORDS, checks, "batched",
+                                              lambda k: batched_kernel_bytes(k, ctx, B_STREAMS, VOCAB))
     ms = 1000.0 * dt / steps
-    hb = head_bytes(m.vocab)
-    ach = hb / (us * 1e-6) / 1e9
-    # int8 MFMA work of one head launch: 4 byte-plane products of 64 x 768 x vocab (2 ops per multiply-add)
-    ops = 4 * 2 * B_STREAMS * 768 * m.vocab
-    ctx_mean = B_PROMPT + B_WORDS / 2.0
-    sb = step_bytes(m.vocab, 0) + B_STREAMS * KV_BYTES * ctx_mean
-    return {"streams": B_STREAMS, "value": round(B_STREAMS * steps / dt, 1), "unit": "tokens/s",
-            "ms_per_step": round(ms, 4), "steps": steps,
-            "workload": f"{B_STREAMS} streams, {B_PROMPT}-token random prompts, {B_WORDS} greedy words each "
-                        f"(context to {B_PROMPT + B_WORDS}); streams 0 and 1 checked against base2.py's golden words",
-            "prompt_included": {"value": round(B_STREAMS * B_WORDS / (tp + dt), 1), "unit": "tokens/s",
-                                "prompt_ms": round(1000.0 * tp, 3)},
-            "roofline": {"bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                         "frac": round(ach / HBM_PEAK_GBS, 4), "kernel": "k_head_rows<4,EPI_HEAD>",
-                         "mean_launch_us": round(us, 3), "launches_timed": n,
-                         "int8_tops": round(ops / (us * 1e-6) / 1e12, 1), "int8_frac": round(ops / (us * 1e-6) / 5.0e15, 4)},
-            "step_roofline": {"bytes_per_step": int(sb), "achieved": round(sb / (ms * 1e-3) / 1e9, 1),
-                              "frac": round(sb / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}}
+    sb = WORKLOAD_FIXED + B_STREAMS * KV_WORKLOAD * ctx
+    head = table.get("head", {})
+    out = {"streams": B_STREAMS, "value": round(B_STREAMS * steps / dt, 1), "unit": "tokens/s",
+           "ms_per_step": round(ms, 4), "steps": steps, "graph_steps": GRAPH_STEPS,
+           "workload": f"{B_STREAMS} streams, {B_PROMPT}-token random prompts, {B_WORDS} greedy words each (context "
+                       f"to {B_PROMPT + B_WORDS}); every word of streams " +
+                       ", ".join(f"{s} ({src})" for s, _, src in checks),
+           "prompt_included": {"value": round(B_STREAMS * B_WORDS / (tp + dt), 1), "unit": "tokens/s",
+                               "prompt_ms": round(1000.0 * tp, 3)},
+           "roofline": dominant(table, "b64"),
+           "step_roofline": {"bytes_per_step": int(sb), "achieved": round(sb / (ms * 1e-3) / 1e9, 1),
+                             "frac": round(sb / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+                             "layout_bytes_per_step": int(WORKLOAD_FIXED + B_STREAMS * KV_LAYOUT * ctx)},
+           "kernels": table}
+    if head:
+        ops = 4 * 2 * B_STREAMS * 768 * vocab       # four byte-plane products of 64 x 768 x vocab, 2 ops a MAC
+        out["head_int8"] = {"tops": round(ops / (head["mean_us"] * 1e-6) / 1e12, 1),
+                            "frac": round(ops / (head["mean_us"] * 1e-6) / INT8_PEAK_OPS, 4)}
+    return out
 
 
 def pythia_leg(sm):
-    """The Pythia-160m-shaped machine (random N(0, 0.02) weights from default_rng(5), vocab 50304, rotary on a
-    quarter of each head, parallel residual): 32 streams decoded in lockstep, 64-token prompts (stream s:
-    default_rng(5 + s)), 256 greedy words each, context to 320.  Timed: the 255 decode steps after the prompt
-    pass.  Streams 0 and 1 begin with the golden words pythia_base2.py gives for their prompts."""
-    import torch
     t0 = time.time()
     sd, cfg = sm.pythia.random_pythia(seed=5)
     npz = sm.pythia.convert_pythia(sd, cfg)
     del sd
     lay = tempfile.mkdtemp(prefix="sm_bench_py_")
     sm.pythia.pythia_layout(npz, lay)
-    prompts = [sm.prompt_ids(5 + b, P_PROMPT, 50304) for b in range(P_STREAMS)]
-    gw = golden_words("pythia_golden.json")
-    want = {b: gw[f"py_c5_stream{b}_p64_w4"] for b in (0, 1)}
     del npz
     log(f"pythia: model converted and laid out in {time.time() - t0:.1f}s")
-    m = sm.Machine(lay, max_ctx=P_PROMPT + P_WORDS, max_streams=P_STREAMS, graph_steps=P_WORDS - 1, profile=True,
-                   prefill_rows=PREFILL_ROWS)
-    res = None
-    for it in range(2):                     # the first sequence warms up (graph instantiation)
-        m.reset()
-        torch.cuda.synchronize()
-        t = time.perf_counter()
-        for b, p in enumerate(prompts):
-            m.prefill(p, b)
-        first = m.generate(1)               # the prompt pass and the first word
-        torch.cuda.synchronize()
-        tp = time.perf_counter() - t
-        m.profile(clear=True)
-        t = time.perf_counter()
-        rest = m.generate(P_WORDS - 1)
-        torch.cuda.synchronize()
-        dt = time.perf_counter() - t
-        n, us = m.profile(clear=True)
-        words = np.concatenate([first, rest], axis=1)
-        for b, w in want.items():
-            if [int(x) for x in words[b][:len(w)]] != w:
-                raise RuntimeError(f"pythia stream {b}: GPU words differ from pythia_base2.py's golden words")
-        res = (dt, n, us, tp)
-    vocab = m.vocab
-    m.close()
-    dt, n, us, tp = res
-    steps = P_WORDS - 1
+    prompts = [sm.prompt_ids(5 + b, P_PROMPT, PVOCAB) for b in range(P_STREAMS)]
+    checks = batched_checks("py_c5_stream{}_p64_w256", "py_c5_stream{}_p64_w256", (0, 1), (31,))
+    ctx = P_PROMPT + P_WORDS / 2.0
+    dt, tp, steps, table, vocab = run_batched(sm, lay, P_STREAMS, prompts, P_WORDS, checks, "pythia",
+                                              lambda k: batched_kernel_bytes(k, ctx, P_STREAMS, PVOCAB, head_bias=False))
     ms = 1000.0 * dt / steps
-    hb = head_bytes(vocab) - 8 * vocab                 # no bias on Pythia's head
-    ctx_mean = P_PROMPT + P_WORDS / 2.0
-    layer_w = 12 * (2 * (768 * 2304 + 768 * 768 + 768 * 3072 + 3072 * 768) + 12 * (2304 + 768 + 3072 + 768))
-    sb = layer_w + hb + P_STREAMS * KV_BYTES * ctx_mean
+    fixed = 12 * LAYER_FIXED + 2 * 768 * PVOCAB + 4 * PVOCAB
+    sb = fixed + P_STREAMS * KV_WORKLOAD * ctx
     return {"streams": P_STREAMS, "value": round(P_STREAMS * steps / dt, 1), "unit": "tokens/s",
-            "ms_per_step": round(ms, 4), "steps": steps,
+            "ms_per_step": round(ms, 4), "steps": steps, "graph_steps": GRAPH_STEPS,
             "workload": f"Pythia-160m-shaped integer machine, {P_STREAMS} streams, {P_PROMPT}-token random prompts, "
-                        f"{P_WORDS} greedy words each (context to {P_PROMPT + P_WORDS}); streams 0 and 1 checked "
-                        f"against pythia_base2.py's golden words",
+                        f"{P_WORDS} greedy words each (context to {P_PROMPT + P_WORDS}); every word of streams " +
+                        ", ".join(f"{s} ({src})" for s, _, src in checks),
             "prompt_included": {"value": round(P_STREAMS * P_WORDS / (tp + dt), 1), "unit": "tokens/s",
                                 "prompt_ms": round(1000.0 * tp, 3)},
-            "roofline": {"bound": "hbm", "achieved": round(hb / (us * 1e-6) / 1e9, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                         "frac": round(hb / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4), "kernel": "k_head_rows<2,EPI_PHEAD>",
-                         "mean_launch_us": round(us, 3), "launches_timed": n},
+            "roofline": dominant(table, "pythia"),
             "step_roofline": {"bytes_per_step": int(sb), "achieved": round(sb / (ms * 1e-3) / 1e9, 1),
-                              "frac": round(sb / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}}
+                              "frac": round(sb / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+                              "layout_bytes_per_step": int(fixed + P_STREAMS * KV_LAYOUT * ctx)},
+            "kernels": table}
 
 
-def cpu_baseline(npz, prompt, want, budget_s: float = 20.0):
-    """base2.py's CPU path (numpy restatement): forward(ids + got) per word, as base2.py:123 does."""
-    sys.path.insert(0, REPO)
-    from oracle.base2_np import Base2Numpy
+# ---- config 2: the GEMV microbench ----
+def gemv_leg(sm, rotate_bytes: int = 1 << 30, rounds: int = 3):
+    """int16 plates (uniform, -32768 included) with exponents in [-16, -8] and uniform int16 lights, B = 1;
+    every launch reads a different copy of the plate out of >= 1 GiB of copies (default_rng(2))"""
+    import torch
+    rng = np.random.default_rng(2)
+    shapes = [(768, 2304, 2), (768, 768, 2), (768, 3072, 2), (3072, 768, 1), (768, VOCAB, 4)]
+    out = {}
+    for nin, nout, tc in shapes:
+        w = rng.integers(-32768, 32768, (nin, nout), dtype=np.int16)
+        e = rng.integers(-16, -7, nout, dtype=np.int32)
+        b = np.zeros(nout, np.int64)
+        x = rng.integers(-32768, 32768, nin, dtype=np.int64)
+        plate_b = 2 * nin * nout
+        copies = max(2, -(-rotate_bytes // plate_b))
+        plates = [sm.Plate(w, e, b, tile_cols=tc) for _ in range(copies)]
+        dx = torch.from_numpy(x).cuda()
+        pile = torch.zeros(nout, dtype=torch.int64, device="cuda")
+        plates[0].product(dx.data_ptr(), pile.data_ptr())
+        torch.cuda.synchronize()
+        if not np.array_equal(pile.cpu().numpy(), x @ w.astype(np.int64)):
+            raise RuntimeError(f"gemv {nin}x{nout}: piles differ from the exact product")
+        sm.profile_stages(True)
+        sm.kernel_times(clear=True)
+        for _ in range(rounds):
+            for p in plates:
+                p.product(dx.data_ptr(), pile.data_ptr())
+        cold = sm.kernel_times(clear=True)["plate.gemv"]
+        for _ in range(rounds * 20):
+            plates[0].product(dx.data_ptr(), pile.data_ptr())
+        warm = sm.kernel_times(clear=True)["plate.gemv"]
+        sm.profile_stages(False)
+        for p in plates:
+            p.close()
+        del plates
+        out[f"{nin}x{nout}"] = {
+            "plate_bytes": plate_b, "copies": copies, "tile_cols": tc,
+            "us": round(cold[1], 3), "gbs": round(plate_b / (cold[1] * 1e-6) / 1e9, 1),
+            "frac": round(plate_b / (cold[1] * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+            "warm_us": round(warm[1], 3), "warm_gbs": round(plate_b / (warm[1] * 1e-6) / 1e9, 1)}
+    return {"note": "kernel durations from HIP event pairs stamped by each dispatch; 'us' rotates over >= 1 GiB of "
+                    "plate copies (the Infinity Cache holds none of the plate), 'warm_us' re-reads one copy; bytes "
+                    "are the int16 plate only", "shapes": out}
+
+
+# ---- config 3: one attention step ----
+def attention_leg(sm, reps: int = 50):
+    """12 heads x 64, int16 keys and values uniform at T = 128, 512, 1024 (default_rng(3)), one new q, k, v; the
+    batch-1 attention kernel (sm_stage_attend)"""
+    import torch
+    rng = np.random.default_rng(3)
+    t = sm.Tables(sm.tables())
+    out = {}
+    for T in (128, 512, 1024):
+        ctx = T
+        p = T - 1                                   # the new position; T positions attended
+        k16 = torch.from_numpy(rng.integers(-32768, 32768, (12, ctx, 64), dtype=np.int16)).cuda()
+        km = torch.zeros((12, ctx), dtype=torch.int64, device="cuda")
+        ek = torch.from_numpy(rng.integers(-16, -7, (12, ctx), dtype=np.int32)).cuda()
+        v = torch.from_numpy(rng.integers(-32768, 32768, (12, ctx, 64), dtype=np.int64).astype(np.int32)).cuda()
+        qkv = torch.from_numpy(rng.integers(-32768, 32768, 2304, dtype=np.int64)).cuda()
+        o = torch.zeros(768, dtype=torch.int64, device="cuda")
+        sm.profile_stages(True)
+        sm.kernel_times(clear=True)
+        for _ in range(reps):
+            sm.stages.attend(t, qkv.data_ptr(), k16.data_ptr(), km.data_ptr(), ek.data_ptr(), v.data_ptr(), p, ctx, o.data_ptr())
+        n, us = sm.kernel_times(clear=True)["stage.attend"]
+        sm.profile_stages(False)
+        kv = T * 768 * 2 * 2                         # int16 k and v (SURVEY 8(d) config 3)
+        layout = T * 12 * (128 + 8 + 4 + 256)        # this layout: int16 k, int64 mask, int32 level, int32 v
+        out[str(T)] = {"us": round(us, 3), "kv_bytes": kv, "layout_bytes": layout,
+                       "gbs_layout": round(layout / (us * 1e-6) / 1e9, 1)}
+    t.close()
+    return {"note": "kernel durations from HIP event pairs stamped by each dispatch; the batch-1 attention kernel "
+                    "(one block a head), warm", "T": out}
+
+
+# ---- CPU baseline ----
+def cpu_info():
+    model = ""
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    info = {"nproc": os.cpu_count(), "affinity": len(os.sched_getaffinity(0)), "cpu_model": model or platform.processor(),
+            "numpy": np.__version__}
     try:
         from threadpoolctl import threadpool_info
         blas = [i for i in threadpool_info() if i.get("user_api") == "blas"]
-        cores = int(blas[0]["num_threads"]) if blas else 1
+        if blas:
+            info["blas"] = f"{blas[0].get('internal_api')} {blas[0].get('version')}"
+            info["blas_threads"] = int(blas[0]["num_threads"])
     except Exception:
-        cores = 1
+        pass
+    return info
+
+
+def cpu_baseline(npz, prompt, want, runs: int = 5, words: int = 5):
+    """base2.py's CPU path (numpy restatement, forward(ids + got) per word as base2.py:123 does) on words 2..1+words
+    of the config-1 sequence, median of `runs` after one warm-up, at all cores and one thread; and the KV-cached C
+    oracle over words 2..16"""
+    sys.path.insert(0, REPO)
+    import oracle
+    from oracle.base2_np import Base2Numpy
+    from threadpoolctl import threadpool_limits
+    info = cpu_info()
     nb = Base2Numpy(npz)
-    got, t_total, n = [], 0.0, 0
-    for i in range(len(want)):
+    first = nb.forward(list(prompt))
+    if first != want[0]:
+        raise RuntimeError("cpu baseline: the first word differs from the GPU's")
+
+    def full_run():
+        got = [first]
         t0 = time.perf_counter()
-        w = nb.forward(list(prompt) + got)
+        for _ in range(words):
+            got.append(nb.forward(list(prompt) + got))
         dt = time.perf_counter() - t0
-        got.append(w)
-        if i > 0:                       # decode words only (the first word is the prompt pass)
-            t_total += dt
-            n += 1
-        if t_total > budget_s and n >= 2:
-            break
-    if got != want[:len(got)]:
-        raise RuntimeError(f"cpu baseline words differ from the GPU's: {got} vs {want[:len(got)]}")
-    return {"value": n / t_total, "unit": "tokens/s", "cores": cores, "kind": "port",
-            "sample": f"words 2..{n + 1} of the 8-token-prompt sequence, full recompute per word (context 9..{8 + n}), "
-                      f"numpy float64-BLAS products and the top-down race loop"}
+        if got != want[:len(got)]:
+            raise RuntimeError(f"cpu baseline words differ from the GPU's: {got}")
+        return words / dt
+
+    def median(f):
+        f()
+        return float(np.median([f() for _ in range(runs)]))
+
+    allc = median(full_run)
+    with threadpool_limits(limits=1):
+        one = median(full_run)
+    orc = oracle.Oracle(npz)
+
+    def kv_run():
+        s = orc.session(64)
+        tok = None
+        for i, t in enumerate(prompt):
+            tok = s.step(t, want_head=i == len(prompt) - 1)
+        got = [tok]
+        t0 = time.perf_counter()
+        for _ in range(WORDS - 1):
+            got.append(s.step(got[-1]))
+        dt = time.perf_counter() - t0
+        if got != want:
+            raise RuntimeError("cpu baseline: the KV-cached oracle's words differ from the GPU's")
+        return (WORDS - 1) / dt
+
+    threads = oracle.set_threads(0)
+    kv_all = median(kv_run)
+    oracle.set_threads(1)
+    kv_one = median(kv_run)
+    oracle.set_threads(0)
+    return {"value": round(allc, 3), "unit": "tokens/s", "cores": info.get("blas_threads", info["affinity"]),
+            "kind": "port",
+            "sample": f"words 2..{words + 1} of the 8-token-prompt sequence (context 9..{8 + words}), full recompute "
+                      f"per word as base2.py:123 does, numpy float64-BLAS products and the top-down race loop; "
+                      f"median of {runs} runs after one warm-up",
+            "one_thread": round(one, 3), "median_of": runs, **info,
+            "kv_cached": {"value": round(kv_all, 2), "one_thread": round(kv_one, 2), "threads": threads,
+                          "kind": "port (the C oracle's KV-cached step, OpenMP)",
+                          "sample": f"words 2..{WORDS} of the same sequence (context 9..{8 + WORDS - 1}), median of {runs}"}}
 
 
 def main():
@@ -243,8 +513,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-batched", action="store_true", help="skip the 64-stream leg")
     ap.add_argument("--no-pythia", action="store_true", help="skip the Pythia 32-stream leg")
-    ap.add_argument("--head-grid", type=int, default=0)
-    ap.add_argument("--only", choices=("b1", "b64", "pythia"), default="",
+    ap.add_argument("--no-micro", action="store_true", help="skip the GEMV and attention microbenchmarks")
+    ap.add_argument("--only", choices=("b1", "b64", "pythia", "gemv", "attention"), default="",
                     help="profiling: run one leg and print only its result (not the bench line)")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MB",
                     help="profiling: first copy MB MiB device to device (calibrates HBM byte counters)")
@@ -262,115 +532,81 @@ def main():
     global PREFILL_ROWS
     PREFILL_ROWS = args.prefill_rows
     sm = load_sm()
+    import torch
     if args.copy_probe:
-        import torch
         src = torch.ones(args.copy_probe << 18, dtype=torch.int32, device="cuda")
         dst = torch.empty_like(src)
         dst.copy_(src)
         torch.cuda.synchronize()
         log(f"copy probe: {args.copy_probe} MiB device to device")
         del src, dst
-    if args.only == "b64":
-        print(json.dumps(batched_leg(sm, None)), flush=True)
+    if args.only == "gemv":
+        print(json.dumps(gemv_leg(sm)), flush=True)
+        return
+    if args.only == "attention":
+        print(json.dumps(attention_leg(sm)), flush=True)
         return
     if args.only == "pythia":
         print(json.dumps(pythia_leg(sm)), flush=True)
         return
     t0 = time.time()
-    sd = sm.random_gpt2(seed=0)
-    npz = sm.convert(sd)
-    del sd
+    npz = sm.convert(sm.random_gpt2(seed=0))
     lay = args.layout or tempfile.mkdtemp(prefix="sm_bench_")
     if not os.path.exists(os.path.join(lay, "manifest.json")):
         sm.layout(npz, lay)
     log(f"model converted and laid out in {time.time() - t0:.1f}s")
+    if args.only == "b64":
+        print(json.dumps(batched_leg(sm, lay)), flush=True)
+        return
     prompt = sm.prompt_ids(1, PROMPT)
-
-    # the parity gate: base2.py's own words for this sequence (golden fixture written from the reference)
-    want = golden_words("base2_golden.json")["c1_p8_w16"]
-
-    import torch
-    m = sm.Machine(lay, max_ctx=64, head_grid=args.head_grid, graph_steps=WORDS - 1, profile=True,
-                   prefill_rows=PREFILL_ROWS)
-    vocab = m.vocab
-
-    def sequence(timed: bool):
-        m.reset()
-        torch.cuda.synchronize()
-        t = time.perf_counter()
-        m.prefill(prompt)
-        first = int(m.generate(1)[0, 0])        # the prompt pass and the first word
-        torch.cuda.synchronize()
-        tp = time.perf_counter() - t
-        m.profile(clear=True)
-        t = time.perf_counter()
-        rest = [int(w) for w in m.generate(WORDS - 1)[0]]
-        torch.cuda.synchronize()
-        dt = time.perf_counter() - t
-        words = [first] + rest
-        if words != want:
-            raise RuntimeError(f"GPU words differ from base2.py's golden words: {words} vs {want}")
-        n, us = m.profile(clear=True)
-        return dt, n, us, tp
-
-    for _ in range(max(1, -(-args.warmup // (WORDS - 1)))):
-        sequence(False)
-    total, steps, head_n, head_us_sum, prompt_s, nseq = 0.0, 0, 0, 0.0, 0.0, 0
-    while steps < args.steps:
-        dt, n, us, tp = sequence(True)
-        prompt_s += tp
-        nseq += 1
-        k = min(WORDS - 1, args.steps - steps)
-        total += dt * k / (WORDS - 1)
-        steps += k
-        head_n += n
-        head_us_sum += us * n
-    head_us = head_us_sum / head_n
-    ms_per_step = 1000.0 * total / steps
-    tok_s = steps / total
-    hb = head_bytes(vocab)
-    ach = hb / (head_us * 1e-6) / 1e9
-    ctx_mean = PROMPT + WORDS / 2.0
-    sb = step_bytes(vocab, ctx_mean)
-    step_ach = sb / (ms_per_step * 1e-3) / 1e9
-
-    traffic = None
-    tfile = os.path.join(REPO, "profiles", "head_gemv_traffic.txt")
-    if os.path.exists(tfile):
-        for line in open(tfile):
-            if line.startswith("traffic_bytes_per_launch:"):
-                traffic = int(float(line.split(":")[1]))
-
-    m.close()
+    want = fixture_cases("base2_golden.json")["c1_p8_w16"]["words"]      # base2.py's own words for this sequence
+    b1 = b1_leg(sm, lay, args.steps, args.warmup, prompt, want)
+    log(f"batch 1: {b1['tok_s']:.1f} tokens/s, {b1['ms']:.4f} ms/step")
+    table = b1["table"]
+    sb = WORKLOAD_FIXED + KV_WORKLOAD * b1["ctx"]
+    step_ach = sb / (b1["ms"] * 1e-3) / 1e9
+    warm_sum = sum(r["us_per_step"] for r in table.values())
+    cold_sum = sum(r["us_per_step"] for r in b1["cold"].values())
+    cold = {"note": "1 GiB streamed through the device before each step (outside the timed launches); kernel "
+                    "durations from the profiled pass", "steps": 15,
+            "kernel_us_per_step": round(cold_sum, 2), "warm_kernel_us_per_step": round(warm_sum, 2),
+            "kernels": {k: {"mean_us": r["mean_us"], "warm_us": table[k]["mean_us"] if k in table else None,
+                            **({"gbs": r["gbs"], "frac": r["frac"]} if "gbs" in r else {})}
+                        for k, r in b1["cold"].items()}}
     if args.only == "b1":
-        print(json.dumps({"value": round(tok_s, 2), "ms_per_step": round(ms_per_step, 4), "head_us": round(head_us, 3),
-                          "prompt_ms": round(1000.0 * prompt_s / nseq, 3)}), flush=True)
+        print(json.dumps({"value": round(b1["tok_s"], 2), "ms_per_step": round(b1["ms"], 4), "kernels": table,
+                          "cold": cold, "prompt_ms": round(b1["prompt_ms"], 3)}), flush=True)
         return
     batched = None if args.no_batched else batched_leg(sm, lay)
     if batched:
-        log(f"batched: {batched['value']} tokens/s, {batched['ms_per_step']} ms/step, head {batched['roofline']['mean_launch_us']} us")
+        log(f"batched: {batched['value']} tokens/s, {batched['ms_per_step']} ms/step")
     pyleg = None if args.no_pythia else pythia_leg(sm)
     if pyleg:
-        log(f"pythia: {pyleg['value']} tokens/s, {pyleg['ms_per_step']} ms/step, head {pyleg['roofline']['mean_launch_us']} us")
+        log(f"pythia: {pyleg['value']} tokens/s, {pyleg['ms_per_step']} ms/step")
+    gemv = None if args.no_micro else gemv_leg(sm)
+    att = None if args.no_micro else attention_leg(sm)
     cpu = None if args.no_cpu else cpu_baseline(npz, prompt, want)
     out = {
-        "metric": METRIC, "value": round(tok_s, 2), "unit": "tokens/s", "n_gpus": 1, "steps": steps,
-        "warmup": args.warmup, "ms_per_step": round(ms_per_step, 4), "higher_is_better": True, "scaling": "weak",
+        "metric": METRIC, "value": round(b1["tok_s"], 2), "unit": "tokens/s", "n_gpus": 1, "steps": b1["steps"],
+        "warmup": args.warmup, "ms_per_step": round(b1["ms"], 4), "higher_is_better": True, "scaling": "weak",
         "vs_baseline": None, "dtype": "int64", "data": "synthetic",
         "config": {"workload": "GPT-2 124M integer base-2 decode, batch 1, 8-token random prompt, 16 greedy words "
                                "per sequence (15 decode steps, context 9..23), random-init N(0,0.02) seed 0",
-                   "batch": 1, "prompt": PROMPT, "words": WORDS, "vocab": vocab},
-        "roofline": {"bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": traffic,
-                     "kernel": "k_gemv<768,4,4,PRO_GAUGE,EPI_HEAD> (head plate read; the race is its own launch)",
-                     "bytes_per_launch": hb, "mean_launch_us": round(head_us, 3), "launches_timed": head_n},
-        "step_roofline": {"bytes_per_step": int(sb), "achieved": round(step_ach, 1), "frac": round(step_ach / HBM_PEAK_GBS, 4)},
-        "prompt_included": {"value": round(WORDS / (prompt_s / nseq + ms_per_step * 1e-3 * (WORDS - 1)), 2), "unit": "tokens/s",
-                            "prompt_ms": round(1000.0 * prompt_s / nseq, 3),
+                   "batch": 1, "prompt": PROMPT, "words": WORDS, "vocab": VOCAB},
+        "roofline": dominant(table, "b1"),
+        "step_roofline": {"bytes_per_step": int(sb), "achieved": round(step_ach, 1), "frac": round(step_ach / HBM_PEAK_GBS, 4),
+                          "bytes": "SURVEY 8(d): 248,662,476 + 73,728 T at mean T = 16",
+                          "layout_bytes_per_step": int(WORKLOAD_FIXED + KV_LAYOUT * b1["ctx"])},
+        "kernels": table,
+        "cold": cold,
+        "prompt_included": {"value": round(WORDS / (b1["prompt_ms"] * 1e-3 + b1["ms"] * 1e-3 * (WORDS - 1)), 2),
+                            "unit": "tokens/s", "prompt_ms": round(b1["prompt_ms"], 3),
                             "note": "16 words per sequence over the prompt pass (7 prompt rows through the int8 MFMA "
                                     "banks, then the first word's step) plus 15 decode steps"},
         "batched": batched,
         "pythia": pyleg,
+        "gemv": gemv,
+        "attention": att,
         "cpu_baseline": cpu,
     }
     print(json.dumps(out), flush=True)

@@ -41,7 +41,8 @@ typedef struct {
     int32_t use_graph;     /* 1: replay captured HIP graphs of decode steps; 0: plain launches */
     int32_t head_grid;     /* blocks of the head's plate read (0: default) */
     int32_t graph_steps;   /* decode steps per captured graph (0: 16) */
-    int32_t profile;       /* 1: time every head launch with a HIP event pair on the machine's stream */
+    int32_t profile;       /* 1: launch the decode steps kernel by kernel (no graphs), each launch stamped with a HIP
+                              event pair by its own dispatch (sm_profile, sm_profile_kernels) */
     int32_t table_mode;    /* 0: read the tables from memory; 1: recompute each entry from its formula when every
                               loaded entry matches it (checked on the device at create), else read the tables */
     int32_t prefill_rows;  /* 0: the prompt runs position by position through the decode step; 1..64: every prompt
@@ -101,8 +102,19 @@ enum {
 int sm_read(sm_machine* m, int32_t what, int32_t layer, int32_t stream, int32_t pos, void* dst, size_t bytes);
 
 /* Head-launch timing gathered with profile = 1: launches seen and their summed duration (microseconds,
- * HIP events on the machine's stream).  Replaces fr2's bench= timing (base2_stream_fr2.swift:1060-1075). */
+ * HIP events stamped by each head dispatch).  clear = 1 empties the kernel-timing table afterwards.  Replaces fr2's
+ * bench= timing (base2_stream_fr2.swift:1060-1075). */
 int sm_profile(sm_machine* m, int64_t* n_heads, double* head_us, int32_t clear);
+
+/* Kernel timing, process-wide.  Launches of a machine created with profile = 1 and, after sm_profile_stages(1),
+ * of the stage and plate entry points are each stamped with a HIP event pair by their own dispatch (the interval a
+ * kernel trace reports).  sm_profile_kernels waits for the device and returns, per kernel name, the launches and
+ * their summed duration in microseconds since the last clear: names receives the names, each ended by '\n'
+ * (names_bytes at most), launches and total_us at most max entries, *n how many; clear = 1 empties the table.
+ * Replaces fr2's sbench= and pbench= timings of fused steps and plate reads (base2_stream_fr2.swift:1077-1149). */
+int sm_profile_stages(int32_t on);
+int sm_profile_kernels(char* names, int32_t names_bytes, int64_t* launches, double* total_us, int32_t max, int32_t* n,
+                       int32_t clear);
 
 /* Facts about a created machine: vocab, max_ctx, max_streams, rows of the position table, and whether the
  * table entries are recomputed from their formulas (1) or read from memory (0). */

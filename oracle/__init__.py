@@ -200,6 +200,15 @@ class KVSession:
         return R
 
 
+def set_threads(n: int) -> int:
+    """OpenMP threads of the C oracle's parallel loops (0: every processor); returns the count in force"""
+    L = ctypes.CDLL(build())
+    L.orc_set_threads.argtypes = [ctypes.c_int]
+    L.orc_get_threads.restype = ctypes.c_int
+    L.orc_set_threads(int(n))
+    return int(L.orc_get_threads())
+
+
 def stage_lib():
     """The C oracle's stage functions with argtypes set (rshift, log2fix, power, edge, to16, gauge_log, product, race)."""
     L = ctypes.CDLL(build())

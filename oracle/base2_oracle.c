@@ -77,6 +77,11 @@ i64 orc_edge1(i64 h, const i64* PHI) {
 }
 
 /* ---------------- vector forms for the stage tests ---------------- */
+/* OpenMP threads for the parallel loops below (the CPU baseline times one thread and all of them) */
+#include <omp.h>
+void orc_set_threads(int n) { omp_set_num_threads(n > 0 ? n : omp_get_num_procs()); }
+int orc_get_threads(void) { return omp_get_max_threads(); }
+
 void orc_rshift(const i64* x, const i64* s, i64* out, i64 n) { for (i64 i = 0; i < n; i++) out[i] = orc_rshift1(x[i], s[i]); }
 void orc_log2fix(const i64* v, i64* out, i64 n, const i64* LOG2) { for (i64 i = 0; i < n; i++) out[i] = orc_log2fix1(v[i], LOG2); }
 void orc_power(const i64* x, const i64* F, i64* out, i64 n, const i64* EXP2) { for (i64 i = 0; i < n; i++) out[i] = orc_power1(x[i], F[i], EXP2); }

@@ -17,7 +17,8 @@ from . import refs  # noqa: F401
 
 def __getattr__(name):
     # the ctypes binding is loaded on first use so that CPU-only callers never need the HIP runtime
-    if name in ("Machine", "Tables", "Plate", "lib", "LIB_PATH", "SmError", "stages", "check"):
+    if name in ("Machine", "Tables", "Plate", "lib", "LIB_PATH", "SmError", "stages", "check", "profile_stages",
+                "kernel_times"):
         from . import machine
         return getattr(machine, name)
     raise AttributeError(name)

@@ -990,5 +990,6 @@ template __global__ void k_embed1<1>(Race1Args);
 // raw piles of a given light (stage entry point)
 template __global__ void k_gemv<768, 2, 4, PRO_X16, EPI_PILE, 0>(GemvArgs);
 template __global__ void k_gemv<768, 8, 4, PRO_X16, EPI_PILE, 0>(GemvArgs);
+template __global__ void k_gemv<768, 4, 4, PRO_X16, EPI_PILE, 0>(GemvArgs);
 template __global__ void k_gemv<3072, 1, 4, PRO_X16, EPI_PILE, 0>(GemvArgs);
 template __global__ void k_gemv<3072, 2, 4, PRO_X16, EPI_PILE, 0>(GemvArgs);

@@ -39,6 +39,76 @@ static int fail(int code, const std::string& msg) {
 extern "C" const char* sm_last_error(void) { return g_err.c_str(); }
 
 // ---------------------------------------------------------------------------------------------------------
+// Kernel timing.  A machine created with profile = 1 (its launches) and, after sm_profile_stages(1), the stage and
+// plate entry points stamp every launch with a HIP event pair by its own dispatch (hipExtLaunchKernelGGL on the
+// launching stream: the interval a kernel trace reports); sm_profile_kernels folds the pairs into launches and
+// summed microseconds per kernel name.  Launches that are not timed pass null events.
+struct KernelTiming {
+    std::mutex mu;
+    bool stages = false;
+    std::vector<std::string> names;
+    std::vector<long long> n;
+    std::vector<double> us;
+    struct Pend { int id; hipEvent_t s, e; };
+    std::vector<Pend> pend;
+    std::vector<hipEvent_t> spare;
+};
+static KernelTiming g_kt;
+
+static int kt_id(const char* name) {                 // (g_kt.mu held)
+    for (size_t i = 0; i < g_kt.names.size(); i++)
+        if (g_kt.names[i] == name) return (int)i;
+    g_kt.names.push_back(name);
+    g_kt.n.push_back(0);
+    g_kt.us.push_back(0.0);
+    return (int)g_kt.names.size() - 1;
+}
+static hipEvent_t kt_event() {                       // (g_kt.mu held)
+    hipEvent_t e = nullptr;
+    if (!g_kt.spare.empty()) {
+        e = g_kt.spare.back();
+        g_kt.spare.pop_back();
+    } else if (hipEventCreate(&e) != hipSuccess) {
+        e = nullptr;
+    }
+    return e;
+}
+
+template <typename F, typename... A>
+static void launch(bool timed, const char* name, F kernel, dim3 grid, dim3 block, size_t shmem, hipStream_t st, A... args) {
+    hipEvent_t s = nullptr, e = nullptr;
+    if (timed) {
+        std::lock_guard<std::mutex> lock(g_kt.mu);
+        s = kt_event();
+        e = kt_event();
+        if (s && e) {
+            g_kt.pend.push_back({kt_id(name), s, e});
+        } else {
+            if (s) g_kt.spare.push_back(s);
+            if (e) g_kt.spare.push_back(e);
+            s = e = nullptr;
+        }
+    }
+    hipExtLaunchKernelGGL(kernel, grid, block, (std::uint32_t)shmem, st, s, e, 0u, args...);
+}
+
+// every pending pair, once the device has finished them, into the per-name sums
+static int kt_fold() {
+    HIP_TRY(hipDeviceSynchronize());
+    std::lock_guard<std::mutex> lock(g_kt.mu);
+    for (const auto& p : g_kt.pend) {
+        float ms = 0.f;
+        if (hipEventElapsedTime(&ms, p.s, p.e) != hipSuccess) return fail(SM_E_HIP, "hipEventElapsedTime");
+        g_kt.n[p.id]++;
+        g_kt.us[p.id] += 1000.0 * ms;
+        g_kt.spare.push_back(p.s);
+        g_kt.spare.push_back(p.e);
+    }
+    g_kt.pend.clear();
+    return SM_OK;
+}
+
+// ---------------------------------------------------------------------------------------------------------
 // plates
 struct DevPlate {
     int nin = 0, nout = 0, tc = 0, ntiles = 0;
@@ -256,9 +326,6 @@ struct sm_machine {
     hipGraph_t graph[4] = {};
     int gsteps = 16;
     // profiling: an event pair around each step's head kernel (the largest single launch)
-    std::vector<hipEvent_t> ev_s, ev_e;
-    double prof_head_us = 0.0;
-    long long prof_n = 0;
     // prompt passes: row r of a pass is position pfmap[r] & 0xFFFF of stream pfmap[r] >> 16
     int* pfmap = nullptr;                               // [B][ctx]
     std::vector<int> h_pfmap;
@@ -357,8 +424,6 @@ static void machine_free(sm_machine* m) {
         if (m->gexec[i]) (void)hipGraphExecDestroy(m->gexec[i]);
         if (m->graph[i]) (void)hipGraphDestroy(m->graph[i]);
     }
-    for (auto e : m->ev_s) (void)hipEventDestroy(e);
-    for (auto e : m->ev_e) (void)hipEventDestroy(e);
     for (int l = 0; l < 12; l++)
         for (int k = 0; k < 4; k++) { free_plate(m->bank[l][k]); free_mfma_plate(m->mbank[l][k]); }
     free_plate(m->head);
@@ -387,7 +452,7 @@ static int head_rows_grid(int ntiles) { return std::min(512, ntiles); }
 // instead of one position of every stream.  Their words are known, so no head runs, and the last layer only
 // stores keys and values (its attention and banks feed the head alone); nothing is recorded.
 template <int RT>
-static int launch_step_batched(sm_machine* m, int parts, hipEvent_t hs, hipEvent_t he, int nrows = 0,
+static int launch_step_batched(sm_machine* m, int parts, int nrows = 0,
                                const int* rowmap = nullptr) {
     const Tables tb = m->T.tb();
     int* ctl = m->ctl;
@@ -407,7 +472,7 @@ static int launch_step_batched(sm_machine* m, int parts, hipEvent_t hs, hipEvent
         a.ls_row = ls_row;
         a.part = m->part_acc; a.kin = P.K; a.csum = P.csum; a.we = P.e; a.bias = P.b; a.Y = m->R;
         a.rpile_in = rpile; a.rout_in = rout; a.sfacts = m->sfacts;
-        k_light<768, PRO_ADD_GAUGE, 192, 4><<<B, 192, 0, m->st>>>(a);
+        launch(m->cfg.profile, "light.add_gauge", k_light<768, PRO_ADD_GAUGE, 192, 4>, dim3(B), dim3(192), 0, m->st, a);
     };
     auto gemm_args = [&](const MfmaPlate& P, i64* Y, int ystride, i64* rpile, i64* rout) {
         GemmArgs a{};
@@ -423,11 +488,11 @@ static int launch_step_batched(sm_machine* m, int parts, hipEvent_t hs, hipEvent
         i64* rp = m->r_pile + (size_t)l * 4 * 3072;
         if (l == 0) {      // the word enters; later layers get their light from the previous layer's last kernel
             LightArgs a = light_args(768, m->R, rx, re);
-            k_light<768, PRO_EMBED, 192, 1><<<B, 192, 0, m->st>>>(a);
+            launch(m->cfg.profile, "light.embed", k_light<768, PRO_EMBED, 192, 1>, dim3(B), dim3(192), 0, m->st, a);
         }
         {
             GemmArgs a = gemm_args(m->mbank[l][0], m->QKV, 2304, rp, m->r_qkv + l * 2304);
-            k_gemm<768, 1, 1, EPI_GAUGED><<<dim3(m->mbank[l][0].ntiles, RT), 256, 0, m->st>>>(a);
+            launch(m->cfg.profile, "qkv", k_gemm<768, 1, 1, EPI_GAUGED>, dim3(m->mbank[l][0].ntiles, RT), dim3(256), 0, m->st, a);
         }
         {
             AttArgs a{};
@@ -436,11 +501,11 @@ static int launch_step_batched(sm_machine* m, int parts, hipEvent_t hs, hipEvent
             a.out = m->att; a.pos = ctl + CTL_POS; a.ctx = m->ctx; a.tb = tb; a.err = ctl + CTL_ERR;
             a.rec_pos = recp; a.ratt = m->r_att + l * 768; a.rowmap = rowmap; a.out_or = m->attor;
             if (rowmap) {
-                k_kv_rows<0><<<dim3(12, B), 128, 0, m->st>>>(a);
+                launch(m->cfg.profile, "kv_rows", k_kv_rows<0>, dim3(12, B), dim3(128), 0, m->st, a);
                 if (l == 11) break;
-                k_attend<0, 0, 1><<<dim3(12, B), NTHR, (size_t)m->ctx * 12, m->st>>>(a);
+                launch(m->cfg.profile, "attend", k_attend<0, 0, 1>, dim3(12, B), dim3(NTHR), (size_t)m->ctx * 12, m->st, a);
             } else {
-                k_attend<0, 0, 1><<<dim3(12, m->B), NTHR, (size_t)m->ctx * 12, m->st>>>(a);
+                launch(m->cfg.profile, "attend", k_attend<0, 0, 1>, dim3(12, m->B), dim3(NTHR), (size_t)m->ctx * 12, m->st, a);
             }
         }
         {   // proj: the attention rows' light formed in the bank, the plain bank added into the stream; then the
@@ -448,20 +513,20 @@ static int launch_step_batched(sm_machine* m, int parts, hipEvent_t hs, hipEvent
             // table reads would follow the row's conversion there)
             GemmArgs a = gemm_args(m->mbank[l][1], m->R, 768, rp + 3072, m->r_resid + (l * 2 + 0) * 768);
             a.X = m->att; a.xstride = 768; a.orw = m->attor; a.rx16 = rx + 3072; a.rexls = re + 2;
-            k_gemm<768, 1, 1, EPI_PLAIN_ADD, 12><<<dim3(m->mbank[l][1].ntiles, RT), 256, 0, m->st>>>(a);
+            launch(m->cfg.profile, "proj", k_gemm<768, 1, 1, EPI_PLAIN_ADD, 12>, dim3(m->mbank[l][1].ntiles, RT), dim3(256), 0, m->st, a);
             LightArgs g = light_args(768, m->R, rx + 2 * 3072, re + 4);
-            k_light<768, PRO_GAUGE, 192, 1><<<B, 192, 0, m->st>>>(g);
+            launch(m->cfg.profile, "light.gauge", k_light<768, PRO_GAUGE, 192, 1>, dim3(B), dim3(192), 0, m->st, g);
         }
         {   // fc: gauged, the edge, written (the hidden rows) with their OR words
             GemmArgs a = gemm_args(m->mbank[l][2], m->hid, 3072, rp + 2 * 3072, m->r_hid + l * 3072);
             a.orw_out = m->hidor;
-            k_gemm<768, 1, 1, EPI_GAUGED_EDGE><<<dim3(m->mbank[l][2].ntiles, RT), 256, 0, m->st>>>(a);
+            launch(m->cfg.profile, "fc", k_gemm<768, 1, 1, EPI_GAUGED_EDGE>, dim3(m->mbank[l][2].ntiles, RT), dim3(256), 0, m->st, a);
         }
         {   // mproj: the hidden rows' light formed in each K slice's blocks; partial accumulators and slice facts
             GemmArgs a = gemm_args(m->mbank[l][3], nullptr, 0, nullptr, nullptr);
             a.X = m->hid; a.xstride = 3072; a.orw = m->hidor; a.rx16 = rx + 3 * 3072; a.rexls = re + 6;
             a.sfacts = m->sfacts;
-            k_gemm<3072, 3, 4, EPI_PART, 192><<<dim3(m->mbank[l][3].ntiles / 3 * 4, RT), 256, 0, m->st>>>(a);
+            launch(m->cfg.profile, "mproj.part", k_gemm<3072, 3, 4, EPI_PART, 192>, dim3(m->mbank[l][3].ntiles / 3 * 4, RT), dim3(256), 0, m->st, a);
         }
         const bool last = l == 11;     // the last stream update lights the head
         finish_light(m->mbank[l][3], rp + 3 * 3072, m->r_resid + (l * 2 + 1) * 768,
@@ -473,13 +538,12 @@ static int launch_step_batched(sm_machine* m, int parts, hipEvent_t hs, hipEvent
         // the head: each wave's row tile of lights in registers, weight tiles streamed through LDS
         const int grid = head_rows_grid(m->mhead.ntiles), parts = grid;
         a.part_v = m->part_v; a.part_i = m->part_i; a.nblk = parts; a.rlogits = m->r_logits;
-        if (hs) hipExtLaunchKernelGGL(k_head_rows<RT, EPI_HEAD>, dim3(grid), dim3(256), 0, m->st, hs, he, 0, a);
-        else k_head_rows<RT, EPI_HEAD><<<grid, 256, 0, m->st>>>(a);
+        launch(m->cfg.profile, "head", k_head_rows<RT, EPI_HEAD>, dim3(grid), dim3(256), 0, m->st, a);
         RaceArgs r{};
         r.part_v = m->part_v; r.part_i = m->part_i; r.nblk = parts; r.seq = m->seq; r.seq_stride = m->ctx + 1;
         r.words = m->words; r.words_stride = m->ctx + 1; r.pos = ctl + CTL_POS; r.plen = ctl + CTL_PLEN;
         r.nwords = ctl + CTL_NWORDS; r.counter = reinterpret_cast<unsigned*>(ctl + CTL_COUNTER);
-        k_race_rows<<<B, 256, 0, m->st>>>(r);
+        launch(m->cfg.profile, "race", k_race_rows, dim3(B), dim3(256), 0, m->st, r);
     }
     HIP_TRY(hipGetLastError());
     return SM_OK;
@@ -505,36 +569,29 @@ static Race1Args race1_args(sm_machine* m) {
     return r;
 }
 static void launch_race1(sm_machine* m) {
-    if (m->kind == 1) k_race1<1><<<1, 256, 0, m->st>>>(race1_args(m));
-    else k_race1<0><<<1, 256, 0, m->st>>>(race1_args(m));
+    if (m->kind == 1) launch(m->cfg.profile, "race", k_race1<1>, dim3(1), dim3(256), 0, m->st, race1_args(m));
+    else launch(m->cfg.profile, "race", k_race1<0>, dim3(1), dim3(256), 0, m->st, race1_args(m));
 }
 static void launch_embed1(sm_machine* m) {
-    if (m->kind == 1) k_embed1<1><<<1, 256, 0, m->st>>>(race1_args(m));
-    else k_embed1<0><<<1, 256, 0, m->st>>>(race1_args(m));
+    if (m->kind == 1) launch(m->cfg.profile, "embed", k_embed1<1>, dim3(1), dim3(256), 0, m->st, race1_args(m));
+    else launch(m->cfg.profile, "embed", k_embed1<0>, dim3(1), dim3(256), 0, m->st, race1_args(m));
 }
 
-// a batch-1 GEMV phase: rec selects the instantiation that records (launched only for the recorded step); an
-// event pair (hs, he) is stamped by the dispatch itself when given
+// a batch-1 GEMV phase: rec selects the instantiation that records (launched only for the recorded step)
 template <int NIN, int TC, int WPB, int PRO, int EPI>
-static void gemv(sm_machine* m, bool rec, int grid, const GemvArgs& a, hipEvent_t hs = nullptr, hipEvent_t he = nullptr) {
-    if (hs) {
-        if (rec) hipExtLaunchKernelGGL(k_gemv<NIN, TC, WPB, PRO, EPI, 1>, dim3(grid), dim3(64 * WPB), 0, m->st, hs, he, 0, a);
-        else hipExtLaunchKernelGGL(k_gemv<NIN, TC, WPB, PRO, EPI, 0>, dim3(grid), dim3(64 * WPB), 0, m->st, hs, he, 0, a);
-    } else if (rec) {
-        k_gemv<NIN, TC, WPB, PRO, EPI, 1><<<grid, 64 * WPB, 0, m->st>>>(a);
-    } else {
-        k_gemv<NIN, TC, WPB, PRO, EPI, 0><<<grid, 64 * WPB, 0, m->st>>>(a);
-    }
+static void gemv(sm_machine* m, bool rec, const char* name, int grid, const GemvArgs& a) {
+    if (rec) launch(m->cfg.profile, name, k_gemv<NIN, TC, WPB, PRO, EPI, 1>, dim3(grid), dim3(64 * WPB), 0, m->st, a);
+    else launch(m->cfg.profile, name, k_gemv<NIN, TC, WPB, PRO, EPI, 0>, dim3(grid), dim3(64 * WPB), 0, m->st, a);
 }
 template <int MODEL>
 static void attend1(sm_machine* m, bool rec, const AttArgs& a) {
-    if (rec) k_attend<MODEL, 1, 1><<<dim3(12, 1), NTHR, (size_t)m->ctx * 12, m->st>>>(a);
-    else k_attend<MODEL, 1, 0><<<dim3(12, 1), NTHR, (size_t)m->ctx * 12, m->st>>>(a);
+    if (rec) launch(m->cfg.profile, "attend", k_attend<MODEL, 1, 1>, dim3(12, 1), dim3(NTHR), (size_t)m->ctx * 12, m->st, a);
+    else launch(m->cfg.profile, "attend", k_attend<MODEL, 1, 0>, dim3(12, 1), dim3(NTHR), (size_t)m->ctx * 12, m->st, a);
 }
 
 // The Pythia machine at batch 1 (foundation0/pythia_base2.py:153-160), five phases a layer.  Both gauges read
 // the stream before either half adds to it (the parallel residual R + At + Mo, :155-157): qkv and fc first.
-static int launch_step_pythia(sm_machine* m, int parts, hipEvent_t hs, hipEvent_t he, bool rec) {
+static int launch_step_pythia(sm_machine* m, int parts, bool rec) {
     const Tables tb = m->T.tb();
     int* ctl = m->ctl;
     for (int l = 0; l < 12 && (parts & STEP_LAYERS); l++) {
@@ -555,7 +612,7 @@ static int launch_step_pythia(sm_machine* m, int parts, hipEvent_t hs, hipEvent_
             plate(a, P, 0);
             a.X = Rin; a.Y = m->QKV; a.rout = m->r_qkv + l * 2304; a.rg = m->r_gauge + (l * 2 + 0) * 768;
             a.ng = m->ng[l][0]; a.nb = m->nb[l][0]; a.nge = m->nge[l][0];
-            gemv<768, 2, 4, PRO_PGAUGE, EPI_PLAIN>(m, rec, (P.ntiles + 3) / 4, a);
+            gemv<768, 2, 4, PRO_PGAUGE, EPI_PLAIN>(m, rec, "qkv", (P.ntiles + 3) / 4, a);
         }
         // fc: gauge ln2 of the same R, plain, edge (:156)
         {
@@ -565,7 +622,7 @@ static int launch_step_pythia(sm_machine* m, int parts, hipEvent_t hs, hipEvent_
             a.X = Rin; a.Y = m->hid; a.rout = m->r_fcpre + l * 3072; a.rout2 = m->r_hid + l * 3072;
             a.rg = m->r_gauge + (l * 2 + 1) * 768;
             a.ng = m->ng[l][1]; a.nb = m->nb[l][1]; a.nge = m->nge[l][1];
-            gemv<768, 2, 4, PRO_PGAUGE, EPI_PLAIN_EDGE>(m, rec, (P.ntiles + 3) / 4, a);
+            gemv<768, 2, 4, PRO_PGAUGE, EPI_PLAIN_EDGE>(m, rec, "fc", (P.ntiles + 3) / 4, a);
         }
         // attention with turns (:125-141)
         {
@@ -581,7 +638,7 @@ static int launch_step_pythia(sm_machine* m, int parts, hipEvent_t hs, hipEvent_
             plate(g, P, 1);
             g.X = m->att; g.Y = m->R; g.Yb = Rin; g.rout = m->r_resid + (l * 2 + 0) * 768;
             attend1<1>(m, rec, a);
-            gemv<768, 2, 2, PRO_TO16, EPI_PLAIN_ADD>(m, rec, (P.ntiles + 1) / 2, g);
+            gemv<768, 2, 2, PRO_TO16, EPI_PLAIN_ADD>(m, rec, "proj", (P.ntiles + 1) / 2, g);
         }
         // mproj: plain of the edge row, added to R (Mo)
         {
@@ -589,7 +646,7 @@ static int launch_step_pythia(sm_machine* m, int parts, hipEvent_t hs, hipEvent_
             const DevPlate& P = m->bank[l][3];
             plate(a, P, 3);
             a.X = m->hid; a.Y = m->R; a.Yb = m->R; a.rout = m->r_resid + (l * 2 + 1) * 768;
-            gemv<3072, 1, 4, PRO_TO16, EPI_PLAIN_ADD>(m, rec, (P.ntiles + 3) / 4, a);
+            gemv<3072, 1, 4, PRO_TO16, EPI_PLAIN_ADD>(m, rec, "mproj", (P.ntiles + 3) / 4, a);
         }
     }
     // head: gauge lnf, plain with no bias, race (:158-160)
@@ -603,7 +660,7 @@ static int launch_step_pythia(sm_machine* m, int parts, hipEvent_t hs, hipEvent_
         a.ng = m->fg; a.nb = m->fb; a.nge = m->fge; a.rg = m->r_hgauge;
         a.rx16 = m->r_hx16; a.rexls = m->r_hexls; a.rpile = m->r_hpile; a.rlogits = m->r_logits;
         a.part_v = m->part_v; a.part_i = m->part_i;
-        gemv<768, HEAD_TC, HEAD_WPB, PRO_PGAUGE, EPI_PHEAD>(m, rec, m->head_grid, a, hs, he);
+        gemv<768, HEAD_TC, HEAD_WPB, PRO_PGAUGE, EPI_PHEAD>(m, rec, "head", m->head_grid, a);
         launch_race1(m);
     }
     HIP_TRY(hipGetLastError());
@@ -616,7 +673,7 @@ static int launch_step_pythia(sm_machine* m, int parts, hipEvent_t hs, hipEvent_
 // (the parallel residual) and lights the next layer's two gauges, or the head's.
 // rowmap != null: a pass of nrows prompt rows, as in launch_step_batched.
 template <int RT>
-static int launch_step_pythia_batched(sm_machine* m, int parts, hipEvent_t hs, hipEvent_t he, int nrows = 0,
+static int launch_step_pythia_batched(sm_machine* m, int parts, int nrows = 0,
                                       const int* rowmap = nullptr) {
     const Tables tb = m->T.tb();
     int* ctl = m->ctl;
@@ -656,12 +713,12 @@ static int launch_step_pythia_batched(sm_machine* m, int parts, hipEvent_t hs, h
         if (l == 0) {
             PyRowArgs a = rows_args();
             gauges(a, 0);
-            k_py_rows<PY_EMBED><<<B, 192, 0, m->st>>>(a);
+            launch(m->cfg.profile, "rows.embed", k_py_rows<PY_EMBED>, dim3(B), dim3(192), 0, m->st, a);
         }
         {   // qkv: plain, written
             GemmArgs a = gemm_args(m->mbank[l][0], pA, rA);
             a.Y = m->QKV; a.ystride = 2304; a.rpile = rp; a.rout = m->r_qkv + l * 2304;
-            k_gemm<768, 1, 1, EPI_PLAIN><<<dim3(m->mbank[l][0].ntiles, RT), 256, 0, m->st>>>(a);
+            launch(m->cfg.profile, "qkv", k_gemm<768, 1, 1, EPI_PLAIN>, dim3(m->mbank[l][0].ntiles, RT), dim3(256), 0, m->st, a);
         }
         if (rowmap && l == 11) {   // prompt rows: the last layer only stores its keys and values
             AttArgs a{};
@@ -669,7 +726,7 @@ static int launch_step_pythia_batched(sm_machine* m, int parts, hipEvent_t hs, h
             a.QKV = m->QKV; a.K16 = m->K16 + l * per * 768; a.KM = m->KM + l * per * 12; a.EK = m->EK + l * per * 12; a.V = m->V + l * per * 768;
             a.ctx = m->ctx; a.tb = tb; a.err = ctl + CTL_ERR; a.rowmap = rowmap;
             a.cosT = m->cosT; a.sinT = m->sinT; a.rot = m->rot; a.half = m->half; a.ehalf = m->ehalf;
-            k_kv_rows<1><<<dim3(12, B), 128, 0, m->st>>>(a);
+            launch(m->cfg.profile, "kv_rows", k_kv_rows<1>, dim3(12, B), dim3(128), 0, m->st, a);
             break;
         }
         {   // fc: plain and edged in its bank (the hidden rows), with their OR words
@@ -677,14 +734,14 @@ static int launch_step_pythia_batched(sm_machine* m, int parts, hipEvent_t hs, h
             a.Y = m->hid; a.ystride = 3072;
             a.rpile = rp + 2 * 3072; a.rout = m->r_fcpre + l * 3072; a.rout2 = m->r_hid + l * 3072;
             a.orw_out = m->hidor;
-            k_gemm<768, 1, 1, EPI_PLAIN_EDGE><<<dim3(m->mbank[l][2].ntiles, RT), 256, 0, m->st>>>(a);
+            launch(m->cfg.profile, "fc", k_gemm<768, 1, 1, EPI_PLAIN_EDGE>, dim3(m->mbank[l][2].ntiles, RT), dim3(256), 0, m->st, a);
         }
         {   // mproj: the hidden rows' light formed in each K slice's blocks; partials over four K slices
             GemmArgs a = gemm_args(m->mbank[l][3], nullptr, nullptr);
             a.part = P0;
             a.X = m->hid; a.xstride = 3072; a.orw = m->hidor; a.sfacts = m->sfacts;
             a.rx16 = m->r_x16 + (l * 4 + 3) * 3072; a.rexls = m->r_exls + (l * 4 + 3) * 2;
-            k_gemm<3072, 3, 4, EPI_PART, 192><<<dim3(m->mbank[l][3].ntiles / 3 * 4, RT), 256, 0, m->st>>>(a);
+            launch(m->cfg.profile, "mproj.part", k_gemm<3072, 3, 4, EPI_PART, 192>, dim3(m->mbank[l][3].ntiles / 3 * 4, RT), dim3(256), 0, m->st, a);
         }
         {   // attention with turns
             AttArgs a{};
@@ -694,15 +751,15 @@ static int launch_step_pythia_batched(sm_machine* m, int parts, hipEvent_t hs, h
             a.rec_pos = recp; a.ratt = m->r_att + l * 768; a.rowmap = rowmap;
             a.cosT = m->cosT; a.sinT = m->sinT; a.rot = m->rot; a.half = m->half; a.ehalf = m->ehalf;
             a.out_or = m->attor;
-            if (rowmap) k_kv_rows<1><<<dim3(12, B), 128, 0, m->st>>>(a);
-            k_attend<1, 0, 1><<<dim3(12, B), NTHR, (size_t)m->ctx * 12, m->st>>>(a);
+            if (rowmap) launch(m->cfg.profile, "kv_rows", k_kv_rows<1>, dim3(12, B), dim3(128), 0, m->st, a);
+            launch(m->cfg.profile, "attend", k_attend<1, 0, 1>, dim3(12, B), dim3(NTHR), (size_t)m->ctx * 12, m->st, a);
         }
         {   // proj: the attention rows' light formed in its bank, added into the stream (R + At)
             GemmArgs g = gemm_args(m->mbank[l][1], nullptr, nullptr);
             g.Y = m->R; g.ystride = 768; g.rpile = rp + 3072; g.rout = m->r_resid + (l * 2 + 0) * 768;
             g.X = m->att; g.xstride = 768; g.orw = m->attor;
             g.rx16 = m->r_x16 + (l * 4 + 1) * 3072; g.rexls = m->r_exls + (l * 4 + 1) * 2;
-            k_gemm<768, 1, 1, EPI_PLAIN_ADD, 12><<<dim3(m->mbank[l][1].ntiles, RT), 256, 0, m->st>>>(g);
+            launch(m->cfg.profile, "proj", k_gemm<768, 1, 1, EPI_PLAIN_ADD, 12>, dim3(m->mbank[l][1].ntiles, RT), dim3(256), 0, m->st, g);
         }
         {   // R += Mo (the parallel residual's other half), then the next gauges' lights
             PyRowArgs a = rows_args();
@@ -710,7 +767,7 @@ static int launch_step_pythia_batched(sm_machine* m, int parts, hipEvent_t hs, h
             a.partM = P0; a.kinM = 3072; a.sfactsM = m->sfacts; a.csumM = Pm.csum; a.weM = Pm.e; a.biasM = Pm.b;
             a.rpileM = rp + 3 * 3072; a.routM = m->r_resid + (l * 2 + 1) * 768;
             gauges(a, l + 1);
-            k_py_rows<PY_ADD><<<B, 192, 0, m->st>>>(a);
+            launch(m->cfg.profile, "rows.add", k_py_rows<PY_ADD>, dim3(B), dim3(192), 0, m->st, a);
         }
     }
     if ((parts & STEP_HEAD) && !rowmap) {
@@ -718,35 +775,33 @@ static int launch_step_pythia_batched(sm_machine* m, int parts, hipEvent_t hs, h
         a.rpile = m->r_hpile;
         const int grid = head_rows_grid(m->mhead.ntiles);
         a.part_v = m->part_v; a.part_i = m->part_i; a.nblk = grid; a.rlogits = m->r_logits;
-        if (hs) hipExtLaunchKernelGGL(k_head_rows<RT, EPI_PHEAD>, dim3(grid), dim3(256), 0, m->st, hs, he, 0, a);
-        else k_head_rows<RT, EPI_PHEAD><<<grid, 256, 0, m->st>>>(a);
+        launch(m->cfg.profile, "head", k_head_rows<RT, EPI_PHEAD>, dim3(grid), dim3(256), 0, m->st, a);
         RaceArgs r{};
         r.part_v = m->part_v; r.part_i = m->part_i; r.nblk = grid; r.seq = m->seq; r.seq_stride = m->ctx + 1;
         r.words = m->words; r.words_stride = m->ctx + 1; r.pos = ctl + CTL_POS; r.plen = ctl + CTL_PLEN;
         r.nwords = ctl + CTL_NWORDS; r.counter = reinterpret_cast<unsigned*>(ctl + CTL_COUNTER);
-        k_race_rows<<<B, 256, 0, m->st>>>(r);
+        launch(m->cfg.profile, "race", k_race_rows, dim3(B), dim3(256), 0, m->st, r);
     }
     HIP_TRY(hipGetLastError());
     return SM_OK;
 }
 
 // rec (batch 1): the step runs the kernels that record (sm_record_at's position)
-static int launch_step(sm_machine* m, int parts = STEP_ALL, hipEvent_t hs = nullptr, hipEvent_t he = nullptr,
-                       bool rec = false) {
+static int launch_step(sm_machine* m, int parts = STEP_ALL, bool rec = false) {
     if (m->kind == 1 && m->B > 1) {
         const int RT = (m->B + 15) / 16;
-        if (RT == 1) return launch_step_pythia_batched<1>(m, parts, hs, he);
-        if (RT == 2) return launch_step_pythia_batched<2>(m, parts, hs, he);
-        if (RT == 3) return launch_step_pythia_batched<3>(m, parts, hs, he);
-        return launch_step_pythia_batched<4>(m, parts, hs, he);
+        if (RT == 1) return launch_step_pythia_batched<1>(m, parts);
+        if (RT == 2) return launch_step_pythia_batched<2>(m, parts);
+        if (RT == 3) return launch_step_pythia_batched<3>(m, parts);
+        return launch_step_pythia_batched<4>(m, parts);
     }
-    if (m->kind == 1) return launch_step_pythia(m, parts, hs, he, rec);
+    if (m->kind == 1) return launch_step_pythia(m, parts, rec);
     if (m->B > 1) {
         const int RT = (m->B + 15) / 16;
-        if (RT == 1) return launch_step_batched<1>(m, parts, hs, he);
-        if (RT == 2) return launch_step_batched<2>(m, parts, hs, he);
-        if (RT == 3) return launch_step_batched<3>(m, parts, hs, he);
-        return launch_step_batched<4>(m, parts, hs, he);
+        if (RT == 1) return launch_step_batched<1>(m, parts);
+        if (RT == 2) return launch_step_batched<2>(m, parts);
+        if (RT == 3) return launch_step_batched<3>(m, parts);
+        return launch_step_batched<4>(m, parts);
     }
     const Tables tb = m->T.tb();
     int* ctl = m->ctl;
@@ -764,7 +819,7 @@ static int launch_step(sm_machine* m, int parts = STEP_ALL, hipEvent_t hs = null
             a.X = Rin; a.Y = m->QKV;
             a.rx16 = m->r_x16 + (l * 4 + 0) * 3072; a.rexls = m->r_exls + (l * 4 + 0) * 2;
             a.rpile = m->r_pile + (l * 4 + 0) * 3072; a.rout = m->r_qkv + l * 2304;
-            gemv<768, 2, 4, PRO_GAUGE, EPI_GAUGED>(m, rec, (P.ntiles + 3) / 4, a);
+            gemv<768, 2, 4, PRO_GAUGE, EPI_GAUGED>(m, rec, "qkv", (P.ntiles + 3) / 4, a);
         }
         // attention (base2.py:85-100) on the KV cache of layer l
         {
@@ -782,7 +837,7 @@ static int launch_step(sm_machine* m, int parts = STEP_ALL, hipEvent_t hs = null
             g.rx16 = m->r_x16 + (l * 4 + 1) * 3072; g.rexls = m->r_exls + (l * 4 + 1) * 2;
             g.rpile = m->r_pile + (l * 4 + 1) * 3072; g.rout = m->r_resid + (l * 2 + 0) * 768;
             attend1<0>(m, rec, a);
-            gemv<768, 2, 2, PRO_TO16, EPI_PLAIN_ADD>(m, rec, (P.ntiles + 1) / 2, g);
+            gemv<768, 2, 2, PRO_TO16, EPI_PLAIN_ADD>(m, rec, "proj", (P.ntiles + 1) / 2, g);
         }
         // fc: gauge, product, gauged, edge (base2.py:106)
         {
@@ -792,7 +847,7 @@ static int launch_step(sm_machine* m, int parts = STEP_ALL, hipEvent_t hs = null
             a.X = m->R; a.Y = m->hid;
             a.rx16 = m->r_x16 + (l * 4 + 2) * 3072; a.rexls = m->r_exls + (l * 4 + 2) * 2;
             a.rpile = m->r_pile + (l * 4 + 2) * 3072; a.rout = m->r_hid + l * 3072;
-            gemv<768, 2, 4, PRO_GAUGE, EPI_GAUGED_EDGE>(m, rec, (P.ntiles + 3) / 4, a);
+            gemv<768, 2, 4, PRO_GAUGE, EPI_GAUGED_EDGE>(m, rec, "fc", (P.ntiles + 3) / 4, a);
         }
         // mproj: to16 of the hidden row (3072), product, plain, added to R (base2.py:106)
         {
@@ -802,7 +857,7 @@ static int launch_step(sm_machine* m, int parts = STEP_ALL, hipEvent_t hs = null
             a.X = m->hid; a.Y = m->R; a.Yb = m->R;
             a.rx16 = m->r_x16 + (l * 4 + 3) * 3072; a.rexls = m->r_exls + (l * 4 + 3) * 2;
             a.rpile = m->r_pile + (l * 4 + 3) * 3072; a.rout = m->r_resid + (l * 2 + 1) * 768;
-            gemv<3072, 1, 4, PRO_TO16, EPI_PLAIN_ADD>(m, rec, (P.ntiles + 3) / 4, a);
+            gemv<3072, 1, 4, PRO_TO16, EPI_PLAIN_ADD>(m, rec, "mproj", (P.ntiles + 3) / 4, a);
         }
     }
     // head: gauge, product with the tied word table, power + standing amount, race (base2.py:107-114)
@@ -815,7 +870,7 @@ static int launch_step(sm_machine* m, int parts = STEP_ALL, hipEvent_t hs = null
         a.X = m->R;
         a.rx16 = m->r_hx16; a.rexls = m->r_hexls; a.rpile = m->r_hpile; a.rlogits = m->r_logits;
         a.part_v = m->part_v; a.part_i = m->part_i;      // each block's best; the race runs in k_race1
-        gemv<768, HEAD_TC, HEAD_WPB, PRO_GAUGE, EPI_HEAD>(m, rec, m->head_grid, a, hs, he);
+        gemv<768, HEAD_TC, HEAD_WPB, PRO_GAUGE, EPI_HEAD>(m, rec, "head", m->head_grid, a);
         launch_race1(m);
     }
     HIP_TRY(hipGetLastError());
@@ -836,15 +891,15 @@ static int run_prefill(sm_machine* m, int npos) {
         const int* map = m->pfmap + r0;
         int rc;
         if (m->kind == 1) {
-            rc = RT == 1 ? launch_step_pythia_batched<1>(m, STEP_LAYERS, nullptr, nullptr, n, map)
-               : RT == 2 ? launch_step_pythia_batched<2>(m, STEP_LAYERS, nullptr, nullptr, n, map)
-               : RT == 3 ? launch_step_pythia_batched<3>(m, STEP_LAYERS, nullptr, nullptr, n, map)
-                         : launch_step_pythia_batched<4>(m, STEP_LAYERS, nullptr, nullptr, n, map);
+            rc = RT == 1 ? launch_step_pythia_batched<1>(m, STEP_LAYERS, n, map)
+               : RT == 2 ? launch_step_pythia_batched<2>(m, STEP_LAYERS, n, map)
+               : RT == 3 ? launch_step_pythia_batched<3>(m, STEP_LAYERS, n, map)
+                         : launch_step_pythia_batched<4>(m, STEP_LAYERS, n, map);
         } else {
-            rc = RT == 1 ? launch_step_batched<1>(m, STEP_LAYERS, nullptr, nullptr, n, map)
-               : RT == 2 ? launch_step_batched<2>(m, STEP_LAYERS, nullptr, nullptr, n, map)
-               : RT == 3 ? launch_step_batched<3>(m, STEP_LAYERS, nullptr, nullptr, n, map)
-                         : launch_step_batched<4>(m, STEP_LAYERS, nullptr, nullptr, n, map);
+            rc = RT == 1 ? launch_step_batched<1>(m, STEP_LAYERS, n, map)
+               : RT == 2 ? launch_step_batched<2>(m, STEP_LAYERS, n, map)
+               : RT == 3 ? launch_step_batched<3>(m, STEP_LAYERS, n, map)
+                         : launch_step_batched<4>(m, STEP_LAYERS, n, map);
         }
         if (rc) return rc;
     }
@@ -1016,13 +1071,6 @@ extern "C" int sm_create(const char* layout_dir, const sm_config* cfg, sm_machin
     m->prompts.assign(B, {});
     m->gsteps = c.graph_steps > 0 ? c.graph_steps : 16;
     if (m->gsteps > 256) return bail(fail(SM_E_ARG, "sm_create: graph_steps at most 256"));
-    if (c.profile) {
-        m->ev_s.resize(m->gsteps);
-        m->ev_e.resize(m->gsteps);
-        for (int i = 0; i < m->gsteps; i++)
-            if (hipEventCreate(&m->ev_s[i]) != hipSuccess || hipEventCreate(&m->ev_e[i]) != hipSuccess)
-                return bail(fail(SM_E_HIP, "hipEventCreate"));
-    }
     if ((rc = sm_reset(m))) return bail(rc);
     *out = m;
     return SM_OK;
@@ -1091,43 +1139,11 @@ static int capture(sm_machine* m, int which, int n, int parts) {
     return SM_OK;
 }
 
-// one profiled step: the layers (a captured graph, or plain launches), then the head launched with the HIP
-// event pair its own dispatch stamps, on the machine's stream
-static int profiled_step(sm_machine* m, int slot) {
-    int rc;
-    if (m->cfg.use_graph) {
-        if ((rc = capture(m, 2, 1, STEP_LAYERS))) return rc;
-        HIP_TRY(hipGraphLaunch(m->gexec[2], m->st));
-    } else if ((rc = launch_step(m, STEP_LAYERS))) {
-        return rc;
-    }
-    return launch_step(m, STEP_HEAD, m->ev_s[slot], m->ev_e[slot]);
-}
-
-// wait for the n profiled steps just queued and add their head durations
-static int collect(sm_machine* m, int n) {
-    HIP_TRY(hipStreamSynchronize(m->st));
-    for (int s = 0; s < n; s++) {
-        float ms = 0.f;
-        HIP_TRY(hipEventElapsedTime(&ms, m->ev_s[s], m->ev_e[s]));
-        m->prof_head_us += 1000.0 * ms;
-        m->prof_n++;
-    }
-    return SM_OK;
-}
-
-// n whole decode steps: profiled (event pairs around each head), replayed from captured graphs, or launched
+// n whole decode steps: replayed from captured graphs, or launched one by one (always so with profile = 1, whose
+// launches each carry their event pair)
 static int queue_steps(sm_machine* m, int steps) {
     int rc;
-    if (m->cfg.profile) {
-        while (steps > 0) {
-            const int n = steps < m->gsteps ? steps : m->gsteps;
-            for (int s = 0; s < n; s++)
-                if ((rc = profiled_step(m, s))) return rc;
-            if ((rc = collect(m, n))) return rc;
-            steps -= n;
-        }
-    } else if (m->cfg.use_graph) {
+    if (m->cfg.use_graph && !m->cfg.profile) {
         if (steps >= m->gsteps && (rc = capture(m, 0, m->gsteps, STEP_ALL))) return rc;
         for (; steps >= m->gsteps; steps -= m->gsteps) HIP_TRY(hipGraphLaunch(m->gexec[0], m->st));
         if (steps > 0 && (rc = capture(m, 1, 1, STEP_ALL))) return rc;
@@ -1146,7 +1162,7 @@ static int run_steps(sm_machine* m, int n, int pos0) {
     int rc;
     if (rp >= pos0 && rp < pos0 + n) {
         if ((rc = queue_steps(m, rp - pos0))) return rc;
-        if ((rc = launch_step(m, STEP_ALL, nullptr, nullptr, true))) return rc;
+        if ((rc = launch_step(m, STEP_ALL, true))) return rc;
         return queue_steps(m, pos0 + n - rp - 1);
     }
     return queue_steps(m, n);
@@ -1196,9 +1212,46 @@ extern "C" int sm_generate(sm_machine* m, int32_t n_words, int32_t* out) {
 
 extern "C" int sm_profile(sm_machine* m, int64_t* n_heads, double* head_us, int32_t clear) {
     if (!m) return fail(SM_E_ARG, "sm_profile: null machine");
-    if (n_heads) *n_heads = m->prof_n;
-    if (head_us) *head_us = m->prof_head_us;
-    if (clear) { m->prof_n = 0; m->prof_head_us = 0.0; }
+    int rc;
+    if ((rc = kt_fold())) return rc;
+    std::lock_guard<std::mutex> lock(g_kt.mu);
+    long long n = 0;
+    double us = 0.0;
+    for (size_t i = 0; i < g_kt.names.size(); i++)
+        if (g_kt.names[i] == "head") { n = g_kt.n[i]; us = g_kt.us[i]; }
+    if (n_heads) *n_heads = n;
+    if (head_us) *head_us = us;
+    if (clear)
+        for (size_t i = 0; i < g_kt.names.size(); i++) { g_kt.n[i] = 0; g_kt.us[i] = 0.0; }
+    return SM_OK;
+}
+
+extern "C" int sm_profile_stages(int32_t on) {
+    g_kt.stages = on != 0;
+    return SM_OK;
+}
+
+extern "C" int sm_profile_kernels(char* names, int32_t names_bytes, int64_t* launches, double* total_us, int32_t max,
+                                  int32_t* n, int32_t clear) {
+    if (!names || names_bytes <= 0 || !launches || !total_us || max < 0 || !n) return fail(SM_E_ARG, "sm_profile_kernels: arguments");
+    int rc;
+    if ((rc = kt_fold())) return rc;
+    std::lock_guard<std::mutex> lock(g_kt.mu);
+    std::string all;
+    int k = 0;
+    for (size_t i = 0; i < g_kt.names.size() && k < max; i++) {
+        if (!g_kt.n[i]) continue;
+        all += g_kt.names[i];
+        all += '\n';
+        launches[k] = g_kt.n[i];
+        total_us[k] = g_kt.us[i];
+        k++;
+    }
+    if ((int64_t)all.size() + 1 > names_bytes) return fail(SM_E_ARG, "sm_profile_kernels: names buffer too small");
+    std::memcpy(names, all.c_str(), all.size() + 1);
+    *n = k;
+    if (clear)
+        for (size_t i = 0; i < g_kt.names.size(); i++) { g_kt.n[i] = 0; g_kt.us[i] = 0.0; }
     return SM_OK;
 }
 
@@ -1300,43 +1353,43 @@ static inline int blocks_for(int64_t n, int per) { return (int)((n + per - 1) / 
 
 extern "C" int sm_stage_rshift(const int64_t* x, const int64_t* s, int64_t* out, int64_t n, void* stream) {
     if (n < 0 || (n > 0 && (!x || !s || !out))) return fail(SM_E_ARG, "sm_stage_rshift: arguments");
-    if (n) k_stage_rshift<<<blocks_for(n, 256), 256, 0, (hipStream_t)stream>>>((const i64*)x, (const i64*)s, (i64*)out, n);
+    if (n) launch(g_kt.stages, "stage.rshift", k_stage_rshift, dim3(blocks_for(n, 256)), dim3(256), 0, (hipStream_t)stream, (const i64*)x, (const i64*)s, (i64*)out, n);
     HIP_TRY(hipGetLastError());
     return SM_OK;
 }
 extern "C" int sm_stage_log2fix(const sm_tables* t, const int64_t* v, int64_t* out, int64_t n, void* stream) {
     if (!t || n < 0 || (n > 0 && (!v || !out))) return fail(SM_E_ARG, "sm_stage_log2fix: arguments");
-    if (n) k_stage_log2fix<<<blocks_for(n, 256), 256, 0, (hipStream_t)stream>>>((const i64*)v, (i64*)out, n, t->tb());
+    if (n) launch(g_kt.stages, "stage.log2fix", k_stage_log2fix, dim3(blocks_for(n, 256)), dim3(256), 0, (hipStream_t)stream, (const i64*)v, (i64*)out, n, t->tb());
     HIP_TRY(hipGetLastError());
     return SM_OK;
 }
 extern "C" int sm_stage_power(const sm_tables* t, const int64_t* x, const int64_t* F, int64_t* out, int64_t n, void* stream) {
     if (!t || n < 0 || (n > 0 && (!x || !F || !out))) return fail(SM_E_ARG, "sm_stage_power: arguments");
-    if (n) k_stage_power<<<blocks_for(n, 256), 256, 0, (hipStream_t)stream>>>((const i64*)x, (const i64*)F, (i64*)out, n, t->tb());
+    if (n) launch(g_kt.stages, "stage.power", k_stage_power, dim3(blocks_for(n, 256)), dim3(256), 0, (hipStream_t)stream, (const i64*)x, (const i64*)F, (i64*)out, n, t->tb());
     HIP_TRY(hipGetLastError());
     return SM_OK;
 }
 extern "C" int sm_stage_edge(const sm_tables* t, const int64_t* h, int64_t* out, int64_t n, void* stream) {
     if (!t || n < 0 || (n > 0 && (!h || !out))) return fail(SM_E_ARG, "sm_stage_edge: arguments");
-    if (n) k_stage_edge<<<blocks_for(n, 256), 256, 0, (hipStream_t)stream>>>((const i64*)h, (i64*)out, n, t->tb());
+    if (n) launch(g_kt.stages, "stage.edge", k_stage_edge, dim3(blocks_for(n, 256)), dim3(256), 0, (hipStream_t)stream, (const i64*)h, (i64*)out, n, t->tb());
     HIP_TRY(hipGetLastError());
     return SM_OK;
 }
 extern "C" int sm_stage_to16(const int64_t* X, int32_t rows, int32_t n, int64_t* x16, int64_t* ex, void* stream) {
     if (rows < 0 || n <= 0 || (rows > 0 && (!X || !x16 || !ex))) return fail(SM_E_ARG, "sm_stage_to16: arguments");
-    if (rows) k_stage_rows<<<rows, NTHR, 0, (hipStream_t)stream>>>((const i64*)X, n, 0, (i64*)x16, (i64*)ex, nullptr, Tables{});
+    if (rows) launch(g_kt.stages, "stage.to16", k_stage_rows, dim3(rows), dim3(NTHR), 0, (hipStream_t)stream, (const i64*)X, n, 0, (i64*)x16, (i64*)ex, nullptr, Tables{});
     HIP_TRY(hipGetLastError());
     return SM_OK;
 }
 extern "C" int sm_stage_gauge_log(const sm_tables* t, const int64_t* R, int32_t rows, int64_t* x16, int64_t* ex, int64_t* LS, void* stream) {
     if (!t || rows < 0 || (rows > 0 && (!R || !x16 || !ex || !LS))) return fail(SM_E_ARG, "sm_stage_gauge_log: arguments");
-    if (rows) k_stage_rows<<<rows, NTHR, 0, (hipStream_t)stream>>>((const i64*)R, 768, 1, (i64*)x16, (i64*)ex, (i64*)LS, t->tb());
+    if (rows) launch(g_kt.stages, "stage.gauge_log", k_stage_rows, dim3(rows), dim3(NTHR), 0, (hipStream_t)stream, (const i64*)R, 768, 1, (i64*)x16, (i64*)ex, (i64*)LS, t->tb());
     HIP_TRY(hipGetLastError());
     return SM_OK;
 }
 extern "C" int sm_stage_race(const int64_t* v, int64_t n, int64_t* out_index, void* stream) {
     if (n <= 0 || !v || !out_index) return fail(SM_E_ARG, "sm_stage_race: arguments");
-    k_stage_race<<<1, 1024, 0, (hipStream_t)stream>>>((const i64*)v, n, (i64*)out_index);
+    launch(g_kt.stages, "stage.race", k_stage_race, dim3(1), dim3(1024), 0, (hipStream_t)stream, (const i64*)v, n, (i64*)out_index);
     HIP_TRY(hipGetLastError());
     return SM_OK;
 }
@@ -1350,7 +1403,7 @@ extern "C" int sm_stage_attend(const sm_tables* t, const int64_t* qkv, int16_t* 
     AttArgs a{};
     a.QKV = (const i64*)qkv; a.K16 = k16; a.KM = (i64*)km; a.EK = ek; a.V = v; a.out = (i64*)out; a.pos = t->scratch; a.ctx = ctx;
     a.tb = t->tb(); a.err = t->scratch + 1;
-    k_attend<0, 1, 0><<<dim3(12, 1), NTHR, (size_t)ctx * 12, s>>>(a);
+    launch(g_kt.stages, "stage.attend", k_attend<0, 1, 0>, dim3(12, 1), dim3(NTHR), (size_t)ctx * 12, s, a);
     HIP_TRY(hipGetLastError());
     int err = 0;
     HIP_TRY(hipMemcpyAsync(&err, t->scratch + 1, 4, hipMemcpyDeviceToHost, s));
@@ -1373,7 +1426,7 @@ extern "C" int sm_stage_attend_rows(const sm_tables* t, const int64_t* qkv, int3
     AttArgs a{};
     a.QKV = (const i64*)qkv; a.K16 = k16; a.KM = (i64*)km; a.EK = ek; a.V = v; a.out = (i64*)out; a.pos = t->scratch; a.ctx = ctx;
     a.tb = t->tb(); a.err = t->scratch + 1;
-    k_attend<0, 0, 1><<<dim3(12, rows), NTHR, (size_t)ctx * 12, s>>>(a);      // the batched machine's kernel
+    launch(g_kt.stages, "stage.attend_rows", k_attend<0, 0, 1>, dim3(12, rows), dim3(NTHR), (size_t)ctx * 12, s, a);      // the batched machine's kernel
     HIP_TRY(hipGetLastError());
     int err = 0;
     HIP_TRY(hipMemcpyAsync(&err, t->scratch + 1, 4, hipMemcpyDeviceToHost, s));
@@ -1407,9 +1460,9 @@ static void plate_free(sm_plate* p) {
 extern "C" int sm_plate_create(const int16_t* w, const int32_t* e, const int64_t* b, int32_t nin, int32_t nout, int32_t tile_cols, sm_plate** out) {
     if (!w || !e || !b || !out) return fail(SM_E_ARG, "sm_plate_create: null argument");
     if (nout <= 0 || nout > (1 << 24)) return fail(SM_E_ARG, "sm_plate_create: nout out of range");
-    if (!((nin == 768 && (tile_cols == 0 || tile_cols == 2 || tile_cols == 8)) ||
+    if (!((nin == 768 && (tile_cols == 0 || tile_cols == 2 || tile_cols == 4 || tile_cols == 8)) ||
           (nin == 3072 && (tile_cols == 0 || tile_cols == 1 || tile_cols == 2))))
-        return fail(SM_E_ARG, "sm_plate_create: built for (nin, tile_cols) in (768, 0|2|8), (3072, 0|1|2)");
+        return fail(SM_E_ARG, "sm_plate_create: built for (nin, tile_cols) in (768, 0|2|4|8), (3072, 0|1|2)");
     sm_plate* p = new sm_plate();
     int rc;
     if (tile_cols == 0) {
@@ -1455,14 +1508,14 @@ static void rows_product(const sm_plate* p, const int64_t* x16, int32_t rows, in
     ga.K = P.K; ga.N = P.N; ga.rows = rows; ga.RT = RT; ga.W = P.W; ga.csum = P.csum; ga.we = P.e; ga.bias = P.b;
     ga.planes = planes; ga.rowinfo = rowinfo; ga.Y = (i64*)pile; ga.ystride = P.N;
     if (P.K == 768) {
-        k_light<768, PRO_X16, 192, 1><<<rows, 192, 0, s>>>(la);
+        launch(g_kt.stages, "plate.light", k_light<768, PRO_X16, 192, 1>, dim3(rows), dim3(192), 0, s, la);
         if (P.N > 3072)       // head-shaped plates: the head's kernel (light planes in LDS)
-            k_head_rows<RT, EPI_PILE><<<head_rows_grid(P.ntiles), 256, 0, s>>>(ga);
+            launch(g_kt.stages, "plate.head_rows", k_head_rows<RT, EPI_PILE>, dim3(head_rows_grid(P.ntiles)), dim3(256), 0, s, ga);
         else                  // layer-shaped plates: one column tile per block, K split over its four waves
-            k_gemm<768, 1, 1, EPI_PILE><<<dim3(P.ntiles, RT), 256, 0, s>>>(ga);
+            launch(g_kt.stages, "plate.gemm", k_gemm<768, 1, 1, EPI_PILE>, dim3(P.ntiles, RT), dim3(256), 0, s, ga);
     } else {
-        k_light<3072, PRO_X16, 768, 1><<<rows, 768, 0, s>>>(la);
-        k_gemm<3072, 1, 1, EPI_PILE><<<dim3(P.ntiles, RT), 256, 0, s>>>(ga);
+        launch(g_kt.stages, "plate.light", k_light<3072, PRO_X16, 768, 1>, dim3(rows), dim3(768), 0, s, la);
+        launch(g_kt.stages, "plate.gemm", k_gemm<3072, 1, 1, EPI_PILE>, dim3(P.ntiles, RT), dim3(256), 0, s, ga);
     }
 }
 
@@ -1550,11 +1603,11 @@ extern "C" int sm_plate_product_rows_from(const sm_plate* p, const int64_t* X, c
     ga.Y = (i64*)pile; ga.ystride = P.N;
     ga.X = (const i64*)X; ga.xstride = P.K; ga.orw = (const i64*)orw;
     if (P.K == 768) {
-        k_gemm<768, 1, 1, EPI_PILE, 12><<<dim3(P.ntiles, RT), 256, 0, s>>>(ga);
+        launch(g_kt.stages, "plate.gemm_from", k_gemm<768, 1, 1, EPI_PILE, 12>, dim3(P.ntiles, RT), dim3(256), 0, s, ga);
     } else {
         ga.part = p->part; ga.sfacts = p->sfacts;
-        k_gemm<3072, 3, 4, EPI_PART, 192><<<dim3(P.ntiles / 3 * 4, RT), 256, 0, s>>>(ga);
-        k_part_piles<4><<<dim3((P.N + 255) / 256, rows), 256, 0, s>>>(ga);
+        launch(g_kt.stages, "plate.gemm_from", k_gemm<3072, 3, 4, EPI_PART, 192>, dim3(P.ntiles / 3 * 4, RT), dim3(256), 0, s, ga);
+        launch(g_kt.stages, "plate.part_piles", k_part_piles<4>, dim3((P.N + 255) / 256, rows), dim3(256), 0, s, ga);
     }
     HIP_TRY(hipGetLastError());
     return SM_OK;
@@ -1569,10 +1622,11 @@ extern "C" int sm_plate_product(const sm_plate* p, const int64_t* x16, int64_t* 
     a.X = (const i64*)x16; a.Y = (i64*)pile;
     const int g = grid > 0 ? grid : (P.ntiles + 3) / 4;     // four waves per block, one tile per wave
     hipStream_t s = (hipStream_t)stream;
-    if (P.nin == 768 && P.tc == 8) k_gemv<768, 8, 4, PRO_X16, EPI_PILE, 0><<<g, 256, 0, s>>>(a);
-    else if (P.nin == 768 && P.tc == 2) k_gemv<768, 2, 4, PRO_X16, EPI_PILE, 0><<<g, 256, 0, s>>>(a);
-    else if (P.nin == 3072 && P.tc == 1) k_gemv<3072, 1, 4, PRO_X16, EPI_PILE, 0><<<g, 256, 0, s>>>(a);
-    else k_gemv<3072, 2, 4, PRO_X16, EPI_PILE, 0><<<g, 256, 0, s>>>(a);
+    if (P.nin == 768 && P.tc == 8) launch(g_kt.stages, "plate.gemv", k_gemv<768, 8, 4, PRO_X16, EPI_PILE, 0>, dim3(g), dim3(256), 0, s, a);
+    else if (P.nin == 768 && P.tc == 4) launch(g_kt.stages, "plate.gemv", k_gemv<768, 4, 4, PRO_X16, EPI_PILE, 0>, dim3(g), dim3(256), 0, s, a);
+    else if (P.nin == 768 && P.tc == 2) launch(g_kt.stages, "plate.gemv", k_gemv<768, 2, 4, PRO_X16, EPI_PILE, 0>, dim3(g), dim3(256), 0, s, a);
+    else if (P.nin == 3072 && P.tc == 1) launch(g_kt.stages, "plate.gemv", k_gemv<3072, 1, 4, PRO_X16, EPI_PILE, 0>, dim3(g), dim3(256), 0, s, a);
+    else launch(g_kt.stages, "plate.gemv", k_gemv<3072, 2, 4, PRO_X16, EPI_PILE, 0>, dim3(g), dim3(256), 0, s, a);
     HIP_TRY(hipGetLastError());
     return SM_OK;
 }

@@ -66,6 +66,8 @@ def lib():
         L.sm_model_kind.argtypes = [vp]
         L.sm_tables_mode.argtypes = [vp, i32, i32p]
         L.sm_profile.argtypes = [vp, i64p, ctypes.POINTER(ctypes.c_double), i32]
+        L.sm_profile_stages.argtypes = [i32]
+        L.sm_profile_kernels.argtypes = [ctypes.c_char_p, i32, i64p, ctypes.POINTER(ctypes.c_double), i32, i32p, i32]
         L.sm_tables_create.argtypes = [i64p, i64p, i32, i64p, i64p, i64, i64, ctypes.POINTER(vp)]
         L.sm_tables_destroy.argtypes = [vp]
         L.sm_stage_rshift.argtypes = [vp, vp, vp, i64, vp]
@@ -174,6 +176,11 @@ class Machine:
         check(self.L.sm_profile(self.h, ctypes.byref(n), ctypes.byref(us), 1 if clear else 0))
         return n.value, (us.value / n.value if n.value else float("nan"))
 
+    def kernels(self, clear: bool = True) -> dict:
+        """per kernel name: (launches, mean microseconds) of every timed launch since the last clear (profile=True
+        machines; stage entry points after profile_stages(True)); process-wide"""
+        return kernel_times(clear)
+
     def record_at(self, pos: int):
         check(self.L.sm_record_at(self.h, pos))
 
@@ -189,6 +196,24 @@ class Machine:
         out = np.zeros(shape, dtype=dt)
         check(self.L.sm_read(self.h, READ[name], layer, stream, pos, out.ctypes.data, out.nbytes))
         return out
+
+
+def profile_stages(on: bool = True):
+    """stamp every launch of the stage and plate entry points with its own HIP event pair"""
+    check(lib().sm_profile_stages(1 if on else 0))
+
+
+def kernel_times(clear: bool = True) -> dict:
+    """kernel name -> (launches, mean microseconds) of the timed launches since the last clear (process-wide)"""
+    cap = 256
+    names = ctypes.create_string_buffer(cap * 64)
+    n_l = np.zeros(cap, np.int64)
+    us = np.zeros(cap, np.float64)
+    n = i32()
+    check(lib().sm_profile_kernels(names, len(names), n_l.ctypes.data_as(i64p), us.ctypes.data_as(ctypes.POINTER(ctypes.c_double)),
+                                   cap, ctypes.byref(n), 1 if clear else 0))
+    keys = names.value.decode().split("\n")[:n.value]
+    return {k: (int(n_l[i]), float(us[i] / n_l[i])) for i, k in enumerate(keys)}
 
 
 class Tables:

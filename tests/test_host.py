@@ -49,8 +49,11 @@ def test_step_bytes_match_the_published_accounting():
     spec = importlib.util.spec_from_file_location("bench", os.path.join(REPO, "bench.py"))
     bench = importlib.util.module_from_spec(spec)
     spec.loader.exec_module(bench)
-    assert bench.step_bytes(50257, 0) == 248_662_476             # weights + exponents/biases, per token
-    # the KV cache per cached position: 12 layers x (768 int16 keys + 768 int32 values + per head an int32 key
-    # water level and an int64 mask of the +32768 dimensions)
-    assert bench.step_bytes(50257, 16) - bench.step_bytes(50257, 0) == 12 * (768 * 6 + 12 * 12) * 16 == 57_024 * 16
-    assert bench.head_bytes(50257) == 2 * 768 * 50257 + 12 * 50257
+    assert bench.WORKLOAD_FIXED == 248_662_476        # weights + exponents/biases, per token
+    assert bench.KV_WORKLOAD == 73_728                # k and v at 4 B each, 12 layers x 768, per cached position
+    # what this layout reads per cached position: 12 layers x (768 int16 keys + 768 int32 values + per head an
+    # int32 key water level and an int64 mask of the +32768 dimensions)
+    assert bench.KV_LAYOUT == 12 * (768 * 6 + 12 * 12) == 57_024
+    assert bench.bank_bytes(768, 50257) == 2 * 768 * 50257 + 12 * 50257
+    assert sum(bench.b1_kernel_bytes(k, 16) for k in ("qkv", "proj", "fc", "mproj")) * 12 + \
+        bench.b1_kernel_bytes("head", 16) + 12 * bench.b1_kernel_bytes("attend", 16) == 248_662_476 + 73_728 * 16
