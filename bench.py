@@ -55,6 +55,7 @@ B_STREAMS, B_PROMPT, B_WORDS = 64, 32, 128     # the batched workload: 64 stream
 P_STREAMS, P_PROMPT, P_WORDS = 32, 64, 256     # the Pythia-160m-shaped workload: 32 streams, 64-token prompts, 256 words
 GRAPH_STEPS = 16    # decode steps a captured graph holds in the batched legs
 PREFILL_ROWS = 64   # prompt rows a pass through the int8 MFMA banks (0: position by position)
+PLAIN = False       # --plain: one pass of plain launches a leg (no graphs, no event pairs), for counter runs
 VOCAB, PVOCAB = 50257, 50304
 BANKS = {"qkv": (768, 2304), "proj": (768, 768), "fc": (768, 3072), "mproj": (3072, 768)}
 
@@ -130,13 +131,18 @@ def kernel_table(times: dict, steps: int, bytes_of) -> dict:
     return out
 
 
-def read_traffic(kernel: str):
-    """HBM bytes a launch of `kernel` from the FETCH_SIZE / WRITE_SIZE summary in profiles/, when collected"""
-    path = os.path.join(REPO, "profiles", "b1_gemv_traffic.txt")
-    if not os.path.exists(path):
+COUNTER_FILES = {"b1": "b1_kernel_traffic.txt", "b64": "b64_kernel_counters.txt"}
+
+
+def read_counter(where: str, key: str, kernel: str):
+    """a per-launch figure (traffic_bytes_per_launch, mfma_ops_per_launch, mfma_busy_cycles_per_launch) of `kernel`
+    from the rocprofv3 counter summary in profiles/, when it was collected for that workload"""
+    fname = COUNTER_FILES.get(where)
+    path = os.path.join(REPO, "profiles", fname) if fname else ""
+    if not path or not os.path.exists(path):
         return None
     for line in open(path):
-        m = re.match(r"traffic_bytes_per_launch\[(\S+)\]:\s*(\d+)", line)
+        m = re.match(rf"{key}\[(\S+)\]:\s*(\d+)", line)
         if m and m.group(1) == kernel:
             return int(m.group(2))
     return None
@@ -147,7 +153,7 @@ def dominant(table: dict, where: str) -> dict:
     name = max((k for k in table if "bytes_per_launch" in table[k]), key=lambda k: table[k]["us_per_step"])
     r = table[name]
     return {"bound": "hbm", "achieved": r["gbs"], "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": r["frac"],
-            "traffic": read_traffic(name) if where == "b1" else None, "kernel": name,
+            "traffic": read_counter(where, "traffic_bytes_per_launch", name), "kernel": name,
             "bytes_per_launch": r["bytes_per_launch"], "mean_launch_us": r["mean_us"],
             "launches_per_step": r["launches_per_step"], "us_per_step": r["us_per_step"],
             "source": "HIP event pair stamped by each dispatch, profiled pass of the same workload"}
@@ -156,7 +162,7 @@ def dominant(table: dict, where: str) -> dict:
 # ---- batch 1 (config 1) ----
 def b1_leg(sm, lay, steps_req: int, warmup: int, prompt, want, cold_steps: int = 15):
     import torch
-    m = sm.Machine(lay, max_ctx=64, graph_steps=WORDS - 1, prefill_rows=PREFILL_ROWS)
+    m = sm.Machine(lay, max_ctx=64, graph_steps=WORDS - 1, prefill_rows=PREFILL_ROWS, use_graph=not PLAIN)
 
     def sequence(k: int):
         m.reset()
@@ -188,6 +194,9 @@ def b1_leg(sm, lay, steps_req: int, warmup: int, prompt, want, cold_steps: int =
         prompt_s += tp
         nseq += 1
     m.close()
+    if PLAIN:
+        return {"tok_s": steps / total, "ms": 1000.0 * total / steps, "steps": steps, "prompt_ms": 1000.0 * prompt_s / nseq,
+                "table": {}, "cold": {}, "ctx": PROMPT + WORDS / 2.0}
 
     # the same sequences, every launch timed by its own event pair
     mp = sm.Machine(lay, max_ctx=64, profile=True, prefill_rows=PREFILL_ROWS)
@@ -248,9 +257,9 @@ def batched_checks(ref_name, orc_name, streams_ref, streams_orc):
 def run_batched(sm, lay, streams, prompts, n_words, checks, what, bytes_of):
     import torch
     m = sm.Machine(lay, max_ctx=len(prompts[0]) + n_words, max_streams=streams, graph_steps=GRAPH_STEPS,
-                   prefill_rows=PREFILL_ROWS)
+                   prefill_rows=PREFILL_ROWS, use_graph=not PLAIN)
     res = None
-    for it in range(2):                        # the first sequence warms up (graph instantiation)
+    for it in range(1 if PLAIN else 2):        # the first sequence warms up (graph instantiation)
         m.reset()
         torch.cuda.synchronize()
         t = time.perf_counter()
@@ -267,6 +276,8 @@ def run_batched(sm, lay, streams, prompts, n_words, checks, what, bytes_of):
         res = (dt, tp)
     vocab = m.vocab
     m.close()
+    if PLAIN:
+        return res[0], res[1], n_words - 1, {}, vocab
     mp = sm.Machine(lay, max_ctx=len(prompts[0]) + n_words, max_streams=streams, profile=True, prefill_rows=PREFILL_ROWS)
     mp.reset()
     for b, p in enumerate(prompts):
@@ -290,6 +301,8 @@ def batched_leg(sm, lay):
     dt, tp, steps, table, vocab = run_batched(sm, lay, B_STREAMS, prompts, B_WORDS, checks, "batched",
                                               lambda k: batched_kernel_bytes(k, ctx, B_STREAMS, VOCAB))
     ms = 1000.0 * dt / steps
+    if PLAIN:
+        return {"value": round(B_STREAMS * steps / dt, 1), "ms_per_step": round(ms, 4), "plain": True}
     sb = WORKLOAD_FIXED + B_STREAMS * KV_WORKLOAD * ctx
     head = table.get("head", {})
     out = {"streams": B_STREAMS, "value": round(B_STREAMS * steps / dt, 1), "unit": "tokens/s",
@@ -306,8 +319,17 @@ def batched_leg(sm, lay):
            "kernels": table}
     if head:
         ops = 4 * 2 * B_STREAMS * 768 * vocab       # four byte-plane products of 64 x 768 x vocab, 2 ops a MAC
-        out["head_int8"] = {"tops": round(ops / (head["mean_us"] * 1e-6) / 1e12, 1),
-                            "frac": round(ops / (head["mean_us"] * 1e-6) / INT8_PEAK_OPS, 4)}
+        h = {"tops": round(ops / (head["mean_us"] * 1e-6) / 1e12, 1),
+             "frac": round(ops / (head["mean_us"] * 1e-6) / INT8_PEAK_OPS, 4),
+             "ops": "four byte-plane products of 64 x 768 x vocab, 2 ops a multiply-add"}
+        cops = read_counter("b64", "mfma_ops_per_launch", "head")
+        busy = read_counter("b64", "mfma_busy_cycles_per_launch", "head")
+        if cops and busy:
+            h["counters"] = {"ops_per_launch": cops, "tops": round(cops / (head["mean_us"] * 1e-6) / 1e12, 1),
+                             "busy_cycles": busy, "mfma_busy_frac": round(busy / (1024 * head["mean_us"] * 2400.0), 4),
+                             "source": "profiles/b64_kernel_counters.txt (SQ_INSTS_VALU_MFMA_MOPS_I8 x 512, "
+                                       "SQ_VALU_MFMA_BUSY_CYCLES over 1024 SIMDs; the duration at 2.4 GHz is this run's)"}
+        out["head_int8"] = h
     return out
 
 
@@ -326,6 +348,8 @@ def pythia_leg(sm):
     dt, tp, steps, table, vocab = run_batched(sm, lay, P_STREAMS, prompts, P_WORDS, checks, "pythia",
                                               lambda k: batched_kernel_bytes(k, ctx, P_STREAMS, PVOCAB, head_bias=False))
     ms = 1000.0 * dt / steps
+    if PLAIN:
+        return {"value": round(P_STREAMS * steps / dt, 1), "ms_per_step": round(ms, 4), "plain": True}
     fixed = 12 * LAYER_FIXED + 2 * 768 * PVOCAB + 4 * PVOCAB
     sb = fixed + P_STREAMS * KV_WORKLOAD * ctx
     return {"streams": P_STREAMS, "value": round(P_STREAMS * steps / dt, 1), "unit": "tokens/s",
@@ -521,6 +545,8 @@ def main():
     ap.add_argument("--layout", default="", help="reuse a layout directory (else one is built in a temp dir)")
     ap.add_argument("--prefill-rows", type=int, default=64,
                     help="prompt rows a pass through the MFMA banks (0: the prompt position by position)")
+    ap.add_argument("--plain", action="store_true",
+                    help="profiling: plain launches only (no graphs, no event pairs), one pass a leg, with --only b1/b64/pythia")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported (the batched streams would "
@@ -529,8 +555,11 @@ def main():
     if args.steps <= 0 or args.warmup < 0:
         sys.exit("bench.py: --steps must be positive and --warmup non-negative")
 
-    global PREFILL_ROWS
+    global PREFILL_ROWS, PLAIN
     PREFILL_ROWS = args.prefill_rows
+    PLAIN = args.plain
+    if PLAIN and args.only not in ("b1", "b64", "pythia"):
+        sys.exit("bench.py: --plain goes with --only b1, b64 or pythia")
     sm = load_sm()
     import torch
     if args.copy_probe:
@@ -567,6 +596,9 @@ def main():
     step_ach = sb / (b1["ms"] * 1e-3) / 1e9
     warm_sum = sum(r["us_per_step"] for r in table.values())
     cold_sum = sum(r["us_per_step"] for r in b1["cold"].values())
+    if PLAIN:
+        print(json.dumps({"value": round(b1["tok_s"], 2), "ms_per_step": round(b1["ms"], 4), "plain": True}), flush=True)
+        return
     cold = {"note": "1 GiB streamed through the device before each step (outside the timed launches); kernel "
                     "durations from the profiled pass", "steps": 15,
             "kernel_us_per_step": round(cold_sum, 2), "warm_kernel_us_per_step": round(warm_sum, 2),
