@@ -10,9 +10,11 @@ Restates foundation0/pythia_convert.py (the only place a float exists) for one c
   * tables: PHI and the arrival (as base2_convert.py builds them), LOG2/EXP2, cos/sin of the turns at 2^-30 for
     every position (rotary on the first quarter of each head, pairs (i, i + quarter/2)), eps40 = eps d^2 2^40
     and half_log2_hs = log2(head size)/2 at 2^-16 (:109-120).
-The reference converts a finished and a start checkpoint onto one grid (X.w / X.s); with one random checkpoint
-both are the same array, written under both names so the reference's machine loads the file unchanged.
-As in convert.py, ceil(log2(mx / 32767)) is evaluated exactly through frexp.
+The reference converts a finished and a start checkpoint onto one grid (X.w / X.s): each neuron's power of two is
+the smallest that holds the larger of the two checkpoints' largest values (shared16, pythia_convert.py:51-60), the
+norms' gain power likewise (:83-86).  Given no start, the finished checkpoint is written under both names, so the
+reference's machine loads the file unchanged.  As in convert.py, ceil(log2(mx / 32767)) is evaluated exactly
+through frexp.
 """
 from __future__ import annotations
 
@@ -68,15 +70,20 @@ def random_pythia(seed: int = 5, vocab: int = 50304, n_layer: int = 12, std: flo
     return sd, cfg
 
 
-def q16(W: np.ndarray, axis: int):
-    """int16 values with one power of two per neuron along `axis` (0: per column, 1: per row)
-    (pythia_convert.py:57-68 with start == finished)."""
-    mx = np.maximum(np.abs(W).max(axis), 1e-30)
-    e = _ceil_log2(mx / 32767)
-    q = np.round(W / np.exp2(np.expand_dims(e, axis).astype(np.float64))).astype(np.int64)
-    if np.abs(q).max() > 32767:
+def q16(W: np.ndarray, axis: int, Ws: np.ndarray | None = None):
+    """int16 values with one power of two per neuron along `axis` (0: per column, 1: per row), the smallest that
+    holds the larger of W's and (given) Ws's largest values in 16 places; returns W's values, Ws's values (None
+    when not given) and the powers (pythia_convert.py:51-60)."""
+    mx = np.abs(W).max(axis)
+    if Ws is not None:
+        mx = np.maximum(mx, np.abs(Ws).max(axis))
+    e = _ceil_log2(np.maximum(mx, 1e-30) / 32767)
+    sh = np.exp2(np.expand_dims(e, axis).astype(np.float64))
+    q = np.round(W / sh).astype(np.int64)
+    qs = None if Ws is None else np.round(Ws / sh).astype(np.int64)
+    if np.abs(q).max() > 32767 or (qs is not None and np.abs(qs).max() > 32767):
         raise ValueError("q16: a value does not fit 16 places")
-    return q.astype(np.int16), e
+    return q.astype(np.int16), (None if qs is None else qs.astype(np.int16)), e
 
 
 def pythia_tables(d: int, hs: int, rot: int, n_pos: int, base: float, eps: float) -> dict:
@@ -92,13 +99,22 @@ def pythia_tables(d: int, hs: int, rot: int, n_pos: int, base: float, eps: float
             "eps40": np.array(round(eps * d * d * 2 ** 40)), "half_log2_hs": np.array(half)}
 
 
-def convert_pythia(sd: dict, cfg: dict) -> dict:
-    """GPTNeoX-named state dict (numpy or torch) + config -> the npz dictionary pythia_base2.py loads."""
-    def get(k):
-        v = sd[k]
+def convert_pythia(sd: dict, cfg: dict, start: dict | None = None) -> dict:
+    """GPTNeoX-named finished state dict (numpy or torch) + config, and optionally the start checkpoint's state
+    dict, -> the npz dictionary pythia_base2.py loads (X.w finished, X.s start on the same per-neuron power X.e;
+    X.b / X.bs, lnN.g / .gs / .ge / .b / .bs; pythia_convert.py:64-107).  Without a start the finished checkpoint
+    stands for both."""
+    def arr(d, k):
+        v = d[k]
         if hasattr(v, "detach"):
             v = v.detach().cpu().numpy()
         return np.asarray(v, dtype=np.float64)
+
+    def get(k):
+        return arr(sd, k)
+
+    def get0(k):
+        return arr(sd if start is None else start, k)
 
     d, L, nh = cfg["d"], cfg["n_layer"], cfg["n_head"]
     hs = d // nh
@@ -106,19 +122,18 @@ def convert_pythia(sd: dict, cfg: dict) -> dict:
     out = {}
 
     def plate(name, key, bias=True):
-        w, e = q16(get(key + ".weight").T, 0)
-        out[name + ".w"], out[name + ".s"], out[name + ".e"] = w, w, e
+        w, ws, e = q16(get(key + ".weight").T, 0, get0(key + ".weight").T)
+        out[name + ".w"], out[name + ".s"], out[name + ".e"] = w, ws, e
         if bias:
-            b = stream(get(key + ".bias"))
-            out[name + ".b"], out[name + ".bs"] = b, b
+            out[name + ".b"], out[name + ".bs"] = stream(get(key + ".bias")), stream(get0(key + ".bias"))
 
     def norm(name, key):
-        g = get(key + ".weight")
-        ge = int(_ceil_log2(np.array([max(np.abs(g).max(), 1e-30) / 32767]))[0])
-        gq = np.round(g / 2.0 ** ge).astype(np.int64)
-        b = stream(get(key + ".bias"))
-        out[name + ".g"], out[name + ".gs"], out[name + ".ge"] = gq, gq, np.array(ge)
-        out[name + ".b"], out[name + ".bs"] = b, b
+        g, gs = get(key + ".weight"), get0(key + ".weight")
+        ge = int(_ceil_log2(np.array([max(np.abs(g).max(), np.abs(gs).max(), 1e-30) / 32767]))[0])
+        out[name + ".g"] = np.round(g / 2.0 ** ge).astype(np.int64)
+        out[name + ".gs"] = np.round(gs / 2.0 ** ge).astype(np.int64)
+        out[name + ".ge"] = np.array(ge)
+        out[name + ".b"], out[name + ".bs"] = stream(get(key + ".bias")), stream(get0(key + ".bias"))
 
     for l in range(L):
         p = f"gpt_neox.layers.{l}."
@@ -130,8 +145,7 @@ def convert_pythia(sd: dict, cfg: dict) -> dict:
         plate(f"mproj.{l}", p + "mlp.dense_4h_to_h")
     norm("lnf", "gpt_neox.final_layer_norm")
     plate("head", "embed_out", bias=False)
-    ew, ee = q16(get("gpt_neox.embed_in.weight"), 1)
-    out["embed.w"], out["embed.s"], out["embed.e"] = ew, ew, ee
+    out["embed.w"], out["embed.s"], out["embed.e"] = q16(get("gpt_neox.embed_in.weight"), 1, get0("gpt_neox.embed_in.weight"))
     out.update(pythia_tables(d, hs, rot, cfg["n_ctx"], cfg["rotary_emb_base"], cfg["layer_norm_eps"]))
     for k, v in dict(d=d, L=L, heads=nh, hs=hs, rot=rot, vocab=cfg["vocab"]).items():
         out[k] = np.array(v)
