@@ -162,8 +162,14 @@ class Machine:
         return [[int(w) for w in row] for row in self.generate(n_words)]
 
     def stream(self, prompt, n_words: int, stream: int = 0) -> list:
+        """base2.py:123's loop for one prompt: its n_words greedy words.  Every stream of the machine takes the
+        prompt (all streams of a run decode in lockstep from prompts of one length), and stream `stream`'s words
+        are returned."""
+        if not 0 <= stream < self.max_streams:
+            raise SmError(SM_E_ARG, f"stream {stream} outside [0, {self.max_streams})")
         self.reset()
-        self.prefill(prompt, stream)
+        for b in range(self.max_streams):
+            self.prefill(prompt, b)
         return [int(w) for w in self.generate(n_words)[stream]]
 
     def forward(self, ids) -> int:

@@ -227,3 +227,15 @@ def test_batched_continuation_and_errors(sm, batch_machine, full_oracle):
     with pytest.raises(sm.SmError) as e:
         m.generate(1)                               # prompts of different lengths
     assert e.value.code == -7
+
+
+def test_stream_on_a_multi_stream_machine(sm, small_dir, small_oracle):
+    """Machine.stream(prompt, n, stream=k) on a three-stream machine: every stream takes the prompt, row k's words"""
+    prompt = sm.prompt_ids(21, 8, 1000)
+    m = sm.Machine(small_dir, max_ctx=64, max_streams=3)
+    want = small_oracle.generate(prompt, 5)
+    assert m.stream(prompt, 5, stream=2) == want
+    assert m.stream(prompt, 5) == want
+    with pytest.raises(sm.SmError):
+        m.stream(prompt, 5, stream=3)
+    m.close()
