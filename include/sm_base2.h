@@ -49,6 +49,12 @@ typedef struct {
                               position but the last runs through the int8 MFMA banks that many rows a pass, each
                               weight read shared by the pass's rows (base2_stream.swift:74-91, 274-275: the
                               prompt through each layer at once); the last position is the first decode step */
+    int32_t inv;           /* 1: the complement machine (base2_stream.swift:26 `inv`, "the whole machine on the
+                              negative"): the stream row, every plate and every light held bit-complemented, each
+                              pile corrected by the plate's column sum, the light's sum and the input count, stream
+                              updates subtracted, the race won by the smallest complemented logit.  Its words, keys,
+                              values and recorded intermediates are the plain machine's; SM_READ_RESID returns the
+                              complemented stream.  GPT-2, max_streams 1, prefill_rows 0 */
 } sm_config;
 
 /* Replaces base2_stream.swift:151-208 (device, pipelines, loading base2_gpu/ and its buffers) and

@@ -43,6 +43,7 @@ struct GemvArgs {
     const int4* W;              // the plate in column tiles of TC (see sm_machine.hip: tile_plate)
     const int* we;              // per-column power of two
     const i64* bias;            // per-column bias (2^-16)
+    const i64* sw;              // INV = 1: each column's sum over the plain plate (W holds ~w)
     int nout, ntiles;
     const i64* X;               // the row this phase reads (PRO_GAUGE / PRO_TO16 / PRO_X16 / PRO_PGAUGE)
     i64* Y;                     // output row (or the stream R for EPI_PLAIN_ADD)
@@ -60,6 +61,18 @@ struct GemvArgs {
     i64* rg;                                   // record: the gauge's output row
     i64* rout2;                                // record: EPI_PLAIN_EDGE's row after the edge (rout: before)
 };
+
+// The complement machine (base2_stream.swift:26 `inv`, "the whole machine on the negative"): the stream row, every
+// plate and every light are held bit-complemented (~x = -x - 1).  A pile is then
+//   sum (~w)(~x) = sum w x + sum w + sum x + nin,
+// so the plain pile is the product less the plate's column sum, the light's sum and the input count
+// (:72, :90); a stream update ~R - a = ~(R + a) subtracts (:108); the race reads the complemented logits and the
+// smallest wins, ties to the lowest word (:134-139); the entering row is ~(wte + wpe) (:146, :271).
+// "a beats b" for a race entry (value, word); word < 0: no entry
+template <int INV>
+SMD bool race_beats(i64 a, int ai, i64 b, int bi) {
+    return ai >= 0 && (bi < 0 || (INV ? a < b : a > b) || (a == b && ai < bi));
+}
 
 // Batch 1: the race over the head blocks' bests, the word fed back, and the next position's entering row
 // (base2.py:103: wte[word] + wpe[p]; foundation0/pythia_base2.py:153: rshift(embed.w[word], -(embed.e[word] + 16)))

@@ -127,11 +127,16 @@ SMD void prologue_py(const GemvArgs& a, int tid, const i64 (&v)[768 / NT], const
     ex_o = -16 + sh2;
     __syncthreads();
 }
-template <int NIN, int NT, int PRO>
-SMD void prologue(const GemvArgs& a, int tid, const i64 (&v)[NIN / NT], short* xh_s, short* xl_s, int* red, i64& ex_o,
-                  i64& ls_o, i64& e2_o, bool rec) {
+// INV = 1 (the complement machine): a PRO_GAUGE row is the stream, held complemented, and is read back plain; the
+// light is held complemented in LDS, and sx_o returns the plain light's sum (the pile's correction).
+template <int NIN, int NT, int PRO, int INV>
+SMD void prologue(const GemvArgs& a, int tid, const i64 (&vin)[NIN / NT], short* xh_s, short* xl_s, int* red, i64& ex_o,
+                  i64& ls_o, i64& e2_o, i64& sx_o, bool rec) {
     constexpr int PER = NIN / NT, NW = NT / 64;
     const int lane = tid & 63, wave = tid >> 6;
+    i64 v[PER];
+#pragma unroll
+    for (int m = 0; m < PER; m++) v[m] = INV && PRO == PRO_GAUGE ? ~vin[m] : vin[m];
     int sh = 0;
     if (PRO != PRO_X16) {
         u64 o = 0;
@@ -152,8 +157,9 @@ SMD void prologue(const GemvArgs& a, int tid, const i64 (&v)[NIN / NT], short* x
     for (int m = 0; m < PER; m++) {
         int i = tid + NT * m;
         const int xi = PRO == PRO_X16 ? (int)v[m] : (int)rsh(v[m], sh);
-        xh_s[i] = (short)(xi >> 8);
-        xl_s[i] = (short)(xi & 255);
+        const int xs = INV ? ~xi : xi;          // the light as held
+        xh_s[i] = (short)(xs >> 8);             // in [-129, 128]
+        xl_s[i] = (short)(xs & 255);
         s1 += xi;
         s2 += (i64)xi * xi;
         if (rec && a.rx16) a.rx16[i] = xi;
@@ -167,6 +173,15 @@ SMD void prologue(const GemvArgs& a, int tid, const i64 (&v)[NIN / NT], short* x
 #pragma unroll
         for (int w = 0; w < NW; w++) { S1 += red[32 + 3 * w]; S2h += red[33 + 3 * w]; S2l += red[34 + 3 * w]; }
         ls = gauge_ls_pow(S1, (S2h << 16) + S2l, ex, a.tb, e2);
+        sx_o = S1;
+    } else if (INV) {
+        const int w1 = wave_add32(s1);
+        if (lane == 0) red[32 + wave] = w1;
+        __syncthreads();
+        i64 S1 = 0;
+#pragma unroll
+        for (int w = 0; w < NW; w++) S1 += red[32 + w];
+        sx_o = S1;
     } else {
         __syncthreads();
     }
@@ -213,8 +228,10 @@ SMD i64 wtile_partial(const v4i (&w)[U], const short* xh_s, const short* xl_s, i
 // is in flight while the current one is reduced.
 // The first memory requests are the row and the first tile: nothing the kernel reads depends on another read
 // (the position is not needed; REC = 1 instantiations, launched only for a recorded step, compare it).
-template <int NIN, int TC, int WPB, int PRO, int EPI, int REC>
+// INV = 1: the complement machine (GPT-2's phases; see race_beats).  Recorded values are the plain machine's.
+template <int NIN, int TC, int WPB, int PRO, int EPI, int REC, int INV = 0>
 __global__ __launch_bounds__(64 * WPB) void k_gemv(GemvArgs a) {
+    static_assert(!INV || PRO == PRO_GAUGE || PRO == PRO_TO16, "the complement machine is GPT-2's");
     constexpr int NT = 64 * WPB, U = WaveTile<NIN, TC>::U;
     static_assert(NIN % NT == 0, "the block's threads must split the light row evenly");
     __shared__ __align__(16) short xh_s[NIN];
@@ -236,16 +253,17 @@ __global__ __launch_bounds__(64 * WPB) void k_gemv(GemvArgs a) {
         // a tile's exponents and biases are requested before its weights, so waiting for the small loads
         // never waits for the large ones behind them
         v4i wA[U], wB[U];
-        i64 bA = 0, eA = 0, bB = 0, eB = 0;
+        i64 bA = 0, eA = 0, bB = 0, eB = 0, sA = 0, sB = 0;
         // every lane loads (indices clamped into range): a load that writes only some lanes would have to be
         // merged with the register's old value, and that merge waits for the load
-        auto fetch = [&](v4i (&w)[U], i64& we_, i64& b_, int t) {
+        auto fetch = [&](v4i (&w)[U], i64& we_, i64& b_, i64& s_, int t) {
             t = t < a.ntiles ? t : a.ntiles - 1;
             if (EPI != EPI_PILE) {
                 int j = t * TC + col;
                 j = j < 0 ? 0 : (j < a.nout ? j : a.nout - 1);
                 we_ = a.we[j];
                 if (EPI != EPI_PHEAD) b_ = a.bias[j];
+                if (INV) s_ = a.sw[j];
             }
             load_wtile<NIN, TC, U>(w, a.W, t, lane);
         };
@@ -253,25 +271,27 @@ __global__ __launch_bounds__(64 * WPB) void k_gemv(GemvArgs a) {
         i64 row[NIN / NT], nbq[NIN / NT];
         int ngq[NIN / NT];
         prologue_load<NIN, NT, PRO>(a, tid, row, ngq, nbq);   // the row first, then this wave's first tile
-        fetch(wA, eA, bA, tile);                         // unconditional (clamped): no branch for the wait count to merge
+        fetch(wA, eA, bA, sA, tile);                     // unconditional (clamped): no branch for the wait count to merge
         const bool rec = REC && a.rec_pos && *a.rec_pos == (a.pos ? *a.pos : -2);
-        i64 ex, ls = 0, e2 = 0;
+        i64 ex, ls = 0, e2 = 0, sx = 0;
         if constexpr (PRO == PRO_PGAUGE)
             prologue_py<NT>(a, tid, row, ngq, nbq, xh_s, xl_s, red, ex, rec && blockIdx.x == 0);
         else
-            prologue<NIN, NT, PRO>(a, tid, row, xh_s, xl_s, red, ex, ls, e2, rec && blockIdx.x == 0);
+            prologue<NIN, NT, PRO, INV>(a, tid, row, xh_s, xl_s, red, ex, ls, e2, sx, rec && blockIdx.x == 0);
         const i64 fe = wsub(0, ls) & 0xFFFF;          // the fine part of (we + ex + 16) 65536 - LS for every column
-        auto finish = [&](const v4i (&w)[U], i64 wec, i64 bc, int t) {
-            const i64 pile = wave_colsum64<TC>(wtile_partial<NIN, TC, U>(w, xh_s, xl_s, lane));
+        auto finish = [&](const v4i (&w)[U], i64 wec, i64 bc, i64 swc, int t) {
+            i64 pile = wave_colsum64<TC>(wtile_partial<NIN, TC, U>(w, xh_s, xl_s, lane));
+            if (INV) pile = wsub(pile, wadd(wadd(sx, swc), NIN));      // the plain pile
             const int j = t * TC + col;
             if (fin && j < a.nout) {
                 if (rec && a.rpile) a.rpile[j] = pile;
                 if (EPI == EPI_PILE) {
                     a.Y[j] = pile;
                 } else if (EPI == EPI_PLAIN_ADD) {
-                    const i64 r = wadd(a.Yb[j], wadd(rsh(pile, -(wec + ex + 16)), bc));
+                    const i64 add = wadd(rsh(pile, -(wec + ex + 16)), bc);
+                    const i64 r = INV ? wsub(a.Yb[j], add) : wadd(a.Yb[j], add);
                     a.Y[j] = r;
-                    if (rec && a.rout) a.rout[j] = r;
+                    if (rec && a.rout) a.rout[j] = INV ? ~r : r;
                 } else if (EPI == EPI_PLAIN || EPI == EPI_PLAIN_EDGE || EPI == EPI_PHEAD) {
                     i64 y = rsh(pile, -(wec + ex + 16));
                     if (EPI != EPI_PHEAD) y = wadd(y, bc);
@@ -291,7 +311,8 @@ __global__ __launch_bounds__(64 * WPB) void k_gemv(GemvArgs a) {
                     if (EPI == EPI_GAUGED_EDGE) y = edge1(y, a.tb);
                     if (EPI == EPI_HEAD) {
                         if (rec && a.rlogits) a.rlogits[j] = y;
-                        if (best_i < 0 || y > best_v) { best_v = y; best_i = j; }   // j grows: ties keep the first
+                        const i64 u = INV ? ~y : y;                                 // the logit as the race reads it
+                        if (race_beats<INV>(u, j, best_v, best_i)) { best_v = u; best_i = j; }   // j grows
                     } else {
                         a.Y[j] = y;
                         if (rec && a.rout) a.rout[j] = y;
@@ -301,12 +322,12 @@ __global__ __launch_bounds__(64 * WPB) void k_gemv(GemvArgs a) {
         };
         while (tile < a.ntiles) {
             const int t1 = tile + nw;
-            fetch(wB, eB, bB, t1);
-            finish(wA, eA, bA, tile);
+            fetch(wB, eB, bB, sB, t1);
+            finish(wA, eA, bA, sA, tile);
             if (t1 >= a.ntiles) break;
             const int t2 = t1 + nw;
-            fetch(wA, eA, bA, t2);
-            finish(wB, eB, bB, t1);
+            fetch(wA, eA, bA, sA, t2);
+            finish(wB, eB, bB, sB, t1);
             tile = t2;
         }
     }
@@ -318,14 +339,14 @@ __global__ __launch_bounds__(64 * WPB) void k_gemv(GemvArgs a) {
     for (int o = 1; o < TC; o <<= 1) {
         const i64 ov = __shfl_xor(best_v, o, 64);
         const int oi = __shfl_xor(best_i, o, 64);
-        if (oi >= 0 && (best_i < 0 || ov > best_v || (ov == best_v && oi < best_i))) { best_v = ov; best_i = oi; }
+        if (race_beats<INV>(ov, oi, best_v, best_i)) { best_v = ov; best_i = oi; }
     }
     if (lane == 16 - TC) { bestv[wave] = best_v; besti[wave] = best_i; }
     __syncthreads();
     if (tid == 0) {
         i64 bv = 0; int bi = -1;
         for (int w = 0; w < WPB; w++)
-            if (besti[w] >= 0 && (bi < 0 || bestv[w] > bv || (bestv[w] == bv && besti[w] < bi))) { bv = bestv[w]; bi = besti[w]; }
+            if (race_beats<INV>(bestv[w], besti[w], bv, bi)) { bv = bestv[w]; bi = besti[w]; }
         a.part_v[blockIdx.x] = bv;
         a.part_i[blockIdx.x] = bi;
     }
@@ -336,8 +357,10 @@ __global__ __launch_bounds__(64 * WPB) void k_gemv(GemvArgs a) {
 // row R0 written (GPT-2 base2.py:103: wte[word] + wpe[p]; Pythia foundation0/pythia_base2.py:153:
 // rshift(embed.w[word], -(embed.e[word] + 16))), so that the next step's first phase reads a plain row.  At a
 // prompt position the next word is the prompt's.  The bests are requested before the position is read.
-template <int MODEL>
+// INV = 1: the complement machine's race (smallest complemented logit) and entering row ~(wte[word] + wpe[p]).
+template <int MODEL, int INV = 0>
 __global__ __launch_bounds__(256) void k_race1(Race1Args a) {
+    static_assert(!INV || MODEL == 0, "the complement machine is GPT-2's");
     __shared__ i64 bvs[4];
     __shared__ int bis[4];
     __shared__ int tok_s;
@@ -363,19 +386,19 @@ __global__ __launch_bounds__(256) void k_race1(Race1Args a) {
     i64 bv = 0; int bi = -1;
 #pragma unroll
     for (int k = 0; k < PER; k++)
-        if (pi[k] >= 0 && (bi < 0 || pv[k] > bv || (pv[k] == bv && pi[k] < bi))) { bv = pv[k]; bi = pi[k]; }
+        if (race_beats<INV>(pv[k], pi[k], bv, bi)) { bv = pv[k]; bi = pi[k]; }
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) {
         const i64 ov = __shfl_xor(bv, o, 64);
         const int oi = __shfl_xor(bi, o, 64);
-        if (oi >= 0 && (bi < 0 || ov > bv || (ov == bv && oi < bi))) { bv = ov; bi = oi; }
+        if (race_beats<INV>(ov, oi, bv, bi)) { bv = ov; bi = oi; }
     }
     if (lane == 0) { bvs[wave] = bv; bis[wave] = bi; }
     __syncthreads();
     if (tid == 0) {
         bv = bvs[0]; bi = bis[0];
         for (int w = 1; w < 4; w++)
-            if (bis[w] >= 0 && (bi < 0 || bvs[w] > bv || (bvs[w] == bv && bis[w] < bi))) { bv = bvs[w]; bi = bis[w]; }
+            if (race_beats<INV>(bvs[w], bis[w], bv, bi)) { bv = bvs[w]; bi = bis[w]; }
         int tok;
         if (known) {
             tok = a.seq[q];
@@ -393,7 +416,10 @@ __global__ __launch_bounds__(256) void k_race1(Race1Args a) {
     const size_t tok = (size_t)tok_s;
     if (MODEL == 0) {
 #pragma unroll
-        for (int m = 0; m < 3; m++) a.R0[tid + 256 * m] = wadd(a.wte[tok * 768 + tid + 256 * m], wp[m]);
+        for (int m = 0; m < 3; m++) {
+            const i64 e = wadd(a.wte[tok * 768 + tid + 256 * m], wp[m]);
+            a.R0[tid + 256 * m] = INV ? ~e : e;
+        }
     } else {
         const i64 es = -((i64)a.ee[tok] + 16);
 #pragma unroll
@@ -402,8 +428,9 @@ __global__ __launch_bounds__(256) void k_race1(Race1Args a) {
 }
 
 // Batch 1: the entering row of the current position (the first step of a run; later steps' rows come from the race)
-template <int MODEL>
+template <int MODEL, int INV = 0>
 __global__ __launch_bounds__(256) void k_embed1(Race1Args a) {
+    static_assert(!INV || MODEL == 0, "the complement machine is GPT-2's");
     const int tid = threadIdx.x;
     const int p = *a.pos;
     const size_t tok = (size_t)a.seq[p];
@@ -411,7 +438,8 @@ __global__ __launch_bounds__(256) void k_embed1(Race1Args a) {
 #pragma unroll
         for (int m = 0; m < 3; m++) {
             const int i = tid + 256 * m;
-            a.R0[i] = wadd(a.wte[tok * 768 + i], a.wpe[(size_t)p * 768 + i]);
+            const i64 e = wadd(a.wte[tok * 768 + i], a.wpe[(size_t)p * 768 + i]);
+            a.R0[i] = INV ? ~e : e;
         }
     } else {
         const i64 es = -((i64)a.ee[tok] + 16);

@@ -115,6 +115,7 @@ struct DevPlate {
     int16_t* W = nullptr;
     int* e = nullptr;
     i64* b = nullptr;
+    i64* sw = nullptr;      // the complement machine: each column's sum over the plain plate (W then holds ~w)
 };
 
 // input-major [nin][nout] -> column tiles of tc: unit u of tile t holds inputs 8 (u / tc) .. + 8 of column
@@ -145,13 +146,23 @@ static int dalloc(T** p, size_t count) {
     return SM_OK;
 }
 
-static int upload_plate(DevPlate& P, const int16_t* w, const int32_t* e, const i64* b, int nin, int nout, int tc) {
+// inv: the plate held complemented, with its plain column sums (base2_stream.swift:189-190)
+static int upload_plate(DevPlate& P, const int16_t* w, const int32_t* e, const i64* b, int nin, int nout, int tc,
+                        bool inv = false) {
     if (nin % 8 || nin <= 0 || nout <= 0 || (tc != 1 && tc != 2 && tc != 4 && tc != 8))
         return fail(SM_E_ARG, "plate: nin must be a multiple of 8 and tile_cols one of 1, 2, 4, 8");
     P.nin = nin; P.nout = nout; P.tc = tc; P.ntiles = (nout + tc - 1) / tc;
     std::vector<int16_t> t = tile_plate(w, nin, nout, tc);
     int rc;
     if ((rc = dalloc(&P.W, t.size())) || (rc = dalloc(&P.e, (size_t)nout)) || (rc = dalloc(&P.b, (size_t)nout))) return rc;
+    if (inv) {
+        std::vector<i64> sw((size_t)nout, 0);
+        for (int k = 0; k < nin; k++)
+            for (int j = 0; j < nout; j++) sw[j] += w[(size_t)k * nout + j];
+        for (auto& x : t) x = (int16_t)~x;
+        if ((rc = dalloc(&P.sw, (size_t)nout))) return rc;
+        HIP_TRY(hipMemcpy(P.sw, sw.data(), (size_t)nout * 8, hipMemcpyHostToDevice));
+    }
     HIP_TRY(hipMemcpy(P.W, t.data(), t.size() * 2, hipMemcpyHostToDevice));
     HIP_TRY(hipMemcpy(P.e, e, (size_t)nout * 4, hipMemcpyHostToDevice));
     HIP_TRY(hipMemcpy(P.b, b, (size_t)nout * 8, hipMemcpyHostToDevice));
@@ -159,7 +170,7 @@ static int upload_plate(DevPlate& P, const int16_t* w, const int32_t* e, const i
 }
 
 static void free_plate(DevPlate& P) {
-    hfree(P.W); hfree(P.e); hfree(P.b);
+    hfree(P.W); hfree(P.e); hfree(P.b); hfree(P.sw);
     P = DevPlate();
 }
 
@@ -570,16 +581,26 @@ static Race1Args race1_args(sm_machine* m) {
 }
 static void launch_race1(sm_machine* m) {
     if (m->kind == 1) launch(m->cfg.profile, "race", k_race1<1>, dim3(1), dim3(256), 0, m->st, race1_args(m));
+    else if (m->cfg.inv) launch(m->cfg.profile, "race", k_race1<0, 1>, dim3(1), dim3(256), 0, m->st, race1_args(m));
     else launch(m->cfg.profile, "race", k_race1<0>, dim3(1), dim3(256), 0, m->st, race1_args(m));
 }
 static void launch_embed1(sm_machine* m) {
     if (m->kind == 1) launch(m->cfg.profile, "embed", k_embed1<1>, dim3(1), dim3(256), 0, m->st, race1_args(m));
+    else if (m->cfg.inv) launch(m->cfg.profile, "embed", k_embed1<0, 1>, dim3(1), dim3(256), 0, m->st, race1_args(m));
     else launch(m->cfg.profile, "embed", k_embed1<0>, dim3(1), dim3(256), 0, m->st, race1_args(m));
 }
 
-// a batch-1 GEMV phase: rec selects the instantiation that records (launched only for the recorded step)
+// a batch-1 GEMV phase: rec selects the instantiation that records (launched only for the recorded step); the
+// complement machine (GPT-2's phases only) its INV = 1 instantiations
 template <int NIN, int TC, int WPB, int PRO, int EPI>
 static void gemv(sm_machine* m, bool rec, const char* name, int grid, const GemvArgs& a) {
+    if constexpr (PRO == PRO_GAUGE || PRO == PRO_TO16) {
+        if (m->cfg.inv) {
+            if (rec) launch(m->cfg.profile, name, k_gemv<NIN, TC, WPB, PRO, EPI, 1, 1>, dim3(grid), dim3(64 * WPB), 0, m->st, a);
+            else launch(m->cfg.profile, name, k_gemv<NIN, TC, WPB, PRO, EPI, 0, 1>, dim3(grid), dim3(64 * WPB), 0, m->st, a);
+            return;
+        }
+    }
     if (rec) launch(m->cfg.profile, name, k_gemv<NIN, TC, WPB, PRO, EPI, 1>, dim3(grid), dim3(64 * WPB), 0, m->st, a);
     else launch(m->cfg.profile, name, k_gemv<NIN, TC, WPB, PRO, EPI, 0>, dim3(grid), dim3(64 * WPB), 0, m->st, a);
 }
@@ -600,7 +621,7 @@ static int launch_step_pythia(sm_machine* m, int parts, bool rec) {
         base.pos = ctl + CTL_POS;
         base.rec_pos = ctl + CTL_RECPOS;
         auto plate = [&](GemvArgs& a, const DevPlate& P, int k) {
-            a.W = reinterpret_cast<const int4*>(P.W); a.we = P.e; a.bias = P.b; a.nout = P.nout; a.ntiles = P.ntiles;
+            a.W = reinterpret_cast<const int4*>(P.W); a.we = P.e; a.bias = P.b; a.sw = P.sw; a.nout = P.nout; a.ntiles = P.ntiles;
             a.rx16 = m->r_x16 + (l * 4 + k) * 3072; a.rexls = m->r_exls + (l * 4 + k) * 2;
             a.rpile = m->r_pile + (l * 4 + k) * 3072;
         };
@@ -655,7 +676,7 @@ static int launch_step_pythia(sm_machine* m, int parts, bool rec) {
         a.tb = tb;
         a.pos = ctl + CTL_POS; a.rec_pos = ctl + CTL_RECPOS;
         const DevPlate& P = m->head;
-        a.W = reinterpret_cast<const int4*>(P.W); a.we = P.e; a.bias = P.b; a.nout = P.nout; a.ntiles = P.ntiles;
+        a.W = reinterpret_cast<const int4*>(P.W); a.we = P.e; a.bias = P.b; a.sw = P.sw; a.nout = P.nout; a.ntiles = P.ntiles;
         a.X = m->R;
         a.ng = m->fg; a.nb = m->fb; a.nge = m->fge; a.rg = m->r_hgauge;
         a.rx16 = m->r_hx16; a.rexls = m->r_hexls; a.rpile = m->r_hpile; a.rlogits = m->r_logits;
@@ -815,7 +836,7 @@ static int launch_step(sm_machine* m, int parts = STEP_ALL, bool rec = false) {
         {
             GemvArgs a = base;
             const DevPlate& P = m->bank[l][0];
-            a.W = reinterpret_cast<const int4*>(P.W); a.we = P.e; a.bias = P.b; a.nout = P.nout; a.ntiles = P.ntiles;
+            a.W = reinterpret_cast<const int4*>(P.W); a.we = P.e; a.bias = P.b; a.sw = P.sw; a.nout = P.nout; a.ntiles = P.ntiles;
             a.X = Rin; a.Y = m->QKV;
             a.rx16 = m->r_x16 + (l * 4 + 0) * 3072; a.rexls = m->r_exls + (l * 4 + 0) * 2;
             a.rpile = m->r_pile + (l * 4 + 0) * 3072; a.rout = m->r_qkv + l * 2304;
@@ -832,7 +853,7 @@ static int launch_step(sm_machine* m, int parts = STEP_ALL, bool rec = false) {
             // the entering row)
             GemvArgs g = base;
             const DevPlate& P = m->bank[l][1];
-            g.W = reinterpret_cast<const int4*>(P.W); g.we = P.e; g.bias = P.b; g.nout = P.nout; g.ntiles = P.ntiles;
+            g.W = reinterpret_cast<const int4*>(P.W); g.we = P.e; g.bias = P.b; g.sw = P.sw; g.nout = P.nout; g.ntiles = P.ntiles;
             g.X = m->att; g.Y = m->R; g.Yb = Rin;
             g.rx16 = m->r_x16 + (l * 4 + 1) * 3072; g.rexls = m->r_exls + (l * 4 + 1) * 2;
             g.rpile = m->r_pile + (l * 4 + 1) * 3072; g.rout = m->r_resid + (l * 2 + 0) * 768;
@@ -843,7 +864,7 @@ static int launch_step(sm_machine* m, int parts = STEP_ALL, bool rec = false) {
         {
             GemvArgs a = base;
             const DevPlate& P = m->bank[l][2];
-            a.W = reinterpret_cast<const int4*>(P.W); a.we = P.e; a.bias = P.b; a.nout = P.nout; a.ntiles = P.ntiles;
+            a.W = reinterpret_cast<const int4*>(P.W); a.we = P.e; a.bias = P.b; a.sw = P.sw; a.nout = P.nout; a.ntiles = P.ntiles;
             a.X = m->R; a.Y = m->hid;
             a.rx16 = m->r_x16 + (l * 4 + 2) * 3072; a.rexls = m->r_exls + (l * 4 + 2) * 2;
             a.rpile = m->r_pile + (l * 4 + 2) * 3072; a.rout = m->r_hid + l * 3072;
@@ -853,7 +874,7 @@ static int launch_step(sm_machine* m, int parts = STEP_ALL, bool rec = false) {
         {
             GemvArgs a = base;
             const DevPlate& P = m->bank[l][3];
-            a.W = reinterpret_cast<const int4*>(P.W); a.we = P.e; a.bias = P.b; a.nout = P.nout; a.ntiles = P.ntiles;
+            a.W = reinterpret_cast<const int4*>(P.W); a.we = P.e; a.bias = P.b; a.sw = P.sw; a.nout = P.nout; a.ntiles = P.ntiles;
             a.X = m->hid; a.Y = m->R; a.Yb = m->R;
             a.rx16 = m->r_x16 + (l * 4 + 3) * 3072; a.rexls = m->r_exls + (l * 4 + 3) * 2;
             a.rpile = m->r_pile + (l * 4 + 3) * 3072; a.rout = m->r_resid + (l * 2 + 1) * 768;
@@ -866,7 +887,7 @@ static int launch_step(sm_machine* m, int parts = STEP_ALL, bool rec = false) {
         a.tb = tb;
         a.pos = ctl + CTL_POS; a.rec_pos = ctl + CTL_RECPOS;
         const DevPlate& P = m->head;
-        a.W = reinterpret_cast<const int4*>(P.W); a.we = P.e; a.bias = P.b; a.nout = P.nout; a.ntiles = P.ntiles;
+        a.W = reinterpret_cast<const int4*>(P.W); a.we = P.e; a.bias = P.b; a.sw = P.sw; a.nout = P.nout; a.ntiles = P.ntiles;
         a.X = m->R;
         a.rx16 = m->r_hx16; a.rexls = m->r_hexls; a.rpile = m->r_hpile; a.rlogits = m->r_logits;
         a.part_v = m->part_v; a.part_i = m->part_i;      // each block's best; the race runs in k_race1
@@ -911,7 +932,7 @@ static int run_prefill(sm_machine* m, int npos) {
 extern "C" int sm_create(const char* layout_dir, const sm_config* cfg, sm_machine** out) {
     if (!layout_dir || !out) return fail(SM_E_ARG, "sm_create: null argument");
     *out = nullptr;
-    sm_config c{1, 1024, 1, 0, 16, 0, 0, 64};
+    sm_config c{1, 1024, 1, 0, 16, 0, 0, 64, 0};
     if (cfg) c = *cfg;
     if (c.max_streams < 1 || c.max_streams > 64) return fail(SM_E_ARG, "sm_create: max_streams must be in [1, 64]");
     if (c.prefill_rows < 0 || c.prefill_rows > 64) return fail(SM_E_ARG, "sm_create: prefill_rows must be in [0, 64]");
@@ -933,6 +954,8 @@ extern "C" int sm_create(const char* layout_dir, const sm_config* cfg, sm_machin
         if (hs != 64 || rot <= 0 || rot > 64 || rot % 2) return fail(SM_E_IO, "manifest.json: built for 12 heads of 64 and an even turned width");
         if ((rc = parse_norms(mtext, norms))) return rc;
     }
+    if (c.inv && (py || c.max_streams != 1 || c.prefill_rows != 0))
+        return fail(SM_E_ARG, "sm_create: the complement machine (inv) runs GPT-2 with max_streams 1 and prefill_rows 0");
     auto find = [&](const std::string& n) -> const BankInfo* {
         for (auto& b : banks) if (b.name == n) return &b;
         return nullptr;
@@ -959,7 +982,7 @@ extern "C" int sm_create(const char* layout_dir, const sm_config* cfg, sm_machin
             if ((rc = read_array(dir + name + ".wc", w, (size_t)NIN[k] * NOUT[k])) || (rc = read_array(dir + name + ".e", e, NOUT[k])) ||
                 (rc = read_array(dir + name + ".b", b, NOUT[k])))
                 return bail(rc);
-            if (m->B == 1 && (rc = upload_plate(m->bank[l][k], w.data(), e.data(), b.data(), NIN[k], NOUT[k], TCOLS[k]))) return bail(rc);
+            if (m->B == 1 && (rc = upload_plate(m->bank[l][k], w.data(), e.data(), b.data(), NIN[k], NOUT[k], TCOLS[k], c.inv))) return bail(rc);
             if (mfma && (rc = upload_mfma_plate(m->mbank[l][k], w.data(), e.data(), b.data(), NIN[k], NOUT[k]))) return bail(rc);
         }
     }
@@ -972,7 +995,7 @@ extern "C" int sm_create(const char* layout_dir, const sm_config* cfg, sm_machin
             return bail(rc);
         if (py) b.assign(m->vocab, 0);         // Pythia's head has no bias (foundation0/pythia_base2.py:159)
         else if ((rc = read_array(dir + "head.b", b, m->vocab))) return bail(rc);
-        if (m->B == 1 && (rc = upload_plate(m->head, w.data(), e.data(), b.data(), 768, m->vocab, HEAD_TC))) return bail(rc);
+        if (m->B == 1 && (rc = upload_plate(m->head, w.data(), e.data(), b.data(), 768, m->vocab, HEAD_TC, c.inv))) return bail(rc);
         if (m->B > 1 && (rc = upload_mfma_plate(m->mhead, w.data(), e.data(), b.data(), 768, m->vocab))) return bail(rc);
     }
     // word and position tables
@@ -1618,7 +1641,7 @@ extern "C" int sm_plate_product(const sm_plate* p, const int64_t* x16, int64_t* 
     if (p->mfma) return fail(SM_E_ARG, "sm_plate_product: the plate was made for rows (tile_cols == 0)");
     const DevPlate& P = p->P;
     GemvArgs a{};
-    a.W = reinterpret_cast<const int4*>(P.W); a.we = P.e; a.bias = P.b; a.nout = P.nout; a.ntiles = P.ntiles;
+    a.W = reinterpret_cast<const int4*>(P.W); a.we = P.e; a.bias = P.b; a.sw = P.sw; a.nout = P.nout; a.ntiles = P.ntiles;
     a.X = (const i64*)x16; a.Y = (i64*)pile;
     const int g = grid > 0 ? grid : (P.ntiles + 3) / 4;     // four waves per block, one tile per wave
     hipStream_t s = (hipStream_t)stream;

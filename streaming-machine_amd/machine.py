@@ -31,7 +31,7 @@ class SmError(RuntimeError):
 class SmConfig(ctypes.Structure):
     _fields_ = [("max_streams", ctypes.c_int32), ("max_ctx", ctypes.c_int32), ("use_graph", ctypes.c_int32),
                 ("head_grid", ctypes.c_int32), ("graph_steps", ctypes.c_int32), ("profile", ctypes.c_int32),
-                ("table_mode", ctypes.c_int32), ("prefill_rows", ctypes.c_int32)]
+                ("table_mode", ctypes.c_int32), ("prefill_rows", ctypes.c_int32), ("inv", ctypes.c_int32)]
 
 
 _LIB = None
@@ -107,6 +107,8 @@ class Machine:
             arrival="int")
       prefill_rows: every prompt position but the last goes through the int8 MFMA banks that many rows a pass
       (base2_stream.swift:274: the prompt through each layer at once); 0 runs it position by position.
+      inv: the complement machine (base2_stream.swift:26 `inv`): stream, plates and lights held bit-complemented on
+      the device; the same words (GPT-2, one stream, prefill_rows=0).
       .stream(prompt_ids, n_words) -> list of words        (base2.py:123's loop, KV-cached on the device)
       .forward(ids) -> word                                 (base2.py:forward's contract)
       .reset(); .prefill(ids, stream=0); .generate(n_words) -> int32 [n_streams][n_words]
@@ -117,13 +119,14 @@ class Machine:
 
     def __init__(self, layout_dir: str, max_ctx: int = 1024, max_streams: int = 1, use_graph: bool = True,
                  head_grid: int = 0, graph_steps: int = 16, profile: bool = False, memory_tables: bool = True,
-                 prefill_rows: int = 64, gauge: str = "int", edge: str = "int", arrival: str = "int", turn: str = "int"):
+                 prefill_rows: int = 64, gauge: str = "int", edge: str = "int", arrival: str = "int", turn: str = "int",
+                 inv: bool = False):
         for name, v in (("gauge", gauge), ("edge", edge), ("arrival", arrival), ("turn", turn)):
             if v != "int":
                 raise NotImplementedError(f"{name}={v}: the GPU machine runs the integer stages only")
         self.L = lib()
         cfg = SmConfig(max_streams, max_ctx, 1 if use_graph else 0, head_grid, graph_steps, 1 if profile else 0,
-                       0 if memory_tables else 1, prefill_rows)
+                       0 if memory_tables else 1, prefill_rows, 1 if inv else 0)
         h = vp()
         check(self.L.sm_create(os.fsencode(layout_dir), ctypes.byref(cfg), ctypes.byref(h)))
         self.h = h
