@@ -55,7 +55,19 @@ typedef struct {
                               updates subtracted, the race won by the smallest complemented logit.  Its words, keys,
                               values and recorded intermediates are the plain machine's; SM_READ_RESID returns the
                               complemented stream.  GPT-2, max_streams 1, prefill_rows 0 */
+    int32_t float_stages;  /* SM_FLOAT_* bits: those stages back in float64, as base2.py:10-11 switches them
+                              (gauge=, edge=, arrival=; base2.py:66-69, 79-80, 89-92, 110-113) and
+                              foundation0/pythia_base2.py:21-27 (gauge=, turn=, edge=, arrival=).  Diagnostics,
+                              compared with the reference at the word level.  max_streams 1, prefill_rows 0, inv 0;
+                              turn is the Pythia machine's (its layout's cosf.bin / sinf.bin).  With arrival the
+                              cache holds each key as float64, not k16 / ek */
+    int32_t top_read;      /* 1: the collapsing top read (base2_stream_fr.swift:4-15, its top=fr): the head reads
+                              the high-byte plane of the word table (w >> 8) for every word, bounds each word's
+                              score exactly, and reads the low bytes (w & 255) of the words that can still win;
+                              the same words as the full read.  GPT-2, max_streams 1, head_grid 393..512 */
 } sm_config;
+
+enum { SM_FLOAT_GAUGE = 1, SM_FLOAT_EDGE = 2, SM_FLOAT_ARRIVAL = 4, SM_FLOAT_TURN = 8 };
 
 /* Replaces base2_stream.swift:151-208 (device, pipelines, loading base2_gpu/ and its buffers) and
  * base2.py:12-16 (np.load of the converted model).  layout_dir is a base2_gpu.py directory
@@ -101,7 +113,9 @@ enum {
     /* the Pythia machine (foundation0/pythia_base2.py) only */
     SM_READ_REC_GAUGE = 21, /* [12][2][768] the gauge rows (ln1, ln2) of each layer (:100-110) */
     SM_READ_REC_FCPRE = 22, /* [12][3072] fc's plain output before the edge */
-    SM_READ_REC_HGAUGE = 23 /* [768] the head's gauge row (lnf) */
+    SM_READ_REC_HGAUGE = 23,/* [768] the head's gauge row (lnf) */
+    SM_READ_TOP = 24        /* int64 [1 + 3 x 1024] the collapsing top read's last step: the survivor count, then
+                               (word, exact pile, score) of the first 1024 survivors */
 };
 /* Copies one device array to host memory dst (bytes must match).  Replaces reading MTLBuffer contents
  * (base2_stream.swift:282-286) for per-intermediate parity. */

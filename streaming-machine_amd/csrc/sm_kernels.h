@@ -21,7 +21,16 @@ enum { EPI_GAUGED = 0,       // power(pile, (we + ex + 16) 65536 - LS) + b      
        // the Pythia machine: every plate is plain (foundation0/pythia_base2.py:112-114)
        EPI_PLAIN = 6,        // rshift(pile, -(we + ex + 16)) + b, written
        EPI_PLAIN_EDGE = 7,   // the same, then the edge (:147)
-       EPI_PHEAD = 8 };      // rshift(pile, -(we + ex + 16)) with no bias, then the race (:158-160)
+       EPI_PHEAD = 8,        // rshift(pile, -(we + ex + 16)) with no bias, then the race (:158-160)
+       // the collapsing top read (base2_stream_fr.swift:4-15): the high-byte plane's coarse pile and each word's
+       // exact bounds, the block's best low and its candidates
+       EPI_TOP1 = 9 };
+
+// k_gemv's MODE bits (batch 1): the complement machine, and two of the stages back in float64 (base2.py:10-11,
+// foundation0/pythia_base2.py:21-27: diagnostics that put one stage back to float; compared at the word level)
+enum { MODE_INV = 1,       // the complement machine (see race_beats)
+       MODE_FGAUGE = 2,    // gauge=float: GPT-2 base2.py:66-69, 110-113; Pythia foundation0/pythia_base2.py:94-96
+       MODE_FEDGE = 4 };   // edge=float: GPT-2's tanh form base2.py:79-80; Pythia's erf form pythia_base2.py:145-147
 
 // Record of one position's intermediates (stream 0), written when the position equals *pos.
 struct Rec {
@@ -43,7 +52,7 @@ struct GemvArgs {
     const int4* W;              // the plate in column tiles of TC (see sm_machine.hip: tile_plate)
     const int* we;              // per-column power of two
     const i64* bias;            // per-column bias (2^-16)
-    const i64* sw;              // INV = 1: each column's sum over the plain plate (W holds ~w)
+    const i64* sw;              // MODE_INV: each column's sum over the plain plate (W holds ~w)
     int nout, ntiles;
     const i64* X;               // the row this phase reads (PRO_GAUGE / PRO_TO16 / PRO_X16 / PRO_PGAUGE)
     i64* Y;                     // output row (or the stream R for EPI_PLAIN_ADD)
@@ -60,7 +69,13 @@ struct GemvArgs {
     const int* ng; const i64* nb; int nge;     // gain (16 places), offset (2^-16), the gain's power of two
     i64* rg;                                   // record: the gauge's output row
     i64* rout2;                                // record: EPI_PLAIN_EDGE's row after the edge (rout: before)
+    // EPI_TOP1: each block's candidates (word, high bound, coarse pile) in slots [block][TOP_CAP], their count in
+    // part_i[block] and the block's best low in part_v[block]; block 0 also writes the light (tx: 768 values) and
+    // its facts (tf: ex, LS, EXP2 of the fine part)
+    int* cand_j; i64* cand_h; i64* cand_c;
+    int* tx; i64* tf;
 };
+#define TOP_ITERS 8                 // EPI_TOP1: tiles a wave may finish (the grid is sized for it)
 
 // The complement machine (base2_stream.swift:26 `inv`, "the whole machine on the negative"): the stream row, every
 // plate and every light are held bit-complemented (~x = -x - 1).  A pile is then
@@ -85,6 +100,19 @@ struct Race1Args {
     const short* ew; const int* ee;             // Pythia
 };
 
+// The collapsing top read's second stage, batch 1 (one block): the survivors' low bytes, their exact scores, the
+// race, then k_race1's word feed and entering row
+struct TopArgs {
+    Race1Args r;                    // part_v: the first stage's block lows; part_i: their candidate counts
+    int cap;                        // candidate slots a block
+    const int* cand_j; const i64* cand_h; const i64* cand_c;
+    const int* tx; const i64* tf;   // the light and its facts (from the first stage's block 0)
+    const unsigned char* lo;        // [vocab][768] each word's low bytes (w & 255), word by word
+    const int* we; const i64* bias;
+    Tables tb;
+    int* tn; int* tw; i64* tpile; i64* tscore; int tmax;   // the step's survivors: count, word, exact pile, score
+};
+
 struct AttArgs {
     const i64* QKV;     // [B][2304]
     // the cache, head-major so that a (stream, head)'s positions are contiguous: [B][12 heads][ctx][64]
@@ -102,6 +130,8 @@ struct AttArgs {
     const int* rec_pos; i64* ratt;
     // the Pythia machine: turns on the first rot dims of q and k, the scores' half-log2(head size)
     const int* cosT; const int* sinT;   // [npos][rot / 2] at 2^-30
+    const double* cosF; const double* sinF;   // turn=float: [npos][rot / 2] float64 (pythia_base2.py:117-118)
+    double* KF;         // arrival=float: [12][ctx][64] each cached key as float64 (its raw gauged value)
     int rot; i64 half; i64 ehalf;       // ehalf = EXP2[(-half) & 0xFFFF]
     // prompt rows: row r is position rowmap[r] & 0xFFFF of stream rowmap[r] >> 16 (null: row r is stream r at
     // *pos).  Their keys and values are in the cache already (k_kv_rows), so the attention only reads it.

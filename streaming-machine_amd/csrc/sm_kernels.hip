@@ -18,6 +18,10 @@
 //     value per block (f = -LS mod 2^16 for every column), and with arithmetic tables no table read remains.
 #include "sm_kernels.h"
 
+// The float stages below evaluate each float64 operation of the reference's expression on its own, rounded once
+// in numpy's order: no multiply and add are fused into one rounding anywhere in this library.
+#pragma clang fp contract(off)
+
 #define NTHR 256
 
 // ---------------------------------------------------------------------------------------------------------
@@ -45,6 +49,44 @@ SMD void block_sum2(i64& a, i64& b, i64* red, int tid) {
 }
 
 // ---------------------------------------------------------------------------------------------------------
+// The float stages (base2.py:10-11 gauge=/edge=; foundation0/pythia_base2.py:21-27): diagnostics that put one
+// stage back to float64.
+//
+// numpy's sum of 768 float64 values (its pairwise summation): halves at multiples of 8 down to blocks of 96, each
+// block summed by 8 strided accumulators that are combined as ((r0 + r1) + (r2 + r3)) + ((r4 + r5) + (r6 + r7)).
+// One wave: lane l runs accumulator l % 8 of block l / 8; the butterfly over lane bits 0-2, then 3-5, forms the
+// same tree (a + b == b + a exactly), and every lane ends with the total.  val(i) gives element i.
+template <typename F>
+SMD double np_sum768(F val, int lane) {
+    const int base = 96 * (lane >> 3) + (lane & 7);
+    double r = val(base);
+#pragma unroll
+    for (int t = 1; t < 12; t++) r += val(base + 8 * t);
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) r += __shfl_xor(r, o, 64);
+    return r;
+}
+// the float gauge's size of a 768-wide row held as float64 in LDS: mean, then sqrt(mean((x - mean)^2) + 1e-5)
+// (base2.py:67, 111; foundation0/pythia_base2.py:95); the mean returned in mu
+SMD double np_sigma768(const double* xf, int lane, double& mu) {
+    const double m = np_sum768([&](int i) { return xf[i]; }, lane) / 768.0;
+    const double v = np_sum768([&](int i) { const double d = xf[i] - m; return d * d; }, lane) / 768.0;
+    mu = m;
+    return sqrt(v + 1e-5);
+}
+// edge=float, GPT-2 (base2.py:80): round(0.5 h (1 + tanh(0.7978845608028654 (h + 0.044715 h^3))) 2^16), h = H 2^-16
+SMD i64 edge_tanh(i64 H) {
+    const double h = (double)H * (1.0 / 65536.0);
+    const double u = 0.7978845608028654 * (h + 0.044715 * pow(h, 3.0));
+    return (i64)rint(0.5 * h * (1.0 + tanh(u)) * 65536.0);
+}
+// edge=float, Pythia (foundation0/pythia_base2.py:145-147): round(h 0.5 (1 + erf(h / sqrt(2))) 2^16)
+SMD i64 edge_erf(i64 H) {
+    const double h = (double)H * (1.0 / 65536.0);
+    return (i64)rint(h * 0.5 * (1.0 + erf(h / 1.4142135623730951)) * 65536.0);
+}
+
+// ---------------------------------------------------------------------------------------------------------
 // Prologue: the light entering the plate, computed by every block from the row it reads (NIN values over the
 // block's NT threads).  Writes xh/xl (NIN shorts each) into LDS and returns ex, LS and the gauge's power factor.
 // The water level's OR is reduced as two 32-bit words and the gauge's sums as exact 32-bit pieces (S1 < 2^25,
@@ -65,53 +107,69 @@ SMD void prologue_load(const GemvArgs& a, int tid, i64 (&v)[NIN / NT], int (&gq)
 // Pythia's prologue (foundation0/pythia_base2.py:100-110, 113): the gauge of the stream row R with the norm's own
 // gain and offset, then that row's water level.  Three block reductions: R's OR, the sums S1, S2, the gauged
 // row's OR.  c g < 2^41 and EXP2 < 2^17, so c g EXP2[f] is exact in 64 bits as the reference's int64 path is.
-template <int NT>
+// FG (gauge=float, :94-96): round((x - mu) / sigma g 2^ge 2^16) + b with x = R 2^-16 in float64 (xf: 768 doubles
+// of LDS), in place of the first two reductions.
+template <int NT, int FG>
 SMD void prologue_py(const GemvArgs& a, int tid, const i64 (&v)[768 / NT], const int (&gq)[768 / NT],
-                     const i64 (&bq)[768 / NT], short* xh_s, short* xl_s, int* red, i64& ex_o, bool rec) {
+                     const i64 (&bq)[768 / NT], short* xh_s, short* xl_s, int* red, double* xf, i64& ex_o, bool rec) {
     constexpr int PER = 768 / NT, NW = NT / 64;
     const int lane = tid & 63, wave = tid >> 6;
+    i64 g[PER];
+    if constexpr (FG) {
+#pragma unroll
+        for (int m = 0; m < PER; m++) xf[tid + NT * m] = (double)v[m] * (1.0 / 65536.0);
+        __syncthreads();
+        double mu;
+        const double sg = np_sigma768(xf, lane, mu), sc = ldexp(1.0, a.nge + 16);
+#pragma unroll
+        for (int m = 0; m < PER; m++) {
+            const double d = xf[tid + NT * m] - mu;
+            g[m] = wadd((i64)rint(d / sg * (double)gq[m] * sc), bq[m]);
+            if (rec && a.rg) a.rg[tid + NT * m] = g[m];
+        }
+    } else {
+        u64 o = 0;
+#pragma unroll
+        for (int m = 0; m < PER; m++) o |= (u64)iabs64(v[m]);
+        unsigned olo = wave_or32((unsigned)o), ohi = wave_or32((unsigned)(o >> 32));
+        if (lane == 0) { red[2 * wave] = (int)olo; red[2 * wave + 1] = (int)ohi; }
+        __syncthreads();
+        u64 all = 0;
+#pragma unroll
+        for (int w = 0; w < NW; w++) all |= ((u64)(unsigned)red[2 * w + 1] << 32) | (unsigned)red[2 * w];
+        const int sh = water_shift((i64)all);
+        int xi[PER];
+        int s1 = 0;
+        i64 s2 = 0;
+#pragma unroll
+        for (int m = 0; m < PER; m++) {
+            xi[m] = (int)rsh(v[m], sh);
+            s1 += xi[m];
+            s2 += (i64)xi[m] * xi[m];
+        }
+        const int w1 = wave_add32(s1), w2h = wave_add32((int)(s2 >> 16)), w2l = wave_add32((int)(s2 & 0xFFFF));
+        if (lane == 0) { red[32 + 3 * wave] = w1; red[33 + 3 * wave] = w2h; red[34 + 3 * wave] = w2l; }
+        __syncthreads();
+        i64 S1 = 0, S2h = 0, S2l = 0;
+#pragma unroll
+        for (int w = 0; w < NW; w++) { S1 += red[32 + 3 * w]; S2h += red[33 + 3 * w]; S2l += red[34 + 3 * w]; }
+        i64 e2;
+        const i64 ls = pgauge_ls_pow(S1, (S2h << 16) + S2l, -16 + sh, a.tb, e2);
+        const i64 sg = wsub(16, wsub(wmul((i64)a.nge + 16, 65536), ls) >> 16);     // 16 - I of the gauge's power
+#pragma unroll
+        for (int m = 0; m < PER; m++) {
+            const i64 c = 768 * (i64)xi[m] - S1;
+            g[m] = wadd(rsh(wmul(c * gq[m], e2), sg), bq[m]);
+            if (rec && a.rg) a.rg[tid + NT * m] = g[m];
+        }
+    }
     u64 o = 0;
 #pragma unroll
-    for (int m = 0; m < PER; m++) o |= (u64)iabs64(v[m]);
+    for (int m = 0; m < PER; m++) o |= (u64)iabs64(g[m]);
     unsigned olo = wave_or32((unsigned)o), ohi = wave_or32((unsigned)(o >> 32));
-    if (lane == 0) { red[2 * wave] = (int)olo; red[2 * wave + 1] = (int)ohi; }
-    __syncthreads();
-    u64 all = 0;
-#pragma unroll
-    for (int w = 0; w < NW; w++) all |= ((u64)(unsigned)red[2 * w + 1] << 32) | (unsigned)red[2 * w];
-    const int sh = water_shift((i64)all);
-    int xi[PER];
-    int s1 = 0;
-    i64 s2 = 0;
-#pragma unroll
-    for (int m = 0; m < PER; m++) {
-        xi[m] = (int)rsh(v[m], sh);
-        s1 += xi[m];
-        s2 += (i64)xi[m] * xi[m];
-    }
-    const int w1 = wave_add32(s1), w2h = wave_add32((int)(s2 >> 16)), w2l = wave_add32((int)(s2 & 0xFFFF));
-    if (lane == 0) { red[32 + 3 * wave] = w1; red[33 + 3 * wave] = w2h; red[34 + 3 * wave] = w2l; }
-    __syncthreads();
-    i64 S1 = 0, S2h = 0, S2l = 0;
-#pragma unroll
-    for (int w = 0; w < NW; w++) { S1 += red[32 + 3 * w]; S2h += red[33 + 3 * w]; S2l += red[34 + 3 * w]; }
-    i64 e2;
-    const i64 ls = pgauge_ls_pow(S1, (S2h << 16) + S2l, -16 + sh, a.tb, e2);
-    const i64 sg = wsub(16, wsub(wmul((i64)a.nge + 16, 65536), ls) >> 16);     // 16 - I of the gauge's power
-    i64 g[PER];
-    o = 0;
-#pragma unroll
-    for (int m = 0; m < PER; m++) {
-        const i64 c = 768 * (i64)xi[m] - S1;
-        g[m] = wadd(rsh(wmul(c * gq[m], e2), sg), bq[m]);
-        o |= (u64)iabs64(g[m]);
-        if (rec && a.rg) a.rg[tid + NT * m] = g[m];
-    }
-    olo = wave_or32((unsigned)o);
-    ohi = wave_or32((unsigned)(o >> 32));
     if (lane == 0) { red[72 + 2 * wave] = (int)olo; red[73 + 2 * wave] = (int)ohi; }
     __syncthreads();
-    all = 0;
+    u64 all = 0;
 #pragma unroll
     for (int w = 0; w < NW; w++) all |= ((u64)(unsigned)red[73 + 2 * w] << 32) | (unsigned)red[72 + 2 * w];
     const int sh2 = water_shift((i64)all);
@@ -127,16 +185,26 @@ SMD void prologue_py(const GemvArgs& a, int tid, const i64 (&v)[768 / NT], const
     ex_o = -16 + sh2;
     __syncthreads();
 }
-// INV = 1 (the complement machine): a PRO_GAUGE row is the stream, held complemented, and is read back plain; the
+// MODE_INV (the complement machine): a PRO_GAUGE row is the stream, held complemented, and is read back plain; the
 // light is held complemented in LDS, and sx_o returns the plain light's sum (the pile's correction).
-template <int NIN, int NT, int PRO, int INV>
-SMD void prologue(const GemvArgs& a, int tid, const i64 (&vin)[NIN / NT], short* xh_s, short* xl_s, int* red, i64& ex_o,
-                  i64& ls_o, i64& e2_o, i64& sx_o, bool rec) {
+// MODE_FGAUGE with PRO_GAUGE (gauge=float, base2.py:67): sig_o = the row's float64 size (xf: 768 doubles of LDS).
+// TOP (the top read's first stage): the light held in LDS as (x0, x2), (x1, x3) of every group of four inputs (the
+// high-byte plane's pairs), nn_o = the sum of its negative values; block 0 writes the light and its facts.
+template <int NIN, int NT, int PRO, int MODE, bool TOP = false>
+SMD void prologue(const GemvArgs& a, int tid, const i64 (&vin)[NIN / NT], short* xh_s, short* xl_s, int* red,
+                  double* xf, i64& ex_o, i64& ls_o, i64& e2_o, i64& sx_o, double& sig_o, i64& nn_o, bool rec) {
     constexpr int PER = NIN / NT, NW = NT / 64;
+    constexpr bool INV = MODE & MODE_INV, FG = (MODE & MODE_FGAUGE) && PRO == PRO_GAUGE;
+    static_assert(!TOP || (PRO == PRO_GAUGE && NW <= 8 && !INV), "the top read lights the stream row");
+    static_assert(!FG || NIN == 768, "the float gauge reads a 768-wide stream row");
     const int lane = tid & 63, wave = tid >> 6;
     i64 v[PER];
 #pragma unroll
     for (int m = 0; m < PER; m++) v[m] = INV && PRO == PRO_GAUGE ? ~vin[m] : vin[m];
+    if constexpr (FG) {
+#pragma unroll
+        for (int m = 0; m < PER; m++) xf[tid + NT * m] = (double)v[m] * (1.0 / 65536.0);   // (the next barrier serves)
+    }
     int sh = 0;
     if (PRO != PRO_X16) {
         u64 o = 0;
@@ -150,30 +218,48 @@ SMD void prologue(const GemvArgs& a, int tid, const i64 (&vin)[NIN / NT], short*
         for (int w = 0; w < NW; w++) all |= ((u64)(unsigned)red[2 * w + 1] << 32) | (unsigned)red[2 * w];
         sh = water_shift((i64)all);
     }
+    if constexpr (FG) {
+        double mu;
+        sig_o = np_sigma768(xf, lane, mu);
+    }
     const i64 ex = -16 + sh;
-    int s1 = 0;
+    int s1 = 0, sn = 0;
     i64 s2 = 0;
 #pragma unroll
     for (int m = 0; m < PER; m++) {
         int i = tid + NT * m;
         const int xi = PRO == PRO_X16 ? (int)v[m] : (int)rsh(v[m], sh);
         const int xs = INV ? ~xi : xi;          // the light as held
-        xh_s[i] = (short)(xs >> 8);             // in [-129, 128]
-        xl_s[i] = (short)(xs & 255);
+        const int li = TOP ? (i & ~3) | ((i & 1) << 1) | ((i >> 1) & 1) : i;
+        xh_s[li] = (short)(xs >> 8);            // in [-129, 128]
+        xl_s[li] = (short)(xs & 255);
         s1 += xi;
         s2 += (i64)xi * xi;
+        if (TOP) sn += min(xi, 0);
         if (rec && a.rx16) a.rx16[i] = xi;
+        if (TOP && blockIdx.x == 0) a.tx[i] = xi;
     }
     i64 ls = 0, e2 = 0;
     if (PRO == PRO_GAUGE) {
         const int w1 = wave_add32(s1), w2h = wave_add32((int)(s2 >> 16)), w2l = wave_add32((int)(s2 & 0xFFFF));
         if (lane == 0) { red[32 + 3 * wave] = w1; red[33 + 3 * wave] = w2h; red[34 + 3 * wave] = w2l; }
+        if constexpr (TOP) {
+            const int wn = wave_add32(sn);
+            if (lane == 0) red[80 + wave] = wn;
+        }
         __syncthreads();
         i64 S1 = 0, S2h = 0, S2l = 0;
 #pragma unroll
         for (int w = 0; w < NW; w++) { S1 += red[32 + 3 * w]; S2h += red[33 + 3 * w]; S2l += red[34 + 3 * w]; }
         ls = gauge_ls_pow(S1, (S2h << 16) + S2l, ex, a.tb, e2);
         sx_o = S1;
+        if constexpr (TOP) {
+            i64 nn = 0;
+#pragma unroll
+            for (int w = 0; w < NW; w++) nn += red[80 + w];
+            nn_o = nn;
+            if (blockIdx.x == 0 && tid == 0) { a.tf[0] = ex; a.tf[1] = ls; a.tf[2] = e2; }
+        }
     } else if (INV) {
         const int w1 = wave_add32(s1);
         if (lane == 0) red[32 + wave] = w1;
@@ -192,32 +278,51 @@ SMD void prologue(const GemvArgs& a, int tid, const i64 (&vin)[NIN / NT], short*
 }
 
 // ---------------------------------------------------------------------------------------------------------
-// One wave's share of a tile: U = TC NIN / 512 units of 16 bytes per lane (unit u = lane + 64 m).
-template <int NIN, int TC>
+// One wave's share of a tile: U units of 16 bytes per lane (unit u = lane + 64 m).  WB: bytes a weight (2: the
+// int16 plate; 1: the top read's high-byte plane, w >> 8)
+template <int NIN, int TC, int WB = 2>
 struct WaveTile {
-    static constexpr int U = TC * NIN / 8 / 64;
-    static_assert(TC * NIN / 8 % 64 == 0, "a tile must split evenly over the 64 lanes");
+    static constexpr int U = TC * NIN * WB / 16 / 64;
+    static_assert(TC * NIN * WB / 16 % 64 == 0, "a tile must split evenly over the 64 lanes");
 };
 
-template <int NIN, int TC, int U>
+template <int NIN, int TC, int U, int WB = 2>
 SMD void load_wtile(v4i (&w)[U], const int4* __restrict__ W, int tile, int lane) {
-    const v4i* base = reinterpret_cast<const v4i*>(W) + (size_t)tile * (TC * NIN / 8) + lane;
+    const v4i* base = reinterpret_cast<const v4i*>(W) + (size_t)tile * (TC * NIN * WB / 16) + lane;
 #pragma unroll
     for (int m = 0; m < U; m++) w[m] = base[64 * m];      // plain loads: measured 1 % faster a step than nontemporal
 }
 
 // the lane's part of its column's pile: unit u holds inputs 8 (u / TC) .. + 8 of column u % TC = lane % TC
-template <int NIN, int TC, int U>
+// (WB = 1: inputs 16 (u / TC) .. + 16, as signed bytes)
+template <int NIN, int TC, int U, int WB = 2>
 SMD i64 wtile_partial(const v4i (&w)[U], const short* xh_s, const short* xl_s, int lane) {
     int ah = 0, al = 0;
 #pragma unroll
     for (int m = 0; m < U; m++) {
         const int c = (lane + 64 * m) / TC;
-        const int4 xh = reinterpret_cast<const int4*>(xh_s)[c];
-        const int4 xl = reinterpret_cast<const int4*>(xl_s)[c];
         const v4i ww = w[m];
-        ah = dot2(ww.x, xh.x, ah); ah = dot2(ww.y, xh.y, ah); ah = dot2(ww.z, xh.z, ah); ah = dot2(ww.w, xh.w, ah);
-        al = dot2(ww.x, xl.x, al); al = dot2(ww.y, xl.y, al); al = dot2(ww.z, xl.z, al); al = dot2(ww.w, xl.w, al);
+        if constexpr (WB == 2) {
+            const int4 xh = reinterpret_cast<const int4*>(xh_s)[c];
+            const int4 xl = reinterpret_cast<const int4*>(xl_s)[c];
+            ah = dot2(ww.x, xh.x, ah); ah = dot2(ww.y, xh.y, ah); ah = dot2(ww.z, xh.z, ah); ah = dot2(ww.w, xh.w, ah);
+            al = dot2(ww.x, xl.x, al); al = dot2(ww.y, xl.y, al); al = dot2(ww.z, xl.z, al); al = dot2(ww.w, xl.w, al);
+        } else {
+            // dword d holds the bytes of inputs 4d .. 4d + 3; (d << 8) & 0xFF00FF00 and d & 0xFF00FF00 are the
+            // int16 pairs (256 b0, 256 b2) and (256 b1, 256 b3): the high byte's share of the pile with its 256
+            // already in place; the light is held in LDS as (x0, x2), (x1, x3) of every group of four
+            const int4 h0 = reinterpret_cast<const int4*>(xh_s)[2 * c], h1 = reinterpret_cast<const int4*>(xh_s)[2 * c + 1];
+            const int4 l0 = reinterpret_cast<const int4*>(xl_s)[2 * c], l1 = reinterpret_cast<const int4*>(xl_s)[2 * c + 1];
+            const int hx[8] = {h0.x, h0.y, h0.z, h0.w, h1.x, h1.y, h1.z, h1.w};
+            const int lx[8] = {l0.x, l0.y, l0.z, l0.w, l1.x, l1.y, l1.z, l1.w};
+            const int wd[4] = {ww.x, ww.y, ww.z, ww.w};
+#pragma unroll
+            for (int d = 0; d < 4; d++) {
+                const int pa = (int)(((unsigned)wd[d] << 8) & 0xFF00FF00u), pb = (int)((unsigned)wd[d] & 0xFF00FF00u);
+                ah = dot2(pa, hx[2 * d], ah); ah = dot2(pb, hx[2 * d + 1], ah);
+                al = dot2(pa, lx[2 * d], al); al = dot2(pb, lx[2 * d + 1], al);
+            }
+        }
     }
     return (i64)ah * 256 + (i64)al;
 }
@@ -228,24 +333,40 @@ SMD i64 wtile_partial(const v4i (&w)[U], const short* xh_s, const short* xl_s, i
 // is in flight while the current one is reduced.
 // The first memory requests are the row and the first tile: nothing the kernel reads depends on another read
 // (the position is not needed; REC = 1 instantiations, launched only for a recorded step, compare it).
-// INV = 1: the complement machine (GPT-2's phases; see race_beats).  Recorded values are the plain machine's.
-template <int NIN, int TC, int WPB, int PRO, int EPI, int REC, int INV = 0>
+// MODE (batch 1): MODE_INV, the complement machine (GPT-2's phases; see race_beats; recorded values are the plain
+// machine's); MODE_FGAUGE, MODE_FEDGE: the float gauge (gauged phases) and the float edge (the fc phases).
+template <int NIN, int TC, int WPB, int PRO, int EPI, int REC, int MODE = 0>
 __global__ __launch_bounds__(64 * WPB) void k_gemv(GemvArgs a) {
+    constexpr bool INV = MODE & MODE_INV;
+    constexpr bool FG = (MODE & MODE_FGAUGE) && (PRO == PRO_GAUGE || PRO == PRO_PGAUGE);
+    constexpr bool FE = (MODE & MODE_FEDGE) && (EPI == EPI_GAUGED_EDGE || EPI == EPI_PLAIN_EDGE);
     static_assert(!INV || PRO == PRO_GAUGE || PRO == PRO_TO16, "the complement machine is GPT-2's");
-    constexpr int NT = 64 * WPB, U = WaveTile<NIN, TC>::U;
+    constexpr bool TOP = EPI == EPI_TOP1;
+    constexpr int WB = TOP ? 1 : 2;                   // the top read's first stage streams the high-byte plane
+    constexpr int NT = 64 * WPB, U = WaveTile<NIN, TC, WB>::U;
     static_assert(NIN % NT == 0, "the block's threads must split the light row evenly");
     __shared__ __align__(16) short xh_s[NIN];
     __shared__ __align__(16) short xl_s[NIN];
+    __shared__ double xf_s[FG ? 768 : 1];
     __shared__ int red[96];        // prologue: OR words [0, 24), sums [32, 68), second OR [72, 96)
     __shared__ i64 bestv[WPB];
     __shared__ int besti[WPB];
+    // EPI_TOP1: each finished word of the block (slot (wave, tile of the wave, column)): word, high bound, coarse pile
+    constexpr int TSLOTS = TOP ? WPB * TOP_ITERS * TC : 1;
+    __shared__ int top_j[TSLOTS];
+    __shared__ i64 top_h[TSLOTS], top_c[TSLOTS];
+    __shared__ int top_n;
     static_assert(WPB <= 12, "the prologue's LDS slots hold at most 12 waves");
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int col = lane - (16 - TC);                 // the column this lane finishes (valid when 0 <= col < TC)
     const bool fin = col >= 0 && col < TC;
     constexpr bool HEAD = EPI == EPI_HEAD || EPI == EPI_PHEAD;
+    if constexpr (TOP) {                              // (the prologue's barriers come before any slot is written)
+        for (int k = tid; k < TSLOTS; k += NT) top_j[k] = -1;
+        if (tid == 0) top_n = 0;
+    }
 
-    i64 best_v = 0;
+    i64 best_v = TOP ? INT64_MIN : 0;                 // EPI_TOP1: the lane's best low
     int best_i = -1;
     {
         const int gw = blockIdx.x * WPB + wave, nw = gridDim.x * WPB;
@@ -265,7 +386,7 @@ __global__ __launch_bounds__(64 * WPB) void k_gemv(GemvArgs a) {
                 if (EPI != EPI_PHEAD) b_ = a.bias[j];
                 if (INV) s_ = a.sw[j];
             }
-            load_wtile<NIN, TC, U>(w, a.W, t, lane);
+            load_wtile<NIN, TC, U, WB>(w, a.W, t, lane);
         };
         int tile = gw;
         i64 row[NIN / NT], nbq[NIN / NT];
@@ -273,17 +394,39 @@ __global__ __launch_bounds__(64 * WPB) void k_gemv(GemvArgs a) {
         prologue_load<NIN, NT, PRO>(a, tid, row, ngq, nbq);   // the row first, then this wave's first tile
         fetch(wA, eA, bA, sA, tile);                     // unconditional (clamped): no branch for the wait count to merge
         const bool rec = REC && a.rec_pos && *a.rec_pos == (a.pos ? *a.pos : -2);
-        i64 ex, ls = 0, e2 = 0, sx = 0;
+        i64 ex, ls = 0, e2 = 0, sx = 0, nn = 0;
+        double sig = 1.0;
         if constexpr (PRO == PRO_PGAUGE)
-            prologue_py<NT>(a, tid, row, ngq, nbq, xh_s, xl_s, red, ex, rec && blockIdx.x == 0);
+            prologue_py<NT, FG>(a, tid, row, ngq, nbq, xh_s, xl_s, red, xf_s, ex, rec && blockIdx.x == 0);
         else
-            prologue<NIN, NT, PRO, INV>(a, tid, row, xh_s, xl_s, red, ex, ls, e2, sx, rec && blockIdx.x == 0);
+            prologue<NIN, NT, PRO, MODE, TOP>(a, tid, row, xh_s, xl_s, red, xf_s, ex, ls, e2, sx, sig, nn,
+                                              rec && blockIdx.x == 0);
         const i64 fe = wsub(0, ls) & 0xFFFF;          // the fine part of (we + ex + 16) 65536 - LS for every column
+        const i64 np = wsub(sx, nn);                  // EPI_TOP1: the sum of the light's positive values
+        int it = 0;                                   // EPI_TOP1: tiles this wave has finished
         auto finish = [&](const v4i (&w)[U], i64 wec, i64 bc, i64 swc, int t) {
-            i64 pile = wave_colsum64<TC>(wtile_partial<NIN, TC, U>(w, xh_s, xl_s, lane));
+            i64 pile = wave_colsum64<TC>(wtile_partial<NIN, TC, U, WB>(w, xh_s, xl_s, lane));
             if (INV) pile = wsub(pile, wadd(wadd(sx, swc), NIN));      // the plain pile
             const int j = t * TC + col;
-            if (fin && j < a.nout) {
+            if (TOP && fin && j < a.nout) {
+                // the pile lies in [C + 255 nn, C + 255 np] (the low byte w & 255 is in [0, 255]); power never
+                // decreases in its argument while X EXP2 + half stays below 2^63 and the shift is a right shift,
+                // so each end's score bounds the word's score (base2_stream_fr.swift:8-12); otherwise the word
+                // is unsure: always a candidate, and no low
+                const i64 F = wsub(wmul(wec + ex + 16, 65536), ls), sft = wsub(16, F >> 16);
+                const i64 xlo = wadd(pile, wmul(255, nn)), xhi = wadd(pile, wmul(255, np));
+                const bool sure = sft >= 0 && sft <= 62 && iabs64(xlo) < ((i64)1 << 44) && iabs64(xhi) < ((i64)1 << 44);
+                i64 lo = INT64_MIN, hi = INT64_MAX;
+                if (sure) {
+                    lo = wadd(rsh(xlo * e2, sft), bc);
+                    hi = wadd(rsh(xhi * e2, sft), bc);
+                }
+                const int k = (wave * TOP_ITERS + it) * TC + col;
+                top_j[k] = j;
+                top_h[k] = hi;
+                top_c[k] = pile;
+                best_v = max(best_v, lo);
+            } else if (fin && j < a.nout) {
                 if (rec && a.rpile) a.rpile[j] = pile;
                 if (EPI == EPI_PILE) {
                     a.Y[j] = pile;
@@ -301,14 +444,20 @@ __global__ __launch_bounds__(64 * WPB) void k_gemv(GemvArgs a) {
                     } else {
                         if (rec && a.rout) a.rout[j] = y;
                         if (EPI == EPI_PLAIN_EDGE) {
-                            y = edge1(y, a.tb);
+                            y = FE ? edge_erf(y) : edge1(y, a.tb);
                             if (rec && a.rout2) a.rout2[j] = y;
                         }
                         a.Y[j] = y;
                     }
                 } else {
-                    i64 y = wadd(power_e(pile, wsub(wmul(wec + ex + 16, 65536), ls), fe, e2, a.tb), bc);
-                    if (EPI == EPI_GAUGED_EDGE) y = edge1(y, a.tb);
+                    i64 y;
+                    if (FG && EPI == EPI_HEAD)          // base2.py:112-113
+                        y = (i64)rint((ldexp((double)pile, (int)(wec + ex)) / sig + (double)bc * (1.0 / 65536.0)) * 65536.0);
+                    else if (FG)                        // base2.py:68-69
+                        y = wadd((i64)rint(ldexp((double)pile, (int)(wec + ex)) / sig * 65536.0), bc);
+                    else
+                        y = wadd(power_e(pile, wsub(wmul(wec + ex + 16, 65536), ls), fe, e2, a.tb), bc);
+                    if (EPI == EPI_GAUGED_EDGE) y = FE ? edge_tanh(y) : edge1(y, a.tb);
                     if (EPI == EPI_HEAD) {
                         if (rec && a.rlogits) a.rlogits[j] = y;
                         const i64 u = INV ? ~y : y;                                 // the logit as the race reads it
@@ -324,12 +473,39 @@ __global__ __launch_bounds__(64 * WPB) void k_gemv(GemvArgs a) {
             const int t1 = tile + nw;
             fetch(wB, eB, bB, sB, t1);
             finish(wA, eA, bA, sA, tile);
+            it++;
             if (t1 >= a.ntiles) break;
             const int t2 = t1 + nw;
             fetch(wA, eA, bA, sA, t2);
             finish(wB, eB, bB, sB, t1);
+            it++;
             tile = t2;
         }
+    }
+    if constexpr (TOP) {
+        // the block's best low; its candidates are its words whose high reaches it (the winner's high reaches
+        // the grid's best low, which is at least this one), written to the block's slots with their count
+        const i64 wl = wave_reduce64(best_v, OpMax());
+        if (lane == 0) bestv[wave] = wl;
+        __syncthreads();
+        i64 bl = bestv[0];
+#pragma unroll
+        for (int w = 1; w < WPB; w++) bl = max(bl, bestv[w]);
+        for (int k = tid; k < TSLOTS; k += NT) {
+            if (top_j[k] >= 0 && top_h[k] >= bl) {
+                const int n = atomicAdd(&top_n, 1);
+                const size_t o = (size_t)blockIdx.x * TSLOTS + n;
+                a.cand_j[o] = top_j[k];
+                a.cand_h[o] = top_h[k];
+                a.cand_c[o] = top_c[k];
+            }
+        }
+        __syncthreads();
+        if (tid == 0) {
+            a.part_v[blockIdx.x] = bl;
+            a.part_i[blockIdx.x] = top_n;
+        }
+        return;
     }
     if constexpr (!HEAD) return;
 
@@ -352,41 +528,21 @@ __global__ __launch_bounds__(64 * WPB) void k_gemv(GemvArgs a) {
     }
 }
 
-// Batch 1, after the head: the race over its blocks' bests (base2.py:34-40, 114; ties to the lowest word), the
-// word fed straight back (base2_stream.swift:143-146), the position advanced, and the next position's entering
-// row R0 written (GPT-2 base2.py:103: wte[word] + wpe[p]; Pythia foundation0/pythia_base2.py:153:
-// rshift(embed.w[word], -(embed.e[word] + 16))), so that the next step's first phase reads a plain row.  At a
-// prompt position the next word is the prompt's.  The bests are requested before the position is read.
-// INV = 1: the complement machine's race (smallest complemented logit) and entering row ~(wte[word] + wpe[p]).
-template <int MODEL, int INV = 0>
-__global__ __launch_bounds__(256) void k_race1(Race1Args a) {
-    static_assert(!INV || MODEL == 0, "the complement machine is GPT-2's");
+// The batch-1 race's end, one block of 256 threads: each thread's entry (bv, bi) raced over the block (largest,
+// ties to the lowest word; INV: smallest), the word fed straight back (base2_stream.swift:143-146), the position
+// advanced, and the next position's entering row R0 written (GPT-2 base2.py:103: wte[word] + wpe[p]; Pythia
+// foundation0/pythia_base2.py:153: rshift(embed.w[word], -(embed.e[word] + 16))), so that the next step's first
+// phase reads a plain row.  At a prompt position the next word is the prompt's.  wp: the next position's wpe row
+// (GPT-2), requested by the caller early.
+template <int MODEL, int INV>
+SMD void race1_finish(const Race1Args& a, i64 bv, int bi, int p, int plen, const i64 (&wp)[3]) {
     __shared__ i64 bvs[4];
     __shared__ int bis[4];
     __shared__ int tok_s;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    constexpr int PER = 4;                              // bests a thread reads (nblk <= 1024)
-    i64 pv[PER];
-    int pi[PER];
-#pragma unroll
-    for (int k = 0; k < PER; k++) {
-        const int g = tid + 256 * k;
-        pv[k] = g < a.nblk ? a.part_v[g] : 0;
-        pi[k] = g < a.nblk ? a.part_i[g] : -1;
-    }
-    const int p = *a.pos, plen = *a.plen;
     const bool known = p < plen - 1;                    // a prompt position: the next word is the prompt's
     const int q = p + 1;                                // the next position
     const bool embed = q < a.npos;
-    i64 wp[3] = {0, 0, 0};
-    if (MODEL == 0 && embed) {
-#pragma unroll
-        for (int m = 0; m < 3; m++) wp[m] = a.wpe[(size_t)q * 768 + tid + 256 * m];
-    }
-    i64 bv = 0; int bi = -1;
-#pragma unroll
-    for (int k = 0; k < PER; k++)
-        if (race_beats<INV>(pv[k], pi[k], bv, bi)) { bv = pv[k]; bi = pi[k]; }
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) {
         const i64 ov = __shfl_xor(bv, o, 64);
@@ -425,6 +581,132 @@ __global__ __launch_bounds__(256) void k_race1(Race1Args a) {
 #pragma unroll
         for (int m = 0; m < 3; m++) a.R0[tid + 256 * m] = rsh((i64)a.ew[tok * 768 + tid + 256 * m], es);
     }
+}
+
+// Batch 1, after the head: the race over its blocks' bests (base2.py:34-40, 114), then race1_finish.  The bests are
+// requested before the position is read.
+// INV = 1: the complement machine's race (smallest complemented logit) and entering row ~(wte[word] + wpe[p]).
+template <int MODEL, int INV = 0>
+__global__ __launch_bounds__(256) void k_race1(Race1Args a) {
+    static_assert(!INV || MODEL == 0, "the complement machine is GPT-2's");
+    const int tid = threadIdx.x;
+    constexpr int PER = 4;                              // bests a thread reads (nblk <= 1024)
+    i64 pv[PER];
+    int pi[PER];
+#pragma unroll
+    for (int k = 0; k < PER; k++) {
+        const int g = tid + 256 * k;
+        pv[k] = g < a.nblk ? a.part_v[g] : 0;
+        pi[k] = g < a.nblk ? a.part_i[g] : -1;
+    }
+    const int p = *a.pos, plen = *a.plen;
+    const int q = p + 1;
+    i64 wp[3] = {0, 0, 0};
+    if (MODEL == 0 && q < a.npos) {
+#pragma unroll
+        for (int m = 0; m < 3; m++) wp[m] = a.wpe[(size_t)q * 768 + tid + 256 * m];
+    }
+    i64 bv = 0; int bi = -1;
+#pragma unroll
+    for (int k = 0; k < PER; k++)
+        if (race_beats<INV>(pv[k], pi[k], bv, bi)) { bv = pv[k]; bi = pi[k]; }
+    race1_finish<MODEL, INV>(a, bv, bi, p, plen, wp);
+}
+
+// The collapsing top read's second stage (base2_stream_fr.swift:12-14), batch 1 (GPT-2), one block: the grid's
+// best low T over the first stage's blocks; every candidate whose high reaches T survives (a word whose high is
+// below T is below the word that holds T, for sure); each survivor's 768 low bytes (w & 255, word by word) finish
+// its pile exactly, C + sum x (w & 255), and its score power(pile, (we + ex + 16) 65536 - LS) + b
+// (base2.py:114); the race among the survivors (largest, ties to the lowest word), then race1_finish.  The
+// threshold is the best low, not the 5th-best low the reference keeps for its top-5 report: the machine needs the
+// winner only.  Survivors past the LDS list (TOP_LIST) are finished one thread each (exact, slow: a model whose
+// bounds hold almost nothing).  The step's survivors are written out (count, and the first tmax: word, exact pile,
+// score).
+#define TOP_LIST 1024
+__global__ __launch_bounds__(256) void k_race_top(TopArgs t) {
+    const Race1Args& a = t.r;
+    __shared__ int x_s[768];
+    __shared__ int lj[TOP_LIST];
+    __shared__ i64 lc[TOP_LIST];
+    __shared__ i64 red_s[4];
+    __shared__ int ln_s;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    constexpr int PER = 2;                              // first-stage blocks a thread reads (nblk <= 512)
+    i64 bl[PER];
+    int nc[PER];
+#pragma unroll
+    for (int k = 0; k < PER; k++) {
+        const int g = tid + 256 * k;
+        bl[k] = g < a.nblk ? a.part_v[g] : INT64_MIN;
+        nc[k] = g < a.nblk ? a.part_i[g] : 0;
+    }
+#pragma unroll
+    for (int m = 0; m < 3; m++) x_s[tid + 256 * m] = t.tx[tid + 256 * m];
+    const i64 ex = t.tf[0], ls = t.tf[1], e2 = t.tf[2];
+    const int p = *a.pos, plen = *a.plen;
+    const int q = p + 1;
+    i64 wp[3] = {0, 0, 0};
+    if (q < a.npos) {
+#pragma unroll
+        for (int m = 0; m < 3; m++) wp[m] = a.wpe[(size_t)q * 768 + tid + 256 * m];
+    }
+    if (tid == 0) ln_s = 0;
+    i64 T = wave_reduce64(max(bl[0], bl[1]), OpMax());
+    if (lane == 0) red_s[wave] = T;
+    __syncthreads();
+    T = max(max(red_s[0], red_s[1]), max(red_s[2], red_s[3]));
+    // the survivors, into the list
+#pragma unroll
+    for (int k = 0; k < PER; k++) {
+        const size_t o = (size_t)(tid + 256 * k) * t.cap;
+        for (int c = 0; c < nc[k]; c++) {
+            if (t.cand_h[o + c] >= T) {
+                const int n = atomicAdd(&ln_s, 1);
+                if (n < TOP_LIST) { lj[n] = t.cand_j[o + c]; lc[n] = t.cand_c[o + c]; }
+            }
+        }
+    }
+    __syncthreads();
+    const int ns = ln_s;
+    const i64 fe = wsub(0, ls) & 0xFFFF;
+    auto score = [&](int j, i64 pile) {
+        return wadd(power_e(pile, wsub(wmul((i64)t.we[j] + ex + 16, 65536), ls), fe, e2, t.tb), t.bias[j]);
+    };
+    i64 bv = 0;
+    int bi = -1;
+    if (ns <= TOP_LIST) {
+        for (int s = wave; s < ns; s += 4) {              // a wave a survivor: lane l its bytes 12 l .. 12 l + 11
+            const int j = lj[s];
+            const unsigned* lb = reinterpret_cast<const unsigned*>(t.lo + (size_t)j * 768 + 12 * lane);
+            const unsigned d[3] = {lb[0], lb[1], lb[2]};
+            int acc = 0;
+#pragma unroll
+            for (int b = 0; b < 12; b++) acc += x_s[12 * lane + b] * (int)((d[b >> 2] >> (8 * (b & 3))) & 255u);
+            const i64 pile = wadd(lc[s], wave_reduce64((i64)acc, OpAdd()));
+            const i64 y = score(j, pile);
+            if (lane == 0) {
+                if (race_beats<0>(y, j, bv, bi)) { bv = y; bi = j; }
+                if (s < t.tmax) { t.tw[s] = j; t.tpile[s] = pile; t.tscore[s] = y; }
+            }
+        }
+    } else {
+#pragma unroll
+        for (int k = 0; k < PER; k++) {
+            const size_t o = (size_t)(tid + 256 * k) * t.cap;
+            for (int c = 0; c < nc[k]; c++) {
+                if (t.cand_h[o + c] >= T) {
+                    const int j = t.cand_j[o + c];
+                    const unsigned char* lb = t.lo + (size_t)j * 768;
+                    i64 sum = 0;
+                    for (int i = 0; i < 768; i++) sum += (i64)x_s[i] * lb[i];
+                    const i64 y = score(j, wadd(t.cand_c[o + c], sum));
+                    if (race_beats<0>(y, j, bv, bi)) { bv = y; bi = j; }
+                }
+            }
+        }
+    }
+    if (tid == 0) *t.tn = ns;
+    race1_finish<0, 0>(a, bv, bi, p, plen, wp);
 }
 
 // Batch 1: the entering row of the current position (the first step of a run; later steps' rows come from the race)
@@ -508,7 +790,20 @@ SMD i64 dot16_mask(const v4i (&q)[4], unsigned mb) {
 // (base2.py:93-99 / pythia_base2.py:129-141).  q_s, w_s: 64 ints of LDS each.
 // Returns lane's output dimension; store: this wave writes the new key and value into the cache and reports
 // errors.
-template <int MODEL>
+// The turn of one lane's value (foundation0/pythia_base2.py:116-123): dimension i < rot/2 pairs with i + rot/2;
+// x' = x c - x_partner s (lower half) or x c + x_partner s (upper half).  Integer: rshift(., 30) with cos and sin
+// at 2^-30; FTURN (turn=float, :117-119): round(.) in float64 with the float64 tables.
+template <int FTURN>
+SMD i64 turn1(i64 x, i64 partner, bool lower, i64 ci, i64 si, double cf, double sf) {
+    if constexpr (FTURN) {
+        const double xd = (double)x, pd = (double)partner;
+        return (i64)rint(lower ? xd * cf - pd * sf : xd * cf + pd * sf);
+    } else {
+        return lower ? rsh(wsub(wmul(x, ci), wmul(partner, si)), 30) : rsh(wadd(wmul(x, ci), wmul(partner, si)), 30);
+    }
+}
+
+template <int MODEL, int FTURN = 0>
 SMD i64 attend_short(const AttArgs& a, int p, int h, int b, int* q_s, int* w_s, i64 qv, i64 kv, const i64 vv, bool store) {
     const int lane = threadIdx.x & 63;
     const size_t hb = ((size_t)b * 12 + h) * a.ctx;         // this (stream, head)'s cache rows
@@ -519,11 +814,16 @@ SMD i64 attend_short(const AttArgs& a, int p, int h, int b, int* q_s, int* w_s, 
     // (the new q, k, v were requested by the caller before the position was read; the cached rows follow)
     // Pythia: the turn's cos and sin for dimension lane, ahead of the cached rows (lanes past rot read zeros)
     int tcos = 0, tsin = 0;
+    double fcos = 0.0, fsin = 0.0;
     if constexpr (MODEL == 1) {
         const int r = a.rot >> 1, ti = lane < r ? lane : lane - r;
-        const unsigned lim = (unsigned)((p + 1) * r) * 4u, off = (unsigned)(p * r + ti) * 4u;
-        tcos = buf_load1(buf_rsrc(a.cosT, lim), off);
-        tsin = buf_load1(buf_rsrc(a.sinT, lim), off);
+        if constexpr (FTURN) {
+            if (lane < a.rot) { fcos = a.cosF[(size_t)p * r + ti]; fsin = a.sinF[(size_t)p * r + ti]; }
+        } else {
+            const unsigned lim = (unsigned)((p + 1) * r) * 4u, off = (unsigned)(p * r + ti) * 4u;
+            tcos = buf_load1(buf_rsrc(a.cosT, lim), off);
+            tsin = buf_load1(buf_rsrc(a.sinT, lim), off);
+        }
     }
     // the cached rows s < p (lanes and columns past p read zeros without a memory request)
     const __amdgpu_buffer_rsrc_t rk = buf_rsrc(K16, (unsigned)p * 128), re = buf_rsrc(EK, (unsigned)p * 4),
@@ -542,10 +842,9 @@ SMD i64 attend_short(const AttArgs& a, int p, int h, int b, int* q_s, int* w_s, 
         const i64 pq = __shfl(qv, lane < r ? lane + r : lane - r, 64);
         const i64 pk = __shfl(kv, lane < r ? lane + r : lane - r, 64);
         if (lane < a.rot) {
-            if (store && (iabs64(qv) >= ((i64)1 << 31) || iabs64(kv) >= ((i64)1 << 31))) atomicOr(a.err, SM_ERR_RANGE);
-            const i64 c = tcos, sn = tsin;
-            qv = lane < r ? rsh(wsub(wmul(qv, c), wmul(pq, sn)), 30) : rsh(wadd(wmul(qv, c), wmul(pq, sn)), 30);
-            kv = lane < r ? rsh(wsub(wmul(kv, c), wmul(pk, sn)), 30) : rsh(wadd(wmul(kv, c), wmul(pk, sn)), 30);
+            if (!FTURN && store && (iabs64(qv) >= ((i64)1 << 31) || iabs64(kv) >= ((i64)1 << 31))) atomicOr(a.err, SM_ERR_RANGE);
+            qv = turn1<FTURN>(qv, pq, lane < r, tcos, tsin, fcos, fsin);
+            kv = turn1<FTURN>(kv, pk, lane < r, tcos, tsin, fcos, fsin);
         }
     }
     // the water levels of q and k (base2.py:93)
@@ -637,8 +936,10 @@ template <bool B> struct Flag { static constexpr bool value = B; };
 // ONE = 1: one stream (the short-context path is available, full registers); ONE = 0: many streams, three waves
 // a SIMD so that 768 blocks are resident at once
 // REC = 0: nothing is recorded (no record position is read)
-template <int MODEL, int ONE, int REC>
+// FTURN = 1 (one stream, Pythia): turn=float
+template <int MODEL, int ONE, int REC, int FTURN = 0>
 __global__ __launch_bounds__(NTHR, ONE ? 1 : 3) void k_attend(AttArgs a) {
+    static_assert(!FTURN || (MODEL == 1 && ONE), "turn=float is the one-stream Pythia machine's");
     extern __shared__ __align__(16) unsigned char smem[];
     i64* sc = reinterpret_cast<i64*>(smem);                  // [ctx] scores
     int* arr = reinterpret_cast<int*>(sc + a.ctx);           // [ctx] arrivals
@@ -668,7 +969,7 @@ __global__ __launch_bounds__(NTHR, ONE ? 1 : 3) void k_attend(AttArgs a) {
     if constexpr (ONE) {
         if (p < 64) {                                        // one stream, short context: one wave, no barriers
             if (wave == 0) {
-                const i64 o = attend_short<MODEL>(a, p, h, b, q16s, vs, xnew, xk1, xv1, true);
+                const i64 o = attend_short<MODEL, FTURN>(a, p, h, b, q16s, vs, xnew, xk1, xv1, true);
                 a.out[(size_t)b * 768 + h * 64 + lane] = o;
                 if (a.out_or) {
                     const i64 w = wave_or64(iabs64(o));
@@ -689,11 +990,16 @@ __global__ __launch_bounds__(NTHR, ONE ? 1 : 3) void k_attend(AttArgs a) {
     // Pythia: the turn's cos and sin of dimension lane (lanes < rot) with the new position, ahead of the keys, so
     // that the turn waits for them alone (row p of the [npos][rot / 2] tables; other lanes read past it: zeros)
     int tcos = 0, tsin = 0;
+    double fcos = 0.0, fsin = 0.0;
     if constexpr (MODEL == 1) {
         const int r = a.rot >> 1, ti = lane < r ? lane : lane - r;
-        const unsigned lim = (unsigned)((p + 1) * r) * 4u, off = (unsigned)(p * r + ti) * 4u;
-        tcos = buf_load1(buf_rsrc(a.cosT, lim), off);
-        tsin = buf_load1(buf_rsrc(a.sinT, lim), off);
+        if constexpr (FTURN) {
+            if (wave < 2 && lane < a.rot) { fcos = a.cosF[(size_t)p * r + ti]; fsin = a.sinF[(size_t)p * r + ti]; }
+        } else {
+            const unsigned lim = (unsigned)((p + 1) * r) * 4u, off = (unsigned)(p * r + ti) * 4u;
+            tcos = buf_load1(buf_rsrc(a.cosT, lim), off);
+            tsin = buf_load1(buf_rsrc(a.sinT, lim), off);
+        }
     }
     // (buffer loads bounded at position p: rows past it read zeros and cost no memory traffic)
     const __amdgpu_buffer_rsrc_t rk = buf_rsrc(K16, (unsigned)p * 128), re = buf_rsrc(EK, (unsigned)p * 4),
@@ -716,9 +1022,8 @@ __global__ __launch_bounds__(NTHR, ONE ? 1 : 3) void k_attend(AttArgs a) {
         const int r = a.rot >> 1;
         const i64 partner = __shfl(xnew, lane < r ? lane + r : lane - r, 64);
         if (lane < a.rot) {
-            if (iabs64(xnew) >= ((i64)1 << 31)) atomicOr(a.err, SM_ERR_RANGE);
-            const i64 c = tcos, sn = tsin;
-            xnew = lane < r ? rsh(wsub(wmul(xnew, c), wmul(partner, sn)), 30) : rsh(wadd(wmul(xnew, c), wmul(partner, sn)), 30);
+            if (!FTURN && iabs64(xnew) >= ((i64)1 << 31)) atomicOr(a.err, SM_ERR_RANGE);
+            xnew = turn1<FTURN>(xnew, partner, lane < r, tcos, tsin, fcos, fsin);
         }
     }
     // the new position's own key and value are used from LDS: this block never reads back what it wrote
@@ -880,6 +1185,93 @@ __global__ __launch_bounds__(NTHR, ONE ? 1 : 3) void k_attend(AttArgs a) {
             if (lane == 0) a.out_or[(size_t)b * 12 + h] = w;
         }
         if (rec) a.ratt[h * 64 + lane] = o;
+    }
+}
+
+// arrival=float (base2.py:89-92; foundation0/pythia_base2.py:131-134), one stream, one block per head: scores
+// (q 2^-16) . (k 2^-16) / 8 in float64 against every cached key (held as float64 in KF: its raw gauged value),
+// their exponentials after the row's maximum, each over their sum, out = round(sum a v).  Pythia's q and k are
+// turned first (the integer turn, or FTURN).  The additions inside the dot products and sums run in this
+// kernel's own order (numpy's follow its BLAS): the float arrival is compared at the word level.
+// Dynamic LDS: ctx doubles.
+template <int MODEL, int FTURN, int REC>
+__global__ __launch_bounds__(256) void k_attend_f(AttArgs a) {
+    extern __shared__ __align__(16) unsigned char smem[];
+    double* e_s = reinterpret_cast<double*>(smem);          // [ctx] scores, then their exponentials
+    __shared__ double q_s[64], k_s[64];
+    __shared__ int v_s[64];
+    __shared__ double red[4];
+    __shared__ double acc[4][64];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, h = blockIdx.x;
+    const int p = *a.pos;
+    const size_t hb = (size_t)h * a.ctx;                     // stream 0's rows of head h
+    double* KF = a.KF + hb * 64;
+    int* V = a.V + hb * 64;
+    if (wave == 0) {
+        auto at = [&](int part) { return MODEL == 1 ? h * 192 + part * 64 + lane : part * 768 + h * 64 + lane; };
+        i64 q = a.QKV[at(0)], k = a.QKV[at(1)];
+        const i64 v = a.QKV[at(2)];
+        if constexpr (MODEL == 1) {
+            const int r = a.rot >> 1, ti = lane < r ? lane : lane - r;
+            const i64 pq = __shfl(q, lane < r ? lane + r : lane - r, 64);
+            const i64 pk = __shfl(k, lane < r ? lane + r : lane - r, 64);
+            if (lane < a.rot) {
+                if (!FTURN && (iabs64(q) >= ((i64)1 << 31) || iabs64(k) >= ((i64)1 << 31))) atomicOr(a.err, SM_ERR_RANGE);
+                const size_t t = (size_t)p * r + ti;
+                const i64 ci = FTURN ? 0 : a.cosT[t], si = FTURN ? 0 : a.sinT[t];
+                const double cf = FTURN ? a.cosF[t] : 0.0, sf = FTURN ? a.sinF[t] : 0.0;
+                q = turn1<FTURN>(q, pq, lane < r, ci, si, cf, sf);
+                k = turn1<FTURN>(k, pk, lane < r, ci, si, cf, sf);
+            }
+        }
+        q_s[lane] = (double)q * (1.0 / 65536.0);
+        k_s[lane] = (double)k;
+        v_s[lane] = (int)v;
+        KF[(size_t)p * 64 + lane] = (double)k;
+        if (v < (i64)INT32_MIN || v > (i64)INT32_MAX) atomicOr(a.err, SM_ERR_V32);
+        V[(size_t)p * 64 + lane] = (int)v;
+    }
+    __syncthreads();
+    // the scores (thread t: positions t, t + 256, ..; the new one from LDS) and their maximum
+    double mx = -INFINITY;
+    for (int j = tid; j <= p; j += 256) {
+        const double* kr = j == p ? k_s : KF + (size_t)j * 64;
+        double sc = 0.0;
+        for (int d = 0; d < 64; d++) sc += q_s[d] * (kr[d] * (1.0 / 65536.0));
+        sc = sc / 8.0;
+        e_s[j] = sc;
+        mx = fmax(mx, sc);
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) mx = fmax(mx, __shfl_xor(mx, o, 64));
+    if (lane == 0) red[wave] = mx;
+    __syncthreads();
+    mx = fmax(fmax(red[0], red[1]), fmax(red[2], red[3]));
+    __syncthreads();
+    // the exponentials and their sum
+    double z = 0.0;
+    for (int j = tid; j <= p; j += 256) {
+        const double e = exp(e_s[j] - mx);
+        e_s[j] = e;
+        z += e;
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) z += __shfl_xor(z, o, 64);
+    if (lane == 0) red[wave] = z;
+    __syncthreads();
+    z = (red[0] + red[1]) + (red[2] + red[3]);
+    // out = sum over positions of (e / z) v: wave w takes positions w, w + 4, ..; lane = dimension
+    double o = 0.0;
+    for (int j = wave; j <= p; j += 4) {
+        const int vj = j == p ? v_s[lane] : V[(size_t)j * 64 + lane];
+        o += e_s[j] / z * (double)vj;
+    }
+    acc[wave][lane] = o;
+    __syncthreads();
+    if (wave == 0) {
+        const i64 r = (i64)rint((acc[0][lane] + acc[1][lane]) + (acc[2][lane] + acc[3][lane]));
+        a.out[h * 64 + lane] = r;
+        if (REC && a.rec_pos && *a.rec_pos == p) a.ratt[h * 64 + lane] = r;
     }
 }
 

@@ -169,6 +169,25 @@ static int upload_plate(DevPlate& P, const int16_t* w, const int32_t* e, const i
     return SM_OK;
 }
 
+// the top read's high-byte plane in column tiles of tc: unit u of tile t holds inputs 16 (u / tc) .. + 16 of
+// column t tc + u % tc, each as w >> 8 (padding columns zero); and its low bytes w & 255, word by word
+static std::vector<int8_t> tile_hi_plane(const int16_t* w, int nin, int nout, int tc) {
+    const int ntiles = (nout + tc - 1) / tc;
+    std::vector<int8_t> t((size_t)ntiles * tc * nin, 0);
+    for (int k = 0; k < nin; k++) {
+        const int16_t* row = w + (size_t)k * nout;
+        const size_t kb = (size_t)(k / 16) * tc * 16 + (k % 16);
+        for (int j = 0; j < nout; j++) t[(size_t)(j / tc) * tc * nin + kb + (size_t)(j % tc) * 16] = (int8_t)(row[j] >> 8);
+    }
+    return t;
+}
+static std::vector<uint8_t> lo_plane(const int16_t* w, int nin, int nout) {
+    std::vector<uint8_t> t((size_t)nout * nin);
+    for (int k = 0; k < nin; k++)
+        for (int j = 0; j < nout; j++) t[(size_t)j * nin + k] = (uint8_t)(w[(size_t)k * nout + j] & 255);
+    return t;
+}
+
 static void free_plate(DevPlate& P) {
     hfree(P.W); hfree(P.e); hfree(P.b); hfree(P.sw);
     P = DevPlate();
@@ -313,6 +332,17 @@ struct sm_machine {
     short* ew = nullptr;  int* ee = nullptr;
     int* cosT = nullptr;  int* sinT = nullptr;  int rot = 0;
     i64 half = 0, ehalf = 0;
+    // batch 1: k_gemv's MODE bits (the complement machine, the float gauge and edge), the float turn and arrival
+    int mode = 0;
+    bool fturn = false, farr = false;
+    double *cosF = nullptr, *sinF = nullptr;            // turn=float: [npos][rot / 2]
+    double* KF = nullptr;                               // arrival=float: [L][12 heads][ctx][64] keys as float64
+    // the collapsing top read (batch 1): planes, the first stage's candidates, the light, the step's survivors
+    int8_t* top_hi = nullptr;                           // high bytes in the head's column tiles
+    uint8_t* top_lo = nullptr;                          // [vocab][768] low bytes, word by word
+    int* cand_j = nullptr; i64* cand_h = nullptr; i64* cand_c = nullptr;   // [head_grid][TOP_CAP]
+    int* top_x = nullptr; i64* top_f = nullptr;         // [768], [4]
+    int* top_n = nullptr; int* top_w = nullptr; i64* top_pile = nullptr; i64* top_score = nullptr;   // [1], [1024] x3
     sm_tables T;
     // state
     i64 *R = nullptr, *QKV = nullptr, *att = nullptr, *hid = nullptr;
@@ -443,7 +473,9 @@ static void machine_free(sm_machine* m) {
     void* ps[] = {m->pfmap, m->planes, m->part_acc, m->rowinfo, m->wte, m->wpe, m->R, m->R0, m->QKV, m->att, m->attor, m->hidor, m->sfacts, m->hid, m->K16, m->KM, m->EK, m->V, m->seq, m->words, m->ctl,
                   m->part_v, m->part_i, m->r_x16, m->r_exls, m->r_pile, m->r_qkv, m->r_att, m->r_hid, m->r_resid,
                   m->r_hx16, m->r_hexls, m->r_hpile, m->r_logits, m->r_gauge, m->r_fcpre, m->r_hgauge,
-                  m->fg, m->fb, m->ew, m->ee, m->cosT, m->sinT};
+                  m->fg, m->fb, m->ew, m->ee, m->cosT, m->sinT, m->cosF, m->sinF, m->KF,
+                  m->top_hi, m->top_lo, m->cand_j, m->cand_h, m->cand_c, m->top_x, m->top_f, m->top_n, m->top_w,
+                  m->top_pile, m->top_score};
     for (void* p : ps) hfree(p);
     for (int l = 0; l < 12; l++)
         for (int j = 0; j < 2; j++) { hfree(m->ng[l][j]); hfree(m->nb[l][j]); }
@@ -565,6 +597,7 @@ static int launch_step_batched(sm_machine* m, int parts, int nrows = 0,
 // SIMD, 256 VGPRs), at 512 blocks 19.2 us; 2-column tiles at 768 blocks 16.2 us)
 #define HEAD_WPB 4
 #define HEAD_TC 4
+#define TOP_RECORD 1024       // survivors of the top read's last step kept for sm_read
 
 // the race over the head's per-block bests, one block per stream; it also advances the position
 // batch 1: the race over the head blocks' bests, the word fed back, the next position's entering row (k_race1);
@@ -590,24 +623,48 @@ static void launch_embed1(sm_machine* m) {
     else launch(m->cfg.profile, "embed", k_embed1<0>, dim3(1), dim3(256), 0, m->st, race1_args(m));
 }
 
-// a batch-1 GEMV phase: rec selects the instantiation that records (launched only for the recorded step); the
-// complement machine (GPT-2's phases only) its INV = 1 instantiations
+// a batch-1 GEMV phase: rec selects the instantiation that records (launched only for the recorded step), the
+// machine's MODE bits the rest (only those the phase has; the complement machine is never mixed with float stages)
+static constexpr int phase_modes(int PRO, int EPI) {
+    return (PRO == PRO_GAUGE || PRO == PRO_TO16 ? MODE_INV : 0) | (PRO == PRO_GAUGE || PRO == PRO_PGAUGE ? MODE_FGAUGE : 0) |
+           (EPI == EPI_GAUGED_EDGE || EPI == EPI_PLAIN_EDGE ? MODE_FEDGE : 0);
+}
+template <int NIN, int TC, int WPB, int PRO, int EPI, int M = 0>
+static void gemv_mode(sm_machine* m, int mode, bool rec, const char* name, int grid, const GemvArgs& a) {
+    if constexpr (M < 8) {
+        if constexpr ((M & ~phase_modes(PRO, EPI)) == 0 && (M == MODE_INV || !(M & MODE_INV))) {
+            if (mode == M) {
+                if (rec) launch(m->cfg.profile, name, k_gemv<NIN, TC, WPB, PRO, EPI, 1, M>, dim3(grid), dim3(64 * WPB), 0, m->st, a);
+                else launch(m->cfg.profile, name, k_gemv<NIN, TC, WPB, PRO, EPI, 0, M>, dim3(grid), dim3(64 * WPB), 0, m->st, a);
+                return;
+            }
+        }
+        gemv_mode<NIN, TC, WPB, PRO, EPI, M + 1>(m, mode, rec, name, grid, a);
+    }
+}
 template <int NIN, int TC, int WPB, int PRO, int EPI>
 static void gemv(sm_machine* m, bool rec, const char* name, int grid, const GemvArgs& a) {
-    if constexpr (PRO == PRO_GAUGE || PRO == PRO_TO16) {
-        if (m->cfg.inv) {
-            if (rec) launch(m->cfg.profile, name, k_gemv<NIN, TC, WPB, PRO, EPI, 1, 1>, dim3(grid), dim3(64 * WPB), 0, m->st, a);
-            else launch(m->cfg.profile, name, k_gemv<NIN, TC, WPB, PRO, EPI, 0, 1>, dim3(grid), dim3(64 * WPB), 0, m->st, a);
-            return;
-        }
+    gemv_mode<NIN, TC, WPB, PRO, EPI>(m, m->mode & phase_modes(PRO, EPI), rec, name, grid, a);
+}
+// batch-1 attention: the integer arrival (turn=float: its FTURN instantiation), or arrival=float
+template <int MODEL, int FTURN>
+static void attend1_t(sm_machine* m, bool rec, const AttArgs& a) {
+    if (m->farr) {
+        if (rec) launch(m->cfg.profile, "attend", k_attend_f<MODEL, FTURN, 1>, dim3(12), dim3(256), (size_t)m->ctx * 8, m->st, a);
+        else launch(m->cfg.profile, "attend", k_attend_f<MODEL, FTURN, 0>, dim3(12), dim3(256), (size_t)m->ctx * 8, m->st, a);
+        return;
     }
-    if (rec) launch(m->cfg.profile, name, k_gemv<NIN, TC, WPB, PRO, EPI, 1>, dim3(grid), dim3(64 * WPB), 0, m->st, a);
-    else launch(m->cfg.profile, name, k_gemv<NIN, TC, WPB, PRO, EPI, 0>, dim3(grid), dim3(64 * WPB), 0, m->st, a);
+    if (rec) launch(m->cfg.profile, "attend", k_attend<MODEL, 1, 1, FTURN>, dim3(12, 1), dim3(NTHR), (size_t)m->ctx * 12, m->st, a);
+    else launch(m->cfg.profile, "attend", k_attend<MODEL, 1, 0, FTURN>, dim3(12, 1), dim3(NTHR), (size_t)m->ctx * 12, m->st, a);
 }
 template <int MODEL>
-static void attend1(sm_machine* m, bool rec, const AttArgs& a) {
-    if (rec) launch(m->cfg.profile, "attend", k_attend<MODEL, 1, 1>, dim3(12, 1), dim3(NTHR), (size_t)m->ctx * 12, m->st, a);
-    else launch(m->cfg.profile, "attend", k_attend<MODEL, 1, 0>, dim3(12, 1), dim3(NTHR), (size_t)m->ctx * 12, m->st, a);
+static void attend1(sm_machine* m, bool rec, AttArgs a, int layer) {
+    a.cosF = m->cosF; a.sinF = m->sinF;
+    a.KF = m->KF ? m->KF + (size_t)layer * 12 * m->ctx * 64 : nullptr;
+    if constexpr (MODEL == 1) {
+        if (m->fturn) { attend1_t<1, 1>(m, rec, a); return; }
+    }
+    attend1_t<MODEL, 0>(m, rec, a);
 }
 
 // The Pythia machine at batch 1 (foundation0/pythia_base2.py:153-160), five phases a layer.  Both gauges read
@@ -658,7 +715,7 @@ static int launch_step_pythia(sm_machine* m, int parts, bool rec) {
             const DevPlate& P = m->bank[l][1];
             plate(g, P, 1);
             g.X = m->att; g.Y = m->R; g.Yb = Rin; g.rout = m->r_resid + (l * 2 + 0) * 768;
-            attend1<1>(m, rec, a);
+            attend1<1>(m, rec, a, l);
             gemv<768, 2, 2, PRO_TO16, EPI_PLAIN_ADD>(m, rec, "proj", (P.ntiles + 1) / 2, g);
         }
         // mproj: plain of the edge row, added to R (Mo)
@@ -857,7 +914,7 @@ static int launch_step(sm_machine* m, int parts = STEP_ALL, bool rec = false) {
             g.X = m->att; g.Y = m->R; g.Yb = Rin;
             g.rx16 = m->r_x16 + (l * 4 + 1) * 3072; g.rexls = m->r_exls + (l * 4 + 1) * 2;
             g.rpile = m->r_pile + (l * 4 + 1) * 3072; g.rout = m->r_resid + (l * 2 + 0) * 768;
-            attend1<0>(m, rec, a);
+            attend1<0>(m, rec, a, l);
             gemv<768, 2, 2, PRO_TO16, EPI_PLAIN_ADD>(m, rec, "proj", (P.ntiles + 1) / 2, g);
         }
         // fc: gauge, product, gauged, edge (base2.py:106)
@@ -891,8 +948,24 @@ static int launch_step(sm_machine* m, int parts = STEP_ALL, bool rec = false) {
         a.X = m->R;
         a.rx16 = m->r_hx16; a.rexls = m->r_hexls; a.rpile = m->r_hpile; a.rlogits = m->r_logits;
         a.part_v = m->part_v; a.part_i = m->part_i;      // each block's best; the race runs in k_race1
-        gemv<768, HEAD_TC, HEAD_WPB, PRO_GAUGE, EPI_HEAD>(m, rec, "head", m->head_grid, a);
-        launch_race1(m);
+        if (m->cfg.top_read && !rec) {
+            // the collapsing top read: the high-byte plane with each word's bounds, then the survivors' low
+            // bytes and the race (a recorded step reads the full table, so that every logit is recorded)
+            a.W = reinterpret_cast<const int4*>(m->top_hi);
+            a.cand_j = m->cand_j; a.cand_h = m->cand_h; a.cand_c = m->cand_c; a.tx = m->top_x; a.tf = m->top_f;
+            launch(m->cfg.profile, "head.top", k_gemv<768, HEAD_TC, HEAD_WPB, PRO_GAUGE, EPI_TOP1, 0, 0>, dim3(m->head_grid),
+                   dim3(64 * HEAD_WPB), 0, m->st, a);
+            TopArgs t{};
+            t.r = race1_args(m);
+            t.cap = HEAD_WPB * TOP_ITERS * HEAD_TC;
+            t.cand_j = m->cand_j; t.cand_h = m->cand_h; t.cand_c = m->cand_c; t.tx = m->top_x; t.tf = m->top_f;
+            t.lo = m->top_lo; t.we = P.e; t.bias = P.b; t.tb = tb;
+            t.tn = m->top_n; t.tw = m->top_w; t.tpile = m->top_pile; t.tscore = m->top_score; t.tmax = TOP_RECORD;
+            launch(m->cfg.profile, "race.top", k_race_top, dim3(1), dim3(256), 0, m->st, t);
+        } else {
+            gemv<768, HEAD_TC, HEAD_WPB, PRO_GAUGE, EPI_HEAD>(m, rec, "head", m->head_grid, a);
+            launch_race1(m);
+        }
     }
     HIP_TRY(hipGetLastError());
     return SM_OK;
@@ -932,7 +1005,7 @@ static int run_prefill(sm_machine* m, int npos) {
 extern "C" int sm_create(const char* layout_dir, const sm_config* cfg, sm_machine** out) {
     if (!layout_dir || !out) return fail(SM_E_ARG, "sm_create: null argument");
     *out = nullptr;
-    sm_config c{1, 1024, 1, 0, 16, 0, 0, 64, 0};
+    sm_config c{1, 1024, 1, 0, 16, 0, 0, 64, 0, 0, 0};
     if (cfg) c = *cfg;
     if (c.max_streams < 1 || c.max_streams > 64) return fail(SM_E_ARG, "sm_create: max_streams must be in [1, 64]");
     if (c.prefill_rows < 0 || c.prefill_rows > 64) return fail(SM_E_ARG, "sm_create: prefill_rows must be in [0, 64]");
@@ -956,6 +1029,13 @@ extern "C" int sm_create(const char* layout_dir, const sm_config* cfg, sm_machin
     }
     if (c.inv && (py || c.max_streams != 1 || c.prefill_rows != 0))
         return fail(SM_E_ARG, "sm_create: the complement machine (inv) runs GPT-2 with max_streams 1 and prefill_rows 0");
+    if (c.float_stages & ~(SM_FLOAT_GAUGE | SM_FLOAT_EDGE | SM_FLOAT_ARRIVAL | SM_FLOAT_TURN))
+        return fail(SM_E_ARG, "sm_create: unknown float_stages bits");
+    if (c.float_stages && (c.max_streams != 1 || c.prefill_rows != 0 || c.inv))
+        return fail(SM_E_ARG, "sm_create: the float stages run with max_streams 1 and prefill_rows 0, without inv");
+    if ((c.float_stages & SM_FLOAT_TURN) && !py) return fail(SM_E_ARG, "sm_create: turn=float is the Pythia machine's");
+    if (c.top_read && (py || c.max_streams != 1 || c.inv || c.float_stages))
+        return fail(SM_E_ARG, "sm_create: the collapsing top read runs GPT-2 with max_streams 1, without inv or float stages");
     auto find = [&](const std::string& n) -> const BankInfo* {
         for (auto& b : banks) if (b.name == n) return &b;
         return nullptr;
@@ -965,6 +1045,10 @@ extern "C" int sm_create(const char* layout_dir, const sm_config* cfg, sm_machin
     m->B = c.max_streams;
     m->RC = std::max(m->B, c.prefill_rows);
     m->kind = py ? 1 : 0;
+    m->mode = (c.inv ? MODE_INV : 0) | (c.float_stages & SM_FLOAT_GAUGE ? MODE_FGAUGE : 0) |
+              (c.float_stages & SM_FLOAT_EDGE ? MODE_FEDGE : 0);
+    m->fturn = c.float_stages & SM_FLOAT_TURN;
+    m->farr = c.float_stages & SM_FLOAT_ARRIVAL;
     const bool mfma = m->B > 1 || c.prefill_rows > 0;     // the MFMA banks: batched streams or prompt passes
 
     auto bail = [&](int code) { machine_free(m); return code; };
@@ -996,6 +1080,14 @@ extern "C" int sm_create(const char* layout_dir, const sm_config* cfg, sm_machin
         if (py) b.assign(m->vocab, 0);         // Pythia's head has no bias (foundation0/pythia_base2.py:159)
         else if ((rc = read_array(dir + "head.b", b, m->vocab))) return bail(rc);
         if (m->B == 1 && (rc = upload_plate(m->head, w.data(), e.data(), b.data(), 768, m->vocab, HEAD_TC, c.inv))) return bail(rc);
+        if (c.top_read) {
+            const std::vector<int8_t> hi = tile_hi_plane(w.data(), 768, m->vocab, HEAD_TC);
+            const std::vector<uint8_t> lo = lo_plane(w.data(), 768, m->vocab);
+            if ((rc = dalloc(&m->top_hi, hi.size())) || (rc = dalloc(&m->top_lo, lo.size()))) return bail(rc);
+            if (hipMemcpy(m->top_hi, hi.data(), hi.size(), hipMemcpyHostToDevice) != hipSuccess ||
+                hipMemcpy(m->top_lo, lo.data(), lo.size(), hipMemcpyHostToDevice) != hipSuccess)
+                return bail(fail(SM_E_HIP, "upload the top read's planes"));
+        }
         if (m->B > 1 && (rc = upload_mfma_plate(m->mhead, w.data(), e.data(), b.data(), 768, m->vocab))) return bail(rc);
     }
     // word and position tables
@@ -1023,6 +1115,15 @@ extern "C" int sm_create(const char* layout_dir, const sm_config* cfg, sm_machin
             hipMemcpy(m->sinT, s32.data(), s32.size() * 4, hipMemcpyHostToDevice) != hipSuccess)
             return bail(fail(SM_E_HIP, "upload embed / turns"));
         m->rot = (int)rot;
+        if (m->fturn) {        // turn=float: the float64 cos and sin the layout wrote with numpy
+            std::vector<double> cf, sf;
+            if ((rc = read_array(dir + "cosf.bin", cf, cs.size())) || (rc = read_array(dir + "sinf.bin", sf, cs.size())))
+                return bail(rc);
+            if ((rc = dalloc(&m->cosF, cf.size())) || (rc = dalloc(&m->sinF, sf.size()))) return bail(rc);
+            if (hipMemcpy(m->cosF, cf.data(), cf.size() * 8, hipMemcpyHostToDevice) != hipSuccess ||
+                hipMemcpy(m->sinF, sf.data(), sf.size() * 8, hipMemcpyHostToDevice) != hipSuccess)
+                return bail(fail(SM_E_HIP, "upload cosf / sinf"));
+        }
         m->half = half;
         // the norms: gain on 16 places, offset at 2^-16, one power of two each
         auto norm = [&](const std::string& name, int*& g, i64*& b, int& ge) -> int {
@@ -1068,6 +1169,18 @@ extern "C" int sm_create(const char* layout_dir, const sm_config* cfg, sm_machin
     m->ctx = c.max_ctx < m->npos ? c.max_ctx : m->npos;
     m->head_grid = c.head_grid > 0 ? c.head_grid : 512;     // two blocks per CU (measured best)
     if (m->head_grid > 1024) return bail(fail(SM_E_ARG, "sm_create: head_grid at most 1024"));
+    if (c.top_read) {      // every wave finishes at most TOP_ITERS tiles; the race reads at most 512 blocks
+        const long long nt = (m->vocab + HEAD_TC - 1) / HEAD_TC;
+        if (m->head_grid > 512 || (long long)m->head_grid * HEAD_WPB * TOP_ITERS < nt)
+            return bail(fail(SM_E_ARG, "sm_create: the top read needs head_grid in [" +
+                                           std::to_string((nt + HEAD_WPB * TOP_ITERS - 1) / (HEAD_WPB * TOP_ITERS)) + ", 512]"));
+        const size_t cap = (size_t)HEAD_WPB * TOP_ITERS * HEAD_TC, g = m->head_grid;
+        if ((rc = dalloc(&m->cand_j, g * cap)) || (rc = dalloc(&m->cand_h, g * cap)) || (rc = dalloc(&m->cand_c, g * cap)) ||
+            (rc = dalloc(&m->top_x, (size_t)768)) || (rc = dalloc(&m->top_f, (size_t)4)) || (rc = dalloc(&m->top_n, (size_t)1)) ||
+            (rc = dalloc(&m->top_w, (size_t)TOP_RECORD)) || (rc = dalloc(&m->top_pile, (size_t)TOP_RECORD)) ||
+            (rc = dalloc(&m->top_score, (size_t)TOP_RECORD)))
+            return bail(rc);
+    }
     const size_t nparts = m->B == 1 ? (size_t)m->head_grid : (size_t)m->B * head_rows_grid((m->vocab + 15) / 16);
     // state
     const size_t B = m->B, ctx = m->ctx, RC = m->RC;
@@ -1077,7 +1190,7 @@ extern "C" int sm_create(const char* layout_dir, const sm_config* cfg, sm_machin
         (rc = dalloc(&m->hid, RC * 3072)) || (rc = dalloc(&m->K16, 12 * B * ctx * 768)) || (rc = dalloc(&m->KM, 12 * B * ctx * 12)) ||
         (rc = dalloc(&m->EK, 12 * B * ctx * 12)) ||
         (rc = dalloc(&m->pfmap, B * ctx)) ||
-        (rc = dalloc(&m->V, 12 * B * ctx * 768)) || (rc = dalloc(&m->seq, B * (ctx + 1))) || (rc = dalloc(&m->words, B * (ctx + 1))) ||
+        (rc = dalloc(&m->V, 12 * B * ctx * 768)) || (m->farr && (rc = dalloc(&m->KF, 12 * ctx * 768))) || (rc = dalloc(&m->seq, B * (ctx + 1))) || (rc = dalloc(&m->words, B * (ctx + 1))) ||
         (rc = dalloc(&m->ctl, (size_t)CTL_N)) || (rc = dalloc(&m->part_v, nparts)) ||
         (rc = dalloc(&m->part_i, nparts)) || (rc = dalloc(&m->r_x16, (size_t)12 * 4 * 3072)) ||
         (rc = dalloc(&m->planes, (size_t)4 * 48 * 3 * 1024 * nsets)) || (rc = dalloc(&m->rowinfo, RC * 8 * nsets)) ||
@@ -1324,6 +1437,22 @@ extern "C" int sm_read(sm_machine* m, int32_t what, int32_t layer, int32_t strea
         case SM_READ_REC_GAUGE: src = m->r_gauge; need = 12 * 2 * 768 * 8; break;
         case SM_READ_REC_FCPRE: src = m->r_fcpre; need = 12 * 3072 * 8; break;
         case SM_READ_REC_HGAUGE: src = m->r_hgauge; need = 768 * 8; break;
+        case SM_READ_TOP: {
+            if (!m->top_n) return fail(SM_E_STATE, "sm_read: the machine has no top read");
+            if (bytes != (1 + 3 * TOP_RECORD) * 8) return fail(SM_E_ARG, "sm_read: expected " + std::to_string((1 + 3 * TOP_RECORD) * 8) + " bytes");
+            HIP_TRY(hipStreamSynchronize(m->st));
+            int n = 0;
+            std::vector<int> w(TOP_RECORD);
+            std::vector<i64> pl(TOP_RECORD), sc(TOP_RECORD);
+            HIP_TRY(hipMemcpy(&n, m->top_n, 4, hipMemcpyDeviceToHost));
+            HIP_TRY(hipMemcpy(w.data(), m->top_w, TOP_RECORD * 4, hipMemcpyDeviceToHost));
+            HIP_TRY(hipMemcpy(pl.data(), m->top_pile, TOP_RECORD * 8, hipMemcpyDeviceToHost));
+            HIP_TRY(hipMemcpy(sc.data(), m->top_score, TOP_RECORD * 8, hipMemcpyDeviceToHost));
+            i64* out = static_cast<i64*>(dst);
+            out[0] = n;
+            for (int k = 0; k < TOP_RECORD; k++) { out[1 + 3 * k] = w[k]; out[2 + 3 * k] = pl[k]; out[3 + 3 * k] = sc[k]; }
+            return SM_OK;
+        }
         default: return fail(SM_E_ARG, "sm_read: unknown array");
     }
     if (bytes != need) return fail(SM_E_ARG, "sm_read: expected " + std::to_string(need) + " bytes");

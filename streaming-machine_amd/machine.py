@@ -19,7 +19,7 @@ CODES = {SM_E_ARG: "SM_E_ARG", SM_E_IO: "SM_E_IO", SM_E_HIP: "SM_E_HIP", SM_E_OO
          SM_E_OVERFLOW: "SM_E_OVERFLOW", SM_E_STATE: "SM_E_STATE"}
 
 READ = dict(k16=1, ek=2, v=3, resid=4, seq=5, x16=10, exls=11, pile=12, qkv=13, att=14, hid=15, rresid=16,
-            hx16=17, hexls=18, hpile=19, logits=20, gauge=21, fcpre=22, hgauge=23)
+            hx16=17, hexls=18, hpile=19, logits=20, gauge=21, fcpre=22, hgauge=23, top=24)
 
 
 class SmError(RuntimeError):
@@ -31,7 +31,11 @@ class SmError(RuntimeError):
 class SmConfig(ctypes.Structure):
     _fields_ = [("max_streams", ctypes.c_int32), ("max_ctx", ctypes.c_int32), ("use_graph", ctypes.c_int32),
                 ("head_grid", ctypes.c_int32), ("graph_steps", ctypes.c_int32), ("profile", ctypes.c_int32),
-                ("table_mode", ctypes.c_int32), ("prefill_rows", ctypes.c_int32), ("inv", ctypes.c_int32)]
+                ("table_mode", ctypes.c_int32), ("prefill_rows", ctypes.c_int32), ("inv", ctypes.c_int32),
+                ("float_stages", ctypes.c_int32), ("top_read", ctypes.c_int32)]
+
+
+FLOAT_STAGES = dict(gauge=1, edge=2, arrival=4, turn=8)     # SM_FLOAT_* of include/sm_base2.h
 
 
 _LIB = None
@@ -109,24 +113,33 @@ class Machine:
       (base2_stream.swift:274: the prompt through each layer at once); 0 runs it position by position.
       inv: the complement machine (base2_stream.swift:26 `inv`): stream, plates and lights held bit-complemented on
       the device; the same words (GPT-2, one stream, prefill_rows=0).
+      top: "plain" (the whole word table read a step) or "fr" (base2_stream_fr.swift's collapsing top read: the
+      high bytes of every word, then the low bytes of the words that can still win; the same words; GPT-2, one
+      stream).  .top() gives the last step's survivors.
       .stream(prompt_ids, n_words) -> list of words        (base2.py:123's loop, KV-cached on the device)
       .forward(ids) -> word                                 (base2.py:forward's contract)
       .reset(); .prefill(ids, stream=0); .generate(n_words) -> int32 [n_streams][n_words]
       .record_at(pos); .read(name, layer=0, stream=0, pos=0)
-    The stage switches of base2.py:10-11 are accepted for API parity; the device machine is the integer
-    machine, so any value other than "int" raises (the float stages are diagnostics of the CPU script).
+    gauge / edge / arrival ("int" or "float"; base2.py:10-11) and turn (the Pythia machine,
+    foundation0/pythia_base2.py:21-27) put that stage back to float64 on the device, as the reference's switches
+    do: diagnostics, compared with the reference at the word level (one stream, prefill_rows=0).  With
+    arrival="float" the cache holds each key as float64 (read("k16") / read("ek") are not kept).
     """
 
     def __init__(self, layout_dir: str, max_ctx: int = 1024, max_streams: int = 1, use_graph: bool = True,
                  head_grid: int = 0, graph_steps: int = 16, profile: bool = False, memory_tables: bool = True,
                  prefill_rows: int = 64, gauge: str = "int", edge: str = "int", arrival: str = "int", turn: str = "int",
-                 inv: bool = False):
+                 inv: bool = False, top: str = "plain"):
+        fs = 0
         for name, v in (("gauge", gauge), ("edge", edge), ("arrival", arrival), ("turn", turn)):
-            if v != "int":
-                raise NotImplementedError(f"{name}={v}: the GPU machine runs the integer stages only")
+            if v not in ("int", "float"):
+                raise ValueError(f"{name}={v}: each stage is int or float")
+            fs |= FLOAT_STAGES[name] if v == "float" else 0
+        if top not in ("plain", "fr"):
+            raise ValueError(f"top={top}: plain or fr")
         self.L = lib()
         cfg = SmConfig(max_streams, max_ctx, 1 if use_graph else 0, head_grid, graph_steps, 1 if profile else 0,
-                       0 if memory_tables else 1, prefill_rows, 1 if inv else 0)
+                       0 if memory_tables else 1, prefill_rows, 1 if inv else 0, fs, 1 if top == "fr" else 0)
         h = vp()
         check(self.L.sm_create(os.fsencode(layout_dir), ctypes.byref(cfg), ctypes.byref(h)))
         self.h = h
@@ -205,6 +218,14 @@ class Machine:
         out = np.zeros(shape, dtype=dt)
         check(self.L.sm_read(self.h, READ[name], layer, stream, pos, out.ctypes.data, out.nbytes))
         return out
+
+    def top(self) -> tuple:
+        """the collapsing top read's last step: (survivor count, [(word, exact pile, score)] of the first 1024)"""
+        out = np.zeros(1 + 3 * 1024, dtype=np.int64)
+        check(self.L.sm_read(self.h, READ["top"], 0, 0, 0, out.ctypes.data, out.nbytes))
+        n = int(out[0])
+        rows = out[1:].reshape(1024, 3)[:min(n, 1024)]
+        return n, [tuple(int(v) for v in r) for r in rows]
 
 
 def profile_stages(on: bool = True):

@@ -161,6 +161,7 @@ def pythia_layout(npz: dict, out_dir: str) -> str:
       embed.wc / embed.e                     int16 [vocab][768], int32 [vocab] (a power of two per word)
       {ln1,ln2}.{l}.g / .b, lnf.g / .b       int32 [768] gain on 16 places, int64 [768] offset at 2^-16
       phi.bin arrival.bin log2.bin exp2.bin cos.bin sin.bin   int64 (cos / sin [positions][rot / 2] at 2^-30)
+      cosf.bin sinf.bin                      float64 [positions][rot / 2]: the float turn's cos and sin
       manifest.json  {"kind": "pythia", "banks": [...], "norms": [{"name", "ge"}, ...], "hs", "rot",
                       "half_log2_hs", "log2_768", "eps40", "arrival_len", "vocab"}
     """
@@ -182,6 +183,11 @@ def pythia_layout(npz: dict, out_dir: str) -> str:
     np.asarray(npz["embed.e"]).astype(np.int32).tofile(os.path.join(out_dir, "embed.e"))
     for k in ("phi", "arrival", "log2", "exp2", "cos", "sin"):
         np.ascontiguousarray(npz[k]).astype(np.int64).tofile(os.path.join(out_dir, f"{k}.bin"))
+    # turn=float (foundation0/pythia_base2.py:117-118): numpy's float64 cos and sin of position x 10000^(-2i/rot)
+    rot = int(npz["rot"])
+    ang = np.arange(len(npz["cos"]))[:, None] * (10000.0 ** (-np.arange(0, rot, 2) / rot))[None, :]
+    np.cos(ang).astype(np.float64).tofile(os.path.join(out_dir, "cosf.bin"))
+    np.sin(ang).astype(np.float64).tofile(os.path.join(out_dir, "sinf.bin"))
     man = dict(kind="pythia", banks=banks, norms=norms, hs=int(npz["hs"]), rot=int(npz["rot"]),
                half_log2_hs=int(npz["half_log2_hs"]), log2_768=round(math.log2(768) * 65536), eps40=int(npz["eps40"]),
                arrival_len=int(len(npz["arrival"])), vocab=int(npz["vocab"]))

@@ -43,9 +43,17 @@ def test_create_reports_io_errors_before_any_device_call(sm, tmp_path):
     assert e.value.code == -2
 
 
-def test_float_switches_are_not_silently_routed(sm, tmp_path):
-    with pytest.raises(NotImplementedError):
-        sm.Machine(str(tmp_path), gauge="float")
+def test_stage_switches(sm, tmp_path):
+    """each stage is int or float (base2.py:10-11); the bits the binding sends are the header's SM_FLOAT_*"""
+    with pytest.raises(ValueError):
+        sm.Machine(str(tmp_path), gauge="half")
+    import re
+    from streaming_machine_amd import machine
+    hdr = open(os.path.join(REPO, "include", "sm_base2.h")).read()
+    bits = dict(re.findall(r"SM_FLOAT_([A-Z]+) = (\d+)", hdr))
+    assert {k.lower(): int(v) for k, v in bits.items()} == machine.FLOAT_STAGES
+    names = [f[0] for f in machine.SmConfig._fields_]
+    assert names[-3:] == ["inv", "float_stages", "top_read"]
 
 
 def test_last_error_is_a_string(sm):
