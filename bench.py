@@ -101,6 +101,8 @@ def b1_kernel_bytes(name: str, ctx: float, vocab: int = VOCAB) -> float:
         return bank_bytes(*BANKS[name])
     if name == "head":
         return bank_bytes(768, vocab)
+    if name == "head.top":                  # the collapsing top read's first stage: the high-byte plane, e and b
+        return 768 * vocab + 12 * vocab
     if name == "attend":
         return KV_WORKLOAD / 12 * ctx
     return 0.0
@@ -160,9 +162,9 @@ def dominant(table: dict, where: str) -> dict:
 
 
 # ---- batch 1 (config 1) ----
-def b1_leg(sm, lay, steps_req: int, warmup: int, prompt, want, cold_steps: int = 15):
+def b1_leg(sm, lay, steps_req: int, warmup: int, prompt, want, cold_steps: int = 15, top: str = "plain"):
     import torch
-    m = sm.Machine(lay, max_ctx=64, graph_steps=WORDS - 1, prefill_rows=PREFILL_ROWS, use_graph=not PLAIN)
+    m = sm.Machine(lay, max_ctx=64, graph_steps=WORDS - 1, prefill_rows=PREFILL_ROWS, use_graph=not PLAIN, top=top)
 
     def sequence(k: int):
         m.reset()
@@ -199,7 +201,7 @@ def b1_leg(sm, lay, steps_req: int, warmup: int, prompt, want, cold_steps: int =
                 "table": {}, "cold": {}, "ctx": PROMPT + WORDS / 2.0}
 
     # the same sequences, every launch timed by its own event pair
-    mp = sm.Machine(lay, max_ctx=64, profile=True, prefill_rows=PREFILL_ROWS)
+    mp = sm.Machine(lay, max_ctx=64, profile=True, prefill_rows=PREFILL_ROWS, top=top)
     for it in range(3):
         mp.reset()
         mp.prefill(prompt)
@@ -211,6 +213,18 @@ def b1_leg(sm, lay, steps_req: int, warmup: int, prompt, want, cold_steps: int =
         times = sm.kernel_times(clear=True)
     ctx = PROMPT + WORDS / 2.0                     # mean context of the decode steps (9..23)
     table = kernel_table(times, WORDS - 1, lambda k: b1_kernel_bytes(k, ctx))
+    survivors = []
+    if top == "fr":                                # the words left to finish after the high bytes, step by step
+        mp.reset()
+        mp.prefill(prompt)
+        mp.generate(1)
+        for _ in range(WORDS - 1):
+            mp.generate(1)
+            survivors.append(mp.top()[0])
+    if cold_steps == 0:
+        mp.close()
+        return {"tok_s": steps / total, "ms": 1000.0 * total / steps, "steps": steps,
+                "prompt_ms": 1000.0 * prompt_s / nseq, "table": table, "cold": {}, "ctx": ctx, "survivors": survivors}
     # cold: 1 GiB streamed through the device between steps (outside the timed launches)
     src = torch.ones(1 << 28, dtype=torch.int32, device="cuda")
     dst = torch.empty_like(src)
@@ -538,7 +552,8 @@ def main():
     ap.add_argument("--no-batched", action="store_true", help="skip the 64-stream leg")
     ap.add_argument("--no-pythia", action="store_true", help="skip the Pythia 32-stream leg")
     ap.add_argument("--no-micro", action="store_true", help="skip the GEMV and attention microbenchmarks")
-    ap.add_argument("--only", choices=("b1", "b64", "pythia", "gemv", "attention"), default="",
+    ap.add_argument("--no-top", action="store_true", help="skip the collapsing top read's batch-1 leg")
+    ap.add_argument("--only", choices=("b1", "b1top", "b64", "pythia", "gemv", "attention"), default="",
                     help="profiling: run one leg and print only its result (not the bench line)")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MB",
                     help="profiling: first copy MB MiB device to device (calibrates HBM byte counters)")
@@ -589,6 +604,14 @@ def main():
         return
     prompt = sm.prompt_ids(1, PROMPT)
     want = fixture_cases("base2_golden.json")["c1_p8_w16"]["words"]      # base2.py's own words for this sequence
+    top = None
+    if (args.only in ("", "b1top") and not args.no_top) and not PLAIN:
+        top = b1_leg(sm, lay, args.steps, args.warmup, prompt, want, cold_steps=0, top="fr")
+        log(f"batch 1, collapsing top read: {top['tok_s']:.1f} tokens/s, {top['ms']:.4f} ms/step")
+        if args.only == "b1top":
+            print(json.dumps({"value": round(top["tok_s"], 2), "ms_per_step": round(top["ms"], 4), "kernels": top["table"],
+                              "survivors": top["survivors"]}), flush=True)
+            return
     b1 = b1_leg(sm, lay, args.steps, args.warmup, prompt, want)
     log(f"batch 1: {b1['tok_s']:.1f} tokens/s, {b1['ms']:.4f} ms/step")
     table = b1["table"]
@@ -635,6 +658,16 @@ def main():
                             "unit": "tokens/s", "prompt_ms": round(b1["prompt_ms"], 3),
                             "note": "16 words per sequence over the prompt pass (7 prompt rows through the int8 MFMA "
                                     "banks, then the first word's step) plus 15 decode steps"},
+        "top_read": None if top is None else {
+            "value": round(top["tok_s"], 2), "unit": "tokens/s", "ms_per_step": round(top["ms"], 4),
+            "note": "the same batch-1 workload with the collapsing top read (Machine(top='fr'), base2_stream_fr.swift:"
+                    "4-15): the high-byte plane of every word, exact bounds, the low bytes of the words that can still "
+                    "win; words gated on base2.py's like the main line",
+            "head_us_per_step": {"full_read": round(sum(table[k]["us_per_step"] for k in ("head", "race") if k in table), 2),
+                                 "top_read": round(sum(top["table"][k]["us_per_step"] for k in ("head.top", "race.top")
+                                                       if k in top["table"]), 2)},
+            "kernels": {k: v for k, v in top["table"].items() if k in ("head.top", "race.top")},
+            "survivors_per_step": top["survivors"]},
         "batched": batched,
         "pythia": pyleg,
         "gemv": gemv,

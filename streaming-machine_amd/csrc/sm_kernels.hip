@@ -491,19 +491,33 @@ __global__ __launch_bounds__(64 * WPB) void k_gemv(GemvArgs a) {
         i64 bl = bestv[0];
 #pragma unroll
         for (int w = 1; w < WPB; w++) bl = max(bl, bestv[w]);
+        // gathered in LDS, then written in order of falling high (rank = the candidates above it; equal highs in
+        // gathering order), so that the second stage stops reading a block at its first high below the grid's
+        // best low
+        __shared__ int cj_s[TSLOTS];
+        __shared__ i64 ch_s[TSLOTS], cc_s[TSLOTS];
         for (int k = tid; k < TSLOTS; k += NT) {
             if (top_j[k] >= 0 && top_h[k] >= bl) {
                 const int n = atomicAdd(&top_n, 1);
-                const size_t o = (size_t)blockIdx.x * TSLOTS + n;
-                a.cand_j[o] = top_j[k];
-                a.cand_h[o] = top_h[k];
-                a.cand_c[o] = top_c[k];
+                cj_s[n] = top_j[k];
+                ch_s[n] = top_h[k];
+                cc_s[n] = top_c[k];
             }
         }
         __syncthreads();
+        const int n = top_n;
+        for (int k = tid; k < n; k += NT) {
+            const i64 h = ch_s[k];
+            int r = 0;
+            for (int i = 0; i < n; i++) r += ch_s[i] > h || (ch_s[i] == h && i < k);
+            const size_t o = (size_t)blockIdx.x * TSLOTS + r;
+            a.cand_j[o] = cj_s[k];
+            a.cand_h[o] = h;
+            a.cand_c[o] = cc_s[k];
+        }
         if (tid == 0) {
             a.part_v[blockIdx.x] = bl;
-            a.part_i[blockIdx.x] = top_n;
+            a.part_i[blockIdx.x] = n;
         }
         return;
     }
@@ -619,26 +633,36 @@ __global__ __launch_bounds__(256) void k_race1(Race1Args a) {
 // its pile exactly, C + sum x (w & 255), and its score power(pile, (we + ex + 16) 65536 - LS) + b
 // (base2.py:114); the race among the survivors (largest, ties to the lowest word), then race1_finish.  The
 // threshold is the best low, not the 5th-best low the reference keeps for its top-5 report: the machine needs the
-// winner only.  Survivors past the LDS list (TOP_LIST) are finished one thread each (exact, slow: a model whose
-// bounds hold almost nothing).  The step's survivors are written out (count, and the first tmax: word, exact pile,
-// score).
+// winner only.
+// Three rounds of memory requests: the blocks' lows and candidate counts (with the light); each block's
+// candidates from the highest high down, stopping at the first below T (a block's candidates come in order of
+// falling high; the first is requested in round 1); the survivors' low bytes, four lanes a survivor (192 bytes
+// each), 64 survivors a pass.  Survivors
+// past TOP_LIST are finished one thread each (exact, slow: a model whose bounds hold almost nothing).  The step's
+// survivors are written out (count, and the first tmax: word, exact pile, score).
 #define TOP_LIST 1024
 __global__ __launch_bounds__(256) void k_race_top(TopArgs t) {
     const Race1Args& a = t.r;
-    __shared__ int x_s[768];
+    __shared__ __align__(16) int x_s[768];
     __shared__ int lj[TOP_LIST];
     __shared__ i64 lc[TOP_LIST];
     __shared__ i64 red_s[4];
     __shared__ int ln_s;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    constexpr int PER = 2;                              // first-stage blocks a thread reads (nblk <= 512)
-    i64 bl[PER];
-    int nc[PER];
+    // round 1 (with each block's first candidate, its highest high)
+    const int g[2] = {tid, tid + 256};                  // the first stage's blocks of this thread (nblk <= 512)
+    i64 bl[2], h[2] = {INT64_MIN, INT64_MIN}, cv[2] = {0, 0};
+    int nc[2], jv[2] = {0, 0};
 #pragma unroll
-    for (int k = 0; k < PER; k++) {
-        const int g = tid + 256 * k;
-        bl[k] = g < a.nblk ? a.part_v[g] : INT64_MIN;
-        nc[k] = g < a.nblk ? a.part_i[g] : 0;
+    for (int k = 0; k < 2; k++) {
+        bl[k] = g[k] < a.nblk ? a.part_v[g[k]] : INT64_MIN;
+        nc[k] = g[k] < a.nblk ? a.part_i[g[k]] : 0;
+        if (g[k] < a.nblk) {                            // (slot 0 is read whatever the count: it is always allocated)
+            const size_t o = (size_t)g[k] * t.cap;
+            h[k] = t.cand_h[o];
+            jv[k] = t.cand_j[o];
+            cv[k] = t.cand_c[o];
+        }
     }
 #pragma unroll
     for (int m = 0; m < 3; m++) x_s[tid + 256 * m] = t.tx[tid + 256 * m];
@@ -655,14 +679,30 @@ __global__ __launch_bounds__(256) void k_race_top(TopArgs t) {
     if (lane == 0) red_s[wave] = T;
     __syncthreads();
     T = max(max(red_s[0], red_s[1]), max(red_s[2], red_s[3]));
-    // the survivors, into the list
+    // round 2: both blocks' candidates in step, until each one's high falls below T
+    {
+        bool on[2] = {nc[0] > 0, nc[1] > 0};
+        for (int c = 0; on[0] || on[1]; c++) {
+            if (c > 0) {
 #pragma unroll
-    for (int k = 0; k < PER; k++) {
-        const size_t o = (size_t)(tid + 256 * k) * t.cap;
-        for (int c = 0; c < nc[k]; c++) {
-            if (t.cand_h[o + c] >= T) {
-                const int n = atomicAdd(&ln_s, 1);
-                if (n < TOP_LIST) { lj[n] = t.cand_j[o + c]; lc[n] = t.cand_c[o + c]; }
+                for (int k = 0; k < 2; k++) {
+                    if (on[k]) {
+                        const size_t o = (size_t)g[k] * t.cap + c;
+                        h[k] = t.cand_h[o];
+                        jv[k] = t.cand_j[o];
+                        cv[k] = t.cand_c[o];
+                    }
+                }
+            }
+#pragma unroll
+            for (int k = 0; k < 2; k++) {
+                if (on[k]) {
+                    if (h[k] >= T) {
+                        const int n = atomicAdd(&ln_s, 1);
+                        if (n < TOP_LIST) { lj[n] = jv[k]; lc[n] = cv[k]; }
+                    }
+                    on[k] = h[k] >= T && c + 1 < nc[k];
+                }
             }
         }
     }
@@ -675,33 +715,54 @@ __global__ __launch_bounds__(256) void k_race_top(TopArgs t) {
     i64 bv = 0;
     int bi = -1;
     if (ns <= TOP_LIST) {
-        for (int s = wave; s < ns; s += 4) {              // a wave a survivor: lane l its bytes 12 l .. 12 l + 11
-            const int j = lj[s];
-            const unsigned* lb = reinterpret_cast<const unsigned*>(t.lo + (size_t)j * 768 + 12 * lane);
-            const unsigned d[3] = {lb[0], lb[1], lb[2]};
+        // round 3: four lanes a survivor, lane q of the four its bytes 192 q .. 192 q + 191
+        const int gq = lane & 3, slot = lane >> 2;
+        for (int s0 = 16 * wave; s0 < ns; s0 += 64) {
+            const int s = s0 + slot;
+            const bool live = s < ns;
+            const int j = live ? lj[s] : 0;
+            const v4i* lb = reinterpret_cast<const v4i*>(t.lo + (size_t)j * 768 + 192 * gq);
+            v4i d[12];
+#pragma unroll
+            for (int k = 0; k < 12; k++) d[k] = live ? lb[k] : v4i{0, 0, 0, 0};
+            const int wej = t.we[j];
+            const i64 bj = t.bias[j];
+            const int4* xs = reinterpret_cast<const int4*>(x_s + 192 * gq);
             int acc = 0;
 #pragma unroll
-            for (int b = 0; b < 12; b++) acc += x_s[12 * lane + b] * (int)((d[b >> 2] >> (8 * (b & 3))) & 255u);
-            const i64 pile = wadd(lc[s], wave_reduce64((i64)acc, OpAdd()));
-            const i64 y = score(j, pile);
-            if (lane == 0) {
+            for (int k = 0; k < 12; k++) {
+                const int dw[4] = {d[k].x, d[k].y, d[k].z, d[k].w};
+#pragma unroll
+                for (int w = 0; w < 4; w++) {
+                    const int4 xv = xs[4 * k + w];
+                    const unsigned u = (unsigned)dw[w];
+                    acc += xv.x * (int)(u & 255u) + xv.y * (int)((u >> 8) & 255u) + xv.z * (int)((u >> 16) & 255u) +
+                           xv.w * (int)(u >> 24);
+                }
+            }
+            i64 sum = acc;
+            sum += __shfl_xor(sum, 1, 64);
+            sum += __shfl_xor(sum, 2, 64);
+            if (live && gq == 0) {
+                const i64 pile = wadd(lc[s], sum);
+                const i64 y = wadd(power_e(pile, wsub(wmul((i64)wej + ex + 16, 65536), ls), fe, e2, t.tb), bj);
                 if (race_beats<0>(y, j, bv, bi)) { bv = y; bi = j; }
                 if (s < t.tmax) { t.tw[s] = j; t.tpile[s] = pile; t.tscore[s] = y; }
             }
         }
     } else {
+        // every survivor, one thread each
 #pragma unroll
-        for (int k = 0; k < PER; k++) {
-            const size_t o = (size_t)(tid + 256 * k) * t.cap;
+        for (int k = 0; k < 2; k++) {
             for (int c = 0; c < nc[k]; c++) {
-                if (t.cand_h[o + c] >= T) {
-                    const int j = t.cand_j[o + c];
-                    const unsigned char* lb = t.lo + (size_t)j * 768;
-                    i64 sum = 0;
-                    for (int i = 0; i < 768; i++) sum += (i64)x_s[i] * lb[i];
-                    const i64 y = score(j, wadd(t.cand_c[o + c], sum));
-                    if (race_beats<0>(y, j, bv, bi)) { bv = y; bi = j; }
-                }
+                const size_t o = (size_t)g[k] * t.cap + c;
+                if (t.cand_h[o] < T) break;
+                const int j = t.cand_j[o];
+                const unsigned char* lb = t.lo + (size_t)j * 768;
+                i64 sum = 0;
+                for (int i = 0; i < 768; i++) sum += (i64)x_s[i] * lb[i];
+                const i64 y = score(j, wadd(t.cand_c[o], sum));
+                if (race_beats<0>(y, j, bv, bi)) { bv = y; bi = j; }
             }
         }
     }
