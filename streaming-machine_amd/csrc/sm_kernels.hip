@@ -374,7 +374,7 @@ __global__ __launch_bounds__(64 * WPB) void k_gemv(GemvArgs a) {
         // a tile's exponents and biases are requested before its weights, so waiting for the small loads
         // never waits for the large ones behind them
         v4i wA[U], wB[U];
-        i64 bA = 0, eA = 0, bB = 0, eB = 0, sA = 0, sB = 0;
+        i64 bA = 0, eA = 0, bB = 0, eB = 0, sA = 0, sB = 0;     // (EPI_PLAIN_ADD: sA, sB hold the row added to)
         // every lane loads (indices clamped into range): a load that writes only some lanes would have to be
         // merged with the register's old value, and that merge waits for the load
         auto fetch = [&](v4i (&w)[U], i64& we_, i64& b_, i64& s_, int t) {
@@ -385,6 +385,7 @@ __global__ __launch_bounds__(64 * WPB) void k_gemv(GemvArgs a) {
                 we_ = a.we[j];
                 if (EPI != EPI_PHEAD) b_ = a.bias[j];
                 if (INV) s_ = a.sw[j];
+                else if (EPI == EPI_PLAIN_ADD) s_ = a.Yb[j];
             }
             load_wtile<NIN, TC, U, WB>(w, a.W, t, lane);
         };
@@ -393,6 +394,22 @@ __global__ __launch_bounds__(64 * WPB) void k_gemv(GemvArgs a) {
         int ngq[NIN / NT];
         prologue_load<NIN, NT, PRO>(a, tid, row, ngq, nbq);   // the row first, then this wave's first tile
         fetch(wA, eA, bA, sA, tile);                     // unconditional (clamped): no branch for the wait count to merge
+        // then the next phase's lines (a fixed count a thread, clamped to a valid address: no branch around loads);
+        // their values are consumed only after the tiles, where they have long arrived
+        int pfs = 0;
+        {
+            constexpr int PFN = WPB <= 2 ? 2 : 1;
+            const char* pb = a.pf ? a.pf : reinterpret_cast<const char*>(a.W);
+            const int lines = a.pf ? a.pf_lines : 1;
+#pragma unroll
+            for (int k = 0; k < PFN; k++) {
+                const int i = tid + NT * k, r = i / lines, l = i - r * lines;
+                const int b2 = blockIdx.x + r * gridDim.x;
+                const long long li = (long long)b2 * lines + l;
+                const size_t off = a.pf && b2 < a.pf_nblk && li < a.pf_total ? (size_t)li * 128 : 0;
+                pfs += *reinterpret_cast<const int*>(pb + off);
+            }
+        }
         const bool rec = REC && a.rec_pos && *a.rec_pos == (a.pos ? *a.pos : -2);
         i64 ex, ls = 0, e2 = 0, sx = 0, nn = 0;
         double sig = 1.0;
@@ -432,7 +449,8 @@ __global__ __launch_bounds__(64 * WPB) void k_gemv(GemvArgs a) {
                     a.Y[j] = pile;
                 } else if (EPI == EPI_PLAIN_ADD) {
                     const i64 add = wadd(rsh(pile, -(wec + ex + 16)), bc);
-                    const i64 r = INV ? wsub(a.Yb[j], add) : wadd(a.Yb[j], add);
+                    const i64 yb = INV ? a.Yb[j] : swc;          // (the plain machine's row was fetched with the tile)
+                    const i64 r = INV ? wsub(yb, add) : wadd(yb, add);
                     a.Y[j] = r;
                     if (rec && a.rout) a.rout[j] = INV ? ~r : r;
                 } else if (EPI == EPI_PLAIN || EPI == EPI_PLAIN_EDGE || EPI == EPI_PHEAD) {
@@ -481,6 +499,7 @@ __global__ __launch_bounds__(64 * WPB) void k_gemv(GemvArgs a) {
             it++;
             tile = t2;
         }
+        asm volatile("" ::"v"(pfs));                    // the prefetches stay (and are done with by here)
     }
     if constexpr (TOP) {
         // the block's best low; its candidates are its words whose high reaches it (the winner's high reaches

@@ -623,6 +623,28 @@ static void launch_embed1(sm_machine* m) {
     else launch(m->cfg.profile, "embed", k_embed1<0>, dim3(1), dim3(256), 0, m->st, race1_args(m));
 }
 
+// the next GEMV phase's plate for this phase's blocks to pull into their L2 (GemvArgs::pf): its first wpb tiles
+// of every block of its grid
+static void set_pf(GemvArgs& a, const DevPlate& next, int wpb, int grid) {
+    a.pf = reinterpret_cast<const char*>(next.W);
+    a.pf_lines = wpb * next.tc * next.nin * 2 / 128;
+    a.pf_nblk = grid;
+    a.pf_total = (int)((size_t)next.ntiles * next.tc * next.nin * 2 / 128);
+}
+static int grid4(const DevPlate& P) { return (P.ntiles + 3) / 4; }   // four waves a block, a tile a wave
+static int grid2(const DevPlate& P) { return (P.ntiles + 1) / 2; }   // two waves a block
+// the head's first stage for the next phase to pull: the full table's tiles, or the top read's high bytes
+static void set_pf_head(sm_machine* m, GemvArgs& a) {
+    if (m->cfg.top_read) {
+        a.pf = reinterpret_cast<const char*>(m->top_hi);
+        a.pf_lines = HEAD_WPB * HEAD_TC * 768 / 128;
+        a.pf_nblk = m->head_grid;
+        a.pf_total = (int)((size_t)m->head.ntiles * HEAD_TC * 768 / 128);
+    } else {
+        set_pf(a, m->head, HEAD_WPB, m->head_grid);
+    }
+}
+
 // a batch-1 GEMV phase: rec selects the instantiation that records (launched only for the recorded step), the
 // machine's MODE bits the rest (only those the phase has; the complement machine is never mixed with float stages)
 static constexpr int phase_modes(int PRO, int EPI) {
@@ -690,6 +712,7 @@ static int launch_step_pythia(sm_machine* m, int parts, bool rec) {
             plate(a, P, 0);
             a.X = Rin; a.Y = m->QKV; a.rout = m->r_qkv + l * 2304; a.rg = m->r_gauge + (l * 2 + 0) * 768;
             a.ng = m->ng[l][0]; a.nb = m->nb[l][0]; a.nge = m->nge[l][0];
+            set_pf(a, m->bank[l][2], 4, grid4(m->bank[l][2]));
             gemv<768, 2, 4, PRO_PGAUGE, EPI_PLAIN>(m, rec, "qkv", (P.ntiles + 3) / 4, a);
         }
         // fc: gauge ln2 of the same R, plain, edge (:156)
@@ -700,6 +723,7 @@ static int launch_step_pythia(sm_machine* m, int parts, bool rec) {
             a.X = Rin; a.Y = m->hid; a.rout = m->r_fcpre + l * 3072; a.rout2 = m->r_hid + l * 3072;
             a.rg = m->r_gauge + (l * 2 + 1) * 768;
             a.ng = m->ng[l][1]; a.nb = m->nb[l][1]; a.nge = m->nge[l][1];
+            set_pf(a, m->bank[l][1], 2, grid2(m->bank[l][1]));
             gemv<768, 2, 4, PRO_PGAUGE, EPI_PLAIN_EDGE>(m, rec, "fc", (P.ntiles + 3) / 4, a);
         }
         // attention with turns (:125-141)
@@ -715,6 +739,7 @@ static int launch_step_pythia(sm_machine* m, int parts, bool rec) {
             const DevPlate& P = m->bank[l][1];
             plate(g, P, 1);
             g.X = m->att; g.Y = m->R; g.Yb = Rin; g.rout = m->r_resid + (l * 2 + 0) * 768;
+            set_pf(g, m->bank[l][3], 4, grid4(m->bank[l][3]));
             attend1<1>(m, rec, a, l);
             gemv<768, 2, 2, PRO_TO16, EPI_PLAIN_ADD>(m, rec, "proj", (P.ntiles + 1) / 2, g);
         }
@@ -724,6 +749,8 @@ static int launch_step_pythia(sm_machine* m, int parts, bool rec) {
             const DevPlate& P = m->bank[l][3];
             plate(a, P, 3);
             a.X = m->hid; a.Y = m->R; a.Yb = m->R; a.rout = m->r_resid + (l * 2 + 1) * 768;
+            if (l < 11) set_pf(a, m->bank[l + 1][0], 4, grid4(m->bank[l + 1][0]));
+            else set_pf(a, m->head, HEAD_WPB, m->head_grid);
             gemv<3072, 1, 4, PRO_TO16, EPI_PLAIN_ADD>(m, rec, "mproj", (P.ntiles + 3) / 4, a);
         }
     }
@@ -897,6 +924,7 @@ static int launch_step(sm_machine* m, int parts = STEP_ALL, bool rec = false) {
             a.X = Rin; a.Y = m->QKV;
             a.rx16 = m->r_x16 + (l * 4 + 0) * 3072; a.rexls = m->r_exls + (l * 4 + 0) * 2;
             a.rpile = m->r_pile + (l * 4 + 0) * 3072; a.rout = m->r_qkv + l * 2304;
+            set_pf(a, m->bank[l][1], 2, grid2(m->bank[l][1]));
             gemv<768, 2, 4, PRO_GAUGE, EPI_GAUGED>(m, rec, "qkv", (P.ntiles + 3) / 4, a);
         }
         // attention (base2.py:85-100) on the KV cache of layer l
@@ -914,6 +942,7 @@ static int launch_step(sm_machine* m, int parts = STEP_ALL, bool rec = false) {
             g.X = m->att; g.Y = m->R; g.Yb = Rin;
             g.rx16 = m->r_x16 + (l * 4 + 1) * 3072; g.rexls = m->r_exls + (l * 4 + 1) * 2;
             g.rpile = m->r_pile + (l * 4 + 1) * 3072; g.rout = m->r_resid + (l * 2 + 0) * 768;
+            set_pf(g, m->bank[l][2], 4, grid4(m->bank[l][2]));
             attend1<0>(m, rec, a, l);
             gemv<768, 2, 2, PRO_TO16, EPI_PLAIN_ADD>(m, rec, "proj", (P.ntiles + 1) / 2, g);
         }
@@ -925,6 +954,7 @@ static int launch_step(sm_machine* m, int parts = STEP_ALL, bool rec = false) {
             a.X = m->R; a.Y = m->hid;
             a.rx16 = m->r_x16 + (l * 4 + 2) * 3072; a.rexls = m->r_exls + (l * 4 + 2) * 2;
             a.rpile = m->r_pile + (l * 4 + 2) * 3072; a.rout = m->r_hid + l * 3072;
+            set_pf(a, m->bank[l][3], 4, grid4(m->bank[l][3]));
             gemv<768, 2, 4, PRO_GAUGE, EPI_GAUGED_EDGE>(m, rec, "fc", (P.ntiles + 3) / 4, a);
         }
         // mproj: to16 of the hidden row (3072), product, plain, added to R (base2.py:106)
@@ -935,6 +965,8 @@ static int launch_step(sm_machine* m, int parts = STEP_ALL, bool rec = false) {
             a.X = m->hid; a.Y = m->R; a.Yb = m->R;
             a.rx16 = m->r_x16 + (l * 4 + 3) * 3072; a.rexls = m->r_exls + (l * 4 + 3) * 2;
             a.rpile = m->r_pile + (l * 4 + 3) * 3072; a.rout = m->r_resid + (l * 2 + 1) * 768;
+            if (l < 11) set_pf(a, m->bank[l + 1][0], 4, grid4(m->bank[l + 1][0]));
+            else set_pf_head(m, a);
             gemv<3072, 1, 4, PRO_TO16, EPI_PLAIN_ADD>(m, rec, "mproj", (P.ntiles + 3) / 4, a);
         }
     }
