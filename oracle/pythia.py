@@ -19,9 +19,9 @@ import numpy as np
 
 from . import build, _p, i16p, i64p
 
-ERRORS = {1: "product passed 2^53 (pythia_base2.py:76)", 2: "position past the cache or word out of range",
-          3: "rshift left shift past 2^62 (pythia_base2.py:57)", 4: "turn input past 2^31 (pythia_base2.py:121)",
-          5: "attention sum passed 2^62 (pythia_base2.py:138)", 6: "power result past int64 (pythia_base2.py:85)"}
+ERRORS = {1: "product passed 2^53 (pythia_base2.py:75)", 2: "position past the cache or word out of range",
+          3: "rshift left shift past 2^62 (pythia_base2.py:63)", 4: "turn input past 2^31 (pythia_base2.py:121)",
+          5: "attention sum passed 2^62 (pythia_base2.py:139)", 6: "power result past int64 (pythia_base2.py:90)"}
 
 
 class PyModel(ctypes.Structure):

@@ -15,7 +15,7 @@
  *   edge     as base2.py (rshift(H, 4) + 32768 into PHI, rshift(H share, 16))         (:143-147)
  *   layer    R = R + plain(attend(plain(gauge(R, ln1), qkv)), proj) + plain(edge(plain(gauge(R, ln2), fc)), mproj)
  *   head     y16, ey = to16(gauge(R, lnf)); rshift(product(y16, head.w), -(head.e + ey + 16)); race  (:158-160)
- * power is exact here (pythia_base2.py:81-85 takes int64 when every |X| < 2^45 and Python integers beyond, so it
+ * power is exact here (pythia_base2.py:87-90 takes int64 when every |X| < 2^45 and Python integers beyond, so it
  * never wraps): X * EXP2[f] is formed in 128 bits.  The reference's asserts come back as status codes; they are
  * checked per element (the reference checks the largest element of the array against the smallest shift).
  * Additions onto the stream, the edge's product and the turns' products are numpy int64 operations (they wrap).
@@ -25,7 +25,7 @@
  */
 #include "orc_common.h"
 
-#define PYO_E_SHIFT 3     /* rshift: a left shift past 2^62 (pythia_base2.py:57) */
+#define PYO_E_SHIFT 3     /* rshift: a left shift past 2^62 (pythia_base2.py:63) */
 #define PYO_E_TURN 4      /* turn: |X| >= 2^31 in the turned dims (:121) */
 #define PYO_E_ATT 5       /* attention: max|v| sum(a) >= 2^62 (:138) */
 #define PYO_E_POW 6       /* power: the exact result does not fit int64 (:85) */
@@ -59,13 +59,13 @@ static const int PNOUT[4] = {2304, 768, 3072, 768};
 
 static void flag(int* st, int code) { if (!*st) *st = code; }
 
-/* pythia_base2.py:56-60  rshift with the left-shift bound of :57 */
+/* pythia_base2.py:61-65  rshift with the left-shift bound of :63 */
 static i64 prsh(i64 x, i64 s, int* st) {
     if (s < 0 && (62 + s <= 0 || iabs(x) >= ((i64)1 << (62 + s)))) flag(st, PYO_E_SHIFT);
     return orc_rshift1(x, s);
 }
 
-/* pythia_base2.py:81-85  power(X, F) = X x 2^(F/65536), exact */
+/* pythia_base2.py:87-90  power(X, F) = X x 2^(F/65536), exact */
 static i64 ppow(i64 x, i64 F, const i64* EXP2, int* st) {
     const i64 I = F >> 16, f = F & 0xFFFF;
     const i128 X = (i128)x * EXP2[f];
@@ -84,7 +84,7 @@ static i64 ppow(i64 x, i64 F, const i64* EXP2, int* st) {
     return (i64)r;
 }
 
-/* pythia_base2.py:75-79  product: exact sums; the assert sum|x16| max|w| < 2^53 */
+/* pythia_base2.py:74-80  product: exact sums; the assert sum|x16| max|w| < 2^53 */
 static void pprod(const i64* x16, i64 nin, const int16_t* w, i64 nout, double wmax, i64* pile, int* st) {
     double sa = 0;
     for (i64 i = 0; i < nin; i++) sa += (double)iabs(x16[i]);
@@ -186,7 +186,7 @@ static double plate_max(const int16_t* w, i64 n) {
     return (double)m;
 }
 
-/* the largest |w| of every plate (product's assert, pythia_base2.py:76) */
+/* the largest |w| of every plate (product's assert, pythia_base2.py:75) */
 void pyo_prepare(py_model* M) {
     for (i64 l = 0; l < M->L; l++)
         for (int k = 0; k < 4; k++) M->wmax[l][k] = plate_max(M->w[l][k], (i64)PNIN[k] * PNOUT[k]);

@@ -59,6 +59,7 @@ struct GemmArgs {
     int* sfacts;                  // EPI_PART with SRC > 0: [KSPLIT][rows][4] each K slice's SXh, SXl, n32768, ex
     i64* orw_out;                 // EPI_GAUGED_EDGE / EPI_PLAIN_EDGE (when non-null): [rows][N / 16] OR of |y| over
                                   // each block's 16 columns, the consumer's water level
+    int* err;                     // the Pythia machine: its rshift assert sets SM_ERR_RANGE here
 };
 
 // Where a bank's A operand comes from:
@@ -528,8 +529,11 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs a) {
         } else if (EPI == EPI_PLAIN_ADD) {             // the stream takes the plain bank (base2.py:73-76, 105)
             const int j = (nt * NB + nb) * 16 + (lane & 15);
             const i64 old = j < a.N ? a.Y[(size_t)row * a.ystride + j] : 0;
+            if (a.err && j < a.N && pyshift_fails(pile[nb], -(we[nb] + ex + 16))) atomicOr(a.err, SM_ERR_RANGE);
             y1[nb] = y2[nb] = wadd(old, wadd(rsh(pile[nb], -(we[nb] + ex + 16)), bc[nb]));
         } else if (EPI == EPI_PLAIN || EPI == EPI_PLAIN_EDGE) {   // the Pythia machine's banks (:112-114, 156)
+            const int j = (nt * NB + nb) * 16 + (lane & 15);
+            if (a.err && j < a.N && pyshift_fails(pile[nb], -(we[nb] + ex + 16))) atomicOr(a.err, SM_ERR_RANGE);
             y1[nb] = wadd(rsh(pile[nb], -(we[nb] + ex + 16)), bc[nb]);
             y2[nb] = EPI == EPI_PLAIN_EDGE ? edge1(y1[nb], a.tb) : y1[nb];
         } else {
@@ -679,6 +683,7 @@ __global__ __launch_bounds__(256, 2) void k_head_rows(GemmArgs a) {     // two b
             if (EPI == EPI_PILE) {
                 a.Y[(size_t)row * a.ystride + j] = pile;
             } else {
+                if (EPI == EPI_PHEAD && a.err && pyshift_fails(pile, -(we + rc[row][1]))) atomicOr(a.err, SM_ERR_RANGE);
                 const i64 y = EPI == EPI_PHEAD ? rsh(pile, -(we + rc[row][1]))            // Pythia: plain, no bias
                                                : wadd(rsh(wmul(pile, rc[row][2]), 16 - we - rc[row][1]), bc);
                 if (rec && a.rlogits) a.rlogits[j] = y;
@@ -768,6 +773,7 @@ struct PyRowArgs {
     i64* rg1; i64* rx1; i64* rex1; i64* rg2; i64* rx2; i64* rex2;   // the gauges and their lights
     i64* rpileM; i64* routM;                                         // PY_ADD: mproj's pile, the stream after it
     const int* rowmap;                            // prompt rows (PY_EMBED): stream << 16 | position per row
+    int* err;                                     // its rshift assert (PY_ADD) sets SM_ERR_RANGE here
 };
 enum { PY_EMBED = 0, PY_ADD = 1 };
 
@@ -794,7 +800,7 @@ SMD void plain4_load(Plain4<KS>& P, const int* part, int rows, int N, const int*
     }
 }
 template <int KS>
-SMD void plain4_finish(const Plain4<KS>& P, int kin, const int* ri, i64 (&pile)[4], i64 (&y)[4]) {
+SMD void plain4_finish(const Plain4<KS>& P, int kin, const int* ri, i64 (&pile)[4], i64 (&y)[4], int* err) {
     v4l_p h = P.h[0], mi = P.mi[0], lo = P.lo[0];
 #pragma unroll
     for (int q = 1; q < KS; q++) { h += P.h[q]; mi += P.mi[q]; lo += P.lo[q]; }
@@ -805,6 +811,7 @@ SMD void plain4_finish(const Plain4<KS>& P, int kin, const int* ri, i64 (&pile)[
     for (int j = 0; j < 4; j++) {
         pile[j] = 65536 * (i64)h[j] + 256 * (i64)mi[j] + lo[j] + 32768 * (sxh + sw[2 * j]) + 128 * (sxl + sw[2 * j + 1]) +
                   16384 * (i64)kin + 128 * n32;
+        if (err && pyshift_fails(pile[j], -((i64)P.wv[j] + ex + 16))) atomicOr(err, SM_ERR_RANGE);
         y[j] = wadd(rsh(pile[j], -((i64)P.wv[j] + ex + 16)), bc[j]);
     }
 }
@@ -861,7 +868,7 @@ __global__ __launch_bounds__(192) void k_py_rows(PyRowArgs a) {
                 gn[gi][0] = g4[0]; gn[gi][1] = g4[1]; gn[gi][2] = g4[2]; gn[gi][3] = g4[3];
                 gb[gi][0] = b01[0]; gb[gi][1] = b01[1]; gb[gi][2] = b23[0]; gb[gi][3] = b23[1];
             }
-            plain4_finish<4>(PM, a.kinM, rim, pM, yM);
+            plain4_finish<4>(PM, a.kinM, rim, pM, yM, a.err);
 #pragma unroll
             for (int j = 0; j < 4; j++) {
                 R4[j] = wadd(rr[j], yM[j]);

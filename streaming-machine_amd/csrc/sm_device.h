@@ -36,6 +36,12 @@ SMD int bitlen_u(u64 a) { return a ? 64 - __clzll((long long)a) : 0; }
 SMD int bitlen_py(i64 v) { return bitlen_u(v < 0 ? (u64)0 - (u64)v : (u64)v); }
 // np.abs on int64 (INT64_MIN stays INT64_MIN)
 SMD i64 iabs64(i64 v) { return v < 0 ? (i64)((u64)0 - (u64)v) : v; }
+// foundation0/pythia_base2.py:63: the Pythia reference's rshift asserts |X| < 2^(62 + s) before a left shift
+// (s < 0).  Checked here element by element (the reference checks an array's largest |X| against its most
+// negative s, so it can stop where an element-wise check does not).
+SMD bool pyshift_fails(i64 x, i64 s) {
+    return s < 0 && (s < -62 ? x != 0 : (u64)iabs64(x) >= ((u64)1 << (62 + s)));
+}
 
 // ---- the tables' defining formulas, term for term as base2_convert.py:49-59 evaluates them (round half even)
 SMD int log2_entry(int m) { return (int)rint(log2(1.0 + (double)m / 65536.0) * 65536.0); }
@@ -137,7 +143,7 @@ SMD i64 gauge_ls(i64 s1, i64 s2, i64 ex, const Tables& tb) {
     i64 V = wadd(wsub(wmul(768, s2), wmul(s1, s1)), eps_term(tb.eps40, ex));
     return wadd(wsub(log2fix(V, tb) >> 1, tb.log768), wmul(ex, 65536));
 }
-// foundation0/pythia_base2.py:106-108  Pythia's gauge level LS = log2fix(V) >> 1 (no log2(d), no ex term: the
+// foundation0/pythia_base2.py:108-109  Pythia's gauge level LS = log2fix(V) >> 1 (no log2(d), no ex term: the
 // centred lane is d x - S1, not x - S1 / d) and EXP2[(-LS) & 0xFFFF], its power factor for every lane
 SMD i64 pgauge_ls_pow(i64 s1, i64 s2, i64 ex, const Tables& tb, i64& e2) {
     i64 V = wadd(wsub(wmul(768, s2), wmul(s1, s1)), eps_term(tb.eps40, ex));

@@ -29,8 +29,8 @@ enum { EPI_GAUGED = 0,       // power(pile, (we + ex + 16) 65536 - LS) + b      
 // k_gemv's MODE bits (batch 1): the complement machine, and two of the stages back in float64 (base2.py:10-11,
 // foundation0/pythia_base2.py:21-27: diagnostics that put one stage back to float; compared at the word level)
 enum { MODE_INV = 1,       // the complement machine (see race_beats)
-       MODE_FGAUGE = 2,    // gauge=float: GPT-2 base2.py:66-69, 110-113; Pythia foundation0/pythia_base2.py:94-96
-       MODE_FEDGE = 4 };   // edge=float: GPT-2's tanh form base2.py:79-80; Pythia's erf form pythia_base2.py:145-147
+       MODE_FGAUGE = 2,    // gauge=float: GPT-2 base2.py:66-69, 110-113; Pythia foundation0/pythia_base2.py:102-104
+       MODE_FEDGE = 4 };   // edge=float: GPT-2's tanh form base2.py:79-80; Pythia's erf form pythia_base2.py:144-146
 
 // Record of one position's intermediates (stream 0), written when the position equals *pos.
 struct Rec {
@@ -77,6 +77,7 @@ struct GemvArgs {
     // the next GEMV phase's plate, pulled into this block's L2 while this phase runs: block b requests the
     // 128-byte lines that the next kernel's blocks b, b + gridDim.x, .. read (block b of every launch runs on XCD
     // b % 8, and both grids are multiples of 8); null: none
+    int* err;                                  // the Pythia machine: its rshift assert sets SM_ERR_RANGE here
     const char* pf; int pf_lines; int pf_nblk;       // plate, lines a next-kernel block reads, the next grid
     int pf_total;                                    // the plate's lines (none past them is requested)
 };
@@ -135,7 +136,7 @@ struct AttArgs {
     const int* rec_pos; i64* ratt;
     // the Pythia machine: turns on the first rot dims of q and k, the scores' half-log2(head size)
     const int* cosT; const int* sinT;   // [npos][rot / 2] at 2^-30
-    const double* cosF; const double* sinF;   // turn=float: [npos][rot / 2] float64 (pythia_base2.py:117-118)
+    const double* cosF; const double* sinF;   // turn=float: [npos][rot / 2] float64 (pythia_base2.py:118-119)
     double* KF;         // arrival=float: [12][ctx][64] each cached key as float64 (its raw gauged value)
     int rot; i64 half; i64 ehalf;       // ehalf = EXP2[(-half) & 0xFFFF]
     // prompt rows: row r is position rowmap[r] & 0xFFFF of stream rowmap[r] >> 16 (null: row r is stream r at

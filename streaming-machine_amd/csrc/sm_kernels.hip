@@ -67,7 +67,7 @@ SMD double np_sum768(F val, int lane) {
     return r;
 }
 // the float gauge's size of a 768-wide row held as float64 in LDS: mean, then sqrt(mean((x - mean)^2) + 1e-5)
-// (base2.py:67, 111; foundation0/pythia_base2.py:95); the mean returned in mu
+// (base2.py:67, 111; foundation0/pythia_base2.py:103); the mean returned in mu
 SMD double np_sigma768(const double* xf, int lane, double& mu) {
     const double m = np_sum768([&](int i) { return xf[i]; }, lane) / 768.0;
     const double v = np_sum768([&](int i) { const double d = xf[i] - m; return d * d; }, lane) / 768.0;
@@ -80,7 +80,7 @@ SMD i64 edge_tanh(i64 H) {
     const double u = 0.7978845608028654 * (h + 0.044715 * pow(h, 3.0));
     return (i64)rint(0.5 * h * (1.0 + tanh(u)) * 65536.0);
 }
-// edge=float, Pythia (foundation0/pythia_base2.py:145-147): round(h 0.5 (1 + erf(h / sqrt(2))) 2^16)
+// edge=float, Pythia (foundation0/pythia_base2.py:144-146): round(h 0.5 (1 + erf(h / sqrt(2))) 2^16)
 SMD i64 edge_erf(i64 H) {
     const double h = (double)H * (1.0 / 65536.0);
     return (i64)rint(h * 0.5 * (1.0 + erf(h / 1.4142135623730951)) * 65536.0);
@@ -107,7 +107,7 @@ SMD void prologue_load(const GemvArgs& a, int tid, i64 (&v)[NIN / NT], int (&gq)
 // Pythia's prologue (foundation0/pythia_base2.py:100-110, 113): the gauge of the stream row R with the norm's own
 // gain and offset, then that row's water level.  Three block reductions: R's OR, the sums S1, S2, the gauged
 // row's OR.  c g < 2^41 and EXP2 < 2^17, so c g EXP2[f] is exact in 64 bits as the reference's int64 path is.
-// FG (gauge=float, :94-96): round((x - mu) / sigma g 2^ge 2^16) + b with x = R 2^-16 in float64 (xf: 768 doubles
+// FG (gauge=float, :102-104): round((x - mu) / sigma g 2^ge 2^16) + b with x = R 2^-16 in float64 (xf: 768 doubles
 // of LDS), in place of the first two reductions.
 template <int NT, int FG>
 SMD void prologue_py(const GemvArgs& a, int tid, const i64 (&v)[768 / NT], const int (&gq)[768 / NT],
@@ -448,12 +448,14 @@ __global__ __launch_bounds__(64 * WPB) void k_gemv(GemvArgs a) {
                 if (EPI == EPI_PILE) {
                     a.Y[j] = pile;
                 } else if (EPI == EPI_PLAIN_ADD) {
+                    if (a.err && pyshift_fails(pile, -(wec + ex + 16))) atomicOr(a.err, SM_ERR_RANGE);
                     const i64 add = wadd(rsh(pile, -(wec + ex + 16)), bc);
                     const i64 yb = INV ? a.Yb[j] : swc;          // (the plain machine's row was fetched with the tile)
                     const i64 r = INV ? wsub(yb, add) : wadd(yb, add);
                     a.Y[j] = r;
                     if (rec && a.rout) a.rout[j] = INV ? ~r : r;
                 } else if (EPI == EPI_PLAIN || EPI == EPI_PLAIN_EDGE || EPI == EPI_PHEAD) {
+                    if (a.err && pyshift_fails(pile, -(wec + ex + 16))) atomicOr(a.err, SM_ERR_RANGE);
                     i64 y = rsh(pile, -(wec + ex + 16));
                     if (EPI != EPI_PHEAD) y = wadd(y, bc);
                     if (EPI == EPI_PHEAD) {
@@ -872,7 +874,7 @@ SMD i64 dot16_mask(const v4i (&q)[4], unsigned mb) {
 // errors.
 // The turn of one lane's value (foundation0/pythia_base2.py:116-123): dimension i < rot/2 pairs with i + rot/2;
 // x' = x c - x_partner s (lower half) or x c + x_partner s (upper half).  Integer: rshift(., 30) with cos and sin
-// at 2^-30; FTURN (turn=float, :117-119): round(.) in float64 with the float64 tables.
+// at 2^-30; FTURN (turn=float, :118-120): round(.) in float64 with the float64 tables.
 template <int FTURN>
 SMD i64 turn1(i64 x, i64 partner, bool lower, i64 ci, i64 si, double cf, double sf) {
     if constexpr (FTURN) {
@@ -1137,7 +1139,7 @@ __global__ __launch_bounds__(NTHR, ONE ? 1 : 3) void k_attend(AttArgs a) {
 #pragma unroll
     for (int i = 0; i < NV; i++) vp[i] = buf_load4(rv, (unsigned)(g + 16 * i) * 256 + d4 * 16);
 
-    // scores (base2.py:94 / pythia_base2.py:133) and their maximum
+    // scores (base2.py:94 / pythia_base2.py:135) and their maximum
     const i64 eq = eqs;
     v4i qv[4];                                              // dimensions 16 qd .. + 15
 #pragma unroll
@@ -1268,7 +1270,7 @@ __global__ __launch_bounds__(NTHR, ONE ? 1 : 3) void k_attend(AttArgs a) {
     }
 }
 
-// arrival=float (base2.py:89-92; foundation0/pythia_base2.py:131-134), one stream, one block per head: scores
+// arrival=float (base2.py:89-92; foundation0/pythia_base2.py:130-133), one stream, one block per head: scores
 // (q 2^-16) . (k 2^-16) / 8 in float64 against every cached key (held as float64 in KF: its raw gauged value),
 // their exponentials after the row's maximum, each over their sum, out = round(sum a v).  Pythia's q and k are
 // turned first (the integer turn, or FTURN).  The additions inside the dot products and sums run in this

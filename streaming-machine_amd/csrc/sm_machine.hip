@@ -699,6 +699,7 @@ static int launch_step_pythia(sm_machine* m, int parts, bool rec) {
         base.tb = tb;
         base.pos = ctl + CTL_POS;
         base.rec_pos = ctl + CTL_RECPOS;
+        base.err = ctl + CTL_ERR;                      // the reference's rshift assert (pythia_base2.py:63)
         auto plate = [&](GemvArgs& a, const DevPlate& P, int k) {
             a.W = reinterpret_cast<const int4*>(P.W); a.we = P.e; a.bias = P.b; a.sw = P.sw; a.nout = P.nout; a.ntiles = P.ntiles;
             a.rx16 = m->r_x16 + (l * 4 + k) * 3072; a.rexls = m->r_exls + (l * 4 + k) * 2;
@@ -758,6 +759,7 @@ static int launch_step_pythia(sm_machine* m, int parts, bool rec) {
     if (parts & STEP_HEAD) {
         GemvArgs a{};
         a.tb = tb;
+        a.err = ctl + CTL_ERR;
         a.pos = ctl + CTL_POS; a.rec_pos = ctl + CTL_RECPOS;
         const DevPlate& P = m->head;
         a.W = reinterpret_cast<const int4*>(P.W); a.we = P.e; a.bias = P.b; a.sw = P.sw; a.nout = P.nout; a.ntiles = P.ntiles;
@@ -793,10 +795,12 @@ static int launch_step_pythia_batched(sm_machine* m, int parts, int nrows = 0,
         a.K = P.K; a.N = P.N; a.rows = B; a.RT = RT; a.W = P.W; a.csum = P.csum; a.we = P.e; a.bias = P.b;
         a.planes = planes; a.rowinfo = rowinfo; a.tb = tb;
         a.pos = ctl + CTL_POS; a.plen = ctl + CTL_PLEN; a.rec_pos = recp;
+        a.err = ctl + CTL_ERR;                         // the reference's rshift assert (pythia_base2.py:63)
         return a;
     };
     auto rows_args = [&]() {
         PyRowArgs a{};
+        a.err = ctl + CTL_ERR;
         a.rows = B; a.R = m->R; a.ew = m->ew; a.ee = m->ee; a.seq = m->seq; a.seq_stride = m->ctx + 1; a.pos = ctl + CTL_POS;
         a.tb = tb; a.rec_pos = recp; a.rowmap = rowmap;
         return a;

@@ -183,7 +183,7 @@ def pythia_layout(npz: dict, out_dir: str) -> str:
     np.asarray(npz["embed.e"]).astype(np.int32).tofile(os.path.join(out_dir, "embed.e"))
     for k in ("phi", "arrival", "log2", "exp2", "cos", "sin"):
         np.ascontiguousarray(npz[k]).astype(np.int64).tofile(os.path.join(out_dir, f"{k}.bin"))
-    # turn=float (foundation0/pythia_base2.py:117-118): numpy's float64 cos and sin of position x 10000^(-2i/rot)
+    # turn=float (foundation0/pythia_base2.py:118-119): numpy's float64 cos and sin of position x 10000^(-2i/rot)
     rot = int(npz["rot"])
     ang = np.arange(len(npz["cos"]))[:, None] * (10000.0 ** (-np.arange(0, rot, 2) / rot))[None, :]
     np.cos(ang).astype(np.float64).tofile(os.path.join(out_dir, "cosf.bin"))

@@ -175,3 +175,25 @@ def test_config5_thirty_two_streams(sm, py_full_dir, py_full_npz, pgolden):
             assert np.array_equal(m.read("ek", l, 31, p), ek)
             assert np.array_equal(m.read("v", l, 31, p), v)
     m.close()
+
+
+@pytest.mark.parametrize("streams", [1, 3])
+def test_rshift_assert(sm, py_small_npz, tmp_path, streams):
+    """foundation0/pythia_base2.py:63: a left shift past 2^(62 + s) stops the reference.  A planted head power of
+    two (word 5: 2^40) turns the head's plain shift into a left shift of 40 and more places: the oracle stops, and
+    the device reports SM_E_OVERFLOW (batch 1: the GEMV head; 3 streams: the MFMA head)"""
+    from oracle.pythia import PythiaOracle
+    npz = dict(py_small_npz)
+    e = np.array(npz["head.e"]).copy()
+    e[5] = 40
+    npz["head.e"] = e
+    prompt = sm.prompt_ids(50, 8, 1000)
+    with pytest.raises(ArithmeticError):
+        PythiaOracle(npz).generate(prompt, 4)
+    d = str(tmp_path / f"py_shift_{streams}")
+    sm.pythia.pythia_layout(npz, d)
+    m = sm.Machine(d, max_ctx=32, max_streams=streams)
+    with pytest.raises(sm.SmError) as ex:
+        m.streams([prompt] * streams, 4)
+    assert ex.value.code == -6
+    m.close()
