@@ -152,6 +152,48 @@ def convert_pythia(sd: dict, cfg: dict, start: dict | None = None) -> dict:
     return out
 
 
+def select_plates(npz: dict, plates: str = "finished") -> dict:
+    """foundation0/pythia_base2.py:44-46's `plates=`: "finished" (the converted checkpoint's plates, biases, norms
+    and word tables) or "start" (the start checkpoint's, which the converter keeps beside them as .s / .bs / .gs on
+    the same powers of two).  Its third choice, "built" (finished - start, digit for digit), needs 17 bits a digit,
+    and the device's plates are int16: refused."""
+    if plates == "finished":
+        return dict(npz)
+    if plates != "start":
+        raise ValueError(f"plates={plates}: finished or start (built needs 17-bit digits)")
+    out = dict(npz)
+    for k in npz:
+        for tail, start in ((".w", ".s"), (".b", ".bs"), (".g", ".gs")):
+            if k.endswith(tail) and k[:-len(tail)] + start in npz:
+                out[k] = npz[k[:-len(tail)] + start]
+    return out
+
+
+def shuffle_order(npz: dict, seed: int = 12345) -> dict:
+    """foundation0/pythia_base2.py:42, 48-58's `order=shuffle` (an order-free check): the stream's 768 lanes in the
+    order default_rng(seed).permutation(768); every plate that reads the stream (qkv, fc, the head) takes its rows
+    in that order, every plate that writes it (proj, mproj) its columns, powers and biases, the norms their gains
+    and offsets, the embed table its columns.  Every sum is of whole numbers, so every pile is the same number in
+    its new place: the words and the head's piles are the plain machine's."""
+    d = int(npz["d"])
+    perm = np.random.default_rng(seed).permutation(d)
+    out = dict(npz)
+    for l in range(int(npz["L"])):
+        for nm in P_NORMS:
+            k = f"{nm}.{l}"
+            out[k + ".g"], out[k + ".b"] = np.asarray(npz[k + ".g"])[perm], np.asarray(npz[k + ".b"])[perm]
+        for nm in ("qkv", "fc"):
+            out[f"{nm}.{l}.w"] = np.ascontiguousarray(np.asarray(npz[f"{nm}.{l}.w"])[perm])
+        for nm in ("proj", "mproj"):
+            k = f"{nm}.{l}"
+            out[k + ".w"] = np.ascontiguousarray(np.asarray(npz[k + ".w"])[:, perm])
+            out[k + ".e"], out[k + ".b"] = np.asarray(npz[k + ".e"])[perm], np.asarray(npz[k + ".b"])[perm]
+    out["lnf.g"], out["lnf.b"] = np.asarray(npz["lnf.g"])[perm], np.asarray(npz["lnf.b"])[perm]
+    out["head.w"] = np.ascontiguousarray(np.asarray(npz["head.w"])[perm])
+    out["embed.w"] = np.ascontiguousarray(np.asarray(npz["embed.w"])[:, perm])
+    return out
+
+
 def pythia_layout(npz: dict, out_dir: str) -> str:
     """Write a converted Pythia model as a device-image directory for the HIP library.  The reference runs this
     machine on the CPU only and has no device format for it; this one extends base2_gpu.py's:

@@ -197,3 +197,31 @@ def test_rshift_assert(sm, py_small_npz, tmp_path, streams):
         m.streams([prompt] * streams, 4)
     assert ex.value.code == -6
     m.close()
+
+
+@pytest.mark.parametrize("streams", [1, 2])
+def test_plate_and_order_switches(sm, tmp_path, streams):
+    """pythia_base2.py's plates=finished|start and order=shuffle (the finished-and-start model of
+    modes_golden.json): words and every recorded intermediate of the last position against the reference run
+    with each switch (the shuffled machine's intermediates in their shuffled places)"""
+    from test_oracle_pythia import _modes, modes_npz
+    g = _modes()
+    if g is None:
+        pytest.skip("modes_golden.json not written")
+    for case in g["cases"]:
+        d = str(tmp_path / f"{case['name']}_{streams}")
+        sm.pythia.pythia_layout(modes_npz(sm, case), d)
+        m = sm.Machine(d, max_ctx=32, max_streams=streams)
+        last = case["records"]["last"]
+        m.reset()
+        m.record_at(last["position"])
+        for s in range(streams):
+            m.prefill(case["prompt"], s)
+        got = m.generate(len(case["words"]))
+        assert all([int(w) for w in row] == case["words"] for row in got), case["name"]
+        rec = machine_record(m, np.zeros(768, dtype=np.int64))
+        m.close()
+        keys = [k for k in last if k in rec and k not in ("stream.0", "out.proj.0")]
+        assert len(keys) > 200
+        bad = sorted(k for k in keys if rec[k] != last[k])
+        assert not bad, f"{case['name']}: {len(bad)} intermediates differ, first {bad[:6]}"

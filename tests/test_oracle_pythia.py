@@ -3,9 +3,13 @@ itself, plus negative controls that plant mistakes in the oracle's inputs and sh
 from __future__ import annotations
 
 import hashlib
+import os
 
 import numpy as np
 import pytest
+
+from conftest import REPO
+from oracle.pythia import PythiaOracle
 
 
 def h64(a) -> str:
@@ -125,3 +129,34 @@ def test_planted_gain_offset_is_caught(py_small_npz, pgolden):
     _, got = run_case(_planted(py_small_npz, **{"ln2.3.g": g}), case)
     want = case["records"]["last"]
     assert got["gauge.ln2.2"] == want["gauge.ln2.2"] and got["gauge.ln2.3"] != want["gauge.ln2.3"]
+
+
+def _modes():
+    import json
+    path = os.path.join(REPO, "tests", "golden", "modes_golden.json")
+    return json.load(open(path)) if os.path.exists(path) else None
+
+
+def modes_npz(sm, case):
+    """the plate / order switch of a modes_golden.json case applied to the finished-and-start model"""
+    fin, cfg = sm.pythia.random_pythia(seed=5, vocab=1000)
+    start, _ = sm.pythia.random_pythia(seed=6, vocab=1000)
+    npz = sm.pythia.convert_pythia(fin, cfg, start=start)
+    sw = dict(s.split("=") for s in case["switches"])
+    npz = sm.pythia.select_plates(npz, sw.get("plates", "finished"))
+    return sm.pythia.shuffle_order(npz) if sw.get("order") == "shuffle" else npz
+
+
+def test_plate_and_order_switches(sm):
+    """pythia_base2.py's plates=start and order=shuffle (its order-free check) as package transforms of the
+    converted model: the oracle on them gives the words the reference gave with those switches"""
+    g = _modes()
+    if g is None:
+        pytest.skip("modes_golden.json not written")
+    fin, cfg = sm.pythia.random_pythia(seed=5, vocab=1000)
+    start, _ = sm.pythia.random_pythia(seed=6, vocab=1000)
+    assert sm.array_digest(sm.pythia.convert_pythia(fin, cfg, start=start)) == g["model"]["digest"]
+    for case in g["cases"]:
+        assert PythiaOracle(modes_npz(sm, case)).generate(case["prompt"], len(case["words"])) == case["words"], case["name"]
+    with pytest.raises(ValueError):
+        sm.pythia.select_plates({}, "built")
