@@ -18,6 +18,9 @@ Printed: one JSON line with the driver's fields plus
                  with the bytes this layout reads beside them
   cold           the same profiled step with 1 GiB streamed through the device between steps (the 256 MB
                  Infinity Cache holds none of the step's bytes), beside the warm figures
+  head_read      the machine's default read of the word table at batch 1 is the collapsing top read
+                 (base2_stream_fr.swift:4-15; measured faster than the full read here): the words left to finish
+                 after the high bytes, step by step, and the same workload with the full read beside it
   prompt_included  words per second counting the prompt pass, as the reference also reports
   batched        64 streams in lockstep (int8 MFMA banks), 32-token prompts, 128 words each; every word of
                  streams 0 and 1 checked against base2.py's, of streams 31 and 63 against the oracle's fixture
@@ -162,7 +165,7 @@ def dominant(table: dict, where: str) -> dict:
 
 
 # ---- batch 1 (config 1) ----
-def b1_leg(sm, lay, steps_req: int, warmup: int, prompt, want, cold_steps: int = 15, top: str = "plain"):
+def b1_leg(sm, lay, steps_req: int, warmup: int, prompt, want, cold_steps: int = 15, top: str = "auto"):
     import torch
     m = sm.Machine(lay, max_ctx=64, graph_steps=WORDS - 1, prefill_rows=PREFILL_ROWS, use_graph=not PLAIN, top=top)
 
@@ -214,7 +217,7 @@ def b1_leg(sm, lay, steps_req: int, warmup: int, prompt, want, cold_steps: int =
     ctx = PROMPT + WORDS / 2.0                     # mean context of the decode steps (9..23)
     table = kernel_table(times, WORDS - 1, lambda k: b1_kernel_bytes(k, ctx))
     survivors = []
-    if top == "fr":                                # the words left to finish after the high bytes, step by step
+    if mp.top_read:                                # the words left to finish after the high bytes, step by step
         mp.reset()
         mp.prefill(prompt)
         mp.generate(1)
@@ -242,7 +245,7 @@ def b1_leg(sm, lay, steps_req: int, warmup: int, prompt, want, cold_steps: int =
     ctable = kernel_table(ctimes, cold_steps, lambda k: b1_kernel_bytes(k, ctx))
     ms = 1000.0 * total / steps
     return {"tok_s": steps / total, "ms": ms, "steps": steps, "prompt_ms": 1000.0 * prompt_s / nseq,
-            "table": table, "cold": ctable, "ctx": ctx}
+            "table": table, "cold": ctable, "ctx": ctx, "survivors": survivors}
 
 
 # ---- batched legs (configs 4 and 5) ----
@@ -552,8 +555,8 @@ def main():
     ap.add_argument("--no-batched", action="store_true", help="skip the 64-stream leg")
     ap.add_argument("--no-pythia", action="store_true", help="skip the Pythia 32-stream leg")
     ap.add_argument("--no-micro", action="store_true", help="skip the GEMV and attention microbenchmarks")
-    ap.add_argument("--no-top", action="store_true", help="skip the collapsing top read's batch-1 leg")
-    ap.add_argument("--only", choices=("b1", "b1top", "b64", "pythia", "gemv", "attention"), default="",
+    ap.add_argument("--no-full-read", action="store_true", help="skip the batch-1 leg with the full read of the word table")
+    ap.add_argument("--only", choices=("b1", "b1full", "b64", "pythia", "gemv", "attention"), default="",
                     help="profiling: run one leg and print only its result (not the bench line)")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MB",
                     help="profiling: first copy MB MiB device to device (calibrates HBM byte counters)")
@@ -604,13 +607,13 @@ def main():
         return
     prompt = sm.prompt_ids(1, PROMPT)
     want = fixture_cases("base2_golden.json")["c1_p8_w16"]["words"]      # base2.py's own words for this sequence
-    top = None
-    if (args.only in ("", "b1top") and not args.no_top) and not PLAIN:
-        top = b1_leg(sm, lay, args.steps, args.warmup, prompt, want, cold_steps=0, top="fr")
-        log(f"batch 1, collapsing top read: {top['tok_s']:.1f} tokens/s, {top['ms']:.4f} ms/step")
-        if args.only == "b1top":
-            print(json.dumps({"value": round(top["tok_s"], 2), "ms_per_step": round(top["ms"], 4), "kernels": top["table"],
-                              "survivors": top["survivors"]}), flush=True)
+    full = None
+    if (args.only in ("", "b1full") and not args.no_full_read) and not PLAIN:
+        full = b1_leg(sm, lay, args.steps, args.warmup, prompt, want, cold_steps=0, top="plain")
+        log(f"batch 1, full read of the word table: {full['tok_s']:.1f} tokens/s, {full['ms']:.4f} ms/step")
+        if args.only == "b1full":
+            print(json.dumps({"value": round(full["tok_s"], 2), "ms_per_step": round(full["ms"], 4),
+                              "kernels": full["table"]}), flush=True)
             return
     b1 = b1_leg(sm, lay, args.steps, args.warmup, prompt, want)
     log(f"batch 1: {b1['tok_s']:.1f} tokens/s, {b1['ms']:.4f} ms/step")
@@ -630,7 +633,7 @@ def main():
                         for k, r in b1["cold"].items()}}
     if args.only == "b1":
         print(json.dumps({"value": round(b1["tok_s"], 2), "ms_per_step": round(b1["ms"], 4), "kernels": table,
-                          "cold": cold, "prompt_ms": round(b1["prompt_ms"], 3)}), flush=True)
+                          "cold": cold, "prompt_ms": round(b1["prompt_ms"], 3), "survivors": b1["survivors"]}), flush=True)
         return
     batched = None if args.no_batched else batched_leg(sm, lay)
     if batched:
@@ -658,16 +661,17 @@ def main():
                             "unit": "tokens/s", "prompt_ms": round(b1["prompt_ms"], 3),
                             "note": "16 words per sequence over the prompt pass (7 prompt rows through the int8 MFMA "
                                     "banks, then the first word's step) plus 15 decode steps"},
-        "top_read": None if top is None else {
-            "value": round(top["tok_s"], 2), "unit": "tokens/s", "ms_per_step": round(top["ms"], 4),
-            "note": "the same batch-1 workload with the collapsing top read (Machine(top='fr'), base2_stream_fr.swift:"
-                    "4-15): the high-byte plane of every word, exact bounds, the low bytes of the words that can still "
-                    "win; words gated on base2.py's like the main line",
-            "head_us_per_step": {"full_read": round(sum(table[k]["us_per_step"] for k in ("head", "race") if k in table), 2),
-                                 "top_read": round(sum(top["table"][k]["us_per_step"] for k in ("head.top", "race.top")
-                                                       if k in top["table"]), 2)},
-            "kernels": {k: v for k, v in top["table"].items() if k in ("head.top", "race.top")},
-            "survivors_per_step": top["survivors"]},
+        "head_read": {
+            "default": "the collapsing top read (base2_stream_fr.swift:4-15): the high-byte plane of every word, exact "
+                       "bounds, the low bytes of the words that can still win (the main line)",
+            "survivors_per_step": b1["survivors"],
+            "head_us_per_step": round(sum(table[k]["us_per_step"] for k in ("head.top", "race.top") if k in table), 2),
+            "full_read": None if full is None else {
+                "value": round(full["tok_s"], 2), "unit": "tokens/s", "ms_per_step": round(full["ms"], 4),
+                "head_us_per_step": round(sum(full["table"][k]["us_per_step"] for k in ("head", "race")
+                                              if k in full["table"]), 2),
+                "note": "the same workload with the whole word table read every step (Machine(top='plain')); words "
+                        "gated on base2.py's like the main line"}},
         "batched": batched,
         "pythia": pyleg,
         "gemv": gemv,

@@ -61,10 +61,12 @@ typedef struct {
                               compared with the reference at the word level.  max_streams 1, prefill_rows 0, inv 0;
                               turn is the Pythia machine's (its layout's cosf.bin / sinf.bin).  With arrival the
                               cache holds each key as float64, not k16 / ek */
-    int32_t top_read;      /* 1: the collapsing top read (base2_stream_fr.swift:4-15, its top=fr): the head reads
-                              the high-byte plane of the word table (w >> 8) for every word, bounds each word's
-                              score exactly, and reads the low bytes (w & 255) of the words that can still win;
-                              the same words as the full read.  GPT-2, max_streams 1, head_grid 393..512 */
+    int32_t top_read;      /* the head's read of the word table.  1: the collapsing top read (base2_stream_fr.swift:
+                              4-15, its top=fr): the high-byte plane (w >> 8) for every word, each word's score
+                              bounded exactly, the low bytes (w & 255) of the words that can still win; the same
+                              words as the full read (GPT-2, max_streams 1, no inv or float stages, head_grid
+                              393..512).  0: the full read.  2: the collapsing read where it applies, else the
+                              full read (the default: measured faster at batch 1) */
 } sm_config;
 
 enum { SM_FLOAT_GAUGE = 1, SM_FLOAT_EDGE = 2, SM_FLOAT_ARRIVAL = 4, SM_FLOAT_TURN = 8 };
@@ -122,7 +124,7 @@ enum {
 int sm_read(sm_machine* m, int32_t what, int32_t layer, int32_t stream, int32_t pos, void* dst, size_t bytes);
 
 /* Head-launch timing gathered with profile = 1: launches seen and their summed duration (microseconds,
- * HIP events stamped by each head dispatch).  clear = 1 empties the kernel-timing table afterwards.  Replaces fr2's
+ * HIP events stamped by each head dispatch; with the collapsing top read, its first stage's).  clear = 1 empties the kernel-timing table afterwards.  Replaces fr2's
  * bench= timing (base2_stream_fr2.swift:1060-1075). */
 int sm_profile(sm_machine* m, int64_t* n_heads, double* head_us, int32_t clear);
 
@@ -141,6 +143,9 @@ int sm_profile_kernels(char* names, int32_t names_bytes, int64_t* launches, doub
 /* Which machine a layout holds: 0 the GPT-2 machine of base2.py, 1 the Pythia machine of
  * foundation0/pythia_base2.py (a layout whose manifest says "kind": "pythia"); negative on error. */
 int sm_model_kind(const sm_machine* m);
+/* Which read of the word table the machine's decode steps use (base2_stream_fr.swift's top= switch, resolved
+ * from sm_config.top_read): 1 the collapsing top read, 0 the full read; negative on error. */
+int sm_top_read(const sm_machine* m);
 int sm_info(const sm_machine* m, int32_t* vocab, int32_t* max_ctx, int32_t* max_streams, int32_t* n_pos,
             int32_t* arith_tables);
 

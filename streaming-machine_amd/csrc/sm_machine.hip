@@ -1041,7 +1041,7 @@ static int run_prefill(sm_machine* m, int npos) {
 extern "C" int sm_create(const char* layout_dir, const sm_config* cfg, sm_machine** out) {
     if (!layout_dir || !out) return fail(SM_E_ARG, "sm_create: null argument");
     *out = nullptr;
-    sm_config c{1, 1024, 1, 0, 16, 0, 0, 64, 0, 0, 0};
+    sm_config c{1, 1024, 1, 0, 16, 0, 0, 64, 0, 0, 2};
     if (cfg) c = *cfg;
     if (c.max_streams < 1 || c.max_streams > 64) return fail(SM_E_ARG, "sm_create: max_streams must be in [1, 64]");
     if (c.prefill_rows < 0 || c.prefill_rows > 64) return fail(SM_E_ARG, "sm_create: prefill_rows must be in [0, 64]");
@@ -1070,7 +1070,9 @@ extern "C" int sm_create(const char* layout_dir, const sm_config* cfg, sm_machin
     if (c.float_stages && (c.max_streams != 1 || c.prefill_rows != 0 || c.inv))
         return fail(SM_E_ARG, "sm_create: the float stages run with max_streams 1 and prefill_rows 0, without inv");
     if ((c.float_stages & SM_FLOAT_TURN) && !py) return fail(SM_E_ARG, "sm_create: turn=float is the Pythia machine's");
-    if (c.top_read && (py || c.max_streams != 1 || c.inv || c.float_stages))
+    if (c.top_read < 0 || c.top_read > 2) return fail(SM_E_ARG, "sm_create: top_read must be 0, 1 or 2");
+    if (c.top_read == 2 && (py || c.max_streams != 1 || c.inv || c.float_stages)) c.top_read = 0;   // where it applies
+    if (c.top_read == 1 && (py || c.max_streams != 1 || c.inv || c.float_stages))
         return fail(SM_E_ARG, "sm_create: the collapsing top read runs GPT-2 with max_streams 1, without inv or float stages");
     auto find = [&](const std::string& n) -> const BankInfo* {
         for (auto& b : banks) if (b.name == n) return &b;
@@ -1109,6 +1111,16 @@ extern "C" int sm_create(const char* layout_dir, const sm_config* cfg, sm_machin
     const BankInfo* hb = find("head");
     if (!hb || hb->nin != 768 || hb->nout <= 0 || hb->nout > (1 << 24)) return bail(fail(SM_E_IO, "manifest.json: head bank missing or of the wrong shape"));
     m->vocab = (int)hb->nout;
+    {   // the top read: every wave of its first stage finishes at most TOP_ITERS tiles, and its race reads at most
+        // 512 blocks (top_read 2 falls back to the full read where the head grid does not allow it)
+        const long long nt = (m->vocab + HEAD_TC - 1) / HEAD_TC, hg = c.head_grid > 0 ? c.head_grid : 512;
+        const bool fits = hg <= 512 && hg * HEAD_WPB * TOP_ITERS >= nt;
+        if (c.top_read == 2 && !fits) c.top_read = 0;
+        if (c.top_read == 1 && !fits)
+            return bail(fail(SM_E_ARG, "sm_create: the top read needs head_grid in [" +
+                                           std::to_string((nt + HEAD_WPB * TOP_ITERS - 1) / (HEAD_WPB * TOP_ITERS)) + ", 512]"));
+        m->cfg.top_read = c.top_read;
+    }
     {
         std::vector<int16_t> w; std::vector<int32_t> e; std::vector<i64> b;
         if ((rc = read_array(dir + "head.wc", w, (size_t)768 * m->vocab)) || (rc = read_array(dir + "head.e", e, m->vocab)))
@@ -1205,11 +1217,7 @@ extern "C" int sm_create(const char* layout_dir, const sm_config* cfg, sm_machin
     m->ctx = c.max_ctx < m->npos ? c.max_ctx : m->npos;
     m->head_grid = c.head_grid > 0 ? c.head_grid : 512;     // two blocks per CU (measured best)
     if (m->head_grid > 1024) return bail(fail(SM_E_ARG, "sm_create: head_grid at most 1024"));
-    if (c.top_read) {      // every wave finishes at most TOP_ITERS tiles; the race reads at most 512 blocks
-        const long long nt = (m->vocab + HEAD_TC - 1) / HEAD_TC;
-        if (m->head_grid > 512 || (long long)m->head_grid * HEAD_WPB * TOP_ITERS < nt)
-            return bail(fail(SM_E_ARG, "sm_create: the top read needs head_grid in [" +
-                                           std::to_string((nt + HEAD_WPB * TOP_ITERS - 1) / (HEAD_WPB * TOP_ITERS)) + ", 512]"));
+    if (c.top_read) {
         const size_t cap = (size_t)HEAD_WPB * TOP_ITERS * HEAD_TC, g = m->head_grid;
         if ((rc = dalloc(&m->cand_j, g * cap)) || (rc = dalloc(&m->cand_h, g * cap)) || (rc = dalloc(&m->cand_c, g * cap)) ||
             (rc = dalloc(&m->top_x, (size_t)768)) || (rc = dalloc(&m->top_f, (size_t)4)) || (rc = dalloc(&m->top_n, (size_t)1)) ||
@@ -1390,7 +1398,7 @@ extern "C" int sm_profile(sm_machine* m, int64_t* n_heads, double* head_us, int3
     long long n = 0;
     double us = 0.0;
     for (size_t i = 0; i < g_kt.names.size(); i++)
-        if (g_kt.names[i] == "head") { n = g_kt.n[i]; us = g_kt.us[i]; }
+        if (g_kt.names[i] == "head" || g_kt.names[i] == "head.top") { n += g_kt.n[i]; us += g_kt.us[i]; }
     if (n_heads) *n_heads = n;
     if (head_us) *head_us = us;
     if (clear)
@@ -1500,6 +1508,11 @@ extern "C" int sm_read(sm_machine* m, int32_t what, int32_t layer, int32_t strea
 extern "C" int sm_model_kind(const sm_machine* m) {
     if (!m) return fail(SM_E_ARG, "sm_model_kind: null machine");
     return m->kind;
+}
+
+extern "C" int sm_top_read(const sm_machine* m) {
+    if (!m) return fail(SM_E_ARG, "sm_top_read: null machine");
+    return m->cfg.top_read ? 1 : 0;
 }
 
 extern "C" int sm_info(const sm_machine* m, int32_t* vocab, int32_t* max_ctx, int32_t* max_streams, int32_t* n_pos,

@@ -68,6 +68,7 @@ def lib():
         L.sm_read.argtypes = [vp, i32, i32, i32, i32, vp, ctypes.c_size_t]
         L.sm_info.argtypes = [vp, i32p, i32p, i32p, i32p, i32p]
         L.sm_model_kind.argtypes = [vp]
+        L.sm_top_read.argtypes = [vp]
         L.sm_tables_mode.argtypes = [vp, i32, i32p]
         L.sm_profile.argtypes = [vp, i64p, ctypes.POINTER(ctypes.c_double), i32]
         L.sm_profile_stages.argtypes = [i32]
@@ -113,9 +114,10 @@ class Machine:
       (base2_stream.swift:274: the prompt through each layer at once); 0 runs it position by position.
       inv: the complement machine (base2_stream.swift:26 `inv`): stream, plates and lights held bit-complemented on
       the device; the same words (GPT-2, one stream, prefill_rows=0).
-      top: "plain" (the whole word table read a step) or "fr" (base2_stream_fr.swift's collapsing top read: the
-      high bytes of every word, then the low bytes of the words that can still win; the same words; GPT-2, one
-      stream).  .top() gives the last step's survivors.
+      top: "fr" (base2_stream_fr.swift's collapsing top read: the high bytes of every word, then the low bytes of
+      the words that can still win; the same words; GPT-2, one stream, no inv or float stages), "plain" (the
+      whole word table read a step), or "auto" (the default: the collapsing read where it applies, measured
+      faster at batch 1).  .top_read says which runs; .top() gives the last step's survivors.
       .stream(prompt_ids, n_words) -> list of words        (base2.py:123's loop, KV-cached on the device)
       .forward(ids) -> word                                 (base2.py:forward's contract)
       .reset(); .prefill(ids, stream=0); .generate(n_words) -> int32 [n_streams][n_words]
@@ -129,17 +131,18 @@ class Machine:
     def __init__(self, layout_dir: str, max_ctx: int = 1024, max_streams: int = 1, use_graph: bool = True,
                  head_grid: int = 0, graph_steps: int = 16, profile: bool = False, memory_tables: bool = True,
                  prefill_rows: int = 64, gauge: str = "int", edge: str = "int", arrival: str = "int", turn: str = "int",
-                 inv: bool = False, top: str = "plain"):
+                 inv: bool = False, top: str = "auto"):
         fs = 0
         for name, v in (("gauge", gauge), ("edge", edge), ("arrival", arrival), ("turn", turn)):
             if v not in ("int", "float"):
                 raise ValueError(f"{name}={v}: each stage is int or float")
             fs |= FLOAT_STAGES[name] if v == "float" else 0
-        if top not in ("plain", "fr"):
-            raise ValueError(f"top={top}: plain or fr")
+        if top not in ("plain", "fr", "auto"):
+            raise ValueError(f"top={top}: plain, fr or auto")
         self.L = lib()
         cfg = SmConfig(max_streams, max_ctx, 1 if use_graph else 0, head_grid, graph_steps, 1 if profile else 0,
-                       0 if memory_tables else 1, prefill_rows, 1 if inv else 0, fs, 1 if top == "fr" else 0)
+                       0 if memory_tables else 1, prefill_rows, 1 if inv else 0, fs,
+                       dict(plain=0, fr=1, auto=2)[top])
         h = vp()
         check(self.L.sm_create(os.fsencode(layout_dir), ctypes.byref(cfg), ctypes.byref(h)))
         self.h = h
@@ -150,6 +153,9 @@ class Machine:
         k = self.L.sm_model_kind(self.h)
         check(min(k, 0))
         self.kind = ("gpt2", "pythia")[k]
+        t = self.L.sm_top_read(self.h)
+        check(min(t, 0))
+        self.top_read = bool(t)
 
     def close(self):
         if getattr(self, "h", None):
