@@ -74,9 +74,9 @@ struct GemvArgs {
     // its facts (tf: ex, LS, EXP2 of the fine part)
     int* cand_j; i64* cand_h; i64* cand_c;
     int* tx; i64* tf;
-    // the next GEMV phase's plate, pulled into this block's L2 while this phase runs: block b requests the
-    // 128-byte lines that the next kernel's blocks b, b + gridDim.x, .. read (block b of every launch runs on XCD
-    // b % 8, and both grids are multiples of 8); null: none
+    // the next GEMV phase's plate, requested while this phase runs: block b requests the 128-byte lines that the
+    // next kernel's blocks b, b + gridDim.x, .. read first.  The lines pass through the memory-side Infinity Cache,
+    // which then serves the next phase's first requests (its own L2 misses them: measured by FETCH_SIZE); null: none
     int* err;                                  // the Pythia machine: its rshift assert sets SM_ERR_RANGE here
     const char* pf; int pf_lines; int pf_nblk;       // plate, lines a next-kernel block reads, the next grid
     int pf_total;                                    // the plate's lines (none past them is requested)

@@ -623,7 +623,7 @@ static void launch_embed1(sm_machine* m) {
     else launch(m->cfg.profile, "embed", k_embed1<0>, dim3(1), dim3(256), 0, m->st, race1_args(m));
 }
 
-// the next GEMV phase's plate for this phase's blocks to pull into their L2 (GemvArgs::pf): its first wpb tiles
+// the next GEMV phase's plate for this phase's blocks to request early (GemvArgs::pf): its first wpb tiles
 // of every block of its grid
 static void set_pf(GemvArgs& a, const DevPlate& next, int wpb, int grid) {
     a.pf = reinterpret_cast<const char*>(next.W);
