@@ -43,8 +43,9 @@ typedef struct {
     int32_t graph_steps;   /* decode steps per captured graph (0: 16) */
     int32_t profile;       /* 1: launch the decode steps kernel by kernel (no graphs), each launch stamped with a HIP
                               event pair by its own dispatch (sm_profile, sm_profile_kernels) */
-    int32_t table_mode;    /* 0: read the tables from memory; 1: recompute each entry from its formula when every
-                              loaded entry matches it (checked on the device at create), else read the tables */
+    int32_t table_mode;    /* the tables are read from memory; every loaded entry is compared with its defining
+                              formula on the device at create.  1: refuse tables that differ (SM_E_IO); 0: accept
+                              them (sm_info reports the check) */
     int32_t prefill_rows;  /* 0: the prompt runs position by position through the decode step; 1..64: every prompt
                               position but the last runs through the int8 MFMA banks that many rows a pass, each
                               weight read shared by the pass's rows (base2_stream.swift:74-91, 274-275: the
@@ -138,8 +139,8 @@ int sm_profile_stages(int32_t on);
 int sm_profile_kernels(char* names, int32_t names_bytes, int64_t* launches, double* total_us, int32_t max, int32_t* n,
                        int32_t clear);
 
-/* Facts about a created machine: vocab, max_ctx, max_streams, rows of the position table, and whether the
- * table entries are recomputed from their formulas (1) or read from memory (0). */
+/* Facts about a created machine: vocab, max_ctx, max_streams, rows of the position table, and whether every
+ * loaded table entry equals its defining formula (base2_convert.py:48-61, checked on the device at create). */
 /* Which machine a layout holds: 0 the GPT-2 machine of base2.py, 1 the Pythia machine of
  * foundation0/pythia_base2.py (a layout whose manifest says "kind": "pythia"); negative on error. */
 int sm_model_kind(const sm_machine* m);
@@ -147,7 +148,7 @@ int sm_model_kind(const sm_machine* m);
  * from sm_config.top_read): 1 the collapsing top read, 0 the full read; negative on error. */
 int sm_top_read(const sm_machine* m);
 int sm_info(const sm_machine* m, int32_t* vocab, int32_t* max_ctx, int32_t* max_streams, int32_t* n_pos,
-            int32_t* arith_tables);
+            int32_t* tables_verified);
 
 const char* sm_last_error(void);
 
@@ -161,9 +162,9 @@ typedef struct sm_tables sm_tables;
 int sm_tables_create(const int64_t* phi, const int64_t* arrival, int32_t alen, const int64_t* log2t,
                      const int64_t* exp2t, int64_t log2_768, int64_t eps40, sm_tables** out);
 int sm_tables_destroy(sm_tables* t);
-/* force_memory: 1 read the tables from memory (the default), 0 recompute verified entries, -1 leave as is;
- * reports the mode in use */
-int sm_tables_mode(sm_tables* t, int32_t force_memory, int32_t* arith_tables);
+/* 1 when every entry of the tables equals its defining formula (base2_convert.py:48-61), checked on the device at
+ * sm_tables_create; 0 when one differs; negative on error */
+int sm_tables_verified(const sm_tables* t);
 
 int sm_stage_rshift(const int64_t* x, const int64_t* s, int64_t* out, int64_t n, void* stream);          /* base2.py:18-22 */
 int sm_stage_log2fix(const sm_tables* t, const int64_t* v, int64_t* out, int64_t n, void* stream);       /* base2.py:42-48 */

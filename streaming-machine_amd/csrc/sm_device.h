@@ -10,14 +10,13 @@ typedef unsigned long long u64;
 
 #define SMD __device__ __forceinline__
 
-// The machine's four tables (base2_convert.py:48-61).  When `arith` is set, every entry is recomputed from its
-// defining formula in double precision instead of being read from memory; sm_create sets it only after an
-// exhaustive device check found every entry of the loaded tables equal to the recomputed one, so both paths give
-// the same integers.  The recomputation takes a dependent memory read off each phase's critical path.
+// The machine's four tables (base2_convert.py:48-61), read from memory.  (Recomputing an entry from its formula in
+// float64 on the device measured slower than the read everywhere it was tried: the gauge's once-a-row entries, the
+// edge's, the arrivals'.  The formulas below serve only the create-time check that the loaded tables are the
+// reference's.)
 struct Tables {
     const int* LOG2; const int* EXP2; const int* PHI; const int* ARR;
     int alen; i64 log768; i64 eps40;
-    int arith;
     // derived, exact integer compositions of the tables above (built on the host at create):
     //   GPOW[r * 65536 + m] = EXP2[(log768 - ((r 65536 + LOG2[m]) >> 1)) & 0xFFFF]   the gauge's power factor
     //   HPOW[m]             = EXP2[(-LOG2[m]) & 0xFFFF]                              the arrivals' divisor
@@ -43,17 +42,18 @@ SMD bool pyshift_fails(i64 x, i64 s) {
     return s < 0 && (s < -62 ? x != 0 : (u64)iabs64(x) >= ((u64)1 << (62 + s)));
 }
 
-// ---- the tables' defining formulas, term for term as base2_convert.py:49-59 evaluates them (round half even)
+// ---- the tables' defining formulas, term for term as base2_convert.py:49-59 evaluates them (round half even);
+// the create-time check compares every loaded entry with them
 SMD int log2_entry(int m) { return (int)rint(log2(1.0 + (double)m / 65536.0) * 65536.0); }
 SMD int exp2_entry(int f) { return (int)rint(pow(2.0, (double)f / 65536.0) * 65536.0); }
 SMD int phi_entry(int i) { return (int)rint(0.5 * (1.0 + erf(((double)(i - 32768) / 4096.0) / 1.4142135623730951)) * 65536.0); }
 SMD int arr_entry(i64 d) { return (int)rint(exp(-(double)d / 1024.0) * 16777216.0); }
 
-SMD i64 tab_log2(const Tables& tb, i64 m) { return tb.arith ? log2_entry((int)m) : tb.LOG2[m]; }
-SMD i64 tab_exp2(const Tables& tb, i64 f) { return tb.arith ? exp2_entry((int)f) : tb.EXP2[f]; }
-SMD i64 tab_phi(const Tables& tb, i64 i) { return tb.arith ? phi_entry((int)i) : tb.PHI[i]; }
+SMD i64 tab_log2(const Tables& tb, i64 m) { return tb.LOG2[m]; }
+SMD i64 tab_exp2(const Tables& tb, i64 f) { return tb.EXP2[f]; }
+SMD i64 tab_phi(const Tables& tb, i64 i) { return tb.PHI[i]; }
 // the arrival: 0 past the table (base2.py:97)
-SMD int tab_arr(const Tables& tb, i64 d) { return d < tb.alen ? (tb.arith ? arr_entry(d) : tb.ARR[d]) : 0; }
+SMD int tab_arr(const Tables& tb, i64 d) { return d < tb.alen ? tb.ARR[d] : 0; }
 
 // base2.py:18-22  rshift(X, s): X * 2^-s rounded half up (s <= 0: a left shift)
 SMD i64 rsh(i64 x, i64 s) {
@@ -78,31 +78,24 @@ SMD void log2_parts(i64 v, int& t, i64& m) {
 typedef const __attribute__((address_space(4))) int* cint_p;
 SMD i64 utab_log2(const Tables& tb, int m) {
     m = __builtin_amdgcn_readfirstlane(m);
-    return tb.arith ? log2_entry(m) : ((cint_p)tb.LOG2)[m];
+    return ((cint_p)tb.LOG2)[m];
 }
 SMD i64 utab_gpow(const Tables& tb, int r, int m) {
     r = __builtin_amdgcn_readfirstlane(r);
     m = __builtin_amdgcn_readfirstlane(m);
-    return tb.arith ? exp2_entry((int)((tb.log768 - (((i64)r * 65536 + log2_entry(m)) >> 1)) & 0xFFFF))
-                    : ((cint_p)tb.GPOW)[r * 65536 + m];
+    return ((cint_p)tb.GPOW)[r * 65536 + m];
 }
 SMD i64 utab_pgpow(const Tables& tb, int r, int m) {
     r = __builtin_amdgcn_readfirstlane(r);
     m = __builtin_amdgcn_readfirstlane(m);
-    return tb.arith ? exp2_entry((int)((-(((i64)r * 65536 + log2_entry(m)) >> 1)) & 0xFFFF))
-                    : ((cint_p)tb.PGPOW)[r * 65536 + m];
+    return ((cint_p)tb.PGPOW)[r * 65536 + m];
 }
 SMD i64 utab_hpow(const Tables& tb, int m) {
     m = __builtin_amdgcn_readfirstlane(m);
-    return tb.arith ? exp2_entry((int)((-(i64)log2_entry(m)) & 0xFFFF)) : ((cint_p)tb.HPOW)[m];
+    return ((cint_p)tb.HPOW)[m];
 }
-SMD i64 tab_gpow(const Tables& tb, int r, i64 m) {
-    return tb.arith ? exp2_entry((int)((tb.log768 - (((i64)r * 65536 + log2_entry((int)m)) >> 1)) & 0xFFFF))
-                    : tb.GPOW[r * 65536 + m];
-}
-SMD i64 tab_hpow(const Tables& tb, i64 m) {
-    return tb.arith ? exp2_entry((int)((-(i64)log2_entry((int)m)) & 0xFFFF)) : tb.HPOW[m];
-}
+SMD i64 tab_gpow(const Tables& tb, int r, i64 m) { return tb.GPOW[r * 65536 + m]; }
+SMD i64 tab_hpow(const Tables& tb, i64 m) { return tb.HPOW[m]; }
 
 // base2.py:50-53  power(X, F) = rshift(X * EXP2[F & 0xFFFF], 16 - (F >> 16))
 SMD i64 power(i64 x, i64 F, const Tables& tb) {
@@ -168,7 +161,7 @@ SMD i64 gauge_ls_pow_v(i64 s1, i64 s2, i64 ex, const Tables& tb, i64& e2) {
     i64 V = wadd(wsub(wmul(768, s2), wmul(s1, s1)), eps_term(tb.eps40, ex));
     int t; i64 m;
     log2_parts(V, t, m);
-    const i64 lg = tb.arith ? log2_entry((int)m) : tb.LOG2[m];
+    const i64 lg = tb.LOG2[m];
     e2 = tab_gpow(tb, t & 1, m);
     const i64 l2 = wadd((i64)t * 65536, lg);
     return wadd(wsub(l2 >> 1, tb.log768), wmul(ex, 65536));

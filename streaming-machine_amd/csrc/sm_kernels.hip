@@ -15,7 +15,7 @@
 //     launch and the next phase needs no extra pass.
 //   * a phase's critical path holds one dependent memory read (the row it consumes): the weights, exponents
 //     and biases of the block's first tile are requested before it, the gauge's power factor EXP2[f] is one
-//     value per block (f = -LS mod 2^16 for every column), and with arithmetic tables no table read remains.
+//     value per block (f = -LS mod 2^16 for every column),.
 #include "sm_kernels.h"
 
 // The float stages below evaluate each float64 operation of the reference's expression on its own, rounded once
@@ -1247,8 +1247,7 @@ __global__ __launch_bounds__(NTHR, ONE ? 1 : 3) void k_attend(AttArgs a) {
         i64 tot = 0;
 #pragma unroll
         for (int i = 0; i < 16; i++) tot += numr[i][lane];
-        const i64 zlg = a.tb.arith ? (i64)log2_entry(zmu) : (i64)zlg_mem;
-        const i64 zhp = a.tb.arith ? (i64)exp2_entry((int)((-(i64)log2_entry(zmu)) & 0xFFFF)) : (i64)zhp_mem;
+        const i64 zlg = zlg_mem, zhp = zhp_mem;
         const i64 F = wsub(0, wadd((i64)zt * 65536, zlg));   // -log2fix(Z), the same in every lane
         i64 o;
         if (MODEL == 1) {
@@ -1387,7 +1386,7 @@ __global__ __launch_bounds__(128) void k_kv_rows(AttArgs a) {
 }
 
 // ---------------------------------------------------------------------------------------------------------
-// Exhaustive check of the loaded tables against their defining formulas (sets Tables.arith when all agree).
+// Exhaustive check of the loaded tables against their defining formulas (counts the entries that differ).
 __global__ void k_check_tables(Tables tb, unsigned* bad) {
     const int i = blockIdx.x * blockDim.x + threadIdx.x;
     if (i < 65536) {

@@ -244,10 +244,9 @@ struct sm_tables {
     int* GPOW = nullptr; int* HPOW = nullptr; int* PGPOW = nullptr;
     int alen = 0;
     i64 log768 = 0, eps40 = 0;
-    int verified = 0;         // every entry equals its defining formula (checked on the device)
-    int force_memory = 1;     // read the tables from memory (the default; the recomputed form is slower)
+    int verified = 0;         // every entry equals its defining formula (checked on the device at create)
     int* scratch = nullptr;   // [0] pos for sm_stage_attend, [1] error bits, [4..7] mismatch counts
-    Tables tb() const { return Tables{LOG2, EXP2, PHI, ARR, alen, log768, eps40, verified && !force_memory, GPOW, HPOW, PGPOW}; }
+    Tables tb() const { return Tables{LOG2, EXP2, PHI, ARR, alen, log768, eps40, GPOW, HPOW, PGPOW}; }
 };
 
 static int upload_table(int** dst, const i64* src, size_t n, i64 lo, i64 hi, const char* name) {
@@ -287,7 +286,7 @@ static int tables_init(sm_tables& T, const i64* phi, const i64* arr, int alen, c
     if ((rc = dalloc(&T.scratch, 16))) return rc;
     HIP_TRY(hipMemset(T.scratch, 0, 64));
     T.alen = alen; T.log768 = log768; T.eps40 = eps40;
-    // every entry against its formula: the arithmetic form is used only if all of them agree
+    // every entry against its formula (table_mode 1 refuses tables that are not the reference's)
     const int n = alen + 1 > 65536 ? alen + 1 : 65536;
     k_check_tables<<<(n + 255) / 256, 256>>>(T.tb(), reinterpret_cast<unsigned*>(T.scratch + 4));
     HIP_TRY(hipGetLastError());
@@ -1212,7 +1211,8 @@ extern "C" int sm_create(const char* layout_dir, const sm_config* cfg, sm_machin
             return bail(rc);
         if ((rc = tables_init(m->T, phi.data(), arr.data(), (int)alen, lg.data(), ep.data(), log768, eps40))) return bail(rc);
         m->ehalf = ep[(-m->half) & 0xFFFF];
-        m->T.force_memory = c.table_mode != 1;
+        if (c.table_mode == 1 && !m->T.verified)
+            return bail(fail(SM_E_IO, "sm_create: a table entry differs from its formula (base2_convert.py:48-61)"));
     }
     m->ctx = c.max_ctx < m->npos ? c.max_ctx : m->npos;
     m->head_grid = c.head_grid > 0 ? c.head_grid : 512;     // two blocks per CU (measured best)
@@ -1516,9 +1516,9 @@ extern "C" int sm_top_read(const sm_machine* m) {
 }
 
 extern "C" int sm_info(const sm_machine* m, int32_t* vocab, int32_t* max_ctx, int32_t* max_streams, int32_t* n_pos,
-                       int32_t* arith_tables) {
+                       int32_t* tables_verified) {
     if (!m) return fail(SM_E_ARG, "sm_info: null machine");
-    if (arith_tables) *arith_tables = m->T.tb().arith;
+    if (tables_verified) *tables_verified = m->T.verified;
     if (vocab) *vocab = m->vocab;
     if (max_ctx) *max_ctx = m->ctx;
     if (max_streams) *max_streams = m->B;
@@ -1538,11 +1538,9 @@ extern "C" int sm_tables_create(const int64_t* phi, const int64_t* arrival, int3
     return SM_OK;
 }
 
-extern "C" int sm_tables_mode(sm_tables* t, int32_t force_memory, int32_t* arith_tables) {
-    if (!t) return fail(SM_E_ARG, "sm_tables_mode: null tables");
-    if (force_memory >= 0) t->force_memory = force_memory != 0;
-    if (arith_tables) *arith_tables = t->tb().arith;
-    return SM_OK;
+extern "C" int sm_tables_verified(const sm_tables* t) {
+    if (!t) return fail(SM_E_ARG, "sm_tables_verified: null tables");
+    return t->verified ? 1 : 0;
 }
 
 extern "C" int sm_tables_destroy(sm_tables* t) {

@@ -69,7 +69,7 @@ def lib():
         L.sm_info.argtypes = [vp, i32p, i32p, i32p, i32p, i32p]
         L.sm_model_kind.argtypes = [vp]
         L.sm_top_read.argtypes = [vp]
-        L.sm_tables_mode.argtypes = [vp, i32, i32p]
+        L.sm_tables_verified.argtypes = [vp]
         L.sm_profile.argtypes = [vp, i64p, ctypes.POINTER(ctypes.c_double), i32]
         L.sm_profile_stages.argtypes = [i32]
         L.sm_profile_kernels.argtypes = [ctypes.c_char_p, i32, i64p, ctypes.POINTER(ctypes.c_double), i32, i32p, i32]
@@ -129,7 +129,7 @@ class Machine:
     """
 
     def __init__(self, layout_dir: str, max_ctx: int = 1024, max_streams: int = 1, use_graph: bool = True,
-                 head_grid: int = 0, graph_steps: int = 16, profile: bool = False, memory_tables: bool = True,
+                 head_grid: int = 0, graph_steps: int = 16, profile: bool = False, verify_tables: bool = False,
                  prefill_rows: int = 64, gauge: str = "int", edge: str = "int", arrival: str = "int", turn: str = "int",
                  inv: bool = False, top: str = "auto"):
         fs = 0
@@ -141,7 +141,7 @@ class Machine:
             raise ValueError(f"top={top}: plain, fr or auto")
         self.L = lib()
         cfg = SmConfig(max_streams, max_ctx, 1 if use_graph else 0, head_grid, graph_steps, 1 if profile else 0,
-                       0 if memory_tables else 1, prefill_rows, 1 if inv else 0, fs,
+                       1 if verify_tables else 0, prefill_rows, 1 if inv else 0, fs,
                        dict(plain=0, fr=1, auto=2)[top])
         h = vp()
         check(self.L.sm_create(os.fsencode(layout_dir), ctypes.byref(cfg), ctypes.byref(h)))
@@ -149,7 +149,7 @@ class Machine:
         v, c, s, n, ar = i32(), i32(), i32(), i32(), i32()
         check(self.L.sm_info(self.h, ctypes.byref(v), ctypes.byref(c), ctypes.byref(s), ctypes.byref(n), ctypes.byref(ar)))
         self.vocab, self.max_ctx, self.max_streams, self.n_pos = v.value, c.value, s.value, n.value
-        self.arith_tables = bool(ar.value)
+        self.tables_verified = bool(ar.value)          # every table entry equals its formula (base2_convert.py:48-61)
         k = self.L.sm_model_kind(self.h)
         check(min(k, 0))
         self.kind = ("gpt2", "pythia")[k]
@@ -265,11 +265,11 @@ class Tables:
                                       int(tabs["eps40"]), ctypes.byref(h)))
         self.h = h
 
-    def mode(self, force_memory: int = -1) -> bool:
-        """force_memory 1/0 switches the table source (-1 leaves it); True when entries are recomputed"""
-        ar = i32()
-        check(self.L.sm_tables_mode(self.h, force_memory, ctypes.byref(ar)))
-        return bool(ar.value)
+    def verified(self) -> bool:
+        """every entry equals its defining formula (base2_convert.py:48-61), checked on the device at create"""
+        v = self.L.sm_tables_verified(self.h)
+        check(min(v, 0))
+        return bool(v)
 
     def close(self):
         if getattr(self, "h", None):

@@ -2,6 +2,8 @@
 cache, bit-exact against base2.py's golden vectors and the oracle."""
 from __future__ import annotations
 
+import os
+
 import numpy as np
 import pytest
 
@@ -49,19 +51,31 @@ def compare_record(got: dict, want: dict):
     assert not bad, f"{len(bad)} intermediates differ, first: {sorted(bad)[:8]}"
 
 
-@pytest.mark.parametrize("use_graph,memory_tables", [(True, True), (False, True), (True, False)])
-def test_small_model_words(sm, small_dir, golden, use_graph, memory_tables):
+@pytest.mark.parametrize("use_graph,verify_tables", [(True, False), (False, False), (True, True)])
+def test_small_model_words(sm, small_dir, golden, use_graph, verify_tables):
     c = golden_case(golden, "small_p8_w8")
-    m = sm.Machine(small_dir, max_ctx=64, use_graph=use_graph, memory_tables=memory_tables)
-    assert m.arith_tables == (not memory_tables)
+    m = sm.Machine(small_dir, max_ctx=64, use_graph=use_graph, verify_tables=verify_tables)
+    assert m.tables_verified          # the layout's tables are base2_convert.py's
     assert m.stream(c["prompt"], len(c["words"])) == c["words"]
     m.close()
 
 
-@pytest.mark.parametrize("memory_tables", [False, True])
-def test_small_model_record(sm, small_dir, golden, memory_tables):
+def test_verify_tables_refuses_a_changed_table(sm, small_dir, small_npz, tmp_path):
+    """verify_tables=True refuses a layout whose tables differ from their formulas; the default reads them as given"""
+    d = sm.layout(small_npz, str(tmp_path))
+    e = np.fromfile(os.path.join(d, "exp2.bin"), dtype=np.int64)
+    e[777] += 1
+    e.tofile(os.path.join(d, "exp2.bin"))
+    with pytest.raises(sm.SmError):
+        sm.Machine(d, max_ctx=64, verify_tables=True)
+    m = sm.Machine(d, max_ctx=64)
+    assert not m.tables_verified
+    m.close()
+
+
+def test_small_model_record(sm, small_dir, golden):
     c = golden_case(golden, "small_p8_w8")
-    m = sm.Machine(small_dir, max_ctx=64, memory_tables=memory_tables)
+    m = sm.Machine(small_dir, max_ctx=64)
     last = c["records"]["last"]
     m.reset()
     m.record_at(last["position"])
