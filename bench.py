@@ -42,6 +42,7 @@ import json
 import os
 import platform
 import re
+import subprocess
 import sys
 import tempfile
 import time
@@ -461,6 +462,21 @@ def attention_leg(sm, reps: int = 50):
 
 
 # ---- CPU baseline ----
+def floor_leg():
+    """The batch-1 step's launch-structure floor (streaming-machine_amd/floor_probe: the step's 62 dependent launches
+    with the machine's grids, empty, then reading their rows and plates and writing their outputs with no
+    arithmetic), run as a child process before this process initialises the GPU."""
+    exe = os.path.join(REPO, "streaming-machine_amd", "floor_probe")
+    if not os.path.exists(exe):
+        log("floor probe not built (make -C streaming-machine_amd/csrc): skipped")
+        return None
+    r = subprocess.run([exe], capture_output=True, text=True, timeout=120)
+    if r.returncode != 0:
+        log(f"floor probe failed ({r.returncode}): {r.stderr.strip()[-300:]}")
+        return None
+    return json.loads(r.stdout.strip().splitlines()[-1])
+
+
 def cpu_info():
     model = ""
     try:
@@ -556,7 +572,8 @@ def main():
     ap.add_argument("--no-pythia", action="store_true", help="skip the Pythia 32-stream leg")
     ap.add_argument("--no-micro", action="store_true", help="skip the GEMV and attention microbenchmarks")
     ap.add_argument("--no-full-read", action="store_true", help="skip the batch-1 leg with the full read of the word table")
-    ap.add_argument("--only", choices=("b1", "b1full", "b64", "pythia", "gemv", "attention"), default="",
+    ap.add_argument("--no-floor", action="store_true", help="skip the batch-1 launch-structure floor probe")
+    ap.add_argument("--only", choices=("b1", "b1full", "b64", "pythia", "gemv", "attention", "floor"), default="",
                     help="profiling: run one leg and print only its result (not the bench line)")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MB",
                     help="profiling: first copy MB MiB device to device (calibrates HBM byte counters)")
@@ -578,6 +595,10 @@ def main():
     PLAIN = args.plain
     if PLAIN and args.only not in ("b1", "b64", "pythia"):
         sys.exit("bench.py: --plain goes with --only b1, b64 or pythia")
+    floor = floor_leg() if (args.only in ("", "floor") and not args.no_floor) else None
+    if args.only == "floor":
+        print(json.dumps(floor), flush=True)
+        return
     sm = load_sm()
     import torch
     if args.copy_probe:
@@ -672,6 +693,12 @@ def main():
                                               if k in full["table"]), 2),
                 "note": "the same workload with the whole word table read every step (Machine(top='plain')); words "
                         "gated on base2.py's like the main line"}},
+        "floor": None if floor is None else {
+            **floor, "step_us": round(1000.0 * b1["ms"], 2), "step_over_bytes_floor": round(1000.0 * b1["ms"] / floor["bytes_us"], 3),
+            "note": "the step's 62 dependent launches with the machine's grids, replayed from graphs of 15 steps: "
+                    "empty_us with empty kernels, bytes_us with every kernel reading its row and its plate share "
+                    "(the top read's high-byte plane for the head) and writing its outputs, no arithmetic "
+                    "(streaming-machine_amd/floor_probe)"},
         "batched": batched,
         "pythia": pyleg,
         "gemv": gemv,

@@ -1,0 +1,134 @@
+// The batch-1 decode step's launch-structure floor, measured: the step's 62 dependent launches (12 layers x
+// [qkv, attend, proj, fc, mproj], the head's first stage, the race) with the machine's grids and block sizes,
+// replayed from a HIP graph of 15 steps, in two forms:
+//   empty  - every kernel returns at once: the cost of 62 dependent launches alone;
+//   bytes  - every kernel reads the row it depends on (the previous kernel's output) and its share of its plate
+//            (the GPT-2 124M shapes: int16 plates of 768x2304, 768x768, 768x3072, 3072x768, and the 768 x 50257
+//            high-byte plane of the top read), the attention reads 16 cached positions of keys (int16) and values
+//            (int32) per head, and each kernel writes its outputs -- no arithmetic beyond folding what it read.
+// The machine's step does all of this plus its arithmetic, so its time over "bytes" is what the arithmetic,
+// the block reductions and the table reads cost.  Prints one JSON line.
+#include <hip/hip_runtime.h>
+#include <cstdio>
+
+#define CHK(x) do { hipError_t e_ = (x); if (e_ != hipSuccess) { fprintf(stderr, "floor_probe: %s at line %d\n", hipGetErrorString(e_), __LINE__); return 1; } } while (0)
+typedef long long i64;
+typedef int v4i __attribute__((ext_vector_type(4)));
+
+// a GEMV-shaped phase: NIN-wide row, tiles of TC columns (WB bytes a weight), WPB waves a block, each wave its
+// tiles t, t + grid waves, ..; HEADK: one output a block (the head's block best) instead of one a column
+template <int NIN, int TC, int WPB, int WB, bool EMPTY, bool HEADK = false>
+__global__ __launch_bounds__(64 * WPB) void k_floor_phase(const i64* X, const v4i* W, int ntiles, i64* Y) {
+    if (EMPTY) return;
+    constexpr int NT = 64 * WPB, PER = NIN / NT, U = TC * NIN * WB / 16 / 64;
+    static_assert(NIN % NT == 0 && TC * NIN * WB % (16 * 64) == 0, "the row and the tile split evenly");
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    i64 acc = 0;
+#pragma unroll
+    for (int m = 0; m < PER; m++) acc ^= X[tid + NT * m];
+    i64 best = 0;
+    for (int t = blockIdx.x * WPB + wave; t < ntiles; t += gridDim.x * WPB) {
+        const v4i* base = W + (size_t)t * (TC * NIN * WB / 16) + lane;
+        i64 a = acc;
+#pragma unroll
+        for (int m = 0; m < U; m++) { const v4i w = base[64 * m]; a += w.x ^ w.y ^ w.z ^ w.w; }
+        a += __shfl_xor(a, 1, 64);
+        if (HEADK) best = a > best ? a : best;
+        else if (lane < TC) Y[t * TC + lane] = a;
+    }
+    if (HEADK && tid == 0) Y[blockIdx.x] = best;
+}
+// one wave a head: the new q, k, v and P cached positions of the head's keys and values
+template <bool EMPTY>
+__global__ __launch_bounds__(256) void k_floor_attend(const i64* QKV, const short* K, const int* V, int P, int ctx, i64* out) {
+    if (EMPTY || threadIdx.x >= 64) return;
+    const int h = blockIdx.x, lane = threadIdx.x;
+    i64 s = QKV[h * 64 + lane] ^ QKV[768 + h * 64 + lane] ^ QKV[1536 + h * 64 + lane];
+    const short* Kh = K + (size_t)h * ctx * 64;
+    const int* Vh = V + (size_t)h * ctx * 64;
+    for (int r = 0; r < P; r++) s += Kh[r * 64 + lane] + Vh[r * 64 + lane];
+    out[h * 64 + lane] = s;
+}
+// one block: the head blocks' bests, then the chosen word's row of the word table written as the next entering row
+template <bool EMPTY>
+__global__ __launch_bounds__(256) void k_floor_race(const i64* part, int n, const i64* wte, int nwords, i64* R0) {
+    if (EMPTY) return;
+    i64 b = 0;
+    for (int i = threadIdx.x; i < n; i += 256) b = part[i] > b ? part[i] : b;
+    b = max(b, __shfl_xor(b, 1, 64));
+    const int word = (int)((unsigned long long)b % (unsigned)nwords);
+    for (int i = threadIdx.x; i < 768; i += 256) R0[i] = wte[(size_t)word * 768 + i] + b;
+}
+
+template <bool EMPTY>
+static int run(double& us) {
+    const size_t qkvB = 768 * 2304 * 2, projB = 768 * 768 * 2, fcB = 768 * 3072 * 2, mpB = 3072 * 768 * 2;
+    const int head_tiles = (50257 + 3) / 4;                     // 4-column tiles of the high-byte plane
+    const size_t headB = (size_t)head_tiles * 4 * 768, layerB = qkvB + projB + fcB + mpB;
+    const int CTX = 64, P = 16, WTE = 1024, STEPS = 15, REPS = 20;
+    char* plates = nullptr;
+    i64 *R, *QKV, *att, *hid, *part, *wte;
+    short* K;
+    int* V;
+    CHK(hipMalloc(&plates, 12 * layerB + headB));
+    CHK(hipMalloc(&R, 768 * 8)); CHK(hipMalloc(&QKV, 2304 * 8)); CHK(hipMalloc(&att, 768 * 8)); CHK(hipMalloc(&hid, 3072 * 8));
+    CHK(hipMalloc(&part, 512 * 8)); CHK(hipMalloc(&wte, (size_t)WTE * 768 * 8));
+    CHK(hipMalloc(&K, (size_t)12 * 12 * CTX * 64 * 2)); CHK(hipMalloc(&V, (size_t)12 * 12 * CTX * 64 * 4));
+    CHK(hipMemset(plates, 1, 12 * layerB + headB));
+    CHK(hipMemset(R, 0, 768 * 8)); CHK(hipMemset(QKV, 0, 2304 * 8)); CHK(hipMemset(att, 0, 768 * 8));
+    CHK(hipMemset(hid, 0, 3072 * 8)); CHK(hipMemset(part, 0, 512 * 8)); CHK(hipMemset(wte, 0, (size_t)WTE * 768 * 8));
+    CHK(hipMemset(K, 0, (size_t)12 * 12 * CTX * 64 * 2)); CHK(hipMemset(V, 0, (size_t)12 * 12 * CTX * 64 * 4));
+    CHK(hipDeviceSynchronize());
+    hipStream_t st;
+    CHK(hipStreamCreateWithFlags(&st, hipStreamNonBlocking));
+    hipGraph_t g;
+    hipGraphExec_t ge;
+    CHK(hipStreamBeginCapture(st, hipStreamCaptureModeGlobal));
+    for (int s = 0; s < STEPS; s++) {
+        const char* pl = plates;
+        for (int l = 0; l < 12; l++) {
+            const v4i* wq = (const v4i*)pl; pl += qkvB;
+            const v4i* wp = (const v4i*)pl; pl += projB;
+            const v4i* wf = (const v4i*)pl; pl += fcB;
+            const v4i* wm = (const v4i*)pl; pl += mpB;
+            const size_t kv = (size_t)l * 12 * CTX * 64;
+            k_floor_phase<768, 2, 4, 2, EMPTY><<<288, 256, 0, st>>>(R, wq, 1152, QKV);
+            k_floor_attend<EMPTY><<<12, 256, 0, st>>>(QKV, K + kv, V + kv, P, CTX, att);
+            k_floor_phase<768, 2, 2, 2, EMPTY><<<192, 128, 0, st>>>(att, wp, 384, R);
+            k_floor_phase<768, 2, 4, 2, EMPTY><<<384, 256, 0, st>>>(R, wf, 1536, hid);
+            k_floor_phase<3072, 1, 4, 2, EMPTY><<<192, 256, 0, st>>>(hid, wm, 768, R);
+        }
+        k_floor_phase<768, 4, 4, 1, EMPTY, true><<<512, 256, 0, st>>>(R, (const v4i*)pl, head_tiles, part);
+        k_floor_race<EMPTY><<<1, 256, 0, st>>>(part, 512, wte, WTE, R);
+    }
+    CHK(hipStreamEndCapture(st, &g));
+    CHK(hipGraphInstantiate(&ge, g, nullptr, nullptr, 0));
+    hipEvent_t e0, e1;
+    CHK(hipEventCreate(&e0)); CHK(hipEventCreate(&e1));
+    for (int i = 0; i < 3; i++) CHK(hipGraphLaunch(ge, st));
+    CHK(hipStreamSynchronize(st));
+    CHK(hipEventRecord(e0, st));
+    for (int i = 0; i < REPS; i++) CHK(hipGraphLaunch(ge, st));
+    CHK(hipEventRecord(e1, st));
+    CHK(hipStreamSynchronize(st));
+    float ms = 0.0f;
+    CHK(hipEventElapsedTime(&ms, e0, e1));
+    us = ms * 1000.0 / (REPS * STEPS);
+    CHK(hipEventDestroy(e0)); CHK(hipEventDestroy(e1));
+    CHK(hipGraphExecDestroy(ge)); CHK(hipGraphDestroy(g)); CHK(hipStreamDestroy(st));
+    for (void* q : {(void*)plates, (void*)R, (void*)QKV, (void*)att, (void*)hid, (void*)part, (void*)wte, (void*)K, (void*)V})
+        CHK(hipFree(q));
+    return 0;
+}
+
+int main() {
+    double empty = 1e30, bytes = 1e30;
+    for (int r = 0; r < 3; r++) {             // the best of three measurements of each form
+        double e, b;
+        if (run<true>(e) || run<false>(b)) return 1;
+        empty = e < empty ? e : empty;
+        bytes = b < bytes ? b : bytes;
+    }
+    printf("{\"launches\": 62, \"empty_us\": %.2f, \"bytes_us\": %.2f, \"ctx\": 16, \"graph_steps\": 15}\n", empty, bytes);
+    return 0;
+}
