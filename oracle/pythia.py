@@ -71,6 +71,10 @@ class PythiaOracle:
         m = PyModel()
 
         def keep(a, dtype):
+            if dtype == np.int16:          # plates and word rows: plates=built's 17-bit digits are not held here
+                a = np.asarray(a)
+                if a.size and (int(a.max()) > 32767 or int(a.min()) < -32768):
+                    raise ValueError("the oracle holds int16 plates: a digit past 16 bits (plates=built)")
             a = np.ascontiguousarray(a, dtype=dtype)
             self._keep.append(a)
             return a

@@ -26,11 +26,15 @@ enum { EPI_GAUGED = 0,       // power(pile, (we + ex + 16) 65536 - LS) + b      
        // exact bounds, the block's best low and its candidates
        EPI_TOP1 = 9 };
 
-// k_gemv's MODE bits (batch 1): the complement machine, and two of the stages back in float64 (base2.py:10-11,
-// foundation0/pythia_base2.py:21-27: diagnostics that put one stage back to float; compared at the word level)
+// k_gemv's MODE bits (batch 1): the complement machine, two of the stages back in float64 (base2.py:10-11,
+// foundation0/pythia_base2.py:21-27: diagnostics that put one stage back to float; compared at the word level), and
+// plates of 17-bit digits
 enum { MODE_INV = 1,       // the complement machine (see race_beats)
        MODE_FGAUGE = 2,    // gauge=float: GPT-2 base2.py:66-69, 110-113; Pythia foundation0/pythia_base2.py:102-104
-       MODE_FEDGE = 4 };   // edge=float: GPT-2's tanh form base2.py:79-80; Pythia's erf form pythia_base2.py:144-146
+       MODE_FEDGE = 4,     // edge=float: GPT-2's tanh form base2.py:79-80; Pythia's erf form pythia_base2.py:144-146
+       MODE_SPLIT = 8 };   // every digit held as the difference of two int16 digits, w = W - W2 (the Pythia machine's
+                           // plates=built, foundation0/pythia_base2.py:44-46: finished - start, 17 bits a digit); the
+                           // pile is the exact integer sum x . W - x . W2
 
 // Record of one position's intermediates (stream 0), written when the position equals *pos.
 struct Rec {
@@ -50,6 +54,7 @@ struct Rec {
 
 struct GemvArgs {
     const int4* W;              // the plate in column tiles of TC (see sm_machine.hip: tile_plate)
+    const int4* W2;             // MODE_SPLIT: the subtracted plate, tiled as W
     const int* we;              // per-column power of two
     const i64* bias;            // per-column bias (2^-16)
     const i64* sw;              // MODE_INV: each column's sum over the plain plate (W holds ~w)
@@ -104,6 +109,7 @@ struct Race1Args {
     int npos;                   // rows of the position table (GPT-2): no entering row past it
     const i64* wte; const i64* wpe;             // GPT-2
     const short* ew; const int* ee;             // Pythia
+    const short* ew2;                           // Pythia, split word table (plates=built): the row is ew - ew2
 };
 
 // The collapsing top read's second stage, batch 1 (one block): the survivors' low bytes, their exact scores, the

@@ -342,8 +342,10 @@ __global__ __launch_bounds__(64 * WPB) void k_gemv(GemvArgs a) {
     constexpr bool FE = (MODE & MODE_FEDGE) && (EPI == EPI_GAUGED_EDGE || EPI == EPI_PLAIN_EDGE);
     static_assert(!INV || PRO == PRO_GAUGE || PRO == PRO_TO16, "the complement machine is GPT-2's");
     constexpr bool TOP = EPI == EPI_TOP1;
+    constexpr bool SPLIT = MODE & MODE_SPLIT;
+    static_assert(!SPLIT || (!TOP && !INV), "split plates are the Pythia machine's");
     constexpr int WB = TOP ? 1 : 2;                   // the top read's first stage streams the high-byte plane
-    constexpr int NT = 64 * WPB, U = WaveTile<NIN, TC, WB>::U;
+    constexpr int NT = 64 * WPB, U = WaveTile<NIN, TC, WB>::U, U2 = SPLIT ? U : 1;
     static_assert(NIN % NT == 0, "the block's threads must split the light row evenly");
     __shared__ __align__(16) short xh_s[NIN];
     __shared__ __align__(16) short xl_s[NIN];
@@ -373,11 +375,11 @@ __global__ __launch_bounds__(64 * WPB) void k_gemv(GemvArgs a) {
         // two named buffers in turn (no register copies, so a prefetch in flight is never waited on early);
         // a tile's exponents and biases are requested before its weights, so waiting for the small loads
         // never waits for the large ones behind them
-        v4i wA[U], wB[U];
+        v4i wA[U], wB[U], wA2[U2], wB2[U2];          // (wA2, wB2: MODE_SPLIT's subtracted plate)
         i64 bA = 0, eA = 0, bB = 0, eB = 0, sA = 0, sB = 0;     // (EPI_PLAIN_ADD: sA, sB hold the row added to)
         // every lane loads (indices clamped into range): a load that writes only some lanes would have to be
         // merged with the register's old value, and that merge waits for the load
-        auto fetch = [&](v4i (&w)[U], i64& we_, i64& b_, i64& s_, int t) {
+        auto fetch = [&](v4i (&w)[U], v4i (&w2)[U2], i64& we_, i64& b_, i64& s_, int t) {
             t = t < a.ntiles ? t : a.ntiles - 1;
             if (EPI != EPI_PILE) {
                 int j = t * TC + col;
@@ -388,12 +390,13 @@ __global__ __launch_bounds__(64 * WPB) void k_gemv(GemvArgs a) {
                 else if (EPI == EPI_PLAIN_ADD) s_ = a.Yb[j];
             }
             load_wtile<NIN, TC, U, WB>(w, a.W, t, lane);
+            if constexpr (SPLIT) load_wtile<NIN, TC, U, WB>(w2, a.W2, t, lane);
         };
         int tile = gw;
         i64 row[NIN / NT], nbq[NIN / NT];
         int ngq[NIN / NT];
         prologue_load<NIN, NT, PRO>(a, tid, row, ngq, nbq);   // the row first, then this wave's first tile
-        fetch(wA, eA, bA, sA, tile);                     // unconditional (clamped): no branch for the wait count to merge
+        fetch(wA, wA2, eA, bA, sA, tile);               // unconditional (clamped): no branch for the wait count to merge
         // then the next phase's lines (a fixed count a thread, clamped to a valid address: no branch around loads);
         // their values are consumed only after the tiles, where they have long arrived
         int pfs = 0;
@@ -421,8 +424,10 @@ __global__ __launch_bounds__(64 * WPB) void k_gemv(GemvArgs a) {
         const i64 fe = wsub(0, ls) & 0xFFFF;          // the fine part of (we + ex + 16) 65536 - LS for every column
         const i64 np = wsub(sx, nn);                  // EPI_TOP1: the sum of the light's positive values
         int it = 0;                                   // EPI_TOP1: tiles this wave has finished
-        auto finish = [&](const v4i (&w)[U], i64 wec, i64 bc, i64 swc, int t) {
-            i64 pile = wave_colsum64<TC>(wtile_partial<NIN, TC, U, WB>(w, xh_s, xl_s, lane));
+        auto finish = [&](const v4i (&w)[U], const v4i (&w2)[U2], i64 wec, i64 bc, i64 swc, int t) {
+            i64 part = wtile_partial<NIN, TC, U, WB>(w, xh_s, xl_s, lane);
+            if constexpr (SPLIT) part -= wtile_partial<NIN, TC, U, WB>(w2, xh_s, xl_s, lane);   // x . W - x . W2
+            i64 pile = wave_colsum64<TC>(part);
             if (INV) pile = wsub(pile, wadd(wadd(sx, swc), NIN));      // the plain pile
             const int j = t * TC + col;
             if (TOP && fin && j < a.nout) {
@@ -491,13 +496,13 @@ __global__ __launch_bounds__(64 * WPB) void k_gemv(GemvArgs a) {
         };
         while (tile < a.ntiles) {
             const int t1 = tile + nw;
-            fetch(wB, eB, bB, sB, t1);
-            finish(wA, eA, bA, sA, tile);
+            fetch(wB, wB2, eB, bB, sB, t1);
+            finish(wA, wA2, eA, bA, sA, tile);
             it++;
             if (t1 >= a.ntiles) break;
             const int t2 = t1 + nw;
-            fetch(wA, eA, bA, sA, t2);
-            finish(wB, eB, bB, sB, t1);
+            fetch(wA, wA2, eA, bA, sA, t2);
+            finish(wB, wB2, eB, bB, sB, t1);
             it++;
             tile = t2;
         }
@@ -614,7 +619,10 @@ SMD void race1_finish(const Race1Args& a, i64 bv, int bi, int p, int plen, const
     } else {
         const i64 es = -((i64)a.ee[tok] + 16);
 #pragma unroll
-        for (int m = 0; m < 3; m++) a.R0[tid + 256 * m] = rsh((i64)a.ew[tok * 768 + tid + 256 * m], es);
+        for (int m = 0; m < 3; m++) {
+            const size_t i = tok * 768 + tid + 256 * m;
+            a.R0[tid + 256 * m] = rsh(a.ew2 ? (i64)a.ew[i] - a.ew2[i] : (i64)a.ew[i], es);   // (split: W - W2)
+        }
     }
 }
 
@@ -808,7 +816,10 @@ __global__ __launch_bounds__(256) void k_embed1(Race1Args a) {
     } else {
         const i64 es = -((i64)a.ee[tok] + 16);
 #pragma unroll
-        for (int m = 0; m < 3; m++) a.R0[tid + 256 * m] = rsh((i64)a.ew[tok * 768 + tid + 256 * m], es);
+        for (int m = 0; m < 3; m++) {
+            const size_t i = tok * 768 + tid + 256 * m;
+            a.R0[tid + 256 * m] = rsh(a.ew2 ? (i64)a.ew[i] - a.ew2[i] : (i64)a.ew[i], es);   // (split: W - W2)
+        }
     }
 }
 

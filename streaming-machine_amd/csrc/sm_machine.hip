@@ -116,6 +116,7 @@ struct DevPlate {
     int* e = nullptr;
     i64* b = nullptr;
     i64* sw = nullptr;      // the complement machine: each column's sum over the plain plate (W then holds ~w)
+    int16_t* W2 = nullptr;  // split digits (MODE_SPLIT): the subtracted plate, tiled as W (the digit is W - W2)
 };
 
 // input-major [nin][nout] -> column tiles of tc: unit u of tile t holds inputs 8 (u / tc) .. + 8 of column
@@ -146,9 +147,10 @@ static int dalloc(T** p, size_t count) {
     return SM_OK;
 }
 
-// inv: the plate held complemented, with its plain column sums (base2_stream.swift:189-190)
+// inv: the plate held complemented, with its plain column sums (base2_stream.swift:189-190); w2 (split digits):
+// the subtracted plate, tiled as w
 static int upload_plate(DevPlate& P, const int16_t* w, const int32_t* e, const i64* b, int nin, int nout, int tc,
-                        bool inv = false) {
+                        bool inv = false, const int16_t* w2 = nullptr) {
     if (nin % 8 || nin <= 0 || nout <= 0 || (tc != 1 && tc != 2 && tc != 4 && tc != 8))
         return fail(SM_E_ARG, "plate: nin must be a multiple of 8 and tile_cols one of 1, 2, 4, 8");
     P.nin = nin; P.nout = nout; P.tc = tc; P.ntiles = (nout + tc - 1) / tc;
@@ -166,6 +168,11 @@ static int upload_plate(DevPlate& P, const int16_t* w, const int32_t* e, const i
     HIP_TRY(hipMemcpy(P.W, t.data(), t.size() * 2, hipMemcpyHostToDevice));
     HIP_TRY(hipMemcpy(P.e, e, (size_t)nout * 4, hipMemcpyHostToDevice));
     HIP_TRY(hipMemcpy(P.b, b, (size_t)nout * 8, hipMemcpyHostToDevice));
+    if (w2) {
+        const std::vector<int16_t> t2 = tile_plate(w2, nin, nout, tc);
+        if ((rc = dalloc(&P.W2, t2.size()))) return rc;
+        HIP_TRY(hipMemcpy(P.W2, t2.data(), t2.size() * 2, hipMemcpyHostToDevice));
+    }
     return SM_OK;
 }
 
@@ -189,7 +196,7 @@ static std::vector<uint8_t> lo_plane(const int16_t* w, int nin, int nout) {
 }
 
 static void free_plate(DevPlate& P) {
-    hfree(P.W); hfree(P.e); hfree(P.b); hfree(P.sw);
+    hfree(P.W); hfree(P.e); hfree(P.b); hfree(P.sw); hfree(P.W2);
     P = DevPlate();
 }
 
@@ -329,9 +336,11 @@ struct sm_machine {
     int* ng[12][2] = {};  i64* nb[12][2] = {};  int nge[12][2] = {};
     int* fg = nullptr;    i64* fb = nullptr;    int fge = 0;
     short* ew = nullptr;  int* ee = nullptr;
+    short* ew2 = nullptr;                               // split digits: the subtracted word table (row = ew - ew2)
     int* cosT = nullptr;  int* sinT = nullptr;  int rot = 0;
     i64 half = 0, ehalf = 0;
-    // batch 1: k_gemv's MODE bits (the complement machine, the float gauge and edge), the float turn and arrival
+    // batch 1: k_gemv's MODE bits (the complement machine, the float gauge and edge, split digits), the float
+    // turn and arrival
     int mode = 0;
     bool fturn = false, farr = false;
     double *cosF = nullptr, *sinF = nullptr;            // turn=float: [npos][rot / 2]
@@ -472,7 +481,7 @@ static void machine_free(sm_machine* m) {
     void* ps[] = {m->pfmap, m->planes, m->part_acc, m->rowinfo, m->wte, m->wpe, m->R, m->R0, m->QKV, m->att, m->attor, m->hidor, m->sfacts, m->hid, m->K16, m->KM, m->EK, m->V, m->seq, m->words, m->ctl,
                   m->part_v, m->part_i, m->r_x16, m->r_exls, m->r_pile, m->r_qkv, m->r_att, m->r_hid, m->r_resid,
                   m->r_hx16, m->r_hexls, m->r_hpile, m->r_logits, m->r_gauge, m->r_fcpre, m->r_hgauge,
-                  m->fg, m->fb, m->ew, m->ee, m->cosT, m->sinT, m->cosF, m->sinF, m->KF,
+                  m->fg, m->fb, m->ew, m->ee, m->ew2, m->cosT, m->sinT, m->cosF, m->sinF, m->KF,
                   m->top_hi, m->top_lo, m->cand_j, m->cand_h, m->cand_c, m->top_x, m->top_f, m->top_n, m->top_w,
                   m->top_pile, m->top_score};
     for (void* p : ps) hfree(p);
@@ -608,7 +617,7 @@ static Race1Args race1_args(sm_machine* m) {
     r.seq = m->seq; r.words = m->words; r.pos = ctl + CTL_POS; r.plen = ctl + CTL_PLEN; r.nwords = ctl + CTL_NWORDS;
     r.R0 = m->R0;
     r.npos = m->kind == 1 ? m->ctx : m->npos;
-    r.wte = m->wte; r.wpe = m->wpe; r.ew = m->ew; r.ee = m->ee;
+    r.wte = m->wte; r.wpe = m->wpe; r.ew = m->ew; r.ee = m->ee; r.ew2 = m->ew2;
     return r;
 }
 static void launch_race1(sm_machine* m) {
@@ -648,11 +657,13 @@ static void set_pf_head(sm_machine* m, GemvArgs& a) {
 // machine's MODE bits the rest (only those the phase has; the complement machine is never mixed with float stages)
 static constexpr int phase_modes(int PRO, int EPI) {
     return (PRO == PRO_GAUGE || PRO == PRO_TO16 ? MODE_INV : 0) | (PRO == PRO_GAUGE || PRO == PRO_PGAUGE ? MODE_FGAUGE : 0) |
-           (EPI == EPI_GAUGED_EDGE || EPI == EPI_PLAIN_EDGE ? MODE_FEDGE : 0);
+           (EPI == EPI_GAUGED_EDGE || EPI == EPI_PLAIN_EDGE ? MODE_FEDGE : 0) |
+           ((PRO == PRO_PGAUGE || PRO == PRO_TO16) && (EPI == EPI_PLAIN || EPI == EPI_PLAIN_EDGE || EPI == EPI_PHEAD ||
+                                                       EPI == EPI_PLAIN_ADD) ? MODE_SPLIT : 0);
 }
 template <int NIN, int TC, int WPB, int PRO, int EPI, int M = 0>
 static void gemv_mode(sm_machine* m, int mode, bool rec, const char* name, int grid, const GemvArgs& a) {
-    if constexpr (M < 8) {
+    if constexpr (M < 16) {
         if constexpr ((M & ~phase_modes(PRO, EPI)) == 0 && (M == MODE_INV || !(M & MODE_INV))) {
             if (mode == M) {
                 if (rec) launch(m->cfg.profile, name, k_gemv<NIN, TC, WPB, PRO, EPI, 1, M>, dim3(grid), dim3(64 * WPB), 0, m->st, a);
@@ -701,6 +712,7 @@ static int launch_step_pythia(sm_machine* m, int parts, bool rec) {
         base.err = ctl + CTL_ERR;                      // the reference's rshift assert (pythia_base2.py:63)
         auto plate = [&](GemvArgs& a, const DevPlate& P, int k) {
             a.W = reinterpret_cast<const int4*>(P.W); a.we = P.e; a.bias = P.b; a.sw = P.sw; a.nout = P.nout; a.ntiles = P.ntiles;
+            a.W2 = reinterpret_cast<const int4*>(P.W2);
             a.rx16 = m->r_x16 + (l * 4 + k) * 3072; a.rexls = m->r_exls + (l * 4 + k) * 2;
             a.rpile = m->r_pile + (l * 4 + k) * 3072;
         };
@@ -762,6 +774,7 @@ static int launch_step_pythia(sm_machine* m, int parts, bool rec) {
         a.pos = ctl + CTL_POS; a.rec_pos = ctl + CTL_RECPOS;
         const DevPlate& P = m->head;
         a.W = reinterpret_cast<const int4*>(P.W); a.we = P.e; a.bias = P.b; a.sw = P.sw; a.nout = P.nout; a.ntiles = P.ntiles;
+        a.W2 = reinterpret_cast<const int4*>(P.W2);
         a.X = m->R;
         a.ng = m->fg; a.nb = m->fb; a.nge = m->fge; a.rg = m->r_hgauge;
         a.rx16 = m->r_hx16; a.rexls = m->r_hexls; a.rpile = m->r_hpile; a.rlogits = m->r_logits;
@@ -1062,6 +1075,12 @@ extern "C" int sm_create(const char* layout_dir, const sm_config* cfg, sm_machin
         if (hs != 64 || rot <= 0 || rot > 64 || rot % 2) return fail(SM_E_IO, "manifest.json: built for 12 heads of 64 and an even turned width");
         if ((rc = parse_norms(mtext, norms))) return rc;
     }
+    // split digits: every plate and the word table come with a subtracted half (X.wsc), the digit being X.wc - X.wsc
+    // (the Pythia machine's plates=built, foundation0/pythia_base2.py:44-46: finished - start, 17 bits a digit)
+    long long splitv = 0;
+    const bool split = py && json_int(mtext, 0, "split", splitv) && splitv != 0;
+    if (split && (c.max_streams != 1 || c.prefill_rows != 0))
+        return fail(SM_E_ARG, "sm_create: a layout of split digits (plates=built) runs with max_streams 1 and prefill_rows 0");
     if (c.inv && (py || c.max_streams != 1 || c.prefill_rows != 0))
         return fail(SM_E_ARG, "sm_create: the complement machine (inv) runs GPT-2 with max_streams 1 and prefill_rows 0");
     if (c.float_stages & ~(SM_FLOAT_GAUGE | SM_FLOAT_EDGE | SM_FLOAT_ARRIVAL | SM_FLOAT_TURN))
@@ -1083,7 +1102,7 @@ extern "C" int sm_create(const char* layout_dir, const sm_config* cfg, sm_machin
     m->RC = std::max(m->B, c.prefill_rows);
     m->kind = py ? 1 : 0;
     m->mode = (c.inv ? MODE_INV : 0) | (c.float_stages & SM_FLOAT_GAUGE ? MODE_FGAUGE : 0) |
-              (c.float_stages & SM_FLOAT_EDGE ? MODE_FEDGE : 0);
+              (c.float_stages & SM_FLOAT_EDGE ? MODE_FEDGE : 0) | (split ? MODE_SPLIT : 0);
     m->fturn = c.float_stages & SM_FLOAT_TURN;
     m->farr = c.float_stages & SM_FLOAT_ARRIVAL;
     const bool mfma = m->B > 1 || c.prefill_rows > 0;     // the MFMA banks: batched streams or prompt passes
@@ -1099,11 +1118,14 @@ extern "C" int sm_create(const char* layout_dir, const sm_config* cfg, sm_machin
             const std::string name = std::string(BANK[k]) + "." + std::to_string(l);
             const BankInfo* bi = find(name);
             if (!bi || bi->nin != NIN[k] || bi->nout != NOUT[k]) return bail(fail(SM_E_IO, "manifest.json: bank " + name + " missing or of the wrong shape"));
-            std::vector<int16_t> w; std::vector<int32_t> e; std::vector<i64> b;
+            std::vector<int16_t> w, w2; std::vector<int32_t> e; std::vector<i64> b;
             if ((rc = read_array(dir + name + ".wc", w, (size_t)NIN[k] * NOUT[k])) || (rc = read_array(dir + name + ".e", e, NOUT[k])) ||
-                (rc = read_array(dir + name + ".b", b, NOUT[k])))
+                (rc = read_array(dir + name + ".b", b, NOUT[k])) ||
+                (split && (rc = read_array(dir + name + ".wsc", w2, (size_t)NIN[k] * NOUT[k]))))
                 return bail(rc);
-            if (m->B == 1 && (rc = upload_plate(m->bank[l][k], w.data(), e.data(), b.data(), NIN[k], NOUT[k], TCOLS[k], c.inv))) return bail(rc);
+            if (m->B == 1 && (rc = upload_plate(m->bank[l][k], w.data(), e.data(), b.data(), NIN[k], NOUT[k], TCOLS[k], c.inv,
+                                                split ? w2.data() : nullptr)))
+                return bail(rc);
             if (mfma && (rc = upload_mfma_plate(m->mbank[l][k], w.data(), e.data(), b.data(), NIN[k], NOUT[k]))) return bail(rc);
         }
     }
@@ -1121,12 +1143,15 @@ extern "C" int sm_create(const char* layout_dir, const sm_config* cfg, sm_machin
         m->cfg.top_read = c.top_read;
     }
     {
-        std::vector<int16_t> w; std::vector<int32_t> e; std::vector<i64> b;
-        if ((rc = read_array(dir + "head.wc", w, (size_t)768 * m->vocab)) || (rc = read_array(dir + "head.e", e, m->vocab)))
+        std::vector<int16_t> w, w2; std::vector<int32_t> e; std::vector<i64> b;
+        if ((rc = read_array(dir + "head.wc", w, (size_t)768 * m->vocab)) || (rc = read_array(dir + "head.e", e, m->vocab)) ||
+            (split && (rc = read_array(dir + "head.wsc", w2, (size_t)768 * m->vocab))))
             return bail(rc);
         if (py) b.assign(m->vocab, 0);         // Pythia's head has no bias (foundation0/pythia_base2.py:159)
         else if ((rc = read_array(dir + "head.b", b, m->vocab))) return bail(rc);
-        if (m->B == 1 && (rc = upload_plate(m->head, w.data(), e.data(), b.data(), 768, m->vocab, HEAD_TC, c.inv))) return bail(rc);
+        if (m->B == 1 && (rc = upload_plate(m->head, w.data(), e.data(), b.data(), 768, m->vocab, HEAD_TC, c.inv,
+                                            split ? w2.data() : nullptr)))
+            return bail(rc);
         if (c.top_read) {
             const std::vector<int8_t> hi = tile_hi_plane(w.data(), 768, m->vocab, HEAD_TC);
             const std::vector<uint8_t> lo = lo_plane(w.data(), 768, m->vocab);
@@ -1139,10 +1164,16 @@ extern "C" int sm_create(const char* layout_dir, const sm_config* cfg, sm_machin
     }
     // word and position tables
     if (py) {
-        std::vector<int16_t> ew; std::vector<int32_t> ee; std::vector<i64> cs, sn;
+        std::vector<int16_t> ew, ew2; std::vector<int32_t> ee; std::vector<i64> cs, sn;
         if ((rc = read_array(dir + "embed.wc", ew, (size_t)m->vocab * 768)) || (rc = read_array(dir + "embed.e", ee, m->vocab)) ||
-            (rc = read_array(dir + "cos.bin", cs, (size_t)-1)) || (rc = read_array(dir + "sin.bin", sn, (size_t)-1)))
+            (rc = read_array(dir + "cos.bin", cs, (size_t)-1)) || (rc = read_array(dir + "sin.bin", sn, (size_t)-1)) ||
+            (split && (rc = read_array(dir + "embed.wsc", ew2, (size_t)m->vocab * 768))))
             return bail(rc);
+        if (split) {
+            if ((rc = dalloc(&m->ew2, ew2.size()))) return bail(rc);
+            if (hipMemcpy(m->ew2, ew2.data(), ew2.size() * 2, hipMemcpyHostToDevice) != hipSuccess)
+                return bail(fail(SM_E_HIP, "upload embed.wsc"));
+        }
         const size_t r2 = (size_t)rot / 2;
         if (cs.empty() || cs.size() % r2 || sn.size() != cs.size()) return bail(fail(SM_E_IO, "cos.bin / sin.bin: not [positions][rot / 2]"));
         m->npos = (int)(cs.size() / r2);
@@ -1181,7 +1212,8 @@ extern "C" int sm_create(const char* layout_dir, const sm_config* cfg, sm_machin
             std::vector<int32_t> gh; std::vector<i64> bh;
             int r;
             if ((r = read_array(dir + name + ".g", gh, 768)) || (r = read_array(dir + name + ".b", bh, 768))) return r;
-            for (int v : gh) if (v < -32767 || v > 32767) return fail(SM_E_IO, name + ".g: a gain past 16 places");
+            const int gmax = split ? 65535 : 32767;      // (split digits: a difference of two 16-place gains)
+            for (int v : gh) if (v < -gmax || v > gmax) return fail(SM_E_IO, name + ".g: a gain past " + (split ? "17" : "16") + " places");
             if (gev < -64 || gev > 16) return fail(SM_E_IO, name + ": gain power out of range");
             if ((r = dalloc(&g, (size_t)768)) || (r = dalloc(&b, (size_t)768))) return r;
             HIP_TRY(hipMemcpy(g, gh.data(), 768 * 4, hipMemcpyHostToDevice));

@@ -154,19 +154,31 @@ def convert_pythia(sd: dict, cfg: dict, start: dict | None = None) -> dict:
 
 def select_plates(npz: dict, plates: str = "finished") -> dict:
     """foundation0/pythia_base2.py:44-46's `plates=`: "finished" (the converted checkpoint's plates, biases, norms
-    and word tables) or "start" (the start checkpoint's, which the converter keeps beside them as .s / .bs / .gs on
-    the same powers of two).  Its third choice, "built" (finished - start, digit for digit), needs 17 bits a digit,
-    and the device's plates are int16: refused."""
-    if plates == "finished":
-        return dict(npz)
-    if plates != "start":
-        raise ValueError(f"plates={plates}: finished or start (built needs 17-bit digits)")
+    and word tables), "start" (the start checkpoint's, which the converter keeps beside them as .s / .bs / .gs on
+    the same powers of two) or "built" (finished - start, digit for digit: every plate, bias, gain, offset and word
+    row, on the same powers of two).  A built digit takes 17 bits (int64 arrays here); pythia_layout writes such
+    plates as two int16 halves whose difference is the digit."""
+    if plates not in ("finished", "start", "built"):
+        raise ValueError(f"plates={plates}: finished, start or built")
     out = dict(npz)
+    if plates == "finished":
+        return out
     for k in npz:
         for tail, start in ((".w", ".s"), (".b", ".bs"), (".g", ".gs")):
             if k.endswith(tail) and k[:-len(tail)] + start in npz:
-                out[k] = npz[k[:-len(tail)] + start]
+                s0 = np.asarray(npz[k[:-len(tail)] + start])
+                out[k] = s0 if plates == "start" else np.asarray(npz[k]).astype(np.int64) - s0.astype(np.int64)
     return out
+
+
+def split_digits(w: np.ndarray):
+    """A plate of digits within +-65535 as two int16 halves a - b = w: a = w clipped to int16, b = a - w (both
+    within int16 since |w| <= 32767 + 32768)."""
+    w = np.asarray(w, dtype=np.int64)
+    if w.size and np.abs(w).max() > 65535:
+        raise ValueError("split_digits: a digit past 17 bits")
+    a = np.clip(w, -32768, 32767)
+    return a.astype(np.int16), (a - w).astype(np.int16)
 
 
 def shuffle_order(npz: dict, seed: int = 12345) -> dict:
@@ -201,27 +213,41 @@ def pythia_layout(npz: dict, out_dir: str) -> str:
       {qkv,proj,fc,mproj}.{l}.wc / .e / .b   int16 [nin][nout], int32 [nout], int64 [nout] (as base2_gpu.py)
       head.wc / head.e                       int16 [768][vocab], int32 [vocab] (no bias)
       embed.wc / embed.e                     int16 [vocab][768], int32 [vocab] (a power of two per word)
+      X.wsc (split digits only)              int16, the subtracted half of plate / word table X (digit = wc - wsc)
       {ln1,ln2}.{l}.g / .b, lnf.g / .b       int32 [768] gain on 16 places, int64 [768] offset at 2^-16
       phi.bin arrival.bin log2.bin exp2.bin cos.bin sin.bin   int64 (cos / sin [positions][rot / 2] at 2^-30)
       cosf.bin sinf.bin                      float64 [positions][rot / 2]: the float turn's cos and sin
       manifest.json  {"kind": "pythia", "banks": [...], "norms": [{"name", "ge"}, ...], "hs", "rot",
-                      "half_log2_hs", "log2_768", "eps40", "arrival_len", "vocab"}
+                      "half_log2_hs", "log2_768", "eps40", "arrival_len", "vocab", "split"}
+    Plates whose digits leave int16 (plates=built) are written split: X.wc - X.wsc is the digit ("split": 1; the
+    machine then runs at one stream, position by position).
     """
     os.makedirs(out_dir, exist_ok=True)
     L = int(npz["L"])
     banks, norms = [], []
-    for name in [f"{b}.{l}" for l in range(L) for b in P_BANKS] + ["head"]:
-        w = np.ascontiguousarray(npz[name + ".w"]).astype(np.int16)
-        w.tofile(os.path.join(out_dir, f"{name}.wc"))
+    plates = [f"{b}.{l}" for l in range(L) for b in P_BANKS] + ["head", "embed"]
+    split = any(int(np.max(npz[n + ".w"])) > 32767 or int(np.min(npz[n + ".w"])) < -32768 for n in plates)
+
+    def write_plate(name):
+        if split:
+            a, b = split_digits(npz[name + ".w"])
+            np.ascontiguousarray(b).tofile(os.path.join(out_dir, f"{name}.wsc"))
+        else:
+            a = np.asarray(npz[name + ".w"]).astype(np.int16)
+        np.ascontiguousarray(a).tofile(os.path.join(out_dir, f"{name}.wc"))
+        return a.shape
+
+    for name in plates[:-1]:
+        w_shape = write_plate(name)
         np.asarray(npz[name + ".e"]).astype(np.int32).tofile(os.path.join(out_dir, f"{name}.e"))
         if name != "head":
             np.asarray(npz[name + ".b"]).astype(np.int64).tofile(os.path.join(out_dir, f"{name}.b"))
-        banks.append(dict(name=name, nin=int(w.shape[0]), nout=int(w.shape[1])))
+        banks.append(dict(name=name, nin=int(w_shape[0]), nout=int(w_shape[1])))
     for name in [f"{n}.{l}" for l in range(L) for n in P_NORMS] + ["lnf"]:
         np.asarray(npz[name + ".g"]).astype(np.int32).tofile(os.path.join(out_dir, f"{name}.g"))
         np.asarray(npz[name + ".b"]).astype(np.int64).tofile(os.path.join(out_dir, f"{name}.b"))
         norms.append(dict(name=name, ge=int(npz[name + ".ge"])))
-    np.ascontiguousarray(npz["embed.w"]).astype(np.int16).tofile(os.path.join(out_dir, "embed.wc"))
+    write_plate("embed")
     np.asarray(npz["embed.e"]).astype(np.int32).tofile(os.path.join(out_dir, "embed.e"))
     for k in ("phi", "arrival", "log2", "exp2", "cos", "sin"):
         np.ascontiguousarray(npz[k]).astype(np.int64).tofile(os.path.join(out_dir, f"{k}.bin"))
@@ -232,7 +258,7 @@ def pythia_layout(npz: dict, out_dir: str) -> str:
     np.sin(ang).astype(np.float64).tofile(os.path.join(out_dir, "sinf.bin"))
     man = dict(kind="pythia", banks=banks, norms=norms, hs=int(npz["hs"]), rot=int(npz["rot"]),
                half_log2_hs=int(npz["half_log2_hs"]), log2_768=round(math.log2(768) * 65536), eps40=int(npz["eps40"]),
-               arrival_len=int(len(npz["arrival"])), vocab=int(npz["vocab"]))
+               arrival_len=int(len(npz["arrival"])), vocab=int(npz["vocab"]), split=int(split))
     with open(os.path.join(out_dir, "manifest.json"), "w") as f:
         json.dump(man, f)
     return out_dir

@@ -1,12 +1,13 @@
 """Write the golden words of pythia_base2.py's plate and order switches (run here, in the build container).
 
 foundation0/pythia_base2.py:21-27, 40-58: plates=finished|start picks which checkpoint's plates, biases, norms and
-word tables the machine runs (the converter keeps both on one grid), and order=shuffle runs the stream's lanes in
-the order default_rng(12345).permutation(768), every plate permuted to match.  This script converts a seeded
+word tables the machine runs (the converter keeps both on one grid), plates=built runs their difference (finished
+- start, digit for digit), and order=shuffle runs the stream's lanes in the order
+default_rng(12345).permutation(768), every plate permuted to match.  This script converts a seeded
 finished checkpoint (random_pythia(seed=5, vocab=1000)) with a different start checkpoint (seed 6) by this
 repository's converter, executes pythia_base2.py's definitions with each switch, and records the greedy words
 and the hashes of the last position's intermediates.  The reference source is read and executed here only;
-modes_golden.json holds words and hashes.
+modes_golden.json holds words and hashes.  Cases already in the file for the same model are kept.
 Usage:  python tests/golden/make_golden_modes.py [/root/reference]
 """
 from __future__ import annotations
@@ -48,10 +49,17 @@ def main():
            "hash": "sha256 of int64 little-endian bytes",
            "model": dict(recipe=dict(finished_seed=5, start_seed=6, vocab=1000), digest=sm.array_digest(npz)),
            "cases": []}
+    if os.path.exists(OUT):
+        old = json.load(open(OUT))
+        if old.get("model") == out["model"]:
+            out["cases"] = old["cases"]
+    have = {tuple(c["switches"]) for c in out["cases"]}
     work = tempfile.mkdtemp(prefix="sm_golden_modes_")
     np.savez(os.path.join(work, "base2_pythia-modes.npz"), **npz)
     prompt = sm.prompt_ids(50, 8, 1000)
-    for switches in (["plates=finished"], ["plates=start"], ["order=shuffle"]):
+    for switches in (["plates=finished"], ["plates=start"], ["order=shuffle"], ["plates=built"]):
+        if tuple(switches) in have:
+            continue
         ns = gf.namespace(os.path.join(REF, "foundation0", "pythia_base2.py"), work,
                           ["pythia_base2.py", "size=modes"] + switches, file_as=os.path.join(work, "pythia_base2.py"))
         rc = gp.Recorder(ns)

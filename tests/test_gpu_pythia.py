@@ -201,9 +201,10 @@ def test_rshift_assert(sm, py_small_npz, tmp_path, streams):
 
 @pytest.mark.parametrize("streams", [1, 2])
 def test_plate_and_order_switches(sm, tmp_path, streams):
-    """pythia_base2.py's plates=finished|start and order=shuffle (the finished-and-start model of
+    """pythia_base2.py's plates=finished|start|built and order=shuffle (the finished-and-start model of
     modes_golden.json): words and every recorded intermediate of the last position against the reference run
-    with each switch (the shuffled machine's intermediates in their shuffled places)"""
+    with each switch (the shuffled machine's intermediates in their shuffled places; plates=built's 17-bit digits
+    as split plates, one stream only)"""
     from test_oracle_pythia import _modes, modes_npz
     g = _modes()
     if g is None:
@@ -211,7 +212,14 @@ def test_plate_and_order_switches(sm, tmp_path, streams):
     for case in g["cases"]:
         d = str(tmp_path / f"{case['name']}_{streams}")
         sm.pythia.pythia_layout(modes_npz(sm, case), d)
-        m = sm.Machine(d, max_ctx=32, max_streams=streams)
+        kw = {}
+        if case["switches"] == ["plates=built"]:      # 17-bit digits, split in two: one stream, position by position
+            if streams > 1:
+                with pytest.raises(sm.SmError):
+                    sm.Machine(d, max_ctx=32, max_streams=streams)
+                continue
+            kw = dict(prefill_rows=0)
+        m = sm.Machine(d, max_ctx=32, max_streams=streams, **kw)
         last = case["records"]["last"]
         m.reset()
         m.record_at(last["position"])

@@ -149,14 +149,51 @@ def modes_npz(sm, case):
 
 def test_plate_and_order_switches(sm):
     """pythia_base2.py's plates=start and order=shuffle (its order-free check) as package transforms of the
-    converted model: the oracle on them gives the words the reference gave with those switches"""
+    converted model: the oracle on them gives the words the reference gave with those switches.  plates=built's
+    17-bit digits the oracle does not hold (it refuses them); the device's run is pinned to the reference's words
+    and records by the GPU test."""
     g = _modes()
     if g is None:
         pytest.skip("modes_golden.json not written")
     fin, cfg = sm.pythia.random_pythia(seed=5, vocab=1000)
     start, _ = sm.pythia.random_pythia(seed=6, vocab=1000)
     assert sm.array_digest(sm.pythia.convert_pythia(fin, cfg, start=start)) == g["model"]["digest"]
+    assert {tuple(c["switches"]) for c in g["cases"]} >= {("plates=start",), ("plates=built",), ("order=shuffle",)}
     for case in g["cases"]:
+        if case["switches"] == ["plates=built"]:
+            with pytest.raises(ValueError):
+                PythiaOracle(modes_npz(sm, case))
+            continue
         assert PythiaOracle(modes_npz(sm, case)).generate(case["prompt"], len(case["words"])) == case["words"], case["name"]
     with pytest.raises(ValueError):
-        sm.pythia.select_plates({}, "built")
+        sm.pythia.select_plates({}, "other")
+
+
+def test_built_plates_and_split_digits(sm, tmp_path):
+    """plates=built (foundation0/pythia_base2.py:44-46): every plate, bias, gain, offset and word row is finished -
+    start; the layout writes digits past int16 as two int16 halves whose difference is the digit"""
+    fin, cfg = sm.pythia.random_pythia(seed=5, vocab=200, n_layer=12)
+    start, _ = sm.pythia.random_pythia(seed=6, vocab=200, n_layer=12)
+    npz = sm.pythia.convert_pythia(fin, cfg, start=start)
+    built = sm.pythia.select_plates(npz, "built")
+    for k, ks in (("qkv.3.w", "qkv.3.s"), ("head.w", "head.s"), ("embed.w", "embed.s"), ("fc.0.b", "fc.0.bs"),
+                  ("ln2.5.g", "ln2.5.gs"), ("lnf.b", "lnf.bs")):
+        assert np.array_equal(built[k], np.asarray(npz[k], np.int64) - np.asarray(npz[ks], np.int64)), k
+    assert np.array_equal(built["qkv.3.e"], npz["qkv.3.e"])          # the same powers of two
+    assert int(np.abs(built["qkv.0.w"]).max()) > 32767               # the seeded pair reaches 17 bits
+    w = np.array([-65535, -32769, -32768, -1, 0, 1, 32767, 32768, 65535], np.int64)
+    a, b = sm.pythia.split_digits(w)
+    assert a.dtype == np.int16 and b.dtype == np.int16
+    assert np.array_equal(a.astype(np.int64) - b.astype(np.int64), w)
+    with pytest.raises(ValueError):
+        sm.pythia.split_digits(np.array([65536]))
+    d = sm.pythia.pythia_layout(built, str(tmp_path / "built"))
+    import json
+    assert json.load(open(os.path.join(d, "manifest.json")))["split"] == 1
+    for name, shape in (("qkv.7", (768, 2304)), ("head", (768, 200)), ("embed", (200, 768))):
+        hi = np.fromfile(os.path.join(d, f"{name}.wc"), np.int16).astype(np.int64)
+        lo = np.fromfile(os.path.join(d, f"{name}.wsc"), np.int16).astype(np.int64)
+        assert np.array_equal((hi - lo).reshape(shape), built[f"{name}.w"]), name
+    plain = sm.pythia.pythia_layout(npz, str(tmp_path / "plain"))
+    assert json.load(open(os.path.join(plain, "manifest.json")))["split"] == 0
+    assert not os.path.exists(os.path.join(plain, "qkv.0.wsc"))
