@@ -46,6 +46,7 @@ struct GemmArgs {
     const int* we; const i64* bias;
     const signed char* planes; const int* rowinfo;
     i64* Y; int ystride;          // output rows [rows][ystride] (or the stream R for EPI_PLAIN_ADD)
+    int* Y32;                     // EPI_GAUGED_EDGE / EPI_PLAIN_EDGE (when non-null): the outputs' low 32 bits
     Tables tb;
     const int* pos; const int* plen;
     i64* part_v; int* part_i; int nblk;   // EPI_HEAD: per (row, block) best
@@ -54,6 +55,7 @@ struct GemmArgs {
     int* part;                    // EPI_PART: [ksplit][3][rows][N] int32
     // the light formed in the bank (SRC > 0): the producing phase's rows, its OR words, stream 0's light record
     const i64* X; int xstride;    // [rows][xstride] int64
+    const int* X32;               // the same rows' low 32 bits (read where a row's OR words show it fits 31 bits)
     const i64* orw;               // [rows][SRC]: OR of |x| over each part of a row the producer wrote
     i64* rx16; i64* rexls;
     int* sfacts;                  // EPI_PART with SRC > 0: [KSPLIT][rows][4] each K slice's SXh, SXl, n32768, ex
@@ -268,7 +270,7 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs a) {
     // wave's operand reads spread over the banks), each row's shift, a wave's "holds +32768" flag, and the plane
     // sums [wave][tile row] (SXh, SXl, n32768)
     constexpr int KR = K / KSPLIT, XSTR = KR / 2 + 4;
-    __shared__ int xs[ROWS ? 16 * XSTR : 1];
+    __shared__ __align__(16) int xs[ROWS ? 16 * XSTR : 1];
     __shared__ int shs[16], cfw[4];
     __shared__ int sfx[ROWS ? 4 * 16 * 4 : 1];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -309,16 +311,18 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs a) {
     }
     v4 wh[NB][NS], wl[NB][NS], xh[NS], xl[NS];
     // SRC > 0: wave w lights tile rows 4 w .. 4 w + 3.  Their OR words (word n = lane + 64 m of the wave's
-    // 4 SRC), then their values as contiguous 1 KB wave loads (value pair 64 c + lane of row j), all ahead of the
-    // weights (their wait then leaves the weights in flight); rows past the last read zeros
-    constexpr int NWD = ROWS ? (4 * SRC + 63) / 64 : 1, NCH = ROWS ? KR / 128 : 1;
+    // 4 SRC), then their values' 32-bit copies as contiguous 1 KB wave loads (values 4 (64 c + lane) .. + 3 of
+    // row j), all ahead of the weights (their wait then leaves the weights in flight); rows past the last read
+    // zeros.  A row whose OR words reach 2^31 is read again at 64 bits (rare: its 32-bit copy is not the value).
+    constexpr int NWD = ROWS ? (4 * SRC + 63) / 64 : 1, NCH = ROWS ? KR / 128 : 1, NCH4 = ROWS ? KR / 256 : 1;
+    static_assert(!ROWS || KR % 256 == 0, "a K slice of whole 256-value chunks");
     const int tr = lane & 15, q4 = lane >> 4;
     i64 ow[NWD];
-    v4 xr[ROWS ? 4 : 1][NCH];
+    v4 xr[ROWS ? 4 : 1][NCH4];
+    const int row0 = 16 * t0 + 4 * wave;
     if constexpr (ROWS) {
         const __amdgpu_buffer_rsrc_t ro = buf_rsrc(a.orw, (unsigned)(a.rows * SRC) * 8u);
-        const __amdgpu_buffer_rsrc_t rx = buf_rsrc(a.X, (unsigned)(a.rows * a.xstride) * 8u);
-        const int row0 = 16 * t0 + 4 * wave;
+        const __amdgpu_buffer_rsrc_t rx = buf_rsrc(a.X32, (unsigned)(a.rows * a.xstride) * 4u);
 #pragma unroll
         for (int m = 0; m < NWD; m++) {
             const int n = lane + 64 * m;
@@ -328,8 +332,8 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs a) {
 #pragma unroll
         for (int jr = 0; jr < 4; jr++)
 #pragma unroll
-            for (int c = 0; c < NCH; c++)
-                xr[jr][c] = buf_load4(rx, (unsigned)((row0 + jr) * a.xstride + kb * KR + 2 * (64 * c + lane)) * 8u);
+            for (int c = 0; c < NCH4; c++)
+                xr[jr][c] = buf_load4(rx, (unsigned)((row0 + jr) * a.xstride + kb * KR + 4 * (64 * c + lane)) * 4u);
     }
 #pragma unroll
     for (int nb = 0; nb < NB; nb++)
@@ -356,30 +360,66 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs a) {
         const int p = a.pos ? *a.pos : 0;
         const bool rec = a.rx16 && t0 == 0 && nt == 0 && a.rec_pos && *a.rec_pos == p;
         int mx = 0;
+        // each row's water level from its OR words (uniform)
+        i64 orr[4];
+        int shv[4];
 #pragma unroll
         for (int jr = 0; jr < 4; jr++) {
-            i64 o = 0;                                   // the row's water level from its OR words
+            i64 o = 0;
 #pragma unroll
             for (int m = 0; m < NWD; m++)
                 if ((lane + 64 * m) / SRC == jr) o |= ow[m];
-            const int sh = water_shift(wave_or64(o));    // uniform
-            const i64 half = sh ? (i64)1 << (sh - 1) : 0;   // rshift(v, sh), sh in [0, 49]: (v + half) >> sh
-            if (lane == 0) shs[4 * wave + jr] = sh;
-#pragma unroll
-            for (int c = 0; c < NCH; c++) {
-                const v4 w = xr[jr][c];
-                const int x0 = (int)(wadd((i64)(((u64)(unsigned)w[1] << 32) | (unsigned)w[0]), half) >> sh);
-                const int x1 = (int)(wadd((i64)(((u64)(unsigned)w[3] << 32) | (unsigned)w[2]), half) >> sh);
-                mx = max(mx, max(x0, x1));
-                if (rec && wave == 0 && jr == 0) {       // stream 0's record
-                    a.rx16[kb * KR + 2 * (64 * c + lane)] = x0;
-                    a.rx16[kb * KR + 2 * (64 * c + lane) + 1] = x1;
-                }
-                // +32768 held as 32767 (the correction plane carries the rest)
-                xs[(4 * wave + jr) * XSTR + 64 * c + lane] =
-                    (int)__builtin_amdgcn_perm((unsigned)min(x1, 32767), (unsigned)min(x0, 32767), 0x05040100u);
+            orr[jr] = wave_or64(o);
+            shv[jr] = water_shift(orr[jr]);
+            if (lane == 0) shs[4 * wave + jr] = shv[jr];
+            if (rec && kb == 0 && wave == 0 && jr == 0 && lane == 0) { a.rexls[0] = shv[0] - 16; a.rexls[1] = 0; }
+        }
+        // light pair q (the slice's values 2 q, 2 q + 1) of row jr: +32768 held as 32767 (the correction plane
+        // carries the rest)
+        auto pair = [&](int jr, int q, int x0, int x1) {
+            mx = max(mx, max(x0, x1));
+            if (rec && wave == 0 && jr == 0) {           // stream 0's record
+                a.rx16[kb * KR + 2 * q] = x0;
+                a.rx16[kb * KR + 2 * q + 1] = x1;
             }
-            if (rec && kb == 0 && wave == 0 && jr == 0 && lane == 0) { a.rexls[0] = sh - 16; a.rexls[1] = 0; }
+            return (int)__builtin_amdgcn_perm((unsigned)min(x1, 32767), (unsigned)min(x0, 32767), 0x05040100u);
+        };
+        bool wide = false;
+#pragma unroll
+        for (int jr = 0; jr < 4; jr++) {
+            const int sh = shv[jr];
+            const i64 half = sh ? (i64)1 << (sh - 1) : 0;   // rshift(v, sh), sh in [0, 49]: (v + half) >> sh
+            int* xrow_s = xs + (4 * wave + jr) * XSTR;
+            if ((u64)orr[jr] < ((u64)1 << 31)) {         // every |value| below 2^31: the 32-bit copies are the values
+#pragma unroll
+                for (int c = 0; c < NCH4; c++) {
+                    const v4 w = xr[jr][c];
+                    const int q = 2 * (64 * c + lane);
+                    const int p0 = pair(jr, q, (int)(((i64)w[0] + half) >> sh), (int)(((i64)w[1] + half) >> sh));
+                    const int p1 = pair(jr, q + 1, (int)(((i64)w[2] + half) >> sh), (int)(((i64)w[3] + half) >> sh));
+                    *reinterpret_cast<int2*>(xrow_s + q) = int2{p0, p1};
+                }
+            } else {
+                wide = true;
+            }
+        }
+        // (rare) a row past 31 bits, read again at 64 bits (value pair 64 c + lane) after every other row, so
+        // that the wait for these loads holds up nothing else
+        if (wide) {
+            const __amdgpu_buffer_rsrc_t r64 = buf_rsrc(a.X, (unsigned)(a.rows * a.xstride) * 8u);
+#pragma unroll
+            for (int jr = 0; jr < 4; jr++) {
+                if ((u64)orr[jr] < ((u64)1 << 31)) continue;
+                const int sh = shv[jr];
+                const i64 half = sh ? (i64)1 << (sh - 1) : 0;
+#pragma unroll
+                for (int c = 0; c < NCH; c++) {
+                    const v4 w = buf_load4(r64, (unsigned)((row0 + jr) * a.xstride + kb * KR + 2 * (64 * c + lane)) * 8u);
+                    const int x0 = (int)(wadd((i64)(((u64)(unsigned)w[1] << 32) | (unsigned)w[0]), half) >> sh);
+                    const int x1 = (int)(wadd((i64)(((u64)(unsigned)w[3] << 32) | (unsigned)w[2]), half) >> sh);
+                    xs[(4 * wave + jr) * XSTR + 64 * c + lane] = pair(jr, 64 * c + lane, x0, x1);
+                }
+            }
         }
         const bool c_here = __ballot(mx == 32768) != 0;
         if (lane == 0) cfw[wave] = c_here;
@@ -548,6 +588,7 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs a) {
         const int j = (nt * NB + nb) * 16 + (lane & 15);
         if (j < a.N) {
             a.Y[(size_t)row * a.ystride + j] = y2[nb];
+            if ((EPI == EPI_GAUGED_EDGE || EPI == EPI_PLAIN_EDGE) && a.Y32) a.Y32[(size_t)row * a.ystride + j] = (int)y2[nb];
             if (rec) {                                   // stream 0's record
                 if (a.rpile) a.rpile[j] = pile[nb];
                 if (a.rout) a.rout[j] = EPI == EPI_PLAIN_EDGE ? y1[nb] : y2[nb];

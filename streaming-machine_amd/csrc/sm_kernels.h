@@ -133,6 +133,8 @@ struct AttArgs {
     int* EK;            // [B][12][ctx]     their water levels
     int* V;             // [B][12][ctx][64] raw gauged values (checked to fit 32 bits)
     i64* out;           // [B][768]
+    int* out32;         // [B][768] (when non-null): the same values' low 32 bits, for a consumer that reads a
+                        // row's 32-bit copy wherever its OR words show that the row fits (k_gemm's SRC path)
     i64* out_or;        // [B][12] (when non-null): OR of |out| over each head's 64 values, the next light's
                         // water level without a pass over the row
     const int* pos;     // position being written and read up to (inclusive)

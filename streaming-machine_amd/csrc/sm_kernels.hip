@@ -1272,6 +1272,7 @@ __global__ __launch_bounds__(NTHR, ONE ? 1 : 3) void k_attend(AttArgs a) {
             o = power_e(tot, F, F & 0xFFFF, zhp, a.tb);
         }
         a.out[(size_t)b * 768 + h * 64 + lane] = o;
+        if (a.out32) a.out32[(size_t)b * 768 + h * 64 + lane] = (int)o;
         if (a.out_or) {
             const i64 w = wave_or64(iabs64(o));
             if (lane == 0) a.out_or[(size_t)b * 12 + h] = w;
@@ -1398,6 +1399,12 @@ __global__ __launch_bounds__(128) void k_kv_rows(AttArgs a) {
 
 // ---------------------------------------------------------------------------------------------------------
 // Exhaustive check of the loaded tables against their defining formulas (counts the entries that differ).
+// the low 32 bits of n int64 values (a caller's rows for k_gemm's SRC path)
+__global__ void k_low32(const i64* x, int* y, i64 n) {
+    const i64 i = (i64)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) y[i] = (int)x[i];
+}
+
 __global__ void k_check_tables(Tables tb, unsigned* bad) {
     const int i = blockIdx.x * blockDim.x + threadIdx.x;
     if (i < 65536) {

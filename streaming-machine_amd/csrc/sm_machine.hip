@@ -354,6 +354,7 @@ struct sm_machine {
     sm_tables T;
     // state
     i64 *R = nullptr, *QKV = nullptr, *att = nullptr, *hid = nullptr;
+    int *att32 = nullptr, *hid32 = nullptr;   // batched: the attention and hidden rows' low 32 bits (k_gemm's SRC)
     i64* R0 = nullptr;                                  // batch 1: the entering row of the next position
     i64* attor = nullptr;                               // [rows][12] OR of |att| over each head's values
     i64* hidor = nullptr;                               // [rows][192] OR of |hid| over each fc tile's columns
@@ -478,7 +479,7 @@ static void machine_free(sm_machine* m) {
     free_plate(m->head);
     free_mfma_plate(m->mhead);
     tables_free(m->T);
-    void* ps[] = {m->pfmap, m->planes, m->part_acc, m->rowinfo, m->wte, m->wpe, m->R, m->R0, m->QKV, m->att, m->attor, m->hidor, m->sfacts, m->hid, m->K16, m->KM, m->EK, m->V, m->seq, m->words, m->ctl,
+    void* ps[] = {m->pfmap, m->planes, m->part_acc, m->rowinfo, m->wte, m->wpe, m->R, m->R0, m->QKV, m->att, m->att32, m->hid32, m->attor, m->hidor, m->sfacts, m->hid, m->K16, m->KM, m->EK, m->V, m->seq, m->words, m->ctl,
                   m->part_v, m->part_i, m->r_x16, m->r_exls, m->r_pile, m->r_qkv, m->r_att, m->r_hid, m->r_resid,
                   m->r_hx16, m->r_hexls, m->r_hpile, m->r_logits, m->r_gauge, m->r_fcpre, m->r_hgauge,
                   m->fg, m->fb, m->ew, m->ee, m->ew2, m->cosT, m->sinT, m->cosF, m->sinF, m->KF,
@@ -550,7 +551,7 @@ static int launch_step_batched(sm_machine* m, int parts, int nrows = 0,
             const size_t per = (size_t)m->B * m->ctx;
             a.QKV = m->QKV; a.K16 = m->K16 + l * per * 768; a.KM = m->KM + l * per * 12; a.EK = m->EK + l * per * 12; a.V = m->V + l * per * 768;
             a.out = m->att; a.pos = ctl + CTL_POS; a.ctx = m->ctx; a.tb = tb; a.err = ctl + CTL_ERR;
-            a.rec_pos = recp; a.ratt = m->r_att + l * 768; a.rowmap = rowmap; a.out_or = m->attor;
+            a.rec_pos = recp; a.ratt = m->r_att + l * 768; a.rowmap = rowmap; a.out_or = m->attor; a.out32 = m->att32;
             if (rowmap) {
                 launch(m->cfg.profile, "kv_rows", k_kv_rows<0>, dim3(12, B), dim3(128), 0, m->st, a);
                 if (l == 11) break;
@@ -563,19 +564,19 @@ static int launch_step_batched(sm_machine* m, int parts, int nrows = 0,
             // stream's light and gauge for fc (a light formed in fc's own blocks measured slower: the gauge's
             // table reads would follow the row's conversion there)
             GemmArgs a = gemm_args(m->mbank[l][1], m->R, 768, rp + 3072, m->r_resid + (l * 2 + 0) * 768);
-            a.X = m->att; a.xstride = 768; a.orw = m->attor; a.rx16 = rx + 3072; a.rexls = re + 2;
+            a.X = m->att; a.X32 = m->att32; a.xstride = 768; a.orw = m->attor; a.rx16 = rx + 3072; a.rexls = re + 2;
             launch(m->cfg.profile, "proj", k_gemm<768, 1, 1, EPI_PLAIN_ADD, 12>, dim3(m->mbank[l][1].ntiles, RT), dim3(256), 0, m->st, a);
             LightArgs g = light_args(768, m->R, rx + 2 * 3072, re + 4);
             launch(m->cfg.profile, "light.gauge", k_light<768, PRO_GAUGE, 192, 1>, dim3(B), dim3(192), 0, m->st, g);
         }
         {   // fc: gauged, the edge, written (the hidden rows) with their OR words
             GemmArgs a = gemm_args(m->mbank[l][2], m->hid, 3072, rp + 2 * 3072, m->r_hid + l * 3072);
-            a.orw_out = m->hidor;
+            a.orw_out = m->hidor; a.Y32 = m->hid32;
             launch(m->cfg.profile, "fc", k_gemm<768, 1, 1, EPI_GAUGED_EDGE>, dim3(m->mbank[l][2].ntiles, RT), dim3(256), 0, m->st, a);
         }
         {   // mproj: the hidden rows' light formed in each K slice's blocks; partial accumulators and slice facts
             GemmArgs a = gemm_args(m->mbank[l][3], nullptr, 0, nullptr, nullptr);
-            a.X = m->hid; a.xstride = 3072; a.orw = m->hidor; a.rx16 = rx + 3 * 3072; a.rexls = re + 6;
+            a.X = m->hid; a.X32 = m->hid32; a.xstride = 3072; a.orw = m->hidor; a.rx16 = rx + 3 * 3072; a.rexls = re + 6;
             a.sfacts = m->sfacts;
             launch(m->cfg.profile, "mproj.part", k_gemm<3072, 3, 4, EPI_PART, 192>, dim3(m->mbank[l][3].ntiles / 3 * 4, RT), dim3(256), 0, m->st, a);
         }
@@ -854,13 +855,13 @@ static int launch_step_pythia_batched(sm_machine* m, int parts, int nrows = 0,
             GemmArgs a = gemm_args(m->mbank[l][2], pB, rB);
             a.Y = m->hid; a.ystride = 3072;
             a.rpile = rp + 2 * 3072; a.rout = m->r_fcpre + l * 3072; a.rout2 = m->r_hid + l * 3072;
-            a.orw_out = m->hidor;
+            a.orw_out = m->hidor; a.Y32 = m->hid32;
             launch(m->cfg.profile, "fc", k_gemm<768, 1, 1, EPI_PLAIN_EDGE>, dim3(m->mbank[l][2].ntiles, RT), dim3(256), 0, m->st, a);
         }
         {   // mproj: the hidden rows' light formed in each K slice's blocks; partials over four K slices
             GemmArgs a = gemm_args(m->mbank[l][3], nullptr, nullptr);
             a.part = P0;
-            a.X = m->hid; a.xstride = 3072; a.orw = m->hidor; a.sfacts = m->sfacts;
+            a.X = m->hid; a.X32 = m->hid32; a.xstride = 3072; a.orw = m->hidor; a.sfacts = m->sfacts;
             a.rx16 = m->r_x16 + (l * 4 + 3) * 3072; a.rexls = m->r_exls + (l * 4 + 3) * 2;
             launch(m->cfg.profile, "mproj.part", k_gemm<3072, 3, 4, EPI_PART, 192>, dim3(m->mbank[l][3].ntiles / 3 * 4, RT), dim3(256), 0, m->st, a);
         }
@@ -871,14 +872,14 @@ static int launch_step_pythia_batched(sm_machine* m, int parts, int nrows = 0,
             a.out = m->att; a.pos = ctl + CTL_POS; a.ctx = m->ctx; a.tb = tb; a.err = ctl + CTL_ERR;
             a.rec_pos = recp; a.ratt = m->r_att + l * 768; a.rowmap = rowmap;
             a.cosT = m->cosT; a.sinT = m->sinT; a.rot = m->rot; a.half = m->half; a.ehalf = m->ehalf;
-            a.out_or = m->attor;
+            a.out_or = m->attor; a.out32 = m->att32;
             if (rowmap) launch(m->cfg.profile, "kv_rows", k_kv_rows<1>, dim3(12, B), dim3(128), 0, m->st, a);
             launch(m->cfg.profile, "attend", k_attend<1, 0, 1>, dim3(12, B), dim3(NTHR), (size_t)m->ctx * 12, m->st, a);
         }
         {   // proj: the attention rows' light formed in its bank, added into the stream (R + At)
             GemmArgs g = gemm_args(m->mbank[l][1], nullptr, nullptr);
             g.Y = m->R; g.ystride = 768; g.rpile = rp + 3072; g.rout = m->r_resid + (l * 2 + 0) * 768;
-            g.X = m->att; g.xstride = 768; g.orw = m->attor;
+            g.X = m->att; g.X32 = m->att32; g.xstride = 768; g.orw = m->attor;
             g.rx16 = m->r_x16 + (l * 4 + 1) * 3072; g.rexls = m->r_exls + (l * 4 + 1) * 2;
             launch(m->cfg.profile, "proj", k_gemm<768, 1, 1, EPI_PLAIN_ADD, 12>, dim3(m->mbank[l][1].ntiles, RT), dim3(256), 0, m->st, g);
         }
@@ -1263,7 +1264,7 @@ extern "C" int sm_create(const char* layout_dir, const sm_config* cfg, sm_machin
     const size_t nsets = m->kind == 1 && mfma ? 2 : 1;      // light-plane sets (the Pythia MFMA phases keep two)
     if ((rc = dalloc(&m->R, RC * 768)) || (rc = dalloc(&m->R0, 768)) || (rc = dalloc(&m->QKV, RC * 2304)) || (rc = dalloc(&m->att, RC * 768)) || (rc = dalloc(&m->attor, RC * 12)) ||
         (rc = dalloc(&m->hidor, RC * 192)) || (rc = dalloc(&m->sfacts, 4 * RC * 4)) ||
-        (rc = dalloc(&m->hid, RC * 3072)) || (rc = dalloc(&m->K16, 12 * B * ctx * 768)) || (rc = dalloc(&m->KM, 12 * B * ctx * 12)) ||
+        (rc = dalloc(&m->hid, RC * 3072)) || (mfma && ((rc = dalloc(&m->att32, RC * 768)) || (rc = dalloc(&m->hid32, RC * 3072)))) || (rc = dalloc(&m->K16, 12 * B * ctx * 768)) || (rc = dalloc(&m->KM, 12 * B * ctx * 12)) ||
         (rc = dalloc(&m->EK, 12 * B * ctx * 12)) ||
         (rc = dalloc(&m->pfmap, B * ctx)) ||
         (rc = dalloc(&m->V, 12 * B * ctx * 768)) || (m->farr && (rc = dalloc(&m->KF, 12 * ctx * 768))) || (rc = dalloc(&m->seq, B * (ctx + 1))) || (rc = dalloc(&m->words, B * (ctx + 1))) ||
@@ -1679,12 +1680,13 @@ struct sm_plate {
     int* rowinfo = nullptr;
     int* part = nullptr;       // nin 3072: the K slices' accumulators and light facts (sm_plate_product_rows_from)
     int* sfacts = nullptr;
+    int* x32 = nullptr;        // sm_plate_product_rows_from: the caller rows' low 32 bits [64][nin]
 };
 
 static void plate_free(sm_plate* p) {
     free_plate(p->P);
     free_mfma_plate(p->M);
-    hfree(p->planes); hfree(p->rowinfo); hfree(p->part); hfree(p->sfacts);
+    hfree(p->planes); hfree(p->rowinfo); hfree(p->part); hfree(p->sfacts); hfree(p->x32);
     delete p;
 }
 
@@ -1700,7 +1702,7 @@ extern "C" int sm_plate_create(const int16_t* w, const int32_t* e, const int64_t
         p->mfma = true;
         const size_t pb = (size_t)4 * (nin / 64) * 3 * 1024;
         if ((rc = upload_mfma_plate(p->M, w, e, (const i64*)b, nin, nout)) || (rc = dalloc(&p->planes, pb)) ||
-            (rc = dalloc(&p->rowinfo, (size_t)64 * 8)) ||
+            (rc = dalloc(&p->rowinfo, (size_t)64 * 8)) || (rc = dalloc(&p->x32, (size_t)64 * nin)) ||
             (nin == 3072 && ((rc = dalloc(&p->part, (size_t)4 * 3 * 64 * (size_t)p->M.ntiles * 16)) ||
                              (rc = dalloc(&p->sfacts, (size_t)4 * 64 * 4))))) {
             plate_free(p);
@@ -1833,6 +1835,11 @@ extern "C" int sm_plate_product_rows_from(const sm_plate* p, const int64_t* X, c
     ga.K = P.K; ga.N = P.N; ga.rows = rows; ga.RT = RT; ga.W = P.W; ga.csum = P.csum; ga.we = P.e; ga.bias = P.b;
     ga.Y = (i64*)pile; ga.ystride = P.N;
     ga.X = (const i64*)X; ga.xstride = P.K; ga.orw = (const i64*)orw;
+    ga.X32 = p->x32;           // the rows' 32-bit copies, read where a row's OR words show that they fit
+    {
+        const i64 n = (i64)rows * P.K;
+        launch(g_kt.stages, "plate.low32", k_low32, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, (const i64*)X, p->x32, n);
+    }
     if (P.K == 768) {
         launch(g_kt.stages, "plate.gemm_from", k_gemm<768, 1, 1, EPI_PILE, 12>, dim3(P.ntiles, RT), dim3(256), 0, s, ga);
     } else {
