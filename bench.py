@@ -694,11 +694,19 @@ def main():
                 "note": "the same workload with the whole word table read every step (Machine(top='plain')); words "
                         "gated on base2.py's like the main line"}},
         "floor": None if floor is None else {
-            **floor, "step_us": round(1000.0 * b1["ms"], 2), "step_over_bytes_floor": round(1000.0 * b1["ms"] / floor["bytes_us"], 3),
+            **{k: v for k, v in floor.items() if k != "b64"},
+            "step_us": round(1000.0 * b1["ms"], 2), "step_over_bytes_floor": round(1000.0 * b1["ms"] / floor["bytes_us"], 3),
             "note": "the step's 62 dependent launches with the machine's grids, replayed from graphs of 15 steps: "
                     "empty_us with empty kernels, bytes_us with every kernel reading its row and its plate share "
                     "(the top read's high-byte plane for the head) and writing its outputs, no arithmetic "
-                    "(streaming-machine_amd/floor_probe)"},
+                    "(streaming-machine_amd/floor_probe)",
+            "b64": None if "b64" not in floor else {
+                **floor["b64"],
+                **({"step_us": round(1000.0 * batched["ms_per_step"], 2),
+                    "step_over_bytes_floor": round(1000.0 * batched["ms_per_step"] / floor["b64"]["bytes_us"], 3)} if batched else {}),
+                "note": "the 64-stream step's 86 launches with the machine's grids, graphs of 16 steps: each bank block "
+                        "reading its light planes or 32-bit rows and its plate share, each attention block 96 positions "
+                        "of its cache rows, the head its plate, no arithmetic"}},
         "batched": batched,
         "pythia": pyleg,
         "gemv": gemv,

@@ -1,4 +1,4 @@
-// The batch-1 decode step's launch-structure floor, measured: the step's 62 dependent launches (12 layers x
+// The decode step's launch-structure floor, measured.  Batch 1: the step's 62 dependent launches (12 layers x
 // [qkv, attend, proj, fc, mproj], the head's first stage, the race) with the machine's grids and block sizes,
 // replayed from a HIP graph of 15 steps, in two forms:
 //   empty  - every kernel returns at once: the cost of 62 dependent launches alone;
@@ -7,7 +7,12 @@
 //            high-byte plane of the top read), the attention reads 16 cached positions of keys (int16) and values
 //            (int32) per head, and each kernel writes its outputs -- no arithmetic beyond folding what it read.
 // The machine's step does all of this plus its arithmetic, so its time over "bytes" is what the arithmetic,
-// the block reductions and the table reads cost.  Prints one JSON line.
+// the block reductions and the table reads cost.
+// 64 streams ("b64"): the batched step's 86 launches (12 layers x [qkv, attend, proj, light, fc, mproj
+// partials, light], the head, the race) with the machine's grids, graphs of 16 steps, the same two forms; in
+// "bytes" each bank block reads its row tile's light planes or int32 rows and its plate share, each attention
+// block 96 positions of its cache rows (38 KB), each light block its row (and the partials), the head its plate.
+// Prints one JSON line with both.
 #include <hip/hip_runtime.h>
 #include <cstdio>
 
@@ -121,14 +126,121 @@ static int run(double& us) {
     return 0;
 }
 
+// ---- 64 streams ----
+// a block reads NA int4 a thread of A (region blockIdx.y ra + blockIdx.x rax) and NB of B (region blockIdx.x rb),
+// then writes NOUT values
+template <int NT, int NA, int NB, int NOUT, bool EMPTY, int ID>
+__global__ __launch_bounds__(NT) void k_floor_move(const v4i* A, size_t ra, size_t rax, const v4i* B, size_t rb, i64* out) {
+    if (EMPTY) return;
+    const int tid = threadIdx.x;
+    const v4i* a = A + (size_t)blockIdx.y * ra + (size_t)blockIdx.x * rax + tid;
+    const v4i* b = B + (size_t)blockIdx.x * rb + tid;
+    int s = 0;
+#pragma unroll
+    for (int i = 0; i < NA; i++) { const v4i v = a[(size_t)NT * i]; s += v.x ^ v.y ^ v.z ^ v.w; }
+#pragma unroll
+    for (int i = 0; i < NB; i++) { const v4i v = b[(size_t)NT * i]; s += v.x ^ v.y ^ v.z ^ v.w; }
+    const size_t blk = (size_t)blockIdx.y * gridDim.x + blockIdx.x;
+    for (int i = tid; i < NOUT; i += NT) out[blk * NOUT + i] = s + i;
+}
+// the head: each block its waves' light planes, then its share of the plate
+template <bool EMPTY>
+__global__ __launch_bounds__(256) void k_floor_head64(const v4i* planes, const v4i* W, size_t nW, i64* part) {
+    if (EMPTY) return;
+    const int tid = threadIdx.x;
+    int s = 0;
+#pragma unroll
+    for (int i = 0; i < 24; i++) { const v4i v = planes[tid + 256 * i]; s += v.x ^ v.y; }
+    for (size_t i = (size_t)blockIdx.x * 256 + tid; i < nW; i += (size_t)gridDim.x * 256) { const v4i v = W[i]; s += v.x ^ v.w; }
+    if (tid < 64) part[(size_t)blockIdx.x * 64 + tid] = s;
+}
+template <bool EMPTY>
+__global__ __launch_bounds__(256) void k_floor_race64(const i64* part, i64* R) {
+    if (EMPTY) return;
+    i64 b = 0;
+    for (int i = threadIdx.x; i < 512; i += 256) b = max(b, part[(size_t)i * 64 + blockIdx.x]);
+    b = max(b, __shfl_xor(b, 1, 64));
+    if (threadIdx.x == 0) R[blockIdx.x] = b;
+}
+
+template <bool EMPTY>
+static int run64(double& us) {
+    const size_t qkvB = 768 * 2304 * 2, projB = 768 * 768 * 2, fcB = 768 * 3072 * 2, mpB = 3072 * 768 * 2;
+    const size_t headB = (size_t)768 * 50272 * 2, layerB = qkvB + projB + fcB + mpB;
+    const size_t kvL = (size_t)64 * 12 * 160 * 396;          // a layer's cache: 64 streams x 12 heads x 160 positions
+    const size_t planesB = 4 * 36864 * 2, rowsB = (size_t)64 * 3072 * 8, partsB = (size_t)4 * 3 * 64 * 768 * 4, NOUTV = 1 << 19;
+    const int STEPS = 16, REPS = 10;
+    char *plates = nullptr, *planes, *rows, *parts, *kv;
+    i64* out;
+    CHK(hipMalloc(&plates, 12 * layerB + headB)); CHK(hipMalloc(&planes, planesB)); CHK(hipMalloc(&rows, rowsB));
+    CHK(hipMalloc(&parts, partsB)); CHK(hipMalloc(&kv, 12 * kvL)); CHK(hipMalloc(&out, NOUTV * 8));
+    CHK(hipMemset(plates, 1, 12 * layerB + headB)); CHK(hipMemset(planes, 1, planesB)); CHK(hipMemset(rows, 1, rowsB));
+    CHK(hipMemset(parts, 1, partsB)); CHK(hipMemset(kv, 1, 12 * kvL)); CHK(hipMemset(out, 0, NOUTV * 8));
+    CHK(hipDeviceSynchronize());
+    hipStream_t st;
+    CHK(hipStreamCreateWithFlags(&st, hipStreamNonBlocking));
+    const v4i *P = (const v4i*)planes, *Rw = (const v4i*)rows, *Pa = (const v4i*)parts;
+    hipGraph_t g;
+    hipGraphExec_t ge;
+    CHK(hipStreamBeginCapture(st, hipStreamCaptureModeGlobal));
+    for (int s = 0; s < STEPS; s++) {
+        const char* pl = plates;
+        for (int l = 0; l < 12; l++) {
+            const v4i* wq = (const v4i*)pl; pl += qkvB;
+            const v4i* wp = (const v4i*)pl; pl += projB;
+            const v4i* wf = (const v4i*)pl; pl += fcB;
+            const v4i* wm = (const v4i*)pl; pl += mpB;
+            const v4i* kvl = (const v4i*)(kv + l * kvL);
+            // qkv: the row tile's light planes (36 KB) and the column tile's plate (24 KB)
+            k_floor_move<256, 9, 6, 256, EMPTY, 1><<<dim3(144, 4), 256, 0, st>>>(P, 2304, 0, wq, 1536, out);
+            // attention: each (head, stream) block 96 positions of its cache rows (38 KB)
+            k_floor_move<256, 9, 0, 64, EMPTY, 2><<<dim3(12, 64), 256, 0, st>>>(kvl, 12 * 2376, 2376, kvl, 0, out);
+            // proj: the tile's attention rows at 32 bits (48 KB) and its plate (24 KB)
+            k_floor_move<256, 12, 6, 256, EMPTY, 3><<<dim3(48, 4), 256, 0, st>>>(Rw, 3072, 0, wp, 1536, out);
+            // the stream's light: a row (6 KB) a block
+            k_floor_move<192, 2, 0, 288, EMPTY, 4><<<dim3(1, 64), 192, 0, st>>>(Rw, 384, 0, Rw, 0, out);
+            // fc: light planes (36 KB) and plate (24 KB)
+            k_floor_move<256, 9, 6, 256, EMPTY, 5><<<dim3(192, 4), 256, 0, st>>>(P, 2304, 0, wf, 1536, out);
+            // mproj partials: the tile's hidden rows of its K slice at 32 bits (48 KB) and three column tiles (72 KB)
+            k_floor_move<256, 12, 18, 1152, EMPTY, 6><<<dim3(64, 4), 256, 0, st>>>(Rw, 3072, 0, wm, 4608, out);
+            // mproj's finish and the next light: four slices' partials (36 KB) and the row a block
+            k_floor_move<192, 12, 2, 1056, EMPTY, 7><<<dim3(1, 64), 192, 0, st>>>(Pa, 2304, 0, Rw, 0, out);
+        }
+        k_floor_head64<EMPTY><<<512, 256, 0, st>>>(P, (const v4i*)pl, headB / 16, out);
+        k_floor_race64<EMPTY><<<64, 256, 0, st>>>(out, out + (1 << 18));
+    }
+    CHK(hipStreamEndCapture(st, &g));
+    CHK(hipGraphInstantiate(&ge, g, nullptr, nullptr, 0));
+    hipEvent_t e0, e1;
+    CHK(hipEventCreate(&e0)); CHK(hipEventCreate(&e1));
+    for (int i = 0; i < 2; i++) CHK(hipGraphLaunch(ge, st));
+    CHK(hipStreamSynchronize(st));
+    CHK(hipEventRecord(e0, st));
+    for (int i = 0; i < REPS; i++) CHK(hipGraphLaunch(ge, st));
+    CHK(hipEventRecord(e1, st));
+    CHK(hipStreamSynchronize(st));
+    float ms = 0.0f;
+    CHK(hipEventElapsedTime(&ms, e0, e1));
+    us = ms * 1000.0 / (REPS * STEPS);
+    CHK(hipEventDestroy(e0)); CHK(hipEventDestroy(e1));
+    CHK(hipGraphExecDestroy(ge)); CHK(hipGraphDestroy(g)); CHK(hipStreamDestroy(st));
+    for (void* q : {(void*)plates, (void*)planes, (void*)rows, (void*)parts, (void*)kv, (void*)out}) CHK(hipFree(q));
+    return 0;
+}
+
 int main() {
-    double empty = 1e30, bytes = 1e30;
+    double empty = 1e30, bytes = 1e30, e64 = 1e30, b64 = 1e30;
     for (int r = 0; r < 3; r++) {             // the best of three measurements of each form
         double e, b;
         if (run<true>(e) || run<false>(b)) return 1;
         empty = e < empty ? e : empty;
         bytes = b < bytes ? b : bytes;
+        if (run64<true>(e) || run64<false>(b)) return 1;
+        e64 = e < e64 ? e : e64;
+        b64 = b < b64 ? b : b64;
     }
-    printf("{\"launches\": 62, \"empty_us\": %.2f, \"bytes_us\": %.2f, \"ctx\": 16, \"graph_steps\": 15}\n", empty, bytes);
+    printf("{\"launches\": 62, \"empty_us\": %.2f, \"bytes_us\": %.2f, \"ctx\": 16, \"graph_steps\": 15, "
+           "\"b64\": {\"launches\": 86, \"empty_us\": %.2f, \"bytes_us\": %.2f, \"ctx\": 96, \"graph_steps\": 16}}\n",
+           empty, bytes, e64, b64);
     return 0;
 }
