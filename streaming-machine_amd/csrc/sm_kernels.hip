@@ -25,14 +25,16 @@
 #define NTHR 256
 
 // ---------------------------------------------------------------------------------------------------------
-// block reductions (4 waves).  red: 8 slots, free on entry; every thread gets the result.
-template <typename F>
+// block reductions (NW waves, 4 by default).  red: NW slots, free on entry; every thread gets the result.
+template <typename F, int NW = 4>
 SMD i64 block_reduce(i64 v, i64* red, F op, int tid) {
     const int lane = tid & 63, wave = tid >> 6;
     v = wave_reduce64(v, op);
     if (lane == 0) red[wave] = v;
     __syncthreads();
-    i64 r = op(op(red[0], red[1]), op(red[2], red[3]));
+    i64 r = red[0];
+#pragma unroll
+    for (int w = 1; w < NW; w++) r = op(r, red[w]);
     __syncthreads();
     return r;
 }
@@ -1022,7 +1024,6 @@ SMD i64 attend_short(const AttArgs& a, int p, int h, int b, int* q_s, int* w_s, 
 // the first rot dims of q and k turned by position before their water level; scores
 // power(q16 . k16, (eq + ek + 10) 65536 - half); the final power exact in 128 bits (the reference's power never
 // wraps, :81-85); its asserts (turn input < 2^31, max|v| sum(a) < 2^62, a result that fits) set SM_ERR_RANGE.
-#define ACH 64
 template <bool B> struct Flag { static constexpr bool value = B; };
 #define ATT_PRE 2            // passes of 64 positions whose keys and values are requested at launch (the ring
                              // of key slots the scores loop refills two passes ahead)
@@ -1030,9 +1031,13 @@ template <bool B> struct Flag { static constexpr bool value = B; };
 // a SIMD so that 768 blocks are resident at once
 // REC = 0: nothing is recorded (no record position is read)
 // FTURN = 1 (one stream, Pythia): turn=float
-template <int MODEL, int ONE, int REC, int FTURN = 0>
-__global__ __launch_bounds__(NTHR, ONE ? 1 : 3) void k_attend(AttArgs a) {
+// NTB: the block's threads (256 or 512): a pass scores NTB / 4 positions (four lanes a position), the value sum
+// runs NTB / 16 position groups; more threads keep more of the cache's loads in flight where the grid is small
+template <int MODEL, int ONE, int REC, int FTURN = 0, int NTB = NTHR>
+__global__ __launch_bounds__(NTB, ONE ? 1 : 3) void k_attend(AttArgs a) {
     static_assert(!FTURN || (MODEL == 1 && ONE), "turn=float is the one-stream Pythia machine's");
+    static_assert(NTB == 256 || (NTB == 512 && !ONE), "256 threads, or 512 for the many-stream kernel");
+    constexpr int NWB = NTB / 64, ACH = NTB / 4, NGR = NTB / 16;   // waves, positions a pass, value-sum groups
     extern __shared__ __align__(16) unsigned char smem[];
     i64* sc = reinterpret_cast<i64*>(smem);                  // [ctx] scores
     int* arr = reinterpret_cast<int*>(sc + a.ctx);           // [ctx] arrivals
@@ -1040,7 +1045,7 @@ __global__ __launch_bounds__(NTHR, ONE ? 1 : 3) void k_attend(AttArgs a) {
     __shared__ __align__(16) int k16s[64];
     __shared__ __align__(16) int vs[64];
     __shared__ i64 red[8];
-    __shared__ i64 numr[16][64];
+    __shared__ i64 numr[NGR][64];
     __shared__ int eqs, eks;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int sl = tid >> 2, qd = tid & 3;                   // scores: position in the pass, lane of the position
@@ -1103,7 +1108,7 @@ __global__ __launch_bounds__(NTHR, ONE ? 1 : 3) void k_attend(AttArgs a) {
     i64 kmp[ATT_PRE];
 #pragma unroll
     for (int c = 0; c < ATT_PRE; c++) {
-        const unsigned sr = sl + 64 * c;
+        const unsigned sr = sl + ACH * c;
         kp[c][0] = buf_load4(rk, sr * 128 + qd * 32);
         kp[c][1] = buf_load4(rk, sr * 128 + qd * 32 + 16);
         ekp[c] = buf_load1(re, sr * 4);
@@ -1143,12 +1148,12 @@ __global__ __launch_bounds__(NTHR, ONE ? 1 : 3) void k_attend(AttArgs a) {
     }
     __syncthreads();
 
-    // the values of positions g, g + 16, .. of the first ATT_PRE passes, requested now: the new q and the
+    // the values of positions g, g + NGR, .. of the first ATT_PRE passes, requested now: the new q and the
     // keys were ahead of them, and they arrive while the scores are formed
-    constexpr int NV = 64 * ATT_PRE / 16;
+    constexpr int NV = ACH * ATT_PRE / NGR;
     v4i vp[NV];
 #pragma unroll
-    for (int i = 0; i < NV; i++) vp[i] = buf_load4(rv, (unsigned)(g + 16 * i) * 256 + d4 * 16);
+    for (int i = 0; i < NV; i++) vp[i] = buf_load4(rv, (unsigned)(g + NGR * i) * 256 + d4 * 16);
 
     // scores (base2.py:94 / pythia_base2.py:135) and their maximum
     const i64 eq = eqs;
@@ -1202,16 +1207,16 @@ __global__ __launch_bounds__(NTHR, ONE ? 1 : 3) void k_attend(AttArgs a) {
             if (s0 + ACH <= p) pass(Flag<true>{}, s0 + ACH, kp[1], ekp[1], kmp[1]);
         }
     }
-    mx = block_reduce(mx, red, OpMax(), tid);   // its barriers also publish sc[]
+    mx = block_reduce<OpMax, NWB>(mx, red, OpMax(), tid);   // its barriers also publish sc[]
 
     // arrivals (base2.py:96-97), one position per thread, into LDS; their sum
     i64 z = 0;
-    for (int s = tid; s <= p; s += NTHR) {
+    for (int s = tid; s <= p; s += NTB) {
         const int w = tab_arr(a.tb, wsub(mx, sc[s]));
         arr[s] = w;
         z += w;
     }
-    z = block_reduce(z, red, OpAdd(), tid);     // its barriers also publish arr[]
+    z = block_reduce<OpAdd, NWB>(z, red, OpAdd(), tid);     // its barriers also publish arr[]
     // the divisor's table entries (base2.py:99), requested now so that their latency passes during the value sum:
     // vector loads behind the values (scalar reads would share the LDS reads' wait counter, and the value sum's
     // first LDS read would wait for them); read unconditionally, the recomputed entries replace them where the
@@ -1229,35 +1234,35 @@ __global__ __launch_bounds__(NTHR, ONE ? 1 : 3) void k_attend(AttArgs a) {
         n0 += (i64)w * x.x; n1 += (i64)w * x.y; n2 += (i64)w * x.z; n3 += (i64)w * x.w;
         if (MODEL == 1 && w) vmax = max(vmax, max(max(abs(x.x), abs(x.y)), max(abs(x.z), abs(x.w))));
     };
-    // below 128 positions every value was requested after the new position came in; beyond, chunks of 16 NV
+    // below 2 ACH positions every value was requested after the new position came in; beyond, chunks of NGR NV
     // positions, each value requested one chunk earlier into the register slot it frees
     if (!longc) {
 #pragma unroll
         for (int i = 0; i < NV; i++) {
-            const int sv = g + 16 * i;
-            if (16 * i > p) break;                  // uniform
+            const int sv = g + NGR * i;
+            if (NGR * i > p) break;                 // uniform
             if (sv < p) acc(arr[sv], vp[i]);
         }
     } else {
-        for (int base = 0; base < p; base += 16 * NV) {
+        for (int base = 0; base < p; base += NGR * NV) {
 #pragma unroll
             for (int i = 0; i < NV; i++) {
-                const int sv = base + g + 16 * i;
+                const int sv = base + g + NGR * i;
                 const v4i x = vp[i];
-                vp[i] = buf_load4(rv, (unsigned)(sv + 16 * NV) * 256 + d4 * 16);
+                vp[i] = buf_load4(rv, (unsigned)(sv + NGR * NV) * 256 + d4 * 16);
                 if (sv < p) acc(arr[sv], x);
             }
         }
     }
-    if ((p & 15) == g) acc(arr[p], reinterpret_cast<const v4i*>(vs)[d4]);   // the new position (from LDS)
+    if (p % NGR == g) acc(arr[p], reinterpret_cast<const v4i*>(vs)[d4]);   // the new position (from LDS)
     if (MODEL == 1 && (double)vmax * (double)z >= 4611686018427387904.0) atomicOr(a.err, SM_ERR_RANGE);
-    // the 16 position groups through LDS, summed by wave 0
+    // the NGR position groups through LDS, summed by wave 0
     numr[g][4 * d4] = n0; numr[g][4 * d4 + 1] = n1; numr[g][4 * d4 + 2] = n2; numr[g][4 * d4 + 3] = n3;
     __syncthreads();
     if (wave == 0) {
         i64 tot = 0;
 #pragma unroll
-        for (int i = 0; i < 16; i++) tot += numr[i][lane];
+        for (int i = 0; i < NGR; i++) tot += numr[i][lane];
         const i64 zlg = zlg_mem, zhp = zhp_mem;
         const i64 F = wsub(0, wadd((i64)zt * 65536, zlg));   // -log2fix(Z), the same in every lane
         i64 o;
@@ -1495,6 +1500,8 @@ INST(768, 2, 4, PRO_PGAUGE, EPI_PLAIN)        // Pythia: qkv
 INST(768, 2, 4, PRO_PGAUGE, EPI_PLAIN_EDGE)   // Pythia: fc
 INST(768, 4, 4, PRO_PGAUGE, EPI_PHEAD)        // Pythia: head
 template __global__ void k_attend<0, 0, 1>(AttArgs);
+template __global__ void k_attend<0, 0, 1, 0, 512>(AttArgs);
+template __global__ void k_attend<1, 0, 1, 0, 512>(AttArgs);
 template __global__ void k_attend<0, 1, 0>(AttArgs);
 template __global__ void k_attend<0, 1, 1>(AttArgs);
 template __global__ void k_attend<1, 0, 1>(AttArgs);

@@ -498,6 +498,21 @@ enum { STEP_ALL = 3, STEP_LAYERS = 1, STEP_HEAD = 2 };
 // the head kernel's blocks: two per CU, each streaming about ntiles / 512 column tiles
 static int head_rows_grid(int ntiles) { return std::min(512, ntiles); }
 
+// the many-stream attention over `rows` rows (one block a head and row): 512-thread blocks where the grid has at
+// most ATT_WIDE_BLOCKS blocks (more of each block's cache loads in flight), else 256.  Measured (same box,
+// identical words): Pythia at 32 streams 62.5 k against 62.0 k tokens/s with 512; GPT-2 at 64 streams 108.5 k
+// against 113.7 k (768 blocks of 512 threads no longer fit three waves a SIMD beside the rest)
+#ifndef ATT_WIDE_BLOCKS
+#define ATT_WIDE_BLOCKS 384
+#endif
+template <int MODEL>
+static void attend_rows(sm_machine* m, int rows, const AttArgs& a) {
+    if (12 * rows <= ATT_WIDE_BLOCKS)
+        launch(m->cfg.profile, "attend", k_attend<MODEL, 0, 1, 0, 512>, dim3(12, rows), dim3(512), (size_t)m->ctx * 12, m->st, a);
+    else
+        launch(m->cfg.profile, "attend", k_attend<MODEL, 0, 1>, dim3(12, rows), dim3(NTHR), (size_t)m->ctx * 12, m->st, a);
+}
+
 // batched streams: every bank is [light kernel (one block per stream) -> MFMA kernel (one block per 16 columns)]
 //
 // rowmap != null: a pass of nrows prompt rows (row r: position rowmap[r] & 0xFFFF of stream rowmap[r] >> 16)
@@ -555,9 +570,9 @@ static int launch_step_batched(sm_machine* m, int parts, int nrows = 0,
             if (rowmap) {
                 launch(m->cfg.profile, "kv_rows", k_kv_rows<0>, dim3(12, B), dim3(128), 0, m->st, a);
                 if (l == 11) break;
-                launch(m->cfg.profile, "attend", k_attend<0, 0, 1>, dim3(12, B), dim3(NTHR), (size_t)m->ctx * 12, m->st, a);
+                attend_rows<0>(m, B, a);
             } else {
-                launch(m->cfg.profile, "attend", k_attend<0, 0, 1>, dim3(12, m->B), dim3(NTHR), (size_t)m->ctx * 12, m->st, a);
+                attend_rows<0>(m, m->B, a);
             }
         }
         {   // proj: the attention rows' light formed in the bank, the plain bank added into the stream; then the
@@ -874,7 +889,7 @@ static int launch_step_pythia_batched(sm_machine* m, int parts, int nrows = 0,
             a.cosT = m->cosT; a.sinT = m->sinT; a.rot = m->rot; a.half = m->half; a.ehalf = m->ehalf;
             a.out_or = m->attor; a.out32 = m->att32;
             if (rowmap) launch(m->cfg.profile, "kv_rows", k_kv_rows<1>, dim3(12, B), dim3(128), 0, m->st, a);
-            launch(m->cfg.profile, "attend", k_attend<1, 0, 1>, dim3(12, B), dim3(NTHR), (size_t)m->ctx * 12, m->st, a);
+            attend_rows<1>(m, B, a);
         }
         {   // proj: the attention rows' light formed in its bank, added into the stream (R + At)
             GemmArgs g = gemm_args(m->mbank[l][1], nullptr, nullptr);
