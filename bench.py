@@ -14,7 +14,8 @@ Printed: one JSON line with the driver's fields plus
                  launches a step, mean microseconds, algorithmic bytes a launch, GB/s, fraction of HBM peak
   roofline       the kernel with the largest share of the step (microseconds a step), from that table;
                  traffic from the HBM counters in profiles/ when they were collected for it
-  step_roofline  the whole step: the workload's bytes of SURVEY 8(d) (248,662,476 + 73,728 T) over its time,
+  step_roofline  the whole step: the workload's bytes (weights with their exponents and biases once a step,
+                 248,662,476, plus k and v at 4 B each a cached position and layer, 73,728 T) over its time,
                  with the bytes this layout reads beside them
   cold           the same profiled step with 1 GiB streamed through the device between steps (the 256 MB
                  Infinity Cache holds none of the step's bytes), beside the warm figures
@@ -26,10 +27,10 @@ Printed: one JSON line with the driver's fields plus
                  streams 0 and 1 checked against base2.py's, of streams 31 and 63 against the oracle's fixture
   pythia         the Pythia-160m-shaped machine, 32 streams, 64-token prompts, 256 words each (streams 0 and 1
                  against pythia_base2.py's words, stream 31 against the oracle's)
-  gemv           config 2: the int16 GEMV at the five GPT-2 shapes, uniform int16 weights and lights, exponents in
+  gemv           the GEMV microbenchmark: the int16 GEMV at the five GPT-2 shapes, uniform int16 weights and lights, exponents in
                  [-16, -8], rotated over >= 1 GiB of plate copies (each launch reads a plate the cache does not
                  hold), pile checked against the exact product
-  attention      config 3: one new position's attention over int16 caches of 128, 512 and 1024 positions
+  attention      the attention microbenchmark: one new position's attention over int16 caches of 128, 512 and 1024 positions
   cpu_baseline   base2.py's CPU path restated in numpy (full recompute per word, float64 products, the top-down
                  race loop) on a bounded sample, median of 5 after a warm-up, all cores and one thread, with the
                  KV-cached C oracle beside it
@@ -88,7 +89,7 @@ def fixture_cases(fname: str) -> dict:
         return {c["name"]: c for c in json.load(f)["cases"]}
 
 
-# ---- algorithmic bytes ----
+# ---- algorithmic bytes of the workload ----
 def bank_bytes(nin: int, nout: int) -> int:
     """a plate read once (int16) with its per-column exponent (int32) and bias (int64)"""
     return 2 * nin * nout + 12 * nout
@@ -96,7 +97,7 @@ def bank_bytes(nin: int, nout: int) -> int:
 
 LAYER_FIXED = sum(bank_bytes(*s) for s in BANKS.values())                 # 14,155,776 + 82,944
 WORKLOAD_FIXED = 12 * LAYER_FIXED + bank_bytes(768, VOCAB)                 # 248,662,476
-KV_WORKLOAD = 12 * 768 * 8        # 73,728 B a cached position: k and v at 4 B each, 12 layers (SURVEY 8(d))
+KV_WORKLOAD = 12 * 768 * 8        # 73,728 B a cached position: k and v at 4 B each, 12 layers
 KV_LAYOUT = 12 * (768 * 6 + 12 * 12)   # what this layout reads: int16 k, int32 v, per head an int32 level, int64 mask
 
 
@@ -165,7 +166,7 @@ def dominant(table: dict, where: str) -> dict:
             "source": "HIP event pair stamped by each dispatch, profiled pass of the same workload"}
 
 
-# ---- batch 1 (config 1) ----
+# ---- batch 1 (GPT-2 124M, 8-token prompt, 16 words) ----
 def b1_leg(sm, lay, steps_req: int, warmup: int, prompt, want, cold_steps: int = 15, top: str = "auto"):
     import torch
     m = sm.Machine(lay, max_ctx=64, graph_steps=WORDS - 1, prefill_rows=PREFILL_ROWS, use_graph=not PLAIN, top=top)
@@ -249,7 +250,7 @@ def b1_leg(sm, lay, steps_req: int, warmup: int, prompt, want, cold_steps: int =
             "table": table, "cold": ctable, "ctx": ctx, "survivors": survivors}
 
 
-# ---- batched legs (configs 4 and 5) ----
+# ---- batched legs (64 GPT-2 streams, 32 Pythia streams) ----
 def gate_words(words, checks, what):
     for stream, want, src in checks:
         if [int(x) for x in words[stream][:len(want)]] != want:
@@ -384,7 +385,7 @@ def pythia_leg(sm):
             "kernels": table}
 
 
-# ---- config 2: the GEMV microbench ----
+# ---- the GEMV microbenchmark ----
 def gemv_leg(sm, rotate_bytes: int = 1 << 30, rounds: int = 3):
     """int16 plates (uniform, -32768 included) with exponents in [-16, -8] and uniform int16 lights, B = 1;
     every launch reads a different copy of the plate out of >= 1 GiB of copies (default_rng(2))"""
@@ -429,7 +430,7 @@ def gemv_leg(sm, rotate_bytes: int = 1 << 30, rounds: int = 3):
                     "are the int16 plate only", "shapes": out}
 
 
-# ---- config 3: one attention step ----
+# ---- the attention microbenchmark: one attention step ----
 def attention_leg(sm, reps: int = 50):
     """12 heads x 64, int16 keys and values uniform at T = 128, 512, 1024 (default_rng(3)), one new q, k, v; the
     batch-1 attention kernel (sm_stage_attend)"""
@@ -452,7 +453,7 @@ def attention_leg(sm, reps: int = 50):
             sm.stages.attend(t, qkv.data_ptr(), k16.data_ptr(), km.data_ptr(), ek.data_ptr(), v.data_ptr(), p, ctx, o.data_ptr())
         n, us = sm.kernel_times(clear=True)["stage.attend"]
         sm.profile_stages(False)
-        kv = T * 768 * 2 * 2                         # int16 k and v
+        kv = T * 768 * 2 * 2                         # int16 k and v (the attention microbenchmark's workload)
         layout = T * 12 * (128 + 8 + 4 + 256)        # this layout: int16 k, int64 mask, int32 level, int32 v
         out[str(T)] = {"us": round(us, 3), "kv_bytes": kv, "layout_bytes": layout,
                        "gbs_layout": round(layout / (us * 1e-6) / 1e9, 1)}
@@ -501,7 +502,7 @@ def cpu_info():
 
 def cpu_baseline(npz, prompt, want, runs: int = 5, words: int = 5):
     """base2.py's CPU path (numpy restatement, forward(ids + got) per word as base2.py:123 does) on words 2..1+words
-    of the config-1 sequence, median of `runs` after one warm-up, at all cores and one thread; and the KV-cached C
+    of the batch-1 sequence, median of `runs` after one warm-up, at all cores and one thread; and the KV-cached C
     oracle over words 2..16"""
     sys.path.insert(0, REPO)
     import oracle
@@ -585,7 +586,7 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported (the batched streams would "
-              f"shard as independent replicas, see DESIGN.md)", file=sys.stderr)
+              f"shard as independent replicas with no exchange)", file=sys.stderr)
         sys.exit(2)
     if args.steps <= 0 or args.warmup < 0:
         sys.exit("bench.py: --steps must be positive and --warmup non-negative")
@@ -674,7 +675,7 @@ def main():
                    "batch": 1, "prompt": PROMPT, "words": WORDS, "vocab": VOCAB},
         "roofline": dominant(table, "b1"),
         "step_roofline": {"bytes_per_step": int(sb), "achieved": round(step_ach, 1), "frac": round(step_ach / HBM_PEAK_GBS, 4),
-                          "bytes": "SURVEY 8(d): 248,662,476 + 73,728 T at mean T = 16",
+                          "bytes": "248,662,476 (weights, exponents, biases) + 73,728 T (k and v at 4 B) at mean T = 16",
                           "layout_bytes_per_step": int(WORKLOAD_FIXED + KV_LAYOUT * b1["ctx"])},
         "kernels": table,
         "cold": cold,

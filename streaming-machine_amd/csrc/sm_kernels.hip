@@ -667,7 +667,7 @@ __global__ __launch_bounds__(256) void k_race1(Race1Args a) {
 // winner only.
 // Three rounds of memory requests: the blocks' lows and candidate counts (with the light); each block's
 // candidates from the highest high down, stopping at the first below T (a block's candidates come in order of
-// falling high; the first is requested in round 1); the survivors' low bytes, four lanes a survivor (192 bytes
+// falling high; the first is requested in the first request); the survivors' low bytes, four lanes a survivor (192 bytes
 // each), 64 survivors a pass.  Survivors
 // past TOP_LIST are finished one thread each (exact, slow: a model whose bounds hold almost nothing).  The step's
 // survivors are written out (count, and the first tmax: word, exact pile, score).
@@ -680,7 +680,7 @@ __global__ __launch_bounds__(256) void k_race_top(TopArgs t) {
     __shared__ i64 red_s[4];
     __shared__ int ln_s;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    // round 1 (with each block's first candidate, its highest high)
+    // first requests (with each block's first candidate, its highest high)
     const int g[2] = {tid, tid + 256};                  // the first stage's blocks of this thread (nblk <= 512)
     i64 bl[2], h[2] = {INT64_MIN, INT64_MIN}, cv[2] = {0, 0};
     int nc[2], jv[2] = {0, 0};
@@ -710,7 +710,7 @@ __global__ __launch_bounds__(256) void k_race_top(TopArgs t) {
     if (lane == 0) red_s[wave] = T;
     __syncthreads();
     T = max(max(red_s[0], red_s[1]), max(red_s[2], red_s[3]));
-    // round 2: both blocks' candidates in step, until each one's high falls below T
+    // second requests: both blocks' candidates in step, until each one's high falls below T
     {
         bool on[2] = {nc[0] > 0, nc[1] > 0};
         for (int c = 0; on[0] || on[1]; c++) {
@@ -746,7 +746,7 @@ __global__ __launch_bounds__(256) void k_race_top(TopArgs t) {
     i64 bv = 0;
     int bi = -1;
     if (ns <= TOP_LIST) {
-        // round 3: four lanes a survivor, lane q of the four its bytes 192 q .. 192 q + 191
+        // third requests: four lanes a survivor, lane q of the four its bytes 192 q .. 192 q + 191
         const int gq = lane & 3, slot = lane >> 2;
         for (int s0 = 16 * wave; s0 < ns; s0 += 64) {
             const int s = s0 + slot;

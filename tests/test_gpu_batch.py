@@ -177,7 +177,7 @@ def batch_machine(sm, full_dir):
     m.close()
 
 
-def test_config4_two_golden_streams(sm, full_dir, golden):
+def test_gpt2_64_streams_two_golden_streams(sm, full_dir, golden):
     """the batched machine's two golden streams of the 64-stream workload, decoded together"""
     cs = [golden_case(golden, f"c4_stream{s}_p32_w4") for s in (0, 1)]
     m = sm.Machine(full_dir, max_ctx=160, max_streams=2)
@@ -185,7 +185,7 @@ def test_config4_two_golden_streams(sm, full_dir, golden):
     m.close()
 
 
-def test_config4_sixty_four_streams(sm, batch_machine, full_oracle, golden):
+def test_gpt2_64_streams_32_token_prompts(sm, batch_machine, full_oracle, golden):
     """64 streams with 32-word prompts: the golden streams and a sample of the rest against the oracle, and the
     KV cache of a late stream"""
     cs = [golden_case(golden, f"c4_stream{s}_p32_w4") for s in (0, 1)]

@@ -8,7 +8,8 @@
   tests/test_oracle_long.py).
 * A 1000-token prompt on a two-stream machine of each model: the prompt pass and the decode steps attend over
   999 to 1006 positions with the batched attention kernel (the block path).
-* The batched attention kernel on config 3's synthetic rows (T = 128, 512, 1024) against base2.py's attention.
+* The batched attention kernel on the attention workload's synthetic rows (T = 128, 512, 1024) against base2.py's
+  attention.
 """
 from __future__ import annotations
 
@@ -47,7 +48,7 @@ def _check_cache(m, case, stream):
     assert h64(m.read("resid", 0, stream)) == case["resid"]
 
 
-def test_config4_sixty_four_streams_full_length(sm, full_dir):
+def test_gpt2_64_streams_128_words_full_length(sm, full_dir):
     """64 streams, 128 words each: streams 0, 1, 31, 63 word for word, stream 63's cache at 0, 128, 158"""
     m = sm.Machine(full_dir, max_ctx=160, max_streams=64)
     prompts = [sm.prompt_ids(4 + s, 32) for s in range(64)]
@@ -61,7 +62,7 @@ def test_config4_sixty_four_streams_full_length(sm, full_dir):
     m.close()
 
 
-def test_config5_thirty_two_streams_full_length(sm, py_full_dir):
+def test_pythia_32_streams_256_words_full_length(sm, py_full_dir):
     """32 Pythia streams, 256 words each: streams 0, 1, 31 word for word, stream 31's cache at 0, 200, 318"""
     m = sm.Machine(py_full_dir, max_ctx=320, max_streams=32)
     prompts = [sm.prompt_ids(5 + s, 64, 50304) for s in range(32)]
@@ -88,7 +89,7 @@ def test_thousand_token_prompt_two_streams(sm, full_dir, py_full_dir, model):
 
 
 def test_batched_attention_kernel_golden(sm, golden):
-    """config 3 (T = 128, 512, 1024) through the batched attention kernel, two streams at once: every row of both
+    """the attention workload (T = 128, 512, 1024) through the batched attention kernel, two streams at once: every row of both
     against base2.py's own attention"""
     t = sm.Tables(sm.tables())
     ctx, rows = 1024, 2

@@ -92,7 +92,7 @@ def full_machine(sm, full_dir):
     m.close()
 
 
-def test_config1_words_and_records(full_machine, golden):
+def test_batch1_8_token_prompt_words_and_records(full_machine, golden):
     """GPT-2 124M, batch 1, 8-token prompt, 16 greedy words: the words and every intermediate of the first and
     the last position against base2.py"""
     m = full_machine
@@ -107,7 +107,7 @@ def test_config1_words_and_records(full_machine, golden):
 
 
 @pytest.mark.parametrize("stream", [0, 1])
-def test_config4_prompts(full_machine, golden, stream):
+def test_gpt2_32_token_prompts(full_machine, golden, stream):
     """32-token prompts of the batched config, one stream at a time"""
     c = golden_case(golden, f"c4_stream{stream}_p32_w4")
     assert full_machine.stream(c["prompt"], len(c["words"])) == c["words"]

@@ -74,7 +74,7 @@ def test_small_model_words_and_records(sm, py_small_dir, py_small_oracle, pgolde
     m.close()
 
 
-def test_config5_golden_streams(sm, py_full_dir, pgolden):
+def test_pythia_32_streams_golden_words(sm, py_full_dir, pgolden):
     """the two golden streams of the 160m-shaped workload: 64-word prompts, 4 words each"""
     m = sm.Machine(py_full_dir, max_ctx=128)
     for c in [c for c in pgolden["cases"] if c["model"] == "pythia_160m"]:
@@ -153,7 +153,7 @@ def test_small_model_batched_record(sm, py_small_dir, py_small_oracle, pgolden, 
     m.close()
 
 
-def test_config5_thirty_two_streams(sm, py_full_dir, py_full_npz, pgolden):
+def test_pythia_32_streams_64_token_prompts(sm, py_full_dir, py_full_npz, pgolden):
     """32 streams of 64-word prompts: the two golden streams, a sample against the oracle, a late stream's cache"""
     from oracle.pythia import PythiaOracle
     cs = [c for c in pgolden["cases"] if c["model"] == "pythia_160m"]

@@ -183,7 +183,7 @@ def _attend_all(sm, dtabs, QKV, ctx):
 
 
 def test_attention_golden(sm, dtabs, golden):
-    """config 3 shapes (T = 128, 512, 1024): every row against base2.py's own attention (golden vectors)"""
+    """the attention workload's shapes (T = 128, 512, 1024): every row against base2.py's own attention (golden vectors)"""
     for case in golden["attention"]:
         Q = synth_qkv(case["seed"], case["P"], case["std"])
         A = _attend_all(sm, dtabs, Q, 1024)

@@ -52,7 +52,7 @@ def _check_survivors(m, full_oracle, prompt, words):
     return n
 
 
-def test_top_read_config1(top_machine, full_oracle, golden):
+def test_top_read_8_token_prompt(top_machine, full_oracle, golden):
     c = golden_case(golden, "c1_p8_w16")
     got = top_machine.stream(c["prompt"], len(c["words"]))
     assert got == c["words"]

@@ -49,7 +49,7 @@ def test_step_bytes_match_the_published_accounting():
     spec = importlib.util.spec_from_file_location("bench", os.path.join(REPO, "bench.py"))
     bench = importlib.util.module_from_spec(spec)
     spec.loader.exec_module(bench)
-    assert bench.WORKLOAD_FIXED == 248_662_476        # weights + exponents/biases, per token (SURVEY 8(d))
+    assert bench.WORKLOAD_FIXED == 248_662_476        # weights + exponents/biases, per token
     assert bench.KV_WORKLOAD == 73_728                # k and v at 4 B each, 12 layers x 768, per cached position
     # what this layout reads per cached position: 12 layers x (768 int16 keys + 768 int32 values + per head an
     # int32 key water level and an int64 mask of the +32768 dimensions)

@@ -85,7 +85,7 @@ def test_numpy_port_words(small_npz, golden):
     assert Base2Numpy(small_npz).generate(c["prompt"], 4) == c["words"][:4]
 
 
-def test_config1_words_and_records(full_oracle, golden):
+def test_batch1_8_token_prompt_words_and_records(full_oracle, golden):
     c = golden_case(golden, "c1_p8_w16")
     for which in ("first", "last"):
         words, got, want = run_recorded(full_oracle, c, which)
@@ -96,7 +96,7 @@ def test_config1_words_and_records(full_oracle, golden):
 
 
 @pytest.mark.parametrize("stream", [0, 1])
-def test_config4_prompt_words(full_oracle, golden, stream):
+def test_gpt2_32_token_prompt_words(full_oracle, golden, stream):
     c = golden_case(golden, f"c4_stream{stream}_p32_w4")
     assert full_oracle.generate(c["prompt"], len(c["words"])) == c["words"]
 
