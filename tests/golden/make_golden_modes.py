@@ -57,7 +57,8 @@ def main():
     work = tempfile.mkdtemp(prefix="sm_golden_modes_")
     np.savez(os.path.join(work, "base2_pythia-modes.npz"), **npz)
     prompt = sm.prompt_ids(50, 8, 1000)
-    for switches in (["plates=finished"], ["plates=start"], ["order=shuffle"], ["plates=built"]):
+    for switches in (["plates=finished"], ["plates=start"], ["order=shuffle"], ["plates=built"],
+                     ["plates=built", "gauge=float"]):
         if tuple(switches) in have:
             continue
         ns = gf.namespace(os.path.join(REF, "foundation0", "pythia_base2.py"), work,

@@ -212,13 +212,13 @@ def test_plate_and_order_switches(sm, tmp_path, streams):
     for case in g["cases"]:
         d = str(tmp_path / f"{case['name']}_{streams}")
         sm.pythia.pythia_layout(modes_npz(sm, case), d)
-        kw = {}
-        if case["switches"] == ["plates=built"]:      # 17-bit digits, split in two: one stream, position by position
+        kw = {s.split("=")[0]: "float" for s in case["switches"] if s.endswith("=float")}
+        if "plates=built" in case["switches"] or kw:  # split digits, float stages: one stream, position by position
             if streams > 1:
                 with pytest.raises(sm.SmError):
-                    sm.Machine(d, max_ctx=32, max_streams=streams)
+                    sm.Machine(d, max_ctx=32, max_streams=streams, **kw)
                 continue
-            kw = dict(prefill_rows=0)
+            kw["prefill_rows"] = 0
         m = sm.Machine(d, max_ctx=32, max_streams=streams, **kw)
         last = case["records"]["last"]
         m.reset()

@@ -160,7 +160,9 @@ def test_plate_and_order_switches(sm):
     assert sm.array_digest(sm.pythia.convert_pythia(fin, cfg, start=start)) == g["model"]["digest"]
     assert {tuple(c["switches"]) for c in g["cases"]} >= {("plates=start",), ("plates=built",), ("order=shuffle",)}
     for case in g["cases"]:
-        if case["switches"] == ["plates=built"]:
+        if any(s.endswith("=float") for s in case["switches"]):
+            continue                                  # (the oracle runs every stage in integers)
+        if "plates=built" in case["switches"]:
             with pytest.raises(ValueError):
                 PythiaOracle(modes_npz(sm, case))
             continue
