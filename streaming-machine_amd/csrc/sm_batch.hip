@@ -714,21 +714,40 @@ __global__ __launch_bounds__(256, 2) void k_head_rows(GemmArgs a) {     // two b
         const v4 f0 = wfs[lane & 15][0], f1 = wfs[lane & 15][1];
         const i64 ccol = 32768 * (i64)f0[0] + 128 * (i64)f0[1], we = f0[2];
         const i64 bc = (i64)(((u64)(unsigned)f1[1] << 32) | (unsigned)f1[0]);
+        if (EPI == EPI_PILE) {
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+                const int row = 16 * t + 4 * (lane >> 4) + q;
+                if (row >= a.rows) continue;
+                const i64 pile = 65536 * (i64)hh[q] + 256 * ((i64)hl[q] + lh[q]) + ll[q] + rc[row][0] + ccol;
+                if (rec0 && row == 0 && a.rpile) a.rpile[j] = pile;
+                a.Y[(size_t)row * a.ystride + j] = pile;
+            }
+            return;
+        }
+        // the logit y = rsh(v, sh): v = pile (Pythia) or pile x the row's power factor, sh = -(we + F_row)
+        // (Pythia) or 16 - we - F_row.  Where every lane's shift is in 1..62 (the usual case) rsh is the rounding
+        // add and one arithmetic shift; otherwise the wave takes the general rsh (and Pythia's range check,
+        // which only a left shift can fail).  Rows past the last are computed from unwritten facts and left out.
 #pragma unroll
         for (int q = 0; q < 4; q++) {
             const int row = 16 * t + 4 * (lane >> 4) + q;
-            if (row >= a.rows) continue;
             const i64 pile = 65536 * (i64)hh[q] + 256 * ((i64)hl[q] + lh[q]) + ll[q] + rc[row][0] + ccol;
-            const bool rec = rec0 && row == 0;
-            if (rec && a.rpile) a.rpile[j] = pile;
-            if (EPI == EPI_PILE) {
-                a.Y[(size_t)row * a.ystride + j] = pile;
+            const i64 v = EPI == EPI_PHEAD ? pile : wmul(pile, rc[row][2]);
+            const i64 s = EPI == EPI_PHEAD ? -(we + rc[row][1]) : 16 - we - rc[row][1];
+            i64 y;
+            if (__ballot(row < a.rows && (u64)(s - 1) >= 62) == 0) {
+                const int s32 = (int)s;
+                y = wadd(v, (i64)1 << (s32 - 1)) >> s32;
             } else {
-                if (EPI == EPI_PHEAD && a.err && pyshift_fails(pile, -(we + rc[row][1]))) atomicOr(a.err, SM_ERR_RANGE);
-                const i64 y = EPI == EPI_PHEAD ? rsh(pile, -(we + rc[row][1]))            // Pythia: plain, no bias
-                                               : wadd(rsh(wmul(pile, rc[row][2]), 16 - we - rc[row][1]), bc);
-                if (rec && a.rlogits) a.rlogits[j] = y;
-                if (bi[q] < 0 || y > bv[q]) { bv[q] = y; bi[q] = j; }      // j grows with the tile
+                if (EPI == EPI_PHEAD && row < a.rows && a.err && pyshift_fails(v, s)) atomicOr(a.err, SM_ERR_RANGE);
+                y = rsh(v, s);
+            }
+            if (EPI == EPI_HEAD) y = wadd(y, bc);                            // Pythia's head has no bias
+            if (row < a.rows && (bi[q] < 0 || y > bv[q])) { bv[q] = y; bi[q] = j; }    // j grows with the tile
+            if (q == 0 && rec0 && t == 0 && lane < 16) {                   // row 0: q = 0 of lanes 0-15
+                if (a.rpile) a.rpile[j] = pile;
+                if (a.rlogits) a.rlogits[j] = y;
             }
         }
     };
@@ -1011,17 +1030,18 @@ __global__ __launch_bounds__(192) void k_py_rows(PyRowArgs a) {
     }
 }
 
-// The race over each stream's per-tile bests (base2.py:34-40, 114): one block per stream; the last block to
-// finish advances the shared position.  At a prompt position whose word is known only the position moves.
+// The race over each stream's per-tile bests (base2.py:34-40, 114): one block per stream; block 0 writes the next
+// position into the other position slot (read by the next step only, so no block waits for the others).  At a
+// prompt position whose word is known only the position moves.
 struct RaceArgs {
     const i64* part_v; const int* part_i; int nblk;
     int* seq; int seq_stride; int* words; int words_stride;
-    int* pos; const int* plen; int* nwords; unsigned* counter;
+    const int* pos; const int* plen; int* nwords;
+    int* pos_next;          // the other position slot: the next step reads it, no block of this launch does
 };
 __global__ __launch_bounds__(256) void k_race_rows(RaceArgs a) {
     __shared__ i64 bvs[4];
     __shared__ int bis[4];
-    __shared__ int last;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, r = blockIdx.x;
     const int p = *a.pos;
     const bool skip = p < *a.plen - 1;
@@ -1049,15 +1069,9 @@ __global__ __launch_bounds__(256) void k_race_rows(RaceArgs a) {
             if (n >= 0) a.words[(size_t)r * a.words_stride + n] = bi;
         }
     }
-    if (tid == 0) {
-        __threadfence();
-        last = atomicAdd(a.counter, 1u) == gridDim.x - 1;
-    }
-    __syncthreads();
-    if (last && tid == 0) {
+    if (r == 0 && tid == 0) {
         *a.nwords = p + 1 - *a.plen + 1;
-        *a.pos = p + 1;
-        *a.counter = 0u;
+        *a.pos_next = p + 1;
     }
 }
 

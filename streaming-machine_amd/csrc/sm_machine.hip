@@ -310,7 +310,11 @@ static void tables_free(sm_tables& T) {
 
 // ---------------------------------------------------------------------------------------------------------
 // the machine
-enum { CTL_POS = 0, CTL_PLEN = 1, CTL_NWORDS = 2, CTL_ERR = 3, CTL_RECPOS = 4, CTL_COUNTER = 5, CTL_N = 8 };
+// CTL_POS / CTL_POS1: the position's two slots.  Batch 1 keeps it in CTL_POS (its race is one block).  Batched
+// streams alternate: a step reads the slot of the machine's parity and its race writes the next position into the
+// other, which no kernel of that step reads, so the race needs no grid-wide handoff (a last-arriving block behind
+// a fence costs more than the kernel boundary it would save)
+enum { CTL_POS = 0, CTL_PLEN = 1, CTL_NWORDS = 2, CTL_ERR = 3, CTL_RECPOS = 4, CTL_POS1 = 6, CTL_N = 8 };
 static const int NIN[4] = {768, 768, 768, 3072};
 static const int NOUT[4] = {2304, 768, 3072, 768};
 static const int TCOLS[4] = {2, 2, 2, 1};      // tile widths: qkv, proj, fc, mproj (one wave per tile)
@@ -371,10 +375,13 @@ struct sm_machine {
     i64 *r_x16 = nullptr, *r_exls = nullptr, *r_pile = nullptr, *r_qkv = nullptr, *r_att = nullptr, *r_hid = nullptr,
         *r_resid = nullptr, *r_hx16 = nullptr, *r_hexls = nullptr, *r_hpile = nullptr, *r_logits = nullptr;
     i64 *r_gauge = nullptr, *r_fcpre = nullptr, *r_hgauge = nullptr;   // Pythia: gauges [L][2][768], fc before the edge
-    // captured decode steps: [0] graph_steps whole steps, [1] one whole step, [2] one step's layers, [3] its head
-    hipGraphExec_t gexec[4] = {};
-    hipGraph_t graph[4] = {};
+    // captured decode steps: [0] graph_steps whole steps, [1] one whole step, [2] one step's layers, [3] its head;
+    // one capture for each position slot a replay starts from (gflip: the replay ends on the other slot)
+    hipGraphExec_t gexec[4][2] = {};
+    hipGraph_t graph[4][2] = {};
+    bool gflip[4] = {};
     int gsteps = 16;
+    int par = 0;                   // batched streams: the slot that holds the position of the next step
     // profiling: an event pair around each step's head kernel (the largest single launch)
     // prompt passes: row r of a pass is position pfmap[r] & 0xFFFF of stream pfmap[r] >> 16
     int* pfmap = nullptr;                               // [B][ctx]
@@ -470,10 +477,11 @@ static int parse_norms(const std::string& text, std::vector<std::pair<std::strin
 
 static void machine_free(sm_machine* m) {
     if (!m) return;
-    for (int i = 0; i < 4; i++) {
-        if (m->gexec[i]) (void)hipGraphExecDestroy(m->gexec[i]);
-        if (m->graph[i]) (void)hipGraphDestroy(m->graph[i]);
-    }
+    for (int i = 0; i < 4; i++)
+        for (int j = 0; j < 2; j++) {
+            if (m->gexec[i][j]) (void)hipGraphExecDestroy(m->gexec[i][j]);
+            if (m->graph[i][j]) (void)hipGraphDestroy(m->graph[i][j]);
+        }
     for (int l = 0; l < 12; l++)
         for (int k = 0; k < 4; k++) { free_plate(m->bank[l][k]); free_mfma_plate(m->mbank[l][k]); }
     free_plate(m->head);
@@ -523,12 +531,13 @@ static int launch_step_batched(sm_machine* m, int parts, int nrows = 0,
                                const int* rowmap = nullptr) {
     const Tables tb = m->T.tb();
     int* ctl = m->ctl;
+    int* const posp = ctl + (m->par ? CTL_POS1 : CTL_POS);
     const int B = rowmap ? nrows : m->B;
     const int* recp = rowmap ? nullptr : ctl + CTL_RECPOS;
     auto light_args = [&](int K, const i64* X, i64* rx16, i64* rexls) {
         LightArgs a{};
         a.K = K; a.rows = B; a.X = X; a.wte = m->wte; a.wpe = m->wpe; a.seq = m->seq; a.seq_stride = m->ctx + 1;
-        a.Rw = m->R; a.pos = ctl + CTL_POS; a.plen = ctl + CTL_PLEN;
+        a.Rw = m->R; a.pos = posp; a.plen = ctl + CTL_PLEN;
         a.planes = m->planes; a.rowinfo = m->rowinfo; a.tb = tb;
         a.rec_pos = recp; a.rx16 = rx16; a.rexls = rexls; a.rowmap = rowmap;
         return a;
@@ -545,7 +554,7 @@ static int launch_step_batched(sm_machine* m, int parts, int nrows = 0,
         GemmArgs a{};
         a.K = P.K; a.N = P.N; a.rows = B; a.RT = RT; a.W = P.W; a.csum = P.csum; a.we = P.e; a.bias = P.b;
         a.planes = m->planes; a.rowinfo = m->rowinfo; a.Y = Y; a.ystride = ystride; a.tb = tb;
-        a.pos = ctl + CTL_POS; a.plen = ctl + CTL_PLEN; a.rec_pos = recp; a.rpile = rpile; a.rout = rout;
+        a.pos = posp; a.plen = ctl + CTL_PLEN; a.rec_pos = recp; a.rpile = rpile; a.rout = rout;
         a.part = m->part_acc;
         return a;
     };
@@ -565,7 +574,7 @@ static int launch_step_batched(sm_machine* m, int parts, int nrows = 0,
             AttArgs a{};
             const size_t per = (size_t)m->B * m->ctx;
             a.QKV = m->QKV; a.K16 = m->K16 + l * per * 768; a.KM = m->KM + l * per * 12; a.EK = m->EK + l * per * 12; a.V = m->V + l * per * 768;
-            a.out = m->att; a.pos = ctl + CTL_POS; a.ctx = m->ctx; a.tb = tb; a.err = ctl + CTL_ERR;
+            a.out = m->att; a.pos = posp; a.ctx = m->ctx; a.tb = tb; a.err = ctl + CTL_ERR;
             a.rec_pos = recp; a.ratt = m->r_att + l * 768; a.rowmap = rowmap; a.out_or = m->attor; a.out32 = m->att32;
             if (rowmap) {
                 launch(m->cfg.profile, "kv_rows", k_kv_rows<0>, dim3(12, B), dim3(128), 0, m->st, a);
@@ -608,9 +617,10 @@ static int launch_step_batched(sm_machine* m, int parts, int nrows = 0,
         launch(m->cfg.profile, "head", k_head_rows<RT, EPI_HEAD>, dim3(grid), dim3(256), 0, m->st, a);
         RaceArgs r{};
         r.part_v = m->part_v; r.part_i = m->part_i; r.nblk = parts; r.seq = m->seq; r.seq_stride = m->ctx + 1;
-        r.words = m->words; r.words_stride = m->ctx + 1; r.pos = ctl + CTL_POS; r.plen = ctl + CTL_PLEN;
-        r.nwords = ctl + CTL_NWORDS; r.counter = reinterpret_cast<unsigned*>(ctl + CTL_COUNTER);
+        r.words = m->words; r.words_stride = m->ctx + 1; r.pos = posp; r.plen = ctl + CTL_PLEN;
+        r.pos_next = ctl + (m->par ? CTL_POS : CTL_POS1); r.nwords = ctl + CTL_NWORDS;
         launch(m->cfg.profile, "race", k_race_rows, dim3(B), dim3(256), 0, m->st, r);
+        m->par ^= 1;                                 // the next step reads the slot this race writes
     }
     HIP_TRY(hipGetLastError());
     return SM_OK;
@@ -623,7 +633,6 @@ static int launch_step_batched(sm_machine* m, int parts, int nrows = 0,
 #define HEAD_TC 4
 #define TOP_RECORD 1024       // survivors of the top read's last step kept for sm_read
 
-// the race over the head's per-block bests, one block per stream; it also advances the position
 // batch 1: the race over the head blocks' bests, the word fed back, the next position's entering row (k_race1);
 // k_embed1 writes the entering row of the current position (the first step of a run)
 static Race1Args race1_args(sm_machine* m) {
@@ -812,6 +821,7 @@ static int launch_step_pythia_batched(sm_machine* m, int parts, int nrows = 0,
                                       const int* rowmap = nullptr) {
     const Tables tb = m->T.tb();
     int* ctl = m->ctl;
+    int* const posp = ctl + (m->par ? CTL_POS1 : CTL_POS);
     const int B = rowmap ? nrows : m->B;
     const int* recp = rowmap ? nullptr : ctl + CTL_RECPOS;
     const size_t PL = (size_t)4 * 48 * 3 * 1024, RC = m->RC;
@@ -822,14 +832,14 @@ static int launch_step_pythia_batched(sm_machine* m, int parts, int nrows = 0,
         GemmArgs a{};
         a.K = P.K; a.N = P.N; a.rows = B; a.RT = RT; a.W = P.W; a.csum = P.csum; a.we = P.e; a.bias = P.b;
         a.planes = planes; a.rowinfo = rowinfo; a.tb = tb;
-        a.pos = ctl + CTL_POS; a.plen = ctl + CTL_PLEN; a.rec_pos = recp;
+        a.pos = posp; a.plen = ctl + CTL_PLEN; a.rec_pos = recp;
         a.err = ctl + CTL_ERR;                         // the reference's rshift assert (pythia_base2.py:63)
         return a;
     };
     auto rows_args = [&]() {
         PyRowArgs a{};
         a.err = ctl + CTL_ERR;
-        a.rows = B; a.R = m->R; a.ew = m->ew; a.ee = m->ee; a.seq = m->seq; a.seq_stride = m->ctx + 1; a.pos = ctl + CTL_POS;
+        a.rows = B; a.R = m->R; a.ew = m->ew; a.ee = m->ee; a.seq = m->seq; a.seq_stride = m->ctx + 1; a.pos = posp;
         a.tb = tb; a.rec_pos = recp; a.rowmap = rowmap;
         return a;
     };
@@ -884,7 +894,7 @@ static int launch_step_pythia_batched(sm_machine* m, int parts, int nrows = 0,
             AttArgs a{};
             const size_t per = (size_t)m->B * m->ctx;
             a.QKV = m->QKV; a.K16 = m->K16 + l * per * 768; a.KM = m->KM + l * per * 12; a.EK = m->EK + l * per * 12; a.V = m->V + l * per * 768;
-            a.out = m->att; a.pos = ctl + CTL_POS; a.ctx = m->ctx; a.tb = tb; a.err = ctl + CTL_ERR;
+            a.out = m->att; a.pos = posp; a.ctx = m->ctx; a.tb = tb; a.err = ctl + CTL_ERR;
             a.rec_pos = recp; a.ratt = m->r_att + l * 768; a.rowmap = rowmap;
             a.cosT = m->cosT; a.sinT = m->sinT; a.rot = m->rot; a.half = m->half; a.ehalf = m->ehalf;
             a.out_or = m->attor; a.out32 = m->att32;
@@ -915,9 +925,10 @@ static int launch_step_pythia_batched(sm_machine* m, int parts, int nrows = 0,
         launch(m->cfg.profile, "head", k_head_rows<RT, EPI_PHEAD>, dim3(grid), dim3(256), 0, m->st, a);
         RaceArgs r{};
         r.part_v = m->part_v; r.part_i = m->part_i; r.nblk = grid; r.seq = m->seq; r.seq_stride = m->ctx + 1;
-        r.words = m->words; r.words_stride = m->ctx + 1; r.pos = ctl + CTL_POS; r.plen = ctl + CTL_PLEN;
-        r.nwords = ctl + CTL_NWORDS; r.counter = reinterpret_cast<unsigned*>(ctl + CTL_COUNTER);
+        r.words = m->words; r.words_stride = m->ctx + 1; r.pos = posp; r.plen = ctl + CTL_PLEN;
+        r.pos_next = ctl + (m->par ? CTL_POS : CTL_POS1); r.nwords = ctl + CTL_NWORDS;
         launch(m->cfg.profile, "race", k_race_rows, dim3(B), dim3(256), 0, m->st, r);
+        m->par ^= 1;                                 // the next step reads the slot this race writes
     }
     HIP_TRY(hipGetLastError());
     return SM_OK;
@@ -1062,7 +1073,7 @@ static int run_prefill(sm_machine* m, int npos) {
         if (rc) return rc;
     }
     m->h_pfpos = npos;
-    HIP_TRY(hipMemcpyAsync(m->ctl + CTL_POS, &m->h_pfpos, 4, hipMemcpyHostToDevice, m->st));
+    HIP_TRY(hipMemcpyAsync(m->ctl + (m->par ? CTL_POS1 : CTL_POS), &m->h_pfpos, 4, hipMemcpyHostToDevice, m->st));
     return SM_OK;
 }
 
@@ -1329,6 +1340,7 @@ extern "C" int sm_reset(sm_machine* m) {
     HIP_TRY(hipStreamSynchronize(m->st));
     m->h_plen = m->h_pos = m->h_words = 0;
     m->h_recpos = -1;
+    m->par = 0;
     for (auto& p : m->prompts) p.clear();
     return SM_OK;
 }
@@ -1353,17 +1365,29 @@ extern "C" int sm_record_at(sm_machine* m, int32_t pos) {
 }
 
 // capture n consecutive launch sequences (parts of a step) into graph slot `which`
+// (for the position slot the next step reads; capturing launches nothing, so the slot is put back)
 static int capture(sm_machine* m, int which, int n, int parts) {
-    if (m->gexec[which]) return SM_OK;
+    const int p0 = m->par;
+    if (m->gexec[which][p0]) return SM_OK;
     HIP_TRY(hipStreamBeginCapture(m->st, hipStreamCaptureModeThreadLocal));
     int rc = SM_OK;
     for (int s = 0; s < n && !rc; s++) rc = launch_step(m, parts);
+    m->gflip[which] = m->par != p0;
+    m->par = p0;
     hipGraph_t g = nullptr;
     hipError_t e = hipStreamEndCapture(m->st, &g);
     if (rc) { if (g) (void)hipGraphDestroy(g); return rc; }
     if (e != hipSuccess) return fail(SM_E_HIP, std::string("hipStreamEndCapture: ") + hipGetErrorString(e));
-    m->graph[which] = g;
-    HIP_TRY(hipGraphInstantiate(&m->gexec[which], g, nullptr, nullptr, 0));
+    m->graph[which][p0] = g;
+    HIP_TRY(hipGraphInstantiate(&m->gexec[which][p0], g, nullptr, nullptr, 0));
+    return SM_OK;
+}
+// replay graph slot `which` from the current position slot
+static int replay(sm_machine* m, int which, int n, int parts) {
+    int rc;
+    if ((rc = capture(m, which, n, parts))) return rc;
+    HIP_TRY(hipGraphLaunch(m->gexec[which][m->par], m->st));
+    m->par ^= (int)m->gflip[which];
     return SM_OK;
 }
 
@@ -1372,10 +1396,10 @@ static int capture(sm_machine* m, int which, int n, int parts) {
 static int queue_steps(sm_machine* m, int steps) {
     int rc;
     if (m->cfg.use_graph && !m->cfg.profile) {
-        if (steps >= m->gsteps && (rc = capture(m, 0, m->gsteps, STEP_ALL))) return rc;
-        for (; steps >= m->gsteps; steps -= m->gsteps) HIP_TRY(hipGraphLaunch(m->gexec[0], m->st));
-        if (steps > 0 && (rc = capture(m, 1, 1, STEP_ALL))) return rc;
-        for (; steps > 0; steps--) HIP_TRY(hipGraphLaunch(m->gexec[1], m->st));
+        for (; steps >= m->gsteps; steps -= m->gsteps)
+            if ((rc = replay(m, 0, m->gsteps, STEP_ALL))) return rc;
+        for (; steps > 0; steps--)
+            if ((rc = replay(m, 1, 1, STEP_ALL))) return rc;
     } else {
         for (; steps > 0; steps--)
             if ((rc = launch_step(m))) return rc;
@@ -1428,7 +1452,7 @@ extern "C" int sm_generate(sm_machine* m, int32_t n_words, int32_t* out) {
     HIP_TRY(hipMemcpy(ctl, m->ctl, sizeof(ctl), hipMemcpyDeviceToHost));
     m->h_pos += total;
     m->h_words = target;
-    if (ctl[CTL_POS] != m->h_pos) return fail(SM_E_STATE, "sm_generate: device position disagrees with the host");
+    if (ctl[m->par ? CTL_POS1 : CTL_POS] != m->h_pos) return fail(SM_E_STATE, "sm_generate: device position disagrees with the host");
     if (ctl[CTL_ERR] & SM_ERR_V32) return fail(SM_E_OVERFLOW, "sm_generate: an attention value left 32 bits (the V cache holds int32)");
     if (ctl[CTL_ERR] & SM_ERR_RANGE)
         return fail(SM_E_OVERFLOW, "sm_generate: a value passed a bound the reference asserts (turn input 2^31, attention sum 2^62)");

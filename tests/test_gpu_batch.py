@@ -153,6 +153,26 @@ def test_small_model_streams(sm, small_dir, small_oracle, B):
         assert got[b] == small_oracle.generate(prompts[b], 10, 64), f"stream {b}"
 
 
+@pytest.mark.parametrize("kw", [dict(graph_steps=3), dict(graph_steps=1), dict(use_graph=False), {}],
+                         ids=["graphs_of_3", "graphs_of_1", "plain", "graphs_of_16"])
+def test_small_model_position_slots(sm, small_dir, small_oracle, kw):
+    """the batched step reads the position from one of two slots and its race writes the next position into the
+    other: graphs of an odd number of steps are replayed from either slot, words asked for in several calls
+    continue where the last call stopped (each call checks the device position), and a reset starts over"""
+    B = 3
+    prompts = [sm.prompt_ids(60 + b, 5, 1000) for b in range(B)]
+    want = [small_oracle.generate(p, 19, 64) for p in prompts]
+    m = sm.Machine(small_dir, max_ctx=64, max_streams=B, **kw)
+    for _ in range(2):
+        m.reset()
+        for b, p in enumerate(prompts):
+            m.prefill(p, b)
+        got = np.concatenate([m.generate(n) for n in (4, 1, 7, 3, 4)], axis=1)
+        for b in range(B):
+            assert [int(w) for w in got[b]] == want[b], f"stream {b}"
+    m.close()
+
+
 @pytest.mark.parametrize("use_graph", [True, False])
 def test_small_model_batched_record(sm, small_dir, golden, use_graph):
     """stream 0 of a batch keeps base2.py's record: every intermediate of the last position"""
