@@ -114,6 +114,8 @@ def b1_kernel_bytes(name: str, ctx: float, vocab: int = VOCAB) -> float:
 
 
 def batched_kernel_bytes(name: str, ctx: float, streams: int, vocab: int, head_bias: bool = True) -> float:
+    if "+" in name:                         # a paired launch (the Pythia machine's two halves): both parts' bytes
+        return sum(batched_kernel_bytes(n, ctx, streams, vocab, head_bias) for n in name.split("+"))
     if name in BANKS:
         return bank_bytes(*BANKS[name])
     if name == "mproj.part":

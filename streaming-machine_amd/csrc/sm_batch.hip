@@ -257,8 +257,9 @@ __global__ __launch_bounds__(NT) void k_light(LightArgs a) {
 // SRC > 0 (a plain epilogue or K-slice partials): each wave lights four rows of the tile from contiguous loads
 // into LDS as 16-bit pairs; after one barrier every wave reads its A operands from there and forms the byte
 // planes and plane sums in registers.  NB > 1 spreads that light over more columns.
+// (bx, by): the block's column group / K slice and row tile (k_gemm passes blockIdx; a paired launch its own)
 template <int K, int NB, int KSPLIT, int EPI, int SRC = 0>
-__global__ __launch_bounds__(256) void k_gemm(GemmArgs a) {
+SMD void gemm_block(const GemmArgs& a, int bx, int by) {
     constexpr int KS = K / 64, NS = KS / (4 * KSPLIT);
     constexpr bool ROWS = SRC > 0;
     static_assert(NS * 4 * KSPLIT == KS, "k steps split evenly over slices and waves");
@@ -275,8 +276,8 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs a) {
     __shared__ int sfx[ROWS ? 4 * 16 * 4 : 1];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int ntiles = (a.N + 15) >> 4, ngr = ntiles / NB;   // ntiles a multiple of NB
-    const int nt = blockIdx.x % ngr, kb = blockIdx.x / ngr;   // column group, K slice
-    const int t0 = blockIdx.y;                               // row tile
+    const int nt = bx % ngr, kb = bx / ngr;                  // column group, K slice
+    const int t0 = by;                                       // row tile
     const int s0 = kb * (KS / KSPLIT) + wave * NS;
     const v4* Wb = reinterpret_cast<const v4*>(a.W) + (size_t)nt * NB * KS * 128 + lane;
     const v4* Ab = reinterpret_cast<const v4*>(a.planes) + lane;
@@ -605,6 +606,36 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs a) {
             o |= dpp64<0x118, 0xf, 0xf>(o, 0);
             if ((lane & 15) == 15) a.orw_out[(size_t)row * ntiles + nt * NB + nb] = o;
         }
+    }
+}
+template <int K, int NB, int KSPLIT, int EPI, int SRC = 0>
+__global__ __launch_bounds__(256) void k_gemm(GemmArgs a) { gemm_block<K, NB, KSPLIT, EPI, SRC>(a, blockIdx.x, blockIdx.y); }
+
+// Paired launches of the Pythia machine's two independent halves of a layer (the parallel residual,
+// foundation0/pythia_base2.py:155-157: the attention half and the MLP half read the stream row through their own
+// gauges, so neither waits for the other).  Blocks [0, na) run the first body, the rest the second, each with the
+// block coordinates its own launch would give it (gx: its grid's x extent); a block's branch is uniform, so each
+// body's barriers stay block-wide, and each body keeps its own LDS.
+//   k_gemm_pair: two 768-input banks (fc with its edge, qkv), both lit by the same row kernel
+//   k_attend_mproj: the attention (one block a head and stream, 256 threads) and mproj's K-slice partials
+template <int EA, int EB>
+__global__ __launch_bounds__(256) void k_gemm_pair(GemmArgs a, GemmArgs b, int na, int gxa, int gxb) {
+    const int i = blockIdx.x;
+    if (i < na) {
+        gemm_block<768, 1, 1, EA>(a, i % gxa, i / gxa);
+    } else {
+        const int j = i - na;
+        gemm_block<768, 1, 1, EB>(b, j % gxb, j / gxb);
+    }
+}
+template <int MODEL>
+__global__ __launch_bounds__(256) void k_attend_mproj(AttArgs a, GemmArgs b, int na, int gxb) {
+    const int i = blockIdx.x;
+    if (i < na) {
+        attend_block<MODEL, 0, 1, 0, 256>(a, i % 12, i / 12);
+    } else {
+        const int j = i - na;
+        gemm_block<3072, 3, 4, EPI_PART, 192>(b, j % gxb, j / gxb);
     }
 }
 

@@ -1033,8 +1033,9 @@ template <bool B> struct Flag { static constexpr bool value = B; };
 // FTURN = 1 (one stream, Pythia): turn=float
 // NTB: the block's threads (256 or 512): a pass scores NTB / 4 positions (four lanes a position), the value sum
 // runs NTB / 16 position groups; more threads keep more of the cache's loads in flight where the grid is small
+// (h, b): the block's head and row (k_attend passes blockIdx; a paired launch its own)
 template <int MODEL, int ONE, int REC, int FTURN = 0, int NTB = NTHR>
-__global__ __launch_bounds__(NTB, ONE ? 1 : 3) void k_attend(AttArgs a) {
+SMD void attend_block(const AttArgs& a, int h, int b) {
     static_assert(!FTURN || (MODEL == 1 && ONE), "turn=float is the one-stream Pythia machine's");
     static_assert(NTB == 256 || (NTB == 512 && !ONE), "256 threads, or 512 for the many-stream kernel");
     constexpr int NWB = NTB / 64, ACH = NTB / 4, NGR = NTB / 16;   // waves, positions a pass, value-sum groups
@@ -1050,7 +1051,7 @@ __global__ __launch_bounds__(NTB, ONE ? 1 : 3) void k_attend(AttArgs a) {
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int sl = tid >> 2, qd = tid & 3;                   // scores: position in the pass, lane of the position
     const int d4 = tid & 15, g = tid >> 4;                   // value sum: four dimensions, position group
-    const int h = blockIdx.x, b = blockIdx.y;               // b: the row (a stream, or a prompt position)
+    // b: the row (a stream, or a prompt position)
     // requests first (vector loads complete in order): the new q, k, v (wave w < 3 its part; in the one-stream
     // kernel wave 0 also k and v for the short path), before the position is read; then the cached keys of the
     // first ATT_PRE passes (a position's four lanes read its 128-byte row, lane qd the 32 bytes of dimensions
@@ -1284,6 +1285,10 @@ __global__ __launch_bounds__(NTB, ONE ? 1 : 3) void k_attend(AttArgs a) {
         }
         if (rec) a.ratt[h * 64 + lane] = o;
     }
+}
+template <int MODEL, int ONE, int REC, int FTURN = 0, int NTB = NTHR>
+__global__ __launch_bounds__(NTB, ONE ? 1 : 3) void k_attend(AttArgs a) {
+    attend_block<MODEL, ONE, REC, FTURN, NTB>(a, blockIdx.x, blockIdx.y);
 }
 
 // arrival=float (base2.py:89-92; foundation0/pythia_base2.py:130-133), one stream, one block per head: scores

@@ -811,11 +811,13 @@ static int launch_step_pythia(sm_machine* m, int parts, bool rec) {
     return SM_OK;
 }
 
-// The Pythia machine, batched: eight launches a layer.  Light sets: A (ln1 -> qkv), B (ln2 -> fc), C (edge row
-// -> mproj, 3072 wide), D (attention row -> proj); partials: fc and mproj share region 0 (fc's are finished
-// before mproj writes), proj's follow mproj's.  The last row kernel of a layer adds both halves to the stream
-// (the parallel residual) and lights the next layer's two gauges, or the head's.
-// rowmap != null: a pass of nrows prompt rows, as in launch_step_batched.
+// The Pythia machine, batched.  Light sets: A (ln1 -> qkv) and B (ln2 -> fc), both made by the row kernel; mproj
+// and proj light their own rows (fc's hidden rows, the attention rows) in their banks.  A decode step runs four
+// launches a layer: [fc | qkv] (one launch), [attention | mproj's K-slice partials] (one launch), proj (R + At),
+// the row kernel (R + Mo from the partials, then the next layer's two gauges, or the head's).  The halves of the
+// parallel residual (foundation0/pythia_base2.py:155-157) are independent until the row kernel, so each paired
+// launch holds one kernel of each.
+// rowmap != null: a pass of nrows prompt rows, as in launch_step_batched, one kernel a launch.
 template <int RT>
 static int launch_step_pythia_batched(sm_machine* m, int parts, int nrows = 0,
                                       const int* rowmap = nullptr) {
@@ -862,10 +864,36 @@ static int launch_step_pythia_batched(sm_machine* m, int parts, int nrows = 0,
             gauges(a, 0);
             launch(m->cfg.profile, "rows.embed", k_py_rows<PY_EMBED>, dim3(B), dim3(192), 0, m->st, a);
         }
-        {   // qkv: plain, written
-            GemmArgs a = gemm_args(m->mbank[l][0], pA, rA);
-            a.Y = m->QKV; a.ystride = 2304; a.rpile = rp; a.rout = m->r_qkv + l * 2304;
-            launch(m->cfg.profile, "qkv", k_gemm<768, 1, 1, EPI_PLAIN>, dim3(m->mbank[l][0].ntiles, RT), dim3(256), 0, m->st, a);
+        GemmArgs aq = gemm_args(m->mbank[l][0], pA, rA);              // qkv: plain, written
+        aq.Y = m->QKV; aq.ystride = 2304; aq.rpile = rp; aq.rout = m->r_qkv + l * 2304;
+        GemmArgs af = gemm_args(m->mbank[l][2], pB, rB);              // fc: plain and edged, with OR words
+        af.Y = m->hid; af.ystride = 3072;
+        af.rpile = rp + 2 * 3072; af.rout = m->r_fcpre + l * 3072; af.rout2 = m->r_hid + l * 3072;
+        af.orw_out = m->hidor; af.Y32 = m->hid32;
+        GemmArgs am = gemm_args(m->mbank[l][3], nullptr, nullptr);   // mproj: K-slice partials
+        am.part = P0;
+        am.X = m->hid; am.X32 = m->hid32; am.xstride = 3072; am.orw = m->hidor; am.sfacts = m->sfacts;
+        am.rx16 = m->r_x16 + (l * 4 + 3) * 3072; am.rexls = m->r_exls + (l * 4 + 3) * 2;
+        AttArgs at{};                                                  // attention with turns
+        {
+            const size_t per = (size_t)m->B * m->ctx;
+            at.QKV = m->QKV; at.K16 = m->K16 + l * per * 768; at.KM = m->KM + l * per * 12; at.EK = m->EK + l * per * 12;
+            at.V = m->V + l * per * 768;
+            at.out = m->att; at.pos = posp; at.ctx = m->ctx; at.tb = tb; at.err = ctl + CTL_ERR;
+            at.rec_pos = recp; at.ratt = m->r_att + l * 768; at.rowmap = rowmap;
+            at.cosT = m->cosT; at.sinT = m->sinT; at.rot = m->rot; at.half = m->half; at.ehalf = m->ehalf;
+            at.out_or = m->attor; at.out32 = m->att32;
+        }
+        const int gq = m->mbank[l][0].ntiles, gf = m->mbank[l][2].ntiles, gm = m->mbank[l][3].ntiles / 3 * 4;
+        if (!rowmap) {
+            // a decode step: the two halves of the layer share launches (fc with qkv, then mproj's partials with
+            // the attention), four launches a layer with proj and the row kernel
+            launch(m->cfg.profile, "fc+qkv", k_gemm_pair<EPI_PLAIN_EDGE, EPI_PLAIN>, dim3(gf * RT + gq * RT), dim3(256), 0,
+                   m->st, af, aq, gf * RT, gf, gq);
+            launch(m->cfg.profile, "attend+mproj.part", k_attend_mproj<1>, dim3(12 * B + gm * RT), dim3(256),
+                   (size_t)m->ctx * 12, m->st, at, am, 12 * B, gm);
+        } else {
+            launch(m->cfg.profile, "qkv", k_gemm<768, 1, 1, EPI_PLAIN>, dim3(gq, RT), dim3(256), 0, m->st, aq);
         }
         if (rowmap && l == 11) {   // prompt rows: the last layer only stores its keys and values
             AttArgs a{};
@@ -876,30 +904,11 @@ static int launch_step_pythia_batched(sm_machine* m, int parts, int nrows = 0,
             launch(m->cfg.profile, "kv_rows", k_kv_rows<1>, dim3(12, B), dim3(128), 0, m->st, a);
             break;
         }
-        {   // fc: plain and edged in its bank (the hidden rows), with their OR words
-            GemmArgs a = gemm_args(m->mbank[l][2], pB, rB);
-            a.Y = m->hid; a.ystride = 3072;
-            a.rpile = rp + 2 * 3072; a.rout = m->r_fcpre + l * 3072; a.rout2 = m->r_hid + l * 3072;
-            a.orw_out = m->hidor; a.Y32 = m->hid32;
-            launch(m->cfg.profile, "fc", k_gemm<768, 1, 1, EPI_PLAIN_EDGE>, dim3(m->mbank[l][2].ntiles, RT), dim3(256), 0, m->st, a);
-        }
-        {   // mproj: the hidden rows' light formed in each K slice's blocks; partials over four K slices
-            GemmArgs a = gemm_args(m->mbank[l][3], nullptr, nullptr);
-            a.part = P0;
-            a.X = m->hid; a.X32 = m->hid32; a.xstride = 3072; a.orw = m->hidor; a.sfacts = m->sfacts;
-            a.rx16 = m->r_x16 + (l * 4 + 3) * 3072; a.rexls = m->r_exls + (l * 4 + 3) * 2;
-            launch(m->cfg.profile, "mproj.part", k_gemm<3072, 3, 4, EPI_PART, 192>, dim3(m->mbank[l][3].ntiles / 3 * 4, RT), dim3(256), 0, m->st, a);
-        }
-        {   // attention with turns
-            AttArgs a{};
-            const size_t per = (size_t)m->B * m->ctx;
-            a.QKV = m->QKV; a.K16 = m->K16 + l * per * 768; a.KM = m->KM + l * per * 12; a.EK = m->EK + l * per * 12; a.V = m->V + l * per * 768;
-            a.out = m->att; a.pos = posp; a.ctx = m->ctx; a.tb = tb; a.err = ctl + CTL_ERR;
-            a.rec_pos = recp; a.ratt = m->r_att + l * 768; a.rowmap = rowmap;
-            a.cosT = m->cosT; a.sinT = m->sinT; a.rot = m->rot; a.half = m->half; a.ehalf = m->ehalf;
-            a.out_or = m->attor; a.out32 = m->att32;
-            if (rowmap) launch(m->cfg.profile, "kv_rows", k_kv_rows<1>, dim3(12, B), dim3(128), 0, m->st, a);
-            attend_rows<1>(m, B, a);
+        if (rowmap) {      // a prompt pass: position by position through each kernel
+            launch(m->cfg.profile, "fc", k_gemm<768, 1, 1, EPI_PLAIN_EDGE>, dim3(gf, RT), dim3(256), 0, m->st, af);
+            launch(m->cfg.profile, "mproj.part", k_gemm<3072, 3, 4, EPI_PART, 192>, dim3(gm, RT), dim3(256), 0, m->st, am);
+            launch(m->cfg.profile, "kv_rows", k_kv_rows<1>, dim3(12, B), dim3(128), 0, m->st, at);
+            attend_rows<1>(m, B, at);
         }
         {   // proj: the attention rows' light formed in its bank, added into the stream (R + At)
             GemmArgs g = gemm_args(m->mbank[l][1], nullptr, nullptr);
