@@ -62,6 +62,10 @@ struct GemmArgs {
     i64* orw_out;                 // EPI_GAUGED_EDGE / EPI_PLAIN_EDGE (when non-null): [rows][N / 16] OR of |y| over
                                   // each block's 16 columns, the consumer's water level
     int* err;                     // the Pythia machine: its rshift assert sets SM_ERR_RANGE here
+    // EPI_PLAIN_ADD2: the second plain bank, as K-slice partials [4][3][rows][N] with its K slices' light facts
+    // [4][rows][4], column facts, input width; its pile and the stream after both halves for stream 0's record
+    const int* part2; const int* sfacts2; const int* csum2; const int* we2; const i64* bias2; int kin2;
+    i64* rpile2; i64* rout2b;
 };
 
 // Where a bank's A operand comes from:
@@ -343,6 +347,43 @@ SMD void gemm_block(const GemmArgs& a, int bx, int by) {
             wh[nb][i] = __builtin_nontemporal_load(Wb + (size_t)nb * KS * 128 + (size_t)(s0 + i) * 128);
             wl[nb][i] = __builtin_nontemporal_load(Wb + (size_t)nb * KS * 128 + (size_t)(s0 + i) * 128 + 64);
         }
+    // a plain bank added into the stream: the stream values this lane's epilogue adds to (its row, its column of
+    // each tile) requested behind the tiles, so the epilogue does not wait on a fresh read (each is read and then
+    // written by this lane alone); EPI_PLAIN_ADD2 also the second bank's partials and facts for them (bounded
+    // loads: rows past the last read zeros with no memory request)
+    constexpr bool ADD = EPI == EPI_PLAIN_ADD || EPI == EPI_PLAIN_ADD2;
+    i64 oldv[NB];
+    int p2[EPI == EPI_PLAIN_ADD2 ? NB : 1][12];
+    int sf2[EPI == EPI_PLAIN_ADD2 ? 4 : 1][4];
+    i64 swh2[NB], swl2[NB], we2[NB], bc2[NB];
+    if constexpr (ADD) {
+        const int orow = 16 * t0 + 4 * (lane >> 4) + wave;
+        const unsigned nbytes = (unsigned)(a.rows * a.ystride) * 8u;
+        const __amdgpu_buffer_rsrc_t ry = buf_rsrc(a.Y, nbytes);
+#pragma unroll
+        for (int nb = 0; nb < NB; nb++)
+            oldv[nb] = buf_load8(ry, (unsigned)(orow * a.ystride + (nt * NB + nb) * 16 + (lane & 15)) * 8u);
+        if constexpr (EPI == EPI_PLAIN_ADD2) {
+            const unsigned n = (unsigned)a.N;
+            const __amdgpu_buffer_rsrc_t rp = buf_rsrc(a.part2, (unsigned)(4 * 3 * a.rows) * n * 4u);
+            const __amdgpu_buffer_rsrc_t rs = buf_rsrc(a.sfacts2, (unsigned)(4 * a.rows * 4) * 4u);
+            const __amdgpu_buffer_rsrc_t rc = buf_rsrc(a.csum2, 8u * n), rw = buf_rsrc(a.we2, 4u * n),
+                                         rb = buf_rsrc(a.bias2, 8u * n);
+#pragma unroll
+            for (int nb = 0; nb < NB; nb++) {
+                const unsigned j = (unsigned)((nt * NB + nb) * 16 + (lane & 15));
+#pragma unroll
+                for (int q = 0; q < 12; q++)       // slice q / 3, accumulator q % 3
+                    p2[nb][q] = buf_load1(rp, (unsigned)((q * a.rows + orow) * (int)n + (int)j) * 4u);
+                swh2[nb] = buf_load1(rc, 8u * j); swl2[nb] = buf_load1(rc, 8u * j + 4u);
+                we2[nb] = buf_load1(rw, 4u * j); bc2[nb] = buf_load8(rb, 8u * j);
+            }
+#pragma unroll
+            for (int q = 0; q < 4; q++)
+#pragma unroll
+                for (int c = 0; c < 4; c++) sf2[q][c] = buf_load1(rs, (unsigned)((q * a.rows + orow) * 4 + c) * 4u);
+        }
+    }
     if constexpr (!ROWS) {
 #pragma unroll
         for (int i = 0; i < NS; i++) {
@@ -567,11 +608,29 @@ SMD void gemm_block(const GemmArgs& a, int bx, int by) {
                    128 * (fsxl + swl[nb]) + 16384 * (i64)K + 128 * fn32;
         if (EPI == EPI_PILE) {
             y1[nb] = y2[nb] = pile[nb];
-        } else if (EPI == EPI_PLAIN_ADD) {             // the stream takes the plain bank (base2.py:73-76, 105)
+        } else if (ADD) {                              // the stream takes the plain bank (base2.py:73-76, 105)
             const int j = (nt * NB + nb) * 16 + (lane & 15);
-            const i64 old = j < a.N ? a.Y[(size_t)row * a.ystride + j] : 0;
             if (a.err && j < a.N && pyshift_fails(pile[nb], -(we[nb] + ex + 16))) atomicOr(a.err, SM_ERR_RANGE);
-            y1[nb] = y2[nb] = wadd(old, wadd(rsh(pile[nb], -(we[nb] + ex + 16)), bc[nb]));
+            y1[nb] = y2[nb] = wadd(oldv[nb], wadd(rsh(pile[nb], -(we[nb] + ex + 16)), bc[nb]));
+            if constexpr (EPI == EPI_PLAIN_ADD2) {
+                // the other half: its pile from the four K slices' accumulators and light facts (the sum the
+                // row kernel would form), its plain result added too
+                int hh = 0, mid = 0, ll = 0, sxh = 0, sxl = 0, n32 = 0;
+#pragma unroll
+                for (int q = 0; q < 4; q++) {
+                    hh += p2[nb][3 * q]; mid += p2[nb][3 * q + 1]; ll += p2[nb][3 * q + 2];
+                    sxh += sf2[q][0]; sxl += sf2[q][1]; n32 += sf2[q][2];
+                }
+                const i64 ex2 = sf2[0][3];
+                const i64 pile2 = 65536 * (i64)hh + 256 * (i64)mid + ll + 32768 * ((i64)sxh + swh2[nb]) +
+                                  128 * ((i64)sxl + swl2[nb]) + 16384 * (i64)a.kin2 + 128 * (i64)n32;
+                if (a.err && j < a.N && pyshift_fails(pile2, -(we2[nb] + ex2 + 16))) atomicOr(a.err, SM_ERR_RANGE);
+                y2[nb] = wadd(y1[nb], wadd(rsh(pile2, -(we2[nb] + ex2 + 16)), bc2[nb]));
+                if (rec && j < a.N) {                    // stream 0's record
+                    if (a.rpile2) a.rpile2[j] = pile2;
+                    if (a.rout2b) a.rout2b[j] = y2[nb];
+                }
+            }
         } else if (EPI == EPI_PLAIN || EPI == EPI_PLAIN_EDGE) {   // the Pythia machine's banks (:112-114, 156)
             const int j = (nt * NB + nb) * 16 + (lane & 15);
             if (a.err && j < a.N && pyshift_fails(pile[nb], -(we[nb] + ex + 16))) atomicOr(a.err, SM_ERR_RANGE);
@@ -592,7 +651,7 @@ SMD void gemm_block(const GemmArgs& a, int bx, int by) {
             if ((EPI == EPI_GAUGED_EDGE || EPI == EPI_PLAIN_EDGE) && a.Y32) a.Y32[(size_t)row * a.ystride + j] = (int)y2[nb];
             if (rec) {                                   // stream 0's record
                 if (a.rpile) a.rpile[j] = pile[nb];
-                if (a.rout) a.rout[j] = EPI == EPI_PLAIN_EDGE ? y1[nb] : y2[nb];
+                if (a.rout) a.rout[j] = EPI == EPI_PLAIN_EDGE || EPI == EPI_PLAIN_ADD2 ? y1[nb] : y2[nb];
                 if (EPI == EPI_PLAIN_EDGE && a.rout2) a.rout2[j] = y2[nb];
             }
         }
@@ -866,7 +925,7 @@ struct PyRowArgs {
     const int* rowmap;                            // prompt rows (PY_EMBED): stream << 16 | position per row
     int* err;                                     // its rshift assert (PY_ADD) sets SM_ERR_RANGE here
 };
-enum { PY_EMBED = 0, PY_ADD = 1 };
+enum { PY_EMBED = 0, PY_ADD = 1, PY_GAUGE = 2 };
 
 // plain(pile) of one bank for columns k .. k + 3 of row r, from its KS K-sliced partial accumulators
 // (:112-114), in two halves so that a caller can have every load of its row in flight before the arithmetic
@@ -911,6 +970,7 @@ SMD void plain4_finish(const Plain4<KS>& P, int kin, const int* ri, i64 (&pile)[
 //   PY_EMBED: R = rshift(embed.w[word], -(embed.e[word] + 16)) (:153), then the two gauges' lights
 //   PY_ADD:   R += plain(mproj) (:155-157; proj's half was added by its bank), then the two gauges' lights (or
 //             lnf's alone)
+//   PY_GAUGE: R complete (proj's bank added both halves, EPI_PLAIN_ADD2), the two gauges' lights (or lnf's)
 // Both gauges share to16(R), S1, S2 and LS (:100-110); only the gain, its power and the offset differ.  The two
 // lights go through their water levels and plane sums together: four barriers in all (the OR of R, S1 and S2,
 // the lights' ORs, their plane sums), each with LDS slots of its own, and the gains and offsets are requested
@@ -943,12 +1003,12 @@ __global__ __launch_bounds__(192) void k_py_rows(PyRowArgs a) {
             i64 pM[4], yM[4];
             // mproj's partials (four K slices) and the stream row, all requested before any use
             Plain4<4> PM;
-            plain4_load<4>(PM, a.partM, a.rows, 768, a.csumM, a.weM, a.biasM, r, k);
+            if (MODE == PY_ADD) plain4_load<4>(PM, a.partM, a.rows, 768, a.csumM, a.weM, a.biasM, r, k);
             const v2q_p r01 = *reinterpret_cast<const v2q_p*>(a.R + (size_t)r * 768 + k);
             const v2q_p r23 = *reinterpret_cast<const v2q_p*>(a.R + (size_t)r * 768 + k + 2);
             const i64 rr[4] = {r01[0], r01[1], r23[0], r23[1]};
             int rim[8];
-            slice_facts<4>(a.sfactsM, a.rows, r, rim);
+            if (MODE == PY_ADD) slice_facts<4>(a.sfactsM, a.rows, r, rim);
             // the gains and offsets (they depend on nothing here)
 #pragma unroll
             for (int gi = 0; gi < 2; gi++) {
@@ -959,14 +1019,19 @@ __global__ __launch_bounds__(192) void k_py_rows(PyRowArgs a) {
                 gn[gi][0] = g4[0]; gn[gi][1] = g4[1]; gn[gi][2] = g4[2]; gn[gi][3] = g4[3];
                 gb[gi][0] = b01[0]; gb[gi][1] = b01[1]; gb[gi][2] = b23[0]; gb[gi][3] = b23[1];
             }
-            plain4_finish<4>(PM, a.kinM, rim, pM, yM, a.err);
+            if (MODE == PY_ADD) {
+                plain4_finish<4>(PM, a.kinM, rim, pM, yM, a.err);
 #pragma unroll
-            for (int j = 0; j < 4; j++) {
-                R4[j] = wadd(rr[j], yM[j]);
-                if (rec) {
-                    if (a.rpileM) a.rpileM[k + j] = pM[j];
-                    if (a.routM) a.routM[k + j] = R4[j];
+                for (int j = 0; j < 4; j++) {
+                    R4[j] = wadd(rr[j], yM[j]);
+                    if (rec) {
+                        if (a.rpileM) a.rpileM[k + j] = pM[j];
+                        if (a.routM) a.routM[k + j] = R4[j];
+                    }
                 }
+            } else {                                     // PY_GAUGE: the stream is complete
+#pragma unroll
+                for (int j = 0; j < 4; j++) R4[j] = rr[j];
             }
         }
         if (MODE == PY_EMBED) {
@@ -978,8 +1043,10 @@ __global__ __launch_bounds__(192) void k_py_rows(PyRowArgs a) {
                 for (int j = 0; j < 4; j++) { gn[gi][j] = ng[k + j]; gb[gi][j] = nb[k + j]; }
             }
         }
+        if (MODE != PY_GAUGE) {
 #pragma unroll
-        for (int j = 0; j < 4; j++) a.R[(size_t)r * 768 + k + j] = R4[j];
+            for (int j = 0; j < 4; j++) a.R[(size_t)r * 768 + k + j] = R4[j];
+        }
     }
     // the gauge (:100-110): to16(R), S1, S2, LS, the power factor
     u64 o = 0;
@@ -1137,6 +1204,7 @@ BINST_L(3072, PRO_X16, 1)
 BINST_L(768, PRO_ADD_GAUGE, 4)
 template __global__ void k_py_rows<PY_EMBED>(PyRowArgs);
 template __global__ void k_py_rows<PY_ADD>(PyRowArgs);
+template __global__ void k_py_rows<PY_GAUGE>(PyRowArgs);
 #define BINST_G(K, NB, KSPLIT, EPI) template __global__ void k_gemm<K, NB, KSPLIT, EPI>(GemmArgs);
 #define BINST_GR(RT) BINST_G(768, RT, 1, EPI_GAUGED) BINST_G(768, RT, 1, EPI_GAUGED_EDGE) BINST_G(768, RT, 1, EPI_PLAIN_ADD) \
     BINST_G(768, RT, 1, EPI_PART) BINST_G(768, RT, 1, EPI_PLAIN_EDGE) BINST_G(3072, RT, 4, EPI_PART) \

@@ -24,7 +24,10 @@ enum { EPI_GAUGED = 0,       // power(pile, (we + ex + 16) 65536 - LS) + b      
        EPI_PHEAD = 8,        // rshift(pile, -(we + ex + 16)) with no bias, then the race (:158-160)
        // the collapsing top read (base2_stream_fr.swift:4-15): the high-byte plane's coarse pile and each word's
        // exact bounds, the block's best low and its candidates
-       EPI_TOP1 = 9 };
+       EPI_TOP1 = 9,
+       // batched Pythia: R += rshift(pile, -(we + ex + 16)) + b and the other half's plain bank, finished here from
+       // its K-slice partial accumulators (the parallel residual, foundation0/pythia_base2.py:155-157)
+       EPI_PLAIN_ADD2 = 10 };
 
 // k_gemv's MODE bits (batch 1): the complement machine, two of the stages back in float64 (base2.py:10-11,
 // foundation0/pythia_base2.py:21-27: diagnostics that put one stage back to float; compared at the word level), and

@@ -813,10 +813,10 @@ static int launch_step_pythia(sm_machine* m, int parts, bool rec) {
 
 // The Pythia machine, batched.  Light sets: A (ln1 -> qkv) and B (ln2 -> fc), both made by the row kernel; mproj
 // and proj light their own rows (fc's hidden rows, the attention rows) in their banks.  A decode step runs four
-// launches a layer: [fc | qkv] (one launch), [attention | mproj's K-slice partials] (one launch), proj (R + At),
-// the row kernel (R + Mo from the partials, then the next layer's two gauges, or the head's).  The halves of the
-// parallel residual (foundation0/pythia_base2.py:155-157) are independent until the row kernel, so each paired
-// launch holds one kernel of each.
+// launches a layer: [fc | qkv] (one launch), [attention | mproj's K-slice partials] (one launch), proj (R + At +
+// Mo: its bank also finishes mproj's partials), the row kernel (the next layer's two gauges, or the head's).  The
+// halves of the parallel residual (foundation0/pythia_base2.py:155-157) are independent until proj's epilogue
+// adds them, so each paired launch holds one kernel of each.
 // rowmap != null: a pass of nrows prompt rows, as in launch_step_batched, one kernel a launch.
 template <int RT>
 static int launch_step_pythia_batched(sm_machine* m, int parts, int nrows = 0,
@@ -915,15 +915,28 @@ static int launch_step_pythia_batched(sm_machine* m, int parts, int nrows = 0,
             g.Y = m->R; g.ystride = 768; g.rpile = rp + 3072; g.rout = m->r_resid + (l * 2 + 0) * 768;
             g.X = m->att; g.X32 = m->att32; g.xstride = 768; g.orw = m->attor;
             g.rx16 = m->r_x16 + (l * 4 + 1) * 3072; g.rexls = m->r_exls + (l * 4 + 1) * 2;
-            launch(m->cfg.profile, "proj", k_gemm<768, 1, 1, EPI_PLAIN_ADD, 12>, dim3(m->mbank[l][1].ntiles, RT), dim3(256), 0, m->st, g);
+            const MfmaPlate& Pm = m->mbank[l][3];
+            if (!rowmap) {     // a decode step: proj's bank also finishes mproj's partials and adds both halves
+                g.part2 = P0; g.sfacts2 = m->sfacts; g.csum2 = Pm.csum; g.we2 = Pm.e; g.bias2 = Pm.b; g.kin2 = 3072;
+                g.rpile2 = rp + 3 * 3072; g.rout2b = m->r_resid + (l * 2 + 1) * 768;
+                launch(m->cfg.profile, "proj", k_gemm<768, 1, 1, EPI_PLAIN_ADD2, 12>, dim3(m->mbank[l][1].ntiles, RT),
+                       dim3(256), 0, m->st, g);
+            } else {
+                launch(m->cfg.profile, "proj", k_gemm<768, 1, 1, EPI_PLAIN_ADD, 12>, dim3(m->mbank[l][1].ntiles, RT),
+                       dim3(256), 0, m->st, g);
+            }
         }
-        {   // R += Mo (the parallel residual's other half), then the next gauges' lights
+        {   // (a prompt pass: R += Mo, the parallel residual's other half,) then the next gauges' lights
             PyRowArgs a = rows_args();
             const MfmaPlate& Pm = m->mbank[l][3];
-            a.partM = P0; a.kinM = 3072; a.sfactsM = m->sfacts; a.csumM = Pm.csum; a.weM = Pm.e; a.biasM = Pm.b;
-            a.rpileM = rp + 3 * 3072; a.routM = m->r_resid + (l * 2 + 1) * 768;
             gauges(a, l + 1);
-            launch(m->cfg.profile, "rows.add", k_py_rows<PY_ADD>, dim3(B), dim3(192), 0, m->st, a);
+            if (!rowmap) {
+                launch(m->cfg.profile, "rows.gauge", k_py_rows<PY_GAUGE>, dim3(B), dim3(192), 0, m->st, a);
+            } else {
+                a.partM = P0; a.kinM = 3072; a.sfactsM = m->sfacts; a.csumM = Pm.csum; a.weM = Pm.e; a.biasM = Pm.b;
+                a.rpileM = rp + 3 * 3072; a.routM = m->r_resid + (l * 2 + 1) * 768;
+                launch(m->cfg.profile, "rows.add", k_py_rows<PY_ADD>, dim3(B), dim3(192), 0, m->st, a);
+            }
         }
     }
     if ((parts & STEP_HEAD) && !rowmap) {
