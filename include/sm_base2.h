@@ -66,8 +66,9 @@ typedef struct {
                               4-15, its top=fr): the high-byte plane (w >> 8) for every word, each word's score
                               bounded exactly, the low bytes (w & 255) of the words that can still win; the same
                               words as the full read (GPT-2, max_streams 1, no inv or float stages, head_grid
-                              393..512).  0: the full read.  2: the collapsing read where it applies, else the
-                              full read (the default: measured faster at batch 1) */
+                              393..512).  0: the full read (the default: measured faster at batch 1 since the
+                              head's logits take a two-instruction rounding shift).  2: the collapsing read where
+                              it applies, else the full read */
 } sm_config;
 
 enum { SM_FLOAT_GAUGE = 1, SM_FLOAT_EDGE = 2, SM_FLOAT_ARRIVAL = 4, SM_FLOAT_TURN = 8 };

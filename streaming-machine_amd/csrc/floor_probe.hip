@@ -1,10 +1,11 @@
 // The decode step's launch-structure floor, measured.  Batch 1: the step's 62 dependent launches (12 layers x
-// [qkv, attend, proj, fc, mproj], the head's first stage, the race) with the machine's grids and block sizes,
+// [qkv, attend, proj, fc, mproj], the head, the race) with the machine's grids and block sizes,
 // replayed from a HIP graph of 15 steps, in two forms:
 //   empty  - every kernel returns at once: the cost of 62 dependent launches alone;
 //   bytes  - every kernel reads the row it depends on (the previous kernel's output) and its share of its plate
 //            (the GPT-2 124M shapes: int16 plates of 768x2304, 768x768, 768x3072, 3072x768, and the 768 x 50257
-//            high-byte plane of the top read), the attention reads 16 cached positions of keys (int16) and values
+//            word table, read whole as the machine's default head does), the attention reads 16 cached positions
+//            of keys (int16) and values
 //            (int32) per head, and each kernel writes its outputs -- no arithmetic beyond folding what it read.
 // The machine's step does all of this plus its arithmetic, so its time over "bytes" is what the arithmetic,
 // the block reductions and the table reads cost.
@@ -68,8 +69,8 @@ __global__ __launch_bounds__(256) void k_floor_race(const i64* part, int n, cons
 template <bool EMPTY>
 static int run(double& us) {
     const size_t qkvB = 768 * 2304 * 2, projB = 768 * 768 * 2, fcB = 768 * 3072 * 2, mpB = 3072 * 768 * 2;
-    const int head_tiles = (50257 + 3) / 4;                     // 4-column tiles of the high-byte plane
-    const size_t headB = (size_t)head_tiles * 4 * 768, layerB = qkvB + projB + fcB + mpB;
+    const int head_tiles = (50257 + 3) / 4;                     // 4-column tiles of the int16 word table
+    const size_t headB = (size_t)head_tiles * 4 * 768 * 2, layerB = qkvB + projB + fcB + mpB;
     const int CTX = 64, P = 16, WTE = 1024, STEPS = 15, REPS = 20;
     char* plates = nullptr;
     i64 *R, *QKV, *att, *hid, *part, *wte;
@@ -103,7 +104,7 @@ static int run(double& us) {
             k_floor_phase<768, 2, 4, 2, EMPTY><<<384, 256, 0, st>>>(R, wf, 1536, hid);
             k_floor_phase<3072, 1, 4, 2, EMPTY><<<192, 256, 0, st>>>(hid, wm, 768, R);
         }
-        k_floor_phase<768, 4, 4, 1, EMPTY, true><<<512, 256, 0, st>>>(R, (const v4i*)pl, head_tiles, part);
+        k_floor_phase<768, 4, 4, 2, EMPTY, true><<<512, 256, 0, st>>>(R, (const v4i*)pl, head_tiles, part);
         k_floor_race<EMPTY><<<1, 256, 0, st>>>(part, 512, wte, WTE, R);
     }
     CHK(hipStreamEndCapture(st, &g));

@@ -116,8 +116,8 @@ class Machine:
       the device; the same words (GPT-2, one stream, prefill_rows=0).
       top: "fr" (base2_stream_fr.swift's collapsing top read: the high bytes of every word, then the low bytes of
       the words that can still win; the same words; GPT-2, one stream, no inv or float stages), "plain" (the
-      whole word table read a step), or "auto" (the default: the collapsing read where it applies, measured
-      faster at batch 1).  .top_read says which runs; .top() gives the last step's survivors.
+      default: the whole word table read a step, measured faster at batch 1), or "auto" (the collapsing read
+      where it applies).  .top_read says which runs; .top() gives the last step's survivors.
       .stream(prompt_ids, n_words) -> list of words        (base2.py:123's loop, KV-cached on the device)
       .forward(ids) -> word                                 (base2.py:forward's contract)
       .reset(); .prefill(ids, stream=0); .generate(n_words) -> int32 [n_streams][n_words]
@@ -131,7 +131,7 @@ class Machine:
     def __init__(self, layout_dir: str, max_ctx: int = 1024, max_streams: int = 1, use_graph: bool = True,
                  head_grid: int = 0, graph_steps: int = 16, profile: bool = False, verify_tables: bool = False,
                  prefill_rows: int = 64, gauge: str = "int", edge: str = "int", arrival: str = "int", turn: str = "int",
-                 inv: bool = False, top: str = "auto"):
+                 inv: bool = False, top: str = "plain"):
         fs = 0
         for name, v in (("gauge", gauge), ("edge", edge), ("arrival", arrival), ("turn", turn)):
             if v not in ("int", "float"):

@@ -83,22 +83,22 @@ def test_top_read_records_a_full_step(top_machine, golden):
 
 @pytest.mark.parametrize("kw", [dict(max_streams=2), dict(head_grid=256), dict(inv=True, prefill_rows=0)])
 def test_top_read_limits(sm, full_dir, kw):
-    """asked for where it does not apply, the top read is refused; "auto" (the default) takes the full read there"""
+    """asked for where it does not apply, the top read is refused; "auto" takes the full read there"""
     with pytest.raises(sm.SmError) as e:
         sm.Machine(full_dir, max_ctx=64, top="fr", **kw)
     assert e.value.code == -1
-    m = sm.Machine(full_dir, max_ctx=64, **kw)
+    m = sm.Machine(full_dir, max_ctx=64, top="auto", **kw)
     assert not m.top_read
     m.close()
 
 
-def test_top_read_is_the_default_at_batch_1(sm, full_dir, py_small_dir):
+def test_full_read_is_the_default_auto_takes_the_top_read(sm, full_dir, py_small_dir):
     m = sm.Machine(full_dir, max_ctx=64)
+    assert not m.top_read
+    m.close()
+    m = sm.Machine(full_dir, max_ctx=64, top="auto")
     assert m.top_read
     m.close()
-    m = sm.Machine(full_dir, max_ctx=64, top="plain")
-    assert not m.top_read
-    m.close()
-    m = sm.Machine(py_small_dir, max_ctx=64)          # the Pythia machine has no top read
+    m = sm.Machine(py_small_dir, max_ctx=64, top="auto")   # the Pythia machine has no top read
     assert not m.top_read
     m.close()
