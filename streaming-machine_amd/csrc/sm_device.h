@@ -73,27 +73,29 @@ SMD void log2_parts(i64 v, int& t, i64& m) {
     t = bitlen_py(v) - 1;
     m = t >= 16 ? (sar(v, t - 16) & 0xFFFF) : (shl(v, 16 - t) & 0xFFFF);
 }
-// The same reads at a wave-uniform index, as scalar loads (constant address space): they are counted apart from
-// the vector loads, so they never wait behind plate tiles still in flight.
+// The same reads at a wave-uniform index, two ways.
+//   VEC = false: scalar loads (constant address space), counted apart from the vector loads, so they never wait
+//   behind tiles still in flight; but they share their wait counter with LDS reads, so the next LDS read waits
+//   for them too.
+//   VEC = true: vector (buffer) loads of one address: in order behind the vector loads issued before them, and
+//   waited for only where their value is used, so LDS reads in between (a GEMV phase's product reading its light)
+//   do not wait for them.
+// Measured at batch 1: the GEMV phases' gauge 1.4 % faster a step as vector loads; the one-wave attention's
+// divisor slower (its value sum is short, so the vector loads' latency shows at the end): it stays scalar.
 typedef const __attribute__((address_space(4))) int* cint_p;
-SMD i64 utab_log2(const Tables& tb, int m) {
-    m = __builtin_amdgcn_readfirstlane(m);
-    return ((cint_p)tb.LOG2)[m];
+template <bool VEC>
+SMD i64 utab(const int* t, unsigned entries, int i) {
+    i = __builtin_amdgcn_readfirstlane(i);
+    if constexpr (VEC)
+        return (int)__builtin_amdgcn_raw_buffer_load_b32(__builtin_amdgcn_make_buffer_rsrc(const_cast<int*>(t), 0,
+                                                         (int)(entries * 4u), 0x00020000), i * 4, 0, 0);
+    else
+        return ((cint_p)t)[i];
 }
-SMD i64 utab_gpow(const Tables& tb, int r, int m) {
-    r = __builtin_amdgcn_readfirstlane(r);
-    m = __builtin_amdgcn_readfirstlane(m);
-    return ((cint_p)tb.GPOW)[r * 65536 + m];
-}
-SMD i64 utab_pgpow(const Tables& tb, int r, int m) {
-    r = __builtin_amdgcn_readfirstlane(r);
-    m = __builtin_amdgcn_readfirstlane(m);
-    return ((cint_p)tb.PGPOW)[r * 65536 + m];
-}
-SMD i64 utab_hpow(const Tables& tb, int m) {
-    m = __builtin_amdgcn_readfirstlane(m);
-    return ((cint_p)tb.HPOW)[m];
-}
+template <bool VEC = false> SMD i64 utab_log2(const Tables& tb, int m) { return utab<VEC>(tb.LOG2, 65536u, m); }
+template <bool VEC = false> SMD i64 utab_gpow(const Tables& tb, int r, int m) { return utab<VEC>(tb.GPOW, 131072u, r * 65536 + m); }
+template <bool VEC = false> SMD i64 utab_pgpow(const Tables& tb, int r, int m) { return utab<VEC>(tb.PGPOW, 131072u, r * 65536 + m); }
+SMD i64 utab_hpow(const Tables& tb, int m) { return utab<false>(tb.HPOW, 65536u, m); }
 SMD i64 tab_gpow(const Tables& tb, int r, i64 m) { return tb.GPOW[r * 65536 + m]; }
 SMD i64 tab_hpow(const Tables& tb, i64 m) { return tb.HPOW[m]; }
 
@@ -142,17 +144,19 @@ SMD i64 pgauge_ls_pow(i64 s1, i64 s2, i64 ex, const Tables& tb, i64& e2) {
     i64 V = wadd(wsub(wmul(768, s2), wmul(s1, s1)), eps_term(tb.eps40, ex));
     int t; i64 m;
     log2_parts(V, t, m);
-    const i64 lg = utab_log2(tb, (int)m);
-    e2 = utab_pgpow(tb, t & 1, (int)m);
+    const i64 lg = utab_log2<true>(tb, (int)m);
+    e2 = utab_pgpow<true>(tb, t & 1, (int)m);
     return wadd((i64)t * 65536, lg) >> 1;
 }
 // the same, also giving EXP2[(-LS) & 0xFFFF] (the power factor every gauged column uses) from one derived read
+// (VEC: the table reads as vector loads, see utab)
+template <bool VEC = false>
 SMD i64 gauge_ls_pow(i64 s1, i64 s2, i64 ex, const Tables& tb, i64& e2) {
     i64 V = wadd(wsub(wmul(768, s2), wmul(s1, s1)), eps_term(tb.eps40, ex));
     int t; i64 m;
     log2_parts(V, t, m);
-    const i64 lg = utab_log2(tb, (int)m);           // V is the same in every lane: scalar reads
-    e2 = utab_gpow(tb, t & 1, (int)m);
+    const i64 lg = utab_log2<VEC>(tb, (int)m);      // V is the same in every lane: one address
+    e2 = utab_gpow<VEC>(tb, t & 1, (int)m);
     const i64 l2 = wadd((i64)t * 65536, lg);
     return wadd(wsub(l2 >> 1, tb.log768), wmul(ex, 65536));
 }

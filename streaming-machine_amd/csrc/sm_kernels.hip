@@ -253,7 +253,7 @@ SMD void prologue(const GemvArgs& a, int tid, const i64 (&vin)[NIN / NT], short*
         i64 S1 = 0, S2h = 0, S2l = 0;
 #pragma unroll
         for (int w = 0; w < NW; w++) { S1 += red[32 + 3 * w]; S2h += red[33 + 3 * w]; S2l += red[34 + 3 * w]; }
-        ls = gauge_ls_pow(S1, (S2h << 16) + S2l, ex, a.tb, e2);
+        ls = gauge_ls_pow<true>(S1, (S2h << 16) + S2l, ex, a.tb, e2);
         sx_o = S1;
         if constexpr (TOP) {
             i64 nn = 0;
