@@ -687,11 +687,11 @@ __global__ __launch_bounds__(256) void k_gemm_pair(GemmArgs a, GemmArgs b, int n
         gemm_block<768, 1, 1, EB>(b, j % gxb, j / gxb);
     }
 }
-template <int MODEL>
+template <int MODEL, int ARRF>
 __global__ __launch_bounds__(256) void k_attend_mproj(AttArgs a, GemmArgs b, int na, int gxb) {
     const int i = blockIdx.x;
     if (i < na) {
-        attend_block<MODEL, 0, 1, 0, 256>(a, i % 12, i / 12);
+        attend_block<MODEL, 0, 1, 0, 256, ARRF>(a, i % 12, i / 12);
     } else {
         const int j = i - na;
         gemm_block<3072, 3, 4, EPI_PART, 192>(b, j % gxb, j / gxb);

@@ -54,6 +54,16 @@ SMD i64 tab_exp2(const Tables& tb, i64 f) { return tb.EXP2[f]; }
 SMD i64 tab_phi(const Tables& tb, i64 i) { return tb.PHI[i]; }
 // the arrival: 0 past the table (base2.py:97)
 SMD int tab_arr(const Tables& tb, i64 d) { return d < tb.alen ? tb.ARR[d] : 0; }
+// ARRF: the entry computed from its defining formula (arr_entry) instead of read, for a machine whose tables the
+// create-time device check found equal to their formulas entry for entry, the arrival's alen + 1 included (so the
+// two agree at every d >= 0): no dependent table read in the attention's chain.  Measured (same box, alternating):
+// the batch-1 step 0.2480-0.2482 against 0.2484-0.2488 ms, Pythia at 32 streams 0.4025-0.4031 against
+// 0.4055-0.4059; GPT-2 at 64 streams slower (0.5648-0.5662 against 0.5617-0.5622), so its attention reads the table
+template <int ARRF>
+SMD int arrival(const Tables& tb, i64 d) {
+    if constexpr (ARRF) return d < tb.alen ? arr_entry(d) : 0;
+    else return tab_arr(tb, d);
+}
 
 // base2.py:18-22  rshift(X, s): X * 2^-s rounded half up (s <= 0: a left shift)
 SMD i64 rsh(i64 x, i64 s) {

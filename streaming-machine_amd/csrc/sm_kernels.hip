@@ -898,7 +898,7 @@ SMD i64 turn1(i64 x, i64 partner, bool lower, i64 ci, i64 si, double cf, double 
     }
 }
 
-template <int MODEL, int FTURN = 0>
+template <int MODEL, int FTURN = 0, int ARRF = 0>
 SMD i64 attend_short(const AttArgs& a, int p, int h, int b, int* q_s, int* w_s, i64 qv, i64 kv, const i64 vv, bool store) {
     const int lane = threadIdx.x & 63;
     const size_t hb = ((size_t)b * 12 + h) * a.ctx;         // this (stream, head)'s cache rows
@@ -977,7 +977,7 @@ SMD i64 attend_short(const AttArgs& a, int p, int h, int b, int* q_s, int* w_s, 
                                    : rsh(d, -(eq + ek + 7));
     const i64 mx = wave_reduce64(sc, OpMax());
     // arrivals (base2.py:96-97) and their sum
-    const int w = lane <= p ? tab_arr(a.tb, wsub(mx, sc)) : 0;
+    const int w = lane <= p ? arrival<ARRF>(a.tb, wsub(mx, sc)) : 0;
     const i64 z = wave_reduce64((i64)w, OpAdd());
     // the divisor's table entries (base2.py:99) are requested now, so their latency passes during the value sum
     int t; i64 m;
@@ -1034,7 +1034,8 @@ template <bool B> struct Flag { static constexpr bool value = B; };
 // NTB: the block's threads (256 or 512): a pass scores NTB / 4 positions (four lanes a position), the value sum
 // runs NTB / 16 position groups; more threads keep more of the cache's loads in flight where the grid is small
 // (h, b): the block's head and row (k_attend passes blockIdx; a paired launch its own)
-template <int MODEL, int ONE, int REC, int FTURN = 0, int NTB = NTHR>
+// ARRF: arrivals from their formula (see arrival)
+template <int MODEL, int ONE, int REC, int FTURN = 0, int NTB = NTHR, int ARRF = 0>
 SMD void attend_block(const AttArgs& a, int h, int b) {
     static_assert(!FTURN || (MODEL == 1 && ONE), "turn=float is the one-stream Pythia machine's");
     static_assert(NTB == 256 || (NTB == 512 && !ONE), "256 threads, or 512 for the many-stream kernel");
@@ -1068,7 +1069,7 @@ SMD void attend_block(const AttArgs& a, int h, int b) {
     if constexpr (ONE) {
         if (p < 64) {                                        // one stream, short context: one wave, no barriers
             if (wave == 0) {
-                const i64 o = attend_short<MODEL, FTURN>(a, p, h, b, q16s, vs, xnew, xk1, xv1, true);
+                const i64 o = attend_short<MODEL, FTURN, ARRF>(a, p, h, b, q16s, vs, xnew, xk1, xv1, true);
                 a.out[(size_t)b * 768 + h * 64 + lane] = o;
                 if (a.out_or) {
                     const i64 w = wave_or64(iabs64(o));
@@ -1213,7 +1214,7 @@ SMD void attend_block(const AttArgs& a, int h, int b) {
     // arrivals (base2.py:96-97), one position per thread, into LDS; their sum
     i64 z = 0;
     for (int s = tid; s <= p; s += NTB) {
-        const int w = tab_arr(a.tb, wsub(mx, sc[s]));
+        const int w = arrival<ARRF>(a.tb, wsub(mx, sc[s]));
         arr[s] = w;
         z += w;
     }
@@ -1286,9 +1287,9 @@ SMD void attend_block(const AttArgs& a, int h, int b) {
         if (rec) a.ratt[h * 64 + lane] = o;
     }
 }
-template <int MODEL, int ONE, int REC, int FTURN = 0, int NTB = NTHR>
+template <int MODEL, int ONE, int REC, int FTURN = 0, int NTB = NTHR, int ARRF = 0>
 __global__ __launch_bounds__(NTB, ONE ? 1 : 3) void k_attend(AttArgs a) {
-    attend_block<MODEL, ONE, REC, FTURN, NTB>(a, blockIdx.x, blockIdx.y);
+    attend_block<MODEL, ONE, REC, FTURN, NTB, ARRF>(a, blockIdx.x, blockIdx.y);
 }
 
 // arrival=float (base2.py:89-92; foundation0/pythia_base2.py:130-133), one stream, one block per head: scores

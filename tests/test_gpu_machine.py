@@ -73,6 +73,33 @@ def test_verify_tables_refuses_a_changed_table(sm, small_dir, small_npz, tmp_pat
     m.close()
 
 
+@pytest.mark.parametrize("streams", [1, 3])
+def test_changed_arrival_table_is_read_as_given(sm, small_npz, tmp_path, streams):
+    """with the reference's tables the machine computes each arrival from its formula (the create-time check found
+    them equal entry for entry); a layout whose arrival table differs is read as given: the attention rows of the
+    recorded position, at batch 1 and with three streams, equal the oracle's run with the same table"""
+    import oracle
+    npz = dict(small_npz)
+    arr = npz["arrival"].copy()
+    arr[1:2048] = arr[1:2048] * 3 // 4                  # every arrival within 2 units of the maximum
+    npz["arrival"] = arr
+    d = sm.layout(npz, str(tmp_path))
+    prompt = sm.prompt_ids(2, 8, 1000)
+    want, base = oracle.new_record(1000), oracle.new_record(1000)
+    oracle.Oracle(npz).forward(prompt, rec=want)          # the last position's intermediates
+    oracle.Oracle(small_npz).forward(prompt, rec=base)
+    assert not np.array_equal(want["att"], base["att"])  # the change reaches the attention
+    m = sm.Machine(d, max_ctx=64, max_streams=streams)
+    assert not m.tables_verified
+    m.reset()
+    m.record_at(len(prompt) - 1)
+    for b in range(streams):
+        m.prefill(prompt, b)
+    m.generate(1)
+    np.testing.assert_array_equal(m.read("att"), want["att"])
+    m.close()
+
+
 def test_small_model_record(sm, small_dir, golden):
     c = golden_case(golden, "small_p8_w8")
     m = sm.Machine(small_dir, max_ctx=64)
