@@ -496,7 +496,12 @@ __global__ __launch_bounds__(64 * WPB) void k_gemv(GemvArgs a) {
                 }
             }
         };
-        while (tile < a.ntiles) {
+        if (a.ntiles <= nw) {
+            // (uniform) one tile a wave, as every layer phase's grid gives: no second fetch.  The loop below would
+            // request the last tile again (clamped) for the wave's empty second slot, and the launch would wait for
+            // those loads at its end: 0.2422-0.2426 against 0.2498-0.2500 ms a step without them
+            if (tile < a.ntiles) finish(wA, wA2, eA, bA, sA, tile);
+        } else while (tile < a.ntiles) {
             const int t1 = tile + nw;
             fetch(wB, wB2, eB, bB, sB, t1);
             finish(wA, wA2, eA, bA, sA, tile);
