@@ -349,8 +349,9 @@ SMD void gemm_block(const GemmArgs& a, int bx, int by) {
         }
     // a plain bank added into the stream: the stream values this lane's epilogue adds to (its row, its column of
     // each tile) requested behind the tiles, so the epilogue does not wait on a fresh read (each is read and then
-    // written by this lane alone); EPI_PLAIN_ADD2 also the second bank's partials and facts for them (bounded
-    // loads: rows past the last read zeros with no memory request)
+    // written by this lane alone); EPI_PLAIN_ADD2 also the second bank's partials and facts for them.  Bounded
+    // loads: a row past the last (a padding row of the tile, whose lanes store nothing) reads zeros past a
+    // buffer's end, or another row's values inside it, never outside the buffer
     constexpr bool ADD = EPI == EPI_PLAIN_ADD || EPI == EPI_PLAIN_ADD2;
     i64 oldv[NB];
     int p2[EPI == EPI_PLAIN_ADD2 ? NB : 1][12];
