@@ -140,7 +140,7 @@ def kernel_table(times: dict, steps: int, bytes_of) -> dict:
     return out
 
 
-COUNTER_FILES = {"b1": "b1_kernel_traffic.txt", "b64": "b64_kernel_counters.txt"}
+COUNTER_FILES = {"b1": "b1_kernel_traffic.txt", "b64": "b64_kernel_counters.txt", "pythia": "b32_pythia_counters.txt"}
 
 
 def read_counter(where: str, key: str, kernel: str):
