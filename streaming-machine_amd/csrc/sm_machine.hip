@@ -347,6 +347,7 @@ struct sm_machine {
     // turn and arrival
     int mode = 0;
     bool fturn = false, farr = false;
+    int* hpin = nullptr;      // pinned host words: the control block and every stream's words of a generate call
     double *cosF = nullptr, *sinF = nullptr;            // turn=float: [npos][rot / 2]
     double* KF = nullptr;                               // arrival=float: [L][12 heads][ctx][64] keys as float64
     // the collapsing top read (batch 1): planes, the first stage's candidates, the light, the step's survivors
@@ -496,6 +497,7 @@ static void machine_free(sm_machine* m) {
     for (void* p : ps) hfree(p);
     for (int l = 0; l < 12; l++)
         for (int j = 0; j < 2; j++) { hfree(m->ng[l][j]); hfree(m->nb[l][j]); }
+    if (m->hpin) (void)hipHostFree(m->hpin);
     if (m->st) (void)hipStreamDestroy(m->st);
     delete m;
 }
@@ -1341,6 +1343,10 @@ extern "C" int sm_create(const char* layout_dir, const sm_config* cfg, sm_machin
         return bail(rc);
     if (hipMemset(m->planes, 0, (size_t)4 * 48 * 3 * 1024 * nsets) != hipSuccess || hipMemset(m->rowinfo, 0, RC * 32 * nsets) != hipSuccess)
         return bail(fail(SM_E_HIP, "hipMemset planes"));
+    if (hipHostMalloc(&m->hpin, (CTL_N + B * (ctx + 1)) * sizeof(int), hipHostMallocDefault) != hipSuccess) {
+        m->hpin = nullptr;
+        return bail(fail(SM_E_OOM, "hipHostMalloc: the generate readback buffer"));
+    }
     m->prompts.assign(B, {});
     m->gsteps = c.graph_steps > 0 ? c.graph_steps : 16;
     if (m->gsteps > 256) return bail(fail(SM_E_ARG, "sm_create: graph_steps at most 256"));
@@ -1481,18 +1487,20 @@ extern "C" int sm_generate(sm_machine* m, int32_t n_words, int32_t* out) {
     if (first && m->B == 1) launch_embed1(m);
     const int total = (m->h_plen - 1 + target) - m->h_pos;
     if ((rc = run_steps(m, total, m->h_pos))) return rc;
+    // the control block and every stream's new words into pinned host memory, queued behind the steps, then one
+    // wait (in place of a synchronous copy per stream)
+    HIP_TRY(hipMemcpyAsync(m->hpin, m->ctl, CTL_N * sizeof(int), hipMemcpyDeviceToHost, m->st));
+    HIP_TRY(hipMemcpy2DAsync(m->hpin + CTL_N, (size_t)n_words * 4, m->words + (target - n_words), (size_t)(m->ctx + 1) * 4,
+                             (size_t)n_words * 4, (size_t)m->B, hipMemcpyDeviceToHost, m->st));
     HIP_TRY(hipStreamSynchronize(m->st));
-    int ctl[CTL_N];
-    HIP_TRY(hipMemcpy(ctl, m->ctl, sizeof(ctl), hipMemcpyDeviceToHost));
+    const int* ctl = m->hpin;
     m->h_pos += total;
     m->h_words = target;
     if (ctl[m->par ? CTL_POS1 : CTL_POS] != m->h_pos) return fail(SM_E_STATE, "sm_generate: device position disagrees with the host");
     if (ctl[CTL_ERR] & SM_ERR_V32) return fail(SM_E_OVERFLOW, "sm_generate: an attention value left 32 bits (the V cache holds int32)");
     if (ctl[CTL_ERR] & SM_ERR_RANGE)
         return fail(SM_E_OVERFLOW, "sm_generate: a value passed a bound the reference asserts (turn input 2^31, attention sum 2^62)");
-    for (int b = 0; b < m->B; b++)
-        HIP_TRY(hipMemcpy(out + (size_t)b * n_words, m->words + (size_t)b * (m->ctx + 1) + (target - n_words), (size_t)n_words * 4,
-                          hipMemcpyDeviceToHost));
+    std::memcpy(out, m->hpin + CTL_N, (size_t)m->B * n_words * sizeof(int));
     return SM_OK;
 }
 
