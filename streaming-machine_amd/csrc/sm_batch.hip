@@ -28,8 +28,8 @@ struct LightArgs {
                                   // turns ex, S1, S2 into LS and the power factor, off the light's critical path)
     Tables tb;
     const int* rec_pos; i64* rx16; i64* rexls;    // stream 0's record
-    // PRO_ADD_GAUGE: the producing bank's epilogue first, from its partial accumulators
-    const int* part; int kin;                     // [K slices][3][rows][K] int32 (HH, MID, LL); the bank's K
+    // PRO_ADD_GAUGE: the producing bank's epilogue first, from its partial piles
+    const i64* part; int kin;                     // [K slices][rows][K] partial piles 65536 HH + 256 MID + LL; the bank's K
     const int* csum; const int* we; const i64* bias;   // the producing plate's column facts
     i64* Y;                                       // [rows][K]: the epilogue's row (R: read and written)
     i64* rpile_in; i64* rout_in;                  // stream 0's record of the producing bank
@@ -52,7 +52,7 @@ struct GemmArgs {
     i64* part_v; int* part_i; int nblk;   // EPI_HEAD: per (row, block) best
     const int* rec_pos; i64* rpile; i64* rout; i64* rlogits;
     i64* rout2;                   // EPI_PLAIN_EDGE: the record after the edge (rout: before it)
-    int* part;                    // EPI_PART: [ksplit][3][rows][N] int32
+    i64* part;                    // EPI_PART: [ksplit][rows][N] the slice's partial pile 65536 HH + 256 MID + LL
     // the light formed in the bank (SRC > 0): the producing phase's rows, its OR words, stream 0's light record
     const i64* X; int xstride;    // [rows][xstride] int64
     const int* X32;               // the same rows' low 32 bits (read where a row's OR words show it fits 31 bits)
@@ -62,9 +62,9 @@ struct GemmArgs {
     i64* orw_out;                 // EPI_GAUGED_EDGE / EPI_PLAIN_EDGE (when non-null): [rows][N / 16] OR of |y| over
                                   // each block's 16 columns, the consumer's water level
     int* err;                     // the Pythia machine: its rshift assert sets SM_ERR_RANGE here
-    // EPI_PLAIN_ADD2: the second plain bank, as K-slice partials [4][3][rows][N] with its K slices' light facts
+    // EPI_PLAIN_ADD2: the second plain bank, as K-slice partial piles [4][rows][N] with its K slices' light facts
     // [4][rows][4], column facts, input width; its pile and the stream after both halves for stream 0's record
-    const int* part2; const int* sfacts2; const int* csum2; const int* we2; const i64* bias2; int kin2;
+    const i64* part2; const int* sfacts2; const int* csum2; const int* we2; const i64* bias2; int kin2;
     i64* rpile2; i64* rout2b;
 };
 
@@ -115,8 +115,8 @@ __global__ __launch_bounds__(NT) void k_light(LightArgs a) {
         i_sxh = ri[4]; i_sxl = ri[5]; i_n32 = ri[6];
     }
     constexpr int GA = PRO == PRO_ADD_GAUGE ? GPT : 1, KA = PRO == PRO_ADD_GAUGE ? KSP : 1;
-    v4l c0[GA], c1[GA], wv[GA], hq[GA][KA], mq[GA][KA], lq[GA][KA];
-    v2q b01[GA], b23[GA], y01[GA], y23[GA];
+    v4l c0[GA], c1[GA], wv[GA];
+    v2q b01[GA], b23[GA], y01[GA], y23[GA], pa[GA][KA], pb[GA][KA];
 #pragma unroll
     for (int m = 0; m < GPT; m++) {
         const int g = tid + NT * m;
@@ -132,10 +132,9 @@ __global__ __launch_bounds__(NT) void k_light(LightArgs a) {
             y23[m] = *reinterpret_cast<const v2q*>(a.Y + (size_t)r * K + k + 2);
 #pragma unroll
             for (int ks = 0; ks < KSP; ks++) {
-                const int* q = a.part + ((size_t)ks * 3 * a.rows + r) * K + k;
-                hq[m][ks] = *reinterpret_cast<const v4l*>(q);
-                mq[m][ks] = *reinterpret_cast<const v4l*>(q + (size_t)a.rows * K);
-                lq[m][ks] = *reinterpret_cast<const v4l*>(q + (size_t)2 * a.rows * K);
+                const i64* q = a.part + ((size_t)ks * a.rows + r) * K + k;
+                pa[m][ks] = *reinterpret_cast<const v2q*>(q);
+                pb[m][ks] = *reinterpret_cast<const v2q*>(q + 2);
             }
         } else if constexpr (PRO != PRO_EMBED) {
 #pragma unroll
@@ -151,15 +150,16 @@ __global__ __launch_bounds__(NT) void k_light(LightArgs a) {
         if (g >= NG) continue;
         const int k = 4 * g;
         if constexpr (PRO == PRO_ADD_GAUGE) {
-            v4l h = hq[m][0], mi = mq[m][0], lo = lq[m][0];
+            v2q s01 = pa[m][0], s23 = pb[m][0];
 #pragma unroll
-            for (int ks = 1; ks < KSP; ks++) { h += hq[m][ks]; mi += mq[m][ks]; lo += lq[m][ks]; }
+            for (int ks = 1; ks < KSP; ks++) { s01 += pa[m][ks]; s23 += pb[m][ks]; }
+            const i64 ps[4] = {s01[0], s01[1], s23[0], s23[1]};
             const int sw[8] = {c0[m][0], c0[m][1], c0[m][2], c0[m][3], c1[m][0], c1[m][1], c1[m][2], c1[m][3]};
             const i64 bcs[4] = {b01[m][0], b01[m][1], b23[m][0], b23[m][1]}, ys[4] = {y01[m][0], y01[m][1], y23[m][0], y23[m][1]};
 #pragma unroll
             for (int j = 0; j < 4; j++) {
-                const i64 pile = 65536 * (i64)h[j] + 256 * (i64)mi[j] + lo[j] + 32768 * (i_sxh + sw[2 * j]) +
-                                 128 * (i_sxl + sw[2 * j + 1]) + 16384 * (i64)a.kin + 128 * i_n32;
+                const i64 pile = ps[j] + 32768 * (i_sxh + sw[2 * j]) + 128 * (i_sxl + sw[2 * j + 1]) +
+                                 16384 * (i64)a.kin + 128 * i_n32;
                 const i64 y = wadd(ys[j], wadd(rsh(pile, -((i64)wv[m][j] + i_ex + 16)), bcs[j]));
                 a.Y[(size_t)r * K + k + j] = y;
                 v[m][j] = y;
@@ -256,7 +256,7 @@ __global__ __launch_bounds__(NT) void k_light(LightArgs a) {
 // three int32 accumulators: HH, MID = HL + LH (+ CH), LL (+ CL).  Wave w then finishes rows 4 (l / 16) + w of the
 // row tile for column l % 16 of every tile.  Everything the block reads that depends on nothing else (weights,
 // lights, row and column facts) is issued before the first MFMA.
-//   EPI_PART: the accumulators go to part[kslice][3][rows][N]; the consumer's prologue finishes them.
+//   EPI_PART: the slice's partial pile 65536 HH + 256 MID + LL goes to part[kslice][rows][N]; the consumer finishes it.
 //   EPI_GAUGED / EPI_GAUGED_EDGE / EPI_PLAIN_ADD / EPI_PILE: one K slice; the epilogue runs here.
 // SRC > 0 (a plain epilogue or K-slice partials): each wave lights four rows of the tile from contiguous loads
 // into LDS as 16-bit pairs; after one barrier every wave reads its A operands from there and forms the byte
@@ -354,7 +354,7 @@ SMD void gemm_block(const GemmArgs& a, int bx, int by) {
     // buffer's end, or another row's values inside it, never outside the buffer
     constexpr bool ADD = EPI == EPI_PLAIN_ADD || EPI == EPI_PLAIN_ADD2;
     i64 oldv[NB];
-    int p2[EPI == EPI_PLAIN_ADD2 ? NB : 1][12];
+    i64 p2[EPI == EPI_PLAIN_ADD2 ? NB : 1][4];
     int sf2[EPI == EPI_PLAIN_ADD2 ? 4 : 1][4];
     i64 swh2[NB], swl2[NB], we2[NB], bc2[NB];
     if constexpr (ADD) {
@@ -366,7 +366,7 @@ SMD void gemm_block(const GemmArgs& a, int bx, int by) {
             oldv[nb] = buf_load8(ry, (unsigned)(orow * a.ystride + (nt * NB + nb) * 16 + (lane & 15)) * 8u);
         if constexpr (EPI == EPI_PLAIN_ADD2) {
             const unsigned n = (unsigned)a.N;
-            const __amdgpu_buffer_rsrc_t rp = buf_rsrc(a.part2, (unsigned)(4 * 3 * a.rows) * n * 4u);
+            const __amdgpu_buffer_rsrc_t rp = buf_rsrc(a.part2, (unsigned)(4 * a.rows) * n * 8u);
             const __amdgpu_buffer_rsrc_t rs = buf_rsrc(a.sfacts2, (unsigned)(4 * a.rows * 4) * 4u);
             const __amdgpu_buffer_rsrc_t rc = buf_rsrc(a.csum2, 8u * n), rw = buf_rsrc(a.we2, 4u * n),
                                          rb = buf_rsrc(a.bias2, 8u * n);
@@ -374,8 +374,8 @@ SMD void gemm_block(const GemmArgs& a, int bx, int by) {
             for (int nb = 0; nb < NB; nb++) {
                 const unsigned j = (unsigned)((nt * NB + nb) * 16 + (lane & 15));
 #pragma unroll
-                for (int q = 0; q < 12; q++)       // slice q / 3, accumulator q % 3
-                    p2[nb][q] = buf_load1(rp, (unsigned)((q * a.rows + orow) * (int)n + (int)j) * 4u);
+                for (int q = 0; q < 4; q++)        // slice q's partial pile
+                    p2[nb][q] = buf_load8(rp, (unsigned)((q * a.rows + orow) * (int)n + (int)j) * 8u);
                 swh2[nb] = buf_load1(rc, 8u * j); swl2[nb] = buf_load1(rc, 8u * j + 4u);
                 we2[nb] = buf_load1(rw, 4u * j); bc2[nb] = buf_load8(rb, 8u * j);
             }
@@ -600,8 +600,7 @@ SMD void gemm_block(const GemmArgs& a, int bx, int by) {
         if (EPI == EPI_PART) {
             const int j = (nt * NB + nb) * 16 + (lane & 15);
             if (j < a.N) {
-#pragma unroll
-                for (int k3 = 0; k3 < 3; k3++) a.part[(((size_t)kb * 3 + k3) * a.rows + row) * a.N + j] = fin[k3];
+                a.part[((size_t)kb * a.rows + row) * a.N + j] = 65536 * (i64)fin[0] + 256 * (i64)fin[1] + fin[2];
             }
             continue;
         }
@@ -616,15 +615,16 @@ SMD void gemm_block(const GemmArgs& a, int bx, int by) {
             if constexpr (EPI == EPI_PLAIN_ADD2) {
                 // the other half: its pile from the four K slices' accumulators and light facts (the sum the
                 // row kernel would form), its plain result added too
-                int hh = 0, mid = 0, ll = 0, sxh = 0, sxl = 0, n32 = 0;
+                i64 ps2 = 0;
+                int sxh = 0, sxl = 0, n32 = 0;
 #pragma unroll
                 for (int q = 0; q < 4; q++) {
-                    hh += p2[nb][3 * q]; mid += p2[nb][3 * q + 1]; ll += p2[nb][3 * q + 2];
+                    ps2 += p2[nb][q];
                     sxh += sf2[q][0]; sxl += sf2[q][1]; n32 += sf2[q][2];
                 }
                 const i64 ex2 = sf2[0][3];
-                const i64 pile2 = 65536 * (i64)hh + 256 * (i64)mid + ll + 32768 * ((i64)sxh + swh2[nb]) +
-                                  128 * ((i64)sxl + swl2[nb]) + 16384 * (i64)a.kin2 + 128 * (i64)n32;
+                const i64 pile2 = ps2 + 32768 * ((i64)sxh + swh2[nb]) + 128 * ((i64)sxl + swl2[nb]) +
+                                  16384 * (i64)a.kin2 + 128 * (i64)n32;
                 if (a.err && j < a.N && pyshift_fails(pile2, -(we2[nb] + ex2 + 16))) atomicOr(a.err, SM_ERR_RANGE);
                 y2[nb] = wadd(y1[nb], wadd(rsh(pile2, -(we2[nb] + ex2 + 16)), bc2[nb]));
                 if (rec && j < a.N) {                    // stream 0's record
@@ -927,8 +927,8 @@ struct PyRowArgs {
     const int* ng2; const i64* nb2; int nge2;     // gauge 2 (ln2); null: one gauge only
     signed char* planes1; int* rowinfo1;          // light of gauge 1
     signed char* planes2; int* rowinfo2;          // light of gauge 2
-    // PY_ADD: mproj's four K slices of partial accumulators, finished here (proj's half is already in R)
-    const int* partM; int kinM; const int* csumM; const int* weM; const i64* biasM;
+    // PY_ADD: mproj's four K slices of partial piles, finished here (proj's half is already in R)
+    const i64* partM; int kinM; const int* csumM; const int* weM; const i64* biasM;
     const int* sfactsM;                           // mproj's K slices' light facts [4][rows][4]
     Tables tb;
     const int* rec_pos;
@@ -939,14 +939,14 @@ struct PyRowArgs {
 };
 enum { PY_EMBED = 0, PY_ADD = 1, PY_GAUGE = 2 };
 
-// plain(pile) of one bank for columns k .. k + 3 of row r, from its KS K-sliced partial accumulators
+// plain(pile) of one bank for columns k .. k + 3 of row r, from its KS K-sliced partial piles
 // (:112-114), in two halves so that a caller can have every load of its row in flight before the arithmetic
 typedef int v4l_p __attribute__((ext_vector_type(4)));
 typedef i64 v2q_p __attribute__((ext_vector_type(2)));
 template <int KS>
-struct Plain4 { v4l_p h[KS], mi[KS], lo[KS], c0, c1, wv; v2q_p b01, b23; };
+struct Plain4 { v2q_p pa[KS], pb[KS]; v4l_p c0, c1, wv; v2q_p b01, b23; };
 template <int KS>
-SMD void plain4_load(Plain4<KS>& P, const int* part, int rows, int N, const int* csum, const int* we, const i64* bias,
+SMD void plain4_load(Plain4<KS>& P, const i64* part, int rows, int N, const int* csum, const int* we, const i64* bias,
                      int r, int k) {
     P.c0 = *reinterpret_cast<const v4l_p*>(csum + 2 * k);
     P.c1 = *reinterpret_cast<const v4l_p*>(csum + 2 * k + 4);
@@ -955,24 +955,23 @@ SMD void plain4_load(Plain4<KS>& P, const int* part, int rows, int N, const int*
     P.b23 = *reinterpret_cast<const v2q_p*>(bias + k + 2);
 #pragma unroll
     for (int q = 0; q < KS; q++) {
-        const int* src = part + ((size_t)q * 3 * rows + r) * N + k;
-        P.h[q] = *reinterpret_cast<const v4l_p*>(src);
-        P.mi[q] = *reinterpret_cast<const v4l_p*>(src + (size_t)rows * N);
-        P.lo[q] = *reinterpret_cast<const v4l_p*>(src + (size_t)2 * rows * N);
+        const i64* src = part + ((size_t)q * rows + r) * N + k;
+        P.pa[q] = *reinterpret_cast<const v2q_p*>(src);
+        P.pb[q] = *reinterpret_cast<const v2q_p*>(src + 2);
     }
 }
 template <int KS>
 SMD void plain4_finish(const Plain4<KS>& P, int kin, const int* ri, i64 (&pile)[4], i64 (&y)[4], int* err) {
-    v4l_p h = P.h[0], mi = P.mi[0], lo = P.lo[0];
+    v2q_p s01 = P.pa[0], s23 = P.pb[0];
 #pragma unroll
-    for (int q = 1; q < KS; q++) { h += P.h[q]; mi += P.mi[q]; lo += P.lo[q]; }
+    for (int q = 1; q < KS; q++) { s01 += P.pa[q]; s23 += P.pb[q]; }
+    const i64 ps[4] = {s01[0], s01[1], s23[0], s23[1]};
     const int sw[8] = {P.c0[0], P.c0[1], P.c0[2], P.c0[3], P.c1[0], P.c1[1], P.c1[2], P.c1[3]};
     const i64 bc[4] = {P.b01[0], P.b01[1], P.b23[0], P.b23[1]};
     const i64 ex = ri[0], sxh = ri[4], sxl = ri[5], n32 = ri[6];
 #pragma unroll
     for (int j = 0; j < 4; j++) {
-        pile[j] = 65536 * (i64)h[j] + 256 * (i64)mi[j] + lo[j] + 32768 * (sxh + sw[2 * j]) + 128 * (sxl + sw[2 * j + 1]) +
-                  16384 * (i64)kin + 128 * n32;
+        pile[j] = ps[j] + 32768 * (sxh + sw[2 * j]) + 128 * (sxl + sw[2 * j + 1]) + 16384 * (i64)kin + 128 * n32;
         if (err && pyshift_fails(pile[j], -((i64)P.wv[j] + ex + 16))) atomicOr(err, SM_ERR_RANGE);
         y[j] = wadd(rsh(pile[j], -((i64)P.wv[j] + ex + 16)), bc[j]);
     }
@@ -1193,16 +1192,11 @@ __global__ __launch_bounds__(256) void k_part_piles(GemmArgs a) {
     int ri[8];
     slice_facts<KSP>(a.sfacts, a.rows, r, ri);
     for (int j = blockIdx.x * 256 + threadIdx.x; j < a.N; j += gridDim.x * 256) {
-        int hh = 0, mid = 0, ll = 0;                 // (as the machine's finisher sums them: each below 2^28)
+        i64 ps = 0;                                  // (as the machine's finishers sum them)
 #pragma unroll
-        for (int q = 0; q < KSP; q++) {
-            const int* src = a.part + ((size_t)q * 3 * a.rows + r) * a.N + j;
-            hh += src[0];
-            mid += src[(size_t)a.rows * a.N];
-            ll += src[(size_t)2 * a.rows * a.N];
-        }
-        a.Y[(size_t)r * a.ystride + j] = 65536 * (i64)hh + 256 * (i64)mid + ll + 32768 * ((i64)ri[4] + a.csum[2 * j]) +
-                                         128 * ((i64)ri[5] + a.csum[2 * j + 1]) + 16384 * (i64)a.K + 128 * (i64)ri[6];
+        for (int q = 0; q < KSP; q++) ps += a.part[((size_t)q * a.rows + r) * a.N + j];
+        a.Y[(size_t)r * a.ystride + j] = ps + 32768 * ((i64)ri[4] + a.csum[2 * j]) + 128 * ((i64)ri[5] + a.csum[2 * j + 1]) +
+                                         16384 * (i64)a.K + 128 * (i64)ri[6];
     }
 }
 

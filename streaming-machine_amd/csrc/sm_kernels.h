@@ -7,7 +7,7 @@ enum { PRO_GAUGE = 0,   // gauge_log of the stream row R (768): x16, ex, LS (bas
        PRO_TO16 = 1,    // to16 of an activation row (768 or 3072): x16, ex (base2.py:24-27)
        PRO_EMBED = 2,   // batched lights: the word enters, R = wte[word] + wpe[pos] (base2.py:103), then PRO_GAUGE
        PRO_X16 = 3,     // the light is given (int64 x16 values, ex = -16): the raw product test
-       // batched streams: the producing bank's epilogue from its partial accumulators, then the light
+       // batched streams: the producing bank's epilogue from its partial piles, then the light
        PRO_ADD_GAUGE = 4,   // R += rshift(pile, -(we + ex + 16)) + b, then PRO_GAUGE of R   (base2.py:105-106, 55-60)
        // the Pythia machine (foundation0/pythia_base2.py)
        PRO_PGAUGE = 6 };    // its gauge with the norm's gain and offset, then to16 of that row     (:100-110, 113)
@@ -26,7 +26,7 @@ enum { EPI_GAUGED = 0,       // power(pile, (we + ex + 16) 65536 - LS) + b      
        // exact bounds, the block's best low and its candidates
        EPI_TOP1 = 9,
        // batched Pythia: R += rshift(pile, -(we + ex + 16)) + b and the other half's plain bank, finished here from
-       // its K-slice partial accumulators (the parallel residual, foundation0/pythia_base2.py:155-157)
+       // its K-slice partial piles (the parallel residual, foundation0/pythia_base2.py:155-157)
        EPI_PLAIN_ADD2 = 10 };
 
 // k_gemv's MODE bits (batch 1): the complement machine, two of the stages back in float64 (base2.py:10-11,

@@ -330,7 +330,7 @@ struct sm_machine {
     MfmaPlate mbank[12][4];        // batched streams: MFMA byte planes
     MfmaPlate mhead;
     signed char* planes = nullptr;  // [4][48][3][1024] light planes of the current phase
-    int* part_acc = nullptr;        // batched: a bank's partial accumulators [K slices][3][streams][N] int32
+    i64* part_acc = nullptr;        // batched: a bank's partial piles [K slices][streams][N]
     int* rowinfo = nullptr;        // [B][8]
     i64* wte = nullptr;
     i64* wpe = nullptr;
@@ -545,7 +545,7 @@ static int launch_step_batched(sm_machine* m, int parts, int nrows = 0,
         a.rec_pos = recp; a.rx16 = rx16; a.rexls = rexls; a.rowmap = rowmap;
         return a;
     };
-    // mproj's epilogue (from its four K slices of partial accumulators) added into the stream, then the next light
+    // mproj's epilogue (from its four K slices of partial piles) added into the stream, then the next light
     auto finish_light = [&](const MfmaPlate& P, i64* rpile, i64* rout, i64* rx16, i64* rexls, int ls_row) {
         LightArgs a = light_args(P.N, nullptr, rx16, rexls);
         a.ls_row = ls_row;
@@ -601,7 +601,7 @@ static int launch_step_batched(sm_machine* m, int parts, int nrows = 0,
             a.orw_out = m->hidor; a.Y32 = m->hid32;
             launch(m->cfg.profile, "fc", k_gemm<768, 1, 1, EPI_GAUGED_EDGE>, dim3(m->mbank[l][2].ntiles, RT), dim3(256), 0, m->st, a);
         }
-        {   // mproj: the hidden rows' light formed in each K slice's blocks; partial accumulators and slice facts
+        {   // mproj: the hidden rows' light formed in each K slice's blocks; partial piles and slice facts
             GemmArgs a = gemm_args(m->mbank[l][3], nullptr, 0, nullptr, nullptr);
             a.X = m->hid; a.X32 = m->hid32; a.xstride = 3072; a.orw = m->hidor; a.rx16 = rx + 3 * 3072; a.rexls = re + 6;
             a.sfacts = m->sfacts;
@@ -839,7 +839,7 @@ static int launch_step_pythia_batched(sm_machine* m, int parts, int nrows = 0,
     const size_t PL = (size_t)4 * 48 * 3 * 1024, RC = m->RC;
     signed char* pA = m->planes; signed char* pB = m->planes + PL;      // the two gauges' lights (qkv, fc)
     int* rA = m->rowinfo; int* rB = m->rowinfo + RC * 8;
-    int* P0 = m->part_acc;                          // mproj's partial accumulators
+    i64* P0 = m->part_acc;                          // mproj's partial piles
     auto gemm_args = [&](const MfmaPlate& P, signed char* planes, int* rowinfo) {
         GemmArgs a{};
         a.K = P.K; a.N = P.N; a.rows = B; a.RT = RT; a.W = P.W; a.csum = P.csum; a.we = P.e; a.bias = P.b;
@@ -1333,7 +1333,7 @@ extern "C" int sm_create(const char* layout_dir, const sm_config* cfg, sm_machin
         (rc = dalloc(&m->ctl, (size_t)CTL_N)) || (rc = dalloc(&m->part_v, nparts)) ||
         (rc = dalloc(&m->part_i, nparts)) || (rc = dalloc(&m->r_x16, (size_t)12 * 4 * 3072)) ||
         (rc = dalloc(&m->planes, (size_t)4 * 48 * 3 * 1024 * nsets)) || (rc = dalloc(&m->rowinfo, RC * 8 * nsets)) ||
-        (rc = dalloc(&m->part_acc, mfma ? (size_t)4 * 3 * RC * 3072 : (size_t)1)) ||
+        (rc = dalloc(&m->part_acc, mfma ? (size_t)4 * RC * 3072 : (size_t)1)) ||
         (rc = dalloc(&m->r_exls, (size_t)12 * 4 * 2)) || (rc = dalloc(&m->r_pile, (size_t)12 * 4 * 3072)) ||
         (rc = dalloc(&m->r_qkv, (size_t)12 * 2304)) || (rc = dalloc(&m->r_att, (size_t)12 * 768)) ||
         (rc = dalloc(&m->r_hid, (size_t)12 * 3072)) || (rc = dalloc(&m->r_resid, (size_t)12 * 2 * 768)) ||
@@ -1759,7 +1759,7 @@ struct sm_plate {
     bool mfma = false;
     signed char* planes = nullptr;
     int* rowinfo = nullptr;
-    int* part = nullptr;       // nin 3072: the K slices' accumulators and light facts (sm_plate_product_rows_from)
+    i64* part = nullptr;       // nin 3072: the K slices' partial piles and light facts (sm_plate_product_rows_from)
     int* sfacts = nullptr;
     int* x32 = nullptr;        // sm_plate_product_rows_from: the caller rows' low 32 bits [64][nin]
 };
@@ -1784,7 +1784,7 @@ extern "C" int sm_plate_create(const int16_t* w, const int32_t* e, const int64_t
         const size_t pb = (size_t)4 * (nin / 64) * 3 * 1024;
         if ((rc = upload_mfma_plate(p->M, w, e, (const i64*)b, nin, nout)) || (rc = dalloc(&p->planes, pb)) ||
             (rc = dalloc(&p->rowinfo, (size_t)64 * 8)) || (rc = dalloc(&p->x32, (size_t)64 * nin)) ||
-            (nin == 3072 && ((rc = dalloc(&p->part, (size_t)4 * 3 * 64 * (size_t)p->M.ntiles * 16)) ||
+            (nin == 3072 && ((rc = dalloc(&p->part, (size_t)4 * 64 * (size_t)p->M.ntiles * 16)) ||
                              (rc = dalloc(&p->sfacts, (size_t)4 * 64 * 4))))) {
             plate_free(p);
             return rc;
