@@ -128,11 +128,15 @@ def batched_kernel_bytes(name: str, ctx: float, streams: int, vocab: int, head_b
 
 
 def kernel_table(times: dict, steps: int, bytes_of) -> dict:
-    """kernel name -> launches a step, mean us, us a step, bytes a launch, GB/s, fraction of HBM peak"""
+    """kernel name -> launches a step, mean us, us a step, bytes a launch, GB/s, fraction of HBM peak (and the
+    device function's name as a kernel trace gives it, when the timings carry it)"""
     out = {}
-    for k, (n, us) in sorted(times.items(), key=lambda kv: -kv[1][0] * kv[1][1]):
+    for k, t in sorted(times.items(), key=lambda kv: -kv[1][0] * kv[1][1]):
+        n, us = t[0], t[1]
         b = bytes_of(k)
         row = {"launches_per_step": round(n / steps, 3), "mean_us": round(us, 3), "us_per_step": round(n * us / steps, 2)}
+        if len(t) > 2 and t[2]:
+            row["symbol"] = t[2]
         if b:
             row.update({"bytes_per_launch": int(b), "gbs": round(b / (us * 1e-6) / 1e9, 1),
                         "frac": round(b / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)})
@@ -143,29 +147,42 @@ def kernel_table(times: dict, steps: int, bytes_of) -> dict:
 COUNTER_FILES = {"b1": "b1_kernel_traffic.txt", "b64": "b64_kernel_counters.txt", "pythia": "b32_pythia_counters.txt"}
 
 
-def read_counter(where: str, key: str, kernel: str):
+def read_counter(where: str, key: str, kernel: str, symbol: str | None):
     """a per-launch figure (traffic_bytes_per_launch, mfma_ops_per_launch, mfma_busy_cycles_per_launch) of `kernel`
-    from the rocprofv3 counter summary in profiles/, when it was collected for that workload"""
+    from the rocprofv3 counter summary in profiles/, only when the summary's trace name for it is `symbol`, the
+    device function this run timed under that name (a summary collected for another build of the kernel gives
+    None)"""
     fname = COUNTER_FILES.get(where)
     path = os.path.join(REPO, "profiles", fname) if fname else ""
-    if not path or not os.path.exists(path):
+    if not symbol or not path or not os.path.exists(path):
         return None
+    value, traced = None, None
     for line in open(path):
         m = re.match(rf"{key}\[(\S+)\]:\s*(\d+)", line)
         if m and m.group(1) == kernel:
-            return int(m.group(2))
-    return None
+            value = int(m.group(2))
+        m = re.match(r"trace_name\[(\S+)\]:\s*(.+?)\s*$", line)
+        if m and m.group(1) == kernel:
+            traced = m.group(2)
+    return value if traced == symbol else None
 
 
 def dominant(table: dict, where: str) -> dict:
-    """the roofline object of the kernel with the largest share of the step"""
+    """the roofline object of the kernel with the largest share of the step.  Its roofline is HBM's (every kernel
+    here streams integers: no GEMM-shaped work reaches the MFMA ridge); `limit` says what its time is spent on when
+    the bytes explain little of it"""
     name = max((k for k in table if "bytes_per_launch" in table[k]), key=lambda k: table[k]["us_per_step"])
     r = table[name]
+    sym = r.get("symbol")
+    limit = ("hbm" if r["frac"] >= 0.5 else
+             "latency: the launch and its chain of dependent loads (row, tables, reductions), not the bytes")
     return {"bound": "hbm", "achieved": r["gbs"], "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": r["frac"],
-            "traffic": read_counter(where, "traffic_bytes_per_launch", name), "kernel": name,
+            "traffic": read_counter(where, "traffic_bytes_per_launch", name, sym), "kernel": name,
+            "symbol": sym, "limit": limit,
             "bytes_per_launch": r["bytes_per_launch"], "mean_launch_us": r["mean_us"],
             "launches_per_step": r["launches_per_step"], "us_per_step": r["us_per_step"],
-            "source": "HIP event pair stamped by each dispatch, profiled pass of the same workload"}
+            "source": "HIP event pair stamped by each dispatch, profiled pass of the same workload; traffic: "
+                      "rocprofv3 FETCH_SIZE + WRITE_SIZE of the same device function (profiles/), else null"}
 
 
 # ---- batch 1 (GPT-2 124M, 8-token prompt, 16 words) ----
@@ -217,7 +234,7 @@ def b1_leg(sm, lay, steps_req: int, warmup: int, prompt, want, cold_steps: int =
         rest = [int(w) for w in mp.generate(WORDS - 1)[0]]
         if rest != want[1:]:
             raise RuntimeError("profiled pass: GPU words differ from base2.py's golden words")
-        times = sm.kernel_times(clear=True)
+        times = sm.kernel_times(clear=True, symbols=True)
     ctx = PROMPT + WORDS / 2.0                     # mean context of the decode steps (9..23)
     table = kernel_table(times, WORDS - 1, lambda k: b1_kernel_bytes(k, ctx))
     survivors = []
@@ -306,7 +323,7 @@ def run_batched(sm, lay, streams, prompts, n_words, checks, what, bytes_of):
     first = mp.generate(1)
     sm.kernel_times(clear=True)
     rest = mp.generate(n_words - 1)
-    times = sm.kernel_times(clear=True)
+    times = sm.kernel_times(clear=True, symbols=True)
     gate_words(np.concatenate([first, rest], axis=1), checks, what + " (profiled pass)")
     mp.close()
     dt, tp = res
@@ -343,8 +360,8 @@ def batched_leg(sm, lay):
         h = {"tops": round(ops / (head["mean_us"] * 1e-6) / 1e12, 1),
              "frac": round(ops / (head["mean_us"] * 1e-6) / INT8_PEAK_OPS, 4),
              "ops": "four byte-plane products of 64 x 768 x vocab, 2 ops a multiply-add"}
-        cops = read_counter("b64", "mfma_ops_per_launch", "head")
-        busy = read_counter("b64", "mfma_busy_cycles_per_launch", "head")
+        cops = read_counter("b64", "mfma_ops_per_launch", "head", head.get("symbol"))
+        busy = read_counter("b64", "mfma_busy_cycles_per_launch", "head", head.get("symbol"))
         if cops and busy:
             h["counters"] = {"ops_per_launch": cops, "tops": round(cops / (head["mean_us"] * 1e-6) / 1e12, 1),
                              "busy_cycles": busy, "mfma_busy_frac": round(busy / (1024 * head["mean_us"] * 2400.0), 4),
@@ -602,8 +619,8 @@ def main():
     if args.only == "floor":
         print(json.dumps(floor), flush=True)
         return
+    import torch      # first: its HIP runtime (the soname the library links) is then the process's one
     sm = load_sm()
-    import torch
     if args.copy_probe:
         src = torch.ones(args.copy_probe << 18, dtype=torch.int32, device="cuda")
         dst = torch.empty_like(src)

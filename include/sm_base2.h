@@ -40,7 +40,7 @@ typedef struct {
     int32_t max_ctx;       /* positions per stream, at most the position table's rows */
     int32_t use_graph;     /* 1: replay captured HIP graphs of decode steps; 0: plain launches */
     int32_t head_grid;     /* blocks of the head's plate read (0: default) */
-    int32_t graph_steps;   /* decode steps per captured graph (0: 16) */
+    int32_t graph_steps;   /* decode steps per captured graph, at most 16 (0: 16) */
     int32_t profile;       /* 1: launch the decode steps kernel by kernel (no graphs), each launch stamped with a HIP
                               event pair by its own dispatch (sm_profile, sm_profile_kernels) */
     int32_t table_mode;    /* the tables are read from memory; every loaded entry is compared with its defining
@@ -133,8 +133,8 @@ int sm_profile(sm_machine* m, int64_t* n_heads, double* head_us, int32_t clear);
 /* Kernel timing, process-wide.  Launches of a machine created with profile = 1 and, after sm_profile_stages(1),
  * of the stage and plate entry points are each stamped with a HIP event pair by their own dispatch (the interval a
  * kernel trace reports).  sm_profile_kernels waits for the device and returns, per kernel name, the launches and
- * their summed duration in microseconds since the last clear: names receives the names, each ended by '\n'
- * (names_bytes at most), launches and total_us at most max entries, *n how many; clear = 1 empties the table.
+ * their summed duration in microseconds since the last clear: names receives "name\tsymbol\n" a kernel (symbol: the
+ * demangled device function with the most of those launches, as a kernel trace names it; names_bytes at most), launches and total_us at most max entries, *n how many; clear = 1 empties the table.
  * Replaces fr2's sbench= and pbench= timings of fused steps and plate reads (base2_stream_fr2.swift:1077-1149). */
 int sm_profile_stages(int32_t on);
 int sm_profile_kernels(char* names, int32_t names_bytes, int64_t* launches, double* total_us, int32_t max, int32_t* n,
@@ -217,7 +217,8 @@ int sm_plate_product_rows_from(const sm_plate* p, const int64_t* X, const int64_
  * device array of the library (590 KB, held by every GPU it runs on until the process ends), not to the plate's own
  * scratch.  No counterpart in the reference: it is for callers that cannot allocate device memory (code under HIP
  * graph capture, tight serving loops, harnesses that forbid hipMalloc).  rows 1..64 (more is refused with
- * SM_E_ARG); the same piles as sm_plate_product_rows.  Every call on one GPU uses that GPU's one array, so calls
+ * SM_E_ARG); the same piles as sm_plate_product_rows.  Its launches are never timed (sm_profile_stages does not
+ * apply: timing would create and record HIP events).  Every call on one GPU uses that GPU's one array, so calls
  * that overlap on one GPU (other streams, other threads) race; the caller serialises them. */
 int sm_plate_product_rows_noalloc(const sm_plate* p, const int64_t* x16, int32_t rows, int64_t* pile, void* stream);
 /* bytes of the device plate (for bandwidth accounting) */

@@ -19,6 +19,10 @@
 #include <cstdio>
 #include <cstring>
 #include <fstream>
+#include <atomic>
+#include <cstdlib>
+#include <cxxabi.h>
+#include <map>
 #include <mutex>
 #include <string>
 #include <vector>
@@ -45,10 +49,13 @@ extern "C" const char* sm_last_error(void) { return g_err.c_str(); }
 // summed microseconds per kernel name.  Launches that are not timed pass null events.
 struct KernelTiming {
     std::mutex mu;
-    bool stages = false;
+    std::atomic<bool> stages{false};   // read by every stage launch without the lock
     std::vector<std::string> names;
     std::vector<long long> n;
     std::vector<double> us;
+    // per name: timed launches by kernel symbol (the demangled device function, as a kernel trace names it)
+    std::vector<std::map<std::string, long long>> syms;
+    std::map<const void*, std::string> symbol_of;
     struct Pend { int id; hipEvent_t s, e; };
     std::vector<Pend> pend;
     std::vector<hipEvent_t> spare;
@@ -61,7 +68,20 @@ static int kt_id(const char* name) {                 // (g_kt.mu held)
     g_kt.names.push_back(name);
     g_kt.n.push_back(0);
     g_kt.us.push_back(0.0);
+    g_kt.syms.emplace_back();
     return (int)g_kt.names.size() - 1;
+}
+static const std::string& kt_symbol(const void* kernel, hipStream_t st) {   // (g_kt.mu held)
+    auto it = g_kt.symbol_of.find(kernel);
+    if (it != g_kt.symbol_of.end()) return it->second;
+    std::string sym = "?";
+    if (const char* raw = hipKernelNameRefByPtr(kernel, st)) {
+        int status = 0;
+        char* dm = abi::__cxa_demangle(raw, nullptr, nullptr, &status);
+        sym = status == 0 && dm ? dm : raw;
+        std::free(dm);
+    }
+    return g_kt.symbol_of.emplace(kernel, sym).first->second;
 }
 static hipEvent_t kt_event() {                       // (g_kt.mu held)
     hipEvent_t e = nullptr;
@@ -82,7 +102,9 @@ static void launch(bool timed, const char* name, F kernel, dim3 grid, dim3 block
         s = kt_event();
         e = kt_event();
         if (s && e) {
-            g_kt.pend.push_back({kt_id(name), s, e});
+            const int id = kt_id(name);
+            g_kt.syms[id][kt_symbol(reinterpret_cast<const void*>(kernel), st)]++;
+            g_kt.pend.push_back({id, s, e});
         } else {
             if (s) g_kt.spare.push_back(s);
             if (e) g_kt.spare.push_back(e);
@@ -1121,6 +1143,9 @@ extern "C" int sm_create(const char* layout_dir, const sm_config* cfg, sm_machin
     if (c.max_streams < 1 || c.max_streams > 64) return fail(SM_E_ARG, "sm_create: max_streams must be in [1, 64]");
     if (c.prefill_rows < 0 || c.prefill_rows > 64) return fail(SM_E_ARG, "sm_create: prefill_rows must be in [0, 64]");
     if (c.max_ctx <= 0) return fail(SM_E_ARG, "sm_create: max_ctx must be positive");
+    // graphs of at most 16 steps, the largest that has run: a profiled run of a 127-step graph ended in a SIGSEGV
+    // inside the profiled process, unexplained, so longer captures are refused rather than reached
+    if (c.graph_steps < 0 || c.graph_steps > 16) return fail(SM_E_ARG, "sm_create: graph_steps must be in [0, 16]");
     const std::string dir = std::string(layout_dir) + "/";
     std::vector<char> mj;
     if (!read_file(dir + "manifest.json", mj)) return fail(SM_E_IO, "cannot read " + dir + "manifest.json");
@@ -1349,7 +1374,6 @@ extern "C" int sm_create(const char* layout_dir, const sm_config* cfg, sm_machin
     }
     m->prompts.assign(B, {});
     m->gsteps = c.graph_steps > 0 ? c.graph_steps : 16;
-    if (m->gsteps > 256) return bail(fail(SM_E_ARG, "sm_create: graph_steps at most 256"));
     if ((rc = sm_reset(m))) return bail(rc);
     *out = m;
     return SM_OK;
@@ -1501,6 +1525,9 @@ extern "C" int sm_generate(sm_machine* m, int32_t n_words, int32_t* out) {
     if (ctl[CTL_ERR] & SM_ERR_RANGE)
         return fail(SM_E_OVERFLOW, "sm_generate: a value passed a bound the reference asserts (turn input 2^31, attention sum 2^62)");
     std::memcpy(out, m->hpin + CTL_N, (size_t)m->B * n_words * sizeof(int));
+    // a profiled machine folds its event pairs into the per-kernel sums now, so that their events are reused by the
+    // next call instead of piling up over a long run
+    if (m->cfg.profile && (rc = kt_fold())) return rc;
     return SM_OK;
 }
 
@@ -1516,7 +1543,7 @@ extern "C" int sm_profile(sm_machine* m, int64_t* n_heads, double* head_us, int3
     if (n_heads) *n_heads = n;
     if (head_us) *head_us = us;
     if (clear)
-        for (size_t i = 0; i < g_kt.names.size(); i++) { g_kt.n[i] = 0; g_kt.us[i] = 0.0; }
+        for (size_t i = 0; i < g_kt.names.size(); i++) { g_kt.n[i] = 0; g_kt.us[i] = 0.0; g_kt.syms[i].clear(); }
     return SM_OK;
 }
 
@@ -1536,6 +1563,12 @@ extern "C" int sm_profile_kernels(char* names, int32_t names_bytes, int64_t* lau
     for (size_t i = 0; i < g_kt.names.size() && k < max; i++) {
         if (!g_kt.n[i]) continue;
         all += g_kt.names[i];
+        const std::string* top = nullptr;                 // the symbol with the most launches under this name
+        long long most = -1;
+        for (const auto& kv : g_kt.syms[i])
+            if (kv.second > most) { most = kv.second; top = &kv.first; }
+        all += '\t';
+        all += top ? *top : std::string("?");
         all += '\n';
         launches[k] = g_kt.n[i];
         total_us[k] = g_kt.us[i];
@@ -1545,7 +1578,7 @@ extern "C" int sm_profile_kernels(char* names, int32_t names_bytes, int64_t* lau
     std::memcpy(names, all.c_str(), all.size() + 1);
     *n = k;
     if (clear)
-        for (size_t i = 0; i < g_kt.names.size(); i++) { g_kt.n[i] = 0; g_kt.us[i] = 0.0; }
+        for (size_t i = 0; i < g_kt.names.size(); i++) { g_kt.n[i] = 0; g_kt.us[i] = 0.0; g_kt.syms[i].clear(); }
     return SM_OK;
 }
 
@@ -1812,9 +1845,11 @@ extern "C" int64_t sm_plate_bytes(const sm_plate* p) {
 
 // the rows' light planes and row facts go to planes / rowinfo (the plate's own, or the static scratch of
 // sm_plate_product_rows_noalloc)
+// timed: each launch stamped with an event pair (sm_profile_stages); the allocation-free entry point never is, since
+// an event pair creates HIP events and records them
 template <int RT>
 static void rows_product(const sm_plate* p, const int64_t* x16, int32_t rows, int64_t* pile, hipStream_t s,
-                         signed char* planes, int* rowinfo) {
+                         signed char* planes, int* rowinfo, bool timed) {
     const MfmaPlate& P = p->M;
     LightArgs la{};
     la.K = P.K; la.rows = rows; la.X = (const i64*)x16; la.planes = planes; la.rowinfo = rowinfo;
@@ -1822,14 +1857,14 @@ static void rows_product(const sm_plate* p, const int64_t* x16, int32_t rows, in
     ga.K = P.K; ga.N = P.N; ga.rows = rows; ga.RT = RT; ga.W = P.W; ga.csum = P.csum; ga.we = P.e; ga.bias = P.b;
     ga.planes = planes; ga.rowinfo = rowinfo; ga.Y = (i64*)pile; ga.ystride = P.N;
     if (P.K == 768) {
-        launch(g_kt.stages, "plate.light", k_light<768, PRO_X16, 192, 1>, dim3(rows), dim3(192), 0, s, la);
+        launch(timed, "plate.light", k_light<768, PRO_X16, 192, 1>, dim3(rows), dim3(192), 0, s, la);
         if (P.N > 3072)       // head-shaped plates: the head's kernel (light planes in LDS)
-            launch(g_kt.stages, "plate.head_rows", k_head_rows<RT, EPI_PILE>, dim3(head_rows_grid(P.ntiles)), dim3(256), 0, s, ga);
+            launch(timed, "plate.head_rows", k_head_rows<RT, EPI_PILE>, dim3(head_rows_grid(P.ntiles)), dim3(256), 0, s, ga);
         else                  // layer-shaped plates: one column tile per block, K split over its four waves
-            launch(g_kt.stages, "plate.gemm", k_gemm<768, 1, 1, EPI_PILE>, dim3(P.ntiles, RT), dim3(256), 0, s, ga);
+            launch(timed, "plate.gemm", k_gemm<768, 1, 1, EPI_PILE>, dim3(P.ntiles, RT), dim3(256), 0, s, ga);
     } else {
-        launch(g_kt.stages, "plate.light", k_light<3072, PRO_X16, 768, 1>, dim3(rows), dim3(768), 0, s, la);
-        launch(g_kt.stages, "plate.gemm", k_gemm<3072, 1, 1, EPI_PILE>, dim3(P.ntiles, RT), dim3(256), 0, s, ga);
+        launch(timed, "plate.light", k_light<3072, PRO_X16, 768, 1>, dim3(rows), dim3(768), 0, s, la);
+        launch(timed, "plate.gemm", k_gemm<3072, 1, 1, EPI_PILE>, dim3(P.ntiles, RT), dim3(256), 0, s, ga);
     }
 }
 
@@ -1839,10 +1874,11 @@ extern "C" int sm_plate_product_rows(const sm_plate* p, const int64_t* x16, int3
     if (rows < 1 || rows > 64) return fail(SM_E_ARG, "sm_plate_product_rows: rows must be in [1, 64]");
     hipStream_t s = (hipStream_t)stream;
     const int RT = (rows + 15) / 16;
-    if (RT == 1) rows_product<1>(p, x16, rows, pile, s, p->planes, p->rowinfo);
-    else if (RT == 2) rows_product<2>(p, x16, rows, pile, s, p->planes, p->rowinfo);
-    else if (RT == 3) rows_product<3>(p, x16, rows, pile, s, p->planes, p->rowinfo);
-    else rows_product<4>(p, x16, rows, pile, s, p->planes, p->rowinfo);
+    const bool timed = g_kt.stages;
+    if (RT == 1) rows_product<1>(p, x16, rows, pile, s, p->planes, p->rowinfo, timed);
+    else if (RT == 2) rows_product<2>(p, x16, rows, pile, s, p->planes, p->rowinfo, timed);
+    else if (RT == 3) rows_product<3>(p, x16, rows, pile, s, p->planes, p->rowinfo, timed);
+    else rows_product<4>(p, x16, rows, pile, s, p->planes, p->rowinfo, timed);
     HIP_TRY(hipGetLastError());
     return SM_OK;
 }
@@ -1892,10 +1928,11 @@ extern "C" int sm_plate_product_rows_noalloc(const sm_plate* p, const int64_t* x
     signed char* planes = base;
     int* rowinfo = reinterpret_cast<int*>(base + SM_NOALLOC_PLANES);
     hipStream_t s = (hipStream_t)stream;
-    if (RT == 1) rows_product<1>(p, x16, rows, pile, s, planes, rowinfo);
-    else if (RT == 2) rows_product<2>(p, x16, rows, pile, s, planes, rowinfo);
-    else if (RT == 3) rows_product<3>(p, x16, rows, pile, s, planes, rowinfo);
-    else rows_product<4>(p, x16, rows, pile, s, planes, rowinfo);
+    // untimed whatever sm_profile_stages says: no HIP object is created or recorded on this path
+    if (RT == 1) rows_product<1>(p, x16, rows, pile, s, planes, rowinfo, false);
+    else if (RT == 2) rows_product<2>(p, x16, rows, pile, s, planes, rowinfo, false);
+    else if (RT == 3) rows_product<3>(p, x16, rows, pile, s, planes, rowinfo, false);
+    else rows_product<4>(p, x16, rows, pile, s, planes, rowinfo, false);
     HIP_TRY(hipGetLastError());
     return SM_OK;
 }

@@ -48,13 +48,10 @@ def lib():
     """Load the HIP library (built by __graft_entry__.build()); raises if it is not there."""
     global _LIB
     if _LIB is None:
-        # torch bundles a HIP runtime under the same soname (libamdhip64.so.7) as the one this library links: when
-        # torch is present its copy must be the process's, so it is loaded first (whichever the caller imports
-        # later then binds to it); torch initialised on top of the other copy finds no GPU
-        try:
-            import torch  # noqa: F401
-        except ImportError:
-            pass
+        # The library binds whichever HIP runtime (libamdhip64.so.7) the process already holds.  torch bundles its
+        # own copy under that soname and finds no GPU when initialised on top of the other one, so a process that
+        # uses torch imports it before this first load (the tests and bench.py do); the library itself never
+        # imports torch.
         if not os.path.exists(LIB_PATH):
             raise SmError(SM_E_IO, f"{LIB_PATH} is missing: build it (python -c 'import __graft_entry__ as g; g.build()')")
         L = ctypes.CDLL(LIB_PATH)
@@ -239,17 +236,20 @@ def profile_stages(on: bool = True):
     check(lib().sm_profile_stages(1 if on else 0))
 
 
-def kernel_times(clear: bool = True) -> dict:
-    """kernel name -> (launches, mean microseconds) of the timed launches since the last clear (process-wide)"""
+def kernel_times(clear: bool = True, symbols: bool = False) -> dict:
+    """kernel name -> (launches, mean microseconds) of the timed launches since the last clear (process-wide);
+    symbols=True: (launches, mean microseconds, the device function's demangled name as a kernel trace gives it)"""
     cap = 256
-    names = ctypes.create_string_buffer(cap * 64)
+    names = ctypes.create_string_buffer(cap * 256)
     n_l = np.zeros(cap, np.int64)
     us = np.zeros(cap, np.float64)
     n = i32()
     check(lib().sm_profile_kernels(names, len(names), n_l.ctypes.data_as(i64p), us.ctypes.data_as(ctypes.POINTER(ctypes.c_double)),
                                    cap, ctypes.byref(n), 1 if clear else 0))
-    keys = names.value.decode().split("\n")[:n.value]
-    return {k: (int(n_l[i]), float(us[i] / n_l[i])) for i, k in enumerate(keys)}
+    rows = [r.split("\t", 1) for r in names.value.decode().split("\n")[:n.value]]
+    if symbols:
+        return {r[0]: (int(n_l[i]), float(us[i] / n_l[i]), r[1] if len(r) > 1 else "") for i, r in enumerate(rows)}
+    return {r[0]: (int(n_l[i]), float(us[i] / n_l[i])) for i, r in enumerate(rows)}
 
 
 class Tables:

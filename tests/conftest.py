@@ -14,6 +14,13 @@ REPO = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 if REPO not in sys.path:
     sys.path.insert(0, REPO)
 
+# torch's bundled HIP runtime has the soname the library links (libamdhip64.so.7): loaded first, it is the one
+# runtime of this process, so the library and torch's GPU buffers share it
+try:
+    import torch  # noqa: F401
+except ImportError:
+    pass
+
 
 def load_sm():
     if "streaming_machine_amd" in sys.modules:

@@ -66,3 +66,10 @@ def test_null_arguments(sm):
     assert L.sm_create(None, None, None) == -1
     assert L.sm_reset(None) == -1
     assert L.sm_generate(None, 1, None) == -1
+
+
+def test_graph_steps_bounded_before_any_device_call(sm, tmp_path):
+    """captured graphs hold at most 16 decode steps: more is refused with SM_E_ARG before the layout is read"""
+    with pytest.raises(sm.SmError) as e:
+        sm.Machine(str(tmp_path / "no_such_dir"), graph_steps=17)
+    assert e.value.code == -1 and "graph_steps" in str(e.value)

@@ -142,7 +142,8 @@ def test_race(sm, orc, n):
     assert int(host(do)[0]) == orc.race(v) == int(np.argmax(v))
 
 
-SHAPES = [(768, 2304, 2), (768, 768, 2), (768, 3072, 2), (3072, 768, 1), (768, 50257, 8), (3072, 768, 2), (768, 2304, 8)]
+SHAPES = [(768, 2304, 2), (768, 768, 2), (768, 3072, 2), (3072, 768, 1), (768, 50257, 8), (768, 50257, 4), (3072, 768, 2),
+          (768, 2304, 8)]
 
 
 @pytest.mark.parametrize("nin,nout,tc", SHAPES)
