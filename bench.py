@@ -38,6 +38,7 @@ Printed: one JSON line with the driver's fields plus
 from __future__ import annotations
 
 import argparse
+import hashlib
 import importlib.util
 import json
 import os
@@ -450,35 +451,64 @@ def gemv_leg(sm, rotate_bytes: int = 1 << 30, rounds: int = 3):
 
 
 # ---- the attention microbenchmark: one attention step ----
-def attention_leg(sm, reps: int = 50):
-    """12 heads x 64, int16 keys and values uniform at T = 128, 512, 1024 (default_rng(3)), one new q, k, v; the
-    batch-1 attention kernel (sm_stage_attend)"""
-    import torch
+ATT_T = (128, 512, 1024)
+
+
+def attention_workload():
+    """12 heads x 64, int16 keys and values uniform at T = 128, 512, 1024 (default_rng(3), drawn in that order),
+    per-position water levels in [-16, -8], one new q, k, v (int16-range values); the new position is p = T - 1.
+    Yields (T, k16 int16 [12][T][64], ek int32 [12][T], v int32 [12][T][64], qkv int64 [2304])."""
     rng = np.random.default_rng(3)
+    for T in ATT_T:
+        k16 = rng.integers(-32768, 32768, (12, T, 64), dtype=np.int16)
+        ek = rng.integers(-16, -7, (12, T), dtype=np.int32)
+        v = rng.integers(-32768, 32768, (12, T, 64), dtype=np.int64).astype(np.int32)
+        qkv = rng.integers(-32768, 32768, 2304, dtype=np.int64)
+        yield T, k16, ek, v, qkv
+
+
+def attention_leg(sm, reps: int = 50):
+    """the attention workload through both batch-1 attention kernels: one block a head (sm_stage_attend) and spread
+    over chunks of 64 positions (sm_stage_attend_split, three launches); each output checked against the oracle's
+    value for the same caches (tests/golden/attention_cache.json) before any time is reported"""
+    import torch
+    want = {c["T"]: c for c in fixture_cases("attention_cache.json").values()}
     t = sm.Tables(sm.tables())
     out = {}
-    for T in (128, 512, 1024):
-        ctx = T
-        p = T - 1                                   # the new position; T positions attended
-        k16 = torch.from_numpy(rng.integers(-32768, 32768, (12, ctx, 64), dtype=np.int16)).cuda()
+    for T, k16h, ekh, vh, qkvh in attention_workload():
+        ctx, p = T, T - 1                           # T positions attended
+        k16, ek, v = torch.from_numpy(k16h).cuda(), torch.from_numpy(ekh).cuda(), torch.from_numpy(vh).cuda()
         km = torch.zeros((12, ctx), dtype=torch.int64, device="cuda")
-        ek = torch.from_numpy(rng.integers(-16, -7, (12, ctx), dtype=np.int32)).cuda()
-        v = torch.from_numpy(rng.integers(-32768, 32768, (12, ctx, 64), dtype=np.int64).astype(np.int32)).cuda()
-        qkv = torch.from_numpy(rng.integers(-32768, 32768, 2304, dtype=np.int64)).cuda()
-        o = torch.zeros(768, dtype=torch.int64, device="cuda")
-        sm.profile_stages(True)
-        sm.kernel_times(clear=True)
-        for _ in range(reps):
-            sm.stages.attend(t, qkv.data_ptr(), k16.data_ptr(), km.data_ptr(), ek.data_ptr(), v.data_ptr(), p, ctx, o.data_ptr())
-        n, us = sm.kernel_times(clear=True)["stage.attend"]
-        sm.profile_stages(False)
+        qkv = torch.from_numpy(qkvh).cuda()
         kv = T * 768 * 2 * 2                         # int16 k and v (the attention microbenchmark's workload)
         layout = T * 12 * (128 + 8 + 4 + 256)        # this layout: int16 k, int64 mask, int32 level, int32 v
-        out[str(T)] = {"us": round(us, 3), "kv_bytes": kv, "layout_bytes": layout,
-                       "gbs_layout": round(layout / (us * 1e-6) / 1e9, 1)}
+        row = {"kv_bytes": kv, "layout_bytes": layout}
+        for fn, names in (("attend", ("stage.attend",)),
+                          ("attend_split", ("stage.attend.scores", "stage.attend.mix", "stage.attend.finish"))):
+            f = getattr(sm.stages, fn)
+            o = torch.zeros(768, dtype=torch.int64, device="cuda")
+            f(t, qkv.data_ptr(), k16.data_ptr(), km.data_ptr(), ek.data_ptr(), v.data_ptr(), p, ctx, o.data_ptr())
+            got = o.cpu().numpy()
+            w = want.get(T)
+            if w is None or hashlib.sha256(got.tobytes()).hexdigest() != w["out_sha256"]:
+                raise RuntimeError(f"attention T={T} ({fn}): output differs from the oracle's fixture")
+            sm.profile_stages(True)
+            sm.kernel_times(clear=True)
+            for _ in range(reps):
+                f(t, qkv.data_ptr(), k16.data_ptr(), km.data_ptr(), ek.data_ptr(), v.data_ptr(), p, ctx, o.data_ptr())
+            times = sm.kernel_times(clear=True)
+            sm.profile_stages(False)
+            us = sum(times[n][1] for n in names)
+            row[fn] = {"us": round(us, 3), "gbs_layout": round(layout / (us * 1e-6) / 1e9, 1),
+                       "frac_layout": round(layout / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+                       **({"launches_us": {n.split(".")[-1]: round(times[n][1], 3) for n in names}}
+                          if len(names) > 1 else {})}
+        out[str(T)] = row
     t.close()
-    return {"note": "kernel durations from HIP event pairs stamped by each dispatch; the batch-1 attention kernel "
-                    "(one block a head), warm", "T": out}
+    return {"note": "kernel durations from HIP event pairs stamped by each dispatch, warm; attend: one block a head; "
+                    "attend_split: each head's positions in chunks of 64, one block a chunk, three launches (scores "
+                    "and chunk maxima; arrivals and value sums; the divisor), their durations summed; both outputs "
+                    "equal the oracle's on the same caches", "T": out}
 
 
 # ---- CPU baseline ----

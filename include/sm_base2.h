@@ -69,6 +69,11 @@ typedef struct {
                               393..512).  0: the full read (the default: measured faster at batch 1 since the
                               head's logits take a two-instruction rounding shift).  2: the collapsing read where
                               it applies, else the full read */
+    int32_t att_split;     /* batch 1: decode steps at positions from this one on run the attention spread over the
+                              GPU, each head's cached positions in chunks of 64, one block a chunk (the chunks'
+                              scores and maxima, then arrivals against the head's maximum and the value sums added
+                              exactly, then the divisor: three launches); steps before it run one block a head.
+                              0: from position 160; -1: never.  The same numbers either way (base2.py:85-100) */
 } sm_config;
 
 enum { SM_FLOAT_GAUGE = 1, SM_FLOAT_EDGE = 2, SM_FLOAT_ARRIVAL = 4, SM_FLOAT_TURN = 8 };
@@ -183,6 +188,13 @@ int sm_stage_race(const int64_t* v, int64_t n, int64_t* out_index, void* stream)
  * v int32 [12][ctx][64]; out: device int64 [768].  Zeroed caches are empty caches. */
 int sm_stage_attend(const sm_tables* t, const int64_t* qkv, int16_t* k16, int64_t* km, int32_t* ek, int32_t* v,
                     int32_t pos, int32_t ctx, int64_t* out, void* stream);
+
+/* The same attention as sm_stage_attend (the same arguments, caches and results), spread over the GPU as the batch-1
+ * machine runs it from its att_split position on: each head's positions in chunks of 64, one block a chunk, three
+ * launches (scores and chunk maxima; arrivals against the head's maximum with the value sums added exactly; the
+ * divisor).  ctx at most 8192; the first call allocates its scratch (score row, chunk maxima, sums) with the tables. */
+int sm_stage_attend_split(const sm_tables* t, const int64_t* qkv, int16_t* k16, int64_t* km, int32_t* ek, int32_t* v,
+                          int32_t pos, int32_t ctx, int64_t* out, void* stream);
 
 /* The same new position's attention for `rows` independent streams at once, through the batched machine's kernel
  * (one block per head and stream; base2.py:85-100 for each stream's last row).  qkv: device int64 [rows][2304]; the

@@ -91,6 +91,8 @@ class Oracle:
         L.orc_kv_read_resid.argtypes = [ctypes.c_void_p, i64p]
         L.orc_attention.restype = ctypes.c_int
         L.orc_attention.argtypes = [ctypes.POINTER(OrcModel), i64p, ctypes.c_int64, i64p]
+        L.orc_attend_cached.restype = ctypes.c_int
+        L.orc_attend_cached.argtypes = [ctypes.POINTER(OrcModel), i64p, i64p, i64p, i64p, ctypes.c_int64, ctypes.c_int64, i64p]
         self._keep = []
         m = OrcModel()
 
@@ -146,6 +148,20 @@ class Oracle:
         QKV = np.ascontiguousarray(QKV, dtype=np.int64)
         out = np.zeros((QKV.shape[0], 768), dtype=np.int64)
         if self.lib.orc_attention(ctypes.byref(self.m), _p(QKV), QKV.shape[0], _p(out)):
+            raise ArithmeticError("oracle: attention sum passed 2^52")
+        return out
+
+    def attend_cached(self, qkv: np.ndarray, k16: np.ndarray, ek: np.ndarray, v: np.ndarray, p: int) -> np.ndarray:
+        """the newest row p's attention over a given cache (k16 [12][ctx][64], ek [12][ctx], v [12][ctx][64]; rows
+        s < p used) and its own q, k, v from qkv [2304]: the device attention's contract (sm_stage_attend)"""
+        qkv = np.ascontiguousarray(qkv, dtype=np.int64)
+        k16 = np.ascontiguousarray(k16, dtype=np.int64)
+        ek = np.ascontiguousarray(ek, dtype=np.int64)
+        v = np.ascontiguousarray(v, dtype=np.int64)
+        ctx = k16.shape[1]
+        assert k16.shape == (12, ctx, 64) and ek.shape == (12, ctx) and v.shape == (12, ctx, 64) and 0 <= p < ctx
+        out = np.zeros(768, dtype=np.int64)
+        if self.lib.orc_attend_cached(ctypes.byref(self.m), _p(qkv), _p(k16), _p(ek), _p(v), ctx, p, _p(out)):
             raise ArithmeticError("oracle: attention sum passed 2^52")
         return out
 

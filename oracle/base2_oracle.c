@@ -211,6 +211,31 @@ static int attend_row(const orc_model* M, const i64* q16, i64 eq, const i64* k16
     return bad;
 }
 
+/* base2.py:93-99 for the newest row p over a given cache (the device attention's contract, sm_stage_attend):
+ * positions s < p from the caches k16 [12][ctx][64] (the keys' 16-bit lights), ek [12][ctx], v [12][ctx][64] (raw
+ * values); position p from qkv [2304], its q and k through to16 (base2.py:93), its v raw.  out [768].  The same
+ * attend_row as orc_attention, whose rows the golden vectors pin; a cache filled from QKV rows gives its rows. */
+int orc_attend_cached(const orc_model* M, const i64* qkv, const i64* k16c, const i64* ekc, const i64* vc, i64 ctx,
+                      i64 p, i64* out) {
+    int bad = 0;
+    i64* k16 = malloc(sizeof(i64) * (p + 1) * 64); i64* ek = malloc(sizeof(i64) * (p + 1));
+    i64* v = malloc(sizeof(i64) * (p + 1) * 64); i64* sc = malloc(sizeof(i64) * (p + 1));
+    for (int h = 0; h < 12; h++) {
+        i64 q16[64];
+        const i64 eq = orc_to16_row(qkv + h * 64, 64, -16, q16);
+        for (i64 s = 0; s < p; s++) {
+            memcpy(k16 + s * 64, k16c + (h * ctx + s) * 64, sizeof(i64) * 64);
+            ek[s] = ekc[h * ctx + s];
+            memcpy(v + s * 64, vc + (h * ctx + s) * 64, sizeof(i64) * 64);
+        }
+        ek[p] = orc_to16_row(qkv + 768 + h * 64, 64, -16, k16 + p * 64);
+        memcpy(v + p * 64, qkv + 1536 + h * 64, sizeof(i64) * 64);
+        bad |= attend_row(M, q16, eq, k16, ek, v, 64, 64, p, sc, out + h * 64);
+    }
+    free(k16); free(ek); free(v); free(sc);
+    return bad ? ORC_E_BOUND : ORC_OK;
+}
+
 /* base2.py:85-100  attention over all P rows of QKV [P][2304] -> out [P][768] */
 int orc_attention(const orc_model* M, const i64* QKV, i64 P, i64* out) {
     int bad = 0;

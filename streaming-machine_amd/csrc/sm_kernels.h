@@ -153,6 +153,9 @@ struct AttArgs {
     // prompt rows: row r is position rowmap[r] & 0xFFFF of stream rowmap[r] >> 16 (null: row r is stream r at
     // *pos).  Their keys and values are in the cache already (k_kv_rows), so the attention only reads it.
     const int* rowmap;
+    // the batch-1 attention spread over chunks of positions (k_att_scores, k_att_mix, k_att_finish): the score row
+    // [12][ctx], the chunk maxima [12][ncm], the per-head accumulators [12][ACC_W]
+    i64* asc; i64* acm; i64* aacc; int ncm;
 };
 
 // error bits in the device error word

@@ -12,6 +12,7 @@
 // (base2_stream.swift:273-281 commits one command buffer per prompt the same way).
 #include "sm_kernels.hip"
 #include "sm_batch.hip"
+#include "sm_attend_split.hip"
 #include "../../include/sm_base2.h"
 
 #include <hip/hip_ext.h>
@@ -28,6 +29,10 @@
 #include <vector>
 
 static thread_local std::string g_err;
+
+// the batch-1 machine's default split position (sm_config.att_split = 0): from this position on a step's attention
+// runs spread over chunks of 64 positions (sm_attend_split.hip), below it one block a head (k_attend)
+#define SM_ATT_SPLIT_AT 160
 
 static int fail(int code, const std::string& msg) {
     g_err = msg;
@@ -275,6 +280,8 @@ struct sm_tables {
     i64 log768 = 0, eps40 = 0;
     int verified = 0;         // every entry equals its defining formula (checked on the device at create)
     int* scratch = nullptr;   // [0] pos for sm_stage_attend, [1] error bits, [4..7] mismatch counts
+    // sm_stage_attend_split's score row, chunk maxima and accumulators (made at its first call, for ctx <= 8192)
+    i64 *asc = nullptr, *acm = nullptr, *aacc = nullptr;
     Tables tb() const { return Tables{LOG2, EXP2, PHI, ARR, alen, log768, eps40, GPOW, HPOW, PGPOW}; }
 };
 
@@ -327,6 +334,7 @@ static int tables_init(sm_tables& T, const i64* phi, const i64* arr, int alen, c
 
 static void tables_free(sm_tables& T) {
     hfree(T.LOG2); hfree(T.EXP2); hfree(T.PHI); hfree(T.ARR); hfree(T.GPOW); hfree(T.HPOW); hfree(T.PGPOW); hfree(T.scratch);
+    hfree(T.asc); hfree(T.acm); hfree(T.aacc);
     T = sm_tables();
 }
 
@@ -369,6 +377,12 @@ struct sm_machine {
     // turn and arrival
     int mode = 0;
     bool fturn = false, farr = false;
+    // batch 1: steps at positions from att_split on run the attention spread over chunks of positions (-1: never);
+    // att_long is the structure of the steps being launched or captured
+    int att_split = -1;
+    bool att_long = false;
+    i64 *asc = nullptr, *acm = nullptr, *aacc = nullptr;   // its score row [12][ctx], chunk maxima, accumulators
+    int ncm = 0;
     int* hpin = nullptr;      // pinned host words: the control block and every stream's words of a generate call
     double *cosF = nullptr, *sinF = nullptr;            // turn=float: [npos][rot / 2]
     double* KF = nullptr;                               // arrival=float: [L][12 heads][ctx][64] keys as float64
@@ -398,11 +412,12 @@ struct sm_machine {
     i64 *r_x16 = nullptr, *r_exls = nullptr, *r_pile = nullptr, *r_qkv = nullptr, *r_att = nullptr, *r_hid = nullptr,
         *r_resid = nullptr, *r_hx16 = nullptr, *r_hexls = nullptr, *r_hpile = nullptr, *r_logits = nullptr;
     i64 *r_gauge = nullptr, *r_fcpre = nullptr, *r_hgauge = nullptr;   // Pythia: gauges [L][2][768], fc before the edge
-    // captured decode steps: [0] graph_steps whole steps, [1] one whole step, [2] one step's layers, [3] its head;
-    // one capture for each position slot a replay starts from (gflip: the replay ends on the other slot)
-    hipGraphExec_t gexec[4][2] = {};
-    hipGraph_t graph[4][2] = {};
-    bool gflip[4] = {};
+    // captured decode steps: [0] graph_steps whole steps, [1] one whole step, [2] one step's layers, [3] its head,
+    // [4], [5]: [0], [1] with the attention spread over chunks of positions; one capture for each position slot a
+    // replay starts from (gflip: the replay ends on the other slot)
+    hipGraphExec_t gexec[6][2] = {};
+    hipGraph_t graph[6][2] = {};
+    bool gflip[6] = {};
     int gsteps = 16;
     int par = 0;                   // batched streams: the slot that holds the position of the next step
     // profiling: an event pair around each step's head kernel (the largest single launch)
@@ -500,7 +515,7 @@ static int parse_norms(const std::string& text, std::vector<std::pair<std::strin
 
 static void machine_free(sm_machine* m) {
     if (!m) return;
-    for (int i = 0; i < 4; i++)
+    for (int i = 0; i < 6; i++)
         for (int j = 0; j < 2; j++) {
             if (m->gexec[i][j]) (void)hipGraphExecDestroy(m->gexec[i][j]);
             if (m->graph[i][j]) (void)hipGraphDestroy(m->graph[i][j]);
@@ -515,7 +530,7 @@ static void machine_free(sm_machine* m) {
                   m->r_hx16, m->r_hexls, m->r_hpile, m->r_logits, m->r_gauge, m->r_fcpre, m->r_hgauge,
                   m->fg, m->fb, m->ew, m->ee, m->ew2, m->cosT, m->sinT, m->cosF, m->sinF, m->KF,
                   m->top_hi, m->top_lo, m->cand_j, m->cand_h, m->cand_c, m->top_x, m->top_f, m->top_n, m->top_w,
-                  m->top_pile, m->top_score};
+                  m->top_pile, m->top_score, m->asc, m->acm, m->aacc};
     for (void* p : ps) hfree(p);
     for (int l = 0; l < 12; l++)
         for (int j = 0; j < 2; j++) { hfree(m->ng[l][j]); hfree(m->nb[l][j]); }
@@ -730,7 +745,19 @@ static void gemv(sm_machine* m, bool rec, const char* name, int grid, const Gemv
 }
 // batch-1 attention: the integer arrival (turn=float: its FTURN instantiation), or arrival=float
 template <int MODEL, int FTURN>
-static void attend1_t(sm_machine* m, bool rec, const AttArgs& a) {
+static void attend1_t(sm_machine* m, bool rec, AttArgs a) {
+    if constexpr (!FTURN) {
+        if (m->att_long) {                    // the attention spread over chunks of positions (sm_attend_split.hip)
+            a.asc = m->asc; a.acm = m->acm; a.aacc = m->aacc; a.ncm = m->ncm;
+            const dim3 grid(12, m->ncm);
+            launch(m->cfg.profile, "attend.scores", k_att_scores<MODEL>, grid, dim3(256), 0, m->st, a);
+            if (m->T.verified) launch(m->cfg.profile, "attend.mix", k_att_mix<MODEL, 1>, grid, dim3(256), 0, m->st, a);
+            else launch(m->cfg.profile, "attend.mix", k_att_mix<MODEL, 0>, grid, dim3(256), 0, m->st, a);
+            if (rec) launch(m->cfg.profile, "attend.finish", k_att_finish<MODEL, 1>, dim3(12), dim3(64), 0, m->st, a);
+            else launch(m->cfg.profile, "attend.finish", k_att_finish<MODEL, 0>, dim3(12), dim3(64), 0, m->st, a);
+            return;
+        }
+    }
     if (m->farr) {
         if (rec) launch(m->cfg.profile, "attend", k_attend_f<MODEL, FTURN, 1>, dim3(12), dim3(256), (size_t)m->ctx * 8, m->st, a);
         else launch(m->cfg.profile, "attend", k_attend_f<MODEL, FTURN, 0>, dim3(12), dim3(256), (size_t)m->ctx * 8, m->st, a);
@@ -1138,7 +1165,7 @@ static int run_prefill(sm_machine* m, int npos) {
 extern "C" int sm_create(const char* layout_dir, const sm_config* cfg, sm_machine** out) {
     if (!layout_dir || !out) return fail(SM_E_ARG, "sm_create: null argument");
     *out = nullptr;
-    sm_config c{1, 1024, 1, 0, 16, 0, 0, 64, 0, 0, 2};
+    sm_config c{1, 1024, 1, 0, 16, 0, 0, 64, 0, 0, 2, 0};
     if (cfg) c = *cfg;
     if (c.max_streams < 1 || c.max_streams > 64) return fail(SM_E_ARG, "sm_create: max_streams must be in [1, 64]");
     if (c.prefill_rows < 0 || c.prefill_rows > 64) return fail(SM_E_ARG, "sm_create: prefill_rows must be in [0, 64]");
@@ -1146,6 +1173,7 @@ extern "C" int sm_create(const char* layout_dir, const sm_config* cfg, sm_machin
     // graphs of at most 16 steps, the largest that has run: a profiled run of a 127-step graph ended in a SIGSEGV
     // inside the profiled process, unexplained, so longer captures are refused rather than reached
     if (c.graph_steps < 0 || c.graph_steps > 16) return fail(SM_E_ARG, "sm_create: graph_steps must be in [0, 16]");
+    if (c.att_split < -1) return fail(SM_E_ARG, "sm_create: att_split must be -1, 0 or a position");
     const std::string dir = std::string(layout_dir) + "/";
     std::vector<char> mj;
     if (!read_file(dir + "manifest.json", mj)) return fail(SM_E_IO, "cannot read " + dir + "manifest.json");
@@ -1193,6 +1221,8 @@ extern "C" int sm_create(const char* layout_dir, const sm_config* cfg, sm_machin
               (c.float_stages & SM_FLOAT_EDGE ? MODE_FEDGE : 0) | (split ? MODE_SPLIT : 0);
     m->fturn = c.float_stages & SM_FLOAT_TURN;
     m->farr = c.float_stages & SM_FLOAT_ARRIVAL;
+    // the spread attention: batch 1 with the integer arrival and turn
+    if (m->B == 1 && !m->farr && !m->fturn && c.att_split != -1) m->att_split = c.att_split > 0 ? c.att_split : SM_ATT_SPLIT_AT;
     const bool mfma = m->B > 1 || c.prefill_rows > 0;     // the MFMA banks: batched streams or prompt passes
 
     auto bail = [&](int code) { machine_free(m); return code; };
@@ -1366,6 +1396,12 @@ extern "C" int sm_create(const char* layout_dir, const sm_config* cfg, sm_machin
         (rc = dalloc(&m->r_logits, (size_t)m->vocab)) || (rc = dalloc(&m->r_gauge, (size_t)12 * 2 * 768)) ||
         (rc = dalloc(&m->r_fcpre, (size_t)12 * 3072)) || (rc = dalloc(&m->r_hgauge, (size_t)768)))
         return bail(rc);
+    if (m->att_split >= 0) {
+        m->ncm = (int)((ctx + ACH_SPLIT - 1) / ACH_SPLIT);
+        if ((rc = dalloc(&m->asc, 12 * ctx)) || (rc = dalloc(&m->acm, (size_t)12 * m->ncm)) ||
+            (rc = dalloc(&m->aacc, (size_t)12 * ACC_W)))
+            return bail(rc);
+    }
     if (hipMemset(m->planes, 0, (size_t)4 * 48 * 3 * 1024 * nsets) != hipSuccess || hipMemset(m->rowinfo, 0, RC * 32 * nsets) != hipSuccess)
         return bail(fail(SM_E_HIP, "hipMemset planes"));
     if (hipHostMalloc(&m->hpin, (CTL_N + B * (ctx + 1)) * sizeof(int), hipHostMallocDefault) != hipSuccess) {
@@ -1455,20 +1491,35 @@ static int replay(sm_machine* m, int which, int n, int parts) {
     return SM_OK;
 }
 
-// n whole decode steps: replayed from captured graphs, or launched one by one (always so with profile = 1, whose
-// launches each carry their event pair)
-static int queue_steps(sm_machine* m, int steps) {
+// n whole decode steps of one attention structure: replayed from captured graphs, or launched one by one (always so
+// with profile = 1, whose launches each carry their event pair)
+static int queue_run(sm_machine* m, int steps) {
     int rc;
+    const int g = m->att_long ? 4 : 0;
     if (m->cfg.use_graph && !m->cfg.profile) {
         for (; steps >= m->gsteps; steps -= m->gsteps)
-            if ((rc = replay(m, 0, m->gsteps, STEP_ALL))) return rc;
+            if ((rc = replay(m, g, m->gsteps, STEP_ALL))) return rc;
         for (; steps > 0; steps--)
-            if ((rc = replay(m, 1, 1, STEP_ALL))) return rc;
+            if ((rc = replay(m, g + 1, 1, STEP_ALL))) return rc;
     } else {
         for (; steps > 0; steps--)
             if ((rc = launch_step(m))) return rc;
     }
     return SM_OK;
+}
+// n decode steps from position pos: those before the split position with the one-block attention, the rest with
+// the attention spread over chunks of positions
+static int queue_steps(sm_machine* m, int steps, int pos) {
+    int rc;
+    if (m->att_split >= 0 && pos < m->att_split && steps > 0) {
+        const int n = std::min(steps, m->att_split - pos);
+        m->att_long = false;
+        if ((rc = queue_run(m, n))) return rc;
+        steps -= n;
+        pos += n;
+    }
+    m->att_long = m->att_split >= 0 && pos >= m->att_split;
+    return steps > 0 ? queue_run(m, steps) : SM_OK;
 }
 
 // n decode steps from position pos0.  At batch 1 the step at the recorded position runs on its own with the
@@ -1477,11 +1528,12 @@ static int run_steps(sm_machine* m, int n, int pos0) {
     const int rp = m->B == 1 ? m->h_recpos : -1;
     int rc;
     if (rp >= pos0 && rp < pos0 + n) {
-        if ((rc = queue_steps(m, rp - pos0))) return rc;
+        if ((rc = queue_steps(m, rp - pos0, pos0))) return rc;
+        m->att_long = m->att_split >= 0 && rp >= m->att_split;
         if ((rc = launch_step(m, STEP_ALL, true))) return rc;
-        return queue_steps(m, pos0 + n - rp - 1);
+        return queue_steps(m, pos0 + n - rp - 1, rp + 1);
     }
-    return queue_steps(m, n);
+    return queue_steps(m, n, pos0);
 }
 
 extern "C" int sm_generate(sm_machine* m, int32_t n_words, int32_t* out) {
@@ -1757,6 +1809,47 @@ extern "C" int sm_stage_attend(const sm_tables* t, const int64_t* qkv, int16_t* 
     if (err & SM_ERR_V32) {
         HIP_TRY(hipMemset(t->scratch + 1, 0, 4));
         return fail(SM_E_OVERFLOW, "sm_stage_attend: a value left 32 bits");
+    }
+    return SM_OK;
+}
+
+// the same attention spread over chunks of 64 positions, the batch-1 machine's kernels for positions from its split
+// position on (sm_attend_split.hip)
+#define SM_STAGE_ATT_CTX 8192
+extern "C" int sm_stage_attend_split(const sm_tables* t, const int64_t* qkv, int16_t* k16, int64_t* km, int32_t* ek,
+                                     int32_t* v, int32_t pos, int32_t ctx, int64_t* out, void* stream) {
+    if (!t || !qkv || !k16 || !km || !ek || !v || !out || ctx <= 0 || pos < 0 || pos >= ctx || ctx > SM_STAGE_ATT_CTX)
+        return fail(SM_E_ARG, "sm_stage_attend_split: arguments");
+    sm_tables* tt = const_cast<sm_tables*>(t);
+    const int ncm = (SM_STAGE_ATT_CTX + ACH_SPLIT - 1) / ACH_SPLIT;
+    if (!tt->asc) {
+        int rc;
+        if ((rc = dalloc(&tt->asc, (size_t)12 * SM_STAGE_ATT_CTX)) || (rc = dalloc(&tt->acm, (size_t)12 * ncm)) ||
+            (rc = dalloc(&tt->aacc, (size_t)12 * ACC_W))) {
+            hfree(tt->asc); hfree(tt->acm); hfree(tt->aacc);
+            tt->asc = tt->acm = tt->aacc = nullptr;
+            return rc;
+        }
+    }
+    hipStream_t s = (hipStream_t)stream;
+    HIP_TRY(hipMemcpyAsync(t->scratch, &pos, 4, hipMemcpyHostToDevice, s));
+    HIP_TRY(hipStreamSynchronize(s));
+    AttArgs a{};
+    a.QKV = (const i64*)qkv; a.K16 = k16; a.KM = (i64*)km; a.EK = ek; a.V = v; a.out = (i64*)out; a.pos = t->scratch; a.ctx = ctx;
+    a.tb = t->tb(); a.err = t->scratch + 1;
+    a.asc = tt->asc; a.acm = tt->acm; a.aacc = tt->aacc; a.ncm = ncm;
+    const dim3 grid(12, (ctx + ACH_SPLIT - 1) / ACH_SPLIT);
+    const bool timed = g_kt.stages;
+    launch(timed, "stage.attend.scores", k_att_scores<0>, grid, dim3(256), 0, s, a);
+    launch(timed, "stage.attend.mix", k_att_mix<0, 0>, grid, dim3(256), 0, s, a);
+    launch(timed, "stage.attend.finish", k_att_finish<0, 0>, dim3(12), dim3(64), 0, s, a);
+    HIP_TRY(hipGetLastError());
+    int err = 0;
+    HIP_TRY(hipMemcpyAsync(&err, t->scratch + 1, 4, hipMemcpyDeviceToHost, s));
+    HIP_TRY(hipStreamSynchronize(s));
+    if (err & SM_ERR_V32) {
+        HIP_TRY(hipMemset(t->scratch + 1, 0, 4));
+        return fail(SM_E_OVERFLOW, "sm_stage_attend_split: a value left 32 bits");
     }
     return SM_OK;
 }

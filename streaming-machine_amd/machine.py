@@ -32,7 +32,7 @@ class SmConfig(ctypes.Structure):
     _fields_ = [("max_streams", ctypes.c_int32), ("max_ctx", ctypes.c_int32), ("use_graph", ctypes.c_int32),
                 ("head_grid", ctypes.c_int32), ("graph_steps", ctypes.c_int32), ("profile", ctypes.c_int32),
                 ("table_mode", ctypes.c_int32), ("prefill_rows", ctypes.c_int32), ("inv", ctypes.c_int32),
-                ("float_stages", ctypes.c_int32), ("top_read", ctypes.c_int32)]
+                ("float_stages", ctypes.c_int32), ("top_read", ctypes.c_int32), ("att_split", ctypes.c_int32)]
 
 
 FLOAT_STAGES = dict(gauge=1, edge=2, arrival=4, turn=8)     # SM_FLOAT_* of include/sm_base2.h
@@ -80,6 +80,7 @@ def lib():
         L.sm_stage_gauge_log.argtypes = [vp, vp, i32, vp, vp, vp, vp]
         L.sm_stage_race.argtypes = [vp, i64, vp, vp]
         L.sm_stage_attend.argtypes = [vp, vp, vp, vp, vp, vp, i32, i32, vp, vp]
+        L.sm_stage_attend_split.argtypes = [vp, vp, vp, vp, vp, vp, i32, i32, vp, vp]
         L.sm_stage_attend_rows.argtypes = [vp, vp, i32, vp, vp, vp, vp, i32, i32, vp, vp]
         L.sm_plate_create.argtypes = [ctypes.POINTER(ctypes.c_int16), i32p, i64p, i32, i32, i32, ctypes.POINTER(vp)]
         L.sm_plate_destroy.argtypes = [vp]
@@ -119,6 +120,8 @@ class Machine:
       .forward(ids) -> word                                 (base2.py:forward's contract)
       .reset(); .prefill(ids, stream=0); .generate(n_words) -> int32 [n_streams][n_words]
       .record_at(pos); .read(name, layer=0, stream=0, pos=0)
+      att_split: batch 1, the position from which a step's attention runs spread over the GPU (chunks of 64
+      positions, one block a chunk; 0: from position 160, -1: never); the same words either way.
     gauge / edge / arrival ("int" or "float"; base2.py:10-11) and turn (the Pythia machine,
     foundation0/pythia_base2.py:21-27) put that stage back to float64 on the device, as the reference's switches
     do: diagnostics, compared with the reference at the word level (one stream, prefill_rows=0).  With
@@ -128,7 +131,7 @@ class Machine:
     def __init__(self, layout_dir: str, max_ctx: int = 1024, max_streams: int = 1, use_graph: bool = True,
                  head_grid: int = 0, graph_steps: int = 16, profile: bool = False, verify_tables: bool = False,
                  prefill_rows: int = 64, gauge: str = "int", edge: str = "int", arrival: str = "int", turn: str = "int",
-                 inv: bool = False, top: str = "plain"):
+                 inv: bool = False, top: str = "plain", att_split: int = 0):
         fs = 0
         for name, v in (("gauge", gauge), ("edge", edge), ("arrival", arrival), ("turn", turn)):
             if v not in ("int", "float"):
@@ -139,7 +142,7 @@ class Machine:
         self.L = lib()
         cfg = SmConfig(max_streams, max_ctx, 1 if use_graph else 0, head_grid, graph_steps, 1 if profile else 0,
                        1 if verify_tables else 0, prefill_rows, 1 if inv else 0, fs,
-                       dict(plain=0, fr=1, auto=2)[top])
+                       dict(plain=0, fr=1, auto=2)[top], att_split)
         h = vp()
         check(self.L.sm_create(os.fsencode(layout_dir), ctypes.byref(cfg), ctypes.byref(h)))
         self.h = h
@@ -354,6 +357,12 @@ class stages:
         """k16: int16 [12][ctx][64] keys (+32768 held as 32767), km: int64 [12][ctx] masks of the +32768
         dimensions, ek: int32 [12][ctx], v: int32 [12][ctx][64] (device pointers; zeroed = empty)"""
         check(lib().sm_stage_attend(t.h, qkv, k16, km, ek, v, pos, ctx, out, stream))
+
+    @staticmethod
+    def attend_split(t: Tables, qkv, k16, km, ek, v, pos, ctx, out, stream=0):
+        """the same attention (same caches and result) spread over the GPU: each head's positions in chunks of 64,
+        one block a chunk, as the batch-1 machine runs it from its att_split position on (ctx <= 8192)"""
+        check(lib().sm_stage_attend_split(t.h, qkv, k16, km, ek, v, pos, ctx, out, stream))
 
     @staticmethod
     def attend_rows(t: Tables, qkv, rows, k16, km, ek, v, pos, ctx, out, stream=0):

@@ -7,7 +7,7 @@ import os
 import numpy as np
 import pytest
 
-from conftest import golden_case, h64
+from conftest import REPO, golden_case, h64
 
 pytestmark = pytest.mark.gpu
 
@@ -163,9 +163,52 @@ def test_kv_cache_matches_oracle(full_machine, full_oracle, sm):
 
 
 def test_long_context_against_oracle(full_machine, full_oracle, sm):
-    """a 200-token prompt and 40 words (context 240): words equal the KV-cached oracle's"""
+    """a 200-token prompt and 40 words (context 240; the attention spread over chunks of positions, the machine's
+    default past position 128): words equal the KV-cached oracle's"""
     prompt = sm.prompt_ids(9, 200)
     assert full_machine.stream(prompt, 40) == full_oracle.generate(prompt, 40, 256)
+
+
+@pytest.mark.parametrize("att_split", [-1, 1, 150])
+def test_attention_structures_give_the_same_machine(sm, full_dir, full_oracle, golden, att_split):
+    """the batch-1 attention one block a head (att_split -1), spread over chunks from position 1 on, and switching
+    at position 150 inside a run: the same words as the oracle over a 200-token prompt (prompt positions through
+    the decode step, so every position 0..239 runs one of the two), the KV cache late in the context, and base2.py's
+    words and every recorded intermediate of the golden sequence"""
+    m = sm.Machine(full_dir, max_ctx=256, att_split=att_split, prefill_rows=0)
+    prompt = sm.prompt_ids(9, 200)
+    words = m.stream(prompt, 40)
+    assert words == full_oracle.generate(prompt, 40, 256)
+    s = full_oracle.session(256)
+    seq = prompt + words
+    for i, t in enumerate(seq[:-1]):
+        s.step(t, want_head=False)
+    for l in (0, 11):
+        for p in (149, 150, 238):
+            k16, ek, v = s.read_kv(l, p)
+            assert np.array_equal(m.read("k16", l, 0, p), k16)
+            assert np.array_equal(m.read("ek", l, 0, p), ek)
+            assert np.array_equal(m.read("v", l, 0, p), v)
+    c = golden_case(golden, "c1_p8_w16")
+    for which in ("first", "last"):
+        rec = c["records"][which]
+        m.reset()
+        m.record_at(rec["position"])
+        m.prefill(c["prompt"])
+        assert [int(w) for w in m.generate(len(c["words"]))[0]] == c["words"]
+        compare_record(machine_record(m), rec)
+    m.record_at(-1)
+    m.close()
+
+
+def test_thousand_token_prompt_batch1(sm, full_dir):
+    """batch 1, a 1000-token prompt and 8 words: the attention spread over 16 chunks a head (positions 999..1006)"""
+    import json as _json
+    with open(os.path.join(REPO, "tests", "golden", "long_oracle.json")) as f:
+        case = {c["name"]: c for c in _json.load(f)["cases"]}["gpt2_p1000_w8"]
+    m = sm.Machine(full_dir, max_ctx=1008)
+    assert m.stream(case["prompt"], 8) == case["words"]
+    m.close()
 
 
 def test_prompt_of_one_word_and_continuation(full_machine, full_oracle, sm):

@@ -56,9 +56,10 @@ def oracle_stream0(orc, case):
     return rec["stream"][0].copy()
 
 
-@pytest.mark.parametrize("use_graph", [True, False])
-def test_small_model_words_and_records(sm, py_small_dir, py_small_oracle, pgolden, use_graph):
-    m = sm.Machine(py_small_dir, max_ctx=64, use_graph=use_graph)
+@pytest.mark.parametrize("use_graph,att_split", [(True, 0), (False, 0), (True, 1)])
+def test_small_model_words_and_records(sm, py_small_dir, py_small_oracle, pgolden, use_graph, att_split):
+    """att_split 1: every step's attention spread over chunks of positions (the turns and exact power there)"""
+    m = sm.Machine(py_small_dir, max_ctx=64, use_graph=use_graph, att_split=att_split)
     assert m.kind == "pythia"
     for case in small_cases(pgolden):
         last = case["records"]["last"]
@@ -104,9 +105,11 @@ def test_kv_cache_matches_oracle(sm, py_small_dir, py_small_oracle):
     m.close()
 
 
-def test_long_context_against_oracle(sm, py_small_dir, py_small_oracle):
-    """a 300-word prompt and 24 words: turns at positions past 256, context 324"""
-    m = sm.Machine(py_small_dir, max_ctx=400)
+@pytest.mark.parametrize("att_split", [0, -1, 310])
+def test_long_context_against_oracle(sm, py_small_dir, py_small_oracle, att_split):
+    """a 300-word prompt and 24 words: turns at positions past 256, context 324; the attention spread over chunks
+    of positions (the default), one block a head, and switching inside the decode steps"""
+    m = sm.Machine(py_small_dir, max_ctx=400, att_split=att_split)
     prompt = sm.prompt_ids(61, 300, 1000)
     assert m.stream(prompt, 24) == py_small_oracle.generate(prompt, 24, 400)
     m.close()

@@ -2,10 +2,13 @@
 bit-exact against the oracle on seeded random inputs and on the edge values each stage has."""
 from __future__ import annotations
 
+import json
+import os
+
 import numpy as np
 import pytest
 
-from conftest import h64, synth_qkv
+from conftest import REPO, h64, synth_qkv
 
 pytestmark = pytest.mark.gpu
 
@@ -168,8 +171,12 @@ def test_plate_product(sm, nin, nout, tc):
     plate.close()
 
 
-def _attend_all(sm, dtabs, QKV, ctx):
-    """run the device attention position by position over QKV rows (the cache fills as it goes)"""
+ATTEND = ["attend", "attend_split"]       # one block a head; spread over chunks of 64 positions
+
+
+def _attend_all(sm, dtabs, QKV, ctx, fn="attend"):
+    """run the device attention (stage entry point `fn`) position by position over QKV rows (the cache fills as it
+    goes)"""
     P = len(QKV)
     k16 = torch.zeros((ctx, 768), dtype=torch.int16, device="cuda")
     km = torch.zeros((ctx, 12), dtype=torch.int64, device="cuda")
@@ -177,26 +184,30 @@ def _attend_all(sm, dtabs, QKV, ctx):
     v = torch.zeros((ctx, 768), dtype=torch.int32, device="cuda")
     dq = dev(QKV)
     out = torch.zeros((P, 768), dtype=torch.int64, device="cuda")
+    f = getattr(sm.stages, fn)
     for p in range(P):
-        sm.stages.attend(dtabs, dq[p].data_ptr(), k16.data_ptr(), km.data_ptr(), ek.data_ptr(), v.data_ptr(), p, ctx,
-                         out[p].data_ptr())
+        f(dtabs, dq[p].data_ptr(), k16.data_ptr(), km.data_ptr(), ek.data_ptr(), v.data_ptr(), p, ctx, out[p].data_ptr())
     return host(out)
 
 
-def test_attention_golden(sm, dtabs, golden):
-    """the attention workload's shapes (T = 128, 512, 1024): every row against base2.py's own attention (golden vectors)"""
+@pytest.mark.parametrize("fn", ATTEND)
+def test_attention_golden(sm, dtabs, golden, fn):
+    """the attention workload's shapes (T = 128, 512, 1024): every row against base2.py's own attention (golden
+    vectors), through the one-block kernel and through the kernels spread over chunks of positions"""
     for case in golden["attention"]:
         Q = synth_qkv(case["seed"], case["P"], case["std"])
-        A = _attend_all(sm, dtabs, Q, 1024)
+        A = _attend_all(sm, dtabs, Q, 1024, fn)
         rows = [h64(r)[:16] for r in A]
         bad = [i for i, (a, b) in enumerate(zip(rows, case["row_sha16"])) if a != b]
         assert not bad, f"P={case['P']}: first differing row {bad[:5]}"
         assert h64(A) == case["out_sha256"]
 
 
-def test_attention_extreme_keys(sm, dtabs, small_oracle):
+@pytest.mark.parametrize("fn", ATTEND)
+def test_attention_extreme_keys(sm, dtabs, small_oracle, fn):
     """keys at the ends of the 16-bit range, +32768 (held as 32767 with its mask bit) and -32768, in the
-    short path (p < 64), the general one and the long-context ring (p >= 128), against the oracle"""
+    short path (p < 64), the general one and the long-context ring (p >= 128), against the oracle; spread over
+    chunks: one to four chunks, the new position first, inside and last in its chunk"""
     rng = np.random.default_rng(21)
     P = 200
     Q = np.round(rng.standard_normal((P, 2304)) * 0.5 * 65536).astype(np.int64)
@@ -214,15 +225,35 @@ def test_attention_extreme_keys(sm, dtabs, small_oracle):
                 q[(p + h) % 64] = 2 ** 21 - 1
                 q[(p + 3 * h + 1) % 64] = 1 - 2 ** 21
     want = small_oracle.attention(Q)
-    got = _attend_all(sm, dtabs, Q, 256)
+    got = _attend_all(sm, dtabs, Q, 256, fn)
     bad = [i for i in range(P) if not np.array_equal(got[i], want[i])]
     assert not bad, f"first differing positions {bad[:5]}"
 
 
-def test_attention_overflow_flag(sm, dtabs):
+@pytest.mark.parametrize("fn", ATTEND)
+def test_attention_overflow_flag(sm, dtabs, fn):
     """a value past 32 bits cannot enter the int32 V cache: the call reports SM_E_OVERFLOW"""
     Q = np.zeros((1, 2304), np.int64)
     Q[0, 1536] = 2 ** 33
     with pytest.raises(sm.SmError) as ei:
-        _attend_all(sm, dtabs, Q, 16)
+        _attend_all(sm, dtabs, Q, 16, fn)
     assert ei.value.code == -6
+
+
+@pytest.mark.parametrize("fn", ATTEND)
+def test_attention_workload_caches(sm, dtabs, small_oracle, fn):
+    """the attention microbenchmark's own inputs (uniform int16 caches at T = 128, 512, 1024, bench.attention_workload):
+    both kernels' outputs against the oracle on the same caches and against the committed fixture bench gates on"""
+    import hashlib
+    import bench
+    want = {c["T"]: c for c in json.load(open(os.path.join(REPO, "tests", "golden", "attention_cache.json")))["cases"]}
+    f = getattr(sm.stages, fn)
+    for T, k16, ek, v, qkv in bench.attention_workload():
+        dk, de, dv = dev(k16), dev(ek), dev(v)
+        km = torch.zeros((12, T), dtype=torch.int64, device="cuda")
+        dq = dev(qkv)
+        o = torch.zeros(768, dtype=torch.int64, device="cuda")
+        f(dtabs, dq.data_ptr(), dk.data_ptr(), km.data_ptr(), de.data_ptr(), dv.data_ptr(), T - 1, T, o.data_ptr())
+        got = host(o)
+        assert np.array_equal(got, small_oracle.attend_cached(qkv, k16, ek, v, T - 1)), T
+        assert hashlib.sha256(got.tobytes()).hexdigest() == want[T]["out_sha256"], T

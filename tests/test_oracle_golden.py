@@ -116,3 +116,26 @@ def test_kv_step_equals_full_recompute(small_oracle, sm):
         for _ in range(5):
             full.append(small_oracle.forward(prompt + full))
         assert kv == full
+
+
+def test_attention_over_a_cache(full_oracle, golden, sm):
+    """the oracle's attention of the newest row over a given cache (the device attention's contract): a cache
+    filled from the golden QKV rows (each head's k through to16, v raw) gives base2.py's own rows at several
+    positions, and a cache with one value changed does not (it is read)"""
+    import oracle
+    st = oracle.Stages(sm.tables())
+    case = golden["attention"][0]
+    Q = synth_qkv(case["seed"], case["P"], case["std"])
+    P = len(Q)
+    k16 = np.zeros((12, P, 64), np.int64)
+    ek = np.zeros((12, P), np.int64)
+    v = np.zeros((12, P, 64), np.int64)
+    for h in range(12):
+        x16, ex = st.to16(Q[:, 768 + 64 * h: 768 + 64 * h + 64])
+        k16[h], ek[h] = x16, ex
+        v[h] = Q[:, 1536 + 64 * h: 1536 + 64 * h + 64]
+    for p in (0, 1, 63, 64, P - 1):
+        got = full_oracle.attend_cached(Q[p], k16, ek, v, p)
+        assert h64(got)[:16] == case["row_sha16"][p], p
+    v[3, 10, 5] += 1 << 14
+    assert h64(full_oracle.attend_cached(Q[P - 1], k16, ek, v, P - 1))[:16] != case["row_sha16"][P - 1]
