@@ -372,13 +372,16 @@ def batched_leg(sm, lay):
     return out
 
 
-def pythia_leg(sm):
+def pythia_leg(sm, keep: dict | None = None):
+    """keep: receives the converted model (the CPU baseline's oracle reads it)"""
     t0 = time.time()
     sd, cfg = sm.pythia.random_pythia(seed=5)
     npz = sm.pythia.convert_pythia(sd, cfg)
     del sd
     lay = tempfile.mkdtemp(prefix="sm_bench_py_")
     sm.pythia.pythia_layout(npz, lay)
+    if keep is not None:
+        keep["npz"] = npz
     del npz
     log(f"pythia: model converted and laid out in {time.time() - t0:.1f}s")
     prompts = [sm.prompt_ids(5 + b, P_PROMPT, PVOCAB) for b in range(P_STREAMS)]
@@ -612,6 +615,95 @@ def cpu_baseline(npz, prompt, want, runs: int = 5, words: int = 5):
                           "sample": f"words 2..{WORDS} of the same sequence (context 9..{8 + WORDS - 1}), median of {runs}"}}
 
 
+def _kv_rate(session, seq, start: int, n: int, want, runs: int = 3) -> float:
+    """tokens/s of a KV-cached oracle session over positions start .. start + runs n - 1 of seq (the earlier positions
+    fed untimed once): the median over `runs` consecutive chunks of n steps; the words it gives checked against
+    want"""
+    s = session()
+    for i in range(start):
+        s.step(seq[i], want_head=False)
+    rates, got = [], []
+    for r in range(runs):
+        t0 = time.perf_counter()
+        got += [s.step(seq[start + r * n + i]) for i in range(n)]
+        rates.append(n / (time.perf_counter() - t0))
+    if got != want[:len(got)] or len(got) != len(want):
+        raise RuntimeError("cpu baseline: the KV-cached oracle's words differ from the reference's")
+    return float(np.median(rates))
+
+
+def cpu_baseline_b64(npz, words: int = 2):
+    """the 64-stream workload's CPU path on a labelled sample: stream 0 at the workload's mean context (96 positions:
+    its 32-token prompt and first 64 words, the reference's own words from tests/golden/long_golden.json).
+    Full recompute as base2.py:123 does (numpy restatement, all BLAS threads): one warm-up word at context 96, then
+    the next `words` words timed; every stream's every word costs one such forward, so the workload's tokens/s on
+    these cores is the per-word rate at the mean context (the products grow linearly with the context, so the mean
+    context's word stands for the average).  The KV-cached C oracle at the same context beside it (all cores and
+    one thread)."""
+    sys.path.insert(0, REPO)
+    import oracle
+    from oracle.base2_np import Base2Numpy
+    c = fixture_cases("long_golden.json")["c4_stream0_p32_w128"]
+    seq = c["prompt"] + c["words"]
+    mean = B_PROMPT + B_WORDS // 2                    # 96
+    nb = Base2Numpy(npz)
+    if nb.forward(seq[:mean]) != seq[mean]:
+        raise RuntimeError("cpu baseline (64 streams): the full recompute's word differs from the reference's")
+    t0 = time.perf_counter()
+    for k in range(1, words + 1):
+        if nb.forward(seq[:mean + k]) != seq[mean + k]:
+            raise RuntimeError("cpu baseline (64 streams): the full recompute's words differ from the reference's")
+    full = words / (time.perf_counter() - t0)
+    orc = oracle.Oracle(npz)
+    threads = oracle.set_threads(0)
+    start = mean - 1                                  # the step at position 95 gives word 64 (context 96)
+    want = c["words"][start - B_PROMPT + 1:start - B_PROMPT + 25]
+    kv_all = _kv_rate(lambda: orc.session(B_PROMPT + B_WORDS), seq, start, 8, want)
+    oracle.set_threads(1)
+    kv_one = _kv_rate(lambda: orc.session(B_PROMPT + B_WORDS), seq, start, 8, want)
+    oracle.set_threads(0)
+    info = cpu_info()
+    return {"value": round(full, 4), "unit": "tokens/s", "cores": info.get("blas_threads", info["affinity"]),
+            "kind": "port",
+            "sample": f"stream 0 of the 64-stream workload, words {mean - B_PROMPT + 2}..{mean - B_PROMPT + 1 + words} "
+                      f"(context {mean + 1}..{mean + words}) after one warm-up word at context {mean}, full recompute "
+                      f"per word as base2.py:123 does (numpy float64-BLAS products, the top-down race loop); the "
+                      f"workload (64 x {B_WORDS} words) extrapolated at this per-word rate",
+            "workload_s_extrapolated": round(B_STREAMS * B_WORDS / full, 1), **info,
+            "kv_cached": {"value": round(kv_all, 2), "one_thread": round(kv_one, 2), "threads": threads,
+                          "kind": "port (the C oracle's KV-cached step, OpenMP)",
+                          "sample": f"stream 0, 24 steps at positions {start}..{start + 23} (contexts "
+                                    f"{mean}..{mean + 23}), median of three chunks of 8"}}
+
+
+def cpu_baseline_pythia(npz):
+    """the Pythia 32-stream workload's CPU path on a labelled sample: the KV-cached C restatement of
+    pythia_base2.py (foundation0/pythia_base2.py:151-160) on stream 0 at the workload's mean context (192 positions:
+    its 64-token prompt and first 128 words, the reference's own words), 24 steps, all cores and one thread.  The
+    reference's own path recomputes every position for every word (forward(ids + own), :170-175); no
+    full-recompute restatement is timed here, so this KV-cached figure is the stronger CPU number."""
+    sys.path.insert(0, REPO)
+    import oracle
+    from oracle.pythia import PythiaOracle
+    c = fixture_cases("long_golden.json")["py_c5_stream0_p64_w256"]
+    seq = c["prompt"] + c["words"]
+    mean = P_PROMPT + P_WORDS // 2                    # 192
+    start = mean - 1
+    want = c["words"][start - P_PROMPT + 1:start - P_PROMPT + 25]
+    orc = PythiaOracle(npz)
+    threads = oracle.set_threads(0)
+    kv_all = _kv_rate(lambda: orc.session(P_PROMPT + P_WORDS), seq, start, 8, want)
+    oracle.set_threads(1)
+    kv_one = _kv_rate(lambda: orc.session(P_PROMPT + P_WORDS), seq, start, 8, want)
+    oracle.set_threads(0)
+    info = cpu_info()
+    return {"value": round(kv_all, 2), "unit": "tokens/s", "cores": threads, "kind": "port",
+            "sample": f"stream 0 of the Pythia workload, 24 KV-cached steps at positions {start}..{start + 23} "
+                      f"(contexts {mean}..{mean + 23}), the C oracle (OpenMP), median of three chunks of 8; the workload "
+                      f"(32 x {P_WORDS} words) extrapolated at this per-word rate",
+            "one_thread": round(kv_one, 2), "workload_s_extrapolated": round(P_STREAMS * P_WORDS / kv_all, 1), **info}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -713,12 +805,19 @@ def main():
     batched = None if args.no_batched else batched_leg(sm, lay)
     if batched:
         log(f"batched: {batched['value']} tokens/s, {batched['ms_per_step']} ms/step")
-    pyleg = None if args.no_pythia else pythia_leg(sm)
+    pykeep = {}
+    pyleg = None if args.no_pythia else pythia_leg(sm, pykeep)
     if pyleg:
         log(f"pythia: {pyleg['value']} tokens/s, {pyleg['ms_per_step']} ms/step")
     gemv = None if args.no_micro else gemv_leg(sm)
     att = None if args.no_micro else attention_leg(sm)
     cpu = None if args.no_cpu else cpu_baseline(npz, prompt, want)
+    if batched and not args.no_cpu:
+        batched["cpu_baseline"] = cpu_baseline_b64(npz)
+        log(f"cpu baseline, 64-stream workload: {batched['cpu_baseline']['value']} tokens/s full recompute")
+    if pyleg and not args.no_cpu and "npz" in pykeep:
+        pyleg["cpu_baseline"] = cpu_baseline_pythia(pykeep.pop("npz"))
+        log(f"cpu baseline, Pythia workload: {pyleg['cpu_baseline']['value']} tokens/s KV-cached")
     out = {
         "metric": METRIC, "value": round(b1["tok_s"], 2), "unit": "tokens/s", "n_gpus": 1, "steps": b1["steps"],
         "warmup": args.warmup, "ms_per_step": round(b1["ms"], 4), "higher_is_better": True, "scaling": "weak",
