@@ -73,11 +73,12 @@ def test_verify_tables_refuses_a_changed_table(sm, small_dir, small_npz, tmp_pat
     m.close()
 
 
-@pytest.mark.parametrize("streams", [1, 3])
-def test_changed_arrival_table_is_read_as_given(sm, small_npz, tmp_path, streams):
+@pytest.mark.parametrize("streams,att_split", [(1, 0), (3, 0), (1, 1)])
+def test_changed_arrival_table_is_read_as_given(sm, small_npz, tmp_path, streams, att_split):
     """with the reference's tables the machine computes each arrival from its formula (the create-time check found
     them equal entry for entry); a layout whose arrival table differs is read as given: the attention rows of the
-    recorded position, at batch 1 and with three streams, equal the oracle's run with the same table"""
+    recorded position, at batch 1 (one block a head, and spread over chunks of positions) and with three streams,
+    equal the oracle's run with the same table"""
     import oracle
     npz = dict(small_npz)
     arr = npz["arrival"].copy()
@@ -89,7 +90,7 @@ def test_changed_arrival_table_is_read_as_given(sm, small_npz, tmp_path, streams
     oracle.Oracle(npz).forward(prompt, rec=want)          # the last position's intermediates
     oracle.Oracle(small_npz).forward(prompt, rec=base)
     assert not np.array_equal(want["att"], base["att"])  # the change reaches the attention
-    m = sm.Machine(d, max_ctx=64, max_streams=streams)
+    m = sm.Machine(d, max_ctx=64, max_streams=streams, att_split=att_split)
     assert not m.tables_verified
     m.reset()
     m.record_at(len(prompt) - 1)
