@@ -527,7 +527,14 @@ def floor_leg():
     if r.returncode != 0:
         log(f"floor probe failed ({r.returncode}): {r.stderr.strip()[-300:]}")
         return None
-    return json.loads(r.stdout.strip().splitlines()[-1])
+    out = json.loads(r.stdout.strip().splitlines()[-1])
+    # the same step as one persistent kernel (sequence-tagged rows handed over in memory, plates requested ahead)
+    r = subprocess.run([exe, "persist"], capture_output=True, text=True, timeout=120)
+    if r.returncode == 0:
+        out["persistent"] = json.loads(r.stdout.strip().splitlines()[-1])
+    else:
+        log(f"persistent probe failed ({r.returncode}): {r.stderr.strip()[-300:]}")
+    return out
 
 
 def cpu_info():
@@ -852,7 +859,9 @@ def main():
             "note": "the step's 62 dependent launches with the machine's grids, replayed from graphs of 15 steps: "
                     "empty_us with empty kernels, bytes_us with every kernel reading its row and its plate share "
                     "(the whole int16 word table for the head) and writing its outputs, no arithmetic "
-                    "(streaming-machine_amd/floor_probe)",
+                    "(streaming-machine_amd/floor_probe); persistent: the same bytes as one cooperative kernel of "
+                    "256 blocks, each phase's row handed over in memory as sequence-tagged words (61 hand-offs a "
+                    "step, every plate share requested before its wait, every wait bounded)",
             "b64": None if "b64" not in floor else {
                 **floor["b64"],
                 **({"step_us": round(1000.0 * batched["ms_per_step"], 2),
