@@ -854,7 +854,7 @@ def main():
                         "the high-byte plane of every word, exact bounds, the low bytes of the words that can still "
                         "win; words gated on base2.py's like the main line"}},
         "floor": None if floor is None else {
-            **{k: v for k, v in floor.items() if k != "b64"},
+            **{k: v for k, v in floor.items() if k not in ("b64", "pythia32")},
             "step_us": round(1000.0 * b1["ms"], 2), "step_over_bytes_floor": round(1000.0 * b1["ms"] / floor["bytes_us"], 3),
             "note": "the step's 62 dependent launches with the machine's grids, replayed from graphs of 15 steps: "
                     "empty_us with empty kernels, bytes_us with every kernel reading its row and its plate share "
@@ -868,7 +868,15 @@ def main():
                     "step_over_bytes_floor": round(1000.0 * batched["ms_per_step"] / floor["b64"]["bytes_us"], 3)} if batched else {}),
                 "note": "the 64-stream step's 86 launches with the machine's grids, graphs of 16 steps: each bank block "
                         "reading its light planes or 32-bit rows and its plate share, each attention block 96 positions "
-                        "of its cache rows, the head its plate, no arithmetic"}},
+                        "of its cache rows, the head its plate, no arithmetic"},
+            "pythia32": None if "pythia32" not in floor else {
+                **floor["pythia32"],
+                **({"step_us": round(1000.0 * pyleg["ms_per_step"], 2),
+                    "step_over_bytes_floor": round(1000.0 * pyleg["ms_per_step"] / floor["pythia32"]["bytes_us"], 3)}
+                   if pyleg else {}),
+                "note": "the Pythia 32-stream step's 51 launches with the machine's grids, graphs of 16 steps: the "
+                        "paired banks and the paired attention and mproj partials reading their shares (the attention "
+                        "192 positions of cache rows a block), proj, the row kernels, the head, no arithmetic"}},
         "batched": batched,
         "pythia": pyleg,
         "gemv": gemv,

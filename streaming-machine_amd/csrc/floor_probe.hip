@@ -13,6 +13,9 @@
 // partials, light], the head, the race) with the machine's grids, graphs of 16 steps, the same two forms; in
 // "bytes" each bank block reads its row tile's light planes or int32 rows and its plate share, each attention
 // block 96 positions of its cache rows (38 KB), each light block its row (and the partials), the head its plate.
+// The Pythia machine at 32 streams ("pythia32"): its 51 launches a step (the words entering, 12 x [fc | qkv, the
+// attention | mproj partials, proj, the row kernel], the head, the race) with the machine's grids, graphs of 16 steps,
+// the same two forms; the attention blocks read 192 positions of cache rows (the workload's mean context).
 // Prints one JSON line with both.  With the argument "persist": batch 1 as one persistent kernel (below), its step
 // time and, on stderr, block 0's hand-off times in the last step.
 #include <hip/hip_runtime.h>
@@ -147,14 +150,14 @@ __global__ __launch_bounds__(NT) void k_floor_move(const v4i* A, size_t ra, size
     const size_t blk = (size_t)blockIdx.y * gridDim.x + blockIdx.x;
     for (int i = tid; i < NOUT; i += NT) out[blk * NOUT + i] = s + i;
 }
-// the head: each block its waves' light planes, then its share of the plate
-template <bool EMPTY>
+// the head: each block its waves' light planes (NP v4 a thread: 24 for four row tiles), then its share of the plate
+template <bool EMPTY, int NP = 24>
 __global__ __launch_bounds__(256) void k_floor_head64(const v4i* planes, const v4i* W, size_t nW, i64* part) {
     if (EMPTY) return;
     const int tid = threadIdx.x;
     int s = 0;
 #pragma unroll
-    for (int i = 0; i < 24; i++) { const v4i v = planes[tid + 256 * i]; s += v.x ^ v.y; }
+    for (int i = 0; i < NP; i++) { const v4i v = planes[tid + 256 * i]; s += v.x ^ v.y; }
     for (size_t i = (size_t)blockIdx.x * 256 + tid; i < nW; i += (size_t)gridDim.x * 256) { const v4i v = W[i]; s += v.x ^ v.w; }
     if (tid < 64) part[(size_t)blockIdx.x * 64 + tid] = s;
 }
@@ -499,6 +502,90 @@ static int run_persist(double& us, int& late) {
     return 0;
 }
 
+// ---- the Pythia machine at 32 streams ----
+// a paired launch: blocks [0, na) read NA1 int4 a thread of A (the attention: its (head, stream)'s cache rows), the
+// rest NA2 of B and NB2 of C (mproj's partials: the tile's hidden rows and three column tiles)
+template <int NA1, int NA2, int NB2, bool EMPTY>
+__global__ __launch_bounds__(256) void k_floor_pair(const v4i* A, size_t ra, int na, const v4i* B, const v4i* C, size_t rc, i64* out) {
+    if (EMPTY) return;
+    const int tid = threadIdx.x, b = blockIdx.x;
+    int s = 0;
+    if (b < na) {
+        const v4i* a = A + (size_t)b * ra + tid;
+#pragma unroll
+        for (int i = 0; i < NA1; i++) { const v4i v = a[256 * i]; s += v.x ^ v.w; }
+    } else {
+        const v4i* x = B + tid;
+        const v4i* c = C + (size_t)((b - na) % 64) * rc + tid;      // 64 column groups, each read by both row tiles
+#pragma unroll
+        for (int i = 0; i < NA2; i++) { const v4i v = x[256 * i]; s += v.x ^ v.w; }
+#pragma unroll
+        for (int i = 0; i < NB2; i++) { const v4i v = c[256 * i]; s += v.x ^ v.w; }
+    }
+    for (int i = tid; i < 64; i += 256) out[(size_t)b * 64 + i] = s + i;
+}
+
+template <bool EMPTY>
+static int runpy(double& us) {
+    const size_t qkvB = 768 * 2304 * 2, projB = 768 * 768 * 2, fcB = 768 * 3072 * 2, mpB = 3072 * 768 * 2;
+    const size_t headB = (size_t)768 * 50304 * 2, layerB = qkvB + projB + fcB + mpB;
+    const size_t kvL = (size_t)32 * 12 * 320 * 396;          // a layer's cache: 32 streams x 12 heads x 320 positions
+    const size_t planesB = 2 * 36864 * 2, rowsB = (size_t)32 * 3072 * 8, NOUTV = 1 << 19;
+    const int STEPS = 16, REPS = 10;
+    char *plates = nullptr, *planes, *rows, *kv;
+    i64* out;
+    CHK(hipMalloc(&plates, 12 * layerB + headB)); CHK(hipMalloc(&planes, planesB)); CHK(hipMalloc(&rows, rowsB));
+    CHK(hipMalloc(&kv, 12 * kvL)); CHK(hipMalloc(&out, NOUTV * 8));
+    CHK(hipMemset(plates, 1, 12 * layerB + headB)); CHK(hipMemset(planes, 1, planesB)); CHK(hipMemset(rows, 1, rowsB));
+    CHK(hipMemset(kv, 1, 12 * kvL)); CHK(hipMemset(out, 0, NOUTV * 8));
+    CHK(hipDeviceSynchronize());
+    hipStream_t st;
+    CHK(hipStreamCreateWithFlags(&st, hipStreamNonBlocking));
+    const v4i *P = (const v4i*)planes, *Rw = (const v4i*)rows;
+    hipGraph_t g;
+    hipGraphExec_t ge;
+    CHK(hipStreamBeginCapture(st, hipStreamCaptureModeGlobal));
+    for (int s = 0; s < STEPS; s++) {
+        const char* pl = plates;
+        // the words enter: a row a block
+        k_floor_move<192, 2, 0, 288, EMPTY, 8><<<dim3(1, 32), 192, 0, st>>>(Rw, 384, 0, Rw, 0, out);
+        for (int l = 0; l < 12; l++) {
+            const v4i* wq = (const v4i*)pl; pl += qkvB + projB;           // qkv, proj, fc contiguous
+            pl += fcB;
+            const v4i* wm = (const v4i*)pl; pl += mpB;
+            const v4i* kvl = (const v4i*)(kv + l * kvL);
+            // fc | qkv: 336 column tiles x 2 row tiles, each its light planes (36 KB) and its plate tile (24 KB)
+            k_floor_move<256, 9, 6, 256, EMPTY, 11><<<dim3(336, 2), 256, 0, st>>>(P, 2304, 0, wq, 1536, out);
+            // the attention (384 blocks, 192 positions of cache rows: 76 KB) | mproj partials (128 blocks: the tile's
+            // hidden rows at 32 bits, 48 KB, and three column tiles, 72 KB)
+            k_floor_pair<19, 12, 18, EMPTY><<<512, 256, 0, st>>>(kvl, 4752, 384, Rw, wm, 4608, out);
+            // proj: the attention rows at 32 bits (48 KB), its plate tile (24 KB), mproj's partials for its tile (8 KB)
+            k_floor_move<256, 14, 6, 256, EMPTY, 12><<<dim3(48, 2), 256, 0, st>>>(Rw, 3072, 0, wq + (qkvB / 16), 1536, out);
+            // the row kernel: the stream row, both gauges' planes
+            k_floor_move<192, 2, 0, 576, EMPTY, 13><<<dim3(1, 32), 192, 0, st>>>(Rw, 384, 0, Rw, 0, out);
+        }
+        k_floor_head64<EMPTY, 12><<<512, 256, 0, st>>>(P, (const v4i*)pl, headB / 16, out);
+        k_floor_race64<EMPTY><<<32, 256, 0, st>>>(out, out + (1 << 18));
+    }
+    CHK(hipStreamEndCapture(st, &g));
+    CHK(hipGraphInstantiate(&ge, g, nullptr, nullptr, 0));
+    hipEvent_t e0, e1;
+    CHK(hipEventCreate(&e0)); CHK(hipEventCreate(&e1));
+    for (int i = 0; i < 2; i++) CHK(hipGraphLaunch(ge, st));
+    CHK(hipStreamSynchronize(st));
+    CHK(hipEventRecord(e0, st));
+    for (int i = 0; i < REPS; i++) CHK(hipGraphLaunch(ge, st));
+    CHK(hipEventRecord(e1, st));
+    CHK(hipStreamSynchronize(st));
+    float ms = 0.0f;
+    CHK(hipEventElapsedTime(&ms, e0, e1));
+    us = ms * 1000.0 / (REPS * STEPS);
+    CHK(hipEventDestroy(e0)); CHK(hipEventDestroy(e1));
+    CHK(hipGraphExecDestroy(ge)); CHK(hipGraphDestroy(g)); CHK(hipStreamDestroy(st));
+    for (void* q : {(void*)plates, (void*)planes, (void*)rows, (void*)kv, (void*)out}) CHK(hipFree(q));
+    return 0;
+}
+
 int main(int argc, char** argv) {
     if (argc > 1 && std::string(argv[1]) == "persist") {
         double us = 0;
@@ -507,7 +594,7 @@ int main(int argc, char** argv) {
         printf("{\"persist_us\": %.2f, \"late\": %d, \"handoffs\": 61, \"graph_steps\": 15}\n", us, late);
         return 0;
     }
-    double empty = 1e30, bytes = 1e30, e64 = 1e30, b64 = 1e30;
+    double empty = 1e30, bytes = 1e30, e64 = 1e30, b64 = 1e30, epy = 1e30, bpy = 1e30;
     for (int r = 0; r < 3; r++) {             // the best of three measurements of each form
         double e, b;
         if (run<true>(e) || run<false>(b)) return 1;
@@ -516,9 +603,13 @@ int main(int argc, char** argv) {
         if (run64<true>(e) || run64<false>(b)) return 1;
         e64 = e < e64 ? e : e64;
         b64 = b < b64 ? b : b64;
+        if (runpy<true>(e) || runpy<false>(b)) return 1;
+        epy = e < epy ? e : epy;
+        bpy = b < bpy ? b : bpy;
     }
     printf("{\"launches\": 62, \"empty_us\": %.2f, \"bytes_us\": %.2f, \"ctx\": 16, \"graph_steps\": 15, "
-           "\"b64\": {\"launches\": 86, \"empty_us\": %.2f, \"bytes_us\": %.2f, \"ctx\": 96, \"graph_steps\": 16}}\n",
-           empty, bytes, e64, b64);
+           "\"b64\": {\"launches\": 86, \"empty_us\": %.2f, \"bytes_us\": %.2f, \"ctx\": 96, \"graph_steps\": 16}, "
+           "\"pythia32\": {\"launches\": 51, \"empty_us\": %.2f, \"bytes_us\": %.2f, \"ctx\": 192, \"graph_steps\": 16}}\n",
+           empty, bytes, e64, b64, epy, bpy);
     return 0;
 }
