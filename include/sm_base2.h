@@ -74,6 +74,11 @@ typedef struct {
                               scores and maxima, then arrivals against the head's maximum and the value sums added
                               exactly, then the divisor: three launches); steps before it run one block a head.
                               0: from position 160; -1: never.  The same numbers either way (base2.py:85-100) */
+    int32_t v64;           /* the value cache (base2.py's attention weighs each raw int64 value): every value is kept
+                              whole beside its low 32 bits, and a head holding a value past 32 bits reads its values
+                              whole.  0: the others read the 32-bit copy (half the bytes); 1: every head reads its
+                              values whole from the start.  The same numbers either way.  Not with the float arrival,
+                              whose cache holds int32 values (a value past 32 bits is SM_E_OVERFLOW there) */
 } sm_config;
 
 enum { SM_FLOAT_GAUGE = 1, SM_FLOAT_EDGE = 2, SM_FLOAT_ARRIVAL = 4, SM_FLOAT_TURN = 8 };
@@ -105,7 +110,7 @@ int sm_record_at(sm_machine* m, int32_t pos);
 enum {
     SM_READ_K16 = 1,      /* int32 [768]  per-head 16-bit keys at (layer, stream, pos) */
     SM_READ_EK = 2,       /* int32 [12]   their water levels */
-    SM_READ_V = 3,        /* int32 [768]  values */
+    SM_READ_V = 3,        /* int32 [768]  values (their low 32 bits; SM_READ_V64: whole) */
     SM_READ_RESID = 4,    /* [768] the stream R of `stream` after its last position */
     SM_READ_SEQ = 5,      /* int32 [max_ctx + 1] words per position of `stream` */
     SM_READ_REC_X16 = 10, /* [12][4][3072] light entering each bank (qkv, proj, fc, mproj) */
@@ -123,8 +128,9 @@ enum {
     SM_READ_REC_GAUGE = 21, /* [12][2][768] the gauge rows (ln1, ln2) of each layer (:100-110) */
     SM_READ_REC_FCPRE = 22, /* [12][3072] fc's plain output before the edge */
     SM_READ_REC_HGAUGE = 23,/* [768] the head's gauge row (lnf) */
-    SM_READ_TOP = 24        /* int64 [1 + 3 x 1024] the collapsing top read's last step: the survivor count, then
+    SM_READ_TOP = 24,       /* int64 [1 + 3 x 1024] the collapsing top read's last step: the survivor count, then
                                (word, exact pile, score) of the first 1024 survivors */
+    SM_READ_V64 = 25        /* int64 [768]  the values at (layer, stream, pos), whole */
 };
 /* Copies one device array to host memory dst (bytes must match).  Replaces reading MTLBuffer contents
  * (base2_stream.swift:282-286) for per-intermediate parity. */

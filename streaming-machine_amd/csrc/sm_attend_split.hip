@@ -83,8 +83,7 @@ __global__ __launch_bounds__(256) void k_att_scores(AttArgs a) {
             }
         }
     } else if (wave == 2 && mine) {
-        if (xnew < (i64)INT32_MIN || xnew > (i64)INT32_MAX) atomicOr(a.err, SM_ERR_V32);
-        V[(size_t)p * 64 + lane] = (int)xnew;
+        v_store(a, (size_t)h, p, lane, xnew);
     }
     __syncthreads();
     // the chunk's scores (base2.py:94 / pythia_base2.py:135)
@@ -140,6 +139,7 @@ __global__ __launch_bounds__(256) void k_att_mix(AttArgs a) {
     v4i vp[4];
 #pragma unroll
     for (int i = 0; i < 4; i++) vp[i] = buf_load4(rv, (unsigned)(s0 + g + 16 * i) * 256u + d4 * 16);
+    const int vbg = a.vbig ? a.vbig[h] : 0;                 // the head holds a value past 32 bits (read whole below)
     // the clock starts at the head's maximum (base2.py:96)
     const i64 M = block_reduce<OpMax, 4>(tid < nc ? cmv : INT64_MIN, red, OpMax(), tid);
     // arrivals (base2.py:96-97), wave 0 a position each, and their sum
@@ -160,9 +160,24 @@ __global__ __launch_bounds__(256) void k_att_mix(AttArgs a) {
         n0 += (i64)w * x.x; n1 += (i64)w * x.y; n2 += (i64)w * x.z; n3 += (i64)w * x.w;
         if (MODEL == 1 && w) vmax = max(vmax, max(max(abs(x.x), abs(x.y)), max(abs(x.z), abs(x.w))));
     }
+    i64 vm64 = vmax;
+    if (a.V64 && vbg) {                                     // (block-uniform) the head's values whole
+        const i64* v64 = a.V64 + hb * 64 + 4 * d4;
+        n0 = n1 = n2 = n3 = 0;
+        vm64 = 0;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int sv = s0 + g + 16 * i;
+            if (sv > p) break;
+            const i64 w = arr_s[g + 16 * i];
+            const i64* x = v64 + (size_t)sv * 64;
+            n0 = wadd(n0, wmul(w, x[0])); n1 = wadd(n1, wmul(w, x[1])); n2 = wadd(n2, wmul(w, x[2])); n3 = wadd(n3, wmul(w, x[3]));
+            if (MODEL == 1 && w) vm64 = max(max(vm64, max(iabs64(x[0]), iabs64(x[1]))), max(iabs64(x[2]), iabs64(x[3])));
+        }
+    }
     numr[g][4 * d4] = n0; numr[g][4 * d4 + 1] = n1; numr[g][4 * d4 + 2] = n2; numr[g][4 * d4 + 3] = n3;
     i64 vm = 0;
-    if constexpr (MODEL == 1) vm = block_reduce<OpMax, 4>((i64)vmax, red, OpMax(), tid);   // (its barriers publish numr)
+    if constexpr (MODEL == 1) vm = block_reduce<OpMax, 4>(vm64, red, OpMax(), tid);   // (its barriers publish numr)
     else __syncthreads();
     if (wave == 0) {
         i64 tot = 0;

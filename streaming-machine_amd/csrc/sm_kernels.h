@@ -134,7 +134,10 @@ struct AttArgs {
     short* K16;         // [B][12][ctx][64] per-head 16-bit keys (values in [-32768, 32768]; +32768 held as 32767)
     i64* KM;            // [B][12][ctx]     bit d: dimension d of the key is +32768 (one more than K16 holds)
     int* EK;            // [B][12][ctx]     their water levels
-    int* V;             // [B][12][ctx][64] raw gauged values (checked to fit 32 bits)
+    int* V;             // [B][12][ctx][64] raw gauged values: their low 32 bits (every value that fits 32 bits)
+    i64* V64;           // [B][12][ctx][64] (when non-null) the same values whole (base2.py keeps int64 values)
+    int* vbig;          // [B][12] (with V64) nonzero: the (stream, head) holds a value past 32 bits, and the
+                        // attention reads that head's values from V64
     i64* out;           // [B][768]
     int* out32;         // [B][768] (when non-null): the same values' low 32 bits, for a consumer that reads a
                         // row's 32-bit copy wherever its OR words show that the row fits (k_gemm's SRC path)
@@ -143,7 +146,7 @@ struct AttArgs {
     const int* pos;     // position being written and read up to (inclusive)
     int ctx;
     Tables tb;
-    int* err;           // bit 0: a value left 32 bits; bit 1: a value the reference asserts on
+    int* err;           // bit 0: a value left 32 bits with no V64 to hold it; bit 1: a value the reference asserts on
     const int* rec_pos; i64* ratt;
     // the Pythia machine: turns on the first rot dims of q and k, the scores' half-log2(head size)
     const int* cosT; const int* sinT;   // [npos][rot / 2] at 2^-30

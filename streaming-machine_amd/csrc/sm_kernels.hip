@@ -839,6 +839,22 @@ SMD void key_store(short* krow, i64* km, int x16, int lane) {
     const u64 m = __ballot(x16 == 32768);
     if (lane == 0) *km = (i64)m;
 }
+// A value row into the cache (base2.py's attention weighs the raw int64 value): its low 32 bits into V, which holds
+// every value that fits 32 bits exactly; with V64, the whole value there as well, and a value past 32 bits marks its
+// (stream, head) (vbig), whose values the attention then reads whole.  Without V64 a value past 32 bits is an error
+// (SM_ERR_V32).  The whole wave stores one row, lane = dimension; hrow: the (stream, head) of the layer's [B][12].
+SMD void v_store(const AttArgs& a, size_t hrow, int p, int lane, i64 x) {
+    const size_t at = (hrow * a.ctx + p) * 64 + lane;
+    a.V[at] = (int)x;
+    const bool wide = x < (i64)INT32_MIN || x > (i64)INT32_MAX;
+    if (a.V64) {
+        a.V64[at] = x;
+        const bool any = __ballot(wide) != 0;
+        if (any && lane == 0) atomicOr(a.vbig + hrow, 1);
+    } else if (wide) {
+        atomicOr(a.err, SM_ERR_V32);
+    }
+}
 // q . k' by 16-bit dot products (the one-wave short path): q = 256 qh + ql with qh = q >> 8 in [-128, 128] and
 // ql = q & 255, both int16, so that over 64 dimensions sum qh k' stays below 2^28 and sum ql k' below 2^30 in
 // magnitude (|k'| <= 32768): two exact int32 sums, then 256 A + B in 64 bits.
@@ -933,6 +949,7 @@ SMD i64 attend_short(const AttArgs& a, int p, int h, int b, int* q_s, int* w_s, 
     for (int c = 0; c < 8; c++) krow[c] = buf_load4(rk, (unsigned)lane * 128 + 16 * c);
     const int ekl = buf_load1(re, (unsigned)lane * 4);
     const u64 kml = (u64)buf_load8(rm, (unsigned)lane * 8);
+    const int vbg = a.vbig ? a.vbig[(size_t)b * 12 + h] : 0;   // the head's values past 32 bits (read whole below)
     int vcol[64];
 #pragma unroll
     for (int s = 0; s < 64; s++) vcol[s] = buf_load1(rv, (unsigned)(s * 64 + lane) * 4);
@@ -954,8 +971,7 @@ SMD i64 attend_short(const AttArgs& a, int p, int h, int b, int* q_s, int* w_s, 
     if (store) {
         key_store(K16 + (size_t)p * 64, KM + p, k16, lane);
         if (lane == 0) EK[p] = (int)ekn;
-        if (vv < (i64)INT32_MIN || vv > (i64)INT32_MAX) atomicOr(a.err, SM_ERR_V32);
-        V[(size_t)p * 64 + lane] = (int)vv;
+        v_store(a, (size_t)b * 12 + h, p, lane, vv);
     }
     // scores (base2.py:94): lane s < p its cached row, lane p the new key
     q_s[lane] = q16;
@@ -1010,7 +1026,22 @@ SMD i64 attend_short(const AttArgs& a, int p, int h, int b, int* q_s, int* w_s, 
     const int wp = __builtin_amdgcn_readlane(w, p);
     num += (i64)wp * (int)vv;
     if (MODEL == 1 && wp) vmax = max(vmax, abs((int)vv));
-    if (MODEL == 1 && store && (double)vmax * (double)z >= 4611686018427387904.0) atomicOr(a.err, SM_ERR_RANGE);
+    double vmaxd = vmax;
+    if (a.V64 && (vbg || __ballot(vv < (i64)INT32_MIN || vv > (i64)INT32_MAX))) {
+        // (the whole wave) the head holds a value past 32 bits: its values whole from V64, the new one from vv
+        const i64* v64 = a.V64 + hb * 64 + lane;
+        i64 n = 0, vm = 0;
+        for (int s = 0; s < p; s++) {
+            const int ws = w_s[s];
+            const i64 x = v64[(size_t)s * 64];
+            n = wadd(n, wmul(ws, x));
+            if (MODEL == 1 && ws) vm = max(vm, iabs64(x));
+        }
+        num = wadd(n, wmul(wp, vv));
+        if (MODEL == 1 && wp) vm = max(vm, iabs64(vv));
+        vmaxd = (double)vm;
+    }
+    if (MODEL == 1 && store && vmaxd * (double)z >= 4611686018427387904.0) atomicOr(a.err, SM_ERR_RANGE);
     // over the total through its log (base2.py:99)
     i64 o;
     if (MODEL == 1) {
@@ -1051,6 +1082,8 @@ SMD void attend_block(const AttArgs& a, int h, int b) {
     __shared__ __align__(16) int q16s[64];
     __shared__ __align__(16) int k16s[64];
     __shared__ __align__(16) int vs[64];
+    __shared__ i64 vs64[64];                                // the new value whole (a head with values past 32 bits)
+    __shared__ int vwide;                                   // the new value is past 32 bits
     __shared__ i64 red[8];
     __shared__ i64 numr[NGR][64];
     __shared__ int eqs, eks;
@@ -1091,6 +1124,7 @@ SMD void attend_block(const AttArgs& a, int h, int b) {
     int* EK = a.EK + hb;
     int* V = a.V + hb * 64;
     const bool rec = REC && store && b == 0 && a.rec_pos && *a.rec_pos == p;
+    const int vbg = a.vbig ? a.vbig[(size_t)st * 12 + h] : 0;   // the head's values past 32 bits (read whole below)
 
     // Pythia: the turn's cos and sin of dimension lane (lanes < rot) with the new position, ahead of the keys, so
     // that the turn waits for them alone (row p of the [npos][rot / 2] tables; other lanes read past it: zeros)
@@ -1149,9 +1183,12 @@ SMD void attend_block(const AttArgs& a, int h, int b) {
         }
     } else if (wave == 2) {
         const i64 x = xnew;
-        if (x < (i64)INT32_MIN || x > (i64)INT32_MAX) atomicOr(a.err, SM_ERR_V32);
         vs[lane] = (int)x;
-        if (store) V[(size_t)p * 64 + lane] = (int)x;
+        vs64[lane] = x;
+        const bool any = __ballot(x < (i64)INT32_MIN || x > (i64)INT32_MAX) != 0;
+        if (lane == 0) vwide = any;
+        if (store) v_store(a, (size_t)st * 12 + h, p, lane, x);
+        else if (any && !a.V64) atomicOr(a.err, SM_ERR_V32);
     }
     __syncthreads();
 
@@ -1262,7 +1299,20 @@ SMD void attend_block(const AttArgs& a, int h, int b) {
         }
     }
     if (p % NGR == g) acc(arr[p], reinterpret_cast<const v4i*>(vs)[d4]);   // the new position (from LDS)
-    if (MODEL == 1 && (double)vmax * (double)z >= 4611686018427387904.0) atomicOr(a.err, SM_ERR_RANGE);
+    double vmaxd = vmax;
+    if (a.V64 && (vbg || vwide)) {                         // (block-uniform) the head holds a value past 32 bits:
+        const i64* v64 = a.V64 + hb * 64 + 4 * d4;           // its values whole, the new one from LDS
+        i64 m0 = 0, m1 = 0, m2 = 0, m3 = 0, vm = 0;
+        for (int sv = g; sv <= p; sv += NGR) {
+            const i64 w = arr[sv];
+            const i64* x = sv < p ? v64 + (size_t)sv * 64 : vs64 + 4 * d4;
+            m0 = wadd(m0, wmul(w, x[0])); m1 = wadd(m1, wmul(w, x[1])); m2 = wadd(m2, wmul(w, x[2])); m3 = wadd(m3, wmul(w, x[3]));
+            if (MODEL == 1 && w) vm = max(max(vm, max(iabs64(x[0]), iabs64(x[1]))), max(iabs64(x[2]), iabs64(x[3])));
+        }
+        n0 = m0; n1 = m1; n2 = m2; n3 = m3;
+        vmaxd = (double)vm;
+    }
+    if (MODEL == 1 && vmaxd * (double)z >= 4611686018427387904.0) atomicOr(a.err, SM_ERR_RANGE);
     // the NGR position groups through LDS, summed by wave 0
     numr[g][4 * d4] = n0; numr[g][4 * d4 + 1] = n1; numr[g][4 * d4 + 2] = n2; numr[g][4 * d4 + 3] = n3;
     __syncthreads();
@@ -1408,8 +1458,7 @@ __global__ __launch_bounds__(128) void k_kv_rows(AttArgs a) {
         key_store(a.K16 + at * 64, a.KM + at, (int)rsh(x, sh), lane);
         if (lane == 0) a.EK[at] = -16 + sh;
     } else {
-        if (x < (i64)INT32_MIN || x > (i64)INT32_MAX) atomicOr(a.err, SM_ERR_V32);
-        a.V[at * 64 + lane] = (int)x;
+        v_store(a, (size_t)st * 12 + h, p, lane, x);
     }
 }
 

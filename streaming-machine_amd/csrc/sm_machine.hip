@@ -401,6 +401,9 @@ struct sm_machine {
     i64* hidor = nullptr;                               // [rows][192] OR of |hid| over each fc tile's columns
     int* sfacts = nullptr;                              // [4][rows][4] mproj's K slices' light facts
     short* K16 = nullptr;                              // [L][B][12 heads][ctx][64] int16 (+32768 as 32767)
+    i64* V64 = nullptr;                                // [L][B][12 heads][ctx][64] every value whole (not with
+                                                       // the float arrival)
+    int* vbig = nullptr;                               // [L][B][12] heads holding a value past 32 bits
     i64* KM = nullptr;                                 // [L][B][12][ctx] the +32768 dimensions of each key
     int *EK = nullptr, *V = nullptr;                   // [L][B][12][ctx], [L][B][12 heads][ctx][64]
     int* seq = nullptr;                                 // [B][ctx + 1]
@@ -530,7 +533,7 @@ static void machine_free(sm_machine* m) {
                   m->r_hx16, m->r_hexls, m->r_hpile, m->r_logits, m->r_gauge, m->r_fcpre, m->r_hgauge,
                   m->fg, m->fb, m->ew, m->ee, m->ew2, m->cosT, m->sinT, m->cosF, m->sinF, m->KF,
                   m->top_hi, m->top_lo, m->cand_j, m->cand_h, m->cand_c, m->top_x, m->top_f, m->top_n, m->top_w,
-                  m->top_pile, m->top_score, m->asc, m->acm, m->aacc};
+                  m->top_pile, m->top_score, m->asc, m->acm, m->aacc, m->V64, m->vbig};
     for (void* p : ps) hfree(p);
     for (int l = 0; l < 12; l++)
         for (int j = 0; j < 2; j++) { hfree(m->ng[l][j]); hfree(m->nb[l][j]); }
@@ -614,6 +617,7 @@ static int launch_step_batched(sm_machine* m, int parts, int nrows = 0,
             AttArgs a{};
             const size_t per = (size_t)m->B * m->ctx;
             a.QKV = m->QKV; a.K16 = m->K16 + l * per * 768; a.KM = m->KM + l * per * 12; a.EK = m->EK + l * per * 12; a.V = m->V + l * per * 768;
+            a.V64 = m->V64 ? m->V64 + l * per * 768 : nullptr; a.vbig = m->vbig ? m->vbig + (size_t)l * m->B * 12 : nullptr;
             a.out = m->att; a.pos = posp; a.ctx = m->ctx; a.tb = tb; a.err = ctl + CTL_ERR;
             a.rec_pos = recp; a.ratt = m->r_att + l * 768; a.rowmap = rowmap; a.out_or = m->attor; a.out32 = m->att32;
             if (rowmap) {
@@ -827,6 +831,7 @@ static int launch_step_pythia(sm_machine* m, int parts, bool rec) {
             AttArgs a{};
             const size_t per = (size_t)m->B * m->ctx;
             a.QKV = m->QKV; a.K16 = m->K16 + l * per * 768; a.KM = m->KM + l * per * 12; a.EK = m->EK + l * per * 12; a.V = m->V + l * per * 768;
+            a.V64 = m->V64 ? m->V64 + l * per * 768 : nullptr; a.vbig = m->vbig ? m->vbig + (size_t)l * m->B * 12 : nullptr;
             a.out = m->att; a.pos = ctl + CTL_POS; a.ctx = m->ctx; a.tb = tb; a.err = ctl + CTL_ERR;
             a.rec_pos = ctl + CTL_RECPOS; a.ratt = m->r_att + l * 768;
             a.cosT = m->cosT; a.sinT = m->sinT; a.rot = m->rot; a.half = m->half; a.ehalf = m->ehalf;
@@ -938,6 +943,7 @@ static int launch_step_pythia_batched(sm_machine* m, int parts, int nrows = 0,
             const size_t per = (size_t)m->B * m->ctx;
             at.QKV = m->QKV; at.K16 = m->K16 + l * per * 768; at.KM = m->KM + l * per * 12; at.EK = m->EK + l * per * 12;
             at.V = m->V + l * per * 768;
+            at.V64 = m->V64 ? m->V64 + l * per * 768 : nullptr; at.vbig = m->vbig ? m->vbig + (size_t)l * m->B * 12 : nullptr;
             at.out = m->att; at.pos = posp; at.ctx = m->ctx; at.tb = tb; at.err = ctl + CTL_ERR;
             at.rec_pos = recp; at.ratt = m->r_att + l * 768; at.rowmap = rowmap;
             at.cosT = m->cosT; at.sinT = m->sinT; at.rot = m->rot; at.half = m->half; at.ehalf = m->ehalf;
@@ -962,6 +968,7 @@ static int launch_step_pythia_batched(sm_machine* m, int parts, int nrows = 0,
             AttArgs a{};
             const size_t per = (size_t)m->B * m->ctx;
             a.QKV = m->QKV; a.K16 = m->K16 + l * per * 768; a.KM = m->KM + l * per * 12; a.EK = m->EK + l * per * 12; a.V = m->V + l * per * 768;
+            a.V64 = m->V64 ? m->V64 + l * per * 768 : nullptr; a.vbig = m->vbig ? m->vbig + (size_t)l * m->B * 12 : nullptr;
             a.ctx = m->ctx; a.tb = tb; a.err = ctl + CTL_ERR; a.rowmap = rowmap;
             a.cosT = m->cosT; a.sinT = m->sinT; a.rot = m->rot; a.half = m->half; a.ehalf = m->ehalf;
             launch(m->cfg.profile, "kv_rows", k_kv_rows<1>, dim3(12, B), dim3(128), 0, m->st, a);
@@ -1060,6 +1067,7 @@ static int launch_step(sm_machine* m, int parts = STEP_ALL, bool rec = false) {
             AttArgs a{};
             const size_t per = (size_t)m->B * m->ctx;
             a.QKV = m->QKV; a.K16 = m->K16 + l * per * 768; a.KM = m->KM + l * per * 12; a.EK = m->EK + l * per * 12; a.V = m->V + l * per * 768;
+            a.V64 = m->V64 ? m->V64 + l * per * 768 : nullptr; a.vbig = m->vbig ? m->vbig + (size_t)l * m->B * 12 : nullptr;
             a.out = m->att; a.pos = ctl + CTL_POS; a.ctx = m->ctx; a.tb = tb; a.err = ctl + CTL_ERR;
             a.rec_pos = ctl + CTL_RECPOS; a.ratt = m->r_att + l * 768;
             // proj: to16 of the attention row, product, plain shift + bias, added to R (base2.py:105; layer 0: to
@@ -1165,7 +1173,7 @@ static int run_prefill(sm_machine* m, int npos) {
 extern "C" int sm_create(const char* layout_dir, const sm_config* cfg, sm_machine** out) {
     if (!layout_dir || !out) return fail(SM_E_ARG, "sm_create: null argument");
     *out = nullptr;
-    sm_config c{1, 1024, 1, 0, 16, 0, 0, 64, 0, 0, 2, 0};
+    sm_config c{1, 1024, 1, 0, 16, 0, 0, 64, 0, 0, 2, 0, 0};
     if (cfg) c = *cfg;
     if (c.max_streams < 1 || c.max_streams > 64) return fail(SM_E_ARG, "sm_create: max_streams must be in [1, 64]");
     if (c.prefill_rows < 0 || c.prefill_rows > 64) return fail(SM_E_ARG, "sm_create: prefill_rows must be in [0, 64]");
@@ -1174,6 +1182,8 @@ extern "C" int sm_create(const char* layout_dir, const sm_config* cfg, sm_machin
     // inside the profiled process, unexplained, so longer captures are refused rather than reached
     if (c.graph_steps < 0 || c.graph_steps > 16) return fail(SM_E_ARG, "sm_create: graph_steps must be in [0, 16]");
     if (c.att_split < -1) return fail(SM_E_ARG, "sm_create: att_split must be -1, 0 or a position");
+    if (c.v64 < 0 || c.v64 > 1) return fail(SM_E_ARG, "sm_create: v64 must be 0 or 1");
+    if (c.v64 && (c.float_stages & SM_FLOAT_ARRIVAL)) return fail(SM_E_ARG, "sm_create: the float arrival keeps no 64-bit values");
     const std::string dir = std::string(layout_dir) + "/";
     std::vector<char> mj;
     if (!read_file(dir + "manifest.json", mj)) return fail(SM_E_IO, "cannot read " + dir + "manifest.json");
@@ -1396,6 +1406,8 @@ extern "C" int sm_create(const char* layout_dir, const sm_config* cfg, sm_machin
         (rc = dalloc(&m->r_logits, (size_t)m->vocab)) || (rc = dalloc(&m->r_gauge, (size_t)12 * 2 * 768)) ||
         (rc = dalloc(&m->r_fcpre, (size_t)12 * 3072)) || (rc = dalloc(&m->r_hgauge, (size_t)768)))
         return bail(rc);
+    // the values whole beside their low 32 bits (the float arrival keeps the int32 cache and its error)
+    if (!m->farr && ((rc = dalloc(&m->V64, 12 * B * ctx * 768)) || (rc = dalloc(&m->vbig, 12 * B * 12)))) return bail(rc);
     if (m->att_split >= 0) {
         m->ncm = (int)((ctx + ACH_SPLIT - 1) / ACH_SPLIT);
         if ((rc = dalloc(&m->asc, 12 * ctx)) || (rc = dalloc(&m->acm, (size_t)12 * m->ncm)) ||
@@ -1433,6 +1445,8 @@ extern "C" int sm_reset(sm_machine* m) {
     HIP_TRY(hipMemsetAsync(m->KM, 0, 12 * B * ctx * 12 * 8, m->st));
     HIP_TRY(hipMemsetAsync(m->EK, 0, 12 * B * ctx * 12 * 4, m->st));
     HIP_TRY(hipMemsetAsync(m->V, 0, 12 * B * ctx * 768 * 4, m->st));
+    // every head reads its values at 32 bits until one past 32 bits is stored (v64 = 1: whole from the start)
+    if (m->vbig) HIP_TRY(hipMemsetAsync(m->vbig, m->cfg.v64 ? 1 : 0, 12 * B * 12 * 4, m->st));
     HIP_TRY(hipMemsetAsync(m->seq, 0, B * (ctx + 1) * 4, m->st));
     HIP_TRY(hipMemsetAsync(m->words, 0, B * (ctx + 1) * 4, m->st));
     HIP_TRY(hipMemsetAsync(m->R, 0, (size_t)m->RC * 768 * 8, m->st));
@@ -1573,7 +1587,8 @@ extern "C" int sm_generate(sm_machine* m, int32_t n_words, int32_t* out) {
     m->h_pos += total;
     m->h_words = target;
     if (ctl[m->par ? CTL_POS1 : CTL_POS] != m->h_pos) return fail(SM_E_STATE, "sm_generate: device position disagrees with the host");
-    if (ctl[CTL_ERR] & SM_ERR_V32) return fail(SM_E_OVERFLOW, "sm_generate: an attention value left 32 bits (the V cache holds int32)");
+    if (ctl[CTL_ERR] & SM_ERR_V32)
+        return fail(SM_E_OVERFLOW, "sm_generate: an attention value left 32 bits (the float arrival's value cache holds int32)");
     if (ctl[CTL_ERR] & SM_ERR_RANGE)
         return fail(SM_E_OVERFLOW, "sm_generate: a value passed a bound the reference asserts (turn input 2^31, attention sum 2^62)");
     std::memcpy(out, m->hpin + CTL_N, (size_t)m->B * n_words * sizeof(int));
@@ -1642,6 +1657,16 @@ extern "C" int sm_read(sm_machine* m, int32_t what, int32_t layer, int32_t strea
     size_t need = 0;
     auto kv_ok = [&]() { return layer >= 0 && layer < 12 && pos >= 0 && pos < m->ctx; };
     switch (what) {
+        case SM_READ_V64: {
+            // one position's values whole, from the 64-bit copy
+            if (!kv_ok()) return fail(SM_E_ARG, "sm_read: layer/pos");
+            if (!m->V64) return fail(SM_E_STATE, "sm_read: this machine keeps no 64-bit values (float arrival)");
+            if (bytes != 12 * 512) return fail(SM_E_ARG, "sm_read: expected 6144 bytes");
+            const size_t h0 = ((size_t)layer * B + stream) * 12 * ctx + pos;
+            HIP_TRY(hipStreamSynchronize(m->st));
+            HIP_TRY(hipMemcpy2D(dst, 512, m->V64 + h0 * 64, ctx * 512, 512, 12, hipMemcpyDeviceToHost));
+            return SM_OK;
+        }
         case SM_READ_K16: case SM_READ_EK: case SM_READ_V: {
             // one position's row, gathered from the 12 heads of the head-major cache
             if (!kv_ok()) return fail(SM_E_ARG, "sm_read: layer/pos");

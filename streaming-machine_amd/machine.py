@@ -19,7 +19,7 @@ CODES = {SM_E_ARG: "SM_E_ARG", SM_E_IO: "SM_E_IO", SM_E_HIP: "SM_E_HIP", SM_E_OO
          SM_E_OVERFLOW: "SM_E_OVERFLOW", SM_E_STATE: "SM_E_STATE"}
 
 READ = dict(k16=1, ek=2, v=3, resid=4, seq=5, x16=10, exls=11, pile=12, qkv=13, att=14, hid=15, rresid=16,
-            hx16=17, hexls=18, hpile=19, logits=20, gauge=21, fcpre=22, hgauge=23, top=24)
+            hx16=17, hexls=18, hpile=19, logits=20, gauge=21, fcpre=22, hgauge=23, top=24, v64=25)
 
 
 class SmError(RuntimeError):
@@ -32,7 +32,8 @@ class SmConfig(ctypes.Structure):
     _fields_ = [("max_streams", ctypes.c_int32), ("max_ctx", ctypes.c_int32), ("use_graph", ctypes.c_int32),
                 ("head_grid", ctypes.c_int32), ("graph_steps", ctypes.c_int32), ("profile", ctypes.c_int32),
                 ("table_mode", ctypes.c_int32), ("prefill_rows", ctypes.c_int32), ("inv", ctypes.c_int32),
-                ("float_stages", ctypes.c_int32), ("top_read", ctypes.c_int32), ("att_split", ctypes.c_int32)]
+                ("float_stages", ctypes.c_int32), ("top_read", ctypes.c_int32), ("att_split", ctypes.c_int32),
+                ("v64", ctypes.c_int32)]
 
 
 FLOAT_STAGES = dict(gauge=1, edge=2, arrival=4, turn=8)     # SM_FLOAT_* of include/sm_base2.h
@@ -122,6 +123,8 @@ class Machine:
       .record_at(pos); .read(name, layer=0, stream=0, pos=0)
       att_split: batch 1, the position from which a step's attention runs spread over the GPU (chunks of 64
       positions, one block a chunk; 0: from position 160, -1: never); the same words either way.
+      v64: every head reads its cached values whole (64-bit) from the start; by default a head does so once it holds
+      a value past 32 bits (every value is kept whole beside its low 32 bits); the same words either way.
     gauge / edge / arrival ("int" or "float"; base2.py:10-11) and turn (the Pythia machine,
     foundation0/pythia_base2.py:21-27) put that stage back to float64 on the device, as the reference's switches
     do: diagnostics, compared with the reference at the word level (one stream, prefill_rows=0).  With
@@ -131,7 +134,7 @@ class Machine:
     def __init__(self, layout_dir: str, max_ctx: int = 1024, max_streams: int = 1, use_graph: bool = True,
                  head_grid: int = 0, graph_steps: int = 16, profile: bool = False, verify_tables: bool = False,
                  prefill_rows: int = 64, gauge: str = "int", edge: str = "int", arrival: str = "int", turn: str = "int",
-                 inv: bool = False, top: str = "plain", att_split: int = 0):
+                 inv: bool = False, top: str = "plain", att_split: int = 0, v64: bool = False):
         fs = 0
         for name, v in (("gauge", gauge), ("edge", edge), ("arrival", arrival), ("turn", turn)):
             if v not in ("int", "float"):
@@ -142,7 +145,7 @@ class Machine:
         self.L = lib()
         cfg = SmConfig(max_streams, max_ctx, 1 if use_graph else 0, head_grid, graph_steps, 1 if profile else 0,
                        1 if verify_tables else 0, prefill_rows, 1 if inv else 0, fs,
-                       dict(plain=0, fr=1, auto=2)[top], att_split)
+                       dict(plain=0, fr=1, auto=2)[top], att_split, 1 if v64 else 0)
         h = vp()
         check(self.L.sm_create(os.fsencode(layout_dir), ctypes.byref(cfg), ctypes.byref(h)))
         self.h = h
@@ -213,7 +216,7 @@ class Machine:
         check(self.L.sm_record_at(self.h, pos))
 
     def read(self, name: str, layer: int = 0, stream: int = 0, pos: int = 0) -> np.ndarray:
-        shapes = {"k16": ((768,), np.int32), "ek": ((12,), np.int32), "v": ((768,), np.int32),
+        shapes = {"k16": ((768,), np.int32), "ek": ((12,), np.int32), "v": ((768,), np.int32), "v64": ((768,), np.int64),
                   "resid": ((768,), np.int64), "seq": ((self.max_ctx + 1,), np.int32),
                   "x16": ((12, 4, 3072), np.int64), "exls": ((12, 4, 2), np.int64), "pile": ((12, 4, 3072), np.int64),
                   "qkv": ((12, 2304), np.int64), "att": ((12, 768), np.int64), "hid": ((12, 3072), np.int64),

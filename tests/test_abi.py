@@ -53,7 +53,7 @@ def test_stage_switches(sm, tmp_path):
     bits = dict(re.findall(r"SM_FLOAT_([A-Z]+) = (\d+)", hdr))
     assert {k.lower(): int(v) for k, v in bits.items()} == machine.FLOAT_STAGES
     names = [f[0] for f in machine.SmConfig._fields_]
-    assert names[-4:] == ["inv", "float_stages", "top_read", "att_split"]
+    assert names[-5:] == ["inv", "float_stages", "top_read", "att_split", "v64"]
     fields = re.search(r"typedef struct \{(.*?)\} sm_config;", re.sub(r"/\*.*?\*/", "", hdr, flags=re.S), re.S).group(1)
     assert re.findall(r"int32_t (\w+);", fields) == names      # the binding's layout is the header's
 

@@ -139,3 +139,20 @@ def test_attention_over_a_cache(full_oracle, golden, sm):
         assert h64(got)[:16] == case["row_sha16"][p], p
     v[3, 10, 5] += 1 << 14
     assert h64(full_oracle.attend_cached(Q[P - 1], k16, ek, v, P - 1))[:16] != case["row_sha16"][P - 1]
+
+
+def test_bound_switch_keeps_the_exact_integers(sm, small_npz):
+    """past base2.py's 2^52 exactness bound (here: one head's values planted past 2^33) the oracle reports the bound;
+    with bound=False its KV-cached steps give the exact int64 result instead, the same as with the bound where the
+    bound holds"""
+    import oracle
+    prompt = sm.prompt_ids(60, 8, 1000)
+    assert oracle.Oracle(small_npz, bound=False).generate(prompt, 6, 64) == oracle.Oracle(small_npz).generate(prompt, 6, 64)
+    npz = dict(small_npz)
+    b = npz["qkv.0.b"].copy()
+    b[1536:1600] += np.arange(64, dtype=np.int64) * (1 << 26) + (1 << 33)
+    npz["qkv.0.b"] = b
+    with pytest.raises(ArithmeticError):
+        oracle.Oracle(npz).generate(prompt, 6, 64)
+    words = oracle.Oracle(npz, bound=False).generate(prompt, 6, 64)
+    assert words != oracle.Oracle(small_npz).generate(prompt, 6, 64)     # the planted head reaches the words
