@@ -74,11 +74,12 @@ typedef struct {
                               scores and maxima, then arrivals against the head's maximum and the value sums added
                               exactly, then the divisor: three launches); steps before it run one block a head.
                               0: from position 160; -1: never.  The same numbers either way (base2.py:85-100) */
-    int32_t v64;           /* the value cache (base2.py's attention weighs each raw int64 value): every value is kept
-                              whole beside its low 32 bits, and a head holding a value past 32 bits reads its values
-                              whole.  0: the others read the 32-bit copy (half the bytes); 1: every head reads its
-                              values whole from the start.  The same numbers either way.  Not with the float arrival,
-                              whose cache holds int32 values (a value past 32 bits is SM_E_OVERFLOW there) */
+    int32_t v64;           /* the value cache (base2.py's attention weighs each raw int64 value): every value's low
+                              32 bits, and a row holding a value past 32 bits also whole; a head holding such a row
+                              reads its values whole.  0: the others read the 32-bit rows alone (half the bytes);
+                              1: every head reads its values whole from the start.  The same numbers either way.  Not
+                              with the float arrival, whose cache holds int32 values (a value past 32 bits is
+                              SM_E_OVERFLOW there) */
 } sm_config;
 
 enum { SM_FLOAT_GAUGE = 1, SM_FLOAT_EDGE = 2, SM_FLOAT_ARRIVAL = 4, SM_FLOAT_TURN = 8 };

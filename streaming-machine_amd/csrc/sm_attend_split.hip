@@ -139,7 +139,7 @@ __global__ __launch_bounds__(256) void k_att_mix(AttArgs a) {
     v4i vp[4];
 #pragma unroll
     for (int i = 0; i < 4; i++) vp[i] = buf_load4(rv, (unsigned)(s0 + g + 16 * i) * 256u + d4 * 16);
-    const int vbg = a.vbig ? a.vbig[h] : 0;                 // the head holds a value past 32 bits (read whole below)
+    const int vbg = vbig_load(a, (size_t)h);                // the head holds a value past 32 bits (read whole below)
     // the clock starts at the head's maximum (base2.py:96)
     const i64 M = block_reduce<OpMax, 4>(tid < nc ? cmv : INT64_MIN, red, OpMax(), tid);
     // arrivals (base2.py:96-97), wave 0 a position each, and their sum
@@ -161,8 +161,7 @@ __global__ __launch_bounds__(256) void k_att_mix(AttArgs a) {
         if (MODEL == 1 && w) vmax = max(vmax, max(max(abs(x.x), abs(x.y)), max(abs(x.z), abs(x.w))));
     }
     i64 vm64 = vmax;
-    if (a.V64 && vbg) {                                     // (block-uniform) the head's values whole
-        const i64* v64 = a.V64 + hb * 64 + 4 * d4;
+    if (a.V64 && __builtin_amdgcn_readfirstlane(vbg)) {     // (block-uniform) the head's values whole
         n0 = n1 = n2 = n3 = 0;
         vm64 = 0;
 #pragma unroll
@@ -170,7 +169,8 @@ __global__ __launch_bounds__(256) void k_att_mix(AttArgs a) {
             const int sv = s0 + g + 16 * i;
             if (sv > p) break;
             const i64 w = arr_s[g + 16 * i];
-            const i64* x = v64 + (size_t)sv * 64;
+            i64 x[4];
+            for (int j = 0; j < 4; j++) x[j] = v_whole(a, hb, sv, 4 * d4 + j);
             n0 = wadd(n0, wmul(w, x[0])); n1 = wadd(n1, wmul(w, x[1])); n2 = wadd(n2, wmul(w, x[2])); n3 = wadd(n3, wmul(w, x[3]));
             if (MODEL == 1 && w) vm64 = max(max(vm64, max(iabs64(x[0]), iabs64(x[1]))), max(iabs64(x[2]), iabs64(x[3])));
         }

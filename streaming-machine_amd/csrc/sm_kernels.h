@@ -135,9 +135,11 @@ struct AttArgs {
     i64* KM;            // [B][12][ctx]     bit d: dimension d of the key is +32768 (one more than K16 holds)
     int* EK;            // [B][12][ctx]     their water levels
     int* V;             // [B][12][ctx][64] raw gauged values: their low 32 bits (every value that fits 32 bits)
-    i64* V64;           // [B][12][ctx][64] (when non-null) the same values whole (base2.py keeps int64 values)
+    i64* V64;           // [B][12][ctx][64] (when non-null) a row holding a value past 32 bits, whole (base2.py
+                        // keeps int64 values); rows that fit 32 bits are not written here
+    int* VW;            // [B][12][ctx] (with V64) nonzero: row p is in V64 (one of its values is past 32 bits)
     int* vbig;          // [B][12] (with V64) nonzero: the (stream, head) holds a value past 32 bits, and the
-                        // attention reads that head's values from V64
+                        // attention reads that head's values whole (V64 where VW marks the row, else V)
     i64* out;           // [B][768]
     int* out32;         // [B][768] (when non-null): the same values' low 32 bits, for a consumer that reads a
                         // row's 32-bit copy wherever its OR words show that the row fits (k_gemm's SRC path)

@@ -840,20 +840,34 @@ SMD void key_store(short* krow, i64* km, int x16, int lane) {
     if (lane == 0) *km = (i64)m;
 }
 // A value row into the cache (base2.py's attention weighs the raw int64 value): its low 32 bits into V, which holds
-// every value that fits 32 bits exactly; with V64, the whole value there as well, and a value past 32 bits marks its
-// (stream, head) (vbig), whose values the attention then reads whole.  Without V64 a value past 32 bits is an error
-// (SM_ERR_V32).  The whole wave stores one row, lane = dimension; hrow: the (stream, head) of the layer's [B][12].
+// every value that fits 32 bits exactly.  With V64, a row with a value past 32 bits goes there whole as well, VW
+// marks each row written (whole or not) and a whole row marks its (stream, head) (vbig), whose values the attention
+// then reads whole.  Without V64 a value past 32 bits is an error (SM_ERR_V32).  The whole wave stores one row,
+// lane = dimension; hrow: the (stream, head) of the layer's [B][12].
 SMD void v_store(const AttArgs& a, size_t hrow, int p, int lane, i64 x) {
-    const size_t at = (hrow * a.ctx + p) * 64 + lane;
-    a.V[at] = (int)x;
-    const bool wide = x < (i64)INT32_MIN || x > (i64)INT32_MAX;
+    const size_t row = hrow * a.ctx + p;
+    a.V[row * 64 + lane] = (int)x;
+    const bool wide = __ballot(x < (i64)INT32_MIN || x > (i64)INT32_MAX) != 0;
     if (a.V64) {
-        a.V64[at] = x;
-        const bool any = __ballot(wide) != 0;
-        if (any && lane == 0) atomicOr(a.vbig + hrow, 1);
-    } else if (wide) {
+        if (wide) a.V64[row * 64 + lane] = x;
+        if (lane == 0) {
+            a.VW[row] = wide;
+            if (wide) atomicOr(a.vbig + hrow, 1);
+        }
+    } else if (wide && lane == 0) {
         atomicOr(a.err, SM_ERR_V32);
     }
+}
+// The (stream, head)'s mark of values past 32 bits (vbig), as a vector load issued with the cached rows and waited
+// for only where the attention branches on it (a scalar load there is waited for at the kernel's start); without V64
+// the load's empty range reads 0 with no memory request.
+SMD int vbig_load(const AttArgs& a, size_t hrow) {
+    return buf_load1(buf_rsrc(a.vbig ? a.vbig + hrow : nullptr, a.vbig ? 4u : 0u), 0);
+}
+// Value d of cached row s of the rows from hb (the head's first row) whole: V64 where VW marks the row, else V.
+SMD i64 v_whole(const AttArgs& a, size_t hb, int s, int d) {
+    const size_t row = hb + s;
+    return a.VW[row] ? a.V64[row * 64 + d] : (i64)a.V[row * 64 + d];
 }
 // q . k' by 16-bit dot products (the one-wave short path): q = 256 qh + ql with qh = q >> 8 in [-128, 128] and
 // ql = q & 255, both int16, so that over 64 dimensions sum qh k' stays below 2^28 and sum ql k' below 2^30 in
@@ -949,10 +963,10 @@ SMD i64 attend_short(const AttArgs& a, int p, int h, int b, int* q_s, int* w_s, 
     for (int c = 0; c < 8; c++) krow[c] = buf_load4(rk, (unsigned)lane * 128 + 16 * c);
     const int ekl = buf_load1(re, (unsigned)lane * 4);
     const u64 kml = (u64)buf_load8(rm, (unsigned)lane * 8);
-    const int vbg = a.vbig ? a.vbig[(size_t)b * 12 + h] : 0;   // the head's values past 32 bits (read whole below)
     int vcol[64];
 #pragma unroll
     for (int s = 0; s < 64; s++) vcol[s] = buf_load1(rv, (unsigned)(s * 64 + lane) * 4);
+    const int vbg = vbig_load(a, (size_t)b * 12 + h);        // the head's values past 32 bits (read whole below)
     if constexpr (MODEL == 1) __builtin_amdgcn_sched_barrier(0);   // (the loads above stay issued here)
     if (MODEL == 1) {                                        // the turns (pythia_base2.py:116-123)
         const int r = a.rot >> 1;
@@ -1027,13 +1041,12 @@ SMD i64 attend_short(const AttArgs& a, int p, int h, int b, int* q_s, int* w_s, 
     num += (i64)wp * (int)vv;
     if (MODEL == 1 && wp) vmax = max(vmax, abs((int)vv));
     double vmaxd = vmax;
-    if (a.V64 && (vbg || __ballot(vv < (i64)INT32_MIN || vv > (i64)INT32_MAX))) {
+    if (a.V64 && (__builtin_amdgcn_readfirstlane(vbg) || __ballot(vv < (i64)INT32_MIN || vv > (i64)INT32_MAX))) {
         // (the whole wave) the head holds a value past 32 bits: its values whole from V64, the new one from vv
-        const i64* v64 = a.V64 + hb * 64 + lane;
         i64 n = 0, vm = 0;
         for (int s = 0; s < p; s++) {
             const int ws = w_s[s];
-            const i64 x = v64[(size_t)s * 64];
+            const i64 x = v_whole(a, hb, s, lane);
             n = wadd(n, wmul(ws, x));
             if (MODEL == 1 && ws) vm = max(vm, iabs64(x));
         }
@@ -1124,7 +1137,7 @@ SMD void attend_block(const AttArgs& a, int h, int b) {
     int* EK = a.EK + hb;
     int* V = a.V + hb * 64;
     const bool rec = REC && store && b == 0 && a.rec_pos && *a.rec_pos == p;
-    const int vbg = a.vbig ? a.vbig[(size_t)st * 12 + h] : 0;   // the head's values past 32 bits (read whole below)
+    const int vbg = vbig_load(a, (size_t)st * 12 + h);      // the head's values past 32 bits (read whole below)
 
     // Pythia: the turn's cos and sin of dimension lane (lanes < rot) with the new position, ahead of the keys, so
     // that the turn waits for them alone (row p of the [npos][rot / 2] tables; other lanes read past it: zeros)
@@ -1300,12 +1313,13 @@ SMD void attend_block(const AttArgs& a, int h, int b) {
     }
     if (p % NGR == g) acc(arr[p], reinterpret_cast<const v4i*>(vs)[d4]);   // the new position (from LDS)
     double vmaxd = vmax;
-    if (a.V64 && (vbg || vwide)) {                         // (block-uniform) the head holds a value past 32 bits:
-        const i64* v64 = a.V64 + hb * 64 + 4 * d4;           // its values whole, the new one from LDS
+    if (a.V64 && (__builtin_amdgcn_readfirstlane(vbg) || vwide)) {
+        // (block-uniform) the head holds a value past 32 bits: its values whole, the new one from LDS
         i64 m0 = 0, m1 = 0, m2 = 0, m3 = 0, vm = 0;
         for (int sv = g; sv <= p; sv += NGR) {
             const i64 w = arr[sv];
-            const i64* x = sv < p ? v64 + (size_t)sv * 64 : vs64 + 4 * d4;
+            i64 x[4];
+            for (int i = 0; i < 4; i++) x[i] = sv < p ? v_whole(a, hb, sv, 4 * d4 + i) : vs64[4 * d4 + i];
             m0 = wadd(m0, wmul(w, x[0])); m1 = wadd(m1, wmul(w, x[1])); m2 = wadd(m2, wmul(w, x[2])); m3 = wadd(m3, wmul(w, x[3]));
             if (MODEL == 1 && w) vm = max(max(vm, max(iabs64(x[0]), iabs64(x[1]))), max(iabs64(x[2]), iabs64(x[3])));
         }

@@ -401,8 +401,9 @@ struct sm_machine {
     i64* hidor = nullptr;                               // [rows][192] OR of |hid| over each fc tile's columns
     int* sfacts = nullptr;                              // [4][rows][4] mproj's K slices' light facts
     short* K16 = nullptr;                              // [L][B][12 heads][ctx][64] int16 (+32768 as 32767)
-    i64* V64 = nullptr;                                // [L][B][12 heads][ctx][64] every value whole (not with
-                                                       // the float arrival)
+    i64* V64 = nullptr;                                // [L][B][12 heads][ctx][64] rows with a value past 32 bits,
+                                                       // whole (not with the float arrival)
+    int* VW = nullptr;                                 // [L][B][12][ctx] the rows held in V64
     int* vbig = nullptr;                               // [L][B][12] heads holding a value past 32 bits
     i64* KM = nullptr;                                 // [L][B][12][ctx] the +32768 dimensions of each key
     int *EK = nullptr, *V = nullptr;                   // [L][B][12][ctx], [L][B][12 heads][ctx][64]
@@ -533,7 +534,7 @@ static void machine_free(sm_machine* m) {
                   m->r_hx16, m->r_hexls, m->r_hpile, m->r_logits, m->r_gauge, m->r_fcpre, m->r_hgauge,
                   m->fg, m->fb, m->ew, m->ee, m->ew2, m->cosT, m->sinT, m->cosF, m->sinF, m->KF,
                   m->top_hi, m->top_lo, m->cand_j, m->cand_h, m->cand_c, m->top_x, m->top_f, m->top_n, m->top_w,
-                  m->top_pile, m->top_score, m->asc, m->acm, m->aacc, m->V64, m->vbig};
+                  m->top_pile, m->top_score, m->asc, m->acm, m->aacc, m->V64, m->VW, m->vbig};
     for (void* p : ps) hfree(p);
     for (int l = 0; l < 12; l++)
         for (int j = 0; j < 2; j++) { hfree(m->ng[l][j]); hfree(m->nb[l][j]); }
@@ -617,7 +618,8 @@ static int launch_step_batched(sm_machine* m, int parts, int nrows = 0,
             AttArgs a{};
             const size_t per = (size_t)m->B * m->ctx;
             a.QKV = m->QKV; a.K16 = m->K16 + l * per * 768; a.KM = m->KM + l * per * 12; a.EK = m->EK + l * per * 12; a.V = m->V + l * per * 768;
-            a.V64 = m->V64 ? m->V64 + l * per * 768 : nullptr; a.vbig = m->vbig ? m->vbig + (size_t)l * m->B * 12 : nullptr;
+            a.V64 = m->V64 ? m->V64 + l * per * 768 : nullptr; a.VW = m->VW ? m->VW + l * per * 12 : nullptr;
+            a.vbig = m->vbig ? m->vbig + (size_t)l * m->B * 12 : nullptr;
             a.out = m->att; a.pos = posp; a.ctx = m->ctx; a.tb = tb; a.err = ctl + CTL_ERR;
             a.rec_pos = recp; a.ratt = m->r_att + l * 768; a.rowmap = rowmap; a.out_or = m->attor; a.out32 = m->att32;
             if (rowmap) {
@@ -831,7 +833,8 @@ static int launch_step_pythia(sm_machine* m, int parts, bool rec) {
             AttArgs a{};
             const size_t per = (size_t)m->B * m->ctx;
             a.QKV = m->QKV; a.K16 = m->K16 + l * per * 768; a.KM = m->KM + l * per * 12; a.EK = m->EK + l * per * 12; a.V = m->V + l * per * 768;
-            a.V64 = m->V64 ? m->V64 + l * per * 768 : nullptr; a.vbig = m->vbig ? m->vbig + (size_t)l * m->B * 12 : nullptr;
+            a.V64 = m->V64 ? m->V64 + l * per * 768 : nullptr; a.VW = m->VW ? m->VW + l * per * 12 : nullptr;
+            a.vbig = m->vbig ? m->vbig + (size_t)l * m->B * 12 : nullptr;
             a.out = m->att; a.pos = ctl + CTL_POS; a.ctx = m->ctx; a.tb = tb; a.err = ctl + CTL_ERR;
             a.rec_pos = ctl + CTL_RECPOS; a.ratt = m->r_att + l * 768;
             a.cosT = m->cosT; a.sinT = m->sinT; a.rot = m->rot; a.half = m->half; a.ehalf = m->ehalf;
@@ -943,7 +946,8 @@ static int launch_step_pythia_batched(sm_machine* m, int parts, int nrows = 0,
             const size_t per = (size_t)m->B * m->ctx;
             at.QKV = m->QKV; at.K16 = m->K16 + l * per * 768; at.KM = m->KM + l * per * 12; at.EK = m->EK + l * per * 12;
             at.V = m->V + l * per * 768;
-            at.V64 = m->V64 ? m->V64 + l * per * 768 : nullptr; at.vbig = m->vbig ? m->vbig + (size_t)l * m->B * 12 : nullptr;
+            at.V64 = m->V64 ? m->V64 + l * per * 768 : nullptr; at.VW = m->VW ? m->VW + l * per * 12 : nullptr;
+            at.vbig = m->vbig ? m->vbig + (size_t)l * m->B * 12 : nullptr;
             at.out = m->att; at.pos = posp; at.ctx = m->ctx; at.tb = tb; at.err = ctl + CTL_ERR;
             at.rec_pos = recp; at.ratt = m->r_att + l * 768; at.rowmap = rowmap;
             at.cosT = m->cosT; at.sinT = m->sinT; at.rot = m->rot; at.half = m->half; at.ehalf = m->ehalf;
@@ -968,7 +972,8 @@ static int launch_step_pythia_batched(sm_machine* m, int parts, int nrows = 0,
             AttArgs a{};
             const size_t per = (size_t)m->B * m->ctx;
             a.QKV = m->QKV; a.K16 = m->K16 + l * per * 768; a.KM = m->KM + l * per * 12; a.EK = m->EK + l * per * 12; a.V = m->V + l * per * 768;
-            a.V64 = m->V64 ? m->V64 + l * per * 768 : nullptr; a.vbig = m->vbig ? m->vbig + (size_t)l * m->B * 12 : nullptr;
+            a.V64 = m->V64 ? m->V64 + l * per * 768 : nullptr; a.VW = m->VW ? m->VW + l * per * 12 : nullptr;
+            a.vbig = m->vbig ? m->vbig + (size_t)l * m->B * 12 : nullptr;
             a.ctx = m->ctx; a.tb = tb; a.err = ctl + CTL_ERR; a.rowmap = rowmap;
             a.cosT = m->cosT; a.sinT = m->sinT; a.rot = m->rot; a.half = m->half; a.ehalf = m->ehalf;
             launch(m->cfg.profile, "kv_rows", k_kv_rows<1>, dim3(12, B), dim3(128), 0, m->st, a);
@@ -1067,7 +1072,8 @@ static int launch_step(sm_machine* m, int parts = STEP_ALL, bool rec = false) {
             AttArgs a{};
             const size_t per = (size_t)m->B * m->ctx;
             a.QKV = m->QKV; a.K16 = m->K16 + l * per * 768; a.KM = m->KM + l * per * 12; a.EK = m->EK + l * per * 12; a.V = m->V + l * per * 768;
-            a.V64 = m->V64 ? m->V64 + l * per * 768 : nullptr; a.vbig = m->vbig ? m->vbig + (size_t)l * m->B * 12 : nullptr;
+            a.V64 = m->V64 ? m->V64 + l * per * 768 : nullptr; a.VW = m->VW ? m->VW + l * per * 12 : nullptr;
+            a.vbig = m->vbig ? m->vbig + (size_t)l * m->B * 12 : nullptr;
             a.out = m->att; a.pos = ctl + CTL_POS; a.ctx = m->ctx; a.tb = tb; a.err = ctl + CTL_ERR;
             a.rec_pos = ctl + CTL_RECPOS; a.ratt = m->r_att + l * 768;
             // proj: to16 of the attention row, product, plain shift + bias, added to R (base2.py:105; layer 0: to
@@ -1406,8 +1412,11 @@ extern "C" int sm_create(const char* layout_dir, const sm_config* cfg, sm_machin
         (rc = dalloc(&m->r_logits, (size_t)m->vocab)) || (rc = dalloc(&m->r_gauge, (size_t)12 * 2 * 768)) ||
         (rc = dalloc(&m->r_fcpre, (size_t)12 * 3072)) || (rc = dalloc(&m->r_hgauge, (size_t)768)))
         return bail(rc);
-    // the values whole beside their low 32 bits (the float arrival keeps the int32 cache and its error)
-    if (!m->farr && ((rc = dalloc(&m->V64, 12 * B * ctx * 768)) || (rc = dalloc(&m->vbig, 12 * B * 12)))) return bail(rc);
+    // rows with a value past 32 bits whole beside their low 32 bits (the float arrival keeps the int32 cache and its
+    // error)
+    if (!m->farr && ((rc = dalloc(&m->V64, 12 * B * ctx * 768)) || (rc = dalloc(&m->VW, 12 * B * ctx * 12)) ||
+                     (rc = dalloc(&m->vbig, 12 * B * 12))))
+        return bail(rc);
     if (m->att_split >= 0) {
         m->ncm = (int)((ctx + ACH_SPLIT - 1) / ACH_SPLIT);
         if ((rc = dalloc(&m->asc, 12 * ctx)) || (rc = dalloc(&m->acm, (size_t)12 * m->ncm)) ||
@@ -1447,6 +1456,7 @@ extern "C" int sm_reset(sm_machine* m) {
     HIP_TRY(hipMemsetAsync(m->V, 0, 12 * B * ctx * 768 * 4, m->st));
     // every head reads its values at 32 bits until one past 32 bits is stored (v64 = 1: whole from the start)
     if (m->vbig) HIP_TRY(hipMemsetAsync(m->vbig, m->cfg.v64 ? 1 : 0, 12 * B * 12 * 4, m->st));
+    if (m->VW) HIP_TRY(hipMemsetAsync(m->VW, 0, 12 * B * ctx * 12 * 4, m->st));
     HIP_TRY(hipMemsetAsync(m->seq, 0, B * (ctx + 1) * 4, m->st));
     HIP_TRY(hipMemsetAsync(m->words, 0, B * (ctx + 1) * 4, m->st));
     HIP_TRY(hipMemsetAsync(m->R, 0, (size_t)m->RC * 768 * 8, m->st));
@@ -1658,13 +1668,21 @@ extern "C" int sm_read(sm_machine* m, int32_t what, int32_t layer, int32_t strea
     auto kv_ok = [&]() { return layer >= 0 && layer < 12 && pos >= 0 && pos < m->ctx; };
     switch (what) {
         case SM_READ_V64: {
-            // one position's values whole, from the 64-bit copy
+            // one position's values whole: a head's row from the 64-bit copy where the row is there, else its
+            // 32-bit row widened
             if (!kv_ok()) return fail(SM_E_ARG, "sm_read: layer/pos");
             if (!m->V64) return fail(SM_E_STATE, "sm_read: this machine keeps no 64-bit values (float arrival)");
             if (bytes != 12 * 512) return fail(SM_E_ARG, "sm_read: expected 6144 bytes");
             const size_t h0 = ((size_t)layer * B + stream) * 12 * ctx + pos;
+            int vw[12], v32[12 * 64];
             HIP_TRY(hipStreamSynchronize(m->st));
             HIP_TRY(hipMemcpy2D(dst, 512, m->V64 + h0 * 64, ctx * 512, 512, 12, hipMemcpyDeviceToHost));
+            HIP_TRY(hipMemcpy2D(v32, 256, m->V + h0 * 64, ctx * 256, 256, 12, hipMemcpyDeviceToHost));
+            HIP_TRY(hipMemcpy2D(vw, 4, m->VW + h0, ctx * 4, 4, 12, hipMemcpyDeviceToHost));
+            int64_t* o = static_cast<int64_t*>(dst);
+            for (int h = 0; h < 12; h++)
+                if (!vw[h])
+                    for (int d = 0; d < 64; d++) o[h * 64 + d] = v32[h * 64 + d];
             return SM_OK;
         }
         case SM_READ_K16: case SM_READ_EK: case SM_READ_V: {

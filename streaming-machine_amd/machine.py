@@ -124,7 +124,8 @@ class Machine:
       att_split: batch 1, the position from which a step's attention runs spread over the GPU (chunks of 64
       positions, one block a chunk; 0: from position 160, -1: never); the same words either way.
       v64: every head reads its cached values whole (64-bit) from the start; by default a head does so once it holds
-      a value past 32 bits (every value is kept whole beside its low 32 bits); the same words either way.
+      a value past 32 bits (every value's low 32 bits are kept, and a row holding a value past them also whole);
+      the same words either way.
     gauge / edge / arrival ("int" or "float"; base2.py:10-11) and turn (the Pythia machine,
     foundation0/pythia_base2.py:21-27) put that stage back to float64 on the device, as the reference's switches
     do: diagnostics, compared with the reference at the word level (one stream, prefill_rows=0).  With
