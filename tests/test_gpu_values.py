@@ -6,7 +6,10 @@ value past 32 bits reads its values whole.  Checked two ways:
   batched streams, the prompt pass);
 * a model whose layer-0 head-0 values are planted past 2^33 (its qkv bias): the words equal the oracle's exact int64
   run (past base2.py's 2^52 float64 bound the reference itself is not exact there, so the pin is the oracle's integer
-  arithmetic), and the cached values read back whole.
+  arithmetic), and the cached values read back whole;
+* the Pythia machine with layer 0's head-0 values scaled by 2^16 (their column exponents; pythia_base2.py's integer
+  attention is exact up to its 2^62 assert, which these stay below): the oracle's words, layer 0's attention row and
+  the whole cached values.
 """
 from __future__ import annotations
 
@@ -98,4 +101,49 @@ def test_values_past_32_bits(sm, wide, streams, att_split, prefill_rows):
         assert np.abs(v[:64]).min() > 2 ** 31                 # the planted head: every value past 32 bits
         assert np.array_equal(m.read("v64", 0, 0, p), v)
         assert np.array_equal(m.read("v", 0, 0, p), v.astype(np.int32))   # the low 32 bits beside them
+    m.close()
+
+
+@pytest.fixture(scope="module")
+def py_wide(sm, py_small_npz, tmp_path_factory):
+    """the small Pythia model with layer 0's head-0 value columns (128-191 of the interleaved q, k, v) scaled by
+    2^16 through their exponents, laid out: about a third of those values past 32 bits, varying with the position,
+    while the attention sum stays below the reference's 2^62 assert (pythia_base2.py:139)"""
+    from oracle.pythia import PythiaOracle
+    npz = dict(py_small_npz)
+    e = np.array(npz["qkv.0.e"]).copy()
+    e[128:192] += 16
+    npz["qkv.0.e"] = e
+    d = sm.pythia.pythia_layout(npz, str(tmp_path_factory.mktemp("py_wide_layout")))
+    return d, PythiaOracle(npz)
+
+
+@pytest.mark.parametrize("streams,att_split", [(1, 0), (1, 1), (3, 0)], ids=["one_block", "spread", "three_streams"])
+def test_pythia_values_past_32_bits(sm, py_wide, streams, att_split):
+    """the Pythia machine with values past 32 bits in one head: the oracle's words, layer 0's attention row at the
+    last step (stream 0) and the cache's whole values"""
+    from oracle.pythia import new_record
+    d, orc = py_wide
+    prompts = [sm.prompt_ids(60 + b, 8, 1000) for b in range(streams)]
+    m = sm.Machine(d, max_ctx=64, max_streams=streams, att_split=att_split)
+    m.reset()
+    m.record_at(len(prompts[0]) + 8 - 2)
+    for b, p in enumerate(prompts):
+        m.prefill(p, b)
+    got = [[int(w) for w in row] for row in m.generate(8)]
+    for b in range(streams):
+        assert got[b] == orc.generate(prompts[b], 8, 64), f"stream {b}"
+    s = orc.session(64)
+    seq = prompts[0] + got[0]
+    rec = new_record(orc.vocab)
+    for i, t in enumerate(seq[:-1]):
+        s.step(t, want_head=False, rec=rec if i == len(seq) - 2 else None)
+    assert np.array_equal(m.read("att")[0], rec["att"][0])
+    wide = 0
+    for p in range(len(seq) - 1):
+        v = s.read_kv(0, p)[2]
+        wide += int((np.abs(v[:64]) > 2 ** 31).any())
+        assert np.array_equal(m.read("v64", 0, 0, p), v)
+        assert np.array_equal(m.read("v", 0, 0, p), v.astype(np.int32))
+    assert wide >= 8                                            # most positions hold a value past 32 bits
     m.close()
