@@ -72,7 +72,8 @@ typedef struct {
     int32_t att_split;     /* batch 1: decode steps at positions from this one on run the attention spread over the
                               GPU, each head's cached positions in chunks of 64, one block a chunk (the chunks'
                               scores and maxima, then arrivals against the head's maximum and the value sums added
-                              exactly, then the divisor: three launches); steps before it run one block a head.
+                              exactly: two launches; the divisor and the output row are then formed by the next
+                              phase's blocks); steps before it run one block a head.
                               0: from position 160; -1: never.  The same numbers either way (base2.py:85-100) */
     int32_t v64;           /* the value cache (base2.py's attention weighs each raw int64 value): every value's low
                               32 bits, and a row holding a value past 32 bits also whole; a head holding such a row

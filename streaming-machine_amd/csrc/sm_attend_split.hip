@@ -1,6 +1,7 @@
 // The batch-1 attention spread over the GPU: one new position's attention (base2.py:85-100 for the last row;
 // foundation0/pythia_base2.py:125-141) with each head's cached positions cut into chunks of ACH_SPLIT, one block a
-// (head, chunk), in three launches:
+// (head, chunk), in three launches (the machine launches the first two, and proj's blocks then form the output row
+// from the accumulators themselves: PRO_ATT / PRO_PATT in sm_kernels.hip; the stage entry point launches all three):
 //   k_att_scores  the new q (and, in the chunk holding p, the new k and v into the cache) through their water
 //                 levels (base2.py:93); the chunk's scores rshift(q16 . k16, -(eq + ek + 7)) (base2.py:94) into
 //                 a score row, and the chunk's maximum; block (h, 0) empties the head's accumulator

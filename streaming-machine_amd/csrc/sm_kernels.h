@@ -10,7 +10,11 @@ enum { PRO_GAUGE = 0,   // gauge_log of the stream row R (768): x16, ex, LS (bas
        // batched streams: the producing bank's epilogue from its partial piles, then the light
        PRO_ADD_GAUGE = 4,   // R += rshift(pile, -(we + ex + 16)) + b, then PRO_GAUGE of R   (base2.py:105-106, 55-60)
        // the Pythia machine (foundation0/pythia_base2.py)
-       PRO_PGAUGE = 6 };    // its gauge with the norm's gain and offset, then to16 of that row     (:100-110, 113)
+       PRO_PGAUGE = 6,      // its gauge with the norm's gain and offset, then to16 of that row     (:100-110, 113)
+       // batch 1 with the attention spread over chunks of positions (sm_attend_split.hip): the row is the attention's
+       // output, formed by every block from the heads' summed accumulators (aacc), then PRO_TO16 of it
+       PRO_ATT = 7,         // GPT-2: power(num, -log2fix(Z))                                        (base2.py:99)
+       PRO_PATT = 8 };      // Pythia: the same power exact in 128 bits, with the reference's asserts (:139, 90)
 // epilogue: what a phase does with each finished pile
 enum { EPI_GAUGED = 0,       // power(pile, (we + ex + 16) 65536 - LS) + b          (base2.py:70-71)
        EPI_GAUGED_EDGE = 1,  // the same, then the edge                               (base2.py:106, 78-83)
@@ -88,6 +92,9 @@ struct GemvArgs {
     int* err;                                  // the Pythia machine: its rshift assert sets SM_ERR_RANGE here
     const char* pf; int pf_lines; int pf_nblk;       // plate, lines a next-kernel block reads, the next grid
     int pf_total;                                    // the plate's lines (none past them is requested)
+    // PRO_ATT / PRO_PATT: the heads' accumulators [12][68] (64 value sums, the arrival sum, the largest weighed |v|)
+    // and the attention row's record slot (block 0 writes it at the recorded position)
+    const i64* aacc; i64* ratt;
 };
 #define TOP_ITERS 8                 // EPI_TOP1: tiles a wave may finish (the grid is sized for it)
 

@@ -98,6 +98,20 @@ SMD i64 edge_erf(i64 H) {
 template <int NIN, int NT, int PRO>
 SMD void prologue_load(const GemvArgs& a, int tid, i64 (&v)[NIN / NT], int (&gq)[NIN / NT], i64 (&bq)[NIN / NT]) {
     constexpr int PER = NIN / NT;
+    if constexpr (PRO == PRO_ATT || PRO == PRO_PATT) {
+        // element 64 h + d: head h's value sum d; thread t < 12 also head t's arrival sum (bq[0]) and largest
+        // weighed |v| (bq[1]); bounded loads, no branch
+        static_assert(NIN == 768 && PER >= 2, "the attention row is 768 wide");
+#pragma unroll
+        for (int m = 0; m < PER; m++) {
+            const int i = tid + NT * m;
+            v[m] = a.aacc[(i >> 6) * 68 + (i & 63)];
+        }
+        const __amdgpu_buffer_rsrc_t ra = buf_rsrc(a.aacc, 12u * 68u * 8u);
+        bq[0] = buf_load8(ra, (unsigned)(tid * 68 + 64) * 8u);
+        bq[1] = buf_load8(ra, (unsigned)(tid * 68 + 65) * 8u);
+        return;
+    }
 #pragma unroll
     for (int m = 0; m < PER; m++) v[m] = a.X[tid + NT * m];
     if (PRO == PRO_PGAUGE) {
@@ -279,6 +293,43 @@ SMD void prologue(const GemvArgs& a, int tid, const i64 (&vin)[NIN / NT], short*
     e2_o = e2;
 }
 
+// PRO_ATT / PRO_PATT: the attention row from the heads' accumulators, k_att_finish's arithmetic in every block
+// (base2.py:99; pythia_base2.py:139, 90).  Thread t < 12 forms head t's divisor, -log2fix(Z) and its power
+// factor (one gather of the two table entries for the twelve heads), into fz; after one barrier v[m] turns from
+// head h's value sum into its output.  zq: thread t < 12's arrival sum and largest weighed |v|.  Block 0 raises
+// the Pythia asserts and writes the record.
+template <int NT, bool PY>
+SMD void att_row(const GemvArgs& a, int tid, i64 (&v)[768 / NT], const i64 (&zq)[768 / NT], int* fz, bool rec) {
+    constexpr int PER = 768 / NT;
+    if (tid < 12) {
+        int zt;
+        i64 zm;
+        log2_parts(zq[0], zt, zm);
+        fz[2 * tid] = -(zt * 65536 + (int)tab_log2(a.tb, zm));          // -log2fix(Z): |.| < 2^23
+        fz[2 * tid + 1] = (int)tab_hpow(a.tb, zm);
+        if (PY && blockIdx.x == 0 && a.err && (double)zq[1] * (double)zq[0] >= 4611686018427387904.0)
+            atomicOr(a.err, SM_ERR_RANGE);
+    }
+    __syncthreads();
+#pragma unroll
+    for (int m = 0; m < PER; m++) {
+        const int i = tid + NT * m, h = i >> 6;
+        const i64 F = fz[2 * h], zhp = fz[2 * h + 1];
+        i64 o;
+        if constexpr (PY) {
+            const __int128 X = (__int128)v[m] * zhp;
+            const i64 sft = 16 - (F >> 16);
+            const __int128 r = sft >= 100 ? (__int128)0 : (X + ((__int128)1 << (sft - 1))) >> sft;
+            if (blockIdx.x == 0 && a.err && (r > (__int128)INT64_MAX || r < (__int128)INT64_MIN)) atomicOr(a.err, SM_ERR_RANGE);
+            o = (i64)r;
+        } else {
+            o = power_e(v[m], F, F & 0xFFFF, zhp, a.tb);
+        }
+        v[m] = o;
+        if (rec && blockIdx.x == 0 && a.ratt) a.ratt[i] = o;
+    }
+}
+
 // ---------------------------------------------------------------------------------------------------------
 // One wave's share of a tile: U units of 16 bytes per lane (unit u = lane + 64 m).  WB: bytes a weight (2: the
 // int16 plate; 1: the top read's high-byte plane, w >> 8)
@@ -342,7 +393,7 @@ __global__ __launch_bounds__(64 * WPB) void k_gemv(GemvArgs a) {
     constexpr bool INV = MODE & MODE_INV;
     constexpr bool FG = (MODE & MODE_FGAUGE) && (PRO == PRO_GAUGE || PRO == PRO_PGAUGE);
     constexpr bool FE = (MODE & MODE_FEDGE) && (EPI == EPI_GAUGED_EDGE || EPI == EPI_PLAIN_EDGE);
-    static_assert(!INV || PRO == PRO_GAUGE || PRO == PRO_TO16, "the complement machine is GPT-2's");
+    static_assert(!INV || PRO == PRO_GAUGE || PRO == PRO_TO16 || PRO == PRO_ATT, "the complement machine is GPT-2's");
     constexpr bool TOP = EPI == EPI_TOP1;
     constexpr bool SPLIT = MODE & MODE_SPLIT;
     static_assert(!SPLIT || (!TOP && !INV), "split plates are the Pythia machine's");
@@ -353,6 +404,7 @@ __global__ __launch_bounds__(64 * WPB) void k_gemv(GemvArgs a) {
     __shared__ __align__(16) short xl_s[NIN];
     __shared__ double xf_s[FG ? 768 : 1];
     __shared__ int red[96];        // prologue: OR words [0, 24), sums [32, 68), second OR [72, 96)
+    __shared__ int fz[PRO == PRO_ATT || PRO == PRO_PATT ? 24 : 1];   // the heads' divisors (att_row)
     __shared__ i64 bestv[WPB];
     __shared__ int besti[WPB];
     // EPI_TOP1: each finished word of the block (slot (wave, tile of the wave, column)): word, high bound, coarse pile
@@ -418,6 +470,7 @@ __global__ __launch_bounds__(64 * WPB) void k_gemv(GemvArgs a) {
         const bool rec = REC && a.rec_pos && *a.rec_pos == (a.pos ? *a.pos : -2);
         i64 ex, ls = 0, e2 = 0, sx = 0, nn = 0;
         double sig = 1.0;
+        if constexpr (PRO == PRO_ATT || PRO == PRO_PATT) att_row<NT, PRO == PRO_PATT>(a, tid, row, nbq, fz, rec);
         if constexpr (PRO == PRO_PGAUGE)
             prologue_py<NT, FG>(a, tid, row, ngq, nbq, xh_s, xl_s, red, xf_s, ex, rec && blockIdx.x == 0);
         else
@@ -1567,6 +1620,8 @@ __global__ __launch_bounds__(1024) void k_stage_race(const i64* v, i64 n, i64* o
     template __global__ void k_gemv<NIN, TC, WPB, PRO, EPI, 1>(GemvArgs);
 INST(768, 2, 4, PRO_GAUGE, EPI_GAUGED)        // qkv
 INST(768, 2, 2, PRO_TO16, EPI_PLAIN_ADD)      // proj
+INST(768, 2, 2, PRO_ATT, EPI_PLAIN_ADD)       // proj after the attention spread over chunks (GPT-2)
+INST(768, 2, 2, PRO_PATT, EPI_PLAIN_ADD)      // (Pythia)
 INST(768, 2, 4, PRO_GAUGE, EPI_GAUGED_EDGE)   // fc
 INST(3072, 1, 4, PRO_TO16, EPI_PLAIN_ADD)     // mproj
 INST(768, 4, 4, PRO_GAUGE, EPI_HEAD)          // head (the race in its own kernel)

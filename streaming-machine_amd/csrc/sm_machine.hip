@@ -727,10 +727,11 @@ static void set_pf_head(sm_machine* m, GemvArgs& a) {
 // a batch-1 GEMV phase: rec selects the instantiation that records (launched only for the recorded step), the
 // machine's MODE bits the rest (only those the phase has; the complement machine is never mixed with float stages)
 static constexpr int phase_modes(int PRO, int EPI) {
-    return (PRO == PRO_GAUGE || PRO == PRO_TO16 ? MODE_INV : 0) | (PRO == PRO_GAUGE || PRO == PRO_PGAUGE ? MODE_FGAUGE : 0) |
+    return (PRO == PRO_GAUGE || PRO == PRO_TO16 || PRO == PRO_ATT ? MODE_INV : 0) |
+           (PRO == PRO_GAUGE || PRO == PRO_PGAUGE ? MODE_FGAUGE : 0) |
            (EPI == EPI_GAUGED_EDGE || EPI == EPI_PLAIN_EDGE ? MODE_FEDGE : 0) |
-           ((PRO == PRO_PGAUGE || PRO == PRO_TO16) && (EPI == EPI_PLAIN || EPI == EPI_PLAIN_EDGE || EPI == EPI_PHEAD ||
-                                                       EPI == EPI_PLAIN_ADD) ? MODE_SPLIT : 0);
+           ((PRO == PRO_PGAUGE || PRO == PRO_TO16 || PRO == PRO_PATT) &&
+                    (EPI == EPI_PLAIN || EPI == EPI_PLAIN_EDGE || EPI == EPI_PHEAD || EPI == EPI_PLAIN_ADD) ? MODE_SPLIT : 0);
 }
 template <int NIN, int TC, int WPB, int PRO, int EPI, int M = 0>
 static void gemv_mode(sm_machine* m, int mode, bool rec, const char* name, int grid, const GemvArgs& a) {
@@ -754,13 +755,13 @@ template <int MODEL, int FTURN>
 static void attend1_t(sm_machine* m, bool rec, AttArgs a) {
     if constexpr (!FTURN) {
         if (m->att_long) {                    // the attention spread over chunks of positions (sm_attend_split.hip)
+            // two launches: the divisor and the output row are formed by proj's blocks from the accumulators
+            // (PRO_ATT / PRO_PATT), in place of k_att_finish
             a.asc = m->asc; a.acm = m->acm; a.aacc = m->aacc; a.ncm = m->ncm;
             const dim3 grid(12, m->ncm);
             launch(m->cfg.profile, "attend.scores", k_att_scores<MODEL>, grid, dim3(256), 0, m->st, a);
             if (m->T.verified) launch(m->cfg.profile, "attend.mix", k_att_mix<MODEL, 1>, grid, dim3(256), 0, m->st, a);
             else launch(m->cfg.profile, "attend.mix", k_att_mix<MODEL, 0>, grid, dim3(256), 0, m->st, a);
-            if (rec) launch(m->cfg.profile, "attend.finish", k_att_finish<MODEL, 1>, dim3(12), dim3(64), 0, m->st, a);
-            else launch(m->cfg.profile, "attend.finish", k_att_finish<MODEL, 0>, dim3(12), dim3(64), 0, m->st, a);
             return;
         }
     }
@@ -845,7 +846,12 @@ static int launch_step_pythia(sm_machine* m, int parts, bool rec) {
             g.X = m->att; g.Y = m->R; g.Yb = Rin; g.rout = m->r_resid + (l * 2 + 0) * 768;
             set_pf(g, m->bank[l][3], 4, grid4(m->bank[l][3]));
             attend1<1>(m, rec, a, l);
-            gemv<768, 2, 2, PRO_TO16, EPI_PLAIN_ADD>(m, rec, "proj", (P.ntiles + 1) / 2, g);
+            if (m->att_long) {          // the attention's output row formed in proj's blocks
+                g.aacc = m->aacc; g.ratt = m->r_att + l * 768;
+                gemv<768, 2, 2, PRO_PATT, EPI_PLAIN_ADD>(m, rec, "proj", (P.ntiles + 1) / 2, g);
+            } else {
+                gemv<768, 2, 2, PRO_TO16, EPI_PLAIN_ADD>(m, rec, "proj", (P.ntiles + 1) / 2, g);
+            }
         }
         // mproj: plain of the edge row, added to R (Mo)
         {
@@ -1086,7 +1092,12 @@ static int launch_step(sm_machine* m, int parts = STEP_ALL, bool rec = false) {
             g.rpile = m->r_pile + (l * 4 + 1) * 3072; g.rout = m->r_resid + (l * 2 + 0) * 768;
             set_pf(g, m->bank[l][2], 4, grid4(m->bank[l][2]));
             attend1<0>(m, rec, a, l);
-            gemv<768, 2, 2, PRO_TO16, EPI_PLAIN_ADD>(m, rec, "proj", (P.ntiles + 1) / 2, g);
+            if (m->att_long) {          // the attention's output row formed in proj's blocks
+                g.aacc = m->aacc; g.ratt = m->r_att + l * 768;
+                gemv<768, 2, 2, PRO_ATT, EPI_PLAIN_ADD>(m, rec, "proj", (P.ntiles + 1) / 2, g);
+            } else {
+                gemv<768, 2, 2, PRO_TO16, EPI_PLAIN_ADD>(m, rec, "proj", (P.ntiles + 1) / 2, g);
+            }
         }
         // fc: gauge, product, gauged, edge (base2.py:106)
         {
