@@ -202,12 +202,13 @@ def test_rshift_assert(sm, py_small_npz, tmp_path, streams):
     m.close()
 
 
-@pytest.mark.parametrize("streams", [1, 2])
-def test_plate_and_order_switches(sm, tmp_path, streams):
+@pytest.mark.parametrize("streams,att_split", [(1, 0), (2, 0), (1, 1)])
+def test_plate_and_order_switches(sm, tmp_path, streams, att_split):
     """pythia_base2.py's plates=finished|start|built and order=shuffle (the finished-and-start model of
     modes_golden.json): words and every recorded intermediate of the last position against the reference run
     with each switch (the shuffled machine's intermediates in their shuffled places; plates=built's 17-bit digits
-    as split plates, one stream only)"""
+    as split plates, one stream only); att_split 1: one stream with every step's attention spread over chunks of
+    positions and its output row formed in proj's blocks"""
     from test_oracle_pythia import _modes, modes_npz
     g = _modes()
     if g is None:
@@ -216,7 +217,8 @@ def test_plate_and_order_switches(sm, tmp_path, streams):
         d = str(tmp_path / f"{case['name']}_{streams}")
         sm.pythia.pythia_layout(modes_npz(sm, case), d)
         kw = {s.split("=")[0]: "float" for s in case["switches"] if s.endswith("=float")}
-        if "plates=built" in case["switches"] or kw:  # split digits, float stages: one stream, position by position
+        kw["att_split"] = att_split
+        if "plates=built" in case["switches"] or len(kw) > 1:  # split digits, float stages: one stream, position by position
             if streams > 1:
                 with pytest.raises(sm.SmError):
                     sm.Machine(d, max_ctx=32, max_streams=streams, **kw)
