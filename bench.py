@@ -516,7 +516,7 @@ def attention_leg(sm, reps: int = 50):
 
 # ---- CPU baseline ----
 def floor_leg():
-    """The batch-1 step's launch-structure floor (streaming-machine_amd/floor_probe: the step's 62 dependent launches
+    """The batch-1 step's launch-structure floor (streaming-machine_amd/floor_probe: the step's 61 dependent launches
     with the machine's grids, empty, then reading their rows and plates and writing their outputs with no
     arithmetic), run as a child process before this process initialises the GPU."""
     exe = os.path.join(REPO, "streaming-machine_amd", "floor_probe")
@@ -856,7 +856,8 @@ def main():
         "floor": None if floor is None else {
             **{k: v for k, v in floor.items() if k not in ("b64", "pythia32")},
             "step_us": round(1000.0 * b1["ms"], 2), "step_over_bytes_floor": round(1000.0 * b1["ms"] / floor["bytes_us"], 3),
-            "note": "the step's 62 dependent launches with the machine's grids, replayed from graphs of 15 steps: "
+            "note": "the step's dependent launches with the machine's grids (61 a step: the race of the step before runs "
+                    "in layer 0's qkv, and once after a run's last step), replayed from graphs of 15 steps: "
                     "empty_us with empty kernels, bytes_us with every kernel reading its row and its plate share "
                     "(the whole int16 word table for the head) and writing its outputs, no arithmetic "
                     "(streaming-machine_amd/floor_probe); persistent: the same bytes as one cooperative kernel of "

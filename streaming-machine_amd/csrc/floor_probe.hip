@@ -1,7 +1,9 @@
-// The decode step's launch-structure floor, measured.  Batch 1: the step's 62 dependent launches (12 layers x
-// [qkv, attend, proj, fc, mproj], the head, the race) with the machine's grids and block sizes,
-// replayed from a HIP graph of 15 steps, in two forms:
-//   empty  - every kernel returns at once: the cost of 62 dependent launches alone;
+// The decode step's launch-structure floor, measured.  Batch 1: the step's dependent launches (12 layers x
+// [qkv, attend, proj, fc, mproj], the head) with the machine's grids and block sizes, replayed from a HIP graph of
+// 15 steps as the machine runs them: a step after the first takes the race of the step before into its layer-0
+// qkv (every block reads the head's 512 bests and the chosen word's row), and the race runs once, after the last
+// step (61 launches a step, 916 a graph); two forms:
+//   empty  - every kernel returns at once: the cost of the dependent launches alone;
 //   bytes  - every kernel reads the row it depends on (the previous kernel's output) and its share of its plate
 //            (the GPT-2 124M shapes: int16 plates of 768x2304, 768x768, 768x3072, 3072x768, and the 768 x 50257
 //            word table, read whole as the machine's default head does), the attention reads 16 cached positions
@@ -49,6 +51,37 @@ __global__ __launch_bounds__(64 * WPB) void k_floor_phase(const i64* X, const v4
         else if (lane < TC) Y[t * TC + lane] = a;
     }
     if (HEADK && tid == 0) Y[blockIdx.x] = best;
+}
+// layer 0's qkv with the race of the step before: the head's 512 bests (two a thread), their maximum over the
+// block, the chosen word's row as the entering row (block 0 writes it), then the qkv phase's tiles
+template <bool EMPTY>
+__global__ __launch_bounds__(256) void k_floor_qkv_race(const i64* part, const i64* wte, int nwords, const v4i* W,
+                                                        int ntiles, i64* Y, i64* R0) {
+    if (EMPTY) return;
+    __shared__ i64 wb[4];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    i64 b = max(part[tid], part[tid + 256]);
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) b = max(b, __shfl_xor(b, o, 64));
+    if (lane == 0) wb[wave] = b;
+    __syncthreads();
+    b = max(max(wb[0], wb[1]), max(wb[2], wb[3]));
+    const int word = (int)((unsigned long long)b % (unsigned)nwords);
+    i64 acc = 0;
+#pragma unroll
+    for (int m = 0; m < 3; m++) {
+        const i64 x = wte[(size_t)word * 768 + tid + 256 * m];
+        acc ^= x;
+        if (blockIdx.x == 0) R0[tid + 256 * m] = x;
+    }
+    for (int t = blockIdx.x * 4 + wave; t < ntiles; t += gridDim.x * 4) {
+        const v4i* base = W + (size_t)t * (2 * 768 * 2 / 16) + lane;
+        i64 a = acc;
+#pragma unroll
+        for (int m = 0; m < 3; m++) { const v4i w = base[64 * m]; a += w.x ^ w.y ^ w.z ^ w.w; }
+        a += __shfl_xor(a, 1, 64);
+        if (lane < 2) Y[t * 2 + lane] = a;
+    }
 }
 // one wave a head: the new q, k, v and P cached positions of the head's keys and values
 template <bool EMPTY>
@@ -104,14 +137,15 @@ static int run(double& us) {
             const v4i* wf = (const v4i*)pl; pl += fcB;
             const v4i* wm = (const v4i*)pl; pl += mpB;
             const size_t kv = (size_t)l * 12 * CTX * 64;
-            k_floor_phase<768, 2, 4, 2, EMPTY><<<288, 256, 0, st>>>(R, wq, 1152, QKV);
+            if (l == 0 && s > 0) k_floor_qkv_race<EMPTY><<<288, 256, 0, st>>>(part, wte, WTE, wq, 1152, QKV, R);
+            else k_floor_phase<768, 2, 4, 2, EMPTY><<<288, 256, 0, st>>>(R, wq, 1152, QKV);
             k_floor_attend<EMPTY><<<12, 256, 0, st>>>(QKV, K + kv, V + kv, P, CTX, att);
             k_floor_phase<768, 2, 2, 2, EMPTY><<<192, 128, 0, st>>>(att, wp, 384, R);
             k_floor_phase<768, 2, 4, 2, EMPTY><<<384, 256, 0, st>>>(R, wf, 1536, hid);
             k_floor_phase<3072, 1, 4, 2, EMPTY><<<192, 256, 0, st>>>(hid, wm, 768, R);
         }
         k_floor_phase<768, 4, 4, 2, EMPTY, true><<<512, 256, 0, st>>>(R, (const v4i*)pl, head_tiles, part);
-        k_floor_race<EMPTY><<<1, 256, 0, st>>>(part, 512, wte, WTE, R);
+        if (s == STEPS - 1) k_floor_race<EMPTY><<<1, 256, 0, st>>>(part, 512, wte, WTE, R);
     }
     CHK(hipStreamEndCapture(st, &g));
     CHK(hipGraphInstantiate(&ge, g, nullptr, nullptr, 0));
@@ -607,7 +641,7 @@ int main(int argc, char** argv) {
         epy = e < epy ? e : epy;
         bpy = b < bpy ? b : bpy;
     }
-    printf("{\"launches\": 62, \"empty_us\": %.2f, \"bytes_us\": %.2f, \"ctx\": 16, \"graph_steps\": 15, "
+    printf("{\"launches\": 61.07, \"empty_us\": %.2f, \"bytes_us\": %.2f, \"ctx\": 16, \"graph_steps\": 15, "
            "\"b64\": {\"launches\": 86, \"empty_us\": %.2f, \"bytes_us\": %.2f, \"ctx\": 96, \"graph_steps\": 16}, "
            "\"pythia32\": {\"launches\": 51, \"empty_us\": %.2f, \"bytes_us\": %.2f, \"ctx\": 192, \"graph_steps\": 16}}\n",
            empty, bytes, e64, b64, epy, bpy);

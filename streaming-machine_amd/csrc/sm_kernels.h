@@ -14,7 +14,11 @@ enum { PRO_GAUGE = 0,   // gauge_log of the stream row R (768): x16, ex, LS (bas
        // batch 1 with the attention spread over chunks of positions (sm_attend_split.hip): the row is the attention's
        // output, formed by every block from the heads' summed accumulators (aacc), then PRO_TO16 of it
        PRO_ATT = 7,         // GPT-2: power(num, -log2fix(Z))                                        (base2.py:99)
-       PRO_PATT = 8 };      // Pythia: the same power exact in 128 bits, with the reference's asserts (:139, 90)
+       PRO_PATT = 8,        // Pythia: the same power exact in 128 bits, with the reference's asserts (:139, 90)
+       // batch 1 (GPT-2), layer 0's qkv: the race over the step before's head bests (base2.py:34-40, 114) and the
+       // word fed back as the entering row wte[word] + wpe[q] (base2.py:103), in every block (block 0 writes the
+       // word, the counters, the row and the next position), then PRO_GAUGE of that row: k_race1 folded in
+       PRO_RACE = 9 };
 // epilogue: what a phase does with each finished pile
 enum { EPI_GAUGED = 0,       // power(pile, (we + ex + 16) 65536 - LS) + b          (base2.py:70-71)
        EPI_GAUGED_EDGE = 1,  // the same, then the edge                               (base2.py:106, 78-83)
@@ -59,6 +63,18 @@ struct Rec {
     i64* logits; // [vocab]
 };
 
+// batch 1's race over the head blocks' bests and the next entering row (k_race1, k_embed1, PRO_RACE)
+struct Race1Args {
+    const i64* part_v; const int* part_i; int nblk;
+    int* seq; int* words; int* pos; const int* plen; int* nwords;
+    int* pos_next;              // PRO_RACE: the position slot the race writes (pos holds the step before's)
+    i64* R0;                    // the entering row of the next position
+    int npos;                   // rows of the position table (GPT-2): no entering row past it
+    const i64* wte; const i64* wpe;             // GPT-2
+    const short* ew; const int* ee;             // Pythia
+    const short* ew2;                           // Pythia, split word table (plates=built): the row is ew - ew2
+};
+
 struct GemvArgs {
     const int4* W;              // the plate in column tiles of TC (see sm_machine.hip: tile_plate)
     const int4* W2;             // MODE_SPLIT: the subtracted plate, tiled as W
@@ -95,6 +111,8 @@ struct GemvArgs {
     // PRO_ATT / PRO_PATT: the heads' accumulators [12][68] (64 value sums, the arrival sum, the largest weighed |v|)
     // and the attention row's record slot (block 0 writes it at the recorded position)
     const i64* aacc; i64* ratt;
+    // PRO_RACE: the race of the step before (its head's bests, the word fed back, the counters, the entering row)
+    Race1Args race;
 };
 #define TOP_ITERS 8                 // EPI_TOP1: tiles a wave may finish (the grid is sized for it)
 
@@ -112,15 +130,7 @@ SMD bool race_beats(i64 a, int ai, i64 b, int bi) {
 
 // Batch 1: the race over the head blocks' bests, the word fed back, and the next position's entering row
 // (base2.py:103: wte[word] + wpe[p]; foundation0/pythia_base2.py:153: rshift(embed.w[word], -(embed.e[word] + 16)))
-struct Race1Args {
-    const i64* part_v; const int* part_i; int nblk;
-    int* seq; int* words; int* pos; const int* plen; int* nwords;
-    i64* R0;                    // the entering row of the next position
-    int npos;                   // rows of the position table (GPT-2): no entering row past it
-    const i64* wte; const i64* wpe;             // GPT-2
-    const short* ew; const int* ee;             // Pythia
-    const short* ew2;                           // Pythia, split word table (plates=built): the row is ew - ew2
-};
+
 
 // The collapsing top read's second stage, batch 1 (one block): the survivors' low bytes, their exact scores, the
 // race, then k_race1's word feed and entering row

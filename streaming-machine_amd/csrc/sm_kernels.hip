@@ -98,6 +98,25 @@ SMD i64 edge_erf(i64 H) {
 template <int NIN, int NT, int PRO>
 SMD void prologue_load(const GemvArgs& a, int tid, i64 (&v)[NIN / NT], int (&gq)[NIN / NT], i64 (&bq)[NIN / NT]) {
     constexpr int PER = NIN / NT;
+    if constexpr (PRO == PRO_RACE) {
+        // the step before's head bests (two a thread; bounded loads, a best past the last block reads as none),
+        // then its position and the next position's row of wpe; the word's wte row follows the race (race_row)
+        static_assert(NIN == 768 && NT == 256, "layer 0's qkv: 768 inputs over 256 threads");
+        const Race1Args& r = a.race;
+        const __amdgpu_buffer_rsrc_t rv = buf_rsrc(r.part_v, (unsigned)r.nblk * 8u), ri = buf_rsrc(r.part_i, (unsigned)r.nblk * 4u);
+#pragma unroll
+        for (int k = 0; k < 2; k++) {
+            const int g = tid + 256 * k;
+            bq[k] = buf_load8(rv, (unsigned)g * 8u);
+            const int i = buf_load1(ri, (unsigned)g * 4u);
+            gq[k] = g < r.nblk ? i : -1;
+        }
+        const int q = *r.pos + 1;                       // (no row of wpe past its last position: zeros)
+        const __amdgpu_buffer_rsrc_t rp = buf_rsrc(r.wpe + (size_t)(q < r.npos ? q : 0) * 768, q < r.npos ? 768u * 8u : 0u);
+#pragma unroll
+        for (int m = 0; m < PER; m++) v[m] = buf_load8(rp, (unsigned)(tid + NT * m) * 8u);
+        return;
+    }
     if constexpr (PRO == PRO_ATT || PRO == PRO_PATT) {
         // element 64 h + d: head h's value sum d; thread t < 12 also head t's arrival sum (bq[0]) and largest
         // weighed |v| (bq[1]); bounded loads, no branch
@@ -293,6 +312,56 @@ SMD void prologue(const GemvArgs& a, int tid, const i64 (&vin)[NIN / NT], short*
     e2_o = e2;
 }
 
+// PRO_RACE: the race over the step before's head bests (race1_finish's arithmetic, in every block), the word fed
+// back: v[m] turns from the next position's wpe row into the entering row wte[word] + wpe[q] (base2.py:103).
+// A prompt position's next word is the prompt's.  Block 0 writes the word, the counters, the next position slot
+// and the row (proj's layer-0 addition reads it).  pv, pi: the thread's two bests; bvs, bis: a slot a wave.
+template <int NT>
+SMD void race_row(const GemvArgs& a, int tid, i64 (&v)[768 / NT], const i64 (&pv)[768 / NT], const int (&pi)[768 / NT],
+                  i64* bvs, int* bis, int* tok_s) {
+    constexpr int PER = 768 / NT, NW = NT / 64;
+    const Race1Args& r = a.race;
+    const int lane = tid & 63, wave = tid >> 6;
+    i64 bv = 0;
+    int bi = -1;
+#pragma unroll
+    for (int k = 0; k < 2; k++)
+        if (race_beats<0>(pv[k], pi[k], bv, bi)) { bv = pv[k]; bi = pi[k]; }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        const i64 ov = __shfl_xor(bv, o, 64);
+        const int oi = __shfl_xor(bi, o, 64);
+        if (race_beats<0>(ov, oi, bv, bi)) { bv = ov; bi = oi; }
+    }
+    if (lane == 0) { bvs[wave] = bv; bis[wave] = bi; }
+    __syncthreads();
+    if (tid == 0) {
+        bv = bvs[0]; bi = bis[0];
+        for (int w = 1; w < NW; w++)
+            if (race_beats<0>(bvs[w], bis[w], bv, bi)) { bv = bvs[w]; bi = bis[w]; }
+        const int p = *r.pos, plen = *r.plen, q = p + 1;
+        const bool known = p < plen - 1;                // a prompt position: the next word is the prompt's
+        const int tok = known ? r.seq[q] : bi;
+        if (blockIdx.x == 0) {
+            if (!known) {
+                r.seq[q] = bi;
+                r.words[q - plen] = bi;
+            }
+            *r.nwords = q - plen + 1;
+            *r.pos_next = q;
+        }
+        *tok_s = tok;
+    }
+    __syncthreads();
+    const size_t tok = (size_t)*tok_s;
+#pragma unroll
+    for (int m = 0; m < PER; m++) {
+        const int i = tid + NT * m;
+        v[m] = wadd(r.wte[tok * 768 + i], v[m]);
+        if (blockIdx.x == 0) r.R0[i] = v[m];
+    }
+}
+
 // PRO_ATT / PRO_PATT: the attention row from the heads' accumulators, k_att_finish's arithmetic in every block
 // (base2.py:99; pythia_base2.py:139, 90).  Thread t < 12 forms head t's divisor, -log2fix(Z) and its power
 // factor (one gather of the two table entries for the twelve heads), into fz; after one barrier v[m] turns from
@@ -405,6 +474,7 @@ __global__ __launch_bounds__(64 * WPB) void k_gemv(GemvArgs a) {
     __shared__ double xf_s[FG ? 768 : 1];
     __shared__ int red[96];        // prologue: OR words [0, 24), sums [32, 68), second OR [72, 96)
     __shared__ int fz[PRO == PRO_ATT || PRO == PRO_PATT ? 24 : 1];   // the heads' divisors (att_row)
+    __shared__ int race_tok;                                         // PRO_RACE: the word fed back
     __shared__ i64 bestv[WPB];
     __shared__ int besti[WPB];
     // EPI_TOP1: each finished word of the block (slot (wave, tile of the wave, column)): word, high bound, coarse pile
@@ -467,15 +537,17 @@ __global__ __launch_bounds__(64 * WPB) void k_gemv(GemvArgs a) {
                 pfs += *reinterpret_cast<const int*>(pb + off);
             }
         }
-        const bool rec = REC && a.rec_pos && *a.rec_pos == (a.pos ? *a.pos : -2);
+        // (PRO_RACE: a.pos holds the step before's position)
+        const bool rec = REC && a.rec_pos && *a.rec_pos == (a.pos ? *a.pos + (PRO == PRO_RACE ? 1 : 0) : -2);
         i64 ex, ls = 0, e2 = 0, sx = 0, nn = 0;
         double sig = 1.0;
         if constexpr (PRO == PRO_ATT || PRO == PRO_PATT) att_row<NT, PRO == PRO_PATT>(a, tid, row, nbq, fz, rec);
+        if constexpr (PRO == PRO_RACE) race_row<NT>(a, tid, row, nbq, ngq, bestv, besti, &race_tok);
         if constexpr (PRO == PRO_PGAUGE)
             prologue_py<NT, FG>(a, tid, row, ngq, nbq, xh_s, xl_s, red, xf_s, ex, rec && blockIdx.x == 0);
         else
-            prologue<NIN, NT, PRO, MODE, TOP>(a, tid, row, xh_s, xl_s, red, xf_s, ex, ls, e2, sx, sig, nn,
-                                              rec && blockIdx.x == 0);
+            prologue<NIN, NT, PRO == PRO_RACE ? PRO_GAUGE : PRO, MODE, TOP>(a, tid, row, xh_s, xl_s, red, xf_s, ex, ls, e2,
+                                                                          sx, sig, nn, rec && blockIdx.x == 0);
         const i64 fe = wsub(0, ls) & 0xFFFF;          // the fine part of (we + ex + 16) 65536 - LS for every column
         const i64 np = wsub(sx, nn);                  // EPI_TOP1: the sum of the light's positive values
         int it = 0;                                   // EPI_TOP1: tiles this wave has finished
@@ -1619,6 +1691,7 @@ __global__ __launch_bounds__(1024) void k_stage_race(const i64* v, i64 n, i64* o
 #define INST(NIN, TC, WPB, PRO, EPI) template __global__ void k_gemv<NIN, TC, WPB, PRO, EPI, 0>(GemvArgs); \
     template __global__ void k_gemv<NIN, TC, WPB, PRO, EPI, 1>(GemvArgs);
 INST(768, 2, 4, PRO_GAUGE, EPI_GAUGED)        // qkv
+INST(768, 2, 4, PRO_RACE, EPI_GAUGED)         // layer 0's qkv with the step before's race
 INST(768, 2, 2, PRO_TO16, EPI_PLAIN_ADD)      // proj
 INST(768, 2, 2, PRO_ATT, EPI_PLAIN_ADD)       // proj after the attention spread over chunks (GPT-2)
 INST(768, 2, 2, PRO_PATT, EPI_PLAIN_ADD)      // (Pythia)

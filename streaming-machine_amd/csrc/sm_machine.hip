@@ -377,6 +377,9 @@ struct sm_machine {
     // turn and arrival
     int mode = 0;
     bool fturn = false, farr = false;
+    // batch 1, GPT-2 with every stage integer, the full head read and the plain stream: a run's steps after its
+    // first take the race of the step before into layer 0's qkv (PRO_RACE), and the run ends with k_race1
+    bool fold = false;
     // batch 1: steps at positions from att_split on run the attention spread over chunks of positions (-1: never);
     // att_long is the structure of the steps being launched or captured
     int att_split = -1;
@@ -685,7 +688,8 @@ static Race1Args race1_args(sm_machine* m) {
     int* ctl = m->ctl;
     Race1Args r{};
     r.part_v = m->part_v; r.part_i = m->part_i; r.nblk = m->head_grid;
-    r.seq = m->seq; r.words = m->words; r.pos = ctl + CTL_POS; r.plen = ctl + CTL_PLEN; r.nwords = ctl + CTL_NWORDS;
+    r.seq = m->seq; r.words = m->words; r.pos = ctl + (m->par ? CTL_POS1 : CTL_POS); r.plen = ctl + CTL_PLEN;
+    r.nwords = ctl + CTL_NWORDS;
     r.R0 = m->R0;
     r.npos = m->kind == 1 ? m->ctx : m->npos;
     r.wte = m->wte; r.wpe = m->wpe; r.ew = m->ew; r.ee = m->ee; r.ew2 = m->ew2;
@@ -1038,7 +1042,9 @@ static int launch_step_pythia_batched(sm_machine* m, int parts, int nrows = 0,
 }
 
 // rec (batch 1): the step runs the kernels that record (sm_record_at's position)
-static int launch_step(sm_machine* m, int parts = STEP_ALL, bool rec = false) {
+// fused: batch 1 (m->fold), the race of the step before runs in this step's layer-0 qkv; race: the step ends
+// with k_race1 (a run's last step; the other machines always race at the step's end)
+static int launch_step(sm_machine* m, int parts = STEP_ALL, bool rec = false, bool fused = false, bool race = true) {
     if (m->kind == 1 && m->B > 1) {
         const int RT = (m->B + 15) / 16;
         if (RT == 1) return launch_step_pythia_batched<1>(m, parts);
@@ -1056,12 +1062,21 @@ static int launch_step(sm_machine* m, int parts = STEP_ALL, bool rec = false) {
     }
     const Tables tb = m->T.tb();
     int* ctl = m->ctl;
+    // the step's position slot.  With the race of the step before folded in, layer 0's qkv reads that step's slot
+    // and writes the other one, which every later kernel of this step reads (the slots alternate step by step)
+    const bool fold = m->fold && fused && parts == STEP_ALL;
+    if (!m->fold || parts != STEP_ALL) race = true;
+    int* const posA = ctl + (m->par ? CTL_POS1 : CTL_POS);
+    int* const posp = fold ? ctl + (m->par ? CTL_POS : CTL_POS1) : posA;
+    Race1Args rfold = race1_args(m);
+    rfold.pos = posA; rfold.pos_next = posp;
+    if (fold) m->par ^= 1;
     for (int l = 0; l < 12 && (parts & STEP_LAYERS); l++) {
         GemvArgs base{};
         base.tb = tb;
-        base.pos = ctl + CTL_POS;
+        base.pos = posp;
         base.rec_pos = ctl + CTL_RECPOS;
-        const i64* Rin = l == 0 ? m->R0 : m->R;        // layer 0 reads the entering row (k_race1 / k_embed1)
+        const i64* Rin = l == 0 ? m->R0 : m->R;        // layer 0 reads the entering row (k_race1 / k_embed1 / PRO_RACE)
         // qkv: the stream's gauge, the product, power + bias (base2.py:105 gauged_bank(R, "qkv.l"))
         {
             GemvArgs a = base;
@@ -1071,7 +1086,12 @@ static int launch_step(sm_machine* m, int parts = STEP_ALL, bool rec = false) {
             a.rx16 = m->r_x16 + (l * 4 + 0) * 3072; a.rexls = m->r_exls + (l * 4 + 0) * 2;
             a.rpile = m->r_pile + (l * 4 + 0) * 3072; a.rout = m->r_qkv + l * 2304;
             set_pf(a, m->bank[l][1], 2, grid2(m->bank[l][1]));
-            gemv<768, 2, 4, PRO_GAUGE, EPI_GAUGED>(m, rec, "qkv", (P.ntiles + 3) / 4, a);
+            if (l == 0 && fold) {       // the race of the step before, then the gauge of the row it feeds back
+                a.pos = posA; a.race = rfold;
+                gemv<768, 2, 4, PRO_RACE, EPI_GAUGED>(m, rec, "qkv", (P.ntiles + 3) / 4, a);
+            } else {
+                gemv<768, 2, 4, PRO_GAUGE, EPI_GAUGED>(m, rec, "qkv", (P.ntiles + 3) / 4, a);
+            }
         }
         // attention (base2.py:85-100) on the KV cache of layer l
         {
@@ -1080,7 +1100,7 @@ static int launch_step(sm_machine* m, int parts = STEP_ALL, bool rec = false) {
             a.QKV = m->QKV; a.K16 = m->K16 + l * per * 768; a.KM = m->KM + l * per * 12; a.EK = m->EK + l * per * 12; a.V = m->V + l * per * 768;
             a.V64 = m->V64 ? m->V64 + l * per * 768 : nullptr; a.VW = m->VW ? m->VW + l * per * 12 : nullptr;
             a.vbig = m->vbig ? m->vbig + (size_t)l * m->B * 12 : nullptr;
-            a.out = m->att; a.pos = ctl + CTL_POS; a.ctx = m->ctx; a.tb = tb; a.err = ctl + CTL_ERR;
+            a.out = m->att; a.pos = posp; a.ctx = m->ctx; a.tb = tb; a.err = ctl + CTL_ERR;
             a.rec_pos = ctl + CTL_RECPOS; a.ratt = m->r_att + l * 768;
             // proj: to16 of the attention row, product, plain shift + bias, added to R (base2.py:105; layer 0: to
             // the entering row)
@@ -1127,7 +1147,7 @@ static int launch_step(sm_machine* m, int parts = STEP_ALL, bool rec = false) {
     if (parts & STEP_HEAD) {
         GemvArgs a{};
         a.tb = tb;
-        a.pos = ctl + CTL_POS; a.rec_pos = ctl + CTL_RECPOS;
+        a.pos = posp; a.rec_pos = ctl + CTL_RECPOS;
         const DevPlate& P = m->head;
         a.W = reinterpret_cast<const int4*>(P.W); a.we = P.e; a.bias = P.b; a.sw = P.sw; a.nout = P.nout; a.ntiles = P.ntiles;
         a.X = m->R;
@@ -1149,7 +1169,7 @@ static int launch_step(sm_machine* m, int parts = STEP_ALL, bool rec = false) {
             launch(m->cfg.profile, "race.top", k_race_top, dim3(1), dim3(256), 0, m->st, t);
         } else {
             gemv<768, HEAD_TC, HEAD_WPB, PRO_GAUGE, EPI_HEAD>(m, rec, "head", m->head_grid, a);
-            launch_race1(m);
+            if (race) launch_race1(m);
         }
     }
     HIP_TRY(hipGetLastError());
@@ -1250,6 +1270,7 @@ extern "C" int sm_create(const char* layout_dir, const sm_config* cfg, sm_machin
     m->farr = c.float_stages & SM_FLOAT_ARRIVAL;
     // the spread attention: batch 1 with the integer arrival and turn
     if (m->B == 1 && !m->farr && !m->fturn && c.att_split != -1) m->att_split = c.att_split > 0 ? c.att_split : SM_ATT_SPLIT_AT;
+    m->fold = m->B == 1 && !py && m->mode == 0 && !m->farr && !c.top_read;
     const bool mfma = m->B > 1 || c.prefill_rows > 0;     // the MFMA banks: batched streams or prompt passes
 
     auto bail = [&](int code) { machine_free(m); return code; };
@@ -1506,7 +1527,9 @@ static int capture(sm_machine* m, int which, int n, int parts) {
     if (m->gexec[which][p0]) return SM_OK;
     HIP_TRY(hipStreamBeginCapture(m->st, hipStreamCaptureModeThreadLocal));
     int rc = SM_OK;
-    for (int s = 0; s < n && !rc; s++) rc = launch_step(m, parts);
+    // (a run: its first step takes the entering row already written, the later ones fold in the race of the step
+    // before, and the last one races)
+    for (int s = 0; s < n && !rc; s++) rc = launch_step(m, parts, false, s > 0, s == n - 1);
     m->gflip[which] = m->par != p0;
     m->par = p0;
     hipGraph_t g = nullptr;
@@ -1537,8 +1560,8 @@ static int queue_run(sm_machine* m, int steps) {
         for (; steps > 0; steps--)
             if ((rc = replay(m, g + 1, 1, STEP_ALL))) return rc;
     } else {
-        for (; steps > 0; steps--)
-            if ((rc = launch_step(m))) return rc;
+        for (int s = 0; s < steps; s++)
+            if ((rc = launch_step(m, STEP_ALL, false, s > 0, s == steps - 1))) return rc;
     }
     return SM_OK;
 }
