@@ -35,6 +35,10 @@ struct LightArgs {
     i64* rpile_in; i64* rout_in;                  // stream 0's record of the producing bank
     const int* sfacts;                            // its K slices' light facts [KSP][rows][4]: SXh, SXl, n32768, ex
     const int* rowmap;                            // prompt rows (PRO_EMBED): stream << 16 | position per row
+    // PRO_RACE_EMBED: the step before's head bests [rows][nblk], the words, the counters and the position slot the
+    // race writes (pos: the step before's)
+    const i64* part_v; const int* part_i; int nblk;
+    int* words; int words_stride; int* seqw; int* nwords; int* pos_next;
     int ls_row;                                   // gauged: slots 1-3 carry LS lo, LS hi and EXP2[-LS & 0xFFFF]
                                                   // in place of S1, S2 (the head's light)
 };
@@ -115,6 +119,21 @@ __global__ __launch_bounds__(NT) void k_light(LightArgs a) {
         i_sxh = ri[4]; i_sxl = ri[5]; i_n32 = ri[6];
     }
     constexpr int GA = PRO == PRO_ADD_GAUGE ? GPT : 1, KA = PRO == PRO_ADD_GAUGE ? KSP : 1;
+    // PRO_RACE_EMBED: this stream's bests from the step before's head (bounded loads: past the last block none)
+    constexpr int RB = PRO == PRO_RACE_EMBED ? (512 + NT - 1) / NT : 1;
+    i64 rbv[RB];
+    int rbi[RB];
+    if constexpr (PRO == PRO_RACE_EMBED) {
+        const __amdgpu_buffer_rsrc_t rv = buf_rsrc(a.part_v + (size_t)r * a.nblk, (unsigned)a.nblk * 8u),
+                                     ri = buf_rsrc(a.part_i + (size_t)r * a.nblk, (unsigned)a.nblk * 4u);
+#pragma unroll
+        for (int k = 0; k < RB; k++) {
+            const int g = tid + NT * k;
+            rbv[k] = buf_load8(rv, (unsigned)g * 8u);
+            const int ci = buf_load1(ri, (unsigned)g * 4u);
+            rbi[k] = g < a.nblk ? ci : -1;
+        }
+    }
     v4l c0[GA], c1[GA], wv[GA];
     v2q b01[GA], b23[GA], y01[GA], y23[GA], pa[GA][KA], pb[GA][KA];
 #pragma unroll
@@ -136,13 +155,52 @@ __global__ __launch_bounds__(NT) void k_light(LightArgs a) {
                 pa[m][ks] = *reinterpret_cast<const v2q*>(q);
                 pb[m][ks] = *reinterpret_cast<const v2q*>(q + 2);
             }
-        } else if constexpr (PRO != PRO_EMBED) {
+        } else if constexpr (PRO != PRO_EMBED && PRO != PRO_RACE_EMBED) {
 #pragma unroll
             for (int j = 0; j < 4; j++) v[m][j] = a.X[(size_t)r * K + k + j];
         }
     }
-    const int p = a.pos ? *a.pos : 0;              // the stage product (PRO_X16) has no position
+    // the step's position (the stage product, PRO_X16, has none; PRO_RACE_EMBED: a.pos holds the step before's)
+    const int p = a.pos ? *a.pos + (PRO == PRO_RACE_EMBED ? 1 : 0) : 0;
     if (a.skip_prompt && p < *a.plen - 1) return;
+    __shared__ int rtok;
+    if constexpr (PRO == PRO_RACE_EMBED) {
+        // the race over this stream's bests (largest, ties to the lowest word; k_race_rows's arithmetic); a prompt
+        // position keeps the prompt's next word
+        __shared__ i64 wbv[NW];
+        __shared__ int wbi[NW];
+        const int plen = *a.plen;
+        const bool known = p - 1 < plen - 1;
+        i64 bv = 0;
+        int bi = -1;
+#pragma unroll
+        for (int k = 0; k < RB; k++)
+            if (rbi[k] >= 0 && (bi < 0 || rbv[k] > bv || (rbv[k] == bv && rbi[k] < bi))) { bv = rbv[k]; bi = rbi[k]; }
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) {
+            const i64 ov = __shfl_xor(bv, o, 64);
+            const int oi = __shfl_xor(bi, o, 64);
+            if (oi >= 0 && (bi < 0 || ov > bv || (ov == bv && oi < bi))) { bv = ov; bi = oi; }
+        }
+        if (lane == 0) { wbv[wave] = bv; wbi[wave] = bi; }
+        __syncthreads();
+        if (tid == 0) {
+            bv = wbv[0]; bi = wbi[0];
+            for (int w = 1; w < NW; w++)
+                if (wbi[w] >= 0 && (bi < 0 || wbv[w] > bv || (wbv[w] == bv && wbi[w] < bi))) { bv = wbv[w]; bi = wbi[w]; }
+            int* sq = a.seqw + (size_t)r * a.seq_stride;
+            if (!known) {
+                sq[p] = bi;
+                if (p - plen >= 0) a.words[(size_t)r * a.words_stride + p - plen] = bi;
+            }
+            if (r == 0) {
+                *a.nwords = p - plen + 1;
+                *a.pos_next = p;
+            }
+            rtok = known ? sq[p] : bi;
+        }
+        __syncthreads();
+    }
     const bool rec_in = r == 0 && a.rec_pos && *a.rec_pos == p;
 #pragma unroll
     for (int m = 0; m < GPT; m++) {
@@ -166,10 +224,10 @@ __global__ __launch_bounds__(NT) void k_light(LightArgs a) {
                 if (rec_in && a.rpile_in) a.rpile_in[k + j] = pile;
                 if (rec_in && a.rout_in) a.rout_in[k + j] = y;
             }
-        } else if constexpr (PRO == PRO_EMBED) {
+        } else if constexpr (PRO == PRO_EMBED || PRO == PRO_RACE_EMBED) {
             const int pm = a.rowmap ? a.rowmap[r] : 0;
             const int st = a.rowmap ? pm >> 16 : r, q = a.rowmap ? pm & 0xFFFF : p;
-            const i64 tok = a.seq[(size_t)st * a.seq_stride + q];
+            const i64 tok = PRO == PRO_RACE_EMBED ? rtok : a.seq[(size_t)st * a.seq_stride + q];
 #pragma unroll
             for (int j = 0; j < 4; j++) {
                 v[m][j] = wadd(a.wte[tok * 768 + k + j], a.wpe[(i64)q * 768 + k + j]);
@@ -245,7 +303,8 @@ __global__ __launch_bounds__(NT) void k_light(LightArgs a) {
         if (rec && a.rexls) {
             i64 e2;
             a.rexls[0] = ex;
-            a.rexls[1] = PRO == PRO_GAUGE || PRO == PRO_EMBED || PRO == PRO_ADD_GAUGE ? gauge_ls_pow(S1, S2, ex, a.tb, e2) : 0;
+            a.rexls[1] = PRO == PRO_GAUGE || PRO == PRO_EMBED || PRO == PRO_RACE_EMBED || PRO == PRO_ADD_GAUGE
+                             ? gauge_ls_pow(S1, S2, ex, a.tb, e2) : 0;
         }
     }
 }
@@ -1202,6 +1261,7 @@ __global__ __launch_bounds__(256) void k_part_piles(GemmArgs a) {
 
 #define BINST_L(K, PRO, KSP) template __global__ void k_light<K, PRO, (K) / 4, KSP>(LightArgs);
 BINST_L(768, PRO_EMBED, 1)
+BINST_L(768, PRO_RACE_EMBED, 1)
 BINST_L(768, PRO_GAUGE, 1)
 BINST_L(768, PRO_TO16, 1)
 BINST_L(3072, PRO_TO16, 1)

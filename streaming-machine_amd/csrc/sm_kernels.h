@@ -18,7 +18,11 @@ enum { PRO_GAUGE = 0,   // gauge_log of the stream row R (768): x16, ex, LS (bas
        // batch 1 (GPT-2), layer 0's qkv: the race over the step before's head bests (base2.py:34-40, 114) and the
        // word fed back as the entering row wte[word] + wpe[q] (base2.py:103), in every block (block 0 writes the
        // word, the counters, the row and the next position), then PRO_GAUGE of that row: k_race1 folded in
-       PRO_RACE = 9 };
+       PRO_RACE = 9,
+       // batched streams, layer 0's light: the race over the step before's head bests for the row's stream
+       // (k_race_rows's arithmetic; block 0 writes the counters and the next position slot), then PRO_EMBED of the
+       // word it feeds back
+       PRO_RACE_EMBED = 10 };
 // epilogue: what a phase does with each finished pile
 enum { EPI_GAUGED = 0,       // power(pile, (we + ex + 16) 65536 - LS) + b          (base2.py:70-71)
        EPI_GAUGED_EDGE = 1,  // the same, then the edge                               (base2.py:106, 78-83)

@@ -377,8 +377,9 @@ struct sm_machine {
     // turn and arrival
     int mode = 0;
     bool fturn = false, farr = false;
-    // batch 1, GPT-2 with every stage integer, the full head read and the plain stream: a run's steps after its
-    // first take the race of the step before into layer 0's qkv (PRO_RACE), and the run ends with k_race1
+    // a run's steps after its first take the race of the step before into their first kernel, and the run ends
+    // with the race: batch 1 (GPT-2 with every stage integer, the full head read and the plain stream) into layer
+    // 0's qkv (PRO_RACE), the batched GPT-2 machine into the word's light (PRO_RACE_EMBED)
     bool fold = false;
     // batch 1: steps at positions from att_split on run the attention spread over chunks of positions (-1: never);
     // att_long is the structure of the steps being launched or captured
@@ -573,12 +574,18 @@ static void attend_rows(sm_machine* m, int rows, const AttArgs& a) {
 // rowmap != null: a pass of nrows prompt rows (row r: position rowmap[r] & 0xFFFF of stream rowmap[r] >> 16)
 // instead of one position of every stream.  Their words are known, so no head runs, and the last layer only
 // stores keys and values (its attention and banks feed the head alone); nothing is recorded.
+// fused: the race of the step before runs in the word's light (PRO_RACE_EMBED), which reads that step's position
+// slot and writes the other one, read by every later kernel of this step; race: the step ends with k_race_rows
 template <int RT>
 static int launch_step_batched(sm_machine* m, int parts, int nrows = 0,
-                               const int* rowmap = nullptr) {
+                               const int* rowmap = nullptr, bool fused = false, bool race = true) {
     const Tables tb = m->T.tb();
     int* ctl = m->ctl;
-    int* const posp = ctl + (m->par ? CTL_POS1 : CTL_POS);
+    const bool fold = m->fold && fused && !rowmap && parts == STEP_ALL;
+    if (!m->fold || rowmap || parts != STEP_ALL) race = true;
+    int* const posA = ctl + (m->par ? CTL_POS1 : CTL_POS);
+    int* const posp = fold ? ctl + (m->par ? CTL_POS : CTL_POS1) : posA;
+    if (fold) m->par ^= 1;
     const int B = rowmap ? nrows : m->B;
     const int* recp = rowmap ? nullptr : ctl + CTL_RECPOS;
     auto light_args = [&](int K, const i64* X, i64* rx16, i64* rexls) {
@@ -611,7 +618,14 @@ static int launch_step_batched(sm_machine* m, int parts, int nrows = 0,
         i64* rp = m->r_pile + (size_t)l * 4 * 3072;
         if (l == 0) {      // the word enters; later layers get their light from the previous layer's last kernel
             LightArgs a = light_args(768, m->R, rx, re);
-            launch(m->cfg.profile, "light.embed", k_light<768, PRO_EMBED, 192, 1>, dim3(B), dim3(192), 0, m->st, a);
+            if (fold) {    // the race of the step before, then the word it feeds back
+                a.pos = posA; a.pos_next = posp; a.nwords = ctl + CTL_NWORDS;
+                a.part_v = m->part_v; a.part_i = m->part_i; a.nblk = head_rows_grid(m->mhead.ntiles);
+                a.words = m->words; a.words_stride = m->ctx + 1; a.seqw = m->seq;
+                launch(m->cfg.profile, "light.embed", k_light<768, PRO_RACE_EMBED, 192, 1>, dim3(B), dim3(192), 0, m->st, a);
+            } else {
+                launch(m->cfg.profile, "light.embed", k_light<768, PRO_EMBED, 192, 1>, dim3(B), dim3(192), 0, m->st, a);
+            }
         }
         {
             GemmArgs a = gemm_args(m->mbank[l][0], m->QKV, 2304, rp, m->r_qkv + l * 2304);
@@ -668,8 +682,10 @@ static int launch_step_batched(sm_machine* m, int parts, int nrows = 0,
         r.part_v = m->part_v; r.part_i = m->part_i; r.nblk = parts; r.seq = m->seq; r.seq_stride = m->ctx + 1;
         r.words = m->words; r.words_stride = m->ctx + 1; r.pos = posp; r.plen = ctl + CTL_PLEN;
         r.pos_next = ctl + (m->par ? CTL_POS : CTL_POS1); r.nwords = ctl + CTL_NWORDS;
-        launch(m->cfg.profile, "race", k_race_rows, dim3(B), dim3(256), 0, m->st, r);
-        m->par ^= 1;                                 // the next step reads the slot this race writes
+        if (race) {
+            launch(m->cfg.profile, "race", k_race_rows, dim3(B), dim3(256), 0, m->st, r);
+            m->par ^= 1;                             // the next step reads the slot this race writes
+        }
     }
     HIP_TRY(hipGetLastError());
     return SM_OK;
@@ -1055,10 +1071,10 @@ static int launch_step(sm_machine* m, int parts = STEP_ALL, bool rec = false, bo
     if (m->kind == 1) return launch_step_pythia(m, parts, rec);
     if (m->B > 1) {
         const int RT = (m->B + 15) / 16;
-        if (RT == 1) return launch_step_batched<1>(m, parts);
-        if (RT == 2) return launch_step_batched<2>(m, parts);
-        if (RT == 3) return launch_step_batched<3>(m, parts);
-        return launch_step_batched<4>(m, parts);
+        if (RT == 1) return launch_step_batched<1>(m, parts, 0, nullptr, fused, race);
+        if (RT == 2) return launch_step_batched<2>(m, parts, 0, nullptr, fused, race);
+        if (RT == 3) return launch_step_batched<3>(m, parts, 0, nullptr, fused, race);
+        return launch_step_batched<4>(m, parts, 0, nullptr, fused, race);
     }
     const Tables tb = m->T.tb();
     int* ctl = m->ctl;
@@ -1270,7 +1286,7 @@ extern "C" int sm_create(const char* layout_dir, const sm_config* cfg, sm_machin
     m->farr = c.float_stages & SM_FLOAT_ARRIVAL;
     // the spread attention: batch 1 with the integer arrival and turn
     if (m->B == 1 && !m->farr && !m->fturn && c.att_split != -1) m->att_split = c.att_split > 0 ? c.att_split : SM_ATT_SPLIT_AT;
-    m->fold = m->B == 1 && !py && m->mode == 0 && !m->farr && !c.top_read;
+    m->fold = !py && (m->B > 1 || (m->mode == 0 && !m->farr && !c.top_read));
     const bool mfma = m->B > 1 || c.prefill_rows > 0;     // the MFMA banks: batched streams or prompt passes
 
     auto bail = [&](int code) { machine_free(m); return code; };
