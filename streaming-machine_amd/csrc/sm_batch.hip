@@ -99,6 +99,66 @@ SMD void slice_facts(const int* sf, int rows, int r, int (&ri)[8]) {
 // MFMA A planes plus the row's exponent, gauge, power factor and plane sums.  Each thread owns groups of four
 // consecutive k, so every plane byte group goes out as one 32-bit store.  KSP: the producing bank's K slices
 // (PRO_ADD_GAUGE), a compile-time count so that every load of the row is in flight at once.
+// The race of the step before folded into the next step's first kernel, one block a stream (k_race_rows's
+// arithmetic: the largest best, ties to the lowest word).  race_load requests stream r's bests (bounded loads:
+// past the last block none); race_pick reduces them over the block and returns the word fed back (a prompt
+// position keeps the prompt's), block r writing it into the sequence and the words, block 0 the counters and
+// the next position slot (q: the step's position, the one the word enters at).
+constexpr int RACE_NB = 512;       // the head's largest grid
+template <int NT>
+SMD void race_load(const i64* part_v, const int* part_i, int nblk, int r, int tid, i64 (&bv)[(RACE_NB + NT - 1) / NT],
+                   int (&bi)[(RACE_NB + NT - 1) / NT]) {
+    const __amdgpu_buffer_rsrc_t rv = buf_rsrc(part_v + (size_t)r * nblk, (unsigned)nblk * 8u),
+                                 ri = buf_rsrc(part_i + (size_t)r * nblk, (unsigned)nblk * 4u);
+#pragma unroll
+    for (int k = 0; k < (RACE_NB + NT - 1) / NT; k++) {
+        const int g = tid + NT * k;
+        bv[k] = buf_load8(rv, (unsigned)g * 8u);
+        const int ci = buf_load1(ri, (unsigned)g * 4u);
+        bi[k] = g < nblk ? ci : -1;
+    }
+}
+template <int NT>
+SMD int race_pick(const i64 (&rbv)[(RACE_NB + NT - 1) / NT], const int (&rbi)[(RACE_NB + NT - 1) / NT], int r, int tid,
+                  int q, int plen, int* seq, int seq_stride, int* words, int words_stride, int* nwords, int* pos_next) {
+    constexpr int NW = NT / 64;
+    __shared__ i64 wbv[NW];
+    __shared__ int wbi[NW];
+    __shared__ int tok_s;
+    const int lane = tid & 63, wave = tid >> 6;
+    i64 bv = 0;
+    int bi = -1;
+#pragma unroll
+    for (int k = 0; k < (RACE_NB + NT - 1) / NT; k++)
+        if (rbi[k] >= 0 && (bi < 0 || rbv[k] > bv || (rbv[k] == bv && rbi[k] < bi))) { bv = rbv[k]; bi = rbi[k]; }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        const i64 ov = __shfl_xor(bv, o, 64);
+        const int oi = __shfl_xor(bi, o, 64);
+        if (oi >= 0 && (bi < 0 || ov > bv || (ov == bv && oi < bi))) { bv = ov; bi = oi; }
+    }
+    if (lane == 0) { wbv[wave] = bv; wbi[wave] = bi; }
+    __syncthreads();
+    if (tid == 0) {
+        bv = wbv[0]; bi = wbi[0];
+        for (int w = 1; w < NW; w++)
+            if (wbi[w] >= 0 && (bi < 0 || wbv[w] > bv || (wbv[w] == bv && wbi[w] < bi))) { bv = wbv[w]; bi = wbi[w]; }
+        int* sq = seq + (size_t)r * seq_stride;
+        const bool known = q - 1 < plen - 1;          // the step before was a prompt position
+        if (!known) {
+            sq[q] = bi;
+            if (q - plen >= 0) words[(size_t)r * words_stride + q - plen] = bi;
+        }
+        if (r == 0) {
+            *nwords = q - plen + 1;
+            *pos_next = q;
+        }
+        tok_s = known ? sq[q] : bi;
+    }
+    __syncthreads();
+    return tok_s;
+}
+
 template <int K, int PRO, int NT, int KSP>
 __global__ __launch_bounds__(NT) void k_light(LightArgs a) {
     constexpr int NG = K / 4, GPT = (NG + NT - 1) / NT, KS = K / 64, NW = NT / 64;
@@ -119,21 +179,10 @@ __global__ __launch_bounds__(NT) void k_light(LightArgs a) {
         i_sxh = ri[4]; i_sxl = ri[5]; i_n32 = ri[6];
     }
     constexpr int GA = PRO == PRO_ADD_GAUGE ? GPT : 1, KA = PRO == PRO_ADD_GAUGE ? KSP : 1;
-    // PRO_RACE_EMBED: this stream's bests from the step before's head (bounded loads: past the last block none)
-    constexpr int RB = PRO == PRO_RACE_EMBED ? (512 + NT - 1) / NT : 1;
-    i64 rbv[RB];
-    int rbi[RB];
-    if constexpr (PRO == PRO_RACE_EMBED) {
-        const __amdgpu_buffer_rsrc_t rv = buf_rsrc(a.part_v + (size_t)r * a.nblk, (unsigned)a.nblk * 8u),
-                                     ri = buf_rsrc(a.part_i + (size_t)r * a.nblk, (unsigned)a.nblk * 4u);
-#pragma unroll
-        for (int k = 0; k < RB; k++) {
-            const int g = tid + NT * k;
-            rbv[k] = buf_load8(rv, (unsigned)g * 8u);
-            const int ci = buf_load1(ri, (unsigned)g * 4u);
-            rbi[k] = g < a.nblk ? ci : -1;
-        }
-    }
+    // PRO_RACE_EMBED: this stream's bests from the step before's head
+    i64 rbv[(RACE_NB + NT - 1) / NT];
+    int rbi[(RACE_NB + NT - 1) / NT];
+    if constexpr (PRO == PRO_RACE_EMBED) race_load<NT>(a.part_v, a.part_i, a.nblk, r, tid, rbv, rbi);
     v4l c0[GA], c1[GA], wv[GA];
     v2q b01[GA], b23[GA], y01[GA], y23[GA], pa[GA][KA], pb[GA][KA];
 #pragma unroll
@@ -163,44 +212,9 @@ __global__ __launch_bounds__(NT) void k_light(LightArgs a) {
     // the step's position (the stage product, PRO_X16, has none; PRO_RACE_EMBED: a.pos holds the step before's)
     const int p = a.pos ? *a.pos + (PRO == PRO_RACE_EMBED ? 1 : 0) : 0;
     if (a.skip_prompt && p < *a.plen - 1) return;
-    __shared__ int rtok;
-    if constexpr (PRO == PRO_RACE_EMBED) {
-        // the race over this stream's bests (largest, ties to the lowest word; k_race_rows's arithmetic); a prompt
-        // position keeps the prompt's next word
-        __shared__ i64 wbv[NW];
-        __shared__ int wbi[NW];
-        const int plen = *a.plen;
-        const bool known = p - 1 < plen - 1;
-        i64 bv = 0;
-        int bi = -1;
-#pragma unroll
-        for (int k = 0; k < RB; k++)
-            if (rbi[k] >= 0 && (bi < 0 || rbv[k] > bv || (rbv[k] == bv && rbi[k] < bi))) { bv = rbv[k]; bi = rbi[k]; }
-#pragma unroll
-        for (int o = 32; o > 0; o >>= 1) {
-            const i64 ov = __shfl_xor(bv, o, 64);
-            const int oi = __shfl_xor(bi, o, 64);
-            if (oi >= 0 && (bi < 0 || ov > bv || (ov == bv && oi < bi))) { bv = ov; bi = oi; }
-        }
-        if (lane == 0) { wbv[wave] = bv; wbi[wave] = bi; }
-        __syncthreads();
-        if (tid == 0) {
-            bv = wbv[0]; bi = wbi[0];
-            for (int w = 1; w < NW; w++)
-                if (wbi[w] >= 0 && (bi < 0 || wbv[w] > bv || (wbv[w] == bv && wbi[w] < bi))) { bv = wbv[w]; bi = wbi[w]; }
-            int* sq = a.seqw + (size_t)r * a.seq_stride;
-            if (!known) {
-                sq[p] = bi;
-                if (p - plen >= 0) a.words[(size_t)r * a.words_stride + p - plen] = bi;
-            }
-            if (r == 0) {
-                *a.nwords = p - plen + 1;
-                *a.pos_next = p;
-            }
-            rtok = known ? sq[p] : bi;
-        }
-        __syncthreads();
-    }
+    int rtok = 0;                                   // PRO_RACE_EMBED: the word fed back
+    if constexpr (PRO == PRO_RACE_EMBED)
+        rtok = race_pick<NT>(rbv, rbi, r, tid, p, *a.plen, a.seqw, a.seq_stride, a.words, a.words_stride, a.nwords, a.pos_next);
     const bool rec_in = r == 0 && a.rec_pos && *a.rec_pos == p;
 #pragma unroll
     for (int m = 0; m < GPT; m++) {
@@ -995,8 +1009,13 @@ struct PyRowArgs {
     i64* rpileM; i64* routM;                                         // PY_ADD: mproj's pile, the stream after it
     const int* rowmap;                            // prompt rows (PY_EMBED): stream << 16 | position per row
     int* err;                                     // its rshift assert (PY_ADD) sets SM_ERR_RANGE here
+    // PY_RACE_EMBED: the step before's head bests [rows][nblk], the prompt length, the words, the counters and the
+    // position slot the race writes (pos: the step before's)
+    const i64* part_v; const int* part_i; int nblk; const int* plen;
+    int* words; int words_stride; int* seqw; int* nwords; int* pos_next;
 };
-enum { PY_EMBED = 0, PY_ADD = 1, PY_GAUGE = 2 };
+// PY_RACE_EMBED: the race of the step before (race_pick), then PY_EMBED of the word it feeds back
+enum { PY_EMBED = 0, PY_ADD = 1, PY_GAUGE = 2, PY_RACE_EMBED = 3 };
 
 // plain(pile) of one bank for columns k .. k + 3 of row r, from its KS K-sliced partial piles
 // (:112-114), in two halves so that a caller can have every load of its row in flight before the arithmetic
@@ -1054,8 +1073,12 @@ __global__ __launch_bounds__(192) void k_py_rows(PyRowArgs a) {
     int* const rLO = red + 5 * NW;
     int* const rLS = red + 9 * NW;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, r = blockIdx.x;
+    i64 rbv[(RACE_NB + NT - 1) / NT];
+    int rbi[(RACE_NB + NT - 1) / NT];
+    if constexpr (MODE == PY_RACE_EMBED) race_load<NT>(a.part_v, a.part_i, a.nblk, r, tid, rbv, rbi);
     const int pm = a.rowmap ? a.rowmap[r] : 0;
-    const int p = a.rowmap ? pm & 0xFFFF : *a.pos, st = a.rowmap ? pm >> 16 : r;
+    // the step's position (PY_RACE_EMBED: a.pos holds the step before's)
+    const int p = a.rowmap ? pm & 0xFFFF : *a.pos + (MODE == PY_RACE_EMBED ? 1 : 0), st = a.rowmap ? pm >> 16 : r;
     const bool rec = r == 0 && a.rec_pos && *a.rec_pos == p;
     const bool two = a.ng2 != nullptr;             // uniform
     // the stream row (192 threads hold four lanes each)
@@ -1064,8 +1087,10 @@ __global__ __launch_bounds__(192) void k_py_rows(PyRowArgs a) {
     int gn[2][4];
     i64 gb[2][4];
     {
-        if (MODE == PY_EMBED) {
-            const i64 tok = a.seq[(size_t)st * a.seq_stride + p];
+        if (MODE == PY_EMBED || MODE == PY_RACE_EMBED) {
+            const i64 tok = MODE == PY_RACE_EMBED
+                ? race_pick<NT>(rbv, rbi, r, tid, p, *a.plen, a.seqw, a.seq_stride, a.words, a.words_stride, a.nwords, a.pos_next)
+                : a.seq[(size_t)st * a.seq_stride + p];
             const i64 es = -((i64)a.ee[tok] + 16);
 #pragma unroll
             for (int j = 0; j < 4; j++) R4[j] = rsh((i64)a.ew[tok * 768 + k + j], es);
@@ -1104,7 +1129,7 @@ __global__ __launch_bounds__(192) void k_py_rows(PyRowArgs a) {
                 for (int j = 0; j < 4; j++) R4[j] = rr[j];
             }
         }
-        if (MODE == PY_EMBED) {
+        if (MODE == PY_EMBED || MODE == PY_RACE_EMBED) {
 #pragma unroll
             for (int gi = 0; gi < 2; gi++) {
                 const int* ng = gi ? (two ? a.ng2 : a.ng1) : a.ng1;
@@ -1269,6 +1294,7 @@ BINST_L(768, PRO_X16, 1)
 BINST_L(3072, PRO_X16, 1)
 BINST_L(768, PRO_ADD_GAUGE, 4)
 template __global__ void k_py_rows<PY_EMBED>(PyRowArgs);
+template __global__ void k_py_rows<PY_RACE_EMBED>(PyRowArgs);
 template __global__ void k_py_rows<PY_ADD>(PyRowArgs);
 template __global__ void k_py_rows<PY_GAUGE>(PyRowArgs);
 #define BINST_G(K, NB, KSPLIT, EPI) template __global__ void k_gemm<K, NB, KSPLIT, EPI>(GemmArgs);

@@ -379,7 +379,8 @@ struct sm_machine {
     bool fturn = false, farr = false;
     // a run's steps after its first take the race of the step before into their first kernel, and the run ends
     // with the race: batch 1 (GPT-2 with every stage integer, the full head read and the plain stream) into layer
-    // 0's qkv (PRO_RACE), the batched GPT-2 machine into the word's light (PRO_RACE_EMBED)
+    // 0's qkv (PRO_RACE), the batched machines into the word's light or row kernel (PRO_RACE_EMBED,
+    // PY_RACE_EMBED)
     bool fold = false;
     // batch 1: steps at positions from att_split on run the attention spread over chunks of positions (-1: never);
     // att_long is the structure of the steps being launched or captured
@@ -913,10 +914,15 @@ static int launch_step_pythia(sm_machine* m, int parts, bool rec) {
 // rowmap != null: a pass of nrows prompt rows, as in launch_step_batched, one kernel a launch.
 template <int RT>
 static int launch_step_pythia_batched(sm_machine* m, int parts, int nrows = 0,
-                                      const int* rowmap = nullptr) {
+                                      const int* rowmap = nullptr, bool fused = false, bool race = true) {
     const Tables tb = m->T.tb();
     int* ctl = m->ctl;
-    int* const posp = ctl + (m->par ? CTL_POS1 : CTL_POS);
+    // (fused, race: as launch_step_batched; the race of the step before runs in the word's row kernel)
+    const bool fold = m->fold && fused && !rowmap && parts == STEP_ALL;
+    if (!m->fold || rowmap || parts != STEP_ALL) race = true;
+    int* const posA = ctl + (m->par ? CTL_POS1 : CTL_POS);
+    int* const posp = fold ? ctl + (m->par ? CTL_POS : CTL_POS1) : posA;
+    if (fold) m->par ^= 1;
     const int B = rowmap ? nrows : m->B;
     const int* recp = rowmap ? nullptr : ctl + CTL_RECPOS;
     const size_t PL = (size_t)4 * 48 * 3 * 1024, RC = m->RC;
@@ -955,7 +961,14 @@ static int launch_step_pythia_batched(sm_machine* m, int parts, int nrows = 0,
         if (l == 0) {
             PyRowArgs a = rows_args();
             gauges(a, 0);
-            launch(m->cfg.profile, "rows.embed", k_py_rows<PY_EMBED>, dim3(B), dim3(192), 0, m->st, a);
+            if (fold) {    // the race of the step before, then the word it feeds back
+                a.pos = posA; a.pos_next = posp; a.nwords = ctl + CTL_NWORDS; a.plen = ctl + CTL_PLEN;
+                a.part_v = m->part_v; a.part_i = m->part_i; a.nblk = head_rows_grid(m->mhead.ntiles);
+                a.words = m->words; a.words_stride = m->ctx + 1; a.seqw = m->seq;
+                launch(m->cfg.profile, "rows.embed", k_py_rows<PY_RACE_EMBED>, dim3(B), dim3(192), 0, m->st, a);
+            } else {
+                launch(m->cfg.profile, "rows.embed", k_py_rows<PY_EMBED>, dim3(B), dim3(192), 0, m->st, a);
+            }
         }
         GemmArgs aq = gemm_args(m->mbank[l][0], pA, rA);              // qkv: plain, written
         aq.Y = m->QKV; aq.ystride = 2304; aq.rpile = rp; aq.rout = m->r_qkv + l * 2304;
@@ -1050,8 +1063,10 @@ static int launch_step_pythia_batched(sm_machine* m, int parts, int nrows = 0,
         r.part_v = m->part_v; r.part_i = m->part_i; r.nblk = grid; r.seq = m->seq; r.seq_stride = m->ctx + 1;
         r.words = m->words; r.words_stride = m->ctx + 1; r.pos = posp; r.plen = ctl + CTL_PLEN;
         r.pos_next = ctl + (m->par ? CTL_POS : CTL_POS1); r.nwords = ctl + CTL_NWORDS;
-        launch(m->cfg.profile, "race", k_race_rows, dim3(B), dim3(256), 0, m->st, r);
-        m->par ^= 1;                                 // the next step reads the slot this race writes
+        if (race) {
+            launch(m->cfg.profile, "race", k_race_rows, dim3(B), dim3(256), 0, m->st, r);
+            m->par ^= 1;                             // the next step reads the slot this race writes
+        }
     }
     HIP_TRY(hipGetLastError());
     return SM_OK;
@@ -1063,10 +1078,10 @@ static int launch_step_pythia_batched(sm_machine* m, int parts, int nrows = 0,
 static int launch_step(sm_machine* m, int parts = STEP_ALL, bool rec = false, bool fused = false, bool race = true) {
     if (m->kind == 1 && m->B > 1) {
         const int RT = (m->B + 15) / 16;
-        if (RT == 1) return launch_step_pythia_batched<1>(m, parts);
-        if (RT == 2) return launch_step_pythia_batched<2>(m, parts);
-        if (RT == 3) return launch_step_pythia_batched<3>(m, parts);
-        return launch_step_pythia_batched<4>(m, parts);
+        if (RT == 1) return launch_step_pythia_batched<1>(m, parts, 0, nullptr, fused, race);
+        if (RT == 2) return launch_step_pythia_batched<2>(m, parts, 0, nullptr, fused, race);
+        if (RT == 3) return launch_step_pythia_batched<3>(m, parts, 0, nullptr, fused, race);
+        return launch_step_pythia_batched<4>(m, parts, 0, nullptr, fused, race);
     }
     if (m->kind == 1) return launch_step_pythia(m, parts, rec);
     if (m->B > 1) {
@@ -1286,7 +1301,7 @@ extern "C" int sm_create(const char* layout_dir, const sm_config* cfg, sm_machin
     m->farr = c.float_stages & SM_FLOAT_ARRIVAL;
     // the spread attention: batch 1 with the integer arrival and turn
     if (m->B == 1 && !m->farr && !m->fturn && c.att_split != -1) m->att_split = c.att_split > 0 ? c.att_split : SM_ATT_SPLIT_AT;
-    m->fold = !py && (m->B > 1 || (m->mode == 0 && !m->farr && !c.top_read));
+    m->fold = m->B > 1 || (!py && m->mode == 0 && !m->farr && !c.top_read);
     const bool mfma = m->B > 1 || c.prefill_rows > 0;     // the MFMA banks: batched streams or prompt passes
 
     auto bail = [&](int code) { machine_free(m); return code; };
