@@ -875,7 +875,8 @@ def main():
                 **({"step_us": round(1000.0 * pyleg["ms_per_step"], 2),
                     "step_over_bytes_floor": round(1000.0 * pyleg["ms_per_step"] / floor["pythia32"]["bytes_us"], 3)}
                    if pyleg else {}),
-                "note": "the Pythia 32-stream step's 51 launches with the machine's grids, graphs of 16 steps: the "
+                "note": "the Pythia 32-stream step's 50 launches (the race of the step before in the word's row "
+                        "kernel, once more after a graph's last step) with the machine's grids, graphs of 16 steps: the "
                         "paired banks and the paired attention and mproj partials reading their shares (the attention "
                         "192 positions of cache rows a block), proj, the row kernels, the head, no arithmetic"}},
         "batched": batched,
