@@ -105,6 +105,8 @@ KV_LAYOUT = 12 * (768 * 6 + 12 * 12)   # what this layout reads: int16 k, int32 
 def b1_kernel_bytes(name: str, ctx: float, vocab: int = VOCAB) -> float:
     if name in BANKS:
         return bank_bytes(*BANKS[name])
+    if name == "qkv.race":                  # layer 0's qkv with the step before's race: its plate (the race reads
+        return bank_bytes(*BANKS["qkv"])    # 6 KB of head bests and a word's row beside it)
     if name == "head":
         return bank_bytes(768, vocab)
     if name == "head.top":                  # the collapsing top read's first stage: the high-byte plane, e and b

@@ -623,7 +623,7 @@ static int launch_step_batched(sm_machine* m, int parts, int nrows = 0,
                 a.pos = posA; a.pos_next = posp; a.nwords = ctl + CTL_NWORDS;
                 a.part_v = m->part_v; a.part_i = m->part_i; a.nblk = head_rows_grid(m->mhead.ntiles);
                 a.words = m->words; a.words_stride = m->ctx + 1; a.seqw = m->seq;
-                launch(m->cfg.profile, "light.embed", k_light<768, PRO_RACE_EMBED, 192, 1>, dim3(B), dim3(192), 0, m->st, a);
+                launch(m->cfg.profile, "light.embed.race", k_light<768, PRO_RACE_EMBED, 192, 1>, dim3(B), dim3(192), 0, m->st, a);
             } else {
                 launch(m->cfg.profile, "light.embed", k_light<768, PRO_EMBED, 192, 1>, dim3(B), dim3(192), 0, m->st, a);
             }
@@ -965,7 +965,7 @@ static int launch_step_pythia_batched(sm_machine* m, int parts, int nrows = 0,
                 a.pos = posA; a.pos_next = posp; a.nwords = ctl + CTL_NWORDS; a.plen = ctl + CTL_PLEN;
                 a.part_v = m->part_v; a.part_i = m->part_i; a.nblk = head_rows_grid(m->mhead.ntiles);
                 a.words = m->words; a.words_stride = m->ctx + 1; a.seqw = m->seq;
-                launch(m->cfg.profile, "rows.embed", k_py_rows<PY_RACE_EMBED>, dim3(B), dim3(192), 0, m->st, a);
+                launch(m->cfg.profile, "rows.embed.race", k_py_rows<PY_RACE_EMBED>, dim3(B), dim3(192), 0, m->st, a);
             } else {
                 launch(m->cfg.profile, "rows.embed", k_py_rows<PY_EMBED>, dim3(B), dim3(192), 0, m->st, a);
             }
@@ -1119,7 +1119,7 @@ static int launch_step(sm_machine* m, int parts = STEP_ALL, bool rec = false, bo
             set_pf(a, m->bank[l][1], 2, grid2(m->bank[l][1]));
             if (l == 0 && fold) {       // the race of the step before, then the gauge of the row it feeds back
                 a.pos = posA; a.race = rfold;
-                gemv<768, 2, 4, PRO_RACE, EPI_GAUGED>(m, rec, "qkv", (P.ntiles + 3) / 4, a);
+                gemv<768, 2, 4, PRO_RACE, EPI_GAUGED>(m, rec, "qkv.race", (P.ntiles + 3) / 4, a);
             } else {
                 gemv<768, 2, 4, PRO_GAUGE, EPI_GAUGED>(m, rec, "qkv", (P.ntiles + 3) / 4, a);
             }
