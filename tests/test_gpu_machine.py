@@ -245,3 +245,26 @@ def test_profiled_machine_gives_the_same_words(sm, full_dir, golden, use_graph, 
     n, us = m.profile()
     assert n == len(c["words"]) + (len(c["prompt"]) - 1 if rows == 0 else 0) and us > 0
     m.close()
+
+
+@pytest.mark.parametrize("kind,streams,use_graph", [("gpt2", 1, True), ("gpt2", 1, False), ("gpt2", 3, True),
+                                                    ("pythia", 1, True), ("pythia", 3, True)])
+def test_runs_of_steps(sm, small_dir, small_oracle, py_small_dir, py_small_oracle, kind, streams, use_graph):
+    """a generation cut into calls of 5, 1, 4 and 7 words, with graphs of 3 steps and a recorded position part way:
+    runs of one, two and three steps, chunk ends inside a call and a run split by the recorded step.  A run's later
+    steps take the race of the step before into their first kernel and the run ends with the race, so every cut
+    is a place where the machine must hold a raced position; the words are the oracle's"""
+    d, orc = (small_dir, small_oracle) if kind == "gpt2" else (py_small_dir, py_small_oracle)
+    prompts = [sm.prompt_ids(70 + b, 6, 1000) for b in range(streams)]
+    m = sm.Machine(d, max_ctx=64, max_streams=streams, graph_steps=3, use_graph=use_graph)
+    m.reset()
+    m.record_at(6 + 7)
+    for b, p in enumerate(prompts):
+        m.prefill(p, b)
+    got = [[] for _ in range(streams)]
+    for n in (5, 1, 4, 7):
+        for b, row in enumerate(m.generate(n)):
+            got[b] += [int(w) for w in row]
+    m.close()
+    for b in range(streams):
+        assert got[b] == orc.generate(prompts[b], 17, 64), f"stream {b}"
