@@ -340,10 +340,12 @@ static void tables_free(sm_tables& T) {
 
 // ---------------------------------------------------------------------------------------------------------
 // the machine
-// CTL_POS / CTL_POS1: the position's two slots.  Batch 1 keeps it in CTL_POS (its race is one block).  Batched
-// streams alternate: a step reads the slot of the machine's parity and its race writes the next position into the
-// other, which no kernel of that step reads, so the race needs no grid-wide handoff (a last-arriving block behind
-// a fence costs more than the kernel boundary it would save)
+// CTL_POS / CTL_POS1: the position's two slots.  A step reads the slot of the machine's parity; a race run as
+// part of another kernel's blocks (the race of the step before folded into a step's first kernel, and every
+// batched race) writes the next position into the other slot, which no block of that kernel reads, so the race
+// needs no grid-wide handoff (a last-arriving block behind a fence costs more than the kernel boundary it would
+// save).  Batch 1's k_race1 (one block, a run's last step, and the machines that do not fold) advances its slot in
+// place
 enum { CTL_POS = 0, CTL_PLEN = 1, CTL_NWORDS = 2, CTL_ERR = 3, CTL_RECPOS = 4, CTL_POS1 = 6, CTL_N = 8 };
 static const int NIN[4] = {768, 768, 768, 3072};
 static const int NOUT[4] = {2304, 768, 3072, 768};
